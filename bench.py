@@ -1,0 +1,172 @@
+#!/usr/bin/env python3
+"""Benchmark of the torchpairwise hot path on one MI355X.
+
+Workload (BASELINE.json metric): x1, x2 = [16384, 128] fp32 (torch.randn from CPU generators
+seeded 0 and 1, moved to HBM before timing).  One step = one pass of the hot path over that
+batch; the headline is euclidean_distances (the MFMA kernel), with manhattan_distances (VALU)
+and hamming_distances on bool inputs (rand < 0.5, packed once per call) timed the same way
+and reported under "extra".
+
+value = pair-features/s (N*M*D per call / mean call time over the timed steps), inputs
+resident in HBM.  Timing: W untimed warm-up steps, then K steps between two
+torch.cuda.synchronize() calls; per-kernel durations come from HIP events recorded on the
+stream the kernels are launched on (torch's current stream, which the C ABI receives).
+
+roofline (dominant kernel = the MFMA pairwise kernel of euclidean):
+  algorithmic flops per launch = 2*N*M*D (one multiply-add per pair-feature), peak = MI355X
+  dense FP32 MFMA 157.3 TFLOP/s.
+cpu_baseline: the reference's CPU path for euclidean_distances is at::cdist(p=2) -> on the
+  host cores via torch.cdist, timed on a bounded row sample of the same workload.
+
+`python bench.py --gpus N` with N > 1 exits: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_FP32_MFMA = 157.3e12
+PEAK_HBM = 8.0e12
+PEAK_VALU_LANE_OPS = 256 * 64 * 2.4e9  # non-packed VALU issue rate (lane-ops/s)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--n", type=int, default=16384)
+    ap.add_argument("--d", type=int, default=128)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of l2,l1,hamming (default all)")
+    return ap.parse_args()
+
+
+def time_op(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
+    return ev_ms, wall * 1e3 / steps
+
+
+def cpu_baseline_l2(n, d, budget_s=15.0):
+    """torch.cdist(p=2) on the host (the reference's at::cdist) over a row sample of x1
+    against the full x2, scaled to pair-features/s."""
+    import torch
+
+    g1 = torch.Generator().manual_seed(0)
+    g2 = torch.Generator().manual_seed(1)
+    x2 = torch.randn(n, d, generator=g2)
+    rows = 1024
+    x1 = torch.randn(rows, d, generator=g1)
+    torch.cdist(x1, x2, 2)  # warm-up
+    reps, t_total = 0, 0.0
+    while t_total < budget_s and reps < 200:
+        t0 = time.perf_counter()
+        torch.cdist(x1, x2, 2)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    pf = rows * n * d
+    return {"value": pf * reps / t_total, "unit": "pair-features/s",
+            "cores": torch.get_num_threads(), "kind": "reference",
+            "sample": f"torch.cdist(x1[{rows},{d}], x2[{n},{d}], p=2) on CPU (= at::cdist of "
+                      f"euclidean_distances), {reps} reps, {t_total:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; run with --gpus 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+        sys.exit(2)
+    import torch
+
+    from torchpairwise_amd import _capi as capi
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = "cuda"
+    n, d = args.n, args.d
+    g1 = torch.Generator().manual_seed(0)
+    g2 = torch.Generator().manual_seed(1)
+    x1 = torch.randn(n, d, generator=g1).to(dev)
+    x2 = torch.randn(n, d, generator=g2).to(dev)
+    b1 = (torch.rand(n, d, generator=torch.Generator().manual_seed(0)) < 0.5).to(dev)
+    b2 = (torch.rand(n, d, generator=torch.Generator().manual_seed(1)) < 0.5).to(dev)
+    only = set(args.only.split(",")) if args.only else {"l2", "l1", "hamming"}
+    pf = n * n * d
+    extra = {}
+    res = {}
+
+    if "l2" in only:
+        ms, wall_ms = time_op(lambda: capi.pairwise_inner(x1, x2, capi.EPI_EUCLIDEAN),
+                              args.steps, args.warmup)
+        flops = 2.0 * n * n * d
+        res["l2"] = {"ms": ms, "wall_ms": wall_ms, "value": pf / (ms * 1e-3),
+                     "roofline": {"bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12,
+                                  "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                                  "frac": flops / (ms * 1e-3) / PEAK_FP32_MFMA, "traffic": None}}
+    if "l1" in only:
+        ms, wall_ms = time_op(lambda: capi.lp_distances(x1, x2, 1.0), args.steps, args.warmup)
+        ops = 2.0 * pf  # v_sub + abs-modified v_add per pair-feature
+        extra["manhattan_fp32"] = {
+            "value": pf / (ms * 1e-3), "ms_per_call": ms,
+            "roofline": {"bound": "valu", "achieved": ops / (ms * 1e-3) / 1e12,
+                         "peak": PEAK_VALU_LANE_OPS / 1e12, "unit": "Tlane-op/s",
+                         "frac": ops / (ms * 1e-3) / PEAK_VALU_LANE_OPS,
+                         "convention": "2 VALU lane-ops per pair-feature (sub, abs-add) against "
+                                       "the non-packed issue rate 256 CU x 64 lanes x 2.4 GHz"}}
+    if "hamming" in only:
+        ms, wall_ms = time_op(lambda: capi.bool_pairwise_reduce(b1, b2, capi.BIT_NE, capi.RED_MEAN),
+                              args.steps, args.warmup)
+        out_bytes = 4.0 * n * n
+        extra["hamming_bool"] = {
+            "value": pf / (ms * 1e-3), "ms_per_call": ms,
+            "roofline": {"bound": "hbm", "achieved": out_bytes / (ms * 1e-3) / 1e9,
+                         "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                         "frac": out_bytes / (ms * 1e-3) / PEAK_HBM,
+                         "note": "algorithmic bytes = the fp32 output (inputs are 2 x 2 MiB, "
+                                 "packed to 2 x 256 KiB); includes the pack launches"}}
+
+    head = res.get("l2")
+    line = {
+        "metric": "pair-features/s (N·M·D/s) + % roofline, L2/L1/Hamming at 16k×16k×128, 1 GPU",
+        "value": head["value"] if head else None,
+        "unit": "pair-features/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"] if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (torch.randn, CPU generators seeded 0/1, moved to HBM before timing)",
+        "config": {"workload": f"euclidean_distances x1[{n},{d}] x2[{n},{d}] fp32 "
+                               f"(manhattan fp32 and hamming bool at the same shape under extra)",
+                   "n": n, "m": n, "d": d},
+        "roofline": head["roofline"] if head else None,
+        "extra": extra,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_l2(n, d)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

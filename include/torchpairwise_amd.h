@@ -1,0 +1,224 @@
+/*
+ * torchpairwise_amd — C ABI of the gfx950 (MI355X) pairwise-metric kernels.
+ *
+ * The reference (inspiros/torchpairwise v0.3.0) exposes its kernels only through
+ * PyTorch dispatcher registrations (TORCH_LIBRARY_IMPL(torchpairwise, CPU/CUDA, m));
+ * it has no C ABI of its own.  Each entry point below replaces one of those
+ * registered L1 kernels (the reference file:line is given beside it), with plain
+ * device pointers and sizes instead of at::Tensor, so that any host language can
+ * bind it.  The PyTorch extension in torchpairwise_amd/csrc/ops is one such host;
+ * ctypes (tests) is another.
+ *
+ * Conventions shared by every entry point:
+ *   - all pointers are device pointers (HBM) unless stated otherwise;
+ *   - tensors are dense and row-major: x1 is [batch, n, d], x2 is [batch, m, d],
+ *     pairwise outputs are [batch, n, m];
+ *   - `stream` is a hipStream_t (NULL = the null stream); work is only enqueued,
+ *     nothing synchronises;
+ *   - the return value is TPW_OK or an error code; tpw_last_error() gives the
+ *     message of the last failure on the calling thread.
+ *   - no entry point allocates device memory; scratch memory, where a kernel needs
+ *     it, is passed in by the caller (its size is given by a *_workspace_size call).
+ */
+#ifndef TORCHPAIRWISE_AMD_H_
+#define TORCHPAIRWISE_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TPW_OK 0
+#define TPW_ERR_INVALID 1 /* bad argument (shape, dtype, alignment, null pointer) */
+#define TPW_ERR_LAUNCH 2  /* the HIP runtime rejected a launch */
+
+/* element types accepted by the floating-point entry points */
+#define TPW_F32 0
+#define TPW_BF16 1
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *tpw_last_error(void);
+
+/* HIP runtime version the library was built against, as hipRuntimeGetVersion
+ * reports it.  Replaces `_cuda_version()` (torchpairwise/csrc/torchpairwise.cpp:28-40),
+ * which returned CUDA_VERSION or -1. */
+int tpw_runtime_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* Bit-packed boolean family (hamming, jaccard, pw*_sum / pw*_mean on bool)   */
+/* ------------------------------------------------------------------------- */
+
+/* binary ops of the reference's common/binary_ops.h:9-20 that act on bool */
+#define TPW_BIT_AND 0
+#define TPW_BIT_OR 1
+#define TPW_BIT_XOR 2
+#define TPW_BIT_EQ 3
+#define TPW_BIT_NE 4
+/* reductions of common/reduction_ops.h:8-12 that produce float32 */
+#define TPW_RED_SUM 0
+#define TPW_RED_MEAN 1
+
+/* Number of uint32 words per packed row of `d` booleans: ceil(d/32) rounded up
+ * to a multiple of 4 so that rows are 16-byte aligned.  Padding bits are zero. */
+int64_t tpw_packed_words(int64_t d);
+
+/* Pack `rows` rows of `d` bool bytes (0/1, torch.bool layout) into
+ * rows x tpw_packed_words(d) uint32 words, bit k of row r at word k/32, bit k%32.
+ * If `row_popcounts` is not NULL it receives the number of set bits of each row.
+ * Replaces the bool-byte input path of pairwise_binary_reduction_forward_kernel
+ * (csrc/ops/cuda/pairwise_binary_kernels.cu:144-220), which read the bytes
+ * directly for every output. */
+int tpw_pack_bool_rows(const uint8_t *x, int64_t rows, int64_t d, uint32_t *words,
+                       int32_t *row_popcounts, void *stream);
+
+/* out[b,i,j] = reduction_k op(x1[b,i,k], x2[b,j,k]) over packed rows, as float32.
+ * `op` is a TPW_BIT_* code, `reduction` TPW_RED_SUM (count) or TPW_RED_MEAN
+ * (count / d).  Counts are exact integers; the result is the reference's float
+ * accumulator (exact below 2^24, saturating at 2^24) and its `val /= d`.
+ * Replaces pairwise_binary_reduction_forward_kernel<op, Sum|Mean> for bool inputs
+ * (csrc/ops/cuda/pairwise_binary_kernels.cu:32-53,144-220;
+ *  CPU: csrc/ops/cpu/pairwise_binary_kernels.cpp:28-49,118-171).
+ * hamming_distances on bool is (TPW_BIT_NE, TPW_RED_MEAN)
+ * (csrc/ops/pairwise_metrics.cpp:206-213). */
+int tpw_bool_pairwise_reduce(const uint32_t *x1_words, const uint32_t *x2_words,
+                             int64_t batch, int64_t n, int64_t m, int64_t d, int op,
+                             int reduction, float *out, void *stream);
+
+/* jaccard_distances on bool: out = prf_div(xor_count, or_count, "zero"), i.e.
+ * or == 0 ? 0 : fl32(xor) / fl32(or), from AND counts and row popcounts
+ * (xor = pa + pb - 2 and, or = pa + pb - and).  Replaces the three passes
+ * pwxor_sum + pwor_sum + prf_div of csrc/ops/pairwise_metrics.cpp:215-222. */
+int tpw_jaccard_bool(const uint32_t *x1_words, const uint32_t *x2_words,
+                     const int32_t *x1_popcounts, const int32_t *x2_popcounts,
+                     int64_t batch, int64_t n, int64_t m, int64_t d, float *out,
+                     void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* Inner-product family (MFMA): euclidean, sqeuclidean, cosine, linear        */
+/* ------------------------------------------------------------------------- */
+
+#define TPW_EPI_DOT 0         /* s = x1 . x2                                  */
+#define TPW_EPI_EUCLIDEAN 1   /* sqrt(max(0, |x1|^2 + |x2|^2 - 2 s))          */
+#define TPW_EPI_SQEUCLIDEAN 2 /* max(0, |x1|^2 + |x2|^2 - 2 s)                */
+#define TPW_EPI_COSINE_SIM 3  /* prf_div(s, |x1| |x2|, "identity")            */
+#define TPW_EPI_COSINE_DIST 4 /* clip(1 - prf_div(s, |x1||x2|, identity), 0, 2) */
+
+/* norms[r] = sum_k x[r,k]^2 (squared != 0) or its square root, in float32.
+ * Replaces x.pow(2).sum(-1) / x.norm(2, -1) feeding _euclidean_dist
+ * (torch/_decomp/decompositions.py:691-701) and cosine_similarity
+ * (csrc/ops/pairwise_metrics.cpp:118-119). */
+int tpw_row_norms(const void *x, int dtype, int64_t rows, int64_t d, int squared,
+                  float *norms, void *stream);
+
+/* out[b,i,j] = epilogue(x1[b,i,:] . x2[b,j,:], aux1[b*n+i], aux2[b*m+j]) with the
+ * contraction on the matrix cores (fp32: v_mfma_f32_32x32x2_f32; bf16:
+ * v_mfma_f32_32x32x16_bf16, fp32 accumulation).  aux1/aux2 are the squared norms
+ * for EUCLIDEAN/SQEUCLIDEAN, the norms for COSINE_*, unused (may be NULL) for DOT.
+ * `out` has the element type of the inputs.
+ * Replaces at::cdist(x1, x2, 2) on its matrix-product path (_euclidean_dist,
+ * csrc/ops/pairwise_metrics.cpp:24-31), and matmul + prf_div (+ 1 - s, clip) of
+ * cosine_similarity / cosine_distances (csrc/ops/pairwise_metrics.cpp:51-56,112-122). */
+int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int64_t batch,
+                       int64_t n, int64_t m, int64_t d, const float *aux1,
+                       const float *aux2, int epilogue, void *out, void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* Non-GEMM reductions (VALU): manhattan, chebyshev, minkowski                */
+/* ------------------------------------------------------------------------- */
+
+/* out[b,i,j] = (sum_k |x1[b,i,k] - x2[b,j,k]|^p)^(1/p); p = 0 counts non-zero
+ * differences, p = 1 manhattan, p = +inf chebyshev (max).  fp32 only.
+ * Replaces at::_cdist_forward (reached from at::cdist for p != 2, and for p = 2
+ * when both row counts are <= 25) used by manhattan / minkowski / chebyshev
+ * (csrc/ops/pairwise_metrics.cpp:42-49,160-168,299-306). */
+int tpw_lp_distances(const float *x1, const float *x2, int64_t batch, int64_t n,
+                     int64_t m, int64_t d, double p, float *out, void *stream);
+
+/* Workspace (bytes) of tpw_lp_distances_backward for these sizes (0 = none). */
+size_t tpw_lp_backward_workspace_size(int64_t batch, int64_t n, int64_t m, int64_t d);
+
+/* grad_x1[b,i,k] = sum_j dD[b,i,j]/dx1[b,i,k] * grad[b,i,j] for the Lp distance
+ * `dist` produced by tpw_lp_distances (same p), with torch's per-p formulas
+ * (p = 0: zero; 1: g sign(diff); p < 2: sign(diff) |diff|^(p-1) g / dist^(p-1), 0 where
+ * dist == 0 or (diff == 0 and p < 1); 2: g diff / dist; inf: g sign(diff) [|diff| == dist];
+ * other: diff |diff|^(p-2) g / dist^(p-1)).  Here n is the row count of `x1` and m that
+ * of `x2`.  With `transposed` != 0 the same call yields grad_x2: pass x2 as `x1`, x1 as
+ * `x2`, and the original grad and dist, which are then read transposed (as [batch,m,n]).
+ * Replaces at::_cdist_backward (derivatives.yaml:1338-1340: x1 -> _cdist_backward
+ * (grad, x1, x2, p, result); x2 -> _cdist_backward(grad.mT, x2, x1, p, result.mT)). */
+int tpw_lp_distances_backward(const float *grad, const float *x1, const float *x2,
+                              const float *dist, int64_t batch, int64_t n, int64_t m,
+                              int64_t d, double p, int transposed, float *grad_x1,
+                              void *workspace, void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* Backward of the inner-product family                                       */
+/* ------------------------------------------------------------------------- */
+
+/* Workspace (bytes) needed by tpw_euclidean_backward / tpw_cosine_backward: an fp32
+ * [batch, n, m] pair-weight matrix plus small per-row buffers. */
+size_t tpw_inner_backward_workspace_size(int64_t batch, int64_t n, int64_t m, int64_t d);
+
+/* _euclidean_dist_backward: ratio = grad / res (0 where res == 0);
+ * grad_x1 = x1 * sum_j ratio - ratio @ x2, grad_x2 = x2 * sum_i ratio - ratio^T @ x1.
+ * grad and res are [batch,n,m] of the input type; both gradient products run on the
+ * matrix cores.  When x2 is x1 (x2=None upstream), the caller adds the two halves.
+ * Replaces _euclidean_dist_backward (derivatives.yaml:1335-1336) under at::cdist(p=2). */
+int tpw_euclidean_backward(const void *grad, const void *x1, const void *x2,
+                           const void *res, int dtype, int64_t batch, int64_t n,
+                           int64_t m, int64_t d, void *grad_x1, void *grad_x2,
+                           void *workspace, void *stream);
+
+/* Backward of cosine_distances = clip(1 - prf_div(x1 x2^T, n1 n2^T, identity), 0, 2):
+ * the autograd graph of csrc/ops/pairwise_metrics.cpp:51-56,112-122 with the prf_div
+ * backward of csrc/ops/cpu/prf_div_kernel.cpp:258-277, the clamp mask of
+ * derivatives.yaml (grad where min <= x <= max) and torch's 2-norm backward (0 where the
+ * norm is 0).  `norms1`/`norms2` are the fp32 row norms of x1/x2.  With `similarity` != 0
+ * the op is cosine_similarity (no 1 - s, no clip).  When x2 is x1 (x2=None upstream),
+ * the caller adds the two halves. */
+int tpw_cosine_backward(const void *grad, const void *x1, const void *x2,
+                        const float *norms1, const float *norms2, int dtype,
+                        int64_t batch, int64_t n, int64_t m, int64_t d, int similarity,
+                        void *grad_x1, void *grad_x2, void *workspace, void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* Directed Hausdorff                                                         */
+/* ------------------------------------------------------------------------- */
+
+/* Workspace (bytes) for tpw_directed_hausdorff with these sizes. */
+size_t tpw_hausdorff_workspace_size(int64_t batch, int64_t b1, int64_t p1, int64_t b2,
+                                    int64_t p2, int64_t d);
+
+/* out[b,i,j] = sqrt(max_m min_n |x1[b,i,m,:] - x2[b,j,n,:]|^2), x1 [batch,b1,p1,d],
+ * x2 [batch,b2,p2,d] fp32, with the reference's indices: idx1 = the last m (in
+ * iteration order) reaching the maximum, idx2 = the first n reaching that m's
+ * minimum.  Squared distances are summed k = 0..d-1 in fp32 without contraction,
+ * as the reference CPU loop does.  perm1 [batch,p1] / perm2 [batch,p2] give the
+ * iteration order (shuffle=True) or are NULL for natural order; reported indices
+ * are the permuted values.  The full p1 x p2 distance matrix is never formed.
+ * Replaces _directed_hausdorff_forward_kernel
+ * (csrc/ops/cpu/hausdorff_kernel.cpp:12-185; CUDA csrc/ops/cuda/hausdorff_kernel.cu:17-195). */
+int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t batch, int64_t b1,
+                           int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                           const int64_t *perm1, const int64_t *perm2, float *out,
+                           int64_t *idx1, int64_t *idx2, void *workspace, void *stream);
+
+/* grad_x1[b,i,idx1,k] += grad * (x1[idx1,k] - x2[idx2,k]) / out summed over j in
+ * order; grad_x2[b,j,idx2,k] += grad * (x2[idx2,k] - x1[idx1,k]) / out summed over
+ * i in order.  grad_x1/grad_x2 must be zero-filled by the caller.
+ * Replaces the scatter half of _directed_hausdorff_backward_kernel
+ * (csrc/ops/cpu/hausdorff_kernel.cpp:187-235,308-336;
+ *  CUDA csrc/ops/cuda/hausdorff_kernel.cu:199-246). */
+int tpw_directed_hausdorff_backward(const float *grad, const float *x1, const float *x2,
+                                    const float *out, const int64_t *idx1,
+                                    const int64_t *idx2, int64_t batch, int64_t b1,
+                                    int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                    float *grad_x1, float *grad_x2, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORCHPAIRWISE_AMD_H_ */

@@ -1,0 +1,35 @@
+"""CPU oracle for the torchpairwise hot path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may
+import this package, and only as the checker (or the timed CPU baseline), never as the
+product path: the product (``torchpairwise_amd``) fails loudly when its HIP library is
+missing and never routes through here.
+
+Contents (each function cites the reference file:line it restates):
+
+* ``oracle.pairwise`` — numpy / torch restatements:
+  - boolean metrics (hamming, jaccard, pw*_sum / pw*_mean) as integer popcounts followed by
+    the reference's float32 arithmetic (bit-exact);
+  - the ATen-routed metrics (euclidean, manhattan, minkowski, chebyshev) as ``torch.cdist``
+    + autograd on CPU, which *is* the reference's arithmetic (pairwise_metrics.cpp:24-49,
+    160-168,299-306 call at::cdist);
+  - cosine as the reference's torch-op composite with prf_div "identity";
+  - directed Hausdorff as an fp32 brute force with per-operation rounding (no FMA) and the
+    reference's tie rules, plus its backward scatter.
+* ``oracle/cref.c`` (built by ``oracle/Makefile`` into ``oracle/_build/liboracle_cref.so``,
+  wrapped by ``oracle.cref``) — a C restatement of the reference's CPU loops: the
+  sequential early-break Hausdorff loop and the one-output-per-iteration binary
+  reduction, compiled with -ffp-contract=off like the reference's x86-64 build.  It pins
+  the numpy brute force (same bits through a different algorithm) and is the timed CPU
+  baseline ("port") in bench.py.
+
+Pinning (what checks each function; see tests/test_oracle.py):
+  hamming / jaccard / pw* : scipy.spatial.distance.cdist (float64 then float32 — double
+      rounding of a quotient of integers < 2^24 is innocuous), closed forms (d a power of
+      two gives exact dyadics, all-zero rows give jaccard 0), brute force per element, the
+      C restatement, committed golden vectors.
+  cdist-routed metrics    : scipy.spatial.distance.cdist in float64, autograd.gradcheck.
+  cosine                  : sklearn.metrics.pairwise.cosine_distances, gradcheck in float64.
+  directed Hausdorff      : the C early-break restatement (bit-exact value and indices),
+      scipy.spatial.distance.directed_hausdorff (value), hand-built tie cases, gradcheck.
+"""

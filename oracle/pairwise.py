@@ -1,0 +1,240 @@
+"""numpy / torch (CPU) restatements of the reference's hot-path arithmetic.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Citations point into
+/root/reference (inspiros/torchpairwise v0.3.0) unless prefixed with "torch/".
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+F32_EXACT = np.int64(1 << 24)  # a float accumulator of ones stops growing here
+
+BIT_OPS = ("and", "or", "xor", "eq", "ne")
+
+
+def _as3(x: np.ndarray) -> np.ndarray:
+    return x if x.ndim == 3 else x[None]
+
+
+def _pack_u64(x: np.ndarray) -> np.ndarray:
+    """bool [..., d] -> uint64 words [..., ceil(d/64)] (zero padding)."""
+    d = x.shape[-1]
+    nbytes = (d + 7) // 8
+    packed = np.packbits(x.astype(np.uint8), axis=-1, bitorder="little")
+    pad = (-nbytes) % 8
+    if pad:
+        packed = np.concatenate([packed, np.zeros(packed.shape[:-1] + (pad,), np.uint8)], -1)
+    return np.ascontiguousarray(packed).view(np.uint64)
+
+
+def bool_counts(x1: np.ndarray, x2: np.ndarray, op: str, row_block: int = 256) -> np.ndarray:
+    """Exact integer count over k of op(x1[b,i,k], x2[b,j,k]) for bool inputs.
+
+    Restates the per-output loop of pairwise_binary_reduction_forward_kernel_impl
+    (csrc/ops/cpu/pairwise_binary_kernels.cpp:28-49) with the binary ops of
+    common/binary_ops.h (and/or/xor/eq/ne on bool), as integer popcounts.
+    """
+    a, b = _as3(np.asarray(x1, bool)), _as3(np.asarray(x2, bool))
+    d = a.shape[-1]
+    pa, pb = _pack_u64(a), _pack_u64(b)
+    B, n, m = a.shape[0], a.shape[1], b.shape[1]
+    out = np.empty((B, n, m), np.int64)
+    base = {"and": np.bitwise_and, "or": np.bitwise_or, "xor": np.bitwise_xor,
+            "eq": np.bitwise_xor, "ne": np.bitwise_xor}[op]
+    for bb in range(B):
+        for i0 in range(0, n, row_block):
+            w = base(pa[bb, i0:i0 + row_block, None, :], pb[bb, None, :, :])
+            c = np.bitwise_count(w).sum(-1, dtype=np.int64)
+            out[bb, i0:i0 + row_block] = d - c if op == "eq" else c
+    return out if np.ndim(x1) == 3 else out[0]
+
+
+def float_accumulated(count: np.ndarray) -> np.ndarray:
+    """The reference's float32 accumulator of 1.0f per hit: exact below 2^24, then stuck
+    at 2^24 (round-to-nearest-even of 2^24 + 1)."""
+    return np.minimum(count, F32_EXACT).astype(np.float32)
+
+
+def pw_reduce_bool(x1, x2, op: str, reduction: str) -> np.ndarray:
+    """pw{op}_{sum,mean} on bool inputs (csrc/ops/pairwise_binary.cpp:135-160;
+    sum/mean accumulate in float, Mean divides by float(d):
+    csrc/ops/cpu/pairwise_binary_kernels.cpp:40-47, output float32 :146-151)."""
+    c = float_accumulated(bool_counts(x1, x2, op))
+    if reduction == "sum":
+        return c
+    d = np.asarray(x1).shape[-1]
+    return (c / np.float32(d)).astype(np.float32)
+
+
+def hamming_distances(x1, x2=None) -> np.ndarray:
+    """hamming_distances = pwne_mean (csrc/ops/pairwise_metrics.cpp:206-213).  Bool inputs
+    use popcounts; other dtypes compare elementwise with != (no bool coercion)."""
+    x2 = x1 if x2 is None else x2
+    x1, x2 = np.asarray(x1), np.asarray(x2)
+    if x1.dtype == bool and x2.dtype == bool:
+        return pw_reduce_bool(x1, x2, "ne", "mean")
+    a, b = _as3(x1), _as3(x2)
+    cnt = np.stack([(a[bb][:, None, :] != b[bb][None, :, :]).sum(-1) for bb in range(a.shape[0])])
+    res = (float_accumulated(cnt) / np.float32(a.shape[-1])).astype(np.float32)
+    return res if x1.ndim == 3 else res[0]
+
+
+def jaccard_distances(x1, x2=None) -> np.ndarray:
+    """prf_div(pwxor_sum, pwor_sum, "zero") on bool-coerced inputs
+    (csrc/ops/pairwise_metrics.cpp:215-222, pairwise_metrics.h:50-55 coercion,
+    csrc/ops/cpu/prf_divide.h:10-11 zero mode)."""
+    x2 = x1 if x2 is None else x2
+    a, b = np.asarray(x1).astype(bool), np.asarray(x2).astype(bool)
+    x = float_accumulated(bool_counts(a, b, "xor"))
+    o = float_accumulated(bool_counts(a, b, "or"))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = (x / np.where(o == 0, np.float32(1), o)).astype(np.float32)
+    return np.where(o == 0, np.float32(0), q).astype(np.float32)
+
+
+# -------------------------------------------------------------------------------------
+# ATen-routed metrics: the reference calls at::cdist, so torch.cdist on CPU is its
+# arithmetic (csrc/ops/pairwise_metrics.cpp:24-31 euclidean p=2, :42-49 manhattan p=1,
+# :160-168 minkowski p, :299-306 chebyshev p=inf).
+# -------------------------------------------------------------------------------------
+def cdist_reference(x1: torch.Tensor, x2: torch.Tensor | None, p: float) -> torch.Tensor:
+    x1c = x1.detach().cpu().requires_grad_(x1.requires_grad) if x1.is_cuda else x1
+    x2 = x1 if x2 is None else x2
+    return torch.cdist(x1c, x2, p)
+
+
+class _PrfDivIdentity(torch.autograd.Function):
+    """prf_div(x, y, "identity"): y != 0 ? x / y : x (csrc/ops/cpu/prf_divide.h:12-13);
+    backward: g/y and (g/y) * -x / y where y != 0, else g and 0
+    (csrc/ops/cpu/prf_div_kernel.cpp:258-277)."""
+
+    @staticmethod
+    def forward(ctx, x, y):
+        ctx.save_for_backward(x, y)
+        nz = y != 0
+        return torch.where(nz, x / torch.where(nz, y, torch.ones_like(y)), x)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, y = ctx.saved_tensors
+        nz = y != 0
+        ysafe = torch.where(nz, y, torch.ones_like(y))
+        gs = g / ysafe
+        gx = torch.where(nz, gs, g)
+        gy = torch.where(nz, gs * -x / ysafe, torch.zeros_like(g))
+        return gx, gy
+
+
+def prf_div_identity(x, y):
+    return _PrfDivIdentity.apply(x, y)
+
+
+def cosine_similarity(x1: torch.Tensor, x2: torch.Tensor | None = None) -> torch.Tensor:
+    """csrc/ops/pairwise_metrics.cpp:112-122: prf_div(x1 @ x2^T, |x1| |x2|^T, identity);
+    with x2=None the second operand and norm alias the first."""
+    x2_ = x1 if x2 is None else x2
+    n1 = x1.norm(2, -1, keepdim=True)
+    n2 = n1 if x2 is None else x2_.norm(2, -1, keepdim=True)
+    denom = n1.mul(n2.transpose(-1, -2))
+    return prf_div_identity(x1.matmul(x2_.transpose(-1, -2)), denom)
+
+
+def cosine_distances(x1: torch.Tensor, x2: torch.Tensor | None = None) -> torch.Tensor:
+    """csrc/ops/pairwise_metrics.cpp:51-56: cosine_similarity.neg_().add_(1).clip_(0, 2)."""
+    return (1 - cosine_similarity(x1, x2)).clip(0, 2)
+
+
+# -------------------------------------------------------------------------------------
+# directed Hausdorff
+# -------------------------------------------------------------------------------------
+def _as4(x):
+    return x if x.ndim == 4 else x[None]
+
+
+def hausdorff_sqdist_matrix(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """d[m, n] = sum_k (a[m,k] - b[n,k])^2 accumulated k = 0..d-1 in float32 with one
+    rounding per operation (no fused multiply-add), as the reference's loop computes it
+    (csrc/ops/cpu/hausdorff_kernel.cpp:29-33)."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    d = np.zeros((a.shape[0], b.shape[0]), np.float32)
+    for k in range(a.shape[1]):
+        diff = (a[:, None, k] - b[None, :, k]).astype(np.float32)
+        d = (d + (diff * diff).astype(np.float32)).astype(np.float32)
+    return d
+
+
+def directed_hausdorff(x1: np.ndarray, x2: np.ndarray, perm1=None, perm2=None):
+    """Brute-force restatement of _directed_hausdorff_forward_kernel_impl
+    (csrc/ops/cpu/hausdorff_kernel.cpp:12-53; shuffled :55-100): value sqrt(max_m min_n d),
+    x1 index = last m in iteration order whose min equals the max, x2 index = first n in
+    iteration order reaching that min; with perms, iteration order m_ -> perm[b][m_] and
+    the reported indices are the permuted values.  Inputs [(B,) b1, p1, d] / [(B,) b2, p2, d]
+    float32; perms [B, p] int64 or None."""
+    a4, b4 = _as4(np.asarray(x1, np.float32)), _as4(np.asarray(x2, np.float32))
+    B, b1, p1, _ = a4.shape
+    b2, p2 = b4.shape[1], b4.shape[2]
+    out = np.zeros((B, b1, b2), np.float32)
+    i1 = np.zeros((B, b1, b2), np.int64)
+    i2 = np.zeros((B, b1, b2), np.int64)
+    for bb in range(B):
+        o1 = np.arange(p1) if perm1 is None else np.asarray(perm1)[bb]
+        o2 = np.arange(p2) if perm2 is None else np.asarray(perm2)[bb]
+        for i in range(b1):
+            for j in range(b2):
+                if p1 == 0 or p2 == 0:
+                    continue
+                dmat = hausdorff_sqdist_matrix(a4[bb, i][o1], b4[bb, j][o2])
+                mins = dmat.min(1)
+                h = mins.max()
+                mpos = int(np.nonzero(mins == h)[0][-1])
+                npos = int(np.nonzero(dmat[mpos] == mins[mpos])[0][0])
+                out[bb, i, j] = np.sqrt(h, dtype=np.float32)
+                i1[bb, i, j] = o1[mpos]
+                i2[bb, i, j] = o2[npos]
+    if np.ndim(x1) == 3:
+        return out[0], i1[0], i2[0]
+    return out, i1, i2
+
+
+def directed_hausdorff_backward(grad, x1, x2, out, idx1, idx2):
+    """Scatter of _directed_hausdorff_backward_x1/x2_kernel_impl
+    (csrc/ops/cpu/hausdorff_kernel.cpp:187-235): grad_x1[b,i,m*,k] += g * diff / out
+    summed over j in order (and grad_x2 over i in order), float32 throughout."""
+    a4, b4 = _as4(np.asarray(x1, np.float32)), _as4(np.asarray(x2, np.float32))
+    B, b1, p1, d = a4.shape
+    b2 = b4.shape[1]
+    g = np.asarray(grad, np.float32).reshape(B, b1, b2)
+    o = np.asarray(out, np.float32).reshape(B, b1, b2)
+    m_ = np.asarray(idx1).reshape(B, b1, b2)
+    n_ = np.asarray(idx2).reshape(B, b1, b2)
+    gx1 = np.zeros_like(a4)
+    gx2 = np.zeros_like(b4)
+    for bb in range(B):
+        for i in range(b1):
+            for j in range(b2):
+                m, n = m_[bb, i, j], n_[bb, i, j]
+                diff = (a4[bb, i, m] - b4[bb, j, n]).astype(np.float32)
+                v = ((g[bb, i, j] * diff).astype(np.float32) / o[bb, i, j]).astype(np.float32)
+                gx1[bb, i, m] = (gx1[bb, i, m] + v).astype(np.float32)
+        for j in range(b2):
+            for i in range(b1):
+                m, n = m_[bb, i, j], n_[bb, i, j]
+                diff = (b4[bb, j, n] - a4[bb, i, m]).astype(np.float32)
+                v = ((g[bb, i, j] * diff).astype(np.float32) / o[bb, i, j]).astype(np.float32)
+                gx2[bb, j, n] = (gx2[bb, j, n] + v).astype(np.float32)
+    if np.ndim(x1) == 3:
+        return gx1[0], gx2[0]
+    return gx1, gx2
+
+
+def hausdorff_permutations(batch: int, p1: int, p2: int, generator: torch.Generator):
+    """Permutations drawn as the reference draws them: per batch, x1's then x2's, with
+    at::randperm_outf(P, generator) (csrc/ops/cpu/hausdorff_kernel.cpp:149-158)."""
+    perm1 = torch.empty((batch, p1), dtype=torch.int64)
+    perm2 = torch.empty((batch, p2), dtype=torch.int64)
+    for b in range(batch):
+        perm1[b] = torch.randperm(p1, generator=generator)
+        perm2[b] = torch.randperm(p2, generator=generator)
+    return perm1, perm2

@@ -1,0 +1,47 @@
+"""Shared helpers of the test-suite (tolerance checks, seeded inputs)."""
+from __future__ import annotations
+
+import torch
+
+
+def gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(*shape, seed: int, dtype=torch.float32):
+    return torch.randn(*shape, generator=gen(seed), dtype=torch.float32).to(dtype)
+
+
+def rand(*shape, seed: int):
+    return torch.rand(*shape, generator=gen(seed), dtype=torch.float32)
+
+
+def assert_close(actual, expected, *, rtol: float, atol: float, what: str = ""):
+    """|actual - expected| <= atol + rtol * |expected| elementwise (both moved to CPU
+    float64); the message names the worst element."""
+    a = torch.as_tensor(actual).detach().cpu().double()
+    e = torch.as_tensor(expected).detach().cpu().double()
+    assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
+    diff = (a - e).abs()
+    tol = atol + rtol * e.abs()
+    bad = ~(diff <= tol)
+    if bad.any():
+        idx = int(torch.argmax((diff - tol).flatten()))
+        raise AssertionError(
+            f"{what}: {int(bad.sum())}/{bad.numel()} elements beyond rtol={rtol} atol={atol}; "
+            f"worst at flat {idx}: got {a.flatten()[idx].item()!r} want {e.flatten()[idx].item()!r}")
+
+
+def assert_equal(actual, expected, what: str = ""):
+    a = torch.as_tensor(actual).detach().cpu()
+    e = torch.as_tensor(expected).detach().cpu()
+    assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
+    if a.dtype.is_floating_point:
+        same = (a.view(torch.int32 if a.dtype == torch.float32 else torch.int64) ==
+                e.to(a.dtype).view(torch.int32 if a.dtype == torch.float32 else torch.int64))
+    else:
+        same = a == e
+    if not bool(same.all()):
+        idx = int(torch.nonzero(~same.flatten())[0])
+        raise AssertionError(f"{what}: {int((~same).sum())}/{same.numel()} differ; first at flat {idx}: "
+                             f"got {a.flatten()[idx].item()!r} want {e.flatten()[idx].item()!r}")

@@ -1,0 +1,269 @@
+"""GPU parity of every C-ABI entry point against the CPU oracle (same seeded inputs).
+
+Bars: bit-exact for the boolean metrics and for the Hausdorff value, indices and
+gradients; floating-point values and gradients within the tolerance stated per test
+(fp32: rtol 1e-5 plus an absolute floor scaled to the data; bf16: rtol 1e-2 normwise).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cref
+from oracle import pairwise as P
+from tests._util import assert_close, assert_equal, rand, randn
+from torchpairwise_amd import _capi as capi
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+# --------------------------------------------------------------------------------------
+# boolean family: bit-exact
+# --------------------------------------------------------------------------------------
+BOOL_SHAPES = [
+    (1, 1, 1, 1),
+    (1, 5, 7, 33),
+    (1, 130, 257, 128),
+    (3, 64, 200, 1000),
+    (2, 129, 127, 31),
+    (1, 300, 301, 4096 + 17),
+]
+
+
+@pytest.mark.parametrize("B,n,m,d", BOOL_SHAPES)
+@pytest.mark.parametrize("op", ["and", "or", "xor", "eq", "ne"])
+def test_bool_reduce_bit_exact(B, n, m, d, op):
+    x1 = rand(B, n, d, seed=0) < 0.5
+    x2 = rand(B, m, d, seed=1) < 0.3
+    code = {"and": capi.BIT_AND, "or": capi.BIT_OR, "xor": capi.BIT_XOR, "eq": capi.BIT_EQ,
+            "ne": capi.BIT_NE}[op]
+    for red, name in ((capi.RED_SUM, "sum"), (capi.RED_MEAN, "mean")):
+        got = capi.bool_pairwise_reduce(x1.to(DEV), x2.to(DEV), code, red)
+        want = P.pw_reduce_bool(x1.numpy(), x2.numpy(), op, name)
+        assert_equal(got, torch.from_numpy(want), f"pw{op}_{name} {B}x{n}x{m}x{d}")
+
+
+@pytest.mark.parametrize("B,n,m,d", BOOL_SHAPES)
+def test_hamming_matches_c_restatement(B, n, m, d):
+    x1 = rand(B, n, d, seed=3) < 0.5
+    x2 = rand(B, m, d, seed=4) < 0.5
+    got = capi.bool_pairwise_reduce(x1.to(DEV), x2.to(DEV), capi.BIT_NE, capi.RED_MEAN)
+    want = cref.bool_reduce(x1.numpy(), x2.numpy(), "ne", True, threads=8)
+    assert_equal(got, torch.from_numpy(want), "hamming vs C loop")
+
+
+@pytest.mark.parametrize("B,n,m,d", BOOL_SHAPES)
+def test_jaccard_bit_exact(B, n, m, d):
+    x1 = rand(B, n, d, seed=5) < 0.1
+    x2 = rand(B, m, d, seed=6) < 0.1
+    x1[..., : max(1, n // 7), :] = False  # all-zero rows: or == 0 gives 0
+    x2[..., : max(1, m // 5), :] = False
+    got = capi.jaccard_bool(x1.to(DEV), x2.to(DEV))
+    want = P.jaccard_distances(x1.numpy(), x2.numpy())
+    assert_equal(got, torch.from_numpy(want), f"jaccard {B}x{n}x{m}x{d}")
+    want_c = cref.jaccard(x1.numpy(), x2.numpy(), threads=8)
+    assert_equal(got, torch.from_numpy(want_c), "jaccard vs C passes")
+
+
+def test_bool_empty_sizes():
+    x1 = torch.zeros((0, 16), dtype=torch.bool, device=DEV)
+    x2 = torch.zeros((5, 16), dtype=torch.bool, device=DEV)
+    out = capi.bool_pairwise_reduce(x1, x2, capi.BIT_NE, capi.RED_MEAN)
+    assert out.shape == (0, 5)
+
+
+# --------------------------------------------------------------------------------------
+# inner-product family (MFMA)
+# --------------------------------------------------------------------------------------
+INNER_SHAPES = [(1, 40, 33, 64), (1, 300, 257, 128), (2, 129, 190, 256), (1, 64, 64, 3),
+                (1, 50, 70, 1000)]
+
+
+@pytest.mark.parametrize("B,n,m,d", INNER_SHAPES)
+def test_dot_fp32(B, n, m, d):
+    x1, x2 = randn(B, n, d, seed=0), randn(B, m, d, seed=1)
+    got = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_DOT)
+    want = torch.matmul(x1.double(), x2.double().transpose(-1, -2))
+    assert_close(got, want, rtol=1e-5, atol=1e-5 * float(want.abs().max()), what="dot fp32")
+
+
+@pytest.mark.parametrize("B,n,m,d", INNER_SHAPES)
+def test_euclidean_fp32(B, n, m, d):
+    x1, x2 = randn(B, n, d, seed=0), randn(B, m, d, seed=1)
+    got = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_EUCLIDEAN)
+    want = torch.cdist(x1, x2, 2)  # the reference's at::cdist on CPU
+    assert_close(got, want, rtol=1e-5, atol=1e-5 * float(want.abs().max()), what="euclidean fp32")
+
+
+def test_euclidean_self_distance_fp32():
+    x = randn(1, 200, 128, seed=7)
+    got = capi.pairwise_inner(x.to(DEV), x.to(DEV), capi.EPI_EUCLIDEAN)
+    want = torch.cdist(x.double(), x.double(), 2)
+    # the |a|^2 + |b|^2 - 2ab expansion (used by at::cdist too) cancels on the diagonal:
+    # absolute error ~ sqrt(eps * 2|x|^2) there
+    floor = 4 * float(np.sqrt(np.finfo(np.float32).eps * 2 * float((x * x).sum(-1).max())))
+    assert_close(got, want, rtol=1e-5, atol=floor, what="euclidean self")
+
+
+@pytest.mark.parametrize("B,n,m,d", INNER_SHAPES)
+def test_cosine_fp32(B, n, m, d):
+    x1, x2 = randn(B, n, d, seed=0), randn(B, m, d, seed=1)
+    x1[0, 0].zero_()  # zero norm: prf_div identity branch
+    got = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_COSINE_DIST)
+    want = P.cosine_distances(x1.double(), x2.double())
+    assert_close(got, want, rtol=1e-5, atol=2e-6, what="cosine fp32")
+    got_s = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_COSINE_SIM)
+    want_s = P.cosine_similarity(x1.double(), x2.double())
+    assert_close(got_s, want_s, rtol=1e-5, atol=2e-6, what="cosine similarity fp32")
+
+
+@pytest.mark.parametrize("B,n,m,d", [(1, 300, 257, 128), (2, 129, 190, 256), (1, 33, 65, 100)])
+def test_inner_bf16(B, n, m, d):
+    x1 = randn(B, n, d, seed=0, dtype=torch.bfloat16)
+    x2 = randn(B, m, d, seed=1, dtype=torch.bfloat16)
+    for epi, ref in ((capi.EPI_EUCLIDEAN, lambda a, b: torch.cdist(a, b, 2)),
+                     (capi.EPI_COSINE_DIST, P.cosine_distances)):
+        got = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), epi)
+        assert got.dtype == torch.bfloat16
+        want = ref(x1.double(), x2.double())
+        # bf16 output: one bf16 rounding (2^-9 relative) of an fp32-accumulated result
+        assert_close(got.float(), want, rtol=1e-2, atol=1e-2 * float(want.abs().max()),
+                     what=f"bf16 epilogue {epi}")
+
+
+# --------------------------------------------------------------------------------------
+# VALU Lp family
+# --------------------------------------------------------------------------------------
+LP_PS = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.5, float("inf")]
+
+
+@pytest.mark.parametrize("p", LP_PS)
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 257, 128), (2, 33, 64, 7), (1, 5, 300, 65)])
+def test_lp_forward(p, B, n, m, d):
+    x1 = rand(B, n, d, seed=0) * 2 - 1
+    x2 = rand(B, m, d, seed=1) * 2 - 1
+    if p == 0.0:
+        x2[:, :, : d // 2] = x1[:, : 1, : d // 2]  # some exact zeros
+    got = capi.lp_distances(x1.to(DEV), x2.to(DEV), p)
+    want = torch.cdist(x1.double(), x2.double(), p)
+    if p == 0.0:
+        want = torch.cdist(x1, x2, p)  # counts: exact
+        assert_equal(got, want, "p=0 counts")
+        return
+    assert_close(got, want, rtol=1e-5, atol=1e-6 * float(want.abs().max()), what=f"lp p={p}")
+
+
+@pytest.mark.parametrize("p", [1.0, 1.5, 2.0, 3.0, 4.5, float("inf")])
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 40, 33, 5)])
+def test_lp_backward(p, B, n, m, d):
+    x1 = (rand(B, n, d, seed=0) * 2 - 1).double().requires_grad_()
+    x2 = (rand(B, m, d, seed=1) * 2 - 1).double().requires_grad_()
+    g = randn(B, n, m, seed=2).double()
+    dist = torch.cdist(x1, x2, p)
+    gx1_ref, gx2_ref = torch.autograd.grad(dist, (x1, x2), g)
+    dist32 = capi.lp_distances(x1.detach().float().to(DEV), x2.detach().float().to(DEV), p)
+    gx1, gx2 = capi.lp_distances_backward(g.float().to(DEV), x1.detach().float().to(DEV),
+                                          x2.detach().float().to(DEV), dist32, p)
+    for got, want, nm in ((gx1, gx1_ref, "grad_x1"), (gx2, gx2_ref, "grad_x2")):
+        # sums over up to 200 signed terms: normwise floor 1e-5 * max|grad|
+        assert_close(got, want, rtol=1e-4, atol=1e-5 * float(want.abs().max()) + 1e-6,
+                     what=f"lp p={p} {nm}")
+
+
+# --------------------------------------------------------------------------------------
+# inner-product backward
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 64, 33, 256), (1, 300, 290, 128)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_euclidean_backward(B, n, m, d, dtype):
+    x1 = randn(B, n, d, seed=0, dtype=dtype)
+    x2 = randn(B, m, d, seed=1, dtype=dtype)
+    g = randn(B, n, m, seed=2, dtype=dtype)
+    a = x1.double().requires_grad_()
+    b = x2.double().requires_grad_()
+    res = torch.cdist(a, b, 2)
+    gx1_ref, gx2_ref = torch.autograd.grad(res, (a, b), g.double())
+    res_dev = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_EUCLIDEAN)
+    gx1, gx2 = capi.euclidean_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), res_dev)
+    rtol = 1e-4 if dtype == torch.float32 else 2e-2
+    for got, want, nm in ((gx1, gx1_ref, "grad_x1"), (gx2, gx2_ref, "grad_x2")):
+        assert_close(got.float(), want, rtol=rtol, atol=rtol * float(want.abs().max()),
+                     what=f"euclidean {dtype} {nm}")
+
+
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 64, 33, 256)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("similarity", [False, True])
+def test_cosine_backward(B, n, m, d, dtype, similarity):
+    x1 = randn(B, n, d, seed=0, dtype=dtype)
+    x2 = randn(B, m, d, seed=1, dtype=dtype)
+    g = randn(B, n, m, seed=2, dtype=dtype)
+    a = x1.double().requires_grad_()
+    b = x2.double().requires_grad_()
+    f = P.cosine_similarity if similarity else P.cosine_distances
+    gx1_ref, gx2_ref = torch.autograd.grad(f(a, b), (a, b), g.double())
+    gx1, gx2 = capi.cosine_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), similarity=similarity)
+    rtol = 1e-4 if dtype == torch.float32 else 2e-2
+    for got, want, nm in ((gx1, gx1_ref, "grad_x1"), (gx2, gx2_ref, "grad_x2")):
+        assert_close(got.float(), want, rtol=rtol, atol=rtol * float(want.abs().max()),
+                     what=f"cosine sim={similarity} {dtype} {nm}")
+
+
+# --------------------------------------------------------------------------------------
+# directed Hausdorff: bit-exact value, indices and gradients
+# --------------------------------------------------------------------------------------
+HD_SHAPES = [(None, 2, 300, 3, 400, 3), (2, 2, 257, 3, 129, 3), (None, 3, 100, 2, 700, 2),
+             (None, 2, 150, 3, 90, 5), (None, 1, 1, 1, 1, 3), (None, 2, 2100, 2, 3000, 3)]
+
+
+def _hd_inputs(batch, b1, p1, b2, p2, d, seed=0):
+    s1 = (b1, p1, d) if batch is None else (batch, b1, p1, d)
+    s2 = (b2, p2, d) if batch is None else (batch, b2, p2, d)
+    return rand(*s1, seed=seed), rand(*s2, seed=seed + 1) + 0.05
+
+
+@pytest.mark.parametrize("shape", HD_SHAPES)
+def test_hausdorff_forward_bit_exact(shape):
+    x1, x2 = _hd_inputs(*shape)
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV))
+    w_out, w_i1, w_i2 = cref.directed_hausdorff(x1.numpy(), x2.numpy(), threads=8)
+    assert_equal(out, torch.from_numpy(w_out), "hausdorff value")
+    assert_equal(i1, torch.from_numpy(w_i1), "hausdorff x1 index")
+    assert_equal(i2, torch.from_numpy(w_i2), "hausdorff x2 index")
+
+
+def test_hausdorff_shuffled_bit_exact():
+    x1, x2 = _hd_inputs(2, 2, 300, 3, 400, 3)
+    perm1, perm2 = P.hausdorff_permutations(2, 300, 400, torch.Generator().manual_seed(5))
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV), perm1.to(DEV), perm2.to(DEV))
+    w = cref.directed_hausdorff(x1.numpy(), x2.numpy(), perm1.numpy(), perm2.numpy(), threads=8)
+    for got, want, nm in zip((out, i1, i2), w, ("value", "idx1", "idx2")):
+        assert_equal(got, torch.from_numpy(want), f"shuffled {nm}")
+
+
+def test_hausdorff_ties_bit_exact():
+    # integer grid points: many equal distances, so the tie rules decide the indices
+    g = torch.Generator().manual_seed(11)
+    x1 = torch.randint(0, 4, (3, 200, 3), generator=g).float()
+    x2 = torch.randint(0, 4, (2, 150, 3), generator=g).float()
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV))
+    w = cref.directed_hausdorff(x1.numpy(), x2.numpy(), threads=8)
+    for got, want, nm in zip((out, i1, i2), w, ("value", "idx1", "idx2")):
+        assert_equal(got, torch.from_numpy(want), f"ties {nm}")
+    # identical clouds: value 0, last m, first n
+    out, i1, i2 = capi.directed_hausdorff(x1[:1].to(DEV), x1[:1].to(DEV))
+    w = cref.directed_hausdorff(x1[:1].numpy(), x1[:1].numpy(), threads=1)
+    for got, want, nm in zip((out, i1, i2), w, ("value", "idx1", "idx2")):
+        assert_equal(got, torch.from_numpy(want), f"self {nm}")
+
+
+@pytest.mark.parametrize("shape", HD_SHAPES[:4])
+def test_hausdorff_backward_bit_exact(shape):
+    x1, x2 = _hd_inputs(*shape)
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV))
+    g = randn(*out.shape, seed=9)
+    gx1, gx2 = capi.directed_hausdorff_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), out, i1, i2)
+    w1, w2 = P.directed_hausdorff_backward(g.numpy(), x1.numpy(), x2.numpy(), out.cpu().numpy(),
+                                           i1.cpu().numpy(), i2.cpu().numpy())
+    assert_equal(gx1, torch.from_numpy(w1), "hausdorff grad_x1")
+    assert_equal(gx2, torch.from_numpy(w2), "hausdorff grad_x2")

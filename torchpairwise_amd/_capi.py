@@ -1,0 +1,283 @@
+"""ctypes binding of the C ABI in ``include/torchpairwise_amd.h``.
+
+This is a second host of the kernel library next to the PyTorch extension: the GPU
+parity tests and the benchmark drive the kernels through it with raw device pointers
+(``tensor.data_ptr()``) and the current HIP stream, exactly as a non-Python caller
+would.  Every call raises ``RuntimeError`` with ``tpw_last_error()`` on failure.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = _PKG / "libtorchpairwise_hip.so"
+HEADER = _PKG.parent / "include" / "torchpairwise_amd.h"
+
+TPW_F32, TPW_BF16 = 0, 1
+BIT_AND, BIT_OR, BIT_XOR, BIT_EQ, BIT_NE = 0, 1, 2, 3, 4
+RED_SUM, RED_MEAN = 0, 1
+EPI_DOT, EPI_EUCLIDEAN, EPI_SQEUCLIDEAN, EPI_COSINE_SIM, EPI_COSINE_DIST = 0, 1, 2, 3, 4
+
+_i64, _p, _i, _d, _sz = C.c_int64, C.c_void_p, C.c_int, C.c_double, C.c_size_t
+
+_SIGNATURES = {
+    "tpw_last_error": (C.c_char_p, []),
+    "tpw_runtime_version": (_i, []),
+    "tpw_packed_words": (_i64, [_i64]),
+    "tpw_pack_bool_rows": (_i, [_p, _i64, _i64, _p, _p, _p]),
+    "tpw_bool_pairwise_reduce": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
+    "tpw_jaccard_bool": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "tpw_row_norms": (_i, [_p, _i, _i64, _i64, _i, _p, _p]),
+    "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),
+    "tpw_lp_distances": (_i, [_p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
+    "tpw_lp_backward_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "tpw_lp_distances_backward": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _i, _p, _p, _p]),
+    "tpw_inner_backward_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "tpw_euclidean_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "tpw_cosine_backward": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p]),
+    "tpw_hausdorff_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "tpw_directed_hausdorff": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
+    "tpw_directed_hausdorff_backward": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),
+}
+
+_lib = None
+
+
+def header_symbols(header: Path = HEADER) -> list[str]:
+    """Function names declared in the public header."""
+    text = header.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tpw_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built; run torchpairwise_amd._build")
+        l = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"torchpairwise_amd C ABI error {rc}: {lib().tpw_last_error().decode()}")
+
+
+def call(name: str, *args) -> int:
+    rc = getattr(lib(), name)(*args)
+    check(rc)
+    return rc
+
+
+# --------------------------------------------------------------------------------------
+# torch-tensor conveniences (device tensors only; nothing here falls back to the CPU)
+# --------------------------------------------------------------------------------------
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream():
+    import torch
+
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dtype_code(t):
+    import torch
+
+    if t.dtype == torch.float32:
+        return TPW_F32
+    if t.dtype == torch.bfloat16:
+        return TPW_BF16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _as3(x):
+    return x if x.dim() == 3 else x.unsqueeze(0)
+
+
+def pack_bool(x):
+    """x: bool [..., rows, d] cuda -> (words int32 [rows_total, W], popcounts int32)."""
+    import torch
+
+    assert x.is_cuda and x.dtype == torch.bool
+    d = x.shape[-1]
+    rows = x.numel() // d if d else 0
+    W = lib().tpw_packed_words(d)
+    words = torch.empty((rows, W), dtype=torch.int32, device=x.device)
+    pops = torch.empty((rows,), dtype=torch.int32, device=x.device)
+    call("tpw_pack_bool_rows", _ptr(x.contiguous()), rows, d, _ptr(words), _ptr(pops), _stream())
+    return words, pops
+
+
+def bool_pairwise_reduce(x1, x2, op, reduction):
+    import torch
+
+    a, b = _as3(x1), _as3(x2)
+    B, n, d = a.shape
+    m = b.shape[1]
+    wa, _ = pack_bool(a)
+    wb, _ = pack_bool(b)
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    call("tpw_bool_pairwise_reduce", _ptr(wa), _ptr(wb), B, n, m, d, op, reduction, _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def jaccard_bool(x1, x2):
+    import torch
+
+    a, b = _as3(x1), _as3(x2)
+    B, n, d = a.shape
+    m = b.shape[1]
+    wa, pa = pack_bool(a)
+    wb, pb = pack_bool(b)
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    call("tpw_jaccard_bool", _ptr(wa), _ptr(wb), _ptr(pa), _ptr(pb), B, n, m, d, _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def row_norms(x, squared):
+    import torch
+
+    x = x.contiguous()
+    d = x.shape[-1]
+    rows = x.numel() // d if d else 0
+    out = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    call("tpw_row_norms", _ptr(x), _dtype_code(x), rows, d, int(squared), _ptr(out), _stream())
+    return out
+
+
+def pairwise_inner(x1, x2, epilogue, aux1=None, aux2=None):
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    if epilogue in (EPI_EUCLIDEAN, EPI_SQEUCLIDEAN):
+        aux1 = row_norms(a, True) if aux1 is None else aux1
+        aux2 = row_norms(b, True) if aux2 is None else aux2
+    elif epilogue in (EPI_COSINE_SIM, EPI_COSINE_DIST):
+        aux1 = row_norms(a, False) if aux1 is None else aux1
+        aux2 = row_norms(b, False) if aux2 is None else aux2
+    out = torch.empty((B, n, m), dtype=x1.dtype, device=x1.device)
+    call("tpw_pairwise_inner", _ptr(a), _ptr(b), _dtype_code(a), B, n, m, d, _ptr(aux1), _ptr(aux2),
+         epilogue, _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def lp_distances(x1, x2, p):
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    call("tpw_lp_distances", _ptr(a), _ptr(b), B, n, m, d, float(p), _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def lp_distances_backward(grad, x1, x2, dist, p):
+    """(grad_x1, grad_x2) of lp_distances."""
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    g, dd = _as3(grad).contiguous(), _as3(dist).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    gx1 = torch.empty_like(a)
+    gx2 = torch.empty_like(b)
+    ws1 = lib().tpw_lp_backward_workspace_size(B, n, m, d)
+    ws2 = lib().tpw_lp_backward_workspace_size(B, m, n, d)
+    ws = torch.empty((max(ws1, ws2, 1),), dtype=torch.uint8, device=x1.device)
+    call("tpw_lp_distances_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(dd), B, n, m, d, float(p), 0,
+         _ptr(gx1), _ptr(ws), _stream())
+    call("tpw_lp_distances_backward", _ptr(g), _ptr(b), _ptr(a), _ptr(dd), B, m, n, d, float(p), 1,
+         _ptr(gx2), _ptr(ws), _stream())
+    if x1.dim() == 2:
+        return gx1[0], gx2[0]
+    return gx1, gx2
+
+
+def euclidean_backward(grad, x1, x2, res):
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    g, r = _as3(grad).contiguous(), _as3(res).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    ws = torch.empty((lib().tpw_inner_backward_workspace_size(B, n, m, d),), dtype=torch.uint8,
+                     device=a.device)
+    call("tpw_euclidean_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(r), _dtype_code(a), B, n, m, d,
+         _ptr(gx1), _ptr(gx2), _ptr(ws), _stream())
+    if x1.dim() == 2:
+        return gx1[0], gx2[0]
+    return gx1, gx2
+
+
+def cosine_backward(grad, x1, x2, similarity=False):
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    g = _as3(grad).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    n1, n2 = row_norms(a, False), row_norms(b, False)
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    ws = torch.empty((lib().tpw_inner_backward_workspace_size(B, n, m, d),), dtype=torch.uint8,
+                     device=a.device)
+    call("tpw_cosine_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(n1), _ptr(n2), _dtype_code(a), B, n,
+         m, d, int(similarity), _ptr(gx1), _ptr(gx2), _ptr(ws), _stream())
+    if x1.dim() == 2:
+        return gx1[0], gx2[0]
+    return gx1, gx2
+
+
+def _as4(x):
+    return x if x.dim() == 4 else x.unsqueeze(0)
+
+
+def directed_hausdorff(x1, x2, perm1=None, perm2=None):
+    """x1 [(batch,) b1, p1, d], x2 [(batch,) b2, p2, d] fp32 -> (out, idx1, idx2)."""
+    import torch
+
+    a, b = _as4(x1).contiguous(), _as4(x2).contiguous()
+    B, b1, p1, d = a.shape
+    b2, p2 = b.shape[1], b.shape[2]
+    out = torch.empty((B, b1, b2), dtype=torch.float32, device=a.device)
+    i1 = torch.empty((B, b1, b2), dtype=torch.int64, device=a.device)
+    i2 = torch.empty((B, b1, b2), dtype=torch.int64, device=a.device)
+    ws = torch.empty((lib().tpw_hausdorff_workspace_size(B, b1, p1, b2, p2, d),), dtype=torch.uint8,
+                     device=a.device)
+    call("tpw_directed_hausdorff", _ptr(a), _ptr(b), B, b1, p1, b2, p2, d,
+         _ptr(None if perm1 is None else perm1.contiguous()),
+         _ptr(None if perm2 is None else perm2.contiguous()),
+         _ptr(out), _ptr(i1), _ptr(i2), _ptr(ws), _stream())
+    if x1.dim() == 3:
+        return out[0], i1[0], i2[0]
+    return out, i1, i2
+
+
+def directed_hausdorff_backward(grad, x1, x2, out, idx1, idx2):
+    import torch
+
+    a, b = _as4(x1).contiguous(), _as4(x2).contiguous()
+    g = grad.contiguous().reshape(a.shape[0], a.shape[1], b.shape[1])
+    o = out.contiguous().reshape(g.shape)
+    i1, i2 = idx1.contiguous().reshape(g.shape), idx2.contiguous().reshape(g.shape)
+    B, b1, p1, d = a.shape
+    b2, p2 = b.shape[1], b.shape[2]
+    gx1, gx2 = torch.zeros_like(a), torch.zeros_like(b)
+    call("tpw_directed_hausdorff_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(o), _ptr(i1), _ptr(i2),
+         B, b1, p1, b2, p2, d, _ptr(gx1), _ptr(gx2), _stream())
+    if x1.dim() == 3:
+        return gx1[0], gx2[0]
+    return gx1, gx2

@@ -1,0 +1,66 @@
+// Shared helpers of the gfx950 kernel library (device side and host side).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "torchpairwise_amd.h"
+
+namespace tpw {
+
+// Records a printf-style message as the calling thread's last error.
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// Turns a pending launch failure into TPW_ERR_LAUNCH (with a message naming `what`).
+int check_launch(const char *what);
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Largest grid.y / grid.z the launcher may use.
+constexpr int64_t kMaxGridYZ = 65535;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void store_nt(float *p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void store_nt4(float *p, floatx4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(p));
+}
+
+// Correctly rounded fp32 square root.  (On this toolchain __fsqrt_rn lowers to the bare
+// 1-ulp v_sqrt_f32; sqrtf / __builtin_sqrtf get the fma-based rounding fix-up.)
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
+// bf16 (stored as uint16_t bits) <-> fp32; fp32 -> bf16 rounds to nearest even, as
+// c10::BFloat16 does.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(uint16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ void from_f32(float *p, float v) { *p = v; }
+__device__ __forceinline__ void from_f32(uint16_t *p, float v) { *p = f32_to_bf16_rne(v); }
+
+// S = x1 . x2^T in fp32 on the matrix cores for fp32 or bf16 inputs (inner.hip).
+int inner_dot_f32(const void *x1, const void *x2, int dtype, int64_t batch, int64_t n, int64_t m,
+                  int64_t d, float *out, hipStream_t s);
+
+}  // namespace tpw
+
+#define TPW_REQUIRE(cond, ...)          \
+    do {                                \
+        if (!(cond)) {                  \
+            tpw::set_error(__VA_ARGS__); \
+            return TPW_ERR_INVALID;     \
+        }                               \
+    } while (0)

@@ -1,0 +1,477 @@
+// Directed Hausdorff distance between point clouds, as a fused streaming max-min that never
+// forms the p1 x p2 distance matrix.
+//
+// Semantics (reference CPU loop, csrc/ops/cpu/hausdorff_kernel.cpp:25-51): for every cloud
+// pair, value = sqrt(max_m min_n d(m, n)) with d summed over k in order in fp32 without
+// contraction; x1 index = the last m (iteration order) whose min equals the max; x2 index =
+// the first n reaching that m's min.  The reference breaks out of the n loop as soon as
+// d < (max so far); any m it skips that way has min < final max, so the result is the same
+// for any schedule that prunes an m only when it has seen a d below a value that some other
+// m's exact min reaches.  That is what the kernels here do:
+//
+//   1. relayout: each cloud to SoA [d][p] in iteration order (the shuffle permutation, when
+//      given, is applied here, so every later scan is contiguous);
+//   2. seed: per cloud pair, the 8 points of x1 farthest from x2's bounding box get an exact
+//      full scan; their largest min is a first threshold T (a lower bound of the answer);
+//   3. scan: every wave takes one m at a time; its 64 lanes evaluate 64 consecutive n per
+//      step (the first points of x2 come from LDS), and the wave drops m as soon as any lane
+//      sees d < T (a ballot).  An m scanned to the end has its exact min; it is folded into
+//      the pair's key (float bits of min << 32 | m position) with a 64-bit atomicMax, which
+//      also raises T for everyone.  Equal mins resolve to the larger m position = the last m.
+//   4. finalize: one wave per pair rescans the winning m for the first n position reaching
+//      its min, and writes sqrt, and the (permuted) indices.
+//
+// Non-negative fp32 bit patterns order like the values, so the packed key orders by
+// (value, m position) exactly.
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace tpw {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kSeeds = 8;
+constexpr int kLdsFloats = 8192;  // 32 KiB of x2 points per block
+
+__device__ __forceinline__ float sqdist(const float *a, const float *xs, int64_t stride,
+                                        int64_t n, int d) {
+    float s = 0.0f;
+    for (int k = 0; k < d; ++k) {
+        const float diff = a[k] - xs[k * stride + n];
+        s = s + diff * diff;
+    }
+    return s;
+}
+
+template <int D>
+__device__ __forceinline__ float sqdist_fixed(const float (&a)[D], const float *xs, int64_t stride,
+                                              int64_t n) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        const float diff = a[k] - xs[k * stride + n];
+        s = s + diff * diff;
+    }
+    return s;
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ float threshold_of(const unsigned long long *key) {
+    unsigned long long k = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __uint_as_float((uint32_t)(k >> 32));
+}
+
+__device__ __forceinline__ void fold_key(unsigned long long *key, float mn, int64_t m) {
+    const unsigned long long k = ((unsigned long long)__float_as_uint(mn) << 32) | (uint64_t)m;
+    atomicMax(key, k);
+}
+
+// xs[c][k][pos] = x[c][perm ? perm[batch_of(c)][pos] : pos][k]
+__global__ void soa_kernel(const float *__restrict__ x, const int64_t *__restrict__ perm,
+                           int64_t clouds, int64_t clouds_per_batch, int64_t p, int d,
+                           float *__restrict__ xs) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= clouds * p) return;
+    const int64_t c = t / p, pos = t - c * p;
+    const int64_t src = perm ? perm[(c / clouds_per_batch) * p + pos] : pos;
+    const float *s = x + (c * p + src) * d;
+    float *o = xs + c * d * p + pos;
+    for (int k = 0; k < d; ++k) o[(int64_t)k * p] = s[k];
+}
+
+// bbox[c][k][0] = min, [1] = max over the points of cloud c (SoA input)
+__global__ void bbox_kernel(const float *__restrict__ xs, int64_t p, int d,
+                            float *__restrict__ bbox) {
+    __shared__ float red[2][kThreads];
+    const int64_t c = blockIdx.x;
+    for (int k = 0; k < d; ++k) {
+        const float *row = xs + (c * d + k) * p;
+        float lo = INFINITY, hi = -INFINITY;
+        for (int64_t n = threadIdx.x; n < p; n += kThreads) {
+            const float v = row[n];
+            lo = fminf(lo, v);
+            hi = fmaxf(hi, v);
+        }
+        red[0][threadIdx.x] = lo;
+        red[1][threadIdx.x] = hi;
+        __syncthreads();
+        for (int s = kThreads / 2; s > 0; s >>= 1) {
+            if (threadIdx.x < s) {
+                red[0][threadIdx.x] = fminf(red[0][threadIdx.x], red[0][threadIdx.x + s]);
+                red[1][threadIdx.x] = fmaxf(red[1][threadIdx.x], red[1][threadIdx.x + s]);
+            }
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) {
+            bbox[(c * d + k) * 2 + 0] = red[0][0];
+            bbox[(c * d + k) * 2 + 1] = red[1][0];
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void zero_keys_kernel(unsigned long long *keys, int64_t count) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < count) keys[t] = 0ull;
+}
+
+struct PairPtrs {
+    const float *x1;
+    const float *x2;
+};
+
+__device__ __forceinline__ PairPtrs pair_ptrs(const float *xs1, const float *xs2, int64_t pair,
+                                              int64_t b1, int64_t b2, int64_t p1, int64_t p2,
+                                              int d) {
+    const int64_t per_batch = b1 * b2;
+    const int64_t bb = pair / per_batch;
+    const int64_t rem = pair - bb * per_batch;
+    const int64_t i = rem / b2, j = rem - i * b2;
+    PairPtrs r;
+    r.x1 = xs1 + (bb * b1 + i) * d * p1;
+    r.x2 = xs2 + (bb * b2 + j) * d * p2;
+    return r;
+}
+
+// Exact min over all n of d(m, n), computed by one wave (all lanes return it).
+__device__ float full_scan_min(const float *a, const float *X2, int64_t p2, int d) {
+    const int lane = threadIdx.x & 63;
+    float best = INFINITY;
+    for (int64_t n0 = 0; n0 < p2; n0 += 64) {
+        const int64_t n = n0 + lane;
+        if (n < p2) best = fminf(best, sqdist(a, X2, p2, n, d));
+    }
+    return wave_min(best);
+}
+
+__global__ __launch_bounds__(kThreads) void seed_kernel(const float *__restrict__ xs1,
+                                                        const float *__restrict__ xs2,
+                                                        const float *__restrict__ bbox,
+                                                        int64_t b1, int64_t b2, int64_t p1,
+                                                        int64_t p2, int d,
+                                                        unsigned long long *__restrict__ keys) {
+    __shared__ float candL[kThreads];
+    __shared__ int64_t candM[kThreads];
+    __shared__ int64_t seeds[kSeeds];
+    const int64_t pair = blockIdx.x;
+    const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, d);
+    const int64_t bb = pair / (b1 * b2);
+    const int64_t j = pair % b2;
+    const float *box = bbox + (bb * b2 + j) * d * 2;
+
+    float bestL = -1.0f;
+    int64_t bestM = 0;
+    for (int64_t m = threadIdx.x; m < p1; m += kThreads) {
+        float L = 0.0f;
+        for (int k = 0; k < d; ++k) {
+            const float v = P.x1[k * p1 + m];
+            const float e = fmaxf(fmaxf(box[2 * k] - v, v - box[2 * k + 1]), 0.0f);
+            L = L + e * e;
+        }
+        if (L > bestL) {
+            bestL = L;
+            bestM = m;
+        }
+    }
+    candL[threadIdx.x] = bestL;
+    candM[threadIdx.x] = bestM;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int s = 0; s < kSeeds; ++s) {
+            int arg = 0;
+            for (int t = 1; t < kThreads; ++t)
+                if (candL[t] > candL[arg]) arg = t;
+            seeds[s] = candM[arg];
+            candL[arg] = -2.0f;
+        }
+    }
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int s = wave; s < kSeeds; s += kThreads / 64) {
+        const int64_t m = seeds[s];
+        if (m >= p1) continue;
+        float a[64];
+        const int dd = d < 64 ? d : 64;
+        for (int k = 0; k < dd; ++k) a[k] = P.x1[k * p1 + m];
+        const float mn = d <= 64 ? full_scan_min(a, P.x2, p2, d) : 0.0f;
+        if (lane == 0 && d <= 64) fold_key(&keys[pair], mn, m);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void scan_kernel(const float *__restrict__ xs1,
+                                                        const float *__restrict__ xs2,
+                                                        int64_t b1, int64_t b2, int64_t p1,
+                                                        int64_t p2, int64_t m_per_block,
+                                                        int64_t lds_points,
+                                                        unsigned long long *__restrict__ keys) {
+    __shared__ float lds[kLdsFloats];
+    const int64_t pair = blockIdx.y;
+    const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, D);
+    const int64_t chunk = p2 < lds_points ? p2 : lds_points;
+    for (int64_t t = threadIdx.x; t < chunk * D; t += kThreads) {
+        const int64_t k = t / chunk, n = t - k * chunk;
+        lds[t] = P.x2[k * p2 + n];
+    }
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t mbeg = (int64_t)blockIdx.x * m_per_block;
+    const int64_t mend = mbeg + m_per_block < p1 ? mbeg + m_per_block : p1;
+    unsigned long long *key = &keys[pair];
+    for (int64_t m = mbeg + wave; m < mend; m += kThreads / 64) {
+        float a[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) a[k] = P.x1[k * p1 + m];
+        float T = threshold_of(key);
+        float best = INFINITY;
+        bool pruned = false;
+        int64_t n0 = 0;
+        for (; n0 < chunk; n0 += 64) {
+            const int64_t n = n0 + lane;
+            const float dd = n < chunk ? sqdist_fixed<D>(a, lds, chunk, n) : INFINITY;
+            if (__any(dd < T)) {
+                pruned = true;
+                break;
+            }
+            best = fminf(best, dd);
+        }
+        if (!pruned) {
+            for (; n0 < p2; n0 += 64) {
+                const int64_t n = n0 + lane;
+                const float dd = n < p2 ? sqdist_fixed<D>(a, P.x2, p2, n) : INFINITY;
+                if (__any(dd < T)) {
+                    pruned = true;
+                    break;
+                }
+                best = fminf(best, dd);
+                if ((n0 & 4095) == 4032) T = threshold_of(key);
+            }
+        }
+        if (!pruned) {
+            const float mn = wave_min(best);
+            if (lane == 0) fold_key(key, mn, m);
+        }
+    }
+}
+
+// Generic-d variant (features in registers up to 64, x2 read from global memory).
+__global__ __launch_bounds__(kThreads) void scan_kernel_any(const float *__restrict__ xs1,
+                                                            const float *__restrict__ xs2,
+                                                            int64_t b1, int64_t b2, int64_t p1,
+                                                            int64_t p2, int d,
+                                                            int64_t m_per_block,
+                                                            unsigned long long *__restrict__ keys) {
+    const int64_t pair = blockIdx.y;
+    const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, d);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t mbeg = (int64_t)blockIdx.x * m_per_block;
+    const int64_t mend = mbeg + m_per_block < p1 ? mbeg + m_per_block : p1;
+    unsigned long long *key = &keys[pair];
+    for (int64_t m = mbeg + wave; m < mend; m += kThreads / 64) {
+        float a[64];
+        for (int k = 0; k < d; ++k) a[k] = P.x1[k * p1 + m];
+        float T = threshold_of(key);
+        float best = INFINITY;
+        bool pruned = false;
+        for (int64_t n0 = 0; n0 < p2; n0 += 64) {
+            const int64_t n = n0 + lane;
+            const float dd = n < p2 ? sqdist(a, P.x2, p2, n, d) : INFINITY;
+            if (__any(dd < T)) {
+                pruned = true;
+                break;
+            }
+            best = fminf(best, dd);
+            if ((n0 & 4095) == 4032) T = threshold_of(key);
+        }
+        if (!pruned) {
+            const float mn = wave_min(best);
+            if (lane == 0) fold_key(key, mn, m);
+        }
+    }
+}
+
+// One wave per pair: first n position reaching the winning m's min; write the outputs.
+__global__ __launch_bounds__(kThreads) void finalize_kernel(
+    const float *__restrict__ xs1, const float *__restrict__ xs2,
+    const unsigned long long *__restrict__ keys, const int64_t *__restrict__ perm1,
+    const int64_t *__restrict__ perm2, int64_t pairs, int64_t b1, int64_t b2, int64_t p1,
+    int64_t p2, int d, float *__restrict__ out, int64_t *__restrict__ idx1,
+    int64_t *__restrict__ idx2) {
+    const int64_t pair = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (pair >= pairs) return;
+    const int64_t bb = pair / (b1 * b2);
+    if (p1 == 0 || p2 == 0) {
+        if (lane == 0) {
+            out[pair] = 0.0f;
+            idx1[pair] = 0;
+            idx2[pair] = 0;
+        }
+        return;
+    }
+    const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, d);
+    const unsigned long long k = keys[pair];
+    const int64_t m = (int64_t)(k & 0xffffffffull);
+    const float H = __uint_as_float((uint32_t)(k >> 32));
+    float a[64];
+    for (int t = 0; t < d && t < 64; ++t) a[t] = P.x1[(int64_t)t * p1 + m];
+    int64_t npos = p2;
+    for (int64_t n0 = 0; n0 < p2; n0 += 64) {
+        const int64_t n = n0 + lane;
+        const bool hit = n < p2 && sqdist(a, P.x2, p2, n, d) == H;
+        const unsigned long long mask = __ballot(hit);
+        if (mask) {
+            npos = n0 + __builtin_ctzll(mask);
+            break;
+        }
+    }
+    if (lane == 0) {
+        out[pair] = sqrt_rn(H);
+        idx1[pair] = perm1 ? perm1[bb * p1 + m] : m;
+        idx2[pair] = npos < p2 ? (perm2 ? perm2[bb * p2 + npos] : npos) : 0;
+    }
+}
+
+// grad_x1[bb,i,m*,k] += g * (x1[m*,k] - x2[n*,k]) / out, over j in order (one thread per
+// (bb, i, k) owns every update of its slice, so the summation order is the reference's).
+__global__ void backward_x1_kernel(const float *__restrict__ g, const float *__restrict__ x1,
+                                   const float *__restrict__ x2, const float *__restrict__ out,
+                                   const int64_t *__restrict__ idx1,
+                                   const int64_t *__restrict__ idx2, int64_t batch, int64_t b1,
+                                   int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                   float *__restrict__ gx1) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= batch * b1 * d) return;
+    const int64_t k = t % d, i = (t / d) % b1, bb = t / (d * b1);
+    for (int64_t j = 0; j < b2; ++j) {
+        const int64_t pr = (bb * b1 + i) * b2 + j;
+        const int64_t m = idx1[pr], n = idx2[pr];
+        const float diff = x1[((bb * b1 + i) * p1 + m) * d + k] - x2[((bb * b2 + j) * p2 + n) * d + k];
+        float *dst = gx1 + ((bb * b1 + i) * p1 + m) * d + k;
+        *dst = *dst + g[pr] * diff / out[pr];
+    }
+}
+
+__global__ void backward_x2_kernel(const float *__restrict__ g, const float *__restrict__ x1,
+                                   const float *__restrict__ x2, const float *__restrict__ out,
+                                   const int64_t *__restrict__ idx1,
+                                   const int64_t *__restrict__ idx2, int64_t batch, int64_t b1,
+                                   int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                   float *__restrict__ gx2) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= batch * b2 * d) return;
+    const int64_t k = t % d, j = (t / d) % b2, bb = t / (d * b2);
+    for (int64_t i = 0; i < b1; ++i) {
+        const int64_t pr = (bb * b1 + i) * b2 + j;
+        const int64_t m = idx1[pr], n = idx2[pr];
+        const float diff = x2[((bb * b2 + j) * p2 + n) * d + k] - x1[((bb * b1 + i) * p1 + m) * d + k];
+        float *dst = gx2 + ((bb * b2 + j) * p2 + n) * d + k;
+        *dst = *dst + g[pr] * diff / out[pr];
+    }
+}
+
+struct Workspace {
+    float *xs1, *xs2, *bbox;
+    unsigned long long *keys;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+Workspace carve(void *ws, int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d) {
+    char *p = static_cast<char *>(ws);
+    Workspace w;
+    w.keys = reinterpret_cast<unsigned long long *>(p);
+    p += align256(sizeof(unsigned long long) * batch * b1 * b2);
+    w.bbox = reinterpret_cast<float *>(p);
+    p += align256(sizeof(float) * batch * b2 * d * 2);
+    w.xs1 = reinterpret_cast<float *>(p);
+    p += align256(sizeof(float) * batch * b1 * p1 * d);
+    w.xs2 = reinterpret_cast<float *>(p);
+    return w;
+}
+
+}  // namespace
+}  // namespace tpw
+
+using namespace tpw;
+
+extern "C" size_t tpw_hausdorff_workspace_size(int64_t batch, int64_t b1, int64_t p1, int64_t b2,
+                                               int64_t p2, int64_t d) {
+    return align256(sizeof(unsigned long long) * batch * b1 * b2) +
+           align256(sizeof(float) * batch * b2 * d * 2) +
+           align256(sizeof(float) * batch * b1 * p1 * d) +
+           align256(sizeof(float) * batch * b2 * p2 * d);
+}
+
+extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t batch, int64_t b1,
+                                      int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                      const int64_t *perm1, const int64_t *perm2, float *out,
+                                      int64_t *idx1, int64_t *idx2, void *workspace,
+                                      void *stream) {
+    TPW_REQUIRE(batch >= 0 && b1 >= 0 && b2 >= 0 && p1 >= 0 && p2 >= 0 && d >= 0, "invalid sizes");
+    TPW_REQUIRE(d <= 64, "directed_hausdorff supports at most 64 features on the GPU (got %lld)",
+                (long long)d);
+    TPW_REQUIRE(p1 < (int64_t)0xffffffffLL, "too many points in x1 (%lld)", (long long)p1);
+    const int64_t pairs = batch * b1 * b2;
+    if (pairs == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out && idx1 && idx2 && workspace, "null pointer");
+    TPW_REQUIRE(pairs <= kMaxGridYZ, "too many cloud pairs (%lld)", (long long)pairs);
+    hipStream_t s = as_stream(stream);
+    Workspace w = carve(workspace, batch, b1, p1, b2, p2, d);
+    hipLaunchKernelGGL(zero_keys_kernel, dim3((unsigned)cdiv(pairs, 256)), dim3(256), 0, s, w.keys,
+                       pairs);
+    int rc = check_launch("zero_keys_kernel");
+    if (rc) return rc;
+    if (p1 > 0 && p2 > 0 && d > 0) {
+        hipLaunchKernelGGL(soa_kernel, dim3((unsigned)cdiv(batch * b1 * p1, 256)), dim3(256), 0, s,
+                           x1, perm1, batch * b1, b1, p1, (int)d, w.xs1);
+        hipLaunchKernelGGL(soa_kernel, dim3((unsigned)cdiv(batch * b2 * p2, 256)), dim3(256), 0, s,
+                           x2, perm2, batch * b2, b2, p2, (int)d, w.xs2);
+        hipLaunchKernelGGL(bbox_kernel, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2,
+                           p2, (int)d, w.bbox);
+        hipLaunchKernelGGL(seed_kernel, dim3((unsigned)pairs), dim3(kThreads), 0, s, w.xs1, w.xs2,
+                           w.bbox, b1, b2, p1, p2, (int)d, w.keys);
+        rc = check_launch("hausdorff prologue");
+        if (rc) return rc;
+        const int64_t m_per_block = 2048;
+        dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)pairs);
+        const int64_t lds_points = (kLdsFloats / d) / 64 * 64;
+        switch (d) {
+            case 1: hipLaunchKernelGGL(scan_kernel<1>, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys); break;
+            case 2: hipLaunchKernelGGL(scan_kernel<2>, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys); break;
+            case 3: hipLaunchKernelGGL(scan_kernel<3>, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys); break;
+            case 4: hipLaunchKernelGGL(scan_kernel<4>, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys); break;
+            default: hipLaunchKernelGGL(scan_kernel_any, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, (int)d, m_per_block, w.keys); break;
+        }
+        rc = check_launch("hausdorff scan_kernel");
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads),
+                       0, s, w.xs1, w.xs2, w.keys, perm1, perm2, pairs, b1, b2, p1, p2, (int)d, out,
+                       idx1, idx2);
+    return check_launch("hausdorff finalize_kernel");
+}
+
+extern "C" int tpw_directed_hausdorff_backward(const float *grad, const float *x1,
+                                               const float *x2, const float *out,
+                                               const int64_t *idx1, const int64_t *idx2,
+                                               int64_t batch, int64_t b1, int64_t p1, int64_t b2,
+                                               int64_t p2, int64_t d, float *grad_x1,
+                                               float *grad_x2, void *stream) {
+    TPW_REQUIRE(batch >= 0 && b1 >= 0 && b2 >= 0 && p1 >= 0 && p2 >= 0 && d >= 0, "invalid sizes");
+    if (batch * b1 * b2 == 0 || d == 0 || p1 == 0 || p2 == 0) return TPW_OK;
+    TPW_REQUIRE(grad && x1 && x2 && out && idx1 && idx2 && grad_x1 && grad_x2, "null pointer");
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(backward_x1_kernel, dim3((unsigned)cdiv(batch * b1 * d, 256)), dim3(256), 0,
+                       s, grad, x1, x2, out, idx1, idx2, batch, b1, p1, b2, p2, d, grad_x1);
+    hipLaunchKernelGGL(backward_x2_kernel, dim3((unsigned)cdiv(batch * b2 * d, 256)), dim3(256), 0,
+                       s, grad, x1, x2, out, idx1, idx2, batch, b1, p1, b2, p2, d, grad_x2);
+    return check_launch("hausdorff backward");
+}

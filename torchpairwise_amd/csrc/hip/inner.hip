@@ -1,0 +1,349 @@
+// Inner-product family on the CDNA4 matrix cores: out = epilogue(x1 . x2^T, aux1, aux2).
+//
+// Block = 256 threads (4 waves, 2 x 2), output tile 128 x 128, wave tile 64 x 64 = 2 x 2
+// blocks of 32 x 32.  Each K chunk is 128 bytes of every operand row (32 fp32 or 64 bf16
+// features), staged in LDS with a 16-byte pad per row (144-byte stride, conflict-free
+// 16-byte reads for 16 consecutive rows).  The k index inside a chunk is permuted so that
+// every lane feeds the MFMA from one contiguous 64-byte run of its row: lane (i + 32 h)
+// supplies features [h*KC/2, (h+1)*KC/2) of row i, in the order the MFMA k slots consume
+// them; A and B use the same permutation, so the sum over k is unchanged.
+//   fp32: v_mfma_f32_32x32x2_f32, 16 per chunk and 32 x 32 block
+//   bf16: v_mfma_f32_32x32x16_bf16 (gfx950), 4 per chunk and block, fp32 accumulation
+// The epilogue (norms, sqrt, guarded divide, clip) is applied to the accumulators in
+// registers and the result is written once with non-temporal stores.  The next chunk's
+// global loads are issued before the current chunk's MFMAs (register prefetch).
+// Tiles are assigned XCD-contiguously (consecutive workgroup ids go round-robin over the
+// 8 XCDs, so id % 8 selects the XCD) and in groups of 8 tile rows, so that the blocks
+// resident on one XCD share A and B panels in that XCD's L2.
+#include "common.hpp"
+
+namespace tpw {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 128;
+constexpr int kRowVec = 8;              // uint4 per 128-byte chunk row
+constexpr int kLdsStride = kRowVec + 1; // in uint4 (144 bytes)
+constexpr int kGroupRows = 8;
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+    static constexpr int kPer16 = 4;
+    static constexpr int kChunk = 32;
+    __device__ static float load(const float *p) { return *p; }
+};
+template <>
+struct Elem<uint16_t> {  // bf16 bits
+    static constexpr int kPer16 = 8;
+    static constexpr int kChunk = 64;
+};
+
+template <int EPI>
+__device__ __forceinline__ float epilogue(float s, float a1, float a2) {
+    if constexpr (EPI == TPW_EPI_DOT) {
+        return s;
+    } else if constexpr (EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN) {
+        float v = (a1 + a2) - 2.0f * s;
+        v = v > 0.0f ? v : 0.0f;
+        if constexpr (EPI == TPW_EPI_EUCLIDEAN) v = sqrt_rn(v);
+        return v;
+    } else {
+        float den = a1 * a2;
+        float q = den != 0.0f ? __fdiv_rn(s, den) : s;
+        if constexpr (EPI == TPW_EPI_COSINE_SIM) return q;
+        float v = 1.0f - q;
+        return fminf(fmaxf(v, 0.0f), 2.0f);
+    }
+}
+
+__device__ __forceinline__ void store_out(float *p, float v) { store_nt(p, v); }
+__device__ __forceinline__ void store_out(uint16_t *p, float v) {
+    __builtin_nontemporal_store(f32_to_bf16_rne(v), p);
+}
+
+// Loads one 16-byte piece (row r, piece c of chunk kc) of a [rows, d] operand.
+template <typename T, bool VEC>
+__device__ __forceinline__ uint4 load_piece(const T *__restrict__ x, int64_t rows, int64_t d,
+                                            int64_t r, int64_t kbase) {
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (r >= rows) return v;
+    constexpr int E = Elem<T>::kPer16;
+    if constexpr (VEC) {
+        if (kbase < d) v = *reinterpret_cast<const uint4 *>(x + r * d + kbase);
+    } else {
+        const T *p = x + r * d;
+        if constexpr (E == 4) {
+            uint32_t e[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                e[t] = (kbase + t < d) ? __float_as_uint(p[kbase + t]) : 0u;
+            v = make_uint4(e[0], e[1], e[2], e[3]);
+        } else {
+            uint32_t e[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                uint32_t lo = (kbase + 2 * t < d) ? (uint32_t)p[kbase + 2 * t] : 0u;
+                uint32_t hi = (kbase + 2 * t + 1 < d) ? (uint32_t)p[kbase + 2 * t + 1] : 0u;
+                e[t] = lo | (hi << 16);
+            }
+            v = make_uint4(e[0], e[1], e[2], e[3]);
+        }
+    }
+    return v;
+}
+
+__device__ __forceinline__ void mfma_chunk(floatx16 (&acc)[2][2], const uint4 (&a)[2][4],
+                                           const uint4 (&b)[2][4], float) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni) {
+                    const uint32_t av = e == 0 ? a[mi][q].x : e == 1 ? a[mi][q].y : e == 2 ? a[mi][q].z : a[mi][q].w;
+                    const uint32_t bv = e == 0 ? b[ni][q].x : e == 1 ? b[ni][q].y : e == 2 ? b[ni][q].z : b[ni][q].w;
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                        __uint_as_float(av), __uint_as_float(bv), acc[mi][ni], 0, 0, 0);
+                }
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void mfma_chunk(floatx16 (&acc)[2][2], const uint4 (&a)[2][4],
+                                           const uint4 (&b)[2][4], uint16_t) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8, a[mi][q]), __builtin_bit_cast(bf16x8, b[ni][q]),
+                    acc[mi][ni], 0, 0, 0);
+            }
+        }
+    }
+}
+
+// Maps the linear workgroup id to (batch, tile row, tile col).
+__device__ __forceinline__ void tile_of(int64_t bid, int64_t tiles_n, int64_t tiles_m,
+                                        int64_t total, int64_t &b, int64_t &tr, int64_t &tc) {
+    int64_t t = bid;
+    if ((total & 7) == 0) t = (bid & 7) * (total >> 3) + (bid >> 3);
+    const int64_t per_batch = tiles_n * tiles_m;
+    b = t / per_batch;
+    t -= b * per_batch;
+    const int64_t in_group = (int64_t)kGroupRows * tiles_m;
+    const int64_t g = t / in_group;
+    const int64_t first = g * kGroupRows;
+    const int64_t gsize = tiles_n - first < kGroupRows ? tiles_n - first : kGroupRows;
+    const int64_t o = t - g * in_group;
+    tr = first + o % gsize;
+    tc = o / gsize;
+}
+
+template <typename T, typename OutT, int EPI, bool VEC>
+__global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
+    const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
+    const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
+    int64_t tiles_n, int64_t tiles_m, int64_t total) {
+    __shared__ uint4 As[kTile * kLdsStride];
+    __shared__ uint4 Bs[kTile * kLdsStride];
+    constexpr int E = Elem<T>::kPer16;
+    constexpr int KC = Elem<T>::kChunk;
+
+    int64_t b, tr, tc;
+    tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
+    const int64_t row0 = tr * kTile, col0 = tc * kTile;
+    const T *A = x1 + b * n * d;
+    const T *B = x2 + b * m * d;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+
+    const int64_t nchunks = (d + KC - 1) / KC;
+    uint4 pa[4], pb[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int idx = tid + kThreads * q;
+        const int r = idx >> 3, c = idx & 7;
+        pa[q] = load_piece<T, VEC>(A, n, d, row0 + r, (int64_t)c * E);
+        pb[q] = load_piece<T, VEC>(B, m, d, col0 + r, (int64_t)c * E);
+    }
+
+    for (int64_t kc = 0; kc < nchunks; ++kc) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int idx = tid + kThreads * q;
+            const int r = idx >> 3, c = idx & 7;
+            As[r * kLdsStride + c] = pa[q];
+            Bs[r * kLdsStride + c] = pb[q];
+        }
+        __syncthreads();
+        if (kc + 1 < nchunks) {
+            const int64_t kb = (kc + 1) * KC;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int idx = tid + kThreads * q;
+                const int r = idx >> 3, c = idx & 7;
+                pa[q] = load_piece<T, VEC>(A, n, d, row0 + r, kb + (int64_t)c * E);
+                pb[q] = load_piece<T, VEC>(B, m, d, col0 + r, kb + (int64_t)c * E);
+            }
+        }
+        uint4 a[2][4], bv[2][4];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                a[mi][q] = As[(wr + mi * 32 + l32) * kLdsStride + h * 4 + q];
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                bv[ni][q] = Bs[(wc + ni * 32 + l32) * kLdsStride + h * 4 + q];
+        mfma_chunk(acc, a, bv, T{});
+        __syncthreads();
+    }
+
+    // Accumulator layout of the 32 x 32 MFMA: register r of lane l holds
+    // row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+        const int64_t col = col0 + wc + ni * 32 + l32;
+        const bool col_ok = col < m;
+        float a2 = 0.0f;
+        if constexpr (EPI != TPW_EPI_DOT) a2 = col_ok ? aux2[b * m + col] : 0.0f;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wr + mi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < n && col_ok) {
+                    float a1 = 0.0f;
+                    if constexpr (EPI != TPW_EPI_DOT) a1 = aux1[b * n + row];
+                    store_out(out + (b * n + row) * m + col, epilogue<EPI>(acc[mi][ni][r], a1, a2));
+                }
+            }
+        }
+    }
+}
+
+// Row norms: one wave per row, lanes stride over the features.
+template <typename T>
+__global__ void row_norms_kernel(const T *__restrict__ x, int64_t rows, int64_t d, int squared,
+                                 float *__restrict__ out) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const T *p = x + row * d;
+    float s = 0.0f;
+    for (int64_t k = lane; k < d; k += 64) {
+        float v;
+        if constexpr (sizeof(T) == 4) v = p[k];
+        else v = bf16_to_f32(p[k]);
+        s += v * v;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) out[row] = squared ? s : sqrt_rn(s);
+}
+
+template <typename T, int EPI, typename OutT = T>
+int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
+                 const float *aux1, const float *aux2, OutT *out, hipStream_t s) {
+    const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
+    const int64_t total = tiles_n * tiles_m * batch;
+    const bool vec = ((d * (int64_t)sizeof(T)) % 16 == 0) && aligned16(x1) && aligned16(x2);
+    if (vec)
+        hipLaunchKernelGGL((pairwise_inner_kernel<T, OutT, EPI, true>), dim3((unsigned)total),
+                           dim3(kThreads), 0, s, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
+                           tiles_m, total);
+    else
+        hipLaunchKernelGGL((pairwise_inner_kernel<T, OutT, EPI, false>), dim3((unsigned)total),
+                           dim3(kThreads), 0, s, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
+                           tiles_m, total);
+    return check_launch("pairwise_inner_kernel");
+}
+
+template <typename T>
+int dispatch_epi(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
+                 const float *aux1, const float *aux2, int epi, T *out, hipStream_t s) {
+    switch (epi) {
+        case TPW_EPI_DOT: return launch_inner<T, TPW_EPI_DOT>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
+        case TPW_EPI_EUCLIDEAN: return launch_inner<T, TPW_EPI_EUCLIDEAN>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
+        case TPW_EPI_SQEUCLIDEAN: return launch_inner<T, TPW_EPI_SQEUCLIDEAN>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
+        case TPW_EPI_COSINE_SIM: return launch_inner<T, TPW_EPI_COSINE_SIM>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
+        default: return launch_inner<T, TPW_EPI_COSINE_DIST>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
+    }
+}
+
+}  // namespace
+
+// S = x1 . x2^T in fp32 whatever the input type (used by the cosine backward).
+int inner_dot_f32(const void *x1, const void *x2, int dtype, int64_t batch, int64_t n, int64_t m,
+                  int64_t d, float *out, hipStream_t s) {
+    if (dtype == TPW_F32)
+        return launch_inner<float, TPW_EPI_DOT, float>(static_cast<const float *>(x1),
+                                                       static_cast<const float *>(x2), batch, n, m,
+                                                       d, nullptr, nullptr, out, s);
+    return launch_inner<uint16_t, TPW_EPI_DOT, float>(static_cast<const uint16_t *>(x1),
+                                                      static_cast<const uint16_t *>(x2), batch, n,
+                                                      m, d, nullptr, nullptr, out, s);
+}
+
+}  // namespace tpw
+
+using namespace tpw;
+
+extern "C" int tpw_row_norms(const void *x, int dtype, int64_t rows, int64_t d, int squared,
+                             float *norms, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(rows >= 0 && d >= 0, "invalid sizes");
+    if (rows == 0) return TPW_OK;
+    TPW_REQUIRE(x && norms, "null pointer");
+    hipStream_t s = as_stream(stream);
+    if (dtype == TPW_F32)
+        hipLaunchKernelGGL(row_norms_kernel<float>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s,
+                           static_cast<const float *>(x), rows, d, squared, norms);
+    else
+        hipLaunchKernelGGL(row_norms_kernel<uint16_t>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0,
+                           s, static_cast<const uint16_t *>(x), rows, d, squared, norms);
+    return check_launch("row_norms_kernel");
+}
+
+extern "C" int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int64_t batch,
+                                  int64_t n, int64_t m, int64_t d, const float *aux1,
+                                  const float *aux2, int epilogue, void *out, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(epilogue >= TPW_EPI_DOT && epilogue <= TPW_EPI_COSINE_DIST, "unknown epilogue %d",
+                epilogue);
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    TPW_REQUIRE(epilogue == TPW_EPI_DOT || (aux1 && aux2), "norms required for epilogue %d",
+                epilogue);
+    const int64_t total = cdiv(n, kTile) * cdiv(m, kTile) * batch;
+    TPW_REQUIRE(total <= 0x7fffffffLL, "output too large for one launch");
+    hipStream_t s = as_stream(stream);
+    if (dtype == TPW_F32)
+        return dispatch_epi<float>(static_cast<const float *>(x1), static_cast<const float *>(x2),
+                                   batch, n, m, d, aux1, aux2, epilogue, static_cast<float *>(out), s);
+    return dispatch_epi<uint16_t>(static_cast<const uint16_t *>(x1),
+                                  static_cast<const uint16_t *>(x2), batch, n, m, d, aux1, aux2,
+                                  epilogue, static_cast<uint16_t *>(out), s);
+}

@@ -1,0 +1,417 @@
+// Backward of the inner-product family (euclidean via _euclidean_dist, cosine distance and
+// cosine similarity), fp32 and bf16.
+//
+// Both gradients have the shape  grad_x1 = sign * (W @ x2) + coef1[i] * x1[i],
+//                                grad_x2 = sign * (W^T @ x1) + coef2[j] * x2[j],
+// with a per-pair weight matrix W [n, m] and per-row coefficients:
+//   euclidean (derivatives.yaml _euclidean_dist_backward):
+//     W = grad / res (0 where res == 0), sign = -1, coef1 = sum_j W, coef2 = sum_i W;
+//   cosine (autograd graph of csrc/ops/pairwise_metrics.cpp:51-56,112-122):
+//     q = prf_div(S, n1 n2^T, identity), gq = -grad [0 <= 1 - q <= 2] (clip mask; for
+//     cosine_similarity gq = grad), gS = prf_div backward (gq / den, or gq where den == 0),
+//     gden = gS * -S / den (0 where den == 0), W = gS, sign = +1,
+//     coef1 = sum_j gden n2[j] / n1[i], coef2 = sum_i gden n1[i] / n2[j] (0 where the norm
+//     is 0, as torch's norm backward).
+//
+// Pass 1 (VALU, memory-bound) forms W in fp32 in the workspace and writes per-tile partial
+// row and column sums; pass 2 adds the partials in a fixed order (deterministic); pass 3
+// runs the two products on the matrix cores (v_mfma_f32_32x32x2_f32, operands staged
+// k-major in LDS), split over K when the output tiles alone would not fill the GPU, with
+// the sign/coef epilogue fused.  For cosine, S is first recomputed on the MFMA path.
+#include "common.hpp"
+
+namespace tpw {
+namespace {
+
+enum Mode { kEuclid = 0, kCosDist = 1, kCosSim = 2 };
+
+constexpr int kPWRows = 128;
+constexpr int kPWCols = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void pair_weights_kernel(
+    const T *__restrict__ g, const T *__restrict__ res, const float *__restrict__ n1,
+    const float *__restrict__ n2, int64_t n, int64_t m, float *W, float *__restrict__ rowpart,
+    float *__restrict__ colpart, int64_t tiles_i, int64_t tiles_j) {
+    __shared__ float red[4][kPWRows];
+    const int64_t b = blockIdx.z, ti = blockIdx.y, tj = blockIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t j = tj * kPWCols + tid;
+    const bool jok = j < m;
+    float a2 = 0.0f;
+    if constexpr (MODE != kEuclid) a2 = jok ? n2[b * m + j] : 0.0f;
+    float csum = 0.0f;
+    for (int r = 0; r < kPWRows; ++r) {
+        const int64_t i = ti * kPWRows + r;
+        float rt = 0.0f;
+        if (i < n && jok) {
+            const int64_t idx = (b * n + i) * m + j;
+            const float gv = to_f32(g[idx]);
+            float w;
+            if constexpr (MODE == kEuclid) {
+                const float rv = to_f32(res[idx]);
+                w = rv == 0.0f ? 0.0f : __fdiv_rn(gv, rv);
+                rt = w;
+                csum += w;
+            } else {
+                const float s = W[idx];
+                const float a1 = n1[b * n + i];
+                const float den = a1 * a2;
+                const float q = den != 0.0f ? __fdiv_rn(s, den) : s;
+                float gq = gv;
+                if constexpr (MODE == kCosDist) {
+                    const float v = 1.0f - q;
+                    gq = (v >= 0.0f && v <= 2.0f) ? -gv : 0.0f;
+                }
+                const float gS = den != 0.0f ? __fdiv_rn(gq, den) : gq;
+                const float gden = den != 0.0f ? __fdiv_rn(gS * -s, den) : 0.0f;
+                w = gS;
+                rt = gden * a2;
+                csum += gden * a1;
+            }
+            W[idx] = w;
+        }
+        rt = wave_sum(rt);
+        if (lane == 0) red[wave][r] = rt;
+    }
+    __syncthreads();
+    if (tid < kPWRows) {
+        const int64_t i = ti * kPWRows + tid;
+        if (i < n)
+            rowpart[(b * tiles_j + tj) * n + i] = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
+    }
+    if (jok) colpart[(b * tiles_i + ti) * m + j] = csum;
+}
+
+// coef[b][r] = sum_t part[b][t][r] (t in order), divided by norms[b][r] when given
+// (0 where that norm is 0).
+__global__ void reduce_parts_kernel(const float *__restrict__ part, int64_t tiles, int64_t rows,
+                                    int64_t batch, const float *__restrict__ norms,
+                                    float *__restrict__ coef) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= batch * rows) return;
+    const int64_t b = t / rows, r = t - b * rows;
+    const float *p = part + b * tiles * rows + r;
+    float s = 0.0f;
+    for (int64_t q = 0; q < tiles; ++q) s += p[q * rows];
+    if (norms) {
+        const float nv = norms[t];
+        s = nv == 0.0f ? 0.0f : __fdiv_rn(s, nv);
+    }
+    coef[t] = s;
+}
+
+constexpr int kGT = 128;     // output tile rows and cols
+constexpr int kGK = 32;      // k per chunk
+constexpr int kGStride = kGT + 32;  // LDS row stride (floats): lanes 0-31 / 32-63 on disjoint banks
+
+template <typename T>
+__device__ __forceinline__ floatx4 load4(const T *p);
+template <>
+__device__ __forceinline__ floatx4 load4<float>(const float *p) {
+    return *reinterpret_cast<const floatx4 *>(p);
+}
+template <>
+__device__ __forceinline__ floatx4 load4<uint16_t>(const uint16_t *p) {
+    const uint2 v = *reinterpret_cast<const uint2 *>(p);
+    floatx4 r = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                 __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+    return r;
+}
+
+// out = sign * (A @ B) + coef[row] * X[row]  (or raw partial sums when part != nullptr).
+// A is fp32 [M][K] (A_T: stored [K][M]); B and X are T [K][N] / [M][N]; batch strides are
+// M*K, K*N and M*N.  grid = (tiles_N, tiles_M, batch * splits).
+template <typename T, bool A_T, bool VEC>
+__global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(
+    const float *__restrict__ A, const T *__restrict__ B, int64_t M, int64_t N, int64_t K,
+    int64_t k_per_split, int64_t batch, float sign, const float *__restrict__ coef,
+    const T *__restrict__ X, T *__restrict__ out, float *__restrict__ part) {
+    __shared__ float As[kGK * kGStride];
+    __shared__ float Bs[kGK * kGStride];
+    const int64_t split = blockIdx.z / batch, b = blockIdx.z - split * batch;
+    const int64_t row0 = (int64_t)blockIdx.y * kGT, col0 = (int64_t)blockIdx.x * kGT;
+    const int64_t kbeg = split * k_per_split;
+    const int64_t kend = kbeg + k_per_split < K ? kbeg + k_per_split : K;
+    const float *Ab = A + b * M * K;
+    const T *Bb = B + b * K * N;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+
+    for (int64_t k0 = kbeg; k0 < kend; k0 += kGK) {
+        // A chunk: 128 rows x 32 k -> As[k][row]
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int idx = tid + 256 * q;
+            if constexpr (!A_T) {
+                const int r = idx >> 3, c4 = idx & 7;
+                const int64_t gr = row0 + r, gk = k0 + 4 * c4;
+                floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (gr < M) {
+                    const float *src = Ab + gr * K + gk;
+                    if (VEC && gk + 3 < kend) {
+                        v = *reinterpret_cast<const floatx4 *>(src);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (gk + e < kend) v[e] = src[e];
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) As[(4 * c4 + e) * kGStride + r] = v[e];
+            } else {
+                const int kk = idx >> 5, r4 = idx & 31;
+                const int64_t gk = k0 + kk, gr = row0 + 4 * r4;
+                floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (gk < kend) {
+                    const float *src = Ab + gk * M + gr;
+                    if (VEC && gr + 3 < M) {
+                        v = *reinterpret_cast<const floatx4 *>(src);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (gr + e < M) v[e] = src[e];
+                    }
+                }
+                *reinterpret_cast<floatx4 *>(&As[kk * kGStride + 4 * r4]) = v;
+            }
+        }
+        // B chunk: 32 k x 128 cols -> Bs[k][col]
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int idx = tid + 256 * q;
+            const int kk = idx >> 5, c4 = idx & 31;
+            const int64_t gk = k0 + kk, gc = col0 + 4 * c4;
+            floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (gk < kend) {
+                const T *src = Bb + gk * N + gc;
+                if (VEC && gc + 3 < N) {
+                    v = load4<T>(src);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (gc + e < N) v[e] = to_f32(src[e]);
+                }
+            }
+            *reinterpret_cast<floatx4 *>(&Bs[kk * kGStride + 4 * c4]) = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kGK / 2; ++s) {
+            const int kk = 2 * s + h;
+            float a[2], bv[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) a[mi] = As[kk * kGStride + wr + mi * 32 + l32];
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) bv[ni] = Bs[kk * kGStride + wc + ni * 32 + l32];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mi], bv[ni], acc[mi][ni], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+        const int64_t col = col0 + wc + ni * 32 + l32;
+        if (col >= N) continue;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wr + mi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row >= M) continue;
+                if (part) {
+                    part[((split * batch + b) * M + row) * N + col] = acc[mi][ni][r];
+                } else {
+                    const int64_t o = (b * M + row) * N + col;
+                    from_f32(out + o, sign * acc[mi][ni][r] + coef[b * M + row] * to_f32(X[o]));
+                }
+            }
+        }
+    }
+}
+
+template <typename T>
+__global__ void gemm_finish_kernel(const float *__restrict__ part, int64_t splits, int64_t len,
+                                   int64_t M, int64_t N, float sign, const float *__restrict__ coef,
+                                   const T *__restrict__ X, T *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= len) return;
+    float s = part[t];
+    for (int64_t q = 1; q < splits; ++q) s += part[q * len + t];
+    const int64_t row = t / N;  // (b * M + row) flattened
+    from_f32(out + t, sign * s + coef[row] * to_f32(X[t]));
+}
+
+int64_t gemm_splits(int64_t batch, int64_t M, int64_t N, int64_t K) {
+    const int64_t base = cdiv(M, kGT) * cdiv(N, kGT) * batch;
+    int64_t splits = cdiv(512, base);
+    const int64_t by_k = cdiv(K, 256);
+    if (splits > by_k) splits = by_k;
+    if (splits > 16) splits = 16;
+    if (splits < 1) splits = 1;
+    while (splits > 1 && splits * batch > kMaxGridYZ) --splits;
+    return splits;
+}
+
+template <typename T, bool A_T>
+int run_gemm(const float *A, const T *B, int64_t batch, int64_t M, int64_t N, int64_t K,
+             float sign, const float *coef, const T *X, T *out, float *part, hipStream_t s) {
+    const int64_t splits = gemm_splits(batch, M, N, K);
+    const int64_t kps = cdiv(cdiv(K, splits), kGK) * kGK;
+    dim3 grid((unsigned)cdiv(N, kGT), (unsigned)cdiv(M, kGT), (unsigned)(batch * splits));
+    const bool vec = (K % 4 == 0) && (M % 4 == 0) && (N % 4 == 0) && aligned16(A) && aligned16(B);
+    float *dst = splits > 1 ? part : nullptr;
+    if (vec)
+        hipLaunchKernelGGL((bwd_gemm_kernel<T, A_T, true>), grid, dim3(256), 0, s, A, B, M, N, K,
+                           kps, batch, sign, coef, X, out, dst);
+    else
+        hipLaunchKernelGGL((bwd_gemm_kernel<T, A_T, false>), grid, dim3(256), 0, s, A, B, M, N, K,
+                           kps, batch, sign, coef, X, out, dst);
+    int rc = check_launch("bwd_gemm_kernel");
+    if (rc != TPW_OK || splits == 1) return rc;
+    const int64_t len = batch * M * N;
+    hipLaunchKernelGGL((gemm_finish_kernel<T>), dim3((unsigned)cdiv(len, 256)), dim3(256), 0, s,
+                       part, splits, len, M, N, sign, coef, X, out);
+    return check_launch("gemm_finish_kernel");
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct BwdWs {
+    float *W, *rowpart, *colpart, *coef1, *coef2, *part;
+};
+
+BwdWs carve(void *ws, int64_t batch, int64_t n, int64_t m, int64_t d) {
+    char *p = static_cast<char *>(ws);
+    BwdWs w;
+    auto take = [&](size_t bytes) {
+        float *r = reinterpret_cast<float *>(p);
+        p += align256(bytes);
+        return r;
+    };
+    w.W = take(sizeof(float) * batch * n * m);
+    w.rowpart = take(sizeof(float) * batch * cdiv(m, kPWCols) * n);
+    w.colpart = take(sizeof(float) * batch * cdiv(n, kPWRows) * m);
+    w.coef1 = take(sizeof(float) * batch * n);
+    w.coef2 = take(sizeof(float) * batch * m);
+    w.part = reinterpret_cast<float *>(p);
+    return w;
+}
+
+size_t workspace_bytes(int64_t batch, int64_t n, int64_t m, int64_t d) {
+    const int64_t s1 = gemm_splits(batch, n, d, m), s2 = gemm_splits(batch, m, d, n);
+    const int64_t p1 = s1 > 1 ? s1 * batch * n * d : 0, p2 = s2 > 1 ? s2 * batch * m * d : 0;
+    return align256(sizeof(float) * batch * n * m) +
+           align256(sizeof(float) * batch * cdiv(m, kPWCols) * n) +
+           align256(sizeof(float) * batch * cdiv(n, kPWRows) * m) +
+           align256(sizeof(float) * batch * n) + align256(sizeof(float) * batch * m) +
+           sizeof(float) * (p1 > p2 ? p1 : p2);
+}
+
+template <typename T, int MODE>
+int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float *n1,
+                 const float *n2, int dtype, int64_t batch, int64_t n, int64_t m, int64_t d, T *gx1,
+                 T *gx2, void *ws, hipStream_t s) {
+    BwdWs w = carve(ws, batch, n, m, d);
+    int rc;
+    if constexpr (MODE != kEuclid) {
+        rc = inner_dot_f32(x1, x2, dtype, batch, n, m, d, w.W, s);
+        if (rc) return rc;
+    }
+    const int64_t ti = cdiv(n, kPWRows), tj = cdiv(m, kPWCols);
+    hipLaunchKernelGGL((pair_weights_kernel<T, MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
+                       dim3(256), 0, s, g, res, n1, n2, n, m, w.W, w.rowpart, w.colpart, ti, tj);
+    rc = check_launch("pair_weights_kernel");
+    if (rc) return rc;
+    const float *div1 = MODE == kEuclid ? nullptr : n1;
+    const float *div2 = MODE == kEuclid ? nullptr : n2;
+    hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)cdiv(batch * n, 256)), dim3(256), 0, s,
+                       w.rowpart, tj, n, batch, div1, w.coef1);
+    hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)cdiv(batch * m, 256)), dim3(256), 0, s,
+                       w.colpart, ti, m, batch, div2, w.coef2);
+    rc = check_launch("reduce_parts_kernel");
+    if (rc) return rc;
+    const float sign = MODE == kEuclid ? -1.0f : 1.0f;
+    rc = run_gemm<T, false>(w.W, x2, batch, n, d, m, sign, w.coef1, x1, gx1, w.part, s);
+    if (rc) return rc;
+    return run_gemm<T, true>(w.W, x1, batch, m, d, n, sign, w.coef2, x2, gx2, w.part, s);
+}
+
+}  // namespace
+}  // namespace tpw
+
+using namespace tpw;
+
+extern "C" size_t tpw_inner_backward_workspace_size(int64_t batch, int64_t n, int64_t m,
+                                                    int64_t d) {
+    return workspace_bytes(batch, n, m, d);
+}
+
+extern "C" int tpw_euclidean_backward(const void *grad, const void *x1, const void *x2,
+                                      const void *res, int dtype, int64_t batch, int64_t n,
+                                      int64_t m, int64_t d, void *grad_x1, void *grad_x2,
+                                      void *workspace, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    TPW_REQUIRE(grad && x1 && x2 && res && grad_x1 && grad_x2 && workspace, "null pointer");
+    TPW_REQUIRE(cdiv(n, kPWRows) <= kMaxGridYZ && cdiv(m, kGT) <= kMaxGridYZ &&
+                    cdiv(n, kGT) <= kMaxGridYZ && batch <= kMaxGridYZ,
+                "sizes exceed the launch grid");
+    hipStream_t s = as_stream(stream);
+    if (dtype == TPW_F32)
+        return run_backward<float, kEuclid>(
+            static_cast<const float *>(grad), static_cast<const float *>(x1),
+            static_cast<const float *>(x2), static_cast<const float *>(res), nullptr, nullptr,
+            dtype, batch, n, m, d, static_cast<float *>(grad_x1), static_cast<float *>(grad_x2),
+            workspace, s);
+    return run_backward<uint16_t, kEuclid>(
+        static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
+        static_cast<const uint16_t *>(x2), static_cast<const uint16_t *>(res), nullptr, nullptr,
+        dtype, batch, n, m, d, static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2),
+        workspace, s);
+}
+
+extern "C" int tpw_cosine_backward(const void *grad, const void *x1, const void *x2,
+                                   const float *norms1, const float *norms2, int dtype,
+                                   int64_t batch, int64_t n, int64_t m, int64_t d, int similarity,
+                                   void *grad_x1, void *grad_x2, void *workspace, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    TPW_REQUIRE(grad && x1 && x2 && norms1 && norms2 && grad_x1 && grad_x2 && workspace,
+                "null pointer");
+    TPW_REQUIRE(cdiv(n, kPWRows) <= kMaxGridYZ && cdiv(m, kGT) <= kMaxGridYZ &&
+                    cdiv(n, kGT) <= kMaxGridYZ && batch <= kMaxGridYZ,
+                "sizes exceed the launch grid");
+    hipStream_t s = as_stream(stream);
+    if (dtype == TPW_F32) {
+        auto run = similarity ? run_backward<float, kCosSim> : run_backward<float, kCosDist>;
+        return run(static_cast<const float *>(grad), static_cast<const float *>(x1),
+                   static_cast<const float *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
+                   static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s);
+    }
+    auto run = similarity ? run_backward<uint16_t, kCosSim> : run_backward<uint16_t, kCosDist>;
+    return run(static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
+               static_cast<const uint16_t *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
+               static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s);
+}

@@ -1,0 +1,269 @@
+// Bit-packed boolean pairwise reductions (hamming, jaccard, pw{and,or,xor,eq,ne}_{sum,mean}).
+//
+// Layout in HBM: each row of d bools is packed once into W = tpw_packed_words(d) uint32
+// words (zero padding), so a 16384 x 128 bool operand becomes 16384 x 4 words (256 KiB)
+// and stays resident in L2.  The reduction kernel then computes a 128 x 128 output tile
+// per 256-thread block: both word panels are staged in LDS, every thread owns an 8 x 8
+// register block and does one bitwise op plus one v_bcnt_u32_b32 (popcount-accumulate)
+// per word pair.  The float32 output (the only large stream) is written with
+// non-temporal 16-byte stores, 256 contiguous bytes per 16 lanes.
+#include "common.hpp"
+
+namespace tpw {
+namespace {
+
+constexpr int kTile = 128;        // output rows and columns per block
+constexpr int kChunkVec = 4;      // uint4 (4 words) per row and LDS chunk -> 16 words
+constexpr int kThreads = 256;
+constexpr uint32_t kFloatExactLimit = 1u << 24;  // float accumulator of ones saturates here
+
+// 4 bool bytes (each 0 or 1) -> 4 bits, byte t -> bit t.  The multiplier places byte t's
+// bit at position 21 + t; all 16 partial products land on distinct bits (no carries).
+__device__ __forceinline__ uint32_t nibble(uint32_t v) {
+    return (((v & 0x01010101u) * 0x00204081u) >> 21) & 0xFu;
+}
+
+__global__ void pack_bool_kernel(const uint8_t *__restrict__ x, int64_t rows, int64_t d,
+                                 int64_t W, uint32_t *__restrict__ words, bool vec) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows * W) return;
+    int64_t r = t / W, w = t - r * W;
+    int64_t k0 = w * 32;
+    uint32_t word = 0;
+    if (k0 < d) {
+        const uint8_t *p = x + r * d + k0;
+        int64_t cnt = d - k0 < 32 ? d - k0 : 32;
+        if (vec && cnt == 32) {
+            uint4 lo = *reinterpret_cast<const uint4 *>(p);
+            uint4 hi = *reinterpret_cast<const uint4 *>(p + 16);
+            word = nibble(lo.x) | nibble(lo.y) << 4 | nibble(lo.z) << 8 | nibble(lo.w) << 12 |
+                   nibble(hi.x) << 16 | nibble(hi.y) << 20 | nibble(hi.z) << 24 |
+                   nibble(hi.w) << 28;
+        } else {
+            for (int i = 0; i < cnt; ++i) word |= (uint32_t)(p[i] != 0) << i;
+        }
+    }
+    words[t] = word;
+}
+
+__global__ void row_popcount_kernel(const uint32_t *__restrict__ words, int64_t rows,
+                                    int64_t W, int32_t *__restrict__ pops) {
+    int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const uint4 *p = reinterpret_cast<const uint4 *>(words + r * W);
+    uint32_t c = 0;
+    for (int64_t q = 0; q < W / 4; ++q) {
+        uint4 v = p[q];
+        c += __builtin_popcount(v.x) + __builtin_popcount(v.y) + __builtin_popcount(v.z) +
+             __builtin_popcount(v.w);
+    }
+    pops[r] = (int32_t)c;
+}
+
+enum Epi { kSum = 0, kMean = 1, kJaccard = 2 };
+
+template <int OP>
+__device__ __forceinline__ uint32_t bitop(uint32_t a, uint32_t b) {
+    if constexpr (OP == TPW_BIT_AND) return a & b;
+    else if constexpr (OP == TPW_BIT_OR) return a | b;
+    else return a ^ b;  // XOR, NE, and EQ (counted as d - ne)
+}
+
+template <int OP>
+__device__ __forceinline__ uint32_t popacc(uint32_t acc, uint4 a, uint4 b) {
+    acc += __builtin_popcount(bitop<OP>(a.x, b.x));
+    acc += __builtin_popcount(bitop<OP>(a.y, b.y));
+    acc += __builtin_popcount(bitop<OP>(a.z, b.z));
+    acc += __builtin_popcount(bitop<OP>(a.w, b.w));
+    return acc;
+}
+
+// out tile (128 x 128) of batch blockIdx.z.  Thread (ty, tx) owns rows ty + 16 i and
+// columns 64 h + 4 tx + c (i < 8, h < 2, c < 4).
+template <int OP, int EPI>
+__global__ __launch_bounds__(kThreads) void bool_reduce_kernel(
+    const uint32_t *__restrict__ A, const uint32_t *__restrict__ Bw,
+    const int32_t *__restrict__ popA, const int32_t *__restrict__ popB, int64_t n, int64_t m,
+    int64_t W, int64_t d, double inv_d, float *__restrict__ out, bool vec_store) {
+    __shared__ uint4 As[kTile][kChunkVec + 1];
+    __shared__ uint4 Bs[kTile][kChunkVec + 1];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int64_t b = blockIdx.z;
+    const int64_t row0 = (int64_t)blockIdx.y * kTile, col0 = (int64_t)blockIdx.x * kTile;
+    const uint32_t *Ab = A + b * n * W;
+    const uint32_t *Bb = Bw + b * m * W;
+
+    uint32_t acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0;
+
+    for (int64_t w0 = 0; w0 < W; w0 += 4 * kChunkVec) {
+        const int q = (int)((W - w0) / 4 < kChunkVec ? (W - w0) / 4 : kChunkVec);
+        for (int idx = tid; idx < kTile * q; idx += kThreads) {
+            int r = idx / q, c = idx - r * q;
+            int64_t gr = row0 + r, gc = col0 + r;
+            uint4 u = {0u, 0u, 0u, 0u}, v = {0u, 0u, 0u, 0u};
+            if (gr < n) u = *reinterpret_cast<const uint4 *>(Ab + gr * W + w0 + 4 * c);
+            if (gc < m) v = *reinterpret_cast<const uint4 *>(Bb + gc * W + w0 + 4 * c);
+            As[r][c] = u;
+            Bs[r][c] = v;
+        }
+        __syncthreads();
+        for (int c = 0; c < q; ++c) {
+            uint4 a[8], bv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = As[ty + 16 * i][c];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bv[j] = Bs[(j >> 2) * 64 + 4 * tx + (j & 3)][c];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[i][j] = popacc<OP>(acc[i][j], a[i], bv[j]);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t row = row0 + ty + 16 * i;
+        if (row >= n) continue;
+        float *orow = out + (b * n + row) * m;
+        int32_t pa = 0;
+        if constexpr (EPI == kJaccard) pa = popA[b * n + row];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t col = col0 + 64 * h + 4 * tx;
+            float v[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                uint32_t cnt = acc[i][4 * h + c];
+                if constexpr (OP == TPW_BIT_EQ) cnt = (uint32_t)d - cnt;
+                float r;
+                if constexpr (EPI == kSum) {
+                    r = (float)(cnt < kFloatExactLimit ? cnt : kFloatExactLimit);
+                } else if constexpr (EPI == kMean) {
+                    if (inv_d > 0.0) {
+                        // fl32(cnt / d) exactly: the double product is within 2^-52 of
+                        // cnt/d, which is never within 2^-48 of a float rounding midpoint
+                        // for cnt <= d < 2^24, so the final rounding is the correct one.
+                        r = (float)((double)cnt * inv_d);
+                    } else {
+                        r = __fdiv_rn((float)(cnt < kFloatExactLimit ? cnt : kFloatExactLimit),
+                                      (float)d);
+                    }
+                } else {
+                    int64_t cc = col + c;
+                    int32_t pb = cc < m ? popB[b * m + cc] : 0;
+                    uint32_t x = (uint32_t)(pa + pb) - 2u * cnt;
+                    uint32_t o = (uint32_t)(pa + pb) - cnt;
+                    float xf = (float)(x < kFloatExactLimit ? x : kFloatExactLimit);
+                    float of = (float)(o < kFloatExactLimit ? o : kFloatExactLimit);
+                    r = of != 0.0f ? __fdiv_rn(xf, of) : 0.0f;
+                }
+                v[c] = r;
+            }
+            if (vec_store && col + 3 < m) {
+                floatx4 f = {v[0], v[1], v[2], v[3]};
+                store_nt4(orow + col, f);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (col + c < m) store_nt(orow + col + c, v[c]);
+            }
+        }
+    }
+}
+
+template <int OP, int EPI>
+int launch_reduce(const uint32_t *a, const uint32_t *b, const int32_t *pa, const int32_t *pb,
+                  int64_t batch, int64_t n, int64_t m, int64_t d, float *out, hipStream_t s) {
+    const int64_t W = tpw_packed_words(d);
+    dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
+    const double inv_d = d < (int64_t)kFloatExactLimit ? 1.0 / (double)d : 0.0;
+    const bool vec_store = (m % 4 == 0) && aligned16(out);
+    hipLaunchKernelGGL((bool_reduce_kernel<OP, EPI>), grid, dim3(kThreads), 0, s, a, b, pa, pb,
+                       n, m, W, d, inv_d, out, vec_store);
+    return check_launch("bool_reduce_kernel");
+}
+
+int check_reduce_args(const uint32_t *a, const uint32_t *b, int64_t batch, int64_t n, int64_t m,
+                      int64_t d, float *out) {
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 1, "invalid sizes batch=%lld n=%lld m=%lld d=%lld",
+                (long long)batch, (long long)n, (long long)m, (long long)d);
+    TPW_REQUIRE(cdiv(n, kTile) <= kMaxGridYZ && batch <= kMaxGridYZ,
+                "too many rows (n=%lld) or batches (%lld)", (long long)n, (long long)batch);
+    TPW_REQUIRE(d <= (int64_t)0x7fffffff, "d=%lld exceeds the 32-bit count range", (long long)d);
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(a && b && out, "null pointer");
+    TPW_REQUIRE(aligned16(a) && aligned16(b), "packed words must be 16-byte aligned");
+    return TPW_OK;
+}
+
+}  // namespace
+}  // namespace tpw
+
+using namespace tpw;
+
+extern "C" int64_t tpw_packed_words(int64_t d) { return ((d + 31) / 32 + 3) / 4 * 4; }
+
+extern "C" int tpw_pack_bool_rows(const uint8_t *x, int64_t rows, int64_t d, uint32_t *words,
+                                  int32_t *row_popcounts, void *stream) {
+    TPW_REQUIRE(rows >= 0 && d >= 1, "invalid sizes rows=%lld d=%lld", (long long)rows,
+                (long long)d);
+    if (rows == 0) return TPW_OK;
+    TPW_REQUIRE(x && words, "null pointer");
+    TPW_REQUIRE(aligned16(words), "words must be 16-byte aligned");
+    const int64_t W = tpw_packed_words(d);
+    const bool vec = (d % 16 == 0) && aligned16(x);
+    const int64_t total = rows * W;
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(pack_bool_kernel, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, x,
+                       rows, d, W, words, vec);
+    int rc = check_launch("pack_bool_kernel");
+    if (rc != TPW_OK || !row_popcounts) return rc;
+    hipLaunchKernelGGL(row_popcount_kernel, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, s,
+                       words, rows, W, row_popcounts);
+    return check_launch("row_popcount_kernel");
+}
+
+extern "C" int tpw_bool_pairwise_reduce(const uint32_t *x1w, const uint32_t *x2w, int64_t batch,
+                                        int64_t n, int64_t m, int64_t d, int op, int reduction,
+                                        float *out, void *stream) {
+    int rc = check_reduce_args(x1w, x2w, batch, n, m, d, out);
+    if (rc != TPW_OK) return rc;
+    TPW_REQUIRE(op >= TPW_BIT_AND && op <= TPW_BIT_NE, "unknown bit op %d", op);
+    TPW_REQUIRE(reduction == TPW_RED_SUM || reduction == TPW_RED_MEAN, "unknown reduction %d",
+                reduction);
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    hipStream_t s = as_stream(stream);
+#define TPW_CASE(OPC)                                                                         \
+    case OPC:                                                                                 \
+        return reduction == TPW_RED_SUM                                                       \
+                   ? launch_reduce<OPC, kSum>(x1w, x2w, nullptr, nullptr, batch, n, m, d, out, s) \
+                   : launch_reduce<OPC, kMean>(x1w, x2w, nullptr, nullptr, batch, n, m, d, out, s);
+    switch (op) {
+        TPW_CASE(TPW_BIT_AND)
+        TPW_CASE(TPW_BIT_OR)
+        TPW_CASE(TPW_BIT_XOR)
+        TPW_CASE(TPW_BIT_EQ)
+        default:
+            // NE counts exactly like XOR on bits
+            return reduction == TPW_RED_SUM
+                       ? launch_reduce<TPW_BIT_XOR, kSum>(x1w, x2w, nullptr, nullptr, batch, n, m, d, out, s)
+                       : launch_reduce<TPW_BIT_XOR, kMean>(x1w, x2w, nullptr, nullptr, batch, n, m, d, out, s);
+    }
+#undef TPW_CASE
+}
+
+extern "C" int tpw_jaccard_bool(const uint32_t *x1w, const uint32_t *x2w, const int32_t *pop1,
+                                const int32_t *pop2, int64_t batch, int64_t n, int64_t m,
+                                int64_t d, float *out, void *stream) {
+    int rc = check_reduce_args(x1w, x2w, batch, n, m, d, out);
+    if (rc != TPW_OK) return rc;
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(pop1 && pop2, "null popcount pointer");
+    return launch_reduce<TPW_BIT_AND, kJaccard>(x1w, x2w, pop1, pop2, batch, n, m, d, out,
+                                                as_stream(stream));
+}

@@ -2,10 +2,11 @@
 """Benchmark of the torchpairwise hot path on one MI355X.
 
 Workload (BASELINE.json metric): x1, x2 = [16384, 128] fp32 (torch.randn from CPU generators
-seeded 0 and 1, moved to HBM before timing).  One step = one pass of the hot path over that
-batch; the headline is euclidean_distances (the MFMA kernel), with manhattan_distances (VALU)
-and hamming_distances on bool inputs (rand < 0.5, packed once per call) timed the same way
-and reported under "extra".
+seeded 0 and 1, moved to HBM before timing).  One step = one call of the drop-in op
+(torchpairwise_amd.<metric>, i.e. torch.ops.torchpairwise.<metric>) over that batch; the
+headline is euclidean_distances (the MFMA kernel), with manhattan_distances (VALU) and
+hamming_distances on bool inputs (rand < 0.5; the op packs the bits inside every call) timed
+the same way and reported under "extra".
 
 value = pair-features/s (N*M*D per call / mean call time over the timed steps), inputs
 resident in HBM.  Timing: W untimed warm-up steps, then K steps between two
@@ -97,7 +98,7 @@ def main():
         sys.exit(2)
     import torch
 
-    from torchpairwise_amd import _capi as capi
+    import torchpairwise_amd as tp
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = "cuda"
@@ -114,15 +115,14 @@ def main():
     res = {}
 
     if "l2" in only:
-        ms, wall_ms = time_op(lambda: capi.pairwise_inner(x1, x2, capi.EPI_EUCLIDEAN),
-                              args.steps, args.warmup)
+        ms, wall_ms = time_op(lambda: tp.euclidean_distances(x1, x2), args.steps, args.warmup)
         flops = 2.0 * n * n * d
         res["l2"] = {"ms": ms, "wall_ms": wall_ms, "value": pf / (ms * 1e-3),
                      "roofline": {"bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12,
                                   "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                                   "frac": flops / (ms * 1e-3) / PEAK_FP32_MFMA, "traffic": None}}
     if "l1" in only:
-        ms, wall_ms = time_op(lambda: capi.lp_distances(x1, x2, 1.0), args.steps, args.warmup)
+        ms, wall_ms = time_op(lambda: tp.manhattan_distances(x1, x2), args.steps, args.warmup)
         ops = 2.0 * pf  # v_sub + abs-modified v_add per pair-feature
         extra["manhattan_fp32"] = {
             "value": pf / (ms * 1e-3), "ms_per_call": ms,
@@ -132,8 +132,7 @@ def main():
                          "convention": "2 VALU lane-ops per pair-feature (sub, abs-add) against "
                                        "the non-packed issue rate 256 CU x 64 lanes x 2.4 GHz"}}
     if "hamming" in only:
-        ms, wall_ms = time_op(lambda: capi.bool_pairwise_reduce(b1, b2, capi.BIT_NE, capi.RED_MEAN),
-                              args.steps, args.warmup)
+        ms, wall_ms = time_op(lambda: tp.hamming_distances(b1, b2), args.steps, args.warmup)
         out_bytes = 4.0 * n * n
         extra["hamming_bool"] = {
             "value": pf / (ms * 1e-3), "ms_per_call": ms,

@@ -34,9 +34,17 @@ extern "C" {
 #define TPW_ERR_INVALID 1 /* bad argument (shape, dtype, alignment, null pointer) */
 #define TPW_ERR_LAUNCH 2  /* the HIP runtime rejected a launch */
 
-/* element types accepted by the floating-point entry points */
+/* element types (TPW_F32 / TPW_BF16 for the floating-point kernels; all of them for
+ * tpw_compare_reduce) */
 #define TPW_F32 0
 #define TPW_BF16 1
+#define TPW_F16 2
+#define TPW_F64 3
+#define TPW_I8 4
+#define TPW_U8 5
+#define TPW_I16 6
+#define TPW_I32 7
+#define TPW_I64 8
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *tpw_last_error(void);
@@ -94,6 +102,16 @@ int tpw_jaccard_bool(const uint32_t *x1_words, const uint32_t *x2_words,
                      const int32_t *x1_popcounts, const int32_t *x2_popcounts,
                      int64_t batch, int64_t n, int64_t m, int64_t d, float *out,
                      void *stream);
+
+/* Equal / not-equal counts (TPW_BIT_EQ / TPW_BIT_NE, TPW_RED_SUM / TPW_RED_MEAN) of
+ * non-bool inputs of element type `elem_type` (TPW_F32 ... TPW_I64), compared by value
+ * like C++ ==; output float32 [batch, n, m] as tpw_bool_pairwise_reduce.
+ * Replaces pairwise_binary_reduction_forward_kernel<Equal|NotEqual, Sum|Mean> for
+ * non-bool dtypes (csrc/ops/cuda/pairwise_binary_kernels.cu:32-53,144-220), which
+ * hamming_distances reaches without a bool coercion (csrc/ops/pairwise_metrics.cpp:206-213). */
+int tpw_compare_reduce(const void *x1, const void *x2, int elem_type, int64_t batch,
+                       int64_t n, int64_t m, int64_t d, int op, int reduction, float *out,
+                       void *stream);
 
 /* ------------------------------------------------------------------------- */
 /* Inner-product family (MFMA): euclidean, sqeuclidean, cosine, linear        */
@@ -171,6 +189,14 @@ int tpw_euclidean_backward(const void *grad, const void *x1, const void *x2,
                            int64_t m, int64_t d, void *grad_x1, void *grad_x2,
                            void *workspace, void *stream);
 
+/* Backward of sqeuclidean_distances (sum_k (x1 - x2)^2): grad_x1 = x1 * sum_j 2 grad -
+ * (2 grad) @ x2, grad_x2 = x2 * sum_i 2 grad - (2 grad)^T @ x1, i.e. the p = 2 case of
+ * _ppminkowski's backward g p |d|^(p-1) sign(d) (csrc/ops/cpu/ppminkowski_kernel.cpp:122-169)
+ * summed over the other operand. */
+int tpw_sqeuclidean_backward(const void *grad, const void *x1, const void *x2, int dtype,
+                             int64_t batch, int64_t n, int64_t m, int64_t d, void *grad_x1,
+                             void *grad_x2, void *workspace, void *stream);
+
 /* Backward of cosine_distances = clip(1 - prf_div(x1 x2^T, n1 n2^T, identity), 0, 2):
  * the autograd graph of csrc/ops/pairwise_metrics.cpp:51-56,112-122 with the prf_div
  * backward of csrc/ops/cpu/prf_div_kernel.cpp:258-277, the clamp mask of
@@ -182,6 +208,24 @@ int tpw_cosine_backward(const void *grad, const void *x1, const void *x2,
                         const float *norms1, const float *norms2, int dtype,
                         int64_t batch, int64_t n, int64_t m, int64_t d, int similarity,
                         void *grad_x1, void *grad_x2, void *workspace, void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* prf_div (guarded divide)                                                   */
+/* ------------------------------------------------------------------------- */
+
+/* out = y != 0 ? x / y : (identity ? x : 0), elementwise over `numel` elements of type
+ * TPW_F32 / TPW_F64 / TPW_F16 / TPW_BF16 (half types round after each operation).
+ * Replaces prf_div_forward_kernel (csrc/ops/cpu/prf_div_kernel.cpp:14-54,57-;
+ * CUDA csrc/ops/cuda/prf_div_kernel.cu:22-133) with mode "zero" / "identity". */
+int tpw_prf_div(const void *x, const void *y, int dtype, int64_t numel, int identity,
+                void *out, void *stream);
+
+/* grad_x = y != 0 ? g / y : (identity ? g : 0); grad_y = y != 0 ? (g / y) * -x / y : 0.
+ * Replaces prf_div_backward_kernel (csrc/ops/cpu/prf_div_kernel.cpp:258-277;
+ * CUDA csrc/ops/cuda/prf_div_kernel.cu:315-368). */
+int tpw_prf_div_backward(const void *grad, const void *x, const void *y, int dtype,
+                         int64_t numel, int identity, void *grad_x, void *grad_y,
+                         void *stream);
 
 /* ------------------------------------------------------------------------- */
 /* Directed Hausdorff                                                         */

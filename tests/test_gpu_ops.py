@@ -1,0 +1,201 @@
+"""GPU parity of the drop-in ops (torch.ops.torchpairwise on cuda tensors) against the oracle:
+forward values, gradients through autograd, and that the HIP library is what runs."""
+import numpy as np
+import pytest
+import torch
+
+import torchpairwise_amd as tp
+from oracle import cref
+from oracle import pairwise as P
+from tests._util import assert_close, assert_equal, rand, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def test_native_library_is_loaded():
+    maps = open("/proc/self/maps").read()
+    assert "libtorchpairwise_hip.so" in maps and "torchpairwise_amd/_C.so" in maps
+
+
+@pytest.mark.parametrize("shape", [((300, 64), (200, 64)), ((2, 130, 128), (2, 90, 128)),
+                                   ((10, 16), (20, 16)), ((1, 40, 8), (3, 30, 8))])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_euclidean_forward_backward(shape, dtype):
+    x1 = randn(*shape[0], seed=0, dtype=dtype)
+    x2 = randn(*shape[1], seed=1, dtype=dtype)
+    a = x1.to(DEV).requires_grad_()
+    b = x2.to(DEV).requires_grad_()
+    out = tp.euclidean_distances(a, b)
+    g = randn(*out.shape, seed=2, dtype=dtype)
+    out.backward(g.to(DEV))
+    ra, rb = x1.double().requires_grad_(), x2.double().requires_grad_()
+    ref = torch.cdist(ra, rb, 2)
+    ref.backward(g.double())
+    rtol = 1e-5 if dtype == torch.float32 else 1e-2
+    grtol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert out.dtype == dtype
+    assert_close(out.float(), ref, rtol=rtol, atol=rtol * float(ref.abs().max()), what="euclidean")
+    assert_close(a.grad.float(), ra.grad, rtol=grtol, atol=grtol * float(ra.grad.abs().max()), what="grad x1")
+    assert_close(b.grad.float(), rb.grad, rtol=grtol, atol=grtol * float(rb.grad.abs().max()), what="grad x2")
+
+
+def test_euclidean_self_pair_grad():
+    x = randn(200, 32, seed=0)
+    a = x.to(DEV).requires_grad_()
+    out = tp.euclidean_distances(a)
+    g = randn(200, 200, seed=2)
+    out.backward(g.to(DEV))
+    ra = x.double().requires_grad_()
+    ref = torch.cdist(ra, ra, 2)
+    ref.backward(g.double())
+    # diagonal: the reference's ratio uses res == 0 masking; away from it both agree
+    assert_close(a.grad, ra.grad, rtol=1e-3, atol=1e-3 * float(ra.grad.abs().max()), what="self grad")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("fn", ["cosine_distances", "cosine_similarity", "correlation_distances"])
+def test_cosine_family(dtype, fn):
+    x1 = randn(2, 150, 256, seed=0, dtype=dtype)
+    x2 = randn(2, 100, 256, seed=1, dtype=dtype)
+    a = x1.to(DEV).requires_grad_()
+    b = x2.to(DEV).requires_grad_()
+    out = getattr(tp, fn)(a, b)
+    g = randn(*out.shape, seed=2, dtype=dtype)
+    out.backward(g.to(DEV))
+    ra, rb = x1.double().requires_grad_(), x2.double().requires_grad_()
+    if fn == "correlation_distances":
+        ca, cb = ra - ra.mean(-1, keepdim=True), rb - rb.mean(-1, keepdim=True)
+        ref = 1 - P.cosine_similarity(ca, cb)
+    else:
+        ref = getattr(P, fn)(ra, rb)
+    ref.backward(g.double())
+    rtol = 1e-5 if dtype == torch.float32 else 1e-2
+    grtol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert_close(out.float(), ref, rtol=rtol, atol=rtol * float(ref.abs().max()) + 1e-6, what=fn)
+    assert_close(a.grad.float(), ra.grad, rtol=grtol, atol=grtol * float(ra.grad.abs().max()), what="grad x1")
+    assert_close(b.grad.float(), rb.grad, rtol=grtol, atol=grtol * float(rb.grad.abs().max()), what="grad x2")
+
+
+def test_sqeuclidean_forward_backward():
+    x1, x2 = randn(130, 64, seed=0), randn(70, 64, seed=1)
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    out = tp.sqeuclidean_distances(a, b)
+    g = randn(130, 70, seed=2)
+    out.backward(g.to(DEV))
+    ra, rb = x1.double().requires_grad_(), x2.double().requires_grad_()
+    ref = ((ra[:, None, :] - rb[None, :, :]) ** 2).sum(-1)
+    ref.backward(g.double())
+    assert_close(out, ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()), what="sqeuclidean")
+    assert_close(a.grad, ra.grad, rtol=1e-4, atol=1e-4 * float(ra.grad.abs().max()), what="grad x1")
+    assert_close(b.grad, rb.grad, rtol=1e-4, atol=1e-4 * float(rb.grad.abs().max()), what="grad x2")
+
+
+@pytest.mark.parametrize("fn,p", [("manhattan_distances", 1.0), ("chebyshev_distances", float("inf")),
+                                  ("minkowski_distances", 3.0), ("minkowski_distances", 1.5),
+                                  ("linf_distances", float("inf")), ("l1_distances", 1.0)])
+def test_minkowski_family(fn, p):
+    x1 = rand(2, 130, 128, seed=0) * 2 - 1
+    x2 = rand(2, 77, 128, seed=1) * 2 - 1
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    out = getattr(tp, fn)(a, b, p) if fn == "minkowski_distances" else getattr(tp, fn)(a, b)
+    g = torch.ones(out.shape)
+    out.backward(g.to(DEV))
+    ra, rb = x1.double().requires_grad_(), x2.double().requires_grad_()
+    ref = torch.cdist(ra, rb, p)
+    ref.backward(g.double())
+    assert_close(out, ref, rtol=1e-5, atol=1e-6 * float(ref.abs().max()), what=fn)
+    assert_close(a.grad, ra.grad, rtol=1e-4, atol=1e-5 * float(ra.grad.abs().max()) + 1e-6, what="grad x1")
+    assert_close(b.grad, rb.grad, rtol=1e-4, atol=1e-5 * float(rb.grad.abs().max()) + 1e-6, what="grad x2")
+
+
+def test_small_euclidean_uses_direct_sum():
+    # <= 25 rows on both sides: at::cdist's direct path (exact zeros on the diagonal)
+    x = randn(20, 16, seed=0)
+    out = tp.euclidean_distances(x.to(DEV))
+    assert torch.all(out.diagonal() == 0)
+    assert_close(out, torch.cdist(x.double(), x.double()), rtol=1e-5, atol=1e-6, what="small euclidean")
+
+
+@pytest.mark.parametrize("shape", [((2, 300, 1024), (2, 200, 1024)), ((130, 77), (257, 77))])
+def test_boolean_metrics_bit_exact(shape):
+    b1 = rand(*shape[0], seed=0) < 0.5
+    b2 = rand(*shape[1], seed=1) < 0.1
+    assert_equal(tp.hamming_distances(b1.to(DEV), b2.to(DEV)),
+                 torch.from_numpy(P.hamming_distances(b1.numpy(), b2.numpy())), "hamming")
+    assert_equal(tp.jaccard_distances(b1.to(DEV), b2.to(DEV)),
+                 torch.from_numpy(P.jaccard_distances(b1.numpy(), b2.numpy())), "jaccard")
+    for name in ("pwand_sum", "pwor_sum", "pwxor_sum", "pweq_sum", "pwne_sum", "pweq_mean", "pwne_mean"):
+        got = getattr(tp, name)(b1.to(DEV), b2.to(DEV))
+        assert_equal(got, getattr(tp, name)(b1, b2), name)
+
+
+@pytest.mark.parametrize("dtype", [torch.int64, torch.int32, torch.float32, torch.float16, torch.uint8])
+def test_hamming_non_bool(dtype):
+    g = torch.Generator().manual_seed(0)
+    x1 = torch.randint(0, 3, (70, 33), generator=g).to(dtype)
+    x2 = torch.randint(0, 3, (50, 33), generator=g).to(dtype)
+    got = tp.hamming_distances(x1.to(DEV), x2.to(DEV))
+    assert_equal(got, torch.from_numpy(P.hamming_distances(x1.numpy(), x2.numpy())), f"hamming {dtype}")
+
+
+@pytest.mark.parametrize("name", ["dice", "rogerstanimoto", "russellrao", "sokalmichener",
+                                  "sokalsneath", "yule", "kulczynski1"])
+def test_boolean_family_gpu_equals_cpu(name):
+    b1 = rand(60, 100, seed=0) < 0.5
+    b2 = rand(50, 100, seed=1) < 0.5
+    fn = getattr(tp, f"{name}_distances")
+    assert_equal(fn(b1.to(DEV), b2.to(DEV)), fn(b1, b2), name)
+
+
+def test_prf_div_gpu():
+    x = randn(1000, seed=0)
+    y = randn(1000, seed=1)
+    y[::7] = 0
+    for mode in ("zero", "identity"):
+        assert_equal(tp.prf_div(x.to(DEV), y.to(DEV), mode), tp.prf_div(x, y, mode), mode)
+        a, b = x.to(DEV).requires_grad_(), y.to(DEV).requires_grad_()
+        tp.prf_div(a, b, mode).sum().backward()
+        ca, cb = x.clone().requires_grad_(), y.clone().requires_grad_()
+        tp.prf_div(ca, cb, mode).sum().backward()
+        assert_equal(a.grad, ca.grad, f"grad self {mode}")
+        assert_equal(b.grad, cb.grad, f"grad other {mode}")
+
+
+def test_hausdorff_ops_bit_exact_and_grad():
+    c1, c2 = rand(2, 400, 3, seed=0), rand(3, 300, 3, seed=1) + 0.05
+    a = c1.to(DEV).requires_grad_()
+    b = c2.to(DEV).requires_grad_()
+    out, i1, i2 = tp.directed_hausdorff_distances(a, b)
+    w = cref.directed_hausdorff(c1.numpy(), c2.numpy())
+    for got, want, nm in zip((out, i1, i2), w, ("value", "idx1", "idx2")):
+        assert_equal(got, torch.from_numpy(want), nm)
+    g = randn(2, 3, seed=5)
+    out.backward(g.to(DEV))
+    ca, cb = c1.clone().requires_grad_(), c2.clone().requires_grad_()
+    tp.directed_hausdorff_distances(ca, cb)[0].backward(g)
+    assert_equal(a.grad, ca.grad, "grad x1 (GPU vs CPU op)")
+    assert_equal(b.grad, cb.grad, "grad x2 (GPU vs CPU op)")
+
+
+def test_hausdorff_shuffle_generator_replay():
+    c1, c2 = rand(2, 2, 200, 3, seed=0), rand(2, 2, 250, 3, seed=1)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    out, i1, i2 = tp.directed_hausdorff_distances(c1.to(DEV), c2.to(DEV), shuffle=True, generator=gen)
+    gen2 = torch.Generator(device=DEV).manual_seed(3)
+    perm1 = torch.empty((2, 200), dtype=torch.int64, device=DEV)
+    perm2 = torch.empty((2, 250), dtype=torch.int64, device=DEV)
+    for bb in range(2):
+        torch.randperm(200, generator=gen2, out=perm1[bb])
+        torch.randperm(250, generator=gen2, out=perm2[bb])
+    w = cref.directed_hausdorff(c1.numpy(), c2.numpy(), perm1.cpu().numpy(), perm2.cpu().numpy())
+    for got, want, nm in zip((out, i1, i2), w, ("value", "idx1", "idx2")):
+        assert_equal(got, torch.from_numpy(want), f"shuffled {nm}")
+
+
+def test_empty_inputs():
+    e = torch.zeros((0, 8), device=DEV)
+    x = torch.randn(5, 8, device=DEV)
+    assert tp.euclidean_distances(e, x).shape == (0, 5)
+    assert tp.manhattan_distances(x, e).shape == (5, 0)
+    assert tp.hamming_distances(e > 0, x > 0).shape == (0, 5)

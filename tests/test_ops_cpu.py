@@ -1,0 +1,135 @@
+"""The drop-in op layer without a GPU: schemas, CPU paths (the reference's routes), errors,
+TorchScript, autograd on CPU."""
+import warnings
+
+import numpy as np
+import pytest
+import torch
+from scipy.spatial.distance import cdist as scipy_cdist
+
+import torchpairwise_amd as tp
+from oracle import cref
+from oracle import pairwise as P
+from tests._util import assert_close, assert_equal, rand, randn
+
+PUBLIC = [
+    "euclidean_distances", "haversine_distances", "manhattan_distances", "cosine_distances",
+    "linear_kernel", "polynomial_kernel", "sigmoid_kernel", "rbf_kernel", "laplacian_kernel",
+    "cosine_similarity", "additive_chi2_kernel", "chi2_kernel", "directed_hausdorff_distances",
+    "minkowski_distances", "wminkowski_distances", "sqeuclidean_distances",
+    "correlation_distances", "hamming_distances", "jaccard_distances", "kulsinski_distances",
+    "kulczynski1_distances", "seuclidean_distances", "cityblock_distances",
+    "mahalanobis_distances", "chebyshev_distances", "braycurtis_distances",
+    "canberra_distances", "jensenshannon_distances", "yule_distances", "dice_distances",
+    "rogerstanimoto_distances", "russellrao_distances", "sokalmichener_distances",
+    "sokalsneath_distances", "snr_distances", "l1_distances", "l2_distances", "lp_distances",
+    "linf_distances",
+]
+
+
+def test_public_schemas_registered():
+    for name in PUBLIC:
+        op = getattr(torch.ops.torchpairwise, name)
+        assert op is getattr(tp, name)
+    s = str(torch.ops.torchpairwise.directed_hausdorff_distances.default._schema)
+    assert s == ("torchpairwise::directed_hausdorff_distances(Tensor x1, Tensor? x2=None, *, "
+                 "bool shuffle=False, Generator? generator=None) -> (Tensor output, "
+                 "Tensor x1_indices, Tensor x2_indices)")
+    s = str(torch.ops.torchpairwise.polynomial_kernel.default._schema)
+    assert s == ("torchpairwise::polynomial_kernel(Tensor x1, Tensor? x2=None, int degree=3, "
+                 "float? gamma=None, float coef0=1.) -> Tensor")
+
+
+def test_meta_ops():
+    assert tp.has_ops()
+    assert tp.cuda_version() > 0 and tp.with_cuda()
+    assert tp.cuda_arch_list() == ["gfx950"]
+
+
+@pytest.mark.parametrize("p", [0.0, 1.0, 1.5, 2.0, 3.0, float("inf")])
+def test_cdist_family_cpu_is_aten(p):
+    x1, x2 = randn(40, 9, seed=0, dtype=torch.float64), randn(30, 9, seed=1, dtype=torch.float64)
+    got = tp.minkowski_distances(x1, x2, p)
+    assert_equal(got, torch.cdist(x1, x2, p), f"minkowski p={p}")
+    want = scipy_cdist(x1.numpy(), x2.numpy(), "minkowski", p=p) if p not in (0.0, float("inf")) else None
+    if want is not None:
+        assert_close(got, torch.from_numpy(want), rtol=1e-12, atol=1e-12, what="vs scipy")
+
+
+def test_cosine_cpu_matches_sklearn():
+    from sklearn.metrics.pairwise import cosine_distances
+
+    x1, x2 = randn(40, 9, seed=0, dtype=torch.float64), randn(30, 9, seed=1, dtype=torch.float64)
+    assert_close(tp.cosine_distances(x1, x2), torch.from_numpy(cosine_distances(x1.numpy(), x2.numpy())),
+                 rtol=1e-12, atol=1e-12, what="cosine")
+
+
+def test_boolean_cpu_bit_exact():
+    b1, b2 = rand(2, 30, 77, seed=0) < 0.5, rand(2, 20, 77, seed=1) < 0.5
+    assert_equal(tp.hamming_distances(b1, b2), torch.from_numpy(P.hamming_distances(b1.numpy(), b2.numpy())))
+    assert_equal(tp.jaccard_distances(b1, b2), torch.from_numpy(P.jaccard_distances(b1.numpy(), b2.numpy())))
+    i1 = torch.randint(0, 3, (30, 11), generator=torch.Generator().manual_seed(3))
+    i2 = torch.randint(0, 3, (20, 11), generator=torch.Generator().manual_seed(4))
+    assert_equal(tp.hamming_distances(i1, i2), torch.from_numpy(P.hamming_distances(i1.numpy(), i2.numpy())))
+
+
+@pytest.mark.parametrize("name", ["dice", "rogerstanimoto", "russellrao", "sokalmichener", "yule"])
+def test_boolean_family_cpu_vs_scipy(name):
+    b1, b2 = rand(30, 64, seed=0) < 0.5, rand(20, 64, seed=1) < 0.5
+    got = getattr(tp, f"{name}_distances")(b1, b2)
+    want = scipy_cdist(b1.numpy(), b2.numpy(), name)
+    assert_close(got, torch.from_numpy(want), rtol=1e-6, atol=1e-7, what=name)
+
+
+def test_boolean_coercion_warns(capfd):
+    # TORCH_WARN from a dispatcher op reaches the c10 log (stderr), as in the reference
+    x = torch.randint(0, 2, (5, 8))
+    with warnings.catch_warnings(record=True) as rec:
+        warnings.simplefilter("always")
+        tp.jaccard_distances(x, x)
+    text = capfd.readouterr().err + " ".join(str(r.message) for r in rec)
+    assert "converted to Bool" in text
+
+
+def test_hausdorff_cpu_bit_exact_and_gradcheck():
+    c1, c2 = rand(2, 60, 3, seed=0), rand(3, 50, 3, seed=1) + 0.05
+    got = tp.directed_hausdorff_distances(c1, c2)
+    want = cref.directed_hausdorff(c1.numpy(), c2.numpy())
+    for g, w in zip(got, want):
+        assert_equal(g, torch.from_numpy(w))
+    a = c1.double().requires_grad_()
+    b = c2.double().requires_grad_()
+    assert torch.autograd.gradcheck(lambda u, v: tp.directed_hausdorff_distances(u, v)[0], (a, b))
+    gen = torch.Generator().manual_seed(7)
+    assert torch.autograd.gradcheck(
+        lambda u: tp.directed_hausdorff_distances(u, b, shuffle=True, generator=gen)[0], (a,))
+
+
+def test_prf_div_cpu():
+    x = torch.tensor([1.0, 2.0, 3.0, 4.0])
+    y = torch.tensor([2.0, 0.0, 4.0, 0.0])
+    assert_equal(tp.prf_div(x, y), torch.tensor([0.5, 0.0, 0.75, 0.0]))
+    assert_equal(tp.prf_div(x, y, "identity"), torch.tensor([0.5, 2.0, 0.75, 4.0]))
+    with pytest.raises(RuntimeError, match="mode must be either zero or identity"):
+        tp.prf_div(x, y, "bad")
+    xd, yd = x.double().requires_grad_(), (y.double() + 0.5).requires_grad_()
+    assert torch.autograd.gradcheck(lambda a, b: tp.prf_div(a, b, "identity"), (xd, yd))
+
+
+def test_input_errors():
+    with pytest.raises(RuntimeError, match="x1 must be 2D tensor"):
+        tp.euclidean_distances(torch.randn(3))
+    with pytest.raises(RuntimeError, match="same number of features"):
+        tp.euclidean_distances(torch.randn(3, 4), torch.randn(3, 5))
+    with pytest.raises(NotImplementedError, match="not implemented by this MI355X build"):
+        tp.haversine_distances(torch.randn(3, 2))
+
+
+def _scripted(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    return torch.ops.torchpairwise.euclidean_distances(a, b) + torch.ops.torchpairwise.hamming_distances(a > 0, b > 0)
+
+
+def test_torchscript_binds_schemas():
+    f = torch.jit.script(_scripted)
+    a, b = randn(10, 4, seed=0), randn(8, 4, seed=1)
+    assert_close(f(a, b), _scripted(a, b), rtol=0, atol=0, what="scripted")

@@ -5,7 +5,8 @@
 * ``_C.so`` — the PyTorch extension that registers the ``torch.ops.torchpairwise``
   schemas and calls the C ABI (g++ against the installed torch headers).
 
-Run ``python -m torchpairwise_amd._build`` or call :func:`build_all`.
+Run ``python torchpairwise_amd/_build.py [hip|ext|all]`` (by path: importing the package
+needs the built libraries) or call :func:`build_all`.
 """
 from __future__ import annotations
 
@@ -85,7 +86,7 @@ def build_torch_ext(verbose: bool = True) -> Path | None:
     inc, libdir, abi = _torch_paths()
     py_inc = sysconfig.get_paths()["include"]
     flags = [
-        "-O2", "-std=c++17", "-fPIC", "-fopenmp", "-Wno-unused-parameter",
+        "-O2", "-std=c++17", "-fPIC", "-fopenmp", "-ffp-contract=off", "-Wno-unused-parameter",
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
         "-DTORCH_EXTENSION_NAME=_C", *[f"-I{p}" for p in inc], f"-I{py_inc}",
         "-I/opt/rocm/include", f"-I{INCLUDE}", f"-I{OPS_SRC}",

@@ -15,7 +15,7 @@ _PKG = Path(__file__).resolve().parent
 LIB_PATH = _PKG / "libtorchpairwise_hip.so"
 HEADER = _PKG.parent / "include" / "torchpairwise_amd.h"
 
-TPW_F32, TPW_BF16 = 0, 1
+TPW_F32, TPW_BF16, TPW_F16, TPW_F64, TPW_I8, TPW_U8, TPW_I16, TPW_I32, TPW_I64 = range(9)
 BIT_AND, BIT_OR, BIT_XOR, BIT_EQ, BIT_NE = 0, 1, 2, 3, 4
 RED_SUM, RED_MEAN = 0, 1
 EPI_DOT, EPI_EUCLIDEAN, EPI_SQEUCLIDEAN, EPI_COSINE_SIM, EPI_COSINE_DIST = 0, 1, 2, 3, 4
@@ -29,6 +29,7 @@ _SIGNATURES = {
     "tpw_pack_bool_rows": (_i, [_p, _i64, _i64, _p, _p, _p]),
     "tpw_bool_pairwise_reduce": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_jaccard_bool": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "tpw_compare_reduce": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_row_norms": (_i, [_p, _i, _i64, _i64, _i, _p, _p]),
     "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),
     "tpw_lp_distances": (_i, [_p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
@@ -36,7 +37,10 @@ _SIGNATURES = {
     "tpw_lp_distances_backward": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _i, _p, _p, _p]),
     "tpw_inner_backward_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "tpw_euclidean_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "tpw_sqeuclidean_backward": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "tpw_cosine_backward": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p]),
+    "tpw_prf_div": (_i, [_p, _p, _i, _i64, _i, _p, _p]),
+    "tpw_prf_div_backward": (_i, [_p, _p, _p, _i, _i64, _i, _p, _p, _p]),
     "tpw_hausdorff_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "tpw_directed_hausdorff": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "tpw_directed_hausdorff_backward": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),
@@ -142,6 +146,49 @@ def jaccard_bool(x1, x2):
     out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
     call("tpw_jaccard_bool", _ptr(wa), _ptr(wb), _ptr(pa), _ptr(pb), B, n, m, d, _ptr(out), _stream())
     return out if x1.dim() == 3 else out[0]
+
+
+_ELEM_CODES = None
+
+
+def elem_code(dtype):
+    import torch
+
+    global _ELEM_CODES
+    if _ELEM_CODES is None:
+        _ELEM_CODES = {torch.float32: TPW_F32, torch.bfloat16: TPW_BF16, torch.float16: TPW_F16,
+                       torch.float64: TPW_F64, torch.int8: TPW_I8, torch.uint8: TPW_U8,
+                       torch.int16: TPW_I16, torch.int32: TPW_I32, torch.int64: TPW_I64}
+    return _ELEM_CODES[dtype]
+
+
+def compare_reduce(x1, x2, op, reduction):
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    call("tpw_compare_reduce", _ptr(a), _ptr(b), elem_code(a.dtype), B, n, m, d, op, reduction,
+         _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def sqeuclidean_backward(grad, x1, x2):
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    g = _as3(grad).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    ws = torch.empty((lib().tpw_inner_backward_workspace_size(B, n, m, d),), dtype=torch.uint8,
+                     device=a.device)
+    call("tpw_sqeuclidean_backward", _ptr(g), _ptr(a), _ptr(b), _dtype_code(a), B, n, m, d,
+         _ptr(gx1), _ptr(gx2), _ptr(ws), _stream())
+    if x1.dim() == 2:
+        return gx1[0], gx2[0]
+    return gx1, gx2
 
 
 def row_norms(x, squared):

@@ -23,7 +23,7 @@
 namespace tpw {
 namespace {
 
-enum Mode { kEuclid = 0, kCosDist = 1, kCosSim = 2 };
+enum Mode { kEuclid = 0, kCosDist = 1, kCosSim = 2, kSqEuclid = 3 };
 
 constexpr int kPWRows = 128;
 constexpr int kPWCols = 256;
@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
     const int64_t j = tj * kPWCols + tid;
     const bool jok = j < m;
     float a2 = 0.0f;
-    if constexpr (MODE != kEuclid) a2 = jok ? n2[b * m + j] : 0.0f;
+    if constexpr (MODE == kCosDist || MODE == kCosSim) a2 = jok ? n2[b * m + j] : 0.0f;
     float csum = 0.0f;
     for (int r = 0; r < kPWRows; ++r) {
         const int64_t i = ti * kPWRows + r;
@@ -57,6 +57,10 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
             if constexpr (MODE == kEuclid) {
                 const float rv = to_f32(res[idx]);
                 w = rv == 0.0f ? 0.0f : __fdiv_rn(gv, rv);
+                rt = w;
+                csum += w;
+            } else if constexpr (MODE == kSqEuclid) {
+                w = 2.0f * gv;
                 rt = w;
                 csum += w;
             } else {
@@ -333,7 +337,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
                  T *gx2, void *ws, hipStream_t s) {
     BwdWs w = carve(ws, batch, n, m, d);
     int rc;
-    if constexpr (MODE != kEuclid) {
+    if constexpr (MODE == kCosDist || MODE == kCosSim) {
         rc = inner_dot_f32(x1, x2, dtype, batch, n, m, d, w.W, s);
         if (rc) return rc;
     }
@@ -342,15 +346,16 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
                        dim3(256), 0, s, g, res, n1, n2, n, m, w.W, w.rowpart, w.colpart, ti, tj);
     rc = check_launch("pair_weights_kernel");
     if (rc) return rc;
-    const float *div1 = MODE == kEuclid ? nullptr : n1;
-    const float *div2 = MODE == kEuclid ? nullptr : n2;
+    const bool cosine = MODE == kCosDist || MODE == kCosSim;
+    const float *div1 = cosine ? n1 : nullptr;
+    const float *div2 = cosine ? n2 : nullptr;
     hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)cdiv(batch * n, 256)), dim3(256), 0, s,
                        w.rowpart, tj, n, batch, div1, w.coef1);
     hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)cdiv(batch * m, 256)), dim3(256), 0, s,
                        w.colpart, ti, m, batch, div2, w.coef2);
     rc = check_launch("reduce_parts_kernel");
     if (rc) return rc;
-    const float sign = MODE == kEuclid ? -1.0f : 1.0f;
+    const float sign = cosine ? 1.0f : -1.0f;
     rc = run_gemm<T, false>(w.W, x2, batch, n, d, m, sign, w.coef1, x1, gx1, w.part, s);
     if (rc) return rc;
     return run_gemm<T, true>(w.W, x1, batch, m, d, n, sign, w.coef2, x2, gx2, w.part, s);
@@ -414,4 +419,27 @@ extern "C" int tpw_cosine_backward(const void *grad, const void *x1, const void 
     return run(static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
                static_cast<const uint16_t *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
                static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s);
+}
+
+extern "C" int tpw_sqeuclidean_backward(const void *grad, const void *x1, const void *x2,
+                                        int dtype, int64_t batch, int64_t n, int64_t m, int64_t d,
+                                        void *grad_x1, void *grad_x2, void *workspace,
+                                        void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2 && workspace, "null pointer");
+    TPW_REQUIRE(cdiv(n, kPWRows) <= kMaxGridYZ && cdiv(m, kGT) <= kMaxGridYZ &&
+                    cdiv(n, kGT) <= kMaxGridYZ && batch <= kMaxGridYZ,
+                "sizes exceed the launch grid");
+    hipStream_t s = as_stream(stream);
+    if (dtype == TPW_F32)
+        return run_backward<float, kSqEuclid>(
+            static_cast<const float *>(grad), static_cast<const float *>(x1),
+            static_cast<const float *>(x2), nullptr, nullptr, nullptr, dtype, batch, n, m, d,
+            static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s);
+    return run_backward<uint16_t, kSqEuclid>(
+        static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
+        static_cast<const uint16_t *>(x2), nullptr, nullptr, nullptr, dtype, batch, n, m, d,
+        static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s);
 }

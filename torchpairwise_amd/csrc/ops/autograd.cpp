@@ -1,0 +1,127 @@
+// Autograd kernels of the differentiable internal ops.  Each forward redispatches below
+// autograd and saves what its backward op needs:
+//   _pw_inner            -> _pw_inner_backward (the _euclidean_dist_backward formula for
+//                           EUCLIDEAN, the cosine graph of pairwise_metrics.cpp:51-56,112-122)
+//   _pw_lp               -> _pw_lp_backward (at::_cdist_backward formulas)
+//   prf_div              -> _prf_div_backward (csrc/ops/autograd/prf_div_kernel.cpp:9-52)
+//   _directed_hausdorff  -> __directed_hausdorff_backward, with the generator cloned so the
+//                           backward replays the forward's permutations
+//                           (csrc/ops/autograd/hausdorff_kernel.cpp:9-77)
+#include <torch/autograd.h>
+
+#include "tpw_common.h"
+
+namespace tpw_ext {
+namespace {
+
+using torch::autograd::AutogradContext;
+using torch::autograd::Variable;
+using torch::autograd::variable_list;
+
+class PwInnerFunction : public torch::autograd::Function<PwInnerFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x1, const Variable &x2,
+                            int64_t epilogue) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        auto out = pw_inner(x1, x2, epilogue);
+        if (epilogue == kEuclidean)
+            ctx->save_for_backward({x1, x2, out});
+        else
+            ctx->save_for_backward({x1, x2});
+        ctx->saved_data["epilogue"] = epilogue;
+        return out;
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad_output) {
+        auto saved = ctx->get_saved_variables();
+        const int64_t epi = ctx->saved_data["epilogue"].toInt();
+        at::Tensor res = saved.size() > 2 ? saved[2] : at::Tensor();
+        auto grads = pw_inner_backward(grad_output[0], saved[0], saved[1], res, epi);
+        return {std::get<0>(grads), std::get<1>(grads), Variable()};
+    }
+};
+
+class PwLpFunction : public torch::autograd::Function<PwLpFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x1, const Variable &x2, double p) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        auto out = pw_lp(x1, x2, p);
+        ctx->save_for_backward({x1, x2, out});
+        ctx->saved_data["p"] = p;
+        return out;
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad_output) {
+        auto saved = ctx->get_saved_variables();
+        auto grads = pw_lp_backward(grad_output[0], saved[0], saved[1], saved[2],
+                                    ctx->saved_data["p"].toDouble());
+        return {std::get<0>(grads), std::get<1>(grads), Variable()};
+    }
+};
+
+class PrfDivFunction : public torch::autograd::Function<PrfDivFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x, const Variable &y,
+                            c10::string_view mode) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        auto out = prf_div(x, y, mode);
+        ctx->save_for_backward({x, y});
+        ctx->saved_data["mode"] = std::string(mode);
+        return out;
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad_output) {
+        auto saved = ctx->get_saved_variables();
+        const std::string mode = ctx->saved_data["mode"].toStringRef();
+        auto grads = prf_div_backward(grad_output[0], saved[0], saved[1], mode);
+        return {std::get<0>(grads), std::get<1>(grads), Variable()};
+    }
+};
+
+class DirectedHausdorffFunction : public torch::autograd::Function<DirectedHausdorffFunction> {
+   public:
+    static variable_list forward(AutogradContext *ctx, const Variable &x1, const Variable &x2,
+                                 bool shuffle, c10::optional<at::Generator> generator) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        ctx->save_for_backward({x1, x2});
+        ctx->saved_data["shuffle"] = shuffle;
+        ctx->saved_data["generator"] =
+            generator.has_value() ? c10::make_optional(generator->clone()) : generator;
+        auto r = directed_hausdorff(x1, x2, shuffle, generator);
+        ctx->mark_non_differentiable({std::get<1>(r), std::get<2>(r)});
+        return {std::get<0>(r), std::get<1>(r), std::get<2>(r)};
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad_output) {
+        auto saved = ctx->get_saved_variables();
+        auto gen = ctx->saved_data["generator"].toOptional<at::Generator>();
+        auto grads = directed_hausdorff_backward(grad_output[0], saved[0], saved[1],
+                                                 ctx->saved_data["shuffle"].toBool(), gen);
+        return {std::get<0>(grads), std::get<1>(grads), Variable(), Variable()};
+    }
+};
+
+at::Tensor pw_inner_autograd(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue) {
+    return PwInnerFunction::apply(x1, x2, epilogue);
+}
+
+at::Tensor pw_lp_autograd(const at::Tensor &x1, const at::Tensor &x2, double p) {
+    return PwLpFunction::apply(x1, x2, p);
+}
+
+at::Tensor prf_div_autograd(const at::Tensor &x, const at::Tensor &y, c10::string_view mode) {
+    return PrfDivFunction::apply(x, y, mode);
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff_autograd(
+    const at::Tensor &x1, const at::Tensor &x2, bool shuffle, c10::optional<at::Generator> gen) {
+    auto r = DirectedHausdorffFunction::apply(x1, x2, shuffle, gen);
+    return {r[0], r[1], r[2]};
+}
+
+}  // namespace
+
+TORCH_LIBRARY_IMPL(torchpairwise, Autograd, m) {
+    m.impl("_pw_inner", TORCH_FN(pw_inner_autograd));
+    m.impl("_pw_lp", TORCH_FN(pw_lp_autograd));
+    m.impl("prf_div", TORCH_FN(prf_div_autograd));
+    m.impl("_directed_hausdorff", TORCH_FN(directed_hausdorff_autograd));
+}
+
+}  // namespace tpw_ext

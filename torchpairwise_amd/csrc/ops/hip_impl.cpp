@@ -1,0 +1,348 @@
+// GPU (DispatchKey::CUDA, which PyTorch-ROCm uses for HIP tensors) implementations of the
+// internal ops: shape/dtype checks, output allocation from the caching allocator, then one
+// call into the C ABI (include/torchpairwise_amd.h) on the current HIP stream.  There is no
+// other route: a missing kernel library fails at load time, unsupported dtypes raise.
+#include "tpw_common.h"
+
+namespace tpw_ext {
+namespace {
+
+void check_cuda_pair(const char *name, const at::Tensor &x1, const at::Tensor &x2) {
+    TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), name, ": expected GPU tensors");
+    TORCH_CHECK(x1.get_device() == x2.get_device(), name, ": x1 and x2 are on different devices");
+    TORCH_CHECK(x1.dim() == x2.dim() && (x1.dim() == 2 || x1.dim() == 3), name,
+                ": x1 and x2 must both be 2-D or both 3-D");
+    TORCH_CHECK(x1.size(-1) == x2.size(-1), name, ": feature dimension of x1 and x2 do not match.");
+    TORCH_CHECK(x1.dim() == 2 || x1.size(0) == x2.size(0), name, ": batch_size of x1 and x2 do not match.");
+}
+
+int float_dtype(const char *name, const at::Tensor &x) {
+    TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kBFloat16, name,
+                ": supports float32 and bfloat16 on the GPU, got ", x.scalar_type());
+    return x.scalar_type() == at::kFloat ? TPW_F32 : TPW_BF16;
+}
+
+at::Tensor out_shape(const at::Tensor &out3, const at::Tensor &x1) {
+    return x1.dim() == 2 ? out3.squeeze(0) : out3;
+}
+
+// ---------------------------------------------------------------- inner-product (MFMA)
+at::Tensor pw_inner_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue) {
+    check_cuda_pair("_pw_inner", x1, x2);
+    TORCH_CHECK(x1.scalar_type() == x2.scalar_type(), "_pw_inner: x1 and x2 dtypes differ");
+    const int dt = float_dtype("_pw_inner", x1);
+    TORCH_CHECK(epilogue >= TPW_EPI_DOT && epilogue <= TPW_EPI_COSINE_DIST, "_pw_inner: bad epilogue");
+    c10::hip::HIPGuard guard(x1.device());
+    auto a = as3(x1), b = as3(x2);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options());
+    at::Tensor n1, n2;
+    void *s = current_stream();
+    if (epilogue != TPW_EPI_DOT) {
+        const int squared = (epilogue == TPW_EPI_EUCLIDEAN || epilogue == TPW_EPI_SQEUCLIDEAN);
+        n1 = at::empty({B, n}, a.options().dtype(at::kFloat));
+        n2 = at::empty({B, m}, a.options().dtype(at::kFloat));
+        check_rc(tpw_row_norms(a.data_ptr(), dt, B * n, d, squared, n1.data_ptr<float>(), s), "row norms");
+        check_rc(tpw_row_norms(b.data_ptr(), dt, B * m, d, squared, n2.data_ptr<float>(), s), "row norms");
+    }
+    check_rc(tpw_pairwise_inner(a.data_ptr(), b.data_ptr(), dt, B, n, m, d,
+                                n1.defined() ? n1.data_ptr<float>() : nullptr,
+                                n2.defined() ? n2.data_ptr<float>() : nullptr, (int)epilogue,
+                                out.data_ptr(), s),
+             "_pw_inner");
+    return out_shape(out, x1);
+}
+
+std::tuple<at::Tensor, at::Tensor> pw_inner_backward_cuda(const at::Tensor &grad,
+                                                          const at::Tensor &x1,
+                                                          const at::Tensor &x2,
+                                                          const at::Tensor &res, int64_t epilogue) {
+    check_cuda_pair("_pw_inner_backward", x1, x2);
+    const int dt = float_dtype("_pw_inner_backward", x1);
+    c10::hip::HIPGuard guard(x1.device());
+    auto a = as3(x1), b = as3(x2);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto g = grad.to(a.scalar_type()).reshape({B, n, m}).contiguous();
+    auto gx1 = at::empty_like(a), gx2 = at::empty_like(b);
+    auto ws = workspace(tpw_inner_backward_workspace_size(B, n, m, d), a);
+    void *s = current_stream();
+    if (epilogue == TPW_EPI_EUCLIDEAN) {
+        auto r = res.reshape({B, n, m}).contiguous();
+        check_rc(tpw_euclidean_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(), r.data_ptr(), dt, B,
+                                        n, m, d, gx1.data_ptr(), gx2.data_ptr(), ws.data_ptr(), s),
+                 "euclidean backward");
+    } else if (epilogue == TPW_EPI_SQEUCLIDEAN) {
+        check_rc(tpw_sqeuclidean_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(), dt, B, n, m, d,
+                                          gx1.data_ptr(), gx2.data_ptr(), ws.data_ptr(), s),
+                 "sqeuclidean backward");
+    } else if (epilogue == TPW_EPI_COSINE_SIM || epilogue == TPW_EPI_COSINE_DIST) {
+        auto n1 = at::empty({B, n}, a.options().dtype(at::kFloat));
+        auto n2 = at::empty({B, m}, a.options().dtype(at::kFloat));
+        check_rc(tpw_row_norms(a.data_ptr(), dt, B * n, d, 0, n1.data_ptr<float>(), s), "row norms");
+        check_rc(tpw_row_norms(b.data_ptr(), dt, B * m, d, 0, n2.data_ptr<float>(), s), "row norms");
+        check_rc(tpw_cosine_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(), n1.data_ptr<float>(),
+                                     n2.data_ptr<float>(), dt, B, n, m, d,
+                                     epilogue == TPW_EPI_COSINE_SIM, gx1.data_ptr(), gx2.data_ptr(),
+                                     ws.data_ptr(), s),
+                 "cosine backward");
+    } else {
+        TORCH_CHECK(false, "_pw_inner_backward: epilogue ", epilogue, " has no backward");
+    }
+    return {gx1.reshape(x1.sizes()), gx2.reshape(x2.sizes())};
+}
+
+// ---------------------------------------------------------------- Minkowski (VALU)
+at::Tensor pw_lp_cuda(const at::Tensor &x1, const at::Tensor &x2, double p) {
+    check_cuda_pair("_pw_lp", x1, x2);
+    TORCH_CHECK(x1.scalar_type() == at::kFloat && x2.scalar_type() == at::kFloat,
+                "_pw_lp: supports float32 on the GPU");
+    TORCH_CHECK(p >= 0, "cdist only supports non-negative p values");
+    c10::hip::HIPGuard guard(x1.device());
+    auto a = as3(x1), b = as3(x2);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options());
+    check_rc(tpw_lp_distances(a.data_ptr<float>(), b.data_ptr<float>(), B, n, m, d, p,
+                              out.data_ptr<float>(), current_stream()),
+             "_pw_lp");
+    return out_shape(out, x1);
+}
+
+std::tuple<at::Tensor, at::Tensor> pw_lp_backward_cuda(const at::Tensor &grad, const at::Tensor &x1,
+                                                       const at::Tensor &x2, const at::Tensor &dist,
+                                                       double p) {
+    check_cuda_pair("_pw_lp_backward", x1, x2);
+    TORCH_CHECK(x1.scalar_type() == at::kFloat, "_pw_lp_backward: supports float32 on the GPU");
+    c10::hip::HIPGuard guard(x1.device());
+    auto a = as3(x1), b = as3(x2);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto g = grad.to(at::kFloat).reshape({B, n, m}).contiguous();
+    auto dd = dist.reshape({B, n, m}).contiguous();
+    auto gx1 = at::empty_like(a), gx2 = at::empty_like(b);
+    const size_t w1 = tpw_lp_backward_workspace_size(B, n, m, d);
+    const size_t w2 = tpw_lp_backward_workspace_size(B, m, n, d);
+    auto ws = workspace(std::max(w1, w2), a);
+    void *s = current_stream();
+    check_rc(tpw_lp_distances_backward(g.data_ptr<float>(), a.data_ptr<float>(), b.data_ptr<float>(),
+                                       dd.data_ptr<float>(), B, n, m, d, p, 0, gx1.data_ptr<float>(),
+                                       ws.data_ptr(), s),
+             "_pw_lp_backward x1");
+    check_rc(tpw_lp_distances_backward(g.data_ptr<float>(), b.data_ptr<float>(), a.data_ptr<float>(),
+                                       dd.data_ptr<float>(), B, m, n, d, p, 1, gx2.data_ptr<float>(),
+                                       ws.data_ptr(), s),
+             "_pw_lp_backward x2");
+    return {gx1.reshape(x1.sizes()), gx2.reshape(x2.sizes())};
+}
+
+// ---------------------------------------------------------------- boolean family
+void check_binary_shapes(const at::Tensor &x1, const at::Tensor &x2) {
+    // csrc/ops/cpu/pairwise_binary_kernels.cpp:123-133
+    const bool unbatched = x1.dim() == 2;
+    TORCH_CHECK(unbatched || x1.dim() == 3, "x1 must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(unbatched || x2.dim() == 3, "x2 must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(unbatched || x1.size(0) == x2.size(0), "batch_size of x1 and x2 do not match.")
+    TORCH_CHECK((unbatched && x1.size(1) == x2.size(1)) || (!unbatched && x1.size(2) == x2.size(2)),
+                "feature dimension of x1 and x2 do not match.")
+}
+
+// Packs [rows, d] bool rows into uint32 words (+ row popcounts).
+std::pair<at::Tensor, at::Tensor> pack(const at::Tensor &x3, bool with_pops) {
+    const int64_t rows = x3.size(0) * x3.size(1), d = x3.size(2);
+    auto words = at::empty({rows, tpw_packed_words(d)}, x3.options().dtype(at::kInt));
+    at::Tensor pops;
+    if (with_pops) pops = at::empty({rows}, x3.options().dtype(at::kInt));
+    check_rc(tpw_pack_bool_rows(reinterpret_cast<const uint8_t *>(x3.data_ptr<bool>()), rows, d,
+                                reinterpret_cast<uint32_t *>(words.data_ptr<int32_t>()),
+                                with_pops ? pops.data_ptr<int32_t>() : nullptr, current_stream()),
+             "pack bool rows");
+    return {words, pops};
+}
+
+template <int OP, int RED>
+at::Tensor pw_reduce_cuda(const at::Tensor &x1, const at::Tensor &x2) {
+    TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), "expected GPU tensors");
+    check_binary_shapes(x1, x2);
+    c10::hip::HIPGuard guard(x1.device());
+    const auto common = at::result_type(x1, x2);
+    auto a = as3(x1.to(common)), b = as3(x2.to(common));
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options().dtype(at::kFloat));
+    if (B * n * m == 0) return out_shape(out, x1);
+    if (d == 0) {  // empty reduction: sum 0, mean 0/0
+        out.fill_(RED == TPW_RED_SUM ? 0.0 : std::numeric_limits<double>::quiet_NaN());
+        return out_shape(out, x1);
+    }
+    if (common == at::kBool) {
+        auto wa = pack(a, false).first, wb = pack(b, false).first;
+        check_rc(tpw_bool_pairwise_reduce(reinterpret_cast<const uint32_t *>(wa.data_ptr<int32_t>()),
+                                          reinterpret_cast<const uint32_t *>(wb.data_ptr<int32_t>()),
+                                          B, n, m, d, OP, RED, out.data_ptr<float>(), current_stream()),
+                 "pairwise bool reduction");
+    } else {
+        TORCH_CHECK(OP == TPW_BIT_EQ || OP == TPW_BIT_NE, "logical pairwise reductions (and/or/xor) "
+                    "are implemented for Bool only, got ", common);
+        const int code = float_code(common);
+        TORCH_CHECK(code >= 0, "pairwise comparison not implemented for ", common);
+        check_rc(tpw_compare_reduce(a.data_ptr(), b.data_ptr(), code, B, n, m, d, OP, RED,
+                                    out.data_ptr<float>(), current_stream()),
+                 "pairwise comparison reduction");
+    }
+    return out_shape(out, x1);
+}
+
+at::Tensor jaccard_cuda(const at::Tensor &x1, const at::Tensor &x2) {
+    TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), "expected GPU tensors");
+    check_binary_shapes(x1, x2);
+    c10::hip::HIPGuard guard(x1.device());
+    auto a = as3(x1.to(at::kBool)), b = as3(x2.to(at::kBool));
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options().dtype(at::kFloat));
+    if (B * n * m == 0) return out_shape(out, x1);
+    if (d == 0) {
+        out.zero_();
+        return out_shape(out, x1);
+    }
+    auto pa = pack(a, true), pb = pack(b, true);
+    check_rc(tpw_jaccard_bool(reinterpret_cast<const uint32_t *>(pa.first.data_ptr<int32_t>()),
+                              reinterpret_cast<const uint32_t *>(pb.first.data_ptr<int32_t>()),
+                              pa.second.data_ptr<int32_t>(), pb.second.data_ptr<int32_t>(), B, n, m, d,
+                              out.data_ptr<float>(), current_stream()),
+             "jaccard");
+    return out_shape(out, x1);
+}
+
+// ---------------------------------------------------------------- prf_div
+at::Tensor prf_div_cuda(const at::Tensor &x, const at::Tensor &y, c10::string_view mode) {
+    const bool identity = prf_identity(mode);
+    TORCH_CHECK(x.sizes() == y.sizes(), "prf_div: input and other must have the same shape, got ",
+                x.sizes(), " and ", y.sizes());
+    c10::hip::HIPGuard guard(x.device());
+    auto common = at::result_type(x, y);
+    if (!at::isFloatingType(common)) common = at::kFloat;  // integer inputs divide in float32
+    auto a = x.to(common).contiguous(), b = y.to(common).contiguous();
+    auto out = at::empty_like(a);
+    const int code = float_code(common);
+    TORCH_CHECK(code == TPW_F32 || code == TPW_F64 || code == TPW_F16 || code == TPW_BF16,
+                "prf_div: unsupported dtype ", common);
+    check_rc(tpw_prf_div(a.data_ptr(), b.data_ptr(), code, a.numel(), identity, out.data_ptr(),
+                         current_stream()),
+             "prf_div");
+    return out;
+}
+
+std::tuple<at::Tensor, at::Tensor> prf_div_backward_cuda(const at::Tensor &g, const at::Tensor &x,
+                                                         const at::Tensor &y, c10::string_view mode) {
+    const bool identity = prf_identity(mode);
+    c10::hip::HIPGuard guard(x.device());
+    auto common = at::result_type(x, y);
+    if (!at::isFloatingType(common)) common = at::kFloat;
+    auto a = x.to(common).contiguous(), b = y.to(common).contiguous();
+    auto gg = g.to(common).contiguous();
+    auto gx = at::empty_like(a), gy = at::empty_like(b);
+    check_rc(tpw_prf_div_backward(gg.data_ptr(), a.data_ptr(), b.data_ptr(), float_code(common),
+                                  a.numel(), identity, gx.data_ptr(), gy.data_ptr(), current_stream()),
+             "prf_div backward");
+    return {gx, gy};
+}
+
+// ---------------------------------------------------------------- Hausdorff
+struct HdRun {
+    at::Tensor a, b, out, i1, i2;
+};
+
+HdRun hausdorff_run(const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
+                    c10::optional<at::Generator> gen) {
+    check_hausdorff_shapes(x1, x2);
+    TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), "_directed_hausdorff: expected GPU tensors");
+    TORCH_CHECK(x1.scalar_type() == at::kFloat,
+                "_directed_hausdorff: the GPU kernel is float32 only, got ", x1.scalar_type());
+    HdRun r;
+    r.a = x1.dim() == 3 ? x1.unsqueeze(0).contiguous() : x1.contiguous();
+    r.b = x2.dim() == 3 ? x2.unsqueeze(0).contiguous() : x2.contiguous();
+    const int64_t B = r.a.size(0), b1 = r.a.size(1), p1 = r.a.size(2), d = r.a.size(3);
+    const int64_t b2 = r.b.size(1), p2 = r.b.size(2);
+    r.out = at::empty({B, b1, b2}, r.a.options());
+    r.i1 = at::empty({B, b1, b2}, r.a.options().dtype(at::kLong));
+    r.i2 = at::empty({B, b1, b2}, r.a.options().dtype(at::kLong));
+    at::Tensor perm1, perm2;
+    if (shuffle) std::tie(perm1, perm2) = hausdorff_perms(B, p1, p2, r.a.options(), gen);
+    auto ws = workspace(tpw_hausdorff_workspace_size(B, b1, p1, b2, p2, d), r.a);
+    check_rc(tpw_directed_hausdorff(r.a.data_ptr<float>(), r.b.data_ptr<float>(), B, b1, p1, b2, p2, d,
+                                    shuffle ? perm1.data_ptr<int64_t>() : nullptr,
+                                    shuffle ? perm2.data_ptr<int64_t>() : nullptr,
+                                    r.out.data_ptr<float>(), r.i1.data_ptr<int64_t>(),
+                                    r.i2.data_ptr<int64_t>(), ws.data_ptr(), current_stream()),
+             "_directed_hausdorff");
+    return r;
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff_cuda(
+    const at::Tensor &x1, const at::Tensor &x2, bool shuffle, c10::optional<at::Generator> gen) {
+    c10::hip::HIPGuard guard(x1.device());
+    HdRun r = hausdorff_run(x1, x2, shuffle, gen);
+    if (x1.dim() == 3) return {r.out.squeeze(0), r.i1.squeeze(0), r.i2.squeeze(0)};
+    return {r.out, r.i1, r.i2};
+}
+
+std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_cuda(
+    const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
+    c10::optional<at::Generator> gen) {
+    c10::hip::HIPGuard guard(x1.device());
+    // the reference re-runs the forward here (csrc/ops/cpu/hausdorff_kernel.cpp:269-306)
+    HdRun r = hausdorff_run(x1, x2, shuffle, gen);
+    auto g = grad.to(at::kFloat).reshape(r.out.sizes()).contiguous();
+    auto gx1 = at::zeros_like(r.a), gx2 = at::zeros_like(r.b);
+    check_rc(tpw_directed_hausdorff_backward(
+                 g.data_ptr<float>(), r.a.data_ptr<float>(), r.b.data_ptr<float>(),
+                 r.out.data_ptr<float>(), r.i1.data_ptr<int64_t>(), r.i2.data_ptr<int64_t>(),
+                 r.a.size(0), r.a.size(1), r.a.size(2), r.b.size(1), r.b.size(2), r.a.size(3),
+                 gx1.data_ptr<float>(), gx2.data_ptr<float>(), current_stream()),
+             "__directed_hausdorff_backward");
+    if (x1.dim() == 3) return {gx1.squeeze(0), gx2.squeeze(0)};
+    return {gx1, gx2};
+}
+
+// ---------------------------------------------------------------- elementwise pw ops
+template <typename F>
+at::Tensor pw_elementwise(const at::Tensor &x1, const at::Tensor &x2, F f) {
+    // [b, n, d] x [b, m, d] -> [b, n, m, d] (csrc/ops/cpu/pairwise_binary_kernels.cpp:12-26)
+    TORCH_CHECK(x1.dim() >= 2 && x2.dim() >= 2, "x1 and x2 must have at least 2 dimensions.");
+    return f(x1.unsqueeze(-2), x2.unsqueeze(-3));
+}
+
+}  // namespace
+
+TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
+    m.impl("_pw_inner", TORCH_FN(pw_inner_cuda));
+    m.impl("_pw_inner_backward", TORCH_FN(pw_inner_backward_cuda));
+    m.impl("_pw_lp", TORCH_FN(pw_lp_cuda));
+    m.impl("_pw_lp_backward", TORCH_FN(pw_lp_backward_cuda));
+    m.impl("_jaccard", TORCH_FN(jaccard_cuda));
+    m.impl("pwand_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_AND, TPW_RED_SUM>)));
+    m.impl("pwor_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_OR, TPW_RED_SUM>)));
+    m.impl("pwxor_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_XOR, TPW_RED_SUM>)));
+    m.impl("pweq_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_EQ, TPW_RED_SUM>)));
+    m.impl("pwne_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_NE, TPW_RED_SUM>)));
+    m.impl("pweq_mean", TORCH_FN((pw_reduce_cuda<TPW_BIT_EQ, TPW_RED_MEAN>)));
+    m.impl("pwne_mean", TORCH_FN((pw_reduce_cuda<TPW_BIT_NE, TPW_RED_MEAN>)));
+    m.impl("prf_div", TORCH_FN(prf_div_cuda));
+    m.impl("_prf_div_backward", TORCH_FN(prf_div_backward_cuda));
+    m.impl("_directed_hausdorff", TORCH_FN(directed_hausdorff_cuda));
+    m.impl("__directed_hausdorff_backward", TORCH_FN(directed_hausdorff_backward_cuda));
+}
+
+// The unreduced pairwise comparisons ([b, n, m, d] bool) are plain broadcast elementwise ops;
+// they run through ATen on either device (CompositeExplicitAutograd: no gradient, as in the
+// reference, which registers no Autograd kernel for them).
+TORCH_LIBRARY_IMPL(torchpairwise, CompositeExplicitAutograd, m) {
+    m.impl("pwand", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::logical_and(u, v); }); });
+    m.impl("pwor", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::logical_or(u, v); }); });
+    m.impl("pwxor", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::logical_xor(u, v); }); });
+    m.impl("pweq", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::eq(u, v); }); });
+    m.impl("pwne", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::ne(u, v); }); });
+    m.impl("pwlt", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::lt(u, v); }); });
+    m.impl("pwgt", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::gt(u, v); }); });
+    m.impl("pwle", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::le(u, v); }); });
+    m.impl("pwge", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::ge(u, v); }); });
+}
+
+}  // namespace tpw_ext

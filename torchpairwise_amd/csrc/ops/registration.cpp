@@ -1,0 +1,478 @@
+// Schema registration of torch.ops.torchpairwise and the public (CompositeImplicitAutograd)
+// metric functions.
+//
+// Public schemas are byte-for-byte those of the reference (csrc/ops/pairwise_metrics.h:76-424,
+// registered at csrc/ops/pairwise_metrics.cpp:440-486), so torchpairwise.*_distances callers
+// and torch.jit.script code bind unchanged.  Their bodies restate the reference functors:
+// the same input checks (check_pairwise_inputs, pairwise_metrics.h:10-67) and formulas, but
+// GPU tensors of the hot-path dtypes go to this build's internal ops (HIP kernels behind the
+// C ABI) where the reference went to ATen (at::cdist / matmul + prf_div) or to its naive
+// kernels.  CPU tensors take the reference's own route (ATen for the cdist/matmul metrics,
+// this extension's CPU kernels for the custom ops).
+#include "tpw_common.h"
+
+#include <ATen/core/dispatch/Dispatcher.h>
+#include <c10/util/Logging.h>
+
+namespace tpw_ext {
+namespace {
+
+// ------------------------------------------------------------------------------------
+// input checks (restated from csrc/ops/pairwise_metrics.h:10-67)
+// ------------------------------------------------------------------------------------
+template <bool is_boolean_metric = false, bool is_2d_metric = false>
+std::pair<at::Tensor, at::Tensor> check_pairwise_inputs(const char *c, const at::Tensor &x1,
+                                                        const c10::optional<at::Tensor> &x2) {
+    const bool unbatched = x1.dim() == (is_2d_metric ? 3 : 2);
+    if constexpr (is_2d_metric) {
+        TORCH_CHECK(unbatched || x1.dim() == 4, "x1 must be 3D tensor (unbatched) or 4D tensor (batched)")
+    } else {
+        TORCH_CHECK(unbatched || x1.dim() == 3, "x1 must be 2D tensor (unbatched) or 3D tensor (batched)")
+    }
+    if (x2.has_value()) {
+        const at::Tensor &y = x2.value();
+        const int64_t f = (is_2d_metric ? 2 : 1) + (unbatched ? 0 : 1);
+        if constexpr (is_2d_metric) {
+            TORCH_CHECK(unbatched || y.dim() == 4, "x2 must be 3D tensor (unbatched) or 4D tensor (batched)")
+        } else {
+            TORCH_CHECK(unbatched || y.dim() == 3, "x2 must be 2D tensor (unbatched) or 3D tensor (batched)")
+        }
+        TORCH_CHECK(x1.size(f) == y.size(f), "x1 and x2 must have same number of features. Got: x1.size(",
+                    f, ")=", x1.size(f), ", x2.size(", f, ")=", y.size(f))
+        if constexpr (is_boolean_metric) {
+            if (x1.scalar_type() != at::kBool || y.scalar_type() != at::kBool) {
+                TORCH_WARN("Data was converted to ", at::kBool, " for metric ", c)
+            }
+            return {x1.to(at::kBool), y.to(at::kBool)};
+        } else {
+            return {x1, y};
+        }
+    }
+    if constexpr (is_boolean_metric) {
+        if (x1.scalar_type() != at::kBool) {
+            TORCH_WARN("Data was converted to ", at::kBool, " for metric ", c)
+        }
+        auto b = x1.to(at::kBool);
+        return {b, b};
+    } else {
+        return {x1, x1};
+    }
+}
+
+bool hip_float_path(const at::Tensor &a, const at::Tensor &b) {
+    return a.is_cuda() && b.is_cuda() && a.scalar_type() == b.scalar_type() &&
+           (a.scalar_type() == at::kFloat || a.scalar_type() == at::kBFloat16) &&
+           a.dim() == b.dim() && (a.dim() == 2 || a.dim() == 3);
+}
+
+// at::cdist broadcasts the batch dimension; the kernels take equal batches.
+std::pair<at::Tensor, at::Tensor> broadcast_batch(const at::Tensor &a, const at::Tensor &b) {
+    if (a.dim() != 3 || a.size(0) == b.size(0)) return {a, b};
+    const int64_t B = std::max(a.size(0), b.size(0));
+    TORCH_CHECK(a.size(0) == 1 || b.size(0) == 1, "The size of tensor a (", a.size(0),
+                ") must match the size of tensor b (", b.size(0), ") at non-singleton dimension 0");
+    return {a.expand({B, a.size(1), a.size(2)}), b.expand({B, b.size(1), b.size(2)})};
+}
+
+// at::cdist(x1, x2, p) with the same dispatch rule (p == 2 uses the |a|^2 + |b|^2 - 2ab
+// matrix-product form when either operand has more than 25 rows, the direct sum otherwise;
+// torch/functional.py documents the rule), served by the HIP kernels for fp32 / bf16 GPU
+// tensors.  Anything else is at::cdist itself, as in the reference.
+at::Tensor route_cdist(const at::Tensor &x1, const at::Tensor &x2, double p) {
+    if (!hip_float_path(x1, x2)) return at::cdist(x1, x2, p);
+    TORCH_CHECK(p >= 0, "cdist only supports non-negative p values");
+    auto ab = broadcast_batch(x1, x2);
+    const at::Tensor &a = ab.first, &b = ab.second;
+    if (p == 2.0 && (a.size(-2) > 25 || b.size(-2) > 25)) return pw_inner(a, b, kEuclidean);
+    if (a.scalar_type() == at::kBFloat16)
+        return pw_lp(a.to(at::kFloat), b.to(at::kFloat), p).to(at::kBFloat16);
+    return pw_lp(a, b, p);
+}
+
+[[noreturn]] void not_in_build(const char *name) {
+    TORCH_CHECK_NOT_IMPLEMENTED(false, "torchpairwise.", name,
+                                " is not implemented by this MI355X build (outside its hot path: "
+                                "the inner-product, Minkowski, boolean and Hausdorff families)");
+}
+
+// ------------------------------------------------------------------------------------
+// public functions (csrc/ops/pairwise_metrics.cpp)
+// ------------------------------------------------------------------------------------
+at::Tensor euclidean_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("euclidean_distances", x1, x2);
+    return route_cdist(xs.first, xs.second, 2);
+}
+
+at::Tensor manhattan_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("manhattan_distances", x1, x2);
+    return route_cdist(xs.first, xs.second, 1);
+}
+
+at::Tensor cosine_similarity(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("cosine_similarity", x1, x2);
+    if (hip_float_path(xs.first, xs.second)) {
+        auto ab = broadcast_batch(xs.first, xs.second);
+        return pw_inner(ab.first, ab.second, kCosineSim);
+    }
+    // pairwise_metrics.cpp:112-122
+    auto x1_norm = x1.norm(2, -1, true);
+    auto x2_norm = x2.has_value() ? xs.second.norm(2, -1, true) : x1_norm;
+    auto denom = x1_norm.mul(x2_norm.transpose(-1, -2));
+    return prf_div(xs.first.matmul(xs.second.transpose(-1, -2)), denom, "identity");
+}
+
+at::Tensor cosine_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("cosine_distances", x1, x2);
+    if (hip_float_path(xs.first, xs.second)) {
+        auto ab = broadcast_batch(xs.first, xs.second);
+        return pw_inner(ab.first, ab.second, kCosineDist);
+    }
+    return cosine_similarity(x1, x2).neg_().add_(1).clip_(0, 2);  // pairwise_metrics.cpp:51-56
+}
+
+at::Tensor linear_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("linear_kernel", x1, x2);
+    return xs.first.matmul(xs.second.transpose(-1, -2));
+}
+
+at::Tensor polynomial_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
+                             int64_t degree, c10::optional<double> gamma, double coef0) {
+    auto xs = check_pairwise_inputs("polynomial_kernel", x1, x2);
+    const double g = gamma.value_or(1.0 / x1.size(1));
+    return xs.first.matmul(xs.second.transpose(-1, -2)).mul_(g).add_(coef0).pow_(degree);
+}
+
+at::Tensor sigmoid_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
+                          c10::optional<double> gamma, double coef0) {
+    auto xs = check_pairwise_inputs("sigmoid_kernel", x1, x2);
+    const double g = gamma.value_or(1.0 / x1.size(1));
+    return xs.first.matmul(xs.second.transpose(-1, -2)).mul_(g).add_(coef0).tanh_();
+}
+
+at::Tensor sqeuclidean_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("sqeuclidean_distances", x1, x2);
+    if (hip_float_path(xs.first, xs.second)) {
+        auto ab = broadcast_batch(xs.first, xs.second);
+        return pw_inner(ab.first, ab.second, kSqEuclidean);
+    }
+    // the reference's _ppminkowski(p=2) sums (a - b)^2 directly; ATen's direct p=2 path
+    // (compute_mode 2) computes the same sum, then sqrt, which square() undoes
+    return at::cdist(xs.first, xs.second, 2, 2).square();
+}
+
+at::Tensor rbf_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
+                      c10::optional<double> gamma) {
+    const double g = gamma.value_or(1.0 / x1.size(1));
+    return sqeuclidean_distances(x1, x2).mul(-g).exp();
+}
+
+at::Tensor laplacian_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
+                            c10::optional<double> gamma) {
+    auto xs = check_pairwise_inputs("laplacian_kernel", x1, x2);
+    const double g = gamma.value_or(1.0 / x1.size(1));
+    return route_cdist(xs.first, xs.second, 1).mul(-g).exp();
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff_distances(
+    const at::Tensor &x1, const c10::optional<at::Tensor> &x2, bool shuffle,
+    c10::optional<at::Generator> generator) {
+    auto xs = check_pairwise_inputs<false, true>("directed_hausdorff_distances", x1, x2);
+    return directed_hausdorff(xs.first, xs.second, shuffle, generator);
+}
+
+at::Tensor minkowski_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2, double p) {
+    auto xs = check_pairwise_inputs("minkowski_distances", x1, x2);
+    return route_cdist(xs.first, xs.second, p);
+}
+
+at::Tensor wminkowski_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2, double p,
+                                const c10::optional<at::Tensor> &w) {
+    auto xs = check_pairwise_inputs("wminkowski_distances", x1, x2);
+    if (w.has_value()) not_in_build("wminkowski_distances with weights w");
+    return route_cdist(xs.first, xs.second, p);
+}
+
+at::Tensor correlation_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("correlation_distances", x1, x2);
+    // pairwise_metrics.cpp:190-204: centre, then 1 - cosine similarity (no clip)
+    at::Tensor a = xs.first - xs.first.mean(-1, true);
+    at::Tensor b = x2.has_value() ? xs.second - xs.second.mean(-1, true) : a;
+    if (hip_float_path(a, b)) {
+        auto ab = broadcast_batch(a, b);
+        return pw_inner(ab.first, ab.second, kCosineSim).neg().add(1);
+    }
+    auto a_norm = a.norm(2, -1, true);
+    auto b_norm = x2.has_value() ? b.norm(2, -1, true) : a_norm;
+    auto denom = a_norm.mul(b_norm.transpose(-1, -2));
+    return prf_div(a.matmul(b.transpose(-1, -2)), denom, "identity").neg_().add_(1);
+}
+
+at::Tensor hamming_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("hamming_distances", x1, x2);
+    return pw_binary_reduce("pwne_mean", xs.first, xs.second);
+}
+
+at::Tensor jaccard_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs<true>("jaccard_distances", x1, x2);
+    return jaccard_fused(xs.first, xs.second);
+}
+
+at::Tensor kulsinski_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    TORCH_WARN_DEPRECATION("kulsinski_distances is deprecated in SciPy 1.9.0 and might "
+                           "be removed in the future. Please use kulczynski1_distances.")
+    auto xs = check_pairwise_inputs<true>("kulsinski_distances", x1, x2);
+    auto S = pw_binary_reduce("pwxor_sum", xs.first, xs.second);
+    const int64_t D = x1.size(-1);
+    return (S - pw_binary_reduce("pwand_sum", xs.first, xs.second) + D) / (S + D);
+}
+
+at::Tensor kulczynski1_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs<true>("kulczynski1_distances", x1, x2);
+    return pw_binary_reduce("pwand_sum", xs.first, xs.second) /
+           pw_binary_reduce("pwxor_sum", xs.first, xs.second);
+}
+
+at::Tensor cityblock_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    return manhattan_distances(x1, x2);
+}
+
+at::Tensor chebyshev_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("chebyshev_distances", x1, x2);
+    return route_cdist(xs.first, xs.second, std::numeric_limits<double>::infinity());
+}
+
+at::Tensor yule_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs<true>("yule_distances", x1, x2);
+    const at::Tensor &a = xs.first, &b = xs.second;
+    auto half_R = pw_binary_reduce("pwand_sum", a, b.logical_not()) *
+                  pw_binary_reduce("pwand_sum", a.logical_not(), b);
+    return prf_div(2 * half_R,
+                   pw_binary_reduce("pwand_sum", a, b) *
+                           pw_binary_reduce("pwand_sum", a.logical_not(), b.logical_not()) +
+                       half_R,
+                   "zero");
+}
+
+at::Tensor dice_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs<true>("dice_distances", x1, x2);
+    auto R = pw_binary_reduce("pwxor_sum", xs.first, xs.second);
+    return R / (2 * pw_binary_reduce("pwand_sum", xs.first, xs.second) + R);
+}
+
+at::Tensor rogerstanimoto_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs<true>("rogerstanimoto_distances", x1, x2);
+    auto R = 2 * pw_binary_reduce("pwxor_sum", xs.first, xs.second);
+    auto S = pw_binary_reduce("pweq_sum", xs.first, xs.second);
+    return R / (S + R);
+}
+
+at::Tensor russellrao_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs<true>("russellrao_distances", x1, x2);
+    const int64_t D = x1.size(-1);
+    return (D - pw_binary_reduce("pwand_sum", xs.first, xs.second)) / D;
+}
+
+at::Tensor sokalmichener_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs<true>("sokalmichener_distances", x1, x2);
+    auto R = 2 * pw_binary_reduce("pwxor_sum", xs.first, xs.second);
+    auto S = pw_binary_reduce("pweq_sum", xs.first, xs.second);
+    return R / (S + R);
+}
+
+at::Tensor sokalsneath_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs<true>("sokalsneath_distances", x1, x2);
+    auto R = 2 * pw_binary_reduce("pwxor_sum", xs.first, xs.second);
+    return R / (pw_binary_reduce("pwand_sum", xs.first, xs.second) + R);
+}
+
+at::Tensor l1_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    return manhattan_distances(x1, x2);
+}
+at::Tensor l2_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    return euclidean_distances(x1, x2);
+}
+at::Tensor lp_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2, double p) {
+    return minkowski_distances(x1, x2, p);
+}
+at::Tensor linf_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    return chebyshev_distances(x1, x2);
+}
+
+// outside the hot path: registered so the schemas match, but not served by this build
+at::Tensor haversine_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("haversine_distances"); }
+at::Tensor additive_chi2_kernel(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("additive_chi2_kernel"); }
+at::Tensor chi2_kernel(const at::Tensor &, const c10::optional<at::Tensor> &, double) { not_in_build("chi2_kernel"); }
+at::Tensor seuclidean_distances(const at::Tensor &, const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &) { not_in_build("seuclidean_distances"); }
+at::Tensor mahalanobis_distances(const at::Tensor &, const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &) { not_in_build("mahalanobis_distances"); }
+at::Tensor braycurtis_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("braycurtis_distances"); }
+at::Tensor canberra_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("canberra_distances"); }
+at::Tensor jensenshannon_distances(const at::Tensor &, const c10::optional<at::Tensor> &, c10::optional<double>) { not_in_build("jensenshannon_distances"); }
+at::Tensor snr_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("snr_distances"); }
+
+int64_t cuda_version() { return tpw_runtime_version(); }
+std::string cuda_arch_flags() { return "gfx950"; }
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------
+// dispatcher handles of the internal ops
+// ------------------------------------------------------------------------------------
+at::Tensor pw_inner(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue) {
+    static auto op = c10::Dispatcher::singleton().findSchemaOrThrow("torchpairwise::_pw_inner", "")
+                         .typed<at::Tensor(const at::Tensor &, const at::Tensor &, int64_t)>();
+    return op.call(x1, x2, epilogue);
+}
+
+std::tuple<at::Tensor, at::Tensor> pw_inner_backward(const at::Tensor &grad, const at::Tensor &x1,
+                                                     const at::Tensor &x2, const at::Tensor &res,
+                                                     int64_t epilogue) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchpairwise::_pw_inner_backward", "")
+                         .typed<std::tuple<at::Tensor, at::Tensor>(
+                             const at::Tensor &, const at::Tensor &, const at::Tensor &,
+                             const at::Tensor &, int64_t)>();
+    return op.call(grad, x1, x2, res, epilogue);
+}
+
+at::Tensor pw_lp(const at::Tensor &x1, const at::Tensor &x2, double p) {
+    static auto op = c10::Dispatcher::singleton().findSchemaOrThrow("torchpairwise::_pw_lp", "")
+                         .typed<at::Tensor(const at::Tensor &, const at::Tensor &, double)>();
+    return op.call(x1, x2, p);
+}
+
+std::tuple<at::Tensor, at::Tensor> pw_lp_backward(const at::Tensor &grad, const at::Tensor &x1,
+                                                  const at::Tensor &x2, const at::Tensor &dist,
+                                                  double p) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchpairwise::_pw_lp_backward", "")
+                         .typed<std::tuple<at::Tensor, at::Tensor>(
+                             const at::Tensor &, const at::Tensor &, const at::Tensor &,
+                             const at::Tensor &, double)>();
+    return op.call(grad, x1, x2, dist, p);
+}
+
+at::Tensor pw_binary_reduce(const char *name, const at::Tensor &x1, const at::Tensor &x2) {
+    auto op = c10::Dispatcher::singleton()
+                  .findSchemaOrThrow((std::string("torchpairwise::") + name).c_str(), "")
+                  .typed<at::Tensor(const at::Tensor &, const at::Tensor &)>();
+    return op.call(x1, x2);
+}
+
+at::Tensor jaccard_fused(const at::Tensor &x1, const at::Tensor &x2) {
+    static auto op = c10::Dispatcher::singleton().findSchemaOrThrow("torchpairwise::_jaccard", "")
+                         .typed<at::Tensor(const at::Tensor &, const at::Tensor &)>();
+    return op.call(x1, x2);
+}
+
+at::Tensor prf_div(const at::Tensor &x, const at::Tensor &y, c10::string_view mode) {
+    static auto op = c10::Dispatcher::singleton().findSchemaOrThrow("torchpairwise::prf_div", "")
+                         .typed<at::Tensor(const at::Tensor &, const at::Tensor &, c10::string_view)>();
+    return op.call(x, y, mode);
+}
+
+std::tuple<at::Tensor, at::Tensor> prf_div_backward(const at::Tensor &g, const at::Tensor &x,
+                                                    const at::Tensor &y, c10::string_view mode) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchpairwise::_prf_div_backward", "")
+                         .typed<std::tuple<at::Tensor, at::Tensor>(
+                             const at::Tensor &, const at::Tensor &, const at::Tensor &,
+                             c10::string_view)>();
+    return op.call(g, x, y, mode);
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff(
+    const at::Tensor &x1, const at::Tensor &x2, bool shuffle, c10::optional<at::Generator> gen) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchpairwise::_directed_hausdorff", "")
+                         .typed<std::tuple<at::Tensor, at::Tensor, at::Tensor>(
+                             const at::Tensor &, const at::Tensor &, bool,
+                             c10::optional<at::Generator>)>();
+    return op.call(x1, x2, shuffle, gen);
+}
+
+std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward(
+    const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
+    c10::optional<at::Generator> gen) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchpairwise::__directed_hausdorff_backward", "")
+                         .typed<std::tuple<at::Tensor, at::Tensor>(
+                             const at::Tensor &, const at::Tensor &, const at::Tensor &, bool,
+                             c10::optional<at::Generator>)>();
+    return op.call(grad, x1, x2, shuffle, gen);
+}
+
+TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
+    // ---- internal ops of this build (HIP kernels; Autograd in autograd.cpp) ----
+    m.def("_pw_inner(Tensor x1, Tensor x2, int epilogue) -> Tensor");
+    m.def("_pw_inner_backward(Tensor grad, Tensor x1, Tensor x2, Tensor result, int epilogue) -> "
+          "(Tensor grad_x1, Tensor grad_x2)");
+    m.def("_pw_lp(Tensor x1, Tensor x2, float p) -> Tensor");
+    m.def("_pw_lp_backward(Tensor grad, Tensor x1, Tensor x2, Tensor dist, float p) -> "
+          "(Tensor grad_x1, Tensor grad_x2)");
+    m.def("_jaccard(Tensor x1, Tensor x2) -> Tensor");
+
+    // ---- internal ops of the reference (same schemas) ----
+    // csrc/ops/pairwise_binary.cpp:135-160
+    for (const char *op : {"pwand", "pwor", "pwxor", "pweq", "pwne", "pwlt", "pwgt", "pwle", "pwge"})
+        m.def((std::string(op) + "(Tensor x1, Tensor x2) -> Tensor").c_str());
+    for (const char *op : {"pwand_sum", "pwor_sum", "pwxor_sum", "pweq_sum", "pwne_sum", "pweq_mean",
+                           "pwne_mean"})
+        m.def((std::string(op) + "(Tensor x1, Tensor x2) -> Tensor").c_str());
+    // csrc/ops/prf_div.cpp:359-400 (the tensor-tensor forms)
+    m.def("prf_div(Tensor input, Tensor other, str mode=\"zero\") -> Tensor");
+    m.def("_prf_div_backward(Tensor grad, Tensor self, Tensor other, str mode=\"zero\") -> "
+          "(Tensor grad_self, Tensor grad_other)");
+    // csrc/ops/hausdorff.cpp:33-40
+    m.def("_directed_hausdorff(Tensor x1, Tensor x2, *, bool shuffle=False, Generator? generator=None) "
+          "-> (Tensor output, Tensor x1_indices, Tensor x2_indices)");
+    m.def("__directed_hausdorff_backward(Tensor grad, Tensor x1, Tensor x2, *, bool shuffle=False, "
+          "Generator? generator=None) -> (Tensor grad_x1, Tensor grad_x2)");
+    // csrc/torchpairwise.cpp:53-56
+    m.def("_cuda_version() -> int", &cuda_version);
+    m.def("_cuda_arch_flags() -> str", &cuda_arch_flags);
+
+    // ---- public metrics (csrc/ops/pairwise_metrics.h schemas) ----
+#define TPW_PUBLIC(schema, fn) m.def(schema, TORCH_FN(fn))
+    TPW_PUBLIC("euclidean_distances(Tensor x1, Tensor? x2=None) -> Tensor", euclidean_distances);
+    TPW_PUBLIC("haversine_distances(Tensor x1, Tensor? x2=None) -> Tensor", haversine_distances);
+    TPW_PUBLIC("manhattan_distances(Tensor x1, Tensor? x2=None) -> Tensor", manhattan_distances);
+    TPW_PUBLIC("cosine_distances(Tensor x1, Tensor? x2=None) -> Tensor", cosine_distances);
+    TPW_PUBLIC("linear_kernel(Tensor x1, Tensor? x2=None) -> Tensor", linear_kernel);
+    TPW_PUBLIC("polynomial_kernel(Tensor x1, Tensor? x2=None, int degree=3, float? gamma=None, float coef0=1) -> Tensor", polynomial_kernel);
+    TPW_PUBLIC("sigmoid_kernel(Tensor x1, Tensor? x2=None, float? gamma=None, float coef0=1) -> Tensor", sigmoid_kernel);
+    TPW_PUBLIC("rbf_kernel(Tensor x1, Tensor? x2=None, float? gamma=None) -> Tensor", rbf_kernel);
+    TPW_PUBLIC("laplacian_kernel(Tensor x1, Tensor? x2=None, float? gamma=None) -> Tensor", laplacian_kernel);
+    TPW_PUBLIC("cosine_similarity(Tensor x1, Tensor? x2=None) -> Tensor", cosine_similarity);
+    TPW_PUBLIC("additive_chi2_kernel(Tensor x1, Tensor? x2=None) -> Tensor", additive_chi2_kernel);
+    TPW_PUBLIC("chi2_kernel(Tensor x1, Tensor? x2=None, float gamma=1.0) -> Tensor", chi2_kernel);
+    TPW_PUBLIC("directed_hausdorff_distances(Tensor x1, Tensor? x2=None, *, bool shuffle=False, Generator? generator=None) -> (Tensor output, Tensor x1_indices, Tensor x2_indices)", directed_hausdorff_distances);
+    TPW_PUBLIC("minkowski_distances(Tensor x1, Tensor? x2=None, float p=2) -> Tensor", minkowski_distances);
+    TPW_PUBLIC("wminkowski_distances(Tensor x1, Tensor? x2=None, float p=2, Tensor? w=None) -> Tensor", wminkowski_distances);
+    TPW_PUBLIC("sqeuclidean_distances(Tensor x1, Tensor? x2=None) -> Tensor", sqeuclidean_distances);
+    TPW_PUBLIC("correlation_distances(Tensor x1, Tensor? x2=None) -> Tensor", correlation_distances);
+    TPW_PUBLIC("hamming_distances(Tensor x1, Tensor? x2=None) -> Tensor", hamming_distances);
+    TPW_PUBLIC("jaccard_distances(Tensor x1, Tensor? x2=None) -> Tensor", jaccard_distances);
+    TPW_PUBLIC("kulsinski_distances(Tensor x1, Tensor? x2=None) -> Tensor", kulsinski_distances);
+    TPW_PUBLIC("kulczynski1_distances(Tensor x1, Tensor? x2=None) -> Tensor", kulczynski1_distances);
+    TPW_PUBLIC("seuclidean_distances(Tensor x1, Tensor? x2=None, Tensor? V=None) -> Tensor", seuclidean_distances);
+    TPW_PUBLIC("cityblock_distances(Tensor x1, Tensor? x2=None) -> Tensor", cityblock_distances);
+    TPW_PUBLIC("mahalanobis_distances(Tensor x1, Tensor? x2=None, Tensor? VI=None) -> Tensor", mahalanobis_distances);
+    TPW_PUBLIC("chebyshev_distances(Tensor x1, Tensor? x2=None) -> Tensor", chebyshev_distances);
+    TPW_PUBLIC("braycurtis_distances(Tensor x1, Tensor? x2=None) -> Tensor", braycurtis_distances);
+    TPW_PUBLIC("canberra_distances(Tensor x1, Tensor? x2=None) -> Tensor", canberra_distances);
+    TPW_PUBLIC("jensenshannon_distances(Tensor x1, Tensor? x2=None, float? base=None) -> Tensor", jensenshannon_distances);
+    TPW_PUBLIC("yule_distances(Tensor x1, Tensor? x2=None) -> Tensor", yule_distances);
+    TPW_PUBLIC("dice_distances(Tensor x1, Tensor? x2=None) -> Tensor", dice_distances);
+    TPW_PUBLIC("rogerstanimoto_distances(Tensor x1, Tensor? x2=None) -> Tensor", rogerstanimoto_distances);
+    TPW_PUBLIC("russellrao_distances(Tensor x1, Tensor? x2=None) -> Tensor", russellrao_distances);
+    TPW_PUBLIC("sokalmichener_distances(Tensor x1, Tensor? x2=None) -> Tensor", sokalmichener_distances);
+    TPW_PUBLIC("sokalsneath_distances(Tensor x1, Tensor? x2=None) -> Tensor", sokalsneath_distances);
+    TPW_PUBLIC("snr_distances(Tensor x1, Tensor? x2=None) -> Tensor", snr_distances);
+    TPW_PUBLIC("l1_distances(Tensor x1, Tensor? x2=None) -> Tensor", l1_distances);
+    TPW_PUBLIC("l2_distances(Tensor x1, Tensor? x2=None) -> Tensor", l2_distances);
+    TPW_PUBLIC("lp_distances(Tensor x1, Tensor? x2=None, float p=2) -> Tensor", lp_distances);
+    TPW_PUBLIC("linf_distances(Tensor x1, Tensor? x2=None) -> Tensor", linf_distances);
+#undef TPW_PUBLIC
+}
+
+}  // namespace tpw_ext

@@ -1,0 +1,112 @@
+// Shared helpers of the PyTorch extension (host side only; kernels live behind the C ABI).
+#pragma once
+
+#include <ATen/ATen.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <string>
+#include <tuple>
+#include <utility>
+
+#include "torchpairwise_amd.h"
+
+namespace tpw_ext {
+
+// Launch stream of the current device (PyTorch's current HIP stream).
+inline void *current_stream() {
+    return reinterpret_cast<void *>(c10::hip::getCurrentHIPStream().stream());
+}
+
+inline void check_rc(int rc, const char *what) {
+    TORCH_CHECK(rc == TPW_OK, what, ": ", tpw_last_error());
+}
+
+// Scratch memory from the caching allocator on `like`'s device.
+inline at::Tensor workspace(size_t bytes, const at::Tensor &like) {
+    return at::empty({(int64_t)(bytes > 0 ? bytes : 1)}, like.options().dtype(at::kByte));
+}
+
+inline int float_code(at::ScalarType t) {
+    switch (t) {
+        case at::kFloat: return TPW_F32;
+        case at::kBFloat16: return TPW_BF16;
+        case at::kHalf: return TPW_F16;
+        case at::kDouble: return TPW_F64;
+        case at::kChar: return TPW_I8;
+        case at::kByte: return TPW_U8;
+        case at::kShort: return TPW_I16;
+        case at::kInt: return TPW_I32;
+        case at::kLong: return TPW_I64;
+        default: return -1;
+    }
+}
+
+// [n, d] -> [1, n, d]; [b, n, d] unchanged (contiguous either way).
+inline at::Tensor as3(const at::Tensor &x) {
+    return x.dim() == 2 ? x.unsqueeze(0).contiguous() : x.contiguous();
+}
+
+// Epilogue codes of the inner-product internal op (same values as TPW_EPI_*).
+constexpr int64_t kEuclidean = TPW_EPI_EUCLIDEAN;
+constexpr int64_t kSqEuclidean = TPW_EPI_SQEUCLIDEAN;
+constexpr int64_t kCosineSim = TPW_EPI_COSINE_SIM;
+constexpr int64_t kCosineDist = TPW_EPI_COSINE_DIST;
+
+// Dispatcher handles of the internal ops (defined in registration.cpp).
+at::Tensor pw_inner(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue);
+std::tuple<at::Tensor, at::Tensor> pw_inner_backward(const at::Tensor &grad, const at::Tensor &x1,
+                                                     const at::Tensor &x2, const at::Tensor &res,
+                                                     int64_t epilogue);
+at::Tensor pw_lp(const at::Tensor &x1, const at::Tensor &x2, double p);
+std::tuple<at::Tensor, at::Tensor> pw_lp_backward(const at::Tensor &grad, const at::Tensor &x1,
+                                                  const at::Tensor &x2, const at::Tensor &dist,
+                                                  double p);
+at::Tensor pw_binary_reduce(const char *name, const at::Tensor &x1, const at::Tensor &x2);
+at::Tensor jaccard_fused(const at::Tensor &x1, const at::Tensor &x2);
+at::Tensor prf_div(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
+std::tuple<at::Tensor, at::Tensor> prf_div_backward(const at::Tensor &g, const at::Tensor &x,
+                                                    const at::Tensor &y, c10::string_view mode);
+std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff(
+    const at::Tensor &x1, const at::Tensor &x2, bool shuffle, c10::optional<at::Generator> gen);
+std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward(
+    const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
+    c10::optional<at::Generator> gen);
+
+// prf_div mode string -> identity flag (common/prf_div_mode.h:13-23 of the reference).
+inline bool prf_identity(c10::string_view mode) {
+    if (mode == "zero") return false;
+    if (mode == "identity") return true;
+    TORCH_CHECK(false, "mode must be either zero or identity. Got ", std::string(mode));
+}
+
+// Shared shape checks of the Hausdorff ops (csrc/ops/cpu/hausdorff_kernel.cpp:109-123).
+inline void check_hausdorff_shapes(const at::Tensor &x1, const at::Tensor &x2) {
+    at::CheckedFrom c = "_directed_hausdorff_forward";
+    auto args = {at::TensorArg(x1, "x1", 1), at::TensorArg(x2, "x2", 2)};
+    at::checkAllSameType(c, args);
+    const bool unbatched = x1.dim() == 3;
+    TORCH_CHECK(unbatched || x1.dim() == 4, "x1 must be 3-D (unbatched) or 4-D (batched) tensor.")
+    TORCH_CHECK(unbatched || x2.dim() == 4, "x2 must be 3-D (unbatched) or 4-D (batched) tensor.")
+    TORCH_CHECK(unbatched || (x1.size(0) == x2.size(0)), "batch_size of x1 and x2 do not match.")
+    TORCH_CHECK((unbatched && x1.size(2) == x2.size(2)) || (!unbatched && x1.size(3) == x2.size(3)),
+                "feature dimension of x1 and x2 do not match.")
+}
+
+// Hausdorff iteration orders drawn as the reference draws them: per batch, x1's then x2's
+// permutation from `gen` on the inputs' device (csrc/ops/cpu/hausdorff_kernel.cpp:149-158).
+inline std::pair<at::Tensor, at::Tensor> hausdorff_perms(int64_t batch, int64_t p1, int64_t p2,
+                                                         const at::TensorOptions &opts,
+                                                         c10::optional<at::Generator> gen) {
+    auto perm1 = at::empty({batch, p1}, opts.dtype(at::kLong));
+    auto perm2 = at::empty({batch, p2}, opts.dtype(at::kLong));
+    for (int64_t b = 0; b < batch; ++b) {
+        auto r1 = perm1[b], r2 = perm2[b];
+        at::randperm_outf(p1, gen, r1);
+        at::randperm_outf(p2, gen, r2);
+    }
+    return {perm1, perm2};
+}
+
+}  // namespace tpw_ext

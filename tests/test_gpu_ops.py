@@ -145,6 +145,11 @@ def test_boolean_family_gpu_equals_cpu(name):
     b1 = rand(60, 100, seed=0) < 0.5
     b2 = rand(50, 100, seed=1) < 0.5
     fn = getattr(tp, f"{name}_distances")
+    if name == "russellrao":
+        # (D - and_count) / D: ATen divides a GPU tensor by a scalar as a multiply by the
+        # reciprocal, its CPU kernel divides; the counts themselves are exact (1 ulp apart)
+        assert_close(fn(b1.to(DEV), b2.to(DEV)), fn(b1, b2), rtol=1.2e-7, atol=0, what=name)
+        return
     assert_equal(fn(b1.to(DEV), b2.to(DEV)), fn(b1, b2), name)
 
 

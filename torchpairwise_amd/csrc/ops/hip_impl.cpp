@@ -32,7 +32,7 @@ at::Tensor pw_inner_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t epi
     TORCH_CHECK(x1.scalar_type() == x2.scalar_type(), "_pw_inner: x1 and x2 dtypes differ");
     const int dt = float_dtype("_pw_inner", x1);
     TORCH_CHECK(epilogue >= TPW_EPI_DOT && epilogue <= TPW_EPI_COSINE_DIST, "_pw_inner: bad epilogue");
-    c10::hip::HIPGuard guard(x1.device());
+    DeviceGuard guard(x1.device());
     auto a = as3(x1), b = as3(x2);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto out = at::empty({B, n, m}, a.options());
@@ -59,7 +59,7 @@ std::tuple<at::Tensor, at::Tensor> pw_inner_backward_cuda(const at::Tensor &grad
                                                           const at::Tensor &res, int64_t epilogue) {
     check_cuda_pair("_pw_inner_backward", x1, x2);
     const int dt = float_dtype("_pw_inner_backward", x1);
-    c10::hip::HIPGuard guard(x1.device());
+    DeviceGuard guard(x1.device());
     auto a = as3(x1), b = as3(x2);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto g = grad.to(a.scalar_type()).reshape({B, n, m}).contiguous();
@@ -97,7 +97,7 @@ at::Tensor pw_lp_cuda(const at::Tensor &x1, const at::Tensor &x2, double p) {
     TORCH_CHECK(x1.scalar_type() == at::kFloat && x2.scalar_type() == at::kFloat,
                 "_pw_lp: supports float32 on the GPU");
     TORCH_CHECK(p >= 0, "cdist only supports non-negative p values");
-    c10::hip::HIPGuard guard(x1.device());
+    DeviceGuard guard(x1.device());
     auto a = as3(x1), b = as3(x2);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto out = at::empty({B, n, m}, a.options());
@@ -112,7 +112,7 @@ std::tuple<at::Tensor, at::Tensor> pw_lp_backward_cuda(const at::Tensor &grad, c
                                                        double p) {
     check_cuda_pair("_pw_lp_backward", x1, x2);
     TORCH_CHECK(x1.scalar_type() == at::kFloat, "_pw_lp_backward: supports float32 on the GPU");
-    c10::hip::HIPGuard guard(x1.device());
+    DeviceGuard guard(x1.device());
     auto a = as3(x1), b = as3(x2);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto g = grad.to(at::kFloat).reshape({B, n, m}).contiguous();
@@ -161,7 +161,7 @@ template <int OP, int RED>
 at::Tensor pw_reduce_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), "expected GPU tensors");
     check_binary_shapes(x1, x2);
-    c10::hip::HIPGuard guard(x1.device());
+    DeviceGuard guard(x1.device());
     const auto common = at::result_type(x1, x2);
     auto a = as3(x1.to(common)), b = as3(x2.to(common));
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
@@ -192,7 +192,7 @@ at::Tensor pw_reduce_cuda(const at::Tensor &x1, const at::Tensor &x2) {
 at::Tensor jaccard_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), "expected GPU tensors");
     check_binary_shapes(x1, x2);
-    c10::hip::HIPGuard guard(x1.device());
+    DeviceGuard guard(x1.device());
     auto a = as3(x1.to(at::kBool)), b = as3(x2.to(at::kBool));
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto out = at::empty({B, n, m}, a.options().dtype(at::kFloat));
@@ -215,7 +215,7 @@ at::Tensor prf_div_cuda(const at::Tensor &x, const at::Tensor &y, c10::string_vi
     const bool identity = prf_identity(mode);
     TORCH_CHECK(x.sizes() == y.sizes(), "prf_div: input and other must have the same shape, got ",
                 x.sizes(), " and ", y.sizes());
-    c10::hip::HIPGuard guard(x.device());
+    DeviceGuard guard(x.device());
     auto common = at::result_type(x, y);
     if (!at::isFloatingType(common)) common = at::kFloat;  // integer inputs divide in float32
     auto a = x.to(common).contiguous(), b = y.to(common).contiguous();
@@ -232,7 +232,7 @@ at::Tensor prf_div_cuda(const at::Tensor &x, const at::Tensor &y, c10::string_vi
 std::tuple<at::Tensor, at::Tensor> prf_div_backward_cuda(const at::Tensor &g, const at::Tensor &x,
                                                          const at::Tensor &y, c10::string_view mode) {
     const bool identity = prf_identity(mode);
-    c10::hip::HIPGuard guard(x.device());
+    DeviceGuard guard(x.device());
     auto common = at::result_type(x, y);
     if (!at::isFloatingType(common)) common = at::kFloat;
     auto a = x.to(common).contiguous(), b = y.to(common).contiguous();
@@ -277,7 +277,7 @@ HdRun hausdorff_run(const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
 
 std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff_cuda(
     const at::Tensor &x1, const at::Tensor &x2, bool shuffle, c10::optional<at::Generator> gen) {
-    c10::hip::HIPGuard guard(x1.device());
+    DeviceGuard guard(x1.device());
     HdRun r = hausdorff_run(x1, x2, shuffle, gen);
     if (x1.dim() == 3) return {r.out.squeeze(0), r.i1.squeeze(0), r.i2.squeeze(0)};
     return {r.out, r.i1, r.i2};
@@ -286,7 +286,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff_cuda(
 std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_cuda(
     const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
     c10::optional<at::Generator> gen) {
-    c10::hip::HIPGuard guard(x1.device());
+    DeviceGuard guard(x1.device());
     // the reference re-runs the forward here (csrc/ops/cpu/hausdorff_kernel.cpp:269-306)
     HdRun r = hausdorff_run(x1, x2, shuffle, gen);
     auto g = grad.to(at::kFloat).reshape(r.out.sizes()).contiguous();

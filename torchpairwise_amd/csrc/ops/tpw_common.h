@@ -2,8 +2,8 @@
 #pragma once
 
 #include <ATen/ATen.h>
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
 #include <string>
@@ -14,9 +14,13 @@
 
 namespace tpw_ext {
 
+// PyTorch-ROCm tensors report device type "cuda"; its HIP streams and device guards are
+// the *MasqueradingAsCUDA variants.
+using DeviceGuard = c10::hip::HIPGuardMasqueradingAsCUDA;
+
 // Launch stream of the current device (PyTorch's current HIP stream).
 inline void *current_stream() {
-    return reinterpret_cast<void *>(c10::hip::getCurrentHIPStream().stream());
+    return reinterpret_cast<void *>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
 }
 
 inline void check_rc(int rc, const char *what) {

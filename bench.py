@@ -31,7 +31,29 @@ import time
 
 PEAK_FP32_MFMA = 157.3e12
 PEAK_HBM = 8.0e12
-PEAK_VALU_LANE_OPS = 256 * 64 * 2.4e9  # non-packed VALU issue rate (lane-ops/s)
+# FP32 vector peak 157.3 TFLOP/s = 256 CU x 4 SIMD x 32 lanes x 2 (FMA) x 2.4 GHz: a
+# non-packed VALU issue rate of 7.86e13 lane-ops/s
+PEAK_VALU_LANE_OPS = 256 * 4 * 32 * 2.4e9
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "traffic_euclidean_manhattan_hamming_16384x128.txt")
+
+
+def measured_traffic(kernel_prefix):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (KiB per dispatch), each scaled by what the counter read for a plain 1 GiB copy."""
+    try:
+        rows = [l.split() for l in open(TRAFFIC_FILE) if l.strip() and not l.startswith("#")]
+    except OSError:
+        return None
+    kv = {r[0]: float(r[1]) for r in rows if len(r) == 2}
+    if not {"copy_bytes", "copy_fetch_kib", "copy_write_kib"} <= kv.keys():
+        return None
+    f_scale = kv["copy_bytes"] / (kv["copy_fetch_kib"] * 1024)
+    w_scale = kv["copy_bytes"] / (kv["copy_write_kib"] * 1024)
+    for r in rows:
+        if len(r) == 5 and r[0].startswith(kernel_prefix) and r[1] == "fetch_kib":
+            return (float(r[2]) * f_scale + float(r[4]) * w_scale) * 1024
+    return None
 
 
 def parse():
@@ -43,6 +65,12 @@ def parse():
     ap.add_argument("--d", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list of l2,l1,hamming (default all)")
+    ap.add_argument("--with-copy", action="store_true",
+                    help="also run one plain device copy of 1 GiB (torch copy_) so a rocprofv3 "
+                         "--pmc FETCH_SIZE / WRITE_SIZE pass has a known-size reference kernel")
+    ap.add_argument("--config", default="M",
+                    help="M (default: the metric's workload) or C2..C5: time the other "
+                         "BASELINE.json configurations (one JSON line per op, not the headline)")
     return ap.parse_args()
 
 
@@ -90,12 +118,108 @@ def cpu_baseline_l2(n, d, budget_s=15.0):
                       f"euclidean_distances), {reps} reps, {t_total:.1f} s"}
 
 
+def run_config(cfg, steps, warmup):
+    """Times the full-size BASELINE.json configurations C2..C5 through the drop-in ops
+    (forward, and forward + backward where the configuration asks for it)."""
+    import torch
+
+    import torchpairwise_amd as tp
+
+    dev = "cuda"
+    lines = []
+
+    def emit(name, ms, pf, extra=None):
+        d = {"config": cfg, "op": name, "ms_per_call": ms, "pair_features_per_s": pf / (ms * 1e-3)}
+        d.update(extra or {})
+        lines.append(d)
+        print(json.dumps(d), flush=True)
+
+    if cfg == "C2":
+        B, N, D = 8, 8192, 256
+        for dtype in (torch.float32, torch.bfloat16):
+            x1 = torch.randn(B, N, D, generator=torch.Generator().manual_seed(0)).to(dtype).to(dev)
+            x2 = torch.randn(B, N, D, generator=torch.Generator().manual_seed(1)).to(dtype).to(dev)
+            g = torch.randn(B, N, N, generator=torch.Generator().manual_seed(2)).to(dtype).to(dev)
+            pf = B * N * N * D
+            for fn in ("euclidean_distances", "cosine_distances"):
+                f = getattr(tp, fn)
+                ms, _ = time_op(lambda: f(x1, x2), steps, warmup)
+                emit(f"{fn} fwd {dtype}", ms, pf, {"tflops": 2 * pf / (ms * 1e-3) / 1e12})
+                a = x1.detach().requires_grad_()
+                b = x2.detach().requires_grad_()
+
+                def fb():
+                    a.grad = None
+                    b.grad = None
+                    f(a, b).backward(g)
+
+                ms, _ = time_op(fb, steps, warmup)
+                emit(f"{fn} fwd+bwd {dtype}", ms, pf, {"tflops": 6 * pf / (ms * 1e-3) / 1e12})
+            del x1, x2, g
+            torch.cuda.empty_cache()
+    elif cfg == "C3":
+        N, D = 16384, 128
+        x1 = (torch.rand(N, D, generator=torch.Generator().manual_seed(0)) * 2 - 1).to(dev)
+        x2 = (torch.rand(N, D, generator=torch.Generator().manual_seed(1)) * 2 - 1).to(dev)
+        pf = N * N * D
+        ms, _ = time_op(lambda: tp.minkowski_distances(x1, x2, 3.0), steps, warmup)
+        emit("minkowski p=3 fwd", ms, pf)
+        a, b = x1.clone().requires_grad_(), x2.clone().requires_grad_()
+        ones = torch.ones(N, N, device=dev)
+
+        def fb():
+            a.grad = None
+            b.grad = None
+            tp.minkowski_distances(a, b, 3.0).backward(ones)
+
+        ms, _ = time_op(fb, steps, warmup)
+        emit("minkowski p=3 fwd+bwd", ms, pf)
+        ms, _ = time_op(lambda: tp.chebyshev_distances(x1, x2), steps, warmup)
+        emit("chebyshev fwd", ms, pf)
+    elif cfg == "C4":
+        N, D = 32768, 1024
+        h1 = (torch.rand(N, D, generator=torch.Generator().manual_seed(0)) < 0.5).to(dev)
+        h2 = (torch.rand(N, D, generator=torch.Generator().manual_seed(1)) < 0.5).to(dev)
+        pf = N * N * D
+        ms, _ = time_op(lambda: tp.hamming_distances(h1, h2), steps, warmup)
+        emit("hamming fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+        j1 = (torch.rand(N, D, generator=torch.Generator().manual_seed(0)) < 0.1).to(dev)
+        j2 = (torch.rand(N, D, generator=torch.Generator().manual_seed(1)) < 0.1).to(dev)
+        ms, _ = time_op(lambda: tp.jaccard_distances(j1, j2), steps, warmup)
+        emit("jaccard fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+    elif cfg == "C5":
+        C, P, D = 16, 65536, 3
+        x1 = torch.rand(C, P, D, generator=torch.Generator().manual_seed(0)).to(dev)
+        x2 = (torch.rand(C, P, D, generator=torch.Generator().manual_seed(1)) + 0.05).to(dev)
+        pf = C * C * P * P * D
+        ms, _ = time_op(lambda: tp.directed_hausdorff_distances(x1, x2), steps, warmup)
+        emit("directed_hausdorff fwd", ms, pf, {"note": "nominal B1*B2*P1*P2*D pair-features"})
+        a = x1.clone().requires_grad_()
+        g = torch.randn(C, C, generator=torch.Generator().manual_seed(2)).to(dev)
+
+        def fb():
+            a.grad = None
+            tp.directed_hausdorff_distances(a, x2)[0].backward(g)
+
+        ms, _ = time_op(fb, steps, warmup)
+        emit("directed_hausdorff fwd+bwd", ms, pf)
+    else:
+        raise SystemExit(f"unknown config {cfg}")
+    return lines
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; run with --gpus 1 "
                                    "(multi-GPU sharding is described in DESIGN.md, not run)"}))
         sys.exit(2)
+    if args.config != "M":
+        import torch
+
+        assert torch.cuda.is_available(), "bench.py needs a GPU"
+        run_config(args.config, args.steps, args.warmup)
+        return
     import torch
 
     import torchpairwise_amd as tp
@@ -111,6 +235,12 @@ def main():
     b2 = (torch.rand(n, d, generator=torch.Generator().manual_seed(1)) < 0.5).to(dev)
     only = set(args.only.split(",")) if args.only else {"l2", "l1", "hamming"}
     pf = n * n * d
+    if args.with_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     extra = {}
     res = {}
 
@@ -120,7 +250,8 @@ def main():
         res["l2"] = {"ms": ms, "wall_ms": wall_ms, "value": pf / (ms * 1e-3),
                      "roofline": {"bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12,
                                   "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                                  "frac": flops / (ms * 1e-3) / PEAK_FP32_MFMA, "traffic": None}}
+                                  "frac": flops / (ms * 1e-3) / PEAK_FP32_MFMA,
+                                  "traffic": measured_traffic("pairwise_inner_kernel<float,float,1,true>")}}
     if "l1" in only:
         ms, wall_ms = time_op(lambda: tp.manhattan_distances(x1, x2), args.steps, args.warmup)
         ops = 2.0 * pf  # v_sub + abs-modified v_add per pair-feature
@@ -129,8 +260,11 @@ def main():
             "roofline": {"bound": "valu", "achieved": ops / (ms * 1e-3) / 1e12,
                          "peak": PEAK_VALU_LANE_OPS / 1e12, "unit": "Tlane-op/s",
                          "frac": ops / (ms * 1e-3) / PEAK_VALU_LANE_OPS,
-                         "convention": "2 VALU lane-ops per pair-feature (sub, abs-add) against "
-                                       "the non-packed issue rate 256 CU x 64 lanes x 2.4 GHz"}}
+                         "convention": "2 VALU lane-ops per pair-feature (v_sub_f32, abs-modified "
+                                       "v_add_f32) against the non-packed FP32 issue rate "
+                                       "256 CU x 4 SIMD x 32 lanes x 2.4 GHz; against the "
+                                       "157.3 TFLOP/s spec counting each op as one flop the "
+                                       "fraction is half of this"}}
     if "hamming" in only:
         ms, wall_ms = time_op(lambda: tp.hamming_distances(b1, b2), args.steps, args.warmup)
         out_bytes = 4.0 * n * n

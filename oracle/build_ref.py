@@ -1,0 +1,58 @@
+#!/usr/bin/env python3
+"""Compiles the reference's own CPU kernels for the hot path, from the sources where they
+lie under /root/reference, into oracle/_ref/libtorchpairwise_ref.so (git-ignored; it travels
+to the GPU box like the other built libraries).  TEST INFRASTRUCTURE ONLY.
+
+Sources (g++ directly, against the installed torch headers; nothing is copied):
+  csrc/ops/hausdorff.cpp, cpu/hausdorff_kernel.cpp, autograd/hausdorff_kernel.cpp
+  csrc/ops/pairwise_binary.cpp, cpu/pairwise_binary_kernels.cpp
+  csrc/ops/prf_div.cpp, cpu/prf_div_kernel.cpp, autograd/prf_div_kernel.cpp
+The library registers the reference's own torch.ops.torchpairwise schemas, so it is loaded
+only in a separate process (oracle/ref_runner.py), never next to torchpairwise_amd.
+The cdist-routed metrics need no build: their arithmetic is torch's at::cdist.
+"""
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+REF = Path(os.environ.get("TPW_REFERENCE", "/root/reference")) / "torchpairwise" / "csrc"
+OUT = Path(__file__).resolve().parent / "_ref"
+SOURCES = ["ops/hausdorff.cpp", "ops/cpu/hausdorff_kernel.cpp", "ops/autograd/hausdorff_kernel.cpp",
+           "ops/pairwise_binary.cpp", "ops/cpu/pairwise_binary_kernels.cpp",
+           "ops/prf_div.cpp", "ops/cpu/prf_div_kernel.cpp", "ops/autograd/prf_div_kernel.cpp"]
+
+
+def main() -> int:
+    if not REF.exists():
+        print(f"[build_ref] {REF} not present; skipping the reference build")
+        return 0
+    import torch
+    from torch.utils import cpp_extension
+
+    inc = [f"-I{p}" for p in cpp_extension.include_paths()]
+    libdir = os.path.join(os.path.dirname(torch.__file__), "lib")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    OUT.mkdir(exist_ok=True)
+    objs = []
+
+    def compile_one(src):
+        obj = OUT / (src.replace("/", "_") + ".o")
+        subprocess.run(["g++", "-O2", "-std=c++17", "-fPIC", "-fopenmp", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+                        *inc, f"-I{REF}", "-c", str(REF / src), "-o", str(obj)], check=True)
+        return obj
+
+    with cf.ThreadPoolExecutor(8) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
+    lib = OUT / "libtorchpairwise_ref.so"
+    subprocess.run(["g++", "-shared", "-fopenmp", *map(str, objs), "-o", str(lib), f"-L{libdir}",
+                    "-lc10", "-ltorch", "-ltorch_cpu", f"-Wl,-rpath,{libdir}"], check=True)
+    for o in objs:
+        o.unlink()
+    print(f"[build_ref] {lib}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

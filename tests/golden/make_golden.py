@@ -1,0 +1,99 @@
+#!/usr/bin/env python3
+"""Writes the golden fixtures in tests/golden/*.npz.
+
+The reference ships no golden vectors (its tests only print differences), so the expected
+values here come from independent implementations and from hand-derived cases, never from
+this build's oracle:
+
+* hamming / jaccard / dice ...:  scipy.spatial.distance.cdist in float64, rounded to float32
+  (a float64 quotient of integers below 2^24 rounds to the correctly rounded float32 one);
+  the pw*_sum counts by an explicit Python loop over elements;
+* minkowski p = 1, 2, 3, inf:   scipy.spatial.distance.cdist in float64;
+* cosine:                       sklearn.metrics.pairwise.cosine_distances in float64;
+* directed Hausdorff:           scipy.spatial.distance.directed_hausdorff (value, float64) on
+  random clouds, plus hand-built clouds whose maxima / minima tie, with the expected
+  indices derived by hand from the reference's rules (last m reaching the max, first n
+  reaching that m's min; csrc/ops/cpu/hausdorff_kernel.cpp:25-51).
+
+Run from the repository root: python tests/golden/make_golden.py
+"""
+from pathlib import Path
+
+import numpy as np
+from scipy.spatial.distance import cdist, directed_hausdorff
+from sklearn.metrics.pairwise import cosine_distances
+
+OUT = Path(__file__).resolve().parent
+
+
+def boolean():
+    rng = np.random.default_rng(20260101)
+    x1 = rng.random((7, 45)) < 0.5
+    x2 = rng.random((6, 45)) < 0.3
+    x1[0] = False  # all-zero rows: jaccard 0 against an all-zero partner
+    x2[0] = False
+    ops = {"and": np.logical_and, "or": np.logical_or, "xor": np.logical_xor,
+           "eq": np.equal, "ne": np.not_equal}
+    counts = {}
+    for name, f in ops.items():
+        c = np.zeros((7, 6), np.int64)
+        for i in range(7):
+            for j in range(6):
+                c[i, j] = sum(int(f(x1[i, k], x2[j, k])) for k in range(45))
+        counts[f"count_{name}"] = c
+    out = dict(x1=x1, x2=x2, **counts)
+    for metric in ("hamming", "jaccard", "dice", "rogerstanimoto", "russellrao", "sokalsneath", "yule"):
+        with np.errstate(divide="ignore", invalid="ignore"):
+            out[metric] = cdist(x1, x2, metric)
+    out["hamming_f32"] = out["hamming"].astype(np.float32)
+    out["jaccard_f32"] = out["jaccard"].astype(np.float32)
+    # hamming with d a power of two: exact dyadic values k / 64
+    y1 = rng.random((5, 64)) < 0.5
+    y2 = rng.random((4, 64)) < 0.5
+    out["y1"], out["y2"] = y1, y2
+    out["hamming_d64"] = cdist(y1, y2, "hamming").astype(np.float32)
+    np.savez_compressed(OUT / "boolean.npz", **out)
+
+
+def minkowski():
+    rng = np.random.default_rng(20260102)
+    x1 = rng.standard_normal((9, 13))
+    x2 = rng.standard_normal((11, 13))
+    out = dict(x1=x1, x2=x2)
+    for p in (1, 2, 3):
+        out[f"p{p}"] = cdist(x1, x2, "minkowski", p=p)
+    out["pinf"] = cdist(x1, x2, "chebyshev")
+    out["cosine"] = cosine_distances(x1, x2)
+    np.savez_compressed(OUT / "minkowski_cosine.npz", **out)
+
+
+def hausdorff():
+    rng = np.random.default_rng(20260103)
+    a = rng.random((3, 40, 3)).astype(np.float32)
+    b = (rng.random((2, 50, 3)) + 0.05).astype(np.float32)
+    value = np.zeros((3, 2))
+    for i in range(3):
+        for j in range(2):
+            value[i, j] = directed_hausdorff(a[i].astype(np.float64), b[j].astype(np.float64))[0]
+    # hand-built ties (1-D points padded to 3-D)
+    def pts(xs):
+        return np.array([[x, 0.0, 0.0] for x in xs], np.float32)
+
+    # m mins: [0, 0, 1, 1] -> max 1 reached by m = 2 and m = 3 -> last m = 3;
+    # for m = 3 (x = 3), n = 2 (x = 2) and n = 3 (x = 4) tie at 1 -> first n = 2
+    t1 = (pts([0, 1, 3, 3]), pts([0, 1, 2, 4]), 1.0, 3, 2)
+    # single winner in the middle, later points closer: m = 1 (x = 10) min 4 at n = 2 (x = 6)
+    t2 = (pts([0, 10, 1]), pts([0, 1, 6, 14]), 4.0, 1, 2)
+    # identical clouds: every min is 0 -> last m, and its first n at distance 0
+    t3 = (pts([5, 2, 7]), pts([2, 7, 5, 5]), 0.0, 2, 1)
+    np.savez_compressed(
+        OUT / "hausdorff.npz", a=a, b=b, value=value,
+        **{f"t{k}_{f}": v for k, t in enumerate((t1, t2, t3), 1)
+           for f, v in zip(("x1", "x2", "value", "idx1", "idx2"), t)})
+
+
+if __name__ == "__main__":
+    boolean()
+    minkowski()
+    hausdorff()
+    print("wrote", sorted(p.name for p in OUT.glob("*.npz")))

@@ -267,3 +267,36 @@ def test_hausdorff_backward_bit_exact(shape):
                                            i1.cpu().numpy(), i2.cpu().numpy())
     assert_equal(gx1, torch.from_numpy(w1), "hausdorff grad_x1")
     assert_equal(gx2, torch.from_numpy(w2), "hausdorff grad_x2")
+
+
+# --------------------------------------------------------------------------------------
+# against the reference's own compiled CPU kernels (oracle/_ref, run in a child process)
+# --------------------------------------------------------------------------------------
+from oracle import ref_runner  # noqa: E402
+
+needs_ref = pytest.mark.skipif(not ref_runner.available(), reason="oracle/_ref not built")
+
+
+@needs_ref
+def test_hausdorff_gpu_equals_reference_kernels(tmp_path):
+    x1, x2 = _hd_inputs(2, 3, 700, 2, 900, 3, seed=21)
+    ref = ref_runner.run("hausdorff", {"x1": x1.numpy(), "x2": x2.numpy()}, tmp_path)
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV))
+    for got, key in zip((out, i1, i2), ("out", "idx1", "idx2")):
+        assert_equal(got, torch.from_numpy(ref[key]), f"vs reference {key}")
+    g = randn(*out.shape, seed=22)
+    ref = ref_runner.run("hausdorff_backward", {"x1": x1.numpy(), "x2": x2.numpy(), "grad": g.numpy()}, tmp_path)
+    gx1, gx2 = capi.directed_hausdorff_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), out, i1, i2)
+    assert_equal(gx1, torch.from_numpy(ref["grad_x1"]), "grad_x1 vs reference")
+    assert_equal(gx2, torch.from_numpy(ref["grad_x2"]), "grad_x2 vs reference")
+
+
+@needs_ref
+def test_boolean_gpu_equals_reference_kernels(tmp_path):
+    x1 = rand(2, 150, 300, seed=23) < 0.5
+    x2 = rand(2, 140, 300, seed=24) < 0.1
+    ref = ref_runner.run("pw_pwne_mean", {"x1": x1.numpy(), "x2": x2.numpy()}, tmp_path)
+    got = capi.bool_pairwise_reduce(x1.to(DEV), x2.to(DEV), capi.BIT_NE, capi.RED_MEAN)
+    assert_equal(got, torch.from_numpy(ref["out"]), "hamming vs reference")
+    ref = ref_runner.run("jaccard", {"x1": x1.numpy(), "x2": x2.numpy()}, tmp_path)
+    assert_equal(capi.jaccard_bool(x1.to(DEV), x2.to(DEV)), torch.from_numpy(ref["out"]), "jaccard vs reference")

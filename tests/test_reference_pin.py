@@ -1,0 +1,72 @@
+"""The oracle against the reference's own CPU kernels, compiled from its sources
+(oracle/build_ref.py) and run in a child process (oracle/ref_runner.py).  Skipped when that
+library is not built."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cref, ref_runner
+from oracle import pairwise as P
+
+pytestmark = pytest.mark.skipif(not ref_runner.available(), reason="oracle/_ref not built")
+
+
+def test_hausdorff_oracle_equals_reference(tmp_path):
+    rng = np.random.default_rng(11)
+    x1 = rng.random((2, 3, 300, 3)).astype(np.float32)
+    x2 = (rng.random((2, 2, 250, 3)) + 0.05).astype(np.float32)
+    ref = ref_runner.run("hausdorff", {"x1": x1, "x2": x2}, tmp_path)
+    for got, key in zip(cref.directed_hausdorff(x1, x2, threads=4), ("out", "idx1", "idx2")):
+        assert np.array_equal(got, ref[key]), key
+    for got, key in zip(P.directed_hausdorff(x1, x2), ("out", "idx1", "idx2")):
+        assert np.array_equal(got, ref[key]), key
+
+
+def test_hausdorff_ties_and_shuffle_equal_reference(tmp_path):
+    rng = np.random.default_rng(12)
+    x1 = rng.integers(0, 3, (2, 2, 80, 3)).astype(np.float32)
+    x2 = rng.integers(0, 3, (2, 3, 70, 3)).astype(np.float32)
+    ref = ref_runner.run("hausdorff", {"x1": x1, "x2": x2}, tmp_path)
+    for got, key in zip(cref.directed_hausdorff(x1, x2), ("out", "idx1", "idx2")):
+        assert np.array_equal(got, ref[key]), key
+    ref = ref_runner.run("hausdorff", {"x1": x1, "x2": x2, "seed": np.int64(9)}, tmp_path)
+    p1, p2 = P.hausdorff_permutations(2, 80, 70, torch.Generator().manual_seed(9))
+    for got, key in zip(cref.directed_hausdorff(x1, x2, p1.numpy(), p2.numpy()), ("out", "idx1", "idx2")):
+        assert np.array_equal(got, ref[key]), f"shuffled {key}"
+
+
+def test_hausdorff_backward_equals_reference(tmp_path):
+    rng = np.random.default_rng(13)
+    x1 = rng.random((3, 120, 3)).astype(np.float32)
+    x2 = (rng.random((2, 90, 3)) + 0.05).astype(np.float32)
+    g = rng.standard_normal((3, 2)).astype(np.float32)
+    ref = ref_runner.run("hausdorff_backward", {"x1": x1, "x2": x2, "grad": g}, tmp_path)
+    out, i1, i2 = P.directed_hausdorff(x1, x2)
+    gx1, gx2 = P.directed_hausdorff_backward(g, x1, x2, out, i1, i2)
+    assert np.array_equal(gx1, ref["grad_x1"]) and np.array_equal(gx2, ref["grad_x2"])
+
+
+@pytest.mark.parametrize("name", ["pwand_sum", "pwor_sum", "pwxor_sum", "pweq_sum", "pwne_sum",
+                                  "pweq_mean", "pwne_mean"])
+def test_pw_reductions_equal_reference(tmp_path, name):
+    rng = np.random.default_rng(14)
+    x1 = rng.random((2, 37, 70)) < 0.5
+    x2 = rng.random((2, 29, 70)) < 0.3
+    ref = ref_runner.run(f"pw_{name}", {"x1": x1, "x2": x2}, tmp_path)
+    op = name.split("_")[0][2:]
+    got = P.pw_reduce_bool(x1, x2, op, name.split("_")[1])
+    assert np.array_equal(got.view(np.int32), ref["out"].view(np.int32))
+
+
+def test_jaccard_and_non_bool_hamming_equal_reference(tmp_path):
+    rng = np.random.default_rng(15)
+    x1 = rng.random((40, 65)) < 0.1
+    x2 = rng.random((30, 65)) < 0.1
+    x1[:3] = False
+    x2[:2] = False
+    ref = ref_runner.run("jaccard", {"x1": x1, "x2": x2}, tmp_path)
+    assert np.array_equal(P.jaccard_distances(x1, x2).view(np.int32), ref["out"].view(np.int32))
+    i1 = rng.integers(0, 4, (20, 33)).astype(np.int64)
+    i2 = rng.integers(0, 4, (25, 33)).astype(np.int64)
+    ref = ref_runner.run("pw_pwne_mean", {"x1": i1, "x2": i2}, tmp_path)
+    assert np.array_equal(P.hamming_distances(i1, i2), ref["out"])

@@ -25,6 +25,8 @@ constexpr int kTile = 128;
 constexpr int kRowVec = 8;              // uint4 per 128-byte chunk row
 constexpr int kLdsStride = kRowVec + 1; // in uint4 (144 bytes)
 constexpr int kGroupRows = 8;
+constexpr int kStageStride = 68;         // floats per staged output row (64 + 4 pad)
+static_assert(4 * 32 * kStageStride * 4 <= 2 * kTile * kLdsStride * 16, "staging fits the panels");
 
 template <typename T>
 struct Elem;
@@ -47,7 +49,8 @@ __device__ __forceinline__ float epilogue(float s, float a1, float a2) {
     } else if constexpr (EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN) {
         float v = (a1 + a2) - 2.0f * s;
         v = v > 0.0f ? v : 0.0f;
-        if constexpr (EPI == TPW_EPI_EUCLIDEAN) v = sqrt_rn(v);
+        // v_sqrt_f32 (1 ulp): the |a|^2 + |b|^2 - 2ab form already carries more error
+        if constexpr (EPI == TPW_EPI_EUCLIDEAN) v = __builtin_amdgcn_sqrtf(v);
         return v;
     } else {
         float den = a1 * a2;
@@ -94,38 +97,34 @@ __device__ __forceinline__ uint4 load_piece(const T *__restrict__ x, int64_t row
     return v;
 }
 
-__device__ __forceinline__ void mfma_chunk(floatx16 (&acc)[2][2], const uint4 (&a)[2][4],
-                                           const uint4 (&b)[2][4], float) {
+// One 16-byte k-piece of the chunk: a[mi] / b[ni] hold the lane's 4 fp32 (or 8 bf16) features
+// of its A row / B column for this piece.
+__device__ __forceinline__ void mfma_piece(floatx16 (&acc)[2][2], const uint4 (&a)[2],
+                                           const uint4 (&b)[2], float) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int e = 0; e < 4; ++e) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-                for (int ni = 0; ni < 2; ++ni) {
-                    const uint32_t av = e == 0 ? a[mi][q].x : e == 1 ? a[mi][q].y : e == 2 ? a[mi][q].z : a[mi][q].w;
-                    const uint32_t bv = e == 0 ? b[ni][q].x : e == 1 ? b[ni][q].y : e == 2 ? b[ni][q].z : b[ni][q].w;
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                        __uint_as_float(av), __uint_as_float(bv), acc[mi][ni], 0, 0, 0);
-                }
+            for (int ni = 0; ni < 2; ++ni) {
+                const uint32_t av = e == 0 ? a[mi].x : e == 1 ? a[mi].y : e == 2 ? a[mi].z : a[mi].w;
+                const uint32_t bv = e == 0 ? b[ni].x : e == 1 ? b[ni].y : e == 2 ? b[ni].z : b[ni].w;
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                    __uint_as_float(av), __uint_as_float(bv), acc[mi][ni], 0, 0, 0);
             }
         }
     }
 }
 
-__device__ __forceinline__ void mfma_chunk(floatx16 (&acc)[2][2], const uint4 (&a)[2][4],
-                                           const uint4 (&b)[2][4], uint16_t) {
+__device__ __forceinline__ void mfma_piece(floatx16 (&acc)[2][2], const uint4 (&a)[2],
+                                           const uint4 (&b)[2], uint16_t) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
-                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    __builtin_bit_cast(bf16x8, a[mi][q]), __builtin_bit_cast(bf16x8, b[ni][q]),
-                    acc[mi][ni], 0, 0, 0);
-            }
+        for (int ni = 0; ni < 2; ++ni) {
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, a[mi]), __builtin_bit_cast(bf16x8, b[ni]), acc[mi][ni],
+                0, 0, 0);
         }
     }
 }
@@ -152,8 +151,13 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
     const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
     int64_t tiles_n, int64_t tiles_m, int64_t total) {
-    __shared__ uint4 As[kTile * kLdsStride];
-    __shared__ uint4 Bs[kTile * kLdsStride];
+    // operand panels (As, Bs); after the K loop the same bytes stage the fp32 output
+    __shared__ uint4 smem[2 * kTile * kLdsStride];
+    uint4 *As = smem;
+    uint4 *Bs = smem + kTile * kLdsStride;
+    // norms of the tile's rows ([0]) and columns ([1]); published by the first barrier of the
+    // K loop (or the one for d == 0)
+    __shared__ float s_aux[2][kTile];
     constexpr int E = Elem<T>::kPer16;
     constexpr int KC = Elem<T>::kChunk;
 
@@ -168,6 +172,12 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
     const int l32 = lane & 31, h = lane >> 5;
 
+    if constexpr (EPI != TPW_EPI_DOT) {
+        const int i = tid & (kTile - 1);
+        if (tid < kTile) s_aux[0][i] = row0 + i < n ? aux1[b * n + row0 + i] : 0.0f;
+        else s_aux[1][i] = col0 + i < m ? aux2[b * m + col0 + i] : 0.0f;
+    }
+
     floatx16 acc[2][2];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
@@ -177,6 +187,7 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
 
     const int64_t nchunks = (d + KC - 1) / KC;
+    if (nchunks == 0) __syncthreads();
     uint4 pa[4], pb[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -205,39 +216,68 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
                 pb[q] = load_piece<T, VEC>(B, m, d, col0 + r, kb + (int64_t)c * E);
             }
         }
-        uint4 a[2][4], bv[2][4];
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int q = 0; q < 4; ++q) {
+            uint4 a[2], bv[2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                a[mi][q] = As[(wr + mi * 32 + l32) * kLdsStride + h * 4 + q];
+            for (int mi = 0; mi < 2; ++mi) a[mi] = As[(wr + mi * 32 + l32) * kLdsStride + h * 4 + q];
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                bv[ni][q] = Bs[(wc + ni * 32 + l32) * kLdsStride + h * 4 + q];
-        mfma_chunk(acc, a, bv, T{});
+            for (int ni = 0; ni < 2; ++ni) bv[ni] = Bs[(wc + ni * 32 + l32) * kLdsStride + h * 4 + q];
+            mfma_piece(acc, a, bv, T{});
+        }
         __syncthreads();
     }
 
     // Accumulator layout of the 32 x 32 MFMA: register r of lane l holds
     // row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+    const bool full = row0 + kTile <= n && col0 + kTile <= m;
+    float a2v[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) a2v[ni] = EPI != TPW_EPI_DOT ? s_aux[1][wc + ni * 32 + l32] : 0.0f;
+    if constexpr (sizeof(OutT) == 4) {
+        if (full) {
+            // fp32 full tile: each wave stages a 32 x 64 half of its tile in its own LDS slice
+            // (the operand panels are free after the K loop's last barrier) and writes it back
+            // as float4 rows, 16 lanes per 256-byte row segment.
+            float *stage = reinterpret_cast<float *>(smem) + wave * (32 * kStageStride);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
+                        const float a1 = EPI != TPW_EPI_DOT ? s_aux[0][wr + mi * 32 + rr] : 0.0f;
+                        stage[rr * kStageStride + ni * 32 + l32] = epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni]);
+                    }
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+                __builtin_amdgcn_wave_barrier();
+                float *orow = reinterpret_cast<float *>(out) + (b * n + row0 + wr + mi * 32) * m + col0 + wc;
+#pragma unroll
+                for (int it = 0; it < 8; ++it) {
+                    const int rr = it * 4 + (lane >> 4), cc = (lane & 15) * 4;
+                    const floatx4 v = *reinterpret_cast<const floatx4 *>(&stage[rr * kStageStride + cc]);
+                    store_nt4(orow + (int64_t)rr * m + cc, v);
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the slice is rewritten
+                __builtin_amdgcn_wave_barrier();
+            }
+            return;
+        }
+    }
+    OutT *obase = out + (b * n + row0 + wr + 4 * h) * m + col0 + wc + l32;
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
-        const int64_t col = col0 + wc + ni * 32 + l32;
-        const bool col_ok = col < m;
-        float a2 = 0.0f;
-        if constexpr (EPI != TPW_EPI_DOT) a2 = col_ok ? aux2[b * m + col] : 0.0f;
+        const bool col_ok = col0 + wc + ni * 32 + l32 < m;
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int64_t row = row0 + wr + mi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < n && col_ok) {
-                    float a1 = 0.0f;
-                    if constexpr (EPI != TPW_EPI_DOT) a1 = aux1[b * n + row];
-                    store_out(out + (b * n + row) * m + col, epilogue<EPI>(acc[mi][ni][r], a1, a2));
-                }
+                const int rr = mi * 32 + 8 * (r >> 2) + (r & 3);  // row in the wave tile, less 4 h
+                const float a1 = EPI != TPW_EPI_DOT ? s_aux[0][wr + 4 * h + rr] : 0.0f;
+                const float v = epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni]);
+                if (full || (row0 + wr + 4 * h + rr < n && col_ok))
+                    store_out(obase + rr * m + ni * 32, v);
             }
         }
     }
@@ -269,14 +309,9 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
     const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
     const int64_t total = tiles_n * tiles_m * batch;
     const bool vec = ((d * (int64_t)sizeof(T)) % 16 == 0) && aligned16(x1) && aligned16(x2);
-    if (vec)
-        hipLaunchKernelGGL((pairwise_inner_kernel<T, OutT, EPI, true>), dim3((unsigned)total),
-                           dim3(kThreads), 0, s, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
-                           tiles_m, total);
-    else
-        hipLaunchKernelGGL((pairwise_inner_kernel<T, OutT, EPI, false>), dim3((unsigned)total),
-                           dim3(kThreads), 0, s, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
-                           tiles_m, total);
+    auto kernel = vec ? pairwise_inner_kernel<T, OutT, EPI, true> : pairwise_inner_kernel<T, OutT, EPI, false>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(kThreads), 0, s, x1, x2, n, m, d, aux1,
+                       aux2, out, tiles_n, tiles_m, total);
     return check_launch("pairwise_inner_kernel");
 }
 

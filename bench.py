@@ -69,8 +69,9 @@ def parse():
                     help="also run one plain device copy of 1 GiB (torch copy_) so a rocprofv3 "
                          "--pmc FETCH_SIZE / WRITE_SIZE pass has a known-size reference kernel")
     ap.add_argument("--config", default="M",
-                    help="M (default: the metric's workload) or C2..C5: time the other "
-                         "BASELINE.json configurations (one JSON line per op, not the headline)")
+                    help="M (default: the metric's workload), C2..C5: time the other "
+                         "BASELINE.json configurations, NB: the neighbour masks at the metric "
+                         "shape (one JSON line per op, not the headline)")
     return ap.parse_args()
 
 
@@ -203,6 +204,34 @@ def run_config(cfg, steps, warmup):
 
         ms, _ = time_op(fb, steps, warmup)
         emit("directed_hausdorff fwd+bwd", ms, pf)
+    elif cfg == "NB":
+        # neighbour masks at the metric shape: the selection kernel alone on a resident
+        # distance matrix (HBM-bound: 4 B read + 1 B written per entry), the whole drop-in
+        # op, and the reference's own route (argsort + index_put_) on the same GPU
+        N, D = 16384, 128
+        x1 = torch.randn(N, D, generator=torch.Generator().manual_seed(0)).to(dev)
+        x2 = torch.randn(N, D, generator=torch.Generator().manual_seed(1)).to(dev)
+        dist = tp.euclidean_distances(x1, x2)
+        pf = N * N * D
+        for k in (1, 8, 32):
+            ms, _ = time_op(lambda: torch.ops.torchpairwise._row_smallest_mask(dist, k + 1), steps, warmup)
+            emit(f"row_smallest_mask count={k + 1}", ms, pf,
+                 {"hbm_GBps": 5.0 * N * N / (ms * 1e-3) / 1e9,
+                  "hbm_frac": 5.0 * N * N / (ms * 1e-3) / PEAK_HBM})
+        ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, 1), steps, warmup)
+        emit("k_neighbors_mask k=1 (euclidean + selection)", ms, pf)
+        ms, _ = time_op(lambda: tp.radius_neighbors_mask(x1, x2, 14.0), steps, warmup)
+        emit("radius_neighbors_mask eps=14 (euclidean + le)", ms, pf)
+
+        def ref_route():
+            inds = dist.argsort(1, False)[:, :2]
+            first = torch.arange(N, device=dev).view(-1, 1).repeat(1, 2)
+            out = torch.zeros(N, N, dtype=torch.bool, device=dev)
+            out.index_put_((first.flatten(), inds.flatten()), torch.tensor(True, device=dev))
+            return out
+
+        ms, _ = time_op(ref_route, max(1, steps // 5), 1)
+        emit("reference route argsort+index_put_ k=1 (selection only)", ms, pf)
     else:
         raise SystemExit(f"unknown config {cfg}")
     return lines

@@ -261,6 +261,21 @@ int tpw_directed_hausdorff_backward(const float *grad, const float *x1, const fl
                                     int64_t p1, int64_t b2, int64_t p2, int64_t d,
                                     float *grad_x1, float *grad_x2, void *stream);
 
+/* ------------------------------------------------------------------------- */
+/* Neighbour masks                                                            */
+/* ------------------------------------------------------------------------- */
+
+/* mask [rows, cols] (bool bytes, 0/1) = 1 at the `count` smallest entries of each row of
+ * dist [rows, cols] (all entries when count >= cols), 0 elsewhere.  Ascending order with
+ * NaN after +inf and -0 == +0; ties broken by the lower column index, i.e. the first
+ * `count` positions of a stable argsort.  dtype: TPW_F32, TPW_BF16 or TPW_F16;
+ * rows, cols < 2^31.  With count = k + 1 this replaces the argsort + slice + index_put_ of
+ * k_neighbors_mask (torchpairwise/csrc/ops/neighbors.cpp:29-34), which materialises a
+ * full sort of every row; the reference's argsort is unstable, so on ties across the
+ * selection boundary its choice is implementation-defined. */
+int tpw_row_smallest_mask(const void *dist, int dtype, int64_t rows, int64_t cols,
+                          int64_t count, void *mask, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -238,3 +238,29 @@ def hausdorff_permutations(batch: int, p1: int, p2: int, generator: torch.Genera
         perm1[b] = torch.randperm(p1, generator=generator)
         perm2[b] = torch.randperm(p2, generator=generator)
     return perm1, perm2
+
+
+def k_smallest_mask(dist, count: int) -> np.ndarray:
+    """Bool mask of each row's `count` smallest entries of dist [rows, cols].
+
+    The selection of k_neighbors_mask with count = k + 1 (csrc/ops/neighbors.cpp:29-34:
+    argsort(1), keep the first k + 1 columns, index_put_ true).  Ordered by a stable
+    ascending sort (numpy's comparison order: NaN last, -0 == +0), so ties at the selection
+    boundary go to the lower column; the reference's argsort is unstable there and its
+    choice is implementation-defined, everywhere else the two sets are the same.
+    """
+    d = np.asarray(dist)
+    if d.dtype not in (np.float32, np.float64):
+        d = d.astype(np.float32)
+    rows, cols = d.shape
+    mask = np.zeros((rows, cols), bool)
+    c = min(int(count), cols)
+    if c:
+        idx = np.argsort(d, axis=1, kind="stable")[:, :c]
+        np.put_along_axis(mask, idx, True, axis=1)
+    return mask
+
+
+def radius_mask(dist, epsilon: float) -> np.ndarray:
+    """dist <= epsilon (csrc/ops/neighbors.cpp:56-57)."""
+    return np.asarray(dist) <= epsilon

@@ -13,7 +13,11 @@ this build's oracle:
 * directed Hausdorff:           scipy.spatial.distance.directed_hausdorff (value, float64) on
   random clouds, plus hand-built clouds whose maxima / minima tie, with the expected
   indices derived by hand from the reference's rules (last m reaching the max, first n
-  reaching that m's min; csrc/ops/cpu/hausdorff_kernel.cpp:25-51).
+  reaching that m's min; csrc/ops/cpu/hausdorff_kernel.cpp:25-51);
+* neighbour masks:              sklearn.neighbors.NearestNeighbors(algorithm="brute")
+  kneighbors_graph / radius_neighbors_graph (connectivity, float64) on tie-free random
+  points, plus hand-built distance rows with ties, NaN, +-0 and inf whose masks are
+  written out by hand (ascending, NaN last, -0 == +0, ties to the lower column).
 
 Run from the repository root: python tests/golden/make_golden.py
 """
@@ -92,8 +96,42 @@ def hausdorff():
            for f, v in zip(("x1", "x2", "value", "idx1", "idx2"), t)})
 
 
+def neighbors():
+    from sklearn.neighbors import NearestNeighbors
+
+    rng = np.random.default_rng(20260104)
+    x1 = rng.standard_normal((12, 6))
+    x2 = rng.standard_normal((15, 6))
+    out = dict(x1=x1, x2=x2)
+    nn = NearestNeighbors(algorithm="brute").fit(x2)
+    for k in (0, 1, 4):
+        out[f"knn_k{k}"] = nn.kneighbors_graph(x1, n_neighbors=k + 1).toarray().astype(bool)
+    out["radius_eps"] = np.float64(3.0)
+    out["radius"] = nn.radius_neighbors_graph(x1, radius=3.0).toarray().astype(bool)
+    # hand-built rows: (distances, count, expected mask)
+    nan, inf = np.nan, np.inf
+    T, F = True, False
+    cases = [
+        ([3, 1, 1, 0, nan], 3, [F, T, T, T, F]),
+        ([3, 1, 1, 0, nan], 2, [F, T, F, T, F]),            # tie 1/1 -> lower column
+        ([-0.0, 0.0, -1, inf, nan, 2], 2, [T, F, T, F, F, F]),  # -0 == +0 -> lower column
+        ([-0.0, 0.0, -1, inf, nan, 2], 3, [T, T, T, F, F, F]),
+        ([-0.0, 0.0, -1, inf, nan, 2], 5, [T, T, T, T, F, T]),  # inf before NaN
+        ([5, 5, 5, 5], 2, [T, T, F, F]),
+        ([nan, nan, 1], 2, [T, F, T]),                      # NaN ties -> lower column
+        ([2, 7, 1, 8, 2, 8], 4, [T, T, T, F, T, F]),        # 1, 2, 2, 7
+    ]
+    for i, (row, count, want) in enumerate(cases):
+        out[f"row{i}_dist"] = np.array([row], np.float32)
+        out[f"row{i}_count"] = np.int64(count)
+        out[f"row{i}_mask"] = np.array([want], bool)
+    out["n_rows"] = np.int64(len(cases))
+    np.savez_compressed(OUT / "neighbors.npz", **out)
+
+
 if __name__ == "__main__":
     boolean()
     minkowski()
     hausdorff()
+    neighbors()
     print("wrote", sorted(p.name for p in OUT.glob("*.npz")))

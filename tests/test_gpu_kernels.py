@@ -4,6 +4,8 @@ Bars: bit-exact for the boolean metrics and for the Hausdorff value, indices and
 gradients; floating-point values and gradients within the tolerance stated per test
 (fp32: rtol 1e-5 plus an absolute floor scaled to the data; bf16: rtol 1e-2 normwise).
 """
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -300,3 +302,55 @@ def test_boolean_gpu_equals_reference_kernels(tmp_path):
     assert_equal(got, torch.from_numpy(ref["out"]), "hamming vs reference")
     ref = ref_runner.run("jaccard", {"x1": x1.numpy(), "x2": x2.numpy()}, tmp_path)
     assert_equal(capi.jaccard_bool(x1.to(DEV), x2.to(DEV)), torch.from_numpy(ref["out"]), "jaccard vs reference")
+
+
+# --------------------------------------------------------------------------------------
+# k-smallest (neighbour) mask: bit-exact selection
+# --------------------------------------------------------------------------------------
+MASK_SHAPES = [(1, 1), (3, 7), (37, 300), (64, 4096), (5, 16384), (4, 16385), (3, 40000)]
+
+
+@pytest.mark.parametrize("rows,cols", MASK_SHAPES)
+@pytest.mark.parametrize("count", [1, 2, 3, 5, 9, 16, 17, 40, 300])
+def test_row_smallest_mask_random(rows, cols, count):
+    print(f"row_smallest_mask {rows}x{cols} count={count}", flush=True)
+    d = rand(rows, cols, seed=11)
+    got = capi.row_smallest_mask(d.to(DEV), count)
+    assert_equal(got, torch.from_numpy(P.k_smallest_mask(d.numpy(), count)), f"{rows}x{cols} c={count}")
+
+
+@pytest.mark.parametrize("rows,cols", [(16, 1000), (6, 20000)])
+@pytest.mark.parametrize("count", [1, 4, 16, 17, 100, 999])
+def test_row_smallest_mask_ties_nan_signed_zero(rows, cols, count):
+    print(f"row_smallest_mask ties {rows}x{cols} count={count}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    d = torch.randint(0, 7, (rows, cols), generator=g).float() - 3.0  # heavy ties, negatives
+    d[0, ::3] = float("nan")
+    d[1, ::2] = -0.0
+    d[1, 1::4] = 0.0
+    d[2, :] = 5.0  # one value everywhere
+    d[3, ::7] = float("inf")
+    d[3, 1::7] = -float("inf")
+    got = capi.row_smallest_mask(d.to(DEV), count)
+    assert_equal(got, torch.from_numpy(P.k_smallest_mask(d.numpy(), count)), f"ties c={count}")
+
+
+def test_row_smallest_mask_golden_rows_and_edges():
+    g = dict(np.load(Path(__file__).resolve().parent / "golden" / "neighbors.npz"))
+    for i in range(int(g["n_rows"])):
+        got = capi.row_smallest_mask(torch.from_numpy(g[f"row{i}_dist"]).to(DEV), int(g[f"row{i}_count"]))
+        assert np.array_equal(got.cpu().numpy(), g[f"row{i}_mask"]), i
+    d = rand(9, 50, seed=13)
+    for count, want in ((0, False), (50, True), (51, True)):
+        got = capi.row_smallest_mask(d.to(DEV), count)
+        assert bool((got == want).all()), count
+    assert capi.row_smallest_mask(torch.empty(0, 5, device=DEV), 2).shape == (0, 5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("count", [2, 33])
+def test_row_smallest_mask_half_types(dtype, count):
+    d = rand(20, 3000, seed=14).to(dtype)  # rounding to 16 bits creates ties
+    got = capi.row_smallest_mask(d.to(DEV), count)
+    want = P.k_smallest_mask(d.float().numpy(), count)  # exact widening keeps the order
+    assert_equal(got, torch.from_numpy(want), f"{dtype} c={count}")

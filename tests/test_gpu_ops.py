@@ -204,3 +204,57 @@ def test_empty_inputs():
     assert tp.euclidean_distances(e, x).shape == (0, 5)
     assert tp.manhattan_distances(x, e).shape == (5, 0)
     assert tp.hamming_distances(e > 0, x > 0).shape == (0, 5)
+
+
+# --------------------------------------------------------------------------------------
+# cdist(metric=...) and the neighbour masks
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("metric,fn", [("euclidean", "euclidean_distances"), ("cosine", "cosine_distances"),
+                                       ("cityblock", "manhattan_distances"), ("linf", "chebyshev_distances"),
+                                       ("hamming", "hamming_distances")])
+def test_cdist_dispatch_gpu(metric, fn):
+    a, b = randn(70, 24, seed=0).to(DEV), randn(50, 24, seed=1).to(DEV)
+    if metric == "hamming":
+        a, b = a > 0, b > 0
+    assert_equal(tp.cdist(a, b, metric), getattr(tp, fn)(a, b), metric)
+
+
+@pytest.mark.parametrize("metric", ["euclidean", "manhattan", "cosine", "minkowski"])
+@pytest.mark.parametrize("k", [0, 1, 5, 20])
+def test_k_neighbors_mask_gpu(metric, k):
+    print(f"k_neighbors_mask {metric} k={k}", flush=True)
+    x1, x2 = randn(300, 32, seed=0), randn(500, 32, seed=1)
+    kw = {"p": 3.0} if metric == "minkowski" else {}
+    got = tp.k_neighbors_mask(x1.to(DEV), x2.to(DEV), k, metric, **kw)
+    assert got.dtype == torch.bool and got.shape == (300, 500)
+    # selection: bit-exact against the oracle on the same (GPU-computed) distances
+    dist = tp.cdist(x1.to(DEV), x2.to(DEV), metric, **kw).cpu()
+    assert_equal(got, torch.from_numpy(P.k_smallest_mask(dist.numpy(), k + 1)), "vs oracle")
+    # and the reference's own CPU route, except where the boundary is a near-tie that
+    # float rounding of the distances may flip
+    ref = tp.k_neighbors_mask(x1, x2, k, metric, **kw)
+    diff = (got.cpu() != ref).any(1)
+    srt = dist.double().sort(1).values
+    gap = (srt[:, k + 1] - srt[:, k]) / srt[:, k + 1].abs().clamp_min(1e-30)
+    assert bool((gap[diff] < 1e-5).all()), f"{int(diff.sum())} rows differ beyond near-ties"
+
+
+def test_k_neighbors_mask_gpu_ties_and_self():
+    x = torch.randint(0, 3, (400, 8), generator=torch.Generator().manual_seed(3)).float()
+    got = tp.k_neighbors_mask(x.to(DEV), None, 2, "manhattan")  # integer distances: many ties
+    dist = tp.manhattan_distances(x.to(DEV)).cpu()
+    assert_equal(got, torch.from_numpy(P.k_smallest_mask(dist.numpy(), 3)), "ties")
+    xb = x > 0
+    got = tp.k_neighbors_mask(xb.to(DEV), None, 4, "hamming")
+    assert_equal(got, torch.from_numpy(P.k_smallest_mask(tp.hamming_distances(xb).numpy(), 5)), "hamming")
+    a = randn(64, 16, seed=4).to(DEV)
+    assert torch.equal(tp.k_neighbors_mask(a, None, 0).cpu(), torch.eye(64, dtype=torch.bool))
+    with pytest.raises(IndexError):  # k + 1 > M raises, as the reference's index_put_ does
+        tp.k_neighbors_mask(a, a[:3], 3)
+
+
+def test_radius_neighbors_mask_gpu():
+    x1, x2 = randn(200, 16, seed=0), randn(300, 16, seed=1)
+    got = tp.radius_neighbors_mask(x1.to(DEV), x2.to(DEV), 5.0)
+    dist = tp.euclidean_distances(x1.to(DEV), x2.to(DEV)).cpu()
+    assert_equal(got, torch.from_numpy(P.radius_mask(dist.numpy(), 5.0)), "radius")

@@ -1,6 +1,7 @@
 """The drop-in op layer without a GPU: schemas, CPU paths (the reference's routes), errors,
 TorchScript, autograd on CPU."""
 import warnings
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -11,6 +12,8 @@ import torchpairwise_amd as tp
 from oracle import cref
 from oracle import pairwise as P
 from tests._util import assert_close, assert_equal, rand, randn
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
 
 PUBLIC = [
     "euclidean_distances", "haversine_distances", "manhattan_distances", "cosine_distances",
@@ -133,3 +136,97 @@ def test_torchscript_binds_schemas():
     f = torch.jit.script(_scripted)
     a, b = randn(10, 4, seed=0), randn(8, 4, seed=1)
     assert_close(f(a, b), _scripted(a, b), rtol=0, atol=0, what="scripted")
+
+
+# ---------------------------------------------------------------------- cdist / neighbours
+CDIST_METRICS = {
+    "euclidean": lambda a, b: tp.euclidean_distances(a, b),
+    "manhattan": lambda a, b: tp.manhattan_distances(a, b),
+    "cityblock": lambda a, b: tp.manhattan_distances(a, b),
+    "l1": lambda a, b: tp.l1_distances(a, b),
+    "l2": lambda a, b: tp.l2_distances(a, b),
+    "linf": lambda a, b: tp.chebyshev_distances(a, b),
+    "chebyshev": lambda a, b: tp.chebyshev_distances(a, b),
+    "cosine": lambda a, b: tp.cosine_distances(a, b),
+    "sqeuclidean": lambda a, b: tp.sqeuclidean_distances(a, b),
+    "correlation": lambda a, b: tp.correlation_distances(a, b),
+    "minkowski": lambda a, b: tp.minkowski_distances(a, b, 2.0),
+    "lp": lambda a, b: tp.lp_distances(a, b, 2.0),
+}
+
+
+@pytest.mark.parametrize("metric", sorted(CDIST_METRICS))
+def test_cdist_dispatches_to_the_metric(metric):
+    a, b = randn(9, 6, seed=0), randn(11, 6, seed=1)
+    assert_equal(tp.cdist(a, b, metric), CDIST_METRICS[metric](a, b), metric)
+
+
+def test_cdist_extra_arguments():
+    a, b = randn(9, 6, seed=0), randn(11, 6, seed=1)
+    assert_equal(tp.cdist(a, b), tp.minkowski_distances(a, b))  # default metric, p=2
+    assert_equal(tp.cdist(a, b, "minkowski", p=3.0), tp.minkowski_distances(a, b, 3.0))
+    assert_equal(tp.cdist(a, b, "lp", p=1.0), tp.manhattan_distances(a, b))
+    bb, cc = a > 0, b > 0
+    assert_equal(tp.cdist(bb, cc, "hamming"), tp.hamming_distances(bb, cc))
+    assert_equal(tp.cdist(bb, cc, "jaccard"), tp.jaccard_distances(bb, cc))
+    c1, c2 = rand(2, 20, 3, seed=2), rand(3, 25, 3, seed=3)
+    g1, g2 = torch.Generator().manual_seed(5), torch.Generator().manual_seed(5)
+    assert_equal(tp.cdist(c1, c2, "directed_hausdorff", shuffle=True, generator=g1),
+                 tp.directed_hausdorff_distances(c1, c2, shuffle=True, generator=g2)[0])
+
+
+def test_cdist_errors_match_the_reference():
+    a, b = randn(4, 3, seed=0), randn(5, 3, seed=1)
+    with pytest.raises(TypeError) as e:
+        tp.cdist(a, b, "euclidean", p=3.0, w=a)
+    assert str(e.value).startswith(
+        "torchpairwise::euclidean_distances was called with incompatible arguments w, p.\n"
+        "The following signature is supported:\n"
+        "    euclidean_distances(Tensor x1, Tensor? x2=None) -> Tensor\n")
+    with pytest.raises(TypeError, match="incompatible arguments generator"):
+        tp.cdist(a, b, "minkowski", generator=torch.Generator())
+    with pytest.raises(RuntimeError, match=r"Got unkown distance metric: foo\. Supported metrics "
+                                           r"are \[braycurtis, canberra, .*, wminkowski, yule\]"):
+        tp.cdist(a, b, "foo")
+    with pytest.raises(NotImplementedError, match="pdist is yet to be implemented"):
+        tp.pdist(a)
+    with pytest.raises(NotImplementedError):
+        tp.cdist(a, b, "haversine")  # outside this build's path
+    sch = str(torch.ops.torchpairwise.k_neighbors_mask.default._schema)
+    assert sch == ("torchpairwise::k_neighbors_mask(Tensor x1, Tensor? x2=None, int k=1, "
+                   "str metric=\"euclidean\", *, Tensor? w=None, Tensor? V=None, Tensor? VI=None, "
+                   "float? p=None, float? base=None, bool? shuffle=None, Generator? generator=None) "
+                   "-> Tensor")
+
+
+def test_neighbors_cpu_match_sklearn_golden():
+    g = dict(np.load(GOLDEN / "neighbors.npz"))
+    x1, x2 = torch.from_numpy(g["x1"]), torch.from_numpy(g["x2"])
+    for k in (0, 1, 4):
+        assert np.array_equal(tp.k_neighbors_mask(x1, x2, k).numpy(), g[f"knn_k{k}"]), k
+    assert np.array_equal(tp.radius_neighbors_mask(x1, x2, float(g["radius_eps"])).numpy(),
+                          g["radius"])
+    # x2 = None: every point is its own nearest neighbour
+    m = tp.k_neighbors_mask(x1, None, 0)
+    assert torch.equal(m, torch.eye(12, dtype=torch.bool))
+
+
+def test_neighbors_cpu_edge_cases():
+    a, b = randn(6, 3, seed=0), randn(4, 3, seed=1)
+    with pytest.raises(RuntimeError, match="k must be non-negative"):
+        tp.k_neighbors_mask(a, b, -1)
+    with pytest.raises(RuntimeError, match="epsilon must be non-negative"):
+        tp.radius_neighbors_mask(a, b, -0.5)
+    # k + 1 > M: the reference's index_put_ indices do not broadcast, and it raises
+    with pytest.raises(IndexError, match="shape mismatch"):
+        tp.k_neighbors_mask(a, b, 4)
+    m = tp.k_neighbors_mask(a, b, 3, "manhattan")
+    assert torch.equal(m, torch.ones(6, 4, dtype=torch.bool))
+
+
+def test_row_smallest_mask_cpu_hand_built_rows():
+    g = dict(np.load(GOLDEN / "neighbors.npz"))
+    for i in range(int(g["n_rows"])):
+        got = torch.ops.torchpairwise._row_smallest_mask(torch.from_numpy(g[f"row{i}_dist"]),
+                                                         int(g[f"row{i}_count"]))
+        assert np.array_equal(got.numpy(), g[f"row{i}_mask"]), i

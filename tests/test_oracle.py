@@ -225,3 +225,53 @@ def test_pins_catch_xor_for_or(monkeypatch):
     g = npz("boolean.npz")
     wrong = P.bool_counts(g["x1"], g["x2"], "xor")
     assert not np.array_equal(wrong, g["count_or"])
+
+
+# ---------------------------------------------------------------------- neighbour masks
+def test_k_smallest_mask_matches_sklearn_golden():
+    g = npz("neighbors.npz")
+    dist = cdist(g["x1"], g["x2"])  # float64, tie-free random points
+    for k in (0, 1, 4):
+        assert np.array_equal(P.k_smallest_mask(dist, k + 1), g[f"knn_k{k}"]), k
+    assert np.array_equal(P.radius_mask(dist, g["radius_eps"]), g["radius"])
+
+
+def test_k_smallest_mask_hand_built_rows():
+    g = npz("neighbors.npz")
+    for i in range(int(g["n_rows"])):
+        got = P.k_smallest_mask(g[f"row{i}_dist"], int(g[f"row{i}_count"]))
+        assert np.array_equal(got, g[f"row{i}_mask"]), i
+
+
+def test_k_smallest_mask_properties_with_ties():
+    rng = np.random.default_rng(9)
+    d = rng.integers(0, 6, (40, 57)).astype(np.float32)  # heavy ties
+    d[3, ::5] = np.nan
+    for count in (0, 1, 2, 7, 30, 57, 80):
+        m = P.k_smallest_mask(d, count)
+        assert (m.sum(1) == min(count, 57)).all()
+        for r in range(40):
+            sel, rest = d[r][m[r]], d[r][~m[r]]
+            key = np.where(np.isnan(d[r]), np.inf, d[r])
+            if sel.size and rest.size:
+                # every selected entry precedes every unselected one (NaN last) ...
+                ks, kr = key[m[r]], key[~m[r]]
+                assert ks.max() <= kr.min()
+                assert not (np.isnan(sel).any() and not np.isnan(rest).all())
+                # ... and on the tied boundary value the lower columns are taken
+                b = ks.max()
+                tied = np.nonzero(key == b)[0]
+                taken = tied[m[r][tied]]
+                assert np.array_equal(taken, tied[: taken.size])
+
+
+def test_pins_catch_highest_column_on_ties():
+    g = npz("neighbors.npz")
+
+    def wrong(dist, count):  # stable sort of the reversed row: ties go to the higher column
+        d = np.asarray(dist)[:, ::-1]
+        return P.k_smallest_mask(d, count)[:, ::-1]
+
+    bad = sum(not np.array_equal(wrong(g[f"row{i}_dist"], int(g[f"row{i}_count"])), g[f"row{i}_mask"])
+              for i in range(int(g["n_rows"])))
+    assert bad >= 3

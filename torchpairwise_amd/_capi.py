@@ -44,6 +44,7 @@ _SIGNATURES = {
     "tpw_hausdorff_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "tpw_directed_hausdorff": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "tpw_directed_hausdorff_backward": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),
+    "tpw_row_smallest_mask": (_i, [_p, _i, _i64, _i64, _i64, _p, _p]),
 }
 
 _lib = None
@@ -101,6 +102,8 @@ def _dtype_code(t):
         return TPW_F32
     if t.dtype == torch.bfloat16:
         return TPW_BF16
+    if t.dtype == torch.float16:
+        return TPW_F16
     raise TypeError(f"unsupported dtype {t.dtype}")
 
 
@@ -328,3 +331,14 @@ def directed_hausdorff_backward(grad, x1, x2, out, idx1, idx2):
     if x1.dim() == 3:
         return gx1[0], gx2[0]
     return gx1, gx2
+
+
+def row_smallest_mask(dist, count):
+    """dist [rows, cols] (fp32 / bf16 / fp16) -> bool mask of each row's `count` smallest."""
+    import torch
+
+    d = dist.contiguous()
+    mask = torch.empty(d.shape, dtype=torch.bool, device=d.device)
+    call("tpw_row_smallest_mask", _ptr(d), _dtype_code(d), d.shape[0], d.shape[1], int(count),
+         _ptr(mask), _stream())
+    return mask

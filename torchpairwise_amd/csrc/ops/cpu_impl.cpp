@@ -229,6 +229,19 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_cpu(
 
 }  // namespace
 
+// Bool mask of each row's `count` smallest entries: the first `count` positions of a stable
+// ascending argsort (NaN last), the order the HIP kernel implements.
+at::Tensor row_smallest_mask_cpu(const at::Tensor &dist, int64_t count) {
+    TORCH_CHECK(dist.dim() == 2, "_row_smallest_mask: expected a 2-D tensor");
+    TORCH_CHECK(count >= 0, "_row_smallest_mask: count must be non-negative, got ", count);
+    auto mask = at::zeros(dist.sizes(), dist.options().dtype(at::kBool));
+    const int64_t c = std::min(count, dist.size(1));
+    if (dist.numel() == 0 || c == 0) return mask;
+    auto inds = at::argsort(dist, /*stable=*/true, /*dim=*/1, /*descending=*/false).slice(1, 0, c);
+    mask.scatter_(1, inds, true);
+    return mask;
+}
+
 TORCH_LIBRARY_IMPL(torchpairwise, CPU, m) {
     m.impl("pwand_sum", TORCH_FN((pw_reduce_cpu<TPW_BIT_AND, false>)));
     m.impl("pwor_sum", TORCH_FN((pw_reduce_cpu<TPW_BIT_OR, false>)));
@@ -238,6 +251,7 @@ TORCH_LIBRARY_IMPL(torchpairwise, CPU, m) {
     m.impl("pweq_mean", TORCH_FN((pw_reduce_cpu<TPW_BIT_EQ, true>)));
     m.impl("pwne_mean", TORCH_FN((pw_reduce_cpu<TPW_BIT_NE, true>)));
     m.impl("_jaccard", TORCH_FN(jaccard_cpu));
+    m.impl("_row_smallest_mask", TORCH_FN(row_smallest_mask_cpu));
     m.impl("prf_div", TORCH_FN(prf_div_cpu));
     m.impl("_prf_div_backward", TORCH_FN(prf_div_backward_cpu));
     m.impl("_directed_hausdorff", TORCH_FN(directed_hausdorff_cpu));

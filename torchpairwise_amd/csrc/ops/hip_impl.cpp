@@ -210,6 +210,24 @@ at::Tensor jaccard_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     return out_shape(out, x1);
 }
 
+// ---------------------------------------------------------------- neighbour mask
+// Bool mask of each row's `count` smallest entries (stable order: ties to the lower column).
+at::Tensor row_smallest_mask_cuda(const at::Tensor &dist, int64_t count) {
+    TORCH_CHECK(dist.is_cuda() && dist.dim() == 2, "_row_smallest_mask: expected a 2-D GPU tensor");
+    TORCH_CHECK(count >= 0, "_row_smallest_mask: count must be non-negative, got ", count);
+    const int code = float_code(dist.scalar_type());
+    TORCH_CHECK(code == TPW_F32 || code == TPW_BF16 || code == TPW_F16,
+                "_row_smallest_mask: expected float32, bfloat16 or float16 distances, got ",
+                dist.scalar_type());
+    DeviceGuard guard(dist.device());
+    auto d = dist.contiguous();
+    auto mask = at::empty(d.sizes(), d.options().dtype(at::kBool));
+    check_rc(tpw_row_smallest_mask(d.data_ptr(), code, d.size(0), d.size(1), count, mask.data_ptr(),
+                                   current_stream()),
+             "row_smallest_mask");
+    return mask;
+}
+
 // ---------------------------------------------------------------- prf_div
 at::Tensor prf_div_cuda(const at::Tensor &x, const at::Tensor &y, c10::string_view mode) {
     const bool identity = prf_identity(mode);
@@ -317,6 +335,7 @@ TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
     m.impl("_pw_lp", TORCH_FN(pw_lp_cuda));
     m.impl("_pw_lp_backward", TORCH_FN(pw_lp_backward_cuda));
     m.impl("_jaccard", TORCH_FN(jaccard_cuda));
+    m.impl("_row_smallest_mask", TORCH_FN(row_smallest_mask_cuda));
     m.impl("pwand_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_AND, TPW_RED_SUM>)));
     m.impl("pwor_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_OR, TPW_RED_SUM>)));
     m.impl("pwxor_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_XOR, TPW_RED_SUM>)));

@@ -95,6 +95,60 @@ at::Tensor route_cdist(const at::Tensor &x1, const at::Tensor &x2, double p) {
                                 "the inner-product, Minkowski, boolean and Hausdorff families)");
 }
 
+// Public metric schemas, byte-for-byte those of csrc/ops/pairwise_metrics.h:76-424 (also quoted
+// by cdist's incompatible-argument error, as the reference quotes its functors' schema_str).
+struct PublicSchema {
+    const char *name;
+    const char *schema;
+};
+constexpr PublicSchema kPublicSchemas[] = {
+    {"euclidean_distances", "euclidean_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"haversine_distances", "haversine_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"manhattan_distances", "manhattan_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"cosine_distances", "cosine_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"linear_kernel", "linear_kernel(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"polynomial_kernel", "polynomial_kernel(Tensor x1, Tensor? x2=None, int degree=3, float? gamma=None, float coef0=1) -> Tensor"},
+    {"sigmoid_kernel", "sigmoid_kernel(Tensor x1, Tensor? x2=None, float? gamma=None, float coef0=1) -> Tensor"},
+    {"rbf_kernel", "rbf_kernel(Tensor x1, Tensor? x2=None, float? gamma=None) -> Tensor"},
+    {"laplacian_kernel", "laplacian_kernel(Tensor x1, Tensor? x2=None, float? gamma=None) -> Tensor"},
+    {"cosine_similarity", "cosine_similarity(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"additive_chi2_kernel", "additive_chi2_kernel(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"chi2_kernel", "chi2_kernel(Tensor x1, Tensor? x2=None, float gamma=1.0) -> Tensor"},
+    {"directed_hausdorff_distances", "directed_hausdorff_distances(Tensor x1, Tensor? x2=None, *, bool shuffle=False, Generator? generator=None) -> (Tensor output, Tensor x1_indices, Tensor x2_indices)"},
+    {"minkowski_distances", "minkowski_distances(Tensor x1, Tensor? x2=None, float p=2) -> Tensor"},
+    {"wminkowski_distances", "wminkowski_distances(Tensor x1, Tensor? x2=None, float p=2, Tensor? w=None) -> Tensor"},
+    {"sqeuclidean_distances", "sqeuclidean_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"correlation_distances", "correlation_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"hamming_distances", "hamming_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"jaccard_distances", "jaccard_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"kulsinski_distances", "kulsinski_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"kulczynski1_distances", "kulczynski1_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"seuclidean_distances", "seuclidean_distances(Tensor x1, Tensor? x2=None, Tensor? V=None) -> Tensor"},
+    {"cityblock_distances", "cityblock_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"mahalanobis_distances", "mahalanobis_distances(Tensor x1, Tensor? x2=None, Tensor? VI=None) -> Tensor"},
+    {"chebyshev_distances", "chebyshev_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"braycurtis_distances", "braycurtis_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"canberra_distances", "canberra_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"jensenshannon_distances", "jensenshannon_distances(Tensor x1, Tensor? x2=None, float? base=None) -> Tensor"},
+    {"yule_distances", "yule_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"dice_distances", "dice_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"rogerstanimoto_distances", "rogerstanimoto_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"russellrao_distances", "russellrao_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"sokalmichener_distances", "sokalmichener_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"sokalsneath_distances", "sokalsneath_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"snr_distances", "snr_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"l1_distances", "l1_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"l2_distances", "l2_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+    {"lp_distances", "lp_distances(Tensor x1, Tensor? x2=None, float p=2) -> Tensor"},
+    {"linf_distances", "linf_distances(Tensor x1, Tensor? x2=None) -> Tensor"},
+};
+
+const char *schema_of(c10::string_view name) {
+    for (const auto &e : kPublicSchemas)
+        if (name == e.name) return e.schema;
+    TORCH_INTERNAL_ASSERT(false, "no public schema ", std::string(name));
+}
+
 // ------------------------------------------------------------------------------------
 // public functions (csrc/ops/pairwise_metrics.cpp)
 // ------------------------------------------------------------------------------------
@@ -309,6 +363,165 @@ at::Tensor canberra_distances(const at::Tensor &, const c10::optional<at::Tensor
 at::Tensor jensenshannon_distances(const at::Tensor &, const c10::optional<at::Tensor> &, c10::optional<double>) { not_in_build("jensenshannon_distances"); }
 at::Tensor snr_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("snr_distances"); }
 
+// ------------------------------------------------------------------------------------
+// cdist(metric=...) and pdist (csrc/ops/cpdist.cpp)
+// ------------------------------------------------------------------------------------
+struct CdistArgs {
+    const c10::optional<at::Tensor> &w, &V, &VI;
+    c10::optional<double> p, base;
+    c10::optional<bool> shuffle;
+    c10::optional<at::Generator> generator;
+};
+
+// Which optional arguments a metric accepts, in the order the error message lists them
+// (the has_arg table of cpdist.cpp:85-146).
+enum ExtraArg : unsigned { kW = 1, kV = 2, kVI = 4, kP = 8, kBase = 16, kShuffle = 32, kGenerator = 64 };
+
+struct CdistMetric {
+    const char *metric;
+    unsigned accepts;
+    at::Tensor (*call)(const at::Tensor &, const at::Tensor &, const CdistArgs &);
+};
+
+// cpdist.cpp:35-79: arguments given but not accepted raise TypeError quoting the schema.
+void check_extra_args(const CdistMetric &m, const CdistArgs &a) {
+    const std::pair<bool, const char *> given[] = {
+        {a.w.has_value(), "w"},         {a.V.has_value(), "V"},       {a.VI.has_value(), "VI"},
+        {a.p.has_value(), "p"},         {a.base.has_value(), "base"}, {a.shuffle.has_value(), "shuffle"},
+        {a.generator.has_value(), "generator"}};
+    std::string bad;
+    for (int i = 0; i < 7; ++i)
+        if (given[i].first && !(m.accepts & (1u << i))) bad += (bad.empty() ? "" : ", ") + std::string(given[i].second);
+    const std::string fn = std::string(m.metric) + "_distances";
+    TORCH_CHECK_TYPE(bad.empty(), "torchpairwise::", fn, " was called with incompatible arguments ", bad,
+                     ".\nThe following signature is supported:\n", "    ", schema_of(fn), "\n")
+}
+
+#define TPW_METRIC(NAME, ACCEPTS, EXPR) \
+    {#NAME, ACCEPTS, [](const at::Tensor &x1, const at::Tensor &x2, const CdistArgs &a) -> at::Tensor { \
+         (void)a;                                                                                        \
+         return EXPR;                                                                                    \
+     }}
+// dispatch order of cpdist.cpp:184-219
+const CdistMetric kCdistMetrics[] = {
+    TPW_METRIC(euclidean, 0, euclidean_distances(x1, x2)),
+    TPW_METRIC(haversine, 0, haversine_distances(x1, x2)),
+    TPW_METRIC(manhattan, 0, manhattan_distances(x1, x2)),
+    TPW_METRIC(cosine, 0, cosine_distances(x1, x2)),
+    TPW_METRIC(directed_hausdorff, kShuffle | kGenerator,
+               std::get<0>(directed_hausdorff_distances(x1, x2, a.shuffle.value_or(false), a.generator))),
+    TPW_METRIC(minkowski, kP, minkowski_distances(x1, x2, a.p.value_or(2))),
+    TPW_METRIC(wminkowski, kW | kP, wminkowski_distances(x1, x2, a.p.value_or(2), a.w)),
+    TPW_METRIC(sqeuclidean, 0, sqeuclidean_distances(x1, x2)),
+    TPW_METRIC(correlation, 0, correlation_distances(x1, x2)),
+    TPW_METRIC(hamming, 0, hamming_distances(x1, x2)),
+    TPW_METRIC(jaccard, 0, jaccard_distances(x1, x2)),
+    TPW_METRIC(kulsinski, 0, kulsinski_distances(x1, x2)),
+    TPW_METRIC(kulczynski1, 0, kulczynski1_distances(x1, x2)),
+    TPW_METRIC(seuclidean, kV, seuclidean_distances(x1, x2, a.V)),
+    TPW_METRIC(cityblock, 0, cityblock_distances(x1, x2)),
+    TPW_METRIC(mahalanobis, kVI, mahalanobis_distances(x1, x2, a.VI)),
+    TPW_METRIC(chebyshev, 0, chebyshev_distances(x1, x2)),
+    TPW_METRIC(braycurtis, 0, braycurtis_distances(x1, x2)),
+    TPW_METRIC(canberra, 0, canberra_distances(x1, x2)),
+    TPW_METRIC(jensenshannon, kBase, jensenshannon_distances(x1, x2, a.base)),
+    TPW_METRIC(yule, 0, yule_distances(x1, x2)),
+    TPW_METRIC(dice, 0, dice_distances(x1, x2)),
+    TPW_METRIC(rogerstanimoto, 0, rogerstanimoto_distances(x1, x2)),
+    TPW_METRIC(russellrao, 0, russellrao_distances(x1, x2)),
+    TPW_METRIC(sokalmichener, 0, sokalmichener_distances(x1, x2)),
+    TPW_METRIC(sokalsneath, 0, sokalsneath_distances(x1, x2)),
+    TPW_METRIC(snr, 0, snr_distances(x1, x2)),
+    TPW_METRIC(l1, 0, l1_distances(x1, x2)),
+    TPW_METRIC(l2, 0, l2_distances(x1, x2)),
+    TPW_METRIC(lp, kP, lp_distances(x1, x2, a.p.value_or(2))),
+    TPW_METRIC(linf, 0, linf_distances(x1, x2)),
+};
+#undef TPW_METRIC
+
+at::Tensor cdist(const at::Tensor &x1, const at::Tensor &x2, c10::string_view metric,
+                 const c10::optional<at::Tensor> &w, const c10::optional<at::Tensor> &V,
+                 const c10::optional<at::Tensor> &VI, c10::optional<double> p,
+                 c10::optional<double> base, c10::optional<bool> shuffle,
+                 c10::optional<at::Generator> generator) {
+    C10_LOG_API_USAGE_ONCE("torchpairwise.csrc.ops.cpdist.cdist");
+    const CdistArgs args{w, V, VI, p, base, shuffle, std::move(generator)};
+    for (const auto &m : kCdistMetrics) {
+        if (metric == m.metric) {
+            check_extra_args(m, args);
+            return m.call(x1, x2, args);
+        }
+    }
+    // the reference's message, spelling included (cpdist.cpp:180-231)
+    static const char *const supported[] = {
+        "braycurtis", "canberra", "chebyshev", "cityblock", "correlation", "cosine",
+        "dice", "directed_hausdorff", "euclidean", "hamming", "haversine", "jaccard",
+        "jensenshannon", "kulczynski1", "kulsinski", "l1", "l2", "lp", "linf", "mahalanobis",
+        "manhattan", "minkowski", "rogerstanimoto", "russellrao", "seuclidean", "snr",
+        "sokalmichener", "sokalsneath", "sqeuclidean", "wminkowski", "yule"};
+    std::string list;
+    for (const char *s : supported) list += (list.empty() ? "" : ", ") + std::string(s);
+    TORCH_CHECK(false, "Got unkown distance metric: ", std::string(metric), ". Supported metrics are [",
+                list, "]")
+}
+
+at::Tensor pdist(const at::Tensor &, c10::string_view, const c10::optional<at::Tensor> &,
+                 const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &,
+                 c10::optional<double>, c10::optional<double>, c10::optional<bool>,
+                 c10::optional<at::Generator>) {
+    C10_LOG_API_USAGE_ONCE("torchpairwise.csrc.ops.cpdist.pdist");
+    TORCH_CHECK_NOT_IMPLEMENTED(false, "pdist is yet to be implemented.")  // cpdist.cpp:244-245
+}
+
+// ------------------------------------------------------------------------------------
+// neighbour masks (csrc/ops/neighbors.cpp)
+// ------------------------------------------------------------------------------------
+// neighbors.cpp:29-34 literally: argsort every row, keep the first k + 1 columns, scatter
+// true.  (When k + 1 exceeds the number of columns the two index tensors of index_put_ do
+// not broadcast and ATen raises; that behaviour is kept by running this same code.)
+at::Tensor k_neighbors_from_argsort(const at::Tensor &dists, int64_t k, int64_t n1, int64_t n2) {
+    auto neighbors_inds = dists.argsort(1, false).slice(1, 0, k + 1);
+    auto first_dim = at::arange(0, n1, neighbors_inds.options()).view({-1, 1}).repeat({1, k + 1});
+    auto output = at::zeros({n1, n2}, dists.options().dtype(at::kBool));
+    output.index_put_({first_dim.flatten(), neighbors_inds.flatten()}, true);
+    return output;
+}
+
+at::Tensor k_neighbors_mask(const at::Tensor &x1, const c10::optional<at::Tensor> &x2, int64_t k,
+                            c10::string_view metric, const c10::optional<at::Tensor> &w,
+                            const c10::optional<at::Tensor> &V, const c10::optional<at::Tensor> &VI,
+                            c10::optional<double> p, c10::optional<double> base,
+                            c10::optional<bool> shuffle, c10::optional<at::Generator> generator) {
+    C10_LOG_API_USAGE_ONCE("torchpairwise.csrc.ops.neighbors.k_neighbors_mask");
+    auto xs = check_pairwise_inputs("k_neighbors_mask", x1, x2);
+    TORCH_CHECK(k >= 0, "k must be non-negative. Got k=", k)
+    at::NoGradGuard no_grad_guard;
+    auto dists = cdist(xs.first, xs.second, metric, w, V, VI, p, base, shuffle, std::move(generator));
+    const int64_t n1 = x1.size(0), n2 = xs.second.size(0);
+    // GPU: one pass over the distances selecting each row's k + 1 smallest (HIP kernel)
+    if (dists.is_cuda() && dists.dim() == 2 && dists.size(0) == n1 && dists.size(1) == n2 &&
+        k < n2 &&
+        (dists.scalar_type() == at::kFloat || dists.scalar_type() == at::kBFloat16 ||
+         dists.scalar_type() == at::kHalf))
+        return row_smallest_mask(dists, k + 1);
+    return k_neighbors_from_argsort(dists, k, n1, n2);
+}
+
+at::Tensor radius_neighbors_mask(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
+                                 double epsilon, c10::string_view metric,
+                                 const c10::optional<at::Tensor> &w, const c10::optional<at::Tensor> &V,
+                                 const c10::optional<at::Tensor> &VI, c10::optional<double> p,
+                                 c10::optional<double> base, c10::optional<bool> shuffle,
+                                 c10::optional<at::Generator> generator) {
+    // (the reference logs this one under the k_neighbors_mask key too, neighbors.cpp:49)
+    C10_LOG_API_USAGE_ONCE("torchpairwise.csrc.ops.neighbors.k_neighbors_mask");
+    auto xs = check_pairwise_inputs("radius_neighbors_mask", x1, x2);
+    TORCH_CHECK(epsilon >= 0., "epsilon must be non-negative. Got epsilon=", epsilon)
+    at::NoGradGuard no_grad_guard;
+    auto dists = cdist(xs.first, xs.second, metric, w, V, VI, p, base, shuffle, std::move(generator));
+    return dists.le(epsilon);
+}
+
 int64_t cuda_version() { return tpw_runtime_version(); }
 std::string cuda_arch_flags() { return "gfx950"; }
 
@@ -401,6 +614,13 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward(
     return op.call(grad, x1, x2, shuffle, gen);
 }
 
+at::Tensor row_smallest_mask(const at::Tensor &dist, int64_t count) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchpairwise::_row_smallest_mask", "")
+                         .typed<at::Tensor(const at::Tensor &, int64_t)>();
+    return op.call(dist, count);
+}
+
 TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     // ---- internal ops of this build (HIP kernels; Autograd in autograd.cpp) ----
     m.def("_pw_inner(Tensor x1, Tensor x2, int epilogue) -> Tensor");
@@ -410,6 +630,7 @@ TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     m.def("_pw_lp_backward(Tensor grad, Tensor x1, Tensor x2, Tensor dist, float p) -> "
           "(Tensor grad_x1, Tensor grad_x2)");
     m.def("_jaccard(Tensor x1, Tensor x2) -> Tensor");
+    m.def("_row_smallest_mask(Tensor dist, int count) -> Tensor");
 
     // ---- internal ops of the reference (same schemas) ----
     // csrc/ops/pairwise_binary.cpp:135-160
@@ -432,47 +653,55 @@ TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     m.def("_cuda_arch_flags() -> str", &cuda_arch_flags);
 
     // ---- public metrics (csrc/ops/pairwise_metrics.h schemas) ----
-#define TPW_PUBLIC(schema, fn) m.def(schema, TORCH_FN(fn))
-    TPW_PUBLIC("euclidean_distances(Tensor x1, Tensor? x2=None) -> Tensor", euclidean_distances);
-    TPW_PUBLIC("haversine_distances(Tensor x1, Tensor? x2=None) -> Tensor", haversine_distances);
-    TPW_PUBLIC("manhattan_distances(Tensor x1, Tensor? x2=None) -> Tensor", manhattan_distances);
-    TPW_PUBLIC("cosine_distances(Tensor x1, Tensor? x2=None) -> Tensor", cosine_distances);
-    TPW_PUBLIC("linear_kernel(Tensor x1, Tensor? x2=None) -> Tensor", linear_kernel);
-    TPW_PUBLIC("polynomial_kernel(Tensor x1, Tensor? x2=None, int degree=3, float? gamma=None, float coef0=1) -> Tensor", polynomial_kernel);
-    TPW_PUBLIC("sigmoid_kernel(Tensor x1, Tensor? x2=None, float? gamma=None, float coef0=1) -> Tensor", sigmoid_kernel);
-    TPW_PUBLIC("rbf_kernel(Tensor x1, Tensor? x2=None, float? gamma=None) -> Tensor", rbf_kernel);
-    TPW_PUBLIC("laplacian_kernel(Tensor x1, Tensor? x2=None, float? gamma=None) -> Tensor", laplacian_kernel);
-    TPW_PUBLIC("cosine_similarity(Tensor x1, Tensor? x2=None) -> Tensor", cosine_similarity);
-    TPW_PUBLIC("additive_chi2_kernel(Tensor x1, Tensor? x2=None) -> Tensor", additive_chi2_kernel);
-    TPW_PUBLIC("chi2_kernel(Tensor x1, Tensor? x2=None, float gamma=1.0) -> Tensor", chi2_kernel);
-    TPW_PUBLIC("directed_hausdorff_distances(Tensor x1, Tensor? x2=None, *, bool shuffle=False, Generator? generator=None) -> (Tensor output, Tensor x1_indices, Tensor x2_indices)", directed_hausdorff_distances);
-    TPW_PUBLIC("minkowski_distances(Tensor x1, Tensor? x2=None, float p=2) -> Tensor", minkowski_distances);
-    TPW_PUBLIC("wminkowski_distances(Tensor x1, Tensor? x2=None, float p=2, Tensor? w=None) -> Tensor", wminkowski_distances);
-    TPW_PUBLIC("sqeuclidean_distances(Tensor x1, Tensor? x2=None) -> Tensor", sqeuclidean_distances);
-    TPW_PUBLIC("correlation_distances(Tensor x1, Tensor? x2=None) -> Tensor", correlation_distances);
-    TPW_PUBLIC("hamming_distances(Tensor x1, Tensor? x2=None) -> Tensor", hamming_distances);
-    TPW_PUBLIC("jaccard_distances(Tensor x1, Tensor? x2=None) -> Tensor", jaccard_distances);
-    TPW_PUBLIC("kulsinski_distances(Tensor x1, Tensor? x2=None) -> Tensor", kulsinski_distances);
-    TPW_PUBLIC("kulczynski1_distances(Tensor x1, Tensor? x2=None) -> Tensor", kulczynski1_distances);
-    TPW_PUBLIC("seuclidean_distances(Tensor x1, Tensor? x2=None, Tensor? V=None) -> Tensor", seuclidean_distances);
-    TPW_PUBLIC("cityblock_distances(Tensor x1, Tensor? x2=None) -> Tensor", cityblock_distances);
-    TPW_PUBLIC("mahalanobis_distances(Tensor x1, Tensor? x2=None, Tensor? VI=None) -> Tensor", mahalanobis_distances);
-    TPW_PUBLIC("chebyshev_distances(Tensor x1, Tensor? x2=None) -> Tensor", chebyshev_distances);
-    TPW_PUBLIC("braycurtis_distances(Tensor x1, Tensor? x2=None) -> Tensor", braycurtis_distances);
-    TPW_PUBLIC("canberra_distances(Tensor x1, Tensor? x2=None) -> Tensor", canberra_distances);
-    TPW_PUBLIC("jensenshannon_distances(Tensor x1, Tensor? x2=None, float? base=None) -> Tensor", jensenshannon_distances);
-    TPW_PUBLIC("yule_distances(Tensor x1, Tensor? x2=None) -> Tensor", yule_distances);
-    TPW_PUBLIC("dice_distances(Tensor x1, Tensor? x2=None) -> Tensor", dice_distances);
-    TPW_PUBLIC("rogerstanimoto_distances(Tensor x1, Tensor? x2=None) -> Tensor", rogerstanimoto_distances);
-    TPW_PUBLIC("russellrao_distances(Tensor x1, Tensor? x2=None) -> Tensor", russellrao_distances);
-    TPW_PUBLIC("sokalmichener_distances(Tensor x1, Tensor? x2=None) -> Tensor", sokalmichener_distances);
-    TPW_PUBLIC("sokalsneath_distances(Tensor x1, Tensor? x2=None) -> Tensor", sokalsneath_distances);
-    TPW_PUBLIC("snr_distances(Tensor x1, Tensor? x2=None) -> Tensor", snr_distances);
-    TPW_PUBLIC("l1_distances(Tensor x1, Tensor? x2=None) -> Tensor", l1_distances);
-    TPW_PUBLIC("l2_distances(Tensor x1, Tensor? x2=None) -> Tensor", l2_distances);
-    TPW_PUBLIC("lp_distances(Tensor x1, Tensor? x2=None, float p=2) -> Tensor", lp_distances);
-    TPW_PUBLIC("linf_distances(Tensor x1, Tensor? x2=None) -> Tensor", linf_distances);
+#define TPW_PUBLIC(fn) m.def(schema_of(#fn), TORCH_FN(fn))
+    TPW_PUBLIC(euclidean_distances);
+    TPW_PUBLIC(haversine_distances);
+    TPW_PUBLIC(manhattan_distances);
+    TPW_PUBLIC(cosine_distances);
+    TPW_PUBLIC(linear_kernel);
+    TPW_PUBLIC(polynomial_kernel);
+    TPW_PUBLIC(sigmoid_kernel);
+    TPW_PUBLIC(rbf_kernel);
+    TPW_PUBLIC(laplacian_kernel);
+    TPW_PUBLIC(cosine_similarity);
+    TPW_PUBLIC(additive_chi2_kernel);
+    TPW_PUBLIC(chi2_kernel);
+    TPW_PUBLIC(directed_hausdorff_distances);
+    TPW_PUBLIC(minkowski_distances);
+    TPW_PUBLIC(wminkowski_distances);
+    TPW_PUBLIC(sqeuclidean_distances);
+    TPW_PUBLIC(correlation_distances);
+    TPW_PUBLIC(hamming_distances);
+    TPW_PUBLIC(jaccard_distances);
+    TPW_PUBLIC(kulsinski_distances);
+    TPW_PUBLIC(kulczynski1_distances);
+    TPW_PUBLIC(seuclidean_distances);
+    TPW_PUBLIC(cityblock_distances);
+    TPW_PUBLIC(mahalanobis_distances);
+    TPW_PUBLIC(chebyshev_distances);
+    TPW_PUBLIC(braycurtis_distances);
+    TPW_PUBLIC(canberra_distances);
+    TPW_PUBLIC(jensenshannon_distances);
+    TPW_PUBLIC(yule_distances);
+    TPW_PUBLIC(dice_distances);
+    TPW_PUBLIC(rogerstanimoto_distances);
+    TPW_PUBLIC(russellrao_distances);
+    TPW_PUBLIC(sokalmichener_distances);
+    TPW_PUBLIC(sokalsneath_distances);
+    TPW_PUBLIC(snr_distances);
+    TPW_PUBLIC(l1_distances);
+    TPW_PUBLIC(l2_distances);
+    TPW_PUBLIC(lp_distances);
+    TPW_PUBLIC(linf_distances);
 #undef TPW_PUBLIC
+
+    // ---- cdist / pdist (csrc/ops/cpdist.cpp:248-255) and neighbour masks (neighbors.cpp:62-67) ----
+#define TPW_CPDIST_EXTRA "Tensor? w=None, Tensor? V=None, Tensor? VI=None, float? p=None, float? base=None, bool? shuffle=None, Generator? generator=None"
+    m.def("cdist(Tensor x1, Tensor x2, str metric=\"minkowski\", *, " TPW_CPDIST_EXTRA ") -> Tensor", TORCH_FN(cdist));
+    m.def("pdist(Tensor input, str metric=\"minkowski\", *, " TPW_CPDIST_EXTRA ") -> Tensor", TORCH_FN(pdist));
+    m.def("k_neighbors_mask(Tensor x1, Tensor? x2=None, int k=1, str metric=\"euclidean\", *, " TPW_CPDIST_EXTRA ") -> Tensor", TORCH_FN(k_neighbors_mask));
+    m.def("radius_neighbors_mask(Tensor x1, Tensor? x2=None, float epsilon=0., str metric=\"euclidean\", *, " TPW_CPDIST_EXTRA ") -> Tensor", TORCH_FN(radius_neighbors_mask));
+#undef TPW_CPDIST_EXTRA
 }
 
 }  // namespace tpw_ext

@@ -69,6 +69,7 @@ std::tuple<at::Tensor, at::Tensor> pw_lp_backward(const at::Tensor &grad, const 
                                                   double p);
 at::Tensor pw_binary_reduce(const char *name, const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor jaccard_fused(const at::Tensor &x1, const at::Tensor &x2);
+at::Tensor row_smallest_mask(const at::Tensor &dist, int64_t count);
 at::Tensor prf_div(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
 std::tuple<at::Tensor, at::Tensor> prf_div_backward(const at::Tensor &g, const at::Tensor &x,
                                                     const at::Tensor &y, c10::string_view mode);

@@ -1,4 +1,5 @@
-"""Module-level bindings of the ops (reference: torchpairwise/ops/metrics/pairwise.py:4-47)."""
+"""Module-level bindings of the ops (reference: torchpairwise/ops/metrics/pairwise.py:4-47,
+ops/cpdist.py:3-4, ops/metrics/neighbors.py:3-4)."""
 import torch
 
 _METRICS = [
@@ -20,13 +21,14 @@ _METRICS = [
     # it is bound here)
     "l1_distances", "l2_distances", "lp_distances", "linf_distances",
 ]
+_CPDIST = ["cdist", "pdist", "k_neighbors_mask", "radius_neighbors_mask"]
 _INTERNALS = [
     "pwand", "pwor", "pwxor", "pweq", "pwne", "pwlt", "pwgt", "pwle", "pwge",
     "pwand_sum", "pwor_sum", "pwxor_sum", "pweq_sum", "pwne_sum", "pweq_mean", "pwne_mean",
     "prf_div",
 ]
 
-for _name in _METRICS + _INTERNALS:
+for _name in _METRICS + _CPDIST + _INTERNALS:
     globals()[_name] = getattr(torch.ops.torchpairwise, _name)
 
-__all__ = list(_METRICS) + list(_INTERNALS)
+__all__ = list(_METRICS) + list(_CPDIST) + list(_INTERNALS)

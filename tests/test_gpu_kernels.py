@@ -354,3 +354,18 @@ def test_row_smallest_mask_half_types(dtype, count):
     got = capi.row_smallest_mask(d.to(DEV), count)
     want = P.k_smallest_mask(d.float().numpy(), count)  # exact widening keeps the order
     assert_equal(got, torch.from_numpy(want), f"{dtype} c={count}")
+
+
+@pytest.mark.parametrize("cols", [8192, 8191])  # vector (4-column) and scalar row access
+@pytest.mark.parametrize("count", [17, 40, 200])
+def test_row_smallest_mask_list_runs_dry(cols, count):
+    # the smallest entries all belong to workgroup thread 0 (columns 4c..4c+3 with
+    # c = 0, 256, 512, ... for the vector path; columns 0, 256, 512, ... for the scalar
+    # one), so its 16-entry list runs dry and the row falls back to the radix select
+    d = rand(4, cols, seed=15) + 1.0
+    own = torch.arange(0, cols, 1024).repeat_interleave(4) + torch.arange(4).repeat(len(range(0, cols, 1024)))
+    own = own[own < cols] if cols % 4 == 0 else torch.arange(0, cols, 256)
+    d[:, own] = -torch.arange(own.numel(), dtype=torch.float32)  # all distinct, all smallest
+    d[2, own[::2]] = 0.5  # ties among them too
+    got = capi.row_smallest_mask(d.to(DEV), count)
+    assert_equal(got, torch.from_numpy(P.k_smallest_mask(d.numpy(), count)), f"dry {cols} c={count}")

@@ -15,15 +15,15 @@
 // implementation-defined; everywhere else the sets are identical.)
 //
 // Two selection strategies:
-//   * count <= 16: every thread keeps its own sorted list of its L smallest keys (L = next
-//     power of two >= count) while streaming the row; the workgroup then pops the global
-//     minimum of the list heads `count` times.  About one compare per element.
-//   * count > 16: radix-2 select on the 32-bit order keys (one counting pass per bit below
+//   * count <= 256: every thread keeps a sorted list of its 16 (or fewer) smallest keys while
+//     streaming the row once; the workgroup then pops the minimum of the list heads `count`
+//     times.  The popped keys name the selected columns, so the mask is written without a
+//     second read: 4 bytes of distances read and 1 byte of mask written per entry.  When a
+//     thread's list runs dry before the last pop the row falls back to the radix select.
+//   * count > 256: radix-2 select on the 32-bit order keys (one counting pass per bit below
 //     the common prefix of the row's min and max keys), then, only when the boundary value
-//     is tied, a second radix-2 select on the column index among the tied entries.
-// The list selection streams the row twice (the second read mostly hits L2 / the infinity
-// cache); the radix selection caches rows of up to 16384 keys in LDS, longer rows are
-// re-read on each pass.
+//     is tied, a second radix-2 select on the column index among the tied entries; rows of
+//     up to 16384 keys are held in LDS for the passes.
 #include "common.hpp"
 
 namespace tpw {
@@ -121,17 +121,60 @@ struct Reducer {
     }
 };
 
-// The row's order keys, either cached in LDS (CACHED, one HBM read per row) or streamed
-// from memory on every pass, kUnroll loads in flight per thread.
-constexpr int kUnroll = 16;
-constexpr int64_t kCacheCols = 16384;  // 64 KB of keys per workgroup
+// ---------------------------------------------------------------- row access
+// A row is read in chunks of V consecutive columns (V = 4: one 16-byte fp32 / 8-byte
+// 16-bit load, used when cols % 4 == 0 and the row is aligned; V = 1 otherwise).  Thread t
+// owns chunks t, t + 256, t + 512, ...; kUnroll chunks are loaded before any is used.
+constexpr int kUnroll = 4;
+constexpr int64_t kCacheCols = 16384;  // rows whose keys the radix path may hold in LDS
 
-template <typename T, bool CACHED>
+template <typename T, int V>
+__device__ __forceinline__ void load_chunk(const T *p, float (&v)[V]) {
+    if constexpr (V == 1) {
+        v[0] = load_f32(p);
+    } else if constexpr (sizeof(T) == 4) {
+        const floatx4 q = *reinterpret_cast<const floatx4 *>(p);
+        v[0] = q[0], v[1] = q[1], v[2] = q[2], v[3] = q[3];
+    } else {
+        const uint2 q = *reinterpret_cast<const uint2 *>(p);
+        const T h[4] = {__builtin_bit_cast(T, (uint16_t)q.x), __builtin_bit_cast(T, (uint16_t)(q.x >> 16)),
+                        __builtin_bit_cast(T, (uint16_t)q.y), __builtin_bit_cast(T, (uint16_t)(q.y >> 16))};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = load_f32(&h[e]);
+    }
+}
+
+// The row's order keys, streamed from memory (CACHED = false) or held in LDS after one
+// streaming pass (CACHED).  for_each(f) calls f(key, column) for every entry this thread
+// owns.
+template <typename T, int V, bool CACHED>
 struct RowKeys {
     const T *row;
     int64_t cols;
     uint32_t *lds;  // [cols] when CACHED
 
+    __device__ int64_t chunks() const { return cols / V; }
+
+    template <typename F>
+    __device__ void stream(F &&f) const {
+        const int64_t nc = chunks();
+        for (int64_t base = threadIdx.x; base < nc; base += (int64_t)kThreads * kUnroll) {
+            float v[kUnroll][V];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t c = base + (int64_t)u * kThreads;
+                if (c < nc) load_chunk<T, V>(row + c * V, v[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t c = base + (int64_t)u * kThreads;
+                if (c < nc) {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) f(order_key(v[u][e]), (uint32_t)(c * V + e));
+                }
+            }
+        }
+    }
     __device__ void load() {
         if constexpr (CACHED) {
             stream([&](uint32_t k, uint32_t j) { lds[j] = k; });
@@ -139,96 +182,49 @@ struct RowKeys {
         }
     }
     template <typename F>
-    __device__ void stream(F &&f) const {
-        for (int64_t base = 0; base < cols; base += (int64_t)kThreads * kUnroll) {
-            float v[kUnroll];
-#pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const int64_t j = base + threadIdx.x + (int64_t)u * kThreads;
-                v[u] = j < cols ? load_f32(row + j) : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const int64_t j = base + threadIdx.x + (int64_t)u * kThreads;
-                if (j < cols) f(order_key(v[u]), (uint32_t)j);
-            }
-        }
-    }
-    // f(key, column) for every entry of the row owned by this thread
-    template <typename F>
     __device__ void for_each(F &&f) const {
         if constexpr (CACHED) {
-            for (int64_t j = threadIdx.x; j < cols; j += kThreads) f(lds[j], (uint32_t)j);
+            const int64_t nc = chunks();
+            for (int64_t c = threadIdx.x; c < nc; c += kThreads) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) f(lds[c * V + e], (uint32_t)(c * V + e));
+            }
         } else {
             stream(f);
         }
     }
 };
 
-// Writes mask[j] = (key(j) << 32 | j) <= thr for the whole row.
-template <typename T, bool CACHED>
-__device__ void write_mask(const RowKeys<T, CACHED> &keys, uint64_t thr, uint8_t *mrow) {
-    keys.for_each([&](uint32_t k, uint32_t j) {
-        mrow[j] = (((uint64_t)k << 32) | j) <= thr ? 1 : 0;
-    });
-}
-
-// count <= L <= 16: per-thread sorted lists, then `count` pops of the workgroup minimum.
-template <typename T, int L, bool CACHED>
-__global__ __launch_bounds__(kThreads) void smallest_list_kernel(const T *__restrict__ dist,
-                                                                 int64_t cols, int count,
-                                                                 uint8_t *__restrict__ mask) {
-    __shared__ uint64_t slots[2 * kWaves];
-    extern __shared__ uint32_t row_keys[];
-    const int64_t r = blockIdx.x;
-    RowKeys<T, CACHED> keys{dist + r * cols, cols, row_keys};
-    keys.load();
-
-    uint64_t lst[L];
-#pragma unroll
-    for (int s = 0; s < L; ++s) lst[s] = ~0ull;
-    keys.for_each([&](uint32_t k, uint32_t j) {
-        const uint64_t key = ((uint64_t)k << 32) | j;
-        if (key < lst[L - 1]) {
-            lst[L - 1] = key;
-#pragma unroll
-            for (int s = L - 1; s > 0; --s) {
-                if (lst[s] < lst[s - 1]) {
-                    const uint64_t t = lst[s];
-                    lst[s] = lst[s - 1];
-                    lst[s - 1] = t;
-                }
-            }
-        }
-    });
-
-    Reducer red{slots};
-    uint64_t thr = 0;
-    for (int c = 0; c < count; ++c) {
-        thr = red.min_u64(lst[0]);
-        if (lst[0] == thr) {  // keys are unique: exactly one thread owns the minimum
-#pragma unroll
-            for (int s = 0; s < L - 1; ++s) lst[s] = lst[s + 1];
-            lst[L - 1] = ~0ull;
-        }
+// Stores one chunk of the mask: V bytes, byte e = bit e of `bits`.
+template <int V>
+__device__ __forceinline__ void store_mask_chunk(uint8_t *p, uint32_t bits) {
+    if constexpr (V == 1) {
+        *p = (uint8_t)bits;
+    } else {
+        const uint32_t w = (bits & 1u) | ((bits & 2u) << 7) | ((bits & 4u) << 14) | ((bits & 8u) << 21);
+        *reinterpret_cast<uint32_t *>(p) = w;
     }
-    write_mask(keys, thr, mask + r * cols);
 }
 
-// count > 16: radix-2 select on the order key, then on the column among tied keys.
-template <typename T, bool CACHED>
-__global__ __launch_bounds__(kThreads) void smallest_radix_kernel(const T *__restrict__ dist,
-                                                                  int64_t cols, int count,
-                                                                  uint8_t *__restrict__ mask) {
-    __shared__ uint64_t slots[2 * kWaves];
-    extern __shared__ uint32_t row_keys[];
-    const int64_t r = blockIdx.x;
-    RowKeys<T, CACHED> keys{dist + r * cols, cols, row_keys};
-    keys.load();
-    Reducer red{slots};
+// mask[j] = (key(j) << 32 | j) <= thr for the whole row (reads the keys once more).
+template <typename T, int V, bool CACHED>
+__device__ void write_mask_keys(const RowKeys<T, V, CACHED> &keys, uint64_t thr, uint8_t *mrow) {
+    uint32_t bits = 0;
+    keys.for_each([&](uint32_t k, uint32_t j) {
+        const int e = (int)(j % V);
+        bits |= ((((uint64_t)k << 32) | j) <= thr ? 1u : 0u) << e;
+        if (e == V - 1) {
+            store_mask_chunk<V>(mrow + (j - e), bits);
+            bits = 0;
+        }
+    });
+}
 
-    // common prefix of the row's smallest and largest keys: the selected boundary value
-    // shares it, so only the bits below the highest differing bit need a counting pass
+// The count-th smallest 64-bit key (order key << 32 | column) of the row: radix-2 select on
+// the order key below the common prefix of the row's min and max keys, then, only when the
+// boundary value is tied, on the column among the tied entries.
+template <typename T, int V, bool CACHED>
+__device__ uint64_t radix_threshold(const RowKeys<T, V, CACHED> &keys, Reducer &red, int count) {
     uint32_t lo = 0xffffffffu, hi = 0;
     keys.for_each([&](uint32_t k, uint32_t) {
         lo = min(lo, k);
@@ -261,7 +257,7 @@ __global__ __launch_bounds__(kThreads) void smallest_radix_kernel(const T *__res
     if (need < n_eq) {
         // the need-th smallest column among the entries equal to t
         uint32_t jt = 0;
-        const int top = 31 - __builtin_clz((uint32_t)(cols - 1) | 1u);
+        const int top = 31 - __builtin_clz((uint32_t)(keys.cols - 1) | 1u);
         for (int b = top; b >= 0; --b) {
             const uint32_t c = jt | (1u << b);
             uint32_t n = 0;
@@ -270,34 +266,99 @@ __global__ __launch_bounds__(kThreads) void smallest_radix_kernel(const T *__res
         }
         jmax = jt;
     }
-    write_mask(keys, ((uint64_t)t << 32) | jmax, mask + r * cols);
+    return ((uint64_t)t << 32) | jmax;
+}
+
+// count <= kListMax: every thread keeps a sorted list of its L smallest keys while
+// streaming the row; the workgroup then pops the minimum of the list heads `count` times.
+// The popped keys are the selected entries and each belongs to the thread that popped it,
+// so the mask is written from them without reading the row again.  A thread's list can
+// run dry before the last pop only when count > L; the row then falls back to the radix
+// select (exact, re-reads the row).
+constexpr int kListMax = 256;
+
+template <typename T, int V, int L>
+__global__ __launch_bounds__(kThreads) void smallest_list_kernel(const T *__restrict__ dist,
+                                                                 int64_t cols, int count,
+                                                                 uint8_t *__restrict__ mask) {
+    __shared__ uint64_t slots[2 * kWaves];
+    __shared__ int dry;
+    const int64_t r = blockIdx.x;
+    RowKeys<T, V, false> keys{dist + r * cols, cols, nullptr};
+    if (threadIdx.x == 0) dry = 0;
+
+    uint64_t lst[L];
+#pragma unroll
+    for (int s = 0; s < L; ++s) lst[s] = ~0ull;
+    keys.stream([&](uint32_t k, uint32_t j) {
+        const uint64_t key = ((uint64_t)k << 32) | j;
+        if (key < lst[L - 1]) {
+            lst[L - 1] = key;
+#pragma unroll
+            for (int s = L - 1; s > 0; --s) {
+                if (lst[s] < lst[s - 1]) {
+                    const uint64_t x = lst[s];
+                    lst[s] = lst[s - 1];
+                    lst[s - 1] = x;
+                }
+            }
+        }
+    });
+    // entries this thread owns: more than L means its list may not hold all of them
+    const int64_t nc = keys.chunks();
+    const int64_t owned = (nc > threadIdx.x ? (nc - 1 - threadIdx.x) / kThreads + 1 : 0) * V;
+
+    Reducer red{slots};
+    uint32_t picked[L];  // columns this thread popped (0xffffffff = none)
+#pragma unroll
+    for (int s = 0; s < L; ++s) picked[s] = 0xffffffffu;
+    int npop = 0;
+    for (int c = 0; c < count; ++c) {
+        const uint64_t m = red.min_u64(lst[0]);
+        if (lst[0] == m) {  // keys are unique: exactly one thread owns the minimum
+#pragma unroll
+            for (int s = 0; s < L - 1; ++s) {
+                lst[s] = lst[s + 1];
+                picked[s] = picked[s + 1];
+            }
+            lst[L - 1] = ~0ull;
+            picked[L - 1] = (uint32_t)m;
+            if (++npop == L && owned > L && c < count - 1) dry = 1;
+        }
+    }
+    __syncthreads();
+    uint8_t *mrow = mask + r * cols;
+    if (dry) {  // workgroup-uniform
+        write_mask_keys(keys, radix_threshold(keys, red, count), mrow);
+        return;
+    }
+    for (int64_t c = threadIdx.x; c < nc; c += kThreads) {
+        uint32_t bits = 0;
+#pragma unroll
+        for (int s = 0; s < L; ++s)
+            if ((int64_t)(picked[s] / V) == c) bits |= 1u << (picked[s] % V);
+        store_mask_chunk<V>(mrow + c * V, bits);
+    }
+}
+
+// count > kListMax: radix select, with the row's keys in LDS when they fit.
+template <typename T, int V, bool CACHED>
+__global__ __launch_bounds__(kThreads) void smallest_radix_kernel(const T *__restrict__ dist,
+                                                                  int64_t cols, int count,
+                                                                  uint8_t *__restrict__ mask) {
+    __shared__ uint64_t slots[2 * kWaves];
+    extern __shared__ uint32_t row_keys[];
+    const int64_t r = blockIdx.x;
+    RowKeys<T, V, CACHED> keys{dist + r * cols, cols, row_keys};
+    keys.load();
+    Reducer red{slots};
+    write_mask_keys(keys, radix_threshold(keys, red, count), mask + r * cols);
 }
 
 __global__ void fill_kernel(uint8_t *__restrict__ mask, int64_t n, uint8_t value) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
         mask[i] = value;
-}
-
-template <typename T, bool CACHED>
-int launch_rows(const void *dist, int64_t rows, int64_t cols, int count, uint8_t *mask,
-                hipStream_t s) {
-    const T *d = static_cast<const T *>(dist);
-    const dim3 grid((unsigned)rows), block(kThreads);
-    const size_t lds = CACHED ? (size_t)cols * sizeof(uint32_t) : 0;
-    if (count > 16) {
-        hipLaunchKernelGGL((smallest_radix_kernel<T, CACHED>), grid, block, lds, s, d, cols, count, mask);
-        return check_launch("smallest_radix_kernel");
-    }
-#define TPW_LIST(LL)                                                                                       \
-    hipLaunchKernelGGL((smallest_list_kernel<T, LL, CACHED>), grid, block, lds, s, d, cols, count, mask); \
-    return check_launch("smallest_list_kernel")
-    if (count <= 1) { TPW_LIST(1); }
-    if (count <= 2) { TPW_LIST(2); }
-    if (count <= 4) { TPW_LIST(4); }
-    if (count <= 8) { TPW_LIST(8); }
-    TPW_LIST(16);
-#undef TPW_LIST
 }
 
 // LDS a workgroup may allocate on the current device (queried once per device).
@@ -314,15 +375,35 @@ size_t lds_per_block() {
     return cached[dev];
 }
 
-// The list selection reads the row twice (list pass, mask pass) and streams it; the radix
-// selection makes one pass per key bit and caches the row's keys in LDS when they fit
-// (next to the 64 bytes of reduction slots).
+template <typename T, int V>
+int launch_v(const T *d, int64_t rows, int64_t cols, int count, uint8_t *mask, hipStream_t s) {
+    const dim3 grid((unsigned)rows), block(kThreads);
+    if (count > kListMax) {
+        const size_t lds = (size_t)cols * sizeof(uint32_t);
+        if (cols <= kCacheCols && lds + sizeof(uint64_t) * 2 * kWaves <= lds_per_block()) {
+            hipLaunchKernelGGL((smallest_radix_kernel<T, V, true>), grid, block, lds, s, d, cols, count, mask);
+        } else {
+            hipLaunchKernelGGL((smallest_radix_kernel<T, V, false>), grid, block, 0, s, d, cols, count, mask);
+        }
+        return check_launch("smallest_radix_kernel");
+    }
+#define TPW_LIST(LL)                                                                                  \
+    hipLaunchKernelGGL((smallest_list_kernel<T, V, LL>), grid, block, 0, s, d, cols, count, mask); \
+    return check_launch("smallest_list_kernel")
+    if (count <= 1) { TPW_LIST(1); }
+    if (count <= 2) { TPW_LIST(2); }
+    if (count <= 4) { TPW_LIST(4); }
+    if (count <= 8) { TPW_LIST(8); }
+    TPW_LIST(16);
+#undef TPW_LIST
+}
+
 template <typename T>
 int launch(const void *dist, int64_t rows, int64_t cols, int count, uint8_t *mask, hipStream_t s) {
-    if (count > 16 && cols <= kCacheCols &&
-        (size_t)cols * sizeof(uint32_t) + 2 * kWaves * sizeof(uint64_t) <= lds_per_block())
-        return launch_rows<T, true>(dist, rows, cols, count, mask, s);
-    return launch_rows<T, false>(dist, rows, cols, count, mask, s);
+    const T *d = static_cast<const T *>(dist);
+    const bool vec = cols % 4 == 0 && (reinterpret_cast<uintptr_t>(dist) & (4 * sizeof(T) - 1)) == 0 &&
+                     (reinterpret_cast<uintptr_t>(mask) & 3) == 0;
+    return vec ? launch_v<T, 4>(d, rows, cols, count, mask, s) : launch_v<T, 1>(d, rows, cols, count, mask, s);
 }
 
 }  // namespace

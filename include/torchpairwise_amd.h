@@ -172,6 +172,63 @@ int tpw_lp_distances_backward(const float *grad, const float *x1, const float *x
                               void *workspace, void *stream);
 
 /* ------------------------------------------------------------------------- */
+/* The reference's own VALU metric kernels (fp32; x1 [batch,n,d], x2 [batch,m,d]) */
+/* ------------------------------------------------------------------------- */
+
+#define TPW_FAM_PPMINKOWSKI 0
+#define TPW_FAM_WMINKOWSKI 1
+#define TPW_FAM_CANBERRA 2
+#define TPW_FAM_BRAYCURTIS 3
+
+/* out = sum_k |x1 - x2|^p with no root (p = 0: d, as the reference fills; p = +-inf: max /
+ * min of |diff|).  Replaces _ppminkowski (torchpairwise/csrc/ops/ppminkowski.cpp:32-34,
+ * cpu/ppminkowski_kernel.cpp:58-118); sqeuclidean_distances is p = 2. */
+int tpw_ppminkowski(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                    int64_t d, double p, float *out, void *stream);
+
+/* out = (sum_k w[b,k] |x1 - x2|^p)^(1/p) (p = 0: d; p = +-inf: max / min of w |diff|),
+ * w [batch, d].  Replaces _wminkowski (wminkowski.cpp:34-36,
+ * cpu/wminkowski_kernel.cpp:63-128); seuclidean is w = 1 / V, p = 2. */
+int tpw_wminkowski(const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
+                   int64_t m, int64_t d, double p, float *out, void *stream);
+
+/* out = sum_k |x1 - x2| / (|x1| + |x2|), terms with a zero denominator skipped.  Replaces
+ * _canberra (canberra.cpp:30-32, cpu/canberra_kernel.cpp:13-82). */
+int tpw_canberra(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                 int64_t d, float *out, void *stream);
+
+/* out = sum_k |x1 - x2| / sum_k |x1 + x2|.  Replaces _braycurtis (braycurtis.cpp:30-32,
+ * cpu/braycurtis_kernel.cpp:13-81). */
+int tpw_braycurtis(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                   int64_t d, float *out, void *stream);
+
+/* Workspace (bytes) of the backward of family member `metric` (TPW_FAM_*). */
+size_t tpw_family_backward_workspace_size(int metric, int64_t batch, int64_t n, int64_t m,
+                                          int64_t d);
+
+/* Gradients of the four members above with the reference's formulas, summed over pairs in
+ * a fixed order (the reference's GPU kernels use atomics).  p = 0 gives zero gradients, as
+ * in the reference; p = +-inf is rejected (TPW_ERR_INVALID).  `out` is the forward result.
+ * Replace __ppminkowski_backward (ppminkowski.cpp:35-37, cpu/ppminkowski_kernel.cpp:123-
+ * 160,218-290), __wminkowski_backward (wminkowski.cpp:37-39, cpu/wminkowski_kernel.cpp:
+ * 132-410; grad_w [batch, d]), __canberra_backward (canberra.cpp:33-35,
+ * cpu/canberra_kernel.cpp:85-170; no guard: a zero |x1| + |x2| gives NaN, as there) and
+ * __braycurtis_backward (braycurtis.cpp:33-35, cpu/braycurtis_kernel.cpp:84-220). */
+int tpw_ppminkowski_backward(const float *grad, const float *x1, const float *x2, int64_t batch,
+                             int64_t n, int64_t m, int64_t d, double p, float *grad_x1,
+                             float *grad_x2, void *workspace, void *stream);
+int tpw_wminkowski_backward(const float *grad, const float *x1, const float *x2, const float *w,
+                            const float *out, int64_t batch, int64_t n, int64_t m, int64_t d,
+                            double p, float *grad_x1, float *grad_x2, float *grad_w,
+                            void *workspace, void *stream);
+int tpw_canberra_backward(const float *grad, const float *x1, const float *x2, int64_t batch,
+                          int64_t n, int64_t m, int64_t d, float *grad_x1, float *grad_x2,
+                          void *workspace, void *stream);
+int tpw_braycurtis_backward(const float *grad, const float *x1, const float *x2,
+                            const float *out, int64_t batch, int64_t n, int64_t m, int64_t d,
+                            float *grad_x1, float *grad_x2, void *workspace, void *stream);
+
+/* ------------------------------------------------------------------------- */
 /* Backward of the inner-product family                                       */
 /* ------------------------------------------------------------------------- */
 

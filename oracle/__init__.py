@@ -16,7 +16,9 @@ Contents (each function cites the reference file:line it restates):
   - cosine as the reference's torch-op composite with prf_div "identity";
   - directed Hausdorff as an fp32 brute force with per-operation rounding (no FMA) and the
     reference's tie rules, plus its backward scatter;
-  - the neighbour masks: each row's k + 1 smallest by a stable sort, and dist <= epsilon.
+  - the neighbour masks: each row's k + 1 smallest by a stable sort, and dist <= epsilon;
+  - the reference's VALU kernels (_ppminkowski, _wminkowski, _canberra, _braycurtis) as
+    differentiable torch broadcasts over [n, m, d].
 * ``oracle/cref.c`` (built by ``oracle/Makefile`` into ``oracle/_build/liboracle_cref.so``,
   wrapped by ``oracle.cref``) — a C restatement of the reference's CPU loops: the
   sequential early-break Hausdorff loop and the one-output-per-iteration binary
@@ -33,6 +35,9 @@ Pinning (what checks each function; see tests/test_oracle.py):
   cosine                  : sklearn.metrics.pairwise.cosine_distances, gradcheck in float64.
   directed Hausdorff      : the C early-break restatement (bit-exact value and indices),
       scipy.spatial.distance.directed_hausdorff (value), hand-built tie cases, gradcheck.
+  VALU family             : scipy.spatial.distance.cdist fixtures (sqeuclidean, weighted
+      minkowski p = 1, 2, 3, seuclidean, canberra with a 0 / 0 term, braycurtis),
+      gradcheck in float64, closed forms (p = 0 fills d, p = 2 of pp = squared euclidean).
   neighbour masks         : sklearn.neighbors kneighbors_graph / radius_neighbors_graph
       (connectivity) on tie-free data, hand-built ties / NaN / -0 cases with hand-derived
       masks (golden vectors), and the selection properties (row count, every selected

@@ -264,3 +264,46 @@ def k_smallest_mask(dist, count: int) -> np.ndarray:
 def radius_mask(dist, epsilon: float) -> np.ndarray:
     """dist <= epsilon (csrc/ops/neighbors.cpp:56-57)."""
     return np.asarray(dist) <= epsilon
+
+
+# ---------------------------------------------------------------------- VALU family
+def _pair_diff(x1: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
+    return x1.unsqueeze(-2) - x2.unsqueeze(-3)  # [..., n, m, d]
+
+
+def ppminkowski(x1: torch.Tensor, x2: torch.Tensor, p: float) -> torch.Tensor:
+    """sum_k |x1 - x2|^p with no root; p = 0 gives d (the reference fills it), +-inf the
+    max / min of |diff| (cpu/ppminkowski_kernel.cpp:13-52,88-114).  Differentiable torch."""
+    d = _pair_diff(x1, x2).abs()
+    if p == 0:
+        return torch.full(d.shape[:-1], float(x1.shape[-1]), dtype=x1.dtype)
+    if p == float("inf"):
+        return d.amax(-1)
+    if p == -float("inf"):
+        return d.amin(-1)
+    return d.pow(p).sum(-1)
+
+
+def wminkowski(x1: torch.Tensor, x2: torch.Tensor, w: torch.Tensor, p: float) -> torch.Tensor:
+    """(sum_k w_k |x1 - x2|^p)^(1/p); w [d] or [batch, d] (cpu/wminkowski_kernel.cpp:13-60)."""
+    d = _pair_diff(x1, x2).abs()
+    ww = w if w.dim() == 1 else w[:, None, None, :]
+    if p == 0:
+        return torch.full(d.shape[:-1], float(x1.shape[-1]), dtype=x1.dtype)
+    if p == float("inf"):
+        return (d * ww).amax(-1)
+    return (d.pow(p) * ww).sum(-1).pow(1.0 / p)
+
+
+def canberra(x1: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
+    """sum_k |x1 - x2| / (|x1| + |x2|), 0 / 0 terms skipped (cpu/canberra_kernel.cpp:13-30)."""
+    diff = _pair_diff(x1, x2).abs()
+    den = x1.abs().unsqueeze(-2) + x2.abs().unsqueeze(-3)
+    safe = torch.where(den != 0, den, torch.ones_like(den))
+    return torch.where(den != 0, diff / safe, torch.zeros_like(diff)).sum(-1)
+
+
+def braycurtis(x1: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
+    """sum_k |x1 - x2| / sum_k |x1 + x2| (cpu/braycurtis_kernel.cpp:13-29)."""
+    s = x1.unsqueeze(-2) + x2.unsqueeze(-3)
+    return _pair_diff(x1, x2).abs().sum(-1) / s.abs().sum(-1)

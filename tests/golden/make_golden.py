@@ -14,6 +14,9 @@ this build's oracle:
   random clouds, plus hand-built clouds whose maxima / minima tie, with the expected
   indices derived by hand from the reference's rules (last m reaching the max, first n
   reaching that m's min; csrc/ops/cpu/hausdorff_kernel.cpp:25-51);
+* the reference's VALU family (sqeuclidean, weighted minkowski, seuclidean, canberra,
+  braycurtis):                  scipy.spatial.distance.cdist in float64 (with a zero
+  coordinate pair for canberra's skipped 0/0 term);
 * neighbour masks:              sklearn.neighbors.NearestNeighbors(algorithm="brute")
   kneighbors_graph / radius_neighbors_graph (connectivity, float64) on tie-free random
   points, plus hand-built distance rows with ties, NaN, +-0 and inf whose masks are
@@ -96,6 +99,24 @@ def hausdorff():
            for f, v in zip(("x1", "x2", "value", "idx1", "idx2"), t)})
 
 
+def family():
+    rng = np.random.default_rng(20260105)
+    x1 = rng.standard_normal((8, 6))
+    x2 = rng.standard_normal((10, 6))
+    x1[0, 2] = x2[1, 2] = 0.0  # canberra: a 0 / 0 term, skipped
+    w = rng.random(6) + 0.2
+    V = rng.random(6) + 0.5
+    out = dict(x1=x1, x2=x2, w=w, V=V)
+    out["sqeuclidean"] = cdist(x1, x2, "sqeuclidean")
+    out["canberra"] = cdist(x1, x2, "canberra")
+    out["braycurtis"] = cdist(x1, x2, "braycurtis")
+    for p in (1, 2, 3):
+        out[f"wminkowski_p{p}"] = cdist(x1, x2, "minkowski", p=p, w=w)
+    out["seuclidean"] = cdist(x1, x2, "seuclidean", V=V)
+    out["seuclidean_self"] = cdist(x1, x1, "seuclidean", V=x1.var(0, ddof=1))
+    np.savez_compressed(OUT / "family.npz", **out)
+
+
 def neighbors():
     from sklearn.neighbors import NearestNeighbors
 
@@ -133,5 +154,6 @@ if __name__ == "__main__":
     boolean()
     minkowski()
     hausdorff()
+    family()
     neighbors()
     print("wrote", sorted(p.name for p in OUT.glob("*.npz")))

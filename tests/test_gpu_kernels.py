@@ -369,3 +369,76 @@ def test_row_smallest_mask_list_runs_dry(cols, count):
     d[2, own[::2]] = 0.5  # ties among them too
     got = capi.row_smallest_mask(d.to(DEV), count)
     assert_equal(got, torch.from_numpy(P.k_smallest_mask(d.numpy(), count)), f"dry {cols} c={count}")
+
+
+# --------------------------------------------------------------------------------------
+# the reference's VALU family (_ppminkowski, _wminkowski, _canberra, _braycurtis)
+# fp32 bar: values rtol 1e-5 (+ atol 1e-5 * max); gradients rtol 1e-4 (+ atol 1e-4 * max)
+# --------------------------------------------------------------------------------------
+FAM_SHAPES = [(1, 1, 1, 1), (1, 130, 70, 64), (2, 129, 131, 33), (1, 300, 257, 7)]
+
+
+def _fam_ref(metric, a, b, w, p):
+    if metric == capi.FAM_PPMINKOWSKI:
+        return P.ppminkowski(a, b, p)
+    if metric == capi.FAM_WMINKOWSKI:
+        return P.wminkowski(a, b, w, p)
+    if metric == capi.FAM_CANBERRA:
+        return P.canberra(a, b)
+    return P.braycurtis(a, b)
+
+
+def _fam_inputs(B, n, m, d):
+    x1 = randn(B, n, d, seed=20)
+    x2 = randn(B, m, d, seed=21)
+    w = rand(B, d, seed=22) + 0.2
+    return x1, x2, w
+
+
+@pytest.mark.parametrize("B,n,m,d", FAM_SHAPES)
+@pytest.mark.parametrize("metric,p", [(0, 2.0), (0, 1.0), (0, 3.0), (0, 1.5), (0, float("inf")),
+                                      (0, -float("inf")), (0, 0.0), (1, 2.0), (1, 1.0), (1, 3.0),
+                                      (1, 0.7), (1, float("inf")), (2, 1.0), (3, 1.0)])
+def test_family_forward(B, n, m, d, metric, p):
+    print(f"family fwd metric={metric} p={p} {B}x{n}x{m}x{d}", flush=True)
+    x1, x2, w = _fam_inputs(B, n, m, d)
+    if metric == capi.FAM_CANBERRA:
+        x1[..., ::3, 0] = 0.0  # 0 / 0 terms (skipped)
+        x2[..., ::2, 0] = 0.0
+    got = capi.family_forward(metric, x1.to(DEV), x2.to(DEV), w.to(DEV), p)
+    ref = torch.stack([_fam_ref(metric, x1[i].double(), x2[i].double(), w[i].double(), p) for i in range(B)])
+    assert_close(got, ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()), what=f"metric {metric} p={p}")
+
+
+@pytest.mark.parametrize("B,n,m,d", FAM_SHAPES[1:] + [(1, 600, 900, 40)])
+@pytest.mark.parametrize("metric,p", [(0, 2.0), (0, 1.0), (0, 3.0), (0, 1.5), (1, 2.0), (1, 1.0),
+                                      (1, 3.0), (1, 2.5), (2, 1.0), (3, 1.0)])
+def test_family_backward(B, n, m, d, metric, p):
+    print(f"family bwd metric={metric} p={p} {B}x{n}x{m}x{d}", flush=True)
+    x1, x2, w = _fam_inputs(B, n, m, d)
+    g = randn(B, n, m, seed=23)
+    out = capi.family_forward(metric, x1.to(DEV), x2.to(DEV), w.to(DEV), p)
+    got = capi.family_backward(metric, g.to(DEV), x1.to(DEV), x2.to(DEV), w.to(DEV), p, out)
+    refs = []
+    for i in range(B):
+        ins = [x1[i].double().requires_grad_(), x2[i].double().requires_grad_()]
+        if metric == capi.FAM_WMINKOWSKI:
+            ins.append(w[i].double().requires_grad_())
+        val = _fam_ref(metric, ins[0], ins[1], ins[2] if len(ins) == 3 else None, p)
+        val.backward(g[i].double())
+        refs.append([t.grad for t in ins])
+    for k, name in enumerate(["grad_x1", "grad_x2", "grad_w"][:len(got)]):
+        ref = torch.stack([r[k] for r in refs])
+        assert_close(got[k], ref, rtol=1e-4, atol=1e-4 * float(ref.abs().max()), what=f"{name} m{metric} p={p}")
+
+
+def test_family_backward_edge_cases():
+    x1, x2, w = _fam_inputs(1, 40, 30, 9)
+    g = randn(1, 40, 30, seed=24)
+    for metric in (capi.FAM_PPMINKOWSKI, capi.FAM_WMINKOWSKI):  # p = 0: zero gradients
+        out = capi.family_forward(metric, x1.to(DEV), x2.to(DEV), w.to(DEV), 0.0)
+        assert bool((out == 9.0).all())
+        for t in capi.family_backward(metric, g.to(DEV), x1.to(DEV), x2.to(DEV), w.to(DEV), 0.0, out):
+            assert bool((t == 0).all())
+    with pytest.raises(RuntimeError, match="not supported"):  # inf backward is rejected
+        capi.family_backward(capi.FAM_PPMINKOWSKI, g.to(DEV), x1.to(DEV), x2.to(DEV), None, float("inf"))

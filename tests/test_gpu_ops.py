@@ -258,3 +258,38 @@ def test_radius_neighbors_mask_gpu():
     got = tp.radius_neighbors_mask(x1.to(DEV), x2.to(DEV), 5.0)
     dist = tp.euclidean_distances(x1.to(DEV), x2.to(DEV)).cpu()
     assert_equal(got, torch.from_numpy(P.radius_mask(dist.numpy(), 5.0)), "radius")
+
+
+# --------------------------------------------------------------------------------------
+# the reference's VALU family through the drop-in ops
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name", ["sqeuclidean_distances", "canberra_distances", "braycurtis_distances",
+                                  "wminkowski_distances", "seuclidean_distances"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_family_ops_gpu(name, dtype):
+    print(f"{name} {dtype}", flush=True)
+    x1, x2 = randn(150, 24, seed=0, dtype=dtype), randn(90, 24, seed=1, dtype=dtype)
+    w = (rand(24, seed=2) + 0.2).to(dtype)
+    extra = {"wminkowski_distances": (3.0, w), "seuclidean_distances": (w,)}.get(name, ())
+    fn = getattr(tp, name)
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    out = fn(a, b, *[e.to(DEV) if torch.is_tensor(e) else e for e in extra])
+    assert out.dtype == dtype
+    g = randn(150, 90, seed=3)
+    out.backward(g.to(DEV, dtype))
+    ra, rb = x1.double().requires_grad_(), x2.double().requires_grad_()
+    ref = fn(ra, rb, *[e.double() if torch.is_tensor(e) else e for e in extra])  # CPU = reference loops
+    ref.backward(g.double())
+    rtol = 1e-5 if dtype == torch.float32 else 1e-2
+    grtol = 1e-4 if dtype == torch.float32 else 3e-2
+    assert_close(out.float(), ref, rtol=rtol, atol=rtol * float(ref.abs().max()), what=name)
+    assert_close(a.grad.float(), ra.grad, rtol=grtol, atol=grtol * float(ra.grad.abs().max()), what="grad x1")
+    assert_close(b.grad.float(), rb.grad, rtol=grtol, atol=grtol * float(rb.grad.abs().max()), what="grad x2")
+
+
+def test_sqeuclidean_identical_points_are_zero():
+    x = randn(200, 64, seed=5).to(DEV)
+    d = tp.sqeuclidean_distances(x)
+    assert bool((torch.diagonal(d) == 0).all())  # direct sum: no |a|^2 + |b|^2 - 2ab residue
+    with pytest.raises(NotImplementedError):
+        tp.canberra_distances(x.double())

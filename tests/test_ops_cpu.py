@@ -230,3 +230,61 @@ def test_row_smallest_mask_cpu_hand_built_rows():
         got = torch.ops.torchpairwise._row_smallest_mask(torch.from_numpy(g[f"row{i}_dist"]),
                                                          int(g[f"row{i}_count"]))
         assert np.array_equal(got.numpy(), g[f"row{i}_mask"]), i
+
+
+# ---------------------------------------------------------------------- VALU family (CPU)
+def test_family_cpu_match_scipy_golden():
+    g = dict(np.load(GOLDEN / "family.npz"))
+    x1, x2 = torch.from_numpy(g["x1"]), torch.from_numpy(g["x2"])
+    w, V = torch.from_numpy(g["w"]), torch.from_numpy(g["V"])
+    tol = dict(rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(tp.sqeuclidean_distances(x1, x2).numpy(), g["sqeuclidean"], **tol)
+    np.testing.assert_allclose(tp.canberra_distances(x1, x2).numpy(), g["canberra"], **tol)
+    np.testing.assert_allclose(tp.braycurtis_distances(x1, x2).numpy(), g["braycurtis"], **tol)
+    for p in (1, 2, 3):
+        np.testing.assert_allclose(tp.wminkowski_distances(x1, x2, float(p), w).numpy(),
+                                   g[f"wminkowski_p{p}"], **tol)
+    np.testing.assert_allclose(tp.seuclidean_distances(x1, x2, V).numpy(), g["seuclidean"], **tol)
+    np.testing.assert_allclose(tp.seuclidean_distances(x1).numpy(), g["seuclidean_self"], **tol)
+    with pytest.raises(RuntimeError, match="V is required for seuclidean"):
+        tp.seuclidean_distances(x1, x2)
+
+
+@pytest.mark.parametrize("p", [0.0, 1.0, 1.5, 2.0, 3.0, float("inf"), -float("inf")])
+def test_family_cpu_internal_ops_and_grads(p):
+    # batched _wminkowski: the reference checks x1.size(1) (rows) against w.size(1)
+    # (cpu/wminkowski_kernel.cpp:84-86), so rows == features here
+    x1 = torch.randn(2, 5, 5, dtype=torch.float64, generator=torch.Generator().manual_seed(0))
+    x2 = torch.randn(2, 6, 5, dtype=torch.float64, generator=torch.Generator().manual_seed(1))
+    w = torch.rand(2, 5, dtype=torch.float64, generator=torch.Generator().manual_seed(2)) + 0.2
+    ops = torch.ops.torchpairwise
+    assert_close(ops._ppminkowski(x1, x2, p), P.ppminkowski(x1, x2, p), rtol=1e-12, atol=1e-12, what="pp")
+    if p != -float("inf"):
+        assert_close(ops._wminkowski(x1, x2, w, p), P.wminkowski(x1, x2, w, p), rtol=1e-12, atol=1e-12,
+                     what="w")
+    if p in (0.0,):  # p = 0: zero gradients, as the reference's backward returns
+        g = torch.ones(2, 5, 6, dtype=torch.float64)
+        assert all((t == 0).all() for t in ops.__ppminkowski_backward(g, x1, x2, p))
+        return
+    a, b, c = (t.clone().requires_grad_() for t in (x1, x2, w))
+    assert torch.autograd.gradcheck(lambda u, v: ops._ppminkowski(u, v, p), (a, b))
+    if p != -float("inf"):
+        assert torch.autograd.gradcheck(lambda u, v, q: ops._wminkowski(u, v, q, p), (a, b, c))
+
+
+def test_canberra_braycurtis_cpu_grads_and_dtypes():
+    x1 = torch.randn(6, 4, dtype=torch.float64, requires_grad=True)
+    x2 = torch.randn(5, 4, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(tp.canberra_distances, (x1, x2))
+    assert torch.autograd.gradcheck(tp.braycurtis_distances, (x1, x2))
+    for fn in (tp.canberra_distances, tp.braycurtis_distances, tp.sqeuclidean_distances):
+        for dt in (torch.float32, torch.bfloat16):
+            got = fn(x1.detach().to(dt), x2.detach().to(dt))
+            assert got.dtype == dt
+            ref = fn(x1.detach().to(dt).double(), x2.detach().to(dt).double())
+            assert_close(got.double(), ref, rtol=1e-5 if dt == torch.float32 else 2e-2, atol=1e-6,
+                         what=f"{fn} {dt}")
+    with pytest.raises(RuntimeError, match="batch_size of x1 and x2 do not match"):
+        torch.ops.torchpairwise._canberra(torch.randn(2, 3, 4), torch.randn(3, 3, 4))
+    with pytest.raises(RuntimeError, match="feature dimension of x1, x2, and w do not match"):
+        torch.ops.torchpairwise._wminkowski(torch.randn(2, 3, 4), torch.randn(2, 5, 4), torch.rand(2, 4), 2.0)

@@ -275,3 +275,38 @@ def test_pins_catch_highest_column_on_ties():
     bad = sum(not np.array_equal(wrong(g[f"row{i}_dist"], int(g[f"row{i}_count"])), g[f"row{i}_mask"])
               for i in range(int(g["n_rows"])))
     assert bad >= 3
+
+
+# ---------------------------------------------------------------------- VALU family
+def test_family_oracle_matches_scipy_golden():
+    g = npz("family.npz")
+    x1, x2 = torch.from_numpy(g["x1"]), torch.from_numpy(g["x2"])
+    w, V = torch.from_numpy(g["w"]), torch.from_numpy(g["V"])
+    tol = dict(rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(P.ppminkowski(x1, x2, 2.0).numpy(), g["sqeuclidean"], **tol)
+    np.testing.assert_allclose(P.canberra(x1, x2).numpy(), g["canberra"], **tol)
+    np.testing.assert_allclose(P.braycurtis(x1, x2).numpy(), g["braycurtis"], **tol)
+    for p in (1, 2, 3):
+        np.testing.assert_allclose(P.wminkowski(x1, x2, w, float(p)).numpy(), g[f"wminkowski_p{p}"], **tol)
+    np.testing.assert_allclose(P.wminkowski(x1, x2, 1.0 / V, 2.0).numpy(), g["seuclidean"], **tol)
+    # closed forms: p = 0 fills d; pp with p = 2 is the squared euclidean distance
+    assert (P.ppminkowski(x1, x2, 0.0) == 6.0).all()
+    np.testing.assert_allclose(P.ppminkowski(x1, x2, 2.0).numpy(), cdist(g["x1"], g["x2"]) ** 2, rtol=1e-12)
+
+
+def test_family_oracle_gradients():
+    x1 = torch.randn(5, 4, dtype=torch.float64, requires_grad=True)
+    x2 = torch.randn(6, 4, dtype=torch.float64, requires_grad=True)
+    w = (torch.rand(4, dtype=torch.float64) + 0.2).requires_grad_()
+    for p in (1.0, 1.5, 2.0, 3.0, float("inf")):
+        assert torch.autograd.gradcheck(lambda a, b: P.ppminkowski(a, b, p), (x1, x2))
+        assert torch.autograd.gradcheck(lambda a, b, c: P.wminkowski(a, b, c, p), (x1, x2, w))
+    assert torch.autograd.gradcheck(P.canberra, (x1, x2))
+    assert torch.autograd.gradcheck(P.braycurtis, (x1, x2))
+
+
+def test_pins_catch_a_missing_root_or_weight():
+    g = npz("family.npz")
+    x1, x2, w = (torch.from_numpy(g[k]) for k in ("x1", "x2", "w"))
+    assert not np.allclose(P.ppminkowski(x1, x2, 3.0).numpy(), g["wminkowski_p3"])  # root dropped
+    assert not np.allclose(P.wminkowski(x1, x2, torch.ones_like(w), 3.0).numpy(), g["wminkowski_p3"])

@@ -19,6 +19,7 @@ TPW_F32, TPW_BF16, TPW_F16, TPW_F64, TPW_I8, TPW_U8, TPW_I16, TPW_I32, TPW_I64 =
 BIT_AND, BIT_OR, BIT_XOR, BIT_EQ, BIT_NE = 0, 1, 2, 3, 4
 RED_SUM, RED_MEAN = 0, 1
 EPI_DOT, EPI_EUCLIDEAN, EPI_SQEUCLIDEAN, EPI_COSINE_SIM, EPI_COSINE_DIST = 0, 1, 2, 3, 4
+FAM_PPMINKOWSKI, FAM_WMINKOWSKI, FAM_CANBERRA, FAM_BRAYCURTIS = 0, 1, 2, 3
 
 _i64, _p, _i, _d, _sz = C.c_int64, C.c_void_p, C.c_int, C.c_double, C.c_size_t
 
@@ -45,6 +46,15 @@ _SIGNATURES = {
     "tpw_directed_hausdorff": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "tpw_directed_hausdorff_backward": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),
     "tpw_row_smallest_mask": (_i, [_p, _i, _i64, _i64, _i64, _p, _p]),
+    "tpw_ppminkowski": (_i, [_p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
+    "tpw_wminkowski": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
+    "tpw_canberra": (_i, [_p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "tpw_braycurtis": (_i, [_p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "tpw_family_backward_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64]),
+    "tpw_ppminkowski_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p, _p, _p]),
+    "tpw_wminkowski_backward": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p, _p, _p, _p]),
+    "tpw_canberra_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "tpw_braycurtis_backward": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
 }
 
 _lib = None
@@ -342,3 +352,64 @@ def row_smallest_mask(dist, count):
     call("tpw_row_smallest_mask", _ptr(d), _dtype_code(d), d.shape[0], d.shape[1], int(count),
          _ptr(mask), _stream())
     return mask
+
+
+def _as3f(x):
+    x = x.contiguous()
+    return x if x.dim() == 3 else x.unsqueeze(0)
+
+
+def family_forward(metric, x1, x2, w=None, p=2.0):
+    """The reference's VALU kernels on fp32 [(batch,) n, d] x [(batch,) m, d] inputs."""
+    import torch
+
+    a, b = _as3f(x1), _as3f(x2)
+    B, n, d = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=a.device)
+    if metric == FAM_PPMINKOWSKI:
+        call("tpw_ppminkowski", _ptr(a), _ptr(b), B, n, m, d, float(p), _ptr(out), _stream())
+    elif metric == FAM_WMINKOWSKI:
+        ww = w.contiguous().reshape(B, d)
+        call("tpw_wminkowski", _ptr(a), _ptr(b), _ptr(ww), B, n, m, d, float(p), _ptr(out), _stream())
+    elif metric == FAM_CANBERRA:
+        call("tpw_canberra", _ptr(a), _ptr(b), B, n, m, d, _ptr(out), _stream())
+    else:
+        call("tpw_braycurtis", _ptr(a), _ptr(b), B, n, m, d, _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def family_backward(metric, grad, x1, x2, w=None, p=2.0, out=None):
+    """(grad_x1, grad_x2[, grad_w]) of family_forward."""
+    import torch
+
+    a, b = _as3f(x1), _as3f(x2)
+    B, n, d = a.shape
+    m = b.shape[1]
+    g = grad.contiguous().reshape(B, n, m)
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    ws = torch.empty((max(1, lib().tpw_family_backward_workspace_size(metric, B, n, m, d)),),
+                     dtype=torch.uint8, device=a.device)
+    if metric == FAM_PPMINKOWSKI:
+        call("tpw_ppminkowski_backward", _ptr(g), _ptr(a), _ptr(b), B, n, m, d, float(p), _ptr(gx1),
+             _ptr(gx2), _ptr(ws), _stream())
+        res = [gx1, gx2]
+    elif metric == FAM_WMINKOWSKI:
+        ww = w.contiguous().reshape(B, d)
+        gw = torch.empty_like(ww)
+        o = out.contiguous().reshape(B, n, m)
+        call("tpw_wminkowski_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(ww), _ptr(o), B, n, m, d,
+             float(p), _ptr(gx1), _ptr(gx2), _ptr(gw), _ptr(ws), _stream())
+        res = [gx1, gx2, gw]
+    elif metric == FAM_CANBERRA:
+        call("tpw_canberra_backward", _ptr(g), _ptr(a), _ptr(b), B, n, m, d, _ptr(gx1), _ptr(gx2),
+             _ptr(ws), _stream())
+        res = [gx1, gx2]
+    else:
+        o = out.contiguous().reshape(B, n, m)
+        call("tpw_braycurtis_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(o), B, n, m, d, _ptr(gx1),
+             _ptr(gx2), _ptr(ws), _stream())
+        res = [gx1, gx2]
+    if x1.dim() == 2:
+        res = [res[0][0], res[1][0]] + ([res[2][0]] if len(res) == 3 else [])
+    return tuple(res)

@@ -1,5 +1,7 @@
 // Non-GEMM pairwise reductions on the VALU: Minkowski distances for p = 0, 1, 2, 3, inf and
-// general p, and their gradient (at::_cdist_forward / at::_cdist_backward semantics).
+// general p, and their gradient (at::_cdist_forward / at::_cdist_backward semantics), plus
+// the reference's own kernels of the same shape: _ppminkowski (sum of |d|^p, no root),
+// _wminkowski (per-feature weights, root), _canberra and _braycurtis.
 //
 // Forward: 256-thread blocks own a 128 x 128 output tile; thread (ty, tx) owns rows
 // 8 ty + r (r < 8) and columns 64 h + 4 tx + c (h < 2, c < 4).  Both operand panels are
@@ -8,14 +10,17 @@
 // Per pair-feature the VALU does a subtract and an abs-modified accumulate (p = 1: add,
 // p = inf: max), three ops for p = 3 (d * |d| fused into the accumulate), one exp2/log2
 // pair more for general p.  Stores are non-temporal float4 rows (256 B per 16 lanes).
+// Bray-Curtis runs the p = 1 kernel for sum |a - b| and a second pass for sum |a + b| that
+// divides the stored numerator (two accumulators per output would halve the register
+// tile; the VALU work is the same).
 //
-// Backward (grad of x1; x2 by the transposed call): out[i,k] = sum_j F(x1[i,k] - x2[j,k],
-// g[i,j], dist[i,j]).  A block owns 128 rows x 64 features with its x1 values held in
-// registers, streams 32 j at a time (x2 panel [j][k] and the per-pair weight
-// w = g / dist^(p-1) computed while staging into LDS), thread block 8 rows x 4 features.
-// The j range is split over several blocks when the row/feature grid alone would not fill
-// the GPU; the per-split partial sums are then added in split order by a second kernel,
-// so the result is deterministic.
+// Backward (grad of x1; x2 by the transposed call): out[i,k] = sum_j F(x1[i,k], x2[j,k],
+// per-pair weights of (i, j)).  A block owns 128 rows x 64 features with its x1 values held
+// in registers, streams 32 j at a time (x2 panel [j][k] and up to two per-pair weights
+// computed while staging into LDS), thread block 8 rows x 4 features.  The j range is
+// split over several blocks when the row/feature grid alone would not fill the GPU; the
+// per-split partial sums are then added in split order by a second kernel, so the result
+// is deterministic (the reference accumulates with atomics on its GPU path).
 #include <math.h>
 
 #include "common.hpp"
@@ -23,7 +28,17 @@
 namespace tpw {
 namespace {
 
-enum PKind { kP0 = 0, kP1, kP2, kP3, kPInf, kPLt2, kPGen };
+enum PKind { kP0 = 0, kP1, kP2, kP3, kPInf, kPLt2, kPGen, kPNInf };
+
+// What a forward launch computes per (i, j) (PK picks |d|^p for the first three).
+enum Mode {
+    kRoot = 0,  // (sum_k |d|^p)^(1/p)            at::_cdist_forward
+    kSum,       // sum_k |d|^p                     _ppminkowski (cpu/ppminkowski_kernel.cpp:13-29)
+    kWeighted,  // (sum_k w_k |d|^p)^(1/p)         _wminkowski (cpu/wminkowski_kernel.cpp:13-60)
+    kCanberra,  // sum_k |d| / (|a| + |b|), terms with |a| + |b| == 0 skipped (canberra_kernel.cpp:13-30)
+    kBrayDen,   // out = out / sum_k |a + b|, out holding sum_k |a - b| (braycurtis_kernel.cpp:13-29)
+    kPlusSum,   // sum_k |a + b| (the Bray-Curtis denominator, for the backward)
+};
 
 constexpr int kThreads = 256;
 constexpr int kTile = 128;
@@ -35,10 +50,38 @@ __device__ __forceinline__ float lp_step(float acc, float a, float b, float p) {
     const float d = a - b;
     if constexpr (PK == kP1) return acc + fabsf(d);
     else if constexpr (PK == kPInf) return fmaxf(acc, fabsf(d));
+    else if constexpr (PK == kPNInf) return fminf(acc, fabsf(d));
     else if constexpr (PK == kP2) return fmaf(d, d, acc);
     else if constexpr (PK == kP3) return fmaf(d * d, fabsf(d), acc);
     else if constexpr (PK == kP0) return acc + (d != 0.0f ? 1.0f : 0.0f);
     else return acc + exp2f(p * __log2f(fabsf(d)));
+}
+
+template <int MODE, int PK>
+__device__ __forceinline__ float fam_step(float acc, float a, float b, float wk, float p) {
+    if constexpr (MODE == kRoot || MODE == kSum) {
+        return lp_step<PK>(acc, a, b, p);
+    } else if constexpr (MODE == kWeighted) {
+        const float d = a - b;
+        if constexpr (PK == kP1) return fmaf(wk, fabsf(d), acc);
+        else if constexpr (PK == kP2) return fmaf(d * d, wk, acc);
+        else if constexpr (PK == kP3) return fmaf(d * d * fabsf(d), wk, acc);
+        else if constexpr (PK == kPInf) return fmaxf(acc, fabsf(d) * wk);
+        else if constexpr (PK == kPNInf) return fminf(acc, fabsf(d) * wk);
+        else return fmaf(exp2f(p * __log2f(fabsf(d))), wk, acc);
+    } else if constexpr (MODE == kCanberra) {
+        const float den = fabsf(a) + fabsf(b);
+        return den != 0.0f ? acc + __fdividef(fabsf(a - b), den) : acc;
+    } else {  // kBrayDen, kPlusSum
+        return acc + fabsf(a + b);
+    }
+}
+
+template <int MODE, int PK>
+__device__ __forceinline__ float fam_init() {
+    if constexpr ((MODE == kWeighted && PK == kPInf)) return -INFINITY;
+    else if constexpr (PK == kPNInf && (MODE == kWeighted || MODE == kSum)) return INFINITY;
+    else return 0.0f;
 }
 
 template <int PK>
@@ -49,12 +92,21 @@ __device__ __forceinline__ float lp_finish(float acc, float inv_p) {
     else return acc;
 }
 
-template <int PK, bool VEC>
+template <int MODE, int PK>
+__device__ __forceinline__ float fam_finish(float acc, float inv_p, float prev) {
+    if constexpr (MODE == kRoot || MODE == kWeighted) return lp_finish<PK>(acc, inv_p);
+    else if constexpr (MODE == kBrayDen) return prev / acc;
+    else return acc;
+}
+
+// w: per-feature weights [batch, d] (kWeighted only).  out: read first under kBrayDen.
+template <int MODE, int PK, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
-    const float *__restrict__ x1, const float *__restrict__ x2, int64_t n, int64_t m, int64_t d,
-    float p, float inv_p, float *__restrict__ out, int64_t tiles_m) {
+    const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
+    int64_t n, int64_t m, int64_t d, float p, float inv_p, float *__restrict__ out) {
     __shared__ float As[kBK][kTile + kPad];
     __shared__ float Bs[kBK][kTile + kPad];
+    __shared__ float Wk[MODE == kWeighted ? kBK : 1];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     const int64_t b = blockIdx.z;
     const int64_t row0 = (int64_t)blockIdx.y * kTile, col0 = (int64_t)blockIdx.x * kTile;
@@ -65,7 +117,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+        for (int j = 0; j < 8; ++j) acc[i][j] = fam_init<MODE, PK>();
 
     // staging: 128 rows x 32 features per operand = 1024 float4, 4 per thread
     auto load = [&](const float *X, int64_t rows, int64_t r0, int64_t k0, floatx4 (&v)[4]) {
@@ -102,6 +154,9 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
                 Bs[4 * c4 + e][r] = pb[q][e];
             }
         }
+        if constexpr (MODE == kWeighted) {
+            if (tid < kBK) Wk[tid] = k0 + tid < d ? w[b * d + k0 + tid] : 0.0f;
+        }
         __syncthreads();
         if (k0 + kBK < d) {
             load(A, n, row0, k0 + kBK, pa);
@@ -113,12 +168,13 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
             const floatx4 a1 = *reinterpret_cast<const floatx4 *>(&As[k][8 * ty + 4]);
             const floatx4 b0 = *reinterpret_cast<const floatx4 *>(&Bs[k][4 * tx]);
             const floatx4 b1 = *reinterpret_cast<const floatx4 *>(&Bs[k][64 + 4 * tx]);
+            const float wk = MODE == kWeighted ? Wk[MODE == kWeighted ? k : 0] : 0.0f;
             const float av[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
             const float bv[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
 #pragma unroll
             for (int i = 0; i < 8; ++i)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[i][j] = lp_step<PK>(acc[i][j], av[i], bv[j], p);
+                for (int j = 0; j < 8; ++j) acc[i][j] = fam_step<MODE, PK>(acc[i][j], av[i], bv[j], wk, p);
         }
         __syncthreads();
     }
@@ -132,9 +188,19 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int64_t col = col0 + 64 * h + 4 * tx;
+            floatx4 prev = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (MODE == kBrayDen) {
+                if (vec_store && col + 3 < m) {
+                    prev = *reinterpret_cast<const floatx4 *>(orow + col);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (col + c < m) prev[c] = orow[col + c];
+                }
+            }
             floatx4 v;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = lp_finish<PK>(acc[i][4 * h + c], inv_p);
+            for (int c = 0; c < 4; ++c) v[c] = fam_finish<MODE, PK>(acc[i][4 * h + c], inv_p, prev[c]);
             if (vec_store && col + 3 < m) {
                 store_nt4(orow + col, v);
             } else {
@@ -182,15 +248,80 @@ __device__ __forceinline__ float grad_term(float d, float w, float dist, float p
     }
 }
 
-// out[(split, b, i, k)] = sum over this split's j of grad_term.  G(b,i,j) and Dist(b,i,j)
-// are read at g[b*n*m + i*gs_i + j*gs_j] (gs = (m, 1) direct, (1, n) transposed).
-template <int PK, bool TR>
+// |d|^e for the general-p formulas (pow of the reference kernels).
+__device__ __forceinline__ float abs_pow(float d, float e) { return exp2f(e * __log2f(fabsf(d))); }
+
+// The two per-pair weights of the backward, from the upstream grad g and the per-pair
+// arrays aux0 / aux1 of each mode:
+//   kRoot     aux0 = dist           w1 = torch's _cdist_backward weight, w2 = dist
+//   kSum      -                     w1 = g
+//   kWeighted aux0 = out = S^(1/p)  w1 = g * S^(1/p - 1) = g * out^(1 - p)
+//   kCanberra -                     w1 = g
+//   kBrayDen  aux0 = out, aux1 = sum |a + b|:  w1 = g / ss, w2 = w1 * out (= g sd / ss^2)
+template <int MODE, int PK>
+__device__ __forceinline__ void pair_weights(float g, float a0, float a1, float p, float &w1,
+                                             float &w2) {
+    w2 = 0.0f;
+    if constexpr (MODE == kRoot) {
+        w1 = pair_weight<PK>(g, a0, p);
+        w2 = a0;
+    } else if constexpr (MODE == kWeighted) {
+        if constexpr (PK == kP1) w1 = g;
+        else if constexpr (PK == kP2) w1 = __fdiv_rn(g, a0);
+        else if constexpr (PK == kP3) w1 = __fdiv_rn(g, a0 * a0);
+        else w1 = g * powf(a0, 1.0f - p);
+    } else if constexpr (MODE == kBrayDen) {
+        w1 = __fdiv_rn(g, a1);
+        w2 = w1 * a0;
+    } else {
+        w1 = g;
+    }
+}
+
+// Per pair-feature contribution to grad of the first operand (a = own value, b = the other
+// operand's), or, under WGRAD, to the weight gradient (before the sum over rows).  The
+// formulas are those of the reference kernels: _ppminkowski (ppminkowski_kernel.cpp:125-160),
+// _wminkowski (wminkowski_kernel.cpp:140-210), _canberra (canberra_kernel.cpp:85-125),
+// _braycurtis (braycurtis_kernel.cpp:108-152).
+template <int MODE, int PK, bool WGRAD>
+__device__ __forceinline__ float fam_term(float a, float b, float w1, float w2, float wk, float p) {
+    const float d = a - b;
+    if constexpr (MODE == kRoot) {
+        return grad_term<PK>(d, w1, w2, p);
+    } else if constexpr (MODE == kSum) {
+        if constexpr (PK == kP1) return signf(d) * w1;
+        else if constexpr (PK == kP2) return 2.0f * d * w1;
+        else if constexpr (PK == kP3) return 3.0f * d * fabsf(d) * w1;
+        else return p * abs_pow(d, p - 1.0f) * signf(d) * w1;
+    } else if constexpr (MODE == kWeighted && !WGRAD) {
+        if constexpr (PK == kP1) return wk * signf(d) * w1;
+        else if constexpr (PK == kP2) return wk * d * w1;
+        else if constexpr (PK == kP3) return wk * d * fabsf(d) * w1;
+        else return wk * abs_pow(d, p - 1.0f) * signf(d) * w1;
+    } else if constexpr (MODE == kWeighted) {
+        if constexpr (PK == kP1) return fabsf(d) * w1;
+        else if constexpr (PK == kP2) return d * d * 0.5f * w1;
+        else if constexpr (PK == kP3) return d * d * fabsf(d) * (1.0f / 3.0f) * w1;
+        else return abs_pow(d, p) / p * w1;
+    } else if constexpr (MODE == kCanberra) {
+        const float nom = fabsf(a) + fabsf(b);
+        return (signf(d) / nom - signf(a) * fabsf(d) / nom / nom) * w1;
+    } else {
+        return w1 * signf(d) - w2 * signf(a + b);
+    }
+}
+
+// out[(split, b, i, k)] = sum over this split's j of fam_term.  G(b,i,j) and the per-pair
+// arrays are read at [b*n*m + i*gs_i + j*gs_j] (gs = (m, 1) direct, (1, n) transposed).
+template <int MODE, int PK, bool TR, bool WGRAD>
 __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
-    const float *__restrict__ g, const float *__restrict__ dist, const float *__restrict__ x1,
-    const float *__restrict__ x2, int64_t n, int64_t m, int64_t d, float p, int64_t j_per_split,
-    int64_t batch, float *__restrict__ out) {
+    const float *__restrict__ g, const float *__restrict__ aux0, const float *__restrict__ aux1,
+    const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
+    int64_t n, int64_t m, int64_t d, float p, int64_t j_per_split, int64_t batch,
+    float *__restrict__ out) {
+    constexpr bool kTwo = (MODE == kRoot && PK == kPInf) || MODE == kBrayDen;
     __shared__ float Ws[kBJ][kBRows + kPad];
-    __shared__ float Ds[PK == kPInf ? kBJ : 1][kBRows + kPad];
+    __shared__ float Ds[kTwo ? kBJ : 1][kBRows + kPad];
     __shared__ float Xs[kBJ][kBFeat + kPad];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     const int64_t split = blockIdx.z / batch, b = blockIdx.z - split * batch;
@@ -198,11 +329,17 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     const int64_t jbeg = split * j_per_split;
     const int64_t jend = jbeg + j_per_split < m ? jbeg + j_per_split : m;
     const float *G = g + b * n * m;
-    const float *Dm = dist + b * n * m;
+    const float *A0 = aux0 ? aux0 + b * n * m : nullptr;
+    const float *A1 = aux1 ? aux1 + b * n * m : nullptr;
     const float *X1 = x1 + b * n * d;
     const float *X2 = x2 + b * m * d;
 
-    float xv[8][4], acc[8][4];
+    float xv[8][4], acc[8][4], wkv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int64_t k = k0 + 4 * tx + c;
+        wkv[c] = (MODE == kWeighted && k < d) ? w[b * d + k] : 0.0f;
+    }
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         const int64_t i = i0 + 8 * ty + r;
@@ -214,37 +351,31 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         }
     }
 
+    auto stage = [&](int ii, int jj, int64_t i, int64_t j) {
+        float w1 = 0.0f, w2 = 0.0f;
+        if (i < n && j < jend) {
+            const int64_t at = TR ? j * n + i : i * m + j;
+            pair_weights<MODE, PK>(G[at], A0 ? A0[at] : 0.0f, A1 ? A1[at] : 0.0f, p, w1, w2);
+        }
+        Ws[jj][ii] = w1;
+        if constexpr (kTwo) Ds[jj][ii] = w2;
+    };
+
     for (int64_t j0 = jbeg; j0 < jend; j0 += kBJ) {
-        // weights: 128 i x 32 j
+        // weights: 128 i x 32 j (coalesced along j, or along i when transposed)
         if constexpr (!TR) {
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int idx = tid + kThreads * q;
                 const int ii = idx >> 5, jj = idx & 31;
-                const int64_t i = i0 + ii, j = j0 + jj;
-                float w = 0.0f, dd = 0.0f;
-                if (i < n && j < jend) {
-                    const float gv = G[i * m + j];
-                    dd = Dm[i * m + j];
-                    w = pair_weight<PK>(gv, dd, p);
-                }
-                Ws[jj][ii] = w;
-                if constexpr (PK == kPInf) Ds[jj][ii] = dd;
+                stage(ii, jj, i0 + ii, j0 + jj);
             }
         } else {
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int idx = tid + kThreads * q;
                 const int jj = idx >> 7, ii = idx & 127;
-                const int64_t i = i0 + ii, j = j0 + jj;
-                float w = 0.0f, dd = 0.0f;
-                if (i < n && j < jend) {
-                    const float gv = G[j * n + i];
-                    dd = Dm[j * n + i];
-                    w = pair_weight<PK>(gv, dd, p);
-                }
-                Ws[jj][ii] = w;
-                if constexpr (PK == kPInf) Ds[jj][ii] = dd;
+                stage(ii, jj, i0 + ii, j0 + jj);
             }
         }
         // x2 panel: 32 j x 64 k
@@ -263,7 +394,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
             const floatx4 x = *reinterpret_cast<const floatx4 *>(&Xs[jj][4 * tx]);
             const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
             float dv[8];
-            if constexpr (PK == kPInf) {
+            if constexpr (kTwo) {
                 const floatx4 d0 = *reinterpret_cast<const floatx4 *>(&Ds[jj][8 * ty]);
                 const floatx4 d1 = *reinterpret_cast<const floatx4 *>(&Ds[jj][8 * ty + 4]);
                 dv[0] = d0[0]; dv[1] = d0[1]; dv[2] = d0[2]; dv[3] = d0[3];
@@ -276,7 +407,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
             for (int r = 0; r < 8; ++r)
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    acc[r][c] += grad_term<PK>(xv[r][c] - x[c], wv[r], dv[r], p);
+                    acc[r][c] += fam_term<MODE, PK, WGRAD>(xv[r][c], x[c], wv[r], dv[r], wkv[c], p);
         }
         __syncthreads();
     }
@@ -303,9 +434,36 @@ __global__ void sum_splits_kernel(const float *__restrict__ part, int64_t splits
     out[t] = s;
 }
 
-__global__ void fill_zero_kernel(float *__restrict__ p, int64_t len) {
+// Column sums of t [batch, n, d] over n, in a fixed order: blocks of 64 columns x 256 rows
+// write partial sums [batch, chunks, d]; column_finish_kernel adds the chunks in order.
+constexpr int kColRows = 256;
+__global__ void column_partial_kernel(const float *__restrict__ t, int64_t n, int64_t d,
+                                      float *__restrict__ part) {
+    __shared__ float red[4][64];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int64_t k = (int64_t)blockIdx.x * 64 + tx, chunk = blockIdx.y, b = blockIdx.z;
+    const int64_t r0 = chunk * kColRows;
+    float s = 0.0f;
+    if (k < d)
+        for (int64_t r = r0 + ty; r < r0 + kColRows && r < n; r += 4) s += t[(b * n + r) * d + k];
+    red[ty][tx] = s;
+    __syncthreads();
+    if (ty == 0 && k < d)
+        part[(b * gridDim.y + chunk) * d + k] = ((red[0][tx] + red[1][tx]) + red[2][tx]) + red[3][tx];
+}
+__global__ void column_finish_kernel(const float *__restrict__ part, int64_t chunks, int64_t d,
+                                     int64_t batch, float *__restrict__ out) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < len) p[t] = 0.0f;
+    if (t >= batch * d) return;
+    const int64_t b = t / d, k = t - b * d;
+    float s = 0.0f;
+    for (int64_t c = 0; c < chunks; ++c) s += part[(b * chunks + c) * d + k];
+    out[t] = s;
+}
+
+__global__ void fill_kernel(float *__restrict__ p, int64_t len, float v) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < len) p[t] = v;
 }
 
 int pkind_of(double p) {
@@ -313,30 +471,48 @@ int pkind_of(double p) {
     if (p == 1.0) return kP1;
     if (p == 2.0) return kP2;
     if (p == 3.0) return kP3;
-    if (isinf(p)) return kPInf;
-    if (p < 2.0) return kPLt2;
+    if (isinf(p)) return p > 0 ? kPInf : kPNInf;
+    if (p > 0.0 && p < 2.0) return kPLt2;
     return kPGen;
 }
 
-template <int PK>
-int launch_forward(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
-                   int64_t d, double p, float *out, hipStream_t s) {
-    const int64_t tiles_m = cdiv(m, kTile);
-    dim3 grid((unsigned)tiles_m, (unsigned)cdiv(n, kTile), (unsigned)batch);
+template <int MODE, int PK>
+int launch_forward(const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
+                   int64_t m, int64_t d, double p, float *out, hipStream_t s) {
+    dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
     const bool vec = (d % 4 == 0) && aligned16(x1) && aligned16(x2) && aligned16(out);
     const float pf = (float)p, inv_p = (float)(1.0 / p);
     if (vec)
-        hipLaunchKernelGGL((lp_forward_kernel<PK, true>), grid, dim3(kThreads), 0, s, x1, x2, n, m,
-                           d, pf, inv_p, out, tiles_m);
+        hipLaunchKernelGGL((lp_forward_kernel<MODE, PK, true>), grid, dim3(kThreads), 0, s, x1, x2,
+                           w, n, m, d, pf, inv_p, out);
     else
-        hipLaunchKernelGGL((lp_forward_kernel<PK, false>), grid, dim3(kThreads), 0, s, x1, x2, n,
-                           m, d, pf, inv_p, out, tiles_m);
+        hipLaunchKernelGGL((lp_forward_kernel<MODE, PK, false>), grid, dim3(kThreads), 0, s, x1,
+                           x2, w, n, m, d, pf, inv_p, out);
     return check_launch("lp_forward_kernel");
 }
 
-}  // namespace
+template <int MODE>
+int dispatch_forward(int pk, const float *x1, const float *x2, const float *w, int64_t batch,
+                     int64_t n, int64_t m, int64_t d, double p, float *out, hipStream_t s) {
+    switch (pk) {
+        case kP0: return launch_forward<MODE, kP0>(x1, x2, w, batch, n, m, d, p, out, s);
+        case kP1: return launch_forward<MODE, kP1>(x1, x2, w, batch, n, m, d, p, out, s);
+        case kP2: return launch_forward<MODE, kP2>(x1, x2, w, batch, n, m, d, p, out, s);
+        case kP3: return launch_forward<MODE, kP3>(x1, x2, w, batch, n, m, d, p, out, s);
+        case kPInf: return launch_forward<MODE, kPInf>(x1, x2, w, batch, n, m, d, p, out, s);
+        case kPNInf: return launch_forward<MODE, kPNInf>(x1, x2, w, batch, n, m, d, p, out, s);
+        case kPLt2: return launch_forward<MODE, kPLt2>(x1, x2, w, batch, n, m, d, p, out, s);
+        default: return launch_forward<MODE, kPGen>(x1, x2, w, batch, n, m, d, p, out, s);
+    }
+}
 
-// Number of j splits used by the backward for these sizes (1 = no partial buffer).
+int fill(float *p, int64_t len, float v, hipStream_t s) {
+    if (len == 0) return TPW_OK;
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)cdiv(len, 256)), dim3(256), 0, s, p, len, v);
+    return check_launch("fill_kernel");
+}
+
+// The per-(split, row, feature) partial sums exceed the output only when j is split.
 int64_t lp_backward_splits(int64_t batch, int64_t n, int64_t m, int64_t d) {
     const int64_t base = cdiv(n, kBRows) * cdiv(d, kBFeat) * batch;
     int64_t splits = cdiv(1024, base);
@@ -348,15 +524,17 @@ int64_t lp_backward_splits(int64_t batch, int64_t n, int64_t m, int64_t d) {
     return splits;
 }
 
-template <int PK, bool TR>
-static int launch_backward(const float *g, const float *dist, const float *x1, const float *x2,
-                           int64_t batch, int64_t n, int64_t m, int64_t d, double p,
-                           float *grad, float *part, int64_t splits, hipStream_t s) {
+// grad [batch, n, d] of the first operand (x2's gradient: pass x2 as x1, n <-> m, TR).
+template <int MODE, int PK, bool TR, bool WGRAD>
+int launch_backward(const float *g, const float *aux0, const float *aux1, const float *x1,
+                    const float *x2, const float *w, int64_t batch, int64_t n, int64_t m, int64_t d,
+                    double p, float *grad, float *part, hipStream_t s) {
+    const int64_t splits = lp_backward_splits(batch, n, m, d);
     const int64_t jps = cdiv(cdiv(m, splits), kBJ) * kBJ;
     dim3 grid((unsigned)cdiv(d, kBFeat), (unsigned)cdiv(n, kBRows), (unsigned)(splits * batch));
     float *dst = splits > 1 ? part : grad;
-    hipLaunchKernelGGL((lp_backward_kernel<PK, TR>), grid, dim3(kThreads), 0, s, g, dist, x1, x2,
-                       n, m, d, (float)p, jps, batch, dst);
+    hipLaunchKernelGGL((lp_backward_kernel<MODE, PK, TR, WGRAD>), grid, dim3(kThreads), 0, s, g,
+                       aux0, aux1, x1, x2, w, n, m, d, (float)p, jps, batch, dst);
     int rc = check_launch("lp_backward_kernel");
     if (rc != TPW_OK || splits == 1) return rc;
     const int64_t len = batch * n * d;
@@ -365,41 +543,77 @@ static int launch_backward(const float *g, const float *dist, const float *x1, c
     return check_launch("sum_splits_kernel");
 }
 
-template <bool TR>
-static int dispatch_backward(int pk, const float *g, const float *dist, const float *x1,
-                             const float *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
-                             double p, float *grad, float *part, int64_t splits, hipStream_t s) {
+template <int MODE, bool TR, bool WGRAD>
+int dispatch_backward(int pk, const float *g, const float *aux0, const float *aux1,
+                      const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
+                      int64_t m, int64_t d, double p, float *grad, float *part, hipStream_t s) {
+#define TPW_BWD(PKV) \
+    return launch_backward<MODE, PKV, TR, WGRAD>(g, aux0, aux1, x1, x2, w, batch, n, m, d, p, grad, part, s)
     switch (pk) {
-        case kP1: return launch_backward<kP1, TR>(g, dist, x1, x2, batch, n, m, d, p, grad, part, splits, s);
-        case kP2: return launch_backward<kP2, TR>(g, dist, x1, x2, batch, n, m, d, p, grad, part, splits, s);
-        case kP3: return launch_backward<kP3, TR>(g, dist, x1, x2, batch, n, m, d, p, grad, part, splits, s);
-        case kPInf: return launch_backward<kPInf, TR>(g, dist, x1, x2, batch, n, m, d, p, grad, part, splits, s);
-        case kPLt2: return launch_backward<kPLt2, TR>(g, dist, x1, x2, batch, n, m, d, p, grad, part, splits, s);
-        default: return launch_backward<kPGen, TR>(g, dist, x1, x2, batch, n, m, d, p, grad, part, splits, s);
+        case kP1: TPW_BWD(kP1);
+        case kP2: TPW_BWD(kP2);
+        case kP3: TPW_BWD(kP3);
+        case kPInf:
+            if constexpr (MODE == kRoot) { TPW_BWD(kPInf); }
+            break;
+        case kPLt2: TPW_BWD(kPLt2);
+        case kPGen: TPW_BWD(kPGen);
+        default: break;
     }
+#undef TPW_BWD
+    set_error("backward for p = %g is not supported by this kernel", p);
+    return TPW_ERR_INVALID;
 }
 
+// Workspace of the family backward: [part | rows x d buffer | column partials | ss].
+struct FamWorkspace {
+    size_t part, rows, cols, ss, total;
+};
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+FamWorkspace fam_workspace(int metric, int64_t batch, int64_t n, int64_t m, int64_t d) {
+    const int64_t s1 = lp_backward_splits(batch, n, m, d), s2 = lp_backward_splits(batch, m, n, d);
+    FamWorkspace w{};
+    const int64_t part1 = s1 > 1 ? s1 * batch * n * d : 0, part2 = s2 > 1 ? s2 * batch * m * d : 0;
+    w.part = align256(sizeof(float) * (size_t)(part1 > part2 ? part1 : part2));
+    if (metric == TPW_FAM_WMINKOWSKI) {
+        w.rows = align256(sizeof(float) * (size_t)(batch * n * d));
+        w.cols = align256(sizeof(float) * (size_t)(batch * cdiv(n, kColRows) * d));
+    }
+    if (metric == TPW_FAM_BRAYCURTIS) w.ss = align256(sizeof(float) * (size_t)(batch * n * m));
+    w.total = w.part + w.rows + w.cols + w.ss;
+    return w;
+}
+
+// Both operand gradients of one mode; pair arrays aux0 / aux1 as pair_weights describes.
+template <int MODE>
+int both_grads(int pk, const float *g, const float *aux0, const float *aux1, const float *x1,
+               const float *x2, const float *w, int64_t batch, int64_t n, int64_t m, int64_t d,
+               double p, float *gx1, float *gx2, float *part, hipStream_t s) {
+    int rc = dispatch_backward<MODE, false, false>(pk, g, aux0, aux1, x1, x2, w, batch, n, m, d, p,
+                                                   gx1, part, s);
+    if (rc != TPW_OK) return rc;
+    return dispatch_backward<MODE, true, false>(pk, g, aux0, aux1, x2, x1, w, batch, m, n, d, p, gx2,
+                                                part, s);
+}
+
+#define TPW_FAM_CHECKS()                                                                     \
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");                   \
+    TPW_REQUIRE(cdiv(n, kTile) <= kMaxGridYZ && cdiv(m, kTile) <= kMaxGridYZ && batch <= kMaxGridYZ, \
+                "too many rows or batches")
+
+}  // namespace
 }  // namespace tpw
 
 using namespace tpw;
 
 extern "C" int tpw_lp_distances(const float *x1, const float *x2, int64_t batch, int64_t n,
                                 int64_t m, int64_t d, double p, float *out, void *stream) {
-    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    TPW_FAM_CHECKS();
     TPW_REQUIRE(p >= 0.0, "p must be non-negative, got %g", p);
-    TPW_REQUIRE(cdiv(n, kTile) <= kMaxGridYZ && batch <= kMaxGridYZ, "too many rows or batches");
     if (batch == 0 || n == 0 || m == 0) return TPW_OK;
     TPW_REQUIRE(x1 && x2 && out, "null pointer");
-    hipStream_t s = as_stream(stream);
-    switch (pkind_of(p)) {
-        case kP0: return launch_forward<kP0>(x1, x2, batch, n, m, d, p, out, s);
-        case kP1: return launch_forward<kP1>(x1, x2, batch, n, m, d, p, out, s);
-        case kP2: return launch_forward<kP2>(x1, x2, batch, n, m, d, p, out, s);
-        case kP3: return launch_forward<kP3>(x1, x2, batch, n, m, d, p, out, s);
-        case kPInf: return launch_forward<kPInf>(x1, x2, batch, n, m, d, p, out, s);
-        case kPLt2: return launch_forward<kPLt2>(x1, x2, batch, n, m, d, p, out, s);
-        default: return launch_forward<kPGen>(x1, x2, batch, n, m, d, p, out, s);
-    }
+    return dispatch_forward<kRoot>(pkind_of(p), x1, x2, nullptr, batch, n, m, d, p, out,
+                                   as_stream(stream));
 }
 
 extern "C" size_t tpw_lp_backward_workspace_size(int64_t batch, int64_t n, int64_t m, int64_t d) {
@@ -417,19 +631,151 @@ extern "C" int tpw_lp_distances_backward(const float *grad, const float *x1, con
     if (batch == 0 || n == 0 || d == 0) return TPW_OK;
     TPW_REQUIRE(grad_x1, "null pointer");
     hipStream_t s = as_stream(stream);
-    const int64_t len = batch * n * d;
-    if (p == 0.0 || m == 0) {  // zero gradient, as _cdist_backward returns for p == 0
-        hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)cdiv(len, 256)), dim3(256), 0, s,
-                           grad_x1, len);
-        return check_launch("fill_zero_kernel");
-    }
+    if (p == 0.0 || m == 0)  // zero gradient, as _cdist_backward returns for p == 0
+        return fill(grad_x1, batch * n * d, 0.0f, s);
     TPW_REQUIRE(grad && x1 && x2 && dist, "null pointer");
-    const int64_t splits = lp_backward_splits(batch, n, m, d);
-    TPW_REQUIRE(splits == 1 || workspace, "workspace of %zu bytes required",
+    TPW_REQUIRE(lp_backward_splits(batch, n, m, d) == 1 || workspace, "workspace of %zu bytes required",
                 tpw_lp_backward_workspace_size(batch, n, m, d));
     float *part = static_cast<float *>(workspace);
     const int pk = pkind_of(p);
     if (transposed)
-        return dispatch_backward<true>(pk, grad, dist, x1, x2, batch, n, m, d, p, grad_x1, part, splits, s);
-    return dispatch_backward<false>(pk, grad, dist, x1, x2, batch, n, m, d, p, grad_x1, part, splits, s);
+        return dispatch_backward<kRoot, true, false>(pk, grad, dist, nullptr, x1, x2, nullptr, batch,
+                                                     n, m, d, p, grad_x1, part, s);
+    return dispatch_backward<kRoot, false, false>(pk, grad, dist, nullptr, x1, x2, nullptr, batch, n,
+                                                  m, d, p, grad_x1, part, s);
+}
+
+// ----------------------------------------------------------------- reference kernel family
+extern "C" int tpw_ppminkowski(const float *x1, const float *x2, int64_t batch, int64_t n,
+                               int64_t m, int64_t d, double p, float *out, void *stream) {
+    TPW_FAM_CHECKS();
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    hipStream_t s = as_stream(stream);
+    if (p == 0.0) return fill(out, batch * n * m, (float)d, s);  // ppminkowski_kernel.cpp:90-91
+    return dispatch_forward<kSum>(pkind_of(p), x1, x2, nullptr, batch, n, m, d, p, out, s);
+}
+
+extern "C" int tpw_wminkowski(const float *x1, const float *x2, const float *w, int64_t batch,
+                              int64_t n, int64_t m, int64_t d, double p, float *out, void *stream) {
+    TPW_FAM_CHECKS();
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && w && out, "null pointer");
+    hipStream_t s = as_stream(stream);
+    if (p == 0.0) return fill(out, batch * n * m, (float)d, s);  // wminkowski_kernel.cpp:101-102
+    return dispatch_forward<kWeighted>(pkind_of(p), x1, x2, w, batch, n, m, d, p, out, s);
+}
+
+extern "C" int tpw_canberra(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                            int64_t d, float *out, void *stream) {
+    TPW_FAM_CHECKS();
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    return launch_forward<kCanberra, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, out, as_stream(stream));
+}
+
+extern "C" int tpw_braycurtis(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                              int64_t d, float *out, void *stream) {
+    TPW_FAM_CHECKS();
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    hipStream_t s = as_stream(stream);
+    const int rc = launch_forward<kRoot, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, out, s);
+    if (rc != TPW_OK) return rc;
+    return launch_forward<kBrayDen, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, out, s);
+}
+
+extern "C" size_t tpw_family_backward_workspace_size(int metric, int64_t batch, int64_t n,
+                                                     int64_t m, int64_t d) {
+    return fam_workspace(metric, batch, n, m, d).total;
+}
+
+#define TPW_FAM_BWD_PROLOGUE(METRIC)                                                          \
+    TPW_FAM_CHECKS();                                                                        \
+    if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;                           \
+    const FamWorkspace lay = fam_workspace(METRIC, batch, n, m, d);                          \
+    TPW_REQUIRE(lay.total == 0 || workspace, "workspace of %zu bytes required", lay.total); \
+    char *ws = static_cast<char *>(workspace);                                               \
+    float *part = reinterpret_cast<float *>(ws);                                             \
+    hipStream_t s = as_stream(stream)
+
+extern "C" int tpw_ppminkowski_backward(const float *grad, const float *x1, const float *x2,
+                                        int64_t batch, int64_t n, int64_t m, int64_t d, double p,
+                                        float *grad_x1, float *grad_x2, void *workspace,
+                                        void *stream) {
+    TPW_FAM_BWD_PROLOGUE(TPW_FAM_PPMINKOWSKI);
+    TPW_REQUIRE(grad_x1 && grad_x2, "null pointer");
+    if (p == 0.0 || n == 0 || m == 0) {  // zero gradients (ppminkowski_kernel.cpp:236)
+        int rc = fill(grad_x1, batch * n * d, 0.0f, s);
+        return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
+    }
+    TPW_REQUIRE(grad && x1 && x2, "null pointer");
+    return both_grads<kSum>(pkind_of(p), grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, p,
+                            grad_x1, grad_x2, part, s);
+}
+
+extern "C" int tpw_wminkowski_backward(const float *grad, const float *x1, const float *x2,
+                                       const float *w, const float *out, int64_t batch, int64_t n,
+                                       int64_t m, int64_t d, double p, float *grad_x1,
+                                       float *grad_x2, float *grad_w, void *workspace,
+                                       void *stream) {
+    TPW_FAM_BWD_PROLOGUE(TPW_FAM_WMINKOWSKI);
+    TPW_REQUIRE(grad_x1 && grad_x2 && grad_w, "null pointer");
+    if (p == 0.0 || n == 0 || m == 0) {  // zero gradients (wminkowski_kernel.cpp:296)
+        int rc = fill(grad_x1, batch * n * d, 0.0f, s);
+        if (rc == TPW_OK) rc = fill(grad_x2, batch * m * d, 0.0f, s);
+        return rc != TPW_OK ? rc : fill(grad_w, batch * d, 0.0f, s);
+    }
+    TPW_REQUIRE(grad && x1 && x2 && w && out, "null pointer");
+    const int pk = pkind_of(p);
+    int rc = both_grads<kWeighted>(pk, grad, out, nullptr, x1, x2, w, batch, n, m, d, p, grad_x1,
+                                   grad_x2, part, s);
+    if (rc != TPW_OK) return rc;
+    float *rows = reinterpret_cast<float *>(ws + lay.part);
+    float *cols = reinterpret_cast<float *>(ws + lay.part + lay.rows);
+    rc = dispatch_backward<kWeighted, false, true>(pk, grad, out, nullptr, x1, x2, w, batch, n, m, d,
+                                                   p, rows, part, s);
+    if (rc != TPW_OK) return rc;
+    const int64_t chunks = cdiv(n, kColRows);
+    hipLaunchKernelGGL(column_partial_kernel, dim3((unsigned)cdiv(d, 64), (unsigned)chunks, (unsigned)batch),
+                       dim3(256), 0, s, rows, n, d, cols);
+    rc = check_launch("column_partial_kernel");
+    if (rc != TPW_OK) return rc;
+    hipLaunchKernelGGL(column_finish_kernel, dim3((unsigned)cdiv(batch * d, 256)), dim3(256), 0, s,
+                       cols, chunks, d, batch, grad_w);
+    return check_launch("column_finish_kernel");
+}
+
+extern "C" int tpw_canberra_backward(const float *grad, const float *x1, const float *x2,
+                                     int64_t batch, int64_t n, int64_t m, int64_t d,
+                                     float *grad_x1, float *grad_x2, void *workspace,
+                                     void *stream) {
+    TPW_FAM_BWD_PROLOGUE(TPW_FAM_CANBERRA);
+    TPW_REQUIRE(grad_x1 && grad_x2, "null pointer");
+    if (n == 0 || m == 0) {
+        int rc = fill(grad_x1, batch * n * d, 0.0f, s);
+        return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
+    }
+    TPW_REQUIRE(grad && x1 && x2, "null pointer");
+    return both_grads<kCanberra>(kP1, grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 1.0,
+                                 grad_x1, grad_x2, part, s);
+}
+
+extern "C" int tpw_braycurtis_backward(const float *grad, const float *x1, const float *x2,
+                                       const float *out, int64_t batch, int64_t n, int64_t m,
+                                       int64_t d, float *grad_x1, float *grad_x2, void *workspace,
+                                       void *stream) {
+    TPW_FAM_BWD_PROLOGUE(TPW_FAM_BRAYCURTIS);
+    TPW_REQUIRE(grad_x1 && grad_x2, "null pointer");
+    if (n == 0 || m == 0) {
+        int rc = fill(grad_x1, batch * n * d, 0.0f, s);
+        return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
+    }
+    TPW_REQUIRE(grad && x1 && x2 && out, "null pointer");
+    // ss = sum_k |a + b| per pair, recomputed as the reference's backward does
+    float *ss = reinterpret_cast<float *>(ws + lay.part + lay.rows + lay.cols);
+    int rc = launch_forward<kPlusSum, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, ss, s);
+    if (rc != TPW_OK) return rc;
+    return both_grads<kBrayDen>(kP1, grad, out, ss, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1,
+                                grad_x2, part, s);
 }

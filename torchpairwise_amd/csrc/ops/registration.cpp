@@ -205,13 +205,9 @@ at::Tensor sigmoid_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> 
 
 at::Tensor sqeuclidean_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs("sqeuclidean_distances", x1, x2);
-    if (hip_float_path(xs.first, xs.second)) {
-        auto ab = broadcast_batch(xs.first, xs.second);
-        return pw_inner(ab.first, ab.second, kSqEuclidean);
-    }
-    // the reference's _ppminkowski(p=2) sums (a - b)^2 directly; ATen's direct p=2 path
-    // (compute_mode 2) computes the same sum, then sqrt, which square() undoes
-    return at::cdist(xs.first, xs.second, 2, 2).square();
+    // pairwise_metrics.cpp:181-188: the direct sum of squared differences (no
+    // |a|^2 + |b|^2 - 2ab cancellation: identical points give exactly 0)
+    return ppminkowski(xs.first, xs.second, 2);
 }
 
 at::Tensor rbf_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
@@ -242,8 +238,35 @@ at::Tensor minkowski_distances(const at::Tensor &x1, const c10::optional<at::Ten
 at::Tensor wminkowski_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2, double p,
                                 const c10::optional<at::Tensor> &w) {
     auto xs = check_pairwise_inputs("wminkowski_distances", x1, x2);
-    if (w.has_value()) not_in_build("wminkowski_distances with weights w");
-    return route_cdist(xs.first, xs.second, p);
+    // pairwise_metrics.cpp:170-179
+    return w.has_value() ? wminkowski(xs.first, xs.second, w.value(), p) : route_cdist(xs.first, xs.second, p);
+}
+
+at::Tensor seuclidean_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
+                                const c10::optional<at::Tensor> &V) {
+    // pairwise_metrics.cpp:245-263 (it checks its inputs under the name euclidean_distances)
+    TORCH_CHECK(!x2.has_value() || V.has_value(), "V is required for seuclidean when x2 is passed.")
+    auto xs = check_pairwise_inputs("euclidean_distances", x1, x2);
+    at::Tensor V_;
+    if (V.has_value()) {
+        V_ = V.value();
+    } else {
+        at::NoGradGuard no_grad_guard;
+        V_ = xs.first.dim() == 2 ? xs.first.var(at::IntArrayRef{0}) : xs.first.var(at::IntArrayRef{0, 1});
+    }
+    // prf_ldiv(V, 1, "identity") = V != 0 ? 1 / V : 1, differentiable as such
+    auto w = V_.masked_fill(V_ == 0, 1).reciprocal();
+    return wminkowski(xs.first, xs.second, w, 2);
+}
+
+at::Tensor braycurtis_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("braycurtis_distances", x1, x2);  // pairwise_metrics.cpp:307-315
+    return braycurtis(xs.first, xs.second);
+}
+
+at::Tensor canberra_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("canberra_distances", x1, x2);  // pairwise_metrics.cpp:316-324
+    return canberra(xs.first, xs.second);
 }
 
 at::Tensor correlation_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
@@ -356,10 +379,7 @@ at::Tensor linf_distances(const at::Tensor &x1, const c10::optional<at::Tensor> 
 at::Tensor haversine_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("haversine_distances"); }
 at::Tensor additive_chi2_kernel(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("additive_chi2_kernel"); }
 at::Tensor chi2_kernel(const at::Tensor &, const c10::optional<at::Tensor> &, double) { not_in_build("chi2_kernel"); }
-at::Tensor seuclidean_distances(const at::Tensor &, const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &) { not_in_build("seuclidean_distances"); }
 at::Tensor mahalanobis_distances(const at::Tensor &, const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &) { not_in_build("mahalanobis_distances"); }
-at::Tensor braycurtis_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("braycurtis_distances"); }
-at::Tensor canberra_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("canberra_distances"); }
 at::Tensor jensenshannon_distances(const at::Tensor &, const c10::optional<at::Tensor> &, c10::optional<double>) { not_in_build("jensenshannon_distances"); }
 at::Tensor snr_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("snr_distances"); }
 

@@ -70,6 +70,11 @@ std::tuple<at::Tensor, at::Tensor> pw_lp_backward(const at::Tensor &grad, const 
 at::Tensor pw_binary_reduce(const char *name, const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor jaccard_fused(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor row_smallest_mask(const at::Tensor &dist, int64_t count);
+// the reference's VALU metric ops (family.cpp)
+at::Tensor ppminkowski(const at::Tensor &x1, const at::Tensor &x2, double p);
+at::Tensor wminkowski(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &w, double p);
+at::Tensor canberra(const at::Tensor &x1, const at::Tensor &x2);
+at::Tensor braycurtis(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor prf_div(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
 std::tuple<at::Tensor, at::Tensor> prf_div_backward(const at::Tensor &g, const at::Tensor &x,
                                                     const at::Tensor &y, c10::string_view mode);

@@ -154,7 +154,8 @@ int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int64_t batch,
 int tpw_lp_distances(const float *x1, const float *x2, int64_t batch, int64_t n,
                      int64_t m, int64_t d, double p, float *out, void *stream);
 
-/* Workspace (bytes) of tpw_lp_distances_backward for these sizes (0 = none). */
+/* Workspace (bytes) of tpw_lp_distances_backward (either direction: the same size serves
+ * the transposed call) and tpw_lp_distances_backward2 for these sizes. */
 size_t tpw_lp_backward_workspace_size(int64_t batch, int64_t n, int64_t m, int64_t d);
 
 /* grad_x1[b,i,k] = sum_j dD[b,i,j]/dx1[b,i,k] * grad[b,i,j] for the Lp distance
@@ -170,6 +171,14 @@ int tpw_lp_distances_backward(const float *grad, const float *x1, const float *x
                               const float *dist, int64_t batch, int64_t n, int64_t m,
                               int64_t d, double p, int transposed, float *grad_x1,
                               void *workspace, void *stream);
+
+/* Both gradients of tpw_lp_distances in one call (grad_x1 [batch,n,d], grad_x2
+ * [batch,m,d]), sharing the per-pair weight pass; same formulas as above.  Replaces the
+ * pair of _cdist_backward calls of derivatives.yaml:1338-1340. */
+int tpw_lp_distances_backward2(const float *grad, const float *x1, const float *x2,
+                               const float *dist, int64_t batch, int64_t n, int64_t m,
+                               int64_t d, double p, float *grad_x1, float *grad_x2,
+                               void *workspace, void *stream);
 
 /* ------------------------------------------------------------------------- */
 /* The reference's own VALU metric kernels (fp32; x1 [batch,n,d], x2 [batch,m,d]) */

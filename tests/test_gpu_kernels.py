@@ -156,16 +156,18 @@ def test_lp_forward(p, B, n, m, d):
 
 
 @pytest.mark.parametrize("p", [1.0, 1.5, 2.0, 3.0, 4.5, float("inf")])
-@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 40, 33, 5)])
-def test_lp_backward(p, B, n, m, d):
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 40, 33, 5), (1, 700, 1100, 70)])
+@pytest.mark.parametrize("entry", ["single", "both"])
+def test_lp_backward(p, B, n, m, d, entry):
+    print(f"lp backward p={p} {B}x{n}x{m}x{d} {entry}", flush=True)
     x1 = (rand(B, n, d, seed=0) * 2 - 1).double().requires_grad_()
     x2 = (rand(B, m, d, seed=1) * 2 - 1).double().requires_grad_()
     g = randn(B, n, m, seed=2).double()
     dist = torch.cdist(x1, x2, p)
     gx1_ref, gx2_ref = torch.autograd.grad(dist, (x1, x2), g)
     dist32 = capi.lp_distances(x1.detach().float().to(DEV), x2.detach().float().to(DEV), p)
-    gx1, gx2 = capi.lp_distances_backward(g.float().to(DEV), x1.detach().float().to(DEV),
-                                          x2.detach().float().to(DEV), dist32, p)
+    fn = capi.lp_distances_backward if entry == "single" else capi.lp_distances_backward2
+    gx1, gx2 = fn(g.float().to(DEV), x1.detach().float().to(DEV), x2.detach().float().to(DEV), dist32, p)
     for got, want, nm in ((gx1, gx1_ref, "grad_x1"), (gx2, gx2_ref, "grad_x2")):
         # sums over up to 200 signed terms: normwise floor 1e-5 * max|grad|
         assert_close(got, want, rtol=1e-4, atol=1e-5 * float(want.abs().max()) + 1e-6,

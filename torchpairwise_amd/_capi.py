@@ -36,6 +36,7 @@ _SIGNATURES = {
     "tpw_lp_distances": (_i, [_p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
     "tpw_lp_backward_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "tpw_lp_distances_backward": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _i, _p, _p, _p]),
+    "tpw_lp_distances_backward2": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p, _p, _p]),
     "tpw_inner_backward_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "tpw_euclidean_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "tpw_sqeuclidean_backward": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
@@ -261,6 +262,24 @@ def lp_distances_backward(grad, x1, x2, dist, p):
          _ptr(gx1), _ptr(ws), _stream())
     call("tpw_lp_distances_backward", _ptr(g), _ptr(b), _ptr(a), _ptr(dd), B, m, n, d, float(p), 1,
          _ptr(gx2), _ptr(ws), _stream())
+    if x1.dim() == 2:
+        return gx1[0], gx2[0]
+    return gx1, gx2
+
+
+def lp_distances_backward2(grad, x1, x2, dist, p):
+    """(grad_x1, grad_x2) of lp_distances from the two-direction entry point."""
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    g, dd = _as3(grad).contiguous(), _as3(dist).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    ws = torch.empty((max(lib().tpw_lp_backward_workspace_size(B, n, m, d), 1),), dtype=torch.uint8,
+                     device=x1.device)
+    call("tpw_lp_distances_backward2", _ptr(g), _ptr(a), _ptr(b), _ptr(dd), B, n, m, d, float(p),
+         _ptr(gx1), _ptr(gx2), _ptr(ws), _stream())
     if x1.dim() == 2:
         return gx1[0], gx2[0]
     return gx1, gx2

@@ -84,6 +84,21 @@ __device__ __forceinline__ float fam_init() {
     else return 0.0f;
 }
 
+// max (min) of acc, |d0|, |d1| in one instruction.  fmaxf compiles to v_max_f32 plus a
+// canonicalising v_max_f32 of |d| in IEEE mode (3 ops per pair-feature); v_max3_f32 with
+// abs input modifiers takes two features per instruction (1.5 ops).  NaN handling is the
+// IEEE maxNum of fmaxf.
+__device__ __forceinline__ float max3_abs(float acc, float d0, float d1) {
+    float r;
+    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(acc), "v"(d0), "v"(d1));
+    return r;
+}
+__device__ __forceinline__ float min3_abs(float acc, float d0, float d1) {
+    float r;
+    asm("v_min3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(acc), "v"(d0), "v"(d1));
+    return r;
+}
+
 template <int PK>
 __device__ __forceinline__ float lp_finish(float acc, float inv_p) {
     if constexpr (PK == kP2) return sqrt_rn(acc);
@@ -163,7 +178,32 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
             load(B, m, col0, k0 + kBK, pb);
         }
         const int kmax = d - k0 < kBK ? (int)(d - k0) : kBK;
-        for (int k = 0; k < kmax; ++k) {
+        int kbeg = 0;
+        if constexpr ((PK == kPInf || PK == kPNInf) && (MODE == kRoot || MODE == kSum)) {
+            for (; kbeg + 1 < kmax; kbeg += 2) {
+                float av[2][8], bv[2][8];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const floatx4 a0 = *reinterpret_cast<const floatx4 *>(&As[kbeg + h][8 * ty]);
+                    const floatx4 a1 = *reinterpret_cast<const floatx4 *>(&As[kbeg + h][8 * ty + 4]);
+                    const floatx4 b0 = *reinterpret_cast<const floatx4 *>(&Bs[kbeg + h][4 * tx]);
+                    const floatx4 b1 = *reinterpret_cast<const floatx4 *>(&Bs[kbeg + h][64 + 4 * tx]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        av[h][e] = a0[e], av[h][4 + e] = a1[e];
+                        bv[h][e] = b0[e], bv[h][4 + e] = b1[e];
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float d0 = av[0][i] - bv[0][j], d1 = av[1][i] - bv[1][j];
+                        acc[i][j] = PK == kPInf ? max3_abs(acc[i][j], d0, d1) : min3_abs(acc[i][j], d0, d1);
+                    }
+            }
+        }
+        for (int k = kbeg; k < kmax; ++k) {
             const floatx4 a0 = *reinterpret_cast<const floatx4 *>(&As[k][8 * ty]);
             const floatx4 a1 = *reinterpret_cast<const floatx4 *>(&As[k][8 * ty + 4]);
             const floatx4 b0 = *reinterpret_cast<const floatx4 *>(&Bs[k][4 * tx]);
@@ -311,9 +351,30 @@ __device__ __forceinline__ float fam_term(float a, float b, float w1, float w2, 
     }
 }
 
+// Whether the per-pair weights are computed once into an [n, m] array before the
+// gradient kernels (they need a second per-pair operand and arithmetic beyond g itself)
+// rather than while staging: staging then reads one array instead of two.
+template <int MODE, int PK>
+constexpr bool kPrecomputed = (MODE == kRoot && (PK == kP2 || PK == kP3 || PK == kPLt2 || PK == kPGen)) ||
+                              (MODE == kWeighted && PK != kP1) || MODE == kBrayDen;
+
+template <int MODE, int PK>
+__global__ void pair_weight_kernel(const float *__restrict__ g, const float *__restrict__ aux0,
+                                   const float *aux1, int64_t len, float p, float *w1,
+                                   float *__restrict__ w2) {
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < len;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        float a, b;
+        pair_weights<MODE, PK>(g[t], aux0[t], aux1 ? aux1[t] : 0.0f, p, a, b);
+        w1[t] = a;  // may alias aux1 (same element)
+        if (w2) w2[t] = b;
+    }
+}
+
 // out[(split, b, i, k)] = sum over this split's j of fam_term.  G(b,i,j) and the per-pair
 // arrays are read at [b*n*m + i*gs_i + j*gs_j] (gs = (m, 1) direct, (1, n) transposed).
-template <int MODE, int PK, bool TR, bool WGRAD>
+// Under PRE, aux0 / aux1 hold the precomputed weights w1 / w2 and g is not read.
+template <int MODE, int PK, bool TR, bool WGRAD, bool PRE>
 __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     const float *__restrict__ g, const float *__restrict__ aux0, const float *__restrict__ aux1,
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
@@ -355,7 +416,12 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         float w1 = 0.0f, w2 = 0.0f;
         if (i < n && j < jend) {
             const int64_t at = TR ? j * n + i : i * m + j;
-            pair_weights<MODE, PK>(G[at], A0 ? A0[at] : 0.0f, A1 ? A1[at] : 0.0f, p, w1, w2);
+            if constexpr (PRE) {
+                w1 = A0[at];
+                if constexpr (kTwo) w2 = A1[at];
+            } else {
+                pair_weights<MODE, PK>(G[at], A0 ? A0[at] : 0.0f, A1 ? A1[at] : 0.0f, p, w1, w2);
+            }
         }
         Ws[jj][ii] = w1;
         if constexpr (kTwo) Ds[jj][ii] = w2;
@@ -512,10 +578,25 @@ int fill(float *p, int64_t len, float v, hipStream_t s) {
     return check_launch("fill_kernel");
 }
 
-// The per-(split, row, feature) partial sums exceed the output only when j is split.
-int64_t lp_backward_splits(int64_t batch, int64_t n, int64_t m, int64_t d) {
+// Blocks of the backward grid per CU that may be resident at once: the kernels use more
+// than 128 VGPRs (at most 4 waves per SIMD, i.e. 4 blocks of 4 waves per CU).
+constexpr int kMaxBlocksPerCU = 4;
+
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 256;
+    return cus;
+}
+
+// Number of j splits for `slots` resident blocks: the (row block, feature block, batch)
+// grid alone fills base blocks; splitting j multiplies that, and a whole number of
+// resident rounds avoids a partly filled last round.  More slots never give fewer splits,
+// so the workspace is sized with the largest slot count.
+int64_t lp_backward_splits(int64_t slots, int64_t batch, int64_t n, int64_t m, int64_t d) {
     const int64_t base = cdiv(n, kBRows) * cdiv(d, kBFeat) * batch;
-    int64_t splits = cdiv(1024, base);
+    int64_t splits = base >= slots ? 1 : slots / base;
     const int64_t max_by_m = cdiv(m, 512);
     if (splits > max_by_m) splits = max_by_m;
     if (splits > 16) splits = 16;
@@ -523,18 +604,24 @@ int64_t lp_backward_splits(int64_t batch, int64_t n, int64_t m, int64_t d) {
     while (splits > 1 && splits * batch > kMaxGridYZ) --splits;
     return splits;
 }
+int64_t max_slots() { return (int64_t)device_cus() * kMaxBlocksPerCU; }
 
 // grad [batch, n, d] of the first operand (x2's gradient: pass x2 as x1, n <-> m, TR).
-template <int MODE, int PK, bool TR, bool WGRAD>
+template <int MODE, int PK, bool TR, bool WGRAD, bool PRE>
 int launch_backward(const float *g, const float *aux0, const float *aux1, const float *x1,
                     const float *x2, const float *w, int64_t batch, int64_t n, int64_t m, int64_t d,
                     double p, float *grad, float *part, hipStream_t s) {
-    const int64_t splits = lp_backward_splits(batch, n, m, d);
+    auto kern = lp_backward_kernel<MODE, PK, TR, WGRAD, PRE>;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, 0) != hipSuccess || per_cu <= 0)
+        per_cu = 2;
+    if (per_cu > kMaxBlocksPerCU) per_cu = kMaxBlocksPerCU;
+    const int64_t splits = lp_backward_splits((int64_t)device_cus() * per_cu, batch, n, m, d);
     const int64_t jps = cdiv(cdiv(m, splits), kBJ) * kBJ;
     dim3 grid((unsigned)cdiv(d, kBFeat), (unsigned)cdiv(n, kBRows), (unsigned)(splits * batch));
     float *dst = splits > 1 ? part : grad;
-    hipLaunchKernelGGL((lp_backward_kernel<MODE, PK, TR, WGRAD>), grid, dim3(kThreads), 0, s, g,
-                       aux0, aux1, x1, x2, w, n, m, d, (float)p, jps, batch, dst);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s, g, aux0, aux1, x1, x2, w, n, m, d, (float)p,
+                       jps, batch, dst);
     int rc = check_launch("lp_backward_kernel");
     if (rc != TPW_OK || splits == 1) return rc;
     const int64_t len = batch * n * d;
@@ -543,58 +630,102 @@ int launch_backward(const float *g, const float *aux0, const float *aux1, const 
     return check_launch("sum_splits_kernel");
 }
 
-template <int MODE, bool TR, bool WGRAD>
-int dispatch_backward(int pk, const float *g, const float *aux0, const float *aux1,
-                      const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
-                      int64_t m, int64_t d, double p, float *grad, float *part, hipStream_t s) {
-#define TPW_BWD(PKV) \
-    return launch_backward<MODE, PKV, TR, WGRAD>(g, aux0, aux1, x1, x2, w, batch, n, m, d, p, grad, part, s)
+// Per-pair weights into w1 (and w2), for the kPrecomputed cases.
+template <int MODE, int PK>
+int launch_pair_weights(const float *g, const float *aux0, const float *aux1, int64_t len,
+                        double p, float *w1, float *w2, hipStream_t s) {
+    const unsigned grid = (unsigned)(cdiv(len, 256) < 16384 ? cdiv(len, 256) : 16384);
+    hipLaunchKernelGGL((pair_weight_kernel<MODE, PK>), dim3(grid), dim3(256), 0, s, g, aux0, aux1,
+                       len, (float)p, w1, w2);
+    return check_launch("pair_weight_kernel");
+}
+
+// The gradient of the first operand and/or (TWO) of the second, and/or (WG) the row
+// partials of the weight gradient, sharing one weight precomputation.  wbuf1 / wbuf2
+// receive the precomputed weights ([batch, n, m] each) where the case uses them.
+struct BwdJob {
+    const float *g, *aux0, *aux1, *x1, *x2, *w;
+    int64_t batch, n, m, d;
+    double p;
+    float *gx1, *gx2, *rows, *part, *wbuf1, *wbuf2;
+    bool x1_transposed;  // single-direction call for x2's gradient (x1/x2 already swapped)
+};
+
+template <int MODE, int PK>
+int run_backward(const BwdJob &j, hipStream_t s) {
+    constexpr bool PRE = kPrecomputed<MODE, PK>;
+    // staging reads the per-pair arrays only where the weights need them
+    constexpr bool kAux = PRE || (MODE == kRoot && PK == kPInf);
+    const float *a0 = kAux ? j.aux0 : nullptr, *a1 = kAux ? j.aux1 : nullptr;
+    if constexpr (PRE) {
+        constexpr bool two = MODE == kBrayDen;
+        const int rc = launch_pair_weights<MODE, PK>(j.g, j.aux0, j.aux1, j.batch * j.n * j.m, j.p,
+                                                     j.wbuf1, two ? j.wbuf2 : nullptr, s);
+        if (rc != TPW_OK) return rc;
+        a0 = j.wbuf1;
+        a1 = two ? j.wbuf2 : nullptr;
+    }
+    int rc = TPW_OK;
+    if (j.gx1) {
+        if (j.x1_transposed)  // n, m are already those of the operand whose grad is wanted
+            rc = launch_backward<MODE, PK, true, false, PRE>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
+                                                              j.m, j.d, j.p, j.gx1, j.part, s);
+        else
+            rc = launch_backward<MODE, PK, false, false, PRE>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
+                                                               j.m, j.d, j.p, j.gx1, j.part, s);
+    }
+    if (rc == TPW_OK && j.gx2)
+        rc = launch_backward<MODE, PK, true, false, PRE>(j.g, a0, a1, j.x2, j.x1, j.w, j.batch, j.m, j.n,
+                                                          j.d, j.p, j.gx2, j.part, s);
+    if constexpr (MODE == kWeighted) {
+        if (rc == TPW_OK && j.rows)
+            rc = launch_backward<MODE, PK, false, true, PRE>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
+                                                              j.m, j.d, j.p, j.rows, j.part, s);
+    }
+    return rc;
+}
+
+template <int MODE>
+int dispatch_backward(int pk, const BwdJob &j, hipStream_t s) {
     switch (pk) {
-        case kP1: TPW_BWD(kP1);
-        case kP2: TPW_BWD(kP2);
-        case kP3: TPW_BWD(kP3);
+        case kP1: return run_backward<MODE, kP1>(j, s);
+        case kP2: return run_backward<MODE, kP2>(j, s);
+        case kP3: return run_backward<MODE, kP3>(j, s);
         case kPInf:
-            if constexpr (MODE == kRoot) { TPW_BWD(kPInf); }
+            if constexpr (MODE == kRoot) return run_backward<MODE, kPInf>(j, s);
             break;
-        case kPLt2: TPW_BWD(kPLt2);
-        case kPGen: TPW_BWD(kPGen);
+        case kPLt2: return run_backward<MODE, kPLt2>(j, s);
+        case kPGen: return run_backward<MODE, kPGen>(j, s);
         default: break;
     }
-#undef TPW_BWD
-    set_error("backward for p = %g is not supported by this kernel", p);
+    set_error("backward for p = %g is not supported by this kernel", j.p);
     return TPW_ERR_INVALID;
 }
 
-// Workspace of the family backward: [part | rows x d buffer | column partials | ss].
-struct FamWorkspace {
-    size_t part, rows, cols, ss, total;
+// Workspace of the backward: [split partials | weight gradient rows | column partials |
+// pair buffer 1 | pair buffer 2].  Pair buffers hold the precomputed weights (and, for
+// Bray-Curtis, the denominator that buffer 1 is computed from in place).
+struct Workspace {
+    size_t part, rows, cols, pair1, pair2, total;
 };
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
-FamWorkspace fam_workspace(int metric, int64_t batch, int64_t n, int64_t m, int64_t d) {
-    const int64_t s1 = lp_backward_splits(batch, n, m, d), s2 = lp_backward_splits(batch, m, n, d);
-    FamWorkspace w{};
+Workspace workspace_layout(int metric, int64_t batch, int64_t n, int64_t m, int64_t d) {
+    const int64_t slots = max_slots();
+    const int64_t s1 = lp_backward_splits(slots, batch, n, m, d), s2 = lp_backward_splits(slots, batch, m, n, d);
+    Workspace w{};
     const int64_t part1 = s1 > 1 ? s1 * batch * n * d : 0, part2 = s2 > 1 ? s2 * batch * m * d : 0;
     w.part = align256(sizeof(float) * (size_t)(part1 > part2 ? part1 : part2));
+    const size_t pair = align256(sizeof(float) * (size_t)(batch * n * m));
     if (metric == TPW_FAM_WMINKOWSKI) {
         w.rows = align256(sizeof(float) * (size_t)(batch * n * d));
         w.cols = align256(sizeof(float) * (size_t)(batch * cdiv(n, kColRows) * d));
     }
-    if (metric == TPW_FAM_BRAYCURTIS) w.ss = align256(sizeof(float) * (size_t)(batch * n * m));
-    w.total = w.part + w.rows + w.cols + w.ss;
+    if (metric == TPW_FAM_WMINKOWSKI || metric == TPW_FAM_BRAYCURTIS || metric < 0) w.pair1 = pair;
+    if (metric == TPW_FAM_BRAYCURTIS) w.pair2 = pair;
+    w.total = w.part + w.rows + w.cols + w.pair1 + w.pair2;
     return w;
 }
-
-// Both operand gradients of one mode; pair arrays aux0 / aux1 as pair_weights describes.
-template <int MODE>
-int both_grads(int pk, const float *g, const float *aux0, const float *aux1, const float *x1,
-               const float *x2, const float *w, int64_t batch, int64_t n, int64_t m, int64_t d,
-               double p, float *gx1, float *gx2, float *part, hipStream_t s) {
-    int rc = dispatch_backward<MODE, false, false>(pk, g, aux0, aux1, x1, x2, w, batch, n, m, d, p,
-                                                   gx1, part, s);
-    if (rc != TPW_OK) return rc;
-    return dispatch_backward<MODE, true, false>(pk, g, aux0, aux1, x2, x1, w, batch, m, n, d, p, gx2,
-                                                part, s);
-}
+constexpr int kLpMetric = -1;  // the Minkowski (cdist) backward in workspace_layout
 
 #define TPW_FAM_CHECKS()                                                                     \
     TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");                   \
@@ -617,8 +748,7 @@ extern "C" int tpw_lp_distances(const float *x1, const float *x2, int64_t batch,
 }
 
 extern "C" size_t tpw_lp_backward_workspace_size(int64_t batch, int64_t n, int64_t m, int64_t d) {
-    const int64_t splits = lp_backward_splits(batch, n, m, d);
-    return splits > 1 ? (size_t)(splits * batch * n * d) * sizeof(float) : 0;
+    return workspace_layout(kLpMetric, batch, n, m, d).total;
 }
 
 extern "C" int tpw_lp_distances_backward(const float *grad, const float *x1, const float *x2,
@@ -634,15 +764,37 @@ extern "C" int tpw_lp_distances_backward(const float *grad, const float *x1, con
     if (p == 0.0 || m == 0)  // zero gradient, as _cdist_backward returns for p == 0
         return fill(grad_x1, batch * n * d, 0.0f, s);
     TPW_REQUIRE(grad && x1 && x2 && dist, "null pointer");
-    TPW_REQUIRE(lp_backward_splits(batch, n, m, d) == 1 || workspace, "workspace of %zu bytes required",
-                tpw_lp_backward_workspace_size(batch, n, m, d));
-    float *part = static_cast<float *>(workspace);
-    const int pk = pkind_of(p);
-    if (transposed)
-        return dispatch_backward<kRoot, true, false>(pk, grad, dist, nullptr, x1, x2, nullptr, batch,
-                                                     n, m, d, p, grad_x1, part, s);
-    return dispatch_backward<kRoot, false, false>(pk, grad, dist, nullptr, x1, x2, nullptr, batch, n,
-                                                  m, d, p, grad_x1, part, s);
+    const Workspace lay = workspace_layout(kLpMetric, batch, n, m, d);
+    TPW_REQUIRE(workspace, "workspace of %zu bytes required", lay.total);
+    char *ws = static_cast<char *>(workspace);
+    BwdJob j{grad, dist, nullptr, x1, x2, nullptr, batch, n, m, d, p, grad_x1, nullptr, nullptr,
+             reinterpret_cast<float *>(ws), reinterpret_cast<float *>(ws + lay.part + lay.rows + lay.cols),
+             nullptr, transposed != 0};
+    return dispatch_backward<kRoot>(pkind_of(p), j, s);
+}
+
+extern "C" int tpw_lp_distances_backward2(const float *grad, const float *x1, const float *x2,
+                                          const float *dist, int64_t batch, int64_t n, int64_t m,
+                                          int64_t d, double p, float *grad_x1, float *grad_x2,
+                                          void *workspace, void *stream) {
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    TPW_REQUIRE(p >= 0.0, "p must be non-negative, got %g", p);
+    TPW_REQUIRE(cdiv(n, kBRows) <= kMaxGridYZ && cdiv(m, kBRows) <= kMaxGridYZ, "too many rows");
+    if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    TPW_REQUIRE(grad_x1 && grad_x2, "null pointer");
+    hipStream_t s = as_stream(stream);
+    if (p == 0.0 || n == 0 || m == 0) {
+        const int rc = fill(grad_x1, batch * n * d, 0.0f, s);
+        return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
+    }
+    TPW_REQUIRE(grad && x1 && x2 && dist, "null pointer");
+    const Workspace lay = workspace_layout(kLpMetric, batch, n, m, d);
+    TPW_REQUIRE(workspace, "workspace of %zu bytes required", lay.total);
+    char *ws = static_cast<char *>(workspace);
+    BwdJob j{grad, dist, nullptr, x1, x2, nullptr, batch, n, m, d, p, grad_x1, grad_x2, nullptr,
+             reinterpret_cast<float *>(ws), reinterpret_cast<float *>(ws + lay.part + lay.rows + lay.cols),
+             nullptr, false};
+    return dispatch_backward<kRoot>(pkind_of(p), j, s);
 }
 
 // ----------------------------------------------------------------- reference kernel family
@@ -687,16 +839,21 @@ extern "C" int tpw_braycurtis(const float *x1, const float *x2, int64_t batch, i
 
 extern "C" size_t tpw_family_backward_workspace_size(int metric, int64_t batch, int64_t n,
                                                      int64_t m, int64_t d) {
-    return fam_workspace(metric, batch, n, m, d).total;
+    return workspace_layout(metric, batch, n, m, d).total;
 }
 
 #define TPW_FAM_BWD_PROLOGUE(METRIC)                                                          \
     TPW_FAM_CHECKS();                                                                        \
     if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;                           \
-    const FamWorkspace lay = fam_workspace(METRIC, batch, n, m, d);                          \
+    const Workspace lay = workspace_layout(METRIC, batch, n, m, d);                          \
     TPW_REQUIRE(lay.total == 0 || workspace, "workspace of %zu bytes required", lay.total); \
     char *ws = static_cast<char *>(workspace);                                               \
     float *part = reinterpret_cast<float *>(ws);                                             \
+    float *rows = reinterpret_cast<float *>(ws + lay.part);                                  \
+    float *cols = reinterpret_cast<float *>(ws + lay.part + lay.rows);                       \
+    float *pair1 = reinterpret_cast<float *>(ws + lay.part + lay.rows + lay.cols);           \
+    float *pair2 = reinterpret_cast<float *>(ws + lay.part + lay.rows + lay.cols + lay.pair1); \
+    (void)rows, (void)cols, (void)pair1, (void)pair2;                                        \
     hipStream_t s = as_stream(stream)
 
 extern "C" int tpw_ppminkowski_backward(const float *grad, const float *x1, const float *x2,
@@ -710,8 +867,9 @@ extern "C" int tpw_ppminkowski_backward(const float *grad, const float *x1, cons
         return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
     }
     TPW_REQUIRE(grad && x1 && x2, "null pointer");
-    return both_grads<kSum>(pkind_of(p), grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, p,
-                            grad_x1, grad_x2, part, s);
+    BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, p, grad_x1, grad_x2, nullptr,
+             part, nullptr, nullptr, false};
+    return dispatch_backward<kSum>(pkind_of(p), j, s);
 }
 
 extern "C" int tpw_wminkowski_backward(const float *grad, const float *x1, const float *x2,
@@ -727,14 +885,9 @@ extern "C" int tpw_wminkowski_backward(const float *grad, const float *x1, const
         return rc != TPW_OK ? rc : fill(grad_w, batch * d, 0.0f, s);
     }
     TPW_REQUIRE(grad && x1 && x2 && w && out, "null pointer");
-    const int pk = pkind_of(p);
-    int rc = both_grads<kWeighted>(pk, grad, out, nullptr, x1, x2, w, batch, n, m, d, p, grad_x1,
-                                   grad_x2, part, s);
-    if (rc != TPW_OK) return rc;
-    float *rows = reinterpret_cast<float *>(ws + lay.part);
-    float *cols = reinterpret_cast<float *>(ws + lay.part + lay.rows);
-    rc = dispatch_backward<kWeighted, false, true>(pk, grad, out, nullptr, x1, x2, w, batch, n, m, d,
-                                                   p, rows, part, s);
+    BwdJob j{grad, out, nullptr, x1, x2, w, batch, n, m, d, p, grad_x1, grad_x2, rows, part, pair1,
+             nullptr, false};
+    int rc = dispatch_backward<kWeighted>(pkind_of(p), j, s);
     if (rc != TPW_OK) return rc;
     const int64_t chunks = cdiv(n, kColRows);
     hipLaunchKernelGGL(column_partial_kernel, dim3((unsigned)cdiv(d, 64), (unsigned)chunks, (unsigned)batch),
@@ -757,8 +910,9 @@ extern "C" int tpw_canberra_backward(const float *grad, const float *x1, const f
         return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
     }
     TPW_REQUIRE(grad && x1 && x2, "null pointer");
-    return both_grads<kCanberra>(kP1, grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 1.0,
-                                 grad_x1, grad_x2, part, s);
+    BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1, grad_x2, nullptr,
+             part, nullptr, nullptr, false};
+    return dispatch_backward<kCanberra>(kP1, j, s);
 }
 
 extern "C" int tpw_braycurtis_backward(const float *grad, const float *x1, const float *x2,
@@ -772,10 +926,11 @@ extern "C" int tpw_braycurtis_backward(const float *grad, const float *x1, const
         return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
     }
     TPW_REQUIRE(grad && x1 && x2 && out, "null pointer");
-    // ss = sum_k |a + b| per pair, recomputed as the reference's backward does
-    float *ss = reinterpret_cast<float *>(ws + lay.part + lay.rows + lay.cols);
-    int rc = launch_forward<kPlusSum, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, ss, s);
+    // ss = sum_k |a + b| per pair into pair buffer 1, recomputed as the reference's backward
+    // does; the weights then overwrite it in place (w1) and fill pair buffer 2 (w2)
+    int rc = launch_forward<kPlusSum, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, pair1, s);
     if (rc != TPW_OK) return rc;
-    return both_grads<kBrayDen>(kP1, grad, out, ss, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1,
-                                grad_x2, part, s);
+    BwdJob j{grad, out, pair1, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1, grad_x2, nullptr, part,
+             pair1, pair2, false};
+    return dispatch_backward<kBrayDen>(kP1, j, s);
 }

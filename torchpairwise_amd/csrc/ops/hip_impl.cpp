@@ -118,18 +118,11 @@ std::tuple<at::Tensor, at::Tensor> pw_lp_backward_cuda(const at::Tensor &grad, c
     auto g = grad.to(at::kFloat).reshape({B, n, m}).contiguous();
     auto dd = dist.reshape({B, n, m}).contiguous();
     auto gx1 = at::empty_like(a), gx2 = at::empty_like(b);
-    const size_t w1 = tpw_lp_backward_workspace_size(B, n, m, d);
-    const size_t w2 = tpw_lp_backward_workspace_size(B, m, n, d);
-    auto ws = workspace(std::max(w1, w2), a);
-    void *s = current_stream();
-    check_rc(tpw_lp_distances_backward(g.data_ptr<float>(), a.data_ptr<float>(), b.data_ptr<float>(),
-                                       dd.data_ptr<float>(), B, n, m, d, p, 0, gx1.data_ptr<float>(),
-                                       ws.data_ptr(), s),
-             "_pw_lp_backward x1");
-    check_rc(tpw_lp_distances_backward(g.data_ptr<float>(), b.data_ptr<float>(), a.data_ptr<float>(),
-                                       dd.data_ptr<float>(), B, m, n, d, p, 1, gx2.data_ptr<float>(),
-                                       ws.data_ptr(), s),
-             "_pw_lp_backward x2");
+    auto ws = workspace(tpw_lp_backward_workspace_size(B, n, m, d), a);
+    check_rc(tpw_lp_distances_backward2(g.data_ptr<float>(), a.data_ptr<float>(), b.data_ptr<float>(),
+                                        dd.data_ptr<float>(), B, n, m, d, p, gx1.data_ptr<float>(),
+                                        gx2.data_ptr<float>(), ws.data_ptr(), current_stream()),
+             "_pw_lp_backward");
     return {gx1.reshape(x1.sizes()), gx2.reshape(x2.sizes())};
 }
 

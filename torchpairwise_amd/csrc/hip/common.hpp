@@ -55,6 +55,11 @@ __device__ __forceinline__ void from_f32(uint16_t *p, float v) { *p = f32_to_bf1
 int inner_dot_f32(const void *x1, const void *x2, int dtype, int64_t batch, int64_t n, int64_t m,
                   int64_t d, float *out, hipStream_t s);
 
+// out[b] = sign * (A[b] . B[b]^T) + coef[b*M + row] * X[b][row][col] on the matrix cores,
+// A [batch, M, K], B [batch, N, K], X and out [batch, M, N] of type dtype (inner.hip).
+int inner_grad_gemm(const void *A, const void *B, int dtype, int64_t batch, int64_t M, int64_t N,
+                    int64_t K, float sign, const float *coef, const void *X, void *out, hipStream_t s);
+
 }  // namespace tpw
 
 #define TPW_REQUIRE(cond, ...)          \

@@ -42,9 +42,13 @@ struct Elem<uint16_t> {  // bf16 bits
     static constexpr int kChunk = 64;
 };
 
+// Gradient products of the backward (not a public epilogue code): out = sign * s +
+// aux1[row] * X[row, col], X having the output's type and shape.
+constexpr int kEpiGrad = 100;
+
 template <int EPI>
 __device__ __forceinline__ float epilogue(float s, float a1, float a2) {
-    if constexpr (EPI == TPW_EPI_DOT) {
+    if constexpr (EPI == TPW_EPI_DOT || EPI == kEpiGrad) {
         return s;
     } else if constexpr (EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN) {
         float v = (a1 + a2) - 2.0f * s;
@@ -150,7 +154,7 @@ template <typename T, typename OutT, int EPI, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
     const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
-    int64_t tiles_n, int64_t tiles_m, int64_t total) {
+    int64_t tiles_n, int64_t tiles_m, int64_t total, const OutT *__restrict__ X, float sign) {
     // operand panels (As, Bs); after the K loop the same bytes stage the fp32 output
     __shared__ uint4 smem[2 * kTile * kLdsStride];
     uint4 *As = smem;
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     if constexpr (EPI != TPW_EPI_DOT) {
         const int i = tid & (kTile - 1);
         if (tid < kTile) s_aux[0][i] = row0 + i < n ? aux1[b * n + row0 + i] : 0.0f;
-        else s_aux[1][i] = col0 + i < m ? aux2[b * m + col0 + i] : 0.0f;
+        else if (EPI != kEpiGrad) s_aux[1][i] = col0 + i < m ? aux2[b * m + col0 + i] : 0.0f;
     }
 
     floatx16 acc[2][2];
@@ -233,12 +237,16 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     const bool full = row0 + kTile <= n && col0 + kTile <= m;
     float a2v[2];
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) a2v[ni] = EPI != TPW_EPI_DOT ? s_aux[1][wc + ni * 32 + l32] : 0.0f;
-    if constexpr (sizeof(OutT) == 4) {
-        if (full) {
-            // fp32 full tile: each wave stages a 32 x 64 half of its tile in its own LDS slice
-            // (the operand panels are free after the K loop's last barrier) and writes it back
-            // as float4 rows, 16 lanes per 256-byte row segment.
+    for (int ni = 0; ni < 2; ++ni)
+        a2v[ni] = (EPI != TPW_EPI_DOT && EPI != kEpiGrad) ? s_aux[1][wc + ni * 32 + l32] : 0.0f;
+    // bf16 rows are written 8 values (16 bytes) per lane: needs m % 8 == 0 for alignment
+    const bool staged = full && (sizeof(OutT) == 4 || m % 8 == 0);
+    {
+        if (staged) {
+            // full tile: each wave stages a 32 x 64 half of its tile in fp32 in its own LDS
+            // slice (the operand panels are free after the K loop's last barrier) and writes
+            // it back in row segments: fp32 as float4 (16 lanes per 256-byte segment), bf16
+            // as 8 rounded values per lane (8 lanes per 128-byte segment).
             float *stage = reinterpret_cast<float *>(smem) + wave * (32 * kStageStride);
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi) {
@@ -248,16 +256,52 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
                     for (int r = 0; r < 16; ++r) {
                         const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
                         const float a1 = EPI != TPW_EPI_DOT ? s_aux[0][wr + mi * 32 + rr] : 0.0f;
-                        stage[rr * kStageStride + ni * 32 + l32] = epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni]);
+                        stage[rr * kStageStride + ni * 32 + l32] =
+                            EPI == kEpiGrad ? sign * acc[mi][ni][r] : epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni]);
                     }
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
                 __builtin_amdgcn_wave_barrier();
-                float *orow = reinterpret_cast<float *>(out) + (b * n + row0 + wr + mi * 32) * m + col0 + wc;
+                const int64_t ooff = (b * n + row0 + wr + mi * 32) * m + col0 + wc;
+                OutT *orow = out + ooff;
+                if constexpr (sizeof(OutT) == 4) {
 #pragma unroll
-                for (int it = 0; it < 8; ++it) {
-                    const int rr = it * 4 + (lane >> 4), cc = (lane & 15) * 4;
-                    const floatx4 v = *reinterpret_cast<const floatx4 *>(&stage[rr * kStageStride + cc]);
-                    store_nt4(orow + (int64_t)rr * m + cc, v);
+                    for (int it = 0; it < 8; ++it) {
+                        const int rr = it * 4 + (lane >> 4), cc = (lane & 15) * 4;
+                        floatx4 v = *reinterpret_cast<const floatx4 *>(&stage[rr * kStageStride + cc]);
+                        if constexpr (EPI == kEpiGrad) {
+                            const float c = s_aux[0][wr + mi * 32 + rr];
+                            const floatx4 xv = *reinterpret_cast<const floatx4 *>(
+                                reinterpret_cast<const float *>(X) + ooff + (int64_t)rr * m + cc);
+                            v += c * xv;
+                        }
+                        store_nt4(reinterpret_cast<float *>(orow) + (int64_t)rr * m + cc, v);
+                    }
+                } else {
+#pragma unroll
+                    for (int it = 0; it < 4; ++it) {
+                        const int rr = it * 8 + (lane >> 3), cc = (lane & 7) * 8;
+                        floatx4 v0 = *reinterpret_cast<const floatx4 *>(&stage[rr * kStageStride + cc]);
+                        floatx4 v1 = *reinterpret_cast<const floatx4 *>(&stage[rr * kStageStride + cc + 4]);
+                        if constexpr (EPI == kEpiGrad) {
+                            const float c = s_aux[0][wr + mi * 32 + rr];
+                            const uint4 xq = *reinterpret_cast<const uint4 *>(X + ooff + (int64_t)rr * m + cc);
+                            const uint32_t xw[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+                            for (int e = 0; e < 2; ++e) {
+                                v0[2 * e] += c * __uint_as_float(xw[e] << 16);
+                                v0[2 * e + 1] += c * __uint_as_float(xw[e] & 0xffff0000u);
+                                v1[2 * e] += c * __uint_as_float(xw[2 + e] << 16);
+                                v1[2 * e + 1] += c * __uint_as_float(xw[2 + e] & 0xffff0000u);
+                            }
+                        }
+                        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                        u32x4 q;
+                        q[0] = f32_to_bf16_rne(v0[0]) | ((uint32_t)f32_to_bf16_rne(v0[1]) << 16);
+                        q[1] = f32_to_bf16_rne(v0[2]) | ((uint32_t)f32_to_bf16_rne(v0[3]) << 16);
+                        q[2] = f32_to_bf16_rne(v1[0]) | ((uint32_t)f32_to_bf16_rne(v1[1]) << 16);
+                        q[3] = f32_to_bf16_rne(v1[2]) | ((uint32_t)f32_to_bf16_rne(v1[3]) << 16);
+                        __builtin_nontemporal_store(q, reinterpret_cast<u32x4 *>(orow + (int64_t)rr * m + cc));
+                    }
                 }
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the slice is rewritten
                 __builtin_amdgcn_wave_barrier();
@@ -275,9 +319,11 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
             for (int r = 0; r < 16; ++r) {
                 const int rr = mi * 32 + 8 * (r >> 2) + (r & 3);  // row in the wave tile, less 4 h
                 const float a1 = EPI != TPW_EPI_DOT ? s_aux[0][wr + 4 * h + rr] : 0.0f;
-                const float v = epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni]);
-                if (full || (row0 + wr + 4 * h + rr < n && col_ok))
+                if (full || (row0 + wr + 4 * h + rr < n && col_ok)) {
+                    float v = epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni]);
+                    if constexpr (EPI == kEpiGrad) v = sign * v + a1 * to_f32(X[(obase - out) + rr * m + ni * 32]);
                     store_out(obase + rr * m + ni * 32, v);
+                }
             }
         }
     }
@@ -305,13 +351,14 @@ __global__ void row_norms_kernel(const T *__restrict__ x, int64_t rows, int64_t 
 
 template <typename T, int EPI, typename OutT = T>
 int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
-                 const float *aux1, const float *aux2, OutT *out, hipStream_t s) {
+                 const float *aux1, const float *aux2, OutT *out, hipStream_t s,
+                 const OutT *X = nullptr, float sign = 1.0f) {
     const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
     const int64_t total = tiles_n * tiles_m * batch;
     const bool vec = ((d * (int64_t)sizeof(T)) % 16 == 0) && aligned16(x1) && aligned16(x2);
     auto kernel = vec ? pairwise_inner_kernel<T, OutT, EPI, true> : pairwise_inner_kernel<T, OutT, EPI, false>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(kThreads), 0, s, x1, x2, n, m, d, aux1,
-                       aux2, out, tiles_n, tiles_m, total);
+                       aux2, out, tiles_n, tiles_m, total, X, sign);
     return check_launch("pairwise_inner_kernel");
 }
 
@@ -339,6 +386,19 @@ int inner_dot_f32(const void *x1, const void *x2, int dtype, int64_t batch, int6
     return launch_inner<uint16_t, TPW_EPI_DOT, float>(static_cast<const uint16_t *>(x1),
                                                       static_cast<const uint16_t *>(x2), batch, n,
                                                       m, d, nullptr, nullptr, out, s);
+}
+
+// out[b] = sign * (A[b] . B[b]^T) + coef[b*M + row] * X[b][row][col] on the matrix cores
+// (A [batch, M, K], B [batch, N, K], X and out [batch, M, N], all of type dtype).
+int inner_grad_gemm(const void *A, const void *B, int dtype, int64_t batch, int64_t M, int64_t N,
+                    int64_t K, float sign, const float *coef, const void *X, void *out, hipStream_t s) {
+    if (dtype == TPW_F32)
+        return launch_inner<float, kEpiGrad, float>(
+            static_cast<const float *>(A), static_cast<const float *>(B), batch, M, N, K, coef, nullptr,
+            static_cast<float *>(out), s, static_cast<const float *>(X), sign);
+    return launch_inner<uint16_t, kEpiGrad, uint16_t>(
+        static_cast<const uint16_t *>(A), static_cast<const uint16_t *>(B), batch, M, N, K, coef, nullptr,
+        static_cast<uint16_t *>(out), s, static_cast<const uint16_t *>(X), sign);
 }
 
 }  // namespace tpw

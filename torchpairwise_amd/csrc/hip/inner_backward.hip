@@ -39,16 +39,18 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Pass 1.  fp32 (BF16W false): W is written in fp32 over the cosine's S.  bf16 (BF16W): W is
-// rounded to bf16 as the reference's bf16 autograd rounds its ratio tensor, and written
-// twice, [n, m] to Wb and transposed [m, n] to WTb, so that both gradient products read
-// their operands k-contiguous; the row / column sums are taken of the rounded values.
-template <typename T, int MODE, bool BF16W>
+// Pass 1.  W (type T: fp32, or bf16 rounded as the reference's bf16 autograd rounds its
+// ratio tensor) is written [n, m] to Wo and, when WTo is given, transposed [m, n] to WTo,
+// so that both gradient products read their operands k-contiguous.  The row / column sums
+// are taken of the stored values.  For cosine, S is read from the fp32 buffer S.
+template <typename T, int MODE>
 __global__ __launch_bounds__(256) void pair_weights_kernel(
     const T *__restrict__ g, const T *__restrict__ res, const float *__restrict__ n1,
-    const float *__restrict__ n2, int64_t n, int64_t m, float *W, float *__restrict__ rowpart,
-    float *__restrict__ colpart, int64_t tiles_i, int64_t tiles_j, uint16_t *__restrict__ Wb,
-    uint16_t *__restrict__ WTb) {
+    const float *__restrict__ n2, int64_t n, int64_t m, const float *__restrict__ S,
+    float *__restrict__ rowpart, float *__restrict__ colpart, int64_t tiles_i, int64_t tiles_j,
+    T *__restrict__ Wo, T *__restrict__ WTo) {
+    constexpr bool BF16W = sizeof(T) == 2;
+    constexpr int kGrp = BF16W ? 8 : 4;  // rows per 16-byte transposed store
     __shared__ float red[4][kPWRows];
     const int64_t b = blockIdx.z, ti = blockIdx.y, tj = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -57,11 +59,12 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
     float a2 = 0.0f;
     if constexpr (MODE == kCosDist || MODE == kCosSim) a2 = jok ? n2[b * m + j] : 0.0f;
     float csum = 0.0f;
-    uint32_t packed[4] = {0u, 0u, 0u, 0u};  // BF16W: 8 consecutive rows of column j
+    uint32_t packed[4] = {0u, 0u, 0u, 0u};  // kGrp consecutive rows of column j
     for (int r = 0; r < kPWRows; ++r) {
         const int64_t i = ti * kPWRows + r;
         float rt = 0.0f;
         uint16_t wb = 0;
+        float wf = 0.0f;
         if (i < n && jok) {
             const int64_t idx = (b * n + i) * m + j;
             const float gv = to_f32(g[idx]);
@@ -78,7 +81,7 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
                 rt = w;
                 csum += w;
             } else {
-                const float s = W[idx];
+                const float s = S[idx];
                 const float a1 = n1[b * n + i];
                 const float den = a1 * a2;
                 const float q = den != 0.0f ? __fdiv_rn(s, den) : s;
@@ -95,26 +98,28 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
             }
             if constexpr (BF16W) {
                 wb = f32_to_bf16_rne(w);
-                Wb[idx] = wb;
+                Wo[idx] = wb;
             } else {
-                W[idx] = w;
+                Wo[idx] = w;
+                wf = w;
             }
         }
-        if constexpr (BF16W) {
-            packed[(r & 7) >> 1] |= (uint32_t)wb << (16 * (r & 1));
-            if ((r & 7) == 7) {  // rows i-7 .. i of column j, 16 bytes of WTb row j
-                const int64_t i8 = i - 7;
-                if (jok && i8 < n) {
-                    uint16_t *dst = WTb + (b * m + j) * n + i8;
-                    if (i8 + 8 <= n && (n & 7) == 0) {
-                        *reinterpret_cast<uint4 *>(dst) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-                    } else {
-                        for (int e = 0; e < 8 && i8 + e < n; ++e)
-                            dst[e] = (uint16_t)(packed[e >> 1] >> (16 * (e & 1)));
+        if constexpr (BF16W) packed[(r & 7) >> 1] |= (uint32_t)wb << (16 * (r & 1));
+        else packed[r & 3] = __float_as_uint(wf);
+        if (WTo && (r % kGrp) == kGrp - 1) {  // rows i-kGrp+1 .. i of column j: 16 B of WTo row j
+            const int64_t i0 = i - (kGrp - 1);
+            if (jok && i0 < n) {
+                T *dst = WTo + (b * m + j) * n + i0;
+                if (i0 + kGrp <= n && (n % kGrp) == 0) {
+                    *reinterpret_cast<uint4 *>(dst) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+                } else {
+                    for (int e = 0; e < kGrp && i0 + e < n; ++e) {
+                        if constexpr (BF16W) dst[e] = (uint16_t)(packed[e >> 1] >> (16 * (e & 1)));
+                        else dst[e] = __uint_as_float(packed[e]);
                     }
                 }
-                packed[0] = packed[1] = packed[2] = packed[3] = 0u;
             }
+            packed[0] = packed[1] = packed[2] = packed[3] = 0u;
         }
         rt = wave_sum(rt);
         if (lane == 0) red[wave][r] = rt;
@@ -335,31 +340,14 @@ int run_gemm(const float *A, const T *B, int64_t batch, int64_t M, int64_t N, in
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// x [batch, rows, d] bf16 -> xt [batch, d, rows], through a 64 x 64 LDS tile.
-__global__ void transpose_bf16_kernel(const uint16_t *__restrict__ x, int64_t rows, int64_t d,
-                                      uint16_t *__restrict__ xt) {
-    __shared__ uint16_t t[64][66];
-    const int64_t b = blockIdx.z, r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    for (int rr = ty; rr < 64; rr += 4) {
-        const int64_t r = r0 + rr, c = c0 + tx;
-        t[rr][tx] = (r < rows && c < d) ? x[(b * rows + r) * d + c] : 0;
-    }
-    __syncthreads();
-    for (int cc = ty; cc < 64; cc += 4) {
-        const int64_t c = c0 + cc, r = r0 + tx;
-        if (c < d && r < rows) xt[(b * d + c) * rows + r] = t[tx][cc];
-    }
-}
-
 struct BwdWs {
-    float *W, *rowpart, *colpart, *coef1, *coef2, *part;
-    uint16_t *Wb, *WTb, *x1t, *x2t;  // bf16 path
+    float *S, *rowpart, *colpart, *coef1, *coef2, *part;
+    void *W, *WT, *x1t, *x2t;  // element type of the inputs
 };
 
-// [W fp32 | row partials | column partials | coef1 | coef2 | Wb | WTb | x1t | x2t | GEMM split
-// partials].  The fp32 path uses W (and the split partials); the bf16 path uses W only for
-// the cosine's S, and the bf16 buffers.  The size covers both.
+// [S fp32 (cosine) | row partials | column partials | coef1 | coef2 | W | W^T | x1^T | x2^T |
+// GEMM split partials], W and the transposes in the inputs' element type (sized for fp32;
+// the fp32 path uses W and the split partials, the bf16 path W, W^T and the transposes).
 BwdWs carve(void *ws, int64_t batch, int64_t n, int64_t m, int64_t d, size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
     BwdWs w;
@@ -368,15 +356,15 @@ BwdWs carve(void *ws, int64_t batch, int64_t n, int64_t m, int64_t d, size_t *to
         p += align256(bytes);
         return r;
     };
-    w.W = reinterpret_cast<float *>(take(sizeof(float) * batch * n * m));
+    w.S = reinterpret_cast<float *>(take(sizeof(float) * batch * n * m));
     w.rowpart = reinterpret_cast<float *>(take(sizeof(float) * batch * cdiv(m, kPWCols) * n));
     w.colpart = reinterpret_cast<float *>(take(sizeof(float) * batch * cdiv(n, kPWRows) * m));
     w.coef1 = reinterpret_cast<float *>(take(sizeof(float) * batch * n));
     w.coef2 = reinterpret_cast<float *>(take(sizeof(float) * batch * m));
-    w.Wb = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * batch * n * m));
-    w.WTb = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * batch * n * m));
-    w.x1t = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * batch * n * d));
-    w.x2t = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * batch * m * d));
+    w.W = take(sizeof(float) * batch * n * m);
+    w.WT = take(sizeof(float) * batch * n * m);
+    w.x1t = take(sizeof(float) * batch * n * d);
+    w.x2t = take(sizeof(float) * batch * m * d);
     const int64_t s1 = gemm_splits(batch, n, d, m), s2 = gemm_splits(batch, m, d, n);
     const int64_t p1 = s1 > 1 ? s1 * batch * n * d : 0, p2 = s2 > 1 ? s2 * batch * m * d : 0;
     w.part = reinterpret_cast<float *>(take(sizeof(float) * (p1 > p2 ? p1 : p2)));
@@ -390,21 +378,40 @@ size_t workspace_bytes(int64_t batch, int64_t n, int64_t m, int64_t d) {
     return total;
 }
 
+// x [batch, rows, d] -> xt [batch, d, rows], through a 64 x 64 LDS tile.
+template <typename T>
+__global__ void transpose_kernel(const T *__restrict__ x, int64_t rows, int64_t d, T *__restrict__ xt) {
+    __shared__ T t[64][65];
+    const int64_t b = blockIdx.z, r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int rr = ty; rr < 64; rr += 4) {
+        const int64_t r = r0 + rr, c = c0 + tx;
+        t[rr][tx] = (r < rows && c < d) ? x[(b * rows + r) * d + c] : T(0);
+    }
+    __syncthreads();
+    for (int cc = ty; cc < 64; cc += 4) {
+        const int64_t c = c0 + cc, r = r0 + tx;
+        if (c < d && r < rows) xt[(b * d + c) * rows + r] = t[tx][cc];
+    }
+}
+
 template <typename T, int MODE>
 int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float *n1,
                  const float *n2, int dtype, int64_t batch, int64_t n, int64_t m, int64_t d, T *gx1,
                  T *gx2, void *ws, hipStream_t s) {
     BwdWs w = carve(ws, batch, n, m, d);
-    constexpr bool kBf16 = sizeof(T) == 2;
+    T *W = static_cast<T *>(w.W), *WT = static_cast<T *>(w.WT);
+    T *x1t = static_cast<T *>(w.x1t), *x2t = static_cast<T *>(w.x2t);
     int rc;
     if constexpr (MODE == kCosDist || MODE == kCosSim) {
-        rc = inner_dot_f32(x1, x2, dtype, batch, n, m, d, w.W, s);
+        rc = inner_dot_f32(x1, x2, dtype, batch, n, m, d, w.S, s);
         if (rc) return rc;
     }
     const int64_t ti = cdiv(n, kPWRows), tj = cdiv(m, kPWCols);
-    hipLaunchKernelGGL((pair_weights_kernel<T, MODE, kBf16>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
-                       dim3(256), 0, s, g, res, n1, n2, n, m, w.W, w.rowpart, w.colpart, ti, tj, w.Wb,
-                       w.WTb);
+    constexpr bool kBf16 = sizeof(T) == 2;
+    hipLaunchKernelGGL((pair_weights_kernel<T, MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
+                       dim3(256), 0, s, g, res, n1, n2, n, m, w.S, w.rowpart, w.colpart, ti, tj, W,
+                       kBf16 ? WT : nullptr);
     rc = check_launch("pair_weights_kernel");
     if (rc) return rc;
     const bool cosine = MODE == kCosDist || MODE == kCosSim;
@@ -419,20 +426,23 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     const float sign = cosine ? 1.0f : -1.0f;
     if constexpr (kBf16) {
         // both products as A . B^T with k-contiguous operands on the bf16 matrix cores:
-        // gx1 = sign * Wb . (x2^T)^T + coef1 * x1, gx2 = sign * WTb . (x1^T)^T + coef2 * x2
-        hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)cdiv(d, 64), (unsigned)cdiv(n, 64), (unsigned)batch),
-                           dim3(256), 0, s, x1, n, d, w.x1t);
-        hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)cdiv(d, 64), (unsigned)cdiv(m, 64), (unsigned)batch),
-                           dim3(256), 0, s, x2, m, d, w.x2t);
-        rc = check_launch("transpose_bf16_kernel");
+        // gx1 = sign * W . (x2^T)^T + coef1 * x1, gx2 = sign * W^T . (x1^T)^T + coef2 * x2
+        hipLaunchKernelGGL((transpose_kernel<T>), dim3((unsigned)cdiv(d, 64), (unsigned)cdiv(n, 64), (unsigned)batch),
+                           dim3(256), 0, s, x1, n, d, x1t);
+        hipLaunchKernelGGL((transpose_kernel<T>), dim3((unsigned)cdiv(d, 64), (unsigned)cdiv(m, 64), (unsigned)batch),
+                           dim3(256), 0, s, x2, m, d, x2t);
+        rc = check_launch("transpose_kernel");
         if (rc) return rc;
-        rc = inner_grad_gemm(w.Wb, w.x2t, TPW_BF16, batch, n, d, m, sign, w.coef1, x1, gx1, s);
+        rc = inner_grad_gemm(W, x2t, dtype, batch, n, d, m, sign, w.coef1, x1, gx1, s);
         if (rc) return rc;
-        return inner_grad_gemm(w.WTb, w.x1t, TPW_BF16, batch, m, d, n, sign, w.coef2, x2, gx2, s);
+        return inner_grad_gemm(WT, x1t, dtype, batch, m, d, n, sign, w.coef2, x2, gx2, s);
     } else {
-        rc = run_gemm<T, false>(w.W, x2, batch, n, d, m, sign, w.coef1, x1, gx1, w.part, s);
+        // fp32: the k-major GEMM with split-K fills the GPU better for narrow outputs (d
+        // columns) than the NT kernel did (C2 euclidean fwd+bwd 9.1 vs 10.6 ms)
+        const float *Wf = reinterpret_cast<const float *>(W);
+        rc = run_gemm<T, false>(Wf, x2, batch, n, d, m, sign, w.coef1, x1, gx1, w.part, s);
         if (rc) return rc;
-        return run_gemm<T, true>(w.W, x1, batch, m, d, n, sign, w.coef2, x2, gx2, w.part, s);
+        return run_gemm<T, true>(Wf, x1, batch, m, d, n, sign, w.coef2, x2, gx2, w.part, s);
     }
 }
 

@@ -188,6 +188,8 @@ int tpw_lp_distances_backward2(const float *grad, const float *x1, const float *
 #define TPW_FAM_WMINKOWSKI 1
 #define TPW_FAM_CANBERRA 2
 #define TPW_FAM_BRAYCURTIS 3
+#define TPW_FAM_CHI2 4
+#define TPW_FAM_JS 5
 
 /* out = sum_k |x1 - x2|^p with no root (p = 0: d, as the reference fills; p = +-inf: max /
  * min of |diff|).  Replaces _ppminkowski (torchpairwise/csrc/ops/ppminkowski.cpp:32-34,
@@ -211,6 +213,17 @@ int tpw_canberra(const float *x1, const float *x2, int64_t batch, int64_t n, int
 int tpw_braycurtis(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
                    int64_t d, float *out, void *stream);
 
+/* out = -sum_k (x1 - x2)^2 / (x1 + x2), terms with x1 + x2 == 0 skipped.  Replaces
+ * _additive_chi2_kernel (additive_chi2_kernel.cpp:30-32, cpu/additive_chi2_kernel.cpp:13-33,35-70). */
+int tpw_additive_chi2(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                      int64_t d, float *out, void *stream);
+
+/* out = sum_k (rel_entr(x1, mid) + rel_entr(x2, mid)) / divisor, mid = (x1 + x2) / 2, with
+ * rel_entr of cpu/rel_entr.h; divisor = 2, or 2 ln(base).  Replaces _sqjensenshannon
+ * (sqjensenshannon.cpp:33-35, cpu/sqjensenshannon_kernel.cpp:13-31,33-80). */
+int tpw_sqjensenshannon(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                        int64_t d, double divisor, float *out, void *stream);
+
 /* Workspace (bytes) of the backward of family member `metric` (TPW_FAM_*). */
 size_t tpw_family_backward_workspace_size(int metric, int64_t batch, int64_t n, int64_t m,
                                           int64_t d);
@@ -218,11 +231,11 @@ size_t tpw_family_backward_workspace_size(int metric, int64_t batch, int64_t n, 
 /* Gradients of the four members above with the reference's formulas, summed over pairs in
  * a fixed order (the reference's GPU kernels use atomics).  p = 0 gives zero gradients, as
  * in the reference; p = +-inf is rejected (TPW_ERR_INVALID).  `out` is the forward result.
- * Replace __ppminkowski_backward (ppminkowski.cpp:35-37, cpu/ppminkowski_kernel.cpp:123-
- * 160,218-290), __wminkowski_backward (wminkowski.cpp:37-39, cpu/wminkowski_kernel.cpp:
- * 132-410; grad_w [batch, d]), __canberra_backward (canberra.cpp:33-35,
- * cpu/canberra_kernel.cpp:85-170; no guard: a zero |x1| + |x2| gives NaN, as there) and
- * __braycurtis_backward (braycurtis.cpp:33-35, cpu/braycurtis_kernel.cpp:84-220). */
+ * Replace __ppminkowski_backward (ppminkowski.cpp:35-37, cpu/ppminkowski_kernel.cpp:121-
+ * 289), __wminkowski_backward (wminkowski.cpp:37-39, cpu/wminkowski_kernel.cpp:
+ * 131-379; grad_w [batch, d]), __canberra_backward (canberra.cpp:33-35,
+ * cpu/canberra_kernel.cpp:85-179; no guard: a zero |x1| + |x2| gives NaN, as there) and
+ * __braycurtis_backward (braycurtis.cpp:33-35, cpu/braycurtis_kernel.cpp:84-226). */
 int tpw_ppminkowski_backward(const float *grad, const float *x1, const float *x2, int64_t batch,
                              int64_t n, int64_t m, int64_t d, double p, float *grad_x1,
                              float *grad_x2, void *workspace, void *stream);
@@ -236,6 +249,33 @@ int tpw_canberra_backward(const float *grad, const float *x1, const float *x2, i
 int tpw_braycurtis_backward(const float *grad, const float *x1, const float *x2,
                             const float *out, int64_t batch, int64_t n, int64_t m, int64_t d,
                             float *grad_x1, float *grad_x2, void *workspace, void *stream);
+
+/* Gradients of tpw_additive_chi2 and tpw_sqjensenshannon with the reference's formulas
+ * (__additive_chi2_kernel_backward, additive_chi2_kernel.cpp:33-35,
+ * cpu/additive_chi2_kernel.cpp:72-183; __sqjensenshannon_backward, sqjensenshannon.cpp:36-38,
+ * cpu/sqjensenshannon_kernel.cpp:82-197), summed over pairs in a fixed order. */
+int tpw_additive_chi2_backward(const float *grad, const float *x1, const float *x2,
+                               int64_t batch, int64_t n, int64_t m, int64_t d, float *grad_x1,
+                               float *grad_x2, void *workspace, void *stream);
+int tpw_sqjensenshannon_backward(const float *grad, const float *x1, const float *x2,
+                                 int64_t batch, int64_t n, int64_t m, int64_t d, double divisor,
+                                 float *grad_x1, float *grad_x2, void *workspace, void *stream);
+
+/* Workspace (bytes) of tpw_haversine / tpw_haversine_backward. */
+size_t tpw_haversine_workspace_size(int64_t batch, int64_t n, int64_t m);
+
+/* out[b,i,j] = 2 asin(sqrt(sin^2(dlat/2) + cos lat_i cos lat_j sin^2(dlon/2))) for points
+ * x1 [batch, n, 2], x2 [batch, m, 2] given as (latitude, longitude) in radians.  Replaces
+ * _haversine (haversine.cpp:30-32, cpu/haversine_kernel.cpp:13-27,29-75). */
+int tpw_haversine(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                  float *out, void *workspace, void *stream);
+
+/* Gradients of tpw_haversine with the reference's formulas (__haversine_backward,
+ * haversine.cpp:33-35, cpu/haversine_kernel.cpp:78-217; no guard: a zero or antipodal pair
+ * gives inf/NaN, as there), grad_x1 [batch, n, 2], grad_x2 [batch, m, 2]. */
+int tpw_haversine_backward(const float *grad, const float *x1, const float *x2, int64_t batch,
+                           int64_t n, int64_t m, float *grad_x1, float *grad_x2,
+                           void *workspace, void *stream);
 
 /* ------------------------------------------------------------------------- */
 /* Backward of the inner-product family                                       */

@@ -17,7 +17,8 @@ Contents (each function cites the reference file:line it restates):
   - directed Hausdorff as an fp32 brute force with per-operation rounding (no FMA) and the
     reference's tie rules, plus its backward scatter;
   - the neighbour masks: each row's k + 1 smallest by a stable sort, and dist <= epsilon;
-  - the reference's VALU kernels (_ppminkowski, _wminkowski, _canberra, _braycurtis) as
+  - the reference's VALU kernels (_ppminkowski, _wminkowski, _canberra, _braycurtis,
+    _additive_chi2_kernel, _sqjensenshannon, _haversine, _snr, _sqmahalanobis) as
     differentiable torch broadcasts over [n, m, d].
 * ``oracle/cref.c`` (built by ``oracle/Makefile`` into ``oracle/_build/liboracle_cref.so``,
   wrapped by ``oracle.cref``) — a C restatement of the reference's CPU loops: the
@@ -38,6 +39,11 @@ Pinning (what checks each function; see tests/test_oracle.py):
   VALU family             : scipy.spatial.distance.cdist fixtures (sqeuclidean, weighted
       minkowski p = 1, 2, 3, seuclidean, canberra with a 0 / 0 term, braycurtis),
       gradcheck in float64, closed forms (p = 0 fills d, p = 2 of pp = squared euclidean).
+  chi2 / JS / haversine   : sklearn additive_chi2_kernel, chi2_kernel, haversine_distances and
+      scipy jensenshannon (base e and 2) fixtures, gradcheck, closed forms (antipodes are
+      pi apart, disjoint distributions give ln 2).
+  snr                     : the variance ratio var(x2 - x1) / var(x1) in numpy, gradcheck.
+  sqmahalanobis           : scipy cdist 'mahalanobis' fixture, VI = I gives sqeuclidean.
   neighbour masks         : sklearn.neighbors kneighbors_graph / radius_neighbors_graph
       (connectivity) on tie-free data, hand-built ties / NaN / -0 cases with hand-derived
       masks (golden vectors), and the selection properties (row count, every selected

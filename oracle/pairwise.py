@@ -307,3 +307,52 @@ def braycurtis(x1: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
     """sum_k |x1 - x2| / sum_k |x1 + x2| (cpu/braycurtis_kernel.cpp:13-29)."""
     s = x1.unsqueeze(-2) + x2.unsqueeze(-3)
     return _pair_diff(x1, x2).abs().sum(-1) / s.abs().sum(-1)
+
+
+# ---------------------------------------------------------------------- remaining custom ops
+def additive_chi2(x1: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
+    """-sum_k (x1 - x2)^2 / (x1 + x2), 0 / 0 terms skipped (cpu/additive_chi2_kernel.cpp:13-30)."""
+    nom = x1.unsqueeze(-2) + x2.unsqueeze(-3)
+    d = _pair_diff(x1, x2)
+    safe = torch.where(nom != 0, nom, torch.ones_like(nom))
+    return -torch.where(nom != 0, d * d / safe, torch.zeros_like(d)).sum(-1)
+
+
+def _rel_entr(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """cpu/rel_entr.h: x log(x / y) for x, y > 0; 0 for x == 0, y >= 0; +inf otherwise."""
+    pos = (x > 0) & (y > 0)
+    val = torch.where(pos, x * torch.log(torch.where(pos, x, torch.ones_like(x)) /
+                                         torch.where(pos, y, torch.ones_like(y))), torch.zeros_like(x))
+    return torch.where(pos | ((x == 0) & (y >= 0)), val, torch.full_like(x, float("inf")))
+
+
+def sqjensenshannon(x1: torch.Tensor, x2: torch.Tensor, base: float | None = None) -> torch.Tensor:
+    """sum_k rel_entr(a, m) + rel_entr(b, m), m = (a + b) / 2, over 2 (or 2 ln base)
+    (cpu/sqjensenshannon_kernel.cpp:13-31,74)."""
+    a, b = x1.unsqueeze(-2), x2.unsqueeze(-3)
+    m = (a + b) / 2
+    val = (_rel_entr(a.expand_as(m), m) + _rel_entr(b.expand_as(m), m)).sum(-1)
+    return val / (2 * np.log(base) if base is not None else 2.0)
+
+
+def haversine(x1: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
+    """2 asin(sqrt(sin^2(dlat/2) + cos lat1 cos lat2 sin^2(dlon/2))) (cpu/haversine_kernel.cpp:22-24)."""
+    lat1, lon1 = x1[..., 0].unsqueeze(-1), x1[..., 1].unsqueeze(-1)
+    lat2, lon2 = x2[..., 0].unsqueeze(-2), x2[..., 1].unsqueeze(-2)
+    v = torch.sin((lat1 - lat2) / 2) ** 2 + torch.cos(lat1) * torch.cos(lat2) * torch.sin((lon1 - lon2) / 2) ** 2
+    return 2 * torch.asin(torch.sqrt(v))
+
+
+def snr(x1: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
+    """V1[i] / DV[i, j]: V1 = sum_k (x1 - mean)^2, DV the same of d = x2[j] - x1[i]
+    (cpu/snr_kernel.cpp:13-33,96)."""
+    d = -_pair_diff(x1, x2)
+    dv = ((d - d.mean(-1, keepdim=True)) ** 2).sum(-1)
+    v1 = ((x1 - x1.mean(-1, keepdim=True)) ** 2).sum(-1, keepdim=True)
+    return v1 / dv
+
+
+def sqmahalanobis(x1: torch.Tensor, x2: torch.Tensor, VI: torch.Tensor) -> torch.Tensor:
+    """sum_kl d_k VI_kl d_l per pair, directly (cpu/sqmahalanobis_kernel.cpp:13-33)."""
+    d = _pair_diff(x1, x2)  # [..., n, m, d]; a batched VI [b, d, d] broadcasts over n
+    return ((d @ (VI.unsqueeze(-3) if VI.dim() == 3 else VI)) * d).sum(-1)

@@ -18,17 +18,20 @@ def rand(*shape, seed: int):
 
 def assert_close(actual, expected, *, rtol: float, atol: float, what: str = ""):
     """|actual - expected| <= atol + rtol * |expected| elementwise (both moved to CPU
-    float64); the message names the worst element."""
+    float64; ``atol`` may be a per-element tensor); the message names the worst element."""
     a = torch.as_tensor(actual).detach().cpu().double()
     e = torch.as_tensor(expected).detach().cpu().double()
     assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
     diff = (a - e).abs()
+    if torch.is_tensor(atol):
+        atol = atol.detach().cpu().double()
     tol = atol + rtol * e.abs()
     bad = ~(diff <= tol)
     if bad.any():
         idx = int(torch.argmax((diff - tol).flatten()))
+        at = float(atol.flatten()[idx]) if torch.is_tensor(atol) and atol.numel() > 1 else float(atol)
         raise AssertionError(
-            f"{what}: {int(bad.sum())}/{bad.numel()} elements beyond rtol={rtol} atol={atol}; "
+            f"{what}: {int(bad.sum())}/{bad.numel()} elements beyond rtol={rtol} atol={at}; "
             f"worst at flat {idx}: got {a.flatten()[idx].item()!r} want {e.flatten()[idx].item()!r}")
 
 

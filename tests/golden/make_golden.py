@@ -17,6 +17,9 @@ this build's oracle:
 * the reference's VALU family (sqeuclidean, weighted minkowski, seuclidean, canberra,
   braycurtis):                  scipy.spatial.distance.cdist in float64 (with a zero
   coordinate pair for canberra's skipped 0/0 term);
+* chi2 / jensenshannon / haversine / mahalanobis: sklearn additive_chi2_kernel, chi2_kernel,
+  haversine_distances and scipy jensenshannon (base e and 2), cdist 'mahalanobis', in
+  float64 (with a zero coordinate pair for chi2's skipped 0 / 0 term);
 * neighbour masks:              sklearn.neighbors.NearestNeighbors(algorithm="brute")
   kneighbors_graph / radius_neighbors_graph (connectivity, float64) on tie-free random
   points, plus hand-built distance rows with ties, NaN, +-0 and inf whose masks are
@@ -117,6 +120,32 @@ def family():
     np.savez_compressed(OUT / "family.npz", **out)
 
 
+def special():
+    from scipy.spatial.distance import jensenshannon
+    from sklearn.metrics.pairwise import additive_chi2_kernel, chi2_kernel, haversine_distances
+
+    rng = np.random.default_rng(20260106)
+    p1 = rng.random((6, 5))
+    p2 = rng.random((8, 5))
+    p1[0, 1] = p2[3, 1] = 0.0  # chi2: a 0 / 0 term, skipped
+    out = dict(p1=p1, p2=p2)
+    out["additive_chi2"] = additive_chi2_kernel(p1, p2)
+    out["chi2_g07"] = chi2_kernel(p1, p2, gamma=0.7)
+    out["js"] = np.array([[jensenshannon(a, b) for b in p2] for a in p1])
+    out["js_base2"] = np.array([[jensenshannon(a, b, base=2) for b in p2] for a in p1])
+    g1 = rng.random((7, 2)) * np.array([np.pi, 2 * np.pi]) - np.array([np.pi / 2, np.pi])
+    g2 = rng.random((9, 2)) * np.array([np.pi, 2 * np.pi]) - np.array([np.pi / 2, np.pi])
+    out["g1"], out["g2"] = g1, g2
+    out["haversine"] = haversine_distances(g1, g2)
+    x1 = rng.standard_normal((7, 4))
+    x2 = rng.standard_normal((9, 4))
+    a = rng.standard_normal((4, 4))
+    VI = a @ a.T + np.eye(4)
+    out["x1"], out["x2"], out["VI"] = x1, x2, VI
+    out["mahalanobis"] = cdist(x1, x2, "mahalanobis", VI=VI)
+    np.savez_compressed(OUT / "special.npz", **out)
+
+
 def neighbors():
     from sklearn.neighbors import NearestNeighbors
 
@@ -155,5 +184,6 @@ if __name__ == "__main__":
     minkowski()
     hausdorff()
     family()
+    special()
     neighbors()
     print("wrote", sorted(p.name for p in OUT.glob("*.npz")))

@@ -47,3 +47,25 @@ def test_argument_errors_are_reported_without_gpu():
     assert b"p must be non-negative" in l.tpw_last_error()
     rc = l.tpw_bool_pairwise_reduce(None, None, 1, 4, 4, 0, 0, 0, None, None)
     assert rc == 1
+
+
+def test_workspace_queries_accept_empty_sizes():
+    # regression: split counts divided by the number of output tiles, 0 for an empty side;
+    # run in a child so that a host fault fails this test instead of ending the session
+    import subprocess
+    import sys
+
+    code = (
+        "from torchpairwise_amd import _capi\n"
+        "l = _capi.lib()\n"
+        "for n, m, d in ((0, 37, 5), (41, 0, 5), (0, 0, 5), (5, 7, 0)):\n"
+        "    for b in (0, 1):\n"
+        "        [l.tpw_family_backward_workspace_size(k, b, n, m, d) for k in range(6)]\n"
+        "        l.tpw_lp_backward_workspace_size(b, n, m, d)\n"
+        "        l.tpw_inner_backward_workspace_size(b, n, m, d)\n"
+        "        l.tpw_haversine_workspace_size(b, n, m)\n"
+        "        l.tpw_hausdorff_workspace_size(b, 2, n, 3, m, d)\n"
+        "print('ok')\n")
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stderr[-2000:])

@@ -444,3 +444,145 @@ def test_family_backward_edge_cases():
             assert bool((t == 0).all())
     with pytest.raises(RuntimeError, match="not supported"):  # inf backward is rejected
         capi.family_backward(capi.FAM_PPMINKOWSKI, g.to(DEV), x1.to(DEV), x2.to(DEV), None, float("inf"))
+
+
+# --------------------------------------------------------------------------------------
+# _additive_chi2_kernel, _sqjensenshannon, _haversine through the C ABI
+# fp32 bar: values rtol 1e-5 (+ atol 1e-5 * max); gradients rtol 1e-4 (+ atol 1e-4 * max)
+# --------------------------------------------------------------------------------------
+def _prob_inputs(B, n, m, d, zeros):
+    x1 = rand(B, n, d, seed=40) + (0.0 if zeros else 0.05)
+    x2 = rand(B, m, d, seed=41) + (0.0 if zeros else 0.05)
+    if zeros:  # chi2's skipped 0 / 0 terms, JS's rel_entr(0, .) = 0
+        x1[..., ::3, 0] = 0.0
+        x2[..., ::2, 0] = 0.0
+        x1[..., ::5, 1:3] = 0.0
+    return x1, x2
+
+
+def _special_ref(metric, a, b, p):
+    if metric == capi.FAM_CHI2:
+        return P.additive_chi2(a, b)
+    return P.sqjensenshannon(a, b, None if p == 2.0 else float(np.exp(p / 2)))
+
+
+@pytest.mark.parametrize("B,n,m,d", FAM_SHAPES + [(1, 600, 900, 40)])
+@pytest.mark.parametrize("metric,p", [(4, 1.0), (5, 2.0), (5, 2 * float(np.log(3.0)))])
+def test_chi2_js_forward(B, n, m, d, metric, p):
+    print(f"chi2/js fwd metric={metric} p={p} {B}x{n}x{m}x{d}", flush=True)
+    x1, x2 = _prob_inputs(B, n, m, d, zeros=True)
+    got = capi.family_forward(metric, x1.to(DEV), x2.to(DEV), None, p)
+    ref = torch.stack([_special_ref(metric, x1[i].double(), x2[i].double(), p) for i in range(B)])
+    assert_close(got, ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()), what=f"metric {metric} p={p}")
+
+
+@pytest.mark.parametrize("B,n,m,d", FAM_SHAPES[1:] + [(1, 600, 900, 40)])
+@pytest.mark.parametrize("metric,p", [(4, 1.0), (5, 2.0), (5, 2 * float(np.log(3.0)))])
+def test_chi2_js_backward(B, n, m, d, metric, p):
+    print(f"chi2/js bwd metric={metric} p={p} {B}x{n}x{m}x{d}", flush=True)
+    x1, x2 = _prob_inputs(B, n, m, d, zeros=False)
+    g = randn(B, n, m, seed=42)
+    got = capi.family_backward(metric, g.to(DEV), x1.to(DEV), x2.to(DEV), None, p)
+    refs = []
+    for i in range(B):
+        a, b = x1[i].double().requires_grad_(), x2[i].double().requires_grad_()
+        _special_ref(metric, a, b, p).backward(g[i].double())
+        refs.append((a.grad, b.grad))
+    for k, name in enumerate(["grad_x1", "grad_x2"]):
+        ref = torch.stack([r[k] for r in refs])
+        assert_close(got[k], ref, rtol=1e-4, atol=1e-4 * float(ref.abs().max()), what=f"{name} m{metric}")
+
+
+def test_chi2_js_zero_terms_match_the_reference_loops():
+    # gradients with 0 coordinates: the reference's own CPU loops (run in float64) are the bar
+    x1, x2 = _prob_inputs(1, 70, 50, 9, zeros=True)
+    g = randn(1, 70, 50, seed=43)
+    ops = torch.ops.torchpairwise
+    for metric, p in ((capi.FAM_CHI2, 1.0), (capi.FAM_JS, 2.0)):
+        got = capi.family_backward(metric, g.to(DEV), x1.to(DEV), x2.to(DEV), None, p)
+        if metric == capi.FAM_CHI2:
+            ref = ops.__additive_chi2_kernel_backward(g.double(), x1.double(), x2.double())
+        else:
+            ref = ops.__sqjensenshannon_backward(g.double(), x1.double(), x2.double(), None)
+        for t, r in zip(got, ref):
+            fin = torch.isfinite(r)
+            assert bool((torch.isfinite(t.cpu()) == fin).all()), f"non-finite pattern m{metric}"
+            assert_close(t.cpu()[fin], r[fin], rtol=1e-4, atol=1e-4 * float(r[fin].abs().max()),
+                         what=f"zero terms m{metric}")
+
+
+HAV_SHAPES = [(1, 1, 1), (1, 300, 257), (3, 129, 65), (1, 2000, 1500)]
+
+
+def _geo(B, n, seed, octant=False):
+    """Points (latitude, longitude) over the whole sphere, or over one octant (every pair
+    then lies within pi / 2: no ill-conditioned pairs)."""
+    u = rand(B, n, 2, seed=seed)
+    if octant:
+        return u * (np.pi / 2)
+    return torch.stack([u[..., 0] * np.pi - np.pi / 2, u[..., 1] * 2 * np.pi - np.pi], -1)
+
+
+# Haversine's conditioning: with v = sin^2(d / 2) rounded in fp32 (error ~ a few ulp, absolute
+# near v = 1), d = 2 asin(sqrt v) moves by 8 eps / cos(d / 2) and the pair weight
+# 1 / (sqrt(v) sqrt(1 - v)) = 2 / |sin d| by a relative 4 eps / cos^2(d / 2) beyond ordinary
+# rounding.  Any fp32 evaluation of the reference's formula (its own kernel included) has
+# these errors, so nearly antipodal pairs (cos(d / 2) < 0.05, i.e. 1 - v < 2.5e-3) get that
+# first-order allowance on top of the fp32 bar; every other pair is held to the plain bar.
+EPS32 = 2.0 ** -24
+
+
+def _hav_allowance(ref, g):
+    d = ref.detach().double()
+    half_cos = torch.cos(d / 2).abs().clamp_min(1e-30)
+    ill = half_cos < 0.05
+    fwd = torch.where(ill, 16 * EPS32 / half_cos, torch.zeros_like(d))
+    pair = 24 * EPS32 * g.double().abs() / torch.sin(d).abs().clamp_min(1e-30) / half_cos ** 2
+    pair = torch.where(ill, pair, torch.zeros_like(pair))
+    return fwd, pair.sum(-1, keepdim=True), pair.sum(-2).unsqueeze(-1)
+
+
+@pytest.mark.parametrize("B,n,m", HAV_SHAPES)
+@pytest.mark.parametrize("octant", [True, False])
+def test_haversine_forward_backward(B, n, m, octant):
+    print(f"haversine {B}x{n}x{m} octant={octant}", flush=True)
+    x1, x2 = _geo(B, n, 44, octant), _geo(B, m, 45, octant)
+    g = randn(B, n, m, seed=46)
+    got = capi.haversine(x1.to(DEV), x2.to(DEV))
+    a, b = x1.double().requires_grad_(), x2.double().requires_grad_()
+    ref = P.haversine(a, b)
+    fwd, row, col = _hav_allowance(ref, g)
+    if octant:
+        assert not bool(fwd.any()) and not bool(row.any())  # the plain fp32 bar only
+    assert_close(got, ref.detach(), rtol=1e-5, atol=1e-5 * float(ref.abs().max()) + fwd, what="haversine")
+    ref.backward(g.double())
+    gx1, gx2 = capi.haversine_backward(g.to(DEV), x1.to(DEV), x2.to(DEV))
+    assert_close(gx1, a.grad, rtol=1e-4, atol=1e-4 * float(a.grad.abs().max()) + row, what="grad_x1")
+    assert_close(gx2, b.grad, rtol=1e-4, atol=1e-4 * float(b.grad.abs().max()) + col, what="grad_x2")
+
+
+def test_haversine_empty_and_unbatched():
+    x1, x2 = _geo(1, 20, 47)[0], _geo(1, 0, 48)[0]
+    assert capi.haversine(x1.to(DEV), x2.to(DEV)).shape == (20, 0)
+    gx1, gx2 = capi.haversine_backward(torch.empty(20, 0, device=DEV), x1.to(DEV), x2.to(DEV))
+    assert gx1.shape == (20, 2) and bool((gx1 == 0).all()) and gx2.shape == (0, 2)
+
+
+@pytest.mark.parametrize("empty", ["x1", "x2"])
+def test_backward_entries_with_one_empty_side(empty):
+    # no pairs: the non-empty side's gradient is zero (its buffer is written, not left as is);
+    # the empty side's buffer is a null pointer
+    n, m, d = (0, 37, 5) if empty == "x1" else (41, 0, 5)
+    x1, x2 = (rand(1, n, d, seed=50) + 0.1).to(DEV), (rand(1, m, d, seed=51) + 0.1).to(DEV)
+    g = torch.empty(1, n, m, device=DEV)
+    other = lambda res: res[1] if empty == "x1" else res[0]
+    for metric in (capi.FAM_PPMINKOWSKI, capi.FAM_CANBERRA, capi.FAM_CHI2, capi.FAM_JS):
+        res = capi.family_backward(metric, g, x1, x2, None, 2.0)
+        assert bool((other(res) == 0).all()), f"family {metric}"
+    assert bool((other(capi.lp_distances_backward2(g, x1, x2, g, 3.0)) == 0).all()), "lp"
+    for dt in (torch.float32, torch.bfloat16):
+        a, b, gg = x1.to(dt), x2.to(dt), g.to(dt)
+        assert bool((other(capi.euclidean_backward(gg, a, b, gg)) == 0).all()), f"euclidean {dt}"
+        assert bool((other(capi.sqeuclidean_backward(gg, a, b)) == 0).all()), f"sqeuclidean {dt}"
+    geo1, geo2 = x1[..., :2].contiguous(), x2[..., :2].contiguous()
+    assert bool((other(capi.haversine_backward(g, geo1, geo2)) == 0).all()), "haversine"

@@ -293,3 +293,75 @@ def test_sqeuclidean_identical_points_are_zero():
     assert bool((torch.diagonal(d) == 0).all())  # direct sum: no |a|^2 + |b|^2 - 2ab residue
     with pytest.raises(NotImplementedError):
         tp.canberra_distances(x.double())
+
+
+# --------------------------------------------------------------------------------------
+# chi2, jensenshannon, haversine, snr, mahalanobis through the drop-in ops; the CPU op in
+# float64 (the reference's loops) is the bar, forward and backward
+# --------------------------------------------------------------------------------------
+def _special_case(name, dtype):
+    gen = torch.Generator().manual_seed(7)
+    if name in ("additive_chi2_kernel", "chi2_kernel", "jensenshannon_distances"):
+        x1, x2 = torch.rand(150, 24, generator=gen) + 0.05, torch.rand(90, 24, generator=gen) + 0.05
+    elif name == "haversine_distances":
+        u1, u2 = torch.rand(150, 2, generator=gen), torch.rand(90, 2, generator=gen)
+        scale, shift = torch.tensor([np.pi, 2 * np.pi]), torch.tensor([np.pi / 2, np.pi])
+        x1, x2 = u1 * scale - shift, u2 * scale - shift
+    else:
+        x1, x2 = torch.randn(150, 24, generator=gen), torch.randn(90, 24, generator=gen)
+    extra = ()
+    if name == "chi2_kernel":
+        extra = (0.3,)
+    elif name == "jensenshannon_distances":
+        extra = (2.0,)  # base
+    elif name == "mahalanobis_distances":
+        a = torch.randn(24, 24, generator=gen)
+        extra = (a @ a.T / 24 + torch.eye(24),)
+    return x1.to(dtype), x2.to(dtype), extra
+
+
+@pytest.mark.parametrize("name", ["additive_chi2_kernel", "chi2_kernel", "jensenshannon_distances",
+                                  "haversine_distances", "snr_distances", "mahalanobis_distances"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_special_ops_gpu(name, dtype):
+    print(f"{name} {dtype}", flush=True)
+    x1, x2, extra = _special_case(name, dtype)
+    fn = getattr(tp, name)
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    dev_extra = [e.to(DEV, dtype) if torch.is_tensor(e) else e for e in extra]
+    out = fn(a, b, *dev_extra)
+    assert out.dtype == dtype
+    g = randn(150, 90, seed=3)
+    out.backward(g.to(DEV, dtype))
+    ra, rb = x1.detach().double().requires_grad_(), x2.detach().double().requires_grad_()
+    ref = fn(ra, rb, *[e.to(dtype).double() if torch.is_tensor(e) else e for e in extra])
+    ref.backward(g.double())
+    rtol = 1e-5 if dtype == torch.float32 else 1e-2
+    grtol = 1e-4 if dtype == torch.float32 else 3e-2
+    if name == "snr_distances" and dtype == torch.bfloat16:
+        rtol, grtol = 2e-2, 5e-2  # a ratio of two bf16-rounded variances
+    assert_close(out.float(), ref, rtol=rtol, atol=rtol * float(ref.abs().max()), what=name)
+    assert_close(a.grad.float(), ra.grad, rtol=grtol, atol=grtol * float(ra.grad.abs().max()), what="grad x1")
+    assert_close(b.grad.float(), rb.grad, rtol=grtol, atol=grtol * float(rb.grad.abs().max()), what="grad x2")
+
+
+def test_special_ops_gpu_batched_and_cdist():
+    gen = torch.Generator().manual_seed(8)
+    x1, x2 = torch.randn(2, 40, 6, generator=gen), torch.randn(2, 30, 6, generator=gen)
+    a = torch.randn(2, 6, 6, generator=gen)
+    VI = a @ a.transpose(1, 2) + torch.eye(6)
+    ops = torch.ops.torchpairwise
+    for got, ref in ((ops._snr(x1.to(DEV), x2.to(DEV)), ops._snr(x1.double(), x2.double())),
+                     (ops._sqmahalanobis(x1.to(DEV), x2.to(DEV), VI.to(DEV)),
+                      ops._sqmahalanobis(x1.double(), x2.double(), VI.double())),
+                     (ops._haversine(x1[..., :2].to(DEV), x2[..., :2].to(DEV)),
+                      ops._haversine(x1[..., :2].double(), x2[..., :2].double())),
+                     (tp.cdist(x1[0].to(DEV), x2[0].to(DEV), "mahalanobis", VI=VI[0].to(DEV)),
+                      tp.cdist(x1[0].double(), x2[0].double(), "mahalanobis", VI=VI[0].double()))):
+        assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()), what="batched")
+    # mahalanobis gradient of VI on the GPU (composite) against the CPU loop
+    x, y, v = x1[0].to(DEV), x2[0].to(DEV), VI[0].to(DEV).requires_grad_()
+    ops._sqmahalanobis(x, y, v).sum().backward()
+    vr = VI[0].double().requires_grad_()
+    ops._sqmahalanobis(x1[0].double(), x2[0].double(), vr).sum().backward()
+    assert_close(v.grad.cpu(), vr.grad, rtol=1e-4, atol=1e-4 * float(vr.grad.abs().max()), what="grad VI")

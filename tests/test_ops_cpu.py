@@ -124,8 +124,8 @@ def test_input_errors():
         tp.euclidean_distances(torch.randn(3))
     with pytest.raises(RuntimeError, match="same number of features"):
         tp.euclidean_distances(torch.randn(3, 4), torch.randn(3, 5))
-    with pytest.raises(NotImplementedError, match="not implemented by this MI355X build"):
-        tp.haversine_distances(torch.randn(3, 2))
+    with pytest.raises(RuntimeError, match="feature dimension of x1 and x2 must be 2"):
+        tp.haversine_distances(torch.randn(3, 3))
 
 
 def _scripted(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -152,12 +152,18 @@ CDIST_METRICS = {
     "correlation": lambda a, b: tp.correlation_distances(a, b),
     "minkowski": lambda a, b: tp.minkowski_distances(a, b, 2.0),
     "lp": lambda a, b: tp.lp_distances(a, b, 2.0),
+    "braycurtis": lambda a, b: tp.braycurtis_distances(a, b),
+    "canberra": lambda a, b: tp.canberra_distances(a, b),
+    "snr": lambda a, b: tp.snr_distances(a, b),
+    "jensenshannon": lambda a, b: tp.jensenshannon_distances(a.abs(), b.abs()),
 }
 
 
 @pytest.mark.parametrize("metric", sorted(CDIST_METRICS))
 def test_cdist_dispatches_to_the_metric(metric):
     a, b = randn(9, 6, seed=0), randn(11, 6, seed=1)
+    if metric == "jensenshannon":
+        a, b = a.abs(), b.abs()
     assert_equal(tp.cdist(a, b, metric), CDIST_METRICS[metric](a, b), metric)
 
 
@@ -190,8 +196,8 @@ def test_cdist_errors_match_the_reference():
         tp.cdist(a, b, "foo")
     with pytest.raises(NotImplementedError, match="pdist is yet to be implemented"):
         tp.pdist(a)
-    with pytest.raises(NotImplementedError):
-        tp.cdist(a, b, "haversine")  # outside this build's path
+    with pytest.raises(RuntimeError, match="feature dimension of x1 and x2 must be 2"):
+        tp.cdist(a, b, "haversine")  # dispatched to haversine_distances
     sch = str(torch.ops.torchpairwise.k_neighbors_mask.default._schema)
     assert sch == ("torchpairwise::k_neighbors_mask(Tensor x1, Tensor? x2=None, int k=1, "
                    "str metric=\"euclidean\", *, Tensor? w=None, Tensor? V=None, Tensor? VI=None, "
@@ -288,3 +294,77 @@ def test_canberra_braycurtis_cpu_grads_and_dtypes():
         torch.ops.torchpairwise._canberra(torch.randn(2, 3, 4), torch.randn(3, 3, 4))
     with pytest.raises(RuntimeError, match="feature dimension of x1, x2, and w do not match"):
         torch.ops.torchpairwise._wminkowski(torch.randn(2, 3, 4), torch.randn(2, 5, 4), torch.rand(2, 4), 2.0)
+
+
+# ---------------------------------------------------------------------- chi2, JS, haversine, snr, mahalanobis
+def test_special_cpu_match_sklearn_scipy_golden():
+    g = dict(np.load(GOLDEN / "special.npz"))
+    t = {k: torch.from_numpy(v) for k, v in g.items()}
+    tol = dict(rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(tp.additive_chi2_kernel(t["p1"], t["p2"]).numpy(), g["additive_chi2"], **tol)
+    np.testing.assert_allclose(tp.chi2_kernel(t["p1"], t["p2"], 0.7).numpy(), g["chi2_g07"], **tol)
+    np.testing.assert_allclose(tp.jensenshannon_distances(t["p1"], t["p2"]).numpy(), g["js"], **tol)
+    np.testing.assert_allclose(tp.jensenshannon_distances(t["p1"], t["p2"], base=2.0).numpy(),
+                               g["js_base2"], **tol)
+    np.testing.assert_allclose(tp.haversine_distances(t["g1"], t["g2"]).numpy(), g["haversine"], **tol)
+    np.testing.assert_allclose(tp.mahalanobis_distances(t["x1"], t["x2"], t["VI"]).numpy(),
+                               g["mahalanobis"], rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(tp.cdist(t["x1"], t["x2"], "mahalanobis", VI=t["VI"]).numpy(),
+                               g["mahalanobis"], rtol=1e-10, atol=1e-10)
+    with pytest.raises(RuntimeError, match="All elements of x1 and x2 must be positive"):
+        tp.additive_chi2_kernel(-t["p1"], t["p2"])
+    with pytest.raises(RuntimeError, match="VI is required for manhalanobis when x2 is passed"):
+        tp.cdist(t["x1"], t["x2"], "mahalanobis")  # the reference's text, typo included
+
+
+def test_special_cpu_internal_ops_vs_oracle_and_grads():
+    ops = torch.ops.torchpairwise
+    gen = torch.Generator().manual_seed(3)
+    p1 = torch.rand(2, 5, 4, dtype=torch.float64, generator=gen) + 0.05
+    p2 = torch.rand(2, 6, 4, dtype=torch.float64, generator=gen) + 0.05
+    x1 = torch.randn(2, 5, 4, dtype=torch.float64, generator=gen)
+    x2 = torch.randn(2, 6, 4, dtype=torch.float64, generator=gen)
+    a = torch.randn(2, 4, 4, dtype=torch.float64, generator=gen)
+    VI = a @ a.transpose(1, 2) + torch.eye(4, dtype=torch.float64)
+    tol = dict(rtol=1e-12, atol=1e-12)
+    assert_close(ops._additive_chi2_kernel(p1, p2), P.additive_chi2(p1, p2), what="chi2", **tol)
+    for base in (None, 2.0, 3.0):
+        assert_close(ops._sqjensenshannon(p1, p2, base), P.sqjensenshannon(p1, p2, base), what="js", **tol)
+    assert_close(ops._haversine(x1[..., :2], x2[..., :2]), P.haversine(x1[..., :2], x2[..., :2]),
+                 what="haversine", **tol)
+    assert_close(ops._snr(x1, x2), P.snr(x1, x2), what="snr", **tol)
+    assert_close(ops._sqmahalanobis(x1, x2, VI), P.sqmahalanobis(x1, x2, VI), what="maha", **tol)
+    req = lambda *ts: tuple(u.clone().requires_grad_() for u in ts)
+    assert torch.autograd.gradcheck(ops._additive_chi2_kernel, req(p1, p2))
+    for base in (None, 3.0):
+        assert torch.autograd.gradcheck(lambda u, v: ops._sqjensenshannon(u, v, base), req(p1, p2))
+    assert torch.autograd.gradcheck(ops._haversine, req(x1[..., :2], x2[..., :2]))
+    assert torch.autograd.gradcheck(ops._snr, req(x1, x2))
+    assert torch.autograd.gradcheck(ops._sqmahalanobis, req(x1, x2, VI))
+    assert torch.autograd.gradcheck(tp.jensenshannon_distances, req(p1[0], p2[0]))
+
+
+def test_special_cpu_edge_cases():
+    # chi2: a coordinate with x1 + x2 == 0 adds nothing (cpu/additive_chi2_kernel.cpp:22-27)
+    a = torch.tensor([[0.0, 1.0]], dtype=torch.float64)
+    b = torch.tensor([[0.0, 3.0]], dtype=torch.float64)
+    assert float(torch.ops.torchpairwise._additive_chi2_kernel(a, b)) == -1.0
+    # JS of identical distributions is 0; of disjoint supports, (ln 2 + ln 2) / 2 (squared, base e)
+    u = torch.tensor([[0.5, 0.5, 0.0, 0.0]], dtype=torch.float64)
+    v = torch.tensor([[0.0, 0.0, 0.5, 0.5]], dtype=torch.float64)
+    assert float(torch.ops.torchpairwise._sqjensenshannon(u, u, None)) == 0.0
+    assert abs(float(torch.ops.torchpairwise._sqjensenshannon(u, v, None)) - np.log(2)) < 1e-15
+    # haversine: antipodes are pi apart, a point is 0 from itself
+    pts = torch.tensor([[0.3, -1.0], [-0.3, -1.0 + np.pi]], dtype=torch.float64)
+    d = tp.haversine_distances(pts)
+    assert abs(float(d[0, 1]) - np.pi) < 1e-7 and float(d[0, 0]) == 0.0
+    # mahalanobis with VI = I is euclidean
+    x = torch.randn(5, 3, dtype=torch.float64)
+    assert_close(tp.mahalanobis_distances(x, x, torch.eye(3, dtype=torch.float64)),
+                 torch.cdist(x, x), rtol=1e-12, atol=1e-7, what="maha I")
+    # snr is V1 / DV, so it is scale-free in x2 - x1 per row
+    y = torch.randn(4, 3, dtype=torch.float64)
+    assert_close(tp.snr_distances(x, y), torch.ops.torchpairwise._snr(x, y).reciprocal(),
+                 rtol=0, atol=0, what="snr")
+    with pytest.raises(RuntimeError, match="feature dimension"):
+        torch.ops.torchpairwise._sqmahalanobis(x, x, torch.eye(4, dtype=torch.float64))

@@ -310,3 +310,56 @@ def test_pins_catch_a_missing_root_or_weight():
     x1, x2, w = (torch.from_numpy(g[k]) for k in ("x1", "x2", "w"))
     assert not np.allclose(P.ppminkowski(x1, x2, 3.0).numpy(), g["wminkowski_p3"])  # root dropped
     assert not np.allclose(P.wminkowski(x1, x2, torch.ones_like(w), 3.0).numpy(), g["wminkowski_p3"])
+
+
+# ---------------------------------------------------------------------- chi2, JS, haversine, snr, mahalanobis
+def test_special_oracle_matches_sklearn_scipy_golden():
+    g = npz("special.npz")
+    t = {k: torch.from_numpy(v) for k, v in g.items()}
+    tol = dict(rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(P.additive_chi2(t["p1"], t["p2"]).numpy(), g["additive_chi2"], **tol)
+    np.testing.assert_allclose(torch.exp(0.7 * P.additive_chi2(t["p1"], t["p2"])).numpy(), g["chi2_g07"], **tol)
+    # scipy normalises each row to a distribution first
+    q1 = t["p1"] / t["p1"].sum(-1, keepdim=True)
+    q2 = t["p2"] / t["p2"].sum(-1, keepdim=True)
+    np.testing.assert_allclose(P.sqjensenshannon(q1, q2).sqrt().numpy(), g["js"], **tol)
+    np.testing.assert_allclose(P.sqjensenshannon(q1, q2, 2.0).sqrt().numpy(), g["js_base2"], **tol)
+    np.testing.assert_allclose(P.haversine(t["g1"], t["g2"]).numpy(), g["haversine"], **tol)
+    np.testing.assert_allclose(P.sqmahalanobis(t["x1"], t["x2"], t["VI"]).sqrt().numpy(), g["mahalanobis"],
+                               rtol=1e-10, atol=1e-10)
+
+
+def test_snr_oracle_is_the_variance_ratio():
+    # snr distance = var(x2 - x1) / var(x1) (population variances; the count cancels)
+    rng = np.random.default_rng(4)
+    a, b = rng.standard_normal((5, 7)), rng.standard_normal((6, 7))
+    want = np.array([[np.var(y - x) / np.var(x) for y in b] for x in a])
+    np.testing.assert_allclose(P.snr(torch.from_numpy(a), torch.from_numpy(b)).reciprocal().numpy(), want,
+                               rtol=1e-12)
+
+
+def test_special_oracle_closed_forms_and_gradients():
+    # VI = I reduces mahalanobis to squared euclidean; antipodes are pi apart on the sphere
+    x = torch.randn(5, 3, dtype=torch.float64)
+    np.testing.assert_allclose(P.sqmahalanobis(x, x, torch.eye(3, dtype=torch.float64)).numpy(),
+                               cdist(x.numpy(), x.numpy(), "sqeuclidean"), rtol=1e-12, atol=1e-12)
+    pts = torch.tensor([[0.3, -1.0], [-0.3, -1.0 + np.pi]], dtype=torch.float64)
+    assert abs(float(P.haversine(pts, pts)[0, 1]) - np.pi) < 1e-7
+    p1 = torch.rand(4, 5, dtype=torch.float64, requires_grad=True)
+    p2 = torch.rand(3, 5, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(P.additive_chi2, (p1, p2))
+    assert torch.autograd.gradcheck(lambda a, b: P.sqjensenshannon(a + 0.05, b + 0.05), (p1, p2))
+    assert torch.autograd.gradcheck(P.haversine, (p1[:, :2], p2[:, :2]))
+    assert torch.autograd.gradcheck(P.snr, (p1, p2))
+
+
+def test_pins_catch_swapped_coordinates_and_a_dropped_half():
+    g = npz("special.npz")
+    t = {k: torch.from_numpy(v) for k, v in g.items()}
+    assert not np.allclose(P.haversine(t["g1"].flip(-1), t["g2"].flip(-1)).numpy(), g["haversine"])
+    q1 = t["p1"] / t["p1"].sum(-1, keepdim=True)
+    q2 = t["p2"] / t["p2"].sum(-1, keepdim=True)
+    assert not np.allclose((2 * P.sqjensenshannon(q1, q2)).sqrt().numpy(), g["js"])  # the / 2 dropped
+    assert not np.allclose(P.sqjensenshannon(q1, q2).sqrt().numpy(), g["js_base2"])  # base ignored
+    assert not np.allclose(P.sqmahalanobis(t["x1"], t["x2"], torch.linalg.inv(t["VI"])).sqrt().numpy(),
+                           g["mahalanobis"])  # V for VI

@@ -19,7 +19,7 @@ TPW_F32, TPW_BF16, TPW_F16, TPW_F64, TPW_I8, TPW_U8, TPW_I16, TPW_I32, TPW_I64 =
 BIT_AND, BIT_OR, BIT_XOR, BIT_EQ, BIT_NE = 0, 1, 2, 3, 4
 RED_SUM, RED_MEAN = 0, 1
 EPI_DOT, EPI_EUCLIDEAN, EPI_SQEUCLIDEAN, EPI_COSINE_SIM, EPI_COSINE_DIST = 0, 1, 2, 3, 4
-FAM_PPMINKOWSKI, FAM_WMINKOWSKI, FAM_CANBERRA, FAM_BRAYCURTIS = 0, 1, 2, 3
+FAM_PPMINKOWSKI, FAM_WMINKOWSKI, FAM_CANBERRA, FAM_BRAYCURTIS, FAM_CHI2, FAM_JS = 0, 1, 2, 3, 4, 5
 
 _i64, _p, _i, _d, _sz = C.c_int64, C.c_void_p, C.c_int, C.c_double, C.c_size_t
 
@@ -56,6 +56,13 @@ _SIGNATURES = {
     "tpw_wminkowski_backward": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p, _p, _p, _p]),
     "tpw_canberra_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "tpw_braycurtis_backward": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "tpw_additive_chi2": (_i, [_p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "tpw_sqjensenshannon": (_i, [_p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
+    "tpw_additive_chi2_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "tpw_sqjensenshannon_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p, _p, _p]),
+    "tpw_haversine_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "tpw_haversine": (_i, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
+    "tpw_haversine_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p]),
 }
 
 _lib = None
@@ -379,7 +386,10 @@ def _as3f(x):
 
 
 def family_forward(metric, x1, x2, w=None, p=2.0):
-    """The reference's VALU kernels on fp32 [(batch,) n, d] x [(batch,) m, d] inputs."""
+    """The reference's VALU kernels on fp32 [(batch,) n, d] x [(batch,) m, d] inputs.
+
+    ``p`` is the exponent for FAM_PPMINKOWSKI / FAM_WMINKOWSKI and the divisor (2, or
+    2 ln base) for FAM_JS."""
     import torch
 
     a, b = _as3f(x1), _as3f(x2)
@@ -393,6 +403,10 @@ def family_forward(metric, x1, x2, w=None, p=2.0):
         call("tpw_wminkowski", _ptr(a), _ptr(b), _ptr(ww), B, n, m, d, float(p), _ptr(out), _stream())
     elif metric == FAM_CANBERRA:
         call("tpw_canberra", _ptr(a), _ptr(b), B, n, m, d, _ptr(out), _stream())
+    elif metric == FAM_CHI2:
+        call("tpw_additive_chi2", _ptr(a), _ptr(b), B, n, m, d, _ptr(out), _stream())
+    elif metric == FAM_JS:
+        call("tpw_sqjensenshannon", _ptr(a), _ptr(b), B, n, m, d, float(p), _ptr(out), _stream())
     else:
         call("tpw_braycurtis", _ptr(a), _ptr(b), B, n, m, d, _ptr(out), _stream())
     return out if x1.dim() == 3 else out[0]
@@ -424,6 +438,14 @@ def family_backward(metric, grad, x1, x2, w=None, p=2.0, out=None):
         call("tpw_canberra_backward", _ptr(g), _ptr(a), _ptr(b), B, n, m, d, _ptr(gx1), _ptr(gx2),
              _ptr(ws), _stream())
         res = [gx1, gx2]
+    elif metric == FAM_CHI2:
+        call("tpw_additive_chi2_backward", _ptr(g), _ptr(a), _ptr(b), B, n, m, d, _ptr(gx1),
+             _ptr(gx2), _ptr(ws), _stream())
+        res = [gx1, gx2]
+    elif metric == FAM_JS:
+        call("tpw_sqjensenshannon_backward", _ptr(g), _ptr(a), _ptr(b), B, n, m, d, float(p),
+             _ptr(gx1), _ptr(gx2), _ptr(ws), _stream())
+        res = [gx1, gx2]
     else:
         o = out.contiguous().reshape(B, n, m)
         call("tpw_braycurtis_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(o), B, n, m, d, _ptr(gx1),
@@ -432,3 +454,31 @@ def family_backward(metric, grad, x1, x2, w=None, p=2.0, out=None):
     if x1.dim() == 2:
         res = [res[0][0], res[1][0]] + ([res[2][0]] if len(res) == 3 else [])
     return tuple(res)
+
+
+def haversine(x1, x2):
+    """Haversine distances of fp32 [(batch,) n, 2] x [(batch,) m, 2] (latitude, longitude)."""
+    import torch
+
+    a, b = _as3f(x1), _as3f(x2)
+    B, n, _ = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=a.device)
+    ws = torch.empty((lib().tpw_haversine_workspace_size(B, n, m),), dtype=torch.uint8, device=a.device)
+    call("tpw_haversine", _ptr(a), _ptr(b), B, n, m, _ptr(out), _ptr(ws), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def haversine_backward(grad, x1, x2):
+    """(grad_x1, grad_x2) of haversine."""
+    import torch
+
+    a, b = _as3f(x1), _as3f(x2)
+    B, n, _ = a.shape
+    m = b.shape[1]
+    g = grad.contiguous().reshape(B, n, m)
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    ws = torch.empty((lib().tpw_haversine_workspace_size(B, n, m),), dtype=torch.uint8, device=a.device)
+    call("tpw_haversine_backward", _ptr(g), _ptr(a), _ptr(b), B, n, m, _ptr(gx1), _ptr(gx2),
+         _ptr(ws), _stream())
+    return (gx1, gx2) if x1.dim() == 3 else (gx1[0], gx2[0])

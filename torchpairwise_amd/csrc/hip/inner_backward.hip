@@ -307,6 +307,7 @@ __global__ void gemm_finish_kernel(const float *__restrict__ part, int64_t split
 
 int64_t gemm_splits(int64_t batch, int64_t M, int64_t N, int64_t K) {
     const int64_t base = cdiv(M, kGT) * cdiv(N, kGT) * batch;
+    if (base == 0) return 1;  // no output tiles (an empty side): nothing to split
     int64_t splits = cdiv(512, base);
     const int64_t by_k = cdiv(K, 256);
     if (splits > by_k) splits = by_k;
@@ -446,6 +447,23 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     }
 }
 
+// Zero the gradient of the non-empty side when the other has no rows (no pairs, so nothing
+// to sum); the empty side's buffer may be a null pointer.  Both dtypes are whole 16-bit words.
+__global__ void zero_words_kernel(uint16_t *__restrict__ p, int64_t len) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t < len) p[t] = 0;
+}
+
+int zero_other_side(int dtype, int64_t batch, int64_t n, int64_t m, int64_t d, void *grad_x1,
+                    void *grad_x2, hipStream_t s) {
+    void *g = n ? grad_x1 : grad_x2;
+    const int64_t len = batch * (n ? n : m) * d * (dtype == TPW_F32 ? 2 : 1);
+    TPW_REQUIRE(g, "null pointer");
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(len, 256)), dim3(256), 0, s,
+                       static_cast<uint16_t *>(g), len);
+    return check_launch("zero_words_kernel");
+}
+
 }  // namespace
 }  // namespace tpw
 
@@ -463,6 +481,8 @@ extern "C" int tpw_euclidean_backward(const void *grad, const void *x1, const vo
     TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
     TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
     if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    if (n == 0 || m == 0)
+        return zero_other_side(dtype, batch, n, m, d, grad_x1, grad_x2, as_stream(stream));
     TPW_REQUIRE(grad && x1 && x2 && res && grad_x1 && grad_x2 && workspace, "null pointer");
     TPW_REQUIRE(cdiv(n, kPWRows) <= kMaxGridYZ && cdiv(m, kGT) <= kMaxGridYZ &&
                     cdiv(n, kGT) <= kMaxGridYZ && batch <= kMaxGridYZ,
@@ -488,6 +508,8 @@ extern "C" int tpw_cosine_backward(const void *grad, const void *x1, const void 
     TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
     TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
     if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    if (n == 0 || m == 0)
+        return zero_other_side(dtype, batch, n, m, d, grad_x1, grad_x2, as_stream(stream));
     TPW_REQUIRE(grad && x1 && x2 && norms1 && norms2 && grad_x1 && grad_x2 && workspace,
                 "null pointer");
     TPW_REQUIRE(cdiv(n, kPWRows) <= kMaxGridYZ && cdiv(m, kGT) <= kMaxGridYZ &&
@@ -513,6 +535,8 @@ extern "C" int tpw_sqeuclidean_backward(const void *grad, const void *x1, const 
     TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
     TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
     if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    if (n == 0 || m == 0)
+        return zero_other_side(dtype, batch, n, m, d, grad_x1, grad_x2, as_stream(stream));
     TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2 && workspace, "null pointer");
     TPW_REQUIRE(cdiv(n, kPWRows) <= kMaxGridYZ && cdiv(m, kGT) <= kMaxGridYZ &&
                     cdiv(n, kGT) <= kMaxGridYZ && batch <= kMaxGridYZ,

@@ -38,7 +38,19 @@ enum Mode {
     kCanberra,  // sum_k |d| / (|a| + |b|), terms with |a| + |b| == 0 skipped (canberra_kernel.cpp:13-30)
     kBrayDen,   // out = out / sum_k |a + b|, out holding sum_k |a - b| (braycurtis_kernel.cpp:13-29)
     kPlusSum,   // sum_k |a + b| (the Bray-Curtis denominator, for the backward)
+    kChi2,      // -sum_k (a - b)^2 / (a + b), 0 where a + b == 0 (additive_chi2_kernel.cpp:13-30)
+    kJS,        // sum_k rel_entr(a, m) + rel_entr(b, m), m = (a + b) / 2, divided by p
+                // (2, or 2 ln base; sqjensenshannon_kernel.cpp:13-45,74)
 };
+
+// rel_entr of cpu/rel_entr.h: NaN stays NaN; x log(x / y) for x, y > 0; 0 for x == 0 and
+// y >= 0; +inf otherwise.
+__device__ __forceinline__ float rel_entr(float x, float y) {
+    if (x != x) return x;
+    if (x > 0.0f && y > 0.0f) return x * logf(x / y);
+    if (x == 0.0f && y >= 0.0f) return 0.0f;
+    return INFINITY;
+}
 
 constexpr int kThreads = 256;
 constexpr int kTile = 128;
@@ -72,6 +84,12 @@ __device__ __forceinline__ float fam_step(float acc, float a, float b, float wk,
     } else if constexpr (MODE == kCanberra) {
         const float den = fabsf(a) + fabsf(b);
         return den != 0.0f ? acc + __fdividef(fabsf(a - b), den) : acc;
+    } else if constexpr (MODE == kChi2) {
+        const float nom = a + b, d = a - b;
+        return nom != 0.0f ? acc - __fdividef(d * d, nom) : acc;
+    } else if constexpr (MODE == kJS) {
+        const float mid = (a + b) * 0.5f;
+        return acc + (rel_entr(a, mid) + rel_entr(b, mid));
     } else {  // kBrayDen, kPlusSum
         return acc + fabsf(a + b);
     }
@@ -111,6 +129,7 @@ template <int MODE, int PK>
 __device__ __forceinline__ float fam_finish(float acc, float inv_p, float prev) {
     if constexpr (MODE == kRoot || MODE == kWeighted) return lp_finish<PK>(acc, inv_p);
     else if constexpr (MODE == kBrayDen) return prev / acc;
+    else if constexpr (MODE == kJS) return acc / inv_p;  // inv_p carries the divisor here
     else return acc;
 }
 
@@ -313,6 +332,8 @@ __device__ __forceinline__ void pair_weights(float g, float a0, float a1, float 
     } else if constexpr (MODE == kBrayDen) {
         w1 = __fdiv_rn(g, a1);
         w2 = w1 * a0;
+    } else if constexpr (MODE == kJS) {
+        w1 = g / p;  // the forward's divisor (sqjensenshannon_kernel.cpp:166)
     } else {
         w1 = g;
     }
@@ -346,6 +367,18 @@ __device__ __forceinline__ float fam_term(float a, float b, float w1, float w2, 
     } else if constexpr (MODE == kCanberra) {
         const float nom = fabsf(a) + fabsf(b);
         return (signf(d) / nom - signf(a) * fabsf(d) / nom / nom) * w1;
+    } else if constexpr (MODE == kChi2) {  // additive_chi2_kernel.cpp:90-125
+        const float nom = a + b;
+        if (nom == 0.0f) return 0.0f;
+        const float q = __fdividef(d, nom);
+        return (q * q - 2.0f * q) * w1;
+    } else if constexpr (MODE == kJS) {  // sqjensenshannon_kernel.cpp:92-140
+        const float sum = a + b, mid = sum * 0.5f;
+        if (!(mid > 0.0f)) return 0.0f;
+        float t = 0.0f;
+        if (a > 0.0f) t += (b + sum * logf(a / mid)) / sum;
+        if (b > 0.0f) t -= b / sum;
+        return t * w1;
     } else {
         return w1 * signf(d) - w2 * signf(a + b);
     }
@@ -573,7 +606,8 @@ int dispatch_forward(int pk, const float *x1, const float *x2, const float *w, i
 }
 
 int fill(float *p, int64_t len, float v, hipStream_t s) {
-    if (len == 0) return TPW_OK;
+    if (len == 0) return TPW_OK;  // an empty buffer may be a null pointer
+    TPW_REQUIRE(p, "null pointer");
     hipLaunchKernelGGL(fill_kernel, dim3((unsigned)cdiv(len, 256)), dim3(256), 0, s, p, len, v);
     return check_launch("fill_kernel");
 }
@@ -596,6 +630,7 @@ int device_cus() {
 // so the workspace is sized with the largest slot count.
 int64_t lp_backward_splits(int64_t slots, int64_t batch, int64_t n, int64_t m, int64_t d) {
     const int64_t base = cdiv(n, kBRows) * cdiv(d, kBFeat) * batch;
+    if (base == 0) return 1;  // no output rows (empty n, d or batch): nothing to split
     int64_t splits = base >= slots ? 1 : slots / base;
     const int64_t max_by_m = cdiv(m, 512);
     if (splits > max_by_m) splits = max_by_m;
@@ -781,13 +816,12 @@ extern "C" int tpw_lp_distances_backward2(const float *grad, const float *x1, co
     TPW_REQUIRE(p >= 0.0, "p must be non-negative, got %g", p);
     TPW_REQUIRE(cdiv(n, kBRows) <= kMaxGridYZ && cdiv(m, kBRows) <= kMaxGridYZ, "too many rows");
     if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
-    TPW_REQUIRE(grad_x1 && grad_x2, "null pointer");
     hipStream_t s = as_stream(stream);
     if (p == 0.0 || n == 0 || m == 0) {
         const int rc = fill(grad_x1, batch * n * d, 0.0f, s);
         return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
     }
-    TPW_REQUIRE(grad && x1 && x2 && dist, "null pointer");
+    TPW_REQUIRE(grad && x1 && x2 && dist && grad_x1 && grad_x2, "null pointer");
     const Workspace lay = workspace_layout(kLpMetric, batch, n, m, d);
     TPW_REQUIRE(workspace, "workspace of %zu bytes required", lay.total);
     char *ws = static_cast<char *>(workspace);
@@ -861,12 +895,11 @@ extern "C" int tpw_ppminkowski_backward(const float *grad, const float *x1, cons
                                         float *grad_x1, float *grad_x2, void *workspace,
                                         void *stream) {
     TPW_FAM_BWD_PROLOGUE(TPW_FAM_PPMINKOWSKI);
-    TPW_REQUIRE(grad_x1 && grad_x2, "null pointer");
     if (p == 0.0 || n == 0 || m == 0) {  // zero gradients (ppminkowski_kernel.cpp:236)
         int rc = fill(grad_x1, batch * n * d, 0.0f, s);
         return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
     }
-    TPW_REQUIRE(grad && x1 && x2, "null pointer");
+    TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2, "null pointer");
     BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, p, grad_x1, grad_x2, nullptr,
              part, nullptr, nullptr, false};
     return dispatch_backward<kSum>(pkind_of(p), j, s);
@@ -878,13 +911,12 @@ extern "C" int tpw_wminkowski_backward(const float *grad, const float *x1, const
                                        float *grad_x2, float *grad_w, void *workspace,
                                        void *stream) {
     TPW_FAM_BWD_PROLOGUE(TPW_FAM_WMINKOWSKI);
-    TPW_REQUIRE(grad_x1 && grad_x2 && grad_w, "null pointer");
     if (p == 0.0 || n == 0 || m == 0) {  // zero gradients (wminkowski_kernel.cpp:296)
         int rc = fill(grad_x1, batch * n * d, 0.0f, s);
         if (rc == TPW_OK) rc = fill(grad_x2, batch * m * d, 0.0f, s);
         return rc != TPW_OK ? rc : fill(grad_w, batch * d, 0.0f, s);
     }
-    TPW_REQUIRE(grad && x1 && x2 && w && out, "null pointer");
+    TPW_REQUIRE(grad && x1 && x2 && w && out && grad_x1 && grad_x2 && grad_w, "null pointer");
     BwdJob j{grad, out, nullptr, x1, x2, w, batch, n, m, d, p, grad_x1, grad_x2, rows, part, pair1,
              nullptr, false};
     int rc = dispatch_backward<kWeighted>(pkind_of(p), j, s);
@@ -904,12 +936,11 @@ extern "C" int tpw_canberra_backward(const float *grad, const float *x1, const f
                                      float *grad_x1, float *grad_x2, void *workspace,
                                      void *stream) {
     TPW_FAM_BWD_PROLOGUE(TPW_FAM_CANBERRA);
-    TPW_REQUIRE(grad_x1 && grad_x2, "null pointer");
     if (n == 0 || m == 0) {
         int rc = fill(grad_x1, batch * n * d, 0.0f, s);
         return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
     }
-    TPW_REQUIRE(grad && x1 && x2, "null pointer");
+    TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2, "null pointer");
     BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1, grad_x2, nullptr,
              part, nullptr, nullptr, false};
     return dispatch_backward<kCanberra>(kP1, j, s);
@@ -920,12 +951,11 @@ extern "C" int tpw_braycurtis_backward(const float *grad, const float *x1, const
                                        int64_t d, float *grad_x1, float *grad_x2, void *workspace,
                                        void *stream) {
     TPW_FAM_BWD_PROLOGUE(TPW_FAM_BRAYCURTIS);
-    TPW_REQUIRE(grad_x1 && grad_x2, "null pointer");
     if (n == 0 || m == 0) {
         int rc = fill(grad_x1, batch * n * d, 0.0f, s);
         return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
     }
-    TPW_REQUIRE(grad && x1 && x2 && out, "null pointer");
+    TPW_REQUIRE(grad && x1 && x2 && out && grad_x1 && grad_x2, "null pointer");
     // ss = sum_k |a + b| per pair into pair buffer 1, recomputed as the reference's backward
     // does; the weights then overwrite it in place (w1) and fill pair buffer 2 (w2)
     int rc = launch_forward<kPlusSum, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, pair1, s);
@@ -933,4 +963,51 @@ extern "C" int tpw_braycurtis_backward(const float *grad, const float *x1, const
     BwdJob j{grad, out, pair1, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1, grad_x2, nullptr, part,
              pair1, pair2, false};
     return dispatch_backward<kBrayDen>(kP1, j, s);
+}
+
+extern "C" int tpw_additive_chi2(const float *x1, const float *x2, int64_t batch, int64_t n,
+                                 int64_t m, int64_t d, float *out, void *stream) {
+    TPW_FAM_CHECKS();
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    return launch_forward<kChi2, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, out, as_stream(stream));
+}
+
+extern "C" int tpw_sqjensenshannon(const float *x1, const float *x2, int64_t batch, int64_t n,
+                                   int64_t m, int64_t d, double divisor, float *out, void *stream) {
+    TPW_FAM_CHECKS();
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    // launch_forward passes inv_p = 1 / p; the JS epilogue divides by inv_p, so p = 1 / divisor
+    return launch_forward<kJS, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0 / divisor, out, as_stream(stream));
+}
+
+extern "C" int tpw_additive_chi2_backward(const float *grad, const float *x1, const float *x2,
+                                          int64_t batch, int64_t n, int64_t m, int64_t d,
+                                          float *grad_x1, float *grad_x2, void *workspace,
+                                          void *stream) {
+    TPW_FAM_BWD_PROLOGUE(TPW_FAM_CHI2);
+    if (n == 0 || m == 0) {
+        int rc = fill(grad_x1, batch * n * d, 0.0f, s);
+        return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
+    }
+    TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2, "null pointer");
+    BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1, grad_x2, nullptr,
+             part, nullptr, nullptr, false};
+    return dispatch_backward<kChi2>(kP1, j, s);
+}
+
+extern "C" int tpw_sqjensenshannon_backward(const float *grad, const float *x1, const float *x2,
+                                            int64_t batch, int64_t n, int64_t m, int64_t d,
+                                            double divisor, float *grad_x1, float *grad_x2,
+                                            void *workspace, void *stream) {
+    TPW_FAM_BWD_PROLOGUE(TPW_FAM_JS);
+    if (n == 0 || m == 0) {
+        int rc = fill(grad_x1, batch * n * d, 0.0f, s);
+        return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
+    }
+    TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2, "null pointer");
+    BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, divisor, grad_x1, grad_x2,
+             nullptr, part, nullptr, nullptr, false};
+    return dispatch_backward<kJS>(kP1, j, s);
 }

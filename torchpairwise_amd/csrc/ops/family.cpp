@@ -1,5 +1,6 @@
-// The reference's own VALU metric ops: _ppminkowski, _wminkowski, _canberra, _braycurtis
-// and their __*_backward ops (csrc/ops/{ppminkowski,wminkowski,canberra,braycurtis}.cpp),
+// The reference's own VALU metric ops: _ppminkowski, _wminkowski, _canberra, _braycurtis,
+// _additive_chi2_kernel, _sqjensenshannon and their __*_backward ops
+// (csrc/ops/{ppminkowski,wminkowski,canberra,braycurtis,additive_chi2_kernel,sqjensenshannon}.cpp),
 // with CPU, GPU and Autograd kernels.
 //
 // GPU: fp32 kernels behind the C ABI (valu_lp.hip); bfloat16 / float16 inputs are computed
@@ -67,7 +68,16 @@ void for_pairs(int64_t B, int64_t n, int64_t m, F f) {
     });
 }
 
-enum Fam { kPP, kW, kCanb, kBray };
+enum Fam { kPP, kW, kCanb, kBray, kChi2, kJS };
+
+// rel_entr of cpu/rel_entr.h
+template <typename T>
+inline T rel_entr(T x, T y) {
+    if (std::isnan(x)) return x;
+    if (x > T(0) && y > T(0)) return x * std::log(x / y);
+    if (x == T(0) && y >= T(0)) return T(0);
+    return std::numeric_limits<T>::infinity();
+}
 
 // out[b,i,j] for one member, accumulating in acc_t (cpu/*_kernel.cpp forward loops).
 template <Fam F, typename acc_t, typename scalar_t>
@@ -102,6 +112,20 @@ void family_forward_loop(const at::Tensor &a, const at::Tensor &bb, const at::Te
                 const acc_t den = std::fabs((acc_t)u[k]) + std::fabs((acc_t)v[k]);
                 if (den != 0) val += std::fabs((acc_t)u[k] - (acc_t)v[k]) / den;
             }
+        } else if constexpr (F == kChi2) {  // cpu/additive_chi2_kernel.cpp:13-30
+            for (int64_t k = 0; k < d; ++k) {
+                const acc_t nom = (acc_t)u[k] + (acc_t)v[k];
+                if (nom != 0) {
+                    const acc_t den = (acc_t)u[k] - (acc_t)v[k];
+                    val -= den * den / nom;
+                }
+            }
+        } else if constexpr (F == kJS) {  // cpu/sqjensenshannon_kernel.cpp:13-30,74 (p = divisor)
+            for (int64_t k = 0; k < d; ++k) {
+                const acc_t mid = ((acc_t)u[k] + (acc_t)v[k]) / (acc_t)2;
+                val += rel_entr((acc_t)u[k], mid) + rel_entr((acc_t)v[k], mid);
+            }
+            val /= (acc_t)p;
         } else {
             acc_t diff = 0, sum = 0;
             for (int64_t k = 0; k < d; ++k) {
@@ -189,6 +213,17 @@ void family_backward_loop(const at::Tensor &gc, const at::Tensor &a, const at::T
         } else if constexpr (F == kCanb) {
             const acc_t nom = std::fabs(x) + std::fabs(y);
             return sgn(diff) / nom - sgn(x) * std::fabs(diff) / nom / nom;
+        } else if constexpr (F == kChi2) {  // cpu/additive_chi2_kernel.cpp:90-125
+            const acc_t nom = x + y;
+            return nom != 0 ? diff * diff / (nom * nom) - 2 * diff / nom : acc_t(0);
+        } else if constexpr (F == kJS) {  // cpu/sqjensenshannon_kernel.cpp:92-140, before / p
+            const acc_t sum = x + y, mid = sum / (acc_t)2;
+            acc_t t = 0;
+            if (mid > 0) {
+                if (x > 0) t += (y + sum * std::log(x / mid)) / sum;
+                if (y > 0) t += -y / sum;
+            }
+            return t;
         } else {
             return sgn(diff) * f1[at] - sgn(x + y) * f2[at];
         }
@@ -204,7 +239,7 @@ void family_backward_loop(const at::Tensor &gc, const at::Tensor &a, const at::T
                     const size_t at = (size_t)((b * n + i) * m + j);
                     s += (acc_t)G[at] * term((acc_t)X1[r * d + k], (acc_t)X2[(b * m + j) * d + k], wk, at, k);
                 }
-                GX1[r * d + k] = (scalar_t)s;
+                GX1[r * d + k] = (scalar_t)(F == kJS ? s / pp : s);
             }
         }
     });
@@ -218,7 +253,7 @@ void family_backward_loop(const at::Tensor &gc, const at::Tensor &a, const at::T
                     const size_t at = (size_t)((b * n + i) * m + j);
                     s += (acc_t)G[at] * term((acc_t)X2[r * d + k], (acc_t)X1[(b * n + i) * d + k], wk, at, k);
                 }
-                GX2[r * d + k] = (scalar_t)s;
+                GX2[r * d + k] = (scalar_t)(F == kJS ? s / pp : s);
             }
         }
     });
@@ -289,6 +324,8 @@ at::Tensor family_forward_cuda(const at::Tensor &x1, const at::Tensor &x2, const
     if constexpr (F == kPP) rc = tpw_ppminkowski(A, Bp, B, n, m, d, p, O, s);
     else if constexpr (F == kW) rc = tpw_wminkowski(A, Bp, wc.data_ptr<float>(), B, n, m, d, p, O, s);
     else if constexpr (F == kCanb) rc = tpw_canberra(A, Bp, B, n, m, d, O, s);
+    else if constexpr (F == kChi2) rc = tpw_additive_chi2(A, Bp, B, n, m, d, O, s);
+    else if constexpr (F == kJS) rc = tpw_sqjensenshannon(A, Bp, B, n, m, d, p, O, s);
     else rc = tpw_braycurtis(A, Bp, B, n, m, d, O, s);
     check_rc(rc, from);
     return unbatch(out, ub).to(x1.scalar_type());
@@ -321,7 +358,8 @@ std::vector<at::Tensor> family_backward_cuda(const at::Tensor &grad, const at::T
         }
     }
     const int metric = F == kPP ? TPW_FAM_PPMINKOWSKI : F == kW ? TPW_FAM_WMINKOWSKI
-                     : F == kCanb ? TPW_FAM_CANBERRA : TPW_FAM_BRAYCURTIS;
+                     : F == kCanb ? TPW_FAM_CANBERRA : F == kChi2 ? TPW_FAM_CHI2
+                     : F == kJS ? TPW_FAM_JS : TPW_FAM_BRAYCURTIS;
     auto ws = workspace(tpw_family_backward_workspace_size(metric, B, n, m, d), a);
     const float *G = g.data_ptr<float>(), *A = a.data_ptr<float>(), *Bp = bb.data_ptr<float>();
     void *s = current_stream();
@@ -336,6 +374,12 @@ std::vector<at::Tensor> family_backward_cuda(const at::Tensor &grad, const at::T
     else if constexpr (F == kCanb)
         rc = tpw_canberra_backward(G, A, Bp, B, n, m, d, gx1.data_ptr<float>(), gx2.data_ptr<float>(),
                                    ws.data_ptr(), s);
+    else if constexpr (F == kChi2)
+        rc = tpw_additive_chi2_backward(G, A, Bp, B, n, m, d, gx1.data_ptr<float>(), gx2.data_ptr<float>(),
+                                        ws.data_ptr(), s);
+    else if constexpr (F == kJS)
+        rc = tpw_sqjensenshannon_backward(G, A, Bp, B, n, m, d, p, gx1.data_ptr<float>(),
+                                          gx2.data_ptr<float>(), ws.data_ptr(), s);
     else
         rc = tpw_braycurtis_backward(G, A, Bp, out.data_ptr<float>(), B, n, m, d, gx1.data_ptr<float>(),
                                      gx2.data_ptr<float>(), ws.data_ptr(), s);
@@ -414,6 +458,43 @@ std::tuple<at::Tensor, at::Tensor> braycurtis_backward_cuda(const at::Tensor &g,
     return {r[0], r[1]};
 }
 
+// the divisor of _sqjensenshannon: 2, or 2 ln(base) (cpu/sqjensenshannon_kernel.cpp:74)
+double js_divisor(c10::optional<double> base) { return base.has_value() ? 2 * std::log(base.value()) : 2.0; }
+
+at::Tensor chi2_cpu(const at::Tensor &x1, const at::Tensor &x2) {
+    return family_forward_cpu<kChi2>(x1, x2, nullptr, 1.0, "_additive_chi2_kernel_forward");
+}
+at::Tensor chi2_cuda(const at::Tensor &x1, const at::Tensor &x2) {
+    return family_forward_cuda<kChi2>(x1, x2, nullptr, 1.0, "_additive_chi2_kernel_forward");
+}
+std::tuple<at::Tensor, at::Tensor> chi2_backward_cpu(const at::Tensor &g, const at::Tensor &x1,
+                                                     const at::Tensor &x2) {
+    auto r = family_backward_cpu<kChi2>(g, x1, x2, nullptr, 1.0);
+    return {r[0], r[1]};
+}
+std::tuple<at::Tensor, at::Tensor> chi2_backward_cuda(const at::Tensor &g, const at::Tensor &x1,
+                                                      const at::Tensor &x2) {
+    auto r = family_backward_cuda<kChi2>(g, x1, x2, nullptr, 1.0, nullptr, "_additive_chi2_kernel_backward");
+    return {r[0], r[1]};
+}
+
+at::Tensor js_cpu(const at::Tensor &x1, const at::Tensor &x2, c10::optional<double> base) {
+    return family_forward_cpu<kJS>(x1, x2, nullptr, js_divisor(base), "_sqjensenshannon_forward");
+}
+at::Tensor js_cuda(const at::Tensor &x1, const at::Tensor &x2, c10::optional<double> base) {
+    return family_forward_cuda<kJS>(x1, x2, nullptr, js_divisor(base), "_sqjensenshannon_forward");
+}
+std::tuple<at::Tensor, at::Tensor> js_backward_cpu(const at::Tensor &g, const at::Tensor &x1,
+                                                   const at::Tensor &x2, c10::optional<double> base) {
+    auto r = family_backward_cpu<kJS>(g, x1, x2, nullptr, js_divisor(base));
+    return {r[0], r[1]};
+}
+std::tuple<at::Tensor, at::Tensor> js_backward_cuda(const at::Tensor &g, const at::Tensor &x1,
+                                                    const at::Tensor &x2, c10::optional<double> base) {
+    auto r = family_backward_cuda<kJS>(g, x1, x2, nullptr, js_divisor(base), nullptr, "_sqjensenshannon_backward");
+    return {r[0], r[1]};
+}
+
 // ------------------------------------------------------------------------ dispatcher handles
 template <typename Sig>
 c10::TypedOperatorHandle<Sig> op_handle(const char *name) {
@@ -442,6 +523,17 @@ T2 braycurtis_backward_op(const at::Tensor &g, const at::Tensor &x1, const at::T
     static auto op = op_handle<T2(const at::Tensor &, const at::Tensor &, const at::Tensor &)>(
         "torchpairwise::__braycurtis_backward");
     return op.call(g, x1, x2);
+}
+
+T2 chi2_backward_op(const at::Tensor &g, const at::Tensor &x1, const at::Tensor &x2) {
+    static auto op = op_handle<T2(const at::Tensor &, const at::Tensor &, const at::Tensor &)>(
+        "torchpairwise::__additive_chi2_kernel_backward");
+    return op.call(g, x1, x2);
+}
+T2 js_backward_op(const at::Tensor &g, const at::Tensor &x1, const at::Tensor &x2, c10::optional<double> base) {
+    static auto op = op_handle<T2(const at::Tensor &, const at::Tensor &, const at::Tensor &,
+                                  c10::optional<double>)>("torchpairwise::__sqjensenshannon_backward");
+    return op.call(g, x1, x2, base);
 }
 
 // ------------------------------------------------------------------------ autograd
@@ -496,6 +588,25 @@ class PairFunction : public torch::autograd::Function<PairFunction<FWD, BWD>> {
     }
 };
 
+class JSFunction : public torch::autograd::Function<JSFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x1, const Variable &x2,
+                            c10::optional<double> base) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        ctx->save_for_backward({x1, x2});
+        ctx->saved_data["has_base"] = base.has_value();
+        ctx->saved_data["base"] = base.value_or(0.0);
+        return sqjensenshannon(x1, x2, base);
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad) {
+        auto s = ctx->get_saved_variables();
+        c10::optional<double> base;
+        if (ctx->saved_data["has_base"].toBool()) base = ctx->saved_data["base"].toDouble();
+        auto r = js_backward_op(grad[0], s[0], s[1], base);
+        return {std::get<0>(r), std::get<1>(r), Variable()};
+    }
+};
+
 at::Tensor ppminkowski_autograd(const at::Tensor &x1, const at::Tensor &x2, double p) {
     return PPMinkowskiFunction::apply(x1, x2, p);
 }
@@ -507,6 +618,12 @@ at::Tensor canberra_autograd(const at::Tensor &x1, const at::Tensor &x2) {
 }
 at::Tensor braycurtis_autograd(const at::Tensor &x1, const at::Tensor &x2) {
     return PairFunction<braycurtis, braycurtis_backward_op>::apply(x1, x2);
+}
+at::Tensor chi2_autograd(const at::Tensor &x1, const at::Tensor &x2) {
+    return PairFunction<additive_chi2, chi2_backward_op>::apply(x1, x2);
+}
+at::Tensor js_autograd(const at::Tensor &x1, const at::Tensor &x2, c10::optional<double> base) {
+    return JSFunction::apply(x1, x2, base);
 }
 
 }  // namespace
@@ -530,8 +647,19 @@ at::Tensor braycurtis(const at::Tensor &x1, const at::Tensor &x2) {
     static auto op = op_handle<at::Tensor(const at::Tensor &, const at::Tensor &)>("torchpairwise::_braycurtis");
     return op.call(x1, x2);
 }
+at::Tensor additive_chi2(const at::Tensor &x1, const at::Tensor &x2) {
+    static auto op = op_handle<at::Tensor(const at::Tensor &, const at::Tensor &)>(
+        "torchpairwise::_additive_chi2_kernel");
+    return op.call(x1, x2);
+}
+at::Tensor sqjensenshannon(const at::Tensor &x1, const at::Tensor &x2, c10::optional<double> base) {
+    static auto op = op_handle<at::Tensor(const at::Tensor &, const at::Tensor &, c10::optional<double>)>(
+        "torchpairwise::_sqjensenshannon");
+    return op.call(x1, x2, base);
+}
 
-// schemas: csrc/ops/{ppminkowski,wminkowski,canberra,braycurtis}.cpp:30-39
+// schemas: csrc/ops/{ppminkowski,wminkowski,canberra,braycurtis,additive_chi2_kernel,
+// sqjensenshannon}.cpp:30-39
 TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     m.def("_ppminkowski(Tensor x1, Tensor x2, float p=2) -> Tensor");
     m.def("__ppminkowski_backward(Tensor grad, Tensor x1, Tensor x2, float p) -> (Tensor grad_x1, Tensor grad_x2)");
@@ -541,6 +669,10 @@ TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     m.def("__canberra_backward(Tensor grad, Tensor x1, Tensor x2) -> (Tensor grad_x1, Tensor grad_x2)");
     m.def("_braycurtis(Tensor x1, Tensor x2) -> Tensor");
     m.def("__braycurtis_backward(Tensor grad, Tensor x1, Tensor x2) -> (Tensor grad_x1, Tensor grad_x2)");
+    m.def("_additive_chi2_kernel(Tensor x1, Tensor x2) -> Tensor");
+    m.def("__additive_chi2_kernel_backward(Tensor grad, Tensor x1, Tensor x2) -> (Tensor grad_x1, Tensor grad_x2)");
+    m.def("_sqjensenshannon(Tensor x1, Tensor x2, float? base=None) -> Tensor");
+    m.def("__sqjensenshannon_backward(Tensor grad, Tensor x1, Tensor x2, float? base) -> (Tensor grad_x1, Tensor grad_x2)");
 }
 
 TORCH_LIBRARY_IMPL(torchpairwise, CPU, m) {
@@ -552,6 +684,10 @@ TORCH_LIBRARY_IMPL(torchpairwise, CPU, m) {
     m.impl("__canberra_backward", TORCH_FN(canberra_backward_cpu));
     m.impl("_braycurtis", TORCH_FN(braycurtis_cpu));
     m.impl("__braycurtis_backward", TORCH_FN(braycurtis_backward_cpu));
+    m.impl("_additive_chi2_kernel", TORCH_FN(chi2_cpu));
+    m.impl("__additive_chi2_kernel_backward", TORCH_FN(chi2_backward_cpu));
+    m.impl("_sqjensenshannon", TORCH_FN(js_cpu));
+    m.impl("__sqjensenshannon_backward", TORCH_FN(js_backward_cpu));
 }
 
 TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
@@ -563,6 +699,10 @@ TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
     m.impl("__canberra_backward", TORCH_FN(canberra_backward_cuda));
     m.impl("_braycurtis", TORCH_FN(braycurtis_cuda));
     m.impl("__braycurtis_backward", TORCH_FN(braycurtis_backward_cuda));
+    m.impl("_additive_chi2_kernel", TORCH_FN(chi2_cuda));
+    m.impl("__additive_chi2_kernel_backward", TORCH_FN(chi2_backward_cuda));
+    m.impl("_sqjensenshannon", TORCH_FN(js_cuda));
+    m.impl("__sqjensenshannon_backward", TORCH_FN(js_backward_cuda));
 }
 
 TORCH_LIBRARY_IMPL(torchpairwise, Autograd, m) {
@@ -570,6 +710,8 @@ TORCH_LIBRARY_IMPL(torchpairwise, Autograd, m) {
     m.impl("_wminkowski", TORCH_FN(wminkowski_autograd));
     m.impl("_canberra", TORCH_FN(canberra_autograd));
     m.impl("_braycurtis", TORCH_FN(braycurtis_autograd));
+    m.impl("_additive_chi2_kernel", TORCH_FN(chi2_autograd));
+    m.impl("_sqjensenshannon", TORCH_FN(js_autograd));
 }
 
 }  // namespace tpw_ext

@@ -89,11 +89,6 @@ at::Tensor route_cdist(const at::Tensor &x1, const at::Tensor &x2, double p) {
     return pw_lp(a, b, p);
 }
 
-[[noreturn]] void not_in_build(const char *name) {
-    TORCH_CHECK_NOT_IMPLEMENTED(false, "torchpairwise.", name,
-                                " is not implemented by this MI355X build (outside its hot path: "
-                                "the inner-product, Minkowski, boolean and Hausdorff families)");
-}
 
 // Public metric schemas, byte-for-byte those of csrc/ops/pairwise_metrics.h:76-424 (also quoted
 // by cdist's incompatible-argument error, as the reference quotes its functors' schema_str).
@@ -259,6 +254,65 @@ at::Tensor seuclidean_distances(const at::Tensor &x1, const c10::optional<at::Te
     return wminkowski(xs.first, xs.second, w, 2);
 }
 
+// pairwise_metrics.cpp:124-145: non-negative inputs required.  (chi2_kernel checks its
+// inputs under the additive_chi2_kernel name and passes the raw x1, as the reference.)
+void check_non_negative(const at::Tensor &x1, const c10::optional<at::Tensor> &x2, const at::Tensor &x2_) {
+    TORCH_CHECK(x1.ge(0).all().item<bool>() && (!x2.has_value() || x2_.ge(0).all().item<bool>()),
+                "All elements of x1 and x2 must be positive")
+}
+
+at::Tensor additive_chi2_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("additive_chi2_kernel", x1, x2);
+    check_non_negative(xs.first, x2, xs.second);
+    return additive_chi2(xs.first, xs.second);
+}
+
+at::Tensor chi2_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2, double gamma) {
+    auto xs = check_pairwise_inputs("additive_chi2_kernel", x1, x2);
+    check_non_negative(xs.first, x2, xs.second);
+    return additive_chi2(x1, xs.second).mul_(gamma).exp_();
+}
+
+at::Tensor jensenshannon_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
+                                   c10::optional<double> base) {
+    // pairwise_metrics.cpp:325-335: rows normalised to sum 1, then sqrt of _sqjensenshannon
+    auto xs = check_pairwise_inputs("jensenshannon_distances", x1, x2);
+    auto a = xs.first / xs.first.sum(-1, true);
+    auto b = x2.has_value() ? xs.second / xs.second.sum(-1, true) : a;
+    return sqjensenshannon(a, b, base).sqrt_();
+}
+
+at::Tensor haversine_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("haversine_distances", x1, x2);  // pairwise_metrics.cpp:33-40
+    return haversine(xs.first, xs.second);
+}
+
+at::Tensor snr_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
+    auto xs = check_pairwise_inputs("snr_distances", x1, x2);  // pairwise_metrics.cpp:401-408
+    return snr(xs.first, xs.second).reciprocal();
+}
+
+at::Tensor mahalanobis_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
+                                 const c10::optional<at::Tensor> &VI) {
+    // pairwise_metrics.cpp:273-297 (the batched default VI is built as the reference builds it)
+    TORCH_CHECK(!x2.has_value() || VI.has_value(), "VI is required for manhalanobis when x2 is passed.")
+    auto xs = check_pairwise_inputs("mahalanobis_distances", x1, x2);
+    at::Tensor VI_;
+    if (VI.has_value()) {
+        VI_ = VI.value();
+    } else {
+        at::NoGradGuard no_grad_guard;
+        if (xs.first.dim() == 2) {
+            VI_ = at::cov(xs.first.transpose(-1, -2)).inverse().transpose_(-1, -2);
+        } else {
+            auto cov = at::empty({xs.first.size(0), xs.first.size(1), xs.first.size(1)}, xs.first.options());
+            for (int64_t b = 0; b < xs.first.size(0); ++b) cov.index_put_({b}, at::cov(xs.first[b].transpose(-1, -2)));
+            VI_ = cov.inverse().transpose_(-1, -2);
+        }
+    }
+    return sqmahalanobis(xs.first, xs.second, VI_).sqrt_();
+}
+
 at::Tensor braycurtis_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs("braycurtis_distances", x1, x2);  // pairwise_metrics.cpp:307-315
     return braycurtis(xs.first, xs.second);
@@ -376,12 +430,6 @@ at::Tensor linf_distances(const at::Tensor &x1, const c10::optional<at::Tensor> 
 }
 
 // outside the hot path: registered so the schemas match, but not served by this build
-at::Tensor haversine_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("haversine_distances"); }
-at::Tensor additive_chi2_kernel(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("additive_chi2_kernel"); }
-at::Tensor chi2_kernel(const at::Tensor &, const c10::optional<at::Tensor> &, double) { not_in_build("chi2_kernel"); }
-at::Tensor mahalanobis_distances(const at::Tensor &, const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &) { not_in_build("mahalanobis_distances"); }
-at::Tensor jensenshannon_distances(const at::Tensor &, const c10::optional<at::Tensor> &, c10::optional<double>) { not_in_build("jensenshannon_distances"); }
-at::Tensor snr_distances(const at::Tensor &, const c10::optional<at::Tensor> &) { not_in_build("snr_distances"); }
 
 // ------------------------------------------------------------------------------------
 // cdist(metric=...) and pdist (csrc/ops/cpdist.cpp)

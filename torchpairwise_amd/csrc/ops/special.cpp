@@ -1,0 +1,531 @@
+// The reference's remaining custom metric ops: _haversine, _snr and _sqmahalanobis with their
+// __*_backward ops (csrc/ops/{haversine,snr,sqmahalanobis}.cpp), CPU, GPU and Autograd.
+//
+// _haversine runs HIP kernels on the GPU (haversine.hip; fp32, 16-bit types through fp32).
+// _snr and _sqmahalanobis are compositions on the GPU:
+//   _snr(x1, x2)[i, j] = V1[i] / DV[i, j], V1 = sum_k (x1 - mean x1)^2 and
+//     DV = sum_k (d - mean d)^2 with d = x2[j] - x1[i]; since mean d = mean x2[j] - mean x1[i],
+//     DV is the squared distance between the row-centred points, i.e. _ppminkowski(x1c, x2c, 2)
+//     on the VALU kernel;
+//   _sqmahalanobis(x1, x2, VI)[i, j] = d^T VI d = q1[i] + q2[j] - x1[i] (VI + VI^T) x2[j]^T with
+//     q = rowsum((x VI) * x): two library GEMMs instead of the reference's O(d^2) per pair.
+// Their gradients come from autograd through those compositions (the same derivatives as the
+// reference's backward formulas).  CPU tensors run loops restating the reference's kernels.
+#include "tpw_common.h"
+
+#include <ATen/Parallel.h>
+#include <ATen/core/dispatch/Dispatcher.h>
+#include <torch/autograd.h>
+
+#include <cmath>
+
+namespace tpw_ext {
+namespace {
+
+using torch::autograd::AutogradContext;
+using torch::autograd::Variable;
+using torch::autograd::variable_list;
+using T2 = std::tuple<at::Tensor, at::Tensor>;
+using T3 = std::tuple<at::Tensor, at::Tensor, at::Tensor>;
+
+template <typename Sig>
+c10::TypedOperatorHandle<Sig> op_handle(const char *name) {
+    return c10::Dispatcher::singleton().findSchemaOrThrow(name, "").typed<Sig>();
+}
+
+inline at::Tensor batched(const at::Tensor &t, bool ub) { return ub ? t.unsqueeze(0).contiguous() : t.contiguous(); }
+inline at::Tensor unbatch(const at::Tensor &t, bool ub) { return ub ? t.squeeze(0) : t; }
+
+template <typename F>
+void for_rows(int64_t rows, F f) {
+    at::parallel_for(0, rows, 1, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; ++r) f(r);
+    });
+}
+
+// ================================================================== haversine
+bool check_haversine(const at::Tensor &x1, const at::Tensor &x2) {  // cpu/haversine_kernel.cpp:32-47
+    at::CheckedFrom c = "_haversine_forward";
+    auto args = {at::TensorArg(x1, "x1", 1), at::TensorArg(x2, "x2", 2)};
+    at::checkAllSameType(c, args);
+    const bool ub = x1.dim() == 2;
+    TORCH_CHECK(ub || x1.dim() == 3, "x1 must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(ub || x2.dim() == 3, "x2 must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(ub || x1.size(0) == x2.size(0), "batch_size of x1 and x2 do not match.")
+    TORCH_CHECK((ub && x1.size(1) == 2 && x2.size(1) == 2) || (!ub && x1.size(2) == 2 && x2.size(2) == 2),
+                "feature dimension of x1 and x2 must be 2.")
+    return ub;
+}
+
+at::Tensor haversine_cpu(const at::Tensor &x1, const at::Tensor &x2) {
+    const bool ub = check_haversine(x1, x2);
+    auto a = batched(x1, ub), b = batched(x2, ub);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1);
+    auto out = at::empty({B, n, m}, a.options());
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_haversine_cpu", [&] {
+        using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
+        const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>();
+        scalar_t *O = out.data_ptr<scalar_t>();
+        for_rows(B * n, [&](int64_t r) {  // cpu/haversine_kernel.cpp:22-24
+            const int64_t bb = r / n;
+            const acc_t la = P[2 * r], lo = P[2 * r + 1];
+            for (int64_t j = 0; j < m; ++j) {
+                const acc_t lb = Q[2 * (bb * m + j)], lob = Q[2 * (bb * m + j) + 1];
+                const acc_t sa = std::sin((la - lb) / 2), so = std::sin((lo - lob) / 2);
+                O[r * m + j] = (scalar_t)(2 * std::asin(std::sqrt(sa * sa + std::cos(la) * std::cos(lb) * so * so)));
+            }
+        });
+    });
+    return unbatch(out, ub);
+}
+
+T2 haversine_backward_cpu(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2) {
+    const bool ub = x1.dim() == 2;
+    auto a = batched(x1, ub), b = batched(x2, ub), g = batched(grad, ub);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1);
+    auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(b);
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_haversine_backward_cpu", [&] {
+        using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
+        const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>(), *G = g.data_ptr<scalar_t>();
+        scalar_t *GX1 = gx1.data_ptr<scalar_t>(), *GX2 = gx2.data_ptr<scalar_t>();
+        // per pair: grad / (sqrt(val) sqrt(1 - val)) (cpu/haversine_kernel.cpp:88-93)
+        auto weight = [&](int64_t bb, int64_t i, int64_t j) -> acc_t {
+            const acc_t la = P[2 * (bb * n + i)], lo = P[2 * (bb * n + i) + 1];
+            const acc_t lb = Q[2 * (bb * m + j)], lob = Q[2 * (bb * m + j) + 1];
+            const acc_t sa = std::sin((la - lb) / 2), so = std::sin((lo - lob) / 2);
+            const acc_t val = sa * sa + std::cos(la) * std::cos(lb) * so * so;
+            return (acc_t)G[(bb * n + i) * m + j] / (std::sqrt(val) * std::sqrt(1 - val));
+        };
+        for_rows(B * n, [&](int64_t r) {  // :111-116
+            const int64_t bb = r / n, i = r % n;
+            const acc_t la = P[2 * r], lo = P[2 * r + 1];
+            acc_t dlat = 0, dlon = 0;
+            for (int64_t j = 0; j < m; ++j) {
+                const acc_t lb = Q[2 * (bb * m + j)], lob = Q[2 * (bb * m + j) + 1], w = weight(bb, i, j);
+                const acc_t so = std::sin((lo - lob) / 2);
+                dlat += w * (-std::sin(la) * so * so * std::cos(lb) + std::sin(la - lb) / 2);
+                dlon += w * (so * std::cos(la) * std::cos(lb) * std::cos((lo - lob) / 2));
+            }
+            GX1[2 * r] = (scalar_t)dlat;
+            GX1[2 * r + 1] = (scalar_t)dlon;
+        });
+        for_rows(B * m, [&](int64_t r) {  // :138-143
+            const int64_t bb = r / m, j = r % m;
+            const acc_t lb = Q[2 * r], lob = Q[2 * r + 1];
+            acc_t dlat = 0, dlon = 0;
+            for (int64_t i = 0; i < n; ++i) {
+                const acc_t la = P[2 * (bb * n + i)], lo = P[2 * (bb * n + i) + 1], w = weight(bb, i, j);
+                const acc_t so = std::sin((lo - lob) / 2);
+                dlat += w * (-std::sin(lb) * so * so * std::cos(la) - std::sin(la - lb) / 2);
+                dlon += w * (-so * std::cos(la) * std::cos(lb) * std::cos((lo - lob) / 2));
+            }
+            GX2[2 * r] = (scalar_t)dlat;
+            GX2[2 * r + 1] = (scalar_t)dlon;
+        });
+    });
+    return {unbatch(gx1, ub), unbatch(gx2, ub)};
+}
+
+at::Tensor gpu_f32(const at::Tensor &t, const char *from) {
+    TORCH_CHECK_NOT_IMPLEMENTED(t.scalar_type() != at::kDouble, from,
+                                ": float64 GPU tensors are not served by this build's fp32 "
+                                "kernels (use float32, or CPU tensors)");
+    return t.to(at::kFloat).contiguous();
+}
+
+at::Tensor haversine_cuda(const at::Tensor &x1, const at::Tensor &x2) {
+    const bool ub = check_haversine(x1, x2);
+    DeviceGuard guard(x1.device());
+    auto a = batched(gpu_f32(x1, "_haversine"), ub), b = batched(gpu_f32(x2, "_haversine"), ub);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1);
+    auto out = at::empty({B, n, m}, a.options());
+    auto ws = workspace(tpw_haversine_workspace_size(B, n, m), a);
+    check_rc(tpw_haversine(a.data_ptr<float>(), b.data_ptr<float>(), B, n, m, out.data_ptr<float>(),
+                           ws.data_ptr(), current_stream()),
+             "_haversine");
+    return unbatch(out, ub).to(x1.scalar_type());
+}
+
+T2 haversine_backward_cuda(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2) {
+    const bool ub = x1.dim() == 2;
+    DeviceGuard guard(x1.device());
+    auto a = batched(gpu_f32(x1, "_haversine_backward"), ub), b = batched(gpu_f32(x2, "_haversine_backward"), ub);
+    auto g = batched(gpu_f32(grad, "_haversine_backward"), ub);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1);
+    auto gx1 = at::empty_like(a), gx2 = at::empty_like(b);
+    auto ws = workspace(tpw_haversine_workspace_size(B, n, m), a);
+    check_rc(tpw_haversine_backward(g.data_ptr<float>(), a.data_ptr<float>(), b.data_ptr<float>(), B, n, m,
+                                    gx1.data_ptr<float>(), gx2.data_ptr<float>(), ws.data_ptr(),
+                                    current_stream()),
+             "_haversine_backward");
+    return {unbatch(gx1, ub).to(x1.scalar_type()), unbatch(gx2, ub).to(x2.scalar_type())};
+}
+
+// ================================================================== snr
+bool check_snr(const at::Tensor &x1, const at::Tensor &x2) {  // cpu/snr_kernel.cpp:70-85
+    at::CheckedFrom c = "_snr_forward";
+    auto args = {at::TensorArg(x1, "x1", 1), at::TensorArg(x2, "x2", 2)};
+    at::checkAllSameType(c, args);
+    const bool ub = x1.dim() == 2;
+    TORCH_CHECK(ub || x1.dim() == 3, "x1 must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(ub || x2.dim() == 3, "x2 must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(ub || (x1.size(0) == x2.size(0)), "batch_size of x1 and x2 do not match.")
+    TORCH_CHECK((ub && x1.size(1) == x2.size(1)) || (!ub && x1.size(2) == x2.size(2)),
+                "feature dimension of x1 and x2 do not match.")
+    return ub;
+}
+
+// The reference's two passes per pair: mean of d = x2[j] - x1[i], then sum (d - mean)^2.
+template <typename acc_t, typename scalar_t>
+void snr_pair_stats(const scalar_t *u, const scalar_t *v, int64_t d, acc_t &mean, acc_t &var) {
+    mean = 0;
+    for (int64_t k = 0; k < d; ++k) mean += (acc_t)v[k] - (acc_t)u[k];
+    mean /= (acc_t)d;
+    var = 0;
+    for (int64_t k = 0; k < d; ++k) {
+        const acc_t t = (acc_t)v[k] - (acc_t)u[k] - mean;
+        var += t * t;
+    }
+}
+
+at::Tensor snr_cpu(const at::Tensor &x1, const at::Tensor &x2) {
+    const bool ub = check_snr(x1, x2);
+    auto a = batched(x1, ub), b = batched(x2, ub);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options());
+    auto v1 = at::var(a, at::IntArrayRef{2}, /*unbiased=*/false).mul_(d).contiguous();  // cpu/snr_kernel.cpp:96
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_snr_cpu", [&] {
+        using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
+        const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>(), *V = v1.data_ptr<scalar_t>();
+        scalar_t *O = out.data_ptr<scalar_t>();
+        for_rows(B * n, [&](int64_t r) {  // cpu/snr_kernel.cpp:13-33
+            const int64_t bb = r / n;
+            for (int64_t j = 0; j < m; ++j) {
+                acc_t mean, var;
+                snr_pair_stats<acc_t>(P + r * d, Q + (bb * m + j) * d, d, mean, var);
+                O[r * m + j] = (scalar_t)((acc_t)V[r] / var);
+            }
+        });
+    });
+    return unbatch(out, ub);
+}
+
+T2 snr_backward_cpu(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2) {
+    const bool ub = x1.dim() == 2;
+    auto a = batched(x1, ub), b = batched(x2, ub), g = batched(grad, ub);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(b);
+    auto mu1 = a.mean(2).contiguous();
+    auto v1 = at::var(a, at::IntArrayRef{2}, /*unbiased=*/false).mul_(d).contiguous();
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_snr_backward_cpu", [&] {
+        using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
+        const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>(), *G = g.data_ptr<scalar_t>();
+        const scalar_t *MU = mu1.data_ptr<scalar_t>(), *V = v1.data_ptr<scalar_t>();
+        scalar_t *GX1 = gx1.data_ptr<scalar_t>(), *GX2 = gx2.data_ptr<scalar_t>();
+        // cpu/snr_kernel.cpp:118-143 (x1) and 145-168 (x2)
+        for_rows(B * n, [&](int64_t r) {
+            const int64_t bb = r / n;
+            for (int64_t j = 0; j < m; ++j) {
+                const scalar_t *u = P + r * d, *v = Q + (bb * m + j) * d;
+                acc_t mean, var;
+                snr_pair_stats<acc_t>(u, v, d, mean, var);
+                const acc_t gv = G[r * m + j];
+                for (int64_t k = 0; k < d; ++k)
+                    GX1[r * d + k] = (scalar_t)((acc_t)GX1[r * d + k] +
+                        gv * 2 * ((-(acc_t)MU[r] + (acc_t)u[k]) + (-mean + (acc_t)v[k] - (acc_t)u[k]) * (acc_t)V[r] / var) / var);
+            }
+        });
+        for_rows(B * m, [&](int64_t r) {
+            const int64_t bb = r / m, j = r % m;
+            for (int64_t i = 0; i < n; ++i) {
+                const scalar_t *u = P + (bb * n + i) * d, *v = Q + r * d;
+                acc_t mean, var;
+                snr_pair_stats<acc_t>(u, v, d, mean, var);
+                const acc_t gv = G[(bb * n + i) * m + j];
+                for (int64_t k = 0; k < d; ++k)
+                    GX2[r * d + k] = (scalar_t)((acc_t)GX2[r * d + k] +
+                        gv * 2 * (-mean + (acc_t)v[k] - (acc_t)u[k]) * -(acc_t)V[bb * n + i] / (var * var));
+            }
+        });
+    });
+    return {unbatch(gx1, ub), unbatch(gx2, ub)};
+}
+
+// GPU composition (differentiable: autograd runs through it when called with grad mode on)
+at::Tensor snr_composite(const at::Tensor &x1, const at::Tensor &x2) {
+    check_snr(x1, x2);
+    auto a = x1 - x1.mean(-1, true);
+    auto b = x2 - x2.mean(-1, true);
+    auto v1 = (a * a).sum(-1, true);
+    return v1 / ppminkowski(a, b, 2);
+}
+
+at::Tensor snr_cuda(const at::Tensor &x1, const at::Tensor &x2) { return snr_composite(x1, x2); }
+
+// Gradients of a GPU composition by autograd, whatever the caller's grad mode.
+template <typename F>
+variable_list composite_grads(F f, const at::Tensor &grad, std::vector<at::Tensor> inputs) {
+    at::AutoGradMode enable(true);
+    std::vector<Variable> vars;
+    for (auto &t : inputs) vars.push_back(t.detach().requires_grad_(true));
+    auto out = f(vars);
+    return torch::autograd::grad({out}, vars, {grad}, /*retain_graph=*/false, /*create_graph=*/false,
+                                 /*allow_unused=*/true);
+}
+
+T2 snr_backward_cuda(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2) {
+    auto g = composite_grads([](const std::vector<Variable> &v) { return snr_composite(v[0], v[1]); },
+                             grad, {x1, x2});
+    return {g[0], g[1]};
+}
+
+// ================================================================== sqmahalanobis
+bool check_mahalanobis(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
+    at::CheckedFrom c = "_sqmahalanobis_forward";  // cpu/sqmahalanobis_kernel.cpp:42-60
+    auto args = {at::TensorArg(x1, "x1", 1), at::TensorArg(x2, "x2", 2), at::TensorArg(VI, "VI", 3)};
+    at::checkAllSameType(c, args);
+    const bool ub = x1.dim() == 2;
+    TORCH_CHECK(ub || x1.dim() == 3, "x1 must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(ub || x2.dim() == 3, "x2 must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(ub || VI.dim() == 3, "VI must be 2-D (unbatched) or 3-D (batched) tensor.")
+    TORCH_CHECK(ub || (x1.size(0) == x2.size(0) && x1.size(0) == VI.size(0)),
+                "batch_size of x1, x2, and VI do not match.")
+    TORCH_CHECK((ub && x1.size(1) == x2.size(1) && x1.size(1) == VI.size(0)) ||
+                    (!ub && x1.size(2) == x2.size(2) && x1.size(2) == VI.size(1)),
+                "feature dimension of x1, x2, and VI do not match.")
+    return ub;
+}
+
+at::Tensor sqmahalanobis_cpu(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
+    const bool ub = check_mahalanobis(x1, x2, VI);
+    auto a = batched(x1, ub), b = batched(x2, ub), w = batched(VI, ub);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options());
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_sqmahalanobis_cpu", [&] {
+        using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
+        const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>(), *W = w.data_ptr<scalar_t>();
+        scalar_t *O = out.data_ptr<scalar_t>();
+        for_rows(B * n, [&](int64_t r) {  // cpu/sqmahalanobis_kernel.cpp:13-33
+            const int64_t bb = r / n;
+            for (int64_t j = 0; j < m; ++j) {
+                const scalar_t *u = P + r * d, *v = Q + (bb * m + j) * d;
+                acc_t val = 0;
+                for (int64_t k = 0; k < d; ++k)
+                    for (int64_t l = 0; l < d; ++l)
+                        val += ((acc_t)u[k] - (acc_t)v[k]) * (acc_t)W[(bb * d + k) * d + l] * ((acc_t)u[l] - (acc_t)v[l]);
+                O[r * m + j] = (scalar_t)val;
+            }
+        });
+    });
+    return unbatch(out, ub);
+}
+
+T3 sqmahalanobis_backward_cpu(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2,
+                              const at::Tensor &VI) {
+    const bool ub = x1.dim() == 2;
+    auto a = batched(x1, ub), b = batched(x2, ub), w = batched(VI, ub), g = batched(grad, ub);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(b), gw = at::zeros_like(w);
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_sqmahalanobis_backward_cpu", [&] {
+        using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
+        const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>(), *W = w.data_ptr<scalar_t>();
+        const scalar_t *G = g.data_ptr<scalar_t>();
+        scalar_t *GX1 = gx1.data_ptr<scalar_t>(), *GX2 = gx2.data_ptr<scalar_t>(), *GW = gw.data_ptr<scalar_t>();
+        // d/dx1[k] of sum_kl d_k VI_kl d_l = sum_l (VI_kl + VI_lk) d_l (cpu/sqmahalanobis_kernel.cpp:93-139)
+        for_rows(B * n, [&](int64_t r) {
+            const int64_t bb = r / n;
+            for (int64_t k = 0; k < d; ++k) {
+                acc_t s = 0;
+                for (int64_t j = 0; j < m; ++j) {
+                    const scalar_t *v = Q + (bb * m + j) * d;
+                    acc_t t = 0;
+                    for (int64_t l = 0; l < d; ++l) {
+                        const acc_t dl = (acc_t)P[r * d + l] - (acc_t)v[l];
+                        t += ((acc_t)W[(bb * d + k) * d + l] + (acc_t)W[(bb * d + l) * d + k]) * dl;
+                    }
+                    s += (acc_t)G[r * m + j] * t;
+                }
+                GX1[r * d + k] = (scalar_t)s;
+            }
+        });
+        for_rows(B * m, [&](int64_t r) {
+            const int64_t bb = r / m, j = r % m;
+            for (int64_t k = 0; k < d; ++k) {
+                acc_t s = 0;
+                for (int64_t i = 0; i < n; ++i) {
+                    const scalar_t *u = P + (bb * n + i) * d;
+                    acc_t t = 0;
+                    for (int64_t l = 0; l < d; ++l) {
+                        const acc_t dl = (acc_t)u[l] - (acc_t)Q[r * d + l];
+                        t += ((acc_t)W[(bb * d + k) * d + l] + (acc_t)W[(bb * d + l) * d + k]) * dl;
+                    }
+                    s -= (acc_t)G[(bb * n + i) * m + j] * t;
+                }
+                GX2[r * d + k] = (scalar_t)s;
+            }
+        });
+        for_rows(B * d * d, [&](int64_t r) {  // :142-164
+            const int64_t bb = r / (d * d), k = (r / d) % d, l = r % d;
+            acc_t s = 0;
+            for (int64_t i = 0; i < n; ++i)
+                for (int64_t j = 0; j < m; ++j)
+                    s += (acc_t)G[(bb * n + i) * m + j] * ((acc_t)P[(bb * n + i) * d + k] - (acc_t)Q[(bb * m + j) * d + k]) *
+                         ((acc_t)P[(bb * n + i) * d + l] - (acc_t)Q[(bb * m + j) * d + l]);
+            GW[r] = (scalar_t)s;
+        });
+    });
+    return {unbatch(gx1, ub), unbatch(gx2, ub), unbatch(gw, ub)};
+}
+
+// GPU composition: q1 + q2 - x1 (VI + VI^T) x2^T (library GEMMs; right operands contiguous)
+at::Tensor sqmahalanobis_composite(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
+    check_mahalanobis(x1, x2, VI);
+    auto q1 = (at::matmul(x1, VI) * x1).sum(-1);
+    auto q2 = (at::matmul(x2, VI) * x2).sum(-1);
+    auto cross = at::matmul(at::matmul(x1, (VI + VI.mT()).contiguous()), x2.mT().contiguous());
+    return q1.unsqueeze(-1) + q2.unsqueeze(-2) - cross;
+}
+
+at::Tensor sqmahalanobis_cuda(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
+    return sqmahalanobis_composite(x1, x2, VI);
+}
+
+T3 sqmahalanobis_backward_cuda(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2,
+                               const at::Tensor &VI) {
+    auto g = composite_grads(
+        [](const std::vector<Variable> &v) { return sqmahalanobis_composite(v[0], v[1], v[2]); }, grad,
+        {x1, x2, VI});
+    return {g[0], g[1], g[2]};
+}
+
+// ================================================================== autograd
+T2 haversine_backward_op(const at::Tensor &g, const at::Tensor &x1, const at::Tensor &x2) {
+    static auto op = op_handle<T2(const at::Tensor &, const at::Tensor &, const at::Tensor &)>(
+        "torchpairwise::__haversine_backward");
+    return op.call(g, x1, x2);
+}
+T2 snr_backward_op(const at::Tensor &g, const at::Tensor &x1, const at::Tensor &x2) {
+    static auto op = op_handle<T2(const at::Tensor &, const at::Tensor &, const at::Tensor &)>(
+        "torchpairwise::__snr_backward");
+    return op.call(g, x1, x2);
+}
+T3 sqmahalanobis_backward_op(const at::Tensor &g, const at::Tensor &x1, const at::Tensor &x2,
+                             const at::Tensor &VI) {
+    static auto op = op_handle<T3(const at::Tensor &, const at::Tensor &, const at::Tensor &, const at::Tensor &)>(
+        "torchpairwise::__sqmahalanobis_backward");
+    return op.call(g, x1, x2, VI);
+}
+at::Tensor haversine_op(const at::Tensor &x1, const at::Tensor &x2) {
+    static auto op = op_handle<at::Tensor(const at::Tensor &, const at::Tensor &)>("torchpairwise::_haversine");
+    return op.call(x1, x2);
+}
+at::Tensor snr_op(const at::Tensor &x1, const at::Tensor &x2) {
+    static auto op = op_handle<at::Tensor(const at::Tensor &, const at::Tensor &)>("torchpairwise::_snr");
+    return op.call(x1, x2);
+}
+at::Tensor sqmahalanobis_op(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
+    static auto op = op_handle<at::Tensor(const at::Tensor &, const at::Tensor &, const at::Tensor &)>(
+        "torchpairwise::_sqmahalanobis");
+    return op.call(x1, x2, VI);
+}
+
+class HaversineFunction : public torch::autograd::Function<HaversineFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x1, const Variable &x2) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        ctx->save_for_backward({x1, x2});
+        return haversine_op(x1, x2);
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad) {
+        auto s = ctx->get_saved_variables();
+        auto r = haversine_backward_op(grad[0], s[0], s[1]);
+        return {std::get<0>(r), std::get<1>(r)};
+    }
+};
+
+class SnrFunction : public torch::autograd::Function<SnrFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x1, const Variable &x2) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        ctx->save_for_backward({x1, x2});
+        return snr_op(x1, x2);
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad) {
+        auto s = ctx->get_saved_variables();
+        auto r = snr_backward_op(grad[0], s[0], s[1]);
+        return {std::get<0>(r), std::get<1>(r)};
+    }
+};
+
+class SqMahalanobisFunction : public torch::autograd::Function<SqMahalanobisFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x1, const Variable &x2, const Variable &VI) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        ctx->save_for_backward({x1, x2, VI});
+        return sqmahalanobis_op(x1, x2, VI);
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad) {
+        auto s = ctx->get_saved_variables();
+        auto r = sqmahalanobis_backward_op(grad[0], s[0], s[1], s[2]);
+        return {std::get<0>(r), std::get<1>(r), std::get<2>(r)};
+    }
+};
+
+// GPU tensors differentiate through the composition itself (one graph of the VALU kernel's
+// and the GEMMs' own backward); CPU tensors through the reference-formula backward op.
+at::Tensor haversine_autograd(const at::Tensor &x1, const at::Tensor &x2) {
+    return HaversineFunction::apply(x1, x2);
+}
+at::Tensor snr_autograd(const at::Tensor &x1, const at::Tensor &x2) {
+    if (x1.is_cuda()) return snr_composite(x1, x2);
+    return SnrFunction::apply(x1, x2);
+}
+at::Tensor sqmahalanobis_autograd(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
+    if (x1.is_cuda()) return sqmahalanobis_composite(x1, x2, VI);
+    return SqMahalanobisFunction::apply(x1, x2, VI);
+}
+
+}  // namespace
+
+// public handles (the reference's functors call these internal ops)
+at::Tensor haversine(const at::Tensor &x1, const at::Tensor &x2) { return haversine_op(x1, x2); }
+at::Tensor snr(const at::Tensor &x1, const at::Tensor &x2) { return snr_op(x1, x2); }
+at::Tensor sqmahalanobis(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
+    return sqmahalanobis_op(x1, x2, VI);
+}
+
+// schemas: csrc/ops/{haversine,snr,sqmahalanobis}.cpp:30-39
+TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
+    m.def("_haversine(Tensor x1, Tensor x2) -> Tensor");
+    m.def("__haversine_backward(Tensor grad, Tensor x1, Tensor x2) -> (Tensor grad_x1, Tensor grad_x2)");
+    m.def("_snr(Tensor x1, Tensor x2) -> Tensor");
+    m.def("__snr_backward(Tensor grad, Tensor x1, Tensor x2) -> (Tensor grad_x1, Tensor grad_x2)");
+    m.def("_sqmahalanobis(Tensor x1, Tensor x2, Tensor VI) -> Tensor");
+    m.def("__sqmahalanobis_backward(Tensor grad, Tensor x1, Tensor x2, Tensor VI) -> (Tensor grad_x1, Tensor grad_x2, Tensor grad_VI)");
+}
+
+TORCH_LIBRARY_IMPL(torchpairwise, CPU, m) {
+    m.impl("_haversine", TORCH_FN(haversine_cpu));
+    m.impl("__haversine_backward", TORCH_FN(haversine_backward_cpu));
+    m.impl("_snr", TORCH_FN(snr_cpu));
+    m.impl("__snr_backward", TORCH_FN(snr_backward_cpu));
+    m.impl("_sqmahalanobis", TORCH_FN(sqmahalanobis_cpu));
+    m.impl("__sqmahalanobis_backward", TORCH_FN(sqmahalanobis_backward_cpu));
+}
+
+TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
+    m.impl("_haversine", TORCH_FN(haversine_cuda));
+    m.impl("__haversine_backward", TORCH_FN(haversine_backward_cuda));
+    m.impl("_snr", TORCH_FN(snr_cuda));
+    m.impl("__snr_backward", TORCH_FN(snr_backward_cuda));
+    m.impl("_sqmahalanobis", TORCH_FN(sqmahalanobis_cuda));
+    m.impl("__sqmahalanobis_backward", TORCH_FN(sqmahalanobis_backward_cuda));
+}
+
+TORCH_LIBRARY_IMPL(torchpairwise, Autograd, m) {
+    m.impl("_haversine", TORCH_FN(haversine_autograd));
+    m.impl("_snr", TORCH_FN(snr_autograd));
+    m.impl("_sqmahalanobis", TORCH_FN(sqmahalanobis_autograd));
+}
+
+}  // namespace tpw_ext

@@ -75,6 +75,12 @@ at::Tensor ppminkowski(const at::Tensor &x1, const at::Tensor &x2, double p);
 at::Tensor wminkowski(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &w, double p);
 at::Tensor canberra(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor braycurtis(const at::Tensor &x1, const at::Tensor &x2);
+at::Tensor additive_chi2(const at::Tensor &x1, const at::Tensor &x2);
+at::Tensor sqjensenshannon(const at::Tensor &x1, const at::Tensor &x2, c10::optional<double> base);
+// haversine, snr, squared mahalanobis (special.cpp)
+at::Tensor haversine(const at::Tensor &x1, const at::Tensor &x2);
+at::Tensor snr(const at::Tensor &x1, const at::Tensor &x2);
+at::Tensor sqmahalanobis(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI);
 at::Tensor prf_div(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
 std::tuple<at::Tensor, at::Tensor> prf_div_backward(const at::Tensor &g, const at::Tensor &x,
                                                     const at::Tensor &y, c10::string_view mode);

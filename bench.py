@@ -188,6 +188,22 @@ def run_config(cfg, steps, warmup):
         j2 = (torch.rand(N, D, generator=torch.Generator().manual_seed(1)) < 0.1).to(dev)
         ms, _ = time_op(lambda: tp.jaccard_distances(j1, j2), steps, warmup)
         emit("jaccard fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+        # the other boolean count metrics: one fused pass (pack + AND-popcount tile with the
+        # metric's epilogue), the same on rows packed once (PackedBool), and the reference's
+        # composite (2-4 pw*_sum passes + ATen elementwise passes) on the same GPU
+        ops = torch.ops.torchpairwise
+        p1, p2 = tp.PackedBool.pack(h1), tp.PackedBool.pack(h2)
+        for metric in ("dice", "yule"):
+            f = getattr(tp, f"{metric}_distances")
+            ms, _ = time_op(lambda: f(h1, h2), steps, warmup)
+            emit(f"{metric} fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+            ms, _ = time_op(lambda: tp.packed.cdist(p1, p2, metric), steps, warmup)
+            emit(f"{metric} fwd on PackedBool", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+        def dice_composite():
+            R = ops.pwxor_sum(h1, h2)
+            return R / (2 * ops.pwand_sum(h1, h2) + R)
+        ms, _ = time_op(dice_composite, steps, warmup)
+        emit("dice fwd, reference composite route", ms, pf)
     elif cfg == "C5":
         C, P, D = 16, 65536, 3
         x1 = torch.rand(C, P, D, generator=torch.Generator().manual_seed(0)).to(dev)

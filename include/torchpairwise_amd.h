@@ -103,6 +103,40 @@ int tpw_jaccard_bool(const uint32_t *x1_words, const uint32_t *x2_words,
                      int64_t batch, int64_t n, int64_t m, int64_t d, float *out,
                      void *stream);
 
+/* Boolean count metrics of tpw_bool_count_metric */
+#define TPW_BMET_HAMMING 0
+#define TPW_BMET_JACCARD 1
+#define TPW_BMET_DICE 2
+#define TPW_BMET_KULCZYNSKI1 3
+#define TPW_BMET_KULSINSKI 4
+#define TPW_BMET_ROGERSTANIMOTO 5
+#define TPW_BMET_RUSSELLRAO 6
+#define TPW_BMET_SOKALMICHENER 7
+#define TPW_BMET_SOKALSNEATH 8
+#define TPW_BMET_YULE 9
+
+/* One pass for any boolean count metric of packed rows with their popcounts (both from
+ * tpw_pack_bool_rows): the tile counts and = popcount(a & b) per pair; xor = pa + pb - 2 and,
+ * or = pa + pb - and, eq = d - xor, a & ~b = pa - and, ~a & b = pb - and,
+ * ~a & ~b = d - pa - pb + and.  Each count is then what the reference's float32 pw*_sum
+ * accumulator holds (exact below 2^24, then 2^24), and the output follows the reference's
+ * float32 composite over those counts in its operation order, without contraction:
+ *   HAMMING        pwne_mean                       (pairwise_metrics.cpp:206-213)
+ *   JACCARD        prf_div(xor, or, "zero")        (:215-222)
+ *   KULSINSKI      (xor - and + d) / (xor + d)     (:224-234)
+ *   KULCZYNSKI1    and / xor                       (:236-243)
+ *   YULE           prf_div(2 hR, and nor + hR), hR = (a & ~b)(~a & b)   (:339-347)
+ *   DICE           xor / (2 and + xor)             (:349-357)
+ *   ROGERSTANIMOTO, SOKALMICHENER  2 xor / (eq + 2 xor)   (:359-368, :379-388)
+ *   RUSSELLRAO     (d - and) * fl(1 / d): the reference's GPU route, where ATen divides a
+ *                  tensor by a CPU scalar as a multiply by the float reciprocal (:370-377)
+ *   SOKALSNEATH    2 xor / (and + 2 xor)           (:390-399)
+ * Replaces the 2-4 pw*_sum passes and the elementwise passes of each composite. */
+int tpw_bool_count_metric(const uint32_t *x1_words, const uint32_t *x2_words,
+                          const int32_t *x1_popcounts, const int32_t *x2_popcounts,
+                          int64_t batch, int64_t n, int64_t m, int64_t d, int metric, float *out,
+                          void *stream);
+
 /* Equal / not-equal counts (TPW_BIT_EQ / TPW_BIT_NE, TPW_RED_SUM / TPW_RED_MEAN) of
  * non-bool inputs of element type `elem_type` (TPW_F32 ... TPW_I64), compared by value
  * like C++ ==; output float32 [batch, n, m] as tpw_bool_pairwise_reduce.

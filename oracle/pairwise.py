@@ -93,6 +93,68 @@ def jaccard_distances(x1, x2=None) -> np.ndarray:
     return np.where(o == 0, np.float32(0), q).astype(np.float32)
 
 
+BOOL_COUNT_METRICS = ("hamming", "jaccard", "dice", "kulczynski1", "kulsinski", "rogerstanimoto",
+                      "russellrao", "sokalmichener", "sokalsneath", "yule")
+
+
+def bool_count_metric(x1, x2, metric: str, gpu_scalar_divide: bool = False) -> np.ndarray:
+    """The reference's boolean count metrics as float32 composites over the pw*_sum counts
+    (csrc/ops/pairwise_metrics.cpp:206-243,339-399), one numpy float32 rounding per operation
+    in the composite's order.  Counts are float accumulators of ones (float_accumulated).
+    ``gpu_scalar_divide`` evaluates russellrao's ``/ d`` as ATen's GPU route does (a multiply
+    by the float reciprocal of the CPU scalar, torch/aten/src/ATen/native/cuda/
+    BinaryDivTrueKernel.cu); the CPU route divides."""
+    a, b = np.asarray(x1).astype(bool), np.asarray(x2).astype(bool)
+    d = a.shape[-1]
+    f = np.float32
+    AND = float_accumulated(bool_counts(a, b, "and"))
+    XOR = float_accumulated(bool_counts(a, b, "xor"))
+    df = f(d)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        if metric == "hamming":
+            return pw_reduce_bool(a, b, "ne", "mean")
+        if metric == "jaccard":
+            return jaccard_distances(a, b)
+        if metric == "dice":
+            return (XOR / (f(2) * AND + XOR)).astype(f)
+        if metric == "kulczynski1":
+            return (AND / XOR).astype(f)
+        if metric == "kulsinski":
+            return (((XOR - AND) + df) / (XOR + df)).astype(f)
+        if metric in ("rogerstanimoto", "sokalmichener"):
+            R = f(2) * XOR
+            EQ = float_accumulated(bool_counts(a, b, "eq"))
+            return (R / (EQ + R)).astype(f)
+        if metric == "russellrao":
+            num = (df - AND).astype(f)
+            return (num * (f(1) / df) if gpu_scalar_divide else num / df).astype(f)
+        if metric == "sokalsneath":
+            R = f(2) * XOR
+            return (R / (AND + R)).astype(f)
+        if metric == "yule":
+            n10 = float_accumulated(bool_counts(a, ~b, "and"))
+            n01 = float_accumulated(bool_counts(~a, b, "and"))
+            n00 = float_accumulated(bool_counts(~a, ~b, "and"))
+            hR = (n10 * n01).astype(f)
+            den = ((AND * n00).astype(f) + hR).astype(f)
+            q = (f(2) * hR / np.where(den == 0, f(1), den)).astype(f)
+            return np.where(den == 0, f(0), q).astype(f)
+    raise ValueError(metric)
+
+
+def pack_bool_words(x) -> tuple[np.ndarray, np.ndarray]:
+    """Rows of bools -> (uint32 words [..., W], int32 popcounts [...]): bit k at word k // 32,
+    bit k % 32, W = ceil(d / 32) rounded up to a multiple of 4, zero padding."""
+    x = np.asarray(x, bool)
+    d = x.shape[-1]
+    W = ((d + 31) // 32 + 3) // 4 * 4
+    by = np.packbits(x.astype(np.uint8), axis=-1, bitorder="little")
+    full = np.zeros(x.shape[:-1] + (4 * W,), np.uint8)
+    full[..., :by.shape[-1]] = by
+    words = np.ascontiguousarray(full).view("<u4")
+    return words, x.sum(-1).astype(np.int32)
+
+
 # -------------------------------------------------------------------------------------
 # ATen-routed metrics: the reference calls at::cdist, so torch.cdist on CPU is its
 # arithmetic (csrc/ops/pairwise_metrics.cpp:24-31 euclidean p=2, :42-49 manhattan p=1,

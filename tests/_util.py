@@ -35,13 +35,17 @@ def assert_close(actual, expected, *, rtol: float, atol: float, what: str = ""):
             f"worst at flat {idx}: got {a.flatten()[idx].item()!r} want {e.flatten()[idx].item()!r}")
 
 
-def assert_equal(actual, expected, what: str = ""):
+def assert_equal(actual, expected, what: str = "", nan_payload: bool = True):
+    """Bit-for-bit equality; with ``nan_payload=False`` NaNs must sit at the same positions but
+    may differ in sign and payload (devices produce different NaN bit patterns for 0 / 0)."""
     a = torch.as_tensor(actual).detach().cpu()
     e = torch.as_tensor(expected).detach().cpu()
     assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
     if a.dtype.is_floating_point:
         same = (a.view(torch.int32 if a.dtype == torch.float32 else torch.int64) ==
                 e.to(a.dtype).view(torch.int32 if a.dtype == torch.float32 else torch.int64))
+        if not nan_payload:
+            same = same | (torch.isnan(a) & torch.isnan(e.to(a.dtype)))
     else:
         same = a == e
     if not bool(same.all()):

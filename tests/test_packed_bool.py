@@ -1,0 +1,194 @@
+"""The persistent packed-bool format and the one-pass boolean count metrics.
+
+CPU: _pack_bool against numpy packbits (the oracle's restatement of the layout), the packed
+metrics against the public boolean metrics (the reference's composites) bit-exact, the oracle
+restatement of those composites against scipy and against the composites themselves.
+GPU: the C ABI and the ops against the reference's composites evaluated on the GPU (the pw*_sum
+ops and ATen's elementwise GPU kernels, as the reference runs them) bit-exact.
+"""
+import warnings
+
+import numpy as np
+import pytest
+import torch
+from scipy.spatial.distance import cdist as scipy_cdist
+
+import torchpairwise_amd as tp
+from oracle import pairwise as P
+from tests._util import assert_equal, rand
+from torchpairwise_amd import _capi as capi
+
+DEV = "cuda"
+COUNT = P.BOOL_COUNT_METRICS
+PW = ("pwand_sum", "pwor_sum", "pwxor_sum", "pweq_sum", "pwne_sum", "pweq_mean", "pwne_mean")
+DS = (1, 31, 32, 33, 100, 129, 1024)
+
+
+def _rows(B, n, m, d, seed):
+    a = (rand(B, n, d, seed=seed) < 0.5)
+    b = (rand(B, m, d, seed=seed + 1) < 0.3)
+    a[:, 0] = False  # all-zero rows: 0 / 0 in dice, kulczynski1, sokalsneath, ...
+    b[:, 1] = False
+    a[:, 2] = True   # all-one row
+    if m > 3:
+        b[:, 3] = a[:, 3 % n]  # an identical pair
+    return a, b
+
+
+def _public(metric, a, b):
+    name = metric if metric.startswith("pw") else f"{metric}_distances"
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        return getattr(tp, name)(a, b)
+
+
+# ----------------------------------------------------------------------------- CPU
+@pytest.mark.parametrize("d", DS)
+def test_pack_bool_layout_and_popcounts(d):
+    a, _ = _rows(2, 9, 4, d, seed=d)
+    words, pops = torch.ops.torchpairwise._pack_bool(a)
+    want_w, want_p = P.pack_bool_words(a.numpy())
+    assert words.dtype == torch.int32 and words.shape == (2, 9, capi.lib().tpw_packed_words(d))
+    assert np.array_equal(words.numpy().view(np.uint32), want_w)
+    assert np.array_equal(pops.numpy(), want_p)
+    p = tp.PackedBool.pack(a[0])
+    assert p.shape == (9, d) and torch.equal(p.unpack(), a[0])
+
+
+@pytest.mark.parametrize("d", DS)
+def test_packed_metrics_cpu_equal_public_ops(d):
+    a, b = _rows(2, 9, 11, d, seed=10 + d)
+    pa, pb = tp.PackedBool.pack(a), tp.PackedBool.pack(b)
+    for metric in COUNT + PW:
+        assert_equal(tp.packed.cdist(pa, pb, metric), _public(metric, a, b), f"{metric} d={d}")
+    assert_equal(tp.packed.dice_distances(pa), _public("dice", a, a), "x2 = None")
+    assert_equal(tp.packed.pwxor_sum(pa, pb), tp.pwxor_sum(a, b), "bound name")
+
+
+def test_oracle_count_metrics_match_scipy_and_the_composites():
+    a, b = _rows(1, 30, 40, 100, seed=3)
+    a, b = a[0].numpy(), b[0].numpy()
+    a[0], b[1] = True, True  # scipy's dice / kulczynski1 / sokalsneath need nonzero denominators
+    names = {"kulczynski1": None, "kulsinski": None}  # no scipy counterpart in this scipy
+    for metric in COUNT:
+        got = P.bool_count_metric(a, b, metric)
+        assert_equal(got, _public(metric, torch.from_numpy(a), torch.from_numpy(b)), metric)
+        if metric in names:
+            continue
+        with warnings.catch_warnings(), np.errstate(divide="ignore", invalid="ignore"):
+            warnings.simplefilter("ignore")
+            want = scipy_cdist(a, b, metric)
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-7, err_msg=metric)
+    # kulczynski1 (a similarity in the reference: and / xor) and kulsinski from their counts
+    n11 = P.bool_counts(a, b, "and")
+    x = P.bool_counts(a, b, "xor")
+    with np.errstate(divide="ignore", invalid="ignore"):
+        np.testing.assert_allclose(P.bool_count_metric(a, b, "kulczynski1"), n11 / x, rtol=1e-6)
+    np.testing.assert_allclose(P.bool_count_metric(a, b, "kulsinski"), (x - n11 + 100) / (x + 100),
+                               rtol=1e-6)
+
+
+def test_pins_catch_or_for_xor_and_a_true_divide_on_the_gpu_route():
+    a, b = _rows(1, 50, 60, 100, seed=5)
+    a, b = a[0].numpy(), b[0].numpy()
+    pub = _public("dice", torch.from_numpy(a), torch.from_numpy(b)).numpy()
+    OR = P.float_accumulated(P.bool_counts(a, b, "or"))
+    AND = P.float_accumulated(P.bool_counts(a, b, "and"))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        wrong = (OR / (np.float32(2) * AND + OR)).astype(np.float32)
+    assert not np.allclose(wrong, pub, equal_nan=True)
+    cpu = P.bool_count_metric(a, b, "russellrao")
+    gpu = P.bool_count_metric(a, b, "russellrao", gpu_scalar_divide=True)
+    assert not np.array_equal(cpu, gpu)  # d = 100: the reciprocal multiply differs somewhere
+    np.testing.assert_allclose(gpu, cpu, rtol=1.2e-7, atol=0)
+
+
+def test_packed_errors():
+    a = tp.PackedBool.pack(torch.ones(3, 40, dtype=torch.bool))
+    b = tp.PackedBool.pack(torch.ones(3, 41, dtype=torch.bool))
+    with pytest.raises(RuntimeError, match="feature dimension"):
+        tp.packed.hamming_distances(a, b)
+    with pytest.raises(RuntimeError, match="unknown metric"):
+        tp.packed.cdist(a, a, "euclidean")
+    with pytest.raises(TypeError):
+        tp.packed.hamming_distances(torch.ones(3, 40, dtype=torch.bool))
+    with pytest.raises(RuntimeError, match="expected a bool tensor"):
+        torch.ops.torchpairwise._pack_bool(torch.ones(3, 4))
+    with pytest.raises(RuntimeError, match="words per row expected"):
+        torch.ops.torchpairwise._packed_bool_metric(a.words, a.popcounts, a.words, a.popcounts, 200, "dice")
+    assert tp.PackedBool.pack(torch.ones(3, 5)).unpack().all()  # non-bool rows are coerced
+
+
+# ----------------------------------------------------------------------------- GPU
+def _gpu_composite(metric, a, b):
+    """The reference's composite for `metric`, evaluated on the GPU with its own ops
+    (pairwise_metrics.cpp:206-243,339-399): the pw*_sum GPU ops and ATen's GPU elementwise
+    kernels, as the reference runs it."""
+    ops = torch.ops.torchpairwise
+    D = a.shape[-1]
+    if metric == "hamming":
+        return ops.pwne_mean(a, b)
+    if metric == "jaccard":
+        return ops.prf_div(ops.pwxor_sum(a, b), ops.pwor_sum(a, b), "zero")
+    if metric == "kulsinski":
+        S = ops.pwxor_sum(a, b)
+        return (S - ops.pwand_sum(a, b) + D) / (S + D)
+    if metric == "kulczynski1":
+        return ops.pwand_sum(a, b) / ops.pwxor_sum(a, b)
+    if metric == "yule":
+        hR = ops.pwand_sum(a, ~b) * ops.pwand_sum(~a, b)
+        return ops.prf_div(2 * hR, ops.pwand_sum(a, b) * ops.pwand_sum(~a, ~b) + hR, "zero")
+    if metric == "dice":
+        R = ops.pwxor_sum(a, b)
+        return R / (2 * ops.pwand_sum(a, b) + R)
+    if metric in ("rogerstanimoto", "sokalmichener"):
+        R = 2 * ops.pwxor_sum(a, b)
+        return R / (ops.pweq_sum(a, b) + R)
+    if metric == "russellrao":
+        return (D - ops.pwand_sum(a, b)) / D
+    R = 2 * ops.pwxor_sum(a, b)  # sokalsneath
+    return R / (ops.pwand_sum(a, b) + R)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", DS)
+@pytest.mark.parametrize("B,n,m", [(1, 130, 257), (2, 64, 33)])
+def test_bool_count_metric_capi_equals_gpu_composites(B, n, m, d):
+    print(f"bool count metrics {B}x{n}x{m} d={d}", flush=True)
+    a, b = _rows(B, n, m, d, seed=20 + d)
+    a, b = a.to(DEV), b.to(DEV)
+    wa, pa = torch.ops.torchpairwise._pack_bool(a)
+    wb, pb = torch.ops.torchpairwise._pack_bool(b)
+    for code, metric in enumerate(COUNT):
+        out = torch.empty(B, n, m, device=DEV)
+        capi.call("tpw_bool_count_metric", capi._ptr(wa), capi._ptr(wb), capi._ptr(pa), capi._ptr(pb),
+                  B, n, m, d, code, capi._ptr(out), capi._stream())
+        assert_equal(out, _gpu_composite(metric, a, b), f"{metric} d={d}", nan_payload=False)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", DS)
+def test_packed_ops_gpu(d):
+    print(f"packed ops d={d}", flush=True)
+    a, b = _rows(2, 70, 45, d, seed=40 + d)
+    wa, pa = torch.ops.torchpairwise._pack_bool(a.to(DEV))
+    wc, pc = torch.ops.torchpairwise._pack_bool(a)
+    assert_equal(wa, wc, "words")
+    assert_equal(pa, pc, "popcounts")
+    ga, gb = tp.PackedBool.pack(a.to(DEV)), tp.PackedBool.pack(b.to(DEV))
+    ca, cb = tp.PackedBool.pack(a), tp.PackedBool.pack(b)
+    for metric in COUNT + PW:
+        got = tp.packed.cdist(ga, gb, metric)
+        assert_equal(got, _gpu_composite(metric, a.to(DEV), b.to(DEV)) if metric in COUNT
+                     else _public(metric, a.to(DEV), b.to(DEV)), f"{metric} d={d}", nan_payload=False)
+        if metric != "russellrao":  # the reference's own CPU and GPU routes differ by 1 ulp there
+            assert_equal(got, tp.packed.cdist(ca, cb, metric), f"{metric} gpu = cpu", nan_payload=False)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("metric", COUNT[2:])
+def test_public_boolean_metrics_take_the_fused_path(metric):
+    a, b = _rows(1, 300, 200, 77, seed=60)
+    a, b = a[0].to(DEV), b[0].to(DEV)
+    assert_equal(_public(metric, a, b), _gpu_composite(metric, a, b), metric, nan_payload=False)
+    assert_equal(_public(metric, a, None), _gpu_composite(metric, a, a), f"{metric} self", nan_payload=False)

@@ -30,6 +30,7 @@ _SIGNATURES = {
     "tpw_pack_bool_rows": (_i, [_p, _i64, _i64, _p, _p, _p]),
     "tpw_bool_pairwise_reduce": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_jaccard_bool": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
+    "tpw_bool_count_metric": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _p, _p]),
     "tpw_compare_reduce": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_row_norms": (_i, [_p, _i, _i64, _i64, _i, _p, _p]),
     "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),

@@ -60,7 +60,75 @@ __global__ void row_popcount_kernel(const uint32_t *__restrict__ words, int64_t 
     pops[r] = (int32_t)c;
 }
 
-enum Epi { kSum = 0, kMean = 1, kJaccard = 2 };
+enum Epi { kSum = 0, kMean = 1, kJaccard = 2, kCountMetric = 16 };  // + TPW_BMET_*
+
+__device__ __forceinline__ float sat_count(uint32_t c) {
+    return (float)(c < kFloatExactLimit ? c : kFloatExactLimit);
+}
+
+// Output value from the tile's count (of OP) and, for jaccard and the count metrics, the two
+// rows' popcounts.  The count metrics reproduce the reference's float32 composites over the
+// separate pw*_sum passes (pairwise_metrics.cpp:224-243,339-399): every count is what a
+// float accumulator of ones holds (exact below 2^24, then 2^24), and the float operations
+// run in the composites' order, one rounding each, without contraction.  Counts are uint32
+// (d < 2^31, so pa + pb < 2^32): 64-bit counts would double the epilogue's registers over
+// the 64 outputs a thread owns and lower the occupancy of the whole kernel.
+template <int OP, int EPI>
+__device__ __forceinline__ float finish(uint32_t cnt, uint32_t pa, uint32_t pb, uint32_t d,
+                                        double inv_d, float df, float inv_df) {
+#pragma clang fp contract(off)
+    if constexpr (EPI == kSum) {
+        if constexpr (OP == TPW_BIT_EQ) cnt = d - cnt;
+        return sat_count(cnt);
+    } else if constexpr (EPI == kMean) {
+        if constexpr (OP == TPW_BIT_EQ) cnt = d - cnt;
+        // fl32(cnt / d) exactly: the double product is within 2^-52 of cnt/d, which is never
+        // within 2^-48 of a float rounding midpoint for cnt <= d < 2^24, so the final rounding
+        // is the correct one.
+        if (inv_d > 0.0) return (float)((double)cnt * inv_d);
+        return __fdiv_rn(sat_count(cnt), df);
+    } else if constexpr (EPI == kJaccard) {
+        const uint32_t sum = pa + pb;
+        const float xf = sat_count(sum - 2u * cnt), of = sat_count(sum - cnt);
+        return of != 0.0f ? __fdiv_rn(xf, of) : 0.0f;
+    } else {
+        constexpr int MET = EPI - kCountMetric;
+        const uint32_t n11 = cnt, x = pa + pb - 2u * n11;  // and, xor counts
+        const float A = sat_count(n11), S = sat_count(x);
+        if constexpr (MET == TPW_BMET_HAMMING) {  // pwne_mean
+            if (inv_d > 0.0) return (float)((double)x * inv_d);
+            return __fdiv_rn(S, df);
+        } else if constexpr (MET == TPW_BMET_JACCARD) {  // prf_div(xor, or, "zero")
+            const float O = sat_count(pa + pb - n11);
+            return O != 0.0f ? __fdiv_rn(S, O) : 0.0f;
+        } else if constexpr (MET == TPW_BMET_DICE) {  // R / (2 and + R), R = xor
+            return __fdiv_rn(S, 2.0f * A + S);
+        } else if constexpr (MET == TPW_BMET_KULCZYNSKI1) {  // and / xor
+            return __fdiv_rn(A, S);
+        } else if constexpr (MET == TPW_BMET_KULSINSKI) {  // (xor - and + d) / (xor + d)
+            const float num = (S - A) + df, den = S + df;
+            return __fdiv_rn(num, den);
+        } else if constexpr (MET == TPW_BMET_ROGERSTANIMOTO || MET == TPW_BMET_SOKALMICHENER) {
+            const float R = 2.0f * S, E = sat_count(d - x);  // R / (eq + R)
+            return __fdiv_rn(R, E + R);
+        } else if constexpr (MET == TPW_BMET_RUSSELLRAO) {
+            // (d - and) / d with ATen's GPU tensor / CPU-scalar divide: a multiply by the
+            // float reciprocal computed on the host (inv_df = fl(1 / fl(d)))
+            return (df - A) * inv_df;
+        } else if constexpr (MET == TPW_BMET_SOKALSNEATH) {  // R / (and + R), R = 2 xor
+            const float R = 2.0f * S;
+            return __fdiv_rn(R, A + R);
+        } else {  // yule: prf_div(2 hR, and * nor + hR, "zero"), hR = (a & ~b) * (~a & b)
+            const float n10 = sat_count(pa - n11), n01 = sat_count(pb - n11);
+            const float n00 = sat_count(d - (pa + pb - n11));
+            const float hR = n10 * n01;
+            const float num = 2.0f * hR;
+            const float prod = A * n00;
+            const float den = prod + hR;
+            return den != 0.0f ? __fdiv_rn(num, den) : 0.0f;
+        }
+    }
+}
 
 template <int OP>
 __device__ __forceinline__ uint32_t bitop(uint32_t a, uint32_t b) {
@@ -84,7 +152,8 @@ template <int OP, int EPI>
 __global__ __launch_bounds__(kThreads) void bool_reduce_kernel(
     const uint32_t *__restrict__ A, const uint32_t *__restrict__ Bw,
     const int32_t *__restrict__ popA, const int32_t *__restrict__ popB, int64_t n, int64_t m,
-    int64_t W, int64_t d, double inv_d, float *__restrict__ out, bool vec_store) {
+    int64_t W, int64_t d, double inv_d, float inv_df, float *__restrict__ out, bool vec_store) {
+    constexpr bool kPops = EPI >= kJaccard;
     __shared__ uint4 As[kTile][kChunkVec + 1];
     __shared__ uint4 Bs[kTile][kChunkVec + 1];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -130,39 +199,18 @@ __global__ __launch_bounds__(kThreads) void bool_reduce_kernel(
         const int64_t row = row0 + ty + 16 * i;
         if (row >= n) continue;
         float *orow = out + (b * n + row) * m;
-        int32_t pa = 0;
-        if constexpr (EPI == kJaccard) pa = popA[b * n + row];
+        uint32_t pa = 0;
+        if constexpr (kPops) pa = (uint32_t)popA[b * n + row];
+        const float df = (float)d;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int64_t col = col0 + 64 * h + 4 * tx;
             float v[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                uint32_t cnt = acc[i][4 * h + c];
-                if constexpr (OP == TPW_BIT_EQ) cnt = (uint32_t)d - cnt;
-                float r;
-                if constexpr (EPI == kSum) {
-                    r = (float)(cnt < kFloatExactLimit ? cnt : kFloatExactLimit);
-                } else if constexpr (EPI == kMean) {
-                    if (inv_d > 0.0) {
-                        // fl32(cnt / d) exactly: the double product is within 2^-52 of
-                        // cnt/d, which is never within 2^-48 of a float rounding midpoint
-                        // for cnt <= d < 2^24, so the final rounding is the correct one.
-                        r = (float)((double)cnt * inv_d);
-                    } else {
-                        r = __fdiv_rn((float)(cnt < kFloatExactLimit ? cnt : kFloatExactLimit),
-                                      (float)d);
-                    }
-                } else {
-                    int64_t cc = col + c;
-                    int32_t pb = cc < m ? popB[b * m + cc] : 0;
-                    uint32_t x = (uint32_t)(pa + pb) - 2u * cnt;
-                    uint32_t o = (uint32_t)(pa + pb) - cnt;
-                    float xf = (float)(x < kFloatExactLimit ? x : kFloatExactLimit);
-                    float of = (float)(o < kFloatExactLimit ? o : kFloatExactLimit);
-                    r = of != 0.0f ? __fdiv_rn(xf, of) : 0.0f;
-                }
-                v[c] = r;
+                uint32_t pb = 0;
+                if constexpr (kPops) pb = col + c < m ? (uint32_t)popB[b * m + col + c] : 0u;
+                v[c] = finish<OP, EPI>(acc[i][4 * h + c], pa, pb, (uint32_t)d, inv_d, df, inv_df);
             }
             if (vec_store && col + 3 < m) {
                 floatx4 f = {v[0], v[1], v[2], v[3]};
@@ -182,9 +230,10 @@ int launch_reduce(const uint32_t *a, const uint32_t *b, const int32_t *pa, const
     const int64_t W = tpw_packed_words(d);
     dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
     const double inv_d = d < (int64_t)kFloatExactLimit ? 1.0 / (double)d : 0.0;
+    const float inv_df = 1.0f / (float)d;  // as ATen's host-side reciprocal of a CPU scalar
     const bool vec_store = (m % 4 == 0) && aligned16(out);
     hipLaunchKernelGGL((bool_reduce_kernel<OP, EPI>), grid, dim3(kThreads), 0, s, a, b, pa, pb,
-                       n, m, W, d, inv_d, out, vec_store);
+                       n, m, W, d, inv_d, inv_df, out, vec_store);
     return check_launch("bool_reduce_kernel");
 }
 
@@ -266,4 +315,32 @@ extern "C" int tpw_jaccard_bool(const uint32_t *x1w, const uint32_t *x2w, const 
     TPW_REQUIRE(pop1 && pop2, "null popcount pointer");
     return launch_reduce<TPW_BIT_AND, kJaccard>(x1w, x2w, pop1, pop2, batch, n, m, d, out,
                                                 as_stream(stream));
+}
+
+extern "C" int tpw_bool_count_metric(const uint32_t *x1w, const uint32_t *x2w, const int32_t *pop1,
+                                     const int32_t *pop2, int64_t batch, int64_t n, int64_t m,
+                                     int64_t d, int metric, float *out, void *stream) {
+    int rc = check_reduce_args(x1w, x2w, batch, n, m, d, out);
+    if (rc != TPW_OK) return rc;
+    TPW_REQUIRE(metric >= TPW_BMET_HAMMING && metric <= TPW_BMET_YULE, "unknown metric %d", metric);
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(pop1 && pop2, "null popcount pointer");
+    hipStream_t s = as_stream(stream);
+#define TPW_MET(CODE)                                                                             \
+    case CODE:                                                                                    \
+        return launch_reduce<TPW_BIT_AND, kCountMetric + CODE>(x1w, x2w, pop1, pop2, batch, n, m, d, \
+                                                               out, s);
+    switch (metric) {
+        TPW_MET(TPW_BMET_HAMMING)
+        TPW_MET(TPW_BMET_JACCARD)
+        TPW_MET(TPW_BMET_DICE)
+        TPW_MET(TPW_BMET_KULCZYNSKI1)
+        TPW_MET(TPW_BMET_KULSINSKI)
+        TPW_MET(TPW_BMET_ROGERSTANIMOTO)
+        TPW_MET(TPW_BMET_RUSSELLRAO)
+        TPW_MET(TPW_BMET_SOKALMICHENER)
+        TPW_MET(TPW_BMET_SOKALSNEATH)
+        default: return launch_reduce<TPW_BIT_AND, kCountMetric + TPW_BMET_YULE>(x1w, x2w, pop1, pop2, batch, n, m, d, out, s);
+    }
+#undef TPW_MET
 }

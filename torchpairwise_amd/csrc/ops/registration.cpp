@@ -352,6 +352,7 @@ at::Tensor kulsinski_distances(const at::Tensor &x1, const c10::optional<at::Ten
     TORCH_WARN_DEPRECATION("kulsinski_distances is deprecated in SciPy 1.9.0 and might "
                            "be removed in the future. Please use kulczynski1_distances.")
     auto xs = check_pairwise_inputs<true>("kulsinski_distances", x1, x2);
+    if (auto r = bool_count_metric(xs.first, xs.second, "kulsinski"); r.defined()) return r;
     auto S = pw_binary_reduce("pwxor_sum", xs.first, xs.second);
     const int64_t D = x1.size(-1);
     return (S - pw_binary_reduce("pwand_sum", xs.first, xs.second) + D) / (S + D);
@@ -359,6 +360,7 @@ at::Tensor kulsinski_distances(const at::Tensor &x1, const c10::optional<at::Ten
 
 at::Tensor kulczynski1_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs<true>("kulczynski1_distances", x1, x2);
+    if (auto r = bool_count_metric(xs.first, xs.second, "kulczynski1"); r.defined()) return r;
     return pw_binary_reduce("pwand_sum", xs.first, xs.second) /
            pw_binary_reduce("pwxor_sum", xs.first, xs.second);
 }
@@ -374,6 +376,7 @@ at::Tensor chebyshev_distances(const at::Tensor &x1, const c10::optional<at::Ten
 
 at::Tensor yule_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs<true>("yule_distances", x1, x2);
+    if (auto r = bool_count_metric(xs.first, xs.second, "yule"); r.defined()) return r;
     const at::Tensor &a = xs.first, &b = xs.second;
     auto half_R = pw_binary_reduce("pwand_sum", a, b.logical_not()) *
                   pw_binary_reduce("pwand_sum", a.logical_not(), b);
@@ -386,12 +389,14 @@ at::Tensor yule_distances(const at::Tensor &x1, const c10::optional<at::Tensor> 
 
 at::Tensor dice_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs<true>("dice_distances", x1, x2);
+    if (auto r = bool_count_metric(xs.first, xs.second, "dice"); r.defined()) return r;
     auto R = pw_binary_reduce("pwxor_sum", xs.first, xs.second);
     return R / (2 * pw_binary_reduce("pwand_sum", xs.first, xs.second) + R);
 }
 
 at::Tensor rogerstanimoto_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs<true>("rogerstanimoto_distances", x1, x2);
+    if (auto r = bool_count_metric(xs.first, xs.second, "rogerstanimoto"); r.defined()) return r;
     auto R = 2 * pw_binary_reduce("pwxor_sum", xs.first, xs.second);
     auto S = pw_binary_reduce("pweq_sum", xs.first, xs.second);
     return R / (S + R);
@@ -399,12 +404,14 @@ at::Tensor rogerstanimoto_distances(const at::Tensor &x1, const c10::optional<at
 
 at::Tensor russellrao_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs<true>("russellrao_distances", x1, x2);
+    if (auto r = bool_count_metric(xs.first, xs.second, "russellrao"); r.defined()) return r;
     const int64_t D = x1.size(-1);
     return (D - pw_binary_reduce("pwand_sum", xs.first, xs.second)) / D;
 }
 
 at::Tensor sokalmichener_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs<true>("sokalmichener_distances", x1, x2);
+    if (auto r = bool_count_metric(xs.first, xs.second, "sokalmichener"); r.defined()) return r;
     auto R = 2 * pw_binary_reduce("pwxor_sum", xs.first, xs.second);
     auto S = pw_binary_reduce("pweq_sum", xs.first, xs.second);
     return R / (S + R);
@@ -412,6 +419,7 @@ at::Tensor sokalmichener_distances(const at::Tensor &x1, const c10::optional<at:
 
 at::Tensor sokalsneath_distances(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs<true>("sokalsneath_distances", x1, x2);
+    if (auto r = bool_count_metric(xs.first, xs.second, "sokalsneath"); r.defined()) return r;
     auto R = 2 * pw_binary_reduce("pwxor_sum", xs.first, xs.second);
     return R / (pw_binary_reduce("pwand_sum", xs.first, xs.second) + R);
 }

@@ -81,6 +81,12 @@ at::Tensor sqjensenshannon(const at::Tensor &x1, const at::Tensor &x2, c10::opti
 at::Tensor haversine(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor snr(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor sqmahalanobis(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI);
+// bit-packed boolean rows and the one-pass boolean count metrics (packed_bool.cpp);
+// bool_count_metric returns an undefined tensor where the fused GPU path does not apply
+std::tuple<at::Tensor, at::Tensor> pack_bool(const at::Tensor &x);
+at::Tensor packed_bool_metric(const at::Tensor &w1, const at::Tensor &p1, const at::Tensor &w2,
+                              const at::Tensor &p2, int64_t d, c10::string_view metric);
+at::Tensor bool_count_metric(const at::Tensor &x1, const at::Tensor &x2, c10::string_view metric);
 at::Tensor prf_div(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
 std::tuple<at::Tensor, at::Tensor> prf_div_backward(const at::Tensor &g, const at::Tensor &x,
                                                     const at::Tensor &y, c10::string_view mode);

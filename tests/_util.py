@@ -42,8 +42,8 @@ def assert_equal(actual, expected, what: str = "", nan_payload: bool = True):
     e = torch.as_tensor(expected).detach().cpu()
     assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
     if a.dtype.is_floating_point:
-        same = (a.view(torch.int32 if a.dtype == torch.float32 else torch.int64) ==
-                e.to(a.dtype).view(torch.int32 if a.dtype == torch.float32 else torch.int64))
+        iv = {2: torch.int16, 4: torch.int32, 8: torch.int64}[a.element_size()]
+        same = a.view(iv) == e.to(a.dtype).view(iv)
         if not nan_payload:
             same = same | (torch.isnan(a) & torch.isnan(e.to(a.dtype)))
     else:

@@ -586,3 +586,26 @@ def test_backward_entries_with_one_empty_side(empty):
         assert bool((other(capi.sqeuclidean_backward(gg, a, b)) == 0).all()), f"sqeuclidean {dt}"
     geo1, geo2 = x1[..., :2].contiguous(), x2[..., :2].contiguous()
     assert bool((other(capi.haversine_backward(g, geo1, geo2)) == 0).all()), "haversine"
+
+
+@pytest.mark.parametrize("n,m", [(128, 128), (100, 70)])  # staged full tiles / partial tiles
+def test_bf16_outputs_round_to_nearest_even(n, m):
+    # x1[i] . x2[j] = a_i + b_i * s_j with s_j a power of two: exact in the fp32 accumulator, so
+    # the bf16 output is the RNE rounding of a known fp32 value (ties, carries into the exponent,
+    # large magnitudes, signs), compared bit for bit with torch's CPU conversion
+    # a, b = +-(1 + k / 128) (bf16-exact, exponent 0) and s in [2^-9, 4]: every sum needs at
+    # most 19 significant bits, so it is exact in fp32 whatever the MFMA's summation order
+    g = torch.Generator().manual_seed(70)
+    sign = lambda: torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0)
+    a = sign() * (1 + torch.randint(0, 128, (n,), generator=g).float() / 128)
+    b = sign() * (1 + torch.randint(0, 128, (n,), generator=g).float() / 128)
+    a[:4] = torch.tensor([1.0, 1.0078125, -1.0, 2.0e38])  # 1 + 2^-7; a large magnitude
+    b[:4] = torch.tensor([1.0, 1.0, 1.0, 1.0e37])
+    a, b = a.to(torch.bfloat16).float(), b.to(torch.bfloat16).float()
+    s = 2.0 ** torch.randint(-9, 3, (m,), generator=g).float()
+    s[:3] = torch.tensor([2.0 ** -8, 2.0 ** -8, 2.0 ** -9])  # exact ties for rows 0-2
+    x1 = torch.stack([a, b], 1).to(torch.bfloat16)
+    x2 = torch.stack([torch.ones(m), s], 1).to(torch.bfloat16)
+    want = (a[:, None] + b[:, None] * s[None, :]).to(torch.bfloat16)
+    got = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_DOT)
+    assert_equal(got, want, f"bf16 rounding {n}x{m}")

@@ -38,11 +38,18 @@ __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 
 // bf16 (stored as uint16_t bits) <-> fp32; fp32 -> bf16 rounds to nearest even, as
 // c10::BFloat16 does.
+// fp32 -> bf16, round to nearest even, on gfx950's v_cvt_pk_bf16_f32; NaN becomes 0x7fc0, as
+// torch's conversion gives, so elementwise results match the CPU bit for bit.
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    const uint16_t r = __builtin_bit_cast(uint16_t, (__bf16)f);
+    return f != f ? (uint16_t)0x7fc0 : r;
+}
+// Two values in one v_cvt_pk_bf16_f32 (lo in bits 0-15); a NaN keeps the hardware's pattern.
+typedef float tpw_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 tpw_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_rne(float lo, float hi) {
+    const tpw_f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, tpw_bf16x2));
 }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 

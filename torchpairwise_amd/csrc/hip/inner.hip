@@ -296,10 +296,10 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
                         }
                         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
                         u32x4 q;
-                        q[0] = f32_to_bf16_rne(v0[0]) | ((uint32_t)f32_to_bf16_rne(v0[1]) << 16);
-                        q[1] = f32_to_bf16_rne(v0[2]) | ((uint32_t)f32_to_bf16_rne(v0[3]) << 16);
-                        q[2] = f32_to_bf16_rne(v1[0]) | ((uint32_t)f32_to_bf16_rne(v1[1]) << 16);
-                        q[3] = f32_to_bf16_rne(v1[2]) | ((uint32_t)f32_to_bf16_rne(v1[3]) << 16);
+                        q[0] = f32x2_to_bf16x2_rne(v0[0], v0[1]);
+                        q[1] = f32x2_to_bf16x2_rne(v0[2], v0[3]);
+                        q[2] = f32x2_to_bf16x2_rne(v1[0], v1[1]);
+                        q[3] = f32x2_to_bf16x2_rne(v1[2], v1[3]);
                         __builtin_nontemporal_store(q, reinterpret_cast<u32x4 *>(orow + (int64_t)rr * m + cc));
                     }
                 }

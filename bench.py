@@ -234,13 +234,15 @@ def run_config(cfg, steps, warmup):
         x2 = torch.randn(N, D, generator=torch.Generator().manual_seed(1)).to(dev)
         dist = tp.euclidean_distances(x1, x2)
         pf = N * N * D
-        for k in (1, 8, 32):
+        for k in (1, 8, 32, 128, 255, 511):
             ms, _ = time_op(lambda: torch.ops.torchpairwise._row_smallest_mask(dist, k + 1), steps, warmup)
             emit(f"row_smallest_mask count={k + 1}", ms, pf,
                  {"hbm_GBps": 5.0 * N * N / (ms * 1e-3) / 1e9,
                   "hbm_frac": 5.0 * N * N / (ms * 1e-3) / PEAK_HBM})
         ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, 1), steps, warmup)
         emit("k_neighbors_mask k=1 (euclidean + selection)", ms, pf)
+        ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, 16), steps, warmup)
+        emit("k_neighbors_mask k=16 (euclidean + selection)", ms, pf)
         ms, _ = time_op(lambda: tp.radius_neighbors_mask(x1, x2, 14.0), steps, warmup)
         emit("radius_neighbors_mask eps=14 (euclidean + le)", ms, pf)
 

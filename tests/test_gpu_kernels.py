@@ -358,12 +358,13 @@ def test_row_smallest_mask_half_types(dtype, count):
     assert_equal(got, torch.from_numpy(want), f"{dtype} c={count}")
 
 
-@pytest.mark.parametrize("cols", [8192, 8191])  # vector (4-column) and scalar row access
-@pytest.mark.parametrize("count", [17, 40, 200])
+@pytest.mark.parametrize("cols", [8192, 8191, 20480, 20481])  # vector / scalar access; rows
+@pytest.mark.parametrize("count", [17, 40, 200])                  # held in registers / streamed
 def test_row_smallest_mask_list_runs_dry(cols, count):
     # the smallest entries all belong to workgroup thread 0 (columns 4c..4c+3 with
     # c = 0, 256, 512, ... for the vector path; columns 0, 256, 512, ... for the scalar
-    # one), so its 16-entry list runs dry and the row falls back to the radix select
+    # one): on rows longer than 16384 its 16-entry list runs dry and the row falls back to
+    # the radix select; shorter rows take all of them as candidates
     d = rand(4, cols, seed=15) + 1.0
     own = torch.arange(0, cols, 1024).repeat_interleave(4) + torch.arange(4).repeat(len(range(0, cols, 1024)))
     own = own[own < cols] if cols % 4 == 0 else torch.arange(0, cols, 256)
@@ -609,3 +610,16 @@ def test_bf16_outputs_round_to_nearest_even(n, m):
     want = (a[:, None] + b[:, None] * s[None, :]).to(torch.bfloat16)
     got = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_DOT)
     assert_equal(got, want, f"bf16 rounding {n}x{m}")
+
+
+@pytest.mark.parametrize("cols", [16384, 16383, 1000])
+@pytest.mark.parametrize("count", [150, 256])
+def test_row_smallest_mask_candidate_overflow(cols, count):
+    # rows held in registers: the count-th smallest per-thread minimum bounds the selection;
+    # here most threads' entries all lie below it (ties at 0 and a ramp), so more than 2048
+    # candidates qualify and the row takes the exact radix fallback
+    d = rand(3, cols, seed=16) + 1.0
+    d[0, : cols * 3 // 4] = 0.0  # three quarters of the row tied at the minimum
+    d[1, : cols * 3 // 4] = torch.linspace(-1.0, 0.0, cols * 3 // 4)
+    got = capi.row_smallest_mask(d.to(DEV), count)
+    assert_equal(got, torch.from_numpy(P.k_smallest_mask(d.numpy(), count)), f"overflow {cols} c={count}")

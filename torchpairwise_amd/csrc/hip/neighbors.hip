@@ -14,12 +14,18 @@
 // reference's argsort is not stable: on ties across the boundary its choice is
 // implementation-defined; everywhere else the sets are identical.)
 //
-// Two selection strategies:
-//   * count <= 256: every thread keeps a sorted list of its 16 (or fewer) smallest keys while
-//     streaming the row once; the workgroup then pops the minimum of the list heads `count`
-//     times.  The popped keys name the selected columns, so the mask is written without a
-//     second read: 4 bytes of distances read and 1 byte of mask written per entry.  When a
-//     thread's list runs dry before the last pop the row falls back to the radix select.
+// Selection strategies (measured at 16384 x 16384 fp32: 0.25-0.30 ms for count <= 33, i.e.
+// near the HBM time of reading the distances once and writing the mask once):
+//   * count <= 3: every thread keeps a sorted list of its count smallest keys while streaming
+//     the row once; the workgroup then pops the minimum of the list heads `count` times.  The
+//     popped keys name the selected columns, so the mask is written without a second read.
+//     (The list can run dry only when count exceeds its length, which it never does here;
+//     the radix select stays as the exact fallback.)
+//   * 4 <= count <= 256: every thread keeps its 4 smallest keys while streaming the row once;
+//     a bound T0 from the per-thread minima (and, for large counts, the 4th-smallest keys)
+//     limits the candidates to a few times `count`; they are ranked in LDS and the mask is
+//     written from the lists (see smallest_bound_kernel).  Rows whose lists cannot prove
+//     completeness re-stream the candidates from L2; heavy ties take the radix select.
 //   * count > 256: radix-2 select on the 32-bit order keys (one counting pass per bit below
 //     the common prefix of the row's min and max keys), then, only when the boundary value
 //     is tied, a second radix-2 select on the column index among the tied entries; rows of
@@ -341,6 +347,155 @@ __global__ __launch_bounds__(kThreads) void smallest_list_kernel(const T *__rest
     }
 }
 
+constexpr int kCandMax = 2048;  // LDS candidate list of the bound kernel (16 KB)
+constexpr int kLocalMax = 24;   // counts up to this use a per-wave bound (measured best)
+constexpr int kListBound = 192; // counts above this also use the lists' last entries
+
+// Streaming selection for 4 <= count <= kListMax on rows of any length: one read of the row
+// from HBM in the common case.
+//   pass 1: each thread streams its entries keeping its kBL smallest keys (a short sorted
+//           list: few insertions, little divergence) -> per-thread minimum lst[0];
+//   T0:     a key with at least `count` keys at or below it (the count-th smallest of a
+//           wave's 64 minima for count <= 64, of all 256 minima otherwise); the selected set
+//           lies in {key <= T0};
+//   list:   if no thread's kBL-th entry is <= T0, every key <= T0 sits in some thread's list:
+//           the candidates are the list entries <= T0, ranked in LDS to give T* (the count-th
+//           smallest key of the row), and the mask is written from the lists (no re-read);
+//   else:   the candidates come from a second streaming pass (from L2: the row was just
+//           read) and the mask from a third; more than kCandMax candidates (heavy ties) take
+//           the exact radix select.
+template <typename T, int V, int kBL>
+__global__ __launch_bounds__(kThreads) void smallest_bound_kernel(const T *__restrict__ dist,
+                                                                  int64_t cols, int count,
+                                                                  uint8_t *__restrict__ mask) {
+    __shared__ uint64_t minima[kThreads];
+    __shared__ uint64_t cand[kCandMax];
+    __shared__ uint64_t slots[2 * kWaves];
+    __shared__ uint32_t ncand;
+    __shared__ int spill;
+    __shared__ uint64_t thr0[kWaves], thr1;
+    const int tid = threadIdx.x;
+    const int64_t r = blockIdx.x;
+    RowKeys<T, V, false> keys{dist + r * cols, cols, nullptr};
+    if (tid < kWaves) thr0[tid] = ~0ull;
+    if (tid == 0) {
+        ncand = 0;
+        spill = 0;
+        thr1 = ~0ull;
+    }
+    auto at_most = [](uint32_t k, uint32_t j, uint64_t t) {
+        const uint32_t th = (uint32_t)(t >> 32), tl = (uint32_t)t;
+        return k < th || (k == th && j <= tl);
+    };
+    // pass 1
+    uint64_t lst[kBL];
+#pragma unroll
+    for (int q = 0; q < kBL; ++q) lst[q] = ~0ull;
+    keys.stream([&](uint32_t k, uint32_t j) {
+        const uint64_t key = ((uint64_t)k << 32) | j;
+        if (key < lst[kBL - 1]) {
+            lst[kBL - 1] = key;
+#pragma unroll
+            for (int q = kBL - 1; q > 0; --q) {
+                if (lst[q] < lst[q - 1]) {
+                    const uint64_t x = lst[q];
+                    lst[q] = lst[q - 1];
+                    lst[q - 1] = x;
+                }
+            }
+        }
+    });
+    // bounds: the count-th smallest of the threads' minima (of a wave's 64 minima when count
+    // <= kLocalMax: at least count keys are <= it) and, for count > kListBound, the
+    // ceil(count / kBL)-th smallest of the threads' kBL-th smallest keys (at least
+    // kBL * ceil(count / kBL) >= count keys are <= it; far tighter when count nears 256, but
+    // below that it makes rows spill into the streaming pass more often)
+    const uint64_t mymin = lst[0], mylast = lst[kBL - 1];
+    minima[tid] = mymin;
+    cand[tid] = mylast;  // the candidate list is still free
+    __syncthreads();
+    if (mymin != ~0ull) {
+        const bool local = count <= kLocalMax;
+        const uint64_t *mw = minima + (local ? (tid & ~63) : 0);
+        const int len = local ? 64 : kThreads;
+        uint32_t rank = 0;
+#pragma unroll 8
+        for (int w = 0; w < len; ++w) rank += mw[w] < mymin;
+        if (rank == (uint32_t)(count - 1)) thr0[local ? tid >> 6 : 0] = mymin;
+    }
+    if (count > kListBound && mylast != ~0ull) {
+        const uint32_t need = (uint32_t)((count + kBL - 1) / kBL);
+        uint32_t rank = 0;
+#pragma unroll 8
+        for (int w = 0; w < kThreads; ++w) rank += cand[w] < mylast;
+        if (rank == need - 1) thr0[1] = mylast;  // slot 1 is unused by the all-minima bound
+    }
+    __syncthreads();
+    uint64_t t0 = thr0[0];  // ~0: no bound found; every entry is a candidate
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) t0 = thr0[w] < t0 ? thr0[w] : t0;
+    // a list whose last entry is <= T0 may have dropped keys <= T0 (~0 entries are padding)
+    if (lst[kBL - 1] != ~0ull && lst[kBL - 1] <= t0) spill = 1;
+    __syncthreads();  // also orders the bound's reads of cand[] before the appends below
+    const bool from_lists = !spill;  // workgroup-uniform
+    if (from_lists) {
+#pragma unroll
+        for (int q = 0; q < kBL; ++q) {
+            if (lst[q] != ~0ull && lst[q] <= t0) {  // ~0 entries are list padding
+                const uint32_t slot = atomicAdd(&ncand, 1u);
+                if (slot < kCandMax) cand[slot] = lst[q];
+            }
+        }
+    } else {
+        keys.stream([&](uint32_t k, uint32_t j) {
+            if (at_most(k, j, t0)) {
+                const uint32_t slot = atomicAdd(&ncand, 1u);
+                if (slot < kCandMax) cand[slot] = ((uint64_t)k << 32) | j;
+            }
+        });
+    }
+    __syncthreads();
+    const uint32_t n = ncand;
+    uint8_t *mrow = mask + r * cols;
+    if (n > (uint32_t)kCandMax) {  // workgroup-uniform: exact fallback
+        Reducer red{slots};
+        write_mask_keys(keys, radix_threshold(keys, red, count), mrow);
+        return;
+    }
+    for (uint32_t q = tid; q < n; q += kThreads) {
+        const uint64_t x = cand[q];
+        uint32_t rank = 0;
+#pragma unroll 8
+        for (uint32_t w = 0; w < n; ++w) rank += cand[w] < x;
+        if (rank == (uint32_t)(count - 1)) thr1 = x;
+    }
+    __syncthreads();
+    const uint64_t ts = thr1;
+    if (from_lists) {
+        // every selected key is in its owner's list: write this thread's chunks from it
+        const int64_t nc = keys.chunks();
+        for (int64_t c = tid; c < nc; c += kThreads) {
+            uint32_t bits = 0;
+#pragma unroll
+            for (int q = 0; q < kBL; ++q) {
+                const uint32_t j = (uint32_t)lst[q];
+                if (lst[q] != ~0ull && lst[q] <= ts && (int64_t)(j / V) == c) bits |= 1u << (j % V);
+            }
+            store_mask_chunk<V>(mrow + c * V, bits);
+        }
+        return;
+    }
+    uint32_t bits = 0;
+    keys.stream([&](uint32_t k, uint32_t j) {
+        const int e = (int)(j % V);
+        bits |= (at_most(k, j, ts) ? 1u : 0u) << e;
+        if (e == V - 1) {
+            store_mask_chunk<V>(mrow + (j - e), bits);
+            bits = 0;
+        }
+    });
+}
+
 // count > kListMax: radix select, with the row's keys in LDS when they fit.
 template <typename T, int V, bool CACHED>
 __global__ __launch_bounds__(kThreads) void smallest_radix_kernel(const T *__restrict__ dist,
@@ -387,14 +542,16 @@ int launch_v(const T *d, int64_t rows, int64_t cols, int count, uint8_t *mask, h
         }
         return check_launch("smallest_radix_kernel");
     }
+    if (count > 3) {
+        hipLaunchKernelGGL((smallest_bound_kernel<T, V, 4>), grid, block, 0, s, d, cols, count, mask);
+        return check_launch("smallest_bound_kernel");
+    }
 #define TPW_LIST(LL)                                                                                  \
     hipLaunchKernelGGL((smallest_list_kernel<T, V, LL>), grid, block, 0, s, d, cols, count, mask); \
     return check_launch("smallest_list_kernel")
     if (count <= 1) { TPW_LIST(1); }
     if (count <= 2) { TPW_LIST(2); }
-    if (count <= 4) { TPW_LIST(4); }
-    if (count <= 8) { TPW_LIST(8); }
-    TPW_LIST(16);
+    TPW_LIST(4);
 #undef TPW_LIST
 }
 

@@ -75,8 +75,9 @@ def parse():
                          "--pmc FETCH_SIZE / WRITE_SIZE pass has a known-size reference kernel")
     ap.add_argument("--config", default="M",
                     help="M (default: the metric's workload), C2..C5: time the other "
-                         "BASELINE.json configurations, NB: the neighbour masks at the metric "
-                         "shape (one JSON line per op, not the headline)")
+                         "BASELINE.json configurations, NB: the neighbour masks and KF: the "
+                         "polynomial / sigmoid kernels at the metric shape (one JSON line per "
+                         "op, not the headline)")
     return ap.parse_args()
 
 
@@ -209,6 +210,34 @@ def run_config(cfg, steps, warmup):
             return R / (2 * ops.pwand_sum(h1, h2) + R)
         ms, _ = time_op(dice_composite, steps, warmup)
         emit("dice fwd, reference composite route", ms, pf)
+    elif cfg == "KF":
+        # polynomial / sigmoid kernels at the metric shape: the function fused into the MFMA
+        # epilogue against the reference's composite (matmul + mul_ + add_ + pow_ / tanh_) on
+        # the same GPU
+        N, D = 16384, 128
+        x1 = torch.randn(N, D, generator=torch.Generator().manual_seed(0)).to(dev)
+        x2 = torch.randn(N, D, generator=torch.Generator().manual_seed(1)).to(dev)
+        pf = N * N * D
+        ones = torch.ones(N, N, device=dev)
+        g = 1.0 / D
+        for name, f, ref in (
+                ("polynomial_kernel degree=3", lambda a, b: tp.polynomial_kernel(a, b, 3),
+                 lambda a, b: a.matmul(b.transpose(-1, -2)).mul_(g).add_(1.0).pow_(3)),
+                ("sigmoid_kernel", lambda a, b: tp.sigmoid_kernel(a, b),
+                 lambda a, b: a.matmul(b.transpose(-1, -2)).mul_(g).add_(1.0).tanh_())):
+            ms, _ = time_op(lambda: f(x1, x2), steps, warmup)
+            emit(f"{name} fwd", ms, pf, {"tflops": 2 * pf / (ms * 1e-3) / 1e12})
+            ms, _ = time_op(lambda: ref(x1, x2), steps, warmup)
+            emit(f"{name} fwd, reference composite route", ms, pf)
+            a, b = x1.clone().requires_grad_(), x2.clone().requires_grad_()
+
+            def fb():
+                a.grad = None
+                b.grad = None
+                f(a, b).backward(ones)
+
+            ms, _ = time_op(fb, steps, warmup)
+            emit(f"{name} fwd+bwd", ms, pf)
     elif cfg == "C5":
         C, P, D = 16, 65536, 3
         x1 = torch.rand(C, P, D, generator=torch.Generator().manual_seed(0)).to(dev)

@@ -103,6 +103,29 @@ int tpw_jaccard_bool(const uint32_t *x1_words, const uint32_t *x2_words,
                      int64_t batch, int64_t n, int64_t m, int64_t d, float *out,
                      void *stream);
 
+/* Kernel functions of tpw_pairwise_kernel */
+#define TPW_KER_POLYNOMIAL 0
+#define TPW_KER_SIGMOID 1
+
+/* out = (x1 . x2^T * gamma + coef0)^degree (POLYNOMIAL) or tanh(x1 . x2^T * gamma + coef0)
+ * (SIGMOID) on the MFMA kernel, the function applied to the fp32 accumulators before the one
+ * write of out.  Replaces the matmul + mul_ + add_ + pow_ / tanh_ passes of polynomial_kernel
+ * and sigmoid_kernel (pairwise_metrics.cpp:67-78,80-90); degree k = 2, 3 as products, otherwise
+ * powf, as ATen's pow with a scalar exponent.  dtype TPW_F32 or TPW_BF16. */
+int tpw_pairwise_kernel(const void *x1, const void *x2, int dtype, int64_t batch, int64_t n,
+                        int64_t m, int64_t d, int kind, float gamma, float coef0, int degree,
+                        void *out, void *stream);
+
+/* Gradients of tpw_pairwise_kernel, the autograd of the reference's composite: the per-pair
+ * weight grad * degree * (S gamma + coef0)^(degree - 1) * gamma (S recomputed on the MFMA
+ * path) or grad * (1 - out^2) * gamma, then grad_x1 = W . x2, grad_x2 = W^T . x1 on the
+ * matrix cores.  Workspace: tpw_inner_backward_workspace_size(batch, n, m, d) bytes; `out`
+ * (the forward result) is needed for SIGMOID. */
+int tpw_pairwise_kernel_backward(const void *grad, const void *x1, const void *x2,
+                                 const void *out, int dtype, int64_t batch, int64_t n, int64_t m,
+                                 int64_t d, int kind, float gamma, float coef0, int degree,
+                                 void *grad_x1, void *grad_x2, void *workspace, void *stream);
+
 /* Boolean count metrics of tpw_bool_count_metric */
 #define TPW_BMET_HAMMING 0
 #define TPW_BMET_JACCARD 1

@@ -623,3 +623,22 @@ def test_row_smallest_mask_candidate_overflow(cols, count):
     d[1, : cols * 3 // 4] = torch.linspace(-1.0, 0.0, cols * 3 // 4)
     got = capi.row_smallest_mask(d.to(DEV), count)
     assert_equal(got, torch.from_numpy(P.k_smallest_mask(d.numpy(), count)), f"overflow {cols} c={count}")
+
+
+@pytest.mark.parametrize("kind,degree", [(capi.KER_POLYNOMIAL, 3), (capi.KER_POLYNOMIAL, 5),
+                                         (capi.KER_SIGMOID, 0)])
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 257, 129, 96)])
+def test_pairwise_kernel_capi(kind, degree, B, n, m, d):
+    # tpw_pairwise_kernel / _backward against the composite in float64 (fp32 bar as above)
+    x1, x2 = randn(B, n, d, seed=80) / 4, randn(B, m, d, seed=81) / 4
+    g = randn(B, n, m, seed=82)
+    gamma, coef0 = 0.7, 0.4
+    out = capi.pairwise_kernel(x1.to(DEV), x2.to(DEV), kind, gamma, coef0, degree)
+    a, b = x1.double().requires_grad_(), x2.double().requires_grad_()
+    base = (a @ b.transpose(1, 2)) * gamma + coef0
+    ref = base ** degree if kind == capi.KER_POLYNOMIAL else torch.tanh(base)
+    assert_close(out, ref.detach(), rtol=1e-4, atol=1e-5 * float(ref.abs().max()), what="forward")
+    ref.backward(g.double())
+    gx1, gx2 = capi.pairwise_kernel_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), out, kind, gamma, coef0, degree)
+    assert_close(gx1, a.grad, rtol=1e-4, atol=1e-4 * float(a.grad.abs().max()), what="grad_x1")
+    assert_close(gx2, b.grad, rtol=1e-4, atol=1e-4 * float(b.grad.abs().max()), what="grad_x2")

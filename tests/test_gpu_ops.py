@@ -365,3 +365,49 @@ def test_special_ops_gpu_batched_and_cdist():
     vr = VI[0].double().requires_grad_()
     ops._sqmahalanobis(x1[0].double(), x2[0].double(), vr).sum().backward()
     assert_close(v.grad.cpu(), vr.grad, rtol=1e-4, atol=1e-4 * float(vr.grad.abs().max()), what="grad VI")
+
+
+# --------------------------------------------------------------------------------------
+# polynomial_kernel / sigmoid_kernel: the function fused into the MFMA epilogue; the
+# reference's composite (matmul, mul_, add_, pow_ / tanh_) in float64 on the CPU is the bar
+# fp32: values rtol 1e-4 (+ atol 1e-5 * max); grads rtol 1e-4 (+ atol 1e-4 * max)
+# bf16: 3e-2 (+ 3e-2 * max) for values and grads (one bf16 rounding of inputs and output,
+#       amplified by the degree)
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("name,kw", [("polynomial_kernel", dict(degree=3)),
+                                     ("polynomial_kernel", dict(degree=2, gamma=0.3, coef0=0.5)),
+                                     ("polynomial_kernel", dict(degree=4, coef0=-0.25)),
+                                     ("polynomial_kernel", dict(degree=1)),
+                                     ("polynomial_kernel", dict(degree=0)),
+                                     ("sigmoid_kernel", dict()),
+                                     ("sigmoid_kernel", dict(gamma=0.05, coef0=-0.3))])
+def test_kernel_functions_gpu(dtype, name, kw):
+    print(f"{name} {kw} {dtype}", flush=True)
+    x1, x2 = randn(150, 24, seed=0, dtype=dtype), randn(90, 24, seed=1, dtype=dtype)
+    fn = getattr(tp, name)
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    out = fn(a, b, **kw)
+    assert out.dtype == dtype
+    g = randn(150, 90, seed=3)
+    out.backward(g.to(DEV, dtype))
+    ra, rb = x1.detach().double().requires_grad_(), x2.detach().double().requires_grad_()
+    ref = fn(ra, rb, **kw)  # CPU float64: the reference's composite
+    ref.backward(g.double())
+    tol = 1e-4 if dtype == torch.float32 else 3e-2
+    atol_v = (1e-5 if dtype == torch.float32 else 3e-2) * float(ref.abs().max())
+    assert_close(out.float(), ref, rtol=tol, atol=atol_v, what=name)
+    for got, want, nm in ((a.grad, ra.grad, "grad x1"), (b.grad, rb.grad, "grad x2")):
+        assert_close(got.float(), want, rtol=tol, atol=tol * float(want.abs().max()) + 1e-30, what=nm)
+
+
+def test_kernel_functions_gpu_batched_and_self():
+    x1 = randn(2, 130, 40, seed=4).to(DEV)
+    x2 = randn(2, 70, 40, seed=5).to(DEV)
+    for name, kw in (("polynomial_kernel", dict(degree=3)), ("sigmoid_kernel", dict())):
+        fn = getattr(tp, name)
+        ref = fn(x1.cpu().double(), x2.cpu().double(), **kw)
+        assert_close(fn(x1, x2, **kw).cpu(), ref, rtol=1e-4, atol=1e-5 * float(ref.abs().max()), what=name)
+        ref = fn(x1[0].cpu().double(), None, **kw)
+        assert_close(fn(x1[0], None, **kw).cpu(), ref, rtol=1e-4, atol=1e-5 * float(ref.abs().max()),
+                     what=f"{name} x2=None")

@@ -58,6 +58,12 @@ __device__ __forceinline__ float to_f32(uint16_t v) { return bf16_to_f32(v); }
 __device__ __forceinline__ void from_f32(float *p, float v) { *p = v; }
 __device__ __forceinline__ void from_f32(uint16_t *p, float v) { *p = f32_to_bf16_rne(v); }
 
+// Parameters of the kernel-function epilogues (polynomial, sigmoid) of the MFMA kernel.
+struct KerParams {
+    float gamma = 0.0f, coef0 = 0.0f;
+    int degree = 0;
+};
+
 // S = x1 . x2^T in fp32 on the matrix cores for fp32 or bf16 inputs (inner.hip).
 int inner_dot_f32(const void *x1, const void *x2, int dtype, int64_t batch, int64_t n, int64_t m,
                   int64_t d, float *out, hipStream_t s);

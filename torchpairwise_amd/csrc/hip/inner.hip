@@ -45,10 +45,37 @@ struct Elem<uint16_t> {  // bf16 bits
 // Gradient products of the backward (not a public epilogue code): out = sign * s +
 // aux1[row] * X[row, col], X having the output's type and shape.
 constexpr int kEpiGrad = 100;
+// The kernel functions of tpw_pairwise_kernel: (s gamma + coef0)^degree and
+// tanh(s gamma + coef0).
+constexpr int kEpiPoly = 101;
+constexpr int kEpiSigmoid = 102;
+
+// Row / column norms read by the epilogue (aux1 also carries the gradient coefficients).
+template <int EPI>
+constexpr bool kAux1 = EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN ||
+                       EPI == TPW_EPI_COSINE_SIM || EPI == TPW_EPI_COSINE_DIST || EPI == kEpiGrad;
+template <int EPI>
+constexpr bool kAux2 = kAux1<EPI> && EPI != kEpiGrad;
+
+// x^k for an integral k as ATen's pow with a scalar exponent computes it on the GPU: k = 2, 3
+// as products, otherwise the float power function.
+__device__ __forceinline__ float ipow(float x, int k) {
+#pragma clang fp contract(off)
+    if (k == 2) return x * x;
+    if (k == 3) return x * x * x;
+    if (k == 1) return x;
+    if (k == 0) return 1.0f;
+    return powf(x, (float)k);
+}
 
 template <int EPI>
-__device__ __forceinline__ float epilogue(float s, float a1, float a2) {
-    if constexpr (EPI == TPW_EPI_DOT || EPI == kEpiGrad) {
+__device__ __forceinline__ float epilogue(float s, float a1, float a2, const KerParams &kp) {
+#pragma clang fp contract(off)
+    if constexpr (EPI == kEpiPoly || EPI == kEpiSigmoid) {
+        // the reference's matmul(...).mul_(gamma).add_(coef0), then pow_ / tanh_
+        const float base = s * kp.gamma + kp.coef0;
+        return EPI == kEpiPoly ? ipow(base, kp.degree) : tanhf(base);
+    } else if constexpr (EPI == TPW_EPI_DOT || EPI == kEpiGrad) {
         return s;
     } else if constexpr (EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN) {
         float v = (a1 + a2) - 2.0f * s;
@@ -154,7 +181,8 @@ template <typename T, typename OutT, int EPI, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
     const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
-    int64_t tiles_n, int64_t tiles_m, int64_t total, const OutT *__restrict__ X, float sign) {
+    int64_t tiles_n, int64_t tiles_m, int64_t total, const OutT *__restrict__ X, float sign,
+    KerParams kp) {
     // operand panels (As, Bs); after the K loop the same bytes stage the fp32 output
     __shared__ uint4 smem[2 * kTile * kLdsStride];
     uint4 *As = smem;
@@ -176,10 +204,10 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
     const int l32 = lane & 31, h = lane >> 5;
 
-    if constexpr (EPI != TPW_EPI_DOT) {
+    if constexpr (kAux1<EPI>) {
         const int i = tid & (kTile - 1);
         if (tid < kTile) s_aux[0][i] = row0 + i < n ? aux1[b * n + row0 + i] : 0.0f;
-        else if (EPI != kEpiGrad) s_aux[1][i] = col0 + i < m ? aux2[b * m + col0 + i] : 0.0f;
+        else if (kAux2<EPI>) s_aux[1][i] = col0 + i < m ? aux2[b * m + col0 + i] : 0.0f;
     }
 
     floatx16 acc[2][2];
@@ -238,7 +266,7 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     float a2v[2];
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni)
-        a2v[ni] = (EPI != TPW_EPI_DOT && EPI != kEpiGrad) ? s_aux[1][wc + ni * 32 + l32] : 0.0f;
+        a2v[ni] = kAux2<EPI> ? s_aux[1][wc + ni * 32 + l32] : 0.0f;
     // bf16 rows are written 8 values (16 bytes) per lane: needs m % 8 == 0 for alignment
     const bool staged = full && (sizeof(OutT) == 4 || m % 8 == 0);
     {
@@ -255,9 +283,9 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
-                        const float a1 = EPI != TPW_EPI_DOT ? s_aux[0][wr + mi * 32 + rr] : 0.0f;
+                        const float a1 = kAux1<EPI> ? s_aux[0][wr + mi * 32 + rr] : 0.0f;
                         stage[rr * kStageStride + ni * 32 + l32] =
-                            EPI == kEpiGrad ? sign * acc[mi][ni][r] : epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni]);
+                            EPI == kEpiGrad ? sign * acc[mi][ni][r] : epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni], kp);
                     }
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
                 __builtin_amdgcn_wave_barrier();
@@ -318,9 +346,9 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int rr = mi * 32 + 8 * (r >> 2) + (r & 3);  // row in the wave tile, less 4 h
-                const float a1 = EPI != TPW_EPI_DOT ? s_aux[0][wr + 4 * h + rr] : 0.0f;
+                const float a1 = kAux1<EPI> ? s_aux[0][wr + 4 * h + rr] : 0.0f;
                 if (full || (row0 + wr + 4 * h + rr < n && col_ok)) {
-                    float v = epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni]);
+                    float v = epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni], kp);
                     if constexpr (EPI == kEpiGrad) v = sign * v + a1 * to_f32(X[(obase - out) + rr * m + ni * 32]);
                     store_out(obase + rr * m + ni * 32, v);
                 }
@@ -352,13 +380,13 @@ __global__ void row_norms_kernel(const T *__restrict__ x, int64_t rows, int64_t 
 template <typename T, int EPI, typename OutT = T>
 int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
                  const float *aux1, const float *aux2, OutT *out, hipStream_t s,
-                 const OutT *X = nullptr, float sign = 1.0f) {
+                 const OutT *X = nullptr, float sign = 1.0f, KerParams kp = {}) {
     const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
     const int64_t total = tiles_n * tiles_m * batch;
     const bool vec = ((d * (int64_t)sizeof(T)) % 16 == 0) && aligned16(x1) && aligned16(x2);
     auto kernel = vec ? pairwise_inner_kernel<T, OutT, EPI, true> : pairwise_inner_kernel<T, OutT, EPI, false>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(kThreads), 0, s, x1, x2, n, m, d, aux1,
-                       aux2, out, tiles_n, tiles_m, total, X, sign);
+                       aux2, out, tiles_n, tiles_m, total, X, sign, kp);
     return check_launch("pairwise_inner_kernel");
 }
 
@@ -441,4 +469,32 @@ extern "C" int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int
     return dispatch_epi<uint16_t>(static_cast<const uint16_t *>(x1),
                                   static_cast<const uint16_t *>(x2), batch, n, m, d, aux1, aux2,
                                   epilogue, static_cast<uint16_t *>(out), s);
+}
+
+extern "C" int tpw_pairwise_kernel(const void *x1, const void *x2, int dtype, int64_t batch,
+                                   int64_t n, int64_t m, int64_t d, int kind, float gamma,
+                                   float coef0, int degree, void *out, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(kind == TPW_KER_POLYNOMIAL || kind == TPW_KER_SIGMOID, "unknown kernel %d", kind);
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    TPW_REQUIRE(cdiv(n, kTile) * cdiv(m, kTile) * batch <= 0x7fffffffLL, "output too large for one launch");
+    hipStream_t s = as_stream(stream);
+    KerParams kp;
+    kp.gamma = gamma;
+    kp.coef0 = coef0;
+    kp.degree = degree;
+    if (dtype == TPW_F32) {
+        auto a = static_cast<const float *>(x1), b = static_cast<const float *>(x2);
+        auto o = static_cast<float *>(out);
+        return kind == TPW_KER_POLYNOMIAL
+                   ? launch_inner<float, kEpiPoly, float>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr, 1.0f, kp)
+                   : launch_inner<float, kEpiSigmoid, float>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr, 1.0f, kp);
+    }
+    auto a = static_cast<const uint16_t *>(x1), b = static_cast<const uint16_t *>(x2);
+    auto o = static_cast<uint16_t *>(out);
+    return kind == TPW_KER_POLYNOMIAL
+               ? launch_inner<uint16_t, kEpiPoly, uint16_t>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr, 1.0f, kp)
+               : launch_inner<uint16_t, kEpiSigmoid, uint16_t>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr, 1.0f, kp);
 }

@@ -1,5 +1,5 @@
 // Backward of the inner-product family (euclidean via _euclidean_dist, cosine distance and
-// cosine similarity), fp32 and bf16.
+// cosine similarity, and the polynomial / sigmoid kernel functions), fp32 and bf16.
 //
 // Both gradients have the shape  grad_x1 = sign * (W @ x2) + coef1[i] * x1[i],
 //                                grad_x2 = sign * (W^T @ x1) + coef2[j] * x2[j],
@@ -11,7 +11,12 @@
 //     cosine_similarity gq = grad), gS = prf_div backward (gq / den, or gq where den == 0),
 //     gden = gS * -S / den (0 where den == 0), W = gS, sign = +1,
 //     coef1 = sum_j gden n2[j] / n1[i], coef2 = sum_i gden n1[i] / n2[j] (0 where the norm
-//     is 0, as torch's norm backward).
+//     is 0, as torch's norm backward);
+//   polynomial (pairwise_metrics.cpp:67-78, (S gamma + coef0)^degree):
+//     W = grad * degree * (S gamma + coef0)^(degree - 1) * gamma (S recomputed), sign = +1,
+//     no coefficients;
+//   sigmoid (pairwise_metrics.cpp:80-90, tanh(S gamma + coef0)): W = grad * (1 - out^2) *
+//     gamma from the output.
 //
 // Pass 1 (VALU, memory-bound) forms W in the workspace and writes per-tile partial row and
 // column sums; pass 2 adds the partials in a fixed order (deterministic); pass 3 runs the
@@ -28,7 +33,17 @@
 namespace tpw {
 namespace {
 
-enum Mode { kEuclid = 0, kCosDist = 1, kCosSim = 2, kSqEuclid = 3 };
+enum Mode { kEuclid = 0, kCosDist = 1, kCosSim = 2, kSqEuclid = 3, kPoly = 4, kSigmoid = 5 };
+
+// x^k for an integral k as ATen's pow with a scalar exponent computes it on the GPU.
+__device__ __forceinline__ float ipow(float x, int k) {
+#pragma clang fp contract(off)
+    if (k == 2) return x * x;
+    if (k == 3) return x * x * x;
+    if (k == 1) return x;
+    if (k == 0) return 1.0f;
+    return powf(x, (float)k);
+}
 
 constexpr int kPWRows = 128;
 constexpr int kPWCols = 256;
@@ -48,7 +63,8 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
     const T *__restrict__ g, const T *__restrict__ res, const float *__restrict__ n1,
     const float *__restrict__ n2, int64_t n, int64_t m, const float *__restrict__ S,
     float *__restrict__ rowpart, float *__restrict__ colpart, int64_t tiles_i, int64_t tiles_j,
-    T *__restrict__ Wo, T *__restrict__ WTo) {
+    T *__restrict__ Wo, T *__restrict__ WTo, KerParams kp) {
+#pragma clang fp contract(off)
     constexpr bool BF16W = sizeof(T) == 2;
     constexpr int kGrp = BF16W ? 8 : 4;  // rows per 16-byte transposed store
     __shared__ float red[4][kPWRows];
@@ -80,6 +96,16 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
                 if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
                 rt = w;
                 csum += w;
+            } else if constexpr (MODE == kPoly) {
+                // autograd of matmul(...).mul_(gamma).add_(coef0).pow_(degree): pow's
+                // backward grad * (degree * base^(degree - 1)) (zero for degree 0), then * gamma
+                const float base = S[idx] * kp.gamma + kp.coef0;
+                const float fd = kp.degree == 0 ? 0.0f : (float)kp.degree * ipow(base, kp.degree - 1);
+                w = (gv * fd) * kp.gamma;
+            } else if constexpr (MODE == kSigmoid) {
+                // tanh's backward from its output t: grad * (1 - t * t), then * gamma
+                const float t = to_f32(res[idx]);
+                w = (gv * (1.0f - t * t)) * kp.gamma;
             } else {
                 const float s = S[idx];
                 const float a1 = n1[b * n + i];
@@ -399,12 +425,12 @@ __global__ void transpose_kernel(const T *__restrict__ x, int64_t rows, int64_t 
 template <typename T, int MODE>
 int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float *n1,
                  const float *n2, int dtype, int64_t batch, int64_t n, int64_t m, int64_t d, T *gx1,
-                 T *gx2, void *ws, hipStream_t s) {
+                 T *gx2, void *ws, hipStream_t s, KerParams kp = {}) {
     BwdWs w = carve(ws, batch, n, m, d);
     T *W = static_cast<T *>(w.W), *WT = static_cast<T *>(w.WT);
     T *x1t = static_cast<T *>(w.x1t), *x2t = static_cast<T *>(w.x2t);
     int rc;
-    if constexpr (MODE == kCosDist || MODE == kCosSim) {
+    if constexpr (MODE == kCosDist || MODE == kCosSim || MODE == kPoly) {
         rc = inner_dot_f32(x1, x2, dtype, batch, n, m, d, w.S, s);
         if (rc) return rc;
     }
@@ -412,7 +438,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     constexpr bool kBf16 = sizeof(T) == 2;
     hipLaunchKernelGGL((pair_weights_kernel<T, MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
                        dim3(256), 0, s, g, res, n1, n2, n, m, w.S, w.rowpart, w.colpart, ti, tj, W,
-                       kBf16 ? WT : nullptr);
+                       kBf16 ? WT : nullptr, kp);
     rc = check_launch("pair_weights_kernel");
     if (rc) return rc;
     const bool cosine = MODE == kCosDist || MODE == kCosSim;
@@ -424,7 +450,8 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
                        w.colpart, ti, m, batch, div2, w.coef2);
     rc = check_launch("reduce_parts_kernel");
     if (rc) return rc;
-    const float sign = cosine ? 1.0f : -1.0f;
+    // kernel functions: W carries the whole gradient (rowpart / colpart, hence coef, are 0)
+    const float sign = (cosine || MODE == kPoly || MODE == kSigmoid) ? 1.0f : -1.0f;
     if constexpr (kBf16) {
         // both products as A . B^T with k-contiguous operands on the bf16 matrix cores:
         // gx1 = sign * W . (x2^T)^T + coef1 * x1, gx2 = sign * W^T . (x1^T)^T + coef2 * x2
@@ -520,12 +547,14 @@ extern "C" int tpw_cosine_backward(const void *grad, const void *x1, const void 
         auto run = similarity ? run_backward<float, kCosSim> : run_backward<float, kCosDist>;
         return run(static_cast<const float *>(grad), static_cast<const float *>(x1),
                    static_cast<const float *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
-                   static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s);
+                   static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s,
+                   KerParams{});
     }
     auto run = similarity ? run_backward<uint16_t, kCosSim> : run_backward<uint16_t, kCosDist>;
     return run(static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
                static_cast<const uint16_t *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
-               static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s);
+               static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s,
+               KerParams{});
 }
 
 extern "C" int tpw_sqeuclidean_backward(const void *grad, const void *x1, const void *x2,
@@ -551,4 +580,39 @@ extern "C" int tpw_sqeuclidean_backward(const void *grad, const void *x1, const 
         static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
         static_cast<const uint16_t *>(x2), nullptr, nullptr, nullptr, dtype, batch, n, m, d,
         static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s);
+}
+
+extern "C" int tpw_pairwise_kernel_backward(const void *grad, const void *x1, const void *x2,
+                                            const void *out, int dtype, int64_t batch, int64_t n,
+                                            int64_t m, int64_t d, int kind, float gamma,
+                                            float coef0, int degree, void *grad_x1, void *grad_x2,
+                                            void *workspace, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(kind == TPW_KER_POLYNOMIAL || kind == TPW_KER_SIGMOID, "unknown kernel %d", kind);
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    if (n == 0 || m == 0)
+        return zero_other_side(dtype, batch, n, m, d, grad_x1, grad_x2, as_stream(stream));
+    TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2 && workspace, "null pointer");
+    TPW_REQUIRE(kind == TPW_KER_POLYNOMIAL || out, "the sigmoid backward needs the forward output");
+    TPW_REQUIRE(cdiv(n, kPWRows) <= kMaxGridYZ && cdiv(m, kGT) <= kMaxGridYZ &&
+                    cdiv(n, kGT) <= kMaxGridYZ && batch <= kMaxGridYZ,
+                "sizes exceed the launch grid");
+    hipStream_t s = as_stream(stream);
+    KerParams kp;
+    kp.gamma = gamma;
+    kp.coef0 = coef0;
+    kp.degree = degree;
+    if (dtype == TPW_F32) {
+        auto run = kind == TPW_KER_POLYNOMIAL ? run_backward<float, kPoly> : run_backward<float, kSigmoid>;
+        return run(static_cast<const float *>(grad), static_cast<const float *>(x1),
+                   static_cast<const float *>(x2), static_cast<const float *>(out), nullptr, nullptr,
+                   dtype, batch, n, m, d, static_cast<float *>(grad_x1), static_cast<float *>(grad_x2),
+                   workspace, s, kp);
+    }
+    auto run = kind == TPW_KER_POLYNOMIAL ? run_backward<uint16_t, kPoly> : run_backward<uint16_t, kSigmoid>;
+    return run(static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
+               static_cast<const uint16_t *>(x2), static_cast<const uint16_t *>(out), nullptr, nullptr,
+               dtype, batch, n, m, d, static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2),
+               workspace, s, kp);
 }

@@ -2,6 +2,7 @@
 // autograd and saves what its backward op needs:
 //   _pw_inner            -> _pw_inner_backward (the _euclidean_dist_backward formula for
 //                           EUCLIDEAN, the cosine graph of pairwise_metrics.cpp:51-56,112-122)
+//   _pw_kernel           -> _pw_kernel_backward (autograd of the polynomial / sigmoid composites)
 //   _pw_lp               -> _pw_lp_backward (at::_cdist_backward formulas)
 //   prf_div              -> _prf_div_backward (csrc/ops/autograd/prf_div_kernel.cpp:9-52)
 //   _directed_hausdorff  -> __directed_hausdorff_backward, with the generator cloned so the
@@ -37,6 +38,32 @@ class PwInnerFunction : public torch::autograd::Function<PwInnerFunction> {
         at::Tensor res = saved.size() > 2 ? saved[2] : at::Tensor();
         auto grads = pw_inner_backward(grad_output[0], saved[0], saved[1], res, epi);
         return {std::get<0>(grads), std::get<1>(grads), Variable()};
+    }
+};
+
+class PwKernelFunction : public torch::autograd::Function<PwKernelFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x1, const Variable &x2, int64_t kind,
+                            double gamma, double coef0, int64_t degree) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        auto out = pw_kernel(x1, x2, kind, gamma, coef0, degree);
+        if (kind == TPW_KER_SIGMOID)
+            ctx->save_for_backward({x1, x2, out});  // tanh's backward uses its output
+        else
+            ctx->save_for_backward({x1, x2});  // the polynomial's recomputes x1 . x2^T
+        ctx->saved_data["kind"] = kind;
+        ctx->saved_data["gamma"] = gamma;
+        ctx->saved_data["coef0"] = coef0;
+        ctx->saved_data["degree"] = degree;
+        return out;
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad_output) {
+        auto saved = ctx->get_saved_variables();
+        at::Tensor res = saved.size() > 2 ? saved[2] : at::Tensor();
+        auto grads = pw_kernel_backward(grad_output[0], saved[0], saved[1], res,
+                                        ctx->saved_data["kind"].toInt(), ctx->saved_data["gamma"].toDouble(),
+                                        ctx->saved_data["coef0"].toDouble(), ctx->saved_data["degree"].toInt());
+        return {std::get<0>(grads), std::get<1>(grads), Variable(), Variable(), Variable(), Variable()};
     }
 };
 
@@ -97,6 +124,11 @@ class DirectedHausdorffFunction : public torch::autograd::Function<DirectedHausd
     }
 };
 
+at::Tensor pw_kernel_autograd(const at::Tensor &x1, const at::Tensor &x2, int64_t kind, double gamma,
+                              double coef0, int64_t degree) {
+    return PwKernelFunction::apply(x1, x2, kind, gamma, coef0, degree);
+}
+
 at::Tensor pw_inner_autograd(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue) {
     return PwInnerFunction::apply(x1, x2, epilogue);
 }
@@ -119,6 +151,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff_autograd(
 
 TORCH_LIBRARY_IMPL(torchpairwise, Autograd, m) {
     m.impl("_pw_inner", TORCH_FN(pw_inner_autograd));
+    m.impl("_pw_kernel", TORCH_FN(pw_kernel_autograd));
     m.impl("_pw_lp", TORCH_FN(pw_lp_autograd));
     m.impl("prf_div", TORCH_FN(prf_div_autograd));
     m.impl("_directed_hausdorff", TORCH_FN(directed_hausdorff_autograd));

@@ -91,6 +91,44 @@ std::tuple<at::Tensor, at::Tensor> pw_inner_backward_cuda(const at::Tensor &grad
     return {gx1.reshape(x1.sizes()), gx2.reshape(x2.sizes())};
 }
 
+// ---------------------------------------------------------------- kernel functions (MFMA)
+at::Tensor pw_kernel_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t kind, double gamma,
+                          double coef0, int64_t degree) {
+    check_cuda_pair("_pw_kernel", x1, x2);
+    TORCH_CHECK(x1.scalar_type() == x2.scalar_type(), "_pw_kernel: x1 and x2 dtypes differ");
+    const int dt = float_dtype("_pw_kernel", x1);
+    DeviceGuard guard(x1.device());
+    auto a = as3(x1), b = as3(x2);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options());
+    check_rc(tpw_pairwise_kernel(a.data_ptr(), b.data_ptr(), dt, B, n, m, d, (int)kind, (float)gamma,
+                                 (float)coef0, (int)degree, out.data_ptr(), current_stream()),
+             "_pw_kernel");
+    return out_shape(out, x1);
+}
+
+std::tuple<at::Tensor, at::Tensor> pw_kernel_backward_cuda(const at::Tensor &grad, const at::Tensor &x1,
+                                                           const at::Tensor &x2, const at::Tensor &res,
+                                                           int64_t kind, double gamma, double coef0,
+                                                           int64_t degree) {
+    check_cuda_pair("_pw_kernel_backward", x1, x2);
+    const int dt = float_dtype("_pw_kernel_backward", x1);
+    DeviceGuard guard(x1.device());
+    auto a = as3(x1), b = as3(x2);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto g = grad.to(a.scalar_type()).reshape({B, n, m}).contiguous();
+    at::Tensor r;
+    if (res.defined()) r = res.to(a.scalar_type()).reshape({B, n, m}).contiguous();
+    auto gx1 = at::empty_like(a), gx2 = at::empty_like(b);
+    auto ws = workspace(tpw_inner_backward_workspace_size(B, n, m, d), a);
+    check_rc(tpw_pairwise_kernel_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(),
+                                          r.defined() ? r.data_ptr() : nullptr, dt, B, n, m, d, (int)kind,
+                                          (float)gamma, (float)coef0, (int)degree, gx1.data_ptr(),
+                                          gx2.data_ptr(), ws.data_ptr(), current_stream()),
+             "_pw_kernel_backward");
+    return {gx1.reshape(x1.sizes()), gx2.reshape(x2.sizes())};
+}
+
 // ---------------------------------------------------------------- Minkowski (VALU)
 at::Tensor pw_lp_cuda(const at::Tensor &x1, const at::Tensor &x2, double p) {
     check_cuda_pair("_pw_lp", x1, x2);
@@ -325,6 +363,8 @@ at::Tensor pw_elementwise(const at::Tensor &x1, const at::Tensor &x2, F f) {
 TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
     m.impl("_pw_inner", TORCH_FN(pw_inner_cuda));
     m.impl("_pw_inner_backward", TORCH_FN(pw_inner_backward_cuda));
+    m.impl("_pw_kernel", TORCH_FN(pw_kernel_cuda));
+    m.impl("_pw_kernel_backward", TORCH_FN(pw_kernel_backward_cuda));
     m.impl("_pw_lp", TORCH_FN(pw_lp_cuda));
     m.impl("_pw_lp_backward", TORCH_FN(pw_lp_backward_cuda));
     m.impl("_jaccard", TORCH_FN(jaccard_cuda));

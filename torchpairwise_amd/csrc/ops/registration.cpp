@@ -184,10 +184,17 @@ at::Tensor linear_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &
     return xs.first.matmul(xs.second.transpose(-1, -2));
 }
 
+// pairwise_metrics.cpp:67-78,80-90: matmul, then mul_(gamma).add_(coef0).pow_(degree) /
+// tanh_(); fp32 / bf16 GPU tensors run the function in the MFMA kernel's epilogue (one
+// write of the output instead of four passes), everything else the composite.
 at::Tensor polynomial_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
                              int64_t degree, c10::optional<double> gamma, double coef0) {
     auto xs = check_pairwise_inputs("polynomial_kernel", x1, x2);
     const double g = gamma.value_or(1.0 / x1.size(1));
+    if (hip_float_path(xs.first, xs.second)) {
+        auto ab = broadcast_batch(xs.first, xs.second);
+        return pw_kernel(ab.first, ab.second, TPW_KER_POLYNOMIAL, g, coef0, degree);
+    }
     return xs.first.matmul(xs.second.transpose(-1, -2)).mul_(g).add_(coef0).pow_(degree);
 }
 
@@ -195,6 +202,10 @@ at::Tensor sigmoid_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> 
                           c10::optional<double> gamma, double coef0) {
     auto xs = check_pairwise_inputs("sigmoid_kernel", x1, x2);
     const double g = gamma.value_or(1.0 / x1.size(1));
+    if (hip_float_path(xs.first, xs.second)) {
+        auto ab = broadcast_batch(xs.first, xs.second);
+        return pw_kernel(ab.first, ab.second, TPW_KER_SIGMOID, g, coef0, 0);
+    }
     return xs.first.matmul(xs.second.transpose(-1, -2)).mul_(g).add_(coef0).tanh_();
 }
 
@@ -606,6 +617,26 @@ std::string cuda_arch_flags() { return "gfx950"; }
 // ------------------------------------------------------------------------------------
 // dispatcher handles of the internal ops
 // ------------------------------------------------------------------------------------
+at::Tensor pw_kernel(const at::Tensor &x1, const at::Tensor &x2, int64_t kind, double gamma,
+                     double coef0, int64_t degree) {
+    static auto op = c10::Dispatcher::singleton().findSchemaOrThrow("torchpairwise::_pw_kernel", "")
+                         .typed<at::Tensor(const at::Tensor &, const at::Tensor &, int64_t, double,
+                                           double, int64_t)>();
+    return op.call(x1, x2, kind, gamma, coef0, degree);
+}
+
+std::tuple<at::Tensor, at::Tensor> pw_kernel_backward(const at::Tensor &grad, const at::Tensor &x1,
+                                                      const at::Tensor &x2, const at::Tensor &res,
+                                                      int64_t kind, double gamma, double coef0,
+                                                      int64_t degree) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchpairwise::_pw_kernel_backward", "")
+                         .typed<std::tuple<at::Tensor, at::Tensor>(
+                             const at::Tensor &, const at::Tensor &, const at::Tensor &,
+                             const at::Tensor &, int64_t, double, double, int64_t)>();
+    return op.call(grad, x1, x2, res, kind, gamma, coef0, degree);
+}
+
 at::Tensor pw_inner(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue) {
     static auto op = c10::Dispatcher::singleton().findSchemaOrThrow("torchpairwise::_pw_inner", "")
                          .typed<at::Tensor(const at::Tensor &, const at::Tensor &, int64_t)>();
@@ -700,6 +731,9 @@ at::Tensor row_smallest_mask(const at::Tensor &dist, int64_t count) {
 TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     // ---- internal ops of this build (HIP kernels; Autograd in autograd.cpp) ----
     m.def("_pw_inner(Tensor x1, Tensor x2, int epilogue) -> Tensor");
+    m.def("_pw_kernel(Tensor x1, Tensor x2, int kind, float gamma, float coef0, int degree) -> Tensor");
+    m.def("_pw_kernel_backward(Tensor grad, Tensor x1, Tensor x2, Tensor result, int kind, "
+          "float gamma, float coef0, int degree) -> (Tensor, Tensor)");
     m.def("_pw_inner_backward(Tensor grad, Tensor x1, Tensor x2, Tensor result, int epilogue) -> "
           "(Tensor grad_x1, Tensor grad_x2)");
     m.def("_pw_lp(Tensor x1, Tensor x2, float p) -> Tensor");

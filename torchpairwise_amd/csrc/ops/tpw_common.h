@@ -63,6 +63,13 @@ at::Tensor pw_inner(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue
 std::tuple<at::Tensor, at::Tensor> pw_inner_backward(const at::Tensor &grad, const at::Tensor &x1,
                                                      const at::Tensor &x2, const at::Tensor &res,
                                                      int64_t epilogue);
+// the polynomial / sigmoid kernel functions on the MFMA kernel (TPW_KER_*)
+at::Tensor pw_kernel(const at::Tensor &x1, const at::Tensor &x2, int64_t kind, double gamma,
+                     double coef0, int64_t degree);
+std::tuple<at::Tensor, at::Tensor> pw_kernel_backward(const at::Tensor &grad, const at::Tensor &x1,
+                                                      const at::Tensor &x2, const at::Tensor &res,
+                                                      int64_t kind, double gamma, double coef0,
+                                                      int64_t degree);
 at::Tensor pw_lp(const at::Tensor &x1, const at::Tensor &x2, double p);
 std::tuple<at::Tensor, at::Tensor> pw_lp_backward(const at::Tensor &grad, const at::Tensor &x1,
                                                   const at::Tensor &x2, const at::Tensor &dist,

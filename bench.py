@@ -211,9 +211,9 @@ def run_config(cfg, steps, warmup):
         ms, _ = time_op(dice_composite, steps, warmup)
         emit("dice fwd, reference composite route", ms, pf)
     elif cfg == "KF":
-        # polynomial / sigmoid kernels at the metric shape: the function fused into the MFMA
-        # epilogue against the reference's composite (matmul + mul_ + add_ + pow_ / tanh_) on
-        # the same GPU
+        # kernel functions at the metric shape: polynomial / sigmoid fused into the MFMA
+        # epilogue, rbf / laplacian into the VALU kernel's, each against the reference's
+        # composite (distance or matmul, then the elementwise ops) on the same GPU
         N, D = 16384, 128
         x1 = torch.randn(N, D, generator=torch.Generator().manual_seed(0)).to(dev)
         x2 = torch.randn(N, D, generator=torch.Generator().manual_seed(1)).to(dev)
@@ -224,11 +224,19 @@ def run_config(cfg, steps, warmup):
                 ("polynomial_kernel degree=3", lambda a, b: tp.polynomial_kernel(a, b, 3),
                  lambda a, b: a.matmul(b.transpose(-1, -2)).mul_(g).add_(1.0).pow_(3)),
                 ("sigmoid_kernel", lambda a, b: tp.sigmoid_kernel(a, b),
-                 lambda a, b: a.matmul(b.transpose(-1, -2)).mul_(g).add_(1.0).tanh_())):
+                 lambda a, b: a.matmul(b.transpose(-1, -2)).mul_(g).add_(1.0).tanh_()),
+                # unfused: this build's distance kernel, then mul_ and exp_ (at::cdist p = 1, the
+                # reference's laplacian distance, fails to launch at this size on PyTorch-ROCm:
+                # "invalid configuration argument")
+                ("rbf_kernel", lambda a, b: tp.rbf_kernel(a, b),
+                 lambda a, b: torch.ops.torchpairwise._ppminkowski(a, b, 2.0).mul_(-g).exp_()),
+                ("laplacian_kernel", lambda a, b: tp.laplacian_kernel(a, b),
+                 lambda a, b: tp.manhattan_distances(a, b).mul_(-g).exp_())):
             ms, _ = time_op(lambda: f(x1, x2), steps, warmup)
             emit(f"{name} fwd", ms, pf, {"tflops": 2 * pf / (ms * 1e-3) / 1e12})
             ms, _ = time_op(lambda: ref(x1, x2), steps, warmup)
-            emit(f"{name} fwd, reference composite route", ms, pf)
+            emit(f"{name} fwd, " + ("reference composite route" if "kernel" in name and name[0] in "ps"
+                                    else "unfused route (distance kernel, mul_, exp_)"), ms, pf)
             a, b = x1.clone().requires_grad_(), x2.clone().requires_grad_()
 
             def fb():

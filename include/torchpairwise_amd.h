@@ -103,9 +103,12 @@ int tpw_jaccard_bool(const uint32_t *x1_words, const uint32_t *x2_words,
                      int64_t batch, int64_t n, int64_t m, int64_t d, float *out,
                      void *stream);
 
-/* Kernel functions of tpw_pairwise_kernel */
+/* Kernel functions of tpw_pairwise_kernel (POLYNOMIAL, SIGMOID) and tpw_pairwise_exp_kernel
+ * (RBF, LAPLACIAN) */
 #define TPW_KER_POLYNOMIAL 0
 #define TPW_KER_SIGMOID 1
+#define TPW_KER_RBF 2
+#define TPW_KER_LAPLACIAN 3
 
 /* out = (x1 . x2^T * gamma + coef0)^degree (POLYNOMIAL) or tanh(x1 . x2^T * gamma + coef0)
  * (SIGMOID) on the MFMA kernel, the function applied to the fp32 accumulators before the one
@@ -125,6 +128,15 @@ int tpw_pairwise_kernel_backward(const void *grad, const void *x1, const void *x
                                  const void *out, int dtype, int64_t batch, int64_t n, int64_t m,
                                  int64_t d, int kind, float gamma, float coef0, int degree,
                                  void *grad_x1, void *grad_x2, void *workspace, void *stream);
+
+/* out = exp(-gamma * sum_k (x1 - x2)^2) (RBF, the reference's sqeuclidean = _ppminkowski
+ * p = 2, then mul_(-gamma).exp_()) or exp(-gamma * sum_k |x1 - x2|) (LAPLACIAN, cdist p = 1)
+ * on the VALU tile kernel with the exponential in its epilogue: one write of out instead of
+ * three passes.  fp32 [batch, n, d] x [batch, m, d].  Replaces rbf_kernel / laplacian_kernel
+ * (pairwise_metrics.cpp:92-110); their gradients are the reference's exp backward (grad * out
+ * * -gamma) fed to the _ppminkowski / cdist p = 1 backward entry points above. */
+int tpw_pairwise_exp_kernel(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                            int64_t d, int kind, float gamma, float *out, void *stream);
 
 /* Boolean count metrics of tpw_bool_count_metric */
 #define TPW_BMET_HAMMING 0

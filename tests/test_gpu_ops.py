@@ -411,3 +411,40 @@ def test_kernel_functions_gpu_batched_and_self():
         ref = fn(x1[0].cpu().double(), None, **kw)
         assert_close(fn(x1[0], None, **kw).cpu(), ref, rtol=1e-4, atol=1e-5 * float(ref.abs().max()),
                      what=f"{name} x2=None")
+
+
+# --------------------------------------------------------------------------------------
+# rbf_kernel / laplacian_kernel: exp(-gamma * distance) fused into the VALU kernel; the
+# reference's composite in float64 on the CPU is the bar (fp32 rtol 1e-5 values, 1e-4 grads;
+# bf16 2e-2 / 5e-2)
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("name,gamma", [("rbf_kernel", None), ("rbf_kernel", 0.2), ("rbf_kernel", 0.0),
+                                        ("laplacian_kernel", None), ("laplacian_kernel", 0.05)])
+def test_exp_kernels_gpu(dtype, name, gamma):
+    print(f"{name} gamma={gamma} {dtype}", flush=True)
+    x1, x2 = randn(150, 24, seed=0, dtype=dtype), randn(90, 24, seed=1, dtype=dtype)
+    fn = getattr(tp, name)
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    out = fn(a, b, gamma)
+    assert out.dtype == dtype
+    g = randn(150, 90, seed=3)
+    out.backward(g.to(DEV, dtype))
+    ra, rb = x1.detach().double().requires_grad_(), x2.detach().double().requires_grad_()
+    ref = fn(ra, rb, gamma)
+    ref.backward(g.double())
+    rtol, grtol = (1e-5, 1e-4) if dtype == torch.float32 else (2e-2, 5e-2)
+    assert_close(out.float(), ref, rtol=rtol, atol=rtol * float(ref.abs().max()), what=name)
+    for got, want, nm in ((a.grad, ra.grad, "grad x1"), (b.grad, rb.grad, "grad x2")):
+        assert_close(got.float(), want, rtol=grtol, atol=grtol * float(want.abs().max()) + 1e-30, what=nm)
+
+
+def test_exp_kernels_gpu_batched_and_capi():
+    from torchpairwise_amd import _capi as capi
+    x1, x2 = randn(2, 130, 40, seed=4), randn(2, 70, 40, seed=5)
+    for name, kind in (("rbf_kernel", capi.KER_RBF), ("laplacian_kernel", capi.KER_LAPLACIAN)):
+        fn = getattr(tp, name)
+        ref = fn(x1.double(), x2.double(), 0.03)
+        assert_close(fn(x1.to(DEV), x2.to(DEV), 0.03).cpu(), ref, rtol=1e-5, atol=1e-6, what=name)
+        got = capi.pairwise_exp_kernel(x1.to(DEV), x2.to(DEV), kind, 0.03)
+        assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-6, what=f"{name} C ABI")

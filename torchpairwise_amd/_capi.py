@@ -19,7 +19,7 @@ TPW_F32, TPW_BF16, TPW_F16, TPW_F64, TPW_I8, TPW_U8, TPW_I16, TPW_I32, TPW_I64 =
 BIT_AND, BIT_OR, BIT_XOR, BIT_EQ, BIT_NE = 0, 1, 2, 3, 4
 RED_SUM, RED_MEAN = 0, 1
 EPI_DOT, EPI_EUCLIDEAN, EPI_SQEUCLIDEAN, EPI_COSINE_SIM, EPI_COSINE_DIST = 0, 1, 2, 3, 4
-KER_POLYNOMIAL, KER_SIGMOID = 0, 1
+KER_POLYNOMIAL, KER_SIGMOID, KER_RBF, KER_LAPLACIAN = 0, 1, 2, 3
 FAM_PPMINKOWSKI, FAM_WMINKOWSKI, FAM_CANBERRA, FAM_BRAYCURTIS, FAM_CHI2, FAM_JS = 0, 1, 2, 3, 4, 5
 
 _i64, _p, _i, _d, _sz = C.c_int64, C.c_void_p, C.c_int, C.c_double, C.c_size_t
@@ -35,6 +35,7 @@ _SIGNATURES = {
     "tpw_compare_reduce": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_row_norms": (_i, [_p, _i, _i64, _i64, _i, _p, _p]),
     "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),
+    "tpw_pairwise_exp_kernel": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, C.c_float, _p, _p]),
     "tpw_pairwise_kernel": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, C.c_float, C.c_float, _i, _p, _p]),
     "tpw_pairwise_kernel_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, C.c_float,
                                           C.c_float, _i, _p, _p, _p, _p]),
@@ -518,3 +519,15 @@ def pairwise_kernel_backward(grad, x1, x2, out, kind, gamma, coef0=1.0, degree=3
          _dtype_code(a), B, n, m, d, kind, float(gamma), float(coef0), int(degree), _ptr(gx1), _ptr(gx2),
          _ptr(ws), _stream())
     return (gx1, gx2) if x1.dim() == 3 else (gx1[0], gx2[0])
+
+
+def pairwise_exp_kernel(x1, x2, kind, gamma):
+    """exp(-gamma * sqeuclidean) (KER_RBF) or exp(-gamma * L1) (KER_LAPLACIAN), fp32 rows."""
+    import torch
+
+    a, b = _as3f(x1), _as3f(x2)
+    B, n, d = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=a.device)
+    call("tpw_pairwise_exp_kernel", _ptr(a), _ptr(b), B, n, m, d, kind, float(gamma), _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]

@@ -134,10 +134,13 @@ __device__ __forceinline__ float fam_finish(float acc, float inv_p, float prev) 
 }
 
 // w: per-feature weights [batch, d] (kWeighted only).  out: read first under kBrayDen.
+// exp_post: out = exp(value * post), the kernel functions exp(-gamma * distance) of
+// rbf_kernel / laplacian_kernel (one rounding per operation, as mul_ then exp_).
 template <int MODE, int PK, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
-    int64_t n, int64_t m, int64_t d, float p, float inv_p, float *__restrict__ out) {
+    int64_t n, int64_t m, int64_t d, float p, float inv_p, float *__restrict__ out, int exp_post,
+    float post) {
     __shared__ float As[kBK][kTile + kPad];
     __shared__ float Bs[kBK][kTile + kPad];
     __shared__ float Wk[MODE == kWeighted ? kBK : 1];
@@ -260,6 +263,11 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
             floatx4 v;
 #pragma unroll
             for (int c = 0; c < 4; ++c) v[c] = fam_finish<MODE, PK>(acc[i][4 * h + c], inv_p, prev[c]);
+            if (exp_post) {
+#pragma clang fp contract(off)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = expf(v[c] * post);
+            }
             if (vec_store && col + 3 < m) {
                 store_nt4(orow + col, v);
             } else {
@@ -577,16 +585,17 @@ int pkind_of(double p) {
 
 template <int MODE, int PK>
 int launch_forward(const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
-                   int64_t m, int64_t d, double p, float *out, hipStream_t s) {
+                   int64_t m, int64_t d, double p, float *out, hipStream_t s, bool exp_post = false,
+                   float post = 0.0f) {
     dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
     const bool vec = (d % 4 == 0) && aligned16(x1) && aligned16(x2) && aligned16(out);
     const float pf = (float)p, inv_p = (float)(1.0 / p);
     if (vec)
         hipLaunchKernelGGL((lp_forward_kernel<MODE, PK, true>), grid, dim3(kThreads), 0, s, x1, x2,
-                           w, n, m, d, pf, inv_p, out);
+                           w, n, m, d, pf, inv_p, out, (int)exp_post, post);
     else
         hipLaunchKernelGGL((lp_forward_kernel<MODE, PK, false>), grid, dim3(kThreads), 0, s, x1,
-                           x2, w, n, m, d, pf, inv_p, out);
+                           x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post);
     return check_launch("lp_forward_kernel");
 }
 
@@ -1010,4 +1019,19 @@ extern "C" int tpw_sqjensenshannon_backward(const float *grad, const float *x1, 
     BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, divisor, grad_x1, grad_x2,
              nullptr, part, nullptr, nullptr, false};
     return dispatch_backward<kJS>(kP1, j, s);
+}
+
+extern "C" int tpw_pairwise_exp_kernel(const float *x1, const float *x2, int64_t batch, int64_t n,
+                                       int64_t m, int64_t d, int kind, float gamma, float *out,
+                                       void *stream) {
+    TPW_FAM_CHECKS();
+    TPW_REQUIRE(kind == TPW_KER_RBF || kind == TPW_KER_LAPLACIAN, "unknown kernel %d", kind);
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    hipStream_t s = as_stream(stream);
+    // mul_(-gamma) multiplies by the scalar rounded to float; d == 0 gives exp(0) = 1
+    const float post = -gamma;
+    if (kind == TPW_KER_RBF)  // sqeuclidean = _ppminkowski p = 2: sum of squares, no root
+        return launch_forward<kSum, kP2>(x1, x2, nullptr, batch, n, m, d, 2.0, out, s, true, post);
+    return launch_forward<kRoot, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, out, s, true, post);
 }

@@ -495,6 +495,22 @@ std::tuple<at::Tensor, at::Tensor> js_backward_cuda(const at::Tensor &g, const a
     return {r[0], r[1]};
 }
 
+// rbf_kernel / laplacian_kernel (pairwise_metrics.cpp:92-110): exp(-gamma * distance) with the
+// exponential in the VALU kernel's epilogue (sqeuclidean = _ppminkowski p = 2; cdist p = 1).
+at::Tensor exp_kernel_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t kind, double gamma) {
+    const char *from = "_pw_exp_kernel";
+    TORCH_CHECK(kind == TPW_KER_RBF || kind == TPW_KER_LAPLACIAN, from, ": unknown kernel ", kind);
+    const bool ub = check_family_shapes(from, x1, x2, nullptr);
+    DeviceGuard guard(x1.device());
+    auto a = batched(gpu_f32(x1, from), ub), bb = batched(gpu_f32(x2, from), ub);
+    const int64_t B = a.size(0), n = a.size(1), m = bb.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options());
+    check_rc(tpw_pairwise_exp_kernel(a.data_ptr<float>(), bb.data_ptr<float>(), B, n, m, d, (int)kind,
+                                     (float)gamma, out.data_ptr<float>(), current_stream()),
+             from);
+    return unbatch(out, ub).to(x1.scalar_type());
+}
+
 // ------------------------------------------------------------------------ dispatcher handles
 template <typename Sig>
 c10::TypedOperatorHandle<Sig> op_handle(const char *name) {
@@ -607,6 +623,40 @@ class JSFunction : public torch::autograd::Function<JSFunction> {
     }
 };
 
+// The reference's composite differentiated: exp_'s backward grad * out, mul_'s * (-gamma),
+// then the distance's own backward (_ppminkowski p = 2, or cdist p = 1, which does not read
+// its distance argument).
+class ExpKernelFunction : public torch::autograd::Function<ExpKernelFunction> {
+   public:
+    static Variable forward(AutogradContext *ctx, const Variable &x1, const Variable &x2, int64_t kind,
+                            double gamma) {
+        at::AutoDispatchBelowADInplaceOrView g;
+        auto out = pw_exp_kernel(x1, x2, kind, gamma);
+        ctx->save_for_backward({x1, x2, out});
+        ctx->saved_data["kind"] = kind;
+        ctx->saved_data["gamma"] = gamma;
+        return out;
+    }
+    static variable_list backward(AutogradContext *ctx, const variable_list &grad) {
+        auto s = ctx->get_saved_variables();
+        const double gamma = ctx->saved_data["gamma"].toDouble();
+        auto gf = grad[0].mul(s[2]).mul(-gamma);
+        if (ctx->saved_data["kind"].toInt() == TPW_KER_RBF) {
+            T2 r = ppminkowski_backward_op(gf, s[0], s[1], 2.0);  // 16-bit types via fp32 inside
+            return {std::get<0>(r), std::get<1>(r), Variable(), Variable()};
+        }
+        // the L1 backward kernel is fp32 (as cdist's route converts 16-bit operands)
+        const auto f = at::kFloat;
+        T2 r = pw_lp_backward(gf.to(f), s[0].to(f), s[1].to(f), s[2].to(f), 1.0);
+        return {std::get<0>(r).to(s[0].scalar_type()), std::get<1>(r).to(s[1].scalar_type()), Variable(),
+                Variable()};
+    }
+};
+
+at::Tensor exp_kernel_autograd(const at::Tensor &x1, const at::Tensor &x2, int64_t kind, double gamma) {
+    return ExpKernelFunction::apply(x1, x2, kind, gamma);
+}
+
 at::Tensor ppminkowski_autograd(const at::Tensor &x1, const at::Tensor &x2, double p) {
     return PPMinkowskiFunction::apply(x1, x2, p);
 }
@@ -652,6 +702,11 @@ at::Tensor additive_chi2(const at::Tensor &x1, const at::Tensor &x2) {
         "torchpairwise::_additive_chi2_kernel");
     return op.call(x1, x2);
 }
+at::Tensor pw_exp_kernel(const at::Tensor &x1, const at::Tensor &x2, int64_t kind, double gamma) {
+    static auto op = op_handle<at::Tensor(const at::Tensor &, const at::Tensor &, int64_t, double)>(
+        "torchpairwise::_pw_exp_kernel");
+    return op.call(x1, x2, kind, gamma);
+}
 at::Tensor sqjensenshannon(const at::Tensor &x1, const at::Tensor &x2, c10::optional<double> base) {
     static auto op = op_handle<at::Tensor(const at::Tensor &, const at::Tensor &, c10::optional<double>)>(
         "torchpairwise::_sqjensenshannon");
@@ -673,6 +728,8 @@ TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     m.def("__additive_chi2_kernel_backward(Tensor grad, Tensor x1, Tensor x2) -> (Tensor grad_x1, Tensor grad_x2)");
     m.def("_sqjensenshannon(Tensor x1, Tensor x2, float? base=None) -> Tensor");
     m.def("__sqjensenshannon_backward(Tensor grad, Tensor x1, Tensor x2, float? base) -> (Tensor grad_x1, Tensor grad_x2)");
+    // this build's fused rbf / laplacian (no counterpart schema in the reference)
+    m.def("_pw_exp_kernel(Tensor x1, Tensor x2, int kind, float gamma) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(torchpairwise, CPU, m) {
@@ -703,6 +760,7 @@ TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
     m.impl("__additive_chi2_kernel_backward", TORCH_FN(chi2_backward_cuda));
     m.impl("_sqjensenshannon", TORCH_FN(js_cuda));
     m.impl("__sqjensenshannon_backward", TORCH_FN(js_backward_cuda));
+    m.impl("_pw_exp_kernel", TORCH_FN(exp_kernel_cuda));
 }
 
 TORCH_LIBRARY_IMPL(torchpairwise, Autograd, m) {
@@ -712,6 +770,7 @@ TORCH_LIBRARY_IMPL(torchpairwise, Autograd, m) {
     m.impl("_braycurtis", TORCH_FN(braycurtis_autograd));
     m.impl("_additive_chi2_kernel", TORCH_FN(chi2_autograd));
     m.impl("_sqjensenshannon", TORCH_FN(js_autograd));
+    m.impl("_pw_exp_kernel", TORCH_FN(exp_kernel_autograd));
 }
 
 }  // namespace tpw_ext

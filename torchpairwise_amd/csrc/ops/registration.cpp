@@ -216,9 +216,15 @@ at::Tensor sqeuclidean_distances(const at::Tensor &x1, const c10::optional<at::T
     return ppminkowski(xs.first, xs.second, 2);
 }
 
+// pairwise_metrics.cpp:92-110: sqeuclidean (_ppminkowski p = 2) or cdist p = 1, then
+// mul_(-gamma).exp_(); GPU tensors take the exponential in the VALU kernel's epilogue.
 at::Tensor rbf_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
                       c10::optional<double> gamma) {
     const double g = gamma.value_or(1.0 / x1.size(1));
+    if (x1.is_cuda()) {
+        auto xs = check_pairwise_inputs("sqeuclidean_distances", x1, x2);
+        return pw_exp_kernel(xs.first, xs.second, TPW_KER_RBF, g);
+    }
     return sqeuclidean_distances(x1, x2).mul(-g).exp();
 }
 
@@ -226,6 +232,10 @@ at::Tensor laplacian_kernel(const at::Tensor &x1, const c10::optional<at::Tensor
                             c10::optional<double> gamma) {
     auto xs = check_pairwise_inputs("laplacian_kernel", x1, x2);
     const double g = gamma.value_or(1.0 / x1.size(1));
+    if (hip_float_path(xs.first, xs.second)) {
+        auto ab = broadcast_batch(xs.first, xs.second);
+        return pw_exp_kernel(ab.first, ab.second, TPW_KER_LAPLACIAN, g);
+    }
     return route_cdist(xs.first, xs.second, 1).mul(-g).exp();
 }
 

@@ -84,6 +84,8 @@ at::Tensor canberra(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor braycurtis(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor additive_chi2(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor sqjensenshannon(const at::Tensor &x1, const at::Tensor &x2, c10::optional<double> base);
+// rbf / laplacian with the exponential fused into the VALU kernel (TPW_KER_RBF / _LAPLACIAN)
+at::Tensor pw_exp_kernel(const at::Tensor &x1, const at::Tensor &x2, int64_t kind, double gamma);
 // haversine, snr, squared mahalanobis (special.cpp)
 at::Tensor haversine(const at::Tensor &x1, const at::Tensor &x2);
 at::Tensor snr(const at::Tensor &x1, const at::Tensor &x2);

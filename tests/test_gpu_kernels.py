@@ -174,6 +174,45 @@ def test_lp_backward(p, B, n, m, d, entry):
                      what=f"lp p={p} {nm}")
 
 
+def _sign_counts(a, b):
+    """sum_j sign(a[i, k] - b[j, k]) with sign(NaN) = 0: the p = 1 gradient for grad = 1."""
+    diff = a[:, None, :].astype(np.float64) - b[None, :, :].astype(np.float64)
+    return np.nan_to_num(np.sign(diff), nan=0.0).sum(axis=1)
+
+
+@pytest.mark.parametrize("entry", ["single", "both"])
+def test_lp_backward_p1_sign_exact(entry):
+    """p = 1 with grad = 1: every gradient is an integer count, exact in fp32, so the
+    result must equal sign counts bit for bit.  Ties, neighbours one ulp apart and the
+    scalable range's ends (2^-52, 2^52) run on the pre-scaled sign path; tiles and stages
+    holding 2^-60, a denormal, 2^60, inf or NaN run on the signf path."""
+    n, m, d = 300, 1100, 70
+    rng = np.random.default_rng(11)
+    a = (rng.integers(-8, 9, size=(n, d)) * 0.125).astype(np.float32)
+    b = (rng.integers(-8, 9, size=(m, d)) * 0.125).astype(np.float32)
+    one_up = np.nextafter(np.float32(1.0), np.float32(2.0))
+    a[140, 0], b[50, 0], b[51, 0], b[52, 0] = 1.0, one_up, 1.0, np.nextafter(np.float32(1), np.float32(0))
+    lo, hi = np.float32(2.0 ** -52), np.float32(2.0 ** 52)
+    a[150, 1], a[151, 1], b[60, 1], b[61, 1] = lo, -lo, np.nextafter(lo, np.float32(1)), hi
+    a[152, 2], b[62, 2], b[63, 2] = hi, np.nextafter(hi, np.float32(0)), -hi
+    a[5, 3] = np.float32(2.0 ** -60)              # tile (rows 0-127, features 0-63) off the fast path
+    a[200, 66] = np.float32(2.0 ** 60)            # tile (rows 128-255, features 64-69)
+    b[330, 10] = np.nan                           # stages holding these values
+    b[610, 40] = np.inf
+    b[611, 41] = -np.inf
+    a[260, 40] = np.inf                           # inf - inf = NaN: sign 0
+    b[900, 65] = np.float32(2.0 ** 60)
+    b[1000, 2] = np.float32(1e-40)
+    b[1001, 2] = np.float32(-1e-40)
+    x1, x2 = torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV)
+    g = torch.ones(n, m, device=DEV)
+    dist = capi.lp_distances(x1, x2, 1.0)
+    fn = capi.lp_distances_backward if entry == "single" else capi.lp_distances_backward2
+    gx1, gx2 = fn(g, x1, x2, dist, 1.0)
+    assert_equal(gx1.cpu(), torch.from_numpy(_sign_counts(a, b).astype(np.float32)), "p=1 grad_x1")
+    assert_equal(gx2.cpu(), torch.from_numpy(_sign_counts(b, a).astype(np.float32)), "p=1 grad_x2")
+
+
 # --------------------------------------------------------------------------------------
 # inner-product backward
 # --------------------------------------------------------------------------------------

@@ -58,6 +58,19 @@ __device__ __forceinline__ float to_f32(uint16_t v) { return bf16_to_f32(v); }
 __device__ __forceinline__ void from_f32(float *p, float v) { *p = v; }
 __device__ __forceinline__ void from_f32(uint16_t *p, float v) { *p = f32_to_bf16_rne(v); }
 
+// Raw buffer resource over the `elems` floats that start at `base` (word 3 0x00020000: the
+// 32-bit data format of gfx9 raw buffers).  A dword load at a byte offset at or past the end
+// returns 0 without touching memory; elems <= 0 makes every load return 0.  The range is
+// clamped to 2^32 - 1 bytes, so lane offsets must stay below that.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const float *base, int64_t elems) {
+    const int64_t bytes = elems > 0 ? elems * 4 : 0;
+    const uint32_t num = bytes >= (int64_t)0xffffffffLL ? 0xffffffffu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)num, 0x00020000);
+}
+__device__ __forceinline__ float buffer_load(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_offset, 0, 0));
+}
+
 // Parameters of the kernel-function epilogues (polynomial, sigmoid) of the MFMA kernel.
 struct KerParams {
     float gamma = 0.0f, coef0 = 0.0f;

@@ -297,8 +297,26 @@ __device__ __forceinline__ float pair_weight(float g, float dist, float p) {
     else return dist == 0.0f ? 0.0f : __fdiv_rn(g, powf(dist, p - 1.0f));
 }
 
+// sign(d) as ATen's (0 < d) - (d < 0): +-1, and 0 for +-0 and NaN.  copysign(1, d) is one
+// v_bfi_b32 and "d < 0 or d > 0" one ordered not-equal compare (v_cmp_lg_f32), so the p = 1
+// backward step is 5 VALU ops (sub, bfi, cmp, select, fma) instead of 6.
 __device__ __forceinline__ float signf(float d) {
-    return d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
+    const float s = __builtin_copysignf(1.0f, d);
+    return ((d < 0.0f) | (d > 0.0f)) ? s : 0.0f;
+}
+
+// The p = 1 step sign(a - b) * w in three ops (sub, med3, fma) for operands pre-scaled by
+// 2^75: for a, b in {0} u [2^-52, 2^52] the scaled values are exact and finite, a' - b' has
+// the sign of a - b, and a nonzero difference of such values is a multiple of 2^-75 (at
+// least 2^0 after scaling), so clamping it to [-1, 1] gives exactly sign(a - b).  Tiles or
+// stages holding any other value (NaN and inf included) take the signf path.
+constexpr float kSignScale = 0x1p75f, kSignUnscale = 0x1p-75f;
+__device__ __forceinline__ bool sign_scalable(float x) {
+    const float ax = fabsf(x);
+    return ax == 0.0f || (ax >= 0x1p-52f && ax <= 0x1p52f);
+}
+__device__ __forceinline__ float sign_scaled(float d_scaled) {
+    return __builtin_amdgcn_fmed3f(d_scaled, -1.0f, 1.0f);
 }
 
 template <int PK>
@@ -453,48 +471,139 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         }
     }
 
-    auto stage = [&](int ii, int jj, int64_t i, int64_t j) {
-        float w1 = 0.0f, w2 = 0.0f;
-        if (i < n && j < jend) {
-            const int64_t at = TR ? j * n + i : i * m + j;
-            if constexpr (PRE) {
-                w1 = A0[at];
-                if constexpr (kTwo) w2 = A1[at];
-            } else {
-                pair_weights<MODE, PK>(G[at], A0 ? A0[at] : 0.0f, A1 ? A1[at] : 0.0f, p, w1, w2);
-            }
-        }
-        Ws[jj][ii] = w1;
-        if constexpr (kTwo) Ds[jj][ii] = w2;
-    };
+    // Staging is software-pipelined: the per-pair values and the x2 panel of stage j0 + kBJ
+    // are loaded into registers while stage j0 is computed from LDS, and go to LDS after
+    // the stage's closing barrier.  Lane (tid) loads weight q of a stage at
+    //   direct:     row ii = (tid >> 5) + 8 q, column jj = tid & 31   (coalesced along j)
+    //   transposed: row ii = tid & 127,        column jj = (tid >> 7) + 2 q  (along i)
+    // and panel value q at row jj = (tid >> 6) + 4 q, feature kk = tid & 63.  The loads are
+    // raw buffer loads from wave-uniform bases: a lane past the end of an array reads 0, and
+    // lanes past a row's end (j >= m, k >= d) or past jend read values that only reach
+    // accumulators of rows, features or stage steps that are never stored or run, so no
+    // load needs a bounds branch.
+    constexpr bool kReadG = !PRE;                               // upstream grad
+    constexpr bool kReadA0 = PRE || (MODE == kRoot && PK == kPInf);
+    constexpr bool kReadA1 = PRE && kTwo;
+    float rg[kReadG ? 16 : 1], ra0[kReadA0 ? 16 : 1], ra1[kReadA1 ? 16 : 1], rx[8];
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lw_i = TR ? (tid & 127) : (tid >> 5), lw_j = TR ? (tid >> 7) : (tid & 31);
+    const int lx_j = tid >> 6, lx_k = tid & 63;
+    // byte offsets within a wave's rows (the launch keeps them below 2^32)
+    const uint32_t lw_voff = TR ? (uint32_t)lane * 4u : (uint32_t)(((lane >> 5) * m + (lane & 31)) * 4);
+    const uint32_t lx_voff = (uint32_t)lane * 4u;
+    const int64_t nm = n * m, md = m * d;
 
-    for (int64_t j0 = jbeg; j0 < jend; j0 += kBJ) {
-        // weights: 128 i x 32 j (coalesced along j, or along i when transposed)
-        if constexpr (!TR) {
+    // the 16 per-pair values of one array for stage j0
+    auto load_pairs = [&](const float *arr, auto &r, int64_t j0) {
+        // one descriptor per step keeps the lane offset a single register (per-step lane
+        // offsets would be loop-invariant and stay live across the stage loop)
+        if constexpr (TR) {  // 64 rows of one column per wave and step
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const int idx = tid + kThreads * q;
-                const int ii = idx >> 5, jj = idx & 31;
-                stage(ii, jj, i0 + ii, j0 + jj);
+                const int64_t off = (j0 + (wv >> 1) + 2 * q) * n + i0 + (wv & 1) * 64;
+                r[q] = buffer_load(buffer_over(arr + off, nm - off), lw_voff);
             }
-        } else {
+        } else {  // 32 columns of two rows per wave and step
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const int idx = tid + kThreads * q;
-                const int jj = idx >> 7, ii = idx & 127;
-                stage(ii, jj, i0 + ii, j0 + jj);
+                const int64_t off = (i0 + 2 * wv + 8 * q) * m + j0;
+                r[q] = buffer_load(buffer_over(arr + off, nm - off), lw_voff);
             }
         }
-        // x2 panel: 32 j x 64 k
+    };
+    auto load = [&](int64_t j0) {
+        if constexpr (kReadG) load_pairs(G, rg, j0);
+        if constexpr (kReadA0) load_pairs(A0, ra0, j0);
+        if constexpr (kReadA1) load_pairs(A1, ra1, j0);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const int idx = tid + kThreads * q;
-            const int jj = idx >> 6, kk = idx & 63;
-            const int64_t j = j0 + jj, k = k0 + kk;
-            Xs[jj][kk] = (j < jend && k < d) ? X2[j * d + k] : 0.0f;
+            const int64_t off = (j0 + wv + 4 * q) * d + k0;
+            rx[q] = buffer_load(buffer_over(X2 + off, md - off), lx_voff);
+        }
+    };
+    auto store = [&](int64_t j0) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int ii = lw_i + (TR ? 0 : 8 * q), jj = lw_j + (TR ? 2 * q : 0);
+            float w1 = 0.0f, w2 = 0.0f;
+            if (i0 + ii < n && j0 + jj < jend) {
+                if constexpr (PRE) {
+                    w1 = ra0[q];
+                    if constexpr (kTwo) w2 = ra1[q];
+                } else {
+                    pair_weights<MODE, PK>(rg[q], kReadA0 ? ra0[q] : 0.0f, 0.0f, p, w1, w2);
+                }
+            }
+            Ws[jj][ii] = w1;
+            if constexpr (kTwo) Ds[jj][ii] = w2;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) Xs[lx_j + 4 * q][lx_k] = rx[q];
+    };
+
+    // p = 1 sign fast path (sign_scaled): flags[2] marks a tile of x1 outside the scalable
+    // range, flags[s & 1] a panel of stage s.  A wave that finds such a value stores 1 (the
+    // stores race benignly); thread 0 clears the next stage's word, which no thread reads
+    // again before that stage's barrier.
+    constexpr bool kSignFast = PK == kP1 && (MODE == kRoot || MODE == kSum) && !WGRAD;
+    __shared__ int flags[3];
+    bool tile_fast = false, xv_scaled = false;  // xv holds x1 * 2^75 while xv_scaled
+    if constexpr (kSignFast) {
+        bool ok = true;
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ok = ok && sign_scalable(xv[r][c]);
+        if (tid == 0) flags[0] = flags[2] = 0;
+        __syncthreads();
+        if (__any(!ok) && lane == 0) flags[2] = 1;
+    }
+
+    if (jbeg < jend) load(jbeg);
+    int stage = 0;
+    for (int64_t j0 = jbeg; j0 < jend; j0 += kBJ, ++stage) {
+        store(j0);
+        if constexpr (kSignFast) {
+            bool ok = true;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) ok = ok && sign_scalable(rx[q]);
+            if (__any(!ok) && lane == 0) flags[stage & 1] = 1;
+            if (tid == 0) flags[(stage + 1) & 1] = 0;
         }
         __syncthreads();
+        if (j0 + kBJ < jend) load(j0 + kBJ);
         const int jmax = jend - j0 < kBJ ? (int)(jend - j0) : kBJ;
+        if constexpr (kSignFast) {
+            if (stage == 0) tile_fast = flags[2] == 0;
+            const bool fast = tile_fast && flags[stage & 1] == 0;
+            if (fast != xv_scaled) {  // exact both ways: the tile is in the scalable range
+                const float f = fast ? kSignScale : kSignUnscale;
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) xv[r][c] *= f;
+                xv_scaled = fast;
+            }
+            if (fast) {
+                for (int jj = 0; jj < jmax; ++jj) {
+                    const floatx4 w0 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty]);
+                    const floatx4 w1 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty + 4]);
+                    const floatx4 x = *reinterpret_cast<const floatx4 *>(&Xs[jj][4 * tx]);
+                    const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+                    float xs[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) xs[c] = x[c] * kSignScale;
+#pragma unroll
+                    for (int r = 0; r < 8; ++r)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            acc[r][c] = fmaf(sign_scaled(xv[r][c] - xs[c]), wv[r], acc[r][c]);
+                }
+                __syncthreads();
+                continue;
+            }
+        }
         for (int jj = 0; jj < jmax; ++jj) {
             const floatx4 w0 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty]);
             const floatx4 w1 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty + 4]);
@@ -655,6 +764,9 @@ template <int MODE, int PK, bool TR, bool WGRAD, bool PRE>
 int launch_backward(const float *g, const float *aux0, const float *aux1, const float *x1,
                     const float *x2, const float *w, int64_t batch, int64_t n, int64_t m, int64_t d,
                     double p, float *grad, float *part, hipStream_t s) {
+    // the direct layout's staging lanes span two rows of m: their byte offsets are 32-bit
+    TPW_REQUIRE(TR || 4 * m + 128 < ((int64_t)1 << 32),
+                "backward: %lld columns exceed the kernel's 32-bit staging offsets", (long long)m);
     auto kern = lp_backward_kernel<MODE, PK, TR, WGRAD, PRE>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, 0) != hipSuccess || per_cu <= 0)

@@ -417,12 +417,36 @@ template <int MODE, int PK>
 constexpr bool kPrecomputed = (MODE == kRoot && (PK == kP2 || PK == kP3 || PK == kPLt2 || PK == kPGen)) ||
                               (MODE == kWeighted && PK != kP1) || MODE == kBrayDen;
 
-template <int MODE, int PK>
+// VEC: every pointer is 16-byte aligned; four pairs per step with 16-byte accesses, and the
+// len % 4 tail by the first threads.
+template <int MODE, int PK, bool VEC>
 __global__ void pair_weight_kernel(const float *__restrict__ g, const float *__restrict__ aux0,
                                    const float *aux1, int64_t len, float p, float *w1,
                                    float *__restrict__ w2) {
-    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < len;
-         t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t start = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t tail = 0;
+    if constexpr (VEC) {
+        const int64_t len4 = len >> 2;
+        for (int64_t t = start; t < len4; t += stride) {
+            const floatx4 gv = reinterpret_cast<const floatx4 *>(g)[t];
+            const floatx4 a0 = reinterpret_cast<const floatx4 *>(aux0)[t];
+            floatx4 a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (aux1) a1 = reinterpret_cast<const floatx4 *>(aux1)[t];
+            floatx4 r1, r2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float u, v;
+                pair_weights<MODE, PK>(gv[e], a0[e], a1[e], p, u, v);
+                r1[e] = u;
+                r2[e] = v;
+            }
+            reinterpret_cast<floatx4 *>(w1)[t] = r1;  // may alias aux1 (same elements)
+            if (w2) reinterpret_cast<floatx4 *>(w2)[t] = r2;
+        }
+        tail = len4 << 2;
+    }
+    for (int64_t t = tail + start; t < len; t += stride) {
         float a, b;
         pair_weights<MODE, PK>(g[t], aux0[t], aux1 ? aux1[t] : 0.0f, p, a, b);
         w1[t] = a;  // may alias aux1 (same element)
@@ -790,9 +814,15 @@ int launch_backward(const float *g, const float *aux0, const float *aux1, const 
 template <int MODE, int PK>
 int launch_pair_weights(const float *g, const float *aux0, const float *aux1, int64_t len,
                         double p, float *w1, float *w2, hipStream_t s) {
-    const unsigned grid = (unsigned)(cdiv(len, 256) < 16384 ? cdiv(len, 256) : 16384);
-    hipLaunchKernelGGL((pair_weight_kernel<MODE, PK>), dim3(grid), dim3(256), 0, s, g, aux0, aux1,
-                       len, (float)p, w1, w2);
+    const bool vec = aligned16(g) && aligned16(aux0) && aligned16(aux1) && aligned16(w1) && aligned16(w2);
+    const int64_t items = vec ? cdiv(len, 4) : len;
+    const unsigned grid = (unsigned)(cdiv(items, 256) < 16384 ? cdiv(items, 256) : 16384);
+    if (vec)
+        hipLaunchKernelGGL((pair_weight_kernel<MODE, PK, true>), dim3(grid), dim3(256), 0, s, g, aux0, aux1,
+                           len, (float)p, w1, w2);
+    else
+        hipLaunchKernelGGL((pair_weight_kernel<MODE, PK, false>), dim3(grid), dim3(256), 0, s, g, aux0,
+                           aux1, len, (float)p, w1, w2);
     return check_launch("pair_weight_kernel");
 }
 

@@ -172,6 +172,28 @@ int tpw_bool_count_metric(const uint32_t *x1_words, const uint32_t *x2_words,
                           int64_t batch, int64_t n, int64_t m, int64_t d, int metric, float *out,
                           void *stream);
 
+/* Set bytes per row of a [rows, d] bool matrix (torch.bool layout, bytes 0/1), as int32:
+ * the row popcounts of the byte entry points below.  Replaces nothing in the reference (its
+ * kernels count per output pair). */
+int tpw_bool_row_counts(const uint8_t *x, int64_t rows, int64_t d, int32_t *counts, void *stream);
+
+/* The bool reductions and count metrics straight from bool bytes (0/1, torch.bool layout,
+ * [batch, n, d] and [batch, m, d], any alignment) and their row counts
+ * (tpw_bool_row_counts), on the int8 matrix cores: the AND count of two rows is their int8
+ * dot product (v_mfma_i32_32x32x32_i8, int32 accumulation), and or / xor / ne / eq follow
+ * from it and the row counts as listed for tpw_bool_count_metric.  Outputs equal those of
+ * tpw_bool_pairwise_reduce / tpw_bool_count_metric on the packed rows bit for bit, without
+ * the pack pass.  Replaces pairwise_binary_reduction_forward_kernel<op, Sum|Mean> for bool
+ * inputs (csrc/ops/cuda/pairwise_binary_kernels.cu:32-53,144-220; CPU:
+ * csrc/ops/cpu/pairwise_binary_kernels.cpp:28-49,118-171) and the boolean metric composites
+ * of csrc/ops/pairwise_metrics.cpp:206-243,339-399. */
+int tpw_bool_bytes_reduce(const uint8_t *x1, const uint8_t *x2, const int32_t *x1_counts,
+                          const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m, int64_t d,
+                          int op, int reduction, float *out, void *stream);
+int tpw_bool_bytes_count_metric(const uint8_t *x1, const uint8_t *x2, const int32_t *x1_counts,
+                                const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m,
+                                int64_t d, int metric, float *out, void *stream);
+
 /* Equal / not-equal counts (TPW_BIT_EQ / TPW_BIT_NE, TPW_RED_SUM / TPW_RED_MEAN) of
  * non-bool inputs of element type `elem_type` (TPW_F32 ... TPW_I64), compared by value
  * like C++ ==; output float32 [batch, n, m] as tpw_bool_pairwise_reduce.

@@ -192,3 +192,74 @@ def test_public_boolean_metrics_take_the_fused_path(metric):
     a, b = a[0].to(DEV), b[0].to(DEV)
     assert_equal(_public(metric, a, b), _gpu_composite(metric, a, b), metric, nan_payload=False)
     assert_equal(_public(metric, a, None), _gpu_composite(metric, a, a), f"{metric} self", nan_payload=False)
+
+
+# ------------------------------------------------------------- GPU: bool bytes on the int8 MFMA
+BYTES_DS = (1, 31, 100, 128, 1024, 4096 + 17)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", BYTES_DS)
+@pytest.mark.parametrize("B,n,m", [(1, 130, 257), (2, 64, 33), (1, 256, 384)])
+def test_bool_bytes_entry_points_equal_packed_and_oracle(B, n, m, d):
+    """The int8-MFMA byte path against the packed popcount path (bit for bit) and the
+    oracle's float32 composites over exact counts, for every count metric and reduction."""
+    print(f"bool bytes {B}x{n}x{m} d={d}", flush=True)
+    a, b = _rows(B, n, m, d, seed=80 + d)
+    ga, gb = a.to(DEV), b.to(DEV)
+    wa, pa = torch.ops.torchpairwise._pack_bool(ga)
+    wb, pb = torch.ops.torchpairwise._pack_bool(gb)
+    ca, cb = capi.bool_row_counts(ga), capi.bool_row_counts(gb)
+    assert_equal(ca.cpu(), a.reshape(-1, d).sum(-1).to(torch.int32), "row counts")
+    assert_equal(ca, pa.reshape(-1), "row counts = packed popcounts")
+    for code, metric in enumerate(COUNT):
+        got = capi.bool_bytes_count_metric(ga, gb, code)
+        packed = torch.empty(B, n, m, device=DEV)
+        capi.call("tpw_bool_count_metric", capi._ptr(wa), capi._ptr(wb), capi._ptr(pa), capi._ptr(pb),
+                  B, n, m, d, code, capi._ptr(packed), capi._stream())
+        assert_equal(got, packed, f"{metric} bytes = packed d={d}", nan_payload=False)
+        want = np.stack([P.bool_count_metric(a[i].numpy(), b[i].numpy(), metric, gpu_scalar_divide=True)
+                         for i in range(B)])
+        assert_equal(got.cpu(), torch.from_numpy(want), f"{metric} bytes = oracle d={d}", nan_payload=False)
+    for op, opname in ((capi.BIT_AND, "and"), (capi.BIT_OR, "or"), (capi.BIT_XOR, "xor"),
+                       (capi.BIT_EQ, "eq"), (capi.BIT_NE, "ne")):
+        for red, rname in ((capi.RED_SUM, "sum"), (capi.RED_MEAN, "mean")):
+            got = capi.bool_bytes_reduce(ga, gb, op, red)
+            want = np.stack([P.pw_reduce_bool(a[i].numpy(), b[i].numpy(), opname, rname) for i in range(B)])
+            assert_equal(got.cpu(), torch.from_numpy(want), f"pw{opname}_{rname} bytes d={d}")
+
+
+@pytest.mark.gpu
+def test_bool_bytes_empty_and_errors():
+    x = torch.zeros((0, 16), dtype=torch.bool, device=DEV)
+    y = torch.zeros((5, 16), dtype=torch.bool, device=DEV)
+    assert capi.bool_bytes_count_metric(x, y, 0).shape == (0, 5)
+    assert capi.bool_row_counts(x).shape == (0,)
+    l = capi.lib()
+    assert l.tpw_bool_bytes_count_metric(None, None, None, None, 1, 4, 4, 8, 99, None, None) != 0
+    assert b"unknown metric" in l.tpw_last_error()
+    assert l.tpw_bool_bytes_reduce(None, None, None, None, 1, 4, 4, 0, 0, 0, None, None) != 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", (100, 256, 257, 300, 1024))
+def test_public_bool_ops_on_both_routes(d):
+    """Public bool ops around the route threshold (packed up to 256 features for the pw
+    reductions, int8 matrix cores above; count metrics always on the matrix cores) against the
+    oracle bit for bit, with x2 and with x2 = None."""
+    print(f"public bool ops d={d}", flush=True)
+    a, b = _rows(1, 150, 131, d, seed=90 + d)
+    a, b = a[0], b[0]
+    ga, gb = a.to(DEV), b.to(DEV)
+    for name in PW:
+        op, red = name[2:].split("_")
+        got = _public(name, ga, gb)
+        assert_equal(got.cpu(), torch.from_numpy(P.pw_reduce_bool(a.numpy(), b.numpy(), op, red)),
+                     f"{name} d={d}")
+    for metric in COUNT:
+        want = P.bool_count_metric(a.numpy(), b.numpy(), metric, gpu_scalar_divide=True)
+        assert_equal(_public(metric, ga, gb).cpu(), torch.from_numpy(want), f"{metric} d={d}",
+                     nan_payload=False)
+        want_self = P.bool_count_metric(a.numpy(), a.numpy(), metric, gpu_scalar_divide=True)
+        assert_equal(_public(metric, ga, None).cpu(), torch.from_numpy(want_self),
+                     f"{metric} self d={d}", nan_payload=False)

@@ -32,6 +32,9 @@ _SIGNATURES = {
     "tpw_bool_pairwise_reduce": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_jaccard_bool": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
     "tpw_bool_count_metric": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _p, _p]),
+    "tpw_bool_row_counts": (_i, [_p, _i64, _i64, _p, _p]),
+    "tpw_bool_bytes_reduce": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
+    "tpw_bool_bytes_count_metric": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _p, _p]),
     "tpw_compare_reduce": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_row_norms": (_i, [_p, _i, _i64, _i64, _i, _p, _p]),
     "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),
@@ -172,6 +175,61 @@ def jaccard_bool(x1, x2):
     wb, pb = pack_bool(b)
     out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
     call("tpw_jaccard_bool", _ptr(wa), _ptr(wb), _ptr(pa), _ptr(pb), B, n, m, d, _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def bool_count_metric(x1, x2, metric):
+    """A boolean count metric (TPW_BMET_* code) of bool inputs on the packed popcount path."""
+    import torch
+
+    a, b = _as3(x1), _as3(x2)
+    B, n, d = a.shape
+    m = b.shape[1]
+    wa, pa = pack_bool(a)
+    wb, pb = pack_bool(b)
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    call("tpw_bool_count_metric", _ptr(wa), _ptr(wb), _ptr(pa), _ptr(pb), B, n, m, d, metric, _ptr(out),
+         _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def bool_row_counts(x):
+    """x: bool [..., rows, d] cuda -> int32 [rows_total] set bytes per row."""
+    import torch
+
+    assert x.is_cuda and x.dtype == torch.bool
+    d = x.shape[-1]
+    rows = x.numel() // d if d else 0
+    counts = torch.empty((rows,), dtype=torch.int32, device=x.device)
+    call("tpw_bool_row_counts", _ptr(x.contiguous()), rows, d, _ptr(counts), _stream())
+    return counts
+
+
+def bool_bytes_reduce(x1, x2, op, reduction):
+    """The pw{op}_{reduction} of bool inputs on the int8 matrix cores (no packing)."""
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    ca, cb = bool_row_counts(a), bool_row_counts(b)  # held until the launch is queued
+    call("tpw_bool_bytes_reduce", _ptr(a), _ptr(b), _ptr(ca), _ptr(cb), B, n, m, d, op, reduction,
+         _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def bool_bytes_count_metric(x1, x2, metric):
+    """A boolean count metric (TPW_BMET_* code) of bool inputs on the int8 matrix cores."""
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    ca, cb = bool_row_counts(a), bool_row_counts(b)  # held until the launch is queued
+    call("tpw_bool_bytes_count_metric", _ptr(a), _ptr(b), _ptr(ca), _ptr(cb), B, n, m, d, metric,
+         _ptr(out), _stream())
     return out if x1.dim() == 3 else out[0]
 
 

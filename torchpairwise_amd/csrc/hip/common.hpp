@@ -58,6 +58,28 @@ __device__ __forceinline__ float to_f32(uint16_t v) { return bf16_to_f32(v); }
 __device__ __forceinline__ void from_f32(float *p, float v) { *p = v; }
 __device__ __forceinline__ void from_f32(uint16_t *p, float v) { *p = f32_to_bf16_rne(v); }
 
+// Maps a linear workgroup id to (batch, tile row, tile col) of a tiles_n x tiles_m x batch
+// output grid.  Consecutive workgroup ids go round-robin over the 8 XCDs (id % 8 selects
+// the XCD), so when total % 8 == 0 each XCD gets a contiguous range of tiles; within a
+// batch the tiles run in groups of 8 tile rows, column by column, so that the blocks
+// resident on one XCD share operand panels in its L2.
+__device__ __forceinline__ void xcd_tile_of(int64_t bid, int64_t tiles_n, int64_t tiles_m,
+                                            int64_t total, int64_t &b, int64_t &tr, int64_t &tc) {
+    constexpr int64_t kGroupRows = 8;
+    int64_t t = bid;
+    if ((total & 7) == 0) t = (bid & 7) * (total >> 3) + (bid >> 3);
+    const int64_t per_batch = tiles_n * tiles_m;
+    b = t / per_batch;
+    t -= b * per_batch;
+    const int64_t in_group = kGroupRows * tiles_m;
+    const int64_t g = t / in_group;
+    const int64_t first = g * kGroupRows;
+    const int64_t gsize = tiles_n - first < kGroupRows ? tiles_n - first : kGroupRows;
+    const int64_t o = t - g * in_group;
+    tr = first + o % gsize;
+    tc = o / gsize;
+}
+
 // Raw buffer resource over the `elems` floats that start at `base` (word 3 0x00020000: the
 // 32-bit data format of gfx9 raw buffers).  A dword load at a byte offset at or past the end
 // returns 0 without touching memory; elems <= 0 makes every load return 0.  The range is

@@ -24,7 +24,6 @@ constexpr int kThreads = 256;
 constexpr int kTile = 128;
 constexpr int kRowVec = 8;              // uint4 per 128-byte chunk row
 constexpr int kLdsStride = kRowVec + 1; // in uint4 (144 bytes)
-constexpr int kGroupRows = 8;
 constexpr int kStageStride = 68;         // floats per staged output row (64 + 4 pad)
 static_assert(4 * 32 * kStageStride * 4 <= 2 * kTile * kLdsStride * 16, "staging fits the panels");
 
@@ -160,23 +159,6 @@ __device__ __forceinline__ void mfma_piece(floatx16 (&acc)[2][2], const uint4 (&
     }
 }
 
-// Maps the linear workgroup id to (batch, tile row, tile col).
-__device__ __forceinline__ void tile_of(int64_t bid, int64_t tiles_n, int64_t tiles_m,
-                                        int64_t total, int64_t &b, int64_t &tr, int64_t &tc) {
-    int64_t t = bid;
-    if ((total & 7) == 0) t = (bid & 7) * (total >> 3) + (bid >> 3);
-    const int64_t per_batch = tiles_n * tiles_m;
-    b = t / per_batch;
-    t -= b * per_batch;
-    const int64_t in_group = (int64_t)kGroupRows * tiles_m;
-    const int64_t g = t / in_group;
-    const int64_t first = g * kGroupRows;
-    const int64_t gsize = tiles_n - first < kGroupRows ? tiles_n - first : kGroupRows;
-    const int64_t o = t - g * in_group;
-    tr = first + o % gsize;
-    tc = o / gsize;
-}
-
 template <typename T, typename OutT, int EPI, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
@@ -194,7 +176,7 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     constexpr int KC = Elem<T>::kChunk;
 
     int64_t b, tr, tc;
-    tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
     const int64_t row0 = tr * kTile, col0 = tc * kTile;
     const T *A = x1 + b * n * d;
     const T *B = x2 + b * m * d;

@@ -237,6 +237,222 @@ int launch_reduce(const uint32_t *a, const uint32_t *b, const int32_t *pa, const
     return check_launch("bool_reduce_kernel");
 }
 
+// ---------------------------------------------------------------------------------------
+// Bool bytes on the int8 matrix cores.  A torch.bool row is a 0/1 int8 vector, so the AND
+// count of two rows is their int8 dot product: a 128 x 128 output tile is an int32 GEMM tile
+// (v_mfma_i32_32x32x32_i8; 4 waves of 64 x 64 = 2 x 2 blocks of 32 x 32), and the other
+// counts follow exactly from it and the two rows' popcounts: or = pa + pb - and,
+// xor = ne = pa + pb - 2 and, eq = d - xor.  The epilogue is finish<> above, so results are
+// those of the packed popcount kernel bit for bit.  Operands are staged in LDS in 128-byte
+// chunks of each row (16-byte pad: 144-byte stride); lane (i + 32 h) feeds the MFMA bytes
+// [64 h, 64 h + 64) of row i of a chunk as four 16-byte k pieces, A and B alike, so the k
+// order inside a chunk is permuted identically on both sides and every dot product is
+// unchanged.  The next chunk's global loads are issued before the current chunk's MFMAs.
+constexpr int kBRowVec = 8;                // uint4 per 128-byte chunk row
+constexpr int kBStride = kBRowVec + 1;     // in uint4
+constexpr int kBStage = 68;                // floats per staged output row (64 + 4 pad)
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+typedef int int32x16 __attribute__((ext_vector_type(16)));
+
+// 16 bytes k .. k + 15 of row r of a [rows, d] byte matrix, zero past the row's end or the
+// last row.  VEC: d % 16 == 0 and the base is 16-byte aligned.
+template <bool VEC>
+__device__ __forceinline__ uint4 load_bytes16(const uint8_t *__restrict__ x, int64_t rows, int64_t d,
+                                              int64_t r, int64_t k) {
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (r >= rows) return v;
+    if constexpr (VEC) {
+        if (k < d) v = *reinterpret_cast<const uint4 *>(x + r * d + k);
+    } else {
+        const uint8_t *p = x + r * d;
+        uint32_t e[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t kk = k + 4 * t + u;
+                if (kk < d) w |= (uint32_t)p[kk] << (8 * u);
+            }
+            e[t] = w;
+        }
+        v = make_uint4(e[0], e[1], e[2], e[3]);
+    }
+    return v;
+}
+
+// The count of bitop<OP> (what the packed kernel's tile holds) from the AND count.
+template <int OP, int EPI>
+__device__ __forceinline__ uint32_t count_from_and(uint32_t c, uint32_t pa, uint32_t pb) {
+    if constexpr (EPI >= kJaccard || OP == TPW_BIT_AND) return c;
+    else if constexpr (OP == TPW_BIT_OR) return pa + pb - c;
+    else return pa + pb - 2u * c;  // XOR, NE, and EQ (finish turns ne into d - ne)
+}
+
+template <int OP, int EPI, bool VEC>
+__global__ __launch_bounds__(kThreads, 2) void bool_mfma_kernel(
+    const uint8_t *__restrict__ x1, const uint8_t *__restrict__ x2, const int32_t *__restrict__ popA,
+    const int32_t *__restrict__ popB, int64_t n, int64_t m, int64_t d, double inv_d, float inv_df,
+    float *__restrict__ out, int64_t tiles_n, int64_t tiles_m, int64_t total, bool vec_store) {
+    // operand panels (As, Bs); after the K loop the same bytes stage the fp32 output
+    __shared__ uint4 smem[2 * kTile * kBStride];
+    uint4 *As = smem;
+    uint4 *Bs = smem + kTile * kBStride;
+    __shared__ uint32_t s_pop[2][kTile];  // popcounts of the tile's rows ([0]) and columns ([1])
+
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
+    const int64_t row0 = tr * kTile, col0 = tc * kTile;
+    const uint8_t *A = x1 + b * n * d;
+    const uint8_t *B = x2 + b * m * d;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+    {
+        const int i = tid & (kTile - 1);
+        if (tid < kTile) s_pop[0][i] = row0 + i < n ? (uint32_t)popA[b * n + row0 + i] : 0u;
+        else s_pop[1][i] = col0 + i < m ? (uint32_t)popB[b * m + col0 + i] : 0u;
+    }
+
+    int32x16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0;
+
+    const int64_t nchunks = (d + 127) / 128;  // d >= 1
+    uint4 pa[4], pb[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int idx = tid + kThreads * q;
+        const int r = idx >> 3, c = idx & 7;
+        pa[q] = load_bytes16<VEC>(A, n, d, row0 + r, 16 * c);
+        pb[q] = load_bytes16<VEC>(B, m, d, col0 + r, 16 * c);
+    }
+    for (int64_t kc = 0; kc < nchunks; ++kc) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int idx = tid + kThreads * q;
+            const int r = idx >> 3, c = idx & 7;
+            As[r * kBStride + c] = pa[q];
+            Bs[r * kBStride + c] = pb[q];
+        }
+        __syncthreads();
+        if (kc + 1 < nchunks) {
+            const int64_t kb = (kc + 1) * 128;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int idx = tid + kThreads * q;
+                const int r = idx >> 3, c = idx & 7;
+                pa[q] = load_bytes16<VEC>(A, n, d, row0 + r, kb + 16 * c);
+                pb[q] = load_bytes16<VEC>(B, m, d, col0 + r, kb + 16 * c);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            int32x4 a[2], bv[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+                a[mi] = __builtin_bit_cast(int32x4, As[(wr + mi * 32 + l32) * kBStride + h * 4 + q]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+                bv[ni] = __builtin_bit_cast(int32x4, Bs[(wc + ni * 32 + l32) * kBStride + h * 4 + q]);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mi], bv[ni], acc[mi][ni], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    // Accumulator layout of the 32 x 32 MFMA: register r of lane l holds
+    // row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+    const uint32_t du = (uint32_t)d;
+    const float df = (float)d;
+    uint32_t pbv[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) pbv[ni] = s_pop[1][wc + ni * 32 + l32];
+    const bool full = row0 + kTile <= n && col0 + kTile <= m;
+    if (full && vec_store) {
+        // each wave stages a 32 x 64 half of its tile in its own LDS slice (the operand panels
+        // are free after the K loop's last barrier) and writes it as float4 rows, 16 lanes per
+        // 256-byte segment
+        float *stage = reinterpret_cast<float *>(smem) + wave * (32 * kBStage);
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
+                    const uint32_t pav = s_pop[0][wr + mi * 32 + rr];
+                    const uint32_t c = count_from_and<OP, EPI>((uint32_t)acc[mi][ni][r], pav, pbv[ni]);
+                    stage[rr * kBStage + ni * 32 + l32] = finish<OP, EPI>(c, pav, pbv[ni], du, inv_d, df, inv_df);
+                }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+            __builtin_amdgcn_wave_barrier();
+            float *orow = out + (b * n + row0 + wr + mi * 32) * m + col0 + wc;
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const int rr = it * 4 + (lane >> 4), cc = (lane & 15) * 4;
+                store_nt4(orow + (int64_t)rr * m + cc, *reinterpret_cast<const floatx4 *>(&stage[rr * kBStage + cc]));
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the slice is rewritten
+            __builtin_amdgcn_wave_barrier();
+        }
+        return;
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const int64_t col = col0 + wc + ni * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rr = mi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int64_t row = row0 + wr + rr;
+                if (row < n && col < m) {
+                    const uint32_t pav = s_pop[0][wr + rr];
+                    const uint32_t c = count_from_and<OP, EPI>((uint32_t)acc[mi][ni][r], pav, pbv[ni]);
+                    store_nt(out + (b * n + row) * m + col, finish<OP, EPI>(c, pav, pbv[ni], du, inv_d, df, inv_df));
+                }
+            }
+        }
+}
+
+// Set bytes per row of a [rows, d] bool matrix (one wave per row).
+__global__ void bool_row_counts_kernel(const uint8_t *__restrict__ x, int64_t rows, int64_t d,
+                                       int32_t *__restrict__ counts) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const uint8_t *p = x + row * d;
+    uint32_t c = 0;
+    for (int64_t k = lane; k < d; k += 64) c += p[k] != 0;
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    if (lane == 0) counts[row] = (int32_t)c;
+}
+
+template <int OP, int EPI>
+int launch_bool_mfma(const uint8_t *a, const uint8_t *b, const int32_t *pa, const int32_t *pb,
+                     int64_t batch, int64_t n, int64_t m, int64_t d, float *out, hipStream_t s) {
+    const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
+    const int64_t total = tiles_n * tiles_m * batch;
+    const double inv_d = d < (int64_t)kFloatExactLimit ? 1.0 / (double)d : 0.0;
+    const float inv_df = 1.0f / (float)d;  // as ATen's host-side reciprocal of a CPU scalar
+    const bool vec = d % 16 == 0 && aligned16(a) && aligned16(b);
+    const bool vec_store = m % 4 == 0 && aligned16(out);
+    auto kernel = vec ? bool_mfma_kernel<OP, EPI, true> : bool_mfma_kernel<OP, EPI, false>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(kThreads), 0, s, a, b, pa, pb, n, m, d,
+                       inv_d, inv_df, out, tiles_n, tiles_m, total, vec_store);
+    return check_launch("bool_mfma_kernel");
+}
+
 int check_reduce_args(const uint32_t *a, const uint32_t *b, int64_t batch, int64_t n, int64_t m,
                       int64_t d, float *out) {
     TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 1, "invalid sizes batch=%lld n=%lld m=%lld d=%lld",
@@ -343,4 +559,85 @@ extern "C" int tpw_bool_count_metric(const uint32_t *x1w, const uint32_t *x2w, c
         default: return launch_reduce<TPW_BIT_AND, kCountMetric + TPW_BMET_YULE>(x1w, x2w, pop1, pop2, batch, n, m, d, out, s);
     }
 #undef TPW_MET
+}
+
+extern "C" int tpw_bool_row_counts(const uint8_t *x, int64_t rows, int64_t d, int32_t *counts,
+                                   void *stream) {
+    TPW_REQUIRE(rows >= 0 && d >= 0, "invalid sizes rows=%lld d=%lld", (long long)rows, (long long)d);
+    TPW_REQUIRE(d <= (int64_t)0x7fffffff, "d=%lld exceeds the 32-bit count range", (long long)d);
+    if (rows == 0) return TPW_OK;
+    TPW_REQUIRE(x && counts, "null pointer");
+    hipLaunchKernelGGL(bool_row_counts_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0,
+                       as_stream(stream), x, rows, d, counts);
+    return check_launch("bool_row_counts_kernel");
+}
+
+namespace {
+int check_bytes_args(const uint8_t *a, const uint8_t *b, const int32_t *pa, const int32_t *pb,
+                     int64_t batch, int64_t n, int64_t m, int64_t d, float *out) {
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 1, "invalid sizes batch=%lld n=%lld m=%lld d=%lld",
+                (long long)batch, (long long)n, (long long)m, (long long)d);
+    TPW_REQUIRE(d <= (int64_t)0x7fffffff, "d=%lld exceeds the 32-bit count range", (long long)d);
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(cdiv(n, kTile) * cdiv(m, kTile) * batch <= (int64_t)0x7fffffff, "output too large for one launch");
+    TPW_REQUIRE(a && b && pa && pb && out, "null pointer");
+    return TPW_OK;
+}
+}  // namespace
+
+extern "C" int tpw_bool_bytes_reduce(const uint8_t *x1, const uint8_t *x2, const int32_t *x1_counts,
+                                     const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m,
+                                     int64_t d, int op, int reduction, float *out, void *stream) {
+    TPW_REQUIRE(op >= TPW_BIT_AND && op <= TPW_BIT_NE, "unknown bit op %d", op);
+    TPW_REQUIRE(reduction == TPW_RED_SUM || reduction == TPW_RED_MEAN, "unknown reduction %d",
+                reduction);
+    int rc = check_bytes_args(x1, x2, x1_counts, x2_counts, batch, n, m, d, out);
+    if (rc != TPW_OK) return rc;
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    hipStream_t s = as_stream(stream);
+#define TPW_CASE(OPC, K)                                                                        \
+    case OPC:                                                                                   \
+        return reduction == TPW_RED_SUM                                                         \
+                   ? launch_bool_mfma<K, kSum>(x1, x2, x1_counts, x2_counts, batch, n, m, d, out, s) \
+                   : launch_bool_mfma<K, kMean>(x1, x2, x1_counts, x2_counts, batch, n, m, d, out, s);
+    switch (op) {
+        TPW_CASE(TPW_BIT_AND, TPW_BIT_AND)
+        TPW_CASE(TPW_BIT_OR, TPW_BIT_OR)
+        TPW_CASE(TPW_BIT_XOR, TPW_BIT_XOR)
+        TPW_CASE(TPW_BIT_EQ, TPW_BIT_EQ)
+        TPW_CASE(TPW_BIT_NE, TPW_BIT_XOR)  // NE counts exactly like XOR on bits
+        default: break;
+    }
+#undef TPW_CASE
+    return TPW_ERR_INVALID;
+}
+
+extern "C" int tpw_bool_bytes_count_metric(const uint8_t *x1, const uint8_t *x2,
+                                           const int32_t *x1_counts, const int32_t *x2_counts,
+                                           int64_t batch, int64_t n, int64_t m, int64_t d, int metric,
+                                           float *out, void *stream) {
+    TPW_REQUIRE(metric >= TPW_BMET_HAMMING && metric <= TPW_BMET_YULE, "unknown metric %d", metric);
+    int rc = check_bytes_args(x1, x2, x1_counts, x2_counts, batch, n, m, d, out);
+    if (rc != TPW_OK) return rc;
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    hipStream_t s = as_stream(stream);
+#define TPW_MET(CODE)                                                                                 \
+    case CODE:                                                                                        \
+        return launch_bool_mfma<TPW_BIT_AND, kCountMetric + CODE>(x1, x2, x1_counts, x2_counts, batch, n, \
+                                                                  m, d, out, s);
+    switch (metric) {
+        TPW_MET(TPW_BMET_HAMMING)
+        TPW_MET(TPW_BMET_JACCARD)
+        TPW_MET(TPW_BMET_DICE)
+        TPW_MET(TPW_BMET_KULCZYNSKI1)
+        TPW_MET(TPW_BMET_KULSINSKI)
+        TPW_MET(TPW_BMET_ROGERSTANIMOTO)
+        TPW_MET(TPW_BMET_RUSSELLRAO)
+        TPW_MET(TPW_BMET_SOKALMICHENER)
+        TPW_MET(TPW_BMET_SOKALSNEATH)
+        TPW_MET(TPW_BMET_YULE)
+        default: break;
+    }
+#undef TPW_MET
+    return TPW_ERR_INVALID;
 }

@@ -188,6 +188,30 @@ std::pair<at::Tensor, at::Tensor> pack(const at::Tensor &x3, bool with_pops) {
     return {words, pops};
 }
 
+}  // namespace
+
+void bool_bytes_cuda(const at::Tensor &a, const at::Tensor &b, int bmet, int op, int red, at::Tensor &out) {
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    const bool same = b.is_same(a);
+    auto ca = at::empty({B * n}, a.options().dtype(at::kInt));
+    auto cb = same ? ca : at::empty({B * m}, b.options().dtype(at::kInt));
+    const uint8_t *pa = reinterpret_cast<const uint8_t *>(a.data_ptr<bool>());
+    const uint8_t *pb = reinterpret_cast<const uint8_t *>(b.data_ptr<bool>());
+    check_rc(tpw_bool_row_counts(pa, B * n, d, ca.data_ptr<int32_t>(), current_stream()), "bool row counts");
+    if (!same)
+        check_rc(tpw_bool_row_counts(pb, B * m, d, cb.data_ptr<int32_t>(), current_stream()), "bool row counts");
+    if (bmet >= 0)
+        check_rc(tpw_bool_bytes_count_metric(pa, pb, ca.data_ptr<int32_t>(), cb.data_ptr<int32_t>(), B, n, m, d,
+                                             bmet, out.data_ptr<float>(), current_stream()),
+                 "boolean count metric");
+    else
+        check_rc(tpw_bool_bytes_reduce(pa, pb, ca.data_ptr<int32_t>(), cb.data_ptr<int32_t>(), B, n, m, d, op,
+                                       red, out.data_ptr<float>(), current_stream()),
+                 "pairwise bool reduction");
+}
+
+namespace {
+
 template <int OP, int RED>
 at::Tensor pw_reduce_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), "expected GPU tensors");
@@ -202,7 +226,11 @@ at::Tensor pw_reduce_cuda(const at::Tensor &x1, const at::Tensor &x2) {
         out.fill_(RED == TPW_RED_SUM ? 0.0 : std::numeric_limits<double>::quiet_NaN());
         return out_shape(out, x1);
     }
-    if (common == at::kBool) {
+    if (common == at::kBool && d >= kBoolBytesMinFeatures) {
+        a = a.contiguous();
+        b = x2.is_same(x1) ? a : b.contiguous();
+        bool_bytes_cuda(a, b, -1, OP, RED, out);
+    } else if (common == at::kBool) {
         auto wa = pack(a, false).first, wb = pack(b, false).first;
         check_rc(tpw_bool_pairwise_reduce(reinterpret_cast<const uint32_t *>(wa.data_ptr<int32_t>()),
                                           reinterpret_cast<const uint32_t *>(wb.data_ptr<int32_t>()),
@@ -232,12 +260,9 @@ at::Tensor jaccard_cuda(const at::Tensor &x1, const at::Tensor &x2) {
         out.zero_();
         return out_shape(out, x1);
     }
-    auto pa = pack(a, true), pb = pack(b, true);
-    check_rc(tpw_jaccard_bool(reinterpret_cast<const uint32_t *>(pa.first.data_ptr<int32_t>()),
-                              reinterpret_cast<const uint32_t *>(pb.first.data_ptr<int32_t>()),
-                              pa.second.data_ptr<int32_t>(), pb.second.data_ptr<int32_t>(), B, n, m, d,
-                              out.data_ptr<float>(), current_stream()),
-             "jaccard");
+    a = a.contiguous();
+    b = x2.is_same(x1) ? a : b.contiguous();
+    bool_bytes_cuda(a, b, TPW_BMET_JACCARD, 0, 0, out);
     return out_shape(out, x1);
 }
 

@@ -8,11 +8,12 @@
 //       kulczynski1, kulsinski, rogerstanimoto, russellrao, sokalmichener, sokalsneath, yule)
 //       and the reference's pw reductions (pw{and,or,xor,eq,ne}_sum, pw{eq,ne}_mean).
 //
-// A caller that packs once reuses the words across calls.  The public boolean metrics take the
-// same kernel on GPU tensors (bool_count_metric below): the tile counts a & b per pair once and
-// derives every other count from the row popcounts (xor = pa + pb - 2 and, ...), so each metric
-// is one pass instead of the reference's 2-4 pw*_sum passes plus elementwise passes
-// (pairwise_metrics.cpp:206-243,339-399).  Results equal the reference's: each count is the
+// A caller that packs once reuses the words across calls.  The packed kernel counts a & b per
+// pair once and derives every other count from the row popcounts (xor = pa + pb - 2 and, ...),
+// so each metric is one pass instead of the reference's 2-4 pw*_sum passes plus elementwise
+// passes (pairwise_metrics.cpp:206-243,339-399).  The public boolean metrics on GPU bool
+// tensors (bool_count_metric below) take the same counts and epilogue from the int8 matrix
+// cores, straight from the bool bytes.  Results equal the reference's: each count is the
 // float32 accumulator of ones the pw*_sum ops produce (exact below 2^24, then 2^24) and the
 // float operations follow each composite in order, one rounding each.  russellrao's final
 // "/ d" is a true division on the CPU and a multiply by fl(1 / d) on the GPU, as ATen divides
@@ -279,14 +280,22 @@ at::Tensor packed_bool_metric(const at::Tensor &w1, const at::Tensor &p1, const 
 }
 
 at::Tensor bool_count_metric(const at::Tensor &x1, const at::Tensor &x2, c10::string_view metric) {
-    // GPU bool rows of the public metrics: pack (x2 once when it aliases x1), then one pass
-    if (!x1.is_cuda() || x1.scalar_type() != at::kBool || x2.scalar_type() != at::kBool ||
-        x1.size(-1) < 1 || x1.dim() != x2.dim())
+    // GPU bool rows of the public metrics: one pass on the int8 matrix cores straight from the
+    // bytes (the AND count of two 0/1 rows is their int8 dot product); other inputs, shapes the
+    // composites reject and empty rows take the reference's composite
+    if (!x1.is_cuda() || !x2.is_cuda() || x1.scalar_type() != at::kBool || x2.scalar_type() != at::kBool ||
+        x1.dim() != x2.dim() || (x1.dim() != 2 && x1.dim() != 3) || x1.size(-1) < 1 ||
+        x1.size(-1) != x2.size(-1) || (x1.dim() == 3 && x1.size(0) != x2.size(0)) ||
+        x1.device() != x2.device())
         return at::Tensor();
-    auto a = pack_bool(x1);
-    auto b = x2.is_same(x1) ? a : pack_bool(x2);
-    return packed_bool_metric(std::get<0>(a), std::get<1>(a), std::get<0>(b), std::get<1>(b),
-                              x1.size(-1), metric);
+    const MetricName &mt = metric_of(metric);
+    DeviceGuard guard(x1.device());
+    const bool unbatched = x1.dim() == 2;
+    auto a = (unbatched ? x1.unsqueeze(0) : x1).contiguous();
+    auto b = x2.is_same(x1) ? a : (unbatched ? x2.unsqueeze(0) : x2).contiguous();
+    auto out = at::empty({a.size(0), a.size(1), b.size(1)}, a.options().dtype(at::kFloat));
+    if (out.numel() > 0) bool_bytes_cuda(a, b, mt.bmet, mt.op, mt.red, out);
+    return unbatched ? out.squeeze(0) : out;
 }
 
 TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {

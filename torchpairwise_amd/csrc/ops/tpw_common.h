@@ -96,6 +96,14 @@ std::tuple<at::Tensor, at::Tensor> pack_bool(const at::Tensor &x);
 at::Tensor packed_bool_metric(const at::Tensor &w1, const at::Tensor &p1, const at::Tensor &w2,
                               const at::Tensor &p2, int64_t d, c10::string_view metric);
 at::Tensor bool_count_metric(const at::Tensor &x1, const at::Tensor &x2, c10::string_view metric);
+// Boolean count metric (bmet = TPW_BMET_*) or, with bmet < 0, the pw reduction (op, red) of
+// GPU bool rows a [B, n, d], b [B, m, d] (contiguous, d >= 1) straight from the bytes on the
+// int8 matrix cores, into out [B, n, m] float32.  b may be the same tensor as a.
+void bool_bytes_cuda(const at::Tensor &a, const at::Tensor &b, int bmet, int op, int red, at::Tensor &out);
+// Plain pw reductions of bool rows take the packed popcount kernel up to this many features
+// and the int8 matrix cores above (the count metrics always take the matrix cores): the
+// packed rows are 8x smaller, which wins while the output write dominates.
+constexpr int64_t kBoolBytesMinFeatures = 257;
 at::Tensor prf_div(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
 std::tuple<at::Tensor, at::Tensor> prf_div_backward(const at::Tensor &g, const at::Tensor &x,
                                                     const at::Tensor &y, c10::string_view mode);

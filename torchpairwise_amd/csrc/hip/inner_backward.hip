@@ -203,7 +203,8 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(
     const float *__restrict__ A, const T *__restrict__ B, int64_t M, int64_t N, int64_t K,
     int64_t k_per_split, int64_t batch, float sign, const float *__restrict__ coef,
     const T *__restrict__ X, T *__restrict__ out, float *__restrict__ part) {
-    __shared__ float As[kGK * kGStride];
+    constexpr int kAStride = A_T ? kGStride : kGStride + 2;
+    __shared__ float As[kGK * kAStride];
     __shared__ float Bs[kGK * kGStride];
     const int64_t split = blockIdx.z / batch, b = blockIdx.z - split * batch;
     const int64_t row0 = (int64_t)blockIdx.y * kGT, col0 = (int64_t)blockIdx.x * kGT;
@@ -223,15 +224,21 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
 
-    for (int64_t k0 = kbeg; k0 < kend; k0 += kGK) {
-        // A chunk: 128 rows x 32 k -> As[k][row]
+    // Staging is software-pipelined: chunk k0 + kGK is loaded into registers while chunk k0
+    // is multiplied from LDS.  A chunk: 128 rows x 32 k -> As[k][row]; B chunk: 32 k x 128
+    // cols -> Bs[k][col].  Global reads are 16 bytes along the stored rows.  Direct A is
+    // transposed on its way to LDS: 8 lanes per row, 8 rows per 64 lanes, one float store per
+    // k; its row stride kGStride + 2 (4 * 162 = 8 mod 64) puts the 64 lanes of such a store
+    // on 64 distinct banks (with 160 they would share 8).
+    floatx4 va[4], vb[4];
+    auto load = [&](int64_t k0) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int idx = tid + 256 * q;
+            floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
             if constexpr (!A_T) {
                 const int r = idx >> 3, c4 = idx & 7;
                 const int64_t gr = row0 + r, gk = k0 + 4 * c4;
-                floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (gr < M) {
                     const float *src = Ab + gr * K + gk;
                     if (VEC && gk + 3 < kend) {
@@ -242,12 +249,9 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(
                             if (gk + e < kend) v[e] = src[e];
                     }
                 }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) As[(4 * c4 + e) * kGStride + r] = v[e];
             } else {
                 const int kk = idx >> 5, r4 = idx & 31;
                 const int64_t gk = k0 + kk, gr = row0 + 4 * r4;
-                floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (gk < kend) {
                     const float *src = Ab + gk * M + gr;
                     if (VEC && gr + 3 < M) {
@@ -258,8 +262,8 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(
                             if (gr + e < M) v[e] = src[e];
                     }
                 }
-                *reinterpret_cast<floatx4 *>(&As[kk * kGStride + 4 * r4]) = v;
             }
+            va[q] = v;
         }
         // B chunk: 32 k x 128 cols -> Bs[k][col]
 #pragma unroll
@@ -278,15 +282,37 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(
                         if (gc + e < N) v[e] = to_f32(src[e]);
                 }
             }
-            *reinterpret_cast<floatx4 *>(&Bs[kk * kGStride + 4 * c4]) = v;
+            vb[q] = v;
         }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int idx = tid + 256 * q;
+            if constexpr (!A_T) {
+                const int r = idx >> 3, c4 = idx & 7;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) As[(4 * c4 + e) * kAStride + r] = va[q][e];
+            } else {
+                const int kk = idx >> 5, r4 = idx & 31;
+                *reinterpret_cast<floatx4 *>(&As[kk * kAStride + 4 * r4]) = va[q];
+            }
+            const int kk = idx >> 5, c4 = idx & 31;
+            *reinterpret_cast<floatx4 *>(&Bs[kk * kGStride + 4 * c4]) = vb[q];
+        }
+    };
+
+    if (kbeg < kend) load(kbeg);
+    for (int64_t k0 = kbeg; k0 < kend; k0 += kGK) {
+        store();
         __syncthreads();
+        if (k0 + kGK < kend) load(k0 + kGK);
 #pragma unroll
         for (int s = 0; s < kGK / 2; ++s) {
             const int kk = 2 * s + h;
             float a[2], bv[2];
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) a[mi] = As[kk * kGStride + wr + mi * 32 + l32];
+            for (int mi = 0; mi < 2; ++mi) a[mi] = As[kk * kAStride + wr + mi * 32 + l32];
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) bv[ni] = Bs[kk * kGStride + wc + ni * 32 + l32];
 #pragma unroll
@@ -331,16 +357,48 @@ __global__ void gemm_finish_kernel(const float *__restrict__ part, int64_t split
     from_f32(out + t, sign * s + coef[row] * to_f32(X[t]));
 }
 
+// Blocks of the fp32 product kernel resident at once on the current device (CUs x blocks
+// per CU; every variant of the kernel has the same register and LDS footprint), cached per
+// device.  Without a device (a size query on a host without one) 256 CUs x 3.
+int64_t gemm_slots() {
+    static int cache[16];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256 * 3;
+    int &c = cache[dev & 15];
+    if (c == 0) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, bwd_gemm_kernel<float, false, true>, 256, 0) !=
+                hipSuccess || per_cu <= 0)
+            per_cu = 3;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        c = per_cu * cus;
+    }
+    return c;
+}
+
+// Number of K splits: the smallest whose blocks fill the resident rounds to at least 90 %
+// (the output tiles alone are often a round and a third: C2's 1024 tiles on 768 slots run two
+// rounds for 1.33 rounds of work), else the best fill, with at least 256 k per split.
 int64_t gemm_splits(int64_t batch, int64_t M, int64_t N, int64_t K) {
     const int64_t base = cdiv(M, kGT) * cdiv(N, kGT) * batch;
     if (base == 0) return 1;  // no output tiles (an empty side): nothing to split
-    int64_t splits = cdiv(512, base);
-    const int64_t by_k = cdiv(K, 256);
-    if (splits > by_k) splits = by_k;
-    if (splits > 16) splits = 16;
-    if (splits < 1) splits = 1;
-    while (splits > 1 && splits * batch > kMaxGridYZ) --splits;
-    return splits;
+    const int64_t slots = gemm_slots();
+    int64_t cap = K / 256;
+    if (cap > 8) cap = 8;
+    while (cap > 1 && cap * batch > kMaxGridYZ) --cap;
+    int64_t best = 1;
+    double best_fill = 0.0;
+    for (int64_t sp = 1; sp <= (cap < 1 ? 1 : cap); ++sp) {
+        const int64_t blocks = base * sp;
+        const double fill = (double)blocks / (double)(cdiv(blocks, slots) * slots);
+        if (fill >= 0.9) return sp;
+        if (fill > best_fill + 1e-9) {
+            best_fill = fill;
+            best = sp;
+        }
+    }
+    return best;
 }
 
 template <typename T, bool A_T>

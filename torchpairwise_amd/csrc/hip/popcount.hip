@@ -425,15 +425,25 @@ __global__ __launch_bounds__(kThreads, 2) void bool_mfma_kernel(
         }
 }
 
-// Set bytes per row of a [rows, d] bool matrix (one wave per row).
+// Set bytes per row of a [rows, d] bool matrix (one wave per row).  VEC (d % 16 == 0, 16-byte
+// aligned rows): 16 bytes per lane and step; a bool byte is 0 or 1, so the popcount of a word
+// of them is its number of true bytes.
 __global__ void bool_row_counts_kernel(const uint8_t *__restrict__ x, int64_t rows, int64_t d,
-                                       int32_t *__restrict__ counts) {
+                                       int32_t *__restrict__ counts, bool vec) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const uint8_t *p = x + row * d;
     uint32_t c = 0;
-    for (int64_t k = lane; k < d; k += 64) c += p[k] != 0;
+    if (vec) {
+        for (int64_t k = 16 * (int64_t)lane; k < d; k += 1024) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(p + k);
+            c += __builtin_popcount(v.x) + __builtin_popcount(v.y) + __builtin_popcount(v.z) +
+                 __builtin_popcount(v.w);
+        }
+    } else {
+        for (int64_t k = lane; k < d; k += 64) c += p[k] != 0;
+    }
     for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
     if (lane == 0) counts[row] = (int32_t)c;
 }
@@ -568,7 +578,7 @@ extern "C" int tpw_bool_row_counts(const uint8_t *x, int64_t rows, int64_t d, in
     if (rows == 0) return TPW_OK;
     TPW_REQUIRE(x && counts, "null pointer");
     hipLaunchKernelGGL(bool_row_counts_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0,
-                       as_stream(stream), x, rows, d, counts);
+                       as_stream(stream), x, rows, d, counts, d % 16 == 0 && aligned16(x));
     return check_launch("bool_row_counts_kernel");
 }
 

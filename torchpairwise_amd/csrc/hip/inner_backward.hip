@@ -48,12 +48,6 @@ __device__ __forceinline__ float ipow(float x, int k) {
 constexpr int kPWRows = 128;
 constexpr int kPWCols = 256;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 // Pass 1.  W (type T: fp32, or bf16 rounded as the reference's bf16 autograd rounds its
 // ratio tensor) is written [n, m] to Wo and, when WTo is given, transposed [m, n] to WTo,
 // so that both gradient products read their operands k-contiguous.  The row / column sums
@@ -68,6 +62,10 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
     constexpr bool BF16W = sizeof(T) == 2;
     constexpr int kGrp = BF16W ? 8 : 4;  // rows per 16-byte transposed store
     __shared__ float red[4][kPWRows];
+    // bf16 W^T through LDS: 64 rows x 256 columns as [column][8 x 16 bytes] (144-byte stride),
+    // written out as row segments; needs 16-byte aligned W^T rows (n % 8 == 0)
+    __shared__ uint4 tr[BF16W ? kPWCols * 9 : 1];
+    const bool lds_t = BF16W && (n % 8) == 0;
     const int64_t b = blockIdx.z, ti = blockIdx.y, tj = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t j = tj * kPWCols + tid;
@@ -75,80 +73,163 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
     float a2 = 0.0f;
     if constexpr (MODE == kCosDist || MODE == kCosSim) a2 = jok ? n2[b * m + j] : 0.0f;
     float csum = 0.0f;
-    uint32_t packed[4] = {0u, 0u, 0u, 0u};  // kGrp consecutive rows of column j
-    for (int r = 0; r < kPWRows; ++r) {
-        const int64_t i = ti * kPWRows + r;
-        float rt = 0.0f;
-        uint16_t wb = 0;
-        float wf = 0.0f;
-        if (i < n && jok) {
-            const int64_t idx = (b * n + i) * m + j;
-            const float gv = to_f32(g[idx]);
-            float w;
-            if constexpr (MODE == kEuclid) {
-                const float rv = to_f32(res[idx]);
-                w = rv == 0.0f ? 0.0f : __fdiv_rn(gv, rv);
-                if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
-                rt = w;
-                csum += w;
-            } else if constexpr (MODE == kSqEuclid) {
-                w = 2.0f * gv;
-                if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
-                rt = w;
-                csum += w;
-            } else if constexpr (MODE == kPoly) {
-                // autograd of matmul(...).mul_(gamma).add_(coef0).pow_(degree): pow's
-                // backward grad * (degree * base^(degree - 1)) (zero for degree 0), then * gamma
-                const float base = S[idx] * kp.gamma + kp.coef0;
-                const float fd = kp.degree == 0 ? 0.0f : (float)kp.degree * ipow(base, kp.degree - 1);
-                w = (gv * fd) * kp.gamma;
-            } else if constexpr (MODE == kSigmoid) {
-                // tanh's backward from its output t: grad * (1 - t * t), then * gamma
-                const float t = to_f32(res[idx]);
-                w = (gv * (1.0f - t * t)) * kp.gamma;
-            } else {
-                const float s = S[idx];
-                const float a1 = n1[b * n + i];
-                const float den = a1 * a2;
-                const float q = den != 0.0f ? __fdiv_rn(s, den) : s;
-                float gq = gv;
-                if constexpr (MODE == kCosDist) {
-                    const float v = 1.0f - q;
-                    gq = (v >= 0.0f && v <= 2.0f) ? -gv : 0.0f;
-                }
-                const float gS = den != 0.0f ? __fdiv_rn(gq, den) : gq;
-                const float gden = den != 0.0f ? __fdiv_rn(gS * -s, den) : 0.0f;
-                w = gS;
-                rt = gden * a2;
-                csum += gden * a1;
+    // One element from its loaded operands (gv = grad; av = res for euclid / sigmoid, S for
+    // polynomial / cosine; nv = n1[i] for cosine): the stored weight (wf, or its bf16 bits wb)
+    // and the row-sum term rt.
+    constexpr bool kRes = MODE == kEuclid || MODE == kSigmoid;
+    constexpr bool kS = MODE == kPoly || MODE == kCosDist || MODE == kCosSim;
+    constexpr bool kCos = MODE == kCosDist || MODE == kCosSim;
+    auto element = [&](bool ok, int64_t idx, float gv, float av, float nv, float &wf, uint16_t &wb, float &rt) {
+        wf = 0.0f;
+        wb = 0;
+        rt = 0.0f;
+        if (!ok) return;
+        float w;
+        if constexpr (MODE == kEuclid) {
+            w = av == 0.0f ? 0.0f : __fdiv_rn(gv, av);
+            if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
+            rt = w;
+            csum += w;
+        } else if constexpr (MODE == kSqEuclid) {
+            w = 2.0f * gv;
+            if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
+            rt = w;
+            csum += w;
+        } else if constexpr (MODE == kPoly) {
+            // autograd of matmul(...).mul_(gamma).add_(coef0).pow_(degree): pow's
+            // backward grad * (degree * base^(degree - 1)) (zero for degree 0), then * gamma
+            const float base = av * kp.gamma + kp.coef0;
+            const float fd = kp.degree == 0 ? 0.0f : (float)kp.degree * ipow(base, kp.degree - 1);
+            w = (gv * fd) * kp.gamma;
+        } else if constexpr (MODE == kSigmoid) {
+            // tanh's backward from its output t: grad * (1 - t * t), then * gamma
+            w = (gv * (1.0f - av * av)) * kp.gamma;
+        } else {
+            const float sv = av, a1 = nv;
+            const float den = a1 * a2;
+            const float q = den != 0.0f ? __fdiv_rn(sv, den) : sv;
+            float gq = gv;
+            if constexpr (MODE == kCosDist) {
+                const float v = 1.0f - q;
+                gq = (v >= 0.0f && v <= 2.0f) ? -gv : 0.0f;
             }
-            if constexpr (BF16W) {
-                wb = f32_to_bf16_rne(w);
-                Wo[idx] = wb;
-            } else {
-                Wo[idx] = w;
-                wf = w;
-            }
+            const float gS = den != 0.0f ? __fdiv_rn(gq, den) : gq;
+            const float gden = den != 0.0f ? __fdiv_rn(gS * -sv, den) : 0.0f;
+            w = gS;
+            rt = gden * a2;
+            csum += gden * a1;
         }
-        if constexpr (BF16W) packed[(r & 7) >> 1] |= (uint32_t)wb << (16 * (r & 1));
-        else packed[r & 3] = __float_as_uint(wf);
-        if (WTo && (r % kGrp) == kGrp - 1) {  // rows i-kGrp+1 .. i of column j: 16 B of WTo row j
-            const int64_t i0 = i - (kGrp - 1);
+        if constexpr (BF16W) {
+            wb = f32_to_bf16_rne(w);
+            Wo[idx] = wb;
+        } else {
+            Wo[idx] = w;
+            wf = w;
+        }
+    };
+    // Rows in groups of 8.  The group's 8 row sums over this wave's 64 columns take a
+    // transposing butterfly: xor 32, 16, 8 each hand half of the remaining values to the
+    // partner (4 + 2 + 1 shuffles), leaving lane l with a partial of group row
+    // (l >> 3) & 7 (bits 5, 4, 3 of l), which xor 4, 2, 1 complete: 10 shuffles per 8 rows
+    // instead of 6 per row.
+    const int grow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
+    for (int r0 = 0; r0 < kPWRows; r0 += 8) {
+        float wf[8], rt[8];
+        uint16_t wb[8];
+        // the group's loads first (an invalid element reads element 0 of the batch, which
+        // exists whenever the grid does, and is then dropped), so their latencies overlap
+        float gv[8], av[8], nv[8];
+        bool ok[8];
+        int64_t idx[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t i = ti * kPWRows + r0 + u;
+            ok[u] = i < n && jok;
+            idx[u] = ok[u] ? (b * n + i) * m + j : b * n * m;
+            gv[u] = to_f32(g[idx[u]]);
+            av[u] = 0.0f;
+            nv[u] = 0.0f;
+            if constexpr (kRes) av[u] = to_f32(res[idx[u]]);
+            if constexpr (kS) av[u] = S[idx[u]];
+            if constexpr (kCos) nv[u] = n1[b * n + (ok[u] ? i : 0)];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) element(ok[u], idx[u], gv[u], av[u], nv[u], wf[u], wb[u], rt[u]);
+        if (WTo && lds_t) {
+            // bf16 rows r0 .. r0 + 7 of column j -> the LDS transpose tile (written out below)
+            uint4 pk;
+            pk.x = (uint32_t)wb[0] | ((uint32_t)wb[1] << 16);
+            pk.y = (uint32_t)wb[2] | ((uint32_t)wb[3] << 16);
+            pk.z = (uint32_t)wb[4] | ((uint32_t)wb[5] << 16);
+            pk.w = (uint32_t)wb[6] | ((uint32_t)wb[7] << 16);
+            tr[tid * 9 + ((r0 & 63) >> 3)] = pk;
+        } else if (WTo) {  // rows r0 .. r0 + 7 of column j: 16 bytes (bf16) or 2 x 16 bytes of WTo row j
+            const int64_t i0 = ti * kPWRows + r0;
             if (jok && i0 < n) {
                 T *dst = WTo + (b * m + j) * n + i0;
-                if (i0 + kGrp <= n && (n % kGrp) == 0) {
-                    *reinterpret_cast<uint4 *>(dst) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-                } else {
-                    for (int e = 0; e < kGrp && i0 + e < n; ++e) {
-                        if constexpr (BF16W) dst[e] = (uint16_t)(packed[e >> 1] >> (16 * (e & 1)));
-                        else dst[e] = __uint_as_float(packed[e]);
+#pragma unroll
+                for (int hlf = 0; hlf < 8 / kGrp; ++hlf) {
+                    const int e0 = hlf * kGrp;
+                    uint32_t pk[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (BF16W) pk[e] = (uint32_t)wb[2 * e] | ((uint32_t)wb[2 * e + 1] << 16);
+                        else pk[e] = __float_as_uint(wf[e0 + e]);
+                    }
+                    if (i0 + e0 + kGrp <= n && (n % kGrp) == 0) {
+                        *reinterpret_cast<uint4 *>(dst + e0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                    } else {
+                        for (int e = 0; e < kGrp && i0 + e0 + e < n; ++e) {
+                            if constexpr (BF16W) dst[e0 + e] = wb[e0 + e];
+                            else dst[e0 + e] = wf[e0 + e];
+                        }
                     }
                 }
             }
-            packed[0] = packed[1] = packed[2] = packed[3] = 0u;
         }
-        rt = wave_sum(rt);
-        if (lane == 0) red[wave][r] = rt;
+        float v4[4], v2[2];
+        const bool hi32 = (lane & 32) != 0, hi16 = (lane & 16) != 0, hi8 = (lane & 8) != 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float mine = hi32 ? rt[4 + k] : rt[k], other = hi32 ? rt[k] : rt[4 + k];
+            v4[k] = mine + __shfl_xor(other, 32, 64);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float mine = hi16 ? v4[2 + k] : v4[k], other = hi16 ? v4[k] : v4[2 + k];
+            v2[k] = mine + __shfl_xor(other, 16, 64);
+        }
+        float v1;
+        {
+            const float mine = hi8 ? v2[1] : v2[0], other = hi8 ? v2[0] : v2[1];
+            v1 = mine + __shfl_xor(other, 8, 64);
+        }
+        v1 += __shfl_xor(v1, 4, 64);
+        v1 += __shfl_xor(v1, 2, 64);
+        v1 += __shfl_xor(v1, 1, 64);
+        if ((lane & 7) == 0) red[wave][r0 + grow] = v1;
+        if (WTo && lds_t && (r0 & 63) == 56) {
+            // the 64-row half is complete: write W^T rows j0 .. j0 + 255, 128 contiguous bytes
+            // (rows i0 .. i0 + 63) each, 8 lanes per row segment
+            __syncthreads();
+            const int64_t i0 = ti * kPWRows + (r0 & ~63);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int idx = tid + 256 * q, col = idx >> 3, c = idx & 7;
+                const int64_t jj = tj * kPWCols + col, ii = i0 + 8 * c;
+                if (jj < m && ii < n) {
+                    T *dst = WTo + (b * m + jj) * n + ii;
+                    const uint4 v = tr[col * 9 + c];
+                    if (ii + 8 <= n) {
+                        *reinterpret_cast<uint4 *>(dst) = v;
+                    } else {
+                        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+                        for (int e = 0; ii + e < n; ++e) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+                    }
+                }
+            }
+            __syncthreads();
+        }
     }
     __syncthreads();
     if (tid < kPWRows) {

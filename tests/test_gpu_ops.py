@@ -198,6 +198,29 @@ def test_hausdorff_shuffle_generator_replay():
         assert_equal(got, torch.from_numpy(want), f"shuffled {nm}")
 
 
+@pytest.mark.parametrize("shuffle,with_gen", [(False, False), (True, True), (True, False)])
+def test_hausdorff_autograd_equals_recomputing_backward(shuffle, with_gen):
+    """The autograd backward reuses the forward's output and indices where the reference's
+    re-run of the forward would reproduce them (no shuffle, or a replayed generator); the
+    gradients must equal those of __directed_hausdorff_backward, which re-runs it, bit for bit.
+    A shuffle from the default generator keeps the re-run (checked to run, not compared: its
+    permutation is a new draw)."""
+    c1, c2 = rand(2, 2, 300, 3, seed=10), rand(2, 3, 260, 3, seed=11) + 0.05
+    g = randn(2, 2, 3, seed=12).to(DEV)
+    a, b = c1.to(DEV).requires_grad_(), c2.to(DEV).requires_grad_()
+    gen = torch.Generator(device=DEV).manual_seed(7) if with_gen else None
+    out = tp.directed_hausdorff_distances(a, b, shuffle=shuffle, generator=gen)[0]
+    out.backward(g)
+    if shuffle and not with_gen:
+        assert torch.isfinite(a.grad).all() and torch.isfinite(b.grad).all()
+        return
+    gen2 = torch.Generator(device=DEV).manual_seed(7) if with_gen else None  # the forward's state
+    gx1, gx2 = torch.ops.torchpairwise.__directed_hausdorff_backward(
+        g, c1.to(DEV), c2.to(DEV), shuffle=shuffle, generator=gen2)
+    assert_equal(a.grad, gx1, "grad x1 (saved indices vs re-run)")
+    assert_equal(b.grad, gx2, "grad x2 (saved indices vs re-run)")
+
+
 def test_empty_inputs():
     e = torch.zeros((0, 8), device=DEV)
     x = torch.randn(5, 8, device=DEV)

@@ -107,16 +107,31 @@ class DirectedHausdorffFunction : public torch::autograd::Function<DirectedHausd
     static variable_list forward(AutogradContext *ctx, const Variable &x1, const Variable &x2,
                                  bool shuffle, c10::optional<at::Generator> generator) {
         at::AutoDispatchBelowADInplaceOrView g;
-        ctx->save_for_backward({x1, x2});
         ctx->saved_data["shuffle"] = shuffle;
         ctx->saved_data["generator"] =
             generator.has_value() ? c10::make_optional(generator->clone()) : generator;
         auto r = directed_hausdorff(x1, x2, shuffle, generator);
         ctx->mark_non_differentiable({std::get<1>(r), std::get<2>(r)});
+        // The reference's backward re-runs the forward.  Without shuffling, or with a generator
+        // (whose cloned state the backward replays), that re-run returns exactly this forward's
+        // output and indices, so on the GPU the backward takes them from here instead of
+        // scanning again; a shuffle from the default generator draws a new permutation in the
+        // reference's backward and keeps the re-run.
+        const bool reuse = x1.is_cuda() && (!shuffle || generator.has_value());
+        ctx->saved_data["reuse"] = reuse;
+        if (reuse)
+            ctx->save_for_backward({x1, x2, std::get<0>(r), std::get<1>(r), std::get<2>(r)});
+        else
+            ctx->save_for_backward({x1, x2});
         return {std::get<0>(r), std::get<1>(r), std::get<2>(r)};
     }
     static variable_list backward(AutogradContext *ctx, const variable_list &grad_output) {
         auto saved = ctx->get_saved_variables();
+        if (ctx->saved_data["reuse"].toBool()) {
+            auto grads = directed_hausdorff_backward_indexed_cuda(grad_output[0], saved[0], saved[1],
+                                                                  saved[2], saved[3], saved[4]);
+            return {std::get<0>(grads), std::get<1>(grads), Variable(), Variable()};
+        }
         auto gen = ctx->saved_data["generator"].toOptional<at::Generator>();
         auto grads = directed_hausdorff_backward(grad_output[0], saved[0], saved[1],
                                                  ctx->saved_data["shuffle"].toBool(), gen);

@@ -375,6 +375,30 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_cuda(
     return {gx1, gx2};
 }
 
+}  // namespace
+
+std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_indexed_cuda(
+    const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &out,
+    const at::Tensor &i1, const at::Tensor &i2) {
+    DeviceGuard guard(x1.device());
+    auto a = x1.dim() == 3 ? x1.unsqueeze(0).contiguous() : x1.contiguous();
+    auto b = x2.dim() == 3 ? x2.unsqueeze(0).contiguous() : x2.contiguous();
+    const int64_t B = a.size(0), b1 = a.size(1), b2 = b.size(1);
+    auto o = out.reshape({B, b1, b2}).contiguous();
+    auto m1 = i1.reshape({B, b1, b2}).contiguous(), m2 = i2.reshape({B, b1, b2}).contiguous();
+    auto g = grad.to(at::kFloat).reshape({B, b1, b2}).contiguous();
+    auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(b);
+    check_rc(tpw_directed_hausdorff_backward(
+                 g.data_ptr<float>(), a.data_ptr<float>(), b.data_ptr<float>(), o.data_ptr<float>(),
+                 m1.data_ptr<int64_t>(), m2.data_ptr<int64_t>(), B, b1, a.size(2), b2, b.size(2), a.size(3),
+                 gx1.data_ptr<float>(), gx2.data_ptr<float>(), current_stream()),
+             "__directed_hausdorff_backward");
+    if (x1.dim() == 3) return {gx1.squeeze(0), gx2.squeeze(0)};
+    return {gx1, gx2};
+}
+
+namespace {
+
 // ---------------------------------------------------------------- elementwise pw ops
 template <typename F>
 at::Tensor pw_elementwise(const at::Tensor &x1, const at::Tensor &x2, F f) {

@@ -99,6 +99,11 @@ at::Tensor bool_count_metric(const at::Tensor &x1, const at::Tensor &x2, c10::st
 // Boolean count metric (bmet = TPW_BMET_*) or, with bmet < 0, the pw reduction (op, red) of
 // GPU bool rows a [B, n, d], b [B, m, d] (contiguous, d >= 1) straight from the bytes on the
 // int8 matrix cores, into out [B, n, m] float32.  b may be the same tensor as a.
+// Gradients of _directed_hausdorff on GPU float32 from the forward's output and indices (what
+// the reference's re-run of the forward returns when it replays the same point order).
+std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_indexed_cuda(
+    const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &out,
+    const at::Tensor &i1, const at::Tensor &i2);
 void bool_bytes_cuda(const at::Tensor &a, const at::Tensor &b, int bmet, int op, int red, at::Tensor &out);
 // Plain pw reductions of bool rows take the packed popcount kernel up to this many features
 // and the int8 matrix cores above (the count metrics always take the matrix cores): the

@@ -139,6 +139,22 @@ __device__ __forceinline__ PairPtrs pair_ptrs(const float *xs1, const float *xs2
     return r;
 }
 
+// Exact min over all n of d(m, n), computed by one wave (all lanes return it), for a fixed
+// feature count D: the point's coordinates stay in registers and each lane keeps four points
+// in flight (the min is order-independent, so the result is that of one pass).
+template <int D>
+__device__ float full_scan_min_fixed(const float (&a)[D], const float *X2, int64_t p2) {
+    const int lane = threadIdx.x & 63;
+    float best[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+    int64_t n0 = 0;
+    for (; n0 + 256 <= p2; n0 += 256) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) best[u] = fminf(best[u], sqdist_fixed<D>(a, X2, p2, n0 + 64 * u + lane));
+    }
+    for (int64_t n = n0 + lane; n < p2; n += 64) best[0] = fminf(best[0], sqdist_fixed<D>(a, X2, p2, n));
+    return wave_min(fminf(fminf(best[0], best[1]), fminf(best[2], best[3])));
+}
+
 // Exact min over all n of d(m, n), computed by one wave (all lanes return it).
 __device__ float full_scan_min(const float *a, const float *X2, int64_t p2, int d) {
     const int lane = threadIdx.x & 63;
@@ -150,6 +166,8 @@ __device__ float full_scan_min(const float *a, const float *X2, int64_t p2, int 
     return wave_min(best);
 }
 
+// D > 0: a fixed feature count (coordinates in registers); D == 0: any d <= 64.
+template <int D>
 __global__ __launch_bounds__(kThreads) void seed_kernel(const float *__restrict__ xs1,
                                                         const float *__restrict__ xs2,
                                                         const float *__restrict__ bbox,
@@ -196,10 +214,18 @@ __global__ __launch_bounds__(kThreads) void seed_kernel(const float *__restrict_
     for (int s = wave; s < kSeeds; s += kThreads / 64) {
         const int64_t m = seeds[s];
         if (m >= p1) continue;
-        float a[64];
-        const int dd = d < 64 ? d : 64;
-        for (int k = 0; k < dd; ++k) a[k] = P.x1[k * p1 + m];
-        const float mn = d <= 64 ? full_scan_min(a, P.x2, p2, d) : 0.0f;
+        float mn;
+        if constexpr (D > 0) {
+            float a[D];
+#pragma unroll
+            for (int k = 0; k < D; ++k) a[k] = P.x1[k * p1 + m];
+            mn = full_scan_min_fixed<D>(a, P.x2, p2);
+        } else {
+            float a[64];
+            const int dd = d < 64 ? d : 64;
+            for (int k = 0; k < dd; ++k) a[k] = P.x1[k * p1 + m];
+            mn = d <= 64 ? full_scan_min(a, P.x2, p2, d) : 0.0f;
+        }
         if (lane == 0 && d <= 64) fold_key(&keys[pair], mn, m);
     }
 }
@@ -298,6 +324,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel_any(const float *__restr
 }
 
 // One wave per pair: first n position reaching the winning m's min; write the outputs.
+// D > 0: a fixed feature count (coordinates in registers); D == 0: any d <= 64.
+template <int D>
 __global__ __launch_bounds__(kThreads) void finalize_kernel(
     const float *__restrict__ xs1, const float *__restrict__ xs2,
     const unsigned long long *__restrict__ keys, const int64_t *__restrict__ perm1,
@@ -320,12 +348,36 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(
     const unsigned long long k = keys[pair];
     const int64_t m = (int64_t)(k & 0xffffffffull);
     const float H = __uint_as_float((uint32_t)(k >> 32));
-    float a[64];
-    for (int t = 0; t < d && t < 64; ++t) a[t] = P.x1[(int64_t)t * p1 + m];
+    float a[D > 0 ? D : 64];
+    if constexpr (D > 0) {
+#pragma unroll
+        for (int t = 0; t < D; ++t) a[t] = P.x1[(int64_t)t * p1 + m];
+    } else {
+        for (int t = 0; t < d && t < 64; ++t) a[t] = P.x1[(int64_t)t * p1 + m];
+    }
     int64_t npos = p2;
-    for (int64_t n0 = 0; n0 < p2; n0 += 64) {
+    int64_t start = 0;
+    if constexpr (D > 0) {
+        // four 64-point chunks per step, their ballots taken in order (first hit wins)
+        for (; start + 256 <= p2 && npos == p2; start += 256) {
+            float dist[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) dist[u] = sqdist_fixed<D>(a, P.x2, p2, start + 64 * u + lane);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const unsigned long long mask = __ballot(dist[u] == H);
+                if (mask && npos == p2) npos = start + 64 * u + __builtin_ctzll(mask);
+            }
+        }
+    }
+    for (int64_t n0 = start; n0 < p2 && npos == p2; n0 += 64) {
         const int64_t n = n0 + lane;
-        const bool hit = n < p2 && sqdist(a, P.x2, p2, n, d) == H;
+        float dist = 0.0f;
+        if (n < p2) {
+            if constexpr (D > 0) dist = sqdist_fixed<D>(a, P.x2, p2, n);
+            else dist = sqdist(a, P.x2, p2, n, d);
+        }
+        const bool hit = n < p2 && dist == H;
         const unsigned long long mask = __ballot(hit);
         if (mask) {
             npos = n0 + __builtin_ctzll(mask);
@@ -436,7 +488,9 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
                            x2, perm2, batch * b2, b2, p2, (int)d, w.xs2);
         hipLaunchKernelGGL(bbox_kernel, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2,
                            p2, (int)d, w.bbox);
-        hipLaunchKernelGGL(seed_kernel, dim3((unsigned)pairs), dim3(kThreads), 0, s, w.xs1, w.xs2,
+        auto seed = d == 1 ? seed_kernel<1> : d == 2 ? seed_kernel<2> : d == 3 ? seed_kernel<3>
+                  : d == 4 ? seed_kernel<4> : seed_kernel<0>;
+        hipLaunchKernelGGL(seed, dim3((unsigned)pairs), dim3(kThreads), 0, s, w.xs1, w.xs2,
                            w.bbox, b1, b2, p1, p2, (int)d, w.keys);
         rc = check_launch("hausdorff prologue");
         if (rc) return rc;
@@ -453,7 +507,9 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
         rc = check_launch("hausdorff scan_kernel");
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads),
+    auto fin = d == 1 ? finalize_kernel<1> : d == 2 ? finalize_kernel<2> : d == 3 ? finalize_kernel<3>
+             : d == 4 ? finalize_kernel<4> : finalize_kernel<0>;
+    hipLaunchKernelGGL(fin, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads),
                        0, s, w.xs1, w.xs2, w.keys, perm1, perm2, pairs, b1, b2, p1, p2, (int)d, out,
                        idx1, idx2);
     return check_launch("hausdorff finalize_kernel");

@@ -256,7 +256,8 @@ def test_cosine_backward(B, n, m, d, dtype, similarity):
 # directed Hausdorff: bit-exact value, indices and gradients
 # --------------------------------------------------------------------------------------
 HD_SHAPES = [(None, 2, 300, 3, 400, 3), (2, 2, 257, 3, 129, 3), (None, 3, 100, 2, 700, 2),
-             (None, 2, 150, 3, 90, 5), (None, 1, 1, 1, 1, 3), (None, 2, 2100, 2, 3000, 3)]
+             (None, 2, 150, 3, 90, 5), (None, 1, 1, 1, 1, 3), (None, 2, 2100, 2, 3000, 3),
+             (None, 2, 5000, 2, 4100, 1), (None, 1, 4500, 2, 70, 2)]
 
 
 def _hd_inputs(batch, b1, p1, b2, p2, d, seed=0):
@@ -282,6 +283,36 @@ def test_hausdorff_shuffled_bit_exact():
     w = cref.directed_hausdorff(x1.numpy(), x2.numpy(), perm1.numpy(), perm2.numpy(), threads=8)
     for got, want, nm in zip((out, i1, i2), w, ("value", "idx1", "idx2")):
         assert_equal(got, torch.from_numpy(want), f"shuffled {nm}")
+
+
+@pytest.mark.parametrize("d", [1, 2, 3])
+def test_hausdorff_clustered_bit_exact(d):
+    """x2 packed into a few grid cells: the spatially ordered scan's LDS window is capped and
+    most m fall back to the global part of the scan; x1 spread wide, with a far outlier."""
+    g = torch.Generator().manual_seed(30 + d)
+    x1 = torch.rand(2, 6000, d, generator=g) * 4.0 - 2.0
+    x1[1, 17] = 40.0
+    x2 = 0.5 + 1e-3 * torch.rand(3, 9000, d, generator=g)
+    x2[0, :10] = torch.rand(10, d, generator=g) * 4.0 - 2.0
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV))
+    w_out, w_i1, w_i2 = cref.directed_hausdorff(x1.numpy(), x2.numpy(), threads=8)
+    assert_equal(out.cpu(), torch.from_numpy(w_out), f"clustered value d={d}")
+    assert_equal(i1.cpu(), torch.from_numpy(w_i1), f"clustered idx1 d={d}")
+    assert_equal(i2.cpu(), torch.from_numpy(w_i2), f"clustered idx2 d={d}")
+
+
+@pytest.mark.parametrize("d", [1, 2, 3])
+def test_hausdorff_self_distance_bit_exact(d):
+    """x2 = x1: every min is 0 and T stays 0, so no m can be dropped: every m goes through the
+    queued second pass and its full scan, and the tie rules pick the indices."""
+    g = torch.Generator().manual_seed(40 + d)
+    x = torch.rand(2, 3000, d, generator=g)
+    x[:, 100:110] = x[:, 200:210]  # duplicated points
+    out, i1, i2 = capi.directed_hausdorff(x.to(DEV), x.to(DEV))
+    w_out, w_i1, w_i2 = cref.directed_hausdorff(x.numpy(), x.numpy(), threads=8)
+    assert_equal(out.cpu(), torch.from_numpy(w_out), f"self value d={d}")
+    assert_equal(i1.cpu(), torch.from_numpy(w_i1), f"self idx1 d={d}")
+    assert_equal(i2.cpu(), torch.from_numpy(w_i2), f"self idx2 d={d}")
 
 
 def test_hausdorff_ties_bit_exact():

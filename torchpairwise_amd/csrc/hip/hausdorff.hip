@@ -13,11 +13,13 @@
 //      given, is applied here, so every later scan is contiguous);
 //   2. seed: per cloud pair, the 8 points of x1 farthest from x2's bounding box get an exact
 //      full scan; their largest min is a first threshold T (a lower bound of the answer);
-//   3. scan: every wave takes one m at a time; its 64 lanes evaluate 64 consecutive n per
-//      step (the first points of x2 come from LDS), and the wave drops m as soon as any lane
-//      sees d < T (a ballot).  An m scanned to the end has its exact min; it is folded into
-//      the pair's key (float bits of min << 32 | m position) with a 64-bit atomicMax, which
-//      also raises T for everyone.  Equal mins resolve to the larger m position = the last m.
+//   3. scan (d <= 3): x2 clouds are counting-sorted by grid cell once; every lane takes one m
+//      and checks the 64 sorted x2 points at m's cell, stopping at the first d < T; the m left
+//      are scanned by the whole wave (64 n per step, dropping m at the first d < T).
+//      (d > 3: every wave takes one m at a time over x2 in iteration order, the first points
+//      from LDS.)  An m scanned to the end has its exact min; it is folded into the pair's key
+//      (float bits of min << 32 | m position) with a 64-bit atomicMax, which also raises T for
+//      everyone.  Equal mins resolve to the larger m position = the last m.
 //   4. finalize: one wave per pair rescans the winning m for the first n position reaching
 //      its min, and writes sqrt, and the (permuted) indices.
 //
@@ -429,23 +431,243 @@ __global__ void backward_x2_kernel(const float *__restrict__ g, const float *__r
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Scan with a spatial first guess (D = 1, 2, 3).  Pruning an m needs only one distance below
+// T, and an m that is never pruned gets its exact min whatever order x2 is visited in.  Each
+// x2 cloud is therefore counting-sorted once by a grid cell (4096 cells over the cloud's
+// bounding box; Morton order of 16^3 / 64^2 cells, or 4096 intervals for D = 1), and the scan
+// first tries, for every m, the 64 sorted points at m's own cell, which almost always hold
+// one within T.  x1 stays in iteration order, so the m that need more (points far from x2,
+// with mins near T) are spread evenly over the waves.
+constexpr int kCells = 4096;
+
+template <int D>
+__device__ __forceinline__ uint32_t spread_bits(uint32_t v) {
+    if constexpr (D == 3) {  // 4 bits -> every third bit
+        v &= 0xfu;
+        v = (v | (v << 4)) & 0x0c3u;
+        v = (v | (v << 2)) & 0x249u;
+        return v;
+    } else {  // D == 2: 6 bits -> every second bit
+        v &= 0x3fu;
+        v = (v | (v << 4)) & 0x30fu;
+        v = (v | (v << 2)) & 0x333u;
+        v = (v | (v << 1)) & 0x555u;
+        return v;
+    }
+}
+
+// Cell of a point in a frame (lo[k], cells per unit[k]); coordinates outside it clamp to the
+// nearest boundary cell and NaN goes to cell 0.
+template <int D>
+__device__ __forceinline__ uint32_t cell_of(const float (&a)[D], const float (&fr)[2 * D]) {
+    constexpr int kBits = D == 3 ? 4 : D == 2 ? 6 : 12;
+    constexpr float kMax = (float)((1 << kBits) - 1);
+    uint32_t c = 0;
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        const float q = fminf(fmaxf((a[k] - fr[2 * k]) * fr[2 * k + 1], 0.0f), kMax);
+        const uint32_t u = (uint32_t)q;
+        if constexpr (D == 1) c = u;
+        else c |= spread_bits<D>(u) << k;
+    }
+    return c;
+}
+
+// The frame of an x2 cloud from its bounding box (bbox[k][0..1]).
+template <int D>
+__device__ __forceinline__ void frame_of(const float *box, float (&fr)[2 * D]) {
+    constexpr int kBits = D == 3 ? 4 : D == 2 ? 6 : 12;
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        const float lo = box[2 * k], span = box[2 * k + 1] - lo;
+        fr[2 * k] = lo == lo ? lo : 0.0f;
+        fr[2 * k + 1] = span > 0.0f && span < INFINITY ? (float)(1 << kBits) / span : 0.0f;
+    }
+}
+
+// Counting sort of one x2 cloud (block) by cell into xs_sorted (SoA), with the cloud's cell
+// start offsets cstart[kCells + 1].  Points of one cell land in an unspecified order (LDS
+// atomics); nothing depends on it.
+template <int D>
+__global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__restrict__ xs, int64_t p,
+                                                             const float *__restrict__ bbox,
+                                                             float *__restrict__ xs_sorted,
+                                                             int32_t *__restrict__ cstart) {
+    __shared__ uint32_t cnt[kCells];
+    __shared__ uint32_t part[kThreads];
+    const int64_t c = blockIdx.x;
+    const float *X = xs + c * D * p;
+    float fr[2 * D];
+    frame_of<D>(bbox + c * D * 2, fr);
+    for (int t = threadIdx.x; t < kCells; t += kThreads) cnt[t] = 0u;
+    __syncthreads();
+    for (int64_t n = threadIdx.x; n < p; n += kThreads) {
+        float a[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) a[k] = X[k * p + n];
+        atomicAdd(&cnt[cell_of<D>(a, fr)], 1u);
+    }
+    __syncthreads();
+    constexpr int kPer = kCells / kThreads;  // exclusive scan: 16 consecutive cells per thread
+    uint32_t local = 0;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) local += cnt[threadIdx.x * kPer + e];
+    part[threadIdx.x] = local;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0;
+        for (int t = 0; t < kThreads; ++t) {
+            const uint32_t v = part[t];
+            part[t] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    uint32_t run = part[threadIdx.x];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+        const int cell = threadIdx.x * kPer + e;
+        const uint32_t v = cnt[cell];
+        cnt[cell] = run;
+        cstart[c * (kCells + 1) + cell] = (int32_t)run;
+        run += v;
+    }
+    if (threadIdx.x == 0) cstart[c * (kCells + 1) + kCells] = (int32_t)p;
+    __syncthreads();
+    float *O = xs_sorted + c * D * p;
+    for (int64_t n = threadIdx.x; n < p; n += kThreads) {
+        float a[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) a[k] = X[k * p + n];
+        const uint32_t slot = atomicAdd(&cnt[cell_of<D>(a, fr)], 1u);
+#pragma unroll
+        for (int k = 0; k < D; ++k) O[k * p + slot] = a[k];
+    }
+}
+
+// Block = 2048 consecutive m (iteration order) of one pair; each wave takes 64 m at a time,
+// one per lane.  A lane checks the 64 sorted x2 points starting 32 before its cell's start
+// and stops at the first d < T.  The lanes left (ballot) are taken one after another by the
+// whole wave: a circular scan of all of x2 from that start, four 64-point steps in flight,
+// dropping m at the first d < T; an m never dropped folds its exact min.
+template <int D>
+__global__ __launch_bounds__(kThreads) void scan_window_kernel(
+    const float *__restrict__ xs1, const float *__restrict__ xs2s, const int32_t *__restrict__ cstart2,
+    const float *__restrict__ bbox2, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
+    int64_t m_per_block, unsigned long long *__restrict__ keys) {
+    const int64_t pair = blockIdx.y;
+    const int64_t per_batch = b1 * b2;
+    const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
+    const int64_t i = rem / b2, j = rem - i * b2;
+    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
+    const float *X2 = xs2s + (bb * b2 + j) * D * p2;
+    const int32_t *CS = cstart2 + (bb * b2 + j) * (kCells + 1);
+    float fr[2 * D];
+    frame_of<D>(bbox2 + (bb * b2 + j) * D * 2, fr);
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the same in every lane
+    const int64_t mbeg = (int64_t)blockIdx.x * m_per_block;
+    const int64_t mend = mbeg + m_per_block < p1 ? mbeg + m_per_block : p1;
+    const int64_t wstart = p2 > 64 ? p2 - 64 : 0;  // last start of a full 64-point window
+    unsigned long long *key = &keys[pair];
+    for (int64_t m0 = mbeg + 64 * wave; m0 < mend; m0 += 64 * (kThreads / 64)) {
+        const int64_t m = m0 + lane;
+        const bool valid = m < mend;
+        float a[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) a[k] = valid ? X1[k * p1 + m] : 0.0f;
+        int64_t s0 = (int64_t)CS[cell_of<D>(a, fr)] - 32;
+        s0 = s0 > wstart ? wstart : s0;
+        s0 = s0 < 0 ? 0 : s0;
+        float T = threshold_of(key);
+        // per lane: the 64 points of its window (fewer when p2 < 64), 8 per step so that their
+        // loads are in flight together
+        const int64_t wlen = p2 < 64 ? p2 : 64;
+        bool done = !valid;
+        for (int64_t t = 0; t < wlen && !done; t += 8) {
+            bool hit = false;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (t + u < wlen) hit = hit | (sqdist_fixed<D>(a, X2, p2, s0 + t + u) < T);
+            done = hit;
+        }
+        unsigned long long left = __ballot(!done);
+        while (left) {
+            const int l = __builtin_ctzll(left);
+            left &= left - 1;
+            float b[D];
+#pragma unroll
+            for (int k = 0; k < D; ++k) b[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[k]), l));
+            const int64_t st = (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)s0, l);
+            T = threshold_of(key);
+            float best = INFINITY;
+            bool pruned = false;
+            int64_t t0 = 0;
+            for (; t0 + 256 <= p2; t0 += 256) {
+                float dd[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    int64_t n = st + t0 + 64 * u + lane;
+                    if (n >= p2) n -= p2;
+                    dd[u] = sqdist_fixed<D>(b, X2, p2, n);
+                }
+                const float dmin = fminf(fminf(dd[0], dd[1]), fminf(dd[2], dd[3]));
+                if (__any(dmin < T)) {
+                    pruned = true;
+                    break;
+                }
+                best = fminf(best, dmin);
+                if ((t0 & 4095) == 3840) T = threshold_of(key);
+            }
+            if (!pruned) {
+                for (; t0 < p2; t0 += 64) {
+                    const int64_t t = t0 + lane;
+                    int64_t n = st + t;
+                    if (n >= p2) n -= p2;
+                    const float dd = t < p2 ? sqdist_fixed<D>(b, X2, p2, n) : INFINITY;
+                    if (__any(dd < T)) {
+                        pruned = true;
+                        break;
+                    }
+                    best = fminf(best, dd);
+                }
+            }
+            if (!pruned) {
+                const float mn = wave_min(best);
+                if (lane == 0) fold_key(key, mn, m0 + l);
+                T = fmaxf(T, mn);
+            }
+        }
+    }
+}
+
 struct Workspace {
-    float *xs1, *xs2, *bbox;
+    float *xs1, *xs2, *bbox, *xs2s;
     unsigned long long *keys;
+    int32_t *cstart2;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-Workspace carve(void *ws, int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d) {
-    char *p = static_cast<char *>(ws);
+// [keys | x2 bboxes | x1 SoA | x2 SoA | sorted x2 | x2 cell starts]; the last two for d <= 3.
+Workspace carve(void *ws, int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                size_t *total = nullptr) {
+    char *base = static_cast<char *>(ws), *p = base;
+    auto take = [&](size_t bytes) {
+        char *r = p;
+        p += align256(bytes);
+        return r;
+    };
     Workspace w;
-    w.keys = reinterpret_cast<unsigned long long *>(p);
-    p += align256(sizeof(unsigned long long) * batch * b1 * b2);
-    w.bbox = reinterpret_cast<float *>(p);
-    p += align256(sizeof(float) * batch * b2 * d * 2);
-    w.xs1 = reinterpret_cast<float *>(p);
-    p += align256(sizeof(float) * batch * b1 * p1 * d);
-    w.xs2 = reinterpret_cast<float *>(p);
+    w.keys = reinterpret_cast<unsigned long long *>(take(sizeof(unsigned long long) * batch * b1 * b2));
+    w.bbox = reinterpret_cast<float *>(take(sizeof(float) * batch * b2 * d * 2));
+    w.xs1 = reinterpret_cast<float *>(take(sizeof(float) * batch * b1 * p1 * d));
+    w.xs2 = reinterpret_cast<float *>(take(sizeof(float) * batch * b2 * p2 * d));
+    const bool sorted = d >= 1 && d <= 3;
+    w.xs2s = reinterpret_cast<float *>(take(sorted ? sizeof(float) * batch * b2 * p2 * d : 0));
+    w.cstart2 = reinterpret_cast<int32_t *>(take(sorted ? sizeof(int32_t) * batch * b2 * (kCells + 1) : 0));
+    if (total) *total = (size_t)(p - base);
     return w;
 }
 
@@ -456,10 +678,9 @@ using namespace tpw;
 
 extern "C" size_t tpw_hausdorff_workspace_size(int64_t batch, int64_t b1, int64_t p1, int64_t b2,
                                                int64_t p2, int64_t d) {
-    return align256(sizeof(unsigned long long) * batch * b1 * b2) +
-           align256(sizeof(float) * batch * b2 * d * 2) +
-           align256(sizeof(float) * batch * b1 * p1 * d) +
-           align256(sizeof(float) * batch * b2 * p2 * d);
+    size_t total = 0;
+    carve(nullptr, batch, b1, p1, b2, p2, d, &total);
+    return total;
 }
 
 extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t batch, int64_t b1,
@@ -494,6 +715,18 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
                            w.bbox, b1, b2, p1, p2, (int)d, w.keys);
         rc = check_launch("hausdorff prologue");
         if (rc) return rc;
+        if (d <= 3 && p2 < (int64_t)0x7fffffff - 64) {  // cell starts are int32
+            auto sort = d == 1 ? cell_sort_kernel<1> : d == 2 ? cell_sort_kernel<2> : cell_sort_kernel<3>;
+            hipLaunchKernelGGL(sort, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2, p2, w.bbox,
+                               w.xs2s, w.cstart2);
+            auto scan = d == 1 ? scan_window_kernel<1> : d == 2 ? scan_window_kernel<2> : scan_window_kernel<3>;
+            const int64_t m_per_block = 2048;
+            dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)pairs);
+            hipLaunchKernelGGL(scan, grid, dim3(kThreads), 0, s, w.xs1, w.xs2s, w.cstart2, w.bbox, b1, b2,
+                               p1, p2, m_per_block, w.keys);
+            rc = check_launch("hausdorff scan_window_kernel");
+            if (rc) return rc;
+        } else {
         const int64_t m_per_block = 2048;
         dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)pairs);
         const int64_t lds_points = (kLdsFloats / d) / 64 * 64;
@@ -506,6 +739,7 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
         }
         rc = check_launch("hausdorff scan_kernel");
         if (rc) return rc;
+        }
     }
     auto fin = d == 1 ? finalize_kernel<1> : d == 2 ? finalize_kernel<2> : d == 3 ? finalize_kernel<3>
              : d == 4 ? finalize_kernel<4> : finalize_kernel<0>;

@@ -15,7 +15,10 @@
 //      full scan; their largest min is a first threshold T (a lower bound of the answer);
 //   3. scan (d <= 3): x2 clouds are counting-sorted by grid cell once; every lane takes one m
 //      and checks the 64 sorted x2 points at m's cell, stopping at the first d < T; the m left
-//      are scanned by the whole wave (64 n per step, dropping m at the first d < T).
+//      are scanned by the whole wave (64 n per step, dropping m at the first d < T).  When the
+//      flags fit (pairs x p1 bytes <= 256 MiB), x1 is sorted by cell too, in a frame shared
+//      with x2, so that neighbouring lanes check overlapping windows, and the m left are
+//      flagged and scanned in iteration order by a second kernel.
 //      (d > 3: every wave takes one m at a time over x2 in iteration order, the first points
 //      from LDS.)  An m scanned to the end has its exact min; it is folded into the pair's key
 //      (float bits of min << 32 | m position) with a 64-bit atomicMax, which also raises T for
@@ -486,20 +489,23 @@ __device__ __forceinline__ void frame_of(const float *box, float (&fr)[2 * D]) {
     }
 }
 
-// Counting sort of one x2 cloud (block) by cell into xs_sorted (SoA), with the cloud's cell
-// start offsets cstart[kCells + 1].  Points of one cell land in an unspecified order (LDS
+// Counting sort of one cloud (block) by cell, in the frame of boxes[c / clouds_per_box], into
+// xs_sorted (SoA), with, when given, each sorted point's iteration position (pos) and the
+// cloud's cell start offsets (cstart, kCells + 1).  Points of one cell land in an unspecified order (LDS
 // atomics); nothing depends on it.
 template <int D>
 __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__restrict__ xs, int64_t p,
-                                                             const float *__restrict__ bbox,
+                                                             const float *__restrict__ boxes,
+                                                             int64_t clouds_per_box,
                                                              float *__restrict__ xs_sorted,
+                                                             uint32_t *__restrict__ pos,
                                                              int32_t *__restrict__ cstart) {
     __shared__ uint32_t cnt[kCells];
     __shared__ uint32_t part[kThreads];
     const int64_t c = blockIdx.x;
     const float *X = xs + c * D * p;
     float fr[2 * D];
-    frame_of<D>(bbox + c * D * 2, fr);
+    frame_of<D>(boxes + (c / clouds_per_box) * D * 2, fr);
     for (int t = threadIdx.x; t < kCells; t += kThreads) cnt[t] = 0u;
     __syncthreads();
     for (int64_t n = threadIdx.x; n < p; n += kThreads) {
@@ -530,10 +536,10 @@ __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__rest
         const int cell = threadIdx.x * kPer + e;
         const uint32_t v = cnt[cell];
         cnt[cell] = run;
-        cstart[c * (kCells + 1) + cell] = (int32_t)run;
+        if (cstart) cstart[c * (kCells + 1) + cell] = (int32_t)run;
         run += v;
     }
-    if (threadIdx.x == 0) cstart[c * (kCells + 1) + kCells] = (int32_t)p;
+    if (cstart && threadIdx.x == 0) cstart[c * (kCells + 1) + kCells] = (int32_t)p;
     __syncthreads();
     float *O = xs_sorted + c * D * p;
     for (int64_t n = threadIdx.x; n < p; n += kThreads) {
@@ -543,19 +549,69 @@ __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__rest
         const uint32_t slot = atomicAdd(&cnt[cell_of<D>(a, fr)], 1u);
 #pragma unroll
         for (int k = 0; k < D; ++k) O[k * p + slot] = a[k];
+        if (pos) pos[c * p + slot] = (uint32_t)n;
     }
 }
 
-// Block = 2048 consecutive m (iteration order) of one pair; each wave takes 64 m at a time,
-// one per lane.  A lane checks the 64 sorted x2 points starting 32 before its cell's start
-// and stops at the first d < T.  The lanes left (ballot) are taken one after another by the
-// whole wave: a circular scan of all of x2 from that start, four 64-point steps in flight,
-// dropping m at the first d < T; an m never dropped folds its exact min.
+// The whole wave scans all of x2 (sorted) for one m with coordinates b, circularly from st,
+// four 64-point steps in flight, and drops m at the first d < T; an m never dropped folds its
+// exact min with its iteration position mpos.
 template <int D>
+__device__ __forceinline__ void wave_full_scan(const float (&b)[D], const float *X2, int64_t p2, int64_t st,
+                                               unsigned long long *key, int64_t mpos) {
+    const int lane = threadIdx.x & 63;
+    float T = threshold_of(key);
+    float best = INFINITY;
+    int64_t t0 = 0;
+    for (; t0 + 256 <= p2; t0 += 256) {
+        float dd[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            int64_t n = st + t0 + 64 * u + lane;
+            if (n >= p2) n -= p2;
+            dd[u] = sqdist_fixed<D>(b, X2, p2, n);
+        }
+        const float dmin = fminf(fminf(dd[0], dd[1]), fminf(dd[2], dd[3]));
+        if (__any(dmin < T)) return;
+        best = fminf(best, dmin);
+        if ((t0 & 4095) == 3840) T = threshold_of(key);
+    }
+    for (; t0 < p2; t0 += 64) {
+        const int64_t t = t0 + lane;
+        int64_t n = st + t;
+        if (n >= p2) n -= p2;
+        const float dd = t < p2 ? sqdist_fixed<D>(b, X2, p2, n) : INFINITY;
+        if (__any(dd < T)) return;
+        best = fminf(best, dd);
+    }
+    const float mn = wave_min(best);
+    if (lane == 0) fold_key(key, mn, mpos);
+}
+
+// Start of m's 64-point window in the sorted x2 of a cloud: 32 before its cell's first point,
+// clamped to a full window.
+template <int D>
+__device__ __forceinline__ int64_t window_start(const float (&a)[D], const float (&fr)[2 * D],
+                                                const int32_t *CS, int64_t p2) {
+    const int64_t wstart = p2 > 64 ? p2 - 64 : 0;
+    int64_t s0 = (int64_t)CS[cell_of<D>(a, fr)] - 32;
+    s0 = s0 > wstart ? wstart : s0;
+    return s0 < 0 ? 0 : s0;
+}
+
+// Block = 2048 consecutive m of one pair; each wave takes 64 m at a time, one per lane.  A
+// lane checks the 64 sorted x2 points of its window and stops at the first d < T.
+//   SORTED (x1 sorted by cell in the batch frame, pos1 = iteration positions): neighbouring
+//     lanes share windows, so the loads coalesce; each lane writes flag[pair][m position] =
+//     "not dropped", and scan_flagged_kernel scans those m in iteration order.
+//   otherwise (x1 in iteration order, x2 sorted in its cloud's own frame): the lanes left
+//     (ballot) are scanned in turn by the whole wave (wave_full_scan).
+template <int D, bool SORTED>
 __global__ __launch_bounds__(kThreads) void scan_window_kernel(
-    const float *__restrict__ xs1, const float *__restrict__ xs2s, const int32_t *__restrict__ cstart2,
-    const float *__restrict__ bbox2, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
-    int64_t m_per_block, unsigned long long *__restrict__ keys) {
+    const float *__restrict__ xs1, const uint32_t *__restrict__ pos1, const float *__restrict__ xs2s,
+    const int32_t *__restrict__ cstart2, const float *__restrict__ boxes, int64_t b1, int64_t b2,
+    int64_t p1, int64_t p2, int64_t m_per_block, unsigned long long *__restrict__ keys,
+    uint8_t *__restrict__ flags) {
     const int64_t pair = blockIdx.y;
     const int64_t per_batch = b1 * b2;
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
@@ -564,12 +620,12 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
     const float *X2 = xs2s + (bb * b2 + j) * D * p2;
     const int32_t *CS = cstart2 + (bb * b2 + j) * (kCells + 1);
     float fr[2 * D];
-    frame_of<D>(bbox2 + (bb * b2 + j) * D * 2, fr);
+    frame_of<D>(boxes + (SORTED ? bb : bb * b2 + j) * D * 2, fr);
     const int lane = threadIdx.x & 63;
     const int64_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the same in every lane
     const int64_t mbeg = (int64_t)blockIdx.x * m_per_block;
     const int64_t mend = mbeg + m_per_block < p1 ? mbeg + m_per_block : p1;
-    const int64_t wstart = p2 > 64 ? p2 - 64 : 0;  // last start of a full 64-point window
+    const int64_t wlen = p2 < 64 ? p2 : 64;
     unsigned long long *key = &keys[pair];
     for (int64_t m0 = mbeg + 64 * wave; m0 < mend; m0 += 64 * (kThreads / 64)) {
         const int64_t m = m0 + lane;
@@ -577,13 +633,10 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
         float a[D];
 #pragma unroll
         for (int k = 0; k < D; ++k) a[k] = valid ? X1[k * p1 + m] : 0.0f;
-        int64_t s0 = (int64_t)CS[cell_of<D>(a, fr)] - 32;
-        s0 = s0 > wstart ? wstart : s0;
-        s0 = s0 < 0 ? 0 : s0;
-        float T = threshold_of(key);
-        // per lane: the 64 points of its window (fewer when p2 < 64), 8 per step so that their
-        // loads are in flight together
-        const int64_t wlen = p2 < 64 ? p2 : 64;
+        const int64_t s0 = window_start<D>(a, fr, CS, p2);
+        const float T = threshold_of(key);
+        // the window (fewer points when p2 < 64), 8 per step so that their loads are in flight
+        // together
         bool done = !valid;
         for (int64_t t = 0; t < wlen && !done; t += 8) {
             bool hit = false;
@@ -592,65 +645,92 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
                 if (t + u < wlen) hit = hit | (sqdist_fixed<D>(a, X2, p2, s0 + t + u) < T);
             done = hit;
         }
-        unsigned long long left = __ballot(!done);
-        while (left) {
-            const int l = __builtin_ctzll(left);
-            left &= left - 1;
-            float b[D];
+        if constexpr (SORTED) {
+            if (valid) flags[pair * p1 + pos1[(bb * b1 + i) * p1 + m]] = done ? 0 : 1;
+        } else {
+            unsigned long long left = __ballot(!done);
+            while (left) {
+                const int l = __builtin_ctzll(left);
+                left &= left - 1;
+                float b[D];
 #pragma unroll
-            for (int k = 0; k < D; ++k) b[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[k]), l));
-            const int64_t st = (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)s0, l);
-            T = threshold_of(key);
-            float best = INFINITY;
-            bool pruned = false;
-            int64_t t0 = 0;
-            for (; t0 + 256 <= p2; t0 += 256) {
-                float dd[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    int64_t n = st + t0 + 64 * u + lane;
-                    if (n >= p2) n -= p2;
-                    dd[u] = sqdist_fixed<D>(b, X2, p2, n);
-                }
-                const float dmin = fminf(fminf(dd[0], dd[1]), fminf(dd[2], dd[3]));
-                if (__any(dmin < T)) {
-                    pruned = true;
-                    break;
-                }
-                best = fminf(best, dmin);
-                if ((t0 & 4095) == 3840) T = threshold_of(key);
-            }
-            if (!pruned) {
-                for (; t0 < p2; t0 += 64) {
-                    const int64_t t = t0 + lane;
-                    int64_t n = st + t;
-                    if (n >= p2) n -= p2;
-                    const float dd = t < p2 ? sqdist_fixed<D>(b, X2, p2, n) : INFINITY;
-                    if (__any(dd < T)) {
-                        pruned = true;
-                        break;
-                    }
-                    best = fminf(best, dd);
-                }
-            }
-            if (!pruned) {
-                const float mn = wave_min(best);
-                if (lane == 0) fold_key(key, mn, m0 + l);
-                T = fmaxf(T, mn);
+                for (int k = 0; k < D; ++k)
+                    b[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[k]), l));
+                const int64_t st = (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)s0, l);
+                wave_full_scan<D>(b, X2, p2, st, key, m0 + l);
             }
         }
     }
 }
 
+// The m the window pass of the sorted mode left (flags), in iteration order: each wave takes
+// 64 consecutive m, and the flagged ones are scanned in turn by the whole wave.  The m far from
+// x2 cluster in the sorted order; here they are spread over the grid.
+template <int D>
+__global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
+    const float *__restrict__ xs1, const float *__restrict__ xs2s, const int32_t *__restrict__ cstart2,
+    const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
+    unsigned long long *__restrict__ keys, const uint8_t *__restrict__ flags) {
+    const int64_t pair = blockIdx.y;
+    const int64_t per_batch = b1 * b2;
+    const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
+    const int64_t i = rem / b2, j = rem - i * b2;
+    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
+    const float *X2 = xs2s + (bb * b2 + j) * D * p2;
+    const int32_t *CS = cstart2 + (bb * b2 + j) * (kCells + 1);
+    float fr[2 * D];
+    frame_of<D>(boxes + bb * D * 2, fr);
+    const int lane = threadIdx.x & 63;
+    const int64_t m0 = (int64_t)blockIdx.x * kThreads + 64 * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t m = m0 + lane;
+    const bool flagged = m < p1 && flags[pair * p1 + m] != 0;
+    unsigned long long left = __ballot(flagged);
+    while (left) {
+        const int l = __builtin_ctzll(left);
+        left &= left - 1;
+        float b[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + m0 + l];
+        wave_full_scan<D>(b, X2, p2, window_start<D>(b, fr, CS, p2), &keys[pair], m0 + l);
+    }
+}
+
+// bbox of each batch over both sides' cloud bounding boxes (the shared frame of the sorted mode)
+__global__ void batch_box_kernel(const float *__restrict__ bbox1, const float *__restrict__ bbox2,
+                                 int64_t batch, int64_t b1, int64_t b2, int d, float *__restrict__ boxb) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= batch * d) return;
+    const int64_t bb = t / d;
+    const int k = (int)(t - bb * d);
+    float lo = INFINITY, hi = -INFINITY;
+    for (int64_t c = 0; c < b1; ++c) {
+        lo = fminf(lo, bbox1[((bb * b1 + c) * d + k) * 2]);
+        hi = fmaxf(hi, bbox1[((bb * b1 + c) * d + k) * 2 + 1]);
+    }
+    for (int64_t c = 0; c < b2; ++c) {
+        lo = fminf(lo, bbox2[((bb * b2 + c) * d + k) * 2]);
+        hi = fmaxf(hi, bbox2[((bb * b2 + c) * d + k) * 2 + 1]);
+    }
+    boxb[t * 2] = lo;
+    boxb[t * 2 + 1] = hi;
+}
+
+// The sorted mode keeps one flag byte per (pair, m): up to 256 MiB of them.
+inline bool sorted_mode(int64_t pairs, int64_t p1) { return pairs * p1 <= ((int64_t)1 << 28); }
+
 struct Workspace {
-    float *xs1, *xs2, *bbox, *xs2s;
+    float *xs1, *xs2, *bbox, *xs2s, *bbox1, *boxb, *xs1s;
     unsigned long long *keys;
     int32_t *cstart2;
+    uint32_t *pos1;
+    uint8_t *flags;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// [keys | x2 bboxes | x1 SoA | x2 SoA | sorted x2 | x2 cell starts]; the last two for d <= 3.
+// [keys | x2 bboxes | x1 SoA | x2 SoA | sorted x2 | x2 cell starts | x1 bboxes | batch boxes |
+//  sorted x1 | x1 positions | flags]; from sorted x2 on only for d <= 3, from x1 bboxes on only
+// in the sorted mode.
 Workspace carve(void *ws, int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d,
                 size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
@@ -659,16 +739,55 @@ Workspace carve(void *ws, int64_t batch, int64_t b1, int64_t p1, int64_t b2, int
         p += align256(bytes);
         return r;
     };
+    const int64_t pairs = batch * b1 * b2;
     Workspace w;
-    w.keys = reinterpret_cast<unsigned long long *>(take(sizeof(unsigned long long) * batch * b1 * b2));
+    w.keys = reinterpret_cast<unsigned long long *>(take(sizeof(unsigned long long) * pairs));
     w.bbox = reinterpret_cast<float *>(take(sizeof(float) * batch * b2 * d * 2));
     w.xs1 = reinterpret_cast<float *>(take(sizeof(float) * batch * b1 * p1 * d));
     w.xs2 = reinterpret_cast<float *>(take(sizeof(float) * batch * b2 * p2 * d));
-    const bool sorted = d >= 1 && d <= 3;
-    w.xs2s = reinterpret_cast<float *>(take(sorted ? sizeof(float) * batch * b2 * p2 * d : 0));
-    w.cstart2 = reinterpret_cast<int32_t *>(take(sorted ? sizeof(int32_t) * batch * b2 * (kCells + 1) : 0));
+    const bool cells = d >= 1 && d <= 3;
+    const bool sorted = cells && sorted_mode(pairs, p1);
+    w.xs2s = reinterpret_cast<float *>(take(cells ? sizeof(float) * batch * b2 * p2 * d : 0));
+    w.cstart2 = reinterpret_cast<int32_t *>(take(cells ? sizeof(int32_t) * batch * b2 * (kCells + 1) : 0));
+    w.bbox1 = reinterpret_cast<float *>(take(sorted ? sizeof(float) * batch * b1 * d * 2 : 0));
+    w.boxb = reinterpret_cast<float *>(take(sorted ? sizeof(float) * batch * d * 2 : 0));
+    w.xs1s = reinterpret_cast<float *>(take(sorted ? sizeof(float) * batch * b1 * p1 * d : 0));
+    w.pos1 = reinterpret_cast<uint32_t *>(take(sorted ? sizeof(uint32_t) * batch * b1 * p1 : 0));
+    w.flags = reinterpret_cast<uint8_t *>(take(sorted ? (size_t)(pairs * p1) : 0));
     if (total) *total = (size_t)(p - base);
     return w;
+}
+
+// Steps 3-4 for d <= 3 (see the kernels): cell sort of x2 (and, in the sorted mode, of x1),
+// then the window pass and the scan of the m it leaves.
+template <int D>
+int launch_cells(const Workspace &w, int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
+                 hipStream_t s) {
+    const int64_t pairs = batch * b1 * b2;
+    const int64_t m_per_block = 2048;
+    const dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)pairs);
+    if (sorted_mode(pairs, p1)) {
+        hipLaunchKernelGGL(bbox_kernel, dim3((unsigned)(batch * b1)), dim3(kThreads), 0, s, w.xs1, p1, D,
+                           w.bbox1);
+        hipLaunchKernelGGL(batch_box_kernel, dim3((unsigned)cdiv(batch * D, 256)), dim3(256), 0, s, w.bbox1,
+                           w.bbox, batch, b1, b2, D, w.boxb);
+        hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2, p2,
+                           w.boxb, b2, w.xs2s, static_cast<uint32_t *>(nullptr), w.cstart2);
+        hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)(batch * b1)), dim3(kThreads), 0, s, w.xs1, p1,
+                           w.boxb, b1, w.xs1s, w.pos1, static_cast<int32_t *>(nullptr));
+        hipLaunchKernelGGL((scan_window_kernel<D, true>), grid, dim3(kThreads), 0, s, w.xs1s, w.pos1, w.xs2s,
+                           w.cstart2, w.boxb, b1, b2, p1, p2, m_per_block, w.keys, w.flags);
+        hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, kThreads), (unsigned)pairs),
+                           dim3(kThreads), 0, s, w.xs1, w.xs2s, w.cstart2, w.boxb, b1, b2, p1, p2, w.keys,
+                           w.flags);
+    } else {
+        hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2, p2,
+                           w.bbox, (int64_t)1, w.xs2s, static_cast<uint32_t *>(nullptr), w.cstart2);
+        hipLaunchKernelGGL((scan_window_kernel<D, false>), grid, dim3(kThreads), 0, s, w.xs1,
+                           static_cast<const uint32_t *>(nullptr), w.xs2s, w.cstart2, w.bbox, b1, b2, p1, p2,
+                           m_per_block, w.keys, static_cast<uint8_t *>(nullptr));
+    }
+    return check_launch("hausdorff cell scan");
 }
 
 }  // namespace
@@ -716,15 +835,9 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
         rc = check_launch("hausdorff prologue");
         if (rc) return rc;
         if (d <= 3 && p2 < (int64_t)0x7fffffff - 64) {  // cell starts are int32
-            auto sort = d == 1 ? cell_sort_kernel<1> : d == 2 ? cell_sort_kernel<2> : cell_sort_kernel<3>;
-            hipLaunchKernelGGL(sort, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2, p2, w.bbox,
-                               w.xs2s, w.cstart2);
-            auto scan = d == 1 ? scan_window_kernel<1> : d == 2 ? scan_window_kernel<2> : scan_window_kernel<3>;
-            const int64_t m_per_block = 2048;
-            dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)pairs);
-            hipLaunchKernelGGL(scan, grid, dim3(kThreads), 0, s, w.xs1, w.xs2s, w.cstart2, w.bbox, b1, b2,
-                               p1, p2, m_per_block, w.keys);
-            rc = check_launch("hausdorff scan_window_kernel");
+            rc = d == 1 ? launch_cells<1>(w, batch, b1, p1, b2, p2, s)
+               : d == 2 ? launch_cells<2>(w, batch, b1, p1, b2, p2, s)
+                        : launch_cells<3>(w, batch, b1, p1, b2, p2, s);
             if (rc) return rc;
         } else {
         const int64_t m_per_block = 2048;

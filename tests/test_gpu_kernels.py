@@ -287,8 +287,8 @@ def test_hausdorff_shuffled_bit_exact():
 
 @pytest.mark.parametrize("d", [1, 2, 3])
 def test_hausdorff_clustered_bit_exact(d):
-    """x2 packed into a few grid cells: the spatially ordered scan's LDS window is capped and
-    most m fall back to the global part of the scan; x1 spread wide, with a far outlier."""
+    """x2 packed into a few grid cells: the 64-point windows of the cell-sorted scan see only
+    that cluster and most m go on to the full scan; x1 spread wide, with a far outlier."""
     g = torch.Generator().manual_seed(30 + d)
     x1 = torch.rand(2, 6000, d, generator=g) * 4.0 - 2.0
     x1[1, 17] = 40.0
@@ -304,7 +304,7 @@ def test_hausdorff_clustered_bit_exact(d):
 @pytest.mark.parametrize("d", [1, 2, 3])
 def test_hausdorff_self_distance_bit_exact(d):
     """x2 = x1: every min is 0 and T stays 0, so no m can be dropped: every m goes through the
-    queued second pass and its full scan, and the tie rules pick the indices."""
+    second pass and its full scan, and the tie rules pick the indices."""
     g = torch.Generator().manual_seed(40 + d)
     x = torch.rand(2, 3000, d, generator=g)
     x[:, 100:110] = x[:, 200:210]  # duplicated points
@@ -313,6 +313,22 @@ def test_hausdorff_self_distance_bit_exact(d):
     assert_equal(out.cpu(), torch.from_numpy(w_out), f"self value d={d}")
     assert_equal(i1.cpu(), torch.from_numpy(w_i1), f"self idx1 d={d}")
     assert_equal(i2.cpu(), torch.from_numpy(w_i2), f"self idx2 d={d}")
+
+
+@pytest.mark.parametrize("shape", [
+    (None, 2, 700, 2, 900, 4),      # d = 4: parallel seeds and final rescan, plain scan
+    (1100, 1, 40, 1, 50, 2),        # 2200 clouds to sort: one block per cloud
+    (None, 64, 65537, 64, 4, 2),    # pairs x p1 > 2^28: x1 unsorted, leftovers in the wave
+    (None, 1, 9000, 1, 70000, 3),   # seeds over 3 x1 chunks, rescan over 18 x2 chunks
+])
+def test_hausdorff_plan_variants_bit_exact(shape):
+    """The launch plan changes with the sizes: each of these shapes takes another branch."""
+    x1, x2 = _hd_inputs(*shape, seed=21)
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV))
+    w_out, w_i1, w_i2 = cref.directed_hausdorff(x1.numpy(), x2.numpy(), threads=8)
+    assert_equal(out.cpu(), torch.from_numpy(w_out), f"value {shape}")
+    assert_equal(i1.cpu(), torch.from_numpy(w_i1), f"idx1 {shape}")
+    assert_equal(i2.cpu(), torch.from_numpy(w_i2), f"idx2 {shape}")
 
 
 def test_hausdorff_ties_bit_exact():

@@ -28,6 +28,8 @@
 //
 // Non-negative fp32 bit patterns order like the values, so the packed key orders by
 // (value, m position) exactly.
+#include <algorithm>
+
 #include "common.hpp"
 
 #pragma clang fp contract(off)
@@ -90,40 +92,139 @@ __global__ void soa_kernel(const float *__restrict__ x, const int64_t *__restric
     for (int k = 0; k < d; ++k) o[(int64_t)k * p] = s[k];
 }
 
-// bbox[c][k][0] = min, [1] = max over the points of cloud c (SoA input)
-__global__ void bbox_kernel(const float *__restrict__ xs, int64_t p, int d,
-                            float *__restrict__ bbox) {
-    __shared__ float red[2][kThreads];
-    const int64_t c = blockIdx.x;
-    for (int k = 0; k < d; ++k) {
-        const float *row = xs + (c * d + k) * p;
-        float lo = INFINITY, hi = -INFINITY;
-        for (int64_t n = threadIdx.x; n < p; n += kThreads) {
-            const float v = row[n];
-            lo = fminf(lo, v);
-            hi = fmaxf(hi, v);
-        }
-        red[0][threadIdx.x] = lo;
-        red[1][threadIdx.x] = hi;
-        __syncthreads();
-        for (int s = kThreads / 2; s > 0; s >>= 1) {
-            if (threadIdx.x < s) {
-                red[0][threadIdx.x] = fminf(red[0][threadIdx.x], red[0][threadIdx.x + s]);
-                red[1][threadIdx.x] = fmaxf(red[1][threadIdx.x], red[1][threadIdx.x + s]);
-            }
-            __syncthreads();
-        }
-        if (threadIdx.x == 0) {
-            bbox[(c * d + k) * 2 + 0] = red[0][0];
-            bbox[(c * d + k) * 2 + 1] = red[1][0];
-        }
-        __syncthreads();
+// A signed int that orders like the float (NaN excluded): the bit pattern, with the magnitude
+// bits flipped for negative values.  The map is its own inverse.
+__device__ __forceinline__ int ordered_int(float f) {
+    const int i = __float_as_int(f);
+    return i < 0 ? i ^ 0x7fffffff : i;
+}
+__device__ __forceinline__ float ordered_float(int i) { return __int_as_float(i < 0 ? i ^ 0x7fffffff : i); }
+constexpr uint32_t kOrderedPosInf = 0x7f800000u, kOrderedNegInf = 0x807fffffu;
+
+// Up to 8 ranges of 32-bit words to set; word i of a range gets v[i & 1].
+struct Fill {
+    uint32_t *p;
+    int64_t n;
+    uint32_t v[2];
+};
+struct Fills {
+    Fill f[8];
+    int count;
+};
+
+__global__ void fill_kernel(Fills fs) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int r = 0; r < fs.count; ++r) {
+        const Fill f = fs.f[r];
+        for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < f.n; t += stride)
+            f.p[t] = f.v[t & 1];
     }
 }
 
-__global__ void zero_keys_kernel(unsigned long long *keys, int64_t count) {
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int mask) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, mask, 64);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), mask, 64);
+    return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = shfl_xor_u64(v, off);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = shfl_xor_u64(v, off);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+
+// Bounding boxes: row r (one coordinate of one cloud, SoA) is rows [0, rowsA) of xsA (length
+// pA) then rows of xsB (length pB); block (r, y) reduces points [y chunk, (y + 1) chunk) of
+// the row and folds its min / max into keys[r][0..1] (ordered ints, preset to +inf / -inf)
+// with atomics.  NaN is ignored, as fminf / fmaxf ignore it.
+__global__ __launch_bounds__(kThreads) void bbox_rows_kernel(const float *__restrict__ xsA, int64_t rowsA,
+                                                             int64_t pA, const float *__restrict__ xsB,
+                                                             int64_t pB, int64_t chunk, int *__restrict__ keys) {
+    __shared__ float red[2][kThreads / 64];
+    const int64_t r = blockIdx.x;
+    const bool inA = r < rowsA;
+    const int64_t p = inA ? pA : pB;
+    const float *row = inA ? xsA + r * pA : xsB + (r - rowsA) * pB;
+    const int64_t beg = (int64_t)blockIdx.y * chunk;
+    if (beg >= p) return;
+    const int64_t end = beg + chunk < p ? beg + chunk : p;
+    float lo[4] = {INFINITY, INFINITY, INFINITY, INFINITY}, hi[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    int64_t n = beg + threadIdx.x;
+    for (; n + 3 * kThreads < end; n += 4 * kThreads) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float v = row[n + u * kThreads];
+            lo[u] = fminf(lo[u], v);
+            hi[u] = fmaxf(hi[u], v);
+        }
+    }
+    for (; n < end; n += kThreads) {
+        const float v = row[n];
+        lo[0] = fminf(lo[0], v);
+        hi[0] = fmaxf(hi[0], v);
+    }
+    float l = fminf(fminf(lo[0], lo[1]), fminf(lo[2], lo[3]));
+    float h = fmaxf(fmaxf(hi[0], hi[1]), fmaxf(hi[2], hi[3]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        l = fminf(l, __shfl_xor(l, off, 64));
+        h = fmaxf(h, __shfl_xor(h, off, 64));
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        red[0][wave] = l;
+        red[1][wave] = h;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kThreads / 64; ++w) {
+            l = fminf(l, red[0][w]);
+            h = fmaxf(h, red[1][w]);
+        }
+        atomicMin(&keys[r * 2], ordered_int(l));
+        atomicMax(&keys[r * 2 + 1], ordered_int(h));
+    }
+}
+
+// Boxes as floats ([cloud][k][0..1]) from the keys of bbox_rows_kernel: x1 clouds (rows1 rows,
+// when bbox1 is given) and x2 clouds (rows2 rows); then, when boxb is given, each batch's box
+// over both sides' clouds (the frame the sorted mode shares between x1 and x2).
+__global__ void box_finish_kernel(const int *__restrict__ keys, int64_t rows1, int64_t rows2,
+                                  float *__restrict__ bbox1, float *__restrict__ bbox2, int64_t batch,
+                                  int64_t b1, int64_t b2, int d, float *__restrict__ boxb) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < count) keys[t] = 0ull;
+    if (t < rows1) {
+        bbox1[t * 2] = ordered_float(keys[t * 2]);
+        bbox1[t * 2 + 1] = ordered_float(keys[t * 2 + 1]);
+    } else if (t < rows1 + rows2) {
+        const int64_t r = t - rows1;
+        bbox2[r * 2] = ordered_float(keys[t * 2]);
+        bbox2[r * 2 + 1] = ordered_float(keys[t * 2 + 1]);
+    } else if (boxb && t < rows1 + rows2 + batch * d) {
+        const int64_t q = t - rows1 - rows2;
+        const int64_t bb = q / d, k = q - bb * d;
+        int lo = (int)kOrderedPosInf, hi = (int)kOrderedNegInf;
+        for (int64_t c = 0; c < b1; ++c) {
+            lo = min(lo, keys[((bb * b1 + c) * d + k) * 2]);
+            hi = max(hi, keys[((bb * b1 + c) * d + k) * 2 + 1]);
+        }
+        for (int64_t c = 0; c < b2; ++c) {
+            lo = min(lo, keys[(rows1 + (bb * b2 + c) * d + k) * 2]);
+            hi = max(hi, keys[(rows1 + (bb * b2 + c) * d + k) * 2 + 1]);
+        }
+        boxb[q * 2] = ordered_float(lo);
+        boxb[q * 2 + 1] = ordered_float(hi);
+    }
 }
 
 struct PairPtrs {
@@ -396,6 +497,182 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(
     }
 }
 
+// Seeds and the final rescan for a fixed feature count D = 1..4, spread over many blocks per
+// cloud pair.
+//
+// seed_select: block (pair, y) takes x1 points [y chunk, (y + 1) chunk) and each wave offers
+// the point farthest from x2's bounding box as a candidate, cand[pair][4 y + wave] = (that
+// squared distance's bits << 32 | m + 1); 0 = no point.
+template <int D>
+__global__ __launch_bounds__(kThreads) void seed_select_kernel(const float *__restrict__ xs1,
+                                                               const float *__restrict__ bbox2, int64_t b1,
+                                                               int64_t b2, int64_t p1, int64_t chunk,
+                                                               int64_t ncand,
+                                                               unsigned long long *__restrict__ cand) {
+    const int64_t pair = blockIdx.x;
+    const int64_t per_batch = b1 * b2;
+    const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
+    const int64_t i = rem / b2, j = rem - i * b2;
+    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
+    float box[2 * D];
+#pragma unroll
+    for (int k = 0; k < 2 * D; ++k) box[k] = bbox2[(bb * b2 + j) * D * 2 + k];
+    const int64_t beg = (int64_t)blockIdx.y * chunk;
+    const int64_t end = beg + chunk < p1 ? beg + chunk : p1;
+    unsigned long long best = 0;
+    for (int64_t m = beg + threadIdx.x; m < end; m += kThreads) {
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const float v = X1[k * p1 + m];
+            const float e = fmaxf(fmaxf(box[2 * k] - v, v - box[2 * k + 1]), 0.0f);
+            L = L + e * e;
+        }
+        const unsigned long long key = ((unsigned long long)__float_as_uint(L) << 32) | (uint64_t)(m + 1);
+        best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) cand[pair * ncand + blockIdx.y * (kThreads / 64) + (threadIdx.x >> 6)] = best;
+}
+
+// seed_scan: block (pair, y) takes the kSeeds best candidates of the pair (found by wave 0,
+// the same in every block) and the x2 points [y chunk, (y + 1) chunk), and folds each seed's
+// min over them into seedmin[pair][s] (fp32 bits, preset to +inf) with atomicMin; block y = 0
+// records the seeds' positions in seedm[pair][s] (0xffffffff = no seed).
+template <int D>
+__global__ __launch_bounds__(kThreads) void seed_scan_kernel(
+    const float *__restrict__ xs1, const float *__restrict__ xs2, const unsigned long long *__restrict__ cand,
+    int64_t ncand, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t chunk,
+    uint32_t *__restrict__ seedmin, uint32_t *__restrict__ seedm) {
+    __shared__ uint32_t sm[kSeeds];
+    __shared__ float red[kThreads / 64][kSeeds];
+    const int64_t pair = blockIdx.x;
+    const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, D);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (wave == 0) {
+        // kSeeds rounds, each the largest key below the previous one (keys are distinct);
+        // every lane holds the same reduced value, and the round count is fixed
+        const unsigned long long *C = cand + pair * ncand;
+        unsigned long long prev = ~0ull;
+        for (int r = 0; r < kSeeds; ++r) {
+            unsigned long long best = 0;
+            for (int64_t e = lane; e < ncand; e += 64) {
+                const unsigned long long v = C[e];
+                if (v < prev && v > best) best = v;
+            }
+            best = wave_max_u64(best);
+            if (lane == 0) sm[r] = best ? (uint32_t)(best & 0xffffffffull) - 1u : 0xffffffffu;
+            prev = best ? best : prev;
+        }
+    }
+    __syncthreads();
+    float a[kSeeds][D];
+#pragma unroll
+    for (int s = 0; s < kSeeds; ++s) {
+        const uint32_t m = sm[s] == 0xffffffffu ? sm[0] : sm[s];
+#pragma unroll
+        for (int k = 0; k < D; ++k) a[s][k] = P.x1[k * p1 + m];
+    }
+    float best[kSeeds];
+#pragma unroll
+    for (int s = 0; s < kSeeds; ++s) best[s] = INFINITY;
+    const int64_t beg = (int64_t)blockIdx.y * chunk;
+    const int64_t end = beg + chunk < p2 ? beg + chunk : p2;
+    for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
+        float b[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) b[k] = P.x2[k * p2 + n];
+#pragma unroll
+        for (int s = 0; s < kSeeds; ++s) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < D; ++k) {
+                const float diff = a[s][k] - b[k];
+                acc = acc + diff * diff;
+            }
+            best[s] = fminf(best[s], acc);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < kSeeds; ++s) {
+        const float v = wave_min(best[s]);
+        if (lane == 0) red[wave][s] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < kSeeds) {
+        const int s = threadIdx.x;
+        float v = red[0][s];
+        for (int w = 1; w < kThreads / 64; ++w) v = fminf(v, red[w][s]);
+        if (sm[s] != 0xffffffffu) atomicMin(&seedmin[pair * kSeeds + s], __float_as_uint(v));
+        if (blockIdx.y == 0) seedm[pair * kSeeds + s] = sm[s];
+    }
+}
+
+// Each seed's exact min (the fold of all seed_scan blocks) goes into its pair's key.
+__global__ void seed_fold_kernel(const uint32_t *__restrict__ seedmin, const uint32_t *__restrict__ seedm,
+                                 int64_t pairs, unsigned long long *__restrict__ keys) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= pairs * kSeeds || seedm[t] == 0xffffffffu) return;
+    fold_key(&keys[t / kSeeds], __uint_as_float(seedmin[t]), seedm[t]);
+}
+
+// Final rescan: block (pair, y) checks the x2 points [y chunk, (y + 1) chunk) against the
+// winning m of the pair's key and folds the first position n whose d equals the min into
+// first[pair] (preset to all ones) with atomicMin.
+template <int D>
+__global__ __launch_bounds__(kThreads) void first_hit_kernel(
+    const float *__restrict__ xs1, const float *__restrict__ xs2, const unsigned long long *__restrict__ keys,
+    int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t chunk, unsigned long long *__restrict__ first) {
+    __shared__ unsigned long long red[kThreads / 64];
+    const int64_t pair = blockIdx.x;
+    const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, D);
+    const unsigned long long key = keys[pair];
+    const int64_t m = (int64_t)(key & 0xffffffffull);
+    const float H = __uint_as_float((uint32_t)(key >> 32));
+    float a[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) a[k] = P.x1[k * p1 + m];
+    const int64_t beg = (int64_t)blockIdx.y * chunk;
+    const int64_t end = beg + chunk < p2 ? beg + chunk : p2;
+    unsigned long long hit = ~0ull;
+    int64_t n = beg + threadIdx.x;
+    for (; n + 3 * kThreads < end; n += 4 * kThreads) {
+        float dd[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dd[u] = sqdist_fixed<D>(a, P.x2, p2, n + u * kThreads);
+#pragma unroll
+        for (int u = 3; u >= 0; --u)
+            if (dd[u] == H) hit = (unsigned long long)(n + u * kThreads);
+        if (hit != ~0ull) break;
+    }
+    for (; n < end && hit == ~0ull; n += kThreads)
+        if (sqdist_fixed<D>(a, P.x2, p2, n) == H) hit = (unsigned long long)n;
+    hit = wave_min_u64(hit);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = hit;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kThreads / 64; ++w) hit = red[w] < hit ? red[w] : hit;
+        if (hit != ~0ull) atomicMin(&first[pair], hit);
+    }
+}
+
+// One thread per pair: sqrt of the winning min, and the (permuted) positions of m and n.
+__global__ void write_out_kernel(const unsigned long long *__restrict__ keys,
+                                 const unsigned long long *__restrict__ first, const int64_t *__restrict__ perm1,
+                                 const int64_t *__restrict__ perm2, int64_t pairs, int64_t b1, int64_t b2,
+                                 int64_t p1, int64_t p2, float *__restrict__ out, int64_t *__restrict__ idx1,
+                                 int64_t *__restrict__ idx2) {
+    const int64_t pair = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (pair >= pairs) return;
+    const int64_t bb = pair / (b1 * b2);
+    const unsigned long long key = keys[pair];
+    const int64_t m = (int64_t)(key & 0xffffffffull);
+    const unsigned long long n = first[pair];
+    out[pair] = sqrt_rn(__uint_as_float((uint32_t)(key >> 32)));
+    idx1[pair] = perm1 ? perm1[bb * p1 + m] : m;
+    idx2[pair] = n < (unsigned long long)p2 ? (perm2 ? perm2[bb * p2 + (int64_t)n] : (int64_t)n) : 0;
+}
+
 // grad_x1[bb,i,m*,k] += g * (x1[m*,k] - x2[n*,k]) / out, over j in order (one thread per
 // (bb, i, k) owns every update of its slice, so the summation order is the reference's).
 __global__ void backward_x1_kernel(const float *__restrict__ g, const float *__restrict__ x1,
@@ -553,6 +830,123 @@ __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__rest
     }
 }
 
+// The same counting sort spread over many blocks per cloud, for runs with few clouds (one
+// block per cloud would leave most CUs idle).  Clouds [0, A.clouds) come from A, the rest from
+// B; cursor[cloud][cell] (preset to 0) first counts, then holds each cell's next free slot.
+//   cell_count: block (cloud, y) histograms points [y chunk, (y + 1) chunk) in LDS and adds
+//     the non-zero bins to cursor;
+//   cell_scan: one block per cloud turns the counts into start offsets (and cstart);
+//   cell_scatter: block (cloud, y) histograms its points again, reserves a range of each
+//     cell's slots with one atomicAdd per non-zero bin, and writes its points into it.
+struct CellSet {
+    const float *xs;      // [clouds][D][p]
+    float *sorted;        // [clouds][D][p]
+    uint32_t *pos;        // [clouds][p] iteration positions of the sorted points, or null
+    int32_t *cstart;      // [clouds][kCells + 1] cell starts, or null
+    const float *boxes;   // frames, [clouds / clouds_per_box][D][2]
+    int64_t clouds, p, clouds_per_box;
+};
+
+template <int D>
+__device__ __forceinline__ void chunk_histogram(const CellSet &S, int64_t c, int64_t beg, int64_t end,
+                                                const float (&fr)[2 * D], uint32_t *hist) {
+    for (int t = threadIdx.x; t < kCells; t += kThreads) hist[t] = 0u;
+    __syncthreads();
+    const float *X = S.xs + c * D * S.p;
+    for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
+        float a[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) a[k] = X[k * S.p + n];
+        atomicAdd(&hist[cell_of<D>(a, fr)], 1u);
+    }
+    __syncthreads();
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void cell_count_kernel(CellSet A, CellSet B, int64_t chunk,
+                                                              uint32_t *__restrict__ cursor) {
+    __shared__ uint32_t hist[kCells];
+    const int64_t g = blockIdx.x;
+    const bool inA = g < A.clouds;
+    const CellSet &S = inA ? A : B;
+    const int64_t c = inA ? g : g - A.clouds;
+    const int64_t beg = (int64_t)blockIdx.y * chunk;
+    if (beg >= S.p) return;  // the same for the whole block
+    const int64_t end = beg + chunk < S.p ? beg + chunk : S.p;
+    float fr[2 * D];
+    frame_of<D>(S.boxes + (c / S.clouds_per_box) * D * 2, fr);
+    chunk_histogram<D>(S, c, beg, end, fr, hist);
+    for (int t = threadIdx.x; t < kCells; t += kThreads)
+        if (hist[t]) atomicAdd(&cursor[g * kCells + t], hist[t]);
+}
+
+__global__ __launch_bounds__(kThreads) void cell_scan_kernel(CellSet A, CellSet B, uint32_t *__restrict__ cursor) {
+    __shared__ uint32_t part[kThreads];
+    const int64_t g = blockIdx.x;
+    const bool inA = g < A.clouds;
+    const CellSet &S = inA ? A : B;
+    const int64_t c = inA ? g : g - A.clouds;
+    uint32_t *cnt = cursor + g * kCells;
+    constexpr int kPer = kCells / kThreads;  // 16 consecutive cells per thread
+    uint32_t v[kPer];
+    uint32_t local = 0;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+        v[e] = cnt[threadIdx.x * kPer + e];
+        local += v[e];
+    }
+    part[threadIdx.x] = local;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0;
+        for (int t = 0; t < kThreads; ++t) {
+            const uint32_t x = part[t];
+            part[t] = run;
+            run += x;
+        }
+    }
+    __syncthreads();
+    uint32_t run = part[threadIdx.x];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+        const int cell = threadIdx.x * kPer + e;
+        cnt[cell] = run;
+        if (S.cstart) S.cstart[c * (kCells + 1) + cell] = (int32_t)run;
+        run += v[e];
+    }
+    if (S.cstart && threadIdx.x == 0) S.cstart[c * (kCells + 1) + kCells] = (int32_t)S.p;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellSet B, int64_t chunk,
+                                                                uint32_t *__restrict__ cursor) {
+    __shared__ uint32_t hist[kCells];
+    const int64_t g = blockIdx.x;
+    const bool inA = g < A.clouds;
+    const CellSet &S = inA ? A : B;
+    const int64_t c = inA ? g : g - A.clouds;
+    const int64_t beg = (int64_t)blockIdx.y * chunk;
+    if (beg >= S.p) return;  // the same for the whole block
+    const int64_t end = beg + chunk < S.p ? beg + chunk : S.p;
+    float fr[2 * D];
+    frame_of<D>(S.boxes + (c / S.clouds_per_box) * D * 2, fr);
+    chunk_histogram<D>(S, c, beg, end, fr, hist);
+    for (int t = threadIdx.x; t < kCells; t += kThreads)
+        if (hist[t]) hist[t] = atomicAdd(&cursor[g * kCells + t], hist[t]);
+    __syncthreads();
+    const float *X = S.xs + c * D * S.p;
+    float *O = S.sorted + c * D * S.p;
+    for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
+        float a[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) a[k] = X[k * S.p + n];
+        const uint32_t slot = atomicAdd(&hist[cell_of<D>(a, fr)], 1u);
+#pragma unroll
+        for (int k = 0; k < D; ++k) O[k * S.p + slot] = a[k];
+        if (S.pos) S.pos[c * S.p + slot] = (uint32_t)n;
+    }
+}
+
 // The whole wave scans all of x2 (sorted) for one m with coordinates b, circularly from st,
 // four 64-point steps in flight, and drops m at the first d < T; an m never dropped folds its
 // exact min with its iteration position mpos.
@@ -695,99 +1089,168 @@ __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
     }
 }
 
-// bbox of each batch over both sides' cloud bounding boxes (the shared frame of the sorted mode)
-__global__ void batch_box_kernel(const float *__restrict__ bbox1, const float *__restrict__ bbox2,
-                                 int64_t batch, int64_t b1, int64_t b2, int d, float *__restrict__ boxb) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= batch * d) return;
-    const int64_t bb = t / d;
-    const int k = (int)(t - bb * d);
-    float lo = INFINITY, hi = -INFINITY;
-    for (int64_t c = 0; c < b1; ++c) {
-        lo = fminf(lo, bbox1[((bb * b1 + c) * d + k) * 2]);
-        hi = fmaxf(hi, bbox1[((bb * b1 + c) * d + k) * 2 + 1]);
-    }
-    for (int64_t c = 0; c < b2; ++c) {
-        lo = fminf(lo, bbox2[((bb * b2 + c) * d + k) * 2]);
-        hi = fmaxf(hi, bbox2[((bb * b2 + c) * d + k) * 2 + 1]);
-    }
-    boxb[t * 2] = lo;
-    boxb[t * 2 + 1] = hi;
-}
-
 // The sorted mode keeps one flag byte per (pair, m): up to 256 MiB of them.
 inline bool sorted_mode(int64_t pairs, int64_t p1) { return pairs * p1 <= ((int64_t)1 << 28); }
 
+int64_t round_up(int64_t v, int64_t q) { return cdiv(v, q) * q; }
+
+// How a run is split; a function of the sizes only (the workspace size depends on it).
+struct Plan {
+    int64_t batch = 0, pairs = 0, clouds1 = 0, clouds2 = 0;
+    bool active = false;      // points and features on both sides
+    bool fast = false;        // d = 1..4: seeds and final rescan spread over blocks
+    bool cells = false;       // d <= 3 and int32 cell starts: the cell-sorted scan
+    bool sorted = false;      // cells and the flags fit: x1 sorted too, in a shared frame
+    bool multi_sort = false;  // few clouds to sort: the counting sort spread over blocks
+    int64_t box_rows1 = 0, box_rows2 = 0, box_chunk = 1, box_chunks = 0;
+    int64_t chunk1 = 1, ncand = 0;   // x1 points per seed_select block; candidates per pair
+    int64_t chunk2 = 1, nch2 = 0;    // x2 points per seed_scan / first_hit block
+    int64_t sort_clouds = 0, sort_chunk = 1, sort_chunks = 0;
+};
+
+Plan make_plan(int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d) {
+    Plan P;
+    P.batch = batch;
+    P.pairs = batch * b1 * b2;
+    P.clouds1 = batch * b1;
+    P.clouds2 = batch * b2;
+    P.active = P.pairs > 0 && p1 > 0 && p2 > 0 && d > 0;
+    if (!P.active) return P;
+    P.fast = d <= 4;
+    P.cells = d <= 3 && p2 < (int64_t)0x7fffffff - 64;
+    P.sorted = P.cells && sorted_mode(P.pairs, p1);
+    P.box_rows1 = P.sorted ? P.clouds1 * d : 0;
+    P.box_rows2 = P.clouds2 * d;
+    const int64_t pbox = P.sorted && p1 > p2 ? p1 : p2;
+    P.box_chunk = std::max<int64_t>(8192, round_up(cdiv(pbox, kMaxGridYZ), kThreads));
+    P.box_chunks = cdiv(pbox, P.box_chunk);
+    // at most 64 seed_select blocks (256 candidates) per pair, at least 4096 points each
+    P.chunk1 = std::max<int64_t>(4096, round_up(cdiv(p1, 64), kThreads));
+    P.ncand = cdiv(p1, P.chunk1) * (kThreads / 64);
+    P.chunk2 = std::max<int64_t>(4096, round_up(cdiv(p2, kMaxGridYZ), kThreads));
+    P.nch2 = cdiv(p2, P.chunk2);
+    if (P.cells) {
+        P.sort_clouds = P.clouds2 + (P.sorted ? P.clouds1 : 0);
+        P.multi_sort = P.sort_clouds <= 2048;  // cursor <= 32 MiB
+        const int64_t psort = P.sorted && p1 > p2 ? p1 : p2;
+        P.sort_chunk = std::max<int64_t>(4096, round_up(cdiv(psort, kMaxGridYZ), kThreads));
+        P.sort_chunks = cdiv(psort, P.sort_chunk);
+    }
+    return P;
+}
+
 struct Workspace {
     float *xs1, *xs2, *bbox, *xs2s, *bbox1, *boxb, *xs1s;
-    unsigned long long *keys;
+    unsigned long long *keys, *cand, *first;
     int32_t *cstart2;
-    uint32_t *pos1;
+    int *boxkeys;
+    uint32_t *pos1, *seedmin, *seedm, *cursor;
     uint8_t *flags;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// [keys | x2 bboxes | x1 SoA | x2 SoA | sorted x2 | x2 cell starts | x1 bboxes | batch boxes |
-//  sorted x1 | x1 positions | flags]; from sorted x2 on only for d <= 3, from x1 bboxes on only
-// in the sorted mode.
-Workspace carve(void *ws, int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d,
-                size_t *total = nullptr) {
+// [keys | x2 boxes | x1 SoA | x2 SoA | box keys | seeds, candidates, first hits (fast) |
+//  sorted x2, x2 cell starts (cells) | x1 boxes, batch boxes, sorted x1, x1 positions, flags
+//  (sorted) | sort cursors (multi_sort)]
+Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
-    auto take = [&](size_t bytes) {
+    auto take = [&](bool on, size_t bytes) {
         char *r = p;
-        p += align256(bytes);
-        return r;
+        if (on) p += align256(bytes);
+        return on ? r : nullptr;
     };
-    const int64_t pairs = batch * b1 * b2;
     Workspace w;
-    w.keys = reinterpret_cast<unsigned long long *>(take(sizeof(unsigned long long) * pairs));
-    w.bbox = reinterpret_cast<float *>(take(sizeof(float) * batch * b2 * d * 2));
-    w.xs1 = reinterpret_cast<float *>(take(sizeof(float) * batch * b1 * p1 * d));
-    w.xs2 = reinterpret_cast<float *>(take(sizeof(float) * batch * b2 * p2 * d));
-    const bool cells = d >= 1 && d <= 3;
-    const bool sorted = cells && sorted_mode(pairs, p1);
-    w.xs2s = reinterpret_cast<float *>(take(cells ? sizeof(float) * batch * b2 * p2 * d : 0));
-    w.cstart2 = reinterpret_cast<int32_t *>(take(cells ? sizeof(int32_t) * batch * b2 * (kCells + 1) : 0));
-    w.bbox1 = reinterpret_cast<float *>(take(sorted ? sizeof(float) * batch * b1 * d * 2 : 0));
-    w.boxb = reinterpret_cast<float *>(take(sorted ? sizeof(float) * batch * d * 2 : 0));
-    w.xs1s = reinterpret_cast<float *>(take(sorted ? sizeof(float) * batch * b1 * p1 * d : 0));
-    w.pos1 = reinterpret_cast<uint32_t *>(take(sorted ? sizeof(uint32_t) * batch * b1 * p1 : 0));
-    w.flags = reinterpret_cast<uint8_t *>(take(sorted ? (size_t)(pairs * p1) : 0));
+    w.keys = reinterpret_cast<unsigned long long *>(take(true, 8 * P.pairs));
+    w.bbox = reinterpret_cast<float *>(take(true, 4 * P.clouds2 * d * 2));
+    w.xs1 = reinterpret_cast<float *>(take(true, 4 * P.clouds1 * p1 * d));
+    w.xs2 = reinterpret_cast<float *>(take(true, 4 * P.clouds2 * p2 * d));
+    w.boxkeys = reinterpret_cast<int *>(take(P.active, 4 * (P.box_rows1 + P.box_rows2) * 2));
+    w.seedmin = reinterpret_cast<uint32_t *>(take(P.fast, 4 * P.pairs * kSeeds));
+    w.seedm = reinterpret_cast<uint32_t *>(take(P.fast, 4 * P.pairs * kSeeds));
+    w.cand = reinterpret_cast<unsigned long long *>(take(P.fast, 8 * P.pairs * P.ncand));
+    w.first = reinterpret_cast<unsigned long long *>(take(P.fast, 8 * P.pairs));
+    w.xs2s = reinterpret_cast<float *>(take(P.cells, 4 * P.clouds2 * p2 * d));
+    w.cstart2 = reinterpret_cast<int32_t *>(take(P.cells, 4 * P.clouds2 * (kCells + 1)));
+    w.bbox1 = reinterpret_cast<float *>(take(P.sorted, 4 * P.clouds1 * d * 2));
+    w.boxb = reinterpret_cast<float *>(take(P.sorted, 4 * P.batch * d * 2));
+    w.xs1s = reinterpret_cast<float *>(take(P.sorted, 4 * P.clouds1 * p1 * d));
+    w.pos1 = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.clouds1 * p1));
+    w.flags = reinterpret_cast<uint8_t *>(take(P.sorted, (size_t)(P.pairs * p1)));
+    w.cursor = reinterpret_cast<uint32_t *>(take(P.multi_sort, 4 * P.sort_clouds * kCells));
     if (total) *total = (size_t)(p - base);
     return w;
 }
 
-// Steps 3-4 for d <= 3 (see the kernels): cell sort of x2 (and, in the sorted mode, of x1),
-// then the window pass and the scan of the m it leaves.
+// Step 3 for d <= 3: cell sort of x2 (and, in the sorted mode, of x1), then the window pass
+// and the scan of the m it leaves.
 template <int D>
-int launch_cells(const Workspace &w, int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
+int launch_cells(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
                  hipStream_t s) {
-    const int64_t pairs = batch * b1 * b2;
+    const CellSet S2{w.xs2, w.xs2s, nullptr, w.cstart2, P.sorted ? w.boxb : w.bbox, P.clouds2, p2,
+                     P.sorted ? b2 : 1};
+    const CellSet S1{w.xs1, w.xs1s, w.pos1, nullptr, w.boxb, P.sorted ? P.clouds1 : 0, p1, b1};
+    if (P.multi_sort) {
+        const dim3 grid((unsigned)P.sort_clouds, (unsigned)P.sort_chunks);
+        hipLaunchKernelGGL(cell_count_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, w.cursor);
+        hipLaunchKernelGGL(cell_scan_kernel, dim3((unsigned)P.sort_clouds), dim3(kThreads), 0, s, S2, S1,
+                           w.cursor);
+        hipLaunchKernelGGL(cell_scatter_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, w.cursor);
+    } else {
+        hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)P.clouds2), dim3(kThreads), 0, s, w.xs2, p2,
+                           S2.boxes, S2.clouds_per_box, w.xs2s, static_cast<uint32_t *>(nullptr), w.cstart2);
+        if (P.sorted)
+            hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)P.clouds1), dim3(kThreads), 0, s, w.xs1, p1,
+                               w.boxb, b1, w.xs1s, w.pos1, static_cast<int32_t *>(nullptr));
+    }
     const int64_t m_per_block = 2048;
-    const dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)pairs);
-    if (sorted_mode(pairs, p1)) {
-        hipLaunchKernelGGL(bbox_kernel, dim3((unsigned)(batch * b1)), dim3(kThreads), 0, s, w.xs1, p1, D,
-                           w.bbox1);
-        hipLaunchKernelGGL(batch_box_kernel, dim3((unsigned)cdiv(batch * D, 256)), dim3(256), 0, s, w.bbox1,
-                           w.bbox, batch, b1, b2, D, w.boxb);
-        hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2, p2,
-                           w.boxb, b2, w.xs2s, static_cast<uint32_t *>(nullptr), w.cstart2);
-        hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)(batch * b1)), dim3(kThreads), 0, s, w.xs1, p1,
-                           w.boxb, b1, w.xs1s, w.pos1, static_cast<int32_t *>(nullptr));
+    const dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs);
+    if (P.sorted) {
         hipLaunchKernelGGL((scan_window_kernel<D, true>), grid, dim3(kThreads), 0, s, w.xs1s, w.pos1, w.xs2s,
                            w.cstart2, w.boxb, b1, b2, p1, p2, m_per_block, w.keys, w.flags);
-        hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, kThreads), (unsigned)pairs),
+        hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, kThreads), (unsigned)P.pairs),
                            dim3(kThreads), 0, s, w.xs1, w.xs2s, w.cstart2, w.boxb, b1, b2, p1, p2, w.keys,
                            w.flags);
     } else {
-        hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2, p2,
-                           w.bbox, (int64_t)1, w.xs2s, static_cast<uint32_t *>(nullptr), w.cstart2);
         hipLaunchKernelGGL((scan_window_kernel<D, false>), grid, dim3(kThreads), 0, s, w.xs1,
                            static_cast<const uint32_t *>(nullptr), w.xs2s, w.cstart2, w.bbox, b1, b2, p1, p2,
                            m_per_block, w.keys, static_cast<uint8_t *>(nullptr));
     }
     return check_launch("hausdorff cell scan");
+}
+
+// d = 1..4 after the relayout and the boxes: seeds, scan, final rescan and outputs.
+template <int D>
+int launch_fast(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
+                const int64_t *perm1, const int64_t *perm2, float *out, int64_t *idx1, int64_t *idx2,
+                hipStream_t s) {
+    hipLaunchKernelGGL(seed_select_kernel<D>, dim3((unsigned)P.pairs, (unsigned)cdiv(p1, P.chunk1)),
+                       dim3(kThreads), 0, s, w.xs1, w.bbox, b1, b2, p1, P.chunk1, P.ncand, w.cand);
+    hipLaunchKernelGGL(seed_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
+                       w.xs1, w.xs2, w.cand, P.ncand, b1, b2, p1, p2, P.chunk2, w.seedmin, w.seedm);
+    hipLaunchKernelGGL(seed_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s,
+                       w.seedmin, w.seedm, P.pairs, w.keys);
+    int rc = check_launch("hausdorff seeds");
+    if (rc) return rc;
+    if constexpr (D <= 3) {
+        if (P.cells) {
+            rc = launch_cells<D>(P, w, b1, p1, b2, p2, s);
+            if (rc) return rc;
+        }
+    }
+    if (!P.cells) {
+        const int64_t m_per_block = 2048;
+        const int64_t lds_points = (kLdsFloats / D) / 64 * 64;
+        hipLaunchKernelGGL(scan_kernel<D>, dim3((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs),
+                           dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys);
+        rc = check_launch("hausdorff scan_kernel");
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(first_hit_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
+                       w.xs1, w.xs2, w.keys, b1, b2, p1, p2, P.chunk2, w.first);
+    hipLaunchKernelGGL(write_out_kernel, dim3((unsigned)cdiv(P.pairs, 256)), dim3(256), 0, s, w.keys, w.first,
+                       perm1, perm2, P.pairs, b1, b2, p1, p2, out, idx1, idx2);
+    return check_launch("hausdorff final rescan");
 }
 
 }  // namespace
@@ -797,8 +1260,9 @@ using namespace tpw;
 
 extern "C" size_t tpw_hausdorff_workspace_size(int64_t batch, int64_t b1, int64_t p1, int64_t b2,
                                                int64_t p2, int64_t d) {
+    if (batch < 0 || b1 < 0 || b2 < 0 || p1 < 0 || p2 < 0 || d < 0) return 0;
     size_t total = 0;
-    carve(nullptr, batch, b1, p1, b2, p2, d, &total);
+    carve(nullptr, make_plan(batch, b1, p1, b2, p2, d), p1, p2, d, &total);
     return total;
 }
 
@@ -816,49 +1280,53 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     TPW_REQUIRE(x1 && x2 && out && idx1 && idx2 && workspace, "null pointer");
     TPW_REQUIRE(pairs <= kMaxGridYZ, "too many cloud pairs (%lld)", (long long)pairs);
     hipStream_t s = as_stream(stream);
-    Workspace w = carve(workspace, batch, b1, p1, b2, p2, d);
-    hipLaunchKernelGGL(zero_keys_kernel, dim3((unsigned)cdiv(pairs, 256)), dim3(256), 0, s, w.keys,
-                       pairs);
-    int rc = check_launch("zero_keys_kernel");
+    const Plan P = make_plan(batch, b1, p1, b2, p2, d);
+    const Workspace w = carve(workspace, P, p1, p2, d);
+    // presets: keys 0, box keys (+inf, -inf), seed mins +inf, first hits and cursors
+    Fills fs{};
+    int64_t most = 0;
+    auto add = [&](void *ptr, int64_t words, uint32_t v0, uint32_t v1) {
+        if (!ptr || words <= 0) return;
+        fs.f[fs.count++] = Fill{static_cast<uint32_t *>(ptr), words, {v0, v1}};
+        most = std::max(most, words);
+    };
+    add(w.keys, 2 * pairs, 0u, 0u);
+    add(w.boxkeys, 2 * (P.box_rows1 + P.box_rows2), kOrderedPosInf, kOrderedNegInf);
+    add(w.seedmin, pairs * kSeeds, 0x7f800000u, 0x7f800000u);
+    add(w.first, 2 * pairs, 0xffffffffu, 0xffffffffu);
+    add(w.cursor, P.sort_clouds * kCells, 0u, 0u);
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)std::min<int64_t>(cdiv(most, 256), 2048)), dim3(256), 0, s, fs);
+    int rc = check_launch("hausdorff presets");
     if (rc) return rc;
-    if (p1 > 0 && p2 > 0 && d > 0) {
+    if (P.active) {
         hipLaunchKernelGGL(soa_kernel, dim3((unsigned)cdiv(batch * b1 * p1, 256)), dim3(256), 0, s,
                            x1, perm1, batch * b1, b1, p1, (int)d, w.xs1);
         hipLaunchKernelGGL(soa_kernel, dim3((unsigned)cdiv(batch * b2 * p2, 256)), dim3(256), 0, s,
                            x2, perm2, batch * b2, b2, p2, (int)d, w.xs2);
-        hipLaunchKernelGGL(bbox_kernel, dim3((unsigned)(batch * b2)), dim3(kThreads), 0, s, w.xs2,
-                           p2, (int)d, w.bbox);
-        auto seed = d == 1 ? seed_kernel<1> : d == 2 ? seed_kernel<2> : d == 3 ? seed_kernel<3>
-                  : d == 4 ? seed_kernel<4> : seed_kernel<0>;
-        hipLaunchKernelGGL(seed, dim3((unsigned)pairs), dim3(kThreads), 0, s, w.xs1, w.xs2,
-                           w.bbox, b1, b2, p1, p2, (int)d, w.keys);
+        hipLaunchKernelGGL(bbox_rows_kernel, dim3((unsigned)(P.box_rows1 + P.box_rows2), (unsigned)P.box_chunks),
+                           dim3(kThreads), 0, s, w.xs1, P.box_rows1, p1, w.xs2, p2, P.box_chunk, w.boxkeys);
+        const int64_t fin = P.box_rows1 + P.box_rows2 + (P.sorted ? batch * d : 0);
+        hipLaunchKernelGGL(box_finish_kernel, dim3((unsigned)cdiv(fin, 256)), dim3(256), 0, s, w.boxkeys,
+                           P.box_rows1, P.box_rows2, w.bbox1, w.bbox, batch, b1, b2, (int)d, w.boxb);
         rc = check_launch("hausdorff prologue");
         if (rc) return rc;
-        if (d <= 3 && p2 < (int64_t)0x7fffffff - 64) {  // cell starts are int32
-            rc = d == 1 ? launch_cells<1>(w, batch, b1, p1, b2, p2, s)
-               : d == 2 ? launch_cells<2>(w, batch, b1, p1, b2, p2, s)
-                        : launch_cells<3>(w, batch, b1, p1, b2, p2, s);
-            if (rc) return rc;
-        } else {
-        const int64_t m_per_block = 2048;
-        dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)pairs);
-        const int64_t lds_points = (kLdsFloats / d) / 64 * 64;
-        switch (d) {
-            case 1: hipLaunchKernelGGL(scan_kernel<1>, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys); break;
-            case 2: hipLaunchKernelGGL(scan_kernel<2>, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys); break;
-            case 3: hipLaunchKernelGGL(scan_kernel<3>, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys); break;
-            case 4: hipLaunchKernelGGL(scan_kernel<4>, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys); break;
-            default: hipLaunchKernelGGL(scan_kernel_any, grid, dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, (int)d, m_per_block, w.keys); break;
+        if (P.fast) {
+            switch (d) {
+                case 1: return launch_fast<1>(P, w, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+                case 2: return launch_fast<2>(P, w, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+                case 3: return launch_fast<3>(P, w, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+                default: return launch_fast<4>(P, w, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+            }
         }
-        rc = check_launch("hausdorff scan_kernel");
+        hipLaunchKernelGGL(seed_kernel<0>, dim3((unsigned)pairs), dim3(kThreads), 0, s, w.xs1, w.xs2, w.bbox, b1,
+                           b2, p1, p2, (int)d, w.keys);
+        hipLaunchKernelGGL(scan_kernel_any, dim3((unsigned)cdiv(p1, 2048), (unsigned)pairs), dim3(kThreads), 0, s,
+                           w.xs1, w.xs2, b1, b2, p1, p2, (int)d, (int64_t)2048, w.keys);
+        rc = check_launch("hausdorff scan_kernel_any");
         if (rc) return rc;
-        }
     }
-    auto fin = d == 1 ? finalize_kernel<1> : d == 2 ? finalize_kernel<2> : d == 3 ? finalize_kernel<3>
-             : d == 4 ? finalize_kernel<4> : finalize_kernel<0>;
-    hipLaunchKernelGGL(fin, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads),
-                       0, s, w.xs1, w.xs2, w.keys, perm1, perm2, pairs, b1, b2, p1, p2, (int)d, out,
-                       idx1, idx2);
+    hipLaunchKernelGGL(finalize_kernel<0>, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads), 0, s,
+                       w.xs1, w.xs2, w.keys, perm1, perm2, pairs, b1, b2, p1, p2, (int)d, out, idx1, idx2);
     return check_launch("hausdorff finalize_kernel");
 }
 

@@ -320,6 +320,7 @@ def test_hausdorff_self_distance_bit_exact(d):
     (1100, 1, 40, 1, 50, 2),        # 2200 clouds to sort: one block per cloud
     (None, 64, 65537, 64, 4, 2),    # pairs x p1 > 2^28: x1 unsorted, leftovers in the wave
     (None, 1, 9000, 1, 70000, 3),   # seeds over 3 x1 chunks, rescan over 18 x2 chunks
+    (None, 3, 20000, 3, 20000, 3),  # the bench's layout: m with min >= T go to the survivor list
 ])
 def test_hausdorff_plan_variants_bit_exact(shape):
     """The launch plan changes with the sizes: each of these shapes takes another branch."""

@@ -79,6 +79,14 @@ __device__ __forceinline__ void fold_key(unsigned long long *key, float mn, int6
     atomicMax(key, k);
 }
 
+// Whether x1 position m is one of the pair's seeds (whose exact mins are in the key already).
+__device__ __forceinline__ bool is_seed(const uint32_t *seedm, int64_t pair, int64_t m) {
+    bool r = false;
+#pragma unroll
+    for (int s = 0; s < kSeeds; ++s) r = r | (seedm[pair * kSeeds + s] == (uint32_t)m);
+    return r;
+}
+
 // xs[c][k][pos] = x[c][perm ? perm[batch_of(c)][pos] : pos][k]
 __global__ void soa_kernel(const float *__restrict__ x, const int64_t *__restrict__ perm,
                            int64_t clouds, int64_t clouds_per_batch, int64_t p, int d,
@@ -342,6 +350,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const float *__restrict_
                                                         int64_t b1, int64_t b2, int64_t p1,
                                                         int64_t p2, int64_t m_per_block,
                                                         int64_t lds_points,
+                                                        const uint32_t *__restrict__ seedm,
                                                         unsigned long long *__restrict__ keys) {
     __shared__ float lds[kLdsFloats];
     const int64_t pair = blockIdx.y;
@@ -358,6 +367,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const float *__restrict_
     const int64_t mend = mbeg + m_per_block < p1 ? mbeg + m_per_block : p1;
     unsigned long long *key = &keys[pair];
     for (int64_t m = mbeg + wave; m < mend; m += kThreads / 64) {
+        if (is_seed(seedm, pair, m)) continue;  // the same in every lane
         float a[D];
 #pragma unroll
         for (int k = 0; k < D; ++k) a[k] = P.x1[k * p1 + m];
@@ -535,85 +545,101 @@ __global__ __launch_bounds__(kThreads) void seed_select_kernel(const float *__re
     if ((threadIdx.x & 63) == 0) cand[pair * ncand + blockIdx.y * (kThreads / 64) + (threadIdx.x >> 6)] = best;
 }
 
-// seed_scan: block (pair, y) takes the kSeeds best candidates of the pair (found by wave 0,
-// the same in every block) and the x2 points [y chunk, (y + 1) chunk), and folds each seed's
-// min over them into seedmin[pair][s] (fp32 bits, preset to +inf) with atomicMin; block y = 0
-// records the seeds' positions in seedm[pair][s] (0xffffffff = no seed).
-template <int D>
-__global__ __launch_bounds__(kThreads) void seed_scan_kernel(
-    const float *__restrict__ xs1, const float *__restrict__ xs2, const unsigned long long *__restrict__ cand,
-    int64_t ncand, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t chunk,
-    uint32_t *__restrict__ seedmin, uint32_t *__restrict__ seedm) {
-    __shared__ uint32_t sm[kSeeds];
-    __shared__ float red[kThreads / 64][kSeeds];
-    const int64_t pair = blockIdx.x;
-    const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, D);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (wave == 0) {
-        // kSeeds rounds, each the largest key below the previous one (keys are distinct);
-        // every lane holds the same reduced value, and the round count is fixed
-        const unsigned long long *C = cand + pair * ncand;
-        unsigned long long prev = ~0ull;
-        for (int r = 0; r < kSeeds; ++r) {
-            unsigned long long best = 0;
-            for (int64_t e = lane; e < ncand; e += 64) {
-                const unsigned long long v = C[e];
-                if (v < prev && v > best) best = v;
-            }
-            best = wave_max_u64(best);
-            if (lane == 0) sm[r] = best ? (uint32_t)(best & 0xffffffffull) - 1u : 0xffffffffu;
-            prev = best ? best : prev;
+// seed_pick: one wave per pair takes the kSeeds largest candidate keys (keys are distinct; kSeeds
+// rounds, each the largest key below the previous one, every lane holding the same reduced
+// value) and writes their positions to seedm[pair][s] (0xffffffff = no candidate left).
+__global__ __launch_bounds__(kThreads) void seed_pick_kernel(const unsigned long long *__restrict__ cand,
+                                                             int64_t ncand, int64_t pairs,
+                                                             uint32_t *__restrict__ seedm) {
+    const int64_t pair = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (pair >= pairs) return;
+    const int lane = threadIdx.x & 63;
+    const unsigned long long *C = cand + pair * ncand;
+    unsigned long long prev = ~0ull;
+    for (int r = 0; r < kSeeds; ++r) {
+        unsigned long long best = 0;
+        for (int64_t e = lane; e < ncand; e += 64) {
+            const unsigned long long v = C[e];
+            if (v < prev && v > best) best = v;
         }
-    }
-    __syncthreads();
-    float a[kSeeds][D];
-#pragma unroll
-    for (int s = 0; s < kSeeds; ++s) {
-        const uint32_t m = sm[s] == 0xffffffffu ? sm[0] : sm[s];
-#pragma unroll
-        for (int k = 0; k < D; ++k) a[s][k] = P.x1[k * p1 + m];
-    }
-    float best[kSeeds];
-#pragma unroll
-    for (int s = 0; s < kSeeds; ++s) best[s] = INFINITY;
-    const int64_t beg = (int64_t)blockIdx.y * chunk;
-    const int64_t end = beg + chunk < p2 ? beg + chunk : p2;
-    for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
-        float b[D];
-#pragma unroll
-        for (int k = 0; k < D; ++k) b[k] = P.x2[k * p2 + n];
-#pragma unroll
-        for (int s = 0; s < kSeeds; ++s) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < D; ++k) {
-                const float diff = a[s][k] - b[k];
-                acc = acc + diff * diff;
-            }
-            best[s] = fminf(best[s], acc);
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < kSeeds; ++s) {
-        const float v = wave_min(best[s]);
-        if (lane == 0) red[wave][s] = v;
-    }
-    __syncthreads();
-    if (threadIdx.x < kSeeds) {
-        const int s = threadIdx.x;
-        float v = red[0][s];
-        for (int w = 1; w < kThreads / 64; ++w) v = fminf(v, red[w][s]);
-        if (sm[s] != 0xffffffffu) atomicMin(&seedmin[pair * kSeeds + s], __float_as_uint(v));
-        if (blockIdx.y == 0) seedm[pair * kSeeds + s] = sm[s];
+        best = wave_max_u64(best);
+        if (lane == 0) seedm[pair * kSeeds + r] = best ? (uint32_t)(best & 0xffffffffull) - 1u : 0xffffffffu;
+        prev = best ? best : prev;
     }
 }
 
-// Each seed's exact min (the fold of all seed_scan blocks) goes into its pair's key.
-__global__ void seed_fold_kernel(const uint32_t *__restrict__ seedmin, const uint32_t *__restrict__ seedm,
-                                 int64_t pairs, unsigned long long *__restrict__ keys) {
+// Exact mins of listed x1 points, spread over blocks.  list[pair][0..K) holds x1 positions:
+// with cnt, the first min(cnt[pair], K) entries; without, every entry but 0xffffffff (entry 0
+// is then always valid).  Block (pair, y) takes the x2 points [y chunk, (y + 1) chunk) and, eight
+// entries at a time, folds each entry's min over them into lmin[pair][e] (fp32 bits, preset to
+// +inf) with atomicMin.
+template <int D>
+__global__ __launch_bounds__(kThreads) void list_scan_kernel(
+    const float *__restrict__ xs1, const float *__restrict__ xs2, const uint32_t *__restrict__ list,
+    const uint32_t *__restrict__ cnt, int64_t K, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t chunk,
+    uint32_t *__restrict__ lmin) {
+    constexpr int kGroup = 8;
+    __shared__ float red[kThreads / 64][kGroup];
+    const int64_t pair = blockIdx.x;
+    const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, D);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t *L = list + pair * K;
+    const int64_t n = cnt ? std::min<int64_t>(cnt[pair], K) : K;
+    const int64_t beg = (int64_t)blockIdx.y * chunk;
+    const int64_t end = beg + chunk < p2 ? beg + chunk : p2;
+    for (int64_t g0 = 0; g0 < n; g0 += kGroup) {
+        uint32_t ms[kGroup];
+        float a[kGroup][D];
+#pragma unroll
+        for (int s = 0; s < kGroup; ++s) {
+            ms[s] = g0 + s < n ? L[g0 + s] : 0xffffffffu;
+            const uint32_t m = ms[s] == 0xffffffffu ? L[g0] : ms[s];  // L[g0] is valid
+#pragma unroll
+            for (int k = 0; k < D; ++k) a[s][k] = P.x1[k * p1 + m];
+        }
+        float best[kGroup];
+#pragma unroll
+        for (int s = 0; s < kGroup; ++s) best[s] = INFINITY;
+        for (int64_t q = beg + threadIdx.x; q < end; q += kThreads) {
+            float b[D];
+#pragma unroll
+            for (int k = 0; k < D; ++k) b[k] = P.x2[k * p2 + q];
+#pragma unroll
+            for (int s = 0; s < kGroup; ++s) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < D; ++k) {
+                    const float diff = a[s][k] - b[k];
+                    acc = acc + diff * diff;
+                }
+                best[s] = fminf(best[s], acc);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kGroup; ++s) {
+            const float v = wave_min(best[s]);
+            if (lane == 0) red[wave][s] = v;
+        }
+        __syncthreads();
+        if (threadIdx.x < kGroup) {
+            const int s = threadIdx.x;
+            float v = red[0][s];
+            for (int w = 1; w < kThreads / 64; ++w) v = fminf(v, red[w][s]);
+            if (ms[s] != 0xffffffffu) atomicMin(&lmin[pair * K + g0 + s], __float_as_uint(v));
+        }
+        __syncthreads();
+    }
+}
+
+// Each listed point's exact min (the fold of all list_scan blocks) goes into its pair's key.
+__global__ void list_fold_kernel(const uint32_t *__restrict__ lmin, const uint32_t *__restrict__ list,
+                                 const uint32_t *__restrict__ cnt, int64_t K, int64_t pairs,
+                                 unsigned long long *__restrict__ keys) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= pairs * kSeeds || seedm[t] == 0xffffffffu) return;
-    fold_key(&keys[t / kSeeds], __uint_as_float(seedmin[t]), seedm[t]);
+    if (t >= pairs * K) return;
+    const int64_t pair = t / K, e = t - pair * K;
+    const bool valid = cnt ? e < (int64_t)cnt[pair] : list[t] != 0xffffffffu;
+    if (valid) fold_key(&keys[pair], __uint_as_float(lmin[t]), list[t]);
 }
 
 // Final rescan: block (pair, y) checks the x2 points [y chunk, (y + 1) chunk) against the
@@ -982,30 +1008,53 @@ __device__ __forceinline__ void wave_full_scan(const float (&b)[D], const float 
     if (lane == 0) fold_key(key, mn, mpos);
 }
 
-// Start of m's 64-point window in the sorted x2 of a cloud: 32 before its cell's first point,
-// clamped to a full window.
+// Whether the whole wave, scanning `budget` points (a multiple of 256, below p2) of the sorted
+// x2 circularly from st, meets a d < T for the point b (the same answer in every lane).
+template <int D>
+__device__ __forceinline__ bool wave_scan_prunes(const float (&b)[D], const float *X2, int64_t p2, int64_t st,
+                                                 const unsigned long long *key, int64_t budget) {
+    const int lane = threadIdx.x & 63;
+    float T = threshold_of(key);
+    for (int64_t t0 = 0; t0 < budget; t0 += 256) {
+        float dd[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            int64_t n = st + t0 + 64 * u + lane;
+            if (n >= p2) n -= p2;
+            dd[u] = sqdist_fixed<D>(b, X2, p2, n);
+        }
+        const float dmin = fminf(fminf(dd[0], dd[1]), fminf(dd[2], dd[3]));
+        if (__any(dmin < T)) return true;
+        if ((t0 & 1023) == 768) T = threshold_of(key);
+    }
+    return false;
+}
+
+// Start of m's 64-point window in the sorted x2 of a cloud: its cell's first point, clamped to
+// a full window.
 template <int D>
 __device__ __forceinline__ int64_t window_start(const float (&a)[D], const float (&fr)[2 * D],
                                                 const int32_t *CS, int64_t p2) {
     const int64_t wstart = p2 > 64 ? p2 - 64 : 0;
-    int64_t s0 = (int64_t)CS[cell_of<D>(a, fr)] - 32;
-    s0 = s0 > wstart ? wstart : s0;
-    return s0 < 0 ? 0 : s0;
+    const int64_t s0 = (int64_t)CS[cell_of<D>(a, fr)];
+    return s0 > wstart ? wstart : s0;
 }
 
 // Block = 2048 consecutive m of one pair; each wave takes 64 m at a time, one per lane.  A
-// lane checks the 64 sorted x2 points of its window and stops at the first d < T.
+// lane checks the 64 sorted x2 points of its window, first the head of its own cell (which
+// almost always holds a point within T), and stops at the first d < T.  The pair's seeds have
+// their exact mins in the key already and are skipped.
 //   SORTED (x1 sorted by cell in the batch frame, pos1 = iteration positions): neighbouring
-//     lanes share windows, so the loads coalesce; each lane writes flag[pair][m position] =
-//     "not dropped", and scan_flagged_kernel scans those m in iteration order.
+//     lanes share windows, so the loads coalesce; a lane left sets flag[pair][m position]
+//     (preset to 0), and scan_flagged_kernel scans those m in iteration order.
 //   otherwise (x1 in iteration order, x2 sorted in its cloud's own frame): the lanes left
 //     (ballot) are scanned in turn by the whole wave (wave_full_scan).
 template <int D, bool SORTED>
 __global__ __launch_bounds__(kThreads) void scan_window_kernel(
     const float *__restrict__ xs1, const uint32_t *__restrict__ pos1, const float *__restrict__ xs2s,
     const int32_t *__restrict__ cstart2, const float *__restrict__ boxes, int64_t b1, int64_t b2,
-    int64_t p1, int64_t p2, int64_t m_per_block, unsigned long long *__restrict__ keys,
-    uint8_t *__restrict__ flags) {
+    int64_t p1, int64_t p2, int64_t m_per_block, const uint32_t *__restrict__ seedm,
+    unsigned long long *__restrict__ keys, uint8_t *__restrict__ flags) {
     const int64_t pair = blockIdx.y;
     const int64_t per_batch = b1 * b2;
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
@@ -1027,12 +1076,20 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
         float a[D];
 #pragma unroll
         for (int k = 0; k < D; ++k) a[k] = valid ? X1[k * p1 + m] : 0.0f;
+        const int64_t mpos = SORTED ? (valid ? (int64_t)pos1[(bb * b1 + i) * p1 + m] : 0) : m;
         const int64_t s0 = window_start<D>(a, fr, CS, p2);
         const float T = threshold_of(key);
-        // the window (fewer points when p2 < 64), 8 per step so that their loads are in flight
-        // together
-        bool done = !valid;
-        for (int64_t t = 0; t < wlen && !done; t += 8) {
+        bool done = !valid || is_seed(seedm, pair, mpos);
+        // two points first, then 8 per step so that their loads are in flight together (fewer
+        // in all when p2 < 64)
+        {
+            bool hit = false;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                if (u < wlen) hit = hit | (sqdist_fixed<D>(a, X2, p2, s0 + u) < T);
+            done = done || hit;
+        }
+        for (int64_t t = 2; t < wlen && !done; t += 8) {
             bool hit = false;
 #pragma unroll
             for (int u = 0; u < 8; ++u)
@@ -1040,7 +1097,7 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
             done = hit;
         }
         if constexpr (SORTED) {
-            if (valid) flags[pair * p1 + pos1[(bb * b1 + i) * p1 + m]] = done ? 0 : 1;
+            if (!done) flags[pair * p1 + mpos] = 1;
         } else {
             unsigned long long left = __ballot(!done);
             while (left) {
@@ -1058,13 +1115,20 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
 }
 
 // The m the window pass of the sorted mode left (flags), in iteration order: each wave takes
-// 64 consecutive m, and the flagged ones are scanned in turn by the whole wave.  The m far from
-// x2 cluster in the sorted order; here they are spread over the grid.
+// 64 consecutive m, and the flagged ones are scanned in turn by the whole wave, `budget` points
+// from the window's start (or all of x2, when that is no more, folding the exact min).  An m
+// still not dropped after its budget is a survivor: its exact min needs all of x2, which one
+// wave would take a long serial time over, so it goes to survm[pair] (slots reserved with one
+// atomicAdd per block on survcnt[pair], handed to the waves through LDS after a barrier) for
+// list_scan_kernel, which spreads it over many blocks.  Survivors beyond K slots are scanned
+// here in full.
 template <int D>
 __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
     const float *__restrict__ xs1, const float *__restrict__ xs2s, const int32_t *__restrict__ cstart2,
-    const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
-    unsigned long long *__restrict__ keys, const uint8_t *__restrict__ flags) {
+    const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t budget,
+    unsigned long long *__restrict__ keys, const uint8_t *__restrict__ flags, uint32_t *__restrict__ survm,
+    uint32_t *__restrict__ survcnt, int64_t K) {
+    __shared__ uint32_t wn[kThreads / 64], wb[kThreads / 64];
     const int64_t pair = blockIdx.y;
     const int64_t per_batch = b1 * b2;
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
@@ -1075,17 +1139,46 @@ __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
     float fr[2 * D];
     frame_of<D>(boxes + bb * D * 2, fr);
     const int lane = threadIdx.x & 63;
-    const int64_t m0 = (int64_t)blockIdx.x * kThreads + 64 * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = threadIdx.x >> 6;
+    const int64_t m0 = (int64_t)blockIdx.x * kThreads + 64 * __builtin_amdgcn_readfirstlane(wave);
     const int64_t m = m0 + lane;
+    unsigned long long *key = &keys[pair];
     const bool flagged = m < p1 && flags[pair * p1 + m] != 0;
     unsigned long long left = __ballot(flagged);
+    unsigned long long surv = 0;  // built from wave-wide values only
     while (left) {
         const int l = __builtin_ctzll(left);
         left &= left - 1;
         float b[D];
 #pragma unroll
         for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + m0 + l];
-        wave_full_scan<D>(b, X2, p2, window_start<D>(b, fr, CS, p2), &keys[pair], m0 + l);
+        const int64_t st = window_start<D>(b, fr, CS, p2);
+        if (p2 <= budget) wave_full_scan<D>(b, X2, p2, st, key, m0 + l);
+        else if (!wave_scan_prunes<D>(b, X2, p2, st, key, budget)) surv |= 1ull << l;
+    }
+    if (lane == 0) wn[wave] = (uint32_t)__builtin_popcountll(surv);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t tot = 0;
+        for (int w = 0; w < kThreads / 64; ++w) tot += wn[w];
+        uint32_t base = tot ? atomicAdd(&survcnt[pair], tot) : 0u;
+        for (int w = 0; w < kThreads / 64; ++w) {
+            wb[w] = base;
+            base += wn[w];
+        }
+    }
+    __syncthreads();
+    const bool mine = (surv >> lane) & 1ull;
+    const int64_t slot = (int64_t)wb[wave] + __builtin_popcountll(surv & ((1ull << lane) - 1ull));
+    if (mine && slot < K) survm[pair * K + slot] = (uint32_t)m;
+    unsigned long long over = __ballot(mine && slot >= K);
+    while (over) {
+        const int l = __builtin_ctzll(over);
+        over &= over - 1;
+        float b[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + m0 + l];
+        wave_full_scan<D>(b, X2, p2, window_start<D>(b, fr, CS, p2), key, m0 + l);
     }
 }
 
@@ -1139,20 +1232,25 @@ Plan make_plan(int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, in
     return P;
 }
 
+// Survivor slots per pair (full scans spread over blocks) in the sorted mode.
+constexpr int64_t kSurvivors = 64;
+// Points the flagged pass scans for an m before it counts as a survivor.
+constexpr int64_t kBudget = 2048;
+
 struct Workspace {
     float *xs1, *xs2, *bbox, *xs2s, *bbox1, *boxb, *xs1s;
     unsigned long long *keys, *cand, *first;
     int32_t *cstart2;
     int *boxkeys;
-    uint32_t *pos1, *seedmin, *seedm, *cursor;
+    uint32_t *pos1, *seedmin, *seedm, *cursor, *survm, *survmin, *survcnt;
     uint8_t *flags;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // [keys | x2 boxes | x1 SoA | x2 SoA | box keys | seeds, candidates, first hits (fast) |
-//  sorted x2, x2 cell starts (cells) | x1 boxes, batch boxes, sorted x1, x1 positions, flags
-//  (sorted) | sort cursors (multi_sort)]
+//  sorted x2, x2 cell starts (cells) | x1 boxes, batch boxes, sorted x1, x1 positions, flags,
+//  survivors (sorted) | sort cursors (multi_sort)]
 Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
     auto take = [&](bool on, size_t bytes) {
@@ -1177,6 +1275,9 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
     w.xs1s = reinterpret_cast<float *>(take(P.sorted, 4 * P.clouds1 * p1 * d));
     w.pos1 = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.clouds1 * p1));
     w.flags = reinterpret_cast<uint8_t *>(take(P.sorted, (size_t)(P.pairs * p1)));
+    w.survm = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * kSurvivors));
+    w.survmin = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * kSurvivors));
+    w.survcnt = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs));
     w.cursor = reinterpret_cast<uint32_t *>(take(P.multi_sort, 4 * P.sort_clouds * kCells));
     if (total) *total = (size_t)(p - base);
     return w;
@@ -1207,14 +1308,18 @@ int launch_cells(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int6
     const dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs);
     if (P.sorted) {
         hipLaunchKernelGGL((scan_window_kernel<D, true>), grid, dim3(kThreads), 0, s, w.xs1s, w.pos1, w.xs2s,
-                           w.cstart2, w.boxb, b1, b2, p1, p2, m_per_block, w.keys, w.flags);
+                           w.cstart2, w.boxb, b1, b2, p1, p2, m_per_block, w.seedm, w.keys, w.flags);
         hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, kThreads), (unsigned)P.pairs),
-                           dim3(kThreads), 0, s, w.xs1, w.xs2s, w.cstart2, w.boxb, b1, b2, p1, p2, w.keys,
-                           w.flags);
+                           dim3(kThreads), 0, s, w.xs1, w.xs2s, w.cstart2, w.boxb, b1, b2, p1, p2, kBudget, w.keys,
+                           w.flags, w.survm, w.survcnt, kSurvivors);
+        hipLaunchKernelGGL(list_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
+                           w.xs1, w.xs2, w.survm, w.survcnt, kSurvivors, b1, b2, p1, p2, P.chunk2, w.survmin);
+        hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSurvivors, 256)), dim3(256), 0, s,
+                           w.survmin, w.survm, w.survcnt, kSurvivors, P.pairs, w.keys);
     } else {
         hipLaunchKernelGGL((scan_window_kernel<D, false>), grid, dim3(kThreads), 0, s, w.xs1,
                            static_cast<const uint32_t *>(nullptr), w.xs2s, w.cstart2, w.bbox, b1, b2, p1, p2,
-                           m_per_block, w.keys, static_cast<uint8_t *>(nullptr));
+                           m_per_block, w.seedm, w.keys, static_cast<uint8_t *>(nullptr));
     }
     return check_launch("hausdorff cell scan");
 }
@@ -1226,10 +1331,13 @@ int launch_fast(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64
                 hipStream_t s) {
     hipLaunchKernelGGL(seed_select_kernel<D>, dim3((unsigned)P.pairs, (unsigned)cdiv(p1, P.chunk1)),
                        dim3(kThreads), 0, s, w.xs1, w.bbox, b1, b2, p1, P.chunk1, P.ncand, w.cand);
-    hipLaunchKernelGGL(seed_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
-                       w.xs1, w.xs2, w.cand, P.ncand, b1, b2, p1, p2, P.chunk2, w.seedmin, w.seedm);
-    hipLaunchKernelGGL(seed_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s,
-                       w.seedmin, w.seedm, P.pairs, w.keys);
+    hipLaunchKernelGGL(seed_pick_kernel, dim3((unsigned)cdiv(P.pairs, kThreads / 64)), dim3(kThreads), 0, s,
+                       w.cand, P.ncand, P.pairs, w.seedm);
+    hipLaunchKernelGGL(list_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
+                       w.xs1, w.xs2, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1,
+                       p2, P.chunk2, w.seedmin);
+    hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s,
+                       w.seedmin, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, P.pairs, w.keys);
     int rc = check_launch("hausdorff seeds");
     if (rc) return rc;
     if constexpr (D <= 3) {
@@ -1242,7 +1350,8 @@ int launch_fast(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64
         const int64_t m_per_block = 2048;
         const int64_t lds_points = (kLdsFloats / D) / 64 * 64;
         hipLaunchKernelGGL(scan_kernel<D>, dim3((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs),
-                           dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.keys);
+                           dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.seedm,
+                           w.keys);
         rc = check_launch("hausdorff scan_kernel");
         if (rc) return rc;
     }
@@ -1282,7 +1391,8 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     hipStream_t s = as_stream(stream);
     const Plan P = make_plan(batch, b1, p1, b2, p2, d);
     const Workspace w = carve(workspace, P, p1, p2, d);
-    // presets: keys 0, box keys (+inf, -inf), seed mins +inf, first hits and cursors
+    // presets: keys 0, box keys (+inf, -inf), seed and survivor mins +inf, first hits all ones,
+    // cursors, flags and survivor counts 0
     Fills fs{};
     int64_t most = 0;
     auto add = [&](void *ptr, int64_t words, uint32_t v0, uint32_t v1) {
@@ -1295,6 +1405,9 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     add(w.seedmin, pairs * kSeeds, 0x7f800000u, 0x7f800000u);
     add(w.first, 2 * pairs, 0xffffffffu, 0xffffffffu);
     add(w.cursor, P.sort_clouds * kCells, 0u, 0u);
+    add(w.flags, cdiv(P.pairs * p1, 4), 0u, 0u);  // the allocation is rounded up to 256 bytes
+    add(w.survmin, P.pairs * kSurvivors, 0x7f800000u, 0x7f800000u);
+    add(w.survcnt, P.pairs, 0u, 0u);
     hipLaunchKernelGGL(fill_kernel, dim3((unsigned)std::min<int64_t>(cdiv(most, 256), 2048)), dim3(256), 0, s, fs);
     int rc = check_launch("hausdorff presets");
     if (rc) return rc;

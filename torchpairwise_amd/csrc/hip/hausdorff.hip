@@ -79,6 +79,27 @@ __device__ __forceinline__ void fold_key(unsigned long long *key, float mn, int6
     atomicMax(key, k);
 }
 
+// A cell-sorted point is one 16-byte record: its D <= 3 coordinates, then (dword 3) its
+// iteration position, so that one vector load brings the whole point and a sorted point still
+// names its place in the reference's loop order.
+__device__ __forceinline__ float rec_coord(const float4 &v, int k) { return k == 0 ? v.x : k == 1 ? v.y : v.z; }
+__device__ __forceinline__ uint32_t rec_pos(const float4 &v) { return __float_as_uint(v.w); }
+template <int D>
+__device__ __forceinline__ float4 make_rec(const float (&a)[D], uint32_t pos) {
+    return make_float4(a[0], D > 1 ? a[D > 1 ? 1 : 0] : 0.0f, D > 2 ? a[D > 2 ? 2 : 0] : 0.0f, __uint_as_float(pos));
+}
+// d(a, record) summed over k in order, as sqdist_fixed
+template <int D>
+__device__ __forceinline__ float rec_dist(const float (&a)[D], const float4 &v) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        const float diff = a[k] - rec_coord(v, k);
+        s = s + diff * diff;
+    }
+    return s;
+}
+
 // Whether x1 position m is one of the pair's seeds (whose exact mins are in the key already).
 __device__ __forceinline__ bool is_seed(const uint32_t *seedm, int64_t pair, int64_t m) {
     bool r = false;
@@ -572,8 +593,8 @@ __global__ __launch_bounds__(kThreads) void seed_pick_kernel(const unsigned long
 // with cnt, the first min(cnt[pair], K) entries; without, every entry but 0xffffffff (entry 0
 // is then always valid).  Block (pair, y) takes the x2 points [y chunk, (y + 1) chunk) and, eight
 // entries at a time, folds each entry's min over them into lmin[pair][e] (fp32 bits, preset to
-// +inf) with atomicMin.
-template <int D>
+// +inf) with atomicMin.  REC: x2 as cell-sorted records (xs2 then points at them).
+template <int D, bool REC>
 __global__ __launch_bounds__(kThreads) void list_scan_kernel(
     const float *__restrict__ xs1, const float *__restrict__ xs2, const uint32_t *__restrict__ list,
     const uint32_t *__restrict__ cnt, int64_t K, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t chunk,
@@ -582,6 +603,7 @@ __global__ __launch_bounds__(kThreads) void list_scan_kernel(
     __shared__ float red[kThreads / 64][kGroup];
     const int64_t pair = blockIdx.x;
     const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, D);
+    const float4 *R = REC ? reinterpret_cast<const float4 *>(xs2) + (P.x2 - xs2) / D : nullptr;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t *L = list + pair * K;
     const int64_t n = cnt ? std::min<int64_t>(cnt[pair], K) : K;
@@ -602,8 +624,14 @@ __global__ __launch_bounds__(kThreads) void list_scan_kernel(
         for (int s = 0; s < kGroup; ++s) best[s] = INFINITY;
         for (int64_t q = beg + threadIdx.x; q < end; q += kThreads) {
             float b[D];
+            if constexpr (REC) {
+                const float4 v = R[q];
 #pragma unroll
-            for (int k = 0; k < D; ++k) b[k] = P.x2[k * p2 + q];
+                for (int k = 0; k < D; ++k) b[k] = rec_coord(v, k);
+            } else {
+#pragma unroll
+                for (int k = 0; k < D; ++k) b[k] = P.x2[k * p2 + q];
+            }
 #pragma unroll
             for (int s = 0; s < kGroup; ++s) {
                 float acc = 0.0f;
@@ -644,8 +672,9 @@ __global__ void list_fold_kernel(const uint32_t *__restrict__ lmin, const uint32
 
 // Final rescan: block (pair, y) checks the x2 points [y chunk, (y + 1) chunk) against the
 // winning m of the pair's key and folds the first position n whose d equals the min into
-// first[pair] (preset to all ones) with atomicMin.
-template <int D>
+// first[pair] (preset to all ones) with atomicMin.  REC: x2 as cell-sorted records (xs2 then
+// points at them), whose positions are in the records.
+template <int D, bool REC>
 __global__ __launch_bounds__(kThreads) void first_hit_kernel(
     const float *__restrict__ xs1, const float *__restrict__ xs2, const unsigned long long *__restrict__ keys,
     int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t chunk, unsigned long long *__restrict__ first) {
@@ -661,6 +690,15 @@ __global__ __launch_bounds__(kThreads) void first_hit_kernel(
     const int64_t beg = (int64_t)blockIdx.y * chunk;
     const int64_t end = beg + chunk < p2 ? beg + chunk : p2;
     unsigned long long hit = ~0ull;
+    if constexpr (REC) {
+        // sorted order: every point is checked, the smallest position wins
+        const float4 *R = reinterpret_cast<const float4 *>(xs2) + (P.x2 - xs2) / D;
+        for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
+            const float4 v = R[n];
+            const unsigned long long q = rec_pos(v);
+            if (rec_dist<D>(a, v) == H && q < hit) hit = q;
+        }
+    } else {
     int64_t n = beg + threadIdx.x;
     for (; n + 3 * kThreads < end; n += 4 * kThreads) {
         float dd[4];
@@ -673,6 +711,7 @@ __global__ __launch_bounds__(kThreads) void first_hit_kernel(
     }
     for (; n < end && hit == ~0ull; n += kThreads)
         if (sqdist_fixed<D>(a, P.x2, p2, n) == H) hit = (unsigned long long)n;
+    }
     hit = wave_min_u64(hit);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = hit;
     __syncthreads();
@@ -747,6 +786,7 @@ __global__ void backward_x2_kernel(const float *__restrict__ g, const float *__r
 // with mins near T) are spread evenly over the waves.
 constexpr int kCells = 4096;
 
+
 template <int D>
 __device__ __forceinline__ uint32_t spread_bits(uint32_t v) {
     if constexpr (D == 3) {  // 4 bits -> every third bit
@@ -793,15 +833,14 @@ __device__ __forceinline__ void frame_of(const float *box, float (&fr)[2 * D]) {
 }
 
 // Counting sort of one cloud (block) by cell, in the frame of boxes[c / clouds_per_box], into
-// xs_sorted (SoA), with, when given, each sorted point's iteration position (pos) and the
-// cloud's cell start offsets (cstart, kCells + 1).  Points of one cell land in an unspecified order (LDS
+// records (rec, [cloud][p]), with, when given, the cloud's cell start offsets (cstart,
+// kCells + 1).  Points of one cell land in an unspecified order (LDS
 // atomics); nothing depends on it.
 template <int D>
 __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__restrict__ xs, int64_t p,
                                                              const float *__restrict__ boxes,
                                                              int64_t clouds_per_box,
-                                                             float *__restrict__ xs_sorted,
-                                                             uint32_t *__restrict__ pos,
+                                                             float4 *__restrict__ rec,
                                                              int32_t *__restrict__ cstart) {
     __shared__ uint32_t cnt[kCells];
     __shared__ uint32_t part[kThreads];
@@ -844,15 +883,13 @@ __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__rest
     }
     if (cstart && threadIdx.x == 0) cstart[c * (kCells + 1) + kCells] = (int32_t)p;
     __syncthreads();
-    float *O = xs_sorted + c * D * p;
+    float4 *O = rec + c * p;
     for (int64_t n = threadIdx.x; n < p; n += kThreads) {
         float a[D];
 #pragma unroll
         for (int k = 0; k < D; ++k) a[k] = X[k * p + n];
         const uint32_t slot = atomicAdd(&cnt[cell_of<D>(a, fr)], 1u);
-#pragma unroll
-        for (int k = 0; k < D; ++k) O[k * p + slot] = a[k];
-        if (pos) pos[c * p + slot] = (uint32_t)n;
+        O[slot] = make_rec<D>(a, (uint32_t)n);
     }
 }
 
@@ -866,8 +903,7 @@ __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__rest
 //     cell's slots with one atomicAdd per non-zero bin, and writes its points into it.
 struct CellSet {
     const float *xs;      // [clouds][D][p]
-    float *sorted;        // [clouds][D][p]
-    uint32_t *pos;        // [clouds][p] iteration positions of the sorted points, or null
+    float4 *rec;          // [clouds][p] records
     int32_t *cstart;      // [clouds][kCells + 1] cell starts, or null
     const float *boxes;   // frames, [clouds / clouds_per_box][D][2]
     int64_t clouds, p, clouds_per_box;
@@ -961,15 +997,13 @@ __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellS
         if (hist[t]) hist[t] = atomicAdd(&cursor[g * kCells + t], hist[t]);
     __syncthreads();
     const float *X = S.xs + c * D * S.p;
-    float *O = S.sorted + c * D * S.p;
+    float4 *O = S.rec + c * S.p;
     for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
         float a[D];
 #pragma unroll
         for (int k = 0; k < D; ++k) a[k] = X[k * S.p + n];
         const uint32_t slot = atomicAdd(&hist[cell_of<D>(a, fr)], 1u);
-#pragma unroll
-        for (int k = 0; k < D; ++k) O[k * S.p + slot] = a[k];
-        if (S.pos) S.pos[c * S.p + slot] = (uint32_t)n;
+        O[slot] = make_rec<D>(a, (uint32_t)n);
     }
 }
 
@@ -977,7 +1011,7 @@ __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellS
 // four 64-point steps in flight, and drops m at the first d < T; an m never dropped folds its
 // exact min with its iteration position mpos.
 template <int D>
-__device__ __forceinline__ void wave_full_scan(const float (&b)[D], const float *X2, int64_t p2, int64_t st,
+__device__ __forceinline__ void wave_full_scan(const float (&b)[D], const float4 *X2, int64_t p2, int64_t st,
                                                unsigned long long *key, int64_t mpos) {
     const int lane = threadIdx.x & 63;
     float T = threshold_of(key);
@@ -989,7 +1023,7 @@ __device__ __forceinline__ void wave_full_scan(const float (&b)[D], const float 
         for (int u = 0; u < 4; ++u) {
             int64_t n = st + t0 + 64 * u + lane;
             if (n >= p2) n -= p2;
-            dd[u] = sqdist_fixed<D>(b, X2, p2, n);
+            dd[u] = rec_dist<D>(b, X2[n]);
         }
         const float dmin = fminf(fminf(dd[0], dd[1]), fminf(dd[2], dd[3]));
         if (__any(dmin < T)) return;
@@ -1000,7 +1034,7 @@ __device__ __forceinline__ void wave_full_scan(const float (&b)[D], const float 
         const int64_t t = t0 + lane;
         int64_t n = st + t;
         if (n >= p2) n -= p2;
-        const float dd = t < p2 ? sqdist_fixed<D>(b, X2, p2, n) : INFINITY;
+        const float dd = t < p2 ? rec_dist<D>(b, X2[n]) : INFINITY;
         if (__any(dd < T)) return;
         best = fminf(best, dd);
     }
@@ -1011,7 +1045,7 @@ __device__ __forceinline__ void wave_full_scan(const float (&b)[D], const float 
 // Whether the whole wave, scanning `budget` points (a multiple of 256, below p2) of the sorted
 // x2 circularly from st, meets a d < T for the point b (the same answer in every lane).
 template <int D>
-__device__ __forceinline__ bool wave_scan_prunes(const float (&b)[D], const float *X2, int64_t p2, int64_t st,
+__device__ __forceinline__ bool wave_scan_prunes(const float (&b)[D], const float4 *X2, int64_t p2, int64_t st,
                                                  const unsigned long long *key, int64_t budget) {
     const int lane = threadIdx.x & 63;
     float T = threshold_of(key);
@@ -1021,7 +1055,7 @@ __device__ __forceinline__ bool wave_scan_prunes(const float (&b)[D], const floa
         for (int u = 0; u < 4; ++u) {
             int64_t n = st + t0 + 64 * u + lane;
             if (n >= p2) n -= p2;
-            dd[u] = sqdist_fixed<D>(b, X2, p2, n);
+            dd[u] = rec_dist<D>(b, X2[n]);
         }
         const float dmin = fminf(fminf(dd[0], dd[1]), fminf(dd[2], dd[3]));
         if (__any(dmin < T)) return true;
@@ -1044,14 +1078,14 @@ __device__ __forceinline__ int64_t window_start(const float (&a)[D], const float
 // lane checks the 64 sorted x2 points of its window, first the head of its own cell (which
 // almost always holds a point within T), and stops at the first d < T.  The pair's seeds have
 // their exact mins in the key already and are skipped.
-//   SORTED (x1 sorted by cell in the batch frame, pos1 = iteration positions): neighbouring
-//     lanes share windows, so the loads coalesce; a lane left sets flag[pair][m position]
-//     (preset to 0), and scan_flagged_kernel scans those m in iteration order.
+//   SORTED (x1 as cell-sorted records in the batch frame): neighbouring lanes share windows,
+//     so the loads coalesce; a lane left sets flag[pair][m position] (preset to 0), and
+//     scan_flagged_kernel scans those m in iteration order.
 //   otherwise (x1 in iteration order, x2 sorted in its cloud's own frame): the lanes left
 //     (ballot) are scanned in turn by the whole wave (wave_full_scan).
 template <int D, bool SORTED>
 __global__ __launch_bounds__(kThreads) void scan_window_kernel(
-    const float *__restrict__ xs1, const uint32_t *__restrict__ pos1, const float *__restrict__ xs2s,
+    const float *__restrict__ xs1, const float4 *__restrict__ xs1r, const float4 *__restrict__ xs2r,
     const int32_t *__restrict__ cstart2, const float *__restrict__ boxes, int64_t b1, int64_t b2,
     int64_t p1, int64_t p2, int64_t m_per_block, const uint32_t *__restrict__ seedm,
     unsigned long long *__restrict__ keys, uint8_t *__restrict__ flags) {
@@ -1059,8 +1093,9 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
     const int64_t per_batch = b1 * b2;
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
     const int64_t i = rem / b2, j = rem - i * b2;
-    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
-    const float *X2 = xs2s + (bb * b2 + j) * D * p2;
+    const float *X1 = SORTED ? nullptr : xs1 + (bb * b1 + i) * D * p1;
+    const float4 *X1r = SORTED ? xs1r + (bb * b1 + i) * p1 : nullptr;
+    const float4 *X2 = xs2r + (bb * b2 + j) * p2;
     const int32_t *CS = cstart2 + (bb * b2 + j) * (kCells + 1);
     float fr[2 * D];
     frame_of<D>(boxes + (SORTED ? bb : bb * b2 + j) * D * 2, fr);
@@ -1074,9 +1109,16 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
         const int64_t m = m0 + lane;
         const bool valid = m < mend;
         float a[D];
+        int64_t mpos = m;
+        if constexpr (SORTED) {
+            const float4 v = X1r[valid ? m : mbeg];  // mbeg < p1; an invalid lane is done
 #pragma unroll
-        for (int k = 0; k < D; ++k) a[k] = valid ? X1[k * p1 + m] : 0.0f;
-        const int64_t mpos = SORTED ? (valid ? (int64_t)pos1[(bb * b1 + i) * p1 + m] : 0) : m;
+            for (int k = 0; k < D; ++k) a[k] = rec_coord(v, k);
+            mpos = rec_pos(v);
+        } else {
+#pragma unroll
+            for (int k = 0; k < D; ++k) a[k] = valid ? X1[k * p1 + m] : 0.0f;
+        }
         const int64_t s0 = window_start<D>(a, fr, CS, p2);
         const float T = threshold_of(key);
         bool done = !valid || is_seed(seedm, pair, mpos);
@@ -1086,14 +1128,14 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
             bool hit = false;
 #pragma unroll
             for (int u = 0; u < 2; ++u)
-                if (u < wlen) hit = hit | (sqdist_fixed<D>(a, X2, p2, s0 + u) < T);
+                if (u < wlen) hit = hit | (rec_dist<D>(a, X2[s0 + u]) < T);
             done = done || hit;
         }
         for (int64_t t = 2; t < wlen && !done; t += 8) {
             bool hit = false;
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                if (t + u < wlen) hit = hit | (sqdist_fixed<D>(a, X2, p2, s0 + t + u) < T);
+                if (t + u < wlen) hit = hit | (rec_dist<D>(a, X2[s0 + t + u]) < T);
             done = hit;
         }
         if constexpr (SORTED) {
@@ -1124,7 +1166,7 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
 // here in full.
 template <int D>
 __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
-    const float *__restrict__ xs1, const float *__restrict__ xs2s, const int32_t *__restrict__ cstart2,
+    const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
     const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t budget,
     unsigned long long *__restrict__ keys, const uint8_t *__restrict__ flags, uint32_t *__restrict__ survm,
     uint32_t *__restrict__ survcnt, int64_t K) {
@@ -1134,7 +1176,7 @@ __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
     const int64_t i = rem / b2, j = rem - i * b2;
     const float *X1 = xs1 + (bb * b1 + i) * D * p1;
-    const float *X2 = xs2s + (bb * b2 + j) * D * p2;
+    const float4 *X2 = xs2r + (bb * b2 + j) * p2;
     const int32_t *CS = cstart2 + (bb * b2 + j) * (kCells + 1);
     float fr[2 * D];
     frame_of<D>(boxes + bb * D * 2, fr);
@@ -1238,19 +1280,20 @@ constexpr int64_t kSurvivors = 64;
 constexpr int64_t kBudget = 2048;
 
 struct Workspace {
-    float *xs1, *xs2, *bbox, *xs2s, *bbox1, *boxb, *xs1s;
+    float *xs1, *xs2, *bbox, *bbox1, *boxb;
+    float4 *xs2r, *xs1r;
     unsigned long long *keys, *cand, *first;
     int32_t *cstart2;
     int *boxkeys;
-    uint32_t *pos1, *seedmin, *seedm, *cursor, *survm, *survmin, *survcnt;
+    uint32_t *seedmin, *seedm, *cursor, *survm, *survmin, *survcnt;
     uint8_t *flags;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // [keys | x2 boxes | x1 SoA | x2 SoA | box keys | seeds, candidates, first hits (fast) |
-//  sorted x2, x2 cell starts (cells) | x1 boxes, batch boxes, sorted x1, x1 positions, flags,
-//  survivors (sorted) | sort cursors (multi_sort)]
+//  x2 records, x2 cell starts (cells) | x1 boxes, batch boxes, x1 records, flags, survivors
+//  (sorted) | sort cursors (multi_sort)]
 Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
     auto take = [&](bool on, size_t bytes) {
@@ -1268,12 +1311,11 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
     w.seedm = reinterpret_cast<uint32_t *>(take(P.fast, 4 * P.pairs * kSeeds));
     w.cand = reinterpret_cast<unsigned long long *>(take(P.fast, 8 * P.pairs * P.ncand));
     w.first = reinterpret_cast<unsigned long long *>(take(P.fast, 8 * P.pairs));
-    w.xs2s = reinterpret_cast<float *>(take(P.cells, 4 * P.clouds2 * p2 * d));
+    w.xs2r = reinterpret_cast<float4 *>(take(P.cells, 16 * P.clouds2 * p2));
     w.cstart2 = reinterpret_cast<int32_t *>(take(P.cells, 4 * P.clouds2 * (kCells + 1)));
     w.bbox1 = reinterpret_cast<float *>(take(P.sorted, 4 * P.clouds1 * d * 2));
     w.boxb = reinterpret_cast<float *>(take(P.sorted, 4 * P.batch * d * 2));
-    w.xs1s = reinterpret_cast<float *>(take(P.sorted, 4 * P.clouds1 * p1 * d));
-    w.pos1 = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.clouds1 * p1));
+    w.xs1r = reinterpret_cast<float4 *>(take(P.sorted, 16 * P.clouds1 * p1));
     w.flags = reinterpret_cast<uint8_t *>(take(P.sorted, (size_t)(P.pairs * p1)));
     w.survm = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * kSurvivors));
     w.survmin = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * kSurvivors));
@@ -1283,14 +1325,11 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
     return w;
 }
 
-// Step 3 for d <= 3: cell sort of x2 (and, in the sorted mode, of x1), then the window pass
-// and the scan of the m it leaves.
+// Cell sort of x2 (and, in the sorted mode, of x1) into records.
 template <int D>
-int launch_cells(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
-                 hipStream_t s) {
-    const CellSet S2{w.xs2, w.xs2s, nullptr, w.cstart2, P.sorted ? w.boxb : w.bbox, P.clouds2, p2,
-                     P.sorted ? b2 : 1};
-    const CellSet S1{w.xs1, w.xs1s, w.pos1, nullptr, w.boxb, P.sorted ? P.clouds1 : 0, p1, b1};
+void launch_sort(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2, hipStream_t s) {
+    const CellSet S2{w.xs2, w.xs2r, w.cstart2, P.sorted ? w.boxb : w.bbox, P.clouds2, p2, P.sorted ? b2 : 1};
+    const CellSet S1{w.xs1, w.xs1r, nullptr, w.boxb, P.sorted ? P.clouds1 : 0, p1, b1};
     if (P.multi_sort) {
         const dim3 grid((unsigned)P.sort_clouds, (unsigned)P.sort_chunks);
         hipLaunchKernelGGL(cell_count_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, w.cursor);
@@ -1299,64 +1338,85 @@ int launch_cells(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int6
         hipLaunchKernelGGL(cell_scatter_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, w.cursor);
     } else {
         hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)P.clouds2), dim3(kThreads), 0, s, w.xs2, p2,
-                           S2.boxes, S2.clouds_per_box, w.xs2s, static_cast<uint32_t *>(nullptr), w.cstart2);
+                           S2.boxes, S2.clouds_per_box, w.xs2r, w.cstart2);
         if (P.sorted)
             hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)P.clouds1), dim3(kThreads), 0, s, w.xs1, p1,
-                               w.boxb, b1, w.xs1s, w.pos1, static_cast<int32_t *>(nullptr));
+                               w.boxb, b1, w.xs1r, static_cast<int32_t *>(nullptr));
     }
+}
+
+// The cell-sorted scan (d <= 3): window pass, then, in the sorted mode, the flagged m and the
+// survivors' full scans.
+template <int D>
+void launch_cell_scan(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
+                      hipStream_t s) {
     const int64_t m_per_block = 2048;
     const dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs);
     if (P.sorted) {
-        hipLaunchKernelGGL((scan_window_kernel<D, true>), grid, dim3(kThreads), 0, s, w.xs1s, w.pos1, w.xs2s,
-                           w.cstart2, w.boxb, b1, b2, p1, p2, m_per_block, w.seedm, w.keys, w.flags);
+        hipLaunchKernelGGL((scan_window_kernel<D, true>), grid, dim3(kThreads), 0, s,
+                           static_cast<const float *>(nullptr), w.xs1r, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2,
+                           m_per_block, w.seedm, w.keys, w.flags);
         hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, kThreads), (unsigned)P.pairs),
-                           dim3(kThreads), 0, s, w.xs1, w.xs2s, w.cstart2, w.boxb, b1, b2, p1, p2, kBudget, w.keys,
+                           dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2, kBudget, w.keys,
                            w.flags, w.survm, w.survcnt, kSurvivors);
-        hipLaunchKernelGGL(list_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
-                           w.xs1, w.xs2, w.survm, w.survcnt, kSurvivors, b1, b2, p1, p2, P.chunk2, w.survmin);
+        hipLaunchKernelGGL((list_scan_kernel<D, true>), dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads),
+                           0, s, w.xs1, reinterpret_cast<const float *>(w.xs2r), w.survm, w.survcnt, kSurvivors,
+                           b1, b2, p1, p2, P.chunk2, w.survmin);
         hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSurvivors, 256)), dim3(256), 0, s,
                            w.survmin, w.survm, w.survcnt, kSurvivors, P.pairs, w.keys);
     } else {
         hipLaunchKernelGGL((scan_window_kernel<D, false>), grid, dim3(kThreads), 0, s, w.xs1,
-                           static_cast<const uint32_t *>(nullptr), w.xs2s, w.cstart2, w.bbox, b1, b2, p1, p2,
+                           static_cast<const float4 *>(nullptr), w.xs2r, w.cstart2, w.bbox, b1, b2, p1, p2,
                            m_per_block, w.seedm, w.keys, static_cast<uint8_t *>(nullptr));
     }
-    return check_launch("hausdorff cell scan");
 }
 
-// d = 1..4 after the relayout and the boxes: seeds, scan, final rescan and outputs.
+// d = 1..4 after the relayout and the boxes: (cell sort,) seeds, scan, final rescan, outputs.
 template <int D>
 int launch_fast(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
                 const int64_t *perm1, const int64_t *perm2, float *out, int64_t *idx1, int64_t *idx2,
                 hipStream_t s) {
+    constexpr bool kCellsOk = D <= 3;
+    const bool cells = kCellsOk && P.cells;
+    if constexpr (kCellsOk) {
+        if (cells) launch_sort<D>(P, w, b1, p1, b2, p2, s);
+    }
+    const float *x2pts = cells ? reinterpret_cast<const float *>(w.xs2r) : w.xs2;
     hipLaunchKernelGGL(seed_select_kernel<D>, dim3((unsigned)P.pairs, (unsigned)cdiv(p1, P.chunk1)),
                        dim3(kThreads), 0, s, w.xs1, w.bbox, b1, b2, p1, P.chunk1, P.ncand, w.cand);
     hipLaunchKernelGGL(seed_pick_kernel, dim3((unsigned)cdiv(P.pairs, kThreads / 64)), dim3(kThreads), 0, s,
                        w.cand, P.ncand, P.pairs, w.seedm);
-    hipLaunchKernelGGL(list_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
-                       w.xs1, w.xs2, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1,
-                       p2, P.chunk2, w.seedmin);
+    const dim3 grid2((unsigned)P.pairs, (unsigned)P.nch2);
+    if (cells)
+        hipLaunchKernelGGL((list_scan_kernel<D, kCellsOk>), grid2, dim3(kThreads), 0, s, w.xs1, x2pts, w.seedm,
+                           static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunk2,
+                           w.seedmin);
+    else
+        hipLaunchKernelGGL((list_scan_kernel<D, false>), grid2, dim3(kThreads), 0, s, w.xs1, x2pts, w.seedm,
+                           static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunk2,
+                           w.seedmin);
     hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s,
                        w.seedmin, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, P.pairs, w.keys);
     int rc = check_launch("hausdorff seeds");
     if (rc) return rc;
-    if constexpr (D <= 3) {
-        if (P.cells) {
-            rc = launch_cells<D>(P, w, b1, p1, b2, p2, s);
-            if (rc) return rc;
-        }
+    if constexpr (kCellsOk) {
+        if (cells) launch_cell_scan<D>(P, w, b1, p1, b2, p2, s);
     }
-    if (!P.cells) {
+    if (!cells) {
         const int64_t m_per_block = 2048;
         const int64_t lds_points = (kLdsFloats / D) / 64 * 64;
         hipLaunchKernelGGL(scan_kernel<D>, dim3((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs),
                            dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.seedm,
                            w.keys);
-        rc = check_launch("hausdorff scan_kernel");
-        if (rc) return rc;
     }
-    hipLaunchKernelGGL(first_hit_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
-                       w.xs1, w.xs2, w.keys, b1, b2, p1, p2, P.chunk2, w.first);
+    rc = check_launch("hausdorff scan");
+    if (rc) return rc;
+    if (cells)
+        hipLaunchKernelGGL((first_hit_kernel<D, kCellsOk>), grid2, dim3(kThreads), 0, s, w.xs1, x2pts, w.keys, b1,
+                           b2, p1, p2, P.chunk2, w.first);
+    else
+        hipLaunchKernelGGL((first_hit_kernel<D, false>), grid2, dim3(kThreads), 0, s, w.xs1, x2pts, w.keys, b1,
+                           b2, p1, p2, P.chunk2, w.first);
     hipLaunchKernelGGL(write_out_kernel, dim3((unsigned)cdiv(P.pairs, 256)), dim3(256), 0, s, w.keys, w.first,
                        perm1, perm2, P.pairs, b1, b2, p1, p2, out, idx1, idx2);
     return check_launch("hausdorff final rescan");

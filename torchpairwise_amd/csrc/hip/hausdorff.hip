@@ -16,7 +16,7 @@
 //   3. scan (d <= 3): x2 clouds are counting-sorted by grid cell once; every lane takes one m
 //      and checks the 64 sorted x2 points at m's cell, stopping at the first d < T; the m left
 //      are scanned by the whole wave (64 n per step, dropping m at the first d < T).  When the
-//      flags fit (pairs x p1 bytes <= 256 MiB), x1 is sorted by cell too, in a frame shared
+//      flags fit (pairs x p1 bits <= 32 MiB), x1 is sorted by cell too, in a frame shared
 //      with x2, so that neighbouring lanes check overlapping windows, and the m left are
 //      flagged and scanned in iteration order by a second kernel.
 //      (d > 3: every wave takes one m at a time over x2 in iteration order, the first points
@@ -62,6 +62,8 @@ __device__ __forceinline__ float sqdist_fixed(const float (&a)[D], const float *
     }
     return s;
 }
+
+__device__ __forceinline__ int64_t cdiv_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 __device__ __forceinline__ float wave_min(float v) {
 #pragma unroll
@@ -143,10 +145,15 @@ struct Fills {
 
 __global__ void fill_kernel(Fills fs) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int r = 0; r < fs.count; ++r) {
-        const Fill f = fs.f[r];
-        for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < f.n; t += stride)
-            f.p[t] = f.v[t & 1];
+    // constant indices only (a dynamically indexed copy of the argument would live in LDS)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        if (r >= fs.count) break;
+        uint32_t *p = fs.f[r].p;
+        const int64_t n = fs.f[r].n;
+        const uint32_t v0 = fs.f[r].v[0], v1 = fs.f[r].v[1];
+        for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n; t += stride)
+            p[t] = (t & 1) ? v1 : v0;
     }
 }
 
@@ -622,25 +629,37 @@ __global__ __launch_bounds__(kThreads) void list_scan_kernel(
         float best[kGroup];
 #pragma unroll
         for (int s = 0; s < kGroup; ++s) best[s] = INFINITY;
-        for (int64_t q = beg + threadIdx.x; q < end; q += kThreads) {
-            float b[D];
-            if constexpr (REC) {
-                const float4 v = R[q];
+        // four points per thread and step, their loads in flight together
+        for (int64_t q0 = beg + threadIdx.x; q0 < end; q0 += 4 * kThreads) {
+            float b[4][D];
 #pragma unroll
-                for (int k = 0; k < D; ++k) b[k] = rec_coord(v, k);
-            } else {
+            for (int u = 0; u < 4; ++u) {
+                const int64_t q = q0 + u * kThreads;
+                const bool ok = q < end;
+                const int64_t qq = ok ? q : q0;
+                if constexpr (REC) {
+                    const float4 v = R[qq];
 #pragma unroll
-                for (int k = 0; k < D; ++k) b[k] = P.x2[k * p2 + q];
+                    for (int k = 0; k < D; ++k) b[u][k] = rec_coord(v, k);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < D; ++k) b[u][k] = P.x2[k * p2 + qq];
+                }
+                // a missing point: d = inf or NaN, which fminf passes over
+                b[u][0] = ok ? b[u][0] : INFINITY;
             }
 #pragma unroll
-            for (int s = 0; s < kGroup; ++s) {
-                float acc = 0.0f;
+            for (int u = 0; u < 4; ++u) {
 #pragma unroll
-                for (int k = 0; k < D; ++k) {
-                    const float diff = a[s][k] - b[k];
-                    acc = acc + diff * diff;
+                for (int s = 0; s < kGroup; ++s) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < D; ++k) {
+                        const float diff = a[s][k] - b[u][k];
+                        acc = acc + diff * diff;
+                    }
+                    best[s] = fminf(best[s], acc);
                 }
-                best[s] = fminf(best[s], acc);
             }
         }
 #pragma unroll
@@ -1079,8 +1098,8 @@ __device__ __forceinline__ int64_t window_start(const float (&a)[D], const float
 // almost always holds a point within T), and stops at the first d < T.  The pair's seeds have
 // their exact mins in the key already and are skipped.
 //   SORTED (x1 as cell-sorted records in the batch frame): neighbouring lanes share windows,
-//     so the loads coalesce; a lane left sets flag[pair][m position] (preset to 0), and
-//     scan_flagged_kernel scans those m in iteration order.
+//     so the loads coalesce; a lane left sets bit m position of its pair's flag bits (preset
+//     to 0), and scan_flagged_kernel scans those m in iteration order.
 //   otherwise (x1 in iteration order, x2 sorted in its cloud's own frame): the lanes left
 //     (ballot) are scanned in turn by the whole wave (wave_full_scan).
 template <int D, bool SORTED>
@@ -1088,7 +1107,7 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
     const float *__restrict__ xs1, const float4 *__restrict__ xs1r, const float4 *__restrict__ xs2r,
     const int32_t *__restrict__ cstart2, const float *__restrict__ boxes, int64_t b1, int64_t b2,
     int64_t p1, int64_t p2, int64_t m_per_block, const uint32_t *__restrict__ seedm,
-    unsigned long long *__restrict__ keys, uint8_t *__restrict__ flags) {
+    unsigned long long *__restrict__ keys, uint32_t *__restrict__ flagbits) {
     const int64_t pair = blockIdx.y;
     const int64_t per_batch = b1 * b2;
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
@@ -1104,72 +1123,92 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
     const int64_t mbeg = (int64_t)blockIdx.x * m_per_block;
     const int64_t mend = mbeg + m_per_block < p1 ? mbeg + m_per_block : p1;
     const int64_t wlen = p2 < 64 ? p2 : 64;
+    const int64_t fwords = cdiv_dev(p1, 32);
     unsigned long long *key = &keys[pair];
-    for (int64_t m0 = mbeg + 64 * wave; m0 < mend; m0 += 64 * (kThreads / 64)) {
-        const int64_t m = m0 + lane;
-        const bool valid = m < mend;
-        float a[D];
-        int64_t mpos = m;
-        if constexpr (SORTED) {
-            const float4 v = X1r[valid ? m : mbeg];  // mbeg < p1; an invalid lane is done
+    // four groups of 64 m per step (m0, m0 + 256, ...), so that their dependent loads (point,
+    // cell start, window) overlap
+    constexpr int kG = 4;
+    for (int64_t m0 = mbeg + 64 * wave; m0 < mend; m0 += kG * kThreads) {
+        float a[kG][D];
+        int64_t mpos[kG], s0[kG];
+        bool done[kG];
 #pragma unroll
-            for (int k = 0; k < D; ++k) a[k] = rec_coord(v, k);
-            mpos = rec_pos(v);
-        } else {
+        for (int g = 0; g < kG; ++g) {
+            const int64_t m = m0 + g * kThreads + lane;
+            const bool valid = m < mend;
+            mpos[g] = m;
+            if constexpr (SORTED) {
+                const float4 v = X1r[valid ? m : mbeg];  // mbeg < p1; an invalid lane is done
 #pragma unroll
-            for (int k = 0; k < D; ++k) a[k] = valid ? X1[k * p1 + m] : 0.0f;
+                for (int k = 0; k < D; ++k) a[g][k] = rec_coord(v, k);
+                mpos[g] = rec_pos(v);
+            } else {
+#pragma unroll
+                for (int k = 0; k < D; ++k) a[g][k] = X1[k * p1 + (valid ? m : mbeg)];
+            }
+            done[g] = !valid;
         }
-        const int64_t s0 = window_start<D>(a, fr, CS, p2);
+#pragma unroll
+        for (int g = 0; g < kG; ++g) s0[g] = window_start<D>(a[g], fr, CS, p2);
         const float T = threshold_of(key);
-        bool done = !valid || is_seed(seedm, pair, mpos);
-        // two points first, then 8 per step so that their loads are in flight together (fewer
-        // in all when p2 < 64)
-        {
+        // two points first (the head of m's own cell), then 8 per step so that their loads are
+        // in flight together (fewer in all when p2 < 64)
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
             bool hit = false;
 #pragma unroll
             for (int u = 0; u < 2; ++u)
-                if (u < wlen) hit = hit | (rec_dist<D>(a, X2[s0 + u]) < T);
-            done = done || hit;
+                if (u < wlen) hit = hit | (rec_dist<D>(a[g], X2[s0[g] + u]) < T);
+            done[g] = done[g] || hit || is_seed(seedm, pair, mpos[g]);
         }
-        for (int64_t t = 2; t < wlen && !done; t += 8) {
-            bool hit = false;
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (t + u < wlen) hit = hit | (rec_dist<D>(a, X2[s0 + t + u]) < T);
-            done = hit;
+        for (int g = 0; g < kG; ++g) {
+            for (int64_t t = 2; t < wlen && !done[g]; t += 8) {
+                bool hit = false;
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (t + u < wlen) hit = hit | (rec_dist<D>(a[g], X2[s0[g] + t + u]) < T);
+                done[g] = hit;
+            }
         }
-        if constexpr (SORTED) {
-            if (!done) flags[pair * p1 + mpos] = 1;
-        } else {
-            unsigned long long left = __ballot(!done);
-            while (left) {
-                const int l = __builtin_ctzll(left);
-                left &= left - 1;
-                float b[D];
 #pragma unroll
-                for (int k = 0; k < D; ++k)
-                    b[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[k]), l));
-                const int64_t st = (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)s0, l);
-                wave_full_scan<D>(b, X2, p2, st, key, m0 + l);
+        for (int g = 0; g < kG; ++g) {
+            if constexpr (SORTED) {
+                if (!done[g]) atomicOr(&flagbits[pair * fwords + (mpos[g] >> 5)], 1u << (mpos[g] & 31));
+            } else {
+                unsigned long long left = __ballot(!done[g]);
+                while (left) {
+                    const int l = __builtin_ctzll(left);
+                    left &= left - 1;
+                    float b[D];
+#pragma unroll
+                    for (int k = 0; k < D; ++k)
+                        b[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[g][k]), l));
+                    const int64_t st = (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)s0[g], l);
+                    wave_full_scan<D>(b, X2, p2, st, key, m0 + g * kThreads + l);
+                }
             }
         }
     }
 }
 
-// The m the window pass of the sorted mode left (flags), in iteration order: each wave takes
-// 64 consecutive m, and the flagged ones are scanned in turn by the whole wave, `budget` points
-// from the window's start (or all of x2, when that is no more, folding the exact min).  An m
-// still not dropped after its budget is a survivor: its exact min needs all of x2, which one
-// wave would take a long serial time over, so it goes to survm[pair] (slots reserved with one
-// atomicAdd per block on survcnt[pair], handed to the waves through LDS after a barrier) for
-// list_scan_kernel, which spreads it over many blocks.  Survivors beyond K slots are scanned
-// here in full.
+// The m the window pass of the sorted mode left (flag bits), in iteration order: block =
+// 256 words = 8192 m of one pair, each lane one word; the flagged m are scanned in turn by their
+// wave, `budget` points from the window's start (or all of x2, when that is no more, folding the
+// exact min).  An m still not dropped after its budget is a survivor: its exact min needs all
+// of x2, which one wave would take a long serial time over, so it goes to survm[pair] for
+// list_scan_kernel, which spreads it over many blocks.  A wave keeps its survivors in LDS (kept
+// by lane 0, counted alike in every lane); the block reserves slots with one atomicAdd on
+// survcnt[pair], handed to the waves through LDS after a barrier.  Survivors beyond a wave's
+// LDS list or beyond K slots are scanned here in full.
 template <int D>
 __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
     const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
     const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t budget,
-    unsigned long long *__restrict__ keys, const uint8_t *__restrict__ flags, uint32_t *__restrict__ survm,
+    unsigned long long *__restrict__ keys, const uint32_t *__restrict__ flagbits, uint32_t *__restrict__ survm,
     uint32_t *__restrict__ survcnt, int64_t K) {
+    constexpr int kWaveList = 32;
+    __shared__ uint32_t wl[kThreads / 64][kWaveList];
     __shared__ uint32_t wn[kThreads / 64], wb[kThreads / 64];
     const int64_t pair = blockIdx.y;
     const int64_t per_batch = b1 * b2;
@@ -1182,23 +1221,39 @@ __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
     frame_of<D>(boxes + bb * D * 2, fr);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t m0 = (int64_t)blockIdx.x * kThreads + 64 * __builtin_amdgcn_readfirstlane(wave);
-    const int64_t m = m0 + lane;
     unsigned long long *key = &keys[pair];
-    const bool flagged = m < p1 && flags[pair * p1 + m] != 0;
-    unsigned long long left = __ballot(flagged);
-    unsigned long long surv = 0;  // built from wave-wide values only
+    const int64_t fwords = cdiv_dev(p1, 32);
+    const int64_t wi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t word = wi < fwords ? flagbits[pair * fwords + wi] : 0u;
+    const int64_t wbase = ((int64_t)blockIdx.x * kThreads + 64 * __builtin_amdgcn_readfirstlane(wave)) * 32;
+    unsigned long long left = __ballot(word != 0u);
+    uint32_t nsurv = 0;  // the same in every lane
     while (left) {
         const int l = __builtin_ctzll(left);
         left &= left - 1;
-        float b[D];
+        uint32_t bits = (uint32_t)__builtin_amdgcn_readlane((int)word, l);
+        while (bits) {
+            const int bit = __builtin_ctz(bits);
+            bits &= bits - 1;
+            const int64_t mm = wbase + 32 * l + bit;  // < p1: only real m are flagged
+            float b[D];
 #pragma unroll
-        for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + m0 + l];
-        const int64_t st = window_start<D>(b, fr, CS, p2);
-        if (p2 <= budget) wave_full_scan<D>(b, X2, p2, st, key, m0 + l);
-        else if (!wave_scan_prunes<D>(b, X2, p2, st, key, budget)) surv |= 1ull << l;
+            for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + mm];
+            const int64_t st = window_start<D>(b, fr, CS, p2);
+            if (p2 <= budget) {
+                wave_full_scan<D>(b, X2, p2, st, key, mm);
+            } else if (!wave_scan_prunes<D>(b, X2, p2, st, key, budget)) {
+                if (nsurv < kWaveList) {
+                    if (lane == 0) wl[wave][nsurv] = (uint32_t)mm;
+                } else {
+                    wave_full_scan<D>(b, X2, p2, st, key, mm);
+                }
+                ++nsurv;
+            }
+        }
     }
-    if (lane == 0) wn[wave] = (uint32_t)__builtin_popcountll(surv);
+    const uint32_t mine_n = nsurv < kWaveList ? nsurv : kWaveList;
+    if (lane == 0) wn[wave] = mine_n;
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t tot = 0;
@@ -1210,21 +1265,23 @@ __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
         }
     }
     __syncthreads();
-    const bool mine = (surv >> lane) & 1ull;
-    const int64_t slot = (int64_t)wb[wave] + __builtin_popcountll(surv & ((1ull << lane) - 1ull));
-    if (mine && slot < K) survm[pair * K + slot] = (uint32_t)m;
-    unsigned long long over = __ballot(mine && slot >= K);
+    const bool have = (uint32_t)lane < wn[wave];
+    const int64_t slot = (int64_t)wb[wave] + lane;
+    const uint32_t mm = have ? wl[wave][lane] : 0u;
+    if (have && slot < K) survm[pair * K + slot] = mm;
+    unsigned long long over = __ballot(have && slot >= K);
     while (over) {
         const int l = __builtin_ctzll(over);
         over &= over - 1;
+        const int64_t ml = (uint32_t)__builtin_amdgcn_readlane((int)mm, l);
         float b[D];
 #pragma unroll
-        for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + m0 + l];
-        wave_full_scan<D>(b, X2, p2, window_start<D>(b, fr, CS, p2), key, m0 + l);
+        for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + ml];
+        wave_full_scan<D>(b, X2, p2, window_start<D>(b, fr, CS, p2), key, ml);
     }
 }
 
-// The sorted mode keeps one flag byte per (pair, m): up to 256 MiB of them.
+// The sorted mode keeps one flag bit per (pair, m): up to 32 MiB of them.
 inline bool sorted_mode(int64_t pairs, int64_t p1) { return pairs * p1 <= ((int64_t)1 << 28); }
 
 int64_t round_up(int64_t v, int64_t q) { return cdiv(v, q) * q; }
@@ -1239,7 +1296,8 @@ struct Plan {
     bool multi_sort = false;  // few clouds to sort: the counting sort spread over blocks
     int64_t box_rows1 = 0, box_rows2 = 0, box_chunk = 1, box_chunks = 0;
     int64_t chunk1 = 1, ncand = 0;   // x1 points per seed_select block; candidates per pair
-    int64_t chunk2 = 1, nch2 = 0;    // x2 points per seed_scan / first_hit block
+    int64_t chunk2 = 1, nch2 = 0;    // x2 points per first_hit block
+    int64_t chunkL = 1, nchL = 0;    // x2 points per list_scan block of the seeds
     int64_t sort_clouds = 0, sort_chunk = 1, sort_chunks = 0;
 };
 
@@ -1264,6 +1322,8 @@ Plan make_plan(int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, in
     P.ncand = cdiv(p1, P.chunk1) * (kThreads / 64);
     P.chunk2 = std::max<int64_t>(4096, round_up(cdiv(p2, kMaxGridYZ), kThreads));
     P.nch2 = cdiv(p2, P.chunk2);
+    P.chunkL = std::max<int64_t>(16384, round_up(cdiv(p2, kMaxGridYZ), kThreads));
+    P.nchL = cdiv(p2, P.chunkL);
     if (P.cells) {
         P.sort_clouds = P.clouds2 + (P.sorted ? P.clouds1 : 0);
         P.multi_sort = P.sort_clouds <= 2048;  // cursor <= 32 MiB
@@ -1286,13 +1346,13 @@ struct Workspace {
     int32_t *cstart2;
     int *boxkeys;
     uint32_t *seedmin, *seedm, *cursor, *survm, *survmin, *survcnt;
-    uint8_t *flags;
+    uint32_t *flagbits;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // [keys | x2 boxes | x1 SoA | x2 SoA | box keys | seeds, candidates, first hits (fast) |
-//  x2 records, x2 cell starts (cells) | x1 boxes, batch boxes, x1 records, flags, survivors
+//  x2 records, x2 cell starts (cells) | x1 boxes, batch boxes, x1 records, flag bits, survivors
 //  (sorted) | sort cursors (multi_sort)]
 Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
@@ -1316,7 +1376,7 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
     w.bbox1 = reinterpret_cast<float *>(take(P.sorted, 4 * P.clouds1 * d * 2));
     w.boxb = reinterpret_cast<float *>(take(P.sorted, 4 * P.batch * d * 2));
     w.xs1r = reinterpret_cast<float4 *>(take(P.sorted, 16 * P.clouds1 * p1));
-    w.flags = reinterpret_cast<uint8_t *>(take(P.sorted, (size_t)(P.pairs * p1)));
+    w.flagbits = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * cdiv(p1, 32)));
     w.survm = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * kSurvivors));
     w.survmin = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * kSurvivors));
     w.survcnt = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs));
@@ -1355,10 +1415,11 @@ void launch_cell_scan(const Plan &P, const Workspace &w, int64_t b1, int64_t p1,
     if (P.sorted) {
         hipLaunchKernelGGL((scan_window_kernel<D, true>), grid, dim3(kThreads), 0, s,
                            static_cast<const float *>(nullptr), w.xs1r, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2,
-                           m_per_block, w.seedm, w.keys, w.flags);
-        hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, kThreads), (unsigned)P.pairs),
+                           m_per_block, w.seedm, w.keys, w.flagbits);
+        hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, 32 * kThreads), (unsigned)P.pairs),
                            dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2, kBudget, w.keys,
-                           w.flags, w.survm, w.survcnt, kSurvivors);
+                           w.flagbits, w.survm, w.survcnt, kSurvivors);
+        // survivors: counts vary by pair, so small blocks keep the slow pairs spread out
         hipLaunchKernelGGL((list_scan_kernel<D, true>), dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads),
                            0, s, w.xs1, reinterpret_cast<const float *>(w.xs2r), w.survm, w.survcnt, kSurvivors,
                            b1, b2, p1, p2, P.chunk2, w.survmin);
@@ -1367,7 +1428,7 @@ void launch_cell_scan(const Plan &P, const Workspace &w, int64_t b1, int64_t p1,
     } else {
         hipLaunchKernelGGL((scan_window_kernel<D, false>), grid, dim3(kThreads), 0, s, w.xs1,
                            static_cast<const float4 *>(nullptr), w.xs2r, w.cstart2, w.bbox, b1, b2, p1, p2,
-                           m_per_block, w.seedm, w.keys, static_cast<uint8_t *>(nullptr));
+                           m_per_block, w.seedm, w.keys, static_cast<uint32_t *>(nullptr));
     }
 }
 
@@ -1386,14 +1447,14 @@ int launch_fast(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64
                        dim3(kThreads), 0, s, w.xs1, w.bbox, b1, b2, p1, P.chunk1, P.ncand, w.cand);
     hipLaunchKernelGGL(seed_pick_kernel, dim3((unsigned)cdiv(P.pairs, kThreads / 64)), dim3(kThreads), 0, s,
                        w.cand, P.ncand, P.pairs, w.seedm);
-    const dim3 grid2((unsigned)P.pairs, (unsigned)P.nch2);
+    const dim3 grid2((unsigned)P.pairs, (unsigned)P.nch2), gridL((unsigned)P.pairs, (unsigned)P.nchL);
     if (cells)
-        hipLaunchKernelGGL((list_scan_kernel<D, kCellsOk>), grid2, dim3(kThreads), 0, s, w.xs1, x2pts, w.seedm,
-                           static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunk2,
+        hipLaunchKernelGGL((list_scan_kernel<D, kCellsOk>), gridL, dim3(kThreads), 0, s, w.xs1, x2pts, w.seedm,
+                           static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunkL,
                            w.seedmin);
     else
-        hipLaunchKernelGGL((list_scan_kernel<D, false>), grid2, dim3(kThreads), 0, s, w.xs1, x2pts, w.seedm,
-                           static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunk2,
+        hipLaunchKernelGGL((list_scan_kernel<D, false>), gridL, dim3(kThreads), 0, s, w.xs1, x2pts, w.seedm,
+                           static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunkL,
                            w.seedmin);
     hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s,
                        w.seedmin, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, P.pairs, w.keys);
@@ -1465,7 +1526,7 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     add(w.seedmin, pairs * kSeeds, 0x7f800000u, 0x7f800000u);
     add(w.first, 2 * pairs, 0xffffffffu, 0xffffffffu);
     add(w.cursor, P.sort_clouds * kCells, 0u, 0u);
-    add(w.flags, cdiv(P.pairs * p1, 4), 0u, 0u);  // the allocation is rounded up to 256 bytes
+    add(w.flagbits, P.pairs * cdiv(p1, 32), 0u, 0u);
     add(w.survmin, P.pairs * kSurvivors, 0x7f800000u, 0x7f800000u);
     add(w.survcnt, P.pairs, 0u, 0u);
     hipLaunchKernelGGL(fill_kernel, dim3((unsigned)std::min<int64_t>(cdiv(most, 256), 2048)), dim3(256), 0, s, fs);

@@ -600,8 +600,8 @@ __global__ __launch_bounds__(kThreads) void seed_pick_kernel(const unsigned long
 // with cnt, the first min(cnt[pair], K) entries; without, every entry but 0xffffffff (entry 0
 // is then always valid).  Block (pair, y) takes the x2 points [y chunk, (y + 1) chunk) and, eight
 // entries at a time, folds each entry's min over them into lmin[pair][e] (fp32 bits, preset to
-// +inf) with atomicMin.  REC: x2 as cell-sorted records (xs2 then points at them).
-template <int D, bool REC>
+// +inf) with atomicMin.
+template <int D>
 __global__ __launch_bounds__(kThreads) void list_scan_kernel(
     const float *__restrict__ xs1, const float *__restrict__ xs2, const uint32_t *__restrict__ list,
     const uint32_t *__restrict__ cnt, int64_t K, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t chunk,
@@ -610,7 +610,6 @@ __global__ __launch_bounds__(kThreads) void list_scan_kernel(
     __shared__ float red[kThreads / 64][kGroup];
     const int64_t pair = blockIdx.x;
     const PairPtrs P = pair_ptrs(xs1, xs2, pair, b1, b2, p1, p2, D);
-    const float4 *R = REC ? reinterpret_cast<const float4 *>(xs2) + (P.x2 - xs2) / D : nullptr;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t *L = list + pair * K;
     const int64_t n = cnt ? std::min<int64_t>(cnt[pair], K) : K;
@@ -637,14 +636,8 @@ __global__ __launch_bounds__(kThreads) void list_scan_kernel(
                 const int64_t q = q0 + u * kThreads;
                 const bool ok = q < end;
                 const int64_t qq = ok ? q : q0;
-                if constexpr (REC) {
-                    const float4 v = R[qq];
 #pragma unroll
-                    for (int k = 0; k < D; ++k) b[u][k] = rec_coord(v, k);
-                } else {
-#pragma unroll
-                    for (int k = 0; k < D; ++k) b[u][k] = P.x2[k * p2 + qq];
-                }
+                for (int k = 0; k < D; ++k) b[u][k] = P.x2[k * p2 + qq];
                 // a missing point: d = inf or NaN, which fminf passes over
                 b[u][0] = ok ? b[u][0] : INFINITY;
             }
@@ -691,9 +684,8 @@ __global__ void list_fold_kernel(const uint32_t *__restrict__ lmin, const uint32
 
 // Final rescan: block (pair, y) checks the x2 points [y chunk, (y + 1) chunk) against the
 // winning m of the pair's key and folds the first position n whose d equals the min into
-// first[pair] (preset to all ones) with atomicMin.  REC: x2 as cell-sorted records (xs2 then
-// points at them), whose positions are in the records.
-template <int D, bool REC>
+// first[pair] (preset to all ones) with atomicMin.
+template <int D>
 __global__ __launch_bounds__(kThreads) void first_hit_kernel(
     const float *__restrict__ xs1, const float *__restrict__ xs2, const unsigned long long *__restrict__ keys,
     int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t chunk, unsigned long long *__restrict__ first) {
@@ -709,15 +701,6 @@ __global__ __launch_bounds__(kThreads) void first_hit_kernel(
     const int64_t beg = (int64_t)blockIdx.y * chunk;
     const int64_t end = beg + chunk < p2 ? beg + chunk : p2;
     unsigned long long hit = ~0ull;
-    if constexpr (REC) {
-        // sorted order: every point is checked, the smallest position wins
-        const float4 *R = reinterpret_cast<const float4 *>(xs2) + (P.x2 - xs2) / D;
-        for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
-            const float4 v = R[n];
-            const unsigned long long q = rec_pos(v);
-            if (rec_dist<D>(a, v) == H && q < hit) hit = q;
-        }
-    } else {
     int64_t n = beg + threadIdx.x;
     for (; n + 3 * kThreads < end; n += 4 * kThreads) {
         float dd[4];
@@ -730,7 +713,6 @@ __global__ __launch_bounds__(kThreads) void first_hit_kernel(
     }
     for (; n < end && hit == ~0ull; n += kThreads)
         if (sqdist_fixed<D>(a, P.x2, p2, n) == H) hit = (unsigned long long)n;
-    }
     hit = wave_min_u64(hit);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = hit;
     __syncthreads();
@@ -1026,61 +1008,168 @@ __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellS
     }
 }
 
-// The whole wave scans all of x2 (sorted) for one m with coordinates b, circularly from st,
-// four 64-point steps in flight, and drops m at the first d < T; an m never dropped folds its
-// exact min with its iteration position mpos.
+// ---------------------------------------------------------------------------------------
+// Exact nearest-neighbour search over the cell grid, by one wave.  The query's cell c0 (its
+// coordinates clamped into the grid, as cell_of does) is visited first, then the rings of cells
+// at Chebyshev distance R = 1, 2, ... around it.  A cell is scanned only when a lower bound of
+// the squared distance from the query to any point assigned to it is not above the current
+// bound; the search ends at the first ring whose lower bound is above it.  Both bounds are
+// conservative: a point's cell comes from the rounded (x - lo) * scale (off by far less than the
+// 0.01-cell margin taken off every gap), edge cells reach to infinity (clamping), and the bound
+// is scaled by 1 - 2^-12 for the rounding of the computed distances.  Visiting order does not
+// change a min, so the result is that of a scan of all of x2.
+//   kBallPrune: drop the query at the first d < T (returns true); otherwise fold the exact min
+//     with position mpos into key (returns false);
+//   kBallMin: return the exact min (out_min);
+//   kBallFirst: return the smallest position of a point with d == H (all ones if none).
+constexpr int kBallPrune = 0, kBallMin = 1, kBallFirst = 2;
+
 template <int D>
-__device__ __forceinline__ void wave_full_scan(const float (&b)[D], const float4 *X2, int64_t p2, int64_t st,
-                                               unsigned long long *key, int64_t mpos) {
-    const int lane = threadIdx.x & 63;
-    float T = threshold_of(key);
-    float best = INFINITY;
-    int64_t t0 = 0;
-    for (; t0 + 256 <= p2; t0 += 256) {
-        float dd[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            int64_t n = st + t0 + 64 * u + lane;
-            if (n >= p2) n -= p2;
-            dd[u] = rec_dist<D>(b, X2[n]);
+__device__ __forceinline__ constexpr int grid_side() { return D == 3 ? 16 : D == 2 ? 64 : 4096; }
+
+// Offsets of cell t of ring R (0 <= t < ring_count(R)) around the query's cell.
+template <int D>
+__device__ __forceinline__ int64_t ring_count(int R) {
+    if (R == 0) return 1;
+    if constexpr (D == 1) return 2;
+    else if constexpr (D == 2) return 8 * (int64_t)R;
+    else return 24 * (int64_t)R * R + 2;
+}
+template <int D>
+__device__ __forceinline__ void ring_cell(int R, int64_t t, int (&o)[D]) {
+    if constexpr (D == 1) {
+        o[0] = R == 0 ? 0 : (t == 0 ? -R : R);
+    } else if constexpr (D == 2) {
+        const int S = 2 * R + 1;
+        if (R == 0) {
+            o[0] = o[1] = 0;
+        } else if (t < 2 * S) {  // bottom and top rows
+            o[0] = (int)(t % S) - R;
+            o[1] = t < S ? -R : R;
+        } else {                 // left and right columns without the corners
+            const int64_t u = t - 2 * S;
+            o[0] = u < S - 2 ? -R : R;
+            o[1] = (int)(u % (S - 2)) - (R - 1);
         }
-        const float dmin = fminf(fminf(dd[0], dd[1]), fminf(dd[2], dd[3]));
-        if (__any(dmin < T)) return;
-        best = fminf(best, dmin);
-        if ((t0 & 4095) == 3840) T = threshold_of(key);
+    } else {
+        const int S = 2 * R + 1;
+        if (R == 0) {
+            o[0] = o[1] = o[2] = 0;
+        } else if (t < 2 * (int64_t)S * S) {  // faces z = -R, +R
+            const int64_t r = t % ((int64_t)S * S);
+            o[0] = (int)(r % S) - R;
+            o[1] = (int)(r / S) - R;
+            o[2] = t < (int64_t)S * S ? -R : R;
+        } else if (t < 2 * (int64_t)S * S + 2 * (int64_t)S * (S - 2)) {  // faces y = -R, +R, |z| < R
+            const int64_t u = t - 2 * (int64_t)S * S;
+            const int64_t r = u % ((int64_t)S * (S - 2));
+            o[0] = (int)(r % S) - R;
+            o[1] = u < (int64_t)S * (S - 2) ? -R : R;
+            o[2] = (int)(r / S) - (R - 1);
+        } else {  // faces x = -R, +R, |y|, |z| < R
+            const int64_t u = t - 2 * (int64_t)S * S - 2 * (int64_t)S * (S - 2);
+            const int64_t r = u % ((int64_t)(S - 2) * (S - 2));
+            o[0] = u < (int64_t)(S - 2) * (S - 2) ? -R : R;
+            o[1] = (int)(r % (S - 2)) - (R - 1);
+            o[2] = (int)(r / (S - 2)) - (R - 1);
+        }
     }
-    for (; t0 < p2; t0 += 64) {
-        const int64_t t = t0 + lane;
-        int64_t n = st + t;
-        if (n >= p2) n -= p2;
-        const float dd = t < p2 ? rec_dist<D>(b, X2[n]) : INFINITY;
-        if (__any(dd < T)) return;
-        best = fminf(best, dd);
-    }
-    const float mn = wave_min(best);
-    if (lane == 0) fold_key(key, mn, mpos);
 }
 
-// Whether the whole wave, scanning `budget` points (a multiple of 256, below p2) of the sorted
-// x2 circularly from st, meets a d < T for the point b (the same answer in every lane).
-template <int D>
-__device__ __forceinline__ bool wave_scan_prunes(const float (&b)[D], const float4 *X2, int64_t p2, int64_t st,
-                                                 const unsigned long long *key, int64_t budget) {
+template <int D, int MODE>
+__device__ unsigned long long wave_ball_query(const float (&q)[D], const float4 *X2, const int32_t *CS,
+                                              const float (&fr)[2 * D], float T, unsigned long long *key,
+                                              int64_t mpos, float *out_min) {
+    constexpr int G = grid_side<D>();
+    constexpr float kMargin = 0.01f, kShrink = 1.0f - 0x1p-12f;
     const int lane = threadIdx.x & 63;
-    float T = threshold_of(key);
-    for (int64_t t0 = 0; t0 < budget; t0 += 256) {
-        float dd[4];
+    float f[D], inv[D];
+    int c0[D];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            int64_t n = st + t0 + 64 * u + lane;
-            if (n >= p2) n -= p2;
-            dd[u] = rec_dist<D>(b, X2[n]);
-        }
-        const float dmin = fminf(fminf(dd[0], dd[1]), fminf(dd[2], dd[3]));
-        if (__any(dmin < T)) return true;
-        if ((t0 & 1023) == 768) T = threshold_of(key);
+    for (int k = 0; k < D; ++k) {
+        f[k] = (q[k] - fr[2 * k]) * fr[2 * k + 1];
+        c0[k] = (int)fminf(fmaxf(f[k], 0.0f), (float)(G - 1));
+        inv[k] = fr[2 * k + 1] > 0.0f ? 1.0f / fr[2 * k + 1] : 0.0f;  // 0: one cell along k
     }
-    return false;
+    float best = INFINITY;                 // per lane, then wave-wide at each ring
+    unsigned long long first = ~0ull;      // kBallFirst
+    const float bound0 = MODE == kBallFirst ? T : INFINITY;
+    for (int R = 0; R < G; ++R) {
+        float bound = MODE == kBallFirst ? bound0 : wave_min(best);
+        if (R > 0) {
+            // every cell of ring R (and beyond) is at least R - 1 cells away along some axis
+            float lb = INFINITY;
+            bool inside = false;
+#pragma unroll
+            for (int k = 0; k < D; ++k) {
+                if (inv[k] > 0.0f) {
+                    const float g = fmaxf((float)(R - 1) - kMargin, 0.0f) * inv[k];
+                    lb = fminf(lb, g * g);
+                }
+                inside = inside || c0[k] - R >= 0 || c0[k] + R <= G - 1;
+            }
+            if (!inside) break;  // the ring lies outside the grid, and so do the later ones
+            if (lb * kShrink > bound) break;
+        }
+        const int64_t count = ring_count<D>(R);
+        for (int64_t t0 = 0; t0 < count; t0 += 64) {
+            const int64_t t = t0 + lane;
+            int cell = -1;
+            if (t < count) {
+                int o[D];
+                ring_cell<D>(R, t, o);
+                bool in = true;
+                float lbc = 0.0f;
+                uint32_t morton = 0;
+#pragma unroll
+                for (int k = 0; k < D; ++k) {
+                    const int c = c0[k] + o[k];
+                    in = in && c >= 0 && c <= G - 1;
+                    const float lo = c == 0 ? -INFINITY : (float)c;
+                    const float hi = c == G - 1 ? INFINITY : (float)(c + 1);
+                    const float gap = fmaxf(fmaxf(lo - f[k], f[k] - hi) - kMargin, 0.0f) * inv[k];
+                    lbc = lbc + gap * gap;
+                    const uint32_t u = (uint32_t)(c < 0 ? 0 : c > G - 1 ? G - 1 : c);  // used only in grid
+                    if constexpr (D == 1) morton = u;
+                    else morton |= spread_bits<D>(u) << k;
+                }
+                if (in && !(lbc * kShrink > bound) && CS[morton + 1] > CS[morton]) cell = (int)morton;
+            }
+            unsigned long long cand = __ballot(cell >= 0);
+            while (cand) {
+                const int l = __builtin_ctzll(cand);
+                cand &= cand - 1;
+                const int cl = __builtin_amdgcn_readlane(cell, l);
+                const int64_t s = CS[cl], e = CS[cl + 1];
+                for (int64_t n0 = s; n0 < e; n0 += 64) {
+                    const int64_t n = n0 + lane;
+                    const bool ok = n < e;
+                    const float4 v = X2[ok ? n : s];
+                    const float d = ok ? rec_dist<D>(q, v) : INFINITY;
+                    if constexpr (MODE == kBallPrune) {
+                        if (__any(d < T)) return 1ull;
+                    }
+                    if constexpr (MODE == kBallFirst) {
+                        const unsigned long long pos = rec_pos(v);
+                        if (ok && d == T && pos < first) first = pos;
+                    } else {
+                        best = fminf(best, d);
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (MODE == kBallFirst) {
+        return wave_min_u64(first);
+    } else {
+        const float mn = wave_min(best);
+        if constexpr (MODE == kBallPrune) {
+            if (lane == 0) fold_key(key, mn, mpos);
+        } else {
+            *out_min = mn;
+        }
+        return 0ull;
+    }
 }
 
 // Start of m's 64-point window in the sorted x2 of a cloud: its cell's first point, clamped to
@@ -1101,7 +1190,7 @@ __device__ __forceinline__ int64_t window_start(const float (&a)[D], const float
 //     so the loads coalesce; a lane left sets bit m position of its pair's flag bits (preset
 //     to 0), and scan_flagged_kernel scans those m in iteration order.
 //   otherwise (x1 in iteration order, x2 sorted in its cloud's own frame): the lanes left
-//     (ballot) are scanned in turn by the whole wave (wave_full_scan).
+//     (ballot) are taken in turn by the whole wave through a ball query.
 template <int D, bool SORTED>
 __global__ __launch_bounds__(kThreads) void scan_window_kernel(
     const float *__restrict__ xs1, const float4 *__restrict__ xs1r, const float4 *__restrict__ xs2r,
@@ -1184,8 +1273,8 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
 #pragma unroll
                     for (int k = 0; k < D; ++k)
                         b[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[g][k]), l));
-                    const int64_t st = (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)s0[g], l);
-                    wave_full_scan<D>(b, X2, p2, st, key, m0 + g * kThreads + l);
+                    wave_ball_query<D, kBallPrune>(b, X2, CS, fr, threshold_of(key), key, m0 + g * kThreads + l,
+                                                   nullptr);
                 }
             }
         }
@@ -1193,23 +1282,13 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
 }
 
 // The m the window pass of the sorted mode left (flag bits), in iteration order: block =
-// 256 words = 8192 m of one pair, each lane one word; the flagged m are scanned in turn by their
-// wave, `budget` points from the window's start (or all of x2, when that is no more, folding the
-// exact min).  An m still not dropped after its budget is a survivor: its exact min needs all
-// of x2, which one wave would take a long serial time over, so it goes to survm[pair] for
-// list_scan_kernel, which spreads it over many blocks.  A wave keeps its survivors in LDS (kept
-// by lane 0, counted alike in every lane); the block reserves slots with one atomicAdd on
-// survcnt[pair], handed to the waves through LDS after a barrier.  Survivors beyond a wave's
-// LDS list or beyond K slots are scanned here in full.
+// 256 words = 8192 m of one pair, each lane one word; each flagged m is taken by its whole wave
+// through an exact ball query (dropped at the first d < T, or folded with its exact min).
 template <int D>
 __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
     const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
-    const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t budget,
-    unsigned long long *__restrict__ keys, const uint32_t *__restrict__ flagbits, uint32_t *__restrict__ survm,
-    uint32_t *__restrict__ survcnt, int64_t K) {
-    constexpr int kWaveList = 32;
-    __shared__ uint32_t wl[kThreads / 64][kWaveList];
-    __shared__ uint32_t wn[kThreads / 64], wb[kThreads / 64];
+    const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
+    unsigned long long *__restrict__ keys, const uint32_t *__restrict__ flagbits) {
     const int64_t pair = blockIdx.y;
     const int64_t per_batch = b1 * b2;
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
@@ -1219,15 +1298,12 @@ __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
     const int32_t *CS = cstart2 + (bb * b2 + j) * (kCells + 1);
     float fr[2 * D];
     frame_of<D>(boxes + bb * D * 2, fr);
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
     unsigned long long *key = &keys[pair];
     const int64_t fwords = cdiv_dev(p1, 32);
     const int64_t wi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     const uint32_t word = wi < fwords ? flagbits[pair * fwords + wi] : 0u;
-    const int64_t wbase = ((int64_t)blockIdx.x * kThreads + 64 * __builtin_amdgcn_readfirstlane(wave)) * 32;
+    const int64_t wbase = ((int64_t)blockIdx.x * kThreads + 64 * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * 32;
     unsigned long long left = __ballot(word != 0u);
-    uint32_t nsurv = 0;  // the same in every lane
     while (left) {
         const int l = __builtin_ctzll(left);
         left &= left - 1;
@@ -1239,46 +1315,62 @@ __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
             float b[D];
 #pragma unroll
             for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + mm];
-            const int64_t st = window_start<D>(b, fr, CS, p2);
-            if (p2 <= budget) {
-                wave_full_scan<D>(b, X2, p2, st, key, mm);
-            } else if (!wave_scan_prunes<D>(b, X2, p2, st, key, budget)) {
-                if (nsurv < kWaveList) {
-                    if (lane == 0) wl[wave][nsurv] = (uint32_t)mm;
-                } else {
-                    wave_full_scan<D>(b, X2, p2, st, key, mm);
-                }
-                ++nsurv;
-            }
+            wave_ball_query<D, kBallPrune>(b, X2, CS, fr, threshold_of(key), key, mm, nullptr);
         }
     }
-    const uint32_t mine_n = nsurv < kWaveList ? nsurv : kWaveList;
-    if (lane == 0) wn[wave] = mine_n;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t tot = 0;
-        for (int w = 0; w < kThreads / 64; ++w) tot += wn[w];
-        uint32_t base = tot ? atomicAdd(&survcnt[pair], tot) : 0u;
-        for (int w = 0; w < kThreads / 64; ++w) {
-            wb[w] = base;
-            base += wn[w];
-        }
-    }
-    __syncthreads();
-    const bool have = (uint32_t)lane < wn[wave];
-    const int64_t slot = (int64_t)wb[wave] + lane;
-    const uint32_t mm = have ? wl[wave][lane] : 0u;
-    if (have && slot < K) survm[pair * K + slot] = mm;
-    unsigned long long over = __ballot(have && slot >= K);
-    while (over) {
-        const int l = __builtin_ctzll(over);
-        over &= over - 1;
-        const int64_t ml = (uint32_t)__builtin_amdgcn_readlane((int)mm, l);
-        float b[D];
+}
+
+// Seeds on the cell grid: one wave per (pair, seed) finds the seed's exact min with a ball
+// query and folds it into the pair's key.
+template <int D>
+__global__ __launch_bounds__(kThreads) void seed_ball_kernel(
+    const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
+    const float *__restrict__ boxes, bool batch_frame, const uint32_t *__restrict__ seedm, int64_t b1, int64_t b2,
+    int64_t p1, int64_t p2, int64_t pairs, unsigned long long *__restrict__ keys) {
+    const int64_t t = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (t >= pairs * kSeeds) return;  // the same in every lane
+    const int64_t pair = t / kSeeds;
+    const uint32_t m = seedm[t];
+    if (m == 0xffffffffu) return;
+    const int64_t per_batch = b1 * b2;
+    const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
+    const int64_t i = rem / b2, j = rem - i * b2;
+    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
+    float fr[2 * D];
+    frame_of<D>(boxes + (batch_frame ? bb : bb * b2 + j) * D * 2, fr);
+    float q[D];
 #pragma unroll
-        for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + ml];
-        wave_full_scan<D>(b, X2, p2, window_start<D>(b, fr, CS, p2), key, ml);
-    }
+    for (int k = 0; k < D; ++k) q[k] = X1[k * p1 + m];
+    float mn = INFINITY;
+    wave_ball_query<D, kBallMin>(q, xs2r + (bb * b2 + j) * p2, cstart2 + (bb * b2 + j) * (kCells + 1), fr, 0.0f,
+                                 nullptr, 0, &mn);
+    if ((threadIdx.x & 63) == 0) fold_key(&keys[pair], mn, m);
+}
+
+// Final rescan on the cell grid: one wave per pair finds the smallest position of an x2 point
+// at the winning m's min with a ball query.
+template <int D>
+__global__ __launch_bounds__(kThreads) void first_ball_kernel(
+    const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
+    const float *__restrict__ boxes, bool batch_frame, const unsigned long long *__restrict__ keys, int64_t b1,
+    int64_t b2, int64_t p1, int64_t p2, int64_t pairs, unsigned long long *__restrict__ first) {
+    const int64_t pair = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (pair >= pairs) return;  // the same in every lane
+    const int64_t per_batch = b1 * b2;
+    const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
+    const int64_t i = rem / b2, j = rem - i * b2;
+    const unsigned long long key = keys[pair];
+    const int64_t m = (int64_t)(key & 0xffffffffull);
+    const float H = __uint_as_float((uint32_t)(key >> 32));
+    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
+    float fr[2 * D];
+    frame_of<D>(boxes + (batch_frame ? bb : bb * b2 + j) * D * 2, fr);
+    float q[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) q[k] = X1[k * p1 + m];
+    const unsigned long long n = wave_ball_query<D, kBallFirst>(
+        q, xs2r + (bb * b2 + j) * p2, cstart2 + (bb * b2 + j) * (kCells + 1), fr, H, nullptr, 0, nullptr);
+    if ((threadIdx.x & 63) == 0) first[pair] = n;
 }
 
 // The sorted mode keeps one flag bit per (pair, m): up to 32 MiB of them.
@@ -1334,25 +1426,20 @@ Plan make_plan(int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, in
     return P;
 }
 
-// Survivor slots per pair (full scans spread over blocks) in the sorted mode.
-constexpr int64_t kSurvivors = 64;
-// Points the flagged pass scans for an m before it counts as a survivor.
-constexpr int64_t kBudget = 2048;
-
 struct Workspace {
     float *xs1, *xs2, *bbox, *bbox1, *boxb;
     float4 *xs2r, *xs1r;
     unsigned long long *keys, *cand, *first;
     int32_t *cstart2;
     int *boxkeys;
-    uint32_t *seedmin, *seedm, *cursor, *survm, *survmin, *survcnt;
+    uint32_t *seedmin, *seedm, *cursor;
     uint32_t *flagbits;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // [keys | x2 boxes | x1 SoA | x2 SoA | box keys | seeds, candidates, first hits (fast) |
-//  x2 records, x2 cell starts (cells) | x1 boxes, batch boxes, x1 records, flag bits, survivors
+//  x2 records, x2 cell starts (cells) | x1 boxes, batch boxes, x1 records, flag bits
 //  (sorted) | sort cursors (multi_sort)]
 Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
@@ -1377,9 +1464,6 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
     w.boxb = reinterpret_cast<float *>(take(P.sorted, 4 * P.batch * d * 2));
     w.xs1r = reinterpret_cast<float4 *>(take(P.sorted, 16 * P.clouds1 * p1));
     w.flagbits = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * cdiv(p1, 32)));
-    w.survm = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * kSurvivors));
-    w.survmin = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * kSurvivors));
-    w.survcnt = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs));
     w.cursor = reinterpret_cast<uint32_t *>(take(P.multi_sort, 4 * P.sort_clouds * kCells));
     if (total) *total = (size_t)(p - base);
     return w;
@@ -1405,8 +1489,7 @@ void launch_sort(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int6
     }
 }
 
-// The cell-sorted scan (d <= 3): window pass, then, in the sorted mode, the flagged m and the
-// survivors' full scans.
+// The cell-sorted scan (d <= 3): window pass, then, in the sorted mode, the flagged m.
 template <int D>
 void launch_cell_scan(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
                       hipStream_t s) {
@@ -1417,14 +1500,8 @@ void launch_cell_scan(const Plan &P, const Workspace &w, int64_t b1, int64_t p1,
                            static_cast<const float *>(nullptr), w.xs1r, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2,
                            m_per_block, w.seedm, w.keys, w.flagbits);
         hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, 32 * kThreads), (unsigned)P.pairs),
-                           dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2, kBudget, w.keys,
-                           w.flagbits, w.survm, w.survcnt, kSurvivors);
-        // survivors: counts vary by pair, so small blocks keep the slow pairs spread out
-        hipLaunchKernelGGL((list_scan_kernel<D, true>), dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads),
-                           0, s, w.xs1, reinterpret_cast<const float *>(w.xs2r), w.survm, w.survcnt, kSurvivors,
-                           b1, b2, p1, p2, P.chunk2, w.survmin);
-        hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSurvivors, 256)), dim3(256), 0, s,
-                           w.survmin, w.survm, w.survcnt, kSurvivors, P.pairs, w.keys);
+                           dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2, w.keys,
+                           w.flagbits);
     } else {
         hipLaunchKernelGGL((scan_window_kernel<D, false>), grid, dim3(kThreads), 0, s, w.xs1,
                            static_cast<const float4 *>(nullptr), w.xs2r, w.cstart2, w.bbox, b1, b2, p1, p2,
@@ -1439,29 +1516,37 @@ int launch_fast(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64
                 hipStream_t s) {
     constexpr bool kCellsOk = D <= 3;
     const bool cells = kCellsOk && P.cells;
+    const float *frames = P.sorted ? w.boxb : w.bbox;
+    const unsigned per_wave_blocks = (unsigned)cdiv(P.pairs, kThreads / 64);
     if constexpr (kCellsOk) {
         if (cells) launch_sort<D>(P, w, b1, p1, b2, p2, s);
     }
-    const float *x2pts = cells ? reinterpret_cast<const float *>(w.xs2r) : w.xs2;
     hipLaunchKernelGGL(seed_select_kernel<D>, dim3((unsigned)P.pairs, (unsigned)cdiv(p1, P.chunk1)),
                        dim3(kThreads), 0, s, w.xs1, w.bbox, b1, b2, p1, P.chunk1, P.ncand, w.cand);
-    hipLaunchKernelGGL(seed_pick_kernel, dim3((unsigned)cdiv(P.pairs, kThreads / 64)), dim3(kThreads), 0, s,
-                       w.cand, P.ncand, P.pairs, w.seedm);
-    const dim3 grid2((unsigned)P.pairs, (unsigned)P.nch2), gridL((unsigned)P.pairs, (unsigned)P.nchL);
-    if (cells)
-        hipLaunchKernelGGL((list_scan_kernel<D, kCellsOk>), gridL, dim3(kThreads), 0, s, w.xs1, x2pts, w.seedm,
-                           static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunkL,
-                           w.seedmin);
-    else
-        hipLaunchKernelGGL((list_scan_kernel<D, false>), gridL, dim3(kThreads), 0, s, w.xs1, x2pts, w.seedm,
-                           static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunkL,
-                           w.seedmin);
-    hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s,
-                       w.seedmin, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, P.pairs, w.keys);
+    hipLaunchKernelGGL(seed_pick_kernel, dim3(per_wave_blocks), dim3(kThreads), 0, s, w.cand, P.ncand, P.pairs,
+                       w.seedm);
+    if constexpr (kCellsOk) {
+        if (cells)
+            hipLaunchKernelGGL(seed_ball_kernel<D>, dim3((unsigned)cdiv(P.pairs * kSeeds, kThreads / 64)),
+                               dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, frames, P.sorted, w.seedm, b1, b2, p1,
+                               p2, P.pairs, w.keys);
+    }
+    if (!cells) {
+        hipLaunchKernelGGL(list_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nchL), dim3(kThreads), 0, s,
+                           w.xs1, w.xs2, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2,
+                           p1, p2, P.chunkL, w.seedmin);
+        hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s,
+                           w.seedmin, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, P.pairs,
+                           w.keys);
+    }
     int rc = check_launch("hausdorff seeds");
     if (rc) return rc;
     if constexpr (kCellsOk) {
-        if (cells) launch_cell_scan<D>(P, w, b1, p1, b2, p2, s);
+        if (cells) {
+            launch_cell_scan<D>(P, w, b1, p1, b2, p2, s);
+            hipLaunchKernelGGL(first_ball_kernel<D>, dim3(per_wave_blocks), dim3(kThreads), 0, s, w.xs1, w.xs2r,
+                               w.cstart2, frames, P.sorted, w.keys, b1, b2, p1, p2, P.pairs, w.first);
+        }
     }
     if (!cells) {
         const int64_t m_per_block = 2048;
@@ -1469,15 +1554,11 @@ int launch_fast(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64
         hipLaunchKernelGGL(scan_kernel<D>, dim3((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs),
                            dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.seedm,
                            w.keys);
+        hipLaunchKernelGGL(first_hit_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
+                           w.xs1, w.xs2, w.keys, b1, b2, p1, p2, P.chunk2, w.first);
     }
     rc = check_launch("hausdorff scan");
     if (rc) return rc;
-    if (cells)
-        hipLaunchKernelGGL((first_hit_kernel<D, kCellsOk>), grid2, dim3(kThreads), 0, s, w.xs1, x2pts, w.keys, b1,
-                           b2, p1, p2, P.chunk2, w.first);
-    else
-        hipLaunchKernelGGL((first_hit_kernel<D, false>), grid2, dim3(kThreads), 0, s, w.xs1, x2pts, w.keys, b1,
-                           b2, p1, p2, P.chunk2, w.first);
     hipLaunchKernelGGL(write_out_kernel, dim3((unsigned)cdiv(P.pairs, 256)), dim3(256), 0, s, w.keys, w.first,
                        perm1, perm2, P.pairs, b1, b2, p1, p2, out, idx1, idx2);
     return check_launch("hausdorff final rescan");
@@ -1512,8 +1593,8 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     hipStream_t s = as_stream(stream);
     const Plan P = make_plan(batch, b1, p1, b2, p2, d);
     const Workspace w = carve(workspace, P, p1, p2, d);
-    // presets: keys 0, box keys (+inf, -inf), seed and survivor mins +inf, first hits all ones,
-    // cursors, flags and survivor counts 0
+    // presets: keys 0, box keys (+inf, -inf), seed mins +inf, first hits all ones, cursors and
+    // flags 0
     Fills fs{};
     int64_t most = 0;
     auto add = [&](void *ptr, int64_t words, uint32_t v0, uint32_t v1) {
@@ -1527,8 +1608,6 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     add(w.first, 2 * pairs, 0xffffffffu, 0xffffffffu);
     add(w.cursor, P.sort_clouds * kCells, 0u, 0u);
     add(w.flagbits, P.pairs * cdiv(p1, 32), 0u, 0u);
-    add(w.survmin, P.pairs * kSurvivors, 0x7f800000u, 0x7f800000u);
-    add(w.survcnt, P.pairs, 0u, 0u);
     hipLaunchKernelGGL(fill_kernel, dim3((unsigned)std::min<int64_t>(cdiv(most, 256), 2048)), dim3(256), 0, s, fs);
     int rc = check_launch("hausdorff presets");
     if (rc) return rc;

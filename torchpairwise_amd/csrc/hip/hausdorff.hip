@@ -895,17 +895,18 @@ __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__rest
 }
 
 // The same counting sort spread over many blocks per cloud, for runs with few clouds (one
-// block per cloud would leave most CUs idle).  Clouds [0, A.clouds) come from A, the rest from
-// B; cursor[cloud][cell] (preset to 0) first counts, then holds each cell's next free slot.
-//   cell_count: block (cloud, y) histograms points [y chunk, (y + 1) chunk) in LDS and adds
-//     the non-zero bins to cursor;
-//   cell_scan: one block per cloud turns the counts into start offsets (and cstart);
-//   cell_scatter: block (cloud, y) histograms its points again, reserves a range of each
-//     cell's slots with one atomicAdd per non-zero bin, and writes its points into it.
+// block per cloud would leave most CUs idle), with no global atomics.  Clouds [0, A.clouds)
+// come from A, the rest from B; hist[cloud][chunk][cell] holds each chunk's histogram and then
+// its first slot in every cell.
+//   cell_count: block (cloud, y) histograms points [y chunk, (y + 1) chunk) in LDS and writes
+//     it out;
+//   cell_prefix / cell_start: per cell, the counts of the earlier chunks; per cloud, the cell
+//     starts (starts[cloud], the x2 clouds' being their cstart);
+//   cell_scatter: block (cloud, y) starts each cell at start + earlier chunks' count and writes
+//     its points, the slot within a cell taken with an LDS atomicAdd.
 struct CellSet {
     const float *xs;      // [clouds][D][p]
     float4 *rec;          // [clouds][p] records
-    int32_t *cstart;      // [clouds][kCells + 1] cell starts, or null
     const float *boxes;   // frames, [clouds / clouds_per_box][D][2]
     int64_t clouds, p, clouds_per_box;
 };
@@ -926,36 +927,53 @@ __device__ __forceinline__ void chunk_histogram(const CellSet &S, int64_t c, int
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void cell_count_kernel(CellSet A, CellSet B, int64_t chunk,
-                                                              uint32_t *__restrict__ cursor) {
+__global__ __launch_bounds__(kThreads) void cell_count_kernel(CellSet A, CellSet B, int64_t chunk, int64_t chunks,
+                                                              uint32_t *__restrict__ hist_out) {
     __shared__ uint32_t hist[kCells];
     const int64_t g = blockIdx.x;
     const bool inA = g < A.clouds;
     const CellSet &S = inA ? A : B;
     const int64_t c = inA ? g : g - A.clouds;
     const int64_t beg = (int64_t)blockIdx.y * chunk;
-    if (beg >= S.p) return;  // the same for the whole block
-    const int64_t end = beg + chunk < S.p ? beg + chunk : S.p;
+    const int64_t end = beg + chunk < S.p ? beg + chunk : S.p;  // empty when beg >= p
     float fr[2 * D];
     frame_of<D>(S.boxes + (c / S.clouds_per_box) * D * 2, fr);
     chunk_histogram<D>(S, c, beg, end, fr, hist);
-    for (int t = threadIdx.x; t < kCells; t += kThreads)
-        if (hist[t]) atomicAdd(&cursor[g * kCells + t], hist[t]);
+    uint32_t *H = hist_out + (g * chunks + blockIdx.y) * kCells;
+    for (int t = threadIdx.x; t < kCells; t += kThreads) H[t] = hist[t];
 }
 
-__global__ __launch_bounds__(kThreads) void cell_scan_kernel(CellSet A, CellSet B, uint32_t *__restrict__ cursor) {
+// One thread per (cloud, cell): the counts of the earlier chunks in the cell replace each
+// chunk's count, and the cell's total goes to totals[cloud][cell].
+__global__ __launch_bounds__(kThreads) void cell_prefix_kernel(int64_t chunks, uint32_t *__restrict__ hist,
+                                                               uint32_t *__restrict__ totals) {
+    const int64_t g = blockIdx.x;
+    const int cell = blockIdx.y * kThreads + threadIdx.x;
+    uint32_t *H = hist + g * chunks * kCells + cell;
+    uint32_t run = 0;
+    for (int64_t y = 0; y < chunks; ++y) {
+        const uint32_t n = H[y * kCells];
+        H[y * kCells] = run;
+        run += n;
+    }
+    totals[g * kCells + cell] = run;
+}
+
+// One block per cloud: starts[cloud][cell] = exclusive scan of the cell totals, and
+// starts[cloud][kCells] = p.
+__global__ __launch_bounds__(kThreads) void cell_start_kernel(CellSet A, CellSet B,
+                                                              const uint32_t *__restrict__ totals,
+                                                              int32_t *__restrict__ starts) {
     __shared__ uint32_t part[kThreads];
     const int64_t g = blockIdx.x;
-    const bool inA = g < A.clouds;
-    const CellSet &S = inA ? A : B;
-    const int64_t c = inA ? g : g - A.clouds;
-    uint32_t *cnt = cursor + g * kCells;
+    const CellSet &S = g < A.clouds ? A : B;
+    const uint32_t *Tc = totals + g * kCells;
     constexpr int kPer = kCells / kThreads;  // 16 consecutive cells per thread
     uint32_t v[kPer];
     uint32_t local = 0;
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-        v[e] = cnt[threadIdx.x * kPer + e];
+        v[e] = Tc[threadIdx.x * kPer + e];
         local += v[e];
     }
     part[threadIdx.x] = local;
@@ -970,20 +988,20 @@ __global__ __launch_bounds__(kThreads) void cell_scan_kernel(CellSet A, CellSet 
     }
     __syncthreads();
     uint32_t run = part[threadIdx.x];
+    int32_t *St = starts + g * (kCells + 1);
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-        const int cell = threadIdx.x * kPer + e;
-        cnt[cell] = run;
-        if (S.cstart) S.cstart[c * (kCells + 1) + cell] = (int32_t)run;
+        St[threadIdx.x * kPer + e] = (int32_t)run;
         run += v[e];
     }
-    if (S.cstart && threadIdx.x == 0) S.cstart[c * (kCells + 1) + kCells] = (int32_t)S.p;
+    if (threadIdx.x == 0) St[kCells] = (int32_t)S.p;
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellSet B, int64_t chunk,
-                                                                uint32_t *__restrict__ cursor) {
-    __shared__ uint32_t hist[kCells];
+__global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellSet B, int64_t chunk, int64_t chunks,
+                                                                const uint32_t *__restrict__ slots,
+                                                                const int32_t *__restrict__ starts) {
+    __shared__ uint32_t next[kCells];
     const int64_t g = blockIdx.x;
     const bool inA = g < A.clouds;
     const CellSet &S = inA ? A : B;
@@ -993,9 +1011,9 @@ __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellS
     const int64_t end = beg + chunk < S.p ? beg + chunk : S.p;
     float fr[2 * D];
     frame_of<D>(S.boxes + (c / S.clouds_per_box) * D * 2, fr);
-    chunk_histogram<D>(S, c, beg, end, fr, hist);
-    for (int t = threadIdx.x; t < kCells; t += kThreads)
-        if (hist[t]) hist[t] = atomicAdd(&cursor[g * kCells + t], hist[t]);
+    const uint32_t *H = slots + (g * chunks + blockIdx.y) * kCells;
+    const int32_t *St = starts + g * (kCells + 1);
+    for (int t = threadIdx.x; t < kCells; t += kThreads) next[t] = (uint32_t)St[t] + H[t];
     __syncthreads();
     const float *X = S.xs + c * D * S.p;
     float4 *O = S.rec + c * S.p;
@@ -1003,7 +1021,7 @@ __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellS
         float a[D];
 #pragma unroll
         for (int k = 0; k < D; ++k) a[k] = X[k * S.p + n];
-        const uint32_t slot = atomicAdd(&hist[cell_of<D>(a, fr)], 1u);
+        const uint32_t slot = atomicAdd(&next[cell_of<D>(a, fr)], 1u);
         O[slot] = make_rec<D>(a, (uint32_t)n);
     }
 }
@@ -1418,9 +1436,12 @@ Plan make_plan(int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, in
     P.nchL = cdiv(p2, P.chunkL);
     if (P.cells) {
         P.sort_clouds = P.clouds2 + (P.sorted ? P.clouds1 : 0);
-        P.multi_sort = P.sort_clouds <= 2048;  // cursor <= 32 MiB
+        P.multi_sort = P.sort_clouds <= 2048;
+        // chunks of >= 4096 points, at most 4096 (cloud, chunk) histograms (64 MiB)
         const int64_t psort = P.sorted && p1 > p2 ? p1 : p2;
-        P.sort_chunk = std::max<int64_t>(4096, round_up(cdiv(psort, kMaxGridYZ), kThreads));
+        const int64_t most = std::max<int64_t>(1, 4096 / std::max<int64_t>(1, P.sort_clouds));
+        P.sort_chunks = std::min<int64_t>(cdiv(psort, 4096), most);
+        P.sort_chunk = round_up(cdiv(psort, P.sort_chunks), kThreads);
         P.sort_chunks = cdiv(psort, P.sort_chunk);
     }
     return P;
@@ -1432,7 +1453,7 @@ struct Workspace {
     unsigned long long *keys, *cand, *first;
     int32_t *cstart2;
     int *boxkeys;
-    uint32_t *seedmin, *seedm, *cursor;
+    uint32_t *seedmin, *seedm, *cellhist, *celltot;
     uint32_t *flagbits;
 };
 
@@ -1440,7 +1461,7 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // [keys | x2 boxes | x1 SoA | x2 SoA | box keys | seeds, candidates, first hits (fast) |
 //  x2 records, x2 cell starts (cells) | x1 boxes, batch boxes, x1 records, flag bits
-//  (sorted) | sort cursors (multi_sort)]
+//  (sorted) | per-chunk cell histograms (multi_sort)]
 Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
     auto take = [&](bool on, size_t bytes) {
@@ -1459,12 +1480,15 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
     w.cand = reinterpret_cast<unsigned long long *>(take(P.fast, 8 * P.pairs * P.ncand));
     w.first = reinterpret_cast<unsigned long long *>(take(P.fast, 8 * P.pairs));
     w.xs2r = reinterpret_cast<float4 *>(take(P.cells, 16 * P.clouds2 * p2));
-    w.cstart2 = reinterpret_cast<int32_t *>(take(P.cells, 4 * P.clouds2 * (kCells + 1)));
+    // multi_sort: cell starts of every sorted cloud, x2's first (they are x2's cstart)
+    w.cstart2 = reinterpret_cast<int32_t *>(
+        take(P.cells, 4 * (P.multi_sort ? P.sort_clouds : P.clouds2) * (kCells + 1)));
     w.bbox1 = reinterpret_cast<float *>(take(P.sorted, 4 * P.clouds1 * d * 2));
     w.boxb = reinterpret_cast<float *>(take(P.sorted, 4 * P.batch * d * 2));
     w.xs1r = reinterpret_cast<float4 *>(take(P.sorted, 16 * P.clouds1 * p1));
     w.flagbits = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * cdiv(p1, 32)));
-    w.cursor = reinterpret_cast<uint32_t *>(take(P.multi_sort, 4 * P.sort_clouds * kCells));
+    w.cellhist = reinterpret_cast<uint32_t *>(take(P.multi_sort, 4 * P.sort_clouds * P.sort_chunks * kCells));
+    w.celltot = reinterpret_cast<uint32_t *>(take(P.multi_sort, 4 * P.sort_clouds * kCells));
     if (total) *total = (size_t)(p - base);
     return w;
 }
@@ -1472,14 +1496,18 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
 // Cell sort of x2 (and, in the sorted mode, of x1) into records.
 template <int D>
 void launch_sort(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2, hipStream_t s) {
-    const CellSet S2{w.xs2, w.xs2r, w.cstart2, P.sorted ? w.boxb : w.bbox, P.clouds2, p2, P.sorted ? b2 : 1};
-    const CellSet S1{w.xs1, w.xs1r, nullptr, w.boxb, P.sorted ? P.clouds1 : 0, p1, b1};
+    const CellSet S2{w.xs2, w.xs2r, P.sorted ? w.boxb : w.bbox, P.clouds2, p2, P.sorted ? b2 : 1};
+    const CellSet S1{w.xs1, w.xs1r, w.boxb, P.sorted ? P.clouds1 : 0, p1, b1};
     if (P.multi_sort) {
         const dim3 grid((unsigned)P.sort_clouds, (unsigned)P.sort_chunks);
-        hipLaunchKernelGGL(cell_count_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, w.cursor);
-        hipLaunchKernelGGL(cell_scan_kernel, dim3((unsigned)P.sort_clouds), dim3(kThreads), 0, s, S2, S1,
-                           w.cursor);
-        hipLaunchKernelGGL(cell_scatter_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, w.cursor);
+        hipLaunchKernelGGL(cell_count_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, P.sort_chunks,
+                           w.cellhist);
+        hipLaunchKernelGGL(cell_prefix_kernel, dim3((unsigned)P.sort_clouds, kCells / kThreads), dim3(kThreads), 0,
+                           s, P.sort_chunks, w.cellhist, w.celltot);
+        hipLaunchKernelGGL(cell_start_kernel, dim3((unsigned)P.sort_clouds), dim3(kThreads), 0, s, S2, S1,
+                           w.celltot, w.cstart2);
+        hipLaunchKernelGGL(cell_scatter_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, P.sort_chunks,
+                           w.cellhist, w.cstart2);
     } else {
         hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)P.clouds2), dim3(kThreads), 0, s, w.xs2, p2,
                            S2.boxes, S2.clouds_per_box, w.xs2r, w.cstart2);
@@ -1593,8 +1621,7 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     hipStream_t s = as_stream(stream);
     const Plan P = make_plan(batch, b1, p1, b2, p2, d);
     const Workspace w = carve(workspace, P, p1, p2, d);
-    // presets: keys 0, box keys (+inf, -inf), seed mins +inf, first hits all ones, cursors and
-    // flags 0
+    // presets: keys 0, box keys (+inf, -inf), seed mins +inf, first hits all ones, flags 0
     Fills fs{};
     int64_t most = 0;
     auto add = [&](void *ptr, int64_t words, uint32_t v0, uint32_t v1) {
@@ -1606,7 +1633,6 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     add(w.boxkeys, 2 * (P.box_rows1 + P.box_rows2), kOrderedPosInf, kOrderedNegInf);
     add(w.seedmin, pairs * kSeeds, 0x7f800000u, 0x7f800000u);
     add(w.first, 2 * pairs, 0xffffffffu, 0xffffffffu);
-    add(w.cursor, P.sort_clouds * kCells, 0u, 0u);
     add(w.flagbits, P.pairs * cdiv(p1, 32), 0u, 0u);
     hipLaunchKernelGGL(fill_kernel, dim3((unsigned)std::min<int64_t>(cdiv(most, 256), 2048)), dim3(256), 0, s, fs);
     int rc = check_launch("hausdorff presets");

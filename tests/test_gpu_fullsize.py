@@ -1,0 +1,188 @@
+"""GPU parity at the benchmark configurations' full sizes (the metric shape M = 16384^2 x 128
+and C2..C5), with the inputs the benchmark draws.  The full outputs are too large for the
+CPU oracle, so each test checks a seeded sample of output rows (and, for gradients, of
+columns) against the oracle on the same inputs, plus size-independent properties of the
+whole output: exact count grids for boolean metrics, symmetry for x2 = None, and, for
+directed Hausdorff, that every returned index pair realises the value and is the first
+nearest x2 point of the returned x1 point."""
+import numpy as np
+import pytest
+import torch
+
+import torchpairwise_amd as tp
+from oracle import cref
+from oracle import pairwise as P
+from tests._util import assert_close, assert_equal, rand, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _sample(n: int, k: int, seed: int) -> list[int]:
+    """The first and last four indices plus k seeded random ones, sorted and distinct."""
+    g = torch.Generator().manual_seed(seed)
+    picks = torch.randperm(n, generator=g)[:k].tolist()
+    return sorted(set(picks) | set(range(4)) | set(range(n - 4, n)))
+
+
+def _rows_close(out, ref, rtol, what):
+    assert_close(out, ref, rtol=rtol, atol=rtol * float(ref.abs().max()), what=what)
+
+
+# ------------------------------------------------------------------------ M: 16384^2 x 128
+def test_metric_shape_euclidean_manhattan():
+    x1, x2 = randn(16384, 128, seed=0), randn(16384, 128, seed=1)
+    a, b = x1.to(DEV), x2.to(DEV)
+    rows = _sample(16384, 40, seed=3)
+    for name, fn, p in (("euclidean", tp.euclidean_distances, 2.0),
+                        ("manhattan", tp.manhattan_distances, 1.0)):
+        out = fn(a, b)
+        assert out.shape == (16384, 16384) and out.dtype == torch.float32
+        assert bool(torch.isfinite(out).all()) and bool((out >= 0).all()), name
+        ref = torch.cdist(x1[rows].double(), x2.double(), p)
+        _rows_close(out[rows].cpu(), ref, 1e-5, f"{name} sampled rows")
+        del out
+    # x2 = None: the matrix of a cloud against itself is symmetric with a near-zero diagonal
+    d = tp.euclidean_distances(a)
+    scale = float(d.max())
+    assert float((d - d.T).abs().max()) <= 1e-5 * scale
+    # |a|^2 + |a|^2 - 2 a.a in fp32 leaves at most a few ulp of 2|a|^2 under the root
+    floor = 4 * torch.sqrt(torch.finfo(torch.float32).eps * 2 * (x1.double() ** 2).sum(1))
+    assert bool((d.diagonal().cpu().double() <= floor).all())
+
+
+def test_metric_shape_hamming():
+    x1 = rand(16384, 128, seed=0) < 0.5
+    x2 = rand(16384, 128, seed=1) < 0.5
+    out = tp.hamming_distances(x1.to(DEV), x2.to(DEV))
+    assert out.shape == (16384, 16384) and out.dtype == torch.float32
+    # every output is count / 128 exactly: an integer grid over the whole matrix
+    t = out * 128
+    assert bool((t == t.round()).all()) and bool((t >= 0).all()) and bool((t <= 128).all())
+    rows = _sample(16384, 40, seed=4)
+    want = P.hamming_distances(x1[rows].numpy(), x2.numpy())
+    assert_equal(out[rows].cpu(), torch.from_numpy(want), "hamming sampled rows")
+
+
+# ------------------------------------------------------------------ C2: [8, 8192, 256]^2 fwd+bwd
+@pytest.fixture(scope="module")
+def c2_inputs():
+    x1, x2 = randn(8, 8192, 256, seed=0), randn(8, 8192, 256, seed=1)
+    g = randn(8, 8192, 8192, seed=2)
+    return x1, x2, g
+
+
+def _c2_ref(metric, r1, r2, gsl):
+    """Reference value and gradient of one row block (or column block) in float64 on the CPU:
+    the reference's arithmetic (at::cdist for euclidean, the prf_div composite for cosine)."""
+    out = torch.cdist(r1, r2, 2) if metric == "euclidean" else P.cosine_distances(r1, r2)
+    out.backward(gsl)
+    return out.detach()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("metric", ["euclidean", "cosine"])
+def test_c2_forward_backward(c2_inputs, metric, dtype):
+    x1, x2, g = c2_inputs
+    x1, x2, g = x1.to(dtype), x2.to(dtype), g.to(dtype)
+    a = x1.to(DEV).requires_grad_()
+    b = x2.to(DEV).requires_grad_()
+    fn = tp.euclidean_distances if metric == "euclidean" else tp.cosine_distances
+    out = fn(a, b)
+    assert out.shape == (8, 8192, 8192) and out.dtype == dtype
+    out.backward(g.to(DEV))
+    rtol = 1e-5 if dtype == torch.float32 else 1e-2
+    grtol = 1e-4 if dtype == torch.float32 else 2e-2
+    f1, f2 = x1.double(), x2.double()
+    for bb in (0, 5):
+        rows = _sample(8192, 6, seed=10 + bb)
+        r1 = f1[bb, rows].clone().requires_grad_()
+        ref = _c2_ref(metric, r1, f2[bb], g[bb, rows].double())
+        _rows_close(out[bb, rows].detach().float().cpu(), ref, rtol, f"{metric} rows b={bb}")
+        _rows_close(a.grad[bb, rows].float().cpu(), r1.grad, grtol, f"{metric} grad_x1 b={bb}")
+        cols = _sample(8192, 6, seed=20 + bb)
+        r2 = f2[bb, cols].clone().requires_grad_()
+        _c2_ref(metric, f1[bb], r2, g[bb][:, cols].double())
+        _rows_close(b.grad[bb, cols].float().cpu(), r2.grad, grtol, f"{metric} grad_x2 b={bb}")
+
+
+# ------------------------------------------------- C3: minkowski p=3 fwd+bwd, chebyshev, [16384,128]^2
+def test_c3_minkowski_chebyshev():
+    x1 = rand(16384, 128, seed=0) * 2 - 1
+    x2 = rand(16384, 128, seed=1) * 2 - 1
+    a = x1.to(DEV).requires_grad_()
+    b = x2.to(DEV).requires_grad_()
+    out = tp.minkowski_distances(a, b, p=3.0)
+    out.backward(torch.ones_like(out))
+    f1, f2 = x1.double(), x2.double()
+    rows = _sample(16384, 12, seed=5)
+    r1 = f1[rows].clone().requires_grad_()
+    ref = torch.cdist(r1, f2, 3.0)
+    ref.backward(torch.ones_like(ref))
+    _rows_close(out[rows].detach().cpu(), ref.detach(), 1e-5, "minkowski p=3 rows")
+    _rows_close(a.grad[rows].cpu(), r1.grad, 1e-4, "minkowski grad_x1")
+    cols = _sample(16384, 12, seed=6)
+    r2 = f2[cols].clone().requires_grad_()
+    refc = torch.cdist(f1, r2, 3.0)
+    refc.backward(torch.ones_like(refc))
+    _rows_close(b.grad[cols].cpu(), r2.grad, 1e-4, "minkowski grad_x2")
+    del out
+    # chebyshev: max |fl(a - b)| is exact in float32, so the sampled rows are bit-exact
+    cheb = tp.chebyshev_distances(a.detach(), b.detach())
+    rows = _sample(16384, 40, seed=7)
+    assert_equal(cheb[rows].cpu(), torch.cdist(x1[rows], x2, float("inf")), "chebyshev rows")
+
+
+# ----------------------------------------------------------- C4: bool [32768, 1024]^2
+@pytest.mark.parametrize("metric,density", [("hamming", 0.5), ("jaccard", 0.1)])
+def test_c4_boolean(metric, density):
+    x1 = rand(32768, 1024, seed=0) < density
+    x2 = rand(32768, 1024, seed=1) < density
+    fn = tp.hamming_distances if metric == "hamming" else tp.jaccard_distances
+    out = fn(x1.to(DEV), x2.to(DEV))
+    assert out.shape == (32768, 32768) and out.dtype == torch.float32
+    assert bool((out >= 0).all()) and bool((out <= 1).all())
+    if metric == "hamming":
+        t = out * 1024  # count / 1024 exactly: an integer grid over the whole matrix
+        assert bool((t == t.round()).all())
+    rows = _sample(32768, 28, seed=8)
+    ref = (P.hamming_distances if metric == "hamming" else P.jaccard_distances)(
+        x1[rows].numpy(), x2.numpy())
+    assert_equal(out[rows].cpu(), torch.from_numpy(ref), f"{metric} sampled rows")
+
+
+# ---------------------------------------------- C5: directed Hausdorff [16, 65536, 3]^2
+def _first_nearest(cloud2: np.ndarray, point: np.ndarray):
+    """min over n of the reference's float32 squared distance (sequential k, no FMA) from
+    `point` to every point of `cloud2`, and the first n reaching it."""
+    d = np.zeros(cloud2.shape[0], np.float32)
+    for k in range(cloud2.shape[1]):
+        diff = (np.float32(point[k]) - cloud2[:, k]).astype(np.float32)
+        d = (d + (diff * diff).astype(np.float32)).astype(np.float32)
+    n = int(np.argmin(d))  # argmin returns the first position of the minimum
+    return d[n], n
+
+
+def test_c5_directed_hausdorff():
+    x1 = rand(16, 65536, 3, seed=0)
+    x2 = rand(16, 65536, 3, seed=1) + 0.05
+    a = x1.to(DEV).requires_grad_()
+    out, i1, i2 = tp.directed_hausdorff_distances(a, x2.to(DEV))
+    out.backward(torch.ones_like(out))
+    o, m_, n_ = out.detach().cpu().numpy(), i1.cpu().numpy(), i2.cpu().numpy()
+    c1, c2 = x1.numpy(), x2.numpy()
+    # every cloud pair: the returned x1 point's nearest x2 point is the returned one (first on
+    # ties) and its distance is the output, bit for bit
+    for i in range(16):
+        for j in range(16):
+            h, n = _first_nearest(c2[j], c1[i, m_[i, j]])
+            assert n == n_[i, j], (i, j)
+            assert np.sqrt(h, dtype=np.float32) == o[i, j], (i, j)
+    # sampled cloud pairs against the early-break restatement of the reference loop: value
+    # and both indices bit-exact (this also pins that no other m has a larger min)
+    for i, j in ((0, 0), (3, 11), (15, 7)):
+        w = cref.directed_hausdorff(c1[i:i + 1], c2[j:j + 1])
+        assert (o[i, j], m_[i, j], n_[i, j]) == (w[0][0, 0], w[1][0, 0], w[2][0, 0]), (i, j)
+    # backward: the reference's scatter over the forward's (verified) indices
+    gx1, _ = P.directed_hausdorff_backward(np.ones((16, 16), np.float32), c1, c2, o, m_, n_)
+    assert_equal(a.grad.cpu(), torch.from_numpy(gx1), "grad_x1")

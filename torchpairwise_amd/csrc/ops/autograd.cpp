@@ -112,6 +112,8 @@ class DirectedHausdorffFunction : public torch::autograd::Function<DirectedHausd
             generator.has_value() ? c10::make_optional(generator->clone()) : generator;
         auto r = directed_hausdorff(x1, x2, shuffle, generator);
         ctx->mark_non_differentiable({std::get<1>(r), std::get<2>(r)});
+        // only the output's gradient is read: no zero tensors for the index outputs
+        ctx->set_materialize_grads(false);
         // The reference's backward re-runs the forward.  Without shuffling, or with a generator
         // (whose cloned state the backward replays), that re-run returns exactly this forward's
         // output and indices, so on the GPU the backward takes them from here instead of
@@ -126,6 +128,7 @@ class DirectedHausdorffFunction : public torch::autograd::Function<DirectedHausd
         return {std::get<0>(r), std::get<1>(r), std::get<2>(r)};
     }
     static variable_list backward(AutogradContext *ctx, const variable_list &grad_output) {
+        if (!grad_output[0].defined()) return {Variable(), Variable(), Variable(), Variable()};
         auto saved = ctx->get_saved_variables();
         if (ctx->saved_data["reuse"].toBool()) {
             auto grads = directed_hausdorff_backward_indexed_cuda(grad_output[0], saved[0], saved[1],

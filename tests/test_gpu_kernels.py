@@ -29,6 +29,8 @@ BOOL_SHAPES = [
     (3, 64, 200, 1000),
     (2, 129, 127, 31),
     (1, 300, 301, 4096 + 17),
+    (2, 70, 1030, 200),   # 32 x 512 tiles: ragged rows and columns, scalar stores (m % 4 != 0)
+    (1, 33, 1024, 256),   # 32 x 512 tiles at the 8-word limit, full column tiles
 ]
 
 

@@ -146,19 +146,24 @@ __device__ __forceinline__ uint32_t popacc(uint32_t acc, uint4 a, uint4 b) {
     return acc;
 }
 
-// out tile (128 x 128) of batch blockIdx.z.  Thread (ty, tx) owns rows ty + 16 i and
-// columns 64 h + 4 tx + c (i < 8, h < 2, c < 4).
-template <int OP, int EPI>
+// out tile (8 TY rows x 8 TX columns, TX TY = 256 threads) of batch blockIdx.z.  Thread
+// (ty, tx) owns rows ty + TY i and columns 4 TX h + 4 tx + c (i < 8, h < 2, c < 4), so one
+// float4 store instruction of a wave covers 64 / TX rows with 16 TX contiguous bytes each.
+// CV uint4 (4 words) per row and LDS chunk.  128 x 128 (TX = 16) for general rows; 32 x 512
+// (TX = 64) for rows of at most 8 words, where the output write is the whole cost and 2 KB
+// contiguous per row and tile keep the DRAM pages open longer than 512 B.
+template <int OP, int EPI, int TX, int CV>
 __global__ __launch_bounds__(kThreads) void bool_reduce_kernel(
     const uint32_t *__restrict__ A, const uint32_t *__restrict__ Bw,
     const int32_t *__restrict__ popA, const int32_t *__restrict__ popB, int64_t n, int64_t m,
     int64_t W, int64_t d, double inv_d, float inv_df, float *__restrict__ out, bool vec_store) {
     constexpr bool kPops = EPI >= kJaccard;
-    __shared__ uint4 As[kTile][kChunkVec + 1];
-    __shared__ uint4 Bs[kTile][kChunkVec + 1];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    constexpr int TY = kThreads / TX, RT = 8 * TY, CT = 8 * TX;
+    __shared__ uint4 As[RT][CV + 1];
+    __shared__ uint4 Bs[CT][CV + 1];
+    const int tid = threadIdx.x, tx = tid % TX, ty = tid / TX;
     const int64_t b = blockIdx.z;
-    const int64_t row0 = (int64_t)blockIdx.y * kTile, col0 = (int64_t)blockIdx.x * kTile;
+    const int64_t row0 = (int64_t)blockIdx.y * RT, col0 = (int64_t)blockIdx.x * CT;
     const uint32_t *Ab = A + b * n * W;
     const uint32_t *Bb = Bw + b * m * W;
 
@@ -168,24 +173,29 @@ __global__ __launch_bounds__(kThreads) void bool_reduce_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = 0;
 
-    for (int64_t w0 = 0; w0 < W; w0 += 4 * kChunkVec) {
-        const int q = (int)((W - w0) / 4 < kChunkVec ? (W - w0) / 4 : kChunkVec);
-        for (int idx = tid; idx < kTile * q; idx += kThreads) {
-            int r = idx / q, c = idx - r * q;
-            int64_t gr = row0 + r, gc = col0 + r;
-            uint4 u = {0u, 0u, 0u, 0u}, v = {0u, 0u, 0u, 0u};
+    for (int64_t w0 = 0; w0 < W; w0 += 4 * CV) {
+        const int q = (int)((W - w0) / 4 < CV ? (W - w0) / 4 : CV);
+        for (int idx = tid; idx < RT * q; idx += kThreads) {
+            const int r = idx / q, c = idx - r * q;
+            const int64_t gr = row0 + r;
+            uint4 u = {0u, 0u, 0u, 0u};
             if (gr < n) u = *reinterpret_cast<const uint4 *>(Ab + gr * W + w0 + 4 * c);
-            if (gc < m) v = *reinterpret_cast<const uint4 *>(Bb + gc * W + w0 + 4 * c);
             As[r][c] = u;
+        }
+        for (int idx = tid; idx < CT * q; idx += kThreads) {
+            const int r = idx / q, c = idx - r * q;
+            const int64_t gc = col0 + r;
+            uint4 v = {0u, 0u, 0u, 0u};
+            if (gc < m) v = *reinterpret_cast<const uint4 *>(Bb + gc * W + w0 + 4 * c);
             Bs[r][c] = v;
         }
         __syncthreads();
         for (int c = 0; c < q; ++c) {
             uint4 a[8], bv[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) a[i] = As[ty + 16 * i][c];
+            for (int i = 0; i < 8; ++i) a[i] = As[ty + TY * i][c];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bv[j] = Bs[(j >> 2) * 64 + 4 * tx + (j & 3)][c];
+            for (int j = 0; j < 8; ++j) bv[j] = Bs[(j >> 2) * (4 * TX) + 4 * tx + (j & 3)][c];
 #pragma unroll
             for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -196,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void bool_reduce_kernel(
 
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int64_t row = row0 + ty + 16 * i;
+        const int64_t row = row0 + ty + TY * i;
         if (row >= n) continue;
         float *orow = out + (b * n + row) * m;
         uint32_t pa = 0;
@@ -204,7 +214,7 @@ __global__ __launch_bounds__(kThreads) void bool_reduce_kernel(
         const float df = (float)d;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int64_t col = col0 + 64 * h + 4 * tx;
+            const int64_t col = col0 + 4 * TX * h + 4 * tx;
             float v[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -228,12 +238,18 @@ template <int OP, int EPI>
 int launch_reduce(const uint32_t *a, const uint32_t *b, const int32_t *pa, const int32_t *pb,
                   int64_t batch, int64_t n, int64_t m, int64_t d, float *out, hipStream_t s) {
     const int64_t W = tpw_packed_words(d);
-    dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
     const double inv_d = d < (int64_t)kFloatExactLimit ? 1.0 / (double)d : 0.0;
     const float inv_df = 1.0f / (float)d;  // as ATen's host-side reciprocal of a CPU scalar
     const bool vec_store = (m % 4 == 0) && aligned16(out);
-    hipLaunchKernelGGL((bool_reduce_kernel<OP, EPI>), grid, dim3(kThreads), 0, s, a, b, pa, pb,
-                       n, m, W, d, inv_d, inv_df, out, vec_store);
+    if (W <= 8 && m > 256 && cdiv(n, 32) <= kMaxGridYZ) {
+        dim3 grid((unsigned)cdiv(m, 512), (unsigned)cdiv(n, 32), (unsigned)batch);
+        hipLaunchKernelGGL((bool_reduce_kernel<OP, EPI, 64, 2>), grid, dim3(kThreads), 0, s, a, b,
+                           pa, pb, n, m, W, d, inv_d, inv_df, out, vec_store);
+    } else {
+        dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
+        hipLaunchKernelGGL((bool_reduce_kernel<OP, EPI, 16, kChunkVec>), grid, dim3(kThreads), 0, s,
+                           a, b, pa, pb, n, m, W, d, inv_d, inv_df, out, vec_store);
+    }
     return check_launch("bool_reduce_kernel");
 }
 

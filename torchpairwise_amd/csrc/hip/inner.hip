@@ -77,7 +77,8 @@ __device__ __forceinline__ float epilogue(float s, float a1, float a2, const Ker
     } else if constexpr (EPI == TPW_EPI_DOT || EPI == kEpiGrad) {
         return s;
     } else if constexpr (EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN) {
-        float v = (a1 + a2) - 2.0f * s;
+        // (a1 + a2) - 2 s with one rounding: 2 s is exact, so the fma is bit-identical
+        float v = __builtin_fmaf(-2.0f, s, a1 + a2);
         v = v > 0.0f ? v : 0.0f;
         // v_sqrt_f32 (1 ulp): the |a|^2 + |b|^2 - 2ab form already carries more error
         if constexpr (EPI == TPW_EPI_EUCLIDEAN) v = __builtin_amdgcn_sqrtf(v);
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     uint4 *Bs = smem + kTile * kLdsStride;
     // norms of the tile's rows ([0]) and columns ([1]); published by the first barrier of the
     // K loop (or the one for d == 0)
-    __shared__ float s_aux[2][kTile];
+    __shared__ __align__(16) float s_aux[2][kTile];
     constexpr int E = Elem<T>::kPer16;
     constexpr int KC = Elem<T>::kChunk;
 
@@ -260,12 +261,18 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
             float *stage = reinterpret_cast<float *>(smem) + wave * (32 * kStageStride);
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi) {
+                // the norms of the lane's 16 rows: 4 groups of 4 consecutive rows
+                floatx4 a1q[4];
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    a1q[g] = kAux1<EPI> ? *reinterpret_cast<const floatx4 *>(&s_aux[0][wr + mi * 32 + 8 * g + 4 * h])
+                                        : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
-                        const float a1 = kAux1<EPI> ? s_aux[0][wr + mi * 32 + rr] : 0.0f;
+                        const float a1 = a1q[r >> 2][r & 3];
                         stage[rr * kStageStride + ni * 32 + l32] =
                             EPI == kEpiGrad ? sign * acc[mi][ni][r] : epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni], kp);
                     }

@@ -314,7 +314,8 @@ __global__ __launch_bounds__(kThreads, 2) void bool_mfma_kernel(
     __shared__ uint4 smem[2 * kTile * kBStride];
     uint4 *As = smem;
     uint4 *Bs = smem + kTile * kBStride;
-    __shared__ uint32_t s_pop[2][kTile];  // popcounts of the tile's rows ([0]) and columns ([1])
+    // popcounts of the tile's rows ([0]) and columns ([1])
+    __shared__ __align__(16) uint32_t s_pop[2][kTile];
 
     int64_t b, tr, tc;
     xcd_tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
@@ -401,12 +402,18 @@ __global__ __launch_bounds__(kThreads, 2) void bool_mfma_kernel(
         float *stage = reinterpret_cast<float *>(smem) + wave * (32 * kBStage);
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
+            // the popcounts of the lane's 16 rows: 4 groups of 4 consecutive rows
+            uint4 paq[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                paq[g] = *reinterpret_cast<const uint4 *>(&s_pop[0][wr + mi * 32 + 8 * g + 4 * h]);
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
-                    const uint32_t pav = s_pop[0][wr + mi * 32 + rr];
+                    const uint4 q4 = paq[r >> 2];
+                    const uint32_t pav = (r & 3) == 0 ? q4.x : (r & 3) == 1 ? q4.y : (r & 3) == 2 ? q4.z : q4.w;
                     const uint32_t c = count_from_and<OP, EPI>((uint32_t)acc[mi][ni][r], pav, pbv[ni]);
                     stage[rr * kBStage + ni * 32 + l32] = finish<OP, EPI>(c, pav, pbv[ni], du, inv_d, df, inv_df);
                 }

@@ -411,11 +411,23 @@ int tpw_cosine_backward(const void *grad, const void *x1, const void *x2,
 /* ------------------------------------------------------------------------- */
 
 /* out = y != 0 ? x / y : (identity ? x : 0), elementwise over `numel` elements of type
- * TPW_F32 / TPW_F64 / TPW_F16 / TPW_BF16 (half types round after each operation).
- * Replaces prf_div_forward_kernel (csrc/ops/cpu/prf_div_kernel.cpp:14-54,57-;
- * CUDA csrc/ops/cuda/prf_div_kernel.cu:22-133) with mode "zero" / "identity". */
+ * TPW_F32 / TPW_F64 / TPW_F16 / TPW_BF16 (half types round after each operation).  `out`
+ * may be `x` or `y` (the in-place forms); prf_ldiv(a, b) is this with x = b, y = a.
+ * Replaces prf_div_forward_kernel (csrc/ops/cpu/prf_div_kernel.cpp:14-24,58-103;
+ * CUDA csrc/ops/cuda/prf_div_kernel.cu:24-36,76-133) with mode "zero" / "identity", and the
+ * in-place prf_div__forward_kernel (cpu/prf_div_kernel.cpp:153-207; cuda :190-256). */
 int tpw_prf_div(const void *x, const void *y, int dtype, int64_t numel, int identity,
                 void *out, void *stream);
+
+/* The scalar forms.  scalar_first == 0: out = c != 0 ? x / c : (identity ? x : 0)
+ * (prf_div.Scalar, prf_ldiv.rScalar); scalar_first != 0: out = x != 0 ? c / x :
+ * (identity ? c : 0) (prf_ldiv.Scalar, prf_div.rScalar).  c is rounded to the element type
+ * first (to float, then to the half type, as c10::Scalar::to does).  `out` may be `x`.
+ * Replaces the scalar overloads of prf_div_forward_kernel_impl and the Scalar / rScalar /
+ * in-place Scalar kernels (csrc/ops/cpu/prf_div_kernel.cpp:25-54,106-151,210-255;
+ * CUDA csrc/ops/cuda/prf_div_kernel.cu:39-70,136-188,259-306). */
+int tpw_prf_div_scalar(const void *x, double c, int dtype, int64_t numel, int identity,
+                       int scalar_first, void *out, void *stream);
 
 /* grad_x = y != 0 ? g / y : (identity ? g : 0); grad_y = y != 0 ? (g / y) * -x / y : 0.
  * Replaces prf_div_backward_kernel (csrc/ops/cpu/prf_div_kernel.cpp:258-277;
@@ -423,6 +435,16 @@ int tpw_prf_div(const void *x, const void *y, int dtype, int64_t numel, int iden
 int tpw_prf_div_backward(const void *grad, const void *x, const void *y, int dtype,
                          int64_t numel, int identity, void *grad_x, void *grad_y,
                          void *stream);
+
+/* Backward of the scalar forms, into grad_x (every element written).  scalar_first == 0
+ * (z = x / c): grad_x = c != 0 ? g / c : (identity ? g : 0), x unused (may be NULL);
+ * scalar_first != 0 (z = c / x): grad_x = x != 0 ? (g * -c) / (x * x) : 0.
+ * Replaces the scalar overloads of prf_div_backward_kernel_impl and the Scalar / rScalar
+ * backward kernels (csrc/ops/cpu/prf_div_kernel.cpp:279-311,363-450;
+ * CUDA csrc/ops/cuda/prf_div_kernel.cu:336-368,426-525). */
+int tpw_prf_div_scalar_backward(const void *grad, const void *x, double c, int dtype,
+                                int64_t numel, int identity, int scalar_first, void *grad_x,
+                                void *stream);
 
 /* ------------------------------------------------------------------------- */
 /* Directed Hausdorff                                                         */

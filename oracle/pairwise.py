@@ -192,6 +192,82 @@ def prf_div_identity(x, y):
     return _PrfDivIdentity.apply(x, y)
 
 
+# -------------------------------------------------------------------------------------
+# the prf_div family (csrc/ops/prf_div.cpp:359-400; CPU kernels csrc/ops/cpu/prf_div_kernel.cpp)
+# elementwise in numpy.  Values ride in float64 carriers; R rounds a float64 result to the
+# element type the way the reference's scalar_t arithmetic does: float32 directly (a float64
+# quotient or product of float32 values rounds to the same float32 as the float32 operation:
+# 53 >= 2 * 24 + 2), float16 / bfloat16 through float32 first, as c10::Half / c10::BFloat16
+# compute each operation in float and round the result.
+# -------------------------------------------------------------------------------------
+def bf16_round(v) -> np.ndarray:
+    """float32 -> the nearest bfloat16 (ties to even), returned as float32; NaN -> 0x7fc0."""
+    f = np.asarray(v, np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(f), np.float32(np.nan), r)
+
+
+def elem_round(dtype: str):
+    """R: float64 carrier -> float64 carrier of the nearest value of `dtype`."""
+    def f32(v):
+        return np.asarray(v, np.float64).astype(np.float32)
+    if dtype == "float64":
+        return lambda v: np.asarray(v, np.float64)
+    if dtype == "float32":
+        return lambda v: f32(v).astype(np.float64)
+    if dtype == "float16":
+        return lambda v: f32(v).astype(np.float16).astype(np.float64)
+    if dtype == "bfloat16":
+        return lambda v: bf16_round(f32(v)).astype(np.float64)
+    raise ValueError(dtype)
+
+
+def prf_divide(x, y, identity: bool, R) -> np.ndarray:
+    """y != 0 ? x / y : (identity ? x : 0) (csrc/ops/cpu/prf_divide.h:8-16)."""
+    x, y = np.broadcast_arrays(np.asarray(x, np.float64), np.asarray(y, np.float64))
+    with np.errstate(all="ignore"):
+        q = R(x / np.where(y != 0, y, 1.0))
+    return np.where(y != 0, q, x if identity else 0.0)
+
+
+def prf_div_forward(x, y, identity: bool, R, left: bool = False) -> np.ndarray:
+    """prf_div(x, y) / prf_ldiv(x, y) = prf_divide(y, x); either operand may be a scalar
+    already rounded to the element type (the Scalar and rScalar forms,
+    cpu/prf_div_kernel.cpp:14-54,57-151)."""
+    return prf_divide(y, x, identity, R) if left else prf_divide(x, y, identity, R)
+
+
+def prf_div_backward(g, x, y, identity: bool, R):
+    """Gradients of z = x / y, both operands tensors (cpu/prf_div_kernel.cpp:258-277):
+    y != 0: gx = g / y, gy = (gx * -x) / y; y == 0: gx = identity ? g : 0, gy = 0."""
+    g, x, y = np.broadcast_arrays(*(np.asarray(v, np.float64) for v in (g, x, y)))
+    nz = y != 0
+    ys = np.where(nz, y, 1.0)
+    with np.errstate(all="ignore"):
+        gs = R(g / ys)
+        gy = R(R(gs * -x) / ys)
+    return np.where(nz, gs, g if identity else 0.0), np.where(nz, gy, 0.0)
+
+
+def prf_div_scalar_divisor_backward(g, c: float, identity: bool, R) -> np.ndarray:
+    """gx of z = x / c (cpu/prf_div_kernel.cpp:279-297): c != 0 ? g / c : identity ? g : 0."""
+    g = np.asarray(g, np.float64)
+    if c != 0:
+        with np.errstate(all="ignore"):
+            return R(g / c)
+    return g.copy() if identity else np.zeros_like(g)
+
+
+def prf_div_scalar_dividend_backward(g, x, c: float, R) -> np.ndarray:
+    """gx of z = c / x (cpu/prf_div_kernel.cpp:298-311): x != 0 ? (g * -c) / (x * x) : 0."""
+    g, x = np.broadcast_arrays(np.asarray(g, np.float64), np.asarray(x, np.float64))
+    nz = x != 0
+    with np.errstate(all="ignore"):
+        v = R(R(g * -c) / R(x * x))
+    return np.where(nz, v, 0.0)
+
+
 def cosine_similarity(x1: torch.Tensor, x2: torch.Tensor | None = None) -> torch.Tensor:
     """csrc/ops/pairwise_metrics.cpp:112-122: prf_div(x1 @ x2^T, |x1| |x2|^T, identity);
     with x2=None the second operand and norm alias the first."""

@@ -9,7 +9,10 @@ usage: python oracle/ref_runner.py <op> <in.npz> <out.npz>
        hausdorff_backward (grad, x1, x2) -> grad_x1, grad_x2
        pw_<name>    (x1, x2) -> out            e.g. pw_pwne_mean, pw_pwxor_sum
        jaccard     (x1, x2) -> out             (prf_div(pwxor_sum, pwor_sum), the reference's composite)
+       prf         cases (JSON) + c<i>_a / _b / _g arrays -> c<i>_<result> arrays and c<i>_err
+                   messages: the 20 prf_div-family ops through run_prf_case
 """
+import json
 import subprocess
 import sys
 from pathlib import Path
@@ -32,13 +35,115 @@ def run(op: str, inputs: dict, tmpdir) -> dict:
     return dict(np.load(dst, allow_pickle=False))
 
 
+# --------------------------------------------------------------------------- prf_div cases
+# Tensors cross the process boundary as numpy arrays; bfloat16 travels as its int16 bits.
+def tensor_to_np(t) -> tuple:
+    import torch
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy(), "bfloat16"
+    return t.numpy(), str(t.dtype).replace("torch.", "")
+
+
+def np_to_tensor(a, tag: str):
+    import torch
+    t = torch.from_numpy(np.array(a))
+    return t.view(torch.bfloat16) if tag == "bfloat16" else t
+
+
+def run_prf_case(ops, case: dict, a, b, g, device: str) -> dict:
+    """Runs one prf_div-family case on `ops` (a torch.ops.torchpairwise namespace, this
+    build's or the reference's) and returns its results as tensors, or {"err": message}.
+
+    case: kind "fwd" (op prf_div / prf_ldiv, overload default / Scalar / rScalar, autograd
+    backward of grad g when case["grad"]), "inplace" (prf_div_ / prf_ldiv_, default or Scalar,
+    applied to a clone of a leaf), or "bwd" (a _prf_*_backward op called directly)."""
+    import torch
+    kind, name, ov, mode = case["kind"], case["op"], case["ov"], case["mode"]
+    c = case.get("scalar")
+    grad = bool(case.get("grad"))
+    f = getattr(getattr(ops, name), ov)
+    dev = lambda t: None if t is None else t.to(device)  # noqa: E731
+    a, b, g = dev(a), dev(b), dev(g)
+    res = {}
+    try:
+        if kind == "fwd":
+            ta = None if a is None else a.clone().requires_grad_(grad and a.is_floating_point())
+            tb = None if b is None else b.clone().requires_grad_(grad and b.is_floating_point())
+            args = {"default": (ta, tb), "Scalar": (ta, c), "rScalar": (c, tb)}[ov]
+            out = f(*args, mode)
+            res["out"] = out
+            if grad:
+                out.backward(g)
+                for key, t in (("ga", ta), ("gb", tb)):
+                    if t is not None and t.grad is not None:
+                        res[key] = t.grad
+        elif kind == "inplace":
+            leaf = a.clone().requires_grad_(grad)
+            ta = leaf.clone()
+            tb = None if b is None else b.clone().requires_grad_(grad and b.is_floating_point())
+            ret = f(ta, tb if ov == "default" else c, mode)
+            res["out"] = ta
+            res["same"] = torch.tensor(ret.data_ptr() == ta.data_ptr())
+            if grad:
+                ta.backward(g)
+                res["ga"] = leaf.grad
+                if tb is not None and tb.grad is not None:
+                    res["gb"] = tb.grad
+        else:
+            args = {"default": (g, a, b), "Scalar": (g, a, c), "rScalar": (g, c, b)}[ov]
+            r = f(*args, mode)
+            if ov == "default":
+                res["ga"], res["gb"] = r
+            else:
+                res["ga" if ov == "Scalar" else "gb"] = r
+    except Exception as e:  # the message is part of the interface
+        return {"err": f"{type(e).__name__}: {str(e).splitlines()[0]}"}
+    return {k: v.detach().cpu() for k, v in res.items()}
+
+
+def encode_prf_cases(cases) -> dict:
+    """[(case, a, b, g)] -> npz members (tensors as arrays + dtype tags in the JSON)."""
+    arrays, meta = {}, []
+    for i, (case, *ts) in enumerate(cases):
+        tags = {}
+        for key, t in zip("abg", ts):
+            if t is not None:
+                arrays[f"c{i}_{key}"], tags[key] = tensor_to_np(t)
+        meta.append({"case": case, "tags": tags})
+    arrays["cases"] = np.array(json.dumps(meta))
+    return arrays
+
+
+def decode_prf_cases(d: dict):
+    meta = json.loads(str(d["cases"]))
+    out = []
+    for i, m in enumerate(meta):
+        ts = [np_to_tensor(d[f"c{i}_{k}"], m["tags"][k]) if k in m["tags"] else None for k in "abg"]
+        out.append((m["case"], *ts))
+    return out
+
+
+def run_prf_reference(cases, tmpdir) -> list:
+    """The reference's results for [(case, a, b, g)], computed in a child process."""
+    raw = run("prf", encode_prf_cases(cases), tmpdir)
+    meta = json.loads(str(raw["results"]))
+    results = []
+    for i, m in enumerate(meta):
+        if "err" in m:
+            results.append({"err": m["err"]})
+        else:
+            results.append({k: np_to_tensor(raw[f"c{i}_{k}"], tag) for k, tag in m["tags"].items()})
+    return results
+
+
 def main(op: str, src: str, dst: str) -> None:
     import torch
 
     torch.ops.load_library(str(LIB))
     ops = torch.ops.torchpairwise
     d = dict(np.load(src, allow_pickle=False))
-    t = {k: torch.from_numpy(v) for k, v in d.items()}
+    t = {k: torch.from_numpy(v) for k, v in d.items() if v.dtype.kind != "U"}
     if op == "hausdorff":
         kw = {}
         if "seed" in d:
@@ -53,6 +158,19 @@ def main(op: str, src: str, dst: str) -> None:
         np.savez(dst, grad_x1=x1.grad.numpy(), grad_x2=x2.grad.numpy())
     elif op.startswith("pw_"):
         np.savez(dst, out=getattr(ops, op[3:])(t["x1"], t["x2"]).numpy())
+    elif op == "prf":
+        arrays, meta = {}, []
+        for i, (case, a, b, g) in enumerate(decode_prf_cases(d)):
+            r = run_prf_case(ops, case, a, b, g, "cpu")
+            if "err" in r:
+                meta.append({"err": r["err"]})
+                continue
+            tags = {}
+            for k, v in r.items():
+                arrays[f"c{i}_{k}"], tags[k] = tensor_to_np(v)
+            meta.append({"tags": tags})
+        arrays["results"] = np.array(json.dumps(meta))
+        np.savez(dst, **arrays)
     elif op == "jaccard":
         np.savez(dst, out=ops.prf_div(ops.pwxor_sum(t["x1"], t["x2"]), ops.pwor_sum(t["x1"], t["x2"]), "zero").numpy())
     else:

@@ -52,6 +52,8 @@ _SIGNATURES = {
     "tpw_cosine_backward": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p]),
     "tpw_prf_div": (_i, [_p, _p, _i, _i64, _i, _p, _p]),
     "tpw_prf_div_backward": (_i, [_p, _p, _p, _i, _i64, _i, _p, _p, _p]),
+    "tpw_prf_div_scalar": (_i, [_p, _d, _i, _i64, _i, _i, _p, _p]),
+    "tpw_prf_div_scalar_backward": (_i, [_p, _p, _d, _i, _i64, _i, _i, _p, _p]),
     "tpw_hausdorff_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "tpw_directed_hausdorff": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "tpw_directed_hausdorff_backward": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),

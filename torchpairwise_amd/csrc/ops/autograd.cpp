@@ -4,7 +4,7 @@
 //                           EUCLIDEAN, the cosine graph of pairwise_metrics.cpp:51-56,112-122)
 //   _pw_kernel           -> _pw_kernel_backward (autograd of the polynomial / sigmoid composites)
 //   _pw_lp               -> _pw_lp_backward (at::_cdist_backward formulas)
-//   prf_div              -> _prf_div_backward (csrc/ops/autograd/prf_div_kernel.cpp:9-52)
+//   (the prf_div family's autograd functions are in prf_div.cpp)
 //   _directed_hausdorff  -> __directed_hausdorff_backward, with the generator cloned so the
 //                           backward replays the forward's permutations
 //                           (csrc/ops/autograd/hausdorff_kernel.cpp:9-77)
@@ -84,24 +84,6 @@ class PwLpFunction : public torch::autograd::Function<PwLpFunction> {
     }
 };
 
-class PrfDivFunction : public torch::autograd::Function<PrfDivFunction> {
-   public:
-    static Variable forward(AutogradContext *ctx, const Variable &x, const Variable &y,
-                            c10::string_view mode) {
-        at::AutoDispatchBelowADInplaceOrView g;
-        auto out = prf_div(x, y, mode);
-        ctx->save_for_backward({x, y});
-        ctx->saved_data["mode"] = std::string(mode);
-        return out;
-    }
-    static variable_list backward(AutogradContext *ctx, const variable_list &grad_output) {
-        auto saved = ctx->get_saved_variables();
-        const std::string mode = ctx->saved_data["mode"].toStringRef();
-        auto grads = prf_div_backward(grad_output[0], saved[0], saved[1], mode);
-        return {std::get<0>(grads), std::get<1>(grads), Variable()};
-    }
-};
-
 class DirectedHausdorffFunction : public torch::autograd::Function<DirectedHausdorffFunction> {
    public:
     static variable_list forward(AutogradContext *ctx, const Variable &x1, const Variable &x2,
@@ -155,10 +137,6 @@ at::Tensor pw_lp_autograd(const at::Tensor &x1, const at::Tensor &x2, double p) 
     return PwLpFunction::apply(x1, x2, p);
 }
 
-at::Tensor prf_div_autograd(const at::Tensor &x, const at::Tensor &y, c10::string_view mode) {
-    return PrfDivFunction::apply(x, y, mode);
-}
-
 std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff_autograd(
     const at::Tensor &x1, const at::Tensor &x2, bool shuffle, c10::optional<at::Generator> gen) {
     auto r = DirectedHausdorffFunction::apply(x1, x2, shuffle, gen);
@@ -171,7 +149,6 @@ TORCH_LIBRARY_IMPL(torchpairwise, Autograd, m) {
     m.impl("_pw_inner", TORCH_FN(pw_inner_autograd));
     m.impl("_pw_kernel", TORCH_FN(pw_kernel_autograd));
     m.impl("_pw_lp", TORCH_FN(pw_lp_autograd));
-    m.impl("prf_div", TORCH_FN(prf_div_autograd));
     m.impl("_directed_hausdorff", TORCH_FN(directed_hausdorff_autograd));
 }
 

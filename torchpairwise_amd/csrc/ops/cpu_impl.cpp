@@ -1,9 +1,9 @@
 // CPU implementations of the custom internal ops, for CPU tensors (the reference runs these
 // on the CPU too).  They keep the reference's arithmetic: float accumulators for the pairwise
 // reductions (csrc/ops/cpu/pairwise_binary_kernels.cpp:28-49), the early-break max-min loop
-// for Hausdorff (csrc/ops/cpu/hausdorff_kernel.cpp:12-100, 187-235), and the guarded divide
-// (csrc/ops/cpu/prf_divide.h, prf_div_kernel.cpp:258-277), parallel over outputs with ATen's
-// intra-op pool.  GPU tensors never reach this file.
+// for Hausdorff (csrc/ops/cpu/hausdorff_kernel.cpp:12-100, 187-235), parallel over outputs
+// with ATen's intra-op pool (the prf_div family is in prf_div.cpp).  GPU tensors never reach
+// this file.
 #include <ATen/Dispatch.h>
 #include <ATen/Parallel.h>
 
@@ -57,60 +57,11 @@ at::Tensor pw_reduce_cpu(const at::Tensor &x1, const at::Tensor &x2) {
     return unbatched ? out.squeeze(0) : out;
 }
 
-at::Tensor prf_div_cpu(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
-
 at::Tensor jaccard_cpu(const at::Tensor &x1, const at::Tensor &x2) {
     // pairwise_metrics.cpp:215-222: prf_div(pwxor_sum, pwor_sum) ("zero" mode)
     auto a = x1.to(at::kBool), b = x2.to(at::kBool);
     return prf_div_cpu(pw_reduce_cpu<TPW_BIT_XOR, false>(a, b), pw_reduce_cpu<TPW_BIT_OR, false>(a, b),
                        "zero");
-}
-
-// ---------------------------------------------------------------- prf_div
-at::Tensor prf_div_cpu(const at::Tensor &x, const at::Tensor &y, c10::string_view mode) {
-    const bool identity = prf_identity(mode);
-    TORCH_CHECK(x.sizes() == y.sizes(), "prf_div: input and other must have the same shape, got ",
-                x.sizes(), " and ", y.sizes());
-    auto common = at::result_type(x, y);
-    if (!at::isFloatingType(common)) common = at::kFloat;
-    auto a = x.to(common).contiguous(), b = y.to(common).contiguous();
-    auto out = at::empty_like(a);
-    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, common, "prf_div_cpu", [&] {
-        const scalar_t *X = a.data_ptr<scalar_t>(), *Y = b.data_ptr<scalar_t>();
-        scalar_t *O = out.data_ptr<scalar_t>();
-        at::parallel_for(0, a.numel(), 4096, [&](int64_t beg, int64_t end) {
-            for (int64_t i = beg; i < end; ++i)
-                O[i] = Y[i] != scalar_t(0) ? scalar_t(X[i] / Y[i]) : (identity ? X[i] : scalar_t(0));
-        });
-    });
-    return out;
-}
-
-std::tuple<at::Tensor, at::Tensor> prf_div_backward_cpu(const at::Tensor &g, const at::Tensor &x,
-                                                        const at::Tensor &y, c10::string_view mode) {
-    const bool identity = prf_identity(mode);
-    auto common = at::result_type(x, y);
-    if (!at::isFloatingType(common)) common = at::kFloat;
-    auto a = x.to(common).contiguous(), b = y.to(common).contiguous();
-    auto gg = g.to(common).contiguous();
-    auto gx = at::zeros_like(a), gy = at::zeros_like(b);
-    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, common, "prf_div_backward_cpu", [&] {
-        const scalar_t *G = gg.data_ptr<scalar_t>(), *X = a.data_ptr<scalar_t>(), *Y = b.data_ptr<scalar_t>();
-        scalar_t *GX = gx.data_ptr<scalar_t>(), *GY = gy.data_ptr<scalar_t>();
-        at::parallel_for(0, a.numel(), 4096, [&](int64_t beg, int64_t end) {
-            for (int64_t i = beg; i < end; ++i) {
-                const scalar_t o = Y[i];
-                if (o != scalar_t(0)) {
-                    const scalar_t gs = G[i] / o;
-                    GX[i] = gs;
-                    GY[i] = scalar_t(gs * -X[i]) / o;
-                } else if (identity) {
-                    GX[i] = G[i];
-                }
-            }
-        });
-    });
-    return {gx, gy};
 }
 
 // ---------------------------------------------------------------- Hausdorff
@@ -252,8 +203,6 @@ TORCH_LIBRARY_IMPL(torchpairwise, CPU, m) {
     m.impl("pwne_mean", TORCH_FN((pw_reduce_cpu<TPW_BIT_NE, true>)));
     m.impl("_jaccard", TORCH_FN(jaccard_cpu));
     m.impl("_row_smallest_mask", TORCH_FN(row_smallest_mask_cpu));
-    m.impl("prf_div", TORCH_FN(prf_div_cpu));
-    m.impl("_prf_div_backward", TORCH_FN(prf_div_backward_cpu));
     m.impl("_directed_hausdorff", TORCH_FN(directed_hausdorff_cpu));
     m.impl("__directed_hausdorff_backward", TORCH_FN(directed_hausdorff_backward_cpu));
 }

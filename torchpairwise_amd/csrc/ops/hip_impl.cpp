@@ -284,40 +284,6 @@ at::Tensor row_smallest_mask_cuda(const at::Tensor &dist, int64_t count) {
     return mask;
 }
 
-// ---------------------------------------------------------------- prf_div
-at::Tensor prf_div_cuda(const at::Tensor &x, const at::Tensor &y, c10::string_view mode) {
-    const bool identity = prf_identity(mode);
-    TORCH_CHECK(x.sizes() == y.sizes(), "prf_div: input and other must have the same shape, got ",
-                x.sizes(), " and ", y.sizes());
-    DeviceGuard guard(x.device());
-    auto common = at::result_type(x, y);
-    if (!at::isFloatingType(common)) common = at::kFloat;  // integer inputs divide in float32
-    auto a = x.to(common).contiguous(), b = y.to(common).contiguous();
-    auto out = at::empty_like(a);
-    const int code = float_code(common);
-    TORCH_CHECK(code == TPW_F32 || code == TPW_F64 || code == TPW_F16 || code == TPW_BF16,
-                "prf_div: unsupported dtype ", common);
-    check_rc(tpw_prf_div(a.data_ptr(), b.data_ptr(), code, a.numel(), identity, out.data_ptr(),
-                         current_stream()),
-             "prf_div");
-    return out;
-}
-
-std::tuple<at::Tensor, at::Tensor> prf_div_backward_cuda(const at::Tensor &g, const at::Tensor &x,
-                                                         const at::Tensor &y, c10::string_view mode) {
-    const bool identity = prf_identity(mode);
-    DeviceGuard guard(x.device());
-    auto common = at::result_type(x, y);
-    if (!at::isFloatingType(common)) common = at::kFloat;
-    auto a = x.to(common).contiguous(), b = y.to(common).contiguous();
-    auto gg = g.to(common).contiguous();
-    auto gx = at::empty_like(a), gy = at::empty_like(b);
-    check_rc(tpw_prf_div_backward(gg.data_ptr(), a.data_ptr(), b.data_ptr(), float_code(common),
-                                  a.numel(), identity, gx.data_ptr(), gy.data_ptr(), current_stream()),
-             "prf_div backward");
-    return {gx, gy};
-}
-
 // ---------------------------------------------------------------- Hausdorff
 struct HdRun {
     at::Tensor a, b, out, i1, i2;
@@ -425,8 +391,6 @@ TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
     m.impl("pwne_sum", TORCH_FN((pw_reduce_cuda<TPW_BIT_NE, TPW_RED_SUM>)));
     m.impl("pweq_mean", TORCH_FN((pw_reduce_cuda<TPW_BIT_EQ, TPW_RED_MEAN>)));
     m.impl("pwne_mean", TORCH_FN((pw_reduce_cuda<TPW_BIT_NE, TPW_RED_MEAN>)));
-    m.impl("prf_div", TORCH_FN(prf_div_cuda));
-    m.impl("_prf_div_backward", TORCH_FN(prf_div_backward_cuda));
     m.impl("_directed_hausdorff", TORCH_FN(directed_hausdorff_cuda));
     m.impl("__directed_hausdorff_backward", TORCH_FN(directed_hausdorff_backward_cuda));
 }

@@ -759,10 +759,7 @@ TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     for (const char *op : {"pwand_sum", "pwor_sum", "pwxor_sum", "pweq_sum", "pwne_sum", "pweq_mean",
                            "pwne_mean"})
         m.def((std::string(op) + "(Tensor x1, Tensor x2) -> Tensor").c_str());
-    // csrc/ops/prf_div.cpp:359-400 (the tensor-tensor forms)
-    m.def("prf_div(Tensor input, Tensor other, str mode=\"zero\") -> Tensor");
-    m.def("_prf_div_backward(Tensor grad, Tensor self, Tensor other, str mode=\"zero\") -> "
-          "(Tensor grad_self, Tensor grad_other)");
+    // csrc/ops/prf_div.cpp:359-400: the prf_div family is registered in prf_div.cpp
     // csrc/ops/hausdorff.cpp:33-40
     m.def("_directed_hausdorff(Tensor x1, Tensor x2, *, bool shuffle=False, Generator? generator=None) "
           "-> (Tensor output, Tensor x1_indices, Tensor x2_indices)");

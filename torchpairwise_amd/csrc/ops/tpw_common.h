@@ -110,6 +110,8 @@ void bool_bytes_cuda(const at::Tensor &a, const at::Tensor &b, int bmet, int op,
 // packed rows are 8x smaller, which wins while the output write dominates.
 constexpr int64_t kBoolBytesMinFeatures = 257;
 at::Tensor prf_div(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
+// prf_div of two tensors without the dispatcher (for other ops' CPU / GPU bodies; prf_div.cpp)
+at::Tensor prf_div_cpu(const at::Tensor &x, const at::Tensor &y, c10::string_view mode);
 std::tuple<at::Tensor, at::Tensor> prf_div_backward(const at::Tensor &g, const at::Tensor &x,
                                                     const at::Tensor &y, c10::string_view mode);
 std::tuple<at::Tensor, at::Tensor, at::Tensor> directed_hausdorff(

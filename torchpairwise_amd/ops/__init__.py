@@ -25,7 +25,7 @@ _CPDIST = ["cdist", "pdist", "k_neighbors_mask", "radius_neighbors_mask"]
 _INTERNALS = [
     "pwand", "pwor", "pwxor", "pweq", "pwne", "pwlt", "pwgt", "pwle", "pwge",
     "pwand_sum", "pwor_sum", "pwxor_sum", "pweq_sum", "pwne_sum", "pweq_mean", "pwne_mean",
-    "prf_div",
+    "prf_div", "prf_ldiv", "prf_div_", "prf_ldiv_",
 ]
 
 for _name in _METRICS + _CPDIST + _INTERNALS:

@@ -1,6 +1,8 @@
 """Shared helpers of the test-suite (tolerance checks, seeded inputs)."""
 from __future__ import annotations
 
+import os
+
 import torch
 
 
@@ -27,6 +29,11 @@ def assert_close(actual, expected, *, rtol: float, atol: float, what: str = ""):
         atol = atol.detach().cpu().double()
     tol = atol + rtol * e.abs()
     bad = ~(diff <= tol)
+    if os.environ.get("TPW_TOL_REPORT"):
+        # the smallest r with diff <= r * (|want| + max|want|): the rtol this check needs when its
+        # atol is rtol * max|want|
+        need = float((diff / (e.abs() + e.abs().max() + 1e-300)).max()) if diff.numel() else 0.0
+        print(f"[tol] {what}: rtol={rtol} needs {need:.3g}", flush=True)
     if bad.any():
         idx = int(torch.argmax((diff - tol).flatten()))
         at = float(atol.flatten()[idx]) if torch.is_tensor(atol) and atol.numel() > 1 else float(atol)

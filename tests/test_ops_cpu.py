@@ -49,6 +49,20 @@ def test_meta_ops():
     assert tp.cuda_arch_list() == ["gfx950"]
 
 
+def test_c1_manhattan_euclidean_cpu():
+    """BASELINE configs[0] (manhattan + euclidean, fp32, [2048, 64] x [1024, 64], N(0, 1),
+    seeds 0 / 1) on the reference's CPU route: at::cdist in float32, against float64 cdist and
+    scipy for every element."""
+    x1, x2 = randn(2048, 64, seed=0), randn(1024, 64, seed=1)
+    for name, fn, p, sp in (("euclidean", tp.euclidean_distances, 2.0, "euclidean"),
+                            ("manhattan", tp.manhattan_distances, 1.0, "cityblock")):
+        out = fn(x1, x2)
+        assert out.shape == (2048, 1024) and out.dtype == torch.float32
+        assert_equal(out, torch.cdist(x1, x2, p), f"C1 {name} is at::cdist")
+        ref = torch.from_numpy(scipy_cdist(x1.double().numpy(), x2.double().numpy(), sp))
+        assert_close(out, ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()), what=f"C1 {name} vs scipy")
+
+
 @pytest.mark.parametrize("p", [0.0, 1.0, 1.5, 2.0, 3.0, float("inf")])
 def test_cdist_family_cpu_is_aten(p):
     x1, x2 = randn(40, 9, seed=0, dtype=torch.float64), randn(30, 9, seed=1, dtype=torch.float64)

@@ -468,6 +468,22 @@ int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t batch, int6
                            const int64_t *perm1, const int64_t *perm2, float *out,
                            int64_t *idx1, int64_t *idx2, void *workspace, void *stream);
 
+/* Size of the static scratch buffer of tpw_directed_hausdorff_noalloc, in MiB (per GPU). */
+#define TPW_HAUSDORFF_NOALLOC_SCRATCH_MIB 96
+
+/* tpw_directed_hausdorff without a workspace argument: the same kernels and results, with
+ * their scratch in a static device array of TPW_HAUSDORFF_NOALLOC_SCRATCH_MIB MiB that each
+ * GPU holds until the process ends.  It has no counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): it calls no hipMalloc / hipFree.  Sizes whose
+ * tpw_hausdorff_workspace_size exceeds the buffer are rejected with TPW_ERR_INVALID (the
+ * [16, 65536, 3] x [16, 65536, 3] case needs 67 MiB).  Every call on one GPU shares that
+ * GPU's buffer: calls that overlap on one GPU (concurrent streams or threads) race. */
+int tpw_directed_hausdorff_noalloc(const float *x1, const float *x2, int64_t batch, int64_t b1,
+                                   int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                   const int64_t *perm1, const int64_t *perm2, float *out,
+                                   int64_t *idx1, int64_t *idx2, void *stream);
+
 /* grad_x1[b,i,idx1,k] += grad * (x1[idx1,k] - x2[idx2,k]) / out summed over j in
  * order; grad_x2[b,j,idx2,k] += grad * (x2[idx2,k] - x1[idx1,k]) / out summed over
  * i in order.  grad_x1/grad_x2 must be zero-filled by the caller.

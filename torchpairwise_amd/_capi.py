@@ -56,6 +56,7 @@ _SIGNATURES = {
     "tpw_prf_div_scalar_backward": (_i, [_p, _p, _d, _i, _i64, _i, _i, _p, _p]),
     "tpw_hausdorff_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "tpw_directed_hausdorff": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
+    "tpw_directed_hausdorff_noalloc": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "tpw_directed_hausdorff_backward": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),
     "tpw_row_smallest_mask": (_i, [_p, _i, _i64, _i64, _i64, _p, _p]),
     "tpw_ppminkowski": (_i, [_p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
@@ -397,8 +398,9 @@ def _as4(x):
     return x if x.dim() == 4 else x.unsqueeze(0)
 
 
-def directed_hausdorff(x1, x2, perm1=None, perm2=None):
-    """x1 [(batch,) b1, p1, d], x2 [(batch,) b2, p2, d] fp32 -> (out, idx1, idx2)."""
+def directed_hausdorff(x1, x2, perm1=None, perm2=None, noalloc=False):
+    """x1 [(batch,) b1, p1, d], x2 [(batch,) b2, p2, d] fp32 -> (out, idx1, idx2); with
+    noalloc=True through tpw_directed_hausdorff_noalloc (the library's static scratch)."""
     import torch
 
     a, b = _as4(x1).contiguous(), _as4(x2).contiguous()
@@ -407,12 +409,16 @@ def directed_hausdorff(x1, x2, perm1=None, perm2=None):
     out = torch.empty((B, b1, b2), dtype=torch.float32, device=a.device)
     i1 = torch.empty((B, b1, b2), dtype=torch.int64, device=a.device)
     i2 = torch.empty((B, b1, b2), dtype=torch.int64, device=a.device)
-    ws = torch.empty((lib().tpw_hausdorff_workspace_size(B, b1, p1, b2, p2, d),), dtype=torch.uint8,
-                     device=a.device)
-    call("tpw_directed_hausdorff", _ptr(a), _ptr(b), B, b1, p1, b2, p2, d,
-         _ptr(None if perm1 is None else perm1.contiguous()),
-         _ptr(None if perm2 is None else perm2.contiguous()),
-         _ptr(out), _ptr(i1), _ptr(i2), _ptr(ws), _stream())
+    q1 = _ptr(None if perm1 is None else perm1.contiguous())
+    q2 = _ptr(None if perm2 is None else perm2.contiguous())
+    if noalloc:
+        call("tpw_directed_hausdorff_noalloc", _ptr(a), _ptr(b), B, b1, p1, b2, p2, d, q1, q2,
+             _ptr(out), _ptr(i1), _ptr(i2), _stream())
+    else:
+        ws = torch.empty((lib().tpw_hausdorff_workspace_size(B, b1, p1, b2, p2, d),), dtype=torch.uint8,
+                         device=a.device)
+        call("tpw_directed_hausdorff", _ptr(a), _ptr(b), B, b1, p1, b2, p2, d, q1, q2,
+             _ptr(out), _ptr(i1), _ptr(i2), _ptr(ws), _stream())
     if x1.dim() == 3:
         return out[0], i1[0], i2[0]
     return out, i1, i2

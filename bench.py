@@ -9,7 +9,9 @@ hamming_distances on bool inputs (rand < 0.5; the op packs the bits inside every
 the same way and reported under "extra".
 
 value = pair-features/s (N*M*D per call / mean call time over the timed steps), inputs
-resident in HBM.  Timing: W untimed warm-up steps, then K steps between two
+resident in HBM.  Timing: a clock-settle phase (the headline op called for --settle-ms of
+wall time, reported as settle_ms; the GPU leaves its idle clocks only after some tens of
+milliseconds of load), then W untimed warm-up steps, then K steps between two
 torch.cuda.synchronize() calls; per-kernel durations come from HIP events recorded on the
 stream the kernels are launched on (torch's current stream, which the C ABI receives).
 
@@ -20,7 +22,11 @@ roofline (dominant kernel = the MFMA pairwise kernel of euclidean):
   events on the launch stream.  Defaults W = K = 200: shorter warm-ups time the clock ramp
   out of idle.
 cpu_baseline: the reference's CPU path for euclidean_distances is at::cdist(p=2) -> on the
-  host cores via torch.cdist, timed on a bounded row sample of the same workload.
+  host cores via torch.cdist, timed on a bounded row sample of the same workload; beside it
+  manhattan (at::cdist p = 1), and the reference's own compiled CPU kernels (oracle/_ref, in a
+  child process: its OpenMP loops with their compiled-in 32 threads) for hamming, jaccard and
+  directed Hausdorff on samples of M, C4 and C5, plus the oracle's C restatement of the
+  hamming loop on all the cores this process may use.
 
 `python bench.py --gpus N` with N > 1 exits: this build measures one GPU.
 """
@@ -33,6 +39,7 @@ import sys
 import time
 
 PEAK_FP32_MFMA = 157.3e12
+PEAK_BF16_MFMA = 2.5e15
 PEAK_HBM = 8.0e12
 # FP32 vector peak 157.3 TFLOP/s = 256 CU x 4 SIMD x 32 lanes x 2 (FMA) x 2.4 GHz: a
 # non-packed VALU issue rate of 7.86e13 lane-ops/s
@@ -66,6 +73,8 @@ def parse():
     # 5 warm-up steps time the ramp (0.73 ms per headline step instead of 0.63)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--settle-ms", type=float, default=1500.0,
+                    help="wall time of headline-op calls before the counted warm-up (clock ramp)")
     ap.add_argument("--n", type=int, default=16384)
     ap.add_argument("--d", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -81,9 +90,15 @@ def parse():
     return ap.parse_args()
 
 
+_SETTLE = {"ms": 0.0, "done": False, "spent": 0.0}
+
+
 def time_op(fn, steps, warmup):
     import torch
 
+    if not _SETTLE["done"] and _SETTLE["ms"] > 0:  # once per process, before the first timing
+        _SETTLE["spent"] = settle(fn, _SETTLE["ms"])
+        _SETTLE["done"] = True
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -101,28 +116,109 @@ def time_op(fn, steps, warmup):
     return ev_ms, wall * 1e3 / steps
 
 
-def cpu_baseline_l2(n, d, budget_s=15.0):
-    """torch.cdist(p=2) on the host (the reference's at::cdist) over a row sample of x1
-    against the full x2, scaled to pair-features/s."""
+def settle(fn, ms):
+    """Calls fn for about `ms` of wall time (synchronising every 20 calls); returns the time."""
     import torch
 
-    g1 = torch.Generator().manual_seed(0)
-    g2 = torch.Generator().manual_seed(1)
-    x2 = torch.randn(n, d, generator=g2)
-    rows = 1024
-    x1 = torch.randn(rows, d, generator=g1)
-    torch.cdist(x1, x2, 2)  # warm-up
-    reps, t_total = 0, 0.0
-    while t_total < budget_s and reps < 200:
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3
+
+
+def _timed(fn, budget_s, max_reps=200):
+    fn()  # warm-up
+    reps, total = 0, 0.0
+    while total < budget_s and reps < max_reps:
         t0 = time.perf_counter()
-        torch.cdist(x1, x2, 2)
-        t_total += time.perf_counter() - t0
+        fn()
+        total += time.perf_counter() - t0
         reps += 1
-    pf = rows * n * d
-    return {"value": pf * reps / t_total, "unit": "pair-features/s",
-            "cores": torch.get_num_threads(), "kind": "reference",
-            "sample": f"torch.cdist(x1[{rows},{d}], x2[{n},{d}], p=2) on CPU (= at::cdist of "
-                      f"euclidean_distances), {reps} reps, {t_total:.1f} s"}
+    return total / reps, reps
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(n, d, budget_s=3.0):
+    """The reference's CPU paths on the host cores of this process, on bounded samples of the
+    workloads (about 25 s in all), as pair-features/s.  The headline entry is euclidean:
+    torch.cdist(p = 2) = the reference's at::cdist (pairwise_metrics.cpp:24-31), with torch's
+    intra-op threads."""
+    import torch
+
+    threads = torch.get_num_threads()
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    g = lambda s: torch.Generator().manual_seed(s)  # noqa: E731
+    x2 = torch.randn(n, d, generator=g(1))
+    rows = 1024
+    x1 = torch.randn(rows, d, generator=g(0))
+    out = {}
+    for name, p in (("euclidean", 2.0), ("manhattan", 1.0)):
+        t, reps = _timed(lambda: torch.cdist(x1, x2, p), budget_s)
+        out[name] = {"value": rows * n * d / t, "unit": "pair-features/s", "cores": threads,
+                     "kind": "reference",
+                     "sample": f"torch.cdist(x1[{rows},{d}], x2[{n},{d}], p={p:g}) (= at::cdist of "
+                               f"{name}_distances), {reps} reps of {t * 1e3:.1f} ms"}
+    # the reference's own compiled CPU kernels, in a child process (their schemas would collide
+    # with this build's in this one): hamming on M rows, jaccard on C4 rows, one C5 cloud pair
+    try:
+        import tempfile
+
+        import numpy as np
+
+        from oracle import ref_runner
+        if ref_runner.available():
+            hr, jr, jd, cp = 256, 16, 1024, 65536
+            h1 = (torch.rand(hr, d, generator=g(0)) < 0.5).numpy()
+            h2 = (torch.rand(n, d, generator=g(1)) < 0.5).numpy()
+            j1 = (torch.rand(jr, jd, generator=g(0)) < 0.1).numpy()
+            j2 = (torch.rand(32768, jd, generator=g(1)) < 0.1).numpy()
+            c1 = torch.rand(1, cp, 3, generator=g(0)).numpy()
+            c2 = (torch.rand(1, cp, 3, generator=g(1)) + 0.05).numpy()
+            with tempfile.TemporaryDirectory() as tmp:
+                r = ref_runner.run("time", {"h1": h1, "h2": h2, "j1": j1, "j2": j2, "c1": c1, "c2": c2,
+                                            "budget": np.float64(budget_s)}, tmp)
+            res = json.loads(str(r["results"]))
+            for name, work, sample in (
+                    ("hamming", hr * n * d, f"pwne_mean(x1[{hr},{d}] bool, x2[{n},{d}] bool)"),
+                    ("jaccard", jr * 32768 * jd, f"prf_div(pwxor_sum, pwor_sum) on x1[{jr},{jd}], x2[32768,{jd}] bool"),
+                    ("directed_hausdorff", cp * cp * 3, f"_directed_hausdorff of one [{cp},3] cloud pair (C5)")):
+                t = res["hausdorff" if name == "directed_hausdorff" else name]["s_per_call"]
+                # (one cloud pair: the reference's OpenMP loop runs over cloud pairs, so one thread)
+                out[name] = {"value": work / t, "unit": "pair-features/s" if name != "directed_hausdorff"
+                             else "nominal pair-features/s", "cores": 1 if name == "directed_hausdorff" else 32,
+                             "kind": "reference",
+                             "sample": f"{sample}: the reference's compiled CPU kernel (OpenMP, "
+                                       f"num_threads(32) as compiled), "
+                                       f"{res['hausdorff' if name == 'directed_hausdorff' else name]['reps']} reps of "
+                                       f"{t * 1e3:.1f} ms"}
+        from oracle import cref
+        t, reps = _timed(lambda: cref.bool_reduce(h1, h2, "ne", True, threads=usable), budget_s)
+        out["hamming_port_all_cores"] = {
+            "value": 256 * n * d / t, "unit": "pair-features/s", "cores": usable, "kind": "port",
+            "sample": f"oracle/cref.c restatement of the pwne_mean loop on x1[256,{d}], x2[{n},{d}], "
+                      f"{reps} reps of {t * 1e3:.1f} ms"}
+    except Exception as e:  # a missing oracle build must not cost the GPU line
+        out["error"] = f"{type(e).__name__}: {e}"
+    head = dict(out["euclidean"])
+    head["cpu_model"] = _cpu_model()
+    head["os_cpu_count"] = os.cpu_count()
+    head["usable_cores"] = usable
+    head["others"] = {k: v for k, v in out.items() if k != "euclidean"}
+    return head
 
 
 def run_config(cfg, steps, warmup):
@@ -135,8 +231,19 @@ def run_config(cfg, steps, warmup):
     dev = "cuda"
     lines = []
 
+    def roof(bound, amount, ms, convention):
+        """roofline of one line: algorithmic flops / lane-ops / bytes per call over its time"""
+        rate = amount / (ms * 1e-3)
+        peak, unit, scale = {"mfma": (PEAK_FP32_MFMA, "TFLOP/s", 1e12),
+                             "mfma_bf16": (PEAK_BF16_MFMA, "TFLOP/s", 1e12),
+                             "valu": (PEAK_VALU_LANE_OPS, "Tlane-op/s", 1e12),
+                             "hbm": (PEAK_HBM, "GB/s", 1e9)}[bound]
+        return {"roofline": {"bound": bound.split("_")[0], "achieved": rate / scale, "peak": peak / scale,
+                             "unit": unit, "frac": rate / peak, "convention": convention}}
+
     def emit(name, ms, pf, extra=None):
-        d = {"config": cfg, "op": name, "ms_per_call": ms, "pair_features_per_s": pf / (ms * 1e-3)}
+        d = {"config": cfg, "op": name, "ms_per_call": ms, "pair_features_per_s": pf / (ms * 1e-3),
+             "steps": steps, "warmup": warmup, "settle_ms": _SETTLE["spent"]}
         d.update(extra or {})
         lines.append(d)
         print(json.dumps(d), flush=True)
@@ -151,7 +258,11 @@ def run_config(cfg, steps, warmup):
             for fn in ("euclidean_distances", "cosine_distances"):
                 f = getattr(tp, fn)
                 ms, _ = time_op(lambda: f(x1, x2), steps, warmup)
-                emit(f"{fn} fwd {dtype}", ms, pf, {"tflops": 2 * pf / (ms * 1e-3) / 1e12})
+                if dtype == torch.float32:
+                    r = roof("mfma", 2 * pf, ms, "2 flop per pair-feature (one multiply-add)")
+                else:
+                    r = roof("hbm", 2 * B * N * N, ms, "the bf16 output written once (2 B per pair)")
+                emit(f"{fn} fwd {dtype}", ms, pf, {"tflops": 2 * pf / (ms * 1e-3) / 1e12, **r})
                 a = x1.detach().requires_grad_()
                 b = x2.detach().requires_grad_()
 
@@ -161,7 +272,13 @@ def run_config(cfg, steps, warmup):
                     f(a, b).backward(g)
 
                 ms, _ = time_op(fb, steps, warmup)
-                emit(f"{fn} fwd+bwd {dtype}", ms, pf, {"tflops": 6 * pf / (ms * 1e-3) / 1e12})
+                if dtype == torch.float32:
+                    r = roof("mfma", 6 * pf, ms, "forward product + two backward products, 2 flop "
+                                                 "per pair-feature each")
+                else:
+                    r = roof("hbm", 6 * B * N * N, ms, "output written, upstream gradient and output read "
+                                                       "once (3 x 2 B per pair)")
+                emit(f"{fn} fwd+bwd {dtype}", ms, pf, {"tflops": 6 * pf / (ms * 1e-3) / 1e12, **r})
             del x1, x2, g
             torch.cuda.empty_cache()
     elif cfg == "C3":
@@ -170,7 +287,8 @@ def run_config(cfg, steps, warmup):
         x2 = (torch.rand(N, D, generator=torch.Generator().manual_seed(1)) * 2 - 1).to(dev)
         pf = N * N * D
         ms, _ = time_op(lambda: tp.minkowski_distances(x1, x2, 3.0), steps, warmup)
-        emit("minkowski p=3 fwd", ms, pf)
+        emit("minkowski p=3 fwd", ms, pf, roof("valu", 3 * pf, ms, "3 VALU lane-ops per pair-feature "
+                                               "(sub, |d| * d, fma) against the non-packed FP32 issue rate"))
         a, b = x1.clone().requires_grad_(), x2.clone().requires_grad_()
         ones = torch.ones(N, N, device=dev)
 
@@ -180,20 +298,24 @@ def run_config(cfg, steps, warmup):
             tp.minkowski_distances(a, b, 3.0).backward(ones)
 
         ms, _ = time_op(fb, steps, warmup)
-        emit("minkowski p=3 fwd+bwd", ms, pf)
+        emit("minkowski p=3 fwd+bwd", ms, pf, roof("valu", 9 * pf, ms, "3 VALU lane-ops per pair-feature "
+                                                   "forward and in each of the two backward directions"))
         ms, _ = time_op(lambda: tp.chebyshev_distances(x1, x2), steps, warmup)
-        emit("chebyshev fwd", ms, pf)
+        emit("chebyshev fwd", ms, pf, roof("valu", 1.5 * pf, ms, "1.5 VALU lane-ops per pair-feature "
+                                           "(v_sub, and v_max3 over two |d| per instruction)"))
     elif cfg == "C4":
         N, D = 32768, 1024
         h1 = (torch.rand(N, D, generator=torch.Generator().manual_seed(0)) < 0.5).to(dev)
         h2 = (torch.rand(N, D, generator=torch.Generator().manual_seed(1)) < 0.5).to(dev)
         pf = N * N * D
         ms, _ = time_op(lambda: tp.hamming_distances(h1, h2), steps, warmup)
-        emit("hamming fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+        emit("hamming fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9,
+                                     **roof("hbm", 4 * N * N, ms, "the fp32 output written once")})
         j1 = (torch.rand(N, D, generator=torch.Generator().manual_seed(0)) < 0.1).to(dev)
         j2 = (torch.rand(N, D, generator=torch.Generator().manual_seed(1)) < 0.1).to(dev)
         ms, _ = time_op(lambda: tp.jaccard_distances(j1, j2), steps, warmup)
-        emit("jaccard fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+        emit("jaccard fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9,
+                                     **roof("hbm", 4 * N * N, ms, "the fp32 output written once")})
         # the other boolean count metrics: one fused pass (pack + AND-popcount tile with the
         # metric's epilogue), the same on rows packed once (PackedBool), and the reference's
         # composite (2-4 pw*_sum passes + ATen elementwise passes) on the same GPU
@@ -202,14 +324,17 @@ def run_config(cfg, steps, warmup):
         for metric in ("dice", "yule"):
             f = getattr(tp, f"{metric}_distances")
             ms, _ = time_op(lambda: f(h1, h2), steps, warmup)
-            emit(f"{metric} fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+            emit(f"{metric} fwd", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9,
+                                           **roof("hbm", 4 * N * N, ms, "the fp32 output written once")})
             ms, _ = time_op(lambda: tp.packed.cdist(p1, p2, metric), steps, warmup)
-            emit(f"{metric} fwd on PackedBool", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9})
+            emit(f"{metric} fwd on PackedBool", ms, pf, {"out_GBps": 4 * N * N / (ms * 1e-3) / 1e9,
+                                                         **roof("hbm", 4 * N * N, ms, "the fp32 output written once")})
         def dice_composite():
             R = ops.pwxor_sum(h1, h2)
             return R / (2 * ops.pwand_sum(h1, h2) + R)
         ms, _ = time_op(dice_composite, steps, warmup)
-        emit("dice fwd, reference composite route", ms, pf)
+        emit("dice fwd, reference composite route", ms, pf,
+             roof("hbm", 4 * N * N, ms, "the fp32 output written once"))
     elif cfg == "KF":
         # kernel functions at the metric shape: polynomial / sigmoid fused into the MFMA
         # epilogue, rbf / laplacian into the VALU kernel's, each against the reference's
@@ -232,11 +357,16 @@ def run_config(cfg, steps, warmup):
                  lambda a, b: torch.ops.torchpairwise._ppminkowski(a, b, 2.0).mul_(-g).exp_()),
                 ("laplacian_kernel", lambda a, b: tp.laplacian_kernel(a, b),
                  lambda a, b: tp.manhattan_distances(a, b).mul_(-g).exp_())):
+            mf = name[0] in "ps"  # polynomial / sigmoid: the MFMA kernel; rbf / laplacian: VALU
+            conv = ("2 flop per pair-feature (one multiply-add)" if mf else
+                    "2 VALU lane-ops per pair-feature (sub, fma or abs-add)")
             ms, _ = time_op(lambda: f(x1, x2), steps, warmup)
-            emit(f"{name} fwd", ms, pf, {"tflops": 2 * pf / (ms * 1e-3) / 1e12})
+            emit(f"{name} fwd", ms, pf, {"tflops": 2 * pf / (ms * 1e-3) / 1e12,
+                                         **roof("mfma" if mf else "valu", 2 * pf, ms, conv)})
             ms, _ = time_op(lambda: ref(x1, x2), steps, warmup)
             emit(f"{name} fwd, " + ("reference composite route" if "kernel" in name and name[0] in "ps"
-                                    else "unfused route (distance kernel, mul_, exp_)"), ms, pf)
+                                    else "unfused route (distance kernel, mul_, exp_)"), ms, pf,
+                 roof("mfma" if mf else "valu", 2 * pf, ms, conv))
             a, b = x1.clone().requires_grad_(), x2.clone().requires_grad_()
 
             def fb():
@@ -245,14 +375,20 @@ def run_config(cfg, steps, warmup):
                 f(a, b).backward(ones)
 
             ms, _ = time_op(fb, steps, warmup)
-            emit(f"{name} fwd+bwd", ms, pf)
+            emit(f"{name} fwd+bwd", ms, pf, roof("mfma" if mf else "valu", 6 * pf, ms,
+                                                 "forward + two backward directions, 2 per "
+                                                 "pair-feature each"))
     elif cfg == "C5":
         C, P, D = 16, 65536, 3
         x1 = torch.rand(C, P, D, generator=torch.Generator().manual_seed(0)).to(dev)
         x2 = (torch.rand(C, P, D, generator=torch.Generator().manual_seed(1)) + 0.05).to(dev)
         pf = C * C * P * P * D
+        conv = ("brute-force equivalent: 8 VALU lane-ops per nominal point pair (3 sub, 3 mul, 2 add); "
+                "the pruned search evaluates a small fraction of the pairs, so frac above 1 is the "
+                "pruning's gain over a brute-force kernel at the VALU peak, not a VALU utilisation")
         ms, _ = time_op(lambda: tp.directed_hausdorff_distances(x1, x2), steps, warmup)
-        emit("directed_hausdorff fwd", ms, pf, {"note": "nominal B1*B2*P1*P2*D pair-features"})
+        emit("directed_hausdorff fwd", ms, pf, {"note": "nominal B1*B2*P1*P2*D pair-features",
+                                                **roof("valu", 8 * C * C * P * P, ms, conv)})
         a = x1.clone().requires_grad_()
         g = torch.randn(C, C, generator=torch.Generator().manual_seed(2)).to(dev)
 
@@ -261,7 +397,7 @@ def run_config(cfg, steps, warmup):
             tp.directed_hausdorff_distances(a, x2)[0].backward(g)
 
         ms, _ = time_op(fb, steps, warmup)
-        emit("directed_hausdorff fwd+bwd", ms, pf)
+        emit("directed_hausdorff fwd+bwd", ms, pf, roof("valu", 8 * C * C * P * P, ms, conv))
     elif cfg == "NB":
         # neighbour masks at the metric shape: the selection kernel alone on a resident
         # distance matrix (HBM-bound: 4 B read + 1 B written per entry), the whole drop-in
@@ -275,13 +411,15 @@ def run_config(cfg, steps, warmup):
             ms, _ = time_op(lambda: torch.ops.torchpairwise._row_smallest_mask(dist, k + 1), steps, warmup)
             emit(f"row_smallest_mask count={k + 1}", ms, pf,
                  {"hbm_GBps": 5.0 * N * N / (ms * 1e-3) / 1e9,
-                  "hbm_frac": 5.0 * N * N / (ms * 1e-3) / PEAK_HBM})
+                  "hbm_frac": 5.0 * N * N / (ms * 1e-3) / PEAK_HBM,
+                  **roof("hbm", 5.0 * N * N, ms, "each fp32 distance read once, one mask byte written")})
+        conv = "distances written and read once (4 + 4 B per entry) and one mask byte written"
         ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, 1), steps, warmup)
-        emit("k_neighbors_mask k=1 (euclidean + selection)", ms, pf)
+        emit("k_neighbors_mask k=1 (euclidean + selection)", ms, pf, roof("hbm", 9.0 * N * N, ms, conv))
         ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, 16), steps, warmup)
-        emit("k_neighbors_mask k=16 (euclidean + selection)", ms, pf)
+        emit("k_neighbors_mask k=16 (euclidean + selection)", ms, pf, roof("hbm", 9.0 * N * N, ms, conv))
         ms, _ = time_op(lambda: tp.radius_neighbors_mask(x1, x2, 14.0), steps, warmup)
-        emit("radius_neighbors_mask eps=14 (euclidean + le)", ms, pf)
+        emit("radius_neighbors_mask eps=14 (euclidean + le)", ms, pf, roof("hbm", 9.0 * N * N, ms, conv))
 
         def ref_route():
             inds = dist.argsort(1, False)[:, :2]
@@ -291,7 +429,8 @@ def run_config(cfg, steps, warmup):
             return out
 
         ms, _ = time_op(ref_route, max(1, steps // 5), 1)
-        emit("reference route argsort+index_put_ k=1 (selection only)", ms, pf)
+        emit("reference route argsort+index_put_ k=1 (selection only)", ms, pf,
+             roof("hbm", 5.0 * N * N, ms, "each fp32 distance read once, one mask byte written"))
     else:
         raise SystemExit(f"unknown config {cfg}")
     return lines
@@ -303,6 +442,7 @@ def main():
         print(json.dumps({"error": "this build measures one GPU; run with --gpus 1 "
                                    "(multi-GPU sharding is described in DESIGN.md, not run)"}))
         sys.exit(2)
+    _SETTLE["ms"] = args.settle_ms
     if args.config != "M":
         import torch
 
@@ -334,6 +474,7 @@ def main():
     res = {}
 
     if "l2" in only:
+        time_op(lambda: tp.euclidean_distances(x1, x2), 1, 0)  # the settle phase (once)
         ms, wall_ms = time_op(lambda: tp.euclidean_distances(x1, x2), args.steps, args.warmup)
         # the dominant kernel alone: the same MFMA launch through the C ABI with the row norms
         # computed once, timed with events on the stream it is launched on (torch's current)
@@ -347,8 +488,8 @@ def main():
                      "roofline": {"bound": "mfma", "achieved": flops / (k_ms * 1e-3) / 1e12,
                                   "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                                   "frac": flops / (k_ms * 1e-3) / PEAK_FP32_MFMA,
-                                  "traffic": measured_traffic("pairwise_inner_kernel<float,float,1,true>"),
-                                  "kernel": "pairwise_inner_kernel<float,float,1,true>",
+                                  "traffic": measured_traffic("pairwise_inner_kernel<float,float,1,true,true>"),
+                                  "kernel": "pairwise_inner_kernel<float,float,1,true,true>",
                                   "kernel_ms": k_ms}}
     if "l1" in only:
         ms, wall_ms = time_op(lambda: tp.manhattan_distances(x1, x2), args.steps, args.warmup)
@@ -382,6 +523,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": _SETTLE["spent"],
         "ms_per_step": head["ms"] if head else None,
         "higher_is_better": True,
         "scaling": "weak",
@@ -395,7 +537,7 @@ def main():
         "extra": extra,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline_l2(n, d)
+        line["cpu_baseline"] = cpu_baseline(n, d)
     print(json.dumps(line), flush=True)
 
 

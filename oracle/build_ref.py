@@ -3,7 +3,8 @@
 lie under /root/reference, into oracle/_ref/libtorchpairwise_ref.so (git-ignored; it travels
 to the GPU box like the other built libraries).  TEST INFRASTRUCTURE ONLY.
 
-Sources (g++ directly, against the installed torch headers; nothing is copied):
+Sources (g++ directly, against the installed torch headers, with the reference's own OpenMP
+flags; nothing is copied):
   csrc/ops/hausdorff.cpp, cpu/hausdorff_kernel.cpp, autograd/hausdorff_kernel.cpp
   csrc/ops/pairwise_binary.cpp, cpu/pairwise_binary_kernels.cpp
   csrc/ops/prf_div.cpp, cpu/prf_div_kernel.cpp, autograd/prf_div_kernel.cpp
@@ -39,7 +40,10 @@ def main() -> int:
 
     def compile_one(src):
         obj = OUT / (src.replace("/", "_") + ".o")
-        subprocess.run(["g++", "-O2", "-std=c++17", "-fPIC", "-fopenmp", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        # -DAT_PARALLEL_OPENMP + -fopenmp: the reference's setup.py:26-56,89-91 (its CPU loops
+        # then run on OpenMP with num_threads(32), cpu/cpu_helpers.h:6-18)
+        subprocess.run(["g++", "-O2", "-std=c++17", "-fPIC", "-fopenmp", "-DAT_PARALLEL_OPENMP",
+                        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
                         *inc, f"-I{REF}", "-c", str(REF / src), "-o", str(obj)], check=True)
         return obj
 

@@ -11,6 +11,9 @@ usage: python oracle/ref_runner.py <op> <in.npz> <out.npz>
        jaccard     (x1, x2) -> out             (prf_div(pwxor_sum, pwor_sum), the reference's composite)
        prf         cases (JSON) + c<i>_a / _b / _g arrays -> c<i>_<result> arrays and c<i>_err
                    messages: the 20 prf_div-family ops through run_prf_case
+       time        h1, h2 (bool), j1, j2 (bool), c1, c2 (clouds), budget -> seconds per call of
+                   the reference's pwne_mean (hamming), its jaccard composite and its
+                   _directed_hausdorff, each repeated within the budget (the CPU baseline)
 """
 import json
 import subprocess
@@ -171,6 +174,23 @@ def main(op: str, src: str, dst: str) -> None:
             meta.append({"tags": tags})
         arrays["results"] = np.array(json.dumps(meta))
         np.savez(dst, **arrays)
+    elif op == "time":
+        import time
+        budget = float(d["budget"])
+        work = {"hamming": lambda: ops.pwne_mean(t["h1"], t["h2"]),
+                "jaccard": lambda: ops.prf_div(ops.pwxor_sum(t["j1"], t["j2"]), ops.pwor_sum(t["j1"], t["j2"]), "zero"),
+                "hausdorff": lambda: ops._directed_hausdorff(t["c1"], t["c2"])}
+        res = {}
+        for name, fn in work.items():
+            fn()  # warm-up
+            reps, total = 0, 0.0
+            while total < budget and reps < 100:
+                t0 = time.perf_counter()
+                fn()
+                total += time.perf_counter() - t0
+                reps += 1
+            res[name] = {"s_per_call": total / reps, "reps": reps}
+        np.savez(dst, results=np.array(json.dumps(res)))
     elif op == "jaccard":
         np.savez(dst, out=ops.prf_div(ops.pwxor_sum(t["x1"], t["x2"]), ops.pwor_sum(t["x1"], t["x2"]), "zero").numpy())
     else:

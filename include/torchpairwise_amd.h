@@ -355,6 +355,19 @@ int tpw_sqjensenshannon_backward(const float *grad, const float *x1, const float
 /* Workspace (bytes) of tpw_haversine / tpw_haversine_backward. */
 size_t tpw_haversine_workspace_size(int64_t batch, int64_t n, int64_t m);
 
+/* Workspace (bytes) of tpw_sqmahalanobis for these sizes (dtype TPW_F32 or TPW_F64). */
+size_t tpw_sqmahalanobis_workspace_size(int dtype, int64_t batch, int64_t n, int64_t m, int64_t d);
+
+/* out[b,i,j] = d^T VI[b] d with d = x1[b,i,:] - x2[b,j,:] (x1 [batch,n,d], x2 [batch,m,d],
+ * VI [batch,d,d], dtype TPW_F32 or TPW_F64).  Computed as sum_k d_k (P1[i,k] - P2[j,k]) with
+ * the per-row projections P = x VI^T formed once (in double, carried as two floats for
+ * TPW_F32): O(d) per pair instead of the reference's O(d^2), and, as there, the difference
+ * comes first, so identical rows give exactly 0.  x2 may be x1 (n == m): the projection is
+ * then formed once.  Replaces _sqmahalanobis_forward_kernel
+ * (csrc/ops/cpu/sqmahalanobis_kernel.cpp:11-88; CUDA cuda/sqmahalanobis_kernel.cu:16-100). */
+int tpw_sqmahalanobis(const void *x1, const void *x2, const void *VI, int dtype, int64_t batch,
+                      int64_t n, int64_t m, int64_t d, void *out, void *workspace, void *stream);
+
 /* out[b,i,j] = 2 asin(sqrt(sin^2(dlat/2) + cos lat_i cos lat_j sin^2(dlon/2))) for points
  * x1 [batch, n, 2], x2 [batch, m, 2] given as (latitude, longitude) in radians.  Replaces
  * _haversine (haversine.cpp:30-32, cpu/haversine_kernel.cpp:13-27,29-75). */

@@ -399,6 +399,63 @@ def test_special_ops_gpu_batched_and_cdist():
     assert_close(v.grad.cpu(), vr.grad, rtol=1e-4, atol=1e-4 * float(vr.grad.abs().max()), what="grad VI")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64])
+def test_mahalanobis_self_and_near_duplicates(dtype):
+    """mahalanobis_distances(x) with the default VI (inverse covariance): the diagonal is exactly
+    0 and nothing is NaN; rows within 1e-3 of each other match the reference's per-pair loop
+    (the CPU op, cpu/sqmahalanobis_kernel.cpp:13-33, evaluated in float64)."""
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(2000, 24, generator=gen).to(dtype)
+    VI = torch.cov(x.double().T).inverse().T.contiguous()
+    # bf16: at::cov(...).inverse() of the default VI raises for 16-bit types (as in the
+    # reference's functor), so VI is passed
+    kw = {"VI": VI.to(dtype).to(DEV)} if dtype == torch.bfloat16 else {}
+    d = tp.mahalanobis_distances(x.to(DEV), **kw)
+    assert d.dtype == dtype and not bool(torch.isnan(d).any())
+    assert bool((torch.diagonal(d) == 0).all())
+    near = (x.double() + 1e-3 * torch.randn(2000, 24, generator=gen, dtype=torch.float64)).to(dtype)
+    a, b, v = x[:300], near[:200], VI.to(dtype)
+    got = torch.ops.torchpairwise._sqmahalanobis(a.to(DEV), b.to(DEV), v.to(DEV))
+    ref = torch.ops.torchpairwise._sqmahalanobis(a.double(), b.double(), v.double())
+    assert bool((got >= 0).all())  # VI is positive definite
+    rtol = {torch.float32: 1e-5, torch.float64: 1e-12, torch.bfloat16: 1e-2}[dtype]
+    assert_close(got.double(), ref, rtol=rtol, atol=rtol * float(ref.abs().max()), what="near rows")
+    # the near pairs themselves (|d| ~ 1e-3 |x|): relative accuracy, not just absolute
+    idx = torch.arange(200)
+    pair = got.double().cpu()[idx, idx]
+    want = ref[idx, idx]
+    assert_close(pair, want, rtol=64 * rtol if dtype != torch.bfloat16 else 1e-2, atol=0, what="near pairs")
+
+
+def test_sqmahalanobis_capi_shapes():
+    """tpw_sqmahalanobis through the C ABI: edge tiles, d not a multiple of 16, d = 0, x2 the
+    same buffer as x1, batched VI, float64."""
+    from torchpairwise_amd import _capi as capi
+
+    gen = torch.Generator().manual_seed(12)
+    for B, n, m, d, dt in ((1, 65, 130, 17, torch.float32), (3, 7, 5, 1, torch.float32), (2, 40, 33, 0, torch.float32),
+                           (2, 64, 64, 16, torch.float64), (1, 129, 1, 48, torch.float64)):
+        x1 = torch.randn(B, n, d, generator=gen, dtype=dt)
+        x2 = torch.randn(B, m, d, generator=gen, dtype=dt)
+        VI = torch.randn(B, d, d, generator=gen, dtype=dt)
+        code = capi.TPW_F32 if dt == torch.float32 else capi.TPW_F64
+        for same in (False, True):
+            a = x1.to(DEV)
+            b = a if same else x2.to(DEV)
+            mm = n if same else m
+            out = torch.full((B, n, mm), float("nan"), dtype=dt, device=DEV)
+            ws = torch.empty(max(1, capi.lib().tpw_sqmahalanobis_workspace_size(code, B, n, mm, d)),
+                             dtype=torch.uint8, device=DEV)
+            capi.call("tpw_sqmahalanobis", a.data_ptr(), b.data_ptr(), VI.to(DEV).data_ptr(), code, B, n, mm, d,
+                      out.data_ptr(), ws.data_ptr(), capi._stream())
+            want = P.sqmahalanobis(x1.double(), (x1 if same else x2).double(), VI.double())
+            tol = 1e-5 if dt == torch.float32 else 1e-12
+            assert_close(out.cpu().double(), want, rtol=tol, atol=tol * float(want.abs().max()) + 1e-30,
+                         what=f"B={B} n={n} m={mm} d={d} same={same}")
+            if same:
+                assert bool((torch.diagonal(out, dim1=1, dim2=2) == 0).all())
+
+
 # --------------------------------------------------------------------------------------
 # polynomial_kernel / sigmoid_kernel: the function fused into the MFMA epilogue; the
 # reference's composite (matmul, mul_, add_, pow_ / tanh_) in float64 on the CPU is the bar

@@ -2,15 +2,14 @@
 // __*_backward ops (csrc/ops/{haversine,snr,sqmahalanobis}.cpp), CPU, GPU and Autograd.
 //
 // _haversine runs HIP kernels on the GPU (haversine.hip; fp32, 16-bit types through fp32).
-// _snr and _sqmahalanobis are compositions on the GPU:
+// _snr is a composition on the GPU:
 //   _snr(x1, x2)[i, j] = V1[i] / DV[i, j], V1 = sum_k (x1 - mean x1)^2 and
 //     DV = sum_k (d - mean d)^2 with d = x2[j] - x1[i]; since mean d = mean x2[j] - mean x1[i],
 //     DV is the squared distance between the row-centred points, i.e. _ppminkowski(x1c, x2c, 2)
-//     on the VALU kernel;
-//   _sqmahalanobis(x1, x2, VI)[i, j] = d^T VI d = q1[i] + q2[j] - x1[i] (VI + VI^T) x2[j]^T with
-//     q = rowsum((x VI) * x): two library GEMMs instead of the reference's O(d^2) per pair.
-// Their gradients come from autograd through those compositions (the same derivatives as the
-// reference's backward formulas).  CPU tensors run loops restating the reference's kernels.
+//     on the VALU kernel; its gradient comes from autograd through that composition.
+// _sqmahalanobis runs mahalanobis.hip on the GPU: d^T VI d from the difference d and per-row
+// projections x VI^T, O(d) per pair; its backward uses the matrix-core sqeuclidean products.
+// CPU tensors run loops restating the reference's kernels.
 #include "tpw_common.h"
 
 #include <ATen/Parallel.h>
@@ -377,25 +376,72 @@ T3 sqmahalanobis_backward_cpu(const at::Tensor &grad, const at::Tensor &x1, cons
     return {unbatch(gx1, ub), unbatch(gx2, ub), unbatch(gw, ub)};
 }
 
-// GPU composition: q1 + q2 - x1 (VI + VI^T) x2^T (library GEMMs; right operands contiguous)
-at::Tensor sqmahalanobis_composite(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
-    check_mahalanobis(x1, x2, VI);
-    auto q1 = (at::matmul(x1, VI) * x1).sum(-1);
-    auto q2 = (at::matmul(x2, VI) * x2).sum(-1);
-    auto cross = at::matmul(at::matmul(x1, (VI + VI.mT()).contiguous()), x2.mT().contiguous());
-    return q1.unsqueeze(-1) + q2.unsqueeze(-2) - cross;
+// GPU: d^T VI d per pair from the difference d and the per-row projections x VI^T
+// (tpw_sqmahalanobis, mahalanobis.hip).  16-bit types compute in float32, float64 in double.
+at::ScalarType mahalanobis_compute_type(at::ScalarType t) {
+    TORCH_CHECK(at::isFloatingType(t), "\"_sqmahalanobis_forward_cuda\" not implemented for '", t, "'");
+    return t == at::kDouble ? at::kDouble : at::kFloat;
 }
 
 at::Tensor sqmahalanobis_cuda(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
-    return sqmahalanobis_composite(x1, x2, VI);
+    const bool ub = check_mahalanobis(x1, x2, VI);
+    DeviceGuard guard(x1.device());
+    const auto dt = x1.scalar_type(), ct = mahalanobis_compute_type(dt);
+    auto a = batched(x1, ub).to(ct);
+    auto b = x2.is_same(x1) ? a : batched(x2, ub).to(ct);
+    auto w = batched(VI, ub).to(ct);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    const int code = ct == at::kDouble ? TPW_F64 : TPW_F32;
+    auto out = at::empty({B, n, m}, a.options());
+    auto ws = workspace(tpw_sqmahalanobis_workspace_size(code, B, n, m, d), a);
+    check_rc(tpw_sqmahalanobis(a.data_ptr(), b.data_ptr(), w.data_ptr(), code, B, n, m, d, out.data_ptr(),
+                               ws.data_ptr(), current_stream()),
+             "_sqmahalanobis");
+    return unbatch(out.to(dt), ub);
 }
 
+// Gradients with the reference's formulas (cpu/sqmahalanobis_kernel.cpp:91-164), regrouped:
+// with H1[i] = sum_j g[i,j] (x1[i] - x2[j]) and H2[j] = sum_i g[i,j] (x2[j] - x1[i]),
+// grad_x1 = H1 (VI + VI^T), grad_x2 = H2 (VI + VI^T), grad_VI = x1^T H1 + x2^T H2.  H1 and H2
+// are half of the sqeuclidean gradients, whose g x2 / g^T x1 products run on the matrix cores
+// (tpw_sqeuclidean_backward); H (VI + VI^T) runs there too (tpw_pairwise_inner, DOT: the
+// right operand is symmetric).  float64 forms the same sums with ATen products.
 T3 sqmahalanobis_backward_cuda(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2,
                                const at::Tensor &VI) {
-    auto g = composite_grads(
-        [](const std::vector<Variable> &v) { return sqmahalanobis_composite(v[0], v[1], v[2]); }, grad,
-        {x1, x2, VI});
-    return {g[0], g[1], g[2]};
+    const bool ub = check_mahalanobis(x1, x2, VI);
+    DeviceGuard guard(x1.device());
+    const auto dt = x1.scalar_type(), ct = mahalanobis_compute_type(dt);
+    auto a = batched(x1, ub).to(ct), b = batched(x2, ub).to(ct), w = batched(VI, ub).to(ct);
+    auto g = batched(grad, ub).to(ct);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto S = (w + w.mT()).contiguous();
+    at::Tensor H1, H2, gx1, gx2;
+    if (ct == at::kFloat && n > 0 && m > 0 && d > 0) {
+        void *s = current_stream();
+        H1 = at::empty_like(a);
+        H2 = at::empty_like(b);
+        auto ws = workspace(tpw_inner_backward_workspace_size(B, n, m, d), a);
+        check_rc(tpw_sqeuclidean_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(), TPW_F32, B, n, m, d,
+                                          H1.data_ptr(), H2.data_ptr(), ws.data_ptr(), s),
+                 "__sqmahalanobis_backward");
+        H1.mul_(0.5);
+        H2.mul_(0.5);
+        gx1 = at::empty_like(a);
+        gx2 = at::empty_like(b);
+        check_rc(tpw_pairwise_inner(H1.data_ptr(), S.data_ptr(), TPW_F32, B, n, d, d, nullptr, nullptr,
+                                    TPW_EPI_DOT, gx1.data_ptr(), s),
+                 "__sqmahalanobis_backward");
+        check_rc(tpw_pairwise_inner(H2.data_ptr(), S.data_ptr(), TPW_F32, B, m, d, d, nullptr, nullptr,
+                                    TPW_EPI_DOT, gx2.data_ptr(), s),
+                 "__sqmahalanobis_backward");
+    } else {
+        H1 = a * g.sum(-1, true) - at::matmul(g, b);
+        H2 = b * g.sum(-2).unsqueeze(-1) - at::matmul(g.mT(), a);
+        gx1 = at::matmul(H1, S);
+        gx2 = at::matmul(H2, S);
+    }
+    auto gw = at::matmul(a.mT(), H1) + at::matmul(b.mT(), H2);
+    return {unbatch(gx1.to(dt), ub), unbatch(gx2.to(dt), ub), unbatch(gw.to(dt), ub)};
 }
 
 // ================================================================== autograd
@@ -471,8 +517,8 @@ class SqMahalanobisFunction : public torch::autograd::Function<SqMahalanobisFunc
     }
 };
 
-// GPU tensors differentiate through the composition itself (one graph of the VALU kernel's
-// and the GEMMs' own backward); CPU tensors through the reference-formula backward op.
+// GPU snr differentiates through its composition (the VALU kernel's own backward); the other
+// ops, on either device, through the reference-formula backward op.
 at::Tensor haversine_autograd(const at::Tensor &x1, const at::Tensor &x2) {
     return HaversineFunction::apply(x1, x2);
 }
@@ -481,7 +527,6 @@ at::Tensor snr_autograd(const at::Tensor &x1, const at::Tensor &x2) {
     return SnrFunction::apply(x1, x2);
 }
 at::Tensor sqmahalanobis_autograd(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {
-    if (x1.is_cuda()) return sqmahalanobis_composite(x1, x2, VI);
     return SqMahalanobisFunction::apply(x1, x2, VI);
 }
 

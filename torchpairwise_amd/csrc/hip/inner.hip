@@ -10,8 +10,15 @@
 //   fp32: v_mfma_f32_32x32x2_f32, 16 per chunk and 32 x 32 block
 //   bf16: v_mfma_f32_32x32x16_bf16 (gfx950), 4 per chunk and block, fp32 accumulation
 // The epilogue (norms, sqrt, guarded divide, clip) is applied to the accumulators in
-// registers and the result is written once with non-temporal stores.  The next chunk's
-// global loads are issued before the current chunk's MFMAs (register prefetch).
+// registers and the result is written once with non-temporal stores.
+// Operand staging, two paths:
+//   direct (every chunk full: d a multiple of the chunk, 16-byte rows): the chunk goes from
+//     global memory straight into LDS with global_load_lds_dwordx4, no registers in between;
+//     each wave covers 9 x 64 of the 2304 16-byte slots of the padded A|B panels (a pad slot
+//     loads a duplicate piece that is never read; rows past the edge load the last row,
+//     whose outputs are not stored).  120 VGPRs: 4 waves per SIMD, 4 blocks per CU;
+//   register prefetch (any d): the next chunk's global loads are issued into registers
+//     before the current chunk's MFMAs, and stored to LDS after them (zero padding past d).
 // Tiles are assigned XCD-contiguously (consecutive workgroup ids go round-robin over the
 // 8 XCDs, so id % 8 selects the XCD) and in groups of 8 tile rows, so that the blocks
 // resident on one XCD share A and B panels in that XCD's L2.
@@ -160,7 +167,11 @@ __device__ __forceinline__ void mfma_piece(floatx16 (&acc)[2][2], const uint4 (&
     }
 }
 
-template <typename T, typename OutT, int EPI, bool VEC>
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kSlotsPerWave = 9;  // 2 panels x 128 rows x 9 slots / 4 waves / 64 lanes
+
+template <typename T, typename OutT, int EPI, bool VEC, bool DIRECT>
 __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
     const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
@@ -203,32 +214,62 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
 
     const int64_t nchunks = (d + KC - 1) / KC;
     if (nchunks == 0) __syncthreads();
-    uint4 pa[4], pb[4];
+    uint4 pa[DIRECT ? 1 : 4], pb[DIRECT ? 1 : 4];
+    int32_t off[DIRECT ? kSlotsPerWave : 1];
+    if constexpr (DIRECT) {
+        // element offsets (from the panel's batch base) of this lane's slot in each of its 9
+        // wave loads: slot s -> panel s / 1152, row (s % 1152) / 9, piece (s % 1152) % 9
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int idx = tid + kThreads * q;
-        const int r = idx >> 3, c = idx & 7;
-        pa[q] = load_piece<T, VEC>(A, n, d, row0 + r, (int64_t)c * E);
-        pb[q] = load_piece<T, VEC>(B, m, d, col0 + r, (int64_t)c * E);
-    }
-
-    for (int64_t kc = 0; kc < nchunks; ++kc) {
+        for (int j = 0; j < kSlotsPerWave; ++j) {
+            const int sl = (wave * kSlotsPerWave + j) * 64 + lane;
+            const int panel = sl >= kTile * kLdsStride;
+            const int s2 = sl - panel * kTile * kLdsStride;
+            const int r = s2 / kLdsStride, c0 = s2 - r * kLdsStride;
+            const int c = c0 == kRowVec ? kRowVec - 1 : c0;
+            const int64_t lim = panel ? m : n;
+            int64_t row = (panel ? col0 : row0) + r;
+            row = row < lim ? row : lim - 1;
+            off[j] = (int32_t)(row * d + c * E);
+        }
+    } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int idx = tid + kThreads * q;
             const int r = idx >> 3, c = idx & 7;
-            As[r * kLdsStride + c] = pa[q];
-            Bs[r * kLdsStride + c] = pb[q];
+            pa[q] = load_piece<T, VEC>(A, n, d, row0 + r, (int64_t)c * E);
+            pb[q] = load_piece<T, VEC>(B, m, d, col0 + r, (int64_t)c * E);
         }
-        __syncthreads();
-        if (kc + 1 < nchunks) {
-            const int64_t kb = (kc + 1) * KC;
+    }
+
+    for (int64_t kc = 0; kc < nchunks; ++kc) {
+        if constexpr (DIRECT) {
+            const int64_t kb = kc * KC;
+#pragma unroll
+            for (int j = 0; j < kSlotsPerWave; ++j) {
+                const int first = (wave * kSlotsPerWave + j) * 64;  // wave-uniform LDS slot
+                const T *src = (first >= kTile * kLdsStride ? B : A) + kb + off[j];
+                __builtin_amdgcn_global_load_lds((global_void *)src, (lds_void *)(smem + first), 16, 0, 0);
+            }
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's slots have landed
+            __syncthreads();
+        } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int idx = tid + kThreads * q;
                 const int r = idx >> 3, c = idx & 7;
-                pa[q] = load_piece<T, VEC>(A, n, d, row0 + r, kb + (int64_t)c * E);
-                pb[q] = load_piece<T, VEC>(B, m, d, col0 + r, kb + (int64_t)c * E);
+                As[r * kLdsStride + c] = pa[q];
+                Bs[r * kLdsStride + c] = pb[q];
+            }
+            __syncthreads();
+            if (kc + 1 < nchunks) {
+                const int64_t kb = (kc + 1) * KC;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int idx = tid + kThreads * q;
+                    const int r = idx >> 3, c = idx & 7;
+                    pa[q] = load_piece<T, VEC>(A, n, d, row0 + r, kb + (int64_t)c * E);
+                    pb[q] = load_piece<T, VEC>(B, m, d, col0 + r, kb + (int64_t)c * E);
+                }
             }
         }
 #pragma unroll
@@ -373,7 +414,11 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
     const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
     const int64_t total = tiles_n * tiles_m * batch;
     const bool vec = ((d * (int64_t)sizeof(T)) % 16 == 0) && aligned16(x1) && aligned16(x2);
-    auto kernel = vec ? pairwise_inner_kernel<T, OutT, EPI, true> : pairwise_inner_kernel<T, OutT, EPI, false>;
+    // direct LDS loads: every chunk full, and the per-lane element offsets fit in int32
+    const bool direct = vec && d % Elem<T>::kChunk == 0 && d > 0 && (n > m ? n : m) * d < ((int64_t)1 << 31);
+    auto kernel = direct ? pairwise_inner_kernel<T, OutT, EPI, true, true>
+                  : vec  ? pairwise_inner_kernel<T, OutT, EPI, true, false>
+                         : pairwise_inner_kernel<T, OutT, EPI, false, false>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(kThreads), 0, s, x1, x2, n, m, d, aux1,
                        aux2, out, tiles_n, tiles_m, total, X, sign, kp);
     return check_launch("pairwise_inner_kernel");

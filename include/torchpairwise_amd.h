@@ -213,6 +213,7 @@ int tpw_compare_reduce(const void *x1, const void *x2, int elem_type, int64_t ba
 #define TPW_EPI_SQEUCLIDEAN 2 /* max(0, |x1|^2 + |x2|^2 - 2 s)                */
 #define TPW_EPI_COSINE_SIM 3  /* prf_div(s, |x1| |x2|, "identity")            */
 #define TPW_EPI_COSINE_DIST 4 /* clip(1 - prf_div(s, |x1||x2|, identity), 0, 2) */
+#define TPW_EPI_CORRELATION 5 /* 1 - prf_div(s, |x1||x2|, identity), no clip     */
 
 /* norms[r] = sum_k x[r,k]^2 (squared != 0) or its square root, in float32.
  * Replaces x.pow(2).sum(-1) / x.norm(2, -1) feeding _euclidean_dist
@@ -227,8 +228,10 @@ int tpw_row_norms(const void *x, int dtype, int64_t rows, int64_t d, int squared
  * for EUCLIDEAN/SQEUCLIDEAN, the norms for COSINE_*, unused (may be NULL) for DOT.
  * `out` has the element type of the inputs.
  * Replaces at::cdist(x1, x2, 2) on its matrix-product path (_euclidean_dist,
- * csrc/ops/pairwise_metrics.cpp:24-31), and matmul + prf_div (+ 1 - s, clip) of
- * cosine_similarity / cosine_distances (csrc/ops/pairwise_metrics.cpp:51-56,112-122). */
+ * csrc/ops/pairwise_metrics.cpp:24-31), matmul + prf_div (+ 1 - s, clip) of
+ * cosine_similarity / cosine_distances (csrc/ops/pairwise_metrics.cpp:51-56,112-122), the
+ * matmul of linear_kernel (DOT, :58-65) and, on centred rows, correlation_distances'
+ * matmul + prf_div + neg_ + add_(1) (CORRELATION, :190-204). */
 int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int64_t batch,
                        int64_t n, int64_t m, int64_t d, const float *aux1,
                        const float *aux2, int epilogue, void *out, void *stream);
@@ -407,13 +410,21 @@ int tpw_sqeuclidean_backward(const void *grad, const void *x1, const void *x2, i
                              int64_t batch, int64_t n, int64_t m, int64_t d, void *grad_x1,
                              void *grad_x2, void *workspace, void *stream);
 
+/* Backward of linear_kernel (x1 . x2^T): grad_x1 = grad . x2, grad_x2 = grad^T . x1 on the
+ * matrix cores (the autograd of the reference's matmul, pairwise_metrics.cpp:58-65).
+ * Workspace: tpw_inner_backward_workspace_size(batch, n, m, d) bytes. */
+int tpw_linear_backward(const void *grad, const void *x1, const void *x2, int dtype,
+                        int64_t batch, int64_t n, int64_t m, int64_t d, void *grad_x1,
+                        void *grad_x2, void *workspace, void *stream);
+
 /* Backward of cosine_distances = clip(1 - prf_div(x1 x2^T, n1 n2^T, identity), 0, 2):
  * the autograd graph of csrc/ops/pairwise_metrics.cpp:51-56,112-122 with the prf_div
  * backward of csrc/ops/cpu/prf_div_kernel.cpp:258-277, the clamp mask of
  * derivatives.yaml (grad where min <= x <= max) and torch's 2-norm backward (0 where the
- * norm is 0).  `norms1`/`norms2` are the fp32 row norms of x1/x2.  With `similarity` != 0
- * the op is cosine_similarity (no 1 - s, no clip).  When x2 is x1 (x2=None upstream),
- * the caller adds the two halves. */
+ * norm is 0).  `norms1`/`norms2` are the fp32 row norms of x1/x2.  `similarity` = 1: the
+ * op is cosine_similarity (no 1 - s, no clip); 2: correlation_distances' 1 - s without the
+ * clip (pairwise_metrics.cpp:190-204, neg_ then add_(1)) of rows the caller has centred.
+ * When x2 is x1 (x2=None upstream), the caller adds the two halves. */
 int tpw_cosine_backward(const void *grad, const void *x1, const void *x2,
                         const float *norms1, const float *norms2, int dtype,
                         int64_t batch, int64_t n, int64_t m, int64_t d, int similarity,

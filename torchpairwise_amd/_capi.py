@@ -50,6 +50,7 @@ _SIGNATURES = {
     "tpw_euclidean_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "tpw_sqeuclidean_backward": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "tpw_cosine_backward": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p]),
+    "tpw_linear_backward": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "tpw_sqmahalanobis_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64]),
     "tpw_sqmahalanobis": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p]),
     "tpw_prf_div": (_i, [_p, _p, _i, _i64, _i, _p, _p]),

@@ -59,7 +59,8 @@ constexpr int kEpiSigmoid = 102;
 // Row / column norms read by the epilogue (aux1 also carries the gradient coefficients).
 template <int EPI>
 constexpr bool kAux1 = EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN ||
-                       EPI == TPW_EPI_COSINE_SIM || EPI == TPW_EPI_COSINE_DIST || EPI == kEpiGrad;
+                       EPI == TPW_EPI_COSINE_SIM || EPI == TPW_EPI_COSINE_DIST ||
+                       EPI == TPW_EPI_CORRELATION || EPI == kEpiGrad;
 template <int EPI>
 constexpr bool kAux2 = kAux1<EPI> && EPI != kEpiGrad;
 
@@ -95,6 +96,7 @@ __device__ __forceinline__ float epilogue(float s, float a1, float a2, const Ker
         float q = den != 0.0f ? __fdiv_rn(s, den) : s;
         if constexpr (EPI == TPW_EPI_COSINE_SIM) return q;
         float v = 1.0f - q;
+        if constexpr (EPI == TPW_EPI_CORRELATION) return v;
         return fminf(fmaxf(v, 0.0f), 2.0f);
     }
 }
@@ -432,6 +434,7 @@ int dispatch_epi(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
         case TPW_EPI_EUCLIDEAN: return launch_inner<T, TPW_EPI_EUCLIDEAN>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
         case TPW_EPI_SQEUCLIDEAN: return launch_inner<T, TPW_EPI_SQEUCLIDEAN>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
         case TPW_EPI_COSINE_SIM: return launch_inner<T, TPW_EPI_COSINE_SIM>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
+        case TPW_EPI_CORRELATION: return launch_inner<T, TPW_EPI_CORRELATION>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
         default: return launch_inner<T, TPW_EPI_COSINE_DIST>(x1, x2, batch, n, m, d, aux1, aux2, out, s);
     }
 }
@@ -487,7 +490,7 @@ extern "C" int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int
                                   int64_t n, int64_t m, int64_t d, const float *aux1,
                                   const float *aux2, int epilogue, void *out, void *stream) {
     TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
-    TPW_REQUIRE(epilogue >= TPW_EPI_DOT && epilogue <= TPW_EPI_COSINE_DIST, "unknown epilogue %d",
+    TPW_REQUIRE(epilogue >= TPW_EPI_DOT && epilogue <= TPW_EPI_CORRELATION, "unknown epilogue %d",
                 epilogue);
     TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
     if (batch == 0 || n == 0 || m == 0) return TPW_OK;

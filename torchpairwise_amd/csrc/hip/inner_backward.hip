@@ -33,7 +33,7 @@
 namespace tpw {
 namespace {
 
-enum Mode { kEuclid = 0, kCosDist = 1, kCosSim = 2, kSqEuclid = 3, kPoly = 4, kSigmoid = 5 };
+enum Mode { kEuclid = 0, kCosDist = 1, kCosSim = 2, kSqEuclid = 3, kPoly = 4, kSigmoid = 5, kCosCorr = 6, kDot = 7 };
 
 // x^k for an integral k as ATen's pow with a scalar exponent computes it on the GPU.
 __device__ __forceinline__ float ipow(float x, int k) {
@@ -71,14 +71,14 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
     const int64_t j = tj * kPWCols + tid;
     const bool jok = j < m;
     float a2 = 0.0f;
-    if constexpr (MODE == kCosDist || MODE == kCosSim) a2 = jok ? n2[b * m + j] : 0.0f;
+    if constexpr (MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr) a2 = jok ? n2[b * m + j] : 0.0f;
     float csum = 0.0f;
     // One element from its loaded operands (gv = grad; av = res for euclid / sigmoid, S for
     // polynomial / cosine; nv = n1[i] for cosine): the stored weight (wf, or its bf16 bits wb)
     // and the row-sum term rt.
     constexpr bool kRes = MODE == kEuclid || MODE == kSigmoid;
-    constexpr bool kS = MODE == kPoly || MODE == kCosDist || MODE == kCosSim;
-    constexpr bool kCos = MODE == kCosDist || MODE == kCosSim;
+    constexpr bool kS = MODE == kPoly || MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+    constexpr bool kCos = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
     auto element = [&](bool ok, int64_t idx, float gv, float av, float nv, float &wf, uint16_t &wb, float &rt) {
         wf = 0.0f;
         wb = 0;
@@ -104,6 +104,8 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
         } else if constexpr (MODE == kSigmoid) {
             // tanh's backward from its output t: grad * (1 - t * t), then * gamma
             w = (gv * (1.0f - av * av)) * kp.gamma;
+        } else if constexpr (MODE == kDot) {
+            w = gv;  // matmul's backward: the products with grad itself
         } else {
             const float sv = av, a1 = nv;
             const float den = a1 * a2;
@@ -112,6 +114,8 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
             if constexpr (MODE == kCosDist) {
                 const float v = 1.0f - q;
                 gq = (v >= 0.0f && v <= 2.0f) ? -gv : 0.0f;
+            } else if constexpr (MODE == kCosCorr) {
+                gq = -gv;  // neg_ then add_(1): no clamp
             }
             const float gS = den != 0.0f ? __fdiv_rn(gq, den) : gq;
             const float gden = den != 0.0f ? __fdiv_rn(gS * -sv, den) : 0.0f;
@@ -561,6 +565,12 @@ __global__ void transpose_kernel(const T *__restrict__ x, int64_t rows, int64_t 
     }
 }
 
+// Zeroes len 16-bit words (fills with a kernel, not hipMemsetAsync).
+__global__ void zero_words_kernel(uint16_t *__restrict__ p, int64_t len) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t < len) p[t] = 0;
+}
+
 template <typename T, int MODE>
 int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float *n1,
                  const float *n2, int dtype, int64_t batch, int64_t n, int64_t m, int64_t d, T *gx1,
@@ -569,18 +579,31 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     T *W = static_cast<T *>(w.W), *WT = static_cast<T *>(w.WT);
     T *x1t = static_cast<T *>(w.x1t), *x2t = static_cast<T *>(w.x2t);
     int rc;
-    if constexpr (MODE == kCosDist || MODE == kCosSim || MODE == kPoly) {
+    if constexpr (MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr || MODE == kPoly) {
         rc = inner_dot_f32(x1, x2, dtype, batch, n, m, d, w.S, s);
         if (rc) return rc;
     }
-    const int64_t ti = cdiv(n, kPWRows), tj = cdiv(m, kPWCols);
     constexpr bool kBf16 = sizeof(T) == 2;
+    if constexpr (MODE == kDot && !kBf16) {
+        // fp32: grad is the weight matrix as stored; no weight pass, zero coefficients
+        hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(2 * batch * n, 256)), dim3(256), 0, s,
+                           reinterpret_cast<uint16_t *>(w.coef1), 2 * batch * n);
+        hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(2 * batch * m, 256)), dim3(256), 0, s,
+                           reinterpret_cast<uint16_t *>(w.coef2), 2 * batch * m);
+        rc = check_launch("zero_words_kernel");
+        if (rc) return rc;
+        const float *G = reinterpret_cast<const float *>(g);
+        rc = run_gemm<T, false>(G, x2, batch, n, d, m, 1.0f, w.coef1, x1, gx1, w.part, s);
+        if (rc) return rc;
+        return run_gemm<T, true>(G, x1, batch, m, d, n, 1.0f, w.coef2, x2, gx2, w.part, s);
+    }
+    const int64_t ti = cdiv(n, kPWRows), tj = cdiv(m, kPWCols);
     hipLaunchKernelGGL((pair_weights_kernel<T, MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
                        dim3(256), 0, s, g, res, n1, n2, n, m, w.S, w.rowpart, w.colpart, ti, tj, W,
                        kBf16 ? WT : nullptr, kp);
     rc = check_launch("pair_weights_kernel");
     if (rc) return rc;
-    const bool cosine = MODE == kCosDist || MODE == kCosSim;
+    const bool cosine = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
     const float *div1 = cosine ? n1 : nullptr;
     const float *div2 = cosine ? n2 : nullptr;
     hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)cdiv(batch * n, 256)), dim3(256), 0, s,
@@ -590,7 +613,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     rc = check_launch("reduce_parts_kernel");
     if (rc) return rc;
     // kernel functions: W carries the whole gradient (rowpart / colpart, hence coef, are 0)
-    const float sign = (cosine || MODE == kPoly || MODE == kSigmoid) ? 1.0f : -1.0f;
+    const float sign = (cosine || MODE == kPoly || MODE == kSigmoid || MODE == kDot) ? 1.0f : -1.0f;
     if constexpr (kBf16) {
         // both products as A . B^T with k-contiguous operands on the bf16 matrix cores:
         // gx1 = sign * W . (x2^T)^T + coef1 * x1, gx2 = sign * W^T . (x1^T)^T + coef2 * x2
@@ -615,10 +638,6 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
 
 // Zero the gradient of the non-empty side when the other has no rows (no pairs, so nothing
 // to sum); the empty side's buffer may be a null pointer.  Both dtypes are whole 16-bit words.
-__global__ void zero_words_kernel(uint16_t *__restrict__ p, int64_t len) {
-    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (t < len) p[t] = 0;
-}
 
 int zero_other_side(int dtype, int64_t batch, int64_t n, int64_t m, int64_t d, void *grad_x1,
                     void *grad_x2, hipStream_t s) {
@@ -683,13 +702,15 @@ extern "C" int tpw_cosine_backward(const void *grad, const void *x1, const void 
                 "sizes exceed the launch grid");
     hipStream_t s = as_stream(stream);
     if (dtype == TPW_F32) {
-        auto run = similarity ? run_backward<float, kCosSim> : run_backward<float, kCosDist>;
+        auto run = similarity == 2 ? run_backward<float, kCosCorr>
+                   : similarity ? run_backward<float, kCosSim> : run_backward<float, kCosDist>;
         return run(static_cast<const float *>(grad), static_cast<const float *>(x1),
                    static_cast<const float *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
                    static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s,
                    KerParams{});
     }
-    auto run = similarity ? run_backward<uint16_t, kCosSim> : run_backward<uint16_t, kCosDist>;
+    auto run = similarity == 2 ? run_backward<uint16_t, kCosCorr>
+               : similarity ? run_backward<uint16_t, kCosSim> : run_backward<uint16_t, kCosDist>;
     return run(static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
                static_cast<const uint16_t *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
                static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s,
@@ -716,6 +737,31 @@ extern "C" int tpw_sqeuclidean_backward(const void *grad, const void *x1, const 
             static_cast<const float *>(x2), nullptr, nullptr, nullptr, dtype, batch, n, m, d,
             static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s);
     return run_backward<uint16_t, kSqEuclid>(
+        static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
+        static_cast<const uint16_t *>(x2), nullptr, nullptr, nullptr, dtype, batch, n, m, d,
+        static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s);
+}
+
+extern "C" int tpw_linear_backward(const void *grad, const void *x1, const void *x2,
+                                        int dtype, int64_t batch, int64_t n, int64_t m, int64_t d,
+                                        void *grad_x1, void *grad_x2, void *workspace,
+                                        void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (batch == 0 || d == 0 || (n == 0 && m == 0)) return TPW_OK;
+    if (n == 0 || m == 0)
+        return zero_other_side(dtype, batch, n, m, d, grad_x1, grad_x2, as_stream(stream));
+    TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2 && workspace, "null pointer");
+    TPW_REQUIRE(cdiv(n, kPWRows) <= kMaxGridYZ && cdiv(m, kGT) <= kMaxGridYZ &&
+                    cdiv(n, kGT) <= kMaxGridYZ && batch <= kMaxGridYZ,
+                "sizes exceed the launch grid");
+    hipStream_t s = as_stream(stream);
+    if (dtype == TPW_F32)
+        return run_backward<float, kDot>(
+            static_cast<const float *>(grad), static_cast<const float *>(x1),
+            static_cast<const float *>(x2), nullptr, nullptr, nullptr, dtype, batch, n, m, d,
+            static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s);
+    return run_backward<uint16_t, kDot>(
         static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
         static_cast<const uint16_t *>(x2), nullptr, nullptr, nullptr, dtype, batch, n, m, d,
         static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s);

@@ -31,7 +31,7 @@ at::Tensor pw_inner_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t epi
     check_cuda_pair("_pw_inner", x1, x2);
     TORCH_CHECK(x1.scalar_type() == x2.scalar_type(), "_pw_inner: x1 and x2 dtypes differ");
     const int dt = float_dtype("_pw_inner", x1);
-    TORCH_CHECK(epilogue >= TPW_EPI_DOT && epilogue <= TPW_EPI_COSINE_DIST, "_pw_inner: bad epilogue");
+    TORCH_CHECK(epilogue >= TPW_EPI_DOT && epilogue <= TPW_EPI_CORRELATION, "_pw_inner: bad epilogue");
     DeviceGuard guard(x1.device());
     auto a = as3(x1), b = as3(x2);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
@@ -75,15 +75,20 @@ std::tuple<at::Tensor, at::Tensor> pw_inner_backward_cuda(const at::Tensor &grad
         check_rc(tpw_sqeuclidean_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(), dt, B, n, m, d,
                                           gx1.data_ptr(), gx2.data_ptr(), ws.data_ptr(), s),
                  "sqeuclidean backward");
-    } else if (epilogue == TPW_EPI_COSINE_SIM || epilogue == TPW_EPI_COSINE_DIST) {
+    } else if (epilogue == TPW_EPI_DOT) {
+        check_rc(tpw_linear_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(), dt, B, n, m, d,
+                                     gx1.data_ptr(), gx2.data_ptr(), ws.data_ptr(), s),
+                 "linear backward");
+    } else if (epilogue == TPW_EPI_COSINE_SIM || epilogue == TPW_EPI_COSINE_DIST ||
+               epilogue == TPW_EPI_CORRELATION) {
         auto n1 = at::empty({B, n}, a.options().dtype(at::kFloat));
         auto n2 = at::empty({B, m}, a.options().dtype(at::kFloat));
         check_rc(tpw_row_norms(a.data_ptr(), dt, B * n, d, 0, n1.data_ptr<float>(), s), "row norms");
         check_rc(tpw_row_norms(b.data_ptr(), dt, B * m, d, 0, n2.data_ptr<float>(), s), "row norms");
         check_rc(tpw_cosine_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(), n1.data_ptr<float>(),
                                      n2.data_ptr<float>(), dt, B, n, m, d,
-                                     epilogue == TPW_EPI_COSINE_SIM, gx1.data_ptr(), gx2.data_ptr(),
-                                     ws.data_ptr(), s),
+                                     epilogue == TPW_EPI_CORRELATION ? 2 : epilogue == TPW_EPI_COSINE_SIM,
+                                     gx1.data_ptr(), gx2.data_ptr(), ws.data_ptr(), s),
                  "cosine backward");
     } else {
         TORCH_CHECK(false, "_pw_inner_backward: epilogue ", epilogue, " has no backward");

@@ -181,6 +181,12 @@ at::Tensor cosine_distances(const at::Tensor &x1, const c10::optional<at::Tensor
 
 at::Tensor linear_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2) {
     auto xs = check_pairwise_inputs("linear_kernel", x1, x2);
+    // pairwise_metrics.cpp:58-65: x1 @ x2^T; fp32 / bf16 GPU tensors on the MFMA kernel, with
+    // matmul's backward (grad @ x2, grad^T @ x1) on the matrix cores
+    if (hip_float_path(xs.first, xs.second)) {
+        auto ab = broadcast_batch(xs.first, xs.second);
+        return pw_inner(ab.first, ab.second, kDot);
+    }
     return xs.first.matmul(xs.second.transpose(-1, -2));
 }
 
@@ -349,9 +355,9 @@ at::Tensor correlation_distances(const at::Tensor &x1, const c10::optional<at::T
     // pairwise_metrics.cpp:190-204: centre, then 1 - cosine similarity (no clip)
     at::Tensor a = xs.first - xs.first.mean(-1, true);
     at::Tensor b = x2.has_value() ? xs.second - xs.second.mean(-1, true) : a;
-    if (hip_float_path(a, b)) {
+    if (hip_float_path(a, b)) {  // 1 - s fused into the MFMA epilogue
         auto ab = broadcast_batch(a, b);
-        return pw_inner(ab.first, ab.second, kCosineSim).neg().add(1);
+        return pw_inner(ab.first, ab.second, kCorrelation);
     }
     auto a_norm = a.norm(2, -1, true);
     auto b_norm = x2.has_value() ? b.norm(2, -1, true) : a_norm;

@@ -57,6 +57,8 @@ constexpr int64_t kEuclidean = TPW_EPI_EUCLIDEAN;
 constexpr int64_t kSqEuclidean = TPW_EPI_SQEUCLIDEAN;
 constexpr int64_t kCosineSim = TPW_EPI_COSINE_SIM;
 constexpr int64_t kCosineDist = TPW_EPI_COSINE_DIST;
+constexpr int64_t kCorrelation = TPW_EPI_CORRELATION;
+constexpr int64_t kDot = TPW_EPI_DOT;
 
 // Dispatcher handles of the internal ops (defined in registration.cpp).
 at::Tensor pw_inner(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue);

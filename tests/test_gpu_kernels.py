@@ -532,8 +532,16 @@ def test_family_backward_edge_cases():
         assert bool((out == 9.0).all())
         for t in capi.family_backward(metric, g.to(DEV), x1.to(DEV), x2.to(DEV), w.to(DEV), 0.0, out):
             assert bool((t == 0).all())
-    with pytest.raises(RuntimeError, match="not supported"):  # inf backward is rejected
-        capi.family_backward(capi.FAM_PPMINKOWSKI, g.to(DEV), x1.to(DEV), x2.to(DEV), None, float("inf"))
+    # p = +-inf: the first arg-extremum's sign per pair, grad_x1 summed over j and grad_x2 over i
+    # in order (ppminkowski_kernel.cpp:171-208): exact against the CPU loop with ties
+    xi, yi = torch.randint(-3, 4, (1, 40, 9), generator=torch.Generator().manual_seed(5)).float(), \
+        torch.randint(-3, 4, (1, 30, 9), generator=torch.Generator().manual_seed(6)).float()
+    for p in (float("inf"), -float("inf")):
+        got = capi.family_backward(capi.FAM_PPMINKOWSKI, g.to(DEV), xi.to(DEV), yi.to(DEV), None, p)
+        a, b = xi[0].clone().requires_grad_(), yi[0].clone().requires_grad_()
+        torch.ops.torchpairwise._ppminkowski(a, b, p).backward(g[0])
+        assert_equal(got[0][0], a.grad, f"grad_x1 p={p}")
+        assert_equal(got[1][0], b.grad, f"grad_x2 p={p}")
 
 
 # --------------------------------------------------------------------------------------

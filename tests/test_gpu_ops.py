@@ -321,6 +321,32 @@ def test_family_ops_gpu(name, dtype):
     assert_close(b.grad.float(), rb.grad, rtol=grtol, atol=grtol * float(rb.grad.abs().max()), what="grad x2")
 
 
+def test_family_ops_gpu_equal_reference(tmp_path):
+    """The reference's internal metric ops on GPU float32 tensors (forward and autograd
+    backward) against its own compiled CPU kernels on the same float32 inputs (oracle/_ref):
+    values rtol 1e-5, gradients 1e-4 (each + rtol * max); the p = +-inf gradients of x1 and x2
+    (first arg-extremum, summed in the reference's order) bit for bit."""
+    from oracle import ref_runner
+    from tests._family_cases import family_cases
+    from tests.test_reference_pin import _assert_results_close
+
+    if not ref_runner.available():
+        pytest.skip("oracle/_ref not built")
+    cs = family_cases(torch.float32)
+    ref = ref_runner.run_op_reference(cs, tmp_path)
+    ops = torch.ops.torchpairwise
+    for (case, tensors), r in zip(cs, ref):
+        what = f"{case['op']} {case['kind']} {[tuple(t.shape) for t in tensors.values()]}"
+        print(what, flush=True)
+        ours = ref_runner.run_op_case(ops, case, tensors, DEV)
+        inf = case["kind"] in ("p=inf", "p=-inf")
+        exact = ("grad_a", "grad_b") if inf else ()
+        _assert_results_close({k: v for k, v in ours.items() if k.startswith("out")},
+                              {k: v for k, v in r.items() if k.startswith("out")}, 1e-5, what)
+        _assert_results_close({k: v for k, v in ours.items() if k.startswith("grad")},
+                              {k: v for k, v in r.items() if k.startswith("grad")}, 1e-4, what, exact)
+
+
 def test_sqeuclidean_identical_points_are_zero():
     x = randn(200, 64, seed=5).to(DEV)
     d = tp.sqeuclidean_distances(x)
@@ -454,6 +480,31 @@ def test_sqmahalanobis_capi_shapes():
                          what=f"B={B} n={n} m={mm} d={d} same={same}")
             if same:
                 assert bool((torch.diagonal(out, dim1=1, dim2=2) == 0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [((150, 24), (90, 24)), ((2, 130, 64), (2, 70, 64)), ((300, 128), None)])
+def test_linear_kernel_gpu(dtype, shape):
+    """linear_kernel on the MFMA kernel (DOT epilogue) and its backward on the matrix cores,
+    against the reference's x1 @ x2^T and autograd in float64 (pairwise_metrics.cpp:58-65)."""
+    x1 = randn(*shape[0], seed=0, dtype=dtype)
+    x2 = None if shape[1] is None else randn(*shape[1], seed=1, dtype=dtype)
+    a = x1.to(DEV).requires_grad_()
+    b = None if x2 is None else x2.to(DEV).requires_grad_()
+    out = tp.linear_kernel(a, b)
+    assert out.dtype == dtype
+    g = randn(*out.shape, seed=3)
+    out.backward(g.to(DEV, dtype))
+    ra = x1.double().requires_grad_()
+    rb = None if x2 is None else x2.double().requires_grad_()
+    ref = tp.linear_kernel(ra, rb)  # CPU: the reference's matmul
+    ref.backward(g.double())
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert_close(out.float(), ref, rtol=tol, atol=tol * float(ref.abs().max()), what="linear_kernel")
+    gt = 1e-4 if dtype == torch.float32 else 1e-2
+    assert_close(a.grad.float(), ra.grad, rtol=gt, atol=gt * float(ra.grad.abs().max()), what="grad x1")
+    if b is not None:
+        assert_close(b.grad.float(), rb.grad, rtol=gt, atol=gt * float(rb.grad.abs().max()), what="grad x2")
 
 
 # --------------------------------------------------------------------------------------

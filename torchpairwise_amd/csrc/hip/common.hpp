@@ -108,6 +108,11 @@ int inner_dot_f32(const void *x1, const void *x2, int dtype, int64_t batch, int6
 int inner_grad_gemm(const void *A, const void *B, int dtype, int64_t batch, int64_t M, int64_t N,
                     int64_t K, float sign, const float *coef, const void *X, void *out, hipStream_t s);
 
+// Backward of _ppminkowski / _wminkowski (w != nullptr) at p = +-inf (lp_inf_backward.hip):
+// grad_x1, grad_x2 and, weighted, per-row weight-gradient partials wrows [batch, n, d].
+int lp_inf_backward(const float *g, const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
+                    int64_t m, int64_t d, bool neg, float *gx1, float *gx2, float *wrows, hipStream_t s);
+
 }  // namespace tpw
 
 #define TPW_REQUIRE(cond, ...)          \

@@ -1051,6 +1051,8 @@ extern "C" int tpw_ppminkowski_backward(const float *grad, const float *x1, cons
         return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
     }
     TPW_REQUIRE(grad && x1 && x2 && grad_x1 && grad_x2, "null pointer");
+    if (isinf(p))  // the first arg-extremum's sign (ppminkowski_kernel.cpp:171-208)
+        return lp_inf_backward(grad, x1, x2, nullptr, batch, n, m, d, p < 0, grad_x1, grad_x2, nullptr, s);
     BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, p, grad_x1, grad_x2, nullptr,
              part, nullptr, nullptr, false};
     return dispatch_backward<kSum>(pkind_of(p), j, s);
@@ -1068,9 +1070,14 @@ extern "C" int tpw_wminkowski_backward(const float *grad, const float *x1, const
         return rc != TPW_OK ? rc : fill(grad_w, batch * d, 0.0f, s);
     }
     TPW_REQUIRE(grad && x1 && x2 && w && out && grad_x1 && grad_x2 && grad_w, "null pointer");
-    BwdJob j{grad, out, nullptr, x1, x2, w, batch, n, m, d, p, grad_x1, grad_x2, rows, part, pair1,
-             nullptr, false};
-    int rc = dispatch_backward<kWeighted>(pkind_of(p), j, s);
+    int rc;
+    if (isinf(p)) {  // the first weighted arg-extremum (wminkowski_kernel.cpp:214-265)
+        rc = lp_inf_backward(grad, x1, x2, w, batch, n, m, d, p < 0, grad_x1, grad_x2, rows, s);
+    } else {
+        BwdJob j{grad, out, nullptr, x1, x2, w, batch, n, m, d, p, grad_x1, grad_x2, rows, part, pair1,
+                 nullptr, false};
+        rc = dispatch_backward<kWeighted>(pkind_of(p), j, s);
+    }
     if (rc != TPW_OK) return rc;
     const int64_t chunks = cdiv(n, kColRows);
     hipLaunchKernelGGL(column_partial_kernel, dim3((unsigned)cdiv(d, 64), (unsigned)chunks, (unsigned)batch),

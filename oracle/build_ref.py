@@ -4,13 +4,12 @@ lie under /root/reference, into oracle/_ref/libtorchpairwise_ref.so (git-ignored
 to the GPU box like the other built libraries).  TEST INFRASTRUCTURE ONLY.
 
 Sources (g++ directly, against the installed torch headers, with the reference's own OpenMP
-flags; nothing is copied):
-  csrc/ops/hausdorff.cpp, cpu/hausdorff_kernel.cpp, autograd/hausdorff_kernel.cpp
-  csrc/ops/pairwise_binary.cpp, cpu/pairwise_binary_kernels.cpp
-  csrc/ops/prf_div.cpp, cpu/prf_div_kernel.cpp, autograd/prf_div_kernel.cpp
-The library registers the reference's own torch.ops.torchpairwise schemas, so it is loaded
-only in a separate process (oracle/ref_runner.py), never next to torchpairwise_amd.
-The cdist-routed metrics need no build: their arithmetic is torch's at::cdist.
+flags; nothing is copied): every CPU source of the reference — csrc/torchpairwise.cpp (built
+without CUDA: _cuda_version() returns -1), csrc/ops/*.cpp (the public metrics, cdist /
+pdist, the neighbour masks and the internal op stubs), csrc/ops/cpu/*.cpp (the OpenMP kernels)
+and csrc/ops/autograd/*.cpp.  Its CUDA half (csrc/ops/cuda/) needs nvcc and is not built.
+The library registers the reference's own torch.ops.torchpairwise schemas (all 101), so it is
+loaded only in a separate process (oracle/ref_runner.py), never next to torchpairwise_amd.
 """
 import concurrent.futures as cf
 import os
@@ -20,9 +19,12 @@ from pathlib import Path
 
 REF = Path(os.environ.get("TPW_REFERENCE", "/root/reference")) / "torchpairwise" / "csrc"
 OUT = Path(__file__).resolve().parent / "_ref"
-SOURCES = ["ops/hausdorff.cpp", "ops/cpu/hausdorff_kernel.cpp", "ops/autograd/hausdorff_kernel.cpp",
-           "ops/pairwise_binary.cpp", "ops/cpu/pairwise_binary_kernels.cpp",
-           "ops/prf_div.cpp", "ops/cpu/prf_div_kernel.cpp", "ops/autograd/prf_div_kernel.cpp"]
+def sources():
+    """Every CPU source of the reference, relative to csrc/."""
+    found = ["torchpairwise.cpp"]
+    for sub in ("ops", "ops/cpu", "ops/autograd"):
+        found += sorted(f"{sub}/{p.name}" for p in (REF / sub).glob("*.cpp"))
+    return found
 
 
 def main() -> int:
@@ -48,7 +50,7 @@ def main() -> int:
         return obj
 
     with cf.ThreadPoolExecutor(8) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+        objs = list(ex.map(compile_one, sources()))
     lib = OUT / "libtorchpairwise_ref.so"
     subprocess.run(["g++", "-shared", "-fopenmp", *map(str, objs), "-o", str(lib), f"-L{libdir}",
                     "-lc10", "-ltorch", "-ltorch_cpu", f"-Wl,-rpath,{libdir}"], check=True)

@@ -11,6 +11,8 @@ usage: python oracle/ref_runner.py <op> <in.npz> <out.npz>
        jaccard     (x1, x2) -> out             (prf_div(pwxor_sum, pwor_sum), the reference's composite)
        prf         cases (JSON) + c<i>_a / _b / _g arrays -> c<i>_<result> arrays and c<i>_err
                    messages: the 20 prf_div-family ops through run_prf_case
+       ops         cases (JSON) + c<i>_<name> arrays -> results of run_op_case (any op, overload,
+                   tensor / scalar arguments, autograd backward of its first output)
        time        h1, h2 (bool), j1, j2 (bool), c1, c2 (clouds), budget -> seconds per call of
                    the reference's pwne_mean (hamming), its jaccard composite and its
                    _directed_hausdorff, each repeated within the budget (the CPU baseline)
@@ -105,6 +107,58 @@ def run_prf_case(ops, case: dict, a, b, g, device: str) -> dict:
     return {k: v.detach().cpu() for k, v in res.items()}
 
 
+def run_op_case(ops, case: dict, tensors: dict, device: str) -> dict:
+    """Runs one case of any op on `ops` (this build's or the reference's namespace).
+
+    case: {"op": name, "ov": overload ("default"), "args": [item], "kwargs": {name: item},
+    "req": [tensor names that require grad], "grad": tensor name of the upstream gradient of
+    the first output (optional)}; item = {"t": tensor name} or {"v": value}.  Returns
+    {"out<k>": outputs, "grad_<name>": gradients} or {"err": message}."""
+    def item(it, leaves):
+        if "t" not in it:
+            return it["v"]
+        t = tensors[it["t"]].to(device).clone()
+        if it["t"] in case.get("req", ()):
+            t.requires_grad_(True)
+            leaves[it["t"]] = t
+        return t
+    leaves = {}
+    res = {}
+    try:
+        f = getattr(getattr(ops, case["op"]), case.get("ov", "default"))
+        args = [item(a, leaves) for a in case.get("args", [])]
+        kwargs = {k: item(v, leaves) for k, v in case.get("kwargs", {}).items()}
+        out = f(*args, **kwargs)
+        outs = list(out) if isinstance(out, (tuple, list)) else [out]
+        for k, o in enumerate(outs):
+            res[f"out{k}"] = o
+        if case.get("grad"):
+            outs[0].backward(tensors[case["grad"]].to(device))
+            for name, t in leaves.items():
+                if t.grad is not None:
+                    res[f"grad_{name}"] = t.grad
+    except Exception as e:  # the message is part of the interface
+        return {"err": f"{type(e).__name__}: {str(e).splitlines()[0]}"}
+    return {k: v.detach().cpu() for k, v in res.items()}
+
+
+def run_op_reference(cases, tmpdir) -> list:
+    """The reference's results for [(case, {name: tensor})], in a child process."""
+    arrays, meta = {}, []
+    for i, (case, tensors) in enumerate(cases):
+        tags = {}
+        for name, t in tensors.items():
+            arrays[f"c{i}_{name}"], tags[name] = tensor_to_np(t)
+        meta.append({"case": case, "tags": tags})
+    arrays["cases"] = np.array(json.dumps(meta))
+    raw = run("ops", arrays, tmpdir)
+    out = []
+    for i, m in enumerate(json.loads(str(raw["results"]))):
+        out.append({"err": m["err"]} if "err" in m else
+                   {k: np_to_tensor(raw[f"c{i}_{k}"], tag) for k, tag in m["tags"].items()})
+    return out
+
+
 def encode_prf_cases(cases) -> dict:
     """[(case, a, b, g)] -> npz members (tensors as arrays + dtype tags in the JSON)."""
     arrays, meta = {}, []
@@ -165,6 +219,20 @@ def main(op: str, src: str, dst: str) -> None:
         arrays, meta = {}, []
         for i, (case, a, b, g) in enumerate(decode_prf_cases(d)):
             r = run_prf_case(ops, case, a, b, g, "cpu")
+            if "err" in r:
+                meta.append({"err": r["err"]})
+                continue
+            tags = {}
+            for k, v in r.items():
+                arrays[f"c{i}_{k}"], tags[k] = tensor_to_np(v)
+            meta.append({"tags": tags})
+        arrays["results"] = np.array(json.dumps(meta))
+        np.savez(dst, **arrays)
+    elif op == "ops":
+        arrays, meta = {}, []
+        for i, m in enumerate(json.loads(str(d["cases"]))):
+            tensors = {k: np_to_tensor(d[f"c{i}_{k}"], tag) for k, tag in m["tags"].items()}
+            r = run_op_case(ops, m["case"], tensors, "cpu")
             if "err" in r:
                 meta.append({"err": r["err"]})
                 continue

@@ -104,3 +104,38 @@ def test_prf_div_oracle_equals_reference(tmp_path):
         assert_same_result(want, {k: v for k, v in r.items() if k in want}, str(case))
         checked += 1
     assert checked >= 240
+
+
+def _assert_results_close(ours, ref, rtol, what, exact_keys=()):
+    if "err" in ref or "err" in ours:
+        assert ours.get("err") == ref.get("err"), f"{what}: {ours.get('err')!r} != {ref.get('err')!r}"
+        return
+    assert sorted(ours) == sorted(ref), f"{what}: {sorted(ours)} != {sorted(ref)}"
+    from tests._util import assert_close, assert_equal
+    for k in ref:
+        o, r = ours[k].cpu(), ref[k].cpu()
+        assert o.dtype == r.dtype and o.shape == r.shape, f"{what}[{k}]"
+        if k in exact_keys:
+            assert_equal(o, r, f"{what}[{k}]", nan_payload=False)
+            continue
+        if o.is_floating_point():  # NaN where the reference's formulas give NaN, the rest close
+            on, rn = torch.isnan(o), torch.isnan(r)
+            assert torch.equal(on, rn), f"{what}[{k}]: NaN positions differ"
+            o, r = o.masked_fill(on, 0), r.masked_fill(rn, 0)
+        assert_close(o, r, rtol=rtol, atol=rtol * float(r.abs().max()) + 1e-300, what=f"{what}[{k}]")
+
+
+def test_family_ops_cpu_equal_reference(tmp_path):
+    """This build's CPU loops of the reference's internal metric ops, forward and backward,
+    against the reference's own compiled CPU kernels in float64 (and float32)."""
+    from tests._family_cases import family_cases
+
+    import torchpairwise_amd  # noqa: F401
+
+    ops = torch.ops.torchpairwise
+    for dtype, rtol in ((torch.float64, 1e-12), (torch.float32, 1e-5)):
+        cs = family_cases(dtype)
+        ref = ref_runner.run_op_reference(cs, tmp_path)
+        for (case, tensors), r in zip(cs, ref):
+            ours = ref_runner.run_op_case(ops, case, tensors, "cpu")
+            _assert_results_close(ours, r, rtol, f"{case['op']} {case['kind']} {dtype}")

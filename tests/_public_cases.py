@@ -1,0 +1,92 @@
+"""Cases of the public ops (the 39 metric schemas of csrc/ops/pairwise_metrics.h, cdist and
+the neighbour masks) for oracle/ref_runner.run_op_case: each runs on this build and on the
+reference's compiled CPU library with the same inputs.  "exact" cases (boolean metrics,
+directed Hausdorff, masks) compare bit for bit; the others within the fp32 bar."""
+from __future__ import annotations
+
+import torch
+
+BOOL_METRICS = ["hamming", "jaccard", "kulsinski", "kulczynski1", "yule", "dice", "rogerstanimoto",
+                "russellrao", "sokalmichener", "sokalsneath"]
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def public_cases():
+    """[(case, tensors, exact)]; a case may carry "atol_floor": an absolute allowance for values
+    whose form has a known floor (the matrix-product euclidean of a point with itself)."""
+    out = []
+    a = torch.randn(37, 16, generator=_g(1))
+    b = torch.randn(29, 16, generator=_g(2))
+    ab = torch.randn(2, 37, 16, generator=_g(3))
+    bb = torch.randn(2, 29, 16, generator=_g(4))
+    g = torch.randn(37, 29, generator=_g(5))
+    gb = torch.randn(2, 37, 29, generator=_g(6))
+    pa, pb = torch.rand(37, 16, generator=_g(7)) + 0.05, torch.rand(29, 16, generator=_g(8)) + 0.05
+    la = torch.rand(37, 2, generator=_g(9)) * 2 - 1
+    lb = torch.rand(29, 2, generator=_g(10)) * 2 - 1
+    w = torch.rand(16, generator=_g(11)) + 0.2
+    VI = torch.eye(16) + 0.1 * torch.ones(16, 16)
+
+    def add(op, args, tensors, req=(), grad=None, exact=False, kwargs=None):
+        case = {"op": op, "args": args, "kwargs": kwargs or {}, "req": list(req)}
+        if grad:
+            case["grad"] = grad
+        out.append((case, tensors, exact))
+
+    T = lambda name: {"t": name}  # noqa: E731
+    V = lambda v: {"v": v}  # noqa: E731
+    plain = ["euclidean_distances", "manhattan_distances", "cosine_distances", "linear_kernel",
+             "cosine_similarity", "sqeuclidean_distances", "correlation_distances", "cityblock_distances",
+             "chebyshev_distances", "braycurtis_distances", "canberra_distances", "l1_distances",
+             "l2_distances", "linf_distances", "snr_distances"]
+    for name in plain:
+        add(name, [T("a"), T("b")], {"a": a, "b": b, "g": g}, ("a", "b"), "g")
+        add(name, [T("a"), T("b")], {"a": ab, "b": bb, "g": gb}, ("a", "b"), "g")
+    for name in ("euclidean_distances", "cosine_distances", "sqeuclidean_distances"):
+        add(name, [T("a")], {"a": a, "g": torch.randn(37, 37, generator=_g(12))}, ("a",), "g")
+    # x2 = None euclidean: |a|^2 + |a|^2 - 2 a.a in fp32 leaves a few ulp of 2|a|^2 on the diagonal
+    # (the reference's own GPU form, at::cdist's matrix product, does the same)
+    out[-3][0]["atol_floor"] = 4 * float((torch.finfo(torch.float32).eps * 2 * (a * a).sum(1).max()) ** 0.5)
+    for name, extra in (("polynomial_kernel", [V(3), V(None), V(1.0)]), ("polynomial_kernel", [V(2), V(0.3), V(0.5)]),
+                        ("sigmoid_kernel", [V(None), V(1.0)]), ("rbf_kernel", [V(None)]), ("rbf_kernel", [V(0.2)]),
+                        ("laplacian_kernel", [V(None)]), ("minkowski_distances", [V(3.0)]),
+                        ("minkowski_distances", [V(1.5)]), ("lp_distances", [V(2.0)])):
+        add(name, [T("a"), T("b"), *extra], {"a": a, "b": b, "g": g}, ("a", "b"), "g")
+    add("wminkowski_distances", [T("a"), T("b"), V(3.0), T("w")], {"a": a, "b": b, "w": w, "g": g},
+        ("a", "b", "w"), "g")
+    add("seuclidean_distances", [T("a"), T("b"), T("w")], {"a": a, "b": b, "w": w, "g": g}, ("a", "b", "w"), "g")
+    add("mahalanobis_distances", [T("a"), T("b"), T("VI")], {"a": a, "b": b, "VI": VI, "g": g},
+        ("a", "b", "VI"), "g")
+    add("additive_chi2_kernel", [T("a"), T("b")], {"a": pa, "b": pb, "g": g}, ("a", "b"), "g")
+    add("chi2_kernel", [T("a"), T("b"), V(0.7)], {"a": pa, "b": pb, "g": g}, ("a", "b"), "g")
+    add("jensenshannon_distances", [T("a"), T("b"), V(None)], {"a": pa, "b": pb, "g": g}, ("a", "b"), "g")
+    add("jensenshannon_distances", [T("a"), T("b"), V(2.0)], {"a": pa, "b": pb, "g": g}, ("a", "b"), "g")
+    add("haversine_distances", [T("a"), T("b")], {"a": la, "b": lb, "g": g}, ("a", "b"), "g")
+    # boolean metrics: bit-exact counts and the reference's float32 arithmetic
+    ba = torch.rand(37, 70, generator=_g(13)) < 0.3
+    bbo = torch.rand(29, 70, generator=_g(14)) < 0.3
+    ba[:2] = False
+    bbo[:3] = False
+    for m in BOOL_METRICS:
+        add(f"{m}_distances", [T("a"), T("b")], {"a": ba, "b": bbo}, exact=True)
+    add("hamming_distances", [T("a"), T("b")], {"a": torch.randint(0, 3, (37, 21), generator=_g(15)),
+                                                "b": torch.randint(0, 3, (29, 21), generator=_g(16))}, exact=True)
+    # directed Hausdorff: value and indices bit for bit, gradient of the value
+    c1 = torch.rand(3, 200, 3, generator=_g(17))
+    c2 = torch.rand(2, 150, 3, generator=_g(18)) + 0.05
+    add("directed_hausdorff_distances", [T("a"), T("b")], {"a": c1, "b": c2, "g": torch.randn(3, 2, generator=_g(19))},
+        ("a", "b"), "g", exact=True)
+    # cdist by name and the neighbour masks
+    for metric in ("euclidean", "manhattan", "cosine", "chebyshev", "canberra"):
+        add("cdist", [T("a"), T("b"), V(metric)], {"a": a, "b": b})
+    add("cdist", [T("a"), T("b"), V("minkowski")], {"a": a, "b": b}, kwargs={"p": V(3.0)})
+    add("cdist", [T("a"), T("b"), V("jaccard")], {"a": ba, "b": bbo}, exact=True)
+    add("cdist", [T("a"), T("b"), V("nope")], {"a": a, "b": b}, exact=True)
+    add("cdist", [T("a"), T("b"), V("euclidean")], {"a": a, "b": b}, exact=True, kwargs={"p": V(2.0)})
+    add("k_neighbors_mask", [T("a"), T("b"), V(3)], {"a": a, "b": b}, exact=True)
+    add("radius_neighbors_mask", [T("a"), T("b"), V(5.0)], {"a": a, "b": b}, exact=True)
+    add("pdist", [T("a")], {"a": a}, exact=True)
+    return out

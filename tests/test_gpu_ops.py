@@ -347,6 +347,53 @@ def test_family_ops_gpu_equal_reference(tmp_path):
                               {k: v for k, v in r.items() if k.startswith("grad")}, 1e-4, what, exact)
 
 
+@pytest.mark.parametrize("name,extra", [
+    ("sqeuclidean_distances", ()), ("canberra_distances", ()), ("braycurtis_distances", ()),
+    ("wminkowski_distances", (3.0, "w")), ("seuclidean_distances", ("w",)), ("rbf_kernel", ()),
+    ("additive_chi2_kernel", ()), ("chi2_kernel", ()), ("jensenshannon_distances", ()),
+    ("haversine_distances", ()), ("snr_distances", ())])
+def test_float64_gpu_refusals_are_pinned(name, extra):
+    """float64 GPU tensors: the fp32 VALU family (and what is built on it) raises
+    NotImplementedError; the reference runs these in double on CUDA."""
+    d = 2 if name == "haversine_distances" else 6
+    x1 = (torch.rand(7, d, dtype=torch.float64) + 0.1).to(DEV)
+    x2 = (torch.rand(5, d, dtype=torch.float64) + 0.1).to(DEV)
+    args = [torch.rand(d, dtype=torch.float64).to(DEV) + 0.2 if e == "w" else e for e in extra]
+    with pytest.raises(NotImplementedError, match="float64"):
+        getattr(tp, name)(x1, x2, *args)
+
+
+def test_other_gpu_dtypes_served_or_refused():
+    """directed_hausdorff on the GPU is float32 only (float64 and float16 raise
+    NotImplementedError); the cdist metrics, cosine, linear and Mahalanobis run float64."""
+    c1 = torch.rand(2, 30, 3, dtype=torch.float64)
+    c2 = torch.rand(2, 20, 3, dtype=torch.float64)
+    for dt in (torch.float64, torch.float16):
+        with pytest.raises(NotImplementedError, match="float32 only"):
+            tp.directed_hausdorff_distances(c1.to(DEV, dt), c2.to(DEV, dt))
+    x1, x2 = torch.randn(9, 5, dtype=torch.float64), torch.randn(7, 5, dtype=torch.float64)
+    VI = torch.eye(5, dtype=torch.float64) * 2
+    for name, args in (("euclidean_distances", ()), ("manhattan_distances", ()), ("chebyshev_distances", ()),
+                       ("cosine_distances", ()), ("linear_kernel", ()), ("mahalanobis_distances", (VI,))):
+        got = getattr(tp, name)(x1.to(DEV), x2.to(DEV), *[a.to(DEV) for a in args])
+        want = getattr(tp, name)(x1, x2, *args)  # CPU: the reference's route
+        assert got.dtype == torch.float64
+        assert_close(got, want, rtol=1e-12, atol=1e-12 * float(want.abs().max()), what=name)
+
+
+def test_public_ops_gpu_equal_reference(tmp_path):
+    """Every public op on GPU tensors (the 39 metrics, cdist, the neighbour masks, pdist's error)
+    against the reference's compiled CPU library on the same inputs: float values rtol 1e-5,
+    gradients 1e-4 (each + rtol * max), boolean metrics, directed Hausdorff (value, indices,
+    gradients) and the masks bit for bit, and the same error messages."""
+    from oracle import ref_runner
+    from tests.test_reference_pin import _check_public_cases
+
+    if not ref_runner.available():
+        pytest.skip("oracle/_ref not built")
+    _check_public_cases(torch.ops.torchpairwise, DEV, tmp_path, rtol=1e-5, grad_rtol=1e-4)
+
+
 def test_sqeuclidean_identical_points_are_zero():
     x = randn(200, 64, seed=5).to(DEV)
     d = tp.sqeuclidean_distances(x)

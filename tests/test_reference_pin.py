@@ -106,7 +106,7 @@ def test_prf_div_oracle_equals_reference(tmp_path):
     assert checked >= 240
 
 
-def _assert_results_close(ours, ref, rtol, what, exact_keys=()):
+def _assert_results_close(ours, ref, rtol, what, exact_keys=(), atol_floor=0.0):
     if "err" in ref or "err" in ours:
         assert ours.get("err") == ref.get("err"), f"{what}: {ours.get('err')!r} != {ref.get('err')!r}"
         return
@@ -122,7 +122,8 @@ def _assert_results_close(ours, ref, rtol, what, exact_keys=()):
             on, rn = torch.isnan(o), torch.isnan(r)
             assert torch.equal(on, rn), f"{what}[{k}]: NaN positions differ"
             o, r = o.masked_fill(on, 0), r.masked_fill(rn, 0)
-        assert_close(o, r, rtol=rtol, atol=rtol * float(r.abs().max()) + 1e-300, what=f"{what}[{k}]")
+        assert_close(o, r, rtol=rtol, atol=max(rtol * float(r.abs().max()), atol_floor) + 1e-300,
+                     what=f"{what}[{k}]")
 
 
 def test_family_ops_cpu_equal_reference(tmp_path):
@@ -139,3 +140,49 @@ def test_family_ops_cpu_equal_reference(tmp_path):
         for (case, tensors), r in zip(cs, ref):
             ours = ref_runner.run_op_case(ops, case, tensors, "cpu")
             _assert_results_close(ours, r, rtol, f"{case['op']} {case['kind']} {dtype}")
+
+
+def test_public_ops_cpu_equal_reference(tmp_path):
+    """Every public op on CPU tensors (the reference's own routes in this build) against the
+    reference's compiled CPU library: values, gradients and error messages."""
+    from tests._public_cases import public_cases
+
+    import torchpairwise_amd  # noqa: F401
+
+    _check_public_cases(torch.ops.torchpairwise, "cpu", tmp_path)
+
+
+# The reference's own backward of these raises (an in-place op on a tensor its autograd saved):
+# laplacian_kernel runs at::cdist(...).mul_(-gamma).exp_() (pairwise_metrics.cpp:103-110), and
+# cdist's backward needs its output.  This build differentiates them; only the forward compares.
+REFERENCE_BACKWARD_RAISES = "modified by an inplace operation"
+
+
+def _check_public_cases(ops, device, tmp_path, rtol=1e-5, grad_rtol=1e-5):
+    from tests._public_cases import public_cases
+
+    cs = public_cases()
+    ref = ref_runner.run_op_reference([(c, t) for c, t, _ in cs], tmp_path)
+    retry = [(i, dict(c, grad=None, req=[]), t) for i, ((c, t, _), r) in enumerate(zip(cs, ref))
+             if REFERENCE_BACKWARD_RAISES in r.get("err", "")]
+    if retry:
+        for (i, c, t), r in zip(retry, ref_runner.run_op_reference([(c, t) for _, c, t in retry], tmp_path)):
+            cs[i] = (c, cs[i][1], cs[i][2])
+            ref[i] = r
+    failures = []
+    for (case, tensors, exact), r in zip(cs, ref):
+        ours = ref_runner.run_op_case(ops, case, tensors, device)
+        keys = tuple(k for k in r if k != "err") if exact else ()
+        if device != "cpu" and case["op"] == "russellrao_distances":
+            keys = ()  # (D - and) / D: the GPU route's scalar division is 1 ulp from the CPU's
+        what = f"{case['op']} {case['args']} {[tuple(t.shape) for t in tensors.values()]}"
+        try:
+            _assert_results_close({k: v for k, v in ours.items() if not k.startswith("grad")},
+                                  {k: v for k, v in r.items() if not k.startswith("grad")}, rtol, what, keys,
+                                  case.get("atol_floor", 0.0) if device != "cpu" else 0.0)
+            _assert_results_close({k: v for k, v in ours.items() if k.startswith("grad") or k == "err"},
+                                  {k: v for k, v in r.items() if k.startswith("grad") or k == "err"},
+                                  grad_rtol, what, keys)
+        except AssertionError as e:
+            failures.append(str(e).splitlines()[0][:300])
+    assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)

@@ -298,8 +298,8 @@ HdRun hausdorff_run(const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
                     c10::optional<at::Generator> gen) {
     check_hausdorff_shapes(x1, x2);
     TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), "_directed_hausdorff: expected GPU tensors");
-    TORCH_CHECK(x1.scalar_type() == at::kFloat,
-                "_directed_hausdorff: the GPU kernel is float32 only, got ", x1.scalar_type());
+    TORCH_CHECK_NOT_IMPLEMENTED(x1.scalar_type() == at::kFloat,
+                                "_directed_hausdorff: the GPU kernel is float32 only, got ", x1.scalar_type());
     HdRun r;
     r.a = x1.dim() == 3 ? x1.unsqueeze(0).contiguous() : x1.contiguous();
     r.b = x2.dim() == 3 ? x2.unsqueeze(0).contiguous() : x2.contiguous();

@@ -194,6 +194,28 @@ int tpw_bool_bytes_count_metric(const uint8_t *x1, const uint8_t *x2, const int3
                                 const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m,
                                 int64_t d, int metric, float *out, void *stream);
 
+/* Bool rows as fp4 (e2m1) values 0.0 / 1.0: nibble 0x0 or 0x2, feature 2j in the low nibble of
+ * byte j, each row zero-padded to tpw_bool_fp4_row_bytes(d) = ceil(d / 256) * 128 bytes.
+ * tpw_pack_bool_fp4 converts [rows, d] bool bytes (0/1, any alignment) into that layout
+ * (16-byte aligned output) and writes the row counts, in one pass; d < 2^24.
+ * tpw_bool_fp4_reduce / tpw_bool_fp4_count_metric then take the AND counts as fp4 dot products
+ * on the gfx950 scaled matrix cores (v_mfma_scale_f32_32x32x64_f8f6f4, exact: integer partial
+ * sums below 2^24) and finish exactly as tpw_bool_bytes_reduce / tpw_bool_bytes_count_metric,
+ * bit for bit, at half their operand bytes and matrix-core cycles.  x1 / x2 are the packed
+ * [batch, n, row_bytes] / [batch, m, row_bytes] operands; per batch, rows x row bytes < 2^31.
+ * Replace the same reference kernels as the byte entry points above
+ * (csrc/ops/cuda/pairwise_binary_kernels.cu:32-53,144-220;
+ * csrc/ops/pairwise_metrics.cpp:206-243,339-399). */
+int64_t tpw_bool_fp4_row_bytes(int64_t d);
+int tpw_pack_bool_fp4(const uint8_t *x, int64_t rows, int64_t d, uint8_t *fp4, int32_t *counts,
+                      void *stream);
+int tpw_bool_fp4_reduce(const uint8_t *x1, const uint8_t *x2, const int32_t *x1_counts,
+                        const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m, int64_t d,
+                        int op, int reduction, float *out, void *stream);
+int tpw_bool_fp4_count_metric(const uint8_t *x1, const uint8_t *x2, const int32_t *x1_counts,
+                              const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m,
+                              int64_t d, int metric, float *out, void *stream);
+
 /* Equal / not-equal counts (TPW_BIT_EQ / TPW_BIT_NE, TPW_RED_SUM / TPW_RED_MEAN) of
  * non-bool inputs of element type `elem_type` (TPW_F32 ... TPW_I64), compared by value
  * like C++ ==; output float32 [batch, n, m] as tpw_bool_pairwise_reduce.

@@ -229,6 +229,49 @@ def test_bool_bytes_entry_points_equal_packed_and_oracle(B, n, m, d):
             assert_equal(got.cpu(), torch.from_numpy(want), f"pw{opname}_{rname} bytes d={d}")
 
 
+def _fp4_rows(x, rb):
+    """numpy: bool [rows, d] -> fp4 e2m1 nibbles (1.0 = 0x2), feature 2j in the low nibble of byte j."""
+    rows, d = x.shape
+    f = np.zeros((rows, 2 * rb), np.uint8)
+    f[:, :d] = x.astype(np.uint8) * 2
+    return (f[:, 0::2] | (f[:, 1::2] << 4)).astype(np.uint8)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", BYTES_DS + (255, 256, 257, 512))
+@pytest.mark.parametrize("B,n,m", [(1, 130, 257), (2, 64, 33)])
+def test_bool_fp4_entry_points_equal_bytes(B, n, m, d):
+    """The fp4 layout (pack pass, scaled fp4 MFMA) against the int8 byte path, bit for bit, for
+    every count metric and reduction; the packed rows against a numpy restatement."""
+    print(f"bool fp4 {B}x{n}x{m} d={d}", flush=True)
+    a, b = _rows(B, n, m, d, seed=90 + d)
+    ga, gb = a.to(DEV), b.to(DEV)
+    rb = capi.lib().tpw_bool_fp4_row_bytes(d)
+    assert rb == -(-d // 256) * 128
+    fa, ca = capi.pack_bool_fp4(ga)
+    assert_equal(fa.cpu().reshape(-1, rb), torch.from_numpy(_fp4_rows(a.reshape(-1, d).numpy(), rb)), "fp4 rows")
+    assert_equal(ca.cpu(), a.reshape(-1, d).sum(-1).to(torch.int32), "fp4 row counts")
+    for code, metric in enumerate(COUNT):
+        assert_equal(capi.bool_fp4_count_metric(ga, gb, code), capi.bool_bytes_count_metric(ga, gb, code),
+                     f"{metric} fp4 = bytes d={d}", nan_payload=False)
+    for op in (capi.BIT_AND, capi.BIT_OR, capi.BIT_XOR, capi.BIT_EQ, capi.BIT_NE):
+        for red in (capi.RED_SUM, capi.RED_MEAN):
+            assert_equal(capi.bool_fp4_reduce(ga, gb, op, red), capi.bool_bytes_reduce(ga, gb, op, red),
+                         f"op {op} red {red} fp4 = bytes d={d}")
+
+
+@pytest.mark.gpu
+def test_bool_fp4_errors():
+    l = capi.lib()
+    assert l.tpw_bool_fp4_row_bytes(0) == 0 and l.tpw_bool_fp4_row_bytes(1) == 128
+    assert l.tpw_bool_fp4_count_metric(None, None, None, None, 1, 4, 4, 8, 99, None, None) != 0
+    assert b"unknown metric" in l.tpw_last_error()
+    assert l.tpw_pack_bool_fp4(None, 4, 1 << 24, None, None, None) != 0
+    assert b"2^24" in l.tpw_last_error()
+    assert l.tpw_bool_fp4_reduce(None, None, None, None, 1, 1 << 22, 4, 1024, 0, 0, None, None) != 0
+    assert b"2^31" in l.tpw_last_error()
+
+
 @pytest.mark.gpu
 def test_bool_bytes_empty_and_errors():
     x = torch.zeros((0, 16), dtype=torch.bool, device=DEV)

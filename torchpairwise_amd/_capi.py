@@ -35,6 +35,10 @@ _SIGNATURES = {
     "tpw_bool_row_counts": (_i, [_p, _i64, _i64, _p, _p]),
     "tpw_bool_bytes_reduce": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_bool_bytes_count_metric": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _p, _p]),
+    "tpw_bool_fp4_row_bytes": (_i64, [_i64]),
+    "tpw_pack_bool_fp4": (_i, [_p, _i64, _i64, _p, _p, _p]),
+    "tpw_bool_fp4_reduce": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
+    "tpw_bool_fp4_count_metric": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _p, _p]),
     "tpw_compare_reduce": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_row_norms": (_i, [_p, _i, _i64, _i64, _i, _p, _p]),
     "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),
@@ -235,6 +239,45 @@ def bool_bytes_count_metric(x1, x2, metric):
     out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
     ca, cb = bool_row_counts(a), bool_row_counts(b)  # held until the launch is queued
     call("tpw_bool_bytes_count_metric", _ptr(a), _ptr(b), _ptr(ca), _ptr(cb), B, n, m, d, metric,
+         _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def pack_bool_fp4(x):
+    """bool [B, rows, d] cuda -> (uint8 [B, rows, row_bytes] fp4 rows, int32 [B * rows] counts)."""
+    import torch
+
+    a = _as3(x).contiguous()
+    B, rows, d = a.shape
+    rb = lib().tpw_bool_fp4_row_bytes(d)
+    fp4 = torch.empty((B, rows, rb), dtype=torch.uint8, device=x.device)
+    counts = torch.empty((B * rows,), dtype=torch.int32, device=x.device)
+    call("tpw_pack_bool_fp4", _ptr(a), B * rows, d, _ptr(fp4), _ptr(counts), _stream())
+    return fp4, counts
+
+
+def bool_fp4_reduce(x1, x2, op, reduction):
+    """The pw{op}_{reduction} of bool inputs through the fp4 layout on the scaled matrix cores."""
+    import torch
+
+    (fa, ca), (fb, cb) = pack_bool_fp4(x1), pack_bool_fp4(x2)
+    B, n, d = _as3(x1).shape
+    m = _as3(x2).shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    call("tpw_bool_fp4_reduce", _ptr(fa), _ptr(fb), _ptr(ca), _ptr(cb), B, n, m, d, op, reduction,
+         _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def bool_fp4_count_metric(x1, x2, metric):
+    """A boolean count metric (TPW_BMET_* code) through the fp4 layout."""
+    import torch
+
+    (fa, ca), (fb, cb) = pack_bool_fp4(x1), pack_bool_fp4(x2)
+    B, n, d = _as3(x1).shape
+    m = _as3(x2).shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
+    call("tpw_bool_fp4_count_metric", _ptr(fa), _ptr(fb), _ptr(ca), _ptr(cb), B, n, m, d, metric,
          _ptr(out), _stream())
     return out if x1.dim() == 3 else out[0]
 

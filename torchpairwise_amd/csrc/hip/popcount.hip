@@ -305,6 +305,77 @@ __device__ __forceinline__ uint32_t count_from_and(uint32_t c, uint32_t pa, uint
     else return pa + pb - 2u * c;  // XOR, NE, and EQ (finish turns ne into d - ne)
 }
 
+// The AND counts of a 128 x 128 tile (the 32 x 32 MFMA accumulator layout: register r of lane
+// l holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32) -> bitop counts -> the reference's
+// float arithmetic -> the output.  Full tiles are staged per wave in the panels' LDS (free after
+// the K loop's last barrier) and written as float4 rows; edge tiles element by element.
+template <int OP, int EPI>
+__device__ __forceinline__ void bool_epilogue(const int32x16 (&acc)[2][2], uint4 *smem, const uint32_t (&s_pop)[2][kTile],
+                                              int64_t b, int64_t row0, int64_t col0, int64_t n, int64_t m, int64_t d,
+                                              double inv_d, float inv_df, float *__restrict__ out, bool vec_store) {
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+    const uint32_t du = (uint32_t)d;
+    const float df = (float)d;
+    uint32_t pbv[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) pbv[ni] = s_pop[1][wc + ni * 32 + l32];
+    const bool full = row0 + kTile <= n && col0 + kTile <= m;
+    if (full && vec_store) {
+        // each wave stages a 32 x 64 half of its tile in its own LDS slice (the operand panels
+        // are free after the K loop's last barrier) and writes it as float4 rows, 16 lanes per
+        // 256-byte segment
+        float *stage = reinterpret_cast<float *>(smem) + wave * (32 * kBStage);
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+            // the popcounts of the lane's 16 rows: 4 groups of 4 consecutive rows
+            uint4 paq[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                paq[g] = *reinterpret_cast<const uint4 *>(&s_pop[0][wr + mi * 32 + 8 * g + 4 * h]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
+                    const uint4 q4 = paq[r >> 2];
+                    const uint32_t pav = (r & 3) == 0 ? q4.x : (r & 3) == 1 ? q4.y : (r & 3) == 2 ? q4.z : q4.w;
+                    const uint32_t c = count_from_and<OP, EPI>((uint32_t)acc[mi][ni][r], pav, pbv[ni]);
+                    stage[rr * kBStage + ni * 32 + l32] = finish<OP, EPI>(c, pav, pbv[ni], du, inv_d, df, inv_df);
+                }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+            __builtin_amdgcn_wave_barrier();
+            float *orow = out + (b * n + row0 + wr + mi * 32) * m + col0 + wc;
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const int rr = it * 4 + (lane >> 4), cc = (lane & 15) * 4;
+                store_nt4(orow + (int64_t)rr * m + cc, *reinterpret_cast<const floatx4 *>(&stage[rr * kBStage + cc]));
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the slice is rewritten
+            __builtin_amdgcn_wave_barrier();
+        }
+        return;
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const int64_t col = col0 + wc + ni * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rr = mi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int64_t row = row0 + wr + rr;
+                if (row < n && col < m) {
+                    const uint32_t pav = s_pop[0][wr + rr];
+                    const uint32_t c = count_from_and<OP, EPI>((uint32_t)acc[mi][ni][r], pav, pbv[ni]);
+                    store_nt(out + (b * n + row) * m + col, finish<OP, EPI>(c, pav, pbv[ni], du, inv_d, df, inv_df));
+                }
+            }
+        }
+}
+
 template <int OP, int EPI, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void bool_mfma_kernel(
     const uint8_t *__restrict__ x1, const uint8_t *__restrict__ x2, const int32_t *__restrict__ popA,
@@ -387,65 +458,7 @@ __global__ __launch_bounds__(kThreads, 2) void bool_mfma_kernel(
         __syncthreads();
     }
 
-    // Accumulator layout of the 32 x 32 MFMA: register r of lane l holds
-    // row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
-    const uint32_t du = (uint32_t)d;
-    const float df = (float)d;
-    uint32_t pbv[2];
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni) pbv[ni] = s_pop[1][wc + ni * 32 + l32];
-    const bool full = row0 + kTile <= n && col0 + kTile <= m;
-    if (full && vec_store) {
-        // each wave stages a 32 x 64 half of its tile in its own LDS slice (the operand panels
-        // are free after the K loop's last barrier) and writes it as float4 rows, 16 lanes per
-        // 256-byte segment
-        float *stage = reinterpret_cast<float *>(smem) + wave * (32 * kBStage);
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-            // the popcounts of the lane's 16 rows: 4 groups of 4 consecutive rows
-            uint4 paq[4];
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                paq[g] = *reinterpret_cast<const uint4 *>(&s_pop[0][wr + mi * 32 + 8 * g + 4 * h]);
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
-                    const uint4 q4 = paq[r >> 2];
-                    const uint32_t pav = (r & 3) == 0 ? q4.x : (r & 3) == 1 ? q4.y : (r & 3) == 2 ? q4.z : q4.w;
-                    const uint32_t c = count_from_and<OP, EPI>((uint32_t)acc[mi][ni][r], pav, pbv[ni]);
-                    stage[rr * kBStage + ni * 32 + l32] = finish<OP, EPI>(c, pav, pbv[ni], du, inv_d, df, inv_df);
-                }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
-            __builtin_amdgcn_wave_barrier();
-            float *orow = out + (b * n + row0 + wr + mi * 32) * m + col0 + wc;
-#pragma unroll
-            for (int it = 0; it < 8; ++it) {
-                const int rr = it * 4 + (lane >> 4), cc = (lane & 15) * 4;
-                store_nt4(orow + (int64_t)rr * m + cc, *reinterpret_cast<const floatx4 *>(&stage[rr * kBStage + cc]));
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the slice is rewritten
-            __builtin_amdgcn_wave_barrier();
-        }
-        return;
-    }
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const int64_t col = col0 + wc + ni * 32 + l32;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int rr = mi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                const int64_t row = row0 + wr + rr;
-                if (row < n && col < m) {
-                    const uint32_t pav = s_pop[0][wr + rr];
-                    const uint32_t c = count_from_and<OP, EPI>((uint32_t)acc[mi][ni][r], pav, pbv[ni]);
-                    store_nt(out + (b * n + row) * m + col, finish<OP, EPI>(c, pav, pbv[ni], du, inv_d, df, inv_df));
-                }
-            }
-        }
+    bool_epilogue<OP, EPI>(acc, smem, s_pop, b, row0, col0, n, m, d, inv_d, inv_df, out, vec_store);
 }
 
 // Set bytes per row of a [rows, d] bool matrix (one wave per row).  VEC (d % 16 == 0, 16-byte
@@ -497,6 +510,177 @@ int check_reduce_args(const uint32_t *a, const uint32_t *b, int64_t batch, int64
     TPW_REQUIRE(a && b && out, "null pointer");
     TPW_REQUIRE(aligned16(a) && aligned16(b), "packed words must be 16-byte aligned");
     return TPW_OK;
+}
+
+
+// ---------------------------------------------------------------- bool rows as fp4 (e2m1)
+// A bool encoded as the fp4 value 0.0 or 1.0 (nibble 0x0 / 0x2) makes the AND count of two
+// rows their fp4 dot product, which the gfx950 scaled MFMA computes exactly
+// (v_mfma_scale_f32_32x32x64_f8f6f4, scales 1.0, fp32 accumulation: products are 0 or 1 and
+// every partial sum is an integer below 2^24).  Half the bytes of the int8 layout and half its
+// matrix-core cycles per feature.  Rows are 128-byte multiples (256 features), zero-padded;
+// feature 2j is the low nibble of byte j.  A 128-byte chunk goes from global memory straight
+// into LDS (global_load_lds_dwordx4, the 144-byte padded row layout of the int8 kernel); lane
+// (i + 32 h) feeds the MFMA the 16-byte pieces h * 4 + q of row i, A and B alike.
+typedef int int32x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kFp4Slots = 9;  // 2 panels x 128 rows x 9 slots / 4 waves / 64 lanes
+
+// One wave per row: each lane packs 32 features (16 output bytes) per step and counts them.
+__global__ void pack_fp4_kernel(const uint8_t *__restrict__ x, int64_t rows, int64_t d, int64_t rb,
+                                uint8_t *__restrict__ fp4, int32_t *__restrict__ counts, bool vec) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const uint8_t *p = x + row * d;
+    uint8_t *q = fp4 + row * rb;
+    uint32_t c = 0;
+    for (int64_t k = 32 * (int64_t)lane; k < 2 * rb; k += 2048) {  // k: first feature of the piece
+        uint32_t v[8];  // 32 bool bytes, 4 per word
+        if (vec && k + 32 <= d) {
+            const uint4 lo = *reinterpret_cast<const uint4 *>(p + k);
+            const uint4 hi = *reinterpret_cast<const uint4 *>(p + k + 16);
+            v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+            v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int64_t kk = k + 4 * t + u;
+                    if (kk < d) w |= (uint32_t)p[kk] << (8 * u);
+                }
+                v[t] = w;
+            }
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t pair = 0;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                // bytes f0..f3 (bit 0 each) -> nibbles 0x2 at bits 1, 5, 9, 13
+                const uint32_t w = v[2 * t + e] & 0x01010101u;
+                c += __builtin_popcount(w);
+                const uint32_t nib = ((w << 1) & 0x2u) | ((w >> 3) & 0x20u) | ((w >> 7) & 0x200u) | ((w >> 11) & 0x2000u);
+                pair |= nib << (16 * e);
+            }
+            o[t] = pair;
+        }
+        *reinterpret_cast<uint4 *>(q + k / 2) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    if (lane == 0) counts[row] = (int32_t)c;
+}
+
+template <int OP, int EPI>
+__global__ __launch_bounds__(kThreads, 2) void bool_fp4_kernel(
+    const uint8_t *__restrict__ x1, const uint8_t *__restrict__ x2, const int32_t *__restrict__ popA,
+    const int32_t *__restrict__ popB, int64_t n, int64_t m, int64_t d, int64_t rb, double inv_d, float inv_df,
+    float *__restrict__ out, int64_t tiles_n, int64_t tiles_m, int64_t total, bool vec_store) {
+    // operand panels (As, Bs); after the K loop the same bytes stage the fp32 output
+    __shared__ uint4 smem[2 * kTile * kBStride];
+    const uint4 *As = smem;
+    const uint4 *Bs = smem + kTile * kBStride;
+    __shared__ __align__(16) uint32_t s_pop[2][kTile];
+
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
+    const int64_t row0 = tr * kTile, col0 = tc * kTile;
+    const uint8_t *A = x1 + b * n * rb;
+    const uint8_t *B = x2 + b * m * rb;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+    {
+        const int i = tid & (kTile - 1);
+        if (tid < kTile) s_pop[0][i] = row0 + i < n ? (uint32_t)popA[b * n + row0 + i] : 0u;
+        else s_pop[1][i] = col0 + i < m ? (uint32_t)popB[b * m + col0 + i] : 0u;
+    }
+    floatx16 facc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) facc[mi][ni][r] = 0.0f;
+
+    // byte offsets (from the panel's batch base) of this lane's slot in each of its 9 wave
+    // loads: slot s -> panel s / 1152, row (s % 1152) / 9, piece (s % 1152) % 9; the pad slot
+    // loads piece 7 again (never read), rows past the edge load the last row (never stored)
+    int32_t off[kFp4Slots];
+#pragma unroll
+    for (int j = 0; j < kFp4Slots; ++j) {
+        const int sl = (wave * kFp4Slots + j) * 64 + lane;
+        const int panel = sl >= kTile * kBStride;
+        const int s2 = sl - panel * kTile * kBStride;
+        const int r = s2 / kBStride, c0 = s2 - r * kBStride;
+        const int c = c0 == kBRowVec ? kBRowVec - 1 : c0;
+        const int64_t lim = panel ? m : n;
+        int64_t row = (panel ? col0 : row0) + r;
+        row = row < lim ? row : lim - 1;
+        off[j] = (int32_t)(row * rb + c * 16);
+    }
+    const int64_t nchunks = rb / 128;
+    for (int64_t kc = 0; kc < nchunks; ++kc) {
+        const int64_t kb = kc * 128;
+#pragma unroll
+        for (int j = 0; j < kFp4Slots; ++j) {
+            const int first = (wave * kFp4Slots + j) * 64;  // wave-uniform LDS slot
+            const uint8_t *src = (first >= kTile * kBStride ? B : A) + kb + off[j];
+            __builtin_amdgcn_global_load_lds((global_void *)src, (lds_void *)(smem + first), 16, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's slots have landed
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            int32x8 a[2], bv[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                const uint4 v = As[(wr + mi * 32 + l32) * kBStride + h * 4 + q];
+                a[mi] = int32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const uint4 v = Bs[(wc + ni * 32 + l32) * kBStride + h * 4 + q];
+                bv[ni] = int32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)  // formats 4 / 4: fp4 e2m1; E8M0 scales 127 = 1.0
+                    facc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bv[ni], facc[mi][ni], 4, 4,
+                                                                                  0, 127, 0, 127);
+        }
+        __syncthreads();
+    }
+    int32x16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = (int)facc[mi][ni][r];
+    bool_epilogue<OP, EPI>(acc, smem, s_pop, b, row0, col0, n, m, d, inv_d, inv_df, out, vec_store);
+}
+
+int64_t fp4_row_bytes(int64_t d) { return (d + 255) / 256 * 128; }
+
+template <int OP, int EPI>
+int launch_bool_fp4(const uint8_t *a, const uint8_t *b, const int32_t *pa, const int32_t *pb, int64_t batch,
+                    int64_t n, int64_t m, int64_t d, float *out, hipStream_t s) {
+    const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
+    const int64_t total = tiles_n * tiles_m * batch;
+    const double inv_d = d < (int64_t)kFloatExactLimit ? 1.0 / (double)d : 0.0;
+    const float inv_df = 1.0f / (float)d;
+    const bool vec_store = m % 4 == 0 && aligned16(out);
+    hipLaunchKernelGGL((bool_fp4_kernel<OP, EPI>), dim3((unsigned)total), dim3(kThreads), 0, s, a, b, pa, pb, n, m,
+                       d, fp4_row_bytes(d), inv_d, inv_df, out, tiles_n, tiles_m, total, vec_store);
+    return check_launch("bool_fp4_kernel");
 }
 
 }  // namespace
@@ -658,6 +842,93 @@ extern "C" int tpw_bool_bytes_count_metric(const uint8_t *x1, const uint8_t *x2,
     case CODE:                                                                                        \
         return launch_bool_mfma<TPW_BIT_AND, kCountMetric + CODE>(x1, x2, x1_counts, x2_counts, batch, n, \
                                                                   m, d, out, s);
+    switch (metric) {
+        TPW_MET(TPW_BMET_HAMMING)
+        TPW_MET(TPW_BMET_JACCARD)
+        TPW_MET(TPW_BMET_DICE)
+        TPW_MET(TPW_BMET_KULCZYNSKI1)
+        TPW_MET(TPW_BMET_KULSINSKI)
+        TPW_MET(TPW_BMET_ROGERSTANIMOTO)
+        TPW_MET(TPW_BMET_RUSSELLRAO)
+        TPW_MET(TPW_BMET_SOKALMICHENER)
+        TPW_MET(TPW_BMET_SOKALSNEATH)
+        TPW_MET(TPW_BMET_YULE)
+        default: break;
+    }
+#undef TPW_MET
+    return TPW_ERR_INVALID;
+}
+
+extern "C" int64_t tpw_bool_fp4_row_bytes(int64_t d) { return d <= 0 ? 0 : fp4_row_bytes(d); }
+
+extern "C" int tpw_pack_bool_fp4(const uint8_t *x, int64_t rows, int64_t d, uint8_t *fp4, int32_t *counts,
+                                 void *stream) {
+    TPW_REQUIRE(rows >= 0 && d >= 1, "invalid sizes rows=%lld d=%lld", (long long)rows, (long long)d);
+    TPW_REQUIRE(d < (int64_t)kFloatExactLimit, "d=%lld: the fp4 layout counts exactly below 2^24 features",
+                (long long)d);
+    if (rows == 0) return TPW_OK;
+    TPW_REQUIRE(x && fp4 && counts, "null pointer");
+    TPW_REQUIRE(aligned16(fp4), "the fp4 rows must be 16-byte aligned");
+    hipLaunchKernelGGL(pack_fp4_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, as_stream(stream), x, rows, d,
+                       fp4_row_bytes(d), fp4, counts, d % 16 == 0 && aligned16(x));
+    return check_launch("pack_fp4_kernel");
+}
+
+namespace {
+int check_fp4_args(const uint8_t *a, const uint8_t *b, const int32_t *pa, const int32_t *pb, int64_t batch,
+                   int64_t n, int64_t m, int64_t d, float *out) {
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 1, "invalid sizes batch=%lld n=%lld m=%lld d=%lld",
+                (long long)batch, (long long)n, (long long)m, (long long)d);
+    TPW_REQUIRE(d < (int64_t)kFloatExactLimit, "d=%lld: the fp4 layout counts exactly below 2^24 features",
+                (long long)d);
+    TPW_REQUIRE((n > m ? n : m) * fp4_row_bytes(d) < ((int64_t)1 << 31),
+                "rows x row bytes must stay below 2^31 per batch for the fp4 kernel");
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(cdiv(n, kTile) * cdiv(m, kTile) * batch <= (int64_t)0x7fffffff, "output too large for one launch");
+    TPW_REQUIRE(a && b && pa && pb && out, "null pointer");
+    TPW_REQUIRE(aligned16(a) && aligned16(b), "the fp4 rows must be 16-byte aligned");
+    return TPW_OK;
+}
+}  // namespace
+
+extern "C" int tpw_bool_fp4_reduce(const uint8_t *x1, const uint8_t *x2, const int32_t *x1_counts,
+                                   const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m, int64_t d, int op,
+                                   int reduction, float *out, void *stream) {
+    TPW_REQUIRE(op >= TPW_BIT_AND && op <= TPW_BIT_NE, "unknown bit op %d", op);
+    TPW_REQUIRE(reduction == TPW_RED_SUM || reduction == TPW_RED_MEAN, "unknown reduction %d", reduction);
+    int rc = check_fp4_args(x1, x2, x1_counts, x2_counts, batch, n, m, d, out);
+    if (rc != TPW_OK) return rc;
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    hipStream_t s = as_stream(stream);
+#define TPW_CASE(OPC, K)                                                                                  \
+    case OPC:                                                                                             \
+        return reduction == TPW_RED_SUM                                                                   \
+                   ? launch_bool_fp4<K, kSum>(x1, x2, x1_counts, x2_counts, batch, n, m, d, out, s)        \
+                   : launch_bool_fp4<K, kMean>(x1, x2, x1_counts, x2_counts, batch, n, m, d, out, s);
+    switch (op) {
+        TPW_CASE(TPW_BIT_AND, TPW_BIT_AND)
+        TPW_CASE(TPW_BIT_OR, TPW_BIT_OR)
+        TPW_CASE(TPW_BIT_XOR, TPW_BIT_XOR)
+        TPW_CASE(TPW_BIT_EQ, TPW_BIT_EQ)
+        TPW_CASE(TPW_BIT_NE, TPW_BIT_XOR)  // NE counts exactly like XOR on bits
+        default: break;
+    }
+#undef TPW_CASE
+    return TPW_ERR_INVALID;
+}
+
+extern "C" int tpw_bool_fp4_count_metric(const uint8_t *x1, const uint8_t *x2, const int32_t *x1_counts,
+                                         const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m, int64_t d,
+                                         int metric, float *out, void *stream) {
+    TPW_REQUIRE(metric >= TPW_BMET_HAMMING && metric <= TPW_BMET_YULE, "unknown metric %d", metric);
+    int rc = check_fp4_args(x1, x2, x1_counts, x2_counts, batch, n, m, d, out);
+    if (rc != TPW_OK) return rc;
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    hipStream_t s = as_stream(stream);
+#define TPW_MET(CODE)                                                                                       \
+    case CODE:                                                                                              \
+        return launch_bool_fp4<TPW_BIT_AND, kCountMetric + CODE>(x1, x2, x1_counts, x2_counts, batch, n, m, d, \
+                                                                 out, s);
     switch (metric) {
         TPW_MET(TPW_BMET_HAMMING)
         TPW_MET(TPW_BMET_JACCARD)

@@ -198,6 +198,35 @@ std::pair<at::Tensor, at::Tensor> pack(const at::Tensor &x3, bool with_pops) {
 void bool_bytes_cuda(const at::Tensor &a, const at::Tensor &b, int bmet, int op, int red, at::Tensor &out) {
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     const bool same = b.is_same(a);
+    const int64_t rb = tpw_bool_fp4_row_bytes(d);
+    if (d < (int64_t(1) << 24) && std::max(n, m) * rb < (int64_t(1) << 31)) {
+        // fp4 rows (one pack pass per operand: nibbles and row counts), then the scaled matrix
+        // cores; the results equal the int8 byte path's bit for bit
+        auto fa = at::empty({B * n, rb}, a.options().dtype(at::kByte));
+        auto ca = at::empty({B * n}, a.options().dtype(at::kInt));
+        check_rc(tpw_pack_bool_fp4(reinterpret_cast<const uint8_t *>(a.data_ptr<bool>()), B * n, d, fa.data_ptr<uint8_t>(),
+                                   ca.data_ptr<int32_t>(), current_stream()),
+                 "pack bool fp4");
+        at::Tensor fb = fa, cb = ca;
+        if (!same) {
+            fb = at::empty({B * m, rb}, b.options().dtype(at::kByte));
+            cb = at::empty({B * m}, b.options().dtype(at::kInt));
+            check_rc(tpw_pack_bool_fp4(reinterpret_cast<const uint8_t *>(b.data_ptr<bool>()), B * m, d,
+                                       fb.data_ptr<uint8_t>(), cb.data_ptr<int32_t>(), current_stream()),
+                     "pack bool fp4");
+        }
+        if (bmet >= 0)
+            check_rc(tpw_bool_fp4_count_metric(fa.data_ptr<uint8_t>(), fb.data_ptr<uint8_t>(), ca.data_ptr<int32_t>(),
+                                               cb.data_ptr<int32_t>(), B, n, m, d, bmet, out.data_ptr<float>(),
+                                               current_stream()),
+                     "boolean count metric");
+        else
+            check_rc(tpw_bool_fp4_reduce(fa.data_ptr<uint8_t>(), fb.data_ptr<uint8_t>(), ca.data_ptr<int32_t>(),
+                                         cb.data_ptr<int32_t>(), B, n, m, d, op, red, out.data_ptr<float>(),
+                                         current_stream()),
+                     "pairwise bool reduction");
+        return;
+    }
     auto ca = at::empty({B * n}, a.options().dtype(at::kInt));
     auto cb = same ? ca : at::empty({B * m}, b.options().dtype(at::kInt));
     const uint8_t *pa = reinterpret_cast<const uint8_t *>(a.data_ptr<bool>());

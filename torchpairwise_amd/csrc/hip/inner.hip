@@ -23,6 +23,7 @@
 // 8 XCDs, so id % 8 selects the XCD) and in groups of 8 tile rows, so that the blocks
 // resident on one XCD share A and B panels in that XCD's L2.
 #include "common.hpp"
+#include "tile_mfma.hpp"
 
 namespace tpw {
 namespace {
@@ -165,6 +166,35 @@ __device__ __forceinline__ void mfma_piece(floatx16 (&acc)[2][2], const uint4 (&
             acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                 __builtin_bit_cast(bf16x8, a[mi]), __builtin_bit_cast(bf16x8, b[ni]), acc[mi][ni],
                 0, 0, 0);
+        }
+    }
+}
+
+// The same piece with the operands swapped (tile_mfma.hpp's transposed products): the
+// accumulators then hold four consecutive output columns per register quad.
+__device__ __forceinline__ void mfma_piece_t(floatx16 (&acc)[2][2], const uint4 (&a)[2], const uint4 (&b)[2], float) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const uint32_t av = e == 0 ? a[mi].x : e == 1 ? a[mi].y : e == 2 ? a[mi].z : a[mi].w;
+                const uint32_t bv = e == 0 ? b[ni].x : e == 1 ? b[ni].y : e == 2 ? b[ni].z : b[ni].w;
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(bv), __uint_as_float(av),
+                                                                  acc[mi][ni], 0, 0, 0);
+            }
+        }
+    }
+}
+__device__ __forceinline__ void mfma_piece_t(floatx16 (&acc)[2][2], const uint4 (&a)[2], const uint4 (&b)[2],
+                                             uint16_t) {
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, b[ni]), __builtin_bit_cast(bf16x8, a[mi]), acc[mi][ni], 0, 0, 0);
         }
     }
 }
@@ -389,6 +419,84 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     }
 }
 
+// The tile kernel of tile_mfma.hpp for inputs whose K chunks are all full (d * sizeof(T) a
+// multiple of 128 bytes, 16-byte aligned rows) and outputs whose rows split into whole 16-byte
+// units: one 32 KiB operand buffer (4 blocks per CU), the chunk loaded by DMA while no wave
+// reads it, transposed products, and the epilogue applied while the tile is staged for
+// row-segment stores.
+template <typename T, typename OutT, int EPI>
+__global__ __launch_bounds__(tile::kThreads, 4) void inner_tile_kernel(
+    const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
+    const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
+    int64_t tiles_n, int64_t tiles_m, int64_t total, KerParams kp) {
+    using namespace tile;
+    __shared__ uint4 smem[kBuf];
+    __shared__ __align__(16) float s_aux[2 * kT];  // row norms, then column norms
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
+    const int64_t row0 = tr * kT, col0 = tc * kT;
+    const int64_t row_bytes = d * (int64_t)sizeof(T);
+    const uint8_t *A = reinterpret_cast<const uint8_t *>(x1 + b * n * d);
+    const uint8_t *B = reinterpret_cast<const uint8_t *>(x2 + b * m * d);
+    // the tile's norms by DMA as well (a compiler-visible load would leave its register
+    // "pending" for the compiler, which then waits for every store in flight before reusing it)
+    if constexpr (kAux1<EPI>)
+        dma_tile_rows(aux1 + b * n, kAux2<EPI> ? aux2 + b * m : nullptr, kAux2<EPI>, wave, lane, row0, col0, n, m,
+                      s_aux);
+    uint32_t off[kSlots];
+    dma_offsets(off, wave, lane, row0, col0, n, m, row_bytes);
+    dma_chunk(A, B, off, wave, 0, smem);
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+
+    const int nchunks = (int)(row_bytes / 128);
+    for (int kc = 0; kc < nchunks; ++kc) {
+        if (kc > 0) {
+            barrier_lds();  // every wave is done with chunk kc - 1
+            dma_chunk(A, B, off, wave, (int64_t)kc * 128, smem);
+        }
+        barrier_all();  // chunk kc (and, the first time, the norms) has landed
+        const uint4 *As = smem, *Bs = smem + kPanel;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int c = h * 4 + q;
+            uint4 a[2], bv[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) a[mi] = piece(As, wr + mi * 32 + l32, c);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) bv[ni] = piece(Bs, wc + ni * 32 + l32, c);
+            mfma_piece_t(acc, a, bv, T{});
+        }
+    }
+    barrier_lds();  // the operand buffer becomes the output stage
+
+    float a1v[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) a1v[mi] = kAux1<EPI> ? s_aux[wr + mi * 32 + l32] : 0.0f;
+    store_tile<OutT>(
+        smem,
+        [&](int mi, int ni, int g) {
+            const floatx4 a2 = kAux2<EPI> ? *reinterpret_cast<const floatx4 *>(&s_aux[kT + wc + ni * 32 + 8 * g + 4 * h])
+                                          : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            floatx4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = epilogue<EPI>(acc[mi][ni][4 * g + e], a1v[mi], a2[e], kp);
+            return o;
+        },
+        out, b, row0, col0, n, m);
+}
+
 // Row norms: one wave per row, lanes stride over the features.
 template <typename T>
 __global__ void row_norms_kernel(const T *__restrict__ x, int64_t rows, int64_t d, int squared,
@@ -418,6 +526,15 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
     const bool vec = ((d * (int64_t)sizeof(T)) % 16 == 0) && aligned16(x1) && aligned16(x2);
     // direct LDS loads: every chunk full, and the per-lane element offsets fit in int32
     const bool direct = vec && d % Elem<T>::kChunk == 0 && d > 0 && (n > m ? n : m) * d < ((int64_t)1 << 31);
+    if constexpr (EPI != kEpiGrad && EPI != kEpiPoly) {
+        // the tile kernel: byte offsets below 2^32, whole 16-byte units per output row
+        if (direct && (n > m ? n : m) * d * (int64_t)sizeof(T) < ((int64_t)1 << 32) && aligned16(out) &&
+            m % (16 / (int64_t)sizeof(OutT)) == 0) {
+            hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI>), dim3((unsigned)total), dim3(tile::kThreads), 0, s, x1,
+                               x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp);
+            return check_launch("inner_tile_kernel");
+        }
+    }
     auto kernel = direct ? pairwise_inner_kernel<T, OutT, EPI, true, true>
                   : vec  ? pairwise_inner_kernel<T, OutT, EPI, true, false>
                          : pairwise_inner_kernel<T, OutT, EPI, false, false>;

@@ -8,6 +8,7 @@
 // per word pair.  The float32 output (the only large stream) is written with
 // non-temporal 16-byte stores, 256 contiguous bytes per 16 lanes.
 #include "common.hpp"
+#include "tile_mfma.hpp"
 
 namespace tpw {
 namespace {
@@ -668,6 +669,94 @@ __global__ __launch_bounds__(kThreads, 2) void bool_fp4_kernel(
     bool_epilogue<OP, EPI>(acc, smem, s_pop, b, row0, col0, n, m, d, inv_d, inv_df, out, vec_store);
 }
 
+// The tile kernel of tile_mfma.hpp on the fp4 rows (every 128-byte chunk is full by
+// construction): transposed scaled products, the counts finished per element while the tile is
+// staged, float4 row segments out.  Needs m % 4 == 0, a 16-byte aligned output and
+// rows * row bytes < 2^32.
+template <int OP, int EPI>
+__global__ __launch_bounds__(tile::kThreads, 4) void bool_fp4_tile_kernel(
+    const uint8_t *__restrict__ x1, const uint8_t *__restrict__ x2, const int32_t *__restrict__ popA,
+    const int32_t *__restrict__ popB, int64_t n, int64_t m, int64_t d, int64_t rb, double inv_d, float inv_df,
+    float *__restrict__ out, int64_t tiles_n, int64_t tiles_m, int64_t total) {
+    using namespace tile;
+    __shared__ uint4 smem[kBuf];
+    __shared__ __align__(16) uint32_t s_pop[2 * kT];  // row counts, then column counts
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
+    const int64_t row0 = tr * kT, col0 = tc * kT;
+    const uint8_t *A = x1 + b * n * rb;
+    const uint8_t *B = x2 + b * m * rb;
+    dma_tile_rows(popA + b * n, popB + b * m, true, wave, lane, row0, col0, n, m, s_pop);
+    uint32_t off[kSlots];
+    dma_offsets(off, wave, lane, row0, col0, n, m, rb);
+    dma_chunk(A, B, off, wave, 0, smem);
+
+    floatx16 facc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) facc[mi][ni][r] = 0.0f;
+
+    const int nchunks = (int)(rb / 128);
+    for (int kc = 0; kc < nchunks; ++kc) {
+        if (kc > 0) {
+            barrier_lds();  // every wave is done with chunk kc - 1
+            dma_chunk(A, B, off, wave, (int64_t)kc * 128, smem);
+        }
+        barrier_all();  // chunk kc (and, the first time, the counts) has landed
+        const uint4 *As = smem, *Bs = smem + kPanel;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int c = h * 4 + q;
+            int32x8 a[2], bv[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                const uint4 v = piece(As, wr + mi * 32 + l32, c);
+                a[mi] = int32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const uint4 v = piece(Bs, wc + ni * 32 + l32, c);
+                bv[ni] = int32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)  // transposed; formats 4 / 4: fp4 e2m1, E8M0 scales 127 = 1.0
+                    facc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv[ni], a[mi], facc[mi][ni], 4, 4,
+                                                                                  0, 127, 0, 127);
+        }
+    }
+    barrier_lds();  // the operand buffer becomes the output stage
+
+    const uint32_t du = (uint32_t)d;
+    const float df = (float)d;
+    uint32_t pav[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) pav[mi] = s_pop[wr + mi * 32 + l32];
+    store_tile<float>(
+        smem,
+        [&](int mi, int ni, int g) {
+            const uint4 pb = *reinterpret_cast<const uint4 *>(&s_pop[kT + wc + ni * 32 + 8 * g + 4 * h]);
+            const uint32_t pbe[4] = {pb.x, pb.y, pb.z, pb.w};
+            floatx4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t c = count_from_and<OP, EPI>((uint32_t)facc[mi][ni][4 * g + e], pav[mi], pbe[e]);
+                o[e] = finish<OP, EPI>(c, pav[mi], pbe[e], du, inv_d, df, inv_df);
+            }
+            return o;
+        },
+        out, b, row0, col0, n, m);
+}
+
 int64_t fp4_row_bytes(int64_t d) { return (d + 255) / 256 * 128; }
 
 template <int OP, int EPI>
@@ -678,6 +767,11 @@ int launch_bool_fp4(const uint8_t *a, const uint8_t *b, const int32_t *pa, const
     const double inv_d = d < (int64_t)kFloatExactLimit ? 1.0 / (double)d : 0.0;
     const float inv_df = 1.0f / (float)d;
     const bool vec_store = m % 4 == 0 && aligned16(out);
+    if (vec_store && (n > m ? n : m) * fp4_row_bytes(d) < ((int64_t)1 << 32)) {
+        hipLaunchKernelGGL((bool_fp4_tile_kernel<OP, EPI>), dim3((unsigned)total), dim3(tile::kThreads), 0, s, a, b,
+                           pa, pb, n, m, d, fp4_row_bytes(d), inv_d, inv_df, out, tiles_n, tiles_m, total);
+        return check_launch("bool_fp4_tile_kernel");
+    }
     hipLaunchKernelGGL((bool_fp4_kernel<OP, EPI>), dim3((unsigned)total), dim3(kThreads), 0, s, a, b, pa, pb, n, m,
                        d, fp4_row_bytes(d), inv_d, inv_df, out, tiles_n, tiles_m, total, vec_store);
     return check_launch("bool_fp4_kernel");

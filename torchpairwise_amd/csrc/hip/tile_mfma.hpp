@@ -1,0 +1,195 @@
+// Shared pieces of the 128 x 128 matrix-core tile kernels (inner.hip, popcount.hip).
+//
+// Block = 256 threads, 4 waves in a 2 x 2 grid, 64 x 64 outputs per wave as 2 x 2 blocks of a
+// 32 x 32 MFMA.  A K chunk is 128 bytes of every operand row; the chunk's A and B panels
+// (128 rows each) sit in LDS as 16-byte pieces with no padding: piece c of row r is stored at
+// position swz(r, c) of the row, which makes the MFMA's 16-byte reads of one piece across 16
+// consecutive rows conflict-free.  The chunk travels from global memory straight into LDS
+// (global_load_lds_dwordx4, one 16-byte slot per lane and instruction).
+//
+// Products are formed transposed (B rows as the MFMA's first operand), so the accumulator
+// register 4 g + e of lane (l32 + 32 h) holds output row l32 of the 32 x 32 block and column
+// 8 g + 4 h + e: four consecutive columns per register quad.  The epilogue therefore writes
+// 16-byte pieces of output rows into an LDS stage (the operand buffer, free after the K loop)
+// and the whole tile leaves in contiguous row segments (256 bytes of bf16 or 512 bytes of fp32
+// per row and instruction group).
+#pragma once
+
+#include "common.hpp"
+
+namespace tpw {
+namespace tile {
+
+constexpr int kT = 128;           // output rows and columns per tile
+constexpr int kThreads = 256;     // 4 waves
+constexpr int kPanel = kT * 8;    // uint4 per operand panel (128 rows x 8 pieces)
+constexpr int kBuf = 2 * kPanel;  // A | B panels: 32 KiB
+constexpr int kSlots = 8;         // DMA slots per lane and chunk: 2048 pieces / 256 lanes
+
+// Position of logical piece c in row r.  An involution in c for fixed r, so the DMA slot at
+// position p of row r carries logical piece swz(r, p).
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r & 7) ^ ((r >> 3) & 1)); }
+
+// 16 bytes per lane from sbase + voff into LDS at lds_base + 16 * lane.  Issued through inline
+// asm: the compiler cannot tell which LDS bytes a DMA writes and would otherwise wait for every
+// DMA in flight before any later LDS read.  Waits for these loads are explicit (barrier_all).
+__device__ __forceinline__ void dma16(const void *sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+}
+// The same for 4 bytes per lane (LDS lds_base + 4 * lane).
+__device__ __forceinline__ void dma4(const void *sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)p; }
+
+// Per-row values of the tile (128 for its rows, then 128 for its columns, 4 bytes each) into
+// LDS `dst` by DMA: wave w < 2 loads rows 64 w .. 64 w + 63, wave 2 + w the columns; indices past
+// the edge read the last element (never used).  `wave` must be wave-uniform.  Visible after
+// the next barrier_all.
+__device__ __forceinline__ void dma_tile_rows(const void *rows_base, const void *cols_base, bool cols, int wave,
+                                              int lane, int64_t row0, int64_t col0, int64_t n, int64_t m, void *dst) {
+    if (wave >= 2 && !cols) return;
+    const bool c = wave >= 2;
+    const int64_t lim = c ? m : n;
+    int64_t i = (c ? col0 : row0) + 64 * (wave & 1) + lane;
+    i = i < lim ? i : lim - 1;
+    dma4(c ? cols_base : rows_base, (uint32_t)(i * 4), lds_addr(reinterpret_cast<uint32_t *>(dst) + 64 * wave));
+}
+
+// Workgroup barrier after this wave's LDS operations have completed (_all: and its vector
+// memory operations, the DMA included).  Also a compiler barrier for memory accesses.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void barrier_all() {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Byte offsets (from each panel's batch base) of this lane's 8 DMA slots for the tile at
+// (row0, col0): slot s = (8 wave + j) 64 + lane covers panel s >> 10 (A rows, then B rows),
+// row (s >> 3) & 127 and position s & 7; rows past the edge read the last row, whose outputs
+// are never stored.  Requires rows * row_bytes < 2^32.
+__device__ __forceinline__ void dma_offsets(uint32_t (&off)[kSlots], int wave, int lane, int64_t row0, int64_t col0,
+                                            int64_t n, int64_t m, int64_t row_bytes) {
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int s = (wave * kSlots + j) * 64 + lane;
+        const int panel = s >> 10, r = (s >> 3) & (kT - 1), p = s & 7;
+        const int64_t lim = panel ? m : n;
+        int64_t row = (panel ? col0 : row0) + r;
+        row = row < lim ? row : lim - 1;
+        off[j] = (uint32_t)(row * row_bytes + swz(r, p) * 16);
+    }
+}
+
+// DMA of the 128-byte K chunk starting at byte kb of every row into the panels at buf.
+// `wave` must be wave-uniform (an SGPR).
+__device__ __forceinline__ void dma_chunk(const uint8_t *A, const uint8_t *B, const uint32_t (&off)[kSlots], int wave,
+                                          int64_t kb, uint4 *buf) {
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int first = (wave * kSlots + j) * 64;  // the wave's 64 slots lie in one panel
+        dma16((first >= kPanel ? B : A) + kb, off[j], lds_addr(buf + first));
+    }
+}
+
+// Logical piece c of row r of a panel.
+__device__ __forceinline__ uint4 piece(const uint4 *panel, int r, int c) { return panel[r * 8 + swz(r, c)]; }
+
+// Writes the tile through the LDS stage `st` (>= 32 KiB, free) in row segments.  value(mi, ni,
+// g) returns the 4 outputs of the lane's register quad g of block (mi, ni) as float: row
+// wr + 32 mi + l32, columns wc + 32 ni + 8 g + 4 h + (0..3).  Rows >= n and columns >= m are not
+// stored; m must be a multiple of 16 / sizeof(OutT) and out 16-byte aligned (a 16-byte store
+// unit is then wholly inside or outside).  bf16 stages the rounded values of the whole tile (one
+// pass of 128 rows x 256 bytes, one workgroup barrier); fp32 per wave (below).  Stage unit u of
+// row r sits at u ^ (r & 15): conflict-free 16-byte accesses across 16 rows and within 16-unit
+// groups.
+template <typename OutT, class F>
+__device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restrict__ out, int64_t b, int64_t row0,
+                                           int64_t col0, int64_t n, int64_t m) {
+    if constexpr (sizeof(OutT) == 4) {
+        // fp32: each wave stages its own 32 x 64 halves in an 8 KiB slice (no workgroup barrier)
+        // and writes 256-byte row segments, 16 lanes per row
+        const int tid = threadIdx.x, lane = tid & 63;
+        const int wave = tid >> 6;
+        const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+        const int l32 = lane & 31, h = lane >> 5;
+        floatx4 *sl = reinterpret_cast<floatx4 *>(st) + wave * 512;  // 32 rows x 16 units
+        const int ul = lane & 15, rl = lane >> 4;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int u = ni * 8 + 2 * g + h;
+                    sl[l32 * 16 + (u ^ (l32 & 15))] = value(mi, ni, g);
+                }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+            const int64_t gcol = col0 + wc + 4 * ul;
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const int r = it * 4 + rl;
+                const floatx4 v = sl[r * 16 + (ul ^ (r & 15))];
+                const int64_t grow = row0 + wr + mi * 32 + r;
+                if (grow < n && gcol < m)
+                    __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(out + (b * n + grow) * m + gcol));
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is rewritten
+            __builtin_amdgcn_wave_barrier();
+        }
+        return;
+    }
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int UPR = kT * (int)sizeof(OutT) / 16;  // 16-byte units per stage row
+    constexpr int PR = kBuf * 16 / (kT * (int)sizeof(OutT)) < kT ? kBuf * 16 / (kT * (int)sizeof(OutT)) : kT;
+    constexpr int NPASS = kT / PR;
+    constexpr int LPR = UPR;     // lanes per row when storing
+    constexpr int RPI = 64 / LPR;  // rows per store instruction
+    constexpr int ITERS = PR / (4 * RPI);
+    static_assert(PR % 64 == 0 && ITERS * 4 * RPI == PR, "stage geometry");
+#pragma unroll
+    for (int pass = 0; pass < NPASS; ++pass) {
+        if (NPASS == 1 || wr / PR == pass) {
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                const int r = wr + mi * 32 + l32 - pass * PR;  // row within the pass
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const floatx4 o = value(mi, ni, g);
+                        const int col = wc + ni * 32 + 8 * g + 4 * h;
+                        if constexpr (sizeof(OutT) == 2) {
+                            const int u = col >> 3;
+                            reinterpret_cast<uint2 *>(st)[(r * UPR + (u ^ (r & 15))) * 2 + h] =
+                                make_uint2(f32x2_to_bf16x2_rne(o[0], o[1]), f32x2_to_bf16x2_rne(o[2], o[3]));
+                        } else {
+                            const int u = col >> 2;
+                            reinterpret_cast<floatx4 *>(st)[r * UPR + (u ^ (r & 15))] = o;
+                        }
+                    }
+            }
+        }
+        barrier_lds();
+        const int ul = lane % LPR, rl = lane / LPR;
+        const int64_t gcol = col0 + ul * (16 / (int)sizeof(OutT));
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int r = (wave * ITERS + it) * RPI + rl;
+            const u32x4 v = reinterpret_cast<const u32x4 *>(st)[r * UPR + (ul ^ (r & 15))];
+            const int64_t grow = row0 + pass * PR + r;
+            if (grow < n && gcol < m)
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (b * n + grow) * m + gcol));
+        }
+        if (pass + 1 < NPASS) barrier_lds();  // the next pass rewrites the stage
+    }
+}
+
+}  // namespace tile
+}  // namespace tpw

@@ -517,6 +517,66 @@ __global__ void row_norms_kernel(const T *__restrict__ x, int64_t rows, int64_t 
     if (lane == 0) out[row] = squared ? s : sqrt_rn(s);
 }
 
+// Row norms with 16-byte loads (rows of whole 16-byte vectors, 16-byte aligned): G lanes per
+// row (a power of two, G >= the row's vector count up to 64), 64 / G rows per wave; each lane
+// sums the squares of its vectors, then a butterfly over the G lanes.
+template <typename T, int G>
+__global__ __launch_bounds__(256) void row_norms_vec_kernel(const T *__restrict__ x, int64_t rows, int64_t d,
+                                                            int squared, float *__restrict__ out) {
+    constexpr int PER = 16 / (int)sizeof(T);
+    const int lane = threadIdx.x & 63;
+    const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 / G) + lane / G;
+    const int gl = lane % G;
+    float s = 0.0f;
+    if (row < rows) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(x + row * d);
+        const int64_t nv = d / PER;
+        for (int64_t k = gl; k < nv; k += G) {
+            const uint4 v = p[k];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (sizeof(T) == 4) {
+                    const float f = __uint_as_float(w[e]);
+                    s += f * f;
+                } else {
+                    const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
+                    s += lo * lo;
+                    s += hi * hi;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (row < rows && gl == 0) out[row] = squared ? s : sqrt_rn(s);
+}
+
+template <typename T>
+int launch_row_norms(const T *x, int64_t rows, int64_t d, int squared, float *norms, hipStream_t s) {
+    const int64_t nv = d * (int64_t)sizeof(T) / 16;
+    if ((d * (int64_t)sizeof(T)) % 16 != 0 || !aligned16(x) || nv == 0) {
+        hipLaunchKernelGGL(row_norms_kernel<T>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, x, rows, d, squared,
+                           norms);
+        return check_launch("row_norms_kernel");
+    }
+    // the smallest power of two >= nv (at most 64) lanes per row
+    int g = 1;
+    while (g < 64 && g < nv) g *= 2;
+    const int64_t rows_per_block = 4 * (64 / g);
+    const dim3 grid((unsigned)cdiv(rows, rows_per_block));
+    switch (g) {
+        case 1: hipLaunchKernelGGL((row_norms_vec_kernel<T, 1>), grid, dim3(256), 0, s, x, rows, d, squared, norms); break;
+        case 2: hipLaunchKernelGGL((row_norms_vec_kernel<T, 2>), grid, dim3(256), 0, s, x, rows, d, squared, norms); break;
+        case 4: hipLaunchKernelGGL((row_norms_vec_kernel<T, 4>), grid, dim3(256), 0, s, x, rows, d, squared, norms); break;
+        case 8: hipLaunchKernelGGL((row_norms_vec_kernel<T, 8>), grid, dim3(256), 0, s, x, rows, d, squared, norms); break;
+        case 16: hipLaunchKernelGGL((row_norms_vec_kernel<T, 16>), grid, dim3(256), 0, s, x, rows, d, squared, norms); break;
+        case 32: hipLaunchKernelGGL((row_norms_vec_kernel<T, 32>), grid, dim3(256), 0, s, x, rows, d, squared, norms); break;
+        default: hipLaunchKernelGGL((row_norms_vec_kernel<T, 64>), grid, dim3(256), 0, s, x, rows, d, squared, norms); break;
+    }
+    return check_launch("row_norms_vec_kernel");
+}
+
 template <typename T, int EPI, typename OutT = T>
 int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
                  const float *aux1, const float *aux2, OutT *out, hipStream_t s,
@@ -594,13 +654,8 @@ extern "C" int tpw_row_norms(const void *x, int dtype, int64_t rows, int64_t d, 
     if (rows == 0) return TPW_OK;
     TPW_REQUIRE(x && norms, "null pointer");
     hipStream_t s = as_stream(stream);
-    if (dtype == TPW_F32)
-        hipLaunchKernelGGL(row_norms_kernel<float>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s,
-                           static_cast<const float *>(x), rows, d, squared, norms);
-    else
-        hipLaunchKernelGGL(row_norms_kernel<uint16_t>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0,
-                           s, static_cast<const uint16_t *>(x), rows, d, squared, norms);
-    return check_launch("row_norms_kernel");
+    if (dtype == TPW_F32) return launch_row_norms(static_cast<const float *>(x), rows, d, squared, norms, s);
+    return launch_row_norms(static_cast<const uint16_t *>(x), rows, d, squared, norms, s);
 }
 
 extern "C" int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int64_t batch,

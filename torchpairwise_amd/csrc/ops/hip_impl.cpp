@@ -41,9 +41,13 @@ at::Tensor pw_inner_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t epi
     if (epilogue != TPW_EPI_DOT) {
         const int squared = (epilogue == TPW_EPI_EUCLIDEAN || epilogue == TPW_EPI_SQEUCLIDEAN);
         n1 = at::empty({B, n}, a.options().dtype(at::kFloat));
-        n2 = at::empty({B, m}, a.options().dtype(at::kFloat));
         check_rc(tpw_row_norms(a.data_ptr(), dt, B * n, d, squared, n1.data_ptr<float>(), s), "row norms");
-        check_rc(tpw_row_norms(b.data_ptr(), dt, B * m, d, squared, n2.data_ptr<float>(), s), "row norms");
+        if (x2.is_same(x1)) {
+            n2 = n1;  // x2 = None: one set of norms
+        } else {
+            n2 = at::empty({B, m}, a.options().dtype(at::kFloat));
+            check_rc(tpw_row_norms(b.data_ptr(), dt, B * m, d, squared, n2.data_ptr<float>(), s), "row norms");
+        }
     }
     check_rc(tpw_pairwise_inner(a.data_ptr(), b.data_ptr(), dt, B, n, m, d,
                                 n1.defined() ? n1.data_ptr<float>() : nullptr,

@@ -424,13 +424,13 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
 // units: one 32 KiB operand buffer (4 blocks per CU), the chunk loaded by DMA while no wave
 // reads it, transposed products, and the epilogue applied while the tile is staged for
 // row-segment stores.
-template <typename T, typename OutT, int EPI>
-__global__ __launch_bounds__(tile::kThreads, 4) void inner_tile_kernel(
+template <typename T, typename OutT, int EPI, int NB = 1>
+__global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
     const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
-    int64_t tiles_n, int64_t tiles_m, int64_t total, KerParams kp) {
+    int64_t tiles_n, int64_t tiles_m, int64_t total, KerParams kp, const OutT *__restrict__ X, float sign) {
     using namespace tile;
-    __shared__ uint4 smem[kBuf];
+    __shared__ uint4 smem[NB * kBuf];
     __shared__ __align__(16) float s_aux[2 * kT];  // row norms, then column norms
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -462,12 +462,15 @@ __global__ __launch_bounds__(tile::kThreads, 4) void inner_tile_kernel(
 
     const int nchunks = (int)(row_bytes / 128);
     for (int kc = 0; kc < nchunks; ++kc) {
-        if (kc > 0) {
+        if (NB == 1 && kc > 0) {
             barrier_lds();  // every wave is done with chunk kc - 1
             dma_chunk(A, B, off, wave, (int64_t)kc * 128, smem);
         }
         barrier_all();  // chunk kc (and, the first time, the norms) has landed
-        const uint4 *As = smem, *Bs = smem + kPanel;
+        // two buffers: chunk kc + 1 goes to the buffer chunk kc - 1 used, which every wave is
+        // done with (the barrier above), while chunk kc is multiplied
+        if (NB == 2 && kc + 1 < nchunks) dma_chunk(A, B, off, wave, (int64_t)(kc + 1) * 128, smem + ((kc + 1) & 1) * kBuf);
+        const uint4 *As = smem + (NB == 2 ? (kc & 1) * kBuf : 0), *Bs = As + kPanel;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int c = h * 4 + q;
@@ -487,11 +490,30 @@ __global__ __launch_bounds__(tile::kThreads, 4) void inner_tile_kernel(
     store_tile<OutT>(
         smem,
         [&](int mi, int ni, int g) {
-            const floatx4 a2 = kAux2<EPI> ? *reinterpret_cast<const floatx4 *>(&s_aux[kT + wc + ni * 32 + 8 * g + 4 * h])
-                                          : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
             floatx4 o;
+            if constexpr (EPI == kEpiGrad) {
+                // sign * s + coef[row] * X[row][col .. col + 3] (rows and columns past the edge
+                // read nothing and are not stored)
+                const int64_t row = row0 + wr + mi * 32 + l32, col = col0 + wc + ni * 32 + 8 * g + 4 * h;
+                floatx4 xv = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (row < n && col < m) {
+                    const OutT *xp = X + (b * n + row) * m + col;
+                    if constexpr (sizeof(OutT) == 4) {
+                        xv = *reinterpret_cast<const floatx4 *>(xp);
+                    } else {
+                        const uint2 q = *reinterpret_cast<const uint2 *>(xp);
+                        xv = floatx4{__uint_as_float(q.x << 16), __uint_as_float(q.x & 0xffff0000u),
+                                     __uint_as_float(q.y << 16), __uint_as_float(q.y & 0xffff0000u)};
+                    }
+                }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = epilogue<EPI>(acc[mi][ni][4 * g + e], a1v[mi], a2[e], kp);
+                for (int e = 0; e < 4; ++e) o[e] = sign * acc[mi][ni][4 * g + e] + a1v[mi] * xv[e];
+            } else {
+                const floatx4 a2 = kAux2<EPI> ? *reinterpret_cast<const floatx4 *>(&s_aux[kT + wc + ni * 32 + 8 * g + 4 * h])
+                                              : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = epilogue<EPI>(acc[mi][ni][4 * g + e], a1v[mi], a2[e], kp);
+            }
             return o;
         },
         out, b, row0, col0, n, m);
@@ -586,12 +608,19 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
     const bool vec = ((d * (int64_t)sizeof(T)) % 16 == 0) && aligned16(x1) && aligned16(x2);
     // direct LDS loads: every chunk full, and the per-lane element offsets fit in int32
     const bool direct = vec && d % Elem<T>::kChunk == 0 && d > 0 && (n > m ? n : m) * d < ((int64_t)1 << 31);
-    if constexpr (EPI != kEpiGrad && EPI != kEpiPoly) {
-        // the tile kernel: byte offsets below 2^32, whole 16-byte units per output row
+    if constexpr (EPI != kEpiPoly) {
+        // the tile kernel: byte offsets below 2^32, whole 16-byte units per output row (and, for
+        // the gradient products, 16-byte aligned X rows)
         if (direct && (n > m ? n : m) * d * (int64_t)sizeof(T) < ((int64_t)1 << 32) && aligned16(out) &&
-            m % (16 / (int64_t)sizeof(OutT)) == 0) {
-            hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI>), dim3((unsigned)total), dim3(tile::kThreads), 0, s, x1,
-                               x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp);
+            m % (16 / (int64_t)sizeof(OutT)) == 0 && (EPI != kEpiGrad || aligned16(X))) {
+            // long K (16 chunks or more): two operand buffers, the next chunk's DMA in flight
+            // while the current one is multiplied, at two blocks per CU
+            if (d * (int64_t)sizeof(T) >= 16 * 128)
+                hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 2>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                                   s, x1, x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp, X, sign);
+            else
+                hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 1>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                                   s, x1, x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp, X, sign);
             return check_launch("inner_tile_kernel");
         }
     }

@@ -1,0 +1,93 @@
+"""The matrix-core tile kernels (16-byte aligned operands and outputs, output rows of whole
+16-byte units, full K chunks) against the register-staged kernels the same C entry points take
+otherwise (here: operands offset by one element for the inner product, an output offset by one
+element for the fp4 metrics): identical inputs, bit-identical outputs, edge tiles and long K.
+Both paths form each dot product from the same MFMA sequence (the tile kernel with the
+operands swapped) and apply the same epilogue functions."""
+import ctypes as C
+
+import pytest
+import torch
+
+from tests._util import rand, randn
+from torchpairwise_amd import _capi as capi
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+EPIS = [capi.EPI_DOT, capi.EPI_EUCLIDEAN, capi.EPI_SQEUCLIDEAN, capi.EPI_COSINE_SIM,
+        capi.EPI_COSINE_DIST, capi.EPI_CORRELATION]
+
+
+def _inner(x1, x2, epi, misaligned):
+    """tpw_pairwise_inner on 16-byte aligned inputs (the tile kernel), or on copies of them
+    offset by one element (not 16-byte aligned: the register-staged kernel with element loads);
+    the output is aligned either way."""
+    B, n, d = x1.shape
+    m = x2.shape[1]
+    if misaligned:
+        s1 = torch.empty(B * n * d + 16, dtype=x1.dtype, device=DEV)
+        s2 = torch.empty(B * m * d + 16, dtype=x2.dtype, device=DEV)
+        a, b = s1[1:1 + B * n * d].view(B, n, d), s2[1:1 + B * m * d].view(B, m, d)
+        a.copy_(x1)
+        b.copy_(x2)
+    else:
+        a, b = x1, x2
+    squared = epi in (capi.EPI_EUCLIDEAN, capi.EPI_SQEUCLIDEAN)
+    n1 = capi.row_norms(x1, squared) if epi != capi.EPI_DOT else None
+    n2 = capi.row_norms(x2, squared) if epi != capi.EPI_DOT else None
+    out = torch.empty((B, n, m), dtype=x1.dtype, device=DEV)
+    capi.call("tpw_pairwise_inner", C.c_void_p(a.data_ptr()), C.c_void_p(b.data_ptr()), capi._dtype_code(x1),
+              B, n, m, d, capi._ptr(n1), capi._ptr(n2), epi, C.c_void_p(out.data_ptr()), capi._stream())
+    return out
+
+
+def _same_bits(a, b):
+    ia = a.view(torch.int32) if a.dtype == torch.float32 else a.view(torch.int16)
+    ib = b.view(torch.int32) if b.dtype == torch.float32 else b.view(torch.int16)
+    return torch.equal(ia, ib)
+
+
+@pytest.mark.parametrize("dtype,B,n,m,d", [
+    (torch.float32, 1, 300, 260, 32),
+    (torch.float32, 2, 129, 136, 96),
+    (torch.float32, 1, 128, 256, 256),
+    (torch.float32, 1, 130, 260, 512),     # 16 chunks: the double-buffered long-K variant
+    (torch.bfloat16, 1, 300, 264, 64),
+    (torch.bfloat16, 3, 257, 520, 192),
+    (torch.bfloat16, 1, 128, 128, 256),
+    (torch.bfloat16, 1, 200, 136, 1024),   # long K
+])
+@pytest.mark.parametrize("epi", EPIS)
+def test_inner_tile_kernel_equals_staged_kernel(dtype, B, n, m, d, epi):
+    x1 = randn(B, n, d, seed=1).to(DEV, dtype)
+    x2 = randn(B, m, d, seed=2).to(DEV, dtype)
+    x2[:, 3] = 0  # a zero row: the guarded cosine divide
+    if m > 7:
+        x2[:, 7] = x1[:, 0]  # an identical pair: the clamped euclidean floor
+    tile = _inner(x1, x2, epi, False)
+    staged = _inner(x1, x2, epi, True)
+    assert _same_bits(tile, staged)
+
+
+def _fp4_metric(x1, x2, metric, misaligned):
+    (fa, ca), (fb, cb) = capi.pack_bool_fp4(x1), capi.pack_bool_fp4(x2)
+    B, n, d = x1.shape
+    m = x2.shape[1]
+    store = torch.empty(B * n * m + 16, dtype=torch.float32, device=DEV)
+    out = store[1:1 + B * n * m] if misaligned else store[:B * n * m]
+    capi.call("tpw_bool_fp4_count_metric", capi._ptr(fa), capi._ptr(fb), capi._ptr(ca), capi._ptr(cb), B, n, m, d,
+              metric, C.c_void_p(out.data_ptr()), capi._stream())
+    return out.view(B, n, m)
+
+
+@pytest.mark.parametrize("B,n,m,d", [(1, 300, 260, 100), (2, 129, 136, 1000), (1, 128, 256, 256), (1, 70, 132, 3000)])
+@pytest.mark.parametrize("metric", range(10))
+def test_fp4_tile_kernel_equals_staged_kernel(B, n, m, d, metric):
+    x1 = (rand(B, n, d, seed=3) < 0.3).to(DEV)
+    x2 = (rand(B, m, d, seed=4) < 0.3).to(DEV)
+    x2[:, 0] = False  # an all-zero row: the guarded 0 / 0 cases
+    tile = _fp4_metric(x1, x2, metric, False)
+    staged = _fp4_metric(x1, x2, metric, True)
+    assert torch.equal(torch.nan_to_num(tile, nan=-7.0).view(torch.int32),
+                       torch.nan_to_num(staged, nan=-7.0).view(torch.int32))

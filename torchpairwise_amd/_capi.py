@@ -18,7 +18,7 @@ HEADER = _PKG.parent / "include" / "torchpairwise_amd.h"
 TPW_F32, TPW_BF16, TPW_F16, TPW_F64, TPW_I8, TPW_U8, TPW_I16, TPW_I32, TPW_I64 = range(9)
 BIT_AND, BIT_OR, BIT_XOR, BIT_EQ, BIT_NE = 0, 1, 2, 3, 4
 RED_SUM, RED_MEAN = 0, 1
-EPI_DOT, EPI_EUCLIDEAN, EPI_SQEUCLIDEAN, EPI_COSINE_SIM, EPI_COSINE_DIST = 0, 1, 2, 3, 4
+EPI_DOT, EPI_EUCLIDEAN, EPI_SQEUCLIDEAN, EPI_COSINE_SIM, EPI_COSINE_DIST, EPI_CORRELATION = 0, 1, 2, 3, 4, 5
 KER_POLYNOMIAL, KER_SIGMOID, KER_RBF, KER_LAPLACIAN = 0, 1, 2, 3
 FAM_PPMINKOWSKI, FAM_WMINKOWSKI, FAM_CANBERRA, FAM_BRAYCURTIS, FAM_CHI2, FAM_JS = 0, 1, 2, 3, 4, 5
 

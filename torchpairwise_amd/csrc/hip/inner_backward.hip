@@ -48,6 +48,56 @@ __device__ __forceinline__ float ipow(float x, int k) {
 constexpr int kPWRows = 128;
 constexpr int kPWCols = 256;
 
+// One pair's stored weight w (for BF16W the euclidean / sqeuclidean weight is already rounded
+// to bf16, as the reference's bf16 autograd rounds its ratio tensor), its row-sum term rt and
+// column-sum term ct, from the upstream grad gv, av (res for euclid / sigmoid, S for the
+// polynomial and cosine modes), and for cosine the row and column norms nv, a2.
+template <int MODE, bool BF16W>
+__device__ __forceinline__ void weight_terms(float gv, float av, float nv, float a2, const KerParams &kp, float &w,
+                                             float &rt, float &ct) {
+#pragma clang fp contract(off)
+    rt = 0.0f;
+    ct = 0.0f;
+    if constexpr (MODE == kEuclid) {
+        w = av == 0.0f ? 0.0f : __fdiv_rn(gv, av);
+        if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
+        rt = w;
+        ct = w;
+    } else if constexpr (MODE == kSqEuclid) {
+        w = 2.0f * gv;
+        if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
+        rt = w;
+        ct = w;
+    } else if constexpr (MODE == kPoly) {
+        // autograd of matmul(...).mul_(gamma).add_(coef0).pow_(degree): pow's
+        // backward grad * (degree * base^(degree - 1)) (zero for degree 0), then * gamma
+        const float base = av * kp.gamma + kp.coef0;
+        const float fd = kp.degree == 0 ? 0.0f : (float)kp.degree * ipow(base, kp.degree - 1);
+        w = (gv * fd) * kp.gamma;
+    } else if constexpr (MODE == kSigmoid) {
+        // tanh's backward from its output t: grad * (1 - t * t), then * gamma
+        w = (gv * (1.0f - av * av)) * kp.gamma;
+    } else if constexpr (MODE == kDot) {
+        w = gv;  // matmul's backward: the products with grad itself
+    } else {
+        const float sv = av, a1 = nv;
+        const float den = a1 * a2;
+        const float q = den != 0.0f ? __fdiv_rn(sv, den) : sv;
+        float gq = gv;
+        if constexpr (MODE == kCosDist) {
+            const float v = 1.0f - q;
+            gq = (v >= 0.0f && v <= 2.0f) ? -gv : 0.0f;
+        } else if constexpr (MODE == kCosCorr) {
+            gq = -gv;  // neg_ then add_(1): no clamp
+        }
+        const float gS = den != 0.0f ? __fdiv_rn(gq, den) : gq;
+        const float gden = den != 0.0f ? __fdiv_rn(gS * -sv, den) : 0.0f;
+        w = gS;
+        rt = gden * a2;
+        ct = gden * a1;
+    }
+}
+
 // Pass 1.  W (type T: fp32, or bf16 rounded as the reference's bf16 autograd rounds its
 // ratio tensor) is written [n, m] to Wo and, when WTo is given, transposed [m, n] to WTo,
 // so that both gradient products read their operands k-contiguous.  The row / column sums
@@ -84,45 +134,9 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
         wb = 0;
         rt = 0.0f;
         if (!ok) return;
-        float w;
-        if constexpr (MODE == kEuclid) {
-            w = av == 0.0f ? 0.0f : __fdiv_rn(gv, av);
-            if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
-            rt = w;
-            csum += w;
-        } else if constexpr (MODE == kSqEuclid) {
-            w = 2.0f * gv;
-            if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
-            rt = w;
-            csum += w;
-        } else if constexpr (MODE == kPoly) {
-            // autograd of matmul(...).mul_(gamma).add_(coef0).pow_(degree): pow's
-            // backward grad * (degree * base^(degree - 1)) (zero for degree 0), then * gamma
-            const float base = av * kp.gamma + kp.coef0;
-            const float fd = kp.degree == 0 ? 0.0f : (float)kp.degree * ipow(base, kp.degree - 1);
-            w = (gv * fd) * kp.gamma;
-        } else if constexpr (MODE == kSigmoid) {
-            // tanh's backward from its output t: grad * (1 - t * t), then * gamma
-            w = (gv * (1.0f - av * av)) * kp.gamma;
-        } else if constexpr (MODE == kDot) {
-            w = gv;  // matmul's backward: the products with grad itself
-        } else {
-            const float sv = av, a1 = nv;
-            const float den = a1 * a2;
-            const float q = den != 0.0f ? __fdiv_rn(sv, den) : sv;
-            float gq = gv;
-            if constexpr (MODE == kCosDist) {
-                const float v = 1.0f - q;
-                gq = (v >= 0.0f && v <= 2.0f) ? -gv : 0.0f;
-            } else if constexpr (MODE == kCosCorr) {
-                gq = -gv;  // neg_ then add_(1): no clamp
-            }
-            const float gS = den != 0.0f ? __fdiv_rn(gq, den) : gq;
-            const float gden = den != 0.0f ? __fdiv_rn(gS * -sv, den) : 0.0f;
-            w = gS;
-            rt = gden * a2;
-            csum += gden * a1;
-        }
+        float w, ct;
+        weight_terms<MODE, BF16W>(gv, av, nv, a2, kp, w, rt, ct);
+        if constexpr (MODE == kEuclid || MODE == kSqEuclid || kCos) csum += ct;
         if constexpr (BF16W) {
             wb = f32_to_bf16_rne(w);
             Wo[idx] = wb;
@@ -242,6 +256,105 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
             rowpart[(b * tiles_j + tj) * n + i] = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
     }
     if (jok) colpart[(b * tiles_i + ti) * m + j] = csum;
+}
+
+// Pass 1 for fp32 weights without a transposed copy, with 16-byte accesses: the 128 x 256
+// tile of pair_weights_kernel, wave w on rows 32 w .. 32 w + 31, lane l on columns 4 l .. 4 l + 3
+// (m % 4 == 0 and 16-byte aligned arrays, so a lane's 4 columns are all inside or all
+// outside), rows in groups of 4 with the group's loads issued first.  The group's 4 row sums
+// take a transposing butterfly (xor 32 and 16 hand half of the values to the partner, xor 8,
+// 4, 2, 1 complete them): lane l then holds row 2 ((l >> 5) & 1) + ((l >> 4) & 1) of the
+// group.  Column sums meet in LDS.  Same weights (weight_terms) and partials layout as
+// pair_weights_kernel.
+template <int MODE>
+__global__ __launch_bounds__(256) void pair_weights_vec_kernel(
+    const float *__restrict__ g, const float *__restrict__ res, const float *__restrict__ n1,
+    const float *__restrict__ n2, int64_t n, int64_t m, const float *__restrict__ S,
+    float *__restrict__ rowpart, float *__restrict__ colpart, int64_t tiles_i, int64_t tiles_j,
+    float *__restrict__ Wo, KerParams kp) {
+#pragma clang fp contract(off)
+    constexpr bool kRes = MODE == kEuclid || MODE == kSigmoid;
+    constexpr bool kS = MODE == kPoly || MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+    constexpr bool kCos = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+    __shared__ floatx4 red[4][64];
+    const int64_t b = blockIdx.z, ti = blockIdx.y, tj = blockIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t j0 = tj * kPWCols + 4 * lane;
+    const bool jok = j0 < m;
+    floatx4 a2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (kCos)
+        if (jok) a2 = *reinterpret_cast<const floatx4 *>(n2 + b * m + j0);
+    floatx4 csum = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float *Av = kRes ? res : S;
+    const int grow = ((lane >> 5) & 1) * 2 + ((lane >> 4) & 1);
+    const int64_t wrow0 = ti * kPWRows + wave * 32;
+    for (int r0 = 0; r0 < 32; r0 += 4) {
+        floatx4 gv[4], av[4];
+        float nv[4];
+        bool ok[4];
+        int64_t idx[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = wrow0 + r0 + u;
+            ok[u] = i < n && jok;
+            idx[u] = ok[u] ? (b * n + i) * m + j0 : b * n * m;  // element 0 of the batch when invalid
+            gv[u] = *reinterpret_cast<const floatx4 *>(g + idx[u]);
+            av[u] = (kRes || kS) ? *reinterpret_cast<const floatx4 *>(Av + idx[u]) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            nv[u] = kCos ? n1[b * n + (ok[u] ? i : 0)] : 0.0f;
+        }
+        float rs[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            floatx4 wv = {0.0f, 0.0f, 0.0f, 0.0f};
+            float r = 0.0f;
+            if (ok[u]) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float w, rt, ct;
+                    weight_terms<MODE, false>(gv[u][c], av[u][c], nv[u], a2[c], kp, w, rt, ct);
+                    wv[c] = w;
+                    r += rt;
+                    csum[c] += ct;
+                }
+                *reinterpret_cast<floatx4 *>(Wo + idx[u]) = wv;
+            }
+            rs[u] = r;
+        }
+        const bool hi32 = (lane & 32) != 0, hi16 = (lane & 16) != 0;
+        float v2[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float mine = hi32 ? rs[2 + k] : rs[k], other = hi32 ? rs[k] : rs[2 + k];
+            v2[k] = mine + __shfl_xor(other, 32, 64);
+        }
+        float v1;
+        {
+            const float mine = hi16 ? v2[1] : v2[0], other = hi16 ? v2[0] : v2[1];
+            v1 = mine + __shfl_xor(other, 16, 64);
+        }
+        v1 += __shfl_xor(v1, 8, 64);
+        v1 += __shfl_xor(v1, 4, 64);
+        v1 += __shfl_xor(v1, 2, 64);
+        v1 += __shfl_xor(v1, 1, 64);
+        const int64_t i = wrow0 + r0 + grow;
+        if ((lane & 15) == 0 && i < n) rowpart[(b * tiles_j + tj) * n + i] = v1;
+    }
+    // column partials (zero for the kernel functions, whose W carries the whole gradient)
+    red[wave][lane] = csum;
+    __syncthreads();
+    if (tid < 64) {
+        const int64_t j = tj * kPWCols + 4 * tid;
+        floatx4 t = red[0][tid];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const floatx4 o = red[w][tid];
+            t[0] += o[0];
+            t[1] += o[1];
+            t[2] += o[2];
+            t[3] += o[3];
+        }
+        if (j < m) *reinterpret_cast<floatx4 *>(colpart + (b * tiles_i + ti) * m + j) = t;
+    }
 }
 
 // coef[b][r] = sum_t part[b][t][r] (t in order), divided by norms[b][r] when given
@@ -597,11 +710,25 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
         if (rc) return rc;
         return run_gemm<T, true>(G, x1, batch, m, d, n, 1.0f, w.coef2, x2, gx2, w.part, s);
     }
-    const int64_t ti = cdiv(n, kPWRows), tj = cdiv(m, kPWCols);
-    hipLaunchKernelGGL((pair_weights_kernel<T, MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
-                       dim3(256), 0, s, g, res, n1, n2, n, m, w.S, w.rowpart, w.colpart, ti, tj, W,
-                       kBf16 ? WT : nullptr, kp);
-    rc = check_launch("pair_weights_kernel");
+    const int64_t ti = cdiv(n, kPWRows);
+    int64_t tj = cdiv(m, kPWCols);
+    bool vec_pass = false;
+    if constexpr (!kBf16) {
+        const void *av = (MODE == kEuclid || MODE == kSigmoid) ? static_cast<const void *>(res) : w.S;
+        vec_pass = m % 4 == 0 && aligned16(g) && aligned16(av) && aligned16(W) && aligned16(w.colpart) &&
+                   (n2 == nullptr || aligned16(n2));
+    }
+    if (vec_pass) {
+        hipLaunchKernelGGL((pair_weights_vec_kernel<MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
+                           dim3(256), 0, s, reinterpret_cast<const float *>(g), reinterpret_cast<const float *>(res),
+                           n1, n2, n, m, w.S, w.rowpart, w.colpart, ti, tj, reinterpret_cast<float *>(W), kp);
+        rc = check_launch("pair_weights_vec_kernel");
+    } else {
+        hipLaunchKernelGGL((pair_weights_kernel<T, MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
+                           dim3(256), 0, s, g, res, n1, n2, n, m, w.S, w.rowpart, w.colpart, ti, tj, W,
+                           kBf16 ? WT : nullptr, kp);
+        rc = check_launch("pair_weights_kernel");
+    }
     if (rc) return rc;
     const bool cosine = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
     const float *div1 = cosine ? n1 : nullptr;

@@ -91,3 +91,49 @@ def test_fp4_tile_kernel_equals_staged_kernel(B, n, m, d, metric):
     staged = _fp4_metric(x1, x2, metric, True)
     assert torch.equal(torch.nan_to_num(tile, nan=-7.0).view(torch.int32),
                        torch.nan_to_num(staged, nan=-7.0).view(torch.int32))
+
+
+# --------------------------------------------------------------------------------------
+# fp32 backward products on the tile kernel, which reads x2 (for grad_x1) and W, x1 (for
+# grad_x2) k-major in place; inputs offset by one element take the split-K GEMM instead.
+# Bar: float64 autograd of the reference's composite on the CPU, rtol 1e-4 (+ 1e-4 * max);
+# the two device paths agree to 1e-5 * max (different summation orders).
+# --------------------------------------------------------------------------------------
+BWD_OPS = [("euclidean_distances", {}), ("sqeuclidean_distances", {}), ("cosine_distances", {}),
+           ("cosine_similarity", {}), ("correlation_distances", {}),
+           ("polynomial_kernel", dict(degree=3, gamma=0.05)), ("sigmoid_kernel", dict(gamma=0.02)),
+           ("linear_kernel", {})]
+
+
+def _leaf(x, misaligned):
+    if not misaligned:
+        return x.to(DEV).requires_grad_()
+    buf = torch.empty(x.numel() + 16, dtype=x.dtype, device=DEV)
+    v = buf[1:1 + x.numel()].view(x.shape)
+    v.copy_(x)
+    return v.requires_grad_()
+
+
+@pytest.mark.parametrize("B,n,m,d", [(1, 96, 160, 36), (2, 256, 128, 64), (1, 544, 512, 132)])
+@pytest.mark.parametrize("name,kw", BWD_OPS)
+def test_backward_products_tile_fp32(name, kw, B, n, m, d):
+    import torchpairwise_amd as tp
+    from tests._util import assert_close
+
+    print(f"{name} {kw} B={B} n={n} m={m} d={d}", flush=True)
+    fn = getattr(tp, name)
+    x1, x2, g = randn(B, n, d, seed=0), randn(B, m, d, seed=1), randn(B, n, m, seed=2)
+    grads = {}
+    for misaligned in (False, True):
+        a, b = _leaf(x1, misaligned), _leaf(x2, misaligned)
+        assert (a.data_ptr() % 16 != 0) == misaligned
+        fn(a, b, **kw).backward(g.to(DEV))
+        grads[misaligned] = (a.grad.cpu(), b.grad.cpu())
+    ra, rb = x1.double().requires_grad_(), x2.double().requires_grad_()
+    fn(ra, rb, **kw).backward(g.double())
+    for k, want in enumerate((ra.grad, rb.grad)):
+        tile, split = grads[False][k], grads[True][k]
+        scale = float(want.abs().max())
+        assert_close(tile, want, rtol=1e-4, atol=1e-4 * scale, what=f"{name} grad_x{k + 1} (tile)")
+        assert_close(split, want, rtol=1e-4, atol=1e-4 * scale, what=f"{name} grad_x{k + 1} (split-K)")
+        assert_close(tile, split.double(), rtol=0, atol=1e-5 * scale, what=f"{name} grad_x{k + 1} tile vs split-K")

@@ -108,6 +108,15 @@ int inner_dot_f32(const void *x1, const void *x2, int dtype, int64_t batch, int6
 int inner_grad_gemm(const void *A, const void *B, int dtype, int64_t batch, int64_t M, int64_t N,
                     int64_t K, float sign, const float *coef, const void *X, void *out, hipStream_t s);
 
+// The same product in fp32 with either operand stored k-major: A [batch, K, M] when a_kmajor
+// (else [batch, M, K]), B [batch, K, N] when b_kmajor (else [batch, N, K]).  Only the shapes
+// grad_product_f32_fits accepts (whole 32-element K chunks, 16-byte aligned rows and pieces).
+bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t M, int64_t N,
+                           int64_t K, const float *X, const float *out);
+int grad_product_f32(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t batch, int64_t M,
+                     int64_t N, int64_t K, float sign, const float *coef, const float *X, float *out,
+                     hipStream_t s);
+
 // Backward of _ppminkowski / _wminkowski (w != nullptr) at p = +-inf (lp_inf_backward.hip):
 // grad_x1, grad_x2 and, weighted, per-row weight-gradient partials wrows [batch, n, d].
 int lp_inf_backward(const float *g, const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,

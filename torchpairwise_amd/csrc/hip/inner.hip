@@ -423,8 +423,9 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
 // multiple of 128 bytes, 16-byte aligned rows) and outputs whose rows split into whole 16-byte
 // units: one 32 KiB operand buffer (4 blocks per CU), the chunk loaded by DMA while no wave
 // reads it, transposed products, and the epilogue applied while the tile is staged for
-// row-segment stores.
-template <typename T, typename OutT, int EPI, int NB = 1>
+// row-segment stores.  AK / BK (fp32 only): x1 / x2 stored k-major, [d, n] / [d, m] (the
+// backward's products read W^T, x1 and x2 that way, without a transposed copy).
+template <typename T, typename OutT, int EPI, int NB = 1, bool AK = false, bool BK = false>
 __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
     const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
@@ -448,9 +449,12 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
     if constexpr (kAux1<EPI>)
         dma_tile_rows(aux1 + b * n, kAux2<EPI> ? aux2 + b * m : nullptr, kAux2<EPI>, wave, lane, row0, col0, n, m,
                       s_aux);
+    static_assert(!(AK || BK) || sizeof(T) == 4, "k-major operands are fp32");
     uint32_t off[kSlots];
-    dma_offsets(off, wave, lane, row0, col0, n, m, row_bytes);
-    dma_chunk(A, B, off, wave, 0, smem);
+    dma_offsets_k<AK, BK>(off, wave, lane, row0, col0, n, m, row_bytes, n * 4, m * 4);
+    // bytes from one K chunk to the next: 128 along a row, 32 K rows of a k-major operand
+    const int64_t a_step = AK ? 128 * n : 128, b_step = BK ? 128 * m : 128;
+    dma_chunk2(A, B, off, wave, 0, 0, smem);
 
     floatx16 acc[2][2];
 #pragma unroll
@@ -464,21 +468,24 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
     for (int kc = 0; kc < nchunks; ++kc) {
         if (NB == 1 && kc > 0) {
             barrier_lds();  // every wave is done with chunk kc - 1
-            dma_chunk(A, B, off, wave, (int64_t)kc * 128, smem);
+            dma_chunk2(A, B, off, wave, kc * a_step, kc * b_step, smem);
         }
         barrier_all();  // chunk kc (and, the first time, the norms) has landed
         // two buffers: chunk kc + 1 goes to the buffer chunk kc - 1 used, which every wave is
         // done with (the barrier above), while chunk kc is multiplied
-        if (NB == 2 && kc + 1 < nchunks) dma_chunk(A, B, off, wave, (int64_t)(kc + 1) * 128, smem + ((kc + 1) & 1) * kBuf);
+        if (NB == 2 && kc + 1 < nchunks)
+            dma_chunk2(A, B, off, wave, (kc + 1) * a_step, (kc + 1) * b_step, smem + ((kc + 1) & 1) * kBuf);
         const uint4 *As = smem + (NB == 2 ? (kc & 1) * kBuf : 0), *Bs = As + kPanel;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int c = h * 4 + q;
             uint4 a[2], bv[2];
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) a[mi] = piece(As, wr + mi * 32 + l32, c);
+            for (int mi = 0; mi < 2; ++mi)
+                a[mi] = AK ? kpiece(As, wr + mi * 32 + l32, h, q) : piece(As, wr + mi * 32 + l32, c);
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) bv[ni] = piece(Bs, wc + ni * 32 + l32, c);
+            for (int ni = 0; ni < 2; ++ni)
+                bv[ni] = BK ? kpiece(Bs, wc + ni * 32 + l32, h, q) : piece(Bs, wc + ni * 32 + l32, c);
             mfma_piece_t(acc, a, bv, T{});
         }
     }
@@ -670,6 +677,45 @@ int inner_grad_gemm(const void *A, const void *B, int dtype, int64_t batch, int6
     return launch_inner<uint16_t, kEpiGrad, uint16_t>(
         static_cast<const uint16_t *>(A), static_cast<const uint16_t *>(B), batch, M, N, K, coef, nullptr,
         static_cast<uint16_t *>(out), s, static_cast<const uint16_t *>(X), sign);
+}
+
+bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t M, int64_t N,
+                           int64_t K, const float *X, const float *out) {
+    // whole K chunks; k-contiguous rows of whole chunks below 2^32 bytes per batch; k-major
+    // operands of whole 16-byte pieces; output rows of whole 16-byte units
+    auto fits = [&](const float *p, bool kmajor, int64_t rows) {
+        if (!aligned16(p) || rows <= 0) return false;
+        return kmajor ? rows % 4 == 0 && rows * 128 < ((int64_t)1 << 32) : rows * K * 4 < ((int64_t)1 << 32);
+    };
+    return K > 0 && K % Elem<float>::kChunk == 0 && N % 4 == 0 && fits(A, a_kmajor, M) && fits(B, b_kmajor, N) &&
+           aligned16(X) && aligned16(out);
+}
+
+template <bool AK, bool BK>
+int launch_grad_product_f32(const float *A, const float *B, int64_t batch, int64_t M, int64_t N, int64_t K,
+                            float sign, const float *coef, const float *X, float *out, hipStream_t s) {
+    const int64_t tiles_n = cdiv(M, kTile), tiles_m = cdiv(N, kTile), total = tiles_n * tiles_m * batch;
+    if (K * 4 >= 16 * 128)
+        hipLaunchKernelGGL((inner_tile_kernel<float, float, kEpiGrad, 2, AK, BK>), dim3((unsigned)total),
+                           dim3(tile::kThreads), 0, s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total,
+                           KerParams{}, X, sign);
+    else
+        hipLaunchKernelGGL((inner_tile_kernel<float, float, kEpiGrad, 1, AK, BK>), dim3((unsigned)total),
+                           dim3(tile::kThreads), 0, s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total,
+                           KerParams{}, X, sign);
+    return check_launch("inner_tile_kernel");
+}
+
+int grad_product_f32(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t batch, int64_t M,
+                     int64_t N, int64_t K, float sign, const float *coef, const float *X, float *out,
+                     hipStream_t s) {
+    TPW_REQUIRE(grad_product_f32_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out), "unsupported product shape");
+    if (!b_kmajor) {
+        if (!a_kmajor) return launch_inner<float, kEpiGrad, float>(A, B, batch, M, N, K, coef, nullptr, out, s, X, sign);
+        return launch_grad_product_f32<true, false>(A, B, batch, M, N, K, sign, coef, X, out, s);
+    }
+    return a_kmajor ? launch_grad_product_f32<true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
+                    : launch_grad_product_f32<false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
 }
 
 }  // namespace tpw

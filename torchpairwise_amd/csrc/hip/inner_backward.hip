@@ -22,8 +22,10 @@
 // column sums; pass 2 adds the partials in a fixed order (deterministic); pass 3 runs the
 // two products on the matrix cores with the sign/coef epilogue fused.  For cosine, S is
 // first recomputed on the MFMA path.
-//   fp32: W in fp32; v_mfma_f32_32x32x2_f32 with operands staged k-major in LDS, split over
-//         K when the output tiles alone would not fill the GPU.
+//   fp32: W in fp32; both products on the forward's tile kernel (v_mfma_f32_32x32x2_f32),
+//         which reads x2 (for grad_x1) and W, x1 (for grad_x2) k-major in place
+//         (grad_product_f32); other shapes take bwd_gemm_kernel, operands staged k-major
+//         in LDS, split over K when the output tiles alone would not fill the GPU.
 //   bf16: W rounded to bf16 (the precision of the reference's bf16 autograd) and written
 //         both [n, m] and transposed; x1, x2 transposed to [d, rows]; both products are then
 //         A . B^T with k-contiguous rows, i.e. the forward MFMA kernel (v_mfma_f32_32x32x16_bf16)
@@ -684,6 +686,22 @@ __global__ void zero_words_kernel(uint16_t *__restrict__ p, int64_t len) {
     if (t < len) p[t] = 0;
 }
 
+// fp32 gx1 = sign * W . x2 + coef1 * x1 and gx2 = sign * W^T . x1 + coef2 * x2.  The tile
+// kernel reads the operands in place, x2 (for gx1) and W, x1 (for gx2) k-major, where the
+// shapes allow; otherwise the split-K GEMM.
+int products_f32(const float *W, const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
+                 float sign, const BwdWs &w, float *gx1, float *gx2, hipStream_t s) {
+    if (grad_product_f32_fits(W, false, x2, true, n, d, m, x1, gx1) &&
+        grad_product_f32_fits(W, true, x1, true, m, d, n, x2, gx2)) {
+        const int rc = grad_product_f32(W, false, x2, true, batch, n, d, m, sign, w.coef1, x1, gx1, s);
+        if (rc) return rc;
+        return grad_product_f32(W, true, x1, true, batch, m, d, n, sign, w.coef2, x2, gx2, s);
+    }
+    const int rc = run_gemm<float, false>(W, x2, batch, n, d, m, sign, w.coef1, x1, gx1, w.part, s);
+    if (rc) return rc;
+    return run_gemm<float, true>(W, x1, batch, m, d, n, sign, w.coef2, x2, gx2, w.part, s);
+}
+
 template <typename T, int MODE>
 int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float *n1,
                  const float *n2, int dtype, int64_t batch, int64_t n, int64_t m, int64_t d, T *gx1,
@@ -705,10 +723,9 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
                            reinterpret_cast<uint16_t *>(w.coef2), 2 * batch * m);
         rc = check_launch("zero_words_kernel");
         if (rc) return rc;
-        const float *G = reinterpret_cast<const float *>(g);
-        rc = run_gemm<T, false>(G, x2, batch, n, d, m, 1.0f, w.coef1, x1, gx1, w.part, s);
-        if (rc) return rc;
-        return run_gemm<T, true>(G, x1, batch, m, d, n, 1.0f, w.coef2, x2, gx2, w.part, s);
+        return products_f32(reinterpret_cast<const float *>(g), reinterpret_cast<const float *>(x1),
+                            reinterpret_cast<const float *>(x2), batch, n, m, d, 1.0f, w,
+                            reinterpret_cast<float *>(gx1), reinterpret_cast<float *>(gx2), s);
     }
     const int64_t ti = cdiv(n, kPWRows);
     int64_t tj = cdiv(m, kPWCols);
@@ -756,10 +773,9 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     } else {
         // fp32: the k-major GEMM with split-K fills the GPU better for narrow outputs (d
         // columns) than the NT kernel did (C2 euclidean fwd+bwd 9.1 vs 10.6 ms)
-        const float *Wf = reinterpret_cast<const float *>(W);
-        rc = run_gemm<T, false>(Wf, x2, batch, n, d, m, sign, w.coef1, x1, gx1, w.part, s);
-        if (rc) return rc;
-        return run_gemm<T, true>(Wf, x1, batch, m, d, n, sign, w.coef2, x2, gx2, w.part, s);
+        return products_f32(reinterpret_cast<const float *>(W), reinterpret_cast<const float *>(x1),
+                            reinterpret_cast<const float *>(x2), batch, n, m, d, sign, w,
+                            reinterpret_cast<float *>(gx1), reinterpret_cast<float *>(gx2), s);
     }
 }
 

@@ -93,8 +93,61 @@ __device__ __forceinline__ void dma_chunk(const uint8_t *A, const uint8_t *B, co
     }
 }
 
+// k-major fp32 operands (stored [K, rows], `stride` bytes per K row): a chunk is 32 K rows x
+// the tile's 128 rows, each K row 512 contiguous bytes = 32 pieces.  Panel slot s holds K row
+// s >> 5 at position s & 31: logical piece s & 31 for K rows 0..15 and (s & 31) ^ 8 for K rows
+// 16..31 (columns xor 32), so the two half-waves' 4-byte reads below fall on different banks.
+// Pieces past the operand's `lim` rows (a multiple of 4) read its last piece.
+__device__ __forceinline__ uint32_t kmajor_offset(int s, int64_t row0, int64_t lim, int64_t stride) {
+    const int kr = s >> 5, lp = (s & 31) ^ ((kr >> 4) << 3);
+    int64_t r = row0 + 4 * lp;
+    r = r < lim ? r : lim - 4;
+    return (uint32_t)(kr * stride + r * 4);
+}
+
+// dma_offsets for either panel stored k-major (AK: the A rows, BK: the B rows; `a_stride` /
+// `b_stride` bytes per K row) or k-contiguous (`row_bytes` per row).
+template <bool AK, bool BK>
+__device__ __forceinline__ void dma_offsets_k(uint32_t (&off)[kSlots], int wave, int lane, int64_t row0, int64_t col0,
+                                              int64_t n, int64_t m, int64_t row_bytes, int64_t a_stride,
+                                              int64_t b_stride) {
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int s = (wave * kSlots + j) * 64 + lane;
+        const int panel = s >> 10;
+        if ((panel == 0 && AK) || (panel == 1 && BK)) {
+            off[j] = panel ? kmajor_offset(s & (kPanel - 1), col0, m, b_stride)
+                           : kmajor_offset(s & (kPanel - 1), row0, n, a_stride);
+        } else {
+            const int r = (s >> 3) & (kT - 1), p = s & 7;
+            const int64_t lim = panel ? m : n;
+            int64_t row = (panel ? col0 : row0) + r;
+            row = row < lim ? row : lim - 1;
+            off[j] = (uint32_t)(row * row_bytes + swz(r, p) * 16);
+        }
+    }
+}
+
+// dma_chunk with a separate chunk offset per panel (ka bytes into A, kb into B).
+__device__ __forceinline__ void dma_chunk2(const uint8_t *A, const uint8_t *B, const uint32_t (&off)[kSlots], int wave,
+                                           int64_t ka, int64_t kb, uint4 *buf) {
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int first = (wave * kSlots + j) * 64;
+        dma16(first >= kPanel ? B + kb : A + ka, off[j], lds_addr(buf + first));
+    }
+}
+
 // Logical piece c of row r of a panel.
 __device__ __forceinline__ uint4 piece(const uint4 *panel, int r, int c) { return panel[r * 8 + swz(r, c)]; }
+
+// The fp32 values at K = 16 h + 4 q + (0..3) of row r of a k-major panel, as one piece (the same
+// K order as piece(panel, r, 4 h + q) of a k-contiguous panel).
+__device__ __forceinline__ uint4 kpiece(const uint4 *panel, int r, int h, int q) {
+    const float *f = reinterpret_cast<const float *>(panel) + (16 * h + 4 * q) * kT + (r ^ (32 * h));
+    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[kT]), __float_as_uint(f[2 * kT]),
+                      __float_as_uint(f[3 * kT]));
+}
 
 // Writes the tile through the LDS stage `st` (>= 32 KiB, free) in row segments.  value(mi, ni,
 // g) returns the 4 outputs of the lane's register quad g of block (mi, ni) as float: row

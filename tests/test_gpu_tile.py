@@ -94,8 +94,10 @@ def test_fp4_tile_kernel_equals_staged_kernel(B, n, m, d, metric):
 
 
 # --------------------------------------------------------------------------------------
-# fp32 backward products on the tile kernel, which reads x2 (for grad_x1) and W, x1 (for
-# grad_x2) k-major in place; inputs offset by one element take the split-K GEMM instead.
+# fp32 backward on the matrix-core tile kernels: the weights formed inside the grad_x1 product
+# (euclidean, sqeuclidean, polynomial, sigmoid; 128 x 256 tiles, two column tiles at d = 300),
+# x2 (for grad_x1) and W, x1 (for grad_x2) read k-major in place; inputs offset by one element
+# take the weight pass and the split-K GEMM instead.
 # Bar: float64 autograd of the reference's composite on the CPU, rtol 1e-4 (+ 1e-4 * max);
 # the two device paths agree to 1e-5 * max (different summation orders).
 # --------------------------------------------------------------------------------------
@@ -114,7 +116,7 @@ def _leaf(x, misaligned):
     return v.requires_grad_()
 
 
-@pytest.mark.parametrize("B,n,m,d", [(1, 96, 160, 36), (2, 256, 128, 64), (1, 544, 512, 132)])
+@pytest.mark.parametrize("B,n,m,d", [(1, 96, 160, 36), (2, 256, 128, 64), (1, 544, 512, 132), (1, 128, 96, 300)])
 @pytest.mark.parametrize("name,kw", BWD_OPS)
 def test_backward_products_tile_fp32(name, kw, B, n, m, d):
     import torchpairwise_amd as tp

@@ -108,8 +108,9 @@ int inner_dot_f32(const void *x1, const void *x2, int dtype, int64_t batch, int6
 int inner_grad_gemm(const void *A, const void *B, int dtype, int64_t batch, int64_t M, int64_t N,
                     int64_t K, float sign, const float *coef, const void *X, void *out, hipStream_t s);
 
-// The same product in fp32 with either operand stored k-major: A [batch, K, M] when a_kmajor
-// (else [batch, M, K]), B [batch, K, N] when b_kmajor (else [batch, N, K]).  Only the shapes
+// The same product in fp32 with A stored k-major [batch, K, M] when a_kmajor (else [batch, M,
+// K]) and B k-major [batch, K, N] (b_kmajor must be true).  coef == nullptr: coef[row] is the
+// sum over K of A's row (for A = W^T, the column sums of W).  Only the shapes
 // grad_product_f32_fits accepts (whole 32-element K chunks, 16-byte aligned rows and pieces).
 bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t M, int64_t N,
                            int64_t K, const float *X, const float *out);

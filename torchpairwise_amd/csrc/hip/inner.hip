@@ -52,6 +52,8 @@ struct Elem<uint16_t> {  // bf16 bits
 // Gradient products of the backward (not a public epilogue code): out = sign * s +
 // aux1[row] * X[row, col], X having the output's type and shape.
 constexpr int kEpiGrad = 100;
+// The same with coef[row] = the sum over K of A's row (tile kernel only).
+constexpr int kEpiGradA = 101;
 // The kernel functions of tpw_pairwise_kernel: (s gamma + coef0)^degree and
 // tanh(s gamma + coef0).
 constexpr int kEpiPoly = 101;
@@ -463,6 +465,8 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
         for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+    // kEpiGradA: this lane's share of its A rows' sums (its half of every chunk, in K order)
+    float rsum[2] = {0.0f, 0.0f};
 
     const int nchunks = (int)(row_bytes / 128);
     for (int kc = 0; kc < nchunks; ++kc) {
@@ -487,18 +491,32 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
             for (int ni = 0; ni < 2; ++ni)
                 bv[ni] = BK ? kpiece(Bs, wc + ni * 32 + l32, h, q) : piece(Bs, wc + ni * 32 + l32, c);
             mfma_piece_t(acc, a, bv, T{});
+            if constexpr (EPI == kEpiGradA) {
+                // after the products that read the same registers (no wait of its own)
+                static_assert(sizeof(T) == 4, "row sums of fp32 operands");
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi) {
+                    rsum[mi] += __uint_as_float(a[mi].x);
+                    rsum[mi] += __uint_as_float(a[mi].y);
+                    rsum[mi] += __uint_as_float(a[mi].z);
+                    rsum[mi] += __uint_as_float(a[mi].w);
+                }
+            }
         }
     }
     barrier_lds();  // the operand buffer becomes the output stage
 
     float a1v[2];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) a1v[mi] = kAux1<EPI> ? s_aux[wr + mi * 32 + l32] : 0.0f;
+    for (int mi = 0; mi < 2; ++mi)
+        a1v[mi] = EPI == kEpiGradA ? rsum[mi] + __shfl_xor(rsum[mi], 32, 64)  // both K halves
+                  : kAux1<EPI>     ? s_aux[wr + mi * 32 + l32]
+                                   : 0.0f;
     store_tile<OutT>(
         smem,
         [&](int mi, int ni, int g) {
             floatx4 o;
-            if constexpr (EPI == kEpiGrad) {
+            if constexpr (EPI == kEpiGrad || EPI == kEpiGradA) {
                 // sign * s + coef[row] * X[row][col .. col + 3] (rows and columns past the edge
                 // read nothing and are not stored)
                 const int64_t row = row0 + wr + mi * 32 + l32, col = col0 + wc + ni * 32 + 8 * g + 4 * h;
@@ -691,16 +709,16 @@ bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b
            aligned16(X) && aligned16(out);
 }
 
-template <bool AK, bool BK>
+template <int EPI, bool AK, bool BK>
 int launch_grad_product_f32(const float *A, const float *B, int64_t batch, int64_t M, int64_t N, int64_t K,
                             float sign, const float *coef, const float *X, float *out, hipStream_t s) {
     const int64_t tiles_n = cdiv(M, kTile), tiles_m = cdiv(N, kTile), total = tiles_n * tiles_m * batch;
     if (K * 4 >= 16 * 128)
-        hipLaunchKernelGGL((inner_tile_kernel<float, float, kEpiGrad, 2, AK, BK>), dim3((unsigned)total),
+        hipLaunchKernelGGL((inner_tile_kernel<float, float, EPI, 2, AK, BK>), dim3((unsigned)total),
                            dim3(tile::kThreads), 0, s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total,
                            KerParams{}, X, sign);
     else
-        hipLaunchKernelGGL((inner_tile_kernel<float, float, kEpiGrad, 1, AK, BK>), dim3((unsigned)total),
+        hipLaunchKernelGGL((inner_tile_kernel<float, float, EPI, 1, AK, BK>), dim3((unsigned)total),
                            dim3(tile::kThreads), 0, s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total,
                            KerParams{}, X, sign);
     return check_launch("inner_tile_kernel");
@@ -710,12 +728,12 @@ int grad_product_f32(const float *A, bool a_kmajor, const float *B, bool b_kmajo
                      int64_t N, int64_t K, float sign, const float *coef, const float *X, float *out,
                      hipStream_t s) {
     TPW_REQUIRE(grad_product_f32_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out), "unsupported product shape");
-    if (!b_kmajor) {
-        if (!a_kmajor) return launch_inner<float, kEpiGrad, float>(A, B, batch, M, N, K, coef, nullptr, out, s, X, sign);
-        return launch_grad_product_f32<true, false>(A, B, batch, M, N, K, sign, coef, X, out, s);
-    }
-    return a_kmajor ? launch_grad_product_f32<true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
-                    : launch_grad_product_f32<false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
+    TPW_REQUIRE(b_kmajor, "k-contiguous B: inner_grad_gemm");
+    if (coef == nullptr)
+        return a_kmajor ? launch_grad_product_f32<kEpiGradA, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
+                        : launch_grad_product_f32<kEpiGradA, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
+    return a_kmajor ? launch_grad_product_f32<kEpiGrad, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
+                    : launch_grad_product_f32<kEpiGrad, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
 }
 
 }  // namespace tpw

@@ -25,12 +25,16 @@
 //   fp32: W in fp32; both products on the forward's tile kernel (v_mfma_f32_32x32x2_f32),
 //         which reads x2 (for grad_x1) and W, x1 (for grad_x2) k-major in place
 //         (grad_product_f32); other shapes take bwd_gemm_kernel, operands staged k-major
-//         in LDS, split over K when the output tiles alone would not fill the GPU.
+//         in LDS, split over K when the output tiles alone would not fill the GPU.  For the
+//         modes whose row terms are the weights (or zero), passes 1-2 and the grad_x1
+//         product are one kernel (fused_grad1_kernel) and grad_x2 sums W's columns from its
+//         own operand.
 //   bf16: W rounded to bf16 (the precision of the reference's bf16 autograd) and written
 //         both [n, m] and transposed; x1, x2 transposed to [d, rows]; both products are then
 //         A . B^T with k-contiguous rows, i.e. the forward MFMA kernel (v_mfma_f32_32x32x16_bf16)
 //         with a gradient epilogue (inner_grad_gemm).
 #include "common.hpp"
+#include "tile_mfma.hpp"
 
 namespace tpw {
 namespace {
@@ -686,6 +690,153 @@ __global__ void zero_words_kernel(uint16_t *__restrict__ p, int64_t len) {
     if (t < len) p[t] = 0;
 }
 
+// Weight pass and grad_x1 product in one kernel (fp32; the modes whose row terms are the
+// weights themselves or zero: euclidean, sqeuclidean, polynomial, sigmoid).  A block owns a
+// 128 x 256 tile of grad_x1 = sign * W . x2 + coef1 * x1, K = m in 32-column chunks: grad
+// (and res / S) of the tile's rows travel by DMA into k-contiguous panels (tile_mfma.hpp's
+// layout), x2's chunk (32 rows x 256 columns, k-major) into a third panel.  Wave w owns rows
+// 32 w .. 32 w + 31 across all 256 columns (8 MFMA blocks), so each weight is formed once per
+// block, by the lane that feeds it to the MFMA (weight_terms: the same values as the weight
+// pass), and written once to W for the grad_x2 product; coef1[i] = sum_j rt accumulates per
+// lane in K order (each lane sums its half of every chunk; the halves are added at the end).
+// The weights of step q + 1 are formed while step q's products run.  One 64 KiB buffer, two
+// blocks per CU.
+constexpr int kFCols = 256;
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
+    const float *__restrict__ g, const float *__restrict__ av, const float *__restrict__ x2,
+    const float *__restrict__ x1, int64_t n, int64_t m, int64_t d, float *__restrict__ W, float *__restrict__ gx1,
+    int64_t tiles_n, int64_t tiles_c, int64_t total, KerParams kp, float sign) {
+    using namespace tile;
+    constexpr bool kAv = MODE == kEuclid || MODE == kSigmoid || MODE == kPoly;
+    __shared__ uint4 smem[4 * kPanel];  // grad | res or S | x2 (two panels)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave * 32;
+    const int l32 = lane & 31, h = lane >> 5;
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_c, total, b, tr, tc);
+    const int64_t row0 = tr * kT, col0 = tc * kFCols;
+    const uint8_t *G = reinterpret_cast<const uint8_t *>(g + b * n * m);
+    const uint8_t *AV = kAv ? reinterpret_cast<const uint8_t *>(av + b * n * m) : G;
+    const uint8_t *X2 = reinterpret_cast<const uint8_t *>(x2 + b * m * d);
+    // 16 DMA slots per lane and chunk: wave 0 the grad panel, wave 1 the res / S panel, waves
+    // 2 and 3 the x2 panel (K row kr at 64 positions, columns xor 32 for K rows 16..31)
+    uint32_t off[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int s = (wave * 16 + j) * 64 + lane;
+        if (s < 2 * kPanel) {
+            const int r = (s >> 3) & (kT - 1), p = s & 7;
+            const int64_t row = row0 + r < n ? row0 + r : n - 1;
+            off[j] = (uint32_t)(row * m * 4 + swz(r, p) * 16);
+        } else {
+            const int t = s - 2 * kPanel, kr = t >> 6, lp = (t & 63) ^ ((kr >> 4) << 3);
+            int64_t c = col0 + 4 * lp;
+            c = c < d ? c : d - 4;
+            off[j] = (uint32_t)(kr * d * 4 + c * 4);
+        }
+    }
+    floatx16 acc[8];
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[ni][r] = 0.0f;
+    float rsum = 0.0f;
+    // the lane's W row; rows past n store row n - 1, whose weights they duplicate exactly (the
+    // same clamped inputs), as do the tiles of further column blocks: no branches in the K loop
+    const int r = wr + l32;
+    const int64_t wrow = row0 + r < n ? row0 + r : n - 1;
+    float *Wrow = W + (b * n + wrow) * m;
+    const uint4 *Gs = smem, *As = smem + kPanel, *Bs = smem + 2 * kPanel;
+    // the weights of the lane's piece at step q of the chunk (K = 16 h + 4 q + e), and their row
+    // terms into rsum (vector types, not arrays: an array here is placed in LDS by the compiler)
+    auto weights = [&](int q) {
+        const int c = h * 4 + q;
+        const floatx4 gv = __builtin_bit_cast(floatx4, piece(Gs, r, c));
+        const floatx4 avv = kAv ? __builtin_bit_cast(floatx4, piece(As, r, c)) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        floatx4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float we, rt, ct;
+            weight_terms<MODE, false>(gv[e], avv[e], 0.0f, 0.0f, kp, we, rt, ct);
+            w[e] = we;
+            rsum += rt;
+        }
+        return w;
+    };
+    const int nchunks = (int)(m / 32);
+    for (int kc = 0; kc < nchunks; ++kc) {
+        if (kc > 0) barrier_lds();  // every wave is done with chunk kc - 1
+        if (wave != 1 || kAv) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int first = (wave * 16 + j) * 64;
+                const uint8_t *base = first < kPanel       ? G + (int64_t)kc * 128
+                                      : first < 2 * kPanel ? AV + (int64_t)kc * 128
+                                                           : X2 + (int64_t)kc * 128 * d;
+                dma16(base, off[j], lds_addr(smem + first));
+            }
+        }
+        barrier_all();
+        floatx4 wn = weights(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const floatx4 a = wn;
+            floatx4 bv[8];
+#pragma unroll
+            for (int ni = 0; ni < 8; ++ni) {
+                const float *f = reinterpret_cast<const float *>(Bs) + (16 * h + 4 * q) * kFCols +
+                                 ((ni * 32 + l32) ^ (32 * h));
+                bv[ni] = floatx4{f[0], f[kFCols], f[2 * kFCols], f[3 * kFCols]};
+            }
+            *reinterpret_cast<floatx4 *>(Wrow + (int64_t)kc * 32 + 4 * (h * 4 + q)) = a;
+            if (q < 3) wn = weights(q + 1);  // formed while this step's products run
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ni = 0; ni < 8; ++ni)
+                    acc[ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[ni][e], a[e], acc[ni], 0, 0, 0);
+            if (q < 3) {
+                // one product, then two VALU instructions, over the step
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                }
+            }
+        }
+    }
+    barrier_lds();  // the buffer becomes the output stage
+    const float a1v = rsum + __shfl_xor(rsum, 32, 64);  // both K halves
+    floatx4 *sl = reinterpret_cast<floatx4 *>(smem) + wave * 1024;  // 16 KiB per wave
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+        store_wave_rows_f32<4>(
+            sl,
+            [&](int ni, int gq) {
+                const int64_t row = row0 + r, col = col0 + half * 128 + ni * 32 + 8 * gq + 4 * h;
+                floatx4 xv = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (row < n && col < d) xv = *reinterpret_cast<const floatx4 *>(x1 + (b * n + row) * d + col);
+                floatx4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = sign * acc[half * 4 + ni][4 * gq + e] + a1v * xv[e];
+                return o;
+            },
+            gx1, b, row0 + wr, col0 + half * 128, n, d);
+}
+
+// The fused path's shapes: whole K chunks both ways (m and n multiples of 32), d a multiple of
+// 4, 16-byte aligned arrays, per-batch byte offsets of grad below 2^32.
+bool fused_fits(const void *g, const void *av, const float *x1, const float *x2, const void *W, const void *gx1,
+                const void *gx2, int64_t n, int64_t m, int64_t d) {
+    return n > 0 && m > 0 && d > 0 && n % 32 == 0 && m % 32 == 0 && d % 4 == 0 && n * m * 4 < ((int64_t)1 << 32) &&
+           aligned16(g) && aligned16(av) && aligned16(W) && aligned16(gx1) &&
+           grad_product_f32_fits(static_cast<const float *>(W), true, x1, true, m, d, n, x2,
+                                 static_cast<const float *>(gx2)) &&
+           aligned16(x1) && aligned16(x2);
+}
+
 // fp32 gx1 = sign * W . x2 + coef1 * x1 and gx2 = sign * W^T . x1 + coef2 * x2.  The tile
 // kernel reads the operands in place, x2 (for gx1) and W, x1 (for gx2) k-major, where the
 // shapes allow; otherwise the split-K GEMM.
@@ -726,6 +877,30 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
         return products_f32(reinterpret_cast<const float *>(g), reinterpret_cast<const float *>(x1),
                             reinterpret_cast<const float *>(x2), batch, n, m, d, 1.0f, w,
                             reinterpret_cast<float *>(gx1), reinterpret_cast<float *>(gx2), s);
+    }
+    if constexpr (!kBf16 && (MODE == kEuclid || MODE == kSqEuclid || MODE == kSigmoid || MODE == kPoly)) {
+        // fp32: weights formed inside the grad_x1 product (which also writes W); grad_x2 takes
+        // coef2 = the column sums of W from its own operand (zero for the kernel functions)
+        const float *gf = reinterpret_cast<const float *>(g);
+        const float *av = MODE == kPoly ? w.S : reinterpret_cast<const float *>(res);
+        const float *x1f = reinterpret_cast<const float *>(x1), *x2f = reinterpret_cast<const float *>(x2);
+        float *Wf = reinterpret_cast<float *>(W);
+        float *g1 = reinterpret_cast<float *>(gx1), *g2 = reinterpret_cast<float *>(gx2);
+        if (fused_fits(gf, MODE == kSqEuclid ? gf : av, x1f, x2f, Wf, g1, g2, n, m, d)) {
+            const float sign = (MODE == kPoly || MODE == kSigmoid) ? 1.0f : -1.0f;
+            const int64_t tiles_n = cdiv(n, tile::kT), tiles_c = cdiv(d, kFCols), total = tiles_n * tiles_c * batch;
+            hipLaunchKernelGGL((fused_grad1_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, s, gf, av, x2f, x1f,
+                               n, m, d, Wf, g1, tiles_n, tiles_c, total, kp, sign);
+            rc = check_launch("fused_grad1_kernel");
+            if (rc) return rc;
+            if constexpr (MODE == kEuclid || MODE == kSqEuclid)
+                return grad_product_f32(Wf, true, x1f, true, batch, m, d, n, sign, nullptr, x2f, g2, s);
+            hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(2 * batch * m, 256)), dim3(256), 0, s,
+                               reinterpret_cast<uint16_t *>(w.coef2), 2 * batch * m);
+            rc = check_launch("zero_words_kernel");
+            if (rc) return rc;
+            return grad_product_f32(Wf, true, x1f, true, batch, m, d, n, sign, w.coef2, x2f, g2, s);
+        }
     }
     const int64_t ti = cdiv(n, kPWRows);
     int64_t tj = cdiv(m, kPWCols);

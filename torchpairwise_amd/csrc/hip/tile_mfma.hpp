@@ -149,49 +149,59 @@ __device__ __forceinline__ uint4 kpiece(const uint4 *panel, int r, int h, int q)
                       __float_as_uint(f[3 * kT]));
 }
 
+// One wave's 32 x (32 NI) fp32 outputs through its own LDS slice `sl` (NI * 4 KiB; no
+// workgroup barrier), written as (NI * 128)-byte row segments, 8 NI lanes per row.  value(ni,
+// g) returns the lane's register quad g of block ni: row grow0 + l32, columns gcol0 + 32 ni +
+// 8 g + 4 h + (0..3).  Rows >= n and columns >= m are not stored (m a multiple of 4, out
+// 16-byte aligned).  Stage unit u of row r sits at u ^ (r & 15).
+template <int NI, class F>
+__device__ __forceinline__ void store_wave_rows_f32(floatx4 *sl, F &&value, float *__restrict__ out, int64_t b,
+                                                    int64_t grow0, int64_t gcol0, int64_t n, int64_t m) {
+    constexpr int U = NI * 8;    // 16-byte units per stage row
+    constexpr int RPI = 64 / U;  // rows per store instruction
+    const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+    const int ul = lane % U, rl = lane / U;
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int u = ni * 8 + 2 * g + h;
+            sl[l32 * U + (u ^ (l32 & 15))] = value(ni, g);
+        }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    const int64_t gcol = gcol0 + 4 * ul;
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+        const int r = it * RPI + rl;
+        const floatx4 v = sl[r * U + (ul ^ (r & 15))];
+        const int64_t grow = grow0 + r;
+        if (grow < n && gcol < m)
+            __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(out + (b * n + grow) * m + gcol));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is rewritten
+    __builtin_amdgcn_wave_barrier();
+}
+
 // Writes the tile through the LDS stage `st` (>= 32 KiB, free) in row segments.  value(mi, ni,
 // g) returns the 4 outputs of the lane's register quad g of block (mi, ni) as float: row
 // wr + 32 mi + l32, columns wc + 32 ni + 8 g + 4 h + (0..3).  Rows >= n and columns >= m are not
 // stored; m must be a multiple of 16 / sizeof(OutT) and out 16-byte aligned (a 16-byte store
 // unit is then wholly inside or outside).  bf16 stages the rounded values of the whole tile (one
-// pass of 128 rows x 256 bytes, one workgroup barrier); fp32 per wave (below).  Stage unit u of
-// row r sits at u ^ (r & 15): conflict-free 16-byte accesses across 16 rows and within 16-unit
-// groups.
+// pass of 128 rows x 256 bytes, one workgroup barrier); fp32 per wave (store_wave_rows_f32, an
+// 8 KiB slice each).  Stage unit u of row r sits at u ^ (r & 15): conflict-free 16-byte accesses
+// across 16 rows and within 16-unit groups.
 template <typename OutT, class F>
 __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restrict__ out, int64_t b, int64_t row0,
                                            int64_t col0, int64_t n, int64_t m) {
     if constexpr (sizeof(OutT) == 4) {
-        // fp32: each wave stages its own 32 x 64 halves in an 8 KiB slice (no workgroup barrier)
-        // and writes 256-byte row segments, 16 lanes per row
-        const int tid = threadIdx.x, lane = tid & 63;
-        const int wave = tid >> 6;
+        const int wave = threadIdx.x >> 6;
         const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
-        const int l32 = lane & 31, h = lane >> 5;
-        floatx4 *sl = reinterpret_cast<floatx4 *>(st) + wave * 512;  // 32 rows x 16 units
-        const int ul = lane & 15, rl = lane >> 4;
+        floatx4 *sl = reinterpret_cast<floatx4 *>(st) + wave * 512;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int u = ni * 8 + 2 * g + h;
-                    sl[l32 * 16 + (u ^ (l32 & 15))] = value(mi, ni, g);
-                }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_wave_barrier();
-            const int64_t gcol = col0 + wc + 4 * ul;
-#pragma unroll
-            for (int it = 0; it < 8; ++it) {
-                const int r = it * 4 + rl;
-                const floatx4 v = sl[r * 16 + (ul ^ (r & 15))];
-                const int64_t grow = row0 + wr + mi * 32 + r;
-                if (grow < n && gcol < m)
-                    __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(out + (b * n + grow) * m + gcol));
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is rewritten
-            __builtin_amdgcn_wave_barrier();
-        }
+        for (int mi = 0; mi < 2; ++mi)
+            store_wave_rows_f32<2>(
+                sl, [&](int ni, int g) { return value(mi, ni, g); }, out, b, row0 + wr + mi * 32, col0 + wc, n, m);
         return;
     }
     const int tid = threadIdx.x, lane = tid & 63;

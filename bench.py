@@ -45,7 +45,7 @@ PEAK_HBM = 8.0e12
 # non-packed VALU issue rate of 7.86e13 lane-ops/s
 PEAK_VALU_LANE_OPS = 256 * 4 * 32 * 2.4e9
 # the headline's dominant kernel as rocprofv3 names it (euclidean epilogue, fp32 in and out)
-HEADLINE_KERNEL = "inner_tile_kernel<float,float,1>"
+HEADLINE_KERNEL = "inner_tile_kernel<float,float,1,1,false,false>"
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "traffic_euclidean_manhattan_hamming_16384x128.txt")
 

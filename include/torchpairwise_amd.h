@@ -94,6 +94,17 @@ int tpw_bool_pairwise_reduce(const uint32_t *x1_words, const uint32_t *x2_words,
                              int64_t batch, int64_t n, int64_t m, int64_t d, int op,
                              int reduction, float *out, void *stream);
 
+/* The same reduction given the rows' popcounts (tpw_pack_bool_rows' row_popcounts):
+ * for rows of more than 256 features every op's count follows from the AND count
+ * and the popcounts (or = pa + pb - and, xor = ne = pa + pb - 2 and,
+ * eq = d - xor), which the matrix cores form; results equal
+ * tpw_bool_pairwise_reduce's bit for bit.  Replaces the same reference kernels
+ * (csrc/ops/cuda/pairwise_binary_kernels.cu:32-53,144-220). */
+int tpw_bool_pairwise_reduce_counted(const uint32_t *x1_words, const uint32_t *x2_words,
+                                     const int32_t *x1_popcounts, const int32_t *x2_popcounts,
+                                     int64_t batch, int64_t n, int64_t m, int64_t d, int op,
+                                     int reduction, float *out, void *stream);
+
 /* jaccard_distances on bool: out = prf_div(xor_count, or_count, "zero"), i.e.
  * or == 0 ? 0 : fl32(xor) / fl32(or), from AND counts and row popcounts
  * (xor = pa + pb - 2 and, or = pa + pb - and).  Replaces the three passes

@@ -1,9 +1,11 @@
 """The matrix-core tile kernels (16-byte aligned operands and outputs, output rows of whole
-16-byte units, full K chunks) against the register-staged kernels the same C entry points take
-otherwise (here: operands offset by one element for the inner product, an output offset by one
-element for the fp4 metrics): identical inputs, bit-identical outputs, edge tiles and long K.
-Both paths form each dot product from the same MFMA sequence (the tile kernel with the
-operands swapped) and apply the same epilogue functions."""
+16-byte units, full K chunks) against the kernels the same C entry points take otherwise (here:
+operands offset by one element for the inner product, an output offset by one element for the
+fp4 metrics and the bit-packed rows): identical inputs, bit-identical outputs, edge tiles and
+long K.
+The inner-product paths form each dot product from the same MFMA sequence (the tile kernel
+with the operands swapped); the boolean counts are exact integers on every path; all of them
+finish with the same epilogue functions."""
 import ctypes as C
 
 import pytest
@@ -91,6 +93,52 @@ def test_fp4_tile_kernel_equals_staged_kernel(B, n, m, d, metric):
     staged = _fp4_metric(x1, x2, metric, True)
     assert torch.equal(torch.nan_to_num(tile, nan=-7.0).view(torch.int32),
                        torch.nan_to_num(staged, nan=-7.0).view(torch.int32))
+
+
+# --------------------------------------------------------------------------------------
+# Bit-packed rows on the fp4 matrix cores (bool_bits_tile_kernel, rows of more than 256
+# features) against the popcount kernel the same entry points take for an output offset by
+# one element: every count metric, jaccard, and every op x reduction of the counted entry;
+# partial last chunks (d = 257: 3 of 8 pieces; 1500: 2 chunks, the second half full; 2081:
+# 3 chunks, the last one piece), edge tiles.  Bit-identical.
+# --------------------------------------------------------------------------------------
+def _bits_call(x1, x2, kind, code, misaligned):
+    wa, pa = capi.pack_bool(x1)
+    wb, pb = capi.pack_bool(x2)
+    B, n, d = x1.shape
+    m = x2.shape[1]
+    store = torch.empty(B * n * m + 16, dtype=torch.float32, device=DEV)
+    out = store[1:1 + B * n * m] if misaligned else store[:B * n * m]
+    o = C.c_void_p(out.data_ptr())
+    if kind == "metric":
+        capi.call("tpw_bool_count_metric", capi._ptr(wa), capi._ptr(wb), capi._ptr(pa), capi._ptr(pb), B, n, m, d,
+                  code, o, capi._stream())
+    elif kind == "jaccard":
+        capi.call("tpw_jaccard_bool", capi._ptr(wa), capi._ptr(wb), capi._ptr(pa), capi._ptr(pb), B, n, m, d, o,
+                  capi._stream())
+    else:
+        op, red = code
+        capi.call("tpw_bool_pairwise_reduce_counted", capi._ptr(wa), capi._ptr(wb), capi._ptr(pa), capi._ptr(pb),
+                  B, n, m, d, op, red, o, capi._stream())
+    return out.view(B, n, m)
+
+
+BITS_CASES = ([("metric", k) for k in range(10)] + [("jaccard", 0)] +
+              [("reduce", (op, red)) for op in range(5) for red in range(2)])
+
+
+@pytest.mark.parametrize("B,n,m,d", [(1, 300, 260, 257), (2, 129, 136, 1024), (1, 130, 132, 1500),
+                                     (1, 70, 132, 2081)])
+@pytest.mark.parametrize("kind,code", BITS_CASES)
+def test_bits_tile_kernel_equals_popcount_kernel(B, n, m, d, kind, code):
+    x1 = (rand(B, n, d, seed=5) < 0.3).to(DEV)
+    x2 = (rand(B, m, d, seed=6) < 0.3).to(DEV)
+    x2[:, 0] = False  # an all-zero row: the guarded 0 / 0 cases
+    x1[:, 1] = True   # an all-one row
+    tile = _bits_call(x1, x2, kind, code, False)
+    ref = _bits_call(x1, x2, kind, code, True)
+    assert torch.equal(torch.nan_to_num(tile, nan=-7.0).view(torch.int32),
+                       torch.nan_to_num(ref, nan=-7.0).view(torch.int32))
 
 
 # --------------------------------------------------------------------------------------

@@ -30,6 +30,7 @@ _SIGNATURES = {
     "tpw_packed_words": (_i64, [_i64]),
     "tpw_pack_bool_rows": (_i, [_p, _i64, _i64, _p, _p, _p]),
     "tpw_bool_pairwise_reduce": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
+    "tpw_bool_pairwise_reduce_counted": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_jaccard_bool": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
     "tpw_bool_count_metric": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _p, _p]),
     "tpw_bool_row_counts": (_i, [_p, _i64, _i64, _p, _p]),

@@ -757,6 +757,164 @@ __global__ __launch_bounds__(tile::kThreads, 4) void bool_fp4_tile_kernel(
         out, b, row0, col0, n, m);
 }
 
+// The tile kernel of tile_mfma.hpp on bit-packed rows (W uint32 words per row, W % 4 == 0,
+// zero bits past d): a 128-byte chunk of a row is 1024 features, a quarter of the operand
+// bytes the fp4 rows take, and each lane widens the bits it feeds the MFMA into fp4 e2m1
+// nibbles in registers.  Lane (l32 + 32 h) reads logical piece 2 p + h (4 words) of its rows
+// for pair p of the chunk and feeds word t of it to step t: bit 4 i + e of the word becomes
+// nibble i of operand dword e (0x2 = 1.0 or 0), the same permutation of the features on both
+// sides, so every AND count is unchanged.  A partial last chunk (W % 32 != 0) loads an
+// in-row piece into the slots past the row's end and zeroes them in LDS before use.  Counts, popcounts and the epilogue are those of
+// bool_fp4_tile_kernel, so the outputs are the same bit for bit.  Needs d < 2^24, m % 4 == 0,
+// a 16-byte aligned output and rows * W * 4 < 2^32.
+template <int OP, int EPI>
+__global__ __launch_bounds__(tile::kThreads, 4) void bool_bits_tile_kernel(
+    const uint32_t *__restrict__ x1, const uint32_t *__restrict__ x2, const int32_t *__restrict__ popA,
+    const int32_t *__restrict__ popB, int64_t n, int64_t m, int64_t d, int64_t W, double inv_d, float inv_df,
+    float *__restrict__ out, int64_t tiles_n, int64_t tiles_m, int64_t total) {
+    using namespace tile;
+    __shared__ uint4 smem[kBuf];
+    __shared__ __align__(16) uint32_t s_pop[2 * kT];  // row counts, then column counts
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
+    const int64_t row0 = tr * kT, col0 = tc * kT;
+    const int64_t rb = W * 4;
+    const uint8_t *A = reinterpret_cast<const uint8_t *>(x1 + b * n * W);
+    const uint8_t *B = reinterpret_cast<const uint8_t *>(x2 + b * m * W);
+    dma_tile_rows(popA + b * n, popB + b * m, true, wave, lane, row0, col0, n, m, s_pop);
+    uint32_t off[kSlots];
+    dma_offsets(off, wave, lane, row0, col0, n, m, rb);
+    const int nchunks = (int)((W + 31) / 32);
+    const int vp = (int)(W - 32 * (int64_t)(nchunks - 1)) / 4;  // pieces of the last chunk, 1..8
+    // last chunk: slot j of this lane holds logical piece swz(r, s & 7) of its row; past the
+    // row's end it loads the chunk's piece 0 instead (in bounds) and is zeroed after landing
+    uint32_t bad = 0;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int sl = (wave * kSlots + j) * 64 + lane;
+        bad |= (uint32_t)(swz((sl >> 3) & (kT - 1), sl & 7) >= vp) << j;
+    }
+    auto dma = [&](int kc) {
+        const int64_t kb = (int64_t)kc * 128;
+        const bool last = kc == nchunks - 1;
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j) {
+            const int first = (wave * kSlots + j) * 64;  // the wave's 64 slots lie in one panel
+            const int sl = first + lane;
+            const uint32_t o = (last && ((bad >> j) & 1)) ? off[j] - swz((sl >> 3) & (kT - 1), sl & 7) * 16 : off[j];
+            dma16((first >= kPanel ? B : A) + kb, o, lds_addr(smem + first));
+        }
+    };
+    dma(0);
+
+    floatx16 facc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) facc[mi][ni][r] = 0.0f;
+
+    const uint4 *As = smem, *Bs = smem + kPanel;
+    // piece pair p of the chunk in LDS: 4 steps of 64 features
+    auto pair = [&](int p) {
+        uint4 a[2], bv[2];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) a[mi] = piece(As, wr + mi * 32 + l32, 2 * p + h);
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) bv[ni] = piece(Bs, wc + ni * 32 + l32, 2 * p + h);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            int32x8 ax[2], bx[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                const uint32_t x = t == 0 ? a[mi].x : t == 1 ? a[mi].y : t == 2 ? a[mi].z : a[mi].w;
+                ax[mi] = int32x8{(int)((x << 1) & 0x22222222u), (int)(x & 0x22222222u), (int)((x >> 1) & 0x22222222u),
+                                 (int)((x >> 2) & 0x22222222u), 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const uint32_t x = t == 0 ? bv[ni].x : t == 1 ? bv[ni].y : t == 2 ? bv[ni].z : bv[ni].w;
+                bx[ni] = int32x8{(int)((x << 1) & 0x22222222u), (int)(x & 0x22222222u), (int)((x >> 1) & 0x22222222u),
+                                 (int)((x >> 2) & 0x22222222u), 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)  // transposed; formats 4 / 4: fp4 e2m1, E8M0 scales 127 = 1.0
+                    facc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bx[ni], ax[mi], facc[mi][ni], 4,
+                                                                                  4, 0, 127, 0, 127);
+        }
+    };
+    for (int kc = 0; kc < nchunks; ++kc) {
+        if (kc > 0) {
+            barrier_lds();  // every wave is done with chunk kc - 1
+            dma(kc);
+        }
+        barrier_all();  // chunk kc (and, the first time, the counts) has landed
+        if (kc == nchunks - 1 && vp < 8) {
+            // the partial last chunk: zero the slots past the rows' end (they add nothing)
+#pragma unroll
+            for (int j = 0; j < kSlots; ++j)
+                if ((bad >> j) & 1) smem[(wave * kSlots + j) * 64 + lane] = make_uint4(0, 0, 0, 0);
+            barrier_lds();
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) pair(p);
+    }
+    barrier_lds();  // the operand buffer becomes the output stage
+
+    const uint32_t du = (uint32_t)d;
+    const float df = (float)d;
+    uint32_t pav[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) pav[mi] = s_pop[wr + mi * 32 + l32];
+    store_tile<float>(
+        smem,
+        [&](int mi, int ni, int g) {
+            const uint4 pb = *reinterpret_cast<const uint4 *>(&s_pop[kT + wc + ni * 32 + 8 * g + 4 * h]);
+            const uint32_t pbe[4] = {pb.x, pb.y, pb.z, pb.w};
+            floatx4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t c = count_from_and<OP, EPI>((uint32_t)facc[mi][ni][4 * g + e], pav[mi], pbe[e]);
+                o[e] = finish<OP, EPI>(c, pav[mi], pbe[e], du, inv_d, df, inv_df);
+            }
+            return o;
+        },
+        out, b, row0, col0, n, m);
+}
+
+// Whether bool_bits_tile_kernel takes these packed rows (W words per row) and output.
+bool bits_tile_fits(const uint32_t *a, const uint32_t *b, const int32_t *pa, const int32_t *pb, int64_t n,
+                    int64_t m, int64_t d, int64_t W, const float *out) {
+    return pa && pb && d >= 1 && d < (int64_t)kFloatExactLimit && W % 4 == 0 && W * 32 >= d && aligned16(a) &&
+           aligned16(b) && aligned16(out) && m % 4 == 0 && (n > m ? n : m) * W * 4 < ((int64_t)1 << 32);
+}
+
+// Packed rows with their popcounts: the bit tile kernel for rows of more than 256 features
+// where it fits, else the popcount reduce kernel.
+template <int OP, int EPI>
+int launch_counts(const uint32_t *a, const uint32_t *b, const int32_t *pa, const int32_t *pb, int64_t batch,
+                  int64_t n, int64_t m, int64_t d, float *out, hipStream_t s) {
+    const int64_t W = tpw_packed_words(d);
+    if (d > 256 && bits_tile_fits(a, b, pa, pb, n, m, d, W, out)) {
+        const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
+        const int64_t total = tiles_n * tiles_m * batch;
+        const double inv_d = 1.0 / (double)d;
+        const float inv_df = 1.0f / (float)d;
+        hipLaunchKernelGGL((bool_bits_tile_kernel<OP, EPI>), dim3((unsigned)total), dim3(tile::kThreads), 0, s, a, b,
+                           pa, pb, n, m, d, W, inv_d, inv_df, out, tiles_n, tiles_m, total);
+        return check_launch("bool_bits_tile_kernel");
+    }
+    return launch_reduce<OP, EPI>(a, b, pa, pb, batch, n, m, d, out, s);
+}
+
 int64_t fp4_row_bytes(int64_t d) { return (d + 255) / 256 * 128; }
 
 template <int OP, int EPI>
@@ -833,6 +991,36 @@ extern "C" int tpw_bool_pairwise_reduce(const uint32_t *x1w, const uint32_t *x2w
 #undef TPW_CASE
 }
 
+extern "C" int tpw_bool_pairwise_reduce_counted(const uint32_t *x1w, const uint32_t *x2w, const int32_t *pop1,
+                                                const int32_t *pop2, int64_t batch, int64_t n, int64_t m, int64_t d,
+                                                int op, int reduction, float *out, void *stream) {
+    int rc = check_reduce_args(x1w, x2w, batch, n, m, d, out);
+    if (rc != TPW_OK) return rc;
+    TPW_REQUIRE(op >= TPW_BIT_AND && op <= TPW_BIT_NE, "unknown bit op %d", op);
+    TPW_REQUIRE(reduction == TPW_RED_SUM || reduction == TPW_RED_MEAN, "unknown reduction %d",
+                reduction);
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(pop1 && pop2, "null popcount pointer");
+    hipStream_t s = as_stream(stream);
+#define TPW_CASE(OPC, K)                                                                                  \
+    case OPC:                                                                                             \
+        return reduction == TPW_RED_SUM                                                                   \
+                   ? launch_counts<K, kSum>(x1w, x2w, pop1, pop2, batch, n, m, d, out, s)                  \
+                   : launch_counts<K, kMean>(x1w, x2w, pop1, pop2, batch, n, m, d, out, s);
+    switch (op) {
+        TPW_CASE(TPW_BIT_AND, TPW_BIT_AND)
+        TPW_CASE(TPW_BIT_OR, TPW_BIT_OR)
+        TPW_CASE(TPW_BIT_XOR, TPW_BIT_XOR)
+        TPW_CASE(TPW_BIT_EQ, TPW_BIT_EQ)
+        default:
+            // NE counts exactly like XOR on bits
+            return reduction == TPW_RED_SUM
+                       ? launch_counts<TPW_BIT_XOR, kSum>(x1w, x2w, pop1, pop2, batch, n, m, d, out, s)
+                       : launch_counts<TPW_BIT_XOR, kMean>(x1w, x2w, pop1, pop2, batch, n, m, d, out, s);
+    }
+#undef TPW_CASE
+}
+
 extern "C" int tpw_jaccard_bool(const uint32_t *x1w, const uint32_t *x2w, const int32_t *pop1,
                                 const int32_t *pop2, int64_t batch, int64_t n, int64_t m,
                                 int64_t d, float *out, void *stream) {
@@ -840,8 +1028,7 @@ extern "C" int tpw_jaccard_bool(const uint32_t *x1w, const uint32_t *x2w, const 
     if (rc != TPW_OK) return rc;
     if (batch == 0 || n == 0 || m == 0) return TPW_OK;
     TPW_REQUIRE(pop1 && pop2, "null popcount pointer");
-    return launch_reduce<TPW_BIT_AND, kJaccard>(x1w, x2w, pop1, pop2, batch, n, m, d, out,
-                                                as_stream(stream));
+    return launch_counts<TPW_BIT_AND, kJaccard>(x1w, x2w, pop1, pop2, batch, n, m, d, out, as_stream(stream));
 }
 
 extern "C" int tpw_bool_count_metric(const uint32_t *x1w, const uint32_t *x2w, const int32_t *pop1,
@@ -855,7 +1042,7 @@ extern "C" int tpw_bool_count_metric(const uint32_t *x1w, const uint32_t *x2w, c
     hipStream_t s = as_stream(stream);
 #define TPW_MET(CODE)                                                                             \
     case CODE:                                                                                    \
-        return launch_reduce<TPW_BIT_AND, kCountMetric + CODE>(x1w, x2w, pop1, pop2, batch, n, m, d, \
+        return launch_counts<TPW_BIT_AND, kCountMetric + CODE>(x1w, x2w, pop1, pop2, batch, n, m, d, \
                                                                out, s);
     switch (metric) {
         TPW_MET(TPW_BMET_HAMMING)
@@ -867,7 +1054,7 @@ extern "C" int tpw_bool_count_metric(const uint32_t *x1w, const uint32_t *x2w, c
         TPW_MET(TPW_BMET_RUSSELLRAO)
         TPW_MET(TPW_BMET_SOKALMICHENER)
         TPW_MET(TPW_BMET_SOKALSNEATH)
-        default: return launch_reduce<TPW_BIT_AND, kCountMetric + TPW_BMET_YULE>(x1w, x2w, pop1, pop2, batch, n, m, d, out, s);
+        default: return launch_counts<TPW_BIT_AND, kCountMetric + TPW_BMET_YULE>(x1w, x2w, pop1, pop2, batch, n, m, d, out, s);
     }
 #undef TPW_MET
 }

@@ -252,8 +252,9 @@ at::Tensor packed_bool_metric_cuda(const at::Tensor &w1, const at::Tensor &p1, c
                                            t.n, t.m, d, mt.bmet, out.data_ptr<float>(), current_stream()),
                      "_packed_bool_metric");
         else
-            check_rc(tpw_bool_pairwise_reduce(a, b, t.B, t.n, t.m, d, mt.op, mt.red, out.data_ptr<float>(),
-                                              current_stream()),
+            check_rc(tpw_bool_pairwise_reduce_counted(a, b, t.p1.data_ptr<int32_t>(), t.p2.data_ptr<int32_t>(), t.B,
+                                                      t.n, t.m, d, mt.op, mt.red, out.data_ptr<float>(),
+                                                      current_stream()),
                      "_packed_bool_metric");
     }
     return t.unbatched ? out.squeeze(0) : out;

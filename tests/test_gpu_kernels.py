@@ -219,9 +219,10 @@ def test_lp_backward_p1_sign_exact(entry):
 # inner-product backward
 # --------------------------------------------------------------------------------------
 # (2, 96, 160, 36) and (1, 544, 512, 132): fp32 products on the tile kernel with k-major
-# operands (n, m multiples of 32), edge tiles, K of 16 chunks and more
+# operands (n, m multiples of 32), edge tiles, K of 16 chunks and more; (2, 128, 192, 64) and
+# (1, 1088, 1024, 72): the same for bf16 (n, m multiples of 64, d of 8)
 @pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 64, 33, 256), (1, 300, 290, 128), (2, 96, 160, 36),
-                                     (1, 544, 512, 132)])
+                                     (1, 544, 512, 132), (2, 128, 192, 64), (1, 1088, 1024, 72)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_euclidean_backward(B, n, m, d, dtype):
     x1 = randn(B, n, d, seed=0, dtype=dtype)
@@ -239,7 +240,8 @@ def test_euclidean_backward(B, n, m, d, dtype):
                      what=f"euclidean {dtype} {nm}")
 
 
-@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 64, 33, 256), (2, 96, 160, 36), (1, 544, 512, 132)])
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 64, 33, 256), (2, 96, 160, 36), (1, 544, 512, 132),
+                                     (2, 128, 192, 64), (1, 1088, 1024, 72)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("similarity", [False, True])
 def test_cosine_backward(B, n, m, d, dtype, similarity):

@@ -187,3 +187,35 @@ def test_backward_products_tile_fp32(name, kw, B, n, m, d):
         assert_close(tile, want, rtol=1e-4, atol=1e-4 * scale, what=f"{name} grad_x{k + 1} (tile)")
         assert_close(split, want, rtol=1e-4, atol=1e-4 * scale, what=f"{name} grad_x{k + 1} (split-K)")
         assert_close(tile, split.double(), rtol=0, atol=1e-5 * scale, what=f"{name} grad_x{k + 1} tile vs split-K")
+
+
+# bf16: x2 (for grad_x1) and W, x1 (for grad_x2) read k-major through transposing LDS reads,
+# against the path that inputs offset by one element take (W^T and transposed copies of x1, x2
+# written first, and the register-staged kernel for their misaligned X); bar: the bf16 tolerance
+# against float64 autograd, 1e-2 (+ 1e-2 * max), and the two device paths within one bf16 ulp of
+# each other (2^-7 relative, the ulp of values in [1, 2), + 1e-3 * max)
+@pytest.mark.parametrize("B,n,m,d", [(2, 128, 192, 64), (1, 1088, 1024, 72), (1, 256, 128, 264)])
+@pytest.mark.parametrize("name", ["euclidean_distances", "cosine_distances", "polynomial_kernel"])
+def test_backward_products_kmajor_bf16(name, B, n, m, d):
+    import torchpairwise_amd as tp
+    from tests._util import assert_close
+
+    print(f"{name} bf16 B={B} n={n} m={m} d={d}", flush=True)
+    fn = getattr(tp, name)
+    kw = dict(degree=2, gamma=0.05) if name == "polynomial_kernel" else {}
+    x1 = randn(B, n, d, seed=0, dtype=torch.bfloat16)
+    x2 = randn(B, m, d, seed=1, dtype=torch.bfloat16)
+    g = randn(B, n, m, seed=2, dtype=torch.bfloat16)
+    grads = {}
+    for misaligned in (False, True):
+        a, b = _leaf(x1, misaligned), _leaf(x2, misaligned)
+        fn(a, b, **kw).backward(g.to(DEV))
+        grads[misaligned] = (a.grad.float().cpu(), b.grad.float().cpu())
+    ra, rb = x1.double().requires_grad_(), x2.double().requires_grad_()
+    fn(ra, rb, **kw).backward(g.double())
+    for k, want in enumerate((ra.grad, rb.grad)):
+        kmaj, other = grads[False][k], grads[True][k]
+        scale = float(want.abs().max())
+        assert_close(kmaj, want, rtol=1e-2, atol=1e-2 * scale, what=f"{name} grad_x{k + 1} (k-major)")
+        assert_close(kmaj, other.double(), rtol=2.0 ** -7, atol=1e-3 * scale,
+                     what=f"{name} grad_x{k + 1} k-major vs transposed")

@@ -117,6 +117,13 @@ bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b
 int grad_product_f32(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t batch, int64_t M,
                      int64_t N, int64_t K, float sign, const float *coef, const float *X, float *out,
                      hipStream_t s);
+// The same in bf16 (bits), K a multiple of 64, with a coefficient array; k-major bf16 pieces
+// come from transposing LDS reads.
+bool grad_product_bf16_fits(const uint16_t *A, bool a_kmajor, const uint16_t *B, bool b_kmajor, int64_t M,
+                            int64_t N, int64_t K, const uint16_t *X, const uint16_t *out);
+int grad_product_bf16(const uint16_t *A, bool a_kmajor, const uint16_t *B, bool b_kmajor, int64_t batch, int64_t M,
+                      int64_t N, int64_t K, float sign, const float *coef, const uint16_t *X, uint16_t *out,
+                      hipStream_t s);
 
 // Backward of _ppminkowski / _wminkowski (w != nullptr) at p = +-inf (lp_inf_backward.hip):
 // grad_x1, grad_x2 and, weighted, per-row weight-gradient partials wrows [batch, n, d].

@@ -425,8 +425,9 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
 // multiple of 128 bytes, 16-byte aligned rows) and outputs whose rows split into whole 16-byte
 // units: one 32 KiB operand buffer (4 blocks per CU), the chunk loaded by DMA while no wave
 // reads it, transposed products, and the epilogue applied while the tile is staged for
-// row-segment stores.  AK / BK (fp32 only): x1 / x2 stored k-major, [d, n] / [d, m] (the
-// backward's products read W^T, x1 and x2 that way, without a transposed copy).
+// row-segment stores.  AK / BK: x1 / x2 stored k-major, [d, n] / [d, m] (the backward's products
+// read W^T, x1 and x2 that way, without a transposed copy); bf16 k-major pieces come from two
+// transposing LDS reads each.
 template <typename T, typename OutT, int EPI, int NB = 1, bool AK = false, bool BK = false>
 __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
@@ -451,11 +452,12 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
     if constexpr (kAux1<EPI>)
         dma_tile_rows(aux1 + b * n, kAux2<EPI> ? aux2 + b * m : nullptr, kAux2<EPI>, wave, lane, row0, col0, n, m,
                       s_aux);
-    static_assert(!(AK || BK) || sizeof(T) == 4, "k-major operands are fp32");
+    constexpr int ES = (int)sizeof(T);
     uint32_t off[kSlots];
-    dma_offsets_k<AK, BK>(off, wave, lane, row0, col0, n, m, row_bytes, n * 4, m * 4);
-    // bytes from one K chunk to the next: 128 along a row, 32 K rows of a k-major operand
+    dma_offsets_k<AK, BK, ES>(off, wave, lane, row0, col0, n, m, row_bytes, n * ES, m * ES);
+    // bytes from one K chunk to the next: 128 along a row, 128 / ES K rows of a k-major operand
     const int64_t a_step = AK ? 128 * n : 128, b_step = BK ? 128 * m : 128;
+    const int grp = ((lane >> 4) & 1) * 16;  // first row of the lane's 16-lane group (bf16 k-major)
     dma_chunk2(A, B, off, wave, 0, 0, smem);
 
     floatx16 acc[2][2];
@@ -486,10 +488,14 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
             uint4 a[2], bv[2];
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
-                a[mi] = AK ? kpiece(As, wr + mi * 32 + l32, h, q) : piece(As, wr + mi * 32 + l32, c);
+                a[mi] = !AK       ? piece(As, wr + mi * 32 + l32, c)
+                        : ES == 4 ? kpiece(As, wr + mi * 32 + l32, h, q)
+                                  : kpiece_bf16(As, wr + mi * 32 + grp, lane, h, q);
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
-                bv[ni] = BK ? kpiece(Bs, wc + ni * 32 + l32, h, q) : piece(Bs, wc + ni * 32 + l32, c);
+                bv[ni] = !BK      ? piece(Bs, wc + ni * 32 + l32, c)
+                         : ES == 4 ? kpiece(Bs, wc + ni * 32 + l32, h, q)
+                                   : kpiece_bf16(Bs, wc + ni * 32 + grp, lane, h, q);
             mfma_piece_t(acc, a, bv, T{});
             if constexpr (EPI == kEpiGradA) {
                 // after the products that read the same registers (no wait of its own)
@@ -697,43 +703,64 @@ int inner_grad_gemm(const void *A, const void *B, int dtype, int64_t batch, int6
         static_cast<uint16_t *>(out), s, static_cast<const uint16_t *>(X), sign);
 }
 
-bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t M, int64_t N,
-                           int64_t K, const float *X, const float *out) {
-    // whole K chunks; k-contiguous rows of whole chunks below 2^32 bytes per batch; k-major
-    // operands of whole 16-byte pieces; output rows of whole 16-byte units
-    auto fits = [&](const float *p, bool kmajor, int64_t rows) {
+// The gradient products' shapes for the tile kernel: whole K chunks; k-contiguous rows below
+// 2^32 bytes per batch; k-major operands of whole 16-byte pieces; output rows of whole 16-byte
+// units; 16-byte aligned arrays.
+template <typename T>
+bool grad_fits(const T *A, bool a_kmajor, const T *B, bool b_kmajor, int64_t M, int64_t N, int64_t K, const T *X,
+               const T *out) {
+    constexpr int64_t ES = (int64_t)sizeof(T), EPP = 16 / ES;
+    auto fits = [&](const T *p, bool kmajor, int64_t rows) {
         if (!aligned16(p) || rows <= 0) return false;
-        return kmajor ? rows % 4 == 0 && rows * 128 < ((int64_t)1 << 32) : rows * K * 4 < ((int64_t)1 << 32);
+        return kmajor ? rows % EPP == 0 && rows * 128 < ((int64_t)1 << 32) : rows * K * ES < ((int64_t)1 << 32);
     };
-    return K > 0 && K % Elem<float>::kChunk == 0 && N % 4 == 0 && fits(A, a_kmajor, M) && fits(B, b_kmajor, N) &&
+    return K > 0 && K % Elem<T>::kChunk == 0 && N % EPP == 0 && fits(A, a_kmajor, M) && fits(B, b_kmajor, N) &&
            aligned16(X) && aligned16(out);
 }
 
-template <int EPI, bool AK, bool BK>
-int launch_grad_product_f32(const float *A, const float *B, int64_t batch, int64_t M, int64_t N, int64_t K,
-                            float sign, const float *coef, const float *X, float *out, hipStream_t s) {
+template <typename T, int EPI, bool AK, bool BK>
+int launch_grad_product(const T *A, const T *B, int64_t batch, int64_t M, int64_t N, int64_t K, float sign,
+                        const float *coef, const T *X, T *out, hipStream_t s) {
     const int64_t tiles_n = cdiv(M, kTile), tiles_m = cdiv(N, kTile), total = tiles_n * tiles_m * batch;
-    if (K * 4 >= 16 * 128)
-        hipLaunchKernelGGL((inner_tile_kernel<float, float, EPI, 2, AK, BK>), dim3((unsigned)total),
-                           dim3(tile::kThreads), 0, s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total,
-                           KerParams{}, X, sign);
+    if (K * (int64_t)sizeof(T) >= 16 * 128)
+        hipLaunchKernelGGL((inner_tile_kernel<T, T, EPI, 2, AK, BK>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                           s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total, KerParams{}, X, sign);
     else
-        hipLaunchKernelGGL((inner_tile_kernel<float, float, EPI, 1, AK, BK>), dim3((unsigned)total),
-                           dim3(tile::kThreads), 0, s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total,
-                           KerParams{}, X, sign);
+        hipLaunchKernelGGL((inner_tile_kernel<T, T, EPI, 1, AK, BK>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                           s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total, KerParams{}, X, sign);
     return check_launch("inner_tile_kernel");
+}
+
+bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t M, int64_t N,
+                           int64_t K, const float *X, const float *out) {
+    return grad_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out);
 }
 
 int grad_product_f32(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t batch, int64_t M,
                      int64_t N, int64_t K, float sign, const float *coef, const float *X, float *out,
                      hipStream_t s) {
-    TPW_REQUIRE(grad_product_f32_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out), "unsupported product shape");
+    TPW_REQUIRE(grad_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out), "unsupported product shape");
     TPW_REQUIRE(b_kmajor, "k-contiguous B: inner_grad_gemm");
     if (coef == nullptr)
-        return a_kmajor ? launch_grad_product_f32<kEpiGradA, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
-                        : launch_grad_product_f32<kEpiGradA, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
-    return a_kmajor ? launch_grad_product_f32<kEpiGrad, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
-                    : launch_grad_product_f32<kEpiGrad, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
+        return a_kmajor ? launch_grad_product<float, kEpiGradA, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
+                        : launch_grad_product<float, kEpiGradA, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
+    return a_kmajor ? launch_grad_product<float, kEpiGrad, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
+                    : launch_grad_product<float, kEpiGrad, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
+}
+
+bool grad_product_bf16_fits(const uint16_t *A, bool a_kmajor, const uint16_t *B, bool b_kmajor, int64_t M,
+                            int64_t N, int64_t K, const uint16_t *X, const uint16_t *out) {
+    return grad_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out);
+}
+
+int grad_product_bf16(const uint16_t *A, bool a_kmajor, const uint16_t *B, bool b_kmajor, int64_t batch, int64_t M,
+                      int64_t N, int64_t K, float sign, const float *coef, const uint16_t *X, uint16_t *out,
+                      hipStream_t s) {
+    TPW_REQUIRE(grad_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out), "unsupported product shape");
+    TPW_REQUIRE(b_kmajor && coef, "k-major B and a coefficient array");
+    return a_kmajor
+               ? launch_grad_product<uint16_t, kEpiGrad, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
+               : launch_grad_product<uint16_t, kEpiGrad, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
 }
 
 }  // namespace tpw

@@ -29,10 +29,11 @@
 //         modes whose row terms are the weights (or zero), passes 1-2 and the grad_x1
 //         product are one kernel (fused_grad1_kernel) and grad_x2 sums W's columns from its
 //         own operand.
-//   bf16: W rounded to bf16 (the precision of the reference's bf16 autograd) and written
-//         both [n, m] and transposed; x1, x2 transposed to [d, rows]; both products are then
-//         A . B^T with k-contiguous rows, i.e. the forward MFMA kernel (v_mfma_f32_32x32x16_bf16)
-//         with a gradient epilogue (inner_grad_gemm).
+//   bf16: W rounded to bf16 (the precision of the reference's bf16 autograd); both products on
+//         the tile kernel (v_mfma_f32_32x32x16_bf16), which reads x2 (for grad_x1) and W, x1 (for
+//         grad_x2) k-major through transposing LDS reads (grad_product_bf16); other shapes
+//         write W^T and transposed x1, x2 so that both products are A . B^T with k-contiguous
+//         rows (inner_grad_gemm).
 #include "common.hpp"
 #include "tile_mfma.hpp"
 
@@ -904,6 +905,12 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     }
     const int64_t ti = cdiv(n, kPWRows);
     int64_t tj = cdiv(m, kPWCols);
+    // bf16: the tile kernel reads x2 (for gx1) and W, x1 (for gx2) k-major in place where the
+    // shapes allow (no W^T, no transposed inputs)
+    bool bf16_kmajor = false;
+    if constexpr (kBf16)
+        bf16_kmajor = grad_product_bf16_fits(W, false, x2, true, n, d, m, x1, gx1) &&
+                      grad_product_bf16_fits(W, true, x1, true, m, d, n, x2, gx2);
     bool vec_pass = false;
     if constexpr (!kBf16) {
         const void *av = (MODE == kEuclid || MODE == kSigmoid) ? static_cast<const void *>(res) : w.S;
@@ -918,7 +925,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     } else {
         hipLaunchKernelGGL((pair_weights_kernel<T, MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
                            dim3(256), 0, s, g, res, n1, n2, n, m, w.S, w.rowpart, w.colpart, ti, tj, W,
-                           kBf16 ? WT : nullptr, kp);
+                           kBf16 && !bf16_kmajor ? WT : nullptr, kp);
         rc = check_launch("pair_weights_kernel");
     }
     if (rc) return rc;
@@ -934,6 +941,11 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     // kernel functions: W carries the whole gradient (rowpart / colpart, hence coef, are 0)
     const float sign = (cosine || MODE == kPoly || MODE == kSigmoid || MODE == kDot) ? 1.0f : -1.0f;
     if constexpr (kBf16) {
+        if (bf16_kmajor) {
+            rc = grad_product_bf16(W, false, x2, true, batch, n, d, m, sign, w.coef1, x1, gx1, s);
+            if (rc) return rc;
+            return grad_product_bf16(W, true, x1, true, batch, m, d, n, sign, w.coef2, x2, gx2, s);
+        }
         // both products as A . B^T with k-contiguous operands on the bf16 matrix cores:
         // gx1 = sign * W . (x2^T)^T + coef1 * x1, gx2 = sign * W^T . (x1^T)^T + coef2 * x2
         hipLaunchKernelGGL((transpose_kernel<T>), dim3((unsigned)cdiv(d, 64), (unsigned)cdiv(n, 64), (unsigned)batch),

@@ -93,21 +93,28 @@ __device__ __forceinline__ void dma_chunk(const uint8_t *A, const uint8_t *B, co
     }
 }
 
-// k-major fp32 operands (stored [K, rows], `stride` bytes per K row): a chunk is 32 K rows x
-// the tile's 128 rows, each K row 512 contiguous bytes = 32 pieces.  Panel slot s holds K row
-// s >> 5 at position s & 31: logical piece s & 31 for K rows 0..15 and (s & 31) ^ 8 for K rows
-// 16..31 (columns xor 32), so the two half-waves' 4-byte reads below fall on different banks.
-// Pieces past the operand's `lim` rows (a multiple of 4) read its last piece.
+// k-major operands (stored [K, rows], `stride` bytes per K row): a chunk's panel is 1024
+// pieces, 32 fp32 K rows of 512 bytes (the tile's 128 rows, 32 pieces) or 64 bf16 K rows of
+// 256 bytes (16 pieces), each K row's tile segment contiguous in memory.  Panel slot s holds K
+// row s / PK at position s % PK (PK pieces per K row) of logical piece
+//   fp32: (s % 32) ^ 8 for K rows 16..31 (columns xor 32: the two half-waves' 4-byte reads
+//         below fall on different banks),
+//   bf16: (s % 16) ^ 4 (kr & 3) (the four K rows of one transposing read land on disjoint
+//         banks).
+// Pieces past the operand's `lim` rows (a multiple of 16 / ES) read its last piece.
+template <int ES>
 __device__ __forceinline__ uint32_t kmajor_offset(int s, int64_t row0, int64_t lim, int64_t stride) {
-    const int kr = s >> 5, lp = (s & 31) ^ ((kr >> 4) << 3);
-    int64_t r = row0 + 4 * lp;
-    r = r < lim ? r : lim - 4;
-    return (uint32_t)(kr * stride + r * 4);
+    constexpr int PK = 128 * ES / 16, EPP = 16 / ES;  // pieces per K row, elements per piece
+    const int kr = s / PK;
+    const int lp = ES == 4 ? (s % PK) ^ ((kr >> 4) << 3) : (s % PK) ^ (4 * (kr & 3));
+    int64_t r = row0 + EPP * lp;
+    r = r < lim ? r : lim - EPP;
+    return (uint32_t)(kr * stride + r * ES);
 }
 
 // dma_offsets for either panel stored k-major (AK: the A rows, BK: the B rows; `a_stride` /
-// `b_stride` bytes per K row) or k-contiguous (`row_bytes` per row).
-template <bool AK, bool BK>
+// `b_stride` bytes per K row, ES bytes per element) or k-contiguous (`row_bytes` per row).
+template <bool AK, bool BK, int ES = 4>
 __device__ __forceinline__ void dma_offsets_k(uint32_t (&off)[kSlots], int wave, int lane, int64_t row0, int64_t col0,
                                               int64_t n, int64_t m, int64_t row_bytes, int64_t a_stride,
                                               int64_t b_stride) {
@@ -116,8 +123,8 @@ __device__ __forceinline__ void dma_offsets_k(uint32_t (&off)[kSlots], int wave,
         const int s = (wave * kSlots + j) * 64 + lane;
         const int panel = s >> 10;
         if ((panel == 0 && AK) || (panel == 1 && BK)) {
-            off[j] = panel ? kmajor_offset(s & (kPanel - 1), col0, m, b_stride)
-                           : kmajor_offset(s & (kPanel - 1), row0, n, a_stride);
+            off[j] = panel ? kmajor_offset<ES>(s & (kPanel - 1), col0, m, b_stride)
+                           : kmajor_offset<ES>(s & (kPanel - 1), row0, n, a_stride);
         } else {
             const int r = (s >> 3) & (kT - 1), p = s & 7;
             const int64_t lim = panel ? m : n;
@@ -147,6 +154,29 @@ __device__ __forceinline__ uint4 kpiece(const uint4 *panel, int r, int h, int q)
     const float *f = reinterpret_cast<const float *>(panel) + (16 * h + 4 * q) * kT + (r ^ (32 * h));
     return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[kT]), __float_as_uint(f[2 * kT]),
                       __float_as_uint(f[3 * kT]));
+}
+
+// The bf16 values at K = 32 h + 8 q + (0..7) of row rb + (lane % 16) of a k-major panel, as
+// one piece (the same K order as piece(panel, r, 4 h + q) of a k-contiguous bf16 panel); rb is
+// the first of the 16 rows that the lane's group of 16 lanes covers (a multiple of 16).  Two
+// transposing reads (ds_read_b64_tr_b16): within a group of 16 lanes, lane j points at the 4
+// elements of K row K0 + j / 4, rows rb + 4 (j % 4) .. + 3, and lane i receives K rows
+// K0 .. K0 + 3 of row rb + i.
+__device__ __forceinline__ uint4 kpiece_bf16(const uint4 *panel, int rb, int lane, int h, int q) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    const int j = lane & 15;
+    uint2 v[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int kr = 32 * h + 8 * q + 4 * t + (j >> 2);
+        const int byte = 2 * (rb + 4 * (j & 3));  // in the K row's tile segment
+        const int pos = (byte >> 4) ^ (4 * (kr & 3));
+        const uint8_t *addr = reinterpret_cast<const uint8_t *>(panel) + kr * 256 + pos * 16 + (byte & 15);
+        const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s *)(uintptr_t)lds_addr(addr));
+        v[t] = __builtin_bit_cast(uint2, r);
+    }
+    return make_uint4(v[0].x, v[0].y, v[1].x, v[1].y);
 }
 
 // One wave's 32 x (32 NI) fp32 outputs through its own LDS slice `sl` (NI * 4 KiB; no

@@ -190,19 +190,20 @@ def test_backward_products_tile_fp32(name, kw, B, n, m, d):
 
 
 # bf16: x2 (for grad_x1) and W, x1 (for grad_x2) read k-major through transposing LDS reads,
-# against the path that inputs offset by one element take (W^T and transposed copies of x1, x2
+# and (euclidean, sigmoid; n % 128 == 0) the weights formed inside the grad_x1 product, against
+# the path that inputs offset by one element take (W^T and transposed copies of x1, x2
 # written first, and the register-staged kernel for their misaligned X); bar: the bf16 tolerance
 # against float64 autograd, 1e-2 (+ 1e-2 * max), and the two device paths within one bf16 ulp of
 # each other (2^-7 relative, the ulp of values in [1, 2), + 1e-3 * max)
 @pytest.mark.parametrize("B,n,m,d", [(2, 128, 192, 64), (1, 1088, 1024, 72), (1, 256, 128, 264)])
-@pytest.mark.parametrize("name", ["euclidean_distances", "cosine_distances", "polynomial_kernel"])
+@pytest.mark.parametrize("name", ["euclidean_distances", "cosine_distances", "polynomial_kernel", "sigmoid_kernel"])
 def test_backward_products_kmajor_bf16(name, B, n, m, d):
     import torchpairwise_amd as tp
     from tests._util import assert_close
 
     print(f"{name} bf16 B={B} n={n} m={m} d={d}", flush=True)
     fn = getattr(tp, name)
-    kw = dict(degree=2, gamma=0.05) if name == "polynomial_kernel" else {}
+    kw = {"polynomial_kernel": dict(degree=2, gamma=0.05), "sigmoid_kernel": dict(gamma=0.02)}.get(name, {})
     x1 = randn(B, n, d, seed=0, dtype=torch.bfloat16)
     x2 = randn(B, m, d, seed=1, dtype=torch.bfloat16)
     g = randn(B, n, m, seed=2, dtype=torch.bfloat16)

@@ -117,8 +117,8 @@ bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b
 int grad_product_f32(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t batch, int64_t M,
                      int64_t N, int64_t K, float sign, const float *coef, const float *X, float *out,
                      hipStream_t s);
-// The same in bf16 (bits), K a multiple of 64, with a coefficient array; k-major bf16 pieces
-// come from transposing LDS reads.
+// The same in bf16 (bits), K a multiple of 64 (coef == nullptr: the row sums of A's bf16
+// values); k-major bf16 pieces come from transposing LDS reads.
 bool grad_product_bf16_fits(const uint16_t *A, bool a_kmajor, const uint16_t *B, bool b_kmajor, int64_t M,
                             int64_t N, int64_t K, const uint16_t *X, const uint16_t *out);
 int grad_product_bf16(const uint16_t *A, bool a_kmajor, const uint16_t *B, bool b_kmajor, int64_t batch, int64_t M,

@@ -490,22 +490,28 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
             for (int mi = 0; mi < 2; ++mi)
                 a[mi] = !AK       ? piece(As, wr + mi * 32 + l32, c)
                         : ES == 4 ? kpiece(As, wr + mi * 32 + l32, h, q)
-                                  : kpiece_bf16(As, wr + mi * 32 + grp, lane, h, q);
+                                  : kpiece_bf16<256>(As, wr + mi * 32 + grp, lane, h, q);
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
                 bv[ni] = !BK      ? piece(Bs, wc + ni * 32 + l32, c)
                          : ES == 4 ? kpiece(Bs, wc + ni * 32 + l32, h, q)
-                                   : kpiece_bf16(Bs, wc + ni * 32 + grp, lane, h, q);
+                                   : kpiece_bf16<256>(Bs, wc + ni * 32 + grp, lane, h, q);
             mfma_piece_t(acc, a, bv, T{});
             if constexpr (EPI == kEpiGradA) {
-                // after the products that read the same registers (no wait of its own)
-                static_assert(sizeof(T) == 4, "row sums of fp32 operands");
+                // after the products that read the same registers (no wait of its own); the
+                // piece's K values in order (bf16: low half of each word first)
 #pragma unroll
                 for (int mi = 0; mi < 2; ++mi) {
-                    rsum[mi] += __uint_as_float(a[mi].x);
-                    rsum[mi] += __uint_as_float(a[mi].y);
-                    rsum[mi] += __uint_as_float(a[mi].z);
-                    rsum[mi] += __uint_as_float(a[mi].w);
+                    const uint32_t w4[4] = {a[mi].x, a[mi].y, a[mi].z, a[mi].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (ES == 4) {
+                            rsum[mi] += __uint_as_float(w4[e]);
+                        } else {
+                            rsum[mi] += __uint_as_float(w4[e] << 16);
+                            rsum[mi] += __uint_as_float(w4[e] & 0xffff0000u);
+                        }
+                    }
                 }
             }
         }
@@ -757,7 +763,11 @@ int grad_product_bf16(const uint16_t *A, bool a_kmajor, const uint16_t *B, bool 
                       int64_t N, int64_t K, float sign, const float *coef, const uint16_t *X, uint16_t *out,
                       hipStream_t s) {
     TPW_REQUIRE(grad_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out), "unsupported product shape");
-    TPW_REQUIRE(b_kmajor && coef, "k-major B and a coefficient array");
+    TPW_REQUIRE(b_kmajor, "k-contiguous B: inner_grad_gemm");
+    if (coef == nullptr)
+        return a_kmajor
+                   ? launch_grad_product<uint16_t, kEpiGradA, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
+                   : launch_grad_product<uint16_t, kEpiGradA, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);
     return a_kmajor
                ? launch_grad_product<uint16_t, kEpiGrad, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)
                : launch_grad_product<uint16_t, kEpiGrad, false, true>(A, B, batch, M, N, K, sign, coef, X, out, s);

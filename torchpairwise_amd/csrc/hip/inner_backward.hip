@@ -827,6 +827,151 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
             gx1, b, row0 + wr, col0 + half * 128, n, d);
 }
 
+// The same for bf16: 64-column K chunks (128 bytes of a row), grad and res / S as bf16 panels,
+// x2's chunk (64 K rows x 256 columns) k-major, read through transposing LDS reads; each
+// weight is formed in fp32 and rounded to bf16 as the weight pass stores it (weight_terms
+// with BF16W, then round to nearest even), fed to v_mfma_f32_32x32x16_bf16 and written to W;
+// coef1 sums the row terms (the rounded weights for euclidean).  grad_x1 leaves as bf16.
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
+    const uint16_t *__restrict__ g, const uint16_t *__restrict__ av, const uint16_t *__restrict__ x2,
+    const uint16_t *__restrict__ x1, int64_t n, int64_t m, int64_t d, uint16_t *__restrict__ W,
+    uint16_t *__restrict__ gx1, int64_t tiles_n, int64_t tiles_c, int64_t total, KerParams kp, float sign) {
+    using namespace tile;
+    constexpr bool kAv = MODE == kEuclid || MODE == kSigmoid || MODE == kPoly;
+    __shared__ uint4 smem[4 * kPanel];  // grad | res or S | x2 (two panels)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave * 32;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int grp = ((lane >> 4) & 1) * 16;  // first row of the lane's 16-lane group
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_c, total, b, tr, tc);
+    const int64_t row0 = tr * kT, col0 = tc * kFCols;
+    const uint8_t *G = reinterpret_cast<const uint8_t *>(g + b * n * m);
+    const uint8_t *AV = kAv ? reinterpret_cast<const uint8_t *>(av + b * n * m) : G;
+    const uint8_t *X2 = reinterpret_cast<const uint8_t *>(x2 + b * m * d);
+    // 16 DMA slots per lane and chunk, slot j at a wave-uniform stride from a per-lane offset
+    // that depends only on j's parity (two registers): wave 0 the grad panel, wave 1 the res / S
+    // panel (tile row 8 j + lane / 8, position lane % 8; n % 128 == 0, so no row clamps), waves
+    // 2 and 3 the x2 panel (K row 32 (wave - 2) + 2 j + lane / 32 at position lane % 32, logical
+    // piece position ^ 4 (kr & 3))
+    uint32_t off_par[2];
+    int64_t jstride;
+    if (wave < 2) {
+        jstride = 8 * m * 2;
+#pragma unroll
+        for (int par = 0; par < 2; ++par)
+            off_par[par] = (uint32_t)((row0 + (lane >> 3)) * m * 2 + 16 * ((lane & 7) ^ ((lane >> 3) & 7) ^ par));
+    } else {
+        jstride = 2 * d * 2;
+        const int kr0 = 32 * (wave - 2) + (lane >> 5);
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+            const int lp = (lane & 31) ^ (4 * ((kr0 + 2 * par) & 3));
+            int64_t c = col0 + 8 * lp;
+            c = c < d ? c : d - 8;
+            off_par[par] = (uint32_t)(kr0 * d * 2 + c * 2);
+        }
+    }
+    floatx16 acc[8];
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[ni][r] = 0.0f;
+    float rsum = 0.0f;
+    // the lane's W row; rows past n store row n - 1, whose weights they duplicate exactly
+    const int r = wr + l32;
+    const int64_t wrow = row0 + r < n ? row0 + r : n - 1;
+    uint16_t *Wrow = W + (b * n + wrow) * m;
+    const uint4 *Gs = smem, *As = smem + kPanel, *Bs = smem + 2 * kPanel;
+    // the bf16 weights of the lane's piece at step q (K = 32 h + 8 q + e), their row terms
+    // into rsum
+    auto weights = [&](int q) {
+        const int c = h * 4 + q;
+        const uint4 gp = piece(Gs, r, c);
+        const uint4 ap = kAv ? piece(As, r, c) : make_uint4(0, 0, 0, 0);
+        const uint32_t gw[4] = {gp.x, gp.y, gp.z, gp.w}, aw[4] = {ap.x, ap.y, ap.z, ap.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // rt: the rounded weight for euclidean / sqeuclidean (BF16W), 0 for the kernel functions
+            float w0, w1, rt, ct;
+            weight_terms<MODE, true>(__uint_as_float(gw[e] << 16), __uint_as_float(aw[e] << 16), 0.0f, 0.0f, kp,
+                                     w0, rt, ct);
+            rsum += rt;
+            weight_terms<MODE, true>(__uint_as_float(gw[e] & 0xffff0000u), __uint_as_float(aw[e] & 0xffff0000u),
+                                     0.0f, 0.0f, kp, w1, rt, ct);
+            rsum += rt;
+            o[e] = f32x2_to_bf16x2_rne(w0, w1);
+        }
+        return make_uint4(o[0], o[1], o[2], o[3]);
+    };
+    const int nchunks = (int)(m / 64);
+    for (int kc = 0; kc < nchunks; ++kc) {
+        if (kc > 0) barrier_lds();  // every wave is done with chunk kc - 1
+        if (wave != 1 || kAv) {
+            const uint8_t *base = wave == 0 ? G + (int64_t)kc * 128
+                                  : wave == 1 ? AV + (int64_t)kc * 128
+                                              : X2 + (int64_t)kc * 128 * d;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                dma16(base + j * jstride, off_par[j & 1], lds_addr(smem + (wave * 16 + j) * 64));
+        }
+        barrier_all();
+        uint4 an = weights(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 a = an;
+            *reinterpret_cast<uint4 *>(Wrow + (int64_t)kc * 64 + 8 * (h * 4 + q)) = a;
+            if (q < 3) an = weights(q + 1);  // formed while this step's products run
+#pragma unroll
+            for (int ni = 0; ni < 8; ++ni) {
+                const uint4 bv = kpiece_bf16<512>(Bs, ni * 32 + grp, lane, h, q);
+                acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, bv),
+                                                                 __builtin_bit_cast(bf16x8, a), acc[ni], 0, 0, 0);
+            }
+            if (q < 3) {
+                // one product, then eight VALU instructions, over the step
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                }
+            }
+        }
+    }
+    barrier_lds();  // the buffer becomes the output stage
+    const float a1v = rsum + __shfl_xor(rsum, 32, 64);  // both K halves
+    uint4 *sl = smem + wave * 1024;  // 16 KiB per wave
+    store_wave_rows_bf16<8>(
+        sl,
+        [&](int ni, int gq) {
+            const int64_t row = row0 + r, col = col0 + ni * 32 + 8 * gq + 4 * h;
+            floatx4 xv = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (row < n && col < d) {
+                const uint2 qv = *reinterpret_cast<const uint2 *>(x1 + (b * n + row) * d + col);
+                xv = floatx4{__uint_as_float(qv.x << 16), __uint_as_float(qv.x & 0xffff0000u),
+                             __uint_as_float(qv.y << 16), __uint_as_float(qv.y & 0xffff0000u)};
+            }
+            floatx4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = sign * acc[ni][4 * gq + e] + a1v * xv[e];
+            return o;
+        },
+        gx1, b, row0 + wr, col0, n, d);
+}
+
+// The bf16 fused path's shapes: whole 128-row tiles (n % 128 == 0), whole 64-element K chunks
+// both ways, d a multiple of 8,
+// 16-byte aligned arrays, per-batch byte offsets of grad below 2^32.
+bool fused_bf16_fits(const void *g, const void *av, const uint16_t *x1, const uint16_t *x2, const uint16_t *W,
+                     const uint16_t *gx1, const uint16_t *gx2, int64_t n, int64_t m, int64_t d) {
+    return n > 0 && m > 0 && d > 0 && n % 128 == 0 && m % 64 == 0 && d % 8 == 0 && n * m * 2 < ((int64_t)1 << 32) &&
+           aligned16(g) && aligned16(av) && aligned16(W) && aligned16(gx1) && aligned16(x1) && aligned16(x2) &&
+           grad_product_bf16_fits(W, true, x1, true, m, d, n, x2, gx2);
+}
+
 // The fused path's shapes: whole K chunks both ways (m and n multiples of 32), d a multiple of
 // 4, 16-byte aligned arrays, per-batch byte offsets of grad below 2^32.
 bool fused_fits(const void *g, const void *av, const float *x1, const float *x2, const void *W, const void *gx1,
@@ -901,6 +1046,30 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
             rc = check_launch("zero_words_kernel");
             if (rc) return rc;
             return grad_product_f32(Wf, true, x1f, true, batch, m, d, n, sign, w.coef2, x2f, g2, s);
+        }
+    }
+    if constexpr (kBf16 && (MODE == kEuclid || MODE == kSqEuclid || MODE == kSigmoid || MODE == kPoly)) {
+        // bf16: the same fusion; S (polynomial) stays the fp32 recompute
+        if constexpr (MODE != kPoly) {
+            const uint16_t *gb = reinterpret_cast<const uint16_t *>(g), *rb = reinterpret_cast<const uint16_t *>(res);
+            const uint16_t *x1b = reinterpret_cast<const uint16_t *>(x1), *x2b = reinterpret_cast<const uint16_t *>(x2);
+            uint16_t *Wb = reinterpret_cast<uint16_t *>(W);
+            uint16_t *g1 = reinterpret_cast<uint16_t *>(gx1), *g2 = reinterpret_cast<uint16_t *>(gx2);
+            if (fused_bf16_fits(gb, MODE == kSqEuclid ? gb : rb, x1b, x2b, Wb, g1, g2, n, m, d)) {
+                const float sign = MODE == kSigmoid ? 1.0f : -1.0f;
+                const int64_t tiles_n = cdiv(n, tile::kT), tiles_c = cdiv(d, kFCols), total = tiles_n * tiles_c * batch;
+                hipLaunchKernelGGL((fused_grad1_bf16_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, s, gb, rb,
+                                   x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, sign);
+                rc = check_launch("fused_grad1_bf16_kernel");
+                if (rc) return rc;
+                if constexpr (MODE == kEuclid || MODE == kSqEuclid)
+                    return grad_product_bf16(Wb, true, x1b, true, batch, m, d, n, sign, nullptr, x2b, g2, s);
+                hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(2 * batch * m, 256)), dim3(256), 0, s,
+                                   reinterpret_cast<uint16_t *>(w.coef2), 2 * batch * m);
+                rc = check_launch("zero_words_kernel");
+                if (rc) return rc;
+                return grad_product_bf16(Wb, true, x1b, true, batch, m, d, n, sign, w.coef2, x2b, g2, s);
+            }
         }
     }
     const int64_t ti = cdiv(n, kPWRows);

@@ -161,7 +161,9 @@ __device__ __forceinline__ uint4 kpiece(const uint4 *panel, int r, int h, int q)
 // the first of the 16 rows that the lane's group of 16 lanes covers (a multiple of 16).  Two
 // transposing reads (ds_read_b64_tr_b16): within a group of 16 lanes, lane j points at the 4
 // elements of K row K0 + j / 4, rows rb + 4 (j % 4) .. + 3, and lane i receives K rows
-// K0 .. K0 + 3 of row rb + i.
+// K0 .. K0 + 3 of row rb + i.  KRB: bytes per K row in the panel (256: 128 tile rows; 512:
+// 256), piece positions xor 4 (kr & 3).
+template <int KRB = 256>
 __device__ __forceinline__ uint4 kpiece_bf16(const uint4 *panel, int rb, int lane, int h, int q) {
     typedef short v4s __attribute__((ext_vector_type(4)));
     const int j = lane & 15;
@@ -171,7 +173,7 @@ __device__ __forceinline__ uint4 kpiece_bf16(const uint4 *panel, int rb, int lan
         const int kr = 32 * h + 8 * q + 4 * t + (j >> 2);
         const int byte = 2 * (rb + 4 * (j & 3));  // in the K row's tile segment
         const int pos = (byte >> 4) ^ (4 * (kr & 3));
-        const uint8_t *addr = reinterpret_cast<const uint8_t *>(panel) + kr * 256 + pos * 16 + (byte & 15);
+        const uint8_t *addr = reinterpret_cast<const uint8_t *>(panel) + kr * KRB + pos * 16 + (byte & 15);
         const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) v4s *)(uintptr_t)lds_addr(addr));
         v[t] = __builtin_bit_cast(uint2, r);
@@ -208,6 +210,40 @@ __device__ __forceinline__ void store_wave_rows_f32(floatx4 *sl, F &&value, floa
         const int64_t grow = grow0 + r;
         if (grow < n && gcol < m)
             __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(out + (b * n + grow) * m + gcol));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is rewritten
+    __builtin_amdgcn_wave_barrier();
+}
+
+// The same for bf16 outputs (rounded to nearest even): 32 x (32 NI) values through an (NI * 2)
+// KiB slice, (NI * 64)-byte row segments, 4 NI lanes per row; m a multiple of 8.
+template <int NI, class F>
+__device__ __forceinline__ void store_wave_rows_bf16(uint4 *sl, F &&value, uint16_t *__restrict__ out, int64_t b,
+                                                     int64_t grow0, int64_t gcol0, int64_t n, int64_t m) {
+    constexpr int U = NI * 4;    // 16-byte units (8 values) per stage row
+    constexpr int RPI = 64 / U;  // rows per store instruction
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+    const int ul = lane % U, rl = lane / U;
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const floatx4 o = value(ni, g);
+            const int u = ni * 4 + g;  // columns 8 g .. 8 g + 7 of block ni; this lane's half h
+            reinterpret_cast<uint2 *>(sl)[(l32 * U + (u ^ (l32 & 15))) * 2 + h] =
+                make_uint2(f32x2_to_bf16x2_rne(o[0], o[1]), f32x2_to_bf16x2_rne(o[2], o[3]));
+        }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    const int64_t gcol = gcol0 + 8 * ul;
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+        const int r = it * RPI + rl;
+        const u32x4 v = reinterpret_cast<const u32x4 *>(sl)[r * U + (ul ^ (r & 15))];
+        const int64_t grow = grow0 + r;
+        if (grow < n && gcol < m)
+            __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (b * n + grow) * m + gcol));
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is rewritten
     __builtin_amdgcn_wave_barrier();

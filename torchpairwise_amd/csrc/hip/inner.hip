@@ -52,12 +52,12 @@ struct Elem<uint16_t> {  // bf16 bits
 // Gradient products of the backward (not a public epilogue code): out = sign * s +
 // aux1[row] * X[row, col], X having the output's type and shape.
 constexpr int kEpiGrad = 100;
-// The same with coef[row] = the sum over K of A's row (tile kernel only).
-constexpr int kEpiGradA = 101;
 // The kernel functions of tpw_pairwise_kernel: (s gamma + coef0)^degree and
 // tanh(s gamma + coef0).
 constexpr int kEpiPoly = 101;
 constexpr int kEpiSigmoid = 102;
+// kEpiGrad with coef[row] = the sum over K of A's row (tile kernel only).
+constexpr int kEpiGradA = 103;
 
 // Row / column norms read by the epilogue (aux1 also carries the gradient coefficients).
 template <int EPI>
@@ -168,35 +168,6 @@ __device__ __forceinline__ void mfma_piece(floatx16 (&acc)[2][2], const uint4 (&
             acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                 __builtin_bit_cast(bf16x8, a[mi]), __builtin_bit_cast(bf16x8, b[ni]), acc[mi][ni],
                 0, 0, 0);
-        }
-    }
-}
-
-// The same piece with the operands swapped (tile_mfma.hpp's transposed products): the
-// accumulators then hold four consecutive output columns per register quad.
-__device__ __forceinline__ void mfma_piece_t(floatx16 (&acc)[2][2], const uint4 (&a)[2], const uint4 (&b)[2], float) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
-                const uint32_t av = e == 0 ? a[mi].x : e == 1 ? a[mi].y : e == 2 ? a[mi].z : a[mi].w;
-                const uint32_t bv = e == 0 ? b[ni].x : e == 1 ? b[ni].y : e == 2 ? b[ni].z : b[ni].w;
-                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(bv), __uint_as_float(av),
-                                                                  acc[mi][ni], 0, 0, 0);
-            }
-        }
-    }
-}
-__device__ __forceinline__ void mfma_piece_t(floatx16 (&acc)[2][2], const uint4 (&a)[2], const uint4 (&b)[2],
-                                             uint16_t) {
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8, b[ni]), __builtin_bit_cast(bf16x8, a[mi]), acc[mi][ni], 0, 0, 0);
         }
     }
 }

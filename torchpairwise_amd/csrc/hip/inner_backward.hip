@@ -647,8 +647,11 @@ BwdWs carve(void *ws, int64_t batch, int64_t n, int64_t m, int64_t d, size_t *to
         return r;
     };
     w.S = reinterpret_cast<float *>(take(sizeof(float) * batch * n * m));
-    w.rowpart = reinterpret_cast<float *>(take(sizeof(float) * batch * cdiv(m, kPWCols) * n));
-    w.colpart = reinterpret_cast<float *>(take(sizeof(float) * batch * cdiv(n, kPWRows) * m));
+    // partials: the weight pass's tiles (256 columns, 128 rows) or the cosine tile kernel's
+    // halves of 128 x 128 tiles, whichever are more
+    const int64_t tjp = cdiv(m, kPWCols) > 2 * cdiv(m, 128) ? cdiv(m, kPWCols) : 2 * cdiv(m, 128);
+    w.rowpart = reinterpret_cast<float *>(take(sizeof(float) * batch * tjp * n));
+    w.colpart = reinterpret_cast<float *>(take(sizeof(float) * batch * 2 * cdiv(n, 128) * m));
     w.coef1 = reinterpret_cast<float *>(take(sizeof(float) * batch * n));
     w.coef2 = reinterpret_cast<float *>(take(sizeof(float) * batch * m));
     w.W = take(sizeof(float) * batch * n * m);
@@ -972,6 +975,148 @@ bool fused_bf16_fits(const void *g, const void *av, const uint16_t *x1, const ui
            grad_product_bf16_fits(W, true, x1, true, m, d, n, x2, gx2);
 }
 
+// Cosine backward, S and the weight pass in one kernel: S = x1 . x2^T of a 128 x 128 tile on the
+// matrix cores (the tile kernel's K loop), then per element the weight pass's weight_terms from
+// S, grad and the row / column norms.  W leaves through the tile stage (type T; bf16 rounded as
+// the pass stores it); the row terms of each wave's 64 columns go to rowpart (two partials per
+// 128-column tile), the column terms of each wave's 64 rows to colpart (two per 128-row tile):
+// a lane sums its two rows, then lane c sums column c over the 32 lanes through the wave's own
+// LDS slice.  S never leaves the chip.  Two operand buffers (the next chunk's DMA in flight
+// while the current one is multiplied) at two blocks per CU: the epilogue's divides need more
+// than the 128 registers of four blocks.  Needs the tile kernel's direct-load shapes,
+// m % (16 / sizeof(T)) == 0 and 16-byte aligned grad and W.
+template <typename T, int MODE>
+__global__ __launch_bounds__(tile::kThreads, 2) void cos_weights_tile_kernel(
+    const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d, const float *__restrict__ n1,
+    const float *__restrict__ n2, const T *__restrict__ g, T *__restrict__ Wo, float *__restrict__ rowpart,
+    float *__restrict__ colpart, int64_t tiles_n, int64_t tiles_m, int64_t total) {
+    using namespace tile;
+    constexpr bool BF16W = sizeof(T) == 2;
+    __shared__ uint4 smem[2 * kBuf];
+    __shared__ __align__(16) float s_aux[2 * kT];  // row norms, then column norms
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int l32 = lane & 31, h = lane >> 5;
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_m, total, b, tr, tc);
+    const int64_t row0 = tr * kT, col0 = tc * kT;
+    const int64_t row_bytes = d * (int64_t)sizeof(T);
+    const uint8_t *A = reinterpret_cast<const uint8_t *>(x1 + b * n * d);
+    const uint8_t *B = reinterpret_cast<const uint8_t *>(x2 + b * m * d);
+    dma_tile_rows(n1 + b * n, n2 + b * m, true, wave, lane, row0, col0, n, m, s_aux);
+    uint32_t off[kSlots];
+    dma_offsets(off, wave, lane, row0, col0, n, m, row_bytes);
+    dma_chunk(A, B, off, wave, 0, smem);
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+    const int nchunks = (int)(row_bytes / 128);
+    for (int kc = 0; kc < nchunks; ++kc) {
+        barrier_all();  // chunk kc (and, the first time, the norms) has landed
+        // chunk kc + 1 goes to the buffer chunk kc - 1 used, which every wave is done with
+        if (kc + 1 < nchunks) dma_chunk(A, B, off, wave, (int64_t)(kc + 1) * 128, smem + ((kc + 1) & 1) * kBuf);
+        const uint4 *As = smem + (kc & 1) * kBuf, *Bs = As + kPanel;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int c = h * 4 + q;
+            uint4 a[2], bv[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) a[mi] = piece(As, wr + mi * 32 + l32, c);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) bv[ni] = piece(Bs, wc + ni * 32 + l32, c);
+            mfma_piece_t(acc, a, bv, T{});
+        }
+    }
+    barrier_lds();  // the operand buffers become the column-sum slices, then the output stage
+
+    // weights in place of S; row terms per lane; column terms per lane over its two rows, one
+    // column block at a time, into the wave's slice as [row l32][unit u ^ (l32 & 15)]
+    float rs[2] = {0.0f, 0.0f};
+    floatx4 *sl = reinterpret_cast<floatx4 *>(smem) + wave * 512;
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+        floatx4 cs[4];
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) cs[gq] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+            const int64_t row = row0 + wr + mi * 32 + l32;
+            const float a1 = s_aux[wr + mi * 32 + l32];
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                const int cl = wc + ni * 32 + 8 * gq + 4 * h;
+                const int64_t col = col0 + cl;
+                const bool ok = row < n && col < m;  // m % 4 == 0: the quad is all in or all out
+                floatx4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (ok) {
+                    const T *gp = g + (b * n + row) * m + col;
+                    if constexpr (BF16W) {
+                        const uint2 qv = *reinterpret_cast<const uint2 *>(gp);
+                        gv = floatx4{__uint_as_float(qv.x << 16), __uint_as_float(qv.x & 0xffff0000u),
+                                     __uint_as_float(qv.y << 16), __uint_as_float(qv.y & 0xffff0000u)};
+                    } else {
+                        gv = *reinterpret_cast<const floatx4 *>(gp);
+                    }
+                }
+                const floatx4 a2 = *reinterpret_cast<const floatx4 *>(&s_aux[kT + cl]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float w = 0.0f, rt = 0.0f, ct = 0.0f;
+                    if (ok) weight_terms<MODE, BF16W>(gv[e], acc[mi][ni][4 * gq + e], a1, a2[e], KerParams{}, w, rt, ct);
+                    acc[mi][ni][4 * gq + e] = w;
+                    rs[mi] += rt;
+                    cs[gq][e] += ct;
+                }
+            }
+        }
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+            const int u = ni * 8 + 2 * gq + h;
+            sl[l32 * 16 + (u ^ (l32 & 15))] = cs[gq];
+        }
+    }
+    // row partials over the wave's 64 columns
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+        const float v = rs[mi] + __shfl_xor(rs[mi], 32, 64);
+        const int64_t row = row0 + wr + mi * 32 + l32;
+        if (h == 0 && row < n) rowpart[(b * 2 * tiles_m + 2 * tc + (wave & 1)) * n + row] = v;
+    }
+    // column partials over the wave's 64 rows: lane c sums column c of the slice
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    {
+        const float *f = reinterpret_cast<const float *>(sl);
+        float v = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 32; ++r) v += f[r * 64 + (((lane >> 2) ^ (r & 15)) << 2) + (lane & 3)];
+        const int64_t col = col0 + wc + lane;
+        if (col < m) colpart[(b * 2 * tiles_n + 2 * tr + (wave >> 1)) * m + col] = v;
+    }
+    barrier_lds();  // every wave's column reads are done before the stage is rewritten
+    store_tile<T>(
+        smem,
+        [&](int mi, int ni, int gq) {
+            return floatx4{acc[mi][ni][4 * gq], acc[mi][ni][4 * gq + 1], acc[mi][ni][4 * gq + 2],
+                           acc[mi][ni][4 * gq + 3]};
+        },
+        Wo, b, row0, col0, n, m);
+}
+
+// cos_weights_tile_kernel's shapes (the tile kernel's direct-load conditions, whole 16-byte
+// units per W row, 16-byte aligned grad and W).
+template <typename T>
+bool cos_fused_fits(const T *x1, const T *x2, const T *g, const T *W, int64_t n, int64_t m, int64_t d) {
+    constexpr int64_t ES = (int64_t)sizeof(T);
+    return n > 0 && m > 0 && d > 0 && (d * ES) % 128 == 0 && aligned16(x1) && aligned16(x2) && aligned16(g) &&
+           aligned16(W) && m % (16 / ES) == 0 && (n > m ? n : m) * d * ES < ((int64_t)1 << 32);
+}
+
 // The fused path's shapes: whole K chunks both ways (m and n multiples of 32), d a multiple of
 // 4, 16-byte aligned arrays, per-batch byte offsets of grad below 2^32.
 bool fused_fits(const void *g, const void *av, const float *x1, const float *x2, const void *W, const void *gx1,
@@ -1007,11 +1152,24 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     T *W = static_cast<T *>(w.W), *WT = static_cast<T *>(w.WT);
     T *x1t = static_cast<T *>(w.x1t), *x2t = static_cast<T *>(w.x2t);
     int rc;
-    if constexpr (MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr || MODE == kPoly) {
-        rc = inner_dot_f32(x1, x2, dtype, batch, n, m, d, w.S, s);
-        if (rc) return rc;
-    }
     constexpr bool kBf16 = sizeof(T) == 2;
+    constexpr bool kCosMode = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+    // bf16: the tile kernel reads x2 (for gx1) and W, x1 (for gx2) k-major in place where the
+    // shapes allow (no W^T, no transposed inputs)
+    bool bf16_kmajor = false;
+    if constexpr (kBf16)
+        bf16_kmajor = grad_product_bf16_fits(W, false, x2, true, n, d, m, x1, gx1) &&
+                      grad_product_bf16_fits(W, true, x1, true, m, d, n, x2, gx2);
+    // cosine: S and the weight pass in one kernel (cos_weights_tile_kernel) where it fits and,
+    // for bf16, the products need no W^T
+    bool cos_fused = false;
+    if constexpr (kCosMode) cos_fused = cos_fused_fits(x1, x2, g, W, n, m, d) && (!kBf16 || bf16_kmajor);
+    if constexpr (kCosMode || MODE == kPoly) {
+        if (!cos_fused) {
+            rc = inner_dot_f32(x1, x2, dtype, batch, n, m, d, w.S, s);
+            if (rc) return rc;
+        }
+    }
     if constexpr (MODE == kDot && !kBf16) {
         // fp32: grad is the weight matrix as stored; no weight pass, zero coefficients
         hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(2 * batch * n, 256)), dim3(256), 0, s,
@@ -1072,21 +1230,24 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
             }
         }
     }
-    const int64_t ti = cdiv(n, kPWRows);
+    int64_t ti = cdiv(n, kPWRows);
     int64_t tj = cdiv(m, kPWCols);
-    // bf16: the tile kernel reads x2 (for gx1) and W, x1 (for gx2) k-major in place where the
-    // shapes allow (no W^T, no transposed inputs)
-    bool bf16_kmajor = false;
-    if constexpr (kBf16)
-        bf16_kmajor = grad_product_bf16_fits(W, false, x2, true, n, d, m, x1, gx1) &&
-                      grad_product_bf16_fits(W, true, x1, true, m, d, n, x2, gx2);
     bool vec_pass = false;
     if constexpr (!kBf16) {
         const void *av = (MODE == kEuclid || MODE == kSigmoid) ? static_cast<const void *>(res) : w.S;
         vec_pass = m % 4 == 0 && aligned16(g) && aligned16(av) && aligned16(W) && aligned16(w.colpart) &&
                    (n2 == nullptr || aligned16(n2));
     }
-    if (vec_pass) {
+    if (cos_fused) {
+        if constexpr (kCosMode) {
+            ti = 2 * cdiv(n, tile::kT);
+            tj = 2 * cdiv(m, tile::kT);
+            const int64_t tiles_n = cdiv(n, tile::kT), tiles_m = cdiv(m, tile::kT), total = tiles_n * tiles_m * batch;
+            hipLaunchKernelGGL((cos_weights_tile_kernel<T, MODE>), dim3((unsigned)total), dim3(tile::kThreads), 0, s,
+                               x1, x2, n, m, d, n1, n2, g, W, w.rowpart, w.colpart, tiles_n, tiles_m, total);
+            rc = check_launch("cos_weights_tile_kernel");
+        }
+    } else if (vec_pass) {
         hipLaunchKernelGGL((pair_weights_vec_kernel<MODE>), dim3((unsigned)tj, (unsigned)ti, (unsigned)batch),
                            dim3(256), 0, s, reinterpret_cast<const float *>(g), reinterpret_cast<const float *>(res),
                            n1, n2, n, m, w.S, w.rowpart, w.colpart, ti, tj, reinterpret_cast<float *>(W), kp);

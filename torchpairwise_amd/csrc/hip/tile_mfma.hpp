@@ -145,6 +145,36 @@ __device__ __forceinline__ void dma_chunk2(const uint8_t *A, const uint8_t *B, c
     }
 }
 
+// One 16-byte K piece of the lane's two A rows and two B rows into the 2 x 2 accumulator
+// blocks, formed transposed (B rows as the MFMA's first operand): the accumulators hold four
+// consecutive output columns per register quad.  fp32: four 32x32x2 steps; bf16: one 32x32x16.
+__device__ __forceinline__ void mfma_piece_t(floatx16 (&acc)[2][2], const uint4 (&a)[2], const uint4 (&b)[2], float) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const uint32_t av = e == 0 ? a[mi].x : e == 1 ? a[mi].y : e == 2 ? a[mi].z : a[mi].w;
+                const uint32_t bv = e == 0 ? b[ni].x : e == 1 ? b[ni].y : e == 2 ? b[ni].z : b[ni].w;
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(bv), __uint_as_float(av),
+                                                                  acc[mi][ni], 0, 0, 0);
+            }
+        }
+    }
+}
+__device__ __forceinline__ void mfma_piece_t(floatx16 (&acc)[2][2], const uint4 (&a)[2], const uint4 (&b)[2],
+                                             uint16_t) {
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, b[ni]), __builtin_bit_cast(bf16x8, a[mi]), acc[mi][ni], 0, 0, 0);
+        }
+    }
+}
+
 // Logical piece c of row r of a panel.
 __device__ __forceinline__ uint4 piece(const uint4 *panel, int r, int c) { return panel[r * 8 + swz(r, c)]; }
 

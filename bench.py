@@ -420,8 +420,11 @@ def run_config(cfg, steps, warmup):
         emit("k_neighbors_mask k=1 (euclidean + selection)", ms, pf, roof("hbm", 9.0 * N * N, ms, conv))
         ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, 16), steps, warmup)
         emit("k_neighbors_mask k=16 (euclidean + selection)", ms, pf, roof("hbm", 9.0 * N * N, ms, conv))
+        # the radius mask comes straight from the tile kernel's epilogue (no distance matrix,
+        # one byte per entry written): bound by the fp32 matrix-core products
         ms, _ = time_op(lambda: tp.radius_neighbors_mask(x1, x2, 14.0), steps, warmup)
-        emit("radius_neighbors_mask eps=14 (euclidean + le)", ms, pf, roof("hbm", 9.0 * N * N, ms, conv))
+        emit("radius_neighbors_mask eps=14 (euclidean + le, one fused launch)", ms, pf,
+             roof("mfma", 2.0 * N * N * D, ms, "2 flop per pair-feature on fp32 MFMA"))
 
         def ref_route():
             inds = dist.argsort(1, False)[:, :2]

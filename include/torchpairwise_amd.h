@@ -568,6 +568,18 @@ int tpw_directed_hausdorff_backward(const float *grad, const float *x1, const fl
 int tpw_row_smallest_mask(const void *dist, int dtype, int64_t rows, int64_t cols,
                           int64_t count, void *mask, void *stream);
 
+/* radius_neighbors_mask with the euclidean metric in one pass: out[b,i,j] (bool bytes) = 1
+ * where the euclidean distance of x1[b,i] and x2[b,j] -- the value tpw_pairwise_inner
+ * (TPW_EPI_EUCLIDEAN) stores for the same inputs, rounded to bf16 for bf16 -- is <= eps,
+ * 0 elsewhere (NaN: 0).  aux1 / aux2: the squared row norms (tpw_row_norms, squared = 1).
+ * eps is the radius as the inputs' dtype holds it (float32, or the bf16 value of the
+ * float).  The distance matrix is never written.  Replaces cdist(x1, x2, metric).le(epsilon)
+ * of radius_neighbors_mask (torchpairwise/csrc/ops/neighbors.cpp:37-60) for the euclidean
+ * metric on its matrix-product path. */
+int tpw_radius_mask_euclidean(const void *x1, const void *x2, int dtype, int64_t batch,
+                              int64_t n, int64_t m, int64_t d, const float *aux1,
+                              const float *aux2, float eps, uint8_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -287,6 +287,26 @@ def test_k_neighbors_mask_gpu_ties_and_self():
         tp.k_neighbors_mask(a, a[:3], 3)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shapes", [((300, 64), (256, 64)), ((2, 256, 128), None), ((300, 64), (200, 64)),
+                                    ((2, 130, 48), (2, 96, 48)), ((40, 8), (20, 8)), ((2, 160, 64), (1, 136, 64)),
+                                    ((300, 64), None), ((20, 16), (12, 16))])
+def test_radius_mask_fused_equals_distances_le(dtype, shapes):
+    """The euclidean radius mask straight from the MFMA epilogue (the tile kernel for output
+    widths of whole 16-byte units, the register-staged kernel's byte stores otherwise, the
+    unfused route at 25 rows or fewer) against the distances the op itself returns, compared
+    with Tensor.le on the same device: bit for bit, eps = a middle distance and 0 (with
+    x2 = None: exactly the zero distances)."""
+    x1 = randn(*shapes[0], seed=0, dtype=dtype).to(DEV)
+    x2 = None if shapes[1] is None else randn(*shapes[1], seed=1, dtype=dtype).to(DEV)
+    dist = tp.euclidean_distances(x1, x2)
+    for eps in (float(dist.float().median()), 0.0):
+        got = tp.radius_neighbors_mask(x1, x2, eps)
+        want = dist.le(eps)
+        assert got.dtype == torch.bool and got.shape == want.shape
+        assert torch.equal(got, want), f"eps={eps}: {int((got != want).sum())} differences"
+
+
 def test_radius_neighbors_mask_gpu():
     x1, x2 = randn(200, 16, seed=0), randn(300, 16, seed=1)
     got = tp.radius_neighbors_mask(x1.to(DEV), x2.to(DEV), 5.0)

@@ -43,6 +43,7 @@ _SIGNATURES = {
     "tpw_compare_reduce": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_row_norms": (_i, [_p, _i, _i64, _i64, _i, _p, _p]),
     "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),
+    "tpw_radius_mask_euclidean": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, C.c_float, _p, _p]),
     "tpw_pairwise_exp_kernel": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, C.c_float, _p, _p]),
     "tpw_pairwise_kernel": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, C.c_float, C.c_float, _i, _p, _p]),
     "tpw_pairwise_kernel_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, C.c_float,

@@ -97,6 +97,7 @@ __device__ __forceinline__ float buffer_load(__amdgpu_buffer_rsrc_t r, uint32_t 
 struct KerParams {
     float gamma = 0.0f, coef0 = 0.0f;
     int degree = 0;
+    float eps = 0.0f;  // the radius of the neighbour-mask epilogue
 };
 
 // S = x1 . x2^T in fp32 on the matrix cores for fp32 or bf16 inputs (inner.hip).

@@ -58,12 +58,17 @@ constexpr int kEpiPoly = 101;
 constexpr int kEpiSigmoid = 102;
 // kEpiGrad with coef[row] = the sum over K of A's row (tile kernel only).
 constexpr int kEpiGradA = 103;
+// radius_neighbors_mask (euclidean): the euclidean epilogue's value, as the distance op stores it
+// (kEpiRadiusB: rounded to bf16), compared with kp.eps: 1 when d <= eps (NaN: 0), as bool bytes.
+constexpr int kEpiRadius = 104;
+constexpr int kEpiRadiusB = 105;
 
 // Row / column norms read by the epilogue (aux1 also carries the gradient coefficients).
 template <int EPI>
 constexpr bool kAux1 = EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN ||
                        EPI == TPW_EPI_COSINE_SIM || EPI == TPW_EPI_COSINE_DIST ||
-                       EPI == TPW_EPI_CORRELATION || EPI == kEpiGrad;
+                       EPI == TPW_EPI_CORRELATION || EPI == kEpiGrad || EPI == kEpiRadius ||
+                       EPI == kEpiRadiusB;
 template <int EPI>
 constexpr bool kAux2 = kAux1<EPI> && EPI != kEpiGrad;
 
@@ -87,6 +92,10 @@ __device__ __forceinline__ float epilogue(float s, float a1, float a2, const Ker
         return EPI == kEpiPoly ? ipow(base, kp.degree) : tanhf(base);
     } else if constexpr (EPI == TPW_EPI_DOT || EPI == kEpiGrad) {
         return s;
+    } else if constexpr (EPI == kEpiRadius || EPI == kEpiRadiusB) {
+        float v = epilogue<TPW_EPI_EUCLIDEAN>(s, a1, a2, kp);
+        if constexpr (EPI == kEpiRadiusB) v = bf16_to_f32(f32_to_bf16_rne(v));
+        return v <= kp.eps ? 1.0f : 0.0f;
     } else if constexpr (EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN) {
         // (a1 + a2) - 2 s with one rounding: 2 s is exact, so the fma is bit-identical
         float v = __builtin_fmaf(-2.0f, s, a1 + a2);
@@ -108,6 +117,7 @@ __device__ __forceinline__ void store_out(float *p, float v) { store_nt(p, v); }
 __device__ __forceinline__ void store_out(uint16_t *p, float v) {
     __builtin_nontemporal_store(f32_to_bf16_rne(v), p);
 }
+__device__ __forceinline__ void store_out(uint8_t *p, float v) { *p = v != 0.0f ? 1 : 0; }
 
 // Loads one 16-byte piece (row r, piece c of chunk kc) of a [rows, d] operand.
 template <typename T, bool VEC>
@@ -297,7 +307,7 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
     for (int ni = 0; ni < 2; ++ni)
         a2v[ni] = kAux2<EPI> ? s_aux[1][wc + ni * 32 + l32] : 0.0f;
     // bf16 rows are written 8 values (16 bytes) per lane: needs m % 8 == 0 for alignment
-    const bool staged = full && (sizeof(OutT) == 4 || m % 8 == 0);
+    const bool staged = full && (sizeof(OutT) == 4 || (sizeof(OutT) == 2 && m % 8 == 0));
     {
         if (staged) {
             // full tile: each wave stages a 32 x 64 half of its tile in fp32 in its own LDS
@@ -779,6 +789,25 @@ extern "C" int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int
     return dispatch_epi<uint16_t>(static_cast<const uint16_t *>(x1),
                                   static_cast<const uint16_t *>(x2), batch, n, m, d, aux1, aux2,
                                   epilogue, static_cast<uint16_t *>(out), s);
+}
+
+extern "C" int tpw_radius_mask_euclidean(const void *x1, const void *x2, int dtype, int64_t batch, int64_t n,
+                                         int64_t m, int64_t d, const float *aux1, const float *aux2, float eps,
+                                         uint8_t *out, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(batch >= 0 && n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && aux1 && aux2 && out, "null pointer");
+    TPW_REQUIRE(cdiv(n, kTile) * cdiv(m, kTile) * batch <= (int64_t)0x7fffffff, "output too large for one launch");
+    hipStream_t s = as_stream(stream);
+    KerParams kp;
+    kp.eps = eps;
+    if (dtype == TPW_F32)
+        return launch_inner<float, kEpiRadius, uint8_t>(static_cast<const float *>(x1), static_cast<const float *>(x2),
+                                                         batch, n, m, d, aux1, aux2, out, s, nullptr, 1.0f, kp);
+    return launch_inner<uint16_t, kEpiRadiusB, uint8_t>(static_cast<const uint16_t *>(x1),
+                                                         static_cast<const uint16_t *>(x2), batch, n, m, d, aux1,
+                                                         aux2, out, s, nullptr, 1.0f, kp);
 }
 
 extern "C" int tpw_pairwise_kernel(const void *x1, const void *x2, int dtype, int64_t batch,

@@ -306,6 +306,7 @@ __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restric
     const int l32 = lane & 31, h = lane >> 5;
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     constexpr int UPR = kT * (int)sizeof(OutT) / 16;  // 16-byte units per stage row
+    constexpr int XM = UPR < 16 ? UPR - 1 : 15;       // unit swizzle mask (stays inside the row)
     constexpr int PR = kBuf * 16 / (kT * (int)sizeof(OutT)) < kT ? kBuf * 16 / (kT * (int)sizeof(OutT)) : kT;
     constexpr int NPASS = kT / PR;
     constexpr int LPR = UPR;     // lanes per row when storing
@@ -326,8 +327,14 @@ __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restric
                         const int col = wc + ni * 32 + 8 * g + 4 * h;
                         if constexpr (sizeof(OutT) == 2) {
                             const int u = col >> 3;
-                            reinterpret_cast<uint2 *>(st)[(r * UPR + (u ^ (r & 15))) * 2 + h] =
+                            reinterpret_cast<uint2 *>(st)[(r * UPR + (u ^ (r & XM))) * 2 + h] =
                                 make_uint2(f32x2_to_bf16x2_rne(o[0], o[1]), f32x2_to_bf16x2_rne(o[2], o[3]));
+                        } else if constexpr (sizeof(OutT) == 1) {
+                            // bool bytes: 1 where the value is not 0
+                            const int u = col >> 4;
+                            const uint32_t q = (uint32_t)(o[0] != 0.0f) | (uint32_t)(o[1] != 0.0f) << 8 |
+                                               (uint32_t)(o[2] != 0.0f) << 16 | (uint32_t)(o[3] != 0.0f) << 24;
+                            reinterpret_cast<uint32_t *>(st)[(r * UPR + (u ^ (r & XM))) * 4 + ((col >> 2) & 3)] = q;
                         } else {
                             const int u = col >> 2;
                             reinterpret_cast<floatx4 *>(st)[r * UPR + (u ^ (r & 15))] = o;
@@ -341,7 +348,7 @@ __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restric
 #pragma unroll
         for (int it = 0; it < ITERS; ++it) {
             const int r = (wave * ITERS + it) * RPI + rl;
-            const u32x4 v = reinterpret_cast<const u32x4 *>(st)[r * UPR + (ul ^ (r & 15))];
+            const u32x4 v = reinterpret_cast<const u32x4 *>(st)[r * UPR + (ul ^ (r & XM))];
             const int64_t grow = row0 + pass * PR + r;
             if (grow < n && gcol < m)
                 __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (b * n + grow) * m + gcol));

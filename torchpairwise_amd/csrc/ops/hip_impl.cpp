@@ -27,6 +27,32 @@ at::Tensor out_shape(const at::Tensor &out3, const at::Tensor &x1) {
 }
 
 // ---------------------------------------------------------------- inner-product (MFMA)
+// radius_neighbors_mask's euclidean route: the mask straight from the MFMA epilogue (x1, x2 of
+// equal batch, fp32 or bf16); epsilon compared as the inputs' dtype holds it, as Tensor.le does.
+at::Tensor radius_mask_euclidean_cuda(const at::Tensor &x1, const at::Tensor &x2, double epsilon) {
+    check_cuda_pair("_radius_mask_euclidean", x1, x2);
+    TORCH_CHECK(x1.scalar_type() == x2.scalar_type(), "_radius_mask_euclidean: x1 and x2 dtypes differ");
+    const int dt = float_dtype("_radius_mask_euclidean", x1);
+    DeviceGuard guard(x1.device());
+    auto a = as3(x1), b = as3(x2);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options().dtype(at::kBool));
+    void *s = current_stream();
+    auto n1 = at::empty({B, n}, a.options().dtype(at::kFloat));
+    check_rc(tpw_row_norms(a.data_ptr(), dt, B * n, d, 1, n1.data_ptr<float>(), s), "row norms");
+    at::Tensor n2 = n1;
+    if (!x2.is_same(x1)) {
+        n2 = at::empty({B, m}, a.options().dtype(at::kFloat));
+        check_rc(tpw_row_norms(b.data_ptr(), dt, B * m, d, 1, n2.data_ptr<float>(), s), "row norms");
+    }
+    const float eps = x1.scalar_type() == at::kBFloat16 ? static_cast<float>(c10::BFloat16(static_cast<float>(epsilon)))
+                                                         : static_cast<float>(epsilon);
+    check_rc(tpw_radius_mask_euclidean(a.data_ptr(), b.data_ptr(), dt, B, n, m, d, n1.data_ptr<float>(),
+                                       n2.data_ptr<float>(), eps, reinterpret_cast<uint8_t *>(out.data_ptr<bool>()), s),
+             "_radius_mask_euclidean");
+    return out_shape(out, x1);
+}
+
 at::Tensor pw_inner_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue) {
     check_cuda_pair("_pw_inner", x1, x2);
     TORCH_CHECK(x1.scalar_type() == x2.scalar_type(), "_pw_inner: x1 and x2 dtypes differ");
@@ -434,6 +460,7 @@ at::Tensor pw_elementwise(const at::Tensor &x1, const at::Tensor &x2, F f) {
 
 TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
     m.impl("_pw_inner", TORCH_FN(pw_inner_cuda));
+    m.impl("_radius_mask_euclidean", TORCH_FN(radius_mask_euclidean_cuda));
     m.impl("_pw_inner_backward", TORCH_FN(pw_inner_backward_cuda));
     m.impl("_pw_kernel", TORCH_FN(pw_kernel_cuda));
     m.impl("_pw_kernel_backward", TORCH_FN(pw_kernel_backward_cuda));

@@ -621,6 +621,18 @@ at::Tensor radius_neighbors_mask(const at::Tensor &x1, const c10::optional<at::T
     auto xs = check_pairwise_inputs("radius_neighbors_mask", x1, x2);
     TORCH_CHECK(epsilon >= 0., "epsilon must be non-negative. Got epsilon=", epsilon)
     at::NoGradGuard no_grad_guard;
+    // the euclidean metric on the GPU's matrix-product path (route_cdist's rule): the mask straight
+    // from the MFMA epilogue, the same distances compared without writing them
+    if (metric == "euclidean" && !w.has_value() && !V.has_value() && !VI.has_value() && !p.has_value() &&
+        !base.has_value() && !shuffle.has_value() && !generator.has_value() && hip_float_path(xs.first, xs.second)) {
+        auto ab = broadcast_batch(xs.first, xs.second);
+        if (ab.first.size(-2) > 25 || ab.second.size(-2) > 25) {
+            static auto op = c10::Dispatcher::singleton()
+                                 .findSchemaOrThrow("torchpairwise::_radius_mask_euclidean", "")
+                                 .typed<at::Tensor(const at::Tensor &, const at::Tensor &, double)>();
+            return op.call(ab.first, ab.second, epsilon);
+        }
+    }
     auto dists = cdist(xs.first, xs.second, metric, w, V, VI, p, base, shuffle, std::move(generator));
     return dists.le(epsilon);
 }
@@ -747,6 +759,7 @@ at::Tensor row_smallest_mask(const at::Tensor &dist, int64_t count) {
 TORCH_LIBRARY_FRAGMENT(torchpairwise, m) {
     // ---- internal ops of this build (HIP kernels; Autograd in autograd.cpp) ----
     m.def("_pw_inner(Tensor x1, Tensor x2, int epilogue) -> Tensor");
+    m.def("_radius_mask_euclidean(Tensor x1, Tensor x2, float epsilon) -> Tensor");
     m.def("_pw_kernel(Tensor x1, Tensor x2, int kind, float gamma, float coef0, int degree) -> Tensor");
     m.def("_pw_kernel_backward(Tensor grad, Tensor x1, Tensor x2, Tensor result, int kind, "
           "float gamma, float coef0, int degree) -> (Tensor, Tensor)");

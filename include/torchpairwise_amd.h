@@ -388,6 +388,32 @@ int tpw_sqjensenshannon_backward(const float *grad, const float *x1, const float
                                  int64_t batch, int64_t n, int64_t m, int64_t d, double divisor,
                                  float *grad_x1, float *grad_x2, void *workspace, void *stream);
 
+/* float64 forms of the six members above (metric = TPW_FAM_*; w [batch, d] for
+ * TPW_FAM_WMINKOWSKI, else ignored; p is the exponent for the Minkowski members, the divisor
+ * for TPW_FAM_JS, unused otherwise).  Same per-pair expressions as the reference's loops, summed
+ * over k in order, in double.  Replace the double dispatch of the reference's CUDA kernels:
+ * _ppminkowski (cuda/ppminkowski_kernel.cu:102), _wminkowski (cuda/wminkowski_kernel.cu:113),
+ * _canberra (cuda/canberra_kernel.cu:74), _braycurtis (cuda/braycurtis_kernel.cu:73),
+ * _additive_chi2_kernel (cuda/additive_chi2_kernel.cu:75), _sqjensenshannon
+ * (cuda/sqjensenshannon_kernel.cu:74). */
+int tpw_family_f64(int metric, const double *x1, const double *x2, const double *w, int64_t batch,
+                   int64_t n, int64_t m, int64_t d, double p, double *out, void *stream);
+
+/* Workspace (bytes) of tpw_family_f64_backward. */
+size_t tpw_family_f64_backward_workspace_size(int metric, int64_t batch, int64_t n, int64_t m,
+                                              int64_t d, double p);
+
+/* Gradients of tpw_family_f64 with the reference's formulas (p = +-inf included: the first
+ * arg-extremum feature per pair), summed over pairs in a fixed order, in double; grad_w
+ * [batch, d] for TPW_FAM_WMINKOWSKI.  Replace the double dispatch of the reference's
+ * __*_backward CUDA kernels (cuda/ppminkowski_kernel.cu:247, cuda/wminkowski_kernel.cu:299,
+ * cuda/canberra_kernel.cu:162, cuda/braycurtis_kernel.cu:191, cuda/additive_chi2_kernel.cu:167,
+ * cuda/sqjensenshannon_kernel.cu:178). */
+int tpw_family_f64_backward(int metric, const double *grad, const double *x1, const double *x2,
+                            const double *w, int64_t batch, int64_t n, int64_t m, int64_t d,
+                            double p, double *grad_x1, double *grad_x2, double *grad_w,
+                            void *workspace, void *stream);
+
 /* Workspace (bytes) of tpw_haversine / tpw_haversine_backward. */
 size_t tpw_haversine_workspace_size(int64_t batch, int64_t n, int64_t m);
 
@@ -416,6 +442,14 @@ int tpw_haversine(const float *x1, const float *x2, int64_t batch, int64_t n, in
 int tpw_haversine_backward(const float *grad, const float *x1, const float *x2, int64_t batch,
                            int64_t n, int64_t m, float *grad_x1, float *grad_x2,
                            void *workspace, void *stream);
+
+/* float64 forms of tpw_haversine / tpw_haversine_backward (no workspace): the reference's
+ * double dispatch of _haversine and __haversine_backward (cuda/haversine_kernel.cu:69,185). */
+int tpw_haversine_f64(const double *x1, const double *x2, int64_t batch, int64_t n, int64_t m,
+                      double *out, void *stream);
+int tpw_haversine_f64_backward(const double *grad, const double *x1, const double *x2,
+                               int64_t batch, int64_t n, int64_t m, double *grad_x1,
+                               double *grad_x2, void *stream);
 
 /* ------------------------------------------------------------------------- */
 /* Backward of the inner-product family                                       */
@@ -552,6 +586,29 @@ int tpw_directed_hausdorff_backward(const float *grad, const float *x1, const fl
                                     const int64_t *idx2, int64_t batch, int64_t b1,
                                     int64_t p1, int64_t b2, int64_t p2, int64_t d,
                                     float *grad_x1, float *grad_x2, void *stream);
+
+/* Directed Hausdorff for dtype TPW_F64 or TPW_F16 (TPW_F32 also accepted: it gives the
+ * pruned pipeline's results bit for bit): the reference's early-exit loop run in its own order,
+ * one wave per cloud pair, with the element type's arithmetic (float16: each difference,
+ * square and sum computed in float and rounded to half, as c10::Half does).  Same arguments
+ * and outputs as tpw_directed_hausdorff, out in the input dtype, no workspace.  Replaces the
+ * double and half dispatch of _directed_hausdorff_forward_kernel (cuda/hausdorff_kernel.cu:
+ * 16-105,150; cpu/hausdorff_kernel.cpp:12-100). */
+int tpw_directed_hausdorff_exact(int dtype, const void *x1, const void *x2, int64_t batch,
+                                 int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                 const int64_t *perm1, const int64_t *perm2, void *out,
+                                 int64_t *idx1, int64_t *idx2, void *stream);
+
+/* Gradients for tpw_directed_hausdorff_exact's dtypes, from its outputs and indices (which
+ * must lie in [0, p1) and [0, p2)): grad_x1 and grad_x2 are overwritten (zero-filled here),
+ * then the same scatter as tpw_directed_hausdorff_backward in the element type's arithmetic.
+ * Replaces the double and half dispatch of _directed_hausdorff_backward_kernel
+ * (cuda/hausdorff_kernel.cu:199-246,283; cpu/hausdorff_kernel.cpp:187-235). */
+int tpw_directed_hausdorff_exact_backward(int dtype, const void *grad, const void *x1,
+                                          const void *x2, const void *out, const int64_t *idx1,
+                                          const int64_t *idx2, int64_t batch, int64_t b1,
+                                          int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                          void *grad_x1, void *grad_x2, void *stream);
 
 /* ------------------------------------------------------------------------- */
 /* Neighbour masks                                                            */

@@ -367,30 +367,9 @@ def test_family_ops_gpu_equal_reference(tmp_path):
                               {k: v for k, v in r.items() if k.startswith("grad")}, 1e-4, what, exact)
 
 
-@pytest.mark.parametrize("name,extra", [
-    ("sqeuclidean_distances", ()), ("canberra_distances", ()), ("braycurtis_distances", ()),
-    ("wminkowski_distances", (3.0, "w")), ("seuclidean_distances", ("w",)), ("rbf_kernel", ()),
-    ("additive_chi2_kernel", ()), ("chi2_kernel", ()), ("jensenshannon_distances", ()),
-    ("haversine_distances", ()), ("snr_distances", ())])
-def test_float64_gpu_refusals_are_pinned(name, extra):
-    """float64 GPU tensors: the fp32 VALU family (and what is built on it) raises
-    NotImplementedError; the reference runs these in double on CUDA."""
-    d = 2 if name == "haversine_distances" else 6
-    x1 = (torch.rand(7, d, dtype=torch.float64) + 0.1).to(DEV)
-    x2 = (torch.rand(5, d, dtype=torch.float64) + 0.1).to(DEV)
-    args = [torch.rand(d, dtype=torch.float64).to(DEV) + 0.2 if e == "w" else e for e in extra]
-    with pytest.raises(NotImplementedError, match="float64"):
-        getattr(tp, name)(x1, x2, *args)
-
-
-def test_other_gpu_dtypes_served_or_refused():
-    """directed_hausdorff on the GPU is float32 only (float64 and float16 raise
-    NotImplementedError); the cdist metrics, cosine, linear and Mahalanobis run float64."""
-    c1 = torch.rand(2, 30, 3, dtype=torch.float64)
-    c2 = torch.rand(2, 20, 3, dtype=torch.float64)
-    for dt in (torch.float64, torch.float16):
-        with pytest.raises(NotImplementedError, match="float32 only"):
-            tp.directed_hausdorff_distances(c1.to(DEV, dt), c2.to(DEV, dt))
+def test_other_gpu_dtypes_served():
+    """The cdist metrics, cosine, linear and Mahalanobis run float64 on the GPU (the VALU family,
+    haversine and directed Hausdorff: test_gpu_float64.py)."""
     x1, x2 = torch.randn(9, 5, dtype=torch.float64), torch.randn(7, 5, dtype=torch.float64)
     VI = torch.eye(5, dtype=torch.float64) * 2
     for name, args in (("euclidean_distances", ()), ("manhattan_distances", ()), ("chebyshev_distances", ()),
@@ -418,8 +397,7 @@ def test_sqeuclidean_identical_points_are_zero():
     x = randn(200, 64, seed=5).to(DEV)
     d = tp.sqeuclidean_distances(x)
     assert bool((torch.diagonal(d) == 0).all())  # direct sum: no |a|^2 + |b|^2 - 2ab residue
-    with pytest.raises(NotImplementedError):
-        tp.canberra_distances(x.double())
+    assert bool((torch.diagonal(tp.sqeuclidean_distances(x.double())) == 0).all())
 
 
 # --------------------------------------------------------------------------------------

@@ -84,6 +84,15 @@ _SIGNATURES = {
     "tpw_haversine_workspace_size": (_sz, [_i64, _i64, _i64]),
     "tpw_haversine": (_i, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "tpw_haversine_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "tpw_family_f64": (_i, [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
+    "tpw_family_f64_backward_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64, _d]),
+    "tpw_family_f64_backward": (_i, [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p, _p, _p, _p]),
+    "tpw_haversine_f64": (_i, [_p, _p, _i64, _i64, _i64, _p, _p]),
+    "tpw_haversine_f64_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p]),
+    "tpw_directed_hausdorff_exact": (_i, [_i, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p,
+                                          _p]),
+    "tpw_directed_hausdorff_exact_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                                   _i64, _p, _p, _p]),
 }
 
 _lib = None
@@ -143,6 +152,8 @@ def _dtype_code(t):
         return TPW_BF16
     if t.dtype == torch.float16:
         return TPW_F16
+    if t.dtype == torch.float64:
+        return TPW_F64
     raise TypeError(f"unsupported dtype {t.dtype}")
 
 
@@ -470,6 +481,72 @@ def directed_hausdorff(x1, x2, perm1=None, perm2=None, noalloc=False):
     if x1.dim() == 3:
         return out[0], i1[0], i2[0]
     return out, i1, i2
+
+
+def directed_hausdorff_exact(x1, x2, perm1=None, perm2=None):
+    """tpw_directed_hausdorff_exact on float64 / float32 / float16 clouds -> (out, idx1, idx2)."""
+    import torch
+
+    a, b = _as4(x1).contiguous(), _as4(x2).contiguous()
+    B, b1, p1, d = a.shape
+    b2, p2 = b.shape[1], b.shape[2]
+    out = torch.empty((B, b1, b2), dtype=a.dtype, device=a.device)
+    i1 = torch.empty((B, b1, b2), dtype=torch.int64, device=a.device)
+    i2 = torch.empty((B, b1, b2), dtype=torch.int64, device=a.device)
+    q1 = _ptr(None if perm1 is None else perm1.contiguous())
+    q2 = _ptr(None if perm2 is None else perm2.contiguous())
+    call("tpw_directed_hausdorff_exact", _dtype_code(a), _ptr(a), _ptr(b), B, b1, p1, b2, p2, d, q1, q2,
+         _ptr(out), _ptr(i1), _ptr(i2), _stream())
+    if x1.dim() == 3:
+        return out[0], i1[0], i2[0]
+    return out, i1, i2
+
+
+def directed_hausdorff_exact_backward(grad, x1, x2, out, idx1, idx2):
+    import torch
+
+    a, b = _as4(x1).contiguous(), _as4(x2).contiguous()
+    g = grad.contiguous().reshape(a.shape[0], a.shape[1], b.shape[1])
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    call("tpw_directed_hausdorff_exact_backward", _dtype_code(a), _ptr(g), _ptr(a), _ptr(b),
+         _ptr(out.contiguous()), _ptr(idx1.contiguous()), _ptr(idx2.contiguous()), a.shape[0], a.shape[1],
+         a.shape[2], b.shape[1], b.shape[2], a.shape[3], _ptr(gx1), _ptr(gx2), _stream())
+    if x1.dim() == 3:
+        return gx1[0], gx2[0]
+    return gx1, gx2
+
+
+def family_f64(metric, x1, x2, w=None, p=2.0):
+    """tpw_family_f64 on float64 [(batch,) n, d] x [(batch,) m, d]."""
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    wc = None if w is None else (w if w.dim() == 2 else w.unsqueeze(0)).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.float64, device=a.device)
+    call("tpw_family_f64", metric, _ptr(a), _ptr(b), _ptr(wc), B, n, m, d, float(p), _ptr(out), _stream())
+    return out[0] if x1.dim() == 2 else out
+
+
+def family_f64_backward(metric, grad, x1, x2, w=None, p=2.0):
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    wc = None if w is None else (w if w.dim() == 2 else w.unsqueeze(0)).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    g = grad.contiguous().reshape(B, n, m)
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    gw = None if wc is None else torch.empty_like(wc)
+    ws = torch.empty((lib().tpw_family_f64_backward_workspace_size(metric, B, n, m, d, float(p)),),
+                     dtype=torch.uint8, device=a.device)
+    call("tpw_family_f64_backward", metric, _ptr(g), _ptr(a), _ptr(b), _ptr(wc), B, n, m, d, float(p),
+         _ptr(gx1), _ptr(gx2), _ptr(gw), _ptr(ws), _stream())
+    r = [gx1, gx2] if x1.dim() == 3 else [gx1[0], gx2[0]]
+    if gw is not None:
+        r.append(gw if w.dim() == 2 else gw[0])
+    return r
 
 
 def directed_hausdorff_backward(grad, x1, x2, out, idx1, idx2):

@@ -1,0 +1,259 @@
+// Directed Hausdorff distance for float64 and float16 (and float32, where it cross-checks the
+// pruned cell-grid pipeline of hausdorff.hip): the reference's loop
+// (cpu/hausdorff_kernel.cpp:12-100, cuda/hausdorff_kernel.cu:16-105) executed in its own order,
+// one wave per cloud pair:
+//
+//   best = 0
+//   for m in (shuffled) order:                       row_min = inf
+//       for n in (shuffled) order:                   s = sum_k (x1[m,k] - x2[n,k])^2
+//           if s < best: break                       (early exit: this m cannot raise best)
+//           if s < row_min: row_min = s, (m_c, n_c) = (m, n)
+//       if row_min >= best and s >= best: best = row_min, (m_best, n_best) = (m_c, n_c)
+//   out = sqrt(best), indices (m_best, n_best)
+//
+// The wave takes the n loop 64 points at a time: each lane forms one point's s, a ballot finds
+// the first lane that breaks, and the strict running minimum over the lanes before it is the
+// chunk's minimum with its first lane, which is what the sequential loop records.  The state
+// (best, row_min, the last s, the candidate indices, which carry over from one m to the next as
+// in the loop) is the same in every lane.  So outputs and indices equal the CPU loop's bit for
+// bit, ties, NaN and overflowing sums included.
+//
+// Arithmetic follows the element type as c10 does: double in double, float in float, and half
+// with every difference, square and sum computed in float and rounded to half (c10::Half's
+// operators).  Contraction is off in this file.
+//
+// The backward follows the CPU loop too (cpu/hausdorff_kernel.cpp:187-235): one thread per
+// (cloud, k) owns that feature column of its cloud's gradient and adds g * diff / out for every
+// cloud pair in order, so there are no atomics and the sums are the loop's.
+#include "common.hpp"
+
+#include <math.h>
+
+#pragma clang fp contract(off)
+
+namespace tpw {
+namespace {
+
+// Element arithmetic of each dtype: load to the accumulation type, and round a result as the
+// element type would hold it.
+template <int DT>
+struct HdT;
+template <>
+struct HdT<TPW_F64> {
+    using S = double;
+    using A = double;
+    static __device__ __forceinline__ A ld(S v) { return v; }
+    static __device__ __forceinline__ A rn(A v) { return v; }
+    static __device__ __forceinline__ S st(A v) { return v; }
+    static __device__ __forceinline__ A root(A v) { return sqrt(v); }
+};
+template <>
+struct HdT<TPW_F32> {
+    using S = float;
+    using A = float;
+    static __device__ __forceinline__ A ld(S v) { return v; }
+    static __device__ __forceinline__ A rn(A v) { return v; }
+    static __device__ __forceinline__ S st(A v) { return v; }
+    static __device__ __forceinline__ A root(A v) { return sqrt_rn(v); }
+};
+template <>
+struct HdT<TPW_F16> {
+    using S = _Float16;
+    using A = float;
+    static __device__ __forceinline__ A ld(S v) { return (float)v; }
+    static __device__ __forceinline__ A rn(A v) { return (float)(_Float16)v; }
+    static __device__ __forceinline__ S st(A v) { return (_Float16)v; }
+    static __device__ __forceinline__ A root(A v) { return sqrt_rn(v); }
+};
+
+template <typename A>
+__device__ __forceinline__ A wave_min(A v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const A o = __shfl_xor(v, off, 64);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void hd_exact_kernel(
+    const typename HdT<DT>::S *__restrict__ x1, const typename HdT<DT>::S *__restrict__ x2, int64_t pairs,
+    int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d, const int64_t *__restrict__ perm1,
+    const int64_t *__restrict__ perm2, typename HdT<DT>::S *__restrict__ out, int64_t *__restrict__ idx1,
+    int64_t *__restrict__ idx2) {
+    using H = HdT<DT>;
+    using A = typename H::A;
+    const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (pair >= pairs) return;  // the whole wave leaves together
+    const int64_t j = pair % b2, i = (pair / b2) % b1, bb = pair / (b1 * b2);
+    const typename H::S *P = x1 + (bb * b1 + i) * p1 * d, *Q = x2 + (bb * b2 + j) * p2 * d;
+    const A inf = (A)INFINITY;
+    A best = 0, s_last = 0;
+    int64_t m_best = 0, n_best = 0, m_c = 0, n_c = 0;
+    for (int64_t mp = 0; mp < p1; ++mp) {
+        const int64_t mi = perm1 ? perm1[bb * p1 + mp] : mp;
+        const typename H::S *u = P + mi * d;
+        A row_min = inf;
+        for (int64_t base = 0; base < p2; base += 64) {
+            const int64_t np = base + lane;
+            const bool act = np < p2;
+            const int64_t ni = act ? (perm2 ? perm2[bb * p2 + np] : np) : 0;
+            const typename H::S *v = Q + ni * d;
+            A s = 0;
+            for (int64_t k = 0; k < d; ++k) {
+                const A diff = H::rn(H::ld(u[k]) - H::ld(v[k]));
+                s = H::rn(s + H::rn(diff * diff));
+            }
+            const uint64_t brk = __ballot(act && s < best);
+            const int nact = p2 - base < 64 ? (int)(p2 - base) : 64;
+            const int limit = brk ? __builtin_ctzll(brk) : nact;
+            // candidates: the lanes the loop reaches whose s improves on the row's minimum; the
+            // chunk's smallest candidate, first lane on ties, is the loop's last strict update
+            const bool cand = lane < limit && s < row_min;
+            const A cmin = wave_min(cand ? s : inf);
+            if (cmin < row_min) {
+                const uint64_t hit = __ballot(cand && s == cmin);
+                const int fl = __builtin_ctzll(hit);
+                row_min = cmin;
+                m_c = mi;
+                n_c = __shfl(ni, fl, 64);
+            }
+            s_last = __shfl(s, brk ? limit : nact - 1, 64);
+            if (brk) break;
+        }
+        if (row_min >= best && s_last >= best) {
+            best = row_min;
+            m_best = m_c;
+            n_best = n_c;
+        }
+    }
+    if (lane == 0) {
+        out[pair] = H::st(H::root(best));
+        idx1[pair] = m_best;
+        idx2[pair] = n_best;
+    }
+}
+
+template <typename S>
+__global__ void hd_zero_kernel(S *__restrict__ p, int64_t len) {
+    const int64_t t = blockIdx.x * (int64_t)256 + threadIdx.x;
+    if (t < len) p[t] = (S)0;
+}
+
+// SIDE 0: thread (bb, i, k) adds g * (x1[m] - x2[n]) / out into grad_x1[bb, i, m, k] for every
+// j in order; SIDE 1: thread (bb, j, k) adds g * (x2[n] - x1[m]) / out into grad_x2 for every i.
+template <int DT, int SIDE>
+__global__ __launch_bounds__(256) void hd_exact_grad_kernel(
+    const typename HdT<DT>::S *__restrict__ g, const typename HdT<DT>::S *__restrict__ x1,
+    const typename HdT<DT>::S *__restrict__ x2, const typename HdT<DT>::S *__restrict__ out,
+    const int64_t *__restrict__ idx1, const int64_t *__restrict__ idx2, int64_t B, int64_t b1, int64_t p1,
+    int64_t b2, int64_t p2, int64_t d, typename HdT<DT>::S *__restrict__ gout) {
+    using H = HdT<DT>;
+    using A = typename H::A;
+    const int64_t clouds = SIDE == 0 ? b1 : b2, others = SIDE == 0 ? b2 : b1;
+    const int64_t t = blockIdx.x * (int64_t)256 + threadIdx.x;
+    if (t >= B * clouds * d) return;
+    const int64_t k = t % d, c = (t / d) % clouds, bb = t / (d * clouds);
+    for (int64_t o = 0; o < others; ++o) {
+        const int64_t pr = SIDE == 0 ? (bb * b1 + c) * b2 + o : (bb * b1 + o) * b2 + c;
+        const int64_t a1 = ((bb * b1 + (SIDE == 0 ? c : o)) * p1 + idx1[pr]) * d + k;
+        const int64_t a2 = ((bb * b2 + (SIDE == 0 ? o : c)) * p2 + idx2[pr]) * d + k;
+        const A diff = SIDE == 0 ? H::rn(H::ld(x1[a1]) - H::ld(x2[a2])) : H::rn(H::ld(x2[a2]) - H::ld(x1[a1]));
+        const A q = H::rn(H::rn(H::ld(g[pr]) * diff) / H::ld(out[pr]));
+        const int64_t at = SIDE == 0 ? a1 : a2;
+        gout[at] = H::st(H::ld(gout[at]) + q);
+    }
+}
+
+inline unsigned nblocks(int64_t len) { return (unsigned)cdiv(len, 256); }
+
+template <int DT>
+int launch_exact(const void *x1, const void *x2, int64_t B, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
+                 int64_t d, const int64_t *perm1, const int64_t *perm2, void *out, int64_t *idx1, int64_t *idx2,
+                 hipStream_t s) {
+    using S = typename HdT<DT>::S;
+    const int64_t pairs = B * b1 * b2;
+    hipLaunchKernelGGL(hd_exact_kernel<DT>, dim3((unsigned)cdiv(pairs, 4)), dim3(256), 0, s,
+                       static_cast<const S *>(x1), static_cast<const S *>(x2), pairs, b1, p1, b2, p2, d, perm1,
+                       perm2, static_cast<S *>(out), idx1, idx2);
+    return check_launch("hd_exact_kernel");
+}
+
+template <int DT>
+int launch_exact_backward(const void *g, const void *x1, const void *x2, const void *out, const int64_t *idx1,
+                          const int64_t *idx2, int64_t B, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
+                          int64_t d, void *gx1, void *gx2, hipStream_t s) {
+    using S = typename HdT<DT>::S;
+    const int64_t n1 = B * b1 * p1 * d, n2 = B * b2 * p2 * d;
+    if (n1 > 0) {
+        hipLaunchKernelGGL(hd_zero_kernel<S>, dim3(nblocks(n1)), dim3(256), 0, s, static_cast<S *>(gx1), n1);
+        const int rc = check_launch("hd_zero_kernel");
+        if (rc != TPW_OK) return rc;
+    }
+    if (n2 > 0) {
+        hipLaunchKernelGGL(hd_zero_kernel<S>, dim3(nblocks(n2)), dim3(256), 0, s, static_cast<S *>(gx2), n2);
+        const int rc = check_launch("hd_zero_kernel");
+        if (rc != TPW_OK) return rc;
+    }
+    if (B * b1 * b2 == 0 || p1 == 0 || p2 == 0 || d == 0) return TPW_OK;
+    const S *G = static_cast<const S *>(g), *X1 = static_cast<const S *>(x1), *X2 = static_cast<const S *>(x2);
+    const S *O = static_cast<const S *>(out);
+    hipLaunchKernelGGL((hd_exact_grad_kernel<DT, 0>), dim3(nblocks(B * b1 * d)), dim3(256), 0, s, G, X1, X2, O,
+                       idx1, idx2, B, b1, p1, b2, p2, d, static_cast<S *>(gx1));
+    const int rc = check_launch("hd_exact_grad_kernel");
+    if (rc != TPW_OK) return rc;
+    hipLaunchKernelGGL((hd_exact_grad_kernel<DT, 1>), dim3(nblocks(B * b2 * d)), dim3(256), 0, s, G, X1, X2, O,
+                       idx1, idx2, B, b1, p1, b2, p2, d, static_cast<S *>(gx2));
+    return check_launch("hd_exact_grad_kernel");
+}
+
+}  // namespace
+}  // namespace tpw
+
+using namespace tpw;
+
+extern "C" int tpw_directed_hausdorff_exact(int dtype, const void *x1, const void *x2, int64_t batch,
+                                            int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                            const int64_t *perm1, const int64_t *perm2, void *out,
+                                            int64_t *idx1, int64_t *idx2, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F64 || dtype == TPW_F32 || dtype == TPW_F16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(batch >= 0 && b1 >= 0 && p1 >= 0 && b2 >= 0 && p2 >= 0 && d >= 0, "invalid sizes");
+    const int64_t pairs = batch * b1 * b2;
+    if (pairs == 0) return TPW_OK;
+    TPW_REQUIRE(cdiv(pairs, 4) <= 0x7fffffffLL, "too many cloud pairs");
+    TPW_REQUIRE(x1 && x2 && out && idx1 && idx2, "null pointer");
+    hipStream_t s = as_stream(stream);
+    switch (dtype) {
+        case TPW_F64: return launch_exact<TPW_F64>(x1, x2, batch, b1, p1, b2, p2, d, perm1, perm2, out, idx1, idx2, s);
+        case TPW_F32: return launch_exact<TPW_F32>(x1, x2, batch, b1, p1, b2, p2, d, perm1, perm2, out, idx1, idx2, s);
+        default: return launch_exact<TPW_F16>(x1, x2, batch, b1, p1, b2, p2, d, perm1, perm2, out, idx1, idx2, s);
+    }
+}
+
+extern "C" int tpw_directed_hausdorff_exact_backward(int dtype, const void *grad, const void *x1,
+                                                     const void *x2, const void *out, const int64_t *idx1,
+                                                     const int64_t *idx2, int64_t batch, int64_t b1,
+                                                     int64_t p1, int64_t b2, int64_t p2, int64_t d,
+                                                     void *grad_x1, void *grad_x2, void *stream) {
+    TPW_REQUIRE(dtype == TPW_F64 || dtype == TPW_F32 || dtype == TPW_F16, "unsupported dtype %d", dtype);
+    TPW_REQUIRE(batch >= 0 && b1 >= 0 && p1 >= 0 && b2 >= 0 && p2 >= 0 && d >= 0, "invalid sizes");
+    const int64_t n1 = batch * b1 * p1 * d, n2 = batch * b2 * p2 * d;
+    if (n1 == 0 && n2 == 0) return TPW_OK;
+    TPW_REQUIRE((n1 == 0 || grad_x1) && (n2 == 0 || grad_x2), "null pointer");
+    if (batch * b1 * b2 > 0 && p1 > 0 && p2 > 0 && d > 0)
+        TPW_REQUIRE(grad && x1 && x2 && out && idx1 && idx2, "null pointer");
+    hipStream_t s = as_stream(stream);
+    switch (dtype) {
+        case TPW_F64:
+            return launch_exact_backward<TPW_F64>(grad, x1, x2, out, idx1, idx2, batch, b1, p1, b2, p2, d,
+                                                  grad_x1, grad_x2, s);
+        case TPW_F32:
+            return launch_exact_backward<TPW_F32>(grad, x1, x2, out, idx1, idx2, batch, b1, p1, b2, p2, d,
+                                                  grad_x1, grad_x2, s);
+        default:
+            return launch_exact_backward<TPW_F16>(grad, x1, x2, out, idx1, idx2, batch, b1, p1, b2, p2, d,
+                                                  grad_x1, grad_x2, s);
+    }
+}

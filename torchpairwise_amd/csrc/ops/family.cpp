@@ -4,8 +4,7 @@
 // with CPU, GPU and Autograd kernels.
 //
 // GPU: fp32 kernels behind the C ABI (valu_lp.hip); bfloat16 / float16 inputs are computed
-// in fp32 and rounded back.  float64 GPU tensors are not served (the kernels are fp32) and
-// raise.  CPU: loops restating the reference's CPU kernels (one output per iteration,
+// in fp32 and rounded back; float64 runs the fp64 kernels (valu_f64.hip) in double.  CPU: loops restating the reference's CPU kernels (one output per iteration,
 // sequential over k), accumulating in the input type (float / double; float for the 16-bit
 // types).  Autograd: saves (x1, x2[, w]) and calls __*_backward, as the reference's
 // autograd kernels do (autograd/*_kernel.cpp).
@@ -299,13 +298,50 @@ std::vector<at::Tensor> family_backward_cpu(const at::Tensor &grad, const at::Te
 }
 
 // ------------------------------------------------------------------------ GPU
-// fp32 views of the operands (16-bit types computed in fp32), or raise for float64.
+// fp32 views of the operands (16-bit types computed in fp32); float64 takes the fp64 kernels.
 at::Tensor gpu_f32(const at::Tensor &t, const char *from) {
-    TORCH_CHECK_NOT_IMPLEMENTED(t.scalar_type() != at::kDouble, from,
-                                ": float64 GPU tensors are not served by this build's fp32 "
-                                "kernels (use float32, or CPU tensors)");
     TORCH_CHECK(at::isFloatingType(t.scalar_type()), from, ": expected a floating-point tensor");
     return t.to(at::kFloat).contiguous();
+}
+
+constexpr int fam_code(Fam F) {
+    return F == kPP ? TPW_FAM_PPMINKOWSKI : F == kW ? TPW_FAM_WMINKOWSKI : F == kCanb ? TPW_FAM_CANBERRA
+         : F == kChi2 ? TPW_FAM_CHI2 : F == kJS ? TPW_FAM_JS : TPW_FAM_BRAYCURTIS;
+}
+
+// float64: the fp64 kernels (tpw_family_f64*), in double throughout, as the reference's CUDA
+// kernels compute double.
+template <Fam F>
+at::Tensor family_forward_f64(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor *w, double p,
+                              bool ub, const char *from) {
+    auto a = batched(x1, ub), bb = batched(x2, ub);
+    at::Tensor wc = w ? batched(*w, ub) : at::Tensor();
+    const int64_t B = a.size(0), n = a.size(1), m = bb.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options());
+    check_rc(tpw_family_f64(fam_code(F), a.data_ptr<double>(), bb.data_ptr<double>(),
+                            w ? wc.data_ptr<double>() : nullptr, B, n, m, d, p, out.data_ptr<double>(),
+                            current_stream()),
+             from);
+    return unbatch(out, ub);
+}
+
+template <Fam F>
+std::vector<at::Tensor> family_backward_f64(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2,
+                                            const at::Tensor *w, double p, bool ub, const char *from) {
+    auto a = batched(x1, ub), bb = batched(x2, ub), g = batched(grad.to(at::kDouble), ub);
+    at::Tensor wc = w ? batched(*w, ub) : at::Tensor();
+    const int64_t B = a.size(0), n = a.size(1), m = bb.size(1), d = a.size(2);
+    auto gx1 = at::empty_like(a), gx2 = at::empty_like(bb);
+    at::Tensor gw = w ? at::empty_like(wc) : at::Tensor();
+    auto ws = workspace(tpw_family_f64_backward_workspace_size(fam_code(F), B, n, m, d, p), a);
+    check_rc(tpw_family_f64_backward(fam_code(F), g.data_ptr<double>(), a.data_ptr<double>(), bb.data_ptr<double>(),
+                                     w ? wc.data_ptr<double>() : nullptr, B, n, m, d, p, gx1.data_ptr<double>(),
+                                     gx2.data_ptr<double>(), w ? gw.data_ptr<double>() : nullptr, ws.data_ptr(),
+                                     current_stream()),
+             from);
+    std::vector<at::Tensor> r{unbatch(gx1, ub), unbatch(gx2, ub)};
+    if (w) r.push_back(unbatch(gw, ub));
+    return r;
 }
 
 template <Fam F>
@@ -313,6 +349,7 @@ at::Tensor family_forward_cuda(const at::Tensor &x1, const at::Tensor &x2, const
                                double p, const char *from) {
     const bool ub = check_family_shapes(from, x1, x2, w);
     DeviceGuard guard(x1.device());
+    if (x1.scalar_type() == at::kDouble) return family_forward_f64<F>(x1, x2, w, p, ub, from);
     auto a = batched(gpu_f32(x1, from), ub), bb = batched(gpu_f32(x2, from), ub);
     at::Tensor wc = w ? batched(gpu_f32(*w, from), ub) : at::Tensor();
     const int64_t B = a.size(0), n = a.size(1), m = bb.size(1), d = a.size(2);
@@ -337,6 +374,7 @@ std::vector<at::Tensor> family_backward_cuda(const at::Tensor &grad, const at::T
                                              const at::Tensor *out_in, const char *from) {
     const bool ub = x1.dim() == 2;
     DeviceGuard guard(x1.device());
+    if (x1.scalar_type() == at::kDouble) return family_backward_f64<F>(grad, x1, x2, w, p, ub, from);
     auto a = batched(gpu_f32(x1, from), ub), bb = batched(gpu_f32(x2, from), ub);
     auto g = batched(gpu_f32(grad, from), ub);
     at::Tensor wc = w ? batched(gpu_f32(*w, from), ub) : at::Tensor();
@@ -357,9 +395,7 @@ std::vector<at::Tensor> family_backward_cuda(const at::Tensor &grad, const at::T
             check_rc(rc, from);
         }
     }
-    const int metric = F == kPP ? TPW_FAM_PPMINKOWSKI : F == kW ? TPW_FAM_WMINKOWSKI
-                     : F == kCanb ? TPW_FAM_CANBERRA : F == kChi2 ? TPW_FAM_CHI2
-                     : F == kJS ? TPW_FAM_JS : TPW_FAM_BRAYCURTIS;
+    const int metric = fam_code(F);
     auto ws = workspace(tpw_family_backward_workspace_size(metric, B, n, m, d), a);
     const float *G = g.data_ptr<float>(), *A = a.data_ptr<float>(), *Bp = bb.data_ptr<float>();
     void *s = current_stream();
@@ -502,6 +538,9 @@ at::Tensor exp_kernel_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t k
     TORCH_CHECK(kind == TPW_KER_RBF || kind == TPW_KER_LAPLACIAN, from, ": unknown kernel ", kind);
     const bool ub = check_family_shapes(from, x1, x2, nullptr);
     DeviceGuard guard(x1.device());
+    TORCH_CHECK_NOT_IMPLEMENTED(x1.scalar_type() != at::kDouble, from,
+                                ": float64 takes the distance op and ATen's exp (rbf_kernel and "
+                                "laplacian_kernel route it there)");
     auto a = batched(gpu_f32(x1, from), ub), bb = batched(gpu_f32(x2, from), ub);
     const int64_t B = a.size(0), n = a.size(1), m = bb.size(1), d = a.size(2);
     auto out = at::empty({B, n, m}, a.options());

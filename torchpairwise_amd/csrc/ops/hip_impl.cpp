@@ -372,12 +372,21 @@ struct HdRun {
     at::Tensor a, b, out, i1, i2;
 };
 
+// float32 takes the pruned cell-grid pipeline; float64 and float16 the reference's loop in
+// its own order (tpw_directed_hausdorff_exact).  The reference serves the same three types
+// (cuda/hausdorff_kernel.cu:150, AT_DISPATCH_FLOATING_TYPES_AND_HALF) and refuses the others.
+int hd_exact_code(at::ScalarType t, const char *from) {
+    TORCH_CHECK_NOT_IMPLEMENTED(t == at::kDouble || t == at::kHalf, "\"", from,
+                                "\" not implemented for '", c10::toString(t), "'");
+    return t == at::kDouble ? TPW_F64 : TPW_F16;
+}
+
 HdRun hausdorff_run(const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
                     c10::optional<at::Generator> gen) {
     check_hausdorff_shapes(x1, x2);
     TORCH_CHECK(x1.is_cuda() && x2.is_cuda(), "_directed_hausdorff: expected GPU tensors");
-    TORCH_CHECK_NOT_IMPLEMENTED(x1.scalar_type() == at::kFloat,
-                                "_directed_hausdorff: the GPU kernel is float32 only, got ", x1.scalar_type());
+    const bool exact = x1.scalar_type() != at::kFloat;
+    const int code = exact ? hd_exact_code(x1.scalar_type(), "_directed_hausdorff_forward_cuda") : TPW_F32;
     HdRun r;
     r.a = x1.dim() == 3 ? x1.unsqueeze(0).contiguous() : x1.contiguous();
     r.b = x2.dim() == 3 ? x2.unsqueeze(0).contiguous() : x2.contiguous();
@@ -388,6 +397,15 @@ HdRun hausdorff_run(const at::Tensor &x1, const at::Tensor &x2, bool shuffle,
     r.i2 = at::empty({B, b1, b2}, r.a.options().dtype(at::kLong));
     at::Tensor perm1, perm2;
     if (shuffle) std::tie(perm1, perm2) = hausdorff_perms(B, p1, p2, r.a.options(), gen);
+    if (exact) {
+        check_rc(tpw_directed_hausdorff_exact(code, r.a.data_ptr(), r.b.data_ptr(), B, b1, p1, b2, p2, d,
+                                              shuffle ? perm1.data_ptr<int64_t>() : nullptr,
+                                              shuffle ? perm2.data_ptr<int64_t>() : nullptr, r.out.data_ptr(),
+                                              r.i1.data_ptr<int64_t>(), r.i2.data_ptr<int64_t>(),
+                                              current_stream()),
+                 "_directed_hausdorff");
+        return r;
+    }
     auto ws = workspace(tpw_hausdorff_workspace_size(B, b1, p1, b2, p2, d), r.a);
     check_rc(tpw_directed_hausdorff(r.a.data_ptr<float>(), r.b.data_ptr<float>(), B, b1, p1, b2, p2, d,
                                     shuffle ? perm1.data_ptr<int64_t>() : nullptr,
@@ -412,6 +430,18 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_cuda(
     DeviceGuard guard(x1.device());
     // the reference re-runs the forward here (csrc/ops/cpu/hausdorff_kernel.cpp:269-306)
     HdRun r = hausdorff_run(x1, x2, shuffle, gen);
+    if (r.a.scalar_type() != at::kFloat) {
+        auto g = grad.to(r.a.scalar_type()).reshape(r.out.sizes()).contiguous();
+        auto gx1 = at::empty_like(r.a), gx2 = at::empty_like(r.b);
+        check_rc(tpw_directed_hausdorff_exact_backward(
+                     hd_exact_code(r.a.scalar_type(), "_directed_hausdorff_backward_cuda"), g.data_ptr(),
+                     r.a.data_ptr(), r.b.data_ptr(), r.out.data_ptr(), r.i1.data_ptr<int64_t>(),
+                     r.i2.data_ptr<int64_t>(), r.a.size(0), r.a.size(1), r.a.size(2), r.b.size(1), r.b.size(2),
+                     r.a.size(3), gx1.data_ptr(), gx2.data_ptr(), current_stream()),
+                 "__directed_hausdorff_backward");
+        if (x1.dim() == 3) return {gx1.squeeze(0), gx2.squeeze(0)};
+        return {gx1, gx2};
+    }
     auto g = grad.to(at::kFloat).reshape(r.out.sizes()).contiguous();
     auto gx1 = at::zeros_like(r.a), gx2 = at::zeros_like(r.b);
     check_rc(tpw_directed_hausdorff_backward(
@@ -435,6 +465,17 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_indexed_cuda(
     const int64_t B = a.size(0), b1 = a.size(1), b2 = b.size(1);
     auto o = out.reshape({B, b1, b2}).contiguous();
     auto m1 = i1.reshape({B, b1, b2}).contiguous(), m2 = i2.reshape({B, b1, b2}).contiguous();
+    if (a.scalar_type() != at::kFloat) {
+        auto g = grad.to(a.scalar_type()).reshape({B, b1, b2}).contiguous();
+        auto gx1 = at::empty_like(a), gx2 = at::empty_like(b);
+        check_rc(tpw_directed_hausdorff_exact_backward(
+                     hd_exact_code(a.scalar_type(), "_directed_hausdorff_backward_cuda"), g.data_ptr(),
+                     a.data_ptr(), b.data_ptr(), o.data_ptr(), m1.data_ptr<int64_t>(), m2.data_ptr<int64_t>(), B,
+                     b1, a.size(2), b2, b.size(2), a.size(3), gx1.data_ptr(), gx2.data_ptr(), current_stream()),
+                 "__directed_hausdorff_backward");
+        if (x1.dim() == 3) return {gx1.squeeze(0), gx2.squeeze(0)};
+        return {gx1, gx2};
+    }
     auto g = grad.to(at::kFloat).reshape({B, b1, b2}).contiguous();
     auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(b);
     check_rc(tpw_directed_hausdorff_backward(

@@ -1,7 +1,8 @@
 // The reference's remaining custom metric ops: _haversine, _snr and _sqmahalanobis with their
 // __*_backward ops (csrc/ops/{haversine,snr,sqmahalanobis}.cpp), CPU, GPU and Autograd.
 //
-// _haversine runs HIP kernels on the GPU (haversine.hip; fp32, 16-bit types through fp32).
+// _haversine runs HIP kernels on the GPU (haversine.hip: fp32, 16-bit types through fp32;
+// valu_f64.hip: float64).
 // _snr is a composition on the GPU:
 //   _snr(x1, x2)[i, j] = V1[i] / DV[i, j], V1 = sum_k (x1 - mean x1)^2 and
 //     DV = sum_k (d - mean d)^2 with d = x2[j] - x1[i]; since mean d = mean x2[j] - mean x1[i],
@@ -125,16 +126,20 @@ T2 haversine_backward_cpu(const at::Tensor &grad, const at::Tensor &x1, const at
     return {unbatch(gx1, ub), unbatch(gx2, ub)};
 }
 
-at::Tensor gpu_f32(const at::Tensor &t, const char *from) {
-    TORCH_CHECK_NOT_IMPLEMENTED(t.scalar_type() != at::kDouble, from,
-                                ": float64 GPU tensors are not served by this build's fp32 "
-                                "kernels (use float32, or CPU tensors)");
-    return t.to(at::kFloat).contiguous();
-}
+// fp32 operands (16-bit types computed in fp32); float64 takes the fp64 kernels.
+at::Tensor gpu_f32(const at::Tensor &t, const char *) { return t.to(at::kFloat).contiguous(); }
 
 at::Tensor haversine_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     const bool ub = check_haversine(x1, x2);
     DeviceGuard guard(x1.device());
+    if (x1.scalar_type() == at::kDouble) {
+        auto a = batched(x1, ub), b = batched(x2, ub);
+        auto out = at::empty({a.size(0), a.size(1), b.size(1)}, a.options());
+        check_rc(tpw_haversine_f64(a.data_ptr<double>(), b.data_ptr<double>(), a.size(0), a.size(1), b.size(1),
+                                   out.data_ptr<double>(), current_stream()),
+                 "_haversine");
+        return unbatch(out, ub);
+    }
     auto a = batched(gpu_f32(x1, "_haversine"), ub), b = batched(gpu_f32(x2, "_haversine"), ub);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1);
     auto out = at::empty({B, n, m}, a.options());
@@ -148,6 +153,15 @@ at::Tensor haversine_cuda(const at::Tensor &x1, const at::Tensor &x2) {
 T2 haversine_backward_cuda(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2) {
     const bool ub = x1.dim() == 2;
     DeviceGuard guard(x1.device());
+    if (x1.scalar_type() == at::kDouble) {
+        auto a = batched(x1, ub), b = batched(x2, ub), g = batched(grad.to(at::kDouble), ub);
+        auto gx1 = at::empty_like(a), gx2 = at::empty_like(b);
+        check_rc(tpw_haversine_f64_backward(g.data_ptr<double>(), a.data_ptr<double>(), b.data_ptr<double>(),
+                                            a.size(0), a.size(1), b.size(1), gx1.data_ptr<double>(),
+                                            gx2.data_ptr<double>(), current_stream()),
+                 "_haversine_backward");
+        return {unbatch(gx1, ub), unbatch(gx2, ub)};
+    }
     auto a = batched(gpu_f32(x1, "_haversine_backward"), ub), b = batched(gpu_f32(x2, "_haversine_backward"), ub);
     auto g = batched(gpu_f32(grad, "_haversine_backward"), ub);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1);

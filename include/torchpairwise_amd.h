@@ -64,6 +64,11 @@ int tpw_runtime_version(void);
 #define TPW_BIT_XOR 2
 #define TPW_BIT_EQ 3
 #define TPW_BIT_NE 4
+/* the ordering comparisons of the same header (tpw_pairwise_binary only) */
+#define TPW_CMP_LT 5
+#define TPW_CMP_GT 6
+#define TPW_CMP_LE 7
+#define TPW_CMP_GE 8
 /* reductions of common/reduction_ops.h:8-12 that produce float32 */
 #define TPW_RED_SUM 0
 #define TPW_RED_MEAN 1
@@ -413,6 +418,16 @@ int tpw_family_f64_backward(int metric, const double *grad, const double *x1, co
                             const double *w, int64_t batch, int64_t n, int64_t m, int64_t d,
                             double p, double *grad_x1, double *grad_x2, double *grad_w,
                             void *workspace, void *stream);
+
+/* Unreduced pairwise binary op: out[b,i,j,k] = op(x1[b,i,k], x2[b,j,k]) as bool bytes (0/1),
+ * out [batch, n, m, d] 16-byte aligned; x1 [batch, n, d], x2 [batch, m, d] of element type
+ * dtype (TPW_U8 for bool).  op: TPW_BIT_AND / OR / XOR (bool elements only, as the reference
+ * dispatches them), TPW_BIT_EQ / NE, TPW_CMP_LT / GT / LE / GE (float16 and bfloat16 compared
+ * as float).  Replaces pairwise_binary_forward_kernel (cuda/pairwise_binary_kernels.cu:16-30,
+ * 61-141; cpu/pairwise_binary_kernels.cpp:12-26) behind pwand, pwor, pwxor, pweq, pwne, pwlt,
+ * pwgt, pwle, pwge (pairwise_binary.cpp:34-89). */
+int tpw_pairwise_binary(const void *x1, const void *x2, int dtype, int op, int64_t batch, int64_t n,
+                        int64_t m, int64_t d, uint8_t *out, void *stream);
 
 /* Workspace (bytes) of tpw_haversine / tpw_haversine_backward. */
 size_t tpw_haversine_workspace_size(int64_t batch, int64_t n, int64_t m);

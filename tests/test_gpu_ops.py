@@ -632,3 +632,43 @@ def test_exp_kernels_gpu_batched_and_capi():
         assert_close(fn(x1.to(DEV), x2.to(DEV), 0.03).cpu(), ref, rtol=1e-5, atol=1e-6, what=name)
         got = capi.pairwise_exp_kernel(x1.to(DEV), x2.to(DEV), kind, 0.03)
         assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-6, what=f"{name} C ABI")
+
+
+# --------------------------------------------------------------------------------------
+# unreduced pairwise binary ops (pwand ... pwge) on the HIP kernel
+# --------------------------------------------------------------------------------------
+def test_pw_binary_gpu_equal_cpu():
+    """Every case of tests/_pw_binary_cases.py on the GPU against this build's CPU op (which
+    test_pw_binary.py pins to the reference's compiled kernels): outputs and shapes bit for
+    bit, the same errors (with the device in the dispatch name)."""
+    from oracle import ref_runner
+    from tests._pw_binary_cases import pw_binary_cases
+
+    ops = torch.ops.torchpairwise
+    for case, t in pw_binary_cases():
+        ours = ref_runner.run_op_case(ops, case, t, DEV)
+        want = ref_runner.run_op_case(ops, case, t, "cpu")
+        what = f"{case['op']} {t['a'].dtype}/{t['b'].dtype} {tuple(t['a'].shape)} {tuple(t['b'].shape)}"
+        if "err" in want or "err" in ours:
+            assert ours.get("err", "").replace("_cuda", "_cpu") == want.get("err"), what
+            continue
+        assert ours["out0"].shape == want["out0"].shape and torch.equal(ours["out0"], want["out0"]), what
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.int64, torch.float16, torch.bool])
+def test_pw_binary_gpu_large_and_tail(dtype):
+    """A size whose byte count is not a multiple of 16 (a partial last store), batched with
+    trailing feature dims, for each op the dtype allows."""
+    g = torch.Generator().manual_seed(4)
+    if dtype == torch.bool:
+        a, b = torch.rand(3, 301, 7, 2, generator=g) < 0.5, torch.rand(3, 257, 7, 2, generator=g) < 0.5
+        names = ["pwand", "pwor", "pwxor", "pweq", "pwne"]
+    else:
+        a = torch.randint(-3, 4, (3, 301, 7, 2), generator=g).to(dtype)
+        b = torch.randint(-3, 4, (3, 257, 7, 2), generator=g).to(dtype)
+        names = ["pweq", "pwne", "pwlt", "pwgt", "pwle", "pwge"]
+    for name in names:
+        got = getattr(torch.ops.torchpairwise, name)(a.to(DEV), b.to(DEV))
+        want = getattr(torch.ops.torchpairwise, name)(a, b)
+        assert got.shape == (3, 301, 257, 7, 2)
+        assert torch.equal(got.cpu(), want), name

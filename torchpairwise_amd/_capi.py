@@ -18,6 +18,7 @@ HEADER = _PKG.parent / "include" / "torchpairwise_amd.h"
 TPW_F32, TPW_BF16, TPW_F16, TPW_F64, TPW_I8, TPW_U8, TPW_I16, TPW_I32, TPW_I64 = range(9)
 BIT_AND, BIT_OR, BIT_XOR, BIT_EQ, BIT_NE = 0, 1, 2, 3, 4
 RED_SUM, RED_MEAN = 0, 1
+CMP_LT, CMP_GT, CMP_LE, CMP_GE = 5, 6, 7, 8
 EPI_DOT, EPI_EUCLIDEAN, EPI_SQEUCLIDEAN, EPI_COSINE_SIM, EPI_COSINE_DIST, EPI_CORRELATION = 0, 1, 2, 3, 4, 5
 KER_POLYNOMIAL, KER_SIGMOID, KER_RBF, KER_LAPLACIAN = 0, 1, 2, 3
 FAM_PPMINKOWSKI, FAM_WMINKOWSKI, FAM_CANBERRA, FAM_BRAYCURTIS, FAM_CHI2, FAM_JS = 0, 1, 2, 3, 4, 5
@@ -84,6 +85,7 @@ _SIGNATURES = {
     "tpw_haversine_workspace_size": (_sz, [_i64, _i64, _i64]),
     "tpw_haversine": (_i, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "tpw_haversine_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "tpw_pairwise_binary": (_i, [_p, _p, _i, _i, _i64, _i64, _i64, _i64, _p, _p]),
     "tpw_family_f64": (_i, [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
     "tpw_family_f64_backward_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64, _d]),
     "tpw_family_f64_backward": (_i, [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p, _p, _p, _p]),

@@ -193,7 +193,62 @@ at::Tensor row_smallest_mask_cpu(const at::Tensor &dist, int64_t count) {
     return mask;
 }
 
+namespace {
+
+// out[b, i, j, k] = op(x1[b, i, k], x2[b, j, k]) (cpu/pairwise_binary_kernels.cpp:12-26),
+// parallel over (b, i) rows.
+template <int OP, typename T>
+bool pw_apply(T x, T y) {
+    if constexpr (OP == TPW_BIT_AND || OP == TPW_BIT_OR || OP == TPW_BIT_XOR) {
+        const bool p = static_cast<bool>(x), q = static_cast<bool>(y);
+        return OP == TPW_BIT_AND ? (p && q) : OP == TPW_BIT_OR ? (p || q) : (p != q);
+    } else if constexpr (OP == TPW_BIT_EQ) {
+        return x == y;
+    } else if constexpr (OP == TPW_BIT_NE) {
+        return x != y;
+    } else if constexpr (OP == TPW_CMP_LT) {
+        return x < y;
+    } else if constexpr (OP == TPW_CMP_GT) {
+        return x > y;
+    } else if constexpr (OP == TPW_CMP_LE) {
+        return x <= y;
+    } else {
+        return x >= y;
+    }
+}
+
+template <int OP>
+at::Tensor pw_binary_cpu(const at::Tensor &x1, const at::Tensor &x2) {
+    auto r = pw_binary_prepare(OP, x1, x2, "pairwise_binary_forward_cpu");
+    const int64_t B = r.a.size(0), n = r.a.size(1), m = r.b.size(1), d = r.a.size(2);
+    auto out = at::empty({B, n, m, d}, r.a.options().dtype(at::kBool));
+    bool *O = out.data_ptr<bool>();
+    AT_DISPATCH_ALL_TYPES_AND3(at::kHalf, at::kBFloat16, at::kBool, r.a.scalar_type(), "pw_binary_cpu", [&] {
+        const scalar_t *A = r.a.data_ptr<scalar_t>(), *Bp = r.b.data_ptr<scalar_t>();
+        at::parallel_for(0, B * n, 1, [&](int64_t lo, int64_t hi) {
+            for (int64_t bi = lo; bi < hi; ++bi) {
+                const int64_t b = bi / n;
+                for (int64_t j = 0; j < m; ++j)
+                    for (int64_t k = 0; k < d; ++k)
+                        O[(bi * m + j) * d + k] = pw_apply<OP, scalar_t>(A[bi * d + k], Bp[(b * m + j) * d + k]);
+            }
+        });
+    });
+    return out.view(r.out_shape);
+}
+
+}  // namespace
+
 TORCH_LIBRARY_IMPL(torchpairwise, CPU, m) {
+    m.impl("pwand", TORCH_FN(pw_binary_cpu<TPW_BIT_AND>));
+    m.impl("pwor", TORCH_FN(pw_binary_cpu<TPW_BIT_OR>));
+    m.impl("pwxor", TORCH_FN(pw_binary_cpu<TPW_BIT_XOR>));
+    m.impl("pweq", TORCH_FN(pw_binary_cpu<TPW_BIT_EQ>));
+    m.impl("pwne", TORCH_FN(pw_binary_cpu<TPW_BIT_NE>));
+    m.impl("pwlt", TORCH_FN(pw_binary_cpu<TPW_CMP_LT>));
+    m.impl("pwgt", TORCH_FN(pw_binary_cpu<TPW_CMP_GT>));
+    m.impl("pwle", TORCH_FN(pw_binary_cpu<TPW_CMP_LE>));
+    m.impl("pwge", TORCH_FN(pw_binary_cpu<TPW_CMP_GE>));
     m.impl("pwand_sum", TORCH_FN((pw_reduce_cpu<TPW_BIT_AND, false>)));
     m.impl("pwor_sum", TORCH_FN((pw_reduce_cpu<TPW_BIT_OR, false>)));
     m.impl("pwxor_sum", TORCH_FN((pw_reduce_cpu<TPW_BIT_XOR, false>)));

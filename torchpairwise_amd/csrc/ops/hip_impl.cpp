@@ -489,12 +489,19 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_indexed_cuda(
 
 namespace {
 
-// ---------------------------------------------------------------- elementwise pw ops
-template <typename F>
-at::Tensor pw_elementwise(const at::Tensor &x1, const at::Tensor &x2, F f) {
-    // [b, n, d] x [b, m, d] -> [b, n, m, d] (csrc/ops/cpu/pairwise_binary_kernels.cpp:12-26)
-    TORCH_CHECK(x1.dim() >= 2 && x2.dim() >= 2, "x1 and x2 must have at least 2 dimensions.");
-    return f(x1.unsqueeze(-2), x2.unsqueeze(-3));
+// ---------------------------------------------------------------- unreduced pw ops
+template <int OP>
+at::Tensor pw_binary_cuda(const at::Tensor &x1, const at::Tensor &x2) {
+    TORCH_CHECK(x1.device() == x2.device(), "pairwise_binary_forward: x1 and x2 must be on the same device");
+    DeviceGuard guard(x1.device());
+    auto r = pw_binary_prepare(OP, x1, x2, "pairwise_binary_forward_cuda");
+    const int64_t B = r.a.size(0), n = r.a.size(1), m = r.b.size(1), d = r.a.size(2);
+    auto out = at::empty({B, n, m, d}, r.a.options().dtype(at::kBool));
+    const int code = r.a.scalar_type() == at::kBool ? TPW_U8 : float_code(r.a.scalar_type());
+    check_rc(tpw_pairwise_binary(r.a.data_ptr(), r.b.data_ptr(), code, OP, B, n, m, d,
+                                 reinterpret_cast<uint8_t *>(out.data_ptr()), current_stream()),
+             "pairwise_binary_forward");
+    return out.view(r.out_shape);
 }
 
 }  // namespace
@@ -518,21 +525,15 @@ TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
     m.impl("pwne_mean", TORCH_FN((pw_reduce_cuda<TPW_BIT_NE, TPW_RED_MEAN>)));
     m.impl("_directed_hausdorff", TORCH_FN(directed_hausdorff_cuda));
     m.impl("__directed_hausdorff_backward", TORCH_FN(directed_hausdorff_backward_cuda));
-}
-
-// The unreduced pairwise comparisons ([b, n, m, d] bool) are plain broadcast elementwise ops;
-// they run through ATen on either device (CompositeExplicitAutograd: no gradient, as in the
-// reference, which registers no Autograd kernel for them).
-TORCH_LIBRARY_IMPL(torchpairwise, CompositeExplicitAutograd, m) {
-    m.impl("pwand", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::logical_and(u, v); }); });
-    m.impl("pwor", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::logical_or(u, v); }); });
-    m.impl("pwxor", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::logical_xor(u, v); }); });
-    m.impl("pweq", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::eq(u, v); }); });
-    m.impl("pwne", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::ne(u, v); }); });
-    m.impl("pwlt", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::lt(u, v); }); });
-    m.impl("pwgt", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::gt(u, v); }); });
-    m.impl("pwle", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::le(u, v); }); });
-    m.impl("pwge", [](const at::Tensor &a, const at::Tensor &b) { return pw_elementwise(a, b, [](const at::Tensor &u, const at::Tensor &v) { return at::ge(u, v); }); });
+    m.impl("pwand", TORCH_FN(pw_binary_cuda<TPW_BIT_AND>));
+    m.impl("pwor", TORCH_FN(pw_binary_cuda<TPW_BIT_OR>));
+    m.impl("pwxor", TORCH_FN(pw_binary_cuda<TPW_BIT_XOR>));
+    m.impl("pweq", TORCH_FN(pw_binary_cuda<TPW_BIT_EQ>));
+    m.impl("pwne", TORCH_FN(pw_binary_cuda<TPW_BIT_NE>));
+    m.impl("pwlt", TORCH_FN(pw_binary_cuda<TPW_CMP_LT>));
+    m.impl("pwgt", TORCH_FN(pw_binary_cuda<TPW_CMP_GT>));
+    m.impl("pwle", TORCH_FN(pw_binary_cuda<TPW_CMP_LE>));
+    m.impl("pwge", TORCH_FN(pw_binary_cuda<TPW_CMP_GE>));
 }
 
 }  // namespace tpw_ext

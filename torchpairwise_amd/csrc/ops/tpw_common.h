@@ -9,6 +9,7 @@
 #include <string>
 #include <tuple>
 #include <utility>
+#include <vector>
 
 #include "torchpairwise_amd.h"
 
@@ -45,6 +46,52 @@ inline int float_code(at::ScalarType t) {
         case at::kLong: return TPW_I64;
         default: return -1;
     }
+}
+
+// The unreduced pairwise binary ops (pwand ... pwge), as the reference's
+// pairwise_binary_forward_kernel prepares them (cpu/pairwise_binary_kernels.cpp:52-108,
+// cuda/pairwise_binary_kernels.cu:61-141): 2-D inputs are unbatched, others [b, n, ...] with
+// the trailing dims flattened into the features; both in at::result_type; the output
+// [b, n, m, trailing...] (unbatched: [n, m, d]).  Element types as the reference dispatches
+// them: logical ops bool only, eq / ne every integer and floating type and bool, the ordering
+// comparisons every integer and floating type (no bool); others raise NotImplementedError
+// with the reference's dispatch message.
+struct PwBinaryArgs {
+    at::Tensor a, b;  // [B, n, D] and [B, m, D], contiguous, common type
+    std::vector<int64_t> out_shape;
+};
+inline PwBinaryArgs pw_binary_prepare(int op, const at::Tensor &x1, const at::Tensor &x2, const char *name) {
+    const bool unbatched = x1.dim() == 2;
+    TORCH_CHECK(x1.dim() >= 2, "x1 must have at least 2 dimensions.")
+    TORCH_CHECK(x2.dim() >= 2, "x2 must have at least 2 dimensions.")
+    TORCH_CHECK(unbatched || x1.size(0) == x2.size(0), "batch_size of x1 and x2 do not match.")
+    bool same = !unbatched && x1.dim() == x2.dim();
+    for (int64_t d = 2; same && d < x1.dim(); ++d) same = x1.size(d) == x2.size(d);
+    TORCH_CHECK((unbatched && x1.size(1) == x2.size(1)) || (!unbatched && same),
+                "feature dimensions of x1 and x2 do not match.")
+    const auto t = at::result_type(x1, x2);
+    bool ok;
+    if (op <= TPW_BIT_XOR) ok = t == at::kBool;
+    else ok = t == at::kByte || t == at::kChar || t == at::kShort || t == at::kInt || t == at::kLong ||
+              t == at::kFloat || t == at::kDouble || t == at::kHalf || t == at::kBFloat16 ||
+              (t == at::kBool && (op == TPW_BIT_EQ || op == TPW_BIT_NE));
+    TORCH_CHECK_NOT_IMPLEMENTED(ok, "\"", name, "\" not implemented for '", c10::toString(t), "'");
+    PwBinaryArgs r;
+    r.a = x1.to(t).contiguous();
+    r.b = x2.to(t).contiguous();
+    if (unbatched) {
+        r.a = r.a.unsqueeze(0);
+        r.b = r.b.unsqueeze(0);
+    }
+    r.a = r.a.flatten(2);
+    r.b = r.b.flatten(2);
+    if (unbatched) {
+        r.out_shape = {r.a.size(1), r.b.size(1), r.a.size(2)};
+    } else {
+        r.out_shape = {r.a.size(0), r.a.size(1), r.b.size(1)};
+        for (int64_t d = 2; d < x1.dim(); ++d) r.out_shape.push_back(x1.size(d));
+    }
+    return r;
 }
 
 // [n, d] -> [1, n, d]; [b, n, d] unchanged (contiguous either way).

@@ -90,3 +90,37 @@ def public_cases():
     add("radius_neighbors_mask", [T("a"), T("b"), V(5.0)], {"a": a, "b": b}, exact=True)
     add("pdist", [T("a")], {"a": a}, exact=True)
     return out
+
+
+DTYPE_SWEEP = [torch.float64, torch.float16, torch.bfloat16, torch.int64, torch.uint8, torch.bool]
+
+
+def public_dtype_cases():
+    """[(case, tensors)]: the forward cases of public_cases() (directed Hausdorff aside) with
+    every tensor cast to each of DTYPE_SWEEP (integers: small rounded values; bool: != 0).  The
+    reference raises for many of them; its messages are part of the interface."""
+    out = []
+    for case, t, _ in public_cases():
+        if case["op"] == "directed_hausdorff_distances":
+            continue
+        for dt in DTYPE_SWEEP:
+            tt = {}
+            for k, v in t.items():
+                if k == "g":
+                    continue
+                if dt == torch.bool:
+                    tt[k] = v != 0
+                elif v.dtype == torch.bool:
+                    tt[k] = v.to(dt)
+                elif dt in (torch.int64, torch.uint8):
+                    tt[k] = (v * 3).round().clamp(0 if dt == torch.uint8 else -9, 9).to(dt)
+                else:
+                    tt[k] = v.to(dt)
+            c = {k: v for k, v in case.items() if k not in ("grad", "req")}
+            c["req"] = []
+            out.append((c, tt))
+    return out
+
+
+def dtype_tolerance(dtype):
+    return {torch.float64: 1e-10, torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 3e-2}.get(dtype, 0.0)

@@ -317,12 +317,30 @@ def test_radius_neighbors_mask_gpu():
 # --------------------------------------------------------------------------------------
 # the reference's VALU family through the drop-in ops
 # --------------------------------------------------------------------------------------
+# ops whose reference kernels dispatch floating types and half only (no bfloat16), by the
+# kernel name of their refusal (cuda/<op>_kernel.cu)
+NO_BF16 = {"canberra_distances": "_canberra", "braycurtis_distances": "_braycurtis",
+           "additive_chi2_kernel": "_additive_chi2_kernel", "chi2_kernel": "_additive_chi2_kernel",
+           "jensenshannon_distances": "_sqjensenshannon", "snr_distances": "_snr"}
+
+
+def _refused_bf16(name, dtype, args):
+    """bfloat16 where the reference's kernel refuses it: the same NotImplementedError."""
+    if dtype != torch.bfloat16 or name not in NO_BF16:
+        return False
+    with pytest.raises(NotImplementedError, match=f'"{NO_BF16[name]}_forward_cuda" not implemented for'):
+        getattr(tp, name)(*args)
+    return True
+
+
 @pytest.mark.parametrize("name", ["sqeuclidean_distances", "canberra_distances", "braycurtis_distances",
                                   "wminkowski_distances", "seuclidean_distances"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_family_ops_gpu(name, dtype):
     print(f"{name} {dtype}", flush=True)
     x1, x2 = randn(150, 24, seed=0, dtype=dtype), randn(90, 24, seed=1, dtype=dtype)
+    if _refused_bf16(name, dtype, (x1.to(DEV), x2.to(DEV))):
+        return
     w = (rand(24, seed=2) + 0.2).to(dtype)
     extra = {"wminkowski_distances": (3.0, w), "seuclidean_distances": (w,)}.get(name, ())
     fn = getattr(tp, name)
@@ -427,10 +445,13 @@ def _special_case(name, dtype):
 
 @pytest.mark.parametrize("name", ["additive_chi2_kernel", "chi2_kernel", "jensenshannon_distances",
                                   "haversine_distances", "snr_distances", "mahalanobis_distances"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_special_ops_gpu(name, dtype):
     print(f"{name} {dtype}", flush=True)
     x1, x2, extra = _special_case(name, dtype)
+    if _refused_bf16(name, dtype, (x1.to(DEV), x2.to(DEV), *[e.to(DEV, dtype) if torch.is_tensor(e) else e
+                                                               for e in extra])):
+        return
     fn = getattr(tp, name)
     a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
     dev_extra = [e.to(DEV, dtype) if torch.is_tensor(e) else e for e in extra]
@@ -672,3 +693,69 @@ def test_pw_binary_gpu_large_and_tail(dtype):
         want = getattr(torch.ops.torchpairwise, name)(a, b)
         assert got.shape == (3, 301, 257, 7, 2)
         assert torch.equal(got.cpu(), want), name
+
+
+def test_pw_reductions_gpu_equal_cpu():
+    """pw*_sum / pw*_mean on the GPU for every case of pw_reduction_cases (every element type,
+    the refused ones, bad shapes) against this build's CPU op, which test_pw_binary.py pins to
+    the reference's compiled kernels: float32 counts bit for bit, the same errors."""
+    from oracle import ref_runner
+    from tests._pw_binary_cases import pw_reduction_cases
+
+    ops = torch.ops.torchpairwise
+    for case, t in pw_reduction_cases():
+        ours = ref_runner.run_op_case(ops, case, t, DEV)
+        want = ref_runner.run_op_case(ops, case, t, "cpu")
+        what = f"{case['op']} {t['a'].dtype}/{t['b'].dtype} {tuple(t['a'].shape)} {tuple(t['b'].shape)}"
+        if "err" in want or "err" in ours:
+            assert ours.get("err", "").replace("_cuda", "_cpu") == want.get("err"), what
+            continue
+        assert ours["out0"].shape == want["out0"].shape, what
+        assert_equal(ours["out0"], want["out0"], what)
+
+
+def test_public_ops_dtypes_gpu_equal_reference(tmp_path):
+    """Every public op's forward on GPU tensors of float64, float16, bfloat16, int64, uint8 and
+    bool against the reference's compiled CPU library.  Refusals of this build's own ops (the
+    reference's kernel dispatch names) must match, device name aside.  Where ATen decides (the
+    reference calls at::cdist / matmul, whose CUDA dtype support differs from their CPU support,
+    and the reference on a GPU makes the same calls): an ATen CUDA refusal is accepted where the
+    CPU computes, a CPU-side ATen refusal is not compared, except that this build serves
+    bfloat16 for the cdist metrics where at::cdist refuses it.  Results that both produce agree
+    within the dtype's bar (the x2 = None euclidean within the matrix form's self-distance
+    floor, which the reference's own GPU route shares)."""
+    from oracle import ref_runner
+    from tests._public_cases import public_dtype_cases
+    from tests.test_reference_pin import _dtype_sweep_compare
+
+    if not ref_runner.available():
+        pytest.skip("oracle/_ref not built")
+    cs = public_dtype_cases()
+    ref = ref_runner.run_op_reference(cs, tmp_path)
+    ops = torch.ops.torchpairwise
+    own = ('_forward_cpu"', '_backward_cpu"', '"pairwise_binary')
+    failures = []
+    for (case, t), r in zip(cs, ref):
+        dt = next(iter(t.values())).dtype
+        what = f"{case['op']} {dt} {[tuple(v.shape) for v in t.values()]} {case['args'][1:]}"
+        ours = ref_runner.run_op_case(ops, case, t, DEV)
+        try:
+            if "err" in r:
+                if any(s in r["err"] for s in own):
+                    assert ours.get("err", "").replace('_cuda"', '_cpu"') == r["err"], \
+                        f"{what}: {ours.get('err')!r} != {r['err']!r}"
+                elif "err" not in ours:
+                    assert dt == torch.bfloat16 and '"cdist" not implemented' in r["err"], \
+                        f"{what}: computes where the reference raises {r['err']!r}"
+                continue
+            if "err" in ours:
+                assert '_cuda" not implemented for' in ours["err"], f"{what}: raises {ours['err']!r}"
+                continue
+            floor = 0.0
+            if case["op"] == "euclidean_distances" and len(case["args"]) == 1 and dt.is_floating_point:
+                a = t["a"].double()
+                floor = 4 * float((torch.finfo(dt).eps * 2 * (a * a).sum(-1).max()) ** 0.5)
+            _dtype_sweep_compare(ours, r, what, floor)
+        except AssertionError as e:
+            failures.append(str(e).splitlines()[0][:300])
+    assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures[:30])

@@ -65,3 +65,27 @@ def test_pw_binary_cpu_equal_reference(tmp_path):
         if not (ours["out0"].shape == r["out0"].shape and torch.equal(ours["out0"], r["out0"])):
             failures.append(f"{what}: outputs differ")
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures[:20])
+
+
+def test_pw_reductions_cpu_equal_reference(tmp_path):
+    """pw*_sum / pw*_mean on CPU tensors of every element type and the refused ones against the
+    reference's compiled kernels: float32 counts bit for bit, the same errors."""
+    from tests._pw_binary_cases import pw_reduction_cases
+
+    if not ref_runner.available():
+        pytest.skip("oracle/_ref not built")
+    cs = pw_reduction_cases()
+    ref = ref_runner.run_op_reference(cs, tmp_path)
+    ops = torch.ops.torchpairwise
+    failures = []
+    for (case, t), r in zip(cs, ref):
+        ours = ref_runner.run_op_case(ops, case, t, "cpu")
+        what = f"{case['op']} {t['a'].dtype}/{t['b'].dtype} {tuple(t['a'].shape)} {tuple(t['b'].shape)}"
+        if "err" in r or "err" in ours:
+            if ours.get("err") != r.get("err"):
+                failures.append(f"{what}: {ours.get('err')!r} != {r.get('err')!r}")
+            continue
+        o, w = ours["out0"], r["out0"]
+        if not (o.dtype == w.dtype and o.shape == w.shape and torch.equal(o, w)):
+            failures.append(f"{what}: outputs differ")
+    assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures[:30])

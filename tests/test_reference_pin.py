@@ -186,3 +186,47 @@ def _check_public_cases(ops, device, tmp_path, rtol=1e-5, grad_rtol=1e-5):
         except AssertionError as e:
             failures.append(str(e).splitlines()[0][:300])
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)
+
+
+def _dtype_sweep_compare(ours, ref, what, floor=0.0):
+    """Errors equal; bool / integer outputs equal; floating outputs within the dtype's bar
+    (NaN positions equal)."""
+    from tests._public_cases import dtype_tolerance
+
+    assert sorted(ours) == sorted(ref), f"{what}: {ours.get('err')!r} != {ref.get('err')!r}"
+    for k in ref:
+        if k == "err":
+            assert ours[k] == ref[k], f"{what}: {ours[k]!r} != {ref[k]!r}"
+            continue
+        o, r = ours[k].cpu(), ref[k].cpu()
+        assert o.dtype == r.dtype and o.shape == r.shape, f"{what}[{k}]: {o.dtype} {tuple(o.shape)} vs {r.dtype} {tuple(r.shape)}"
+        if not o.is_floating_point():
+            assert torch.equal(o, r), f"{what}[{k}]"
+            continue
+        on, rn = torch.isnan(o), torch.isnan(r)
+        assert torch.equal(on, rn), f"{what}[{k}]: NaN positions differ"
+        of, rf = o.double().masked_fill(on, 0), r.double().masked_fill(rn, 0)
+        tol = dtype_tolerance(o.dtype)
+        atol = tol * max(1.0, float(rf.abs().max())) + floor
+        assert torch.allclose(of, rf, rtol=tol, atol=atol), f"{what}[{k}]: max diff {float((of - rf).abs().max())}"
+
+
+def test_public_ops_dtypes_cpu_equal_reference(tmp_path):
+    """Every public op's forward on CPU tensors of float64, float16, bfloat16, int64, uint8 and
+    bool against the reference's compiled library: the same results, or the same error (the
+    reference refuses many of these; its dispatch messages are part of the interface)."""
+    from tests._public_cases import public_dtype_cases
+
+    import torchpairwise_amd  # noqa: F401
+
+    cs = public_dtype_cases()
+    ref = ref_runner.run_op_reference(cs, tmp_path)
+    ops = torch.ops.torchpairwise
+    failures = []
+    for (case, t), r in zip(cs, ref):
+        what = f"{case['op']} {[str(v.dtype) for v in t.values()]} {[tuple(v.shape) for v in t.values()]}"
+        try:
+            _dtype_sweep_compare(ref_runner.run_op_case(ops, case, t, "cpu"), r, what)
+        except AssertionError as e:
+            failures.append(str(e).splitlines()[0][:300])
+    assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures[:30])

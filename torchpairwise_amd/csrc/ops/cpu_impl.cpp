@@ -24,9 +24,7 @@ at::Tensor pw_reduce_cpu(const at::Tensor &x1, const at::Tensor &x2) {
     TORCH_CHECK(unbatched || x1.size(0) == x2.size(0), "batch_size of x1 and x2 do not match.")
     TORCH_CHECK(x1.size(-1) == x2.size(-1), "feature dimension of x1 and x2 do not match.")
     const auto common = at::result_type(x1, x2);
-    if (OP == TPW_BIT_AND || OP == TPW_BIT_OR || OP == TPW_BIT_XOR)
-        TORCH_CHECK(common == at::kBool, "logical pairwise reductions (and/or/xor) are implemented "
-                    "for Bool only, got ", common);
+    pw_check_dispatch(OP, common, "pairwise_binary_reduction_forward_cpu");
     auto a = as3(x1.to(common)), b = as3(x2.to(common));
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto out = at::empty({B, n, m}, a.options().dtype(at::kFloat));
@@ -118,7 +116,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> hausdorff
     auto i2 = at::empty({B, b1, b2}, a.options().dtype(at::kLong));
     at::Tensor perm1, perm2;
     if (shuffle) std::tie(perm1, perm2) = hausdorff_perms(B, p1, p2, a.options(), gen);
-    AT_DISPATCH_FLOATING_TYPES_AND_HALF(a.scalar_type(), "directed_hausdorff_cpu", [&] {
+    AT_DISPATCH_FLOATING_TYPES_AND_HALF(a.scalar_type(), "_directed_hausdorff_forward_cpu", [&] {
         hausdorff_forward_loop<scalar_t>(a.data_ptr<scalar_t>(), b.data_ptr<scalar_t>(), B, b1, p1,
                                          b2, p2, d, shuffle ? perm1.data_ptr<int64_t>() : nullptr,
                                          shuffle ? perm2.data_ptr<int64_t>() : nullptr,
@@ -146,7 +144,7 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_cpu(
     const int64_t b2 = b.size(1), p2 = b.size(2);
     auto g = grad.to(a.scalar_type()).reshape({B, b1, b2}).contiguous();
     auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(b);
-    AT_DISPATCH_FLOATING_TYPES_AND_HALF(a.scalar_type(), "directed_hausdorff_backward_cpu", [&] {
+    AT_DISPATCH_FLOATING_TYPES_AND_HALF(a.scalar_type(), "_directed_hausdorff_backward_cpu", [&] {
         const scalar_t *X1 = a.data_ptr<scalar_t>(), *X2 = b.data_ptr<scalar_t>();
         const scalar_t *G = g.data_ptr<scalar_t>(), *O = out.data_ptr<scalar_t>();
         const int64_t *M = i1.data_ptr<int64_t>(), *N = i2.data_ptr<int64_t>();

@@ -69,6 +69,16 @@ void for_pairs(int64_t B, int64_t n, int64_t m, F f) {
 
 enum Fam { kPP, kW, kCanb, kBray, kChi2, kJS };
 
+// The reference's kernel names and dtypes: the Minkowski members take bfloat16, the others
+// floating types and half only (cpu/ and cuda/<op>_kernel.*).
+constexpr const char *fam_name(Fam F) {
+    return F == kPP ? "_ppminkowski" : F == kW ? "_wminkowski" : F == kCanb ? "_canberra"
+         : F == kBray ? "_braycurtis" : F == kChi2 ? "_additive_chi2_kernel" : "_sqjensenshannon";
+}
+inline void fam_check_dtype(Fam F, at::ScalarType t, const char *suffix) {
+    check_float_dispatch(t, F == kPP || F == kW, std::string(fam_name(F)) + suffix);
+}
+
 // rel_entr of cpu/rel_entr.h
 template <typename T>
 inline T rel_entr(T x, T y) {
@@ -148,6 +158,7 @@ at::Tensor family_forward_cpu(const at::Tensor &x1, const at::Tensor &x2, const 
         out.fill_(a.size(2));  // ppminkowski_kernel.cpp:90-91, wminkowski_kernel.cpp:101-102
         return unbatch(out, ub);
     }
+    fam_check_dtype(F, a.scalar_type(), "_forward_cpu");
     AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "family_forward", [&] {
         using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
         family_forward_loop<F, acc_t, scalar_t>(a, bb, w ? &wc : nullptr, p, out);
@@ -286,6 +297,7 @@ std::vector<at::Tensor> family_backward_cpu(const at::Tensor &grad, const at::Te
     at::Tensor wc = w ? batched(*w, ub) : at::Tensor();
     auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(bb);
     at::Tensor gw = w ? at::zeros_like(wc) : at::Tensor();
+    if (!((F == kPP || F == kW) && p == 0)) fam_check_dtype(F, g.scalar_type(), "_backward_cpu");
     if (!((F == kPP || F == kW) && p == 0) && a.numel() && bb.numel()) {
         AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "family_backward", [&] {
             using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
@@ -349,6 +361,7 @@ at::Tensor family_forward_cuda(const at::Tensor &x1, const at::Tensor &x2, const
                                double p, const char *from) {
     const bool ub = check_family_shapes(from, x1, x2, w);
     DeviceGuard guard(x1.device());
+    if (!((F == kPP || F == kW) && p == 0)) fam_check_dtype(F, x1.scalar_type(), "_forward_cuda");
     if (x1.scalar_type() == at::kDouble) return family_forward_f64<F>(x1, x2, w, p, ub, from);
     auto a = batched(gpu_f32(x1, from), ub), bb = batched(gpu_f32(x2, from), ub);
     at::Tensor wc = w ? batched(gpu_f32(*w, from), ub) : at::Tensor();
@@ -374,6 +387,7 @@ std::vector<at::Tensor> family_backward_cuda(const at::Tensor &grad, const at::T
                                              const at::Tensor *out_in, const char *from) {
     const bool ub = x1.dim() == 2;
     DeviceGuard guard(x1.device());
+    if (!((F == kPP || F == kW) && p == 0)) fam_check_dtype(F, grad.scalar_type(), "_backward_cuda");
     if (x1.scalar_type() == at::kDouble) return family_backward_f64<F>(grad, x1, x2, w, p, ub, from);
     auto a = batched(gpu_f32(x1, from), ub), bb = batched(gpu_f32(x2, from), ub);
     auto g = batched(gpu_f32(grad, from), ub);

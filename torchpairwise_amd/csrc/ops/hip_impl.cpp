@@ -301,6 +301,7 @@ at::Tensor pw_reduce_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     check_binary_shapes(x1, x2);
     DeviceGuard guard(x1.device());
     const auto common = at::result_type(x1, x2);
+    pw_check_dispatch(OP, common, "pairwise_binary_reduction_forward_cuda");
     auto a = as3(x1.to(common)), b = as3(x2.to(common));
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto out = at::empty({B, n, m}, a.options().dtype(at::kFloat));
@@ -320,8 +321,6 @@ at::Tensor pw_reduce_cuda(const at::Tensor &x1, const at::Tensor &x2) {
                                           B, n, m, d, OP, RED, out.data_ptr<float>(), current_stream()),
                  "pairwise bool reduction");
     } else {
-        TORCH_CHECK(OP == TPW_BIT_EQ || OP == TPW_BIT_NE, "logical pairwise reductions (and/or/xor) "
-                    "are implemented for Bool only, got ", common);
         const int code = float_code(common);
         TORCH_CHECK(code >= 0, "pairwise comparison not implemented for ", common);
         check_rc(tpw_compare_reduce(a.data_ptr(), b.data_ptr(), code, B, n, m, d, OP, RED,

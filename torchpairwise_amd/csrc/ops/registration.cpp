@@ -227,7 +227,8 @@ at::Tensor sqeuclidean_distances(const at::Tensor &x1, const c10::optional<at::T
 at::Tensor rbf_kernel(const at::Tensor &x1, const c10::optional<at::Tensor> &x2,
                       c10::optional<double> gamma) {
     const double g = gamma.value_or(1.0 / x1.size(1));
-    if (x1.is_cuda() && x1.scalar_type() != at::kDouble) {
+    if (x1.is_cuda() && (x1.scalar_type() == at::kFloat || x1.scalar_type() == at::kBFloat16 ||
+                         x1.scalar_type() == at::kHalf)) {
         auto xs = check_pairwise_inputs("sqeuclidean_distances", x1, x2);
         return pw_exp_kernel(xs.first, xs.second, TPW_KER_RBF, g);
     }

@@ -62,7 +62,7 @@ at::Tensor haversine_cpu(const at::Tensor &x1, const at::Tensor &x2) {
     auto a = batched(x1, ub), b = batched(x2, ub);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1);
     auto out = at::empty({B, n, m}, a.options());
-    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_haversine_cpu", [&] {
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_haversine_forward_cpu", [&] {
         using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
         const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>();
         scalar_t *O = out.data_ptr<scalar_t>();
@@ -131,6 +131,7 @@ at::Tensor gpu_f32(const at::Tensor &t, const char *) { return t.to(at::kFloat).
 
 at::Tensor haversine_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     const bool ub = check_haversine(x1, x2);
+    check_float_dispatch(x1.scalar_type(), true, "_haversine_forward_cuda");
     DeviceGuard guard(x1.device());
     if (x1.scalar_type() == at::kDouble) {
         auto a = batched(x1, ub), b = batched(x2, ub);
@@ -152,6 +153,7 @@ at::Tensor haversine_cuda(const at::Tensor &x1, const at::Tensor &x2) {
 
 T2 haversine_backward_cuda(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2) {
     const bool ub = x1.dim() == 2;
+    check_float_dispatch(grad.scalar_type(), true, "_haversine_backward_cuda");
     DeviceGuard guard(x1.device());
     if (x1.scalar_type() == at::kDouble) {
         auto a = batched(x1, ub), b = batched(x2, ub), g = batched(grad.to(at::kDouble), ub);
@@ -207,7 +209,8 @@ at::Tensor snr_cpu(const at::Tensor &x1, const at::Tensor &x2) {
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto out = at::empty({B, n, m}, a.options());
     auto v1 = at::var(a, at::IntArrayRef{2}, /*unbiased=*/false).mul_(d).contiguous();  // cpu/snr_kernel.cpp:96
-    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_snr_cpu", [&] {
+    check_float_dispatch(a.scalar_type(), false, "_snr_forward_cpu");
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_snr_forward_cpu", [&] {
         using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
         const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>(), *V = v1.data_ptr<scalar_t>();
         scalar_t *O = out.data_ptr<scalar_t>();
@@ -230,6 +233,7 @@ T2 snr_backward_cpu(const at::Tensor &grad, const at::Tensor &x1, const at::Tens
     auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(b);
     auto mu1 = a.mean(2).contiguous();
     auto v1 = at::var(a, at::IntArrayRef{2}, /*unbiased=*/false).mul_(d).contiguous();
+    check_float_dispatch(g.scalar_type(), false, "_snr_backward_cpu");
     AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_snr_backward_cpu", [&] {
         using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
         const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>(), *G = g.data_ptr<scalar_t>();
@@ -273,7 +277,18 @@ at::Tensor snr_composite(const at::Tensor &x1, const at::Tensor &x2) {
     return v1 / ppminkowski(a, b, 2);
 }
 
-at::Tensor snr_cuda(const at::Tensor &x1, const at::Tensor &x2) { return snr_composite(x1, x2); }
+// The reference's forward takes at::var of x1 before its dtype dispatch (cuda/snr_kernel.cu:
+// 100-105), so integer inputs fail in at::var and bfloat16 in the dispatch; the same here.
+void snr_check_cuda(const at::Tensor &x1, const at::Tensor &x2) {
+    check_snr(x1, x2);
+    if (!at::isFloatingType(x1.scalar_type())) (void)at::var(x1, -1, false);
+    check_float_dispatch(x1.scalar_type(), false, "_snr_forward_cuda");
+}
+
+at::Tensor snr_cuda(const at::Tensor &x1, const at::Tensor &x2) {
+    snr_check_cuda(x1, x2);
+    return snr_composite(x1, x2);
+}
 
 // Gradients of a GPU composition by autograd, whatever the caller's grad mode.
 template <typename F>
@@ -287,6 +302,7 @@ variable_list composite_grads(F f, const at::Tensor &grad, std::vector<at::Tenso
 }
 
 T2 snr_backward_cuda(const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2) {
+    check_float_dispatch(grad.scalar_type(), false, "_snr_backward_cuda");
     auto g = composite_grads([](const std::vector<Variable> &v) { return snr_composite(v[0], v[1]); },
                              grad, {x1, x2});
     return {g[0], g[1]};
@@ -314,7 +330,7 @@ at::Tensor sqmahalanobis_cpu(const at::Tensor &x1, const at::Tensor &x2, const a
     auto a = batched(x1, ub), b = batched(x2, ub), w = batched(VI, ub);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     auto out = at::empty({B, n, m}, a.options());
-    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_sqmahalanobis_cpu", [&] {
+    AT_DISPATCH_FLOATING_TYPES_AND2(at::kHalf, at::kBFloat16, a.scalar_type(), "_sqmahalanobis_forward_cpu", [&] {
         using acc_t = std::conditional_t<std::is_same_v<scalar_t, double>, double, float>;
         const scalar_t *P = a.data_ptr<scalar_t>(), *Q = b.data_ptr<scalar_t>(), *W = w.data_ptr<scalar_t>();
         scalar_t *O = out.data_ptr<scalar_t>();
@@ -392,8 +408,8 @@ T3 sqmahalanobis_backward_cpu(const at::Tensor &grad, const at::Tensor &x1, cons
 
 // GPU: d^T VI d per pair from the difference d and the per-row projections x VI^T
 // (tpw_sqmahalanobis, mahalanobis.hip).  16-bit types compute in float32, float64 in double.
-at::ScalarType mahalanobis_compute_type(at::ScalarType t) {
-    TORCH_CHECK(at::isFloatingType(t), "\"_sqmahalanobis_forward_cuda\" not implemented for '", t, "'");
+at::ScalarType mahalanobis_compute_type(at::ScalarType t, const char *name = "_sqmahalanobis_forward_cuda") {
+    check_float_dispatch(t, true, name);
     return t == at::kDouble ? at::kDouble : at::kFloat;
 }
 
@@ -424,7 +440,7 @@ T3 sqmahalanobis_backward_cuda(const at::Tensor &grad, const at::Tensor &x1, con
                                const at::Tensor &VI) {
     const bool ub = check_mahalanobis(x1, x2, VI);
     DeviceGuard guard(x1.device());
-    const auto dt = x1.scalar_type(), ct = mahalanobis_compute_type(dt);
+    const auto dt = x1.scalar_type(), ct = mahalanobis_compute_type(grad.scalar_type(), "_sqmahalanobis_backward_cuda");
     auto a = batched(x1, ub).to(ct), b = batched(x2, ub).to(ct), w = batched(VI, ub).to(ct);
     auto g = batched(grad, ub).to(ct);
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
@@ -537,7 +553,10 @@ at::Tensor haversine_autograd(const at::Tensor &x1, const at::Tensor &x2) {
     return HaversineFunction::apply(x1, x2);
 }
 at::Tensor snr_autograd(const at::Tensor &x1, const at::Tensor &x2) {
-    if (x1.is_cuda()) return snr_composite(x1, x2);
+    if (x1.is_cuda()) {
+        snr_check_cuda(x1, x2);
+        return snr_composite(x1, x2);
+    }
     return SnrFunction::apply(x1, x2);
 }
 at::Tensor sqmahalanobis_autograd(const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &VI) {

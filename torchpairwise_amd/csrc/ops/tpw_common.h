@@ -56,6 +56,25 @@ inline int float_code(at::ScalarType t) {
 // them: logical ops bool only, eq / ne every integer and floating type and bool, the ordering
 // comparisons every integer and floating type (no bool); others raise NotImplementedError
 // with the reference's dispatch message.
+// The reference's dtype dispatch of its own metric kernels (cpu/ and cuda/<op>_kernel.*):
+// floating types and half, and bfloat16 where `bf16` (AT_DISPATCH_FLOATING_TYPES_AND2 rather
+// than _AND_HALF); others raise its dispatch message for kernel `name`.
+inline void check_float_dispatch(at::ScalarType t, bool bf16, const std::string &name) {
+    const bool ok = t == at::kFloat || t == at::kDouble || t == at::kHalf || (bf16 && t == at::kBFloat16);
+    TORCH_CHECK_NOT_IMPLEMENTED(ok, "\"", name, "\" not implemented for '", c10::toString(t), "'");
+}
+
+// Whether the reference dispatches binary op `op` (TPW_BIT_* / TPW_CMP_*) for element type t
+// (common/binary_ops.h:69-78); if not, raise its dispatch message for kernel `name`.
+inline void pw_check_dispatch(int op, at::ScalarType t, const char *name) {
+    bool ok;
+    if (op <= TPW_BIT_XOR) ok = t == at::kBool;
+    else ok = t == at::kByte || t == at::kChar || t == at::kShort || t == at::kInt || t == at::kLong ||
+              t == at::kFloat || t == at::kDouble || t == at::kHalf || t == at::kBFloat16 ||
+              (t == at::kBool && (op == TPW_BIT_EQ || op == TPW_BIT_NE));
+    TORCH_CHECK_NOT_IMPLEMENTED(ok, "\"", name, "\" not implemented for '", c10::toString(t), "'");
+}
+
 struct PwBinaryArgs {
     at::Tensor a, b;  // [B, n, D] and [B, m, D], contiguous, common type
     std::vector<int64_t> out_shape;
@@ -70,12 +89,7 @@ inline PwBinaryArgs pw_binary_prepare(int op, const at::Tensor &x1, const at::Te
     TORCH_CHECK((unbatched && x1.size(1) == x2.size(1)) || (!unbatched && same),
                 "feature dimensions of x1 and x2 do not match.")
     const auto t = at::result_type(x1, x2);
-    bool ok;
-    if (op <= TPW_BIT_XOR) ok = t == at::kBool;
-    else ok = t == at::kByte || t == at::kChar || t == at::kShort || t == at::kInt || t == at::kLong ||
-              t == at::kFloat || t == at::kDouble || t == at::kHalf || t == at::kBFloat16 ||
-              (t == at::kBool && (op == TPW_BIT_EQ || op == TPW_BIT_NE));
-    TORCH_CHECK_NOT_IMPLEMENTED(ok, "\"", name, "\" not implemented for '", c10::toString(t), "'");
+    pw_check_dispatch(op, t, name);
     PwBinaryArgs r;
     r.a = x1.to(t).contiguous();
     r.b = x2.to(t).contiguous();

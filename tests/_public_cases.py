@@ -124,3 +124,63 @@ def public_dtype_cases():
 
 def dtype_tolerance(dtype):
     return {torch.float64: 1e-10, torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 3e-2}.get(dtype, 0.0)
+
+
+CDIST_METRICS = ["braycurtis", "canberra", "chebyshev", "cityblock", "correlation", "cosine", "dice",
+                 "directed_hausdorff", "euclidean", "hamming", "haversine", "jaccard", "jensenshannon",
+                 "kulczynski1", "kulsinski", "l1", "l2", "lp", "linf", "mahalanobis", "manhattan", "minkowski",
+                 "rogerstanimoto", "russellrao", "seuclidean", "snr", "sokalmichener", "sokalsneath",
+                 "sqeuclidean", "wminkowski", "yule"]
+BOOL_NAMES = {"dice", "hamming", "jaccard", "kulczynski1", "kulsinski", "rogerstanimoto", "russellrao",
+              "sokalmichener", "sokalsneath", "yule"}
+
+
+def cdist_name_cases():
+    """[(case, tensors, exact)] of cdist(x1, x2, metric, **extra) for every metric the reference's
+    dispatcher knows (cpdist.cpp), with its extra arguments where it takes them (and their
+    defaults), plus one argument it does not take (the reference raises TypeError naming it and
+    the supported signature)."""
+    a = torch.randn(37, 16, generator=_g(31))
+    b = torch.randn(29, 16, generator=_g(32))
+    pa, pb = torch.rand(37, 16, generator=_g(33)) + 0.05, torch.rand(29, 16, generator=_g(34)) + 0.05
+    ba, bb = torch.rand(37, 70, generator=_g(35)) < 0.3, torch.rand(29, 70, generator=_g(36)) < 0.3
+    la, lb = torch.rand(37, 2, generator=_g(37)) * 2 - 1, torch.rand(29, 2, generator=_g(38)) * 2 - 1
+    ca, cb = torch.rand(3, 60, 3, generator=_g(39)), torch.rand(2, 50, 3, generator=_g(40)) + 0.05
+    w = torch.rand(16, generator=_g(41)) + 0.2
+    VI = torch.eye(16) + 0.1 * torch.ones(16, 16)
+    T = lambda name: {"t": name}  # noqa: E731
+    V = lambda v: {"v": v}  # noqa: E731
+    out = []
+    for metric in CDIST_METRICS:
+        if metric in BOOL_NAMES:
+            ts, exact = {"a": ba, "b": bb}, True
+        elif metric == "haversine":
+            ts, exact = {"a": la, "b": lb}, False
+        elif metric == "directed_hausdorff":
+            ts, exact = {"a": ca, "b": cb}, True
+        elif metric == "jensenshannon":
+            ts, exact = {"a": pa, "b": pb}, False
+        else:
+            ts, exact = {"a": a, "b": b}, False
+        variants = [{}]
+        if metric in ("minkowski", "lp"):
+            variants = [{}, {"p": V(3.0)}, {"p": V(1.0)}]
+        elif metric == "wminkowski":
+            ts = dict(ts, w=w)
+            variants = [{"w": T("w")}, {"w": T("w"), "p": V(3.0)}]
+        elif metric == "seuclidean":
+            ts = dict(ts, V=w)
+            variants = [{"V": T("V")}]
+        elif metric == "mahalanobis":
+            ts = dict(ts, VI=VI)
+            variants = [{"VI": T("VI")}]
+        elif metric == "jensenshannon":
+            variants = [{}, {"base": V(2.0)}]
+        elif metric == "directed_hausdorff":
+            variants = [{}, {"shuffle": V(False)}]
+        for kw in variants:
+            out.append(({"op": "cdist", "args": [T("a"), T("b"), V(metric)], "kwargs": kw, "req": []}, ts, exact))
+        bad = {"base": V(2.0)} if metric != "jensenshannon" else {"p": V(2.0)}
+        out.append(({"op": "cdist", "args": [T("a"), T("b"), V(metric)], "kwargs": dict(variants[0], **bad), "req": []},
+                    ts, True))
+    return out

@@ -759,3 +759,31 @@ def test_public_ops_dtypes_gpu_equal_reference(tmp_path):
         except AssertionError as e:
             failures.append(str(e).splitlines()[0][:300])
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures[:30])
+
+
+def test_cdist_names_gpu_equal_reference(tmp_path):
+    """cdist(metric=...) on GPU tensors for every metric name of the reference's dispatcher
+    (with its extra arguments, defaults and a refused argument) against the reference's compiled
+    CPU library: values rtol 1e-5 (+ 1e-5 * max), boolean metrics and Hausdorff bit for bit,
+    the same TypeError texts."""
+    from oracle import ref_runner
+    from tests._public_cases import cdist_name_cases
+    from tests.test_reference_pin import _assert_results_close
+
+    if not ref_runner.available():
+        pytest.skip("oracle/_ref not built")
+    cs = cdist_name_cases()
+    ref = ref_runner.run_op_reference([(c, t) for c, t, _ in cs], tmp_path)
+    ops = torch.ops.torchpairwise
+    failures = []
+    for (case, t, exact), r in zip(cs, ref):
+        what = f"cdist {case['args'][2]['v']} {sorted(case['kwargs'])}"
+        ours = ref_runner.run_op_case(ops, case, t, DEV)
+        keys = tuple(k for k in r if k != "err") if exact else ()
+        if case["args"][2]["v"] == "russellrao":
+            keys = ()  # (D - and) / D: the GPU route's division is 1 ulp from the CPU's
+        try:
+            _assert_results_close(ours, r, 1e-5, what, keys)
+        except AssertionError as e:
+            failures.append(str(e).splitlines()[0][:300])
+    assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)

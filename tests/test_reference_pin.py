@@ -230,3 +230,25 @@ def test_public_ops_dtypes_cpu_equal_reference(tmp_path):
         except AssertionError as e:
             failures.append(str(e).splitlines()[0][:300])
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures[:30])
+
+
+def test_cdist_names_cpu_equal_reference(tmp_path):
+    """cdist(metric=...) for every metric name of the reference's dispatcher, with its extra
+    arguments and defaults, and with an argument it does not take: the same values (boolean
+    metrics and Hausdorff bit for bit) or the same TypeError."""
+    from tests._public_cases import cdist_name_cases
+
+    import torchpairwise_amd  # noqa: F401
+
+    cs = cdist_name_cases()
+    ref = ref_runner.run_op_reference([(c, t) for c, t, _ in cs], tmp_path)
+    ops = torch.ops.torchpairwise
+    failures = []
+    for (case, t, exact), r in zip(cs, ref):
+        what = f"cdist {case['args'][2]['v']} {sorted(case['kwargs'])}"
+        ours = ref_runner.run_op_case(ops, case, t, "cpu")
+        try:
+            _assert_results_close(ours, r, 1e-5, what, tuple(k for k in r if k != "err") if exact else ())
+        except AssertionError as e:
+            failures.append(str(e).splitlines()[0][:300])
+    assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)

@@ -520,7 +520,10 @@ const CdistMetric kCdistMetrics[] = {
     TPW_METRIC(correlation, 0, correlation_distances(x1, x2)),
     TPW_METRIC(hamming, 0, hamming_distances(x1, x2)),
     TPW_METRIC(jaccard, 0, jaccard_distances(x1, x2)),
-    TPW_METRIC(kulsinski, 0, kulsinski_distances(x1, x2)),
+    // kept from the reference: its C++ kulsinski_distances, which cdist calls, forwards to the
+    // kulczynski1 functor (pairwise_metrics.h:557-561), so cdist(metric="kulsinski") gives
+    // kulczynski1 distances (and no deprecation warning); the kulsinski_distances op does not
+    TPW_METRIC(kulsinski, 0, kulczynski1_distances(x1, x2)),
     TPW_METRIC(kulczynski1, 0, kulczynski1_distances(x1, x2)),
     TPW_METRIC(seuclidean, kV, seuclidean_distances(x1, x2, a.V)),
     TPW_METRIC(cityblock, 0, cityblock_distances(x1, x2)),

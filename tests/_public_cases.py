@@ -184,3 +184,61 @@ def cdist_name_cases():
         out.append(({"op": "cdist", "args": [T("a"), T("b"), V(metric)], "kwargs": dict(variants[0], **bad), "req": []},
                     ts, True))
     return out
+
+
+def _margin_eps(d, q):
+    """A radius between two consecutive sorted distances near quantile q whose gap is wide
+    (relative 1e-3), so no device's rounding moves a distance across it."""
+    v = torch.sort(d.flatten().double()).values
+    i0 = int(q * (v.numel() - 1))
+    for off in range(v.numel()):
+        for i in (i0 + off, i0 - off):
+            if 0 <= i < v.numel() - 1 and v[i + 1] - v[i] > 1e-3 * max(1.0, float(v[i].abs())):
+                return float((v[i] + v[i + 1]) / 2)
+    return float(v[-1]) + 1.0
+
+
+def neighbour_cases():
+    """[(case, tensors)] of k_neighbors_mask / radius_neighbors_mask over metrics and their
+    extra arguments, k from 0 past the column count, x2 = None, and the error paths.  Inputs
+    are tie-free random points (the reference's argsort is unstable on ties); radii sit in wide
+    gaps between distances."""
+    import torchpairwise_amd as tp  # the CPU route (at::cdist and this build's CPU loops)
+
+    a = torch.randn(37, 16, generator=_g(51))
+    b = torch.randn(29, 16, generator=_g(52))
+    pa, pb = torch.rand(37, 16, generator=_g(53)) + 0.05, torch.rand(29, 16, generator=_g(54)) + 0.05
+    la, lb = torch.rand(37, 2, generator=_g(55)) * 2 - 1, torch.rand(29, 2, generator=_g(56)) * 2 - 1
+    ba, bb = torch.rand(37, 70, generator=_g(57)) < 0.3, torch.rand(29, 70, generator=_g(58)) < 0.3
+    w = torch.rand(16, generator=_g(59)) + 0.2
+    VI = torch.eye(16) + 0.1 * torch.ones(16, 16)
+    T = lambda name: {"t": name}  # noqa: E731
+    V = lambda v: {"v": v}  # noqa: E731
+    metrics = [("euclidean", {}, "f"), ("manhattan", {}, "f"), ("cosine", {}, "f"), ("chebyshev", {}, "f"),
+               ("minkowski", {"p": V(3.0)}, "f"), ("sqeuclidean", {}, "f"), ("correlation", {}, "f"),
+               ("canberra", {}, "f"), ("braycurtis", {}, "f"), ("wminkowski", {"w": T("w"), "p": V(3.0)}, "f"),
+               ("seuclidean", {"V": T("w")}, "f"), ("mahalanobis", {"VI": T("VI")}, "f"),
+               ("haversine", {}, "l"), ("jensenshannon", {}, "p"), ("jaccard", {}, "b"), ("hamming", {}, "b")]
+    out = []
+    for metric, kw, kind in metrics:
+        x1, x2 = {"f": (a, b), "p": (pa, pb), "l": (la, lb), "b": (ba, bb)}[kind]
+        ts = {"a": x1, "b": x2, "w": w, "VI": VI}
+        extra = {"w": w, "V": w, "VI": VI, "p": 3.0}
+        d = tp.cdist(x1, x2, metric, **{k: extra[k] for k in kw})
+        for q in (0.1, 0.6):
+            out.append(({"op": "radius_neighbors_mask", "args": [T("a"), T("b"), V(_margin_eps(d, q)), V(metric)],
+                         "kwargs": kw, "req": []}, ts))
+        if kind == "b":
+            continue  # many equal distances: the reference's argsort order is unspecified there
+        for k in (0, 1, 4, 40):
+            out.append(({"op": "k_neighbors_mask", "args": [T("a"), T("b"), V(k), V(metric)], "kwargs": kw,
+                         "req": []}, ts))
+    ts = {"a": a, "b": b}
+    out.append(({"op": "k_neighbors_mask", "args": [T("a")], "kwargs": {"k": V(2)}, "req": []}, ts))
+    out.append(({"op": "radius_neighbors_mask", "args": [T("a")], "kwargs": {"epsilon": V(5.0)}, "req": []}, ts))
+    for case in (("k_neighbors_mask", [T("a"), T("b"), V(-1)]), ("radius_neighbors_mask", [T("a"), T("b"), V(-1.0)]),
+                 ("k_neighbors_mask", [T("a"), T("b"), V(1), V("nope")]),
+                 ("radius_neighbors_mask", [T("a"), T("b"), V(1.0), V("euclidean")])):
+        kw = {"p": V(2.0)} if case[1][-1] == V("euclidean") else {}
+        out.append(({"op": case[0], "args": case[1], "kwargs": kw, "req": []}, ts))
+    return out

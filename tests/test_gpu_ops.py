@@ -787,3 +787,28 @@ def test_cdist_names_gpu_equal_reference(tmp_path):
         except AssertionError as e:
             failures.append(str(e).splitlines()[0][:300])
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)
+
+
+def test_neighbour_masks_gpu_equal_reference(tmp_path):
+    """k_neighbors_mask / radius_neighbors_mask on GPU tensors over metrics, extra arguments,
+    k up to past the column count, x2 = None and the error paths, against the reference's
+    compiled CPU library bit for bit (the cases keep the selection boundaries and radii away
+    from near-equal distances, so device rounding cannot move them)."""
+    from oracle import ref_runner
+    from tests._public_cases import neighbour_cases
+    from tests.test_reference_pin import _assert_results_close
+
+    if not ref_runner.available():
+        pytest.skip("oracle/_ref not built")
+    cs = neighbour_cases()
+    ref = ref_runner.run_op_reference(cs, tmp_path)
+    ops = torch.ops.torchpairwise
+    failures = []
+    for (case, t), r in zip(cs, ref):
+        what = f"{case['op']} {case['args'][2:]} {sorted(case['kwargs'])}"
+        try:
+            _assert_results_close(ref_runner.run_op_case(ops, case, t, DEV), r, 0.0, what,
+                                  tuple(k for k in r if k != "err"))
+        except AssertionError as e:
+            failures.append(str(e).splitlines()[0][:300])
+    assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)

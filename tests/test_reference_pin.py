@@ -252,3 +252,25 @@ def test_cdist_names_cpu_equal_reference(tmp_path):
         except AssertionError as e:
             failures.append(str(e).splitlines()[0][:300])
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)
+
+
+def test_neighbour_masks_cpu_equal_reference(tmp_path):
+    """k_neighbors_mask / radius_neighbors_mask on CPU tensors over metrics, extra arguments,
+    k up to past the column count, x2 = None and the error paths: bit for bit (or the same
+    error) against the reference's compiled library."""
+    from tests._public_cases import neighbour_cases
+
+    import torchpairwise_amd  # noqa: F401
+
+    cs = neighbour_cases()
+    ref = ref_runner.run_op_reference(cs, tmp_path)
+    ops = torch.ops.torchpairwise
+    failures = []
+    for (case, t), r in zip(cs, ref):
+        what = f"{case['op']} {case['args'][2:]} {sorted(case['kwargs'])}"
+        try:
+            _assert_results_close(ref_runner.run_op_case(ops, case, t, "cpu"), r, 0.0, what,
+                                  tuple(k for k in r if k != "err"))
+        except AssertionError as e:
+            failures.append(str(e).splitlines()[0][:300])
+    assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)

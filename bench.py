@@ -416,8 +416,17 @@ def run_config(cfg, steps, warmup):
                   "hbm_frac": 5.0 * N * N / (ms * 1e-3) / PEAK_HBM,
                   **roof("hbm", 5.0 * N * N, ms, "each fp32 distance read once, one mask byte written")})
         conv = "distances written and read once (4 + 4 B per entry) and one mask byte written"
-        ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, 1), steps, warmup)
-        emit("k_neighbors_mask k=1 (euclidean + selection)", ms, pf, roof("hbm", 9.0 * N * N, ms, conv))
+        # k + 1 <= 16: the tile kernel keeps each row's candidates per tile (no distance matrix),
+        # bound by the fp32 products like the radius mask; beside it the unfused route
+        # (distances, then the selection kernel) at the same k
+        for k in (1, 3):
+            ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, k), steps, warmup)
+            emit(f"k_neighbors_mask k={k} (euclidean, fused candidates + select)", ms, pf,
+                 roof("mfma", 2.0 * N * N * D, ms, "2 flop per pair-feature on fp32 MFMA"))
+            ms, _ = time_op(lambda: torch.ops.torchpairwise._row_smallest_mask(tp.euclidean_distances(x1, x2), k + 1),
+                            steps, warmup)
+            emit(f"k_neighbors_mask k={k} unfused (euclidean distances + selection)", ms, pf,
+                 roof("hbm", 9.0 * N * N, ms, conv))
         ms, _ = time_op(lambda: tp.k_neighbors_mask(x1, x2, 16), steps, warmup)
         emit("k_neighbors_mask k=16 (euclidean + selection)", ms, pf, roof("hbm", 9.0 * N * N, ms, conv))
         # the radius mask comes straight from the tile kernel's epilogue (no distance matrix,

@@ -652,6 +652,24 @@ int tpw_radius_mask_euclidean(const void *x1, const void *x2, int dtype, int64_t
                               int64_t n, int64_t m, int64_t d, const float *aux1,
                               const float *aux2, float eps, uint8_t *out, void *stream);
 
+/* k_neighbors_mask with the euclidean metric without the distance matrix: mask [n, m] (bool
+ * bytes) = 1 at each row's `count` smallest distances between x1 [n, d] and x2 [m, d] (float32 or
+ * bfloat16; aux1 / aux2 the squared row norms as for TPW_EPI_EUCLIDEAN), in the order of
+ * tpw_row_smallest_mask (ascending, -0 == +0, NaN after +inf, ties to the lower column) over the
+ * distances the euclidean op stores (bfloat16: rounded to bfloat16), so the mask equals that of
+ * tpw_pairwise_inner (TPW_EPI_EUCLIDEAN) followed by tpw_row_smallest_mask bit for bit.  The
+ * tile kernel keeps each row's C >= count smallest (distance, column) keys per 128 columns in
+ * the workspace (tpw_knn_mask_workspace_size bytes, 16-byte aligned); a select kernel merges
+ * them and writes the mask rows.  Sizes: tpw_knn_mask_euclidean_supported (count 1..16 and <= m,
+ * m a multiple of 16, d * element size a multiple of 128 bytes); inputs and mask 16-byte aligned.
+ * Replaces cdist + argsort + index_put_ of k_neighbors_mask (torchpairwise/csrc/ops/
+ * neighbors.cpp:10-35) for the euclidean metric. */
+int tpw_knn_mask_euclidean_supported(int dtype, int64_t n, int64_t m, int64_t d, int64_t count);
+size_t tpw_knn_mask_workspace_size(int64_t n, int64_t m, int64_t count);
+int tpw_knn_mask_euclidean(const void *x1, const void *x2, int dtype, int64_t n, int64_t m, int64_t d,
+                           const float *aux1, const float *aux2, int64_t count, uint8_t *mask,
+                           void *workspace, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -812,3 +812,44 @@ def test_neighbour_masks_gpu_equal_reference(tmp_path):
         except AssertionError as e:
             failures.append(str(e).splitlines()[0][:300])
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,m,d,kind", [(300, 256, 64, "randn"), (257, 272, 128, "ints"), (40, 48, 64, "randn"),
+                                        (600, 1008, 256, "randn"), (304, None, 64, "ints"), (130, 144, 64, "ties")])
+def test_knn_mask_fused_equals_distances_then_selection(dtype, n, m, d, kind):
+    """tpw_knn_mask_euclidean (per-tile candidates + select) against the euclidean distances
+    followed by tpw_row_smallest_mask, bit for bit, for every candidate width (count 1 .. 16),
+    edge tiles, integer inputs with many equal distances (ties go to the lower column), x2 = x1
+    (zero diagonal) and bf16 (distances rounded as stored)."""
+    from torchpairwise_amd import _capi as capi
+
+    g = torch.Generator().manual_seed(n + d)
+    if kind == "randn":
+        x1 = torch.randn(n, d, generator=g)
+    elif kind == "ints":
+        x1 = torch.randint(-2, 3, (n, d), generator=g).float()
+    else:  # a few distinct points repeated: whole rows of equal distances
+        x1 = torch.randint(-1, 2, (4, d), generator=g).float()[torch.randint(0, 4, (n,), generator=g)]
+    x2 = x1 if m is None else (torch.randn(m, d, generator=g) if kind == "randn"
+                               else torch.randint(-2, 3, (m, d), generator=g).float())
+    a = x1.to(DEV, dtype)
+    b = a if m is None else x2.to(DEV, dtype)
+    dist = capi.pairwise_inner(a, b, capi.EPI_EUCLIDEAN)
+    for count in (1, 2, 3, 4, 5, 8, 9, 16):
+        print(f"{dtype} {n} {m} {d} {kind} count={count}", flush=True)
+        got = capi.knn_mask_euclidean(a, b, count)
+        want = capi.row_smallest_mask(dist, count)
+        assert got.sum(1).eq(count).all(), "count per row"
+        assert torch.equal(got, want), f"count={count}: {(got != want).sum().item()} entries differ"
+
+
+def test_knn_mask_op_routes_fused():
+    """k_neighbors_mask on a GPU euclidean case the fused route takes gives the mask of the
+    distances-then-selection route, and k + 1 past the fused limit still works."""
+    g = torch.Generator().manual_seed(5)
+    x1, x2 = torch.randn(300, 64, generator=g).to(DEV), torch.randn(256, 64, generator=g).to(DEV)
+    dist = tp.euclidean_distances(x1, x2)
+    for k in (0, 1, 3, 15, 16, 40):
+        got = tp.k_neighbors_mask(x1, x2, k)
+        assert torch.equal(got, torch.ops.torchpairwise._row_smallest_mask(dist, k + 1)), f"k={k}"

@@ -85,6 +85,9 @@ _SIGNATURES = {
     "tpw_haversine_workspace_size": (_sz, [_i64, _i64, _i64]),
     "tpw_haversine": (_i, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "tpw_haversine_backward": (_i, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "tpw_knn_mask_euclidean_supported": (_i, [_i, _i64, _i64, _i64, _i64]),
+    "tpw_knn_mask_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "tpw_knn_mask_euclidean": (_i, [_p, _p, _i, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p]),
     "tpw_pairwise_binary": (_i, [_p, _p, _i, _i, _i64, _i64, _i64, _i64, _p, _p]),
     "tpw_family_f64": (_i, [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
     "tpw_family_f64_backward_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64, _d]),
@@ -566,6 +569,21 @@ def directed_hausdorff_backward(grad, x1, x2, out, idx1, idx2):
     if x1.dim() == 3:
         return gx1[0], gx2[0]
     return gx1, gx2
+
+
+def knn_mask_euclidean(x1, x2, count):
+    """tpw_knn_mask_euclidean on [n, d] x [m, d] float32 / bfloat16 -> bool mask [n, m]."""
+    import torch
+
+    a, b = x1.contiguous(), x2.contiguous()
+    n, d = a.shape
+    m = b.shape[0]
+    n1, n2 = row_norms(a, True), row_norms(b, True)
+    mask = torch.empty((n, m), dtype=torch.bool, device=a.device)
+    ws = torch.empty((lib().tpw_knn_mask_workspace_size(n, m, count),), dtype=torch.uint8, device=a.device)
+    call("tpw_knn_mask_euclidean", _ptr(a), _ptr(b), _dtype_code(a), n, m, d, _ptr(n1), _ptr(n2), count,
+         _ptr(mask), _ptr(ws), _stream())
+    return mask
 
 
 def row_smallest_mask(dist, count):

@@ -62,13 +62,24 @@ constexpr int kEpiGradA = 103;
 // (kEpiRadiusB: rounded to bf16), compared with kp.eps: 1 when d <= eps (NaN: 0), as bool bytes.
 constexpr int kEpiRadius = 104;
 constexpr int kEpiRadiusB = 105;
+// k_neighbors_mask (euclidean): per output row, the C smallest (distance, column) keys among the
+// tile's 128 columns, written as candidates instead of the distances (topk_tile_epilogue).
+// EPI = kEpiTopK + 2 log2(C / 2) for C = 2, 4, 8, 16, + 1 when the distance is first rounded to
+// bf16, as the bf16 distance op stores it.
+constexpr int kEpiTopK = 106;
+template <int EPI>
+constexpr bool kTopK = EPI >= kEpiTopK && EPI < kEpiTopK + 8;
+template <int EPI>
+constexpr int kTopKC = 2 << ((EPI - kEpiTopK) >> 1);
+template <int EPI>
+constexpr bool kTopKB = ((EPI - kEpiTopK) & 1) != 0;
 
 // Row / column norms read by the epilogue (aux1 also carries the gradient coefficients).
 template <int EPI>
 constexpr bool kAux1 = EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN ||
                        EPI == TPW_EPI_COSINE_SIM || EPI == TPW_EPI_COSINE_DIST ||
                        EPI == TPW_EPI_CORRELATION || EPI == kEpiGrad || EPI == kEpiRadius ||
-                       EPI == kEpiRadiusB;
+                       EPI == kEpiRadiusB || kTopK<EPI>;
 template <int EPI>
 constexpr bool kAux2 = kAux1<EPI> && EPI != kEpiGrad;
 
@@ -111,6 +122,47 @@ __device__ __forceinline__ float epilogue(float s, float a1, float a2, const Ker
         if constexpr (EPI == TPW_EPI_CORRELATION) return v;
         return fminf(fmaxf(v, 0.0f), 2.0f);
     }
+}
+
+// Selection order of the neighbour masks: ascending distance (distances are >= 0 or -0; -0 ==
+// +0, NaN after +inf), then ascending column.  Columns past the edge take the largest key.
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t col) {
+    const uint32_t bits = v != v ? 0xffffffffu : (__float_as_uint(v) & 0x7fffffffu);
+    return ((uint64_t)bits << 32) | col;
+}
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, mask, 64), hi = __shfl_xor((uint32_t)(v >> 32), mask, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+// x into the ascending list L, the largest falling off (a compare-exchange chain).
+template <int C>
+__device__ __forceinline__ void topk_insert(uint64_t (&L)[C], uint64_t x) {
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        const bool lt = x < L[i];
+        const uint64_t lo = lt ? x : L[i];
+        x = lt ? L[i] : x;
+        L[i] = lo;
+    }
+}
+// L := the C smallest of the ascending lists L and R, ascending: the element-wise minimum of L
+// and reversed R is bitonic, and a bitonic merge network sorts it.
+template <int C>
+__device__ __forceinline__ void topk_merge(uint64_t (&L)[C], const uint64_t (&R)[C]) {
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        const uint64_t r = R[C - 1 - i];
+        L[i] = r < L[i] ? r : L[i];
+    }
+#pragma unroll
+    for (int j = C / 2; j > 0; j >>= 1)
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            if ((i & j) == 0) {
+                const uint64_t a = L[i], c = L[i + j];
+                L[i] = a < c ? a : c;
+                L[i + j] = a < c ? c : a;
+            }
 }
 
 __device__ __forceinline__ void store_out(float *p, float v) { store_nt(p, v); }
@@ -505,6 +557,60 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
         a1v[mi] = EPI == kEpiGradA ? rsum[mi] + __shfl_xor(rsum[mi], 32, 64)  // both K halves
                   : kAux1<EPI>     ? s_aux[wr + mi * 32 + l32]
                                    : 0.0f;
+    if constexpr (kTopK<EPI>) {
+        // k-neighbour candidates: per row block mi, each lane keeps the C smallest keys of its 32
+        // columns, merges with the lane holding the row's other 32 columns of this wave (lane ^
+        // 32), and lanes 0-31 leave the list in LDS; then one thread per tile row merges the two
+        // waves' lists and writes the tile's C candidates of that row, out[row][tc][0 .. C - 1].
+        constexpr int C = kTopKC<EPI>;
+        uint64_t *st = reinterpret_cast<uint64_t *>(smem);  // [2 waves][128 rows][C]: <= 32 KiB
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+            uint64_t L[C];
+#pragma unroll
+            for (int i = 0; i < C; ++i) L[i] = ~0ull;
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const floatx4 a2 = *reinterpret_cast<const floatx4 *>(&s_aux[kT + wc + ni * 32 + 8 * g + 4 * h]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float v = epilogue<TPW_EPI_EUCLIDEAN>(acc[mi][ni][4 * g + e], a1v[mi], a2[e], kp);
+                        if constexpr (kTopKB<EPI>) v = bf16_to_f32(f32_to_bf16_rne(v));
+                        const int64_t col = col0 + wc + ni * 32 + 8 * g + 4 * h + e;
+                        topk_insert<C>(L, col < m ? topk_key(v, (uint32_t)col) : ~0ull);
+                    }
+                }
+            uint64_t R[C];
+#pragma unroll
+            for (int i = 0; i < C; ++i) R[i] = shfl_xor64(L[i], 32);
+            topk_merge<C>(L, R);
+            if (h == 0) {
+#pragma unroll
+                for (int i = 0; i < C; ++i) st[((wc >> 6) * kT + wr + mi * 32 + l32) * C + i] = L[i];
+            }
+        }
+        barrier_lds();
+        if (tid < kT) {
+            uint64_t L[C], R[C];
+#pragma unroll
+            for (int i = 0; i < C; ++i) {
+                L[i] = st[tid * C + i];
+                R[i] = st[(kT + tid) * C + i];
+            }
+            topk_merge<C>(L, R);
+            const int64_t row = row0 + tid;
+            if (row < n) {
+                uint4 *dst = reinterpret_cast<uint4 *>(reinterpret_cast<uint64_t *>(out) + ((b * n + row) * tiles_m + tc) * C);
+#pragma unroll
+                for (int i = 0; i < C; i += 2)
+                    dst[i / 2] = make_uint4((uint32_t)L[i], (uint32_t)(L[i] >> 32), (uint32_t)L[i + 1],
+                                            (uint32_t)(L[i + 1] >> 32));
+            }
+        }
+        return;
+    } else {
     store_tile<OutT>(
         smem,
         [&](int mi, int ni, int g) {
@@ -535,6 +641,7 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
             return o;
         },
         out, b, row0, col0, n, m);
+    }
 }
 
 // Row norms: one wave per row, lanes stride over the features.
@@ -648,6 +755,93 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
     hipLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(kThreads), 0, s, x1, x2, n, m, d, aux1,
                        aux2, out, tiles_n, tiles_m, total, X, sign, kp);
     return check_launch("pairwise_inner_kernel");
+}
+
+// Each row's `count` smallest of its tiles' candidate keys (cand [n][tiles_m][C], ascending per
+// tile) -> its bool mask row (mask [n, m], m a multiple of 16): one wave per row; every lane
+// keeps the C smallest of its share, a butterfly of merges gives every lane the row's C
+// smallest, and the lanes write the row in 16-byte units with 1 at the first `count` columns.
+template <int C>
+__global__ __launch_bounds__(256) void topk_select_kernel(const uint64_t *__restrict__ cand, int64_t n,
+                                                          int64_t tiles_m, int64_t m, int count,
+                                                          uint8_t *__restrict__ mask) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= n) return;  // the whole wave
+    const uint64_t *c = cand + row * tiles_m * C;
+    const int64_t total = tiles_m * C;
+    uint64_t L[C], R[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) L[i] = ~0ull;
+    for (int64_t i = lane; i < total; i += 64) topk_insert<C>(L, c[i]);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+        for (int i = 0; i < C; ++i) R[i] = shfl_xor64(L[i], off);
+        topk_merge<C>(L, R);
+    }
+    uint32_t sel[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) sel[i] = i < count ? (uint32_t)L[i] : 0xffffffffu;
+    uint8_t *mrow = mask + row * m;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    for (int64_t u = lane; u < m / 16; u += 64) {
+        uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            const uint32_t col = sel[i];
+            if ((int64_t)(col >> 4) == u) {
+                const uint32_t byte = col & 15, bit = 1u << (8 * (byte & 3));
+                w0 |= (byte >> 2) == 0 ? bit : 0u;
+                w1 |= (byte >> 2) == 1 ? bit : 0u;
+                w2 |= (byte >> 2) == 2 ? bit : 0u;
+                w3 |= (byte >> 2) == 3 ? bit : 0u;
+            }
+        }
+        const u32x4 v = {w0, w1, w2, w3};
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(mrow + 16 * u));
+    }
+}
+
+int topk_width(int64_t count) { return count <= 2 ? 2 : count <= 4 ? 4 : count <= 8 ? 8 : 16; }
+
+bool knn_fits(int dtype, int64_t n, int64_t m, int64_t d, int64_t count) {
+    const int64_t es = dtype == TPW_F32 ? 4 : 2;
+    const int64_t big = n > m ? n : m;
+    return (dtype == TPW_F32 || dtype == TPW_BF16) && count >= 1 && count <= 16 && count <= m && m % 16 == 0 &&
+           d > 0 && (d * es) % 128 == 0 && big * d < ((int64_t)1 << 31) && big * d * es < ((int64_t)1 << 32) &&
+           cdiv(n, kTile) * cdiv(m, kTile) <= 0x7fffffffLL;
+}
+
+template <typename T, int EPI>
+int launch_topk(const T *x1, const T *x2, int64_t n, int64_t m, int64_t d, const float *aux1, const float *aux2,
+                int count, uint64_t *cand, uint8_t *mask, hipStream_t s) {
+    constexpr int C = kTopKC<EPI>;
+    const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile), total = tiles_n * tiles_m;
+    // C >= 8: the lists need the two-blocks-per-CU register budget (at four they spill)
+    if (C >= 8 || d * (int64_t)sizeof(T) >= 16 * 128) {
+        hipLaunchKernelGGL((inner_tile_kernel<T, uint64_t, EPI, 2>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                           s, x1, x2, n, m, d, aux1, aux2, cand, tiles_n, tiles_m, total, KerParams{}, nullptr, 1.0f);
+    } else if constexpr (C < 8) {
+        hipLaunchKernelGGL((inner_tile_kernel<T, uint64_t, EPI, 1>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                           s, x1, x2, n, m, d, aux1, aux2, cand, tiles_n, tiles_m, total, KerParams{}, nullptr, 1.0f);
+    }
+    int rc = check_launch("inner_tile_kernel");
+    if (rc != TPW_OK) return rc;
+    hipLaunchKernelGGL(topk_select_kernel<C>, dim3((unsigned)cdiv(n, 4)), dim3(256), 0, s, cand, n, tiles_m, m, count,
+                       mask);
+    return check_launch("topk_select_kernel");
+}
+
+template <typename T, bool BF>
+int dispatch_topk(const T *x1, const T *x2, int64_t n, int64_t m, int64_t d, const float *aux1, const float *aux2,
+                  int count, uint64_t *cand, uint8_t *mask, hipStream_t s) {
+    switch (topk_width(count)) {
+        case 2: return launch_topk<T, kEpiTopK + BF>(x1, x2, n, m, d, aux1, aux2, count, cand, mask, s);
+        case 4: return launch_topk<T, kEpiTopK + 2 + BF>(x1, x2, n, m, d, aux1, aux2, count, cand, mask, s);
+        case 8: return launch_topk<T, kEpiTopK + 4 + BF>(x1, x2, n, m, d, aux1, aux2, count, cand, mask, s);
+        default: return launch_topk<T, kEpiTopK + 6 + BF>(x1, x2, n, m, d, aux1, aux2, count, cand, mask, s);
+    }
 }
 
 template <typename T>
@@ -808,6 +1002,33 @@ extern "C" int tpw_radius_mask_euclidean(const void *x1, const void *x2, int dty
     return launch_inner<uint16_t, kEpiRadiusB, uint8_t>(static_cast<const uint16_t *>(x1),
                                                          static_cast<const uint16_t *>(x2), batch, n, m, d, aux1,
                                                          aux2, out, s, nullptr, 1.0f, kp);
+}
+
+extern "C" int tpw_knn_mask_euclidean_supported(int dtype, int64_t n, int64_t m, int64_t d, int64_t count) {
+    return n >= 0 && knn_fits(dtype, n, m, d, count) ? 1 : 0;
+}
+
+extern "C" size_t tpw_knn_mask_workspace_size(int64_t n, int64_t m, int64_t count) {
+    return (size_t)(n * cdiv(m, kTile) * topk_width(count)) * sizeof(uint64_t) + 256;
+}
+
+extern "C" int tpw_knn_mask_euclidean(const void *x1, const void *x2, int dtype, int64_t n, int64_t m, int64_t d,
+                                      const float *aux1, const float *aux2, int64_t count, uint8_t *mask,
+                                      void *workspace, void *stream) {
+    TPW_REQUIRE(n >= 0 && m >= 0 && d >= 0, "invalid sizes");
+    if (n == 0) return TPW_OK;
+    TPW_REQUIRE(knn_fits(dtype, n, m, d, count),
+                "unsupported case (dtype %d, n %lld, m %lld, d %lld, count %lld): see "
+                "tpw_knn_mask_euclidean_supported", dtype, (long long)n, (long long)m, (long long)d, (long long)count);
+    TPW_REQUIRE(x1 && x2 && aux1 && aux2 && mask && workspace, "null pointer");
+    TPW_REQUIRE(aligned16(x1) && aligned16(x2) && aligned16(mask) && aligned16(workspace), "16-byte alignment required");
+    hipStream_t s = as_stream(stream);
+    uint64_t *cand = static_cast<uint64_t *>(workspace);
+    if (dtype == TPW_F32)
+        return dispatch_topk<float, false>(static_cast<const float *>(x1), static_cast<const float *>(x2), n, m, d,
+                                           aux1, aux2, (int)count, cand, mask, s);
+    return dispatch_topk<uint16_t, true>(static_cast<const uint16_t *>(x1), static_cast<const uint16_t *>(x2), n, m,
+                                         d, aux1, aux2, (int)count, cand, mask, s);
 }
 
 extern "C" int tpw_pairwise_kernel(const void *x1, const void *x2, int dtype, int64_t batch,

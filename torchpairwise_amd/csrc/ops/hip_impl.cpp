@@ -53,6 +53,35 @@ at::Tensor radius_mask_euclidean_cuda(const at::Tensor &x1, const at::Tensor &x2
     return out_shape(out, x1);
 }
 
+// k_neighbors_mask (euclidean) without the distance matrix: the tile kernel's per-tile candidates
+// and a select pass (tpw_knn_mask_euclidean); the same mask as the distances followed by
+// _row_smallest_mask.
+at::Tensor knn_mask_euclidean_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t count) {
+    check_cuda_pair("_knn_mask_euclidean", x1, x2);
+    TORCH_CHECK(x1.dim() == 2 && x2.dim() == 2, "_knn_mask_euclidean: expected 2-D inputs");
+    TORCH_CHECK(x1.scalar_type() == x2.scalar_type(), "_knn_mask_euclidean: x1 and x2 dtypes differ");
+    const int dt = float_dtype("_knn_mask_euclidean", x1);
+    DeviceGuard guard(x1.device());
+    auto a = x1.contiguous(), b = x2.contiguous();
+    const int64_t n = a.size(0), m = b.size(0), d = a.size(1);
+    TORCH_CHECK(tpw_knn_mask_euclidean_supported(dt, n, m, d, count),
+                "_knn_mask_euclidean: unsupported sizes (n ", n, ", m ", m, ", d ", d, ", count ", count, ")");
+    auto mask = at::empty({n, m}, a.options().dtype(at::kBool));
+    void *s = current_stream();
+    auto n1 = at::empty({n}, a.options().dtype(at::kFloat));
+    check_rc(tpw_row_norms(a.data_ptr(), dt, n, d, 1, n1.data_ptr<float>(), s), "row norms");
+    at::Tensor n2 = n1;
+    if (!x2.is_same(x1)) {
+        n2 = at::empty({m}, a.options().dtype(at::kFloat));
+        check_rc(tpw_row_norms(b.data_ptr(), dt, m, d, 1, n2.data_ptr<float>(), s), "row norms");
+    }
+    auto ws = workspace(tpw_knn_mask_workspace_size(n, m, count), a);
+    check_rc(tpw_knn_mask_euclidean(a.data_ptr(), b.data_ptr(), dt, n, m, d, n1.data_ptr<float>(), n2.data_ptr<float>(),
+                                    count, reinterpret_cast<uint8_t *>(mask.data_ptr<bool>()), ws.data_ptr(), s),
+             "_knn_mask_euclidean");
+    return mask;
+}
+
 at::Tensor pw_inner_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t epilogue) {
     check_cuda_pair("_pw_inner", x1, x2);
     TORCH_CHECK(x1.scalar_type() == x2.scalar_type(), "_pw_inner: x1 and x2 dtypes differ");
@@ -508,6 +537,7 @@ at::Tensor pw_binary_cuda(const at::Tensor &x1, const at::Tensor &x2) {
 TORCH_LIBRARY_IMPL(torchpairwise, CUDA, m) {
     m.impl("_pw_inner", TORCH_FN(pw_inner_cuda));
     m.impl("_radius_mask_euclidean", TORCH_FN(radius_mask_euclidean_cuda));
+    m.impl("_knn_mask_euclidean", TORCH_FN(knn_mask_euclidean_cuda));
     m.impl("_pw_inner_backward", TORCH_FN(pw_inner_backward_cuda));
     m.impl("_pw_kernel", TORCH_FN(pw_kernel_cuda));
     m.impl("_pw_kernel_backward", TORCH_FN(pw_kernel_backward_cuda));

@@ -202,3 +202,39 @@ def test_c5_directed_hausdorff():
     gx1, gx2 = P.directed_hausdorff_backward(np.ones((16, 16), np.float32), c1, c2, o, m_, n_)
     assert_equal(a.grad.cpu(), torch.from_numpy(gx1), "grad_x1")
     assert_equal(b.grad.cpu(), torch.from_numpy(gx2), "grad_x2")
+
+
+@pytest.mark.parametrize("name,kw,dtype", [("polynomial_kernel", {"degree": 3, "gamma": 0.01, "coef0": 0.5}, torch.float32),
+                                           ("sigmoid_kernel", {"gamma": 0.01, "coef0": 0.1}, torch.float32),
+                                           ("sigmoid_kernel", {"gamma": 0.01, "coef0": 0.1}, torch.bfloat16)])
+def test_kernel_function_backward_fused_grid(name, kw, dtype):
+    """The kernel functions' backward where the fused weight + grad_x1 kernel runs (its grid
+    and the grad_x2 product's fill the GPU: n 16384, m 8192, d 1024): gradients of 48 sampled
+    rows of x1 and columns of x2 against the reference's formulas in float64 (the weights from
+    S = x1 x2^T, gamma and coef0; polynomial: degree gamma base^(degree-1), sigmoid:
+    gamma (1 - tanh(base)^2)).  fp32 rtol 1e-4, bf16 2e-2 (each + rtol * max)."""
+    n, m, d = 16384, 8192, 1024
+    g0 = torch.Generator().manual_seed(31)
+    x1, x2 = torch.randn(n, d, generator=g0).to(dtype), torch.randn(m, d, generator=g0).to(dtype)
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    out = getattr(tp, name)(a, b, **kw)
+    g = torch.randn(n, m, generator=g0).to(DEV, dtype)
+    out.backward(g)
+    rows, cols = torch.randperm(n, generator=g0)[:48], torch.randperm(m, generator=g0)[:48]
+    A, B = x1.double(), x2.double()
+    gamma, coef0 = kw["gamma"], kw["coef0"]
+
+    def weight(gs, s):
+        base = s * gamma + coef0
+        if name == "polynomial_kernel":
+            return gs * kw["degree"] * gamma * base ** (kw["degree"] - 1)
+        return gs * gamma * (1 - torch.tanh(base) ** 2)
+
+    gr = g[rows.to(DEV)].double().cpu()
+    gc = g[:, cols.to(DEV)].double().cpu()
+    want1 = weight(gr, A[rows] @ B.T) @ B
+    want2 = weight(gc, A @ B[cols].T).T @ A
+    rtol = 1e-4 if dtype == torch.float32 else 2e-2
+    got1, got2 = a.grad[rows.to(DEV)].double().cpu(), b.grad[cols.to(DEV)].double().cpu()
+    assert_close(got1, want1, rtol=rtol, atol=rtol * float(want1.abs().max()), what=f"{name} grad x1 rows")
+    assert_close(got2, want2, rtol=rtol, atol=rtol * float(want2.abs().max()), what=f"{name} grad x2 cols")

@@ -582,6 +582,28 @@ int64_t gemm_slots() {
     return c;
 }
 
+// Compute units of the current device (256 when the query fails).
+int64_t device_cus() {
+    static int cache[16];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+    int &c = cache[dev & 15];
+    if (c == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        c = cus;
+    }
+    return c;
+}
+
+// The tile-kernel gradient products have one block per 128 x 128 output tile and no split of K,
+// so they run only where that grid gives every CU two blocks; smaller outputs (16384 x 128 from
+// K = 16384: 128 tiles) take the split-K GEMM, whose splits fill the GPU.
+bool tile_grid_fills(int64_t batch, int64_t M, int64_t N) {
+    return cdiv(M, tile::kT) * cdiv(N, tile::kT) * batch >= 2 * device_cus();
+}
+
 // Number of K splits: the smallest whose blocks fill the resident rounds to at least 90 %
 // (the output tiles alone are often a round and a third: C2's 1024 tiles on 768 slots run two
 // rounds for 1.33 rounds of work), else the best fill, with at least 256 k per split.
@@ -706,6 +728,15 @@ __global__ void zero_words_kernel(uint16_t *__restrict__ p, int64_t len) {
 // The weights of step q + 1 are formed while step q's products run.  One 64 KiB buffer, two
 // blocks per CU.
 constexpr int kFCols = 256;
+
+// The fused grad_x1 kernels own a 128 x 256 tile of grad_x1 ([n, d]) and loop over all of m,
+// so their grid is only cdiv(n, 128) cdiv(d, 256) batch blocks: below two per CU they leave the
+// GPU half idle (16384 x 16384 x 128 polynomial: 128 blocks, 3.5 ms against 1.1 ms for the weight
+// pass and the two tile-kernel products), and the unfused path runs instead.
+// (Their grad_x2 product, m x d on the tile kernel, has to fill the GPU as well.)
+bool fused_grid_fills(int64_t batch, int64_t n, int64_t m, int64_t d) {
+    return cdiv(n, tile::kT) * cdiv(d, kFCols) * batch >= 2 * device_cus() && tile_grid_fills(batch, m, d);
+}
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
     const float *__restrict__ g, const float *__restrict__ av, const float *__restrict__ x2,
@@ -1134,7 +1165,8 @@ bool fused_fits(const void *g, const void *av, const float *x1, const float *x2,
 int products_f32(const float *W, const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
                  float sign, const BwdWs &w, float *gx1, float *gx2, hipStream_t s) {
     if (grad_product_f32_fits(W, false, x2, true, n, d, m, x1, gx1) &&
-        grad_product_f32_fits(W, true, x1, true, m, d, n, x2, gx2)) {
+        grad_product_f32_fits(W, true, x1, true, m, d, n, x2, gx2) && tile_grid_fills(batch, n, d) &&
+        tile_grid_fills(batch, m, d)) {
         const int rc = grad_product_f32(W, false, x2, true, batch, n, d, m, sign, w.coef1, x1, gx1, s);
         if (rc) return rc;
         return grad_product_f32(W, true, x1, true, batch, m, d, n, sign, w.coef2, x2, gx2, s);
@@ -1159,7 +1191,8 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     bool bf16_kmajor = false;
     if constexpr (kBf16)
         bf16_kmajor = grad_product_bf16_fits(W, false, x2, true, n, d, m, x1, gx1) &&
-                      grad_product_bf16_fits(W, true, x1, true, m, d, n, x2, gx2);
+                      grad_product_bf16_fits(W, true, x1, true, m, d, n, x2, gx2) &&
+                      tile_grid_fills(batch, n, d) && tile_grid_fills(batch, m, d);
     // cosine: S and the weight pass in one kernel (cos_weights_tile_kernel) where it fits and,
     // for bf16, the products need no W^T
     bool cos_fused = false;
@@ -1190,7 +1223,8 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
         const float *x1f = reinterpret_cast<const float *>(x1), *x2f = reinterpret_cast<const float *>(x2);
         float *Wf = reinterpret_cast<float *>(W);
         float *g1 = reinterpret_cast<float *>(gx1), *g2 = reinterpret_cast<float *>(gx2);
-        if (fused_fits(gf, MODE == kSqEuclid ? gf : av, x1f, x2f, Wf, g1, g2, n, m, d)) {
+        if (fused_fits(gf, MODE == kSqEuclid ? gf : av, x1f, x2f, Wf, g1, g2, n, m, d) &&
+            fused_grid_fills(batch, n, m, d)) {
             const float sign = (MODE == kPoly || MODE == kSigmoid) ? 1.0f : -1.0f;
             const int64_t tiles_n = cdiv(n, tile::kT), tiles_c = cdiv(d, kFCols), total = tiles_n * tiles_c * batch;
             hipLaunchKernelGGL((fused_grad1_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, s, gf, av, x2f, x1f,
@@ -1213,7 +1247,8 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
             const uint16_t *x1b = reinterpret_cast<const uint16_t *>(x1), *x2b = reinterpret_cast<const uint16_t *>(x2);
             uint16_t *Wb = reinterpret_cast<uint16_t *>(W);
             uint16_t *g1 = reinterpret_cast<uint16_t *>(gx1), *g2 = reinterpret_cast<uint16_t *>(gx2);
-            if (fused_bf16_fits(gb, MODE == kSqEuclid ? gb : rb, x1b, x2b, Wb, g1, g2, n, m, d)) {
+            if (fused_bf16_fits(gb, MODE == kSqEuclid ? gb : rb, x1b, x2b, Wb, g1, g2, n, m, d) &&
+                fused_grid_fills(batch, n, m, d)) {
                 const float sign = MODE == kSigmoid ? 1.0f : -1.0f;
                 const int64_t tiles_n = cdiv(n, tile::kT), tiles_c = cdiv(d, kFCols), total = tiles_n * tiles_c * batch;
                 hipLaunchKernelGGL((fused_grad1_bf16_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, s, gb, rb,

@@ -211,12 +211,21 @@ __device__ __forceinline__ uint4 kpiece_bf16(const uint4 *panel, int rb, int lan
     return make_uint4(v[0].x, v[0].y, v[1].x, v[1].y);
 }
 
+// A 16-byte output store: non-temporal (kNT), or a plain store that the L2 holds and combines
+// with the neighbouring waves' pieces of the same rows before write-back (faster for the
+// output-bound boolean kernels, slower by 1-2 % for the matrix-core-bound distance kernels).
+template <bool kNT, typename V>
+__device__ __forceinline__ void store16(V *p, V v) {
+    if constexpr (kNT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
 // One wave's 32 x (32 NI) fp32 outputs through its own LDS slice `sl` (NI * 4 KiB; no
 // workgroup barrier), written as (NI * 128)-byte row segments, 8 NI lanes per row.  value(ni,
 // g) returns the lane's register quad g of block ni: row grow0 + l32, columns gcol0 + 32 ni +
 // 8 g + 4 h + (0..3).  Rows >= n and columns >= m are not stored (m a multiple of 4, out
 // 16-byte aligned).  Stage unit u of row r sits at u ^ (r & 15).
-template <int NI, class F>
+template <int NI, bool kNT = true, class F>
 __device__ __forceinline__ void store_wave_rows_f32(floatx4 *sl, F &&value, float *__restrict__ out, int64_t b,
                                                     int64_t grow0, int64_t gcol0, int64_t n, int64_t m) {
     constexpr int U = NI * 8;    // 16-byte units per stage row
@@ -238,8 +247,7 @@ __device__ __forceinline__ void store_wave_rows_f32(floatx4 *sl, F &&value, floa
         const int r = it * RPI + rl;
         const floatx4 v = sl[r * U + (ul ^ (r & 15))];
         const int64_t grow = grow0 + r;
-        if (grow < n && gcol < m)
-            __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(out + (b * n + grow) * m + gcol));
+        if (grow < n && gcol < m) store16<kNT>(reinterpret_cast<floatx4 *>(out + (b * n + grow) * m + gcol), v);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is rewritten
     __builtin_amdgcn_wave_barrier();
@@ -247,7 +255,7 @@ __device__ __forceinline__ void store_wave_rows_f32(floatx4 *sl, F &&value, floa
 
 // The same for bf16 outputs (rounded to nearest even): 32 x (32 NI) values through an (NI * 2)
 // KiB slice, (NI * 64)-byte row segments, 4 NI lanes per row; m a multiple of 8.
-template <int NI, class F>
+template <int NI, bool kNT = true, class F>
 __device__ __forceinline__ void store_wave_rows_bf16(uint4 *sl, F &&value, uint16_t *__restrict__ out, int64_t b,
                                                      int64_t grow0, int64_t gcol0, int64_t n, int64_t m) {
     constexpr int U = NI * 4;    // 16-byte units (8 values) per stage row
@@ -272,8 +280,7 @@ __device__ __forceinline__ void store_wave_rows_bf16(uint4 *sl, F &&value, uint1
         const int r = it * RPI + rl;
         const u32x4 v = reinterpret_cast<const u32x4 *>(sl)[r * U + (ul ^ (r & 15))];
         const int64_t grow = grow0 + r;
-        if (grow < n && gcol < m)
-            __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (b * n + grow) * m + gcol));
+        if (grow < n && gcol < m) store16<kNT>(reinterpret_cast<u32x4 *>(out + (b * n + grow) * m + gcol), v);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is rewritten
     __builtin_amdgcn_wave_barrier();
@@ -287,7 +294,7 @@ __device__ __forceinline__ void store_wave_rows_bf16(uint4 *sl, F &&value, uint1
 // pass of 128 rows x 256 bytes, one workgroup barrier); fp32 per wave (store_wave_rows_f32, an
 // 8 KiB slice each).  Stage unit u of row r sits at u ^ (r & 15): conflict-free 16-byte accesses
 // across 16 rows and within 16-unit groups.
-template <typename OutT, class F>
+template <typename OutT, bool kNT = true, class F>
 __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restrict__ out, int64_t b, int64_t row0,
                                            int64_t col0, int64_t n, int64_t m) {
     if constexpr (sizeof(OutT) == 4) {
@@ -296,7 +303,7 @@ __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restric
         floatx4 *sl = reinterpret_cast<floatx4 *>(st) + wave * 512;
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
-            store_wave_rows_f32<2>(
+            store_wave_rows_f32<2, kNT>(
                 sl, [&](int ni, int g) { return value(mi, ni, g); }, out, b, row0 + wr + mi * 32, col0 + wc, n, m);
         return;
     }
@@ -350,8 +357,7 @@ __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restric
             const int r = (wave * ITERS + it) * RPI + rl;
             const u32x4 v = reinterpret_cast<const u32x4 *>(st)[r * UPR + (ul ^ (r & XM))];
             const int64_t grow = row0 + pass * PR + r;
-            if (grow < n && gcol < m)
-                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (b * n + grow) * m + gcol));
+            if (grow < n && gcol < m) store16<kNT>(reinterpret_cast<u32x4 *>(out + (b * n + grow) * m + gcol), v);
         }
         if (pass + 1 < NPASS) barrier_lds();  // the next pass rewrites the stage
     }

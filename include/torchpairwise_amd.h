@@ -232,6 +232,16 @@ int tpw_bool_fp4_count_metric(const uint8_t *x1, const uint8_t *x2, const int32_
                               const int32_t *x2_counts, int64_t batch, int64_t n, int64_t m,
                               int64_t d, int metric, float *out, void *stream);
 
+/* Self-check of the quotient the bit and fp4 tile kernels use for rows of at most 2^20
+ * features (reciprocal, one Newton step, one residual correction), which must equal the IEEE
+ * divide for integer numerators in [0, 2^22] and denominators in [1, 2^21].  For every
+ * o in [o_lo, o_hi] and the x_count numerators x = phase(o) + k x_step, adds to *mismatches
+ * the number of quotients whose bits differ from __fdiv_rn's (both the sequence from the
+ * hardware reciprocal and the one from RN(1 / o)).  No counterpart in the reference: a
+ * diagnostic of this library's arithmetic for its tests. */
+int tpw_count_division_check(int64_t o_lo, int64_t o_hi, int64_t x_step, int64_t x_count,
+                             unsigned long long *mismatches, void *stream);
+
 /* Equal / not-equal counts (TPW_BIT_EQ / TPW_BIT_NE, TPW_RED_SUM / TPW_RED_MEAN) of
  * non-bool inputs of element type `elem_type` (TPW_F32 ... TPW_I64), compared by value
  * like C++ ==; output float32 [batch, n, m] as tpw_bool_pairwise_reduce.

@@ -306,3 +306,68 @@ def test_public_bool_ops_on_both_routes(d):
         want_self = P.bool_count_metric(a.numpy(), a.numpy(), metric, gpu_scalar_divide=True)
         assert_equal(_public(metric, ga, None).cpu(), torch.from_numpy(want_self),
                      f"{metric} self d={d}", nan_payload=False)
+
+
+# ------------------------------------------------ GPU: the short divide of the tile kernels
+@pytest.mark.gpu
+@pytest.mark.parametrize("o_lo,o_hi,step,count", [
+    (1, 4096, 1, 8193),                    # every x in [0, 8192] over every o up to 4096
+    ((1 << 21) - (1 << 16) + 1, 1 << 21, 1, 4096),  # the largest denominators, x < 4096
+    (1, 1 << 21, 4093, 1024),              # every o up to 2^21, x strided over [0, 2^22]
+])
+def test_count_division_equals_ieee_divide(o_lo, o_hi, step, count):
+    """The reciprocal + Newton + residual quotient of the bit / fp4 tile kernels (rows of at
+    most 2^20 features) against __fdiv_rn bit for bit: the sequence's error bound proves it for
+    numerators in [0, 2^22] and denominators in [1, 2^21] given a reciprocal within one ulp;
+    this checks that premise and the result on the hardware."""
+    print(f"count division o=[{o_lo},{o_hi}] step={step} count={count}", flush=True)
+    assert capi.count_division_check(o_lo, o_hi, step, count) == 0
+
+
+def test_count_division_check_refuses_outside_its_domain():
+    l = capi.lib()
+    assert l.tpw_count_division_check(0, 4, 1, 1, None, None) != 0
+    assert b"[1, 2^21]" in l.tpw_last_error()
+    assert l.tpw_count_division_check(1, (1 << 21) + 1, 1, 1, None, None) != 0
+    assert l.tpw_count_division_check(1, 4, 1 << 12, 1 << 12, None, None) != 0
+    assert b"[0, 2^22]" in l.tpw_last_error()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", ((1 << 20) - 31, 1 << 20, (1 << 20) + 33))
+def test_tile_kernels_across_the_short_divide_limit(d):
+    """Rows of up to 2^20 features finish in float with the short divide, longer rows on
+    integer counts with the IEEE divide: both sides of the limit, on the bit and fp4 tile
+    kernels, against the int8 byte path (integer epilogue) and the oracle, bit for bit, for
+    every count metric and reduction."""
+    print(f"tile kernels at d={d}", flush=True)
+    B, n, m = 1, 40, 36
+    a, b = _rows(B, n, m, d, seed=7 + d % 97)
+    a[:, 1] = True                     # a full row
+    b[:, 2] = a[:, 3]                  # an identical pair
+    ga, gb = a.to(DEV), b.to(DEV)
+    wa, pa = torch.ops.torchpairwise._pack_bool(ga)
+    wb, pb = torch.ops.torchpairwise._pack_bool(gb)
+    for code, metric in enumerate(COUNT):
+        packed = torch.empty(B, n, m, device=DEV)
+        assert capi.call("tpw_bool_count_metric", capi._ptr(wa), capi._ptr(wb), capi._ptr(pa), capi._ptr(pb),
+                         B, n, m, d, code, capi._ptr(packed), capi._stream()) == 0
+        bytes_ = capi.bool_bytes_count_metric(ga, gb, code)
+        assert_equal(packed, bytes_, f"{metric} packed = bytes d={d}", nan_payload=False)
+        assert_equal(capi.bool_fp4_count_metric(ga, gb, code), bytes_, f"{metric} fp4 = bytes d={d}",
+                     nan_payload=False)
+        want = P.bool_count_metric(a[0].numpy(), b[0].numpy(), metric, gpu_scalar_divide=True)
+        assert_equal(packed[0].cpu(), torch.from_numpy(want), f"{metric} = oracle d={d}", nan_payload=False)
+    jac = torch.empty(B, n, m, device=DEV)
+    assert capi.call("tpw_jaccard_bool", capi._ptr(wa), capi._ptr(wb), capi._ptr(pa), capi._ptr(pb), B, n, m, d,
+                     capi._ptr(jac), capi._stream()) == 0
+    assert_equal(jac[0].cpu(), torch.from_numpy(P.jaccard_distances(a[0].numpy(), b[0].numpy())), f"jaccard d={d}")
+    for op, opname in ((capi.BIT_AND, "and"), (capi.BIT_OR, "or"), (capi.BIT_XOR, "xor"),
+                       (capi.BIT_EQ, "eq"), (capi.BIT_NE, "ne")):
+        for red, rname in ((capi.RED_SUM, "sum"), (capi.RED_MEAN, "mean")):
+            got = torch.empty(B, n, m, device=DEV)
+            assert capi.call("tpw_bool_pairwise_reduce_counted", capi._ptr(wa), capi._ptr(wb), capi._ptr(pa),
+                             capi._ptr(pb), B, n, m, d, op, red, capi._ptr(got), capi._stream()) == 0
+            want = torch.from_numpy(P.pw_reduce_bool(a[0].numpy(), b[0].numpy(), opname, rname))
+            assert_equal(got[0].cpu(), want, f"pw{opname}_{rname} packed d={d}")
+            assert_equal(capi.bool_fp4_reduce(ga, gb, op, red)[0].cpu(), want, f"pw{opname}_{rname} fp4 d={d}")

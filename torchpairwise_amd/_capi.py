@@ -41,6 +41,7 @@ _SIGNATURES = {
     "tpw_pack_bool_fp4": (_i, [_p, _i64, _i64, _p, _p, _p]),
     "tpw_bool_fp4_reduce": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_bool_fp4_count_metric": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _p, _p]),
+    "tpw_count_division_check": (_i, [_i64, _i64, _i64, _i64, _p, _p]),
     "tpw_compare_reduce": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
     "tpw_row_norms": (_i, [_p, _i, _i64, _i64, _i, _p, _p]),
     "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),
@@ -219,6 +220,16 @@ def bool_count_metric(x1, x2, metric):
     call("tpw_bool_count_metric", _ptr(wa), _ptr(wb), _ptr(pa), _ptr(pb), B, n, m, d, metric, _ptr(out),
          _stream())
     return out if x1.dim() == 3 else out[0]
+
+
+def count_division_check(o_lo, o_hi, x_step, x_count, device="cuda"):
+    """Quotients of the tile kernels' short divide that differ from the IEEE divide (see
+    tpw_count_division_check); 0 when the sequence is exact on this domain."""
+    import torch
+
+    bad = torch.zeros(1, dtype=torch.int64, device=device)
+    call("tpw_count_division_check", o_lo, o_hi, x_step, x_count, _ptr(bad), _stream())
+    return int(bad.item())
 
 
 def bool_row_counts(x):

@@ -131,6 +131,93 @@ __device__ __forceinline__ float finish(uint32_t cnt, uint32_t pa, uint32_t pb, 
     }
 }
 
+// Rows of at most kSmallRowLimit features: every count, popcount and composite numerator or
+// denominator is an integer of at most 2^21, held exactly by a float, and the quotients of two
+// such integers are correctly rounded by a short sequence instead of the general IEEE divide.
+//
+// div_count_r(x, o, y) for integers 0 <= x <= 2^22, 1 <= o <= 2^21 and y = (1/o)(1 + e1),
+// |e1| <= u + 6u^2 (u = 2^-24): q0 = RN(x y) is within (x/o)(2u + 7u^2) of x/o; the residual
+// r = x - o q0 is exact (a multiple of ulp(q0) below 4 o ulp(q0) < 2^24 ulp(q0)), so the pre-
+// rounding value of fma(r, y, q0) is x/o + (x/o - q0) e1, within (x/o) 2.0001 u^2 of x/o.  For
+// x/o in [2^e, 2^(e+1)) (e <= 21) the rounding midpoints are odd multiples of 2^(e-24) (and
+// 2^e - 2^(e-25) below the binade), and |x/o - M 2^(e-24)| = |x 2^(24-e) - M o| / (o 2^(24-e))
+// is at least 2^(e-24) / o unless zero; it is never zero (x/o = M 2^-j with M odd of 25 bits
+// would make the odd part of o divide x, and x/o a 24-bit integer times a power of two).
+// (x/o) 2.0001 u^2 < 2^(e+1) o 2.0001 u^2 <= 2^(e-24) / o holds for o <= 2^22 / 1.0001, so
+// the final rounding is that of x/o itself: the result is the correctly rounded quotient,
+// bit-identical to __fdiv_rn.  div_count makes y from the hardware reciprocal (within 1 ulp:
+// |e0| <= 2u) and one Newton step, y = RN(y0 + y0 (1 - o y0)), whose error before rounding
+// is below 6 u^2.
+constexpr int64_t kSmallRowLimit = (int64_t)1 << 20;
+
+__device__ __forceinline__ float div_count_r(float x, float o, float y) {
+    const float q0 = x * y;
+    const float r = __builtin_fmaf(-o, q0, x);
+    return __builtin_fmaf(r, y, q0);
+}
+
+__device__ __forceinline__ float div_count(float x, float o) {
+    const float y0 = __builtin_amdgcn_rcpf(o);
+    const float y = __builtin_fmaf(__builtin_fmaf(-o, y0, 1.0f), y0, y0);
+    return div_count_r(x, o, y);
+}
+
+// x / o as __fdiv_rn gives it, o = 0 included (x / 0 = +inf, 0 / 0 = NaN).
+__device__ __forceinline__ float div_count_z(float x, float o) {
+    return o != 0.0f ? div_count(x, o) : x * __builtin_inff();
+}
+
+// finish<> for rows of at most kSmallRowLimit features, on float counts: c is the AND count
+// (the fp32 MFMA accumulator, exact), pa and pb the two rows' popcounts, df = d and
+// inv_df = RN(1 / d).  Every value is the one finish<> returns for the same counts, bit for
+// bit: the integer steps are exact in float here, and the quotients are correctly rounded.
+template <int OP, int EPI>
+__device__ __forceinline__ float finish_small(float c, float pa, float pb, float df, float inv_df) {
+#pragma clang fp contract(off)
+    const float S = __builtin_fmaf(-2.0f, c, pa) + pb;  // xor count
+    if constexpr (EPI == kSum || EPI == kMean) {
+        float k;
+        if constexpr (OP == TPW_BIT_AND) k = c;
+        else if constexpr (OP == TPW_BIT_OR) k = (pa - c) + pb;
+        else if constexpr (OP == TPW_BIT_EQ) k = __builtin_fmaf(2.0f, c, df - pa) - pb;
+        else k = S;  // XOR, NE
+        if constexpr (EPI == kSum) return k;
+        else return div_count_r(k, df, inv_df);
+    } else if constexpr (EPI == kJaccard) {
+        return div_count(S, __builtin_fmaxf(S + c, 1.0f));  // or = 0 only with xor = 0: 0
+    } else {
+        constexpr int MET = EPI - kCountMetric;
+        const float A = c;
+        if constexpr (MET == TPW_BMET_HAMMING) {
+            return div_count_r(S, df, inv_df);
+        } else if constexpr (MET == TPW_BMET_JACCARD) {
+            return div_count(S, __builtin_fmaxf(S + A, 1.0f));
+        } else if constexpr (MET == TPW_BMET_DICE) {
+            return div_count_z(S, 2.0f * A + S);
+        } else if constexpr (MET == TPW_BMET_KULCZYNSKI1) {
+            return div_count_z(A, S);
+        } else if constexpr (MET == TPW_BMET_KULSINSKI) {
+            return div_count((S - A) + df, S + df);
+        } else if constexpr (MET == TPW_BMET_ROGERSTANIMOTO || MET == TPW_BMET_SOKALMICHENER) {
+            const float R = 2.0f * S;
+            return div_count(R, (df - S) + R);
+        } else if constexpr (MET == TPW_BMET_RUSSELLRAO) {
+            return (df - A) * inv_df;
+        } else if constexpr (MET == TPW_BMET_SOKALSNEATH) {
+            const float R = 2.0f * S;
+            return div_count_z(R, A + R);
+        } else {  // yule: products past 2^24 round, so the general divide
+            const float n10 = pa - A, n01 = pb - A;
+            const float n00 = df - ((pa + pb) - A);
+            const float hR = n10 * n01;
+            const float num = 2.0f * hR;
+            const float prod = A * n00;
+            const float den = prod + hR;
+            return den != 0.0f ? __fdiv_rn(num, den) : 0.0f;
+        }
+    }
+}
+
 template <int OP>
 __device__ __forceinline__ uint32_t bitop(uint32_t a, uint32_t b) {
     if constexpr (OP == TPW_BIT_AND) return a & b;
@@ -673,12 +760,69 @@ __global__ __launch_bounds__(kThreads, 2) void bool_fp4_kernel(
 // construction): transposed scaled products, the counts finished per element while the tile is
 // staged, float4 row segments out.  Needs m % 4 == 0, a 16-byte aligned output and
 // rows * row bytes < 2^32.
-// Output stores of the tile kernels: the plain reductions (a count or a count / d per output)
-// store plainly, which lets the L2 merge the waves' 256-byte row pieces (pwxor_sum at C4 0.95 ->
-// 0.83 ms, hamming 0.96 -> 0.86 ms); the count metrics, whose epilogue divides, are 2 % faster
-// with non-temporal stores (jaccard 1.12 -> 1.09 ms, dice, yule alike).
+// Output stores of the tile kernels: plain stores, which let the L2 merge the waves' 256-byte
+// row pieces (32768^2 x 1024 bits: pwxor_sum 0.95 -> 0.83 ms, hamming 0.96 -> 0.86 ms, jaccard
+// 0.97 -> 0.91 ms), except for yule, whose epilogue keeps the general IEEE divide and runs
+// 4 % faster with non-temporal stores (1.13 -> 1.09 ms).
 template <int EPI>
-constexpr bool kStoreNT = EPI >= kJaccard;
+constexpr bool kStoreNT = EPI == kCountMetric + TPW_BMET_YULE;
+
+// Before the barrier that ends the K loop: rows of at most kSmallRowLimit features turn the
+// tile's popcounts into floats in place (2 kT = kThreads entries, one per thread).
+__device__ __forceinline__ void pops_to_float(bool small, uint32_t *s_pop) {
+    static_assert(2 * tile::kT == tile::kThreads, "one popcount per thread");
+    if (small) s_pop[threadIdx.x] = __float_as_uint((float)s_pop[threadIdx.x]);
+}
+
+// The output of the fp4 / bit tile kernels from their fp32 AND-count accumulators (transposed
+// products: register 4 g + e of lane l32 + 32 h in block (mi, ni) is row wr + 32 mi + l32,
+// column wc + 32 ni + 8 g + 4 h + e of the tile).  Rows of at most kSmallRowLimit features
+// finish in float (finish_small, popcounts already floats in s_pop), longer rows on integer
+// counts (finish); both give the same bits.
+template <int OP, int EPI>
+__device__ __forceinline__ void bool_tile_store(bool small, const floatx16 (&facc)[2][2], uint4 *smem,
+                                                const uint32_t *s_pop, int wr, int wc, int l32, int h, int64_t d,
+                                                double inv_d, float inv_df, float *__restrict__ out, int64_t b,
+                                                int64_t row0, int64_t col0, int64_t n, int64_t m) {
+    using tile::kT;
+    const float df = (float)d;
+    if (small) {
+        float pav[2];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) pav[mi] = __uint_as_float(s_pop[wr + mi * 32 + l32]);
+        tile::store_tile<float, kStoreNT<EPI>>(
+            smem,
+            [&](int mi, int ni, int g) {
+                const uint4 pb = *reinterpret_cast<const uint4 *>(&s_pop[kT + wc + ni * 32 + 8 * g + 4 * h]);
+                const float pbe[4] = {__uint_as_float(pb.x), __uint_as_float(pb.y), __uint_as_float(pb.z),
+                                      __uint_as_float(pb.w)};
+                floatx4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = finish_small<OP, EPI>(facc[mi][ni][4 * g + e], pav[mi], pbe[e], df, inv_df);
+                return o;
+            },
+            out, b, row0, col0, n, m);
+        return;
+    }
+    const uint32_t du = (uint32_t)d;
+    uint32_t pav[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) pav[mi] = s_pop[wr + mi * 32 + l32];
+    tile::store_tile<float, kStoreNT<EPI>>(
+        smem,
+        [&](int mi, int ni, int g) {
+            const uint4 pb = *reinterpret_cast<const uint4 *>(&s_pop[kT + wc + ni * 32 + 8 * g + 4 * h]);
+            const uint32_t pbe[4] = {pb.x, pb.y, pb.z, pb.w};
+            floatx4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t c = count_from_and<OP, EPI>((uint32_t)facc[mi][ni][4 * g + e], pav[mi], pbe[e]);
+                o[e] = finish<OP, EPI>(c, pav[mi], pbe[e], du, inv_d, df, inv_df);
+            }
+            return o;
+        },
+        out, b, row0, col0, n, m);
+}
 
 template <int OP, int EPI>
 __global__ __launch_bounds__(tile::kThreads, 4) void bool_fp4_tile_kernel(
@@ -741,27 +885,10 @@ __global__ __launch_bounds__(tile::kThreads, 4) void bool_fp4_tile_kernel(
                                                                                   0, 127, 0, 127);
         }
     }
+    const bool small = d <= kSmallRowLimit;
+    pops_to_float(small, s_pop);
     barrier_lds();  // the operand buffer becomes the output stage
-
-    const uint32_t du = (uint32_t)d;
-    const float df = (float)d;
-    uint32_t pav[2];
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi) pav[mi] = s_pop[wr + mi * 32 + l32];
-    store_tile<float, kStoreNT<EPI>>(
-        smem,
-        [&](int mi, int ni, int g) {
-            const uint4 pb = *reinterpret_cast<const uint4 *>(&s_pop[kT + wc + ni * 32 + 8 * g + 4 * h]);
-            const uint32_t pbe[4] = {pb.x, pb.y, pb.z, pb.w};
-            floatx4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t c = count_from_and<OP, EPI>((uint32_t)facc[mi][ni][4 * g + e], pav[mi], pbe[e]);
-                o[e] = finish<OP, EPI>(c, pav[mi], pbe[e], du, inv_d, df, inv_df);
-            }
-            return o;
-        },
-        out, b, row0, col0, n, m);
+    bool_tile_store<OP, EPI>(small, facc, smem, s_pop, wr, wc, l32, h, d, inv_d, inv_df, out, b, row0, col0, n, m);
 }
 
 // The tile kernel of tile_mfma.hpp on bit-packed rows (W uint32 words per row, W % 4 == 0,
@@ -874,27 +1001,10 @@ __global__ __launch_bounds__(tile::kThreads, 4) void bool_bits_tile_kernel(
 #pragma unroll
         for (int p = 0; p < 4; ++p) pair(p);
     }
+    const bool small = d <= kSmallRowLimit;
+    pops_to_float(small, s_pop);
     barrier_lds();  // the operand buffer becomes the output stage
-
-    const uint32_t du = (uint32_t)d;
-    const float df = (float)d;
-    uint32_t pav[2];
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi) pav[mi] = s_pop[wr + mi * 32 + l32];
-    store_tile<float, kStoreNT<EPI>>(
-        smem,
-        [&](int mi, int ni, int g) {
-            const uint4 pb = *reinterpret_cast<const uint4 *>(&s_pop[kT + wc + ni * 32 + 8 * g + 4 * h]);
-            const uint32_t pbe[4] = {pb.x, pb.y, pb.z, pb.w};
-            floatx4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t c = count_from_and<OP, EPI>((uint32_t)facc[mi][ni][4 * g + e], pav[mi], pbe[e]);
-                o[e] = finish<OP, EPI>(c, pav[mi], pbe[e], du, inv_d, df, inv_df);
-            }
-            return o;
-        },
-        out, b, row0, col0, n, m);
+    bool_tile_store<OP, EPI>(small, facc, smem, s_pop, wr, wc, l32, h, d, inv_d, inv_df, out, b, row0, col0, n, m);
 }
 
 // Whether bool_bits_tile_kernel takes these packed rows (W words per row) and output.
@@ -1232,4 +1342,40 @@ extern "C" int tpw_bool_fp4_count_metric(const uint8_t *x1, const uint8_t *x2, c
     }
 #undef TPW_MET
     return TPW_ERR_INVALID;
+}
+
+namespace tpw {
+namespace {
+// One thread per denominator o: x = phase + k step (k < count, phase = o 2654435761 mod step)
+// through div_count, and div_count_r with y = RN(1 / o), against __fdiv_rn, bit for bit.
+__global__ __launch_bounds__(256) void count_division_check_kernel(int64_t o_lo, int64_t o_hi, int64_t step,
+                                                                   int64_t count,
+                                                                   unsigned long long *__restrict__ mismatches) {
+    const int64_t o = o_lo + (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (o > o_hi) return;
+    const float of = (float)o;
+    const float y = __fdiv_rn(1.0f, of);
+    const int64_t phase = (int64_t)(((uint64_t)o * 2654435761u) % (uint64_t)step);
+    unsigned long long bad = 0;
+    for (int64_t k = 0; k < count; ++k) {
+        const float xf = (float)(phase + k * step);
+        const uint32_t ref = __float_as_uint(__fdiv_rn(xf, of));
+        bad += __float_as_uint(div_count(xf, of)) != ref;
+        bad += __float_as_uint(div_count_r(xf, of, y)) != ref;
+    }
+    if (bad) atomicAdd(mismatches, bad);
+}
+}  // namespace
+}  // namespace tpw
+
+extern "C" int tpw_count_division_check(int64_t o_lo, int64_t o_hi, int64_t x_step, int64_t x_count,
+                                        unsigned long long *mismatches, void *stream) {
+    TPW_REQUIRE(o_lo >= 1 && o_lo <= o_hi && o_hi <= 2 * kSmallRowLimit, "denominators must lie in [1, 2^21]");
+    TPW_REQUIRE(x_step >= 1 && x_count >= 1 && (x_step - 1) + (x_count - 1) * x_step <= 4 * kSmallRowLimit,
+                "numerators must lie in [0, 2^22]");
+    TPW_REQUIRE((o_hi - o_lo + 1) * x_count <= ((int64_t)1 << 36), "too many quotients for one check");
+    TPW_REQUIRE(mismatches, "null pointer");
+    hipLaunchKernelGGL(count_division_check_kernel, dim3((unsigned)cdiv(o_hi - o_lo + 1, 256)), dim3(256), 0,
+                       as_stream(stream), o_lo, o_hi, x_step, x_count, mismatches);
+    return check_launch("count_division_check_kernel");
 }

@@ -96,11 +96,12 @@ def test_fp4_tile_kernel_equals_staged_kernel(B, n, m, d, metric):
 
 
 # --------------------------------------------------------------------------------------
-# Bit-packed rows on the fp4 matrix cores (bool_bits_tile_kernel, rows of more than 256
-# features) against the popcount kernel the same entry points take for an output offset by
-# one element: every count metric, jaccard, and every op x reduction of the counted entry;
-# partial last chunks (d = 257: 3 of 8 pieces; 1500: 2 chunks, the second half full; 2081:
-# 3 chunks, the last one piece), edge tiles.  Bit-identical.
+# Bit-packed rows on the fp4 matrix cores (bool_bits_tile_kernel: the count metrics at any d,
+# the reductions over more than 256 features) against the popcount kernel the same entry points
+# take for an output offset by one element: every count metric, jaccard, and every op x
+# reduction of the counted entry; partial last chunks (d = 1 .. 256: one chunk of one or two
+# pieces; 257: 3 of 8 pieces; 1500: 2 chunks, the second half full; 2081: 3 chunks, the last
+# one piece), edge tiles.  Bit-identical.
 # --------------------------------------------------------------------------------------
 def _bits_call(x1, x2, kind, code, misaligned):
     wa, pa = capi.pack_bool(x1)
@@ -127,7 +128,8 @@ BITS_CASES = ([("metric", k) for k in range(10)] + [("jaccard", 0)] +
               [("reduce", (op, red)) for op in range(5) for red in range(2)])
 
 
-@pytest.mark.parametrize("B,n,m,d", [(1, 300, 260, 257), (2, 129, 136, 1024), (1, 130, 132, 1500),
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 132, 1), (1, 70, 136, 33), (2, 129, 136, 128), (1, 130, 132, 256),
+                                     (1, 300, 260, 257), (2, 129, 136, 1024), (1, 130, 132, 1500),
                                      (1, 70, 132, 2081)])
 @pytest.mark.parametrize("kind,code", BITS_CASES)
 def test_bits_tile_kernel_equals_popcount_kernel(B, n, m, d, kind, code):

@@ -1014,13 +1014,16 @@ bool bits_tile_fits(const uint32_t *a, const uint32_t *b, const int32_t *pa, con
            aligned16(b) && aligned16(out) && m % 4 == 0 && (n > m ? n : m) * W * 4 < ((int64_t)1 << 32);
 }
 
-// Packed rows with their popcounts: the bit tile kernel for rows of more than 256 features
-// where it fits, else the popcount reduce kernel.
+// Packed rows with their popcounts: the bit tile kernel where it fits, for the count metrics
+// at any d and for the reductions over more than 256 features; else the popcount reduce kernel.
+// Short rows' reductions write faster from the popcount kernel's 2 KB output row runs; their
+// count metrics are faster on the tile kernel's float epilogue (16384^2 x 128: jaccard 0.287 ->
+// 0.220 ms, dice 0.286 -> 0.230 ms).
 template <int OP, int EPI>
 int launch_counts(const uint32_t *a, const uint32_t *b, const int32_t *pa, const int32_t *pb, int64_t batch,
                   int64_t n, int64_t m, int64_t d, float *out, hipStream_t s) {
     const int64_t W = tpw_packed_words(d);
-    if (d > 256 && bits_tile_fits(a, b, pa, pb, n, m, d, W, out)) {
+    if ((d > 256 || EPI >= kJaccard) && bits_tile_fits(a, b, pa, pb, n, m, d, W, out)) {
         const int64_t tiles_n = cdiv(n, kTile), tiles_m = cdiv(m, kTile);
         const int64_t total = tiles_n * tiles_m * batch;
         const double inv_d = 1.0 / (double)d;

@@ -83,7 +83,8 @@ def _fp4_metric(x1, x2, metric, misaligned):
     return out.view(B, n, m)
 
 
-@pytest.mark.parametrize("B,n,m,d", [(1, 300, 260, 100), (2, 129, 136, 1000), (1, 128, 256, 256), (1, 70, 132, 3000)])
+@pytest.mark.parametrize("B,n,m,d", [(1, 300, 260, 100), (2, 129, 136, 1000), (1, 128, 256, 256), (1, 70, 132, 3000),
+                                     (1, 130, 131, 1000), (2, 70, 134, 300)])
 @pytest.mark.parametrize("metric", range(10))
 def test_fp4_tile_kernel_equals_staged_kernel(B, n, m, d, metric):
     x1 = (rand(B, n, d, seed=3) < 0.3).to(DEV)
@@ -101,7 +102,7 @@ def test_fp4_tile_kernel_equals_staged_kernel(B, n, m, d, metric):
 # take for an output offset by one element: every count metric, jaccard, and every op x
 # reduction of the counted entry; partial last chunks (d = 1 .. 256: one chunk of one or two
 # pieces; 257: 3 of 8 pieces; 1500: 2 chunks, the second half full; 2081: 3 chunks, the last
-# one piece), edge tiles.  Bit-identical.
+# one piece), edge tiles, ragged output rows (m % 4 != 0).  Bit-identical.
 # --------------------------------------------------------------------------------------
 def _bits_call(x1, x2, kind, code, misaligned):
     wa, pa = capi.pack_bool(x1)
@@ -130,7 +131,10 @@ BITS_CASES = ([("metric", k) for k in range(10)] + [("jaccard", 0)] +
 
 @pytest.mark.parametrize("B,n,m,d", [(1, 130, 132, 1), (1, 70, 136, 33), (2, 129, 136, 128), (1, 130, 132, 256),
                                      (1, 300, 260, 257), (2, 129, 136, 1024), (1, 130, 132, 1500),
-                                     (1, 70, 132, 2081)])
+                                     (1, 70, 132, 2081),
+                                     # ragged rows (m % 4 != 0): dword row stores
+                                     (1, 130, 131, 1024), (2, 70, 133, 300), (1, 129, 130, 100),
+                                     (1, 257, 259, 33), (1, 40, 1, 512)])
 @pytest.mark.parametrize("kind,code", BITS_CASES)
 def test_bits_tile_kernel_equals_popcount_kernel(B, n, m, d, kind, code):
     x1 = (rand(B, n, d, seed=5) < 0.3).to(DEV)

@@ -758,8 +758,8 @@ __global__ __launch_bounds__(kThreads, 2) void bool_fp4_kernel(
 
 // The tile kernel of tile_mfma.hpp on the fp4 rows (every 128-byte chunk is full by
 // construction): transposed scaled products, the counts finished per element while the tile is
-// staged, float4 row segments out.  Needs m % 4 == 0, a 16-byte aligned output and
-// rows * row bytes < 2^32.
+// staged, float4 row segments out (dword rows when m % 4 != 0).  Needs a 16-byte aligned
+// output and rows * row bytes < 2^32.
 // Output stores of the tile kernels: plain stores, which let the L2 merge the waves' 256-byte
 // row pieces (32768^2 x 1024 bits: pwxor_sum 0.95 -> 0.83 ms, hamming 0.96 -> 0.86 ms, jaccard
 // 0.97 -> 0.91 ms), except for yule, whose epilogue keeps the general IEEE divide and runs
@@ -778,7 +778,8 @@ __device__ __forceinline__ void pops_to_float(bool small, uint32_t *s_pop) {
 // products: register 4 g + e of lane l32 + 32 h in block (mi, ni) is row wr + 32 mi + l32,
 // column wc + 32 ni + 8 g + 4 h + e of the tile).  Rows of at most kSmallRowLimit features
 // finish in float (finish_small, popcounts already floats in s_pop), longer rows on integer
-// counts (finish); both give the same bits.
+// counts (finish); both give the same bits.  Any m: rows of m % 4 != 0 floats are written a
+// dword per lane (the ragged mode of tile::store_tile).
 template <int OP, int EPI>
 __device__ __forceinline__ void bool_tile_store(bool small, const floatx16 (&facc)[2][2], uint4 *smem,
                                                 const uint32_t *s_pop, int wr, int wc, int l32, int h, int64_t d,
@@ -801,7 +802,7 @@ __device__ __forceinline__ void bool_tile_store(bool small, const floatx16 (&fac
                 for (int e = 0; e < 4; ++e) o[e] = finish_small<OP, EPI>(facc[mi][ni][4 * g + e], pav[mi], pbe[e], df, inv_df);
                 return o;
             },
-            out, b, row0, col0, n, m);
+            out, b, row0, col0, n, m, (m & 3) != 0);
         return;
     }
     const uint32_t du = (uint32_t)d;
@@ -821,7 +822,7 @@ __device__ __forceinline__ void bool_tile_store(bool small, const floatx16 (&fac
             }
             return o;
         },
-        out, b, row0, col0, n, m);
+        out, b, row0, col0, n, m, (m & 3) != 0);
 }
 
 template <int OP, int EPI>
@@ -899,8 +900,8 @@ __global__ __launch_bounds__(tile::kThreads, 4) void bool_fp4_tile_kernel(
 // nibble i of operand dword e (0x2 = 1.0 or 0), the same permutation of the features on both
 // sides, so every AND count is unchanged.  A partial last chunk (W % 32 != 0) loads an
 // in-row piece into the slots past the row's end and zeroes them in LDS before use.  Counts, popcounts and the epilogue are those of
-// bool_fp4_tile_kernel, so the outputs are the same bit for bit.  Needs d < 2^24, m % 4 == 0,
-// a 16-byte aligned output and rows * W * 4 < 2^32.
+// bool_fp4_tile_kernel, so the outputs are the same bit for bit.  Needs d < 2^24, a 16-byte
+// aligned output and rows * W * 4 < 2^32.
 template <int OP, int EPI>
 __global__ __launch_bounds__(tile::kThreads, 4) void bool_bits_tile_kernel(
     const uint32_t *__restrict__ x1, const uint32_t *__restrict__ x2, const int32_t *__restrict__ popA,
@@ -1011,7 +1012,7 @@ __global__ __launch_bounds__(tile::kThreads, 4) void bool_bits_tile_kernel(
 bool bits_tile_fits(const uint32_t *a, const uint32_t *b, const int32_t *pa, const int32_t *pb, int64_t n,
                     int64_t m, int64_t d, int64_t W, const float *out) {
     return pa && pb && d >= 1 && d < (int64_t)kFloatExactLimit && W % 4 == 0 && W * 32 >= d && aligned16(a) &&
-           aligned16(b) && aligned16(out) && m % 4 == 0 && (n > m ? n : m) * W * 4 < ((int64_t)1 << 32);
+           aligned16(b) && aligned16(out) && (n > m ? n : m) * W * 4 < ((int64_t)1 << 32);
 }
 
 // Packed rows with their popcounts: the bit tile kernel where it fits, for the count metrics
@@ -1045,7 +1046,7 @@ int launch_bool_fp4(const uint8_t *a, const uint8_t *b, const int32_t *pa, const
     const double inv_d = d < (int64_t)kFloatExactLimit ? 1.0 / (double)d : 0.0;
     const float inv_df = 1.0f / (float)d;
     const bool vec_store = m % 4 == 0 && aligned16(out);
-    if (vec_store && (n > m ? n : m) * fp4_row_bytes(d) < ((int64_t)1 << 32)) {
+    if (aligned16(out) && (n > m ? n : m) * fp4_row_bytes(d) < ((int64_t)1 << 32)) {
         hipLaunchKernelGGL((bool_fp4_tile_kernel<OP, EPI>), dim3((unsigned)total), dim3(tile::kThreads), 0, s, a, b,
                            pa, pb, n, m, d, fp4_row_bytes(d), inv_d, inv_df, out, tiles_n, tiles_m, total);
         return check_launch("bool_fp4_tile_kernel");

@@ -224,10 +224,13 @@ __device__ __forceinline__ void store16(V *p, V v) {
 // workgroup barrier), written as (NI * 128)-byte row segments, 8 NI lanes per row.  value(ni,
 // g) returns the lane's register quad g of block ni: row grow0 + l32, columns gcol0 + 32 ni +
 // 8 g + 4 h + (0..3).  Rows >= n and columns >= m are not stored (m a multiple of 4, out
-// 16-byte aligned).  Stage unit u of row r sits at u ^ (r & 15).
+// 16-byte aligned).  Stage unit u of row r sits at u ^ (r & 15).  With `ragged` (rows of
+// m % 4 != 0 floats, so no 16-byte row segments) each store instruction writes one row's
+// 32 NI values instead, a dword per lane: 128 NI contiguous bytes, 32 instructions per slice.
 template <int NI, bool kNT = true, class F>
 __device__ __forceinline__ void store_wave_rows_f32(floatx4 *sl, F &&value, float *__restrict__ out, int64_t b,
-                                                    int64_t grow0, int64_t gcol0, int64_t n, int64_t m) {
+                                                    int64_t grow0, int64_t gcol0, int64_t n, int64_t m,
+                                                    bool ragged = false) {
     constexpr int U = NI * 8;    // 16-byte units per stage row
     constexpr int RPI = 64 / U;  // rows per store instruction
     const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
@@ -241,13 +244,26 @@ __device__ __forceinline__ void store_wave_rows_f32(floatx4 *sl, F &&value, floa
         }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
-    const int64_t gcol = gcol0 + 4 * ul;
+    if (ragged) {
+        const float *sf = reinterpret_cast<const float *>(sl);
+        const int c = lane % (32 * NI);
+        const int64_t gcol = gcol0 + c;
+        const bool col_ok = lane < 32 * NI && gcol < m;
+#pragma unroll 8
+        for (int r = 0; r < 32; ++r) {
+            const float v = sf[(r * U + ((c >> 2) ^ (r & 15))) * 4 + (c & 3)];
+            const int64_t grow = grow0 + r;
+            if (col_ok && grow < n) store16<kNT>(out + (b * n + grow) * m + gcol, v);
+        }
+    } else {
+        const int64_t gcol = gcol0 + 4 * ul;
 #pragma unroll
-    for (int it = 0; it < 32 / RPI; ++it) {
-        const int r = it * RPI + rl;
-        const floatx4 v = sl[r * U + (ul ^ (r & 15))];
-        const int64_t grow = grow0 + r;
-        if (grow < n && gcol < m) store16<kNT>(reinterpret_cast<floatx4 *>(out + (b * n + grow) * m + gcol), v);
+        for (int it = 0; it < 32 / RPI; ++it) {
+            const int r = it * RPI + rl;
+            const floatx4 v = sl[r * U + (ul ^ (r & 15))];
+            const int64_t grow = grow0 + r;
+            if (grow < n && gcol < m) store16<kNT>(reinterpret_cast<floatx4 *>(out + (b * n + grow) * m + gcol), v);
+        }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is rewritten
     __builtin_amdgcn_wave_barrier();
@@ -290,13 +306,14 @@ __device__ __forceinline__ void store_wave_rows_bf16(uint4 *sl, F &&value, uint1
 // g) returns the 4 outputs of the lane's register quad g of block (mi, ni) as float: row
 // wr + 32 mi + l32, columns wc + 32 ni + 8 g + 4 h + (0..3).  Rows >= n and columns >= m are not
 // stored; m must be a multiple of 16 / sizeof(OutT) and out 16-byte aligned (a 16-byte store
-// unit is then wholly inside or outside).  bf16 stages the rounded values of the whole tile (one
+// unit is then wholly inside or outside), except that fp32 outputs take any m with `ragged`
+// set (m % 4 != 0: dword row stores, store_wave_rows_f32).  bf16 stages the rounded values of the whole tile (one
 // pass of 128 rows x 256 bytes, one workgroup barrier); fp32 per wave (store_wave_rows_f32, an
 // 8 KiB slice each).  Stage unit u of row r sits at u ^ (r & 15): conflict-free 16-byte accesses
 // across 16 rows and within 16-unit groups.
 template <typename OutT, bool kNT = true, class F>
 __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restrict__ out, int64_t b, int64_t row0,
-                                           int64_t col0, int64_t n, int64_t m) {
+                                           int64_t col0, int64_t n, int64_t m, bool ragged = false) {
     if constexpr (sizeof(OutT) == 4) {
         const int wave = threadIdx.x >> 6;
         const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
@@ -304,7 +321,8 @@ __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restric
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
             store_wave_rows_f32<2, kNT>(
-                sl, [&](int ni, int g) { return value(mi, ni, g); }, out, b, row0 + wr + mi * 32, col0 + wc, n, m);
+                sl, [&](int ni, int g) { return value(mi, ni, g); }, out, b, row0 + wr + mi * 32, col0 + wc, n, m,
+                ragged);
         return;
     }
     const int tid = threadIdx.x, lane = tid & 63;

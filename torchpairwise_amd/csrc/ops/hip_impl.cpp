@@ -257,10 +257,11 @@ std::pair<at::Tensor, at::Tensor> pack(const at::Tensor &x3, bool with_pops) {
 void bool_bytes_cuda(const at::Tensor &a, const at::Tensor &b, int bmet, int op, int red, at::Tensor &out) {
     const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
     const bool same = b.is_same(a);
-    if (m % 4 == 0 && d < (int64_t(1) << 24) && std::max(n, m) * tpw_packed_words(d) * 4 < (int64_t(1) << 32)) {
-        // bit-packed rows and row popcounts (one pack pass per operand); rows of more than 256
-        // features then take the bit tile kernel on the fp4 matrix cores, shorter ones the
-        // popcount kernel; the results equal the int8 byte path's bit for bit
+    if (d < (int64_t(1) << 24) && std::max(n, m) * tpw_packed_words(d) * 4 < (int64_t(1) << 32)) {
+        // bit-packed rows and row popcounts (one pack pass per operand); the count metrics, and
+        // the reductions over more than 256 features, then take the bit tile kernel on the fp4
+        // matrix cores (any m), the rest the popcount kernel; the results equal the int8 byte
+        // path's bit for bit
         auto pa = pack(a, true);
         auto pb = same ? pa : pack(b, true);
         const uint32_t *wa = reinterpret_cast<const uint32_t *>(pa.first.data_ptr<int32_t>());

@@ -226,3 +226,25 @@ def test_backward_products_kmajor_bf16(name, B, n, m, d):
         assert_close(kmaj, want, rtol=1e-2, atol=1e-2 * scale, what=f"{name} grad_x{k + 1} (k-major)")
         assert_close(kmaj, other.double(), rtol=2.0 ** -7, atol=1e-3 * scale,
                      what=f"{name} grad_x{k + 1} k-major vs transposed")
+
+
+# --------------------------------------------------------------------------------------
+# Rows that are not whole 128-byte chunks: for outputs of 2^20 entries or more the public
+# inner-product ops copy the operands zero-padded to whole chunks and take the tile kernel;
+# below that, the staged kernel, which zero-fills its last chunk.  Bit-identical either way.
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,n,m,d", [
+    (torch.float32, 1100, 1000, 127), (torch.float32, 1024, 1040, 130), (torch.float32, 1030, 1024, 1),
+    (torch.bfloat16, 1030, 1024, 255), (torch.bfloat16, 1024, 1032, 200),
+])
+@pytest.mark.parametrize("op,epi", [("euclidean_distances", capi.EPI_EUCLIDEAN),
+                                    ("cosine_similarity", capi.EPI_COSINE_SIM),
+                                    ("linear_kernel", capi.EPI_DOT)])
+def test_padded_rows_equal_staged_kernel(dtype, n, m, d, op, epi):
+    print(f"padded {op} {dtype} {n}x{m}x{d}", flush=True)
+    x1 = randn(1, n, d, seed=11).to(DEV, dtype)
+    x2 = randn(1, m, d, seed=12).to(DEV, dtype)
+    x2[:, 5] = x1[:, 0]
+    got = getattr(torch.ops.torchpairwise, op)(x1[0], x2[0])
+    assert _same_bits(got, _inner(x1, x2, epi, True)[0])
+

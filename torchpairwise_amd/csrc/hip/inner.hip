@@ -739,7 +739,9 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
     const bool direct = vec && d % Elem<T>::kChunk == 0 && d > 0 && (n > m ? n : m) * d < ((int64_t)1 << 31);
     if constexpr (EPI != kEpiPoly) {
         // the tile kernel: byte offsets below 2^32, whole 16-byte units per output row (and, for
-        // the gradient products, 16-byte aligned X rows)
+        // the gradient products, 16-byte aligned X rows).  Ragged fp32 rows stay on the staged
+        // kernel: the tile store's dword rows cost the matrix-core-bound products more
+        // (16384 x 16383 x 128 euclidean 0.676 -> 0.716 ms)
         if (direct && (n > m ? n : m) * d * (int64_t)sizeof(T) < ((int64_t)1 << 32) && aligned16(out) &&
             m % (16 / (int64_t)sizeof(OutT)) == 0 && (EPI != kEpiGrad || aligned16(X))) {
             // long K (16 chunks or more): two operand buffers, the next chunk's DMA in flight

@@ -242,6 +242,51 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
     }
 
     const bool vec_store = VEC && (m % 4 == 0);
+    if (!vec_store) {
+        // rows of m % 4 != 0 floats (or unaligned outputs): the tile goes through the operand
+        // LDS (free after the K loop's last barrier) in four 64 x 64 quarters, and each wave
+        // writes whole 64-value row pieces, a dword per lane: 256 contiguous bytes per store
+        // instead of 4-byte stores 16 bytes apart
+        constexpr int kSt = 66;
+        static_assert(64 * kSt <= kBK * (kTile + kPad), "the stage fits in As");
+        float *st = &As[0][0];
+        const int wave = tid >> 6, lane = tid & 63;
+        for (int rh = 0; rh < 2; ++rh)
+            for (int h = 0; h < 2; ++h) {
+                if ((ty >> 3) == rh) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int64_t row = row0 + 8 * ty + i;
+                        const int64_t col = col0 + 64 * h + 4 * tx;
+                        floatx4 prev = {0.0f, 0.0f, 0.0f, 0.0f};
+                        if constexpr (MODE == kBrayDen) {
+#pragma unroll
+                            for (int c = 0; c < 4; ++c)
+                                if (row < n && col + c < m) prev[c] = out[(b * n + row) * m + col + c];
+                        }
+                        floatx4 v;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) v[c] = fam_finish<MODE, PK>(acc[i][4 * h + c], inv_p, prev[c]);
+                        if (exp_post) {
+#pragma clang fp contract(off)
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) v[c] = expf(v[c] * post);
+                        }
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) st[(8 * ty + i - 64 * rh) * kSt + 4 * tx + c] = v[c];
+                    }
+                }
+                __syncthreads();
+                const int64_t col = col0 + 64 * h + lane;
+#pragma unroll 4
+                for (int r = 16 * wave; r < 16 * wave + 16; ++r) {
+                    const int64_t row = row0 + 64 * rh + r;
+                    if (row < n && col < m) store_nt(out + (b * n + row) * m + col, st[r * kSt + lane]);
+                }
+                __syncthreads();  // the quarter is written before the next one is staged
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int64_t row = row0 + 8 * ty + i;

@@ -59,6 +59,12 @@ def _same_bits(a, b):
     (torch.bfloat16, 3, 257, 520, 192),
     (torch.bfloat16, 1, 128, 128, 256),
     (torch.bfloat16, 1, 200, 136, 1024),   # long K
+    # bf16 ragged rows (m % 8 = 1 .. 7): whole units funnel-shifted, head / tail values
+    (torch.bfloat16, 1, 300, 259, 64),
+    (torch.bfloat16, 2, 129, 133, 192),
+    (torch.bfloat16, 1, 130, 262, 1024),
+    (torch.bfloat16, 1, 70, 7, 128),
+    (torch.bfloat16, 1, 257, 140, 256),
 ])
 @pytest.mark.parametrize("epi", EPIS)
 def test_inner_tile_kernel_equals_staged_kernel(dtype, B, n, m, d, epi):

@@ -644,7 +644,7 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
             }
             return o;
         },
-        out, b, row0, col0, n, m);
+        out, b, row0, col0, n, m, sizeof(OutT) == 2 && (m & 7) != 0);
     }
 }
 
@@ -739,11 +739,13 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
     const bool direct = vec && d % Elem<T>::kChunk == 0 && d > 0 && (n > m ? n : m) * d < ((int64_t)1 << 31);
     if constexpr (EPI != kEpiPoly) {
         // the tile kernel: byte offsets below 2^32, whole 16-byte units per output row (and, for
-        // the gradient products, 16-byte aligned X rows).  Ragged fp32 rows stay on the staged
-        // kernel: the tile store's dword rows cost the matrix-core-bound products more
-        // (16384 x 16383 x 128 euclidean 0.676 -> 0.716 ms)
+        // the gradient products, 16-byte aligned X rows).  bf16 outputs of the distance
+        // epilogues also take ragged rows (store_tile's unit + head / tail stores).  Ragged fp32
+        // rows stay on the staged kernel: the tile store's dword rows cost the matrix-core-bound
+        // products more (16384 x 16383 x 128 euclidean 0.676 -> 0.716 ms)
+        constexpr bool kRaggedOk = sizeof(OutT) == 2 && EPI != kEpiGrad && EPI != kEpiGradA;
         if (direct && (n > m ? n : m) * d * (int64_t)sizeof(T) < ((int64_t)1 << 32) && aligned16(out) &&
-            m % (16 / (int64_t)sizeof(OutT)) == 0 && (EPI != kEpiGrad || aligned16(X))) {
+            (m % (16 / (int64_t)sizeof(OutT)) == 0 || kRaggedOk) && (EPI != kEpiGrad || aligned16(X))) {
             // long K (16 chunks or more): two operand buffers, the next chunk's DMA in flight
             // while the current one is multiplied, at two blocks per CU
             if (d * (int64_t)sizeof(T) >= 16 * 128)

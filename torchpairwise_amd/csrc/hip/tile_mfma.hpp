@@ -306,8 +306,9 @@ __device__ __forceinline__ void store_wave_rows_bf16(uint4 *sl, F &&value, uint1
 // g) returns the 4 outputs of the lane's register quad g of block (mi, ni) as float: row
 // wr + 32 mi + l32, columns wc + 32 ni + 8 g + 4 h + (0..3).  Rows >= n and columns >= m are not
 // stored; m must be a multiple of 16 / sizeof(OutT) and out 16-byte aligned (a 16-byte store
-// unit is then wholly inside or outside), except that fp32 outputs take any m with `ragged`
-// set (m % 4 != 0: dword row stores, store_wave_rows_f32).  bf16 stages the rounded values of the whole tile (one
+// unit is then wholly inside or outside), except that fp32 and bf16 outputs take any m with
+// `ragged` set (fp32: dword row stores, store_wave_rows_f32; bf16: whole 16-byte units
+// funnel-shifted from the stage, 2-byte stores for each row piece's head and tail).  bf16 stages the rounded values of the whole tile (one
 // pass of 128 rows x 256 bytes, one workgroup barrier); fp32 per wave (store_wave_rows_f32, an
 // 8 KiB slice each).  Stage unit u of row r sits at u ^ (r & 15): conflict-free 16-byte accesses
 // across 16 rows and within 16-unit groups.
@@ -368,6 +369,50 @@ __device__ __forceinline__ void store_tile(uint4 *st, F &&value, OutT *__restric
             }
         }
         barrier_lds();
+        if constexpr (sizeof(OutT) == 2) {
+            if (ragged) {
+                // rows of m % 8 != 0 values: a row piece starts anywhere inside a 16-byte unit
+                // (out itself 16-byte aligned).  16 lanes per row write the piece's whole units,
+                // each funnel-shifted from two stage units; then 16 lanes per row its head and
+                // tail values (at most 7 + 7), 2 bytes each.
+                static_assert(NPASS == 1 && RPI == 4, "bf16 stage geometry");
+                const int j = lane & 15, rq = lane >> 4;
+                const uint16_t *sh = reinterpret_cast<const uint16_t *>(st);
+                const int V = (int)(m - col0 < kT ? m - col0 : kT);  // values in the piece
+#pragma unroll 2
+                for (int it = 0; it < ITERS; ++it) {
+                    const int r = (wave * ITERS + it) * RPI + rq;
+                    const int64_t grow = row0 + r;
+                    if (grow >= n) continue;
+                    const int64_t e0 = (b * n + grow) * m + col0;  // the piece's first value
+                    const int sft = (int)((8 - (e0 & 7)) & 7);     // values before the first unit
+                    const int K = V > sft ? (V - sft) >> 3 : 0;    // whole units
+                    if (j < K) {
+                        const int c0 = sft + 8 * j, u0 = c0 >> 3;  // value c0 sits at c0 & 7 = sft
+                        const u32x4 A = reinterpret_cast<const u32x4 *>(st)[r * UPR + (u0 ^ (r & XM))];
+                        const u32x4 B = sft != 0 ? reinterpret_cast<const u32x4 *>(st)[r * UPR + ((u0 + 1) ^ (r & XM))] : A;
+                        const uint32_t w[8] = {A[0], A[1], A[2], A[3], B[0], B[1], B[2], B[3]};
+                        const int q = sft >> 1;
+                        u32x4 o;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const uint32_t lo = q == 0 ? w[k] : q == 1 ? w[k + 1] : q == 2 ? w[k + 2] : w[k + 3];
+                            const uint32_t hi = q == 0 ? w[k + 1] : q == 1 ? w[k + 2] : q == 2 ? w[k + 3] : w[k + 4];
+                            o[k] = (sft & 1) ? (lo >> 16) | (hi << 16) : lo;
+                        }
+                        store16<kNT>(reinterpret_cast<u32x4 *>(out + e0 + c0), o);
+                    }
+                    const int headN = sft < V ? sft : V, tail0 = sft + 8 * K;
+                    const int tailN = V > tail0 ? V - tail0 : 0;
+                    if (j < headN + tailN) {
+                        const int c = j < headN ? j : tail0 + (j - headN);
+                        store16<kNT>(reinterpret_cast<uint16_t *>(out + e0 + c),
+                                     sh[(r * UPR + ((c >> 3) ^ (r & XM))) * 8 + (c & 7)]);
+                    }
+                }
+                return;
+            }
+        }
         const int ul = lane % LPR, rl = lane / LPR;
         const int64_t gcol = col0 + ul * (16 / (int)sizeof(OutT));
 #pragma unroll

@@ -465,7 +465,9 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
 // row-segment stores.  AK / BK: x1 / x2 stored k-major, [d, n] / [d, m] (the backward's products
 // read W^T, x1 and x2 that way, without a transposed copy); bf16 k-major pieces come from two
 // transposing LDS reads each.
-template <typename T, typename OutT, int EPI, int NB = 1, bool AK = false, bool BK = false>
+// RG: bf16 output rows of m % 8 != 0 values (store_tile's ragged mode), a separate
+// instantiation so that the aligned kernels' code is unchanged by it.
+template <typename T, typename OutT, int EPI, int NB = 1, bool AK = false, bool BK = false, bool RG = false>
 __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_kernel(
     const T *__restrict__ x1, const T *__restrict__ x2, int64_t n, int64_t m, int64_t d,
     const float *__restrict__ aux1, const float *__restrict__ aux2, OutT *__restrict__ out,
@@ -644,7 +646,7 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
             }
             return o;
         },
-        out, b, row0, col0, n, m, sizeof(OutT) == 2 && (m & 7) != 0);
+        out, b, row0, col0, n, m, RG);
     }
 }
 
@@ -748,6 +750,19 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
             (m % (16 / (int64_t)sizeof(OutT)) == 0 || kRaggedOk) && (EPI != kEpiGrad || aligned16(X))) {
             // long K (16 chunks or more): two operand buffers, the next chunk's DMA in flight
             // while the current one is multiplied, at two blocks per CU
+            if constexpr (kRaggedOk) {
+                if (m % (16 / (int64_t)sizeof(OutT)) != 0) {
+                    if (d * (int64_t)sizeof(T) >= 16 * 128)
+                        hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 2, false, false, true>), dim3((unsigned)total),
+                                           dim3(tile::kThreads), 0, s, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
+                                           tiles_m, total, kp, X, sign);
+                    else
+                        hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 1, false, false, true>), dim3((unsigned)total),
+                                           dim3(tile::kThreads), 0, s, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
+                                           tiles_m, total, kp, X, sign);
+                    return check_launch("inner_tile_kernel");
+                }
+            }
             if (d * (int64_t)sizeof(T) >= 16 * 128)
                 hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 2>), dim3((unsigned)total), dim3(tile::kThreads), 0,
                                    s, x1, x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp, X, sign);

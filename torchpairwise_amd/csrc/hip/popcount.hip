@@ -779,8 +779,9 @@ __device__ __forceinline__ void pops_to_float(bool small, uint32_t *s_pop) {
 // column wc + 32 ni + 8 g + 4 h + e of the tile).  Rows of at most kSmallRowLimit features
 // finish in float (finish_small, popcounts already floats in s_pop), longer rows on integer
 // counts (finish); both give the same bits.  Any m: rows of m % 4 != 0 floats are written a
-// dword per lane (the ragged mode of tile::store_tile).
-template <int OP, int EPI>
+// dword per lane (the ragged mode of tile::store_tile), a separate instantiation (RAGGED) so
+// that the aligned kernels' code is unchanged by it.
+template <int OP, int EPI, bool RAGGED>
 __device__ __forceinline__ void bool_tile_store(bool small, const floatx16 (&facc)[2][2], uint4 *smem,
                                                 const uint32_t *s_pop, int wr, int wc, int l32, int h, int64_t d,
                                                 double inv_d, float inv_df, float *__restrict__ out, int64_t b,
@@ -802,7 +803,7 @@ __device__ __forceinline__ void bool_tile_store(bool small, const floatx16 (&fac
                 for (int e = 0; e < 4; ++e) o[e] = finish_small<OP, EPI>(facc[mi][ni][4 * g + e], pav[mi], pbe[e], df, inv_df);
                 return o;
             },
-            out, b, row0, col0, n, m, (m & 3) != 0);
+            out, b, row0, col0, n, m, RAGGED);
         return;
     }
     const uint32_t du = (uint32_t)d;
@@ -822,10 +823,10 @@ __device__ __forceinline__ void bool_tile_store(bool small, const floatx16 (&fac
             }
             return o;
         },
-        out, b, row0, col0, n, m, (m & 3) != 0);
+        out, b, row0, col0, n, m, RAGGED);
 }
 
-template <int OP, int EPI>
+template <int OP, int EPI, bool RAGGED>
 __global__ __launch_bounds__(tile::kThreads, 4) void bool_fp4_tile_kernel(
     const uint8_t *__restrict__ x1, const uint8_t *__restrict__ x2, const int32_t *__restrict__ popA,
     const int32_t *__restrict__ popB, int64_t n, int64_t m, int64_t d, int64_t rb, double inv_d, float inv_df,
@@ -889,7 +890,7 @@ __global__ __launch_bounds__(tile::kThreads, 4) void bool_fp4_tile_kernel(
     const bool small = d <= kSmallRowLimit;
     pops_to_float(small, s_pop);
     barrier_lds();  // the operand buffer becomes the output stage
-    bool_tile_store<OP, EPI>(small, facc, smem, s_pop, wr, wc, l32, h, d, inv_d, inv_df, out, b, row0, col0, n, m);
+    bool_tile_store<OP, EPI, RAGGED>(small, facc, smem, s_pop, wr, wc, l32, h, d, inv_d, inv_df, out, b, row0, col0, n, m);
 }
 
 // The tile kernel of tile_mfma.hpp on bit-packed rows (W uint32 words per row, W % 4 == 0,
@@ -902,7 +903,7 @@ __global__ __launch_bounds__(tile::kThreads, 4) void bool_fp4_tile_kernel(
 // in-row piece into the slots past the row's end and zeroes them in LDS before use.  Counts, popcounts and the epilogue are those of
 // bool_fp4_tile_kernel, so the outputs are the same bit for bit.  Needs d < 2^24, a 16-byte
 // aligned output and rows * W * 4 < 2^32.
-template <int OP, int EPI>
+template <int OP, int EPI, bool RAGGED>
 __global__ __launch_bounds__(tile::kThreads, 4) void bool_bits_tile_kernel(
     const uint32_t *__restrict__ x1, const uint32_t *__restrict__ x2, const int32_t *__restrict__ popA,
     const int32_t *__restrict__ popB, int64_t n, int64_t m, int64_t d, int64_t W, double inv_d, float inv_df,
@@ -1005,7 +1006,7 @@ __global__ __launch_bounds__(tile::kThreads, 4) void bool_bits_tile_kernel(
     const bool small = d <= kSmallRowLimit;
     pops_to_float(small, s_pop);
     barrier_lds();  // the operand buffer becomes the output stage
-    bool_tile_store<OP, EPI>(small, facc, smem, s_pop, wr, wc, l32, h, d, inv_d, inv_df, out, b, row0, col0, n, m);
+    bool_tile_store<OP, EPI, RAGGED>(small, facc, smem, s_pop, wr, wc, l32, h, d, inv_d, inv_df, out, b, row0, col0, n, m);
 }
 
 // Whether bool_bits_tile_kernel takes these packed rows (W words per row) and output.
@@ -1029,8 +1030,12 @@ int launch_counts(const uint32_t *a, const uint32_t *b, const int32_t *pa, const
         const int64_t total = tiles_n * tiles_m * batch;
         const double inv_d = 1.0 / (double)d;
         const float inv_df = 1.0f / (float)d;
-        hipLaunchKernelGGL((bool_bits_tile_kernel<OP, EPI>), dim3((unsigned)total), dim3(tile::kThreads), 0, s, a, b,
-                           pa, pb, n, m, d, W, inv_d, inv_df, out, tiles_n, tiles_m, total);
+        if (m % 4 == 0)
+            hipLaunchKernelGGL((bool_bits_tile_kernel<OP, EPI, false>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                               s, a, b, pa, pb, n, m, d, W, inv_d, inv_df, out, tiles_n, tiles_m, total);
+        else
+            hipLaunchKernelGGL((bool_bits_tile_kernel<OP, EPI, true>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                               s, a, b, pa, pb, n, m, d, W, inv_d, inv_df, out, tiles_n, tiles_m, total);
         return check_launch("bool_bits_tile_kernel");
     }
     return launch_reduce<OP, EPI>(a, b, pa, pb, batch, n, m, d, out, s);
@@ -1047,8 +1052,14 @@ int launch_bool_fp4(const uint8_t *a, const uint8_t *b, const int32_t *pa, const
     const float inv_df = 1.0f / (float)d;
     const bool vec_store = m % 4 == 0 && aligned16(out);
     if (aligned16(out) && (n > m ? n : m) * fp4_row_bytes(d) < ((int64_t)1 << 32)) {
-        hipLaunchKernelGGL((bool_fp4_tile_kernel<OP, EPI>), dim3((unsigned)total), dim3(tile::kThreads), 0, s, a, b,
-                           pa, pb, n, m, d, fp4_row_bytes(d), inv_d, inv_df, out, tiles_n, tiles_m, total);
+        if (m % 4 == 0)
+            hipLaunchKernelGGL((bool_fp4_tile_kernel<OP, EPI, false>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                               s, a, b, pa, pb, n, m, d, fp4_row_bytes(d), inv_d, inv_df, out, tiles_n, tiles_m,
+                               total);
+        else
+            hipLaunchKernelGGL((bool_fp4_tile_kernel<OP, EPI, true>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                               s, a, b, pa, pb, n, m, d, fp4_row_bytes(d), inv_d, inv_df, out, tiles_n, tiles_m,
+                               total);
         return check_launch("bool_fp4_tile_kernel");
     }
     hipLaunchKernelGGL((bool_fp4_kernel<OP, EPI>), dim3((unsigned)total), dim3(kThreads), 0, s, a, b, pa, pb, n, m,

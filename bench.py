@@ -86,9 +86,10 @@ def parse():
                          "--pmc FETCH_SIZE / WRITE_SIZE pass has a known-size reference kernel")
     ap.add_argument("--config", default="M",
                     help="M (default: the metric's workload), C2..C5: time the other "
-                         "BASELINE.json configurations, NB: the neighbour masks and KF: the "
-                         "polynomial / sigmoid kernels at the metric shape (one JSON line per "
-                         "op, not the headline)")
+                         "BASELINE.json configurations, NB: the neighbour masks, KF: the "
+                         "polynomial / sigmoid kernels at the metric shape and RAGGED: shapes "
+                         "whose rows are not whole 16-byte units beside their aligned twins "
+                         "(one JSON line per op, not the headline)")
     return ap.parse_args()
 
 
@@ -337,6 +338,28 @@ def run_config(cfg, steps, warmup):
         ms, _ = time_op(dice_composite, steps, warmup)
         emit("dice fwd, reference composite route", ms, pf,
              roof("hbm", 4 * N * N, ms, "the fp32 output written once"))
+    elif cfg == "RAGGED":
+        # shapes whose rows are not whole 16-byte units (output m, or operand d) beside their
+        # aligned twins: euclidean fp32 / bf16, manhattan fp32, jaccard bool (forward)
+        g = torch.Generator().manual_seed(0)
+        for (n, m, d) in ((16384, 16384, 128), (16384, 16383, 128), (16384, 16384, 127), (16384, 16384, 130)):
+            x1, x2 = torch.randn(n, d, generator=g).to(dev), torch.randn(m, d, generator=g).to(dev)
+            pf = n * m * d
+            ms, _ = time_op(lambda: tp.euclidean_distances(x1, x2), steps, warmup)
+            emit(f"euclidean fp32 {n}x{m}x{d}", ms, pf, roof("mfma", 2 * pf, ms, "2 flops per pair-feature"))
+            ms, _ = time_op(lambda: tp.manhattan_distances(x1, x2), steps, warmup)
+            emit(f"manhattan fp32 {n}x{m}x{d}", ms, pf, roof("valu", 2 * pf, ms, "2 VALU lane-ops per pair-feature"))
+        for (n, m, d) in ((8192, 8192, 256), (8192, 8191, 256), (8192, 8192, 255)):
+            y1 = torch.randn(8, n, d, generator=g).to(dev).bfloat16()
+            y2 = torch.randn(8, m, d, generator=g).to(dev).bfloat16()
+            ms, _ = time_op(lambda: tp.euclidean_distances(y1, y2), steps, warmup)
+            emit(f"euclidean bf16 8x{n}x{m}x{d}", ms, 8 * n * m * d,
+                 roof("hbm", 2 * 8 * n * m, ms, "the bf16 output written once"))
+        for (n, m, d) in ((16384, 16384, 1024), (16384, 16383, 1024), (16384, 16384, 1023)):
+            b1 = (torch.rand(n, d, generator=g) < 0.3).to(dev)
+            b2 = (torch.rand(m, d, generator=g) < 0.3).to(dev)
+            ms, _ = time_op(lambda: tp.jaccard_distances(b1, b2), steps, warmup)
+            emit(f"jaccard bool {n}x{m}x{d}", ms, n * m * d, roof("hbm", 4 * n * m, ms, "the fp32 output written once"))
     elif cfg == "KF":
         # kernel functions at the metric shape: polynomial / sigmoid fused into the MFMA
         # epilogue, rbf / laplacian into the VALU kernel's, each against the reference's

@@ -12,15 +12,18 @@ value = pair-features/s (N*M*D per call / mean call time over the timed steps), 
 resident in HBM.  Timing: a clock-settle phase (the headline op called for --settle-ms of
 wall time, reported as settle_ms; the GPU leaves its idle clocks only after some tens of
 milliseconds of load), then W untimed warm-up steps, then K steps between two
-torch.cuda.synchronize() calls; per-kernel durations come from HIP events recorded on the
-stream the kernels are launched on (torch's current stream, which the C ABI receives).
+torch.cuda.synchronize() calls, one event pair around them; per-kernel durations come from HIP
+events stamped by the kernels' own dispatches on the stream they are launched on (torch's
+current stream, which the C ABI receives).
 
 roofline (dominant kernel = the MFMA pairwise kernel of euclidean):
   algorithmic flops per launch = 2*N*M*D (one multiply-add per pair-feature), peak = MI355X
-  dense FP32 MFMA 157.3 TFLOP/s; the launch duration is that kernel alone (the same launch
-  through the C ABI with the row norms computed once, K + W steps of its own), timed with
-  events on the launch stream.  Defaults W = K = 200: shorter warm-ups time the clock ramp
-  out of idle.
+  dense FP32 MFMA 157.3 TFLOP/s; the launch duration is the mean device time of the
+  tile-kernel launch inside each of the K timed steps themselves: the C ABI's launch timer
+  (tpw_launch_timer_arm / _read) hands the launch a start / stop event pair that its own
+  dispatch stamps (hipExtLaunchKernelGGL), so kernel_ms <= ms_per_step holds by construction
+  and is asserted.  The extras (manhattan,
+  hamming) report their dominant kernels the same way.  Defaults W = K = 200.
 cpu_baseline: the reference's CPU path for euclidean_distances is at::cdist(p=2) -> on the
   host cores via torch.cdist, timed on a bounded row sample of the same workload; beside it
   manhattan (at::cdist p = 1), and the reference's own compiled CPU kernels (oracle/_ref, in a
@@ -41,8 +44,9 @@ import time
 PEAK_FP32_MFMA = 157.3e12
 PEAK_BF16_MFMA = 2.5e15
 PEAK_HBM = 8.0e12
-# FP32 vector peak 157.3 TFLOP/s = 256 CU x 4 SIMD x 32 lanes x 2 (FMA) x 2.4 GHz: a
-# non-packed VALU issue rate of 7.86e13 lane-ops/s
+# FP32 vector peak 157.3 TFLOP/s = 256 CU x 4 SIMD x 32 lanes x 2 (FMA) x 2.4 GHz.  As an
+# issue rate of non-packed VALU instructions that is 7.86e13 lane-ops/s only with dual issue
+# (two VALU instructions of a wave pair per clock): the dual-issue rate
 PEAK_VALU_LANE_OPS = 256 * 4 * 32 * 2.4e9
 # the headline's dominant kernel as rocprofv3 names it (euclidean epilogue, fp32 in and out)
 HEADLINE_KERNEL = "inner_tile_kernel<float,float,1,1,false,false>"
@@ -96,7 +100,12 @@ def parse():
 _SETTLE = {"ms": 0.0, "done": False, "spent": 0.0}
 
 
-def time_op(fn, steps, warmup):
+def time_op(fn, steps, warmup, family=None):
+    """Time per call (ms) of fn over `steps` back-to-back calls after `warmup` untimed ones (one
+    event pair around the whole timed loop), and the wall time per call.  With `family`, also
+    the mean device duration of that kernel family's launches made by those same timed calls
+    (start / stop events stamped by each launch's own dispatch through the C ABI's launch
+    timer): (step_ms, wall_ms, kernel_ms, launches_per_step)."""
     import torch
 
     if not _SETTLE["done"] and _SETTLE["ms"] > 0:  # once per process, before the first timing
@@ -106,17 +115,29 @@ def time_op(fn, steps, warmup):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    timer = None
+    if family is not None:
+        from torchpairwise_amd import _capi as capi
+
+        timer = capi.LaunchTimer(family, 64 * steps).arm()
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record(stream)
+    start.record(stream)
+    for _ in range(steps):
         fn()
-        ends[i].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ev_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
-    return ev_ms, wall * 1e3 / steps
+    ev_ms = start.elapsed_time(end) / steps
+    if timer is None:
+        return ev_ms, wall * 1e3 / steps
+    kms, dropped = timer.read()
+    assert kms and not dropped, f"launch timer for {family}: {len(kms)} launches, {dropped} dropped"
+    per_step = len(kms) / steps
+    k_ms = sum(kms) / steps  # the family's device time per step
+    # the kernels run inside the steps that contain them: their time cannot exceed the step's
+    assert k_ms <= ev_ms, f"{family}: kernel {k_ms:.4f} ms > step {ev_ms:.4f} ms"
+    return ev_ms, wall * 1e3 / steps, k_ms / per_step, per_step
 
 
 def settle(fn, ms):
@@ -291,7 +312,7 @@ def run_config(cfg, steps, warmup):
         pf = N * N * D
         ms, _ = time_op(lambda: tp.minkowski_distances(x1, x2, 3.0), steps, warmup)
         emit("minkowski p=3 fwd", ms, pf, roof("valu", 3 * pf, ms, "3 VALU lane-ops per pair-feature "
-                                               "(sub, |d| * d, fma) against the non-packed FP32 issue rate"))
+                                               "(sub, |d| * d, fma) against the FP32 VALU dual-issue rate"))
         a, b = x1.clone().requires_grad_(), x2.clone().requires_grad_()
         ones = torch.ones(N, N, device=dev)
 
@@ -512,14 +533,11 @@ def main():
 
     if "l2" in only:
         time_op(lambda: tp.euclidean_distances(x1, x2), 1, 0)  # the settle phase (once)
-        ms, wall_ms = time_op(lambda: tp.euclidean_distances(x1, x2), args.steps, args.warmup)
-        # the dominant kernel alone: the same MFMA launch through the C ABI with the row norms
-        # computed once, timed with events on the stream it is launched on (torch's current)
-        from torchpairwise_amd import _capi as capi
-
-        n1, n2 = capi.row_norms(x1, True), capi.row_norms(x2, True)
-        k_ms, _ = time_op(lambda: capi.pairwise_inner(x1, x2, capi.EPI_EUCLIDEAN, n1, n2),
-                          args.steps, args.warmup)
+        # the dominant kernel's launches are timed inside the op's own timed steps (events
+        # around each tile-kernel launch, on the stream the op launches on)
+        ms, wall_ms, k_ms, per_step = time_op(lambda: tp.euclidean_distances(x1, x2), args.steps,
+                                              args.warmup, family="inner_tile_kernel")
+        assert per_step == 1, f"{per_step} tile-kernel launches per euclidean_distances call"
         flops = 2.0 * n * n * d
         res["l2"] = {"ms": ms, "wall_ms": wall_ms, "value": pf / (ms * 1e-3),
                      "roofline": {"bound": "mfma", "achieved": flops / (k_ms * 1e-3) / 1e12,
@@ -527,30 +545,39 @@ def main():
                                   "frac": flops / (k_ms * 1e-3) / PEAK_FP32_MFMA,
                                   "traffic": measured_traffic(HEADLINE_KERNEL),
                                   "kernel": HEADLINE_KERNEL,
-                                  "kernel_ms": k_ms}}
+                                  "kernel_ms": k_ms,
+                                  "timing": "mean device duration of the tile-kernel launch inside "
+                                            "each timed step (start / stop events stamped by "
+                                            "the launch's own dispatch on the op's stream); "
+                                            "kernel_ms <= ms_per_step is asserted"}}
     if "l1" in only:
-        ms, wall_ms = time_op(lambda: tp.manhattan_distances(x1, x2), args.steps, args.warmup)
+        ms, wall_ms, k_ms, _ = time_op(lambda: tp.manhattan_distances(x1, x2), args.steps, args.warmup,
+                                       family="lp_forward_kernel")
         ops = 2.0 * pf  # v_sub + abs-modified v_add per pair-feature
         extra["manhattan_fp32"] = {
             "value": pf / (ms * 1e-3), "ms_per_call": ms,
-            "roofline": {"bound": "valu", "achieved": ops / (ms * 1e-3) / 1e12,
+            "roofline": {"bound": "valu", "achieved": ops / (k_ms * 1e-3) / 1e12,
                          "peak": PEAK_VALU_LANE_OPS / 1e12, "unit": "Tlane-op/s",
-                         "frac": ops / (ms * 1e-3) / PEAK_VALU_LANE_OPS,
+                         "frac": ops / (k_ms * 1e-3) / PEAK_VALU_LANE_OPS,
+                         "kernel": "lp_forward_kernel<0,1,true>", "kernel_ms": k_ms,
                          "convention": "2 VALU lane-ops per pair-feature (v_sub_f32, abs-modified "
-                                       "v_add_f32) against the non-packed FP32 issue rate "
-                                       "256 CU x 4 SIMD x 32 lanes x 2.4 GHz; against the "
-                                       "157.3 TFLOP/s spec counting each op as one flop the "
-                                       "fraction is half of this"}}
+                                       "v_add_f32) against the FP32 VALU issue rate with dual "
+                                       "issue, 256 CU x 4 SIMD x 32 lanes x 2 x 2.4 GHz = 7.86e13 "
+                                       "lane-ops/s (157.3 TFLOP/s counts an FMA as 2 flops; "
+                                       "neither op here is an FMA, so against that spec, one "
+                                       "flop per op, the fraction is half of this)"}}
     if "hamming" in only:
-        ms, wall_ms = time_op(lambda: tp.hamming_distances(b1, b2), args.steps, args.warmup)
+        ms, wall_ms, k_ms, _ = time_op(lambda: tp.hamming_distances(b1, b2), args.steps, args.warmup,
+                                       family="bool_reduce_kernel")
         out_bytes = 4.0 * n * n
         extra["hamming_bool"] = {
             "value": pf / (ms * 1e-3), "ms_per_call": ms,
-            "roofline": {"bound": "hbm", "achieved": out_bytes / (ms * 1e-3) / 1e9,
+            "roofline": {"bound": "hbm", "achieved": out_bytes / (k_ms * 1e-3) / 1e9,
                          "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                         "frac": out_bytes / (ms * 1e-3) / PEAK_HBM,
+                         "frac": out_bytes / (k_ms * 1e-3) / PEAK_HBM,
+                         "kernel": "bool_reduce_kernel<2,1,64,2>", "kernel_ms": k_ms,
                          "note": "algorithmic bytes = the fp32 output (inputs are 2 x 2 MiB, "
-                                 "packed to 2 x 256 KiB); includes the pack launches"}}
+                                 "packed to 2 x 256 KiB); ms_per_call includes the pack launches"}}
 
     head = res.get("l2")
     line = {

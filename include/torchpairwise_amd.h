@@ -54,6 +54,19 @@ const char *tpw_last_error(void);
  * which returned CUDA_VERSION or -1. */
 int tpw_runtime_version(void);
 
+/* Launch timer (measurement support; no counterpart in the reference).  Arms HIP event
+ * pairs around every launch of one kernel family ("inner_tile_kernel",
+ * "pairwise_inner_kernel", "lp_forward_kernel", "bool_reduce_kernel",
+ * "bool_bits_tile_kernel") made on the current device, at most `capacity` launches (later ones
+ * are counted as dropped).  Events are recorded on the stream each launch goes to, so a caller
+ * reads the device duration of the launches inside its own timed loop.  Creates events the
+ * first time (no device memory).  Not for concurrent use from several threads. */
+int tpw_launch_timer_arm(const char *family, int capacity);
+/* Disarms the timer, waits for the recorded events and writes the first min(count,
+ * capacity) launch durations in ms to ms[]; *count = launches recorded, *dropped (may be
+ * NULL) = launches past the armed capacity. */
+int tpw_launch_timer_read(float *ms, int capacity, int *count, int *dropped);
+
 /* ------------------------------------------------------------------------- */
 /* Bit-packed boolean family (hamming, jaccard, pw*_sum / pw*_mean on bool)   */
 /* ------------------------------------------------------------------------- */

@@ -28,6 +28,8 @@ _i64, _p, _i, _d, _sz = C.c_int64, C.c_void_p, C.c_int, C.c_double, C.c_size_t
 _SIGNATURES = {
     "tpw_last_error": (C.c_char_p, []),
     "tpw_runtime_version": (_i, []),
+    "tpw_launch_timer_arm": (_i, [C.c_char_p, _i]),
+    "tpw_launch_timer_read": (_i, [_p, _i, _p, _p]),
     "tpw_packed_words": (_i64, [_i64]),
     "tpw_pack_bool_rows": (_i, [_p, _i64, _i64, _p, _p, _p]),
     "tpw_bool_pairwise_reduce": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
@@ -139,6 +141,24 @@ def call(name: str, *args) -> int:
 # --------------------------------------------------------------------------------------
 # torch-tensor conveniences (device tensors only; nothing here falls back to the CPU)
 # --------------------------------------------------------------------------------------
+class LaunchTimer:
+    """Device durations (ms) of every launch of one kernel family made while armed, from HIP
+    events recorded on the launch's own stream (``tpw_launch_timer_arm`` / ``_read``)."""
+
+    def __init__(self, family: str, capacity: int):
+        self.family, self.capacity = family, capacity
+
+    def arm(self):
+        call("tpw_launch_timer_arm", self.family.encode(), self.capacity)
+        return self
+
+    def read(self):
+        buf = (C.c_float * self.capacity)()
+        count, dropped = C.c_int(0), C.c_int(0)
+        call("tpw_launch_timer_read", C.cast(buf, C.c_void_p), self.capacity, C.byref(count), C.byref(dropped))
+        return [float(buf[i]) for i in range(min(count.value, self.capacity))], dropped.value
+
+
 def _ptr(t):
     return None if t is None else C.c_void_p(t.data_ptr())
 

@@ -1,6 +1,7 @@
 // Shared helpers of the gfx950 kernel library (device side and host side).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -13,6 +14,15 @@ void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 
 // Turns a pending launch failure into TPW_ERR_LAUNCH (with a message naming `what`).
 int check_launch(const char *what);
+
+// Start / stop events for one kernel launch (hipExtLaunchKernelGGL stamps them as part of the
+// dispatch, so they add no packets of their own): a free event pair of the launch timer when
+// tpw_launch_timer_arm armed it for this kernel family on the current device, else null events
+// (a plain launch).  launch_timer.hip.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents launch_events(const char *family);
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

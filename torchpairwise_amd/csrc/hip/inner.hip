@@ -748,34 +748,36 @@ int launch_inner(const T *x1, const T *x2, int64_t batch, int64_t n, int64_t m, 
         constexpr bool kRaggedOk = sizeof(OutT) == 2 && EPI != kEpiGrad && EPI != kEpiGradA;
         if (direct && (n > m ? n : m) * d * (int64_t)sizeof(T) < ((int64_t)1 << 32) && aligned16(out) &&
             (m % (16 / (int64_t)sizeof(OutT)) == 0 || kRaggedOk) && (EPI != kEpiGrad || aligned16(X))) {
+            const LaunchEvents ev = launch_events("inner_tile_kernel");
             // long K (16 chunks or more): two operand buffers, the next chunk's DMA in flight
             // while the current one is multiplied, at two blocks per CU
             if constexpr (kRaggedOk) {
                 if (m % (16 / (int64_t)sizeof(OutT)) != 0) {
                     if (d * (int64_t)sizeof(T) >= 16 * 128)
-                        hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 2, false, false, true>), dim3((unsigned)total),
-                                           dim3(tile::kThreads), 0, s, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
+                        hipExtLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 2, false, false, true>), dim3((unsigned)total),
+                                           dim3(tile::kThreads), 0, s, ev.start, ev.stop, 0, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
                                            tiles_m, total, kp, X, sign);
                     else
-                        hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 1, false, false, true>), dim3((unsigned)total),
-                                           dim3(tile::kThreads), 0, s, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
+                        hipExtLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 1, false, false, true>), dim3((unsigned)total),
+                                           dim3(tile::kThreads), 0, s, ev.start, ev.stop, 0, x1, x2, n, m, d, aux1, aux2, out, tiles_n,
                                            tiles_m, total, kp, X, sign);
                     return check_launch("inner_tile_kernel");
                 }
             }
             if (d * (int64_t)sizeof(T) >= 16 * 128)
-                hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 2>), dim3((unsigned)total), dim3(tile::kThreads), 0,
-                                   s, x1, x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp, X, sign);
+                hipExtLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 2>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                                   s, ev.start, ev.stop, 0, x1, x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp, X, sign);
             else
-                hipLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 1>), dim3((unsigned)total), dim3(tile::kThreads), 0,
-                                   s, x1, x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp, X, sign);
+                hipExtLaunchKernelGGL((inner_tile_kernel<T, OutT, EPI, 1>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                                   s, ev.start, ev.stop, 0, x1, x2, n, m, d, aux1, aux2, out, tiles_n, tiles_m, total, kp, X, sign);
             return check_launch("inner_tile_kernel");
         }
     }
+    const LaunchEvents ev = launch_events("pairwise_inner_kernel");
     auto kernel = direct ? pairwise_inner_kernel<T, OutT, EPI, true, true>
                   : vec  ? pairwise_inner_kernel<T, OutT, EPI, true, false>
                          : pairwise_inner_kernel<T, OutT, EPI, false, false>;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(kThreads), 0, s, x1, x2, n, m, d, aux1,
+    hipExtLaunchKernelGGL(kernel, dim3((unsigned)total), dim3(kThreads), 0, s, ev.start, ev.stop, 0, x1, x2, n, m, d, aux1,
                        aux2, out, tiles_n, tiles_m, total, X, sign, kp);
     return check_launch("pairwise_inner_kernel");
 }
@@ -926,12 +928,13 @@ template <typename T, int EPI, bool AK, bool BK>
 int launch_grad_product(const T *A, const T *B, int64_t batch, int64_t M, int64_t N, int64_t K, float sign,
                         const float *coef, const T *X, T *out, hipStream_t s) {
     const int64_t tiles_n = cdiv(M, kTile), tiles_m = cdiv(N, kTile), total = tiles_n * tiles_m * batch;
+    const LaunchEvents ev = launch_events("inner_tile_kernel");
     if (K * (int64_t)sizeof(T) >= 16 * 128)
-        hipLaunchKernelGGL((inner_tile_kernel<T, T, EPI, 2, AK, BK>), dim3((unsigned)total), dim3(tile::kThreads), 0,
-                           s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total, KerParams{}, X, sign);
+        hipExtLaunchKernelGGL((inner_tile_kernel<T, T, EPI, 2, AK, BK>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                           s, ev.start, ev.stop, 0, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total, KerParams{}, X, sign);
     else
-        hipLaunchKernelGGL((inner_tile_kernel<T, T, EPI, 1, AK, BK>), dim3((unsigned)total), dim3(tile::kThreads), 0,
-                           s, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total, KerParams{}, X, sign);
+        hipExtLaunchKernelGGL((inner_tile_kernel<T, T, EPI, 1, AK, BK>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                           s, ev.start, ev.stop, 0, A, B, M, N, K, coef, nullptr, out, tiles_n, tiles_m, total, KerParams{}, X, sign);
     return check_launch("inner_tile_kernel");
 }
 

@@ -329,13 +329,14 @@ int launch_reduce(const uint32_t *a, const uint32_t *b, const int32_t *pa, const
     const double inv_d = d < (int64_t)kFloatExactLimit ? 1.0 / (double)d : 0.0;
     const float inv_df = 1.0f / (float)d;  // as ATen's host-side reciprocal of a CPU scalar
     const bool vec_store = (m % 4 == 0) && aligned16(out);
+    const LaunchEvents ev = launch_events("bool_reduce_kernel");
     if (W <= 8 && m > 256 && cdiv(n, 32) <= kMaxGridYZ) {
         dim3 grid((unsigned)cdiv(m, 512), (unsigned)cdiv(n, 32), (unsigned)batch);
-        hipLaunchKernelGGL((bool_reduce_kernel<OP, EPI, 64, 2>), grid, dim3(kThreads), 0, s, a, b,
+        hipExtLaunchKernelGGL((bool_reduce_kernel<OP, EPI, 64, 2>), grid, dim3(kThreads), 0, s, ev.start, ev.stop, 0, a, b,
                            pa, pb, n, m, W, d, inv_d, inv_df, out, vec_store);
     } else {
         dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
-        hipLaunchKernelGGL((bool_reduce_kernel<OP, EPI, 16, kChunkVec>), grid, dim3(kThreads), 0, s,
+        hipExtLaunchKernelGGL((bool_reduce_kernel<OP, EPI, 16, kChunkVec>), grid, dim3(kThreads), 0, s, ev.start, ev.stop, 0,
                            a, b, pa, pb, n, m, W, d, inv_d, inv_df, out, vec_store);
     }
     return check_launch("bool_reduce_kernel");
@@ -1030,12 +1031,13 @@ int launch_counts(const uint32_t *a, const uint32_t *b, const int32_t *pa, const
         const int64_t total = tiles_n * tiles_m * batch;
         const double inv_d = 1.0 / (double)d;
         const float inv_df = 1.0f / (float)d;
+        const LaunchEvents ev = launch_events("bool_bits_tile_kernel");
         if (m % 4 == 0)
-            hipLaunchKernelGGL((bool_bits_tile_kernel<OP, EPI, false>), dim3((unsigned)total), dim3(tile::kThreads), 0,
-                               s, a, b, pa, pb, n, m, d, W, inv_d, inv_df, out, tiles_n, tiles_m, total);
+            hipExtLaunchKernelGGL((bool_bits_tile_kernel<OP, EPI, false>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                               s, ev.start, ev.stop, 0, a, b, pa, pb, n, m, d, W, inv_d, inv_df, out, tiles_n, tiles_m, total);
         else
-            hipLaunchKernelGGL((bool_bits_tile_kernel<OP, EPI, true>), dim3((unsigned)total), dim3(tile::kThreads), 0,
-                               s, a, b, pa, pb, n, m, d, W, inv_d, inv_df, out, tiles_n, tiles_m, total);
+            hipExtLaunchKernelGGL((bool_bits_tile_kernel<OP, EPI, true>), dim3((unsigned)total), dim3(tile::kThreads), 0,
+                               s, ev.start, ev.stop, 0, a, b, pa, pb, n, m, d, W, inv_d, inv_df, out, tiles_n, tiles_m, total);
         return check_launch("bool_bits_tile_kernel");
     }
     return launch_reduce<OP, EPI>(a, b, pa, pb, batch, n, m, d, out, s);

@@ -768,11 +768,12 @@ int launch_forward(const float *x1, const float *x2, const float *w, int64_t bat
     dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
     const bool vec = (d % 4 == 0) && aligned16(x1) && aligned16(x2) && aligned16(out);
     const float pf = (float)p, inv_p = (float)(1.0 / p);
+    const LaunchEvents ev = launch_events("lp_forward_kernel");
     if (vec)
-        hipLaunchKernelGGL((lp_forward_kernel<MODE, PK, true>), grid, dim3(kThreads), 0, s, x1, x2,
+        hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, true>), grid, dim3(kThreads), 0, s, ev.start, ev.stop, 0, x1, x2,
                            w, n, m, d, pf, inv_p, out, (int)exp_post, post);
     else
-        hipLaunchKernelGGL((lp_forward_kernel<MODE, PK, false>), grid, dim3(kThreads), 0, s, x1,
+        hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, false>), grid, dim3(kThreads), 0, s, ev.start, ev.stop, 0, x1,
                            x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post);
     return check_launch("lp_forward_kernel");
 }

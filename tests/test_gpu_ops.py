@@ -385,6 +385,41 @@ def test_family_ops_gpu_equal_reference(tmp_path):
                               {k: v for k, v in r.items() if k.startswith("grad")}, 1e-4, what, exact)
 
 
+def test_lp_inf_backward_long_rows_equal_reference(tmp_path):
+    """The p = +-inf backward past the LDS accumulator's size (4096 features, 2048 weighted):
+    _ppminkowski and _wminkowski at d = 5000 with random and tie-heavy integer inputs against
+    the reference's compiled CPU kernels (oracle/_ref); grad_x1 and grad_x2 bit for bit, the
+    weight gradient rtol 1e-4, the forward rtol 1e-5."""
+    from oracle import ref_runner
+    from tests._family_cases import _g, _inputs
+    from tests.test_reference_pin import _assert_results_close
+
+    if not ref_runner.available():
+        pytest.skip("oracle/_ref not built")
+    d = 5000
+    cs = []
+    for kind in ("normal", "ties"):
+        a, b, g = _inputs((21, d), (13, d), torch.float32, 7, kind)
+        w = torch.rand((d,), generator=_g(8), dtype=torch.float64).float() + 0.25
+        for p in (float("inf"), float("-inf")):
+            cs.append(({"op": "_ppminkowski", "args": [{"t": "a"}, {"t": "b"}, {"v": p}], "req": ["a", "b"],
+                        "grad": "g", "kind": f"p={p} {kind}"}, {"a": a, "b": b, "g": g}))
+            cs.append(({"op": "_wminkowski", "args": [{"t": "a"}, {"t": "b"}, {"t": "w"}, {"v": p}],
+                        "req": ["a", "b", "w"], "grad": "g", "kind": f"p={p} {kind}"},
+                       {"a": a, "b": b, "w": w, "g": g}))
+    ref = ref_runner.run_op_reference(cs, tmp_path)
+    ops = torch.ops.torchpairwise
+    for (case, tensors), r in zip(cs, ref):
+        what = f"{case['op']} {case['kind']} d={d}"
+        print(what, flush=True)
+        ours = ref_runner.run_op_case(ops, case, tensors, DEV)
+        _assert_results_close({k: v for k, v in ours.items() if k.startswith("out")},
+                              {k: v for k, v in r.items() if k.startswith("out")}, 1e-5, what)
+        _assert_results_close({k: v for k, v in ours.items() if k.startswith("grad")},
+                              {k: v for k, v in r.items() if k.startswith("grad")}, 1e-4, what,
+                              ("grad_a", "grad_b"))
+
+
 def test_other_gpu_dtypes_served():
     """The cdist metrics, cosine, linear and Mahalanobis run float64 on the GPU (the VALU family,
     haversine and directed Hausdorff: test_gpu_float64.py)."""

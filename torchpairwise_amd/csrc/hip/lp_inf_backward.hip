@@ -9,9 +9,12 @@
 //     grad_w[k]     += g[i,j] * |d_k|                (weighted only)
 // with sgn(NaN) = sgn(0) = 0.  Here one wave owns one row of the side being differentiated and
 // walks the other side in index order, 64 partners per step (one per lane); the lanes' terms
-// are then added to the row's LDS accumulator one lane at a time in partner order, which is the
+// are then added to the row's accumulator one lane at a time in partner order, which is the
 // reference's order for grad_x1 (j ascending) and grad_x2 (i ascending), without atomics.  The
 // weight gradient is summed per row of x1 (j ascending) and the rows are then added in order.
+// The accumulator is the row's LDS slice while four waves' rows fit in LDS; past that (GACC) it
+// is the wave's own output row in global memory (and its wrows row), which no other wave
+// touches, so lane 0 alone zeroes it and adds into it in the same order: any d, same bits.
 #include "common.hpp"
 
 #pragma clang fp contract(off)
@@ -25,7 +28,7 @@ __device__ __forceinline__ float signum(float v) { return (float)((0.0f < v) - (
 
 // COLS = false: rows of x1 (output grad_x1, and per-row weight-gradient partials when W);
 // COLS = true: rows of x2 (output grad_x2), walking x1.
-template <bool NEG, bool W, bool COLS>
+template <bool NEG, bool W, bool COLS, bool GACC>
 __global__ __launch_bounds__(kWaves * 64) void lp_inf_grad_kernel(
     const float *__restrict__ g, const float *__restrict__ x1, const float *__restrict__ x2,
     const float *__restrict__ w, int64_t n, int64_t m, int64_t d, float *__restrict__ out,
@@ -35,12 +38,24 @@ __global__ __launch_bounds__(kWaves * 64) void lp_inf_grad_kernel(
     const int64_t b = blockIdx.y;
     const int64_t own_rows = COLS ? m : n, other_rows = COLS ? n : m;
     const int64_t r = (int64_t)blockIdx.x * kWaves + wave;
-    float *acc = lds + (int64_t)wave * (W && !COLS ? 2 : 1) * d;
-    float *gacc = acc + d;  // weight-gradient partial of this row (W, rows pass)
     if (r >= own_rows) return;  // a whole wave: no block-wide barrier follows
-    for (int64_t k = lane; k < d; k += 64) {
-        acc[k] = 0.0f;
-        if constexpr (W && !COLS) gacc[k] = 0.0f;
+    float *dst = out + (b * own_rows + r) * d;
+    float *wdst = W && !COLS ? wrows + (b * n + r) * d : nullptr;
+    // LDS slices, or (GACC) the wave's own rows of out / wrows
+    float *acc = GACC ? dst : lds + (int64_t)wave * (W && !COLS ? 2 : 1) * d;
+    float *gacc = GACC ? wdst : acc + d;  // weight-gradient partial of this row (W, rows pass)
+    if constexpr (GACC) {
+        // one lane zeroes and later updates the rows, so every access to them is in its order
+        if (lane == 0)
+            for (int64_t k = 0; k < d; ++k) {
+                acc[k] = 0.0f;
+                if constexpr (W && !COLS) gacc[k] = 0.0f;
+            }
+    } else {
+        for (int64_t k = lane; k < d; k += 64) {
+            acc[k] = 0.0f;
+            if constexpr (W && !COLS) gacc[k] = 0.0f;
+        }
     }
     const float *own = (COLS ? x2 + b * m * d : x1 + b * n * d) + r * d;
     const float *oth = COLS ? x1 + b * n * d : x2 + b * m * d;
@@ -83,20 +98,29 @@ __global__ __launch_bounds__(kWaves * 64) void lp_inf_grad_kernel(
             }
         }
     }
-    float *dst = out + (b * own_rows + r) * d;
-    for (int64_t k = lane; k < d; k += 64) {
-        dst[k] = acc[k];
-        if constexpr (W && !COLS) wrows[(b * n + r) * d + k] = gacc[k];
-    }
+    if constexpr (!GACC)
+        for (int64_t k = lane; k < d; k += 64) {
+            dst[k] = acc[k];
+            if constexpr (W && !COLS) wdst[k] = gacc[k];
+        }
 }
+
+// Largest feature count whose per-row accumulators (four waves' rows) live in LDS.
+int64_t lds_max_features(bool weighted) { return weighted ? 2048 : 4096; }
 
 template <bool NEG, bool W, bool COLS>
 int launch(const float *g, const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
            int64_t m, int64_t d, float *out, float *wrows, hipStream_t s) {
     const int64_t rows = COLS ? m : n;
-    const size_t lds = (size_t)kWaves * (W && !COLS ? 2 : 1) * d * sizeof(float);
-    hipLaunchKernelGGL((lp_inf_grad_kernel<NEG, W, COLS>), dim3((unsigned)cdiv(rows, kWaves), (unsigned)batch),
-                       dim3(kWaves * 64), lds, s, g, x1, x2, w, n, m, d, out, wrows);
+    const dim3 grid((unsigned)cdiv(rows, kWaves), (unsigned)batch);
+    if (d <= lds_max_features(W)) {
+        const size_t lds = (size_t)kWaves * (W && !COLS ? 2 : 1) * d * sizeof(float);
+        hipLaunchKernelGGL((lp_inf_grad_kernel<NEG, W, COLS, false>), grid, dim3(kWaves * 64), lds, s, g, x1, x2,
+                           w, n, m, d, out, wrows);
+    } else {
+        hipLaunchKernelGGL((lp_inf_grad_kernel<NEG, W, COLS, true>), grid, dim3(kWaves * 64), 0, s, g, x1, x2, w,
+                           n, m, d, out, wrows);
+    }
     return check_launch("lp_inf_grad_kernel");
 }
 
@@ -110,16 +134,10 @@ int run(const float *g, const float *x1, const float *x2, const float *w, int64_
 
 }  // namespace
 
-// Largest feature count of lp_inf_backward (its per-row accumulators live in LDS).
-int64_t lp_inf_backward_max_features(bool weighted) { return weighted ? 2048 : 4096; }
-
 // grad_x1 [batch, n, d], grad_x2 [batch, m, d] and, with w, the per-row weight-gradient
 // partials wrows [batch, n, d] (summed over rows by the caller); every element written.
 int lp_inf_backward(const float *g, const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
                     int64_t m, int64_t d, bool neg, float *gx1, float *gx2, float *wrows, hipStream_t s) {
-    TPW_REQUIRE(d <= lp_inf_backward_max_features(w != nullptr),
-                "the p = inf backward supports at most %lld features on the GPU (got %lld)",
-                (long long)lp_inf_backward_max_features(w != nullptr), (long long)d);
     TPW_REQUIRE(batch <= kMaxGridYZ && cdiv(n > m ? n : m, kWaves) <= 0x7fffffffLL, "sizes exceed the launch grid");
     if (w) return neg ? run<true, true>(g, x1, x2, w, batch, n, m, d, gx1, gx2, wrows, s)
                       : run<false, true>(g, x1, x2, w, batch, n, m, d, gx1, gx2, wrows, s);

@@ -158,7 +158,8 @@ def test_lp_forward(p, B, n, m, d):
 
 
 @pytest.mark.parametrize("p", [1.0, 1.5, 2.0, 3.0, 4.5, float("inf")])
-@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 40, 33, 5), (1, 700, 1100, 70), (1, 7, 9, 5)])
+@pytest.mark.parametrize("B,n,m,d", [(1, 130, 200, 64), (2, 40, 33, 5), (1, 700, 1100, 70), (1, 7, 9, 5),
+                                     (1, 300, 257, 128), (2, 65, 130, 200)])
 @pytest.mark.parametrize("entry", ["single", "both"])
 def test_lp_backward(p, B, n, m, d, entry):
     print(f"lp backward p={p} {B}x{n}x{m}x{d} {entry}", flush=True)

@@ -102,6 +102,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const float *base,
 __device__ __forceinline__ float buffer_load(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_offset, 0, 0));
 }
+// Four floats at a 16-byte aligned byte offset (whole in range or whole out: the caller keeps
+// array lengths and offsets multiples of 4 floats).
+typedef unsigned int tpw_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ floatx4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0));
+}
 
 // Parameters of the kernel-function epilogues (polynomial, sigmoid) of the MFMA kernel.
 struct KerParams {

@@ -117,6 +117,69 @@ __device__ __forceinline__ float min3_abs(float acc, float d0, float d1) {
     return r;
 }
 
+// Four independent accumulations of one row value a against four column values b[c], for the
+// p = 1, 2, 3 steps of lp_step, with the same operations and roundings: the four
+// subtractions first, then the four squares (p = 3), then the four accumulates.  A wave's
+// consecutive VALU instructions are then independent; as the compiler orders them (each
+// term's sub, mul and accumulate back to back) the SIMD issues the p = 3 step at about 62 %
+// of its rate at two waves per SIMD, interleaved four ways at about 85 %.
+template <int PK>
+__device__ __forceinline__ void lp_step4(float &c0, float &c1, float &c2, float &c3, float a, float b0, float b1,
+                                         float b2, float b3) {
+    float t0, t1, t2, t3;
+    if constexpr (PK == kP1) {
+        asm("v_sub_f32 %[t0], %[a], %[b0]\n\tv_sub_f32 %[t1], %[a], %[b1]\n\t"
+            "v_sub_f32 %[t2], %[a], %[b2]\n\tv_sub_f32 %[t3], %[a], %[b3]\n\t"
+            "v_add_f32_e64 %[c0], %[c0], |%[t0]|\n\tv_add_f32_e64 %[c1], %[c1], |%[t1]|\n\t"
+            "v_add_f32_e64 %[c2], %[c2], |%[t2]|\n\tv_add_f32_e64 %[c3], %[c3], |%[t3]|"
+            : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [c0] "+v"(c0), [c1] "+v"(c1),
+              [c2] "+v"(c2), [c3] "+v"(c3)
+            : [a] "v"(a), [b0] "v"(b0), [b1] "v"(b1), [b2] "v"(b2), [b3] "v"(b3));
+    } else if constexpr (PK == kP2) {
+        asm("v_sub_f32 %[t0], %[a], %[b0]\n\tv_sub_f32 %[t1], %[a], %[b1]\n\t"
+            "v_sub_f32 %[t2], %[a], %[b2]\n\tv_sub_f32 %[t3], %[a], %[b3]\n\t"
+            "v_fmac_f32 %[c0], %[t0], %[t0]\n\tv_fmac_f32 %[c1], %[t1], %[t1]\n\t"
+            "v_fmac_f32 %[c2], %[t2], %[t2]\n\tv_fmac_f32 %[c3], %[t3], %[t3]"
+            : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [c0] "+v"(c0), [c1] "+v"(c1),
+              [c2] "+v"(c2), [c3] "+v"(c3)
+            : [a] "v"(a), [b0] "v"(b0), [b1] "v"(b1), [b2] "v"(b2), [b3] "v"(b3));
+    } else {
+        static_assert(PK == kP3, "lp_step4: p = 1, 2, 3");
+        float u0, u1, u2, u3;
+        asm("v_sub_f32 %[t0], %[a], %[b0]\n\tv_sub_f32 %[t1], %[a], %[b1]\n\t"
+            "v_sub_f32 %[t2], %[a], %[b2]\n\tv_sub_f32 %[t3], %[a], %[b3]\n\t"
+            "v_mul_f32 %[u0], %[t0], %[t0]\n\tv_mul_f32 %[u1], %[t1], %[t1]\n\t"
+            "v_mul_f32 %[u2], %[t2], %[t2]\n\tv_mul_f32 %[u3], %[t3], %[t3]\n\t"
+            "v_fma_f32 %[c0], %[u0], |%[t0]|, %[c0]\n\tv_fma_f32 %[c1], %[u1], |%[t1]|, %[c1]\n\t"
+            "v_fma_f32 %[c2], %[u2], |%[t2]|, %[c2]\n\tv_fma_f32 %[c3], %[u3], |%[t3]|, %[c3]"
+            : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [u0] "=&v"(u0), [u1] "=&v"(u1),
+              [u2] "=&v"(u2), [u3] "=&v"(u3), [c0] "+v"(c0), [c1] "+v"(c1), [c2] "+v"(c2), [c3] "+v"(c3)
+            : [a] "v"(a), [b0] "v"(b0), [b1] "v"(b1), [b2] "v"(b2), [b3] "v"(b3));
+    }
+}
+
+// Four max3 (min3) steps of two features each, the eight subtractions first (the p = +-inf
+// steps of the forward's paired loop, interleaved four ways as lp_step4 is).
+template <bool MAX>
+__device__ __forceinline__ void max3_step4(float &c0, float &c1, float &c2, float &c3, float a0, float a1,
+                                           floatx4 b0, floatx4 b1) {
+    float t0, t1, t2, t3, u0, u1, u2, u3;
+#define TPW_MAX3_BODY(OP)                                                                             \
+    asm("v_sub_f32 %[t0], %[a0], %[p0]\n\tv_sub_f32 %[u0], %[a1], %[q0]\n\t"                           \
+        "v_sub_f32 %[t1], %[a0], %[p1]\n\tv_sub_f32 %[u1], %[a1], %[q1]\n\t"                           \
+        "v_sub_f32 %[t2], %[a0], %[p2]\n\tv_sub_f32 %[u2], %[a1], %[q2]\n\t"                           \
+        "v_sub_f32 %[t3], %[a0], %[p3]\n\tv_sub_f32 %[u3], %[a1], %[q3]\n\t"                           \
+        OP " %[c0], %[c0], |%[t0]|, |%[u0]|\n\t" OP " %[c1], %[c1], |%[t1]|, |%[u1]|\n\t"                \
+        OP " %[c2], %[c2], |%[t2]|, |%[u2]|\n\t" OP " %[c3], %[c3], |%[t3]|, |%[u3]|"                     \
+        : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [u0] "=&v"(u0), [u1] "=&v"(u1), \
+          [u2] "=&v"(u2), [u3] "=&v"(u3), [c0] "+v"(c0), [c1] "+v"(c1), [c2] "+v"(c2), [c3] "+v"(c3)     \
+        : [a0] "v"(a0), [a1] "v"(a1), [p0] "v"(b0[0]), [p1] "v"(b0[1]), [p2] "v"(b0[2]), [p3] "v"(b0[3]), \
+          [q0] "v"(b1[0]), [q1] "v"(b1[1]), [q2] "v"(b1[2]), [q3] "v"(b1[3]))
+    if constexpr (MAX) TPW_MAX3_BODY("v_max3_f32");
+    else TPW_MAX3_BODY("v_min3_f32");
+#undef TPW_MAX3_BODY
+}
+
 template <int PK>
 __device__ __forceinline__ float lp_finish(float acc, float inv_p) {
     if constexpr (PK == kP2) return sqrt_rn(acc);
@@ -219,10 +282,10 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const float d0 = av[0][i] - bv[0][j], d1 = av[1][i] - bv[1][j];
-                        acc[i][j] = PK == kPInf ? max3_abs(acc[i][j], d0, d1) : min3_abs(acc[i][j], d0, d1);
-                    }
+                    for (int j = 0; j < 8; j += 4)
+                        max3_step4<PK == kPInf>(acc[i][j], acc[i][j + 1], acc[i][j + 2], acc[i][j + 3], av[0][i],
+                                                av[1][i], floatx4{bv[0][j], bv[0][j + 1], bv[0][j + 2], bv[0][j + 3]},
+                                                floatx4{bv[1][j], bv[1][j + 1], bv[1][j + 2], bv[1][j + 3]});
             }
         }
         for (int k = kbeg; k < kmax; ++k) {
@@ -233,10 +296,19 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
             const float wk = MODE == kWeighted ? Wk[MODE == kWeighted ? k : 0] : 0.0f;
             const float av[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
             const float bv[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+            if constexpr ((MODE == kRoot || MODE == kSum) && (PK == kP1 || PK == kP2 || PK == kP3)) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+                for (int i = 0; i < 8; ++i)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[i][j] = fam_step<MODE, PK>(acc[i][j], av[i], bv[j], wk, p);
+                    for (int j = 0; j < 8; j += 4)
+                        lp_step4<PK>(acc[i][j], acc[i][j + 1], acc[i][j + 2], acc[i][j + 3], av[i], bv[j], bv[j + 1],
+                                     bv[j + 2], bv[j + 3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[i][j] = fam_step<MODE, PK>(acc[i][j], av[i], bv[j], wk, p);
+            }
         }
         __syncthreads();
     }
@@ -328,7 +400,8 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 // backward
 // ---------------------------------------------------------------------------------------
 constexpr int kBRows = 128;  // rows (i) per block
-constexpr int kBFeat = 64;   // features (k) per block
+constexpr int kBFeat = 64;   // features (k) per block of the narrow kernel (FW = 64)
+constexpr int kBFeatWide = 128;  // ... of the wide kernel (FW = 128: 8 x 8 per thread)
 constexpr int kBJ = 32;      // j per stage
 
 // Weight of pair (i, j) given upstream grad g and distance dist (torch's _cdist_backward):
@@ -376,6 +449,37 @@ __device__ __forceinline__ float grad_term(float d, float w, float dist, float p
     } else {
         return d * exp2f((p - 2.0f) * __log2f(fabsf(d))) * w;
     }
+}
+
+// Four backward terms of one row, interleaved as lp_step4: acc[c] += w * T(a[c] - b[c]) with
+// T(d) = d |d| (p = 3), d (p = 2) or, for operands pre-scaled by 2^75, med3(d, -1, 1) =
+// sign(d) (the p = 1 fast path), with grad_term's operations and roundings (the product and
+// the accumulate are one fma, as the compiler contracts grad_term's w * T + acc).
+template <int PK, bool SIGN = false>
+__device__ __forceinline__ void grad_step4(float &c0, float &c1, float &c2, float &c3, float a0, float a1, float a2,
+                                           float a3, float b0, float b1, float b2, float b3, float w) {
+    float t0, t1, t2, t3;
+#define TPW_GRAD4(MID)                                                                                          \
+    asm("v_sub_f32 %[t0], %[a0], %[b0]\n\tv_sub_f32 %[t1], %[a1], %[b1]\n\t"                                     \
+        "v_sub_f32 %[t2], %[a2], %[b2]\n\tv_sub_f32 %[t3], %[a3], %[b3]\n\t" MID                                  \
+        "v_fmac_f32 %[c0], %[w], %[t0]\n\tv_fmac_f32 %[c1], %[w], %[t1]\n\t"                                      \
+        "v_fmac_f32 %[c2], %[w], %[t2]\n\tv_fmac_f32 %[c3], %[w], %[t3]"                                           \
+        : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [c0] "+v"(c0), [c1] "+v"(c1),            \
+          [c2] "+v"(c2), [c3] "+v"(c3)                                                                            \
+        : [a0] "v"(a0), [a1] "v"(a1), [a2] "v"(a2), [a3] "v"(a3), [b0] "v"(b0), [b1] "v"(b1), [b2] "v"(b2),       \
+          [b3] "v"(b3), [w] "v"(w))
+    if constexpr (SIGN) {
+        static_assert(PK == kP1, "the sign fast path is p = 1");
+        TPW_GRAD4("v_med3_f32 %[t0], %[t0], -1.0, 1.0\n\tv_med3_f32 %[t1], %[t1], -1.0, 1.0\n\t"
+                  "v_med3_f32 %[t2], %[t2], -1.0, 1.0\n\tv_med3_f32 %[t3], %[t3], -1.0, 1.0\n\t");
+    } else if constexpr (PK == kP3) {
+        TPW_GRAD4("v_mul_f32_e64 %[t0], %[t0], |%[t0]|\n\tv_mul_f32_e64 %[t1], %[t1], |%[t1]|\n\t"
+                  "v_mul_f32_e64 %[t2], %[t2], |%[t2]|\n\tv_mul_f32_e64 %[t3], %[t3], |%[t3]|\n\t");
+    } else {
+        static_assert(PK == kP2, "grad_step4: p = 2, 3 and the p = 1 sign fast path");
+        TPW_GRAD4("");
+    }
+#undef TPW_GRAD4
 }
 
 // |d|^e for the general-p formulas (pow of the reference kernels).
@@ -455,12 +559,19 @@ __device__ __forceinline__ float fam_term(float a, float b, float w1, float w2, 
     }
 }
 
-// Whether the per-pair weights are computed once into an [n, m] array before the
-// gradient kernels (they need a second per-pair operand and arithmetic beyond g itself)
-// rather than while staging: staging then reads one array instead of two.
+// Whether the narrow kernel's per-pair weights are computed once into an [n, m] array before
+// the gradient kernels (they need a second per-pair operand and arithmetic beyond g itself)
+// rather than while staging: staging then reads one array instead of two.  The wide kernel
+// (FW = 128) forms them while staging, from g and the distance: at d <= 128 each pair's weight
+// is then formed once per direction, and no [n, m] array is written and read back.
 template <int MODE, int PK>
 constexpr bool kPrecomputed = (MODE == kRoot && (PK == kP2 || PK == kP3 || PK == kPLt2 || PK == kPGen)) ||
                               (MODE == kWeighted && PK != kP1) || MODE == kBrayDen;
+// The cases the wide kernel serves (above 64 features): the cdist backward at p = 2, 3 and
+// p > 2 in general.  p = inf (a second per-pair array), p = 1 (its sign fast path) and
+// 0 < p < 2 would spill its registers at this width.
+template <int MODE, int PK>
+constexpr bool kWide = MODE == kRoot && (PK == kP2 || PK == kP3 || PK == kPGen);
 
 // VEC: every pointer is 16-byte aligned; four pairs per step with 16-byte accesses, and the
 // len % 4 tail by the first threads.
@@ -501,20 +612,29 @@ __global__ void pair_weight_kernel(const float *__restrict__ g, const float *__r
 
 // out[(split, b, i, k)] = sum over this split's j of fam_term.  G(b,i,j) and the per-pair
 // arrays are read at [b*n*m + i*gs_i + j*gs_j] (gs = (m, 1) direct, (1, n) transposed).
-// Under PRE, aux0 / aux1 hold the precomputed weights w1 / w2 and g is not read.
-template <int MODE, int PK, bool TR, bool WGRAD, bool PRE>
+// Under PRE, aux0 / aux1 hold the precomputed weights w1 / w2 and g is not read.  FW is the
+// block's feature width: 64 (thread block 8 rows x 4 features) or 128 (8 x 8, the forward's
+// ratio of LDS reads to VALU work: per j step two 16-byte reads of weights and two of x2 for 64
+// pair-features).
+template <int MODE, int PK, bool TR, bool WGRAD, bool PRE, int FW = kBFeat>
 __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     const float *__restrict__ g, const float *__restrict__ aux0, const float *__restrict__ aux1,
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
     int64_t n, int64_t m, int64_t d, float p, int64_t j_per_split, int64_t batch,
     float *__restrict__ out) {
     constexpr bool kTwo = (MODE == kRoot && PK == kPInf) || MODE == kBrayDen;
+    constexpr int kCW = FW / 16;                // features per thread
+    constexpr int kWavesPerRow = FW / 64;       // waves staging one x2 panel row
+    constexpr int kPanelQ = kBJ * FW / kThreads;  // x2 panel values per thread and stage
+    static_assert(FW == 64 || FW == 128, "feature width");
     __shared__ float Ws[kBJ][kBRows + kPad];
     __shared__ float Ds[kTwo ? kBJ : 1][kBRows + kPad];
-    __shared__ float Xs[kBJ][kBFeat + kPad];
+    __shared__ float Xs[kBJ][FW + kPad];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    // thread (ty, tx) owns rows 8 ty + r and features 64 (c / 4) + 4 tx + c % 4 of the block
+    auto feat_of = [](int t, int c) { return 64 * (c >> 2) + 4 * t + (c & 3); };
     const int64_t split = blockIdx.z / batch, b = blockIdx.z - split * batch;
-    const int64_t i0 = (int64_t)blockIdx.y * kBRows, k0 = (int64_t)blockIdx.x * kBFeat;
+    const int64_t i0 = (int64_t)blockIdx.y * kBRows, k0 = (int64_t)blockIdx.x * FW;
     const int64_t jbeg = split * j_per_split;
     const int64_t jend = jbeg + j_per_split < m ? jbeg + j_per_split : m;
     const float *G = g + b * n * m;
@@ -523,18 +643,18 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     const float *X1 = x1 + b * n * d;
     const float *X2 = x2 + b * m * d;
 
-    float xv[8][4], acc[8][4], wkv[4];
+    float xv[8][kCW], acc[8][kCW], wkv[kCW];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int64_t k = k0 + 4 * tx + c;
+    for (int c = 0; c < kCW; ++c) {
+        const int64_t k = k0 + feat_of(tx, c);
         wkv[c] = (MODE == kWeighted && k < d) ? w[b * d + k] : 0.0f;
     }
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         const int64_t i = i0 + 8 * ty + r;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int64_t k = k0 + 4 * tx + c;
+        for (int c = 0; c < kCW; ++c) {
+            const int64_t k = k0 + feat_of(tx, c);
             xv[r][c] = (i < n && k < d) ? X1[i * d + k] : 0.0f;
             acc[r][c] = 0.0f;
         }
@@ -545,24 +665,53 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     // the stage's closing barrier.  Lane (tid) loads weight q of a stage at
     //   direct:     row ii = (tid >> 5) + 8 q, column jj = tid & 31   (coalesced along j)
     //   transposed: row ii = tid & 127,        column jj = (tid >> 7) + 2 q  (along i)
-    // and panel value q at row jj = (tid >> 6) + 4 q, feature kk = tid & 63.  The loads are
+    // and panel value q at row jj = wave / kWavesPerRow + (4 / kWavesPerRow) q, feature
+    // kk = 64 (wave % kWavesPerRow) + lane.  The loads are
     // raw buffer loads from wave-uniform bases: a lane past the end of an array reads 0, and
     // lanes past a row's end (j >= m, k >= d) or past jend read values that only reach
     // accumulators of rows, features or stage steps that are never stored or run, so no
     // load needs a bounds branch.
     constexpr bool kReadG = !PRE;                               // upstream grad
-    constexpr bool kReadA0 = PRE || (MODE == kRoot && PK == kPInf);
+    constexpr bool kReadA0 = PRE || (MODE == kRoot && PK != kP1);  // weights, or the distance
     constexpr bool kReadA1 = PRE && kTwo;
-    float rg[kReadG ? 16 : 1], ra0[kReadA0 ? 16 : 1], ra1[kReadA1 ? 16 : 1], rx[8];
+    // The wide kernel (V4) stages with 16-byte loads instead (its launch requires 16-byte
+    // aligned arrays and n, m, d multiples of 4): lane (tid) loads float4 q of a stage at
+    //   direct:     row ii = (tid >> 3) + 32 q, columns jj = 4 (tid & 7) + 0..3
+    //   transposed: column jj = (tid >> 5) + 8 q, rows ii = 4 (tid & 31) + 0..3
+    //   panel:      row jj = (tid >> 5) + 8 q, features kk = 4 (tid & 31) + 0..3
+    // from one descriptor per array and stage with loop-invariant lane offsets.
+    constexpr bool V4 = FW == kBFeatWide;
+    static_assert(!V4 || !kTwo, "the wide kernel stages one per-pair array");
+    float rg[kReadG ? 16 : 1], ra0[kReadA0 ? 16 : 1], ra1[kReadA1 ? 16 : 1], rx[kPanelQ];
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lw_i = TR ? (tid & 127) : (tid >> 5), lw_j = TR ? (tid >> 7) : (tid & 31);
-    const int lx_j = tid >> 6, lx_k = tid & 63;
+    const int lx_j = (tid >> 6) / kWavesPerRow, lx_k = 64 * ((tid >> 6) % kWavesPerRow) + lane;
     // byte offsets within a wave's rows (the launch keeps them below 2^32)
     const uint32_t lw_voff = TR ? (uint32_t)lane * 4u : (uint32_t)(((lane >> 5) * m + (lane & 31)) * 4);
     const uint32_t lx_voff = (uint32_t)lane * 4u;
     const int64_t nm = n * m, md = m * d;
 
+    uint32_t v4_pair_off[V4 ? 4 : 1], v4_panel_off[V4 ? 4 : 1];
+    if constexpr (V4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v4_pair_off[q] = TR ? (uint32_t)((((tid >> 5) + 8 * q) * n + 4 * (tid & 31)) * 4)
+                                : (uint32_t)((((tid >> 3) + 32 * q) * m + 4 * (tid & 7)) * 4);
+            v4_panel_off[q] = (uint32_t)((((tid >> 5) + 8 * q) * d + 4 * (tid & 31)) * 4);
+        }
+    }
+    // V4: the 16 per-pair values of one array for stage j0, as four float4
+    auto load_pairs4 = [&](const float *arr, auto &r, int64_t j0) {
+        const int64_t off = TR ? j0 * n + i0 : i0 * m + j0;
+        const auto rs = buffer_over(arr + off, nm - off);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const floatx4 v = buffer_load4(rs, v4_pair_off[q]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[4 * q + e] = v[e];
+        }
+    };
     // the 16 per-pair values of one array for stage j0
     auto load_pairs = [&](const float *arr, auto &r, int64_t j0) {
         // one descriptor per step keeps the lane offset a single register (per-step lane
@@ -582,16 +731,55 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         }
     };
     auto load = [&](int64_t j0) {
+        if constexpr (V4) {
+            if constexpr (kReadG) load_pairs4(G, rg, j0);
+            if constexpr (kReadA0) load_pairs4(A0, ra0, j0);
+            const int64_t off = j0 * d + k0;
+            const auto rs = buffer_over(X2 + off, md - off);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const floatx4 v = buffer_load4(rs, v4_panel_off[q]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rx[4 * q + e] = v[e];
+            }
+            return;
+        }
         if constexpr (kReadG) load_pairs(G, rg, j0);
         if constexpr (kReadA0) load_pairs(A0, ra0, j0);
         if constexpr (kReadA1) load_pairs(A1, ra1, j0);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int64_t off = (j0 + wv + 4 * q) * d + k0;
+        for (int q = 0; q < kPanelQ; ++q) {
+            const int64_t off = (j0 + wv / kWavesPerRow + (4 / kWavesPerRow) * q) * d + k0 + 64 * (wv % kWavesPerRow);
             rx[q] = buffer_load(buffer_over(X2 + off, md - off), lx_voff);
         }
     };
     auto store = [&](int64_t j0) {
+        if constexpr (V4) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float wq[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int ii = TR ? 4 * (tid & 31) + e : (tid >> 3) + 32 * q;
+                    const int jj = TR ? (tid >> 5) + 8 * q : 4 * (tid & 7) + e;
+                    float w1, w2;
+                    pair_weights<MODE, PK>(kReadG ? rg[4 * q + e] : 0.0f, kReadA0 ? ra0[4 * q + e] : 0.0f, 0.0f, p,
+                                           w1, w2);
+                    if constexpr (PRE) w1 = ra0[4 * q + e];
+                    wq[e] = (i0 + ii < n && j0 + jj < jend) ? w1 : 0.0f;
+                }
+                if constexpr (TR) {
+                    *reinterpret_cast<floatx4 *>(&Ws[(tid >> 5) + 8 * q][4 * (tid & 31)]) =
+                        floatx4{wq[0], wq[1], wq[2], wq[3]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) Ws[4 * (tid & 7) + e][(tid >> 3) + 32 * q] = wq[e];
+                }
+                *reinterpret_cast<floatx4 *>(&Xs[(tid >> 5) + 8 * q][4 * (tid & 31)]) =
+                    floatx4{rx[4 * q], rx[4 * q + 1], rx[4 * q + 2], rx[4 * q + 3]};
+            }
+            return;
+        }
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
             const int ii = lw_i + (TR ? 0 : 8 * q), jj = lw_j + (TR ? 2 * q : 0);
@@ -608,7 +796,18 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
             if constexpr (kTwo) Ds[jj][ii] = w2;
         }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) Xs[lx_j + 4 * q][lx_k] = rx[q];
+        for (int q = 0; q < kPanelQ; ++q) Xs[lx_j + (4 / kWavesPerRow) * q][lx_k] = rx[q];
+    };
+
+    // x2 values of panel row jj at the thread's features feat_of(tcol, c) (one or two 16-byte
+    // LDS reads, 16 bytes apart across the lanes)
+    auto load_panel = [&](float (&x)[kCW], int jj, int tcol) {
+#pragma unroll
+        for (int h = 0; h < kCW / 4; ++h) {
+            const floatx4 v = *reinterpret_cast<const floatx4 *>(&Xs[jj][64 * h + 4 * tcol]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[4 * h + e] = v[e];
+        }
     };
 
     // p = 1 sign fast path (sign_scaled): flags[2] marks a tile of x1 outside the scalable
@@ -623,7 +822,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) ok = ok && sign_scalable(xv[r][c]);
+            for (int c = 0; c < kCW; ++c) ok = ok && sign_scalable(xv[r][c]);
         if (tid == 0) flags[0] = flags[2] = 0;
         __syncthreads();
         if (__any(!ok) && lane == 0) flags[2] = 1;
@@ -636,7 +835,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         if constexpr (kSignFast) {
             bool ok = true;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) ok = ok && sign_scalable(rx[q]);
+            for (int q = 0; q < kPanelQ; ++q) ok = ok && sign_scalable(rx[q]);
             if (__any(!ok) && lane == 0) flags[stage & 1] = 1;
             if (tid == 0) flags[(stage + 1) & 1] = 0;
         }
@@ -651,23 +850,26 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
 #pragma unroll
                 for (int r = 0; r < 8; ++r)
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) xv[r][c] *= f;
+                    for (int c = 0; c < kCW; ++c) xv[r][c] *= f;
                 xv_scaled = fast;
             }
             if (fast) {
                 for (int jj = 0; jj < jmax; ++jj) {
                     const floatx4 w0 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty]);
                     const floatx4 w1 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty + 4]);
-                    const floatx4 x = *reinterpret_cast<const floatx4 *>(&Xs[jj][4 * tx]);
+                    float x[kCW];
+                    load_panel(x, jj, tx);
                     const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-                    float xs[4];
+                    float xs[kCW];
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) xs[c] = x[c] * kSignScale;
+                    for (int c = 0; c < kCW; ++c) xs[c] = x[c] * kSignScale;
 #pragma unroll
                     for (int r = 0; r < 8; ++r)
 #pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            acc[r][c] = fmaf(sign_scaled(xv[r][c] - xs[c]), wv[r], acc[r][c]);
+                        for (int c = 0; c < kCW; c += 4)
+                            grad_step4<kP1, true>(acc[r][c], acc[r][c + 1], acc[r][c + 2], acc[r][c + 3], xv[r][c],
+                                                  xv[r][c + 1], xv[r][c + 2], xv[r][c + 3], xs[c], xs[c + 1],
+                                                  xs[c + 2], xs[c + 3], wv[r]);
                 }
                 __syncthreads();
                 continue;
@@ -676,7 +878,8 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         for (int jj = 0; jj < jmax; ++jj) {
             const floatx4 w0 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty]);
             const floatx4 w1 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty + 4]);
-            const floatx4 x = *reinterpret_cast<const floatx4 *>(&Xs[jj][4 * tx]);
+            float x[kCW];
+            load_panel(x, jj, tx);
             const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
             float dv[8];
             if constexpr (kTwo) {
@@ -688,11 +891,20 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
 #pragma unroll
                 for (int r = 0; r < 8; ++r) dv[r] = 0.0f;
             }
+            if constexpr (MODE == kRoot && (PK == kP2 || PK == kP3)) {
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
+                for (int r = 0; r < 8; ++r)
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    acc[r][c] += fam_term<MODE, PK, WGRAD>(xv[r][c], x[c], wv[r], dv[r], wkv[c], p);
+                    for (int c = 0; c < kCW; c += 4)
+                        grad_step4<PK>(acc[r][c], acc[r][c + 1], acc[r][c + 2], acc[r][c + 3], xv[r][c], xv[r][c + 1],
+                                       xv[r][c + 2], xv[r][c + 3], x[c], x[c + 1], x[c + 2], x[c + 3], wv[r]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+#pragma unroll
+                    for (int c = 0; c < kCW; ++c)
+                        acc[r][c] += fam_term<MODE, PK, WGRAD>(xv[r][c], x[c], wv[r], dv[r], wkv[c], p);
+            }
         }
         __syncthreads();
     }
@@ -703,8 +915,8 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         const int64_t i = i0 + 8 * ty + r;
         if (i >= n) continue;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int64_t k = k0 + 4 * tx + c;
+        for (int c = 0; c < kCW; ++c) {
+            const int64_t k = k0 + feat_of(tx, c);
             if (k < d) o[i * d + k] = acc[r][c];
         }
     }
@@ -816,8 +1028,8 @@ int device_cus() {
 // grid alone fills base blocks; splitting j multiplies that, and a whole number of
 // resident rounds avoids a partly filled last round.  More slots never give fewer splits,
 // so the workspace is sized with the largest slot count.
-int64_t lp_backward_splits(int64_t slots, int64_t batch, int64_t n, int64_t m, int64_t d) {
-    const int64_t base = cdiv(n, kBRows) * cdiv(d, kBFeat) * batch;
+int64_t lp_backward_splits(int64_t slots, int64_t batch, int64_t n, int64_t m, int64_t d, int64_t fw) {
+    const int64_t base = cdiv(n, kBRows) * cdiv(d, fw) * batch;
     if (base == 0) return 1;  // no output rows (empty n, d or batch): nothing to split
     int64_t splits = base >= slots ? 1 : slots / base;
     const int64_t max_by_m = cdiv(m, 512);
@@ -830,21 +1042,21 @@ int64_t lp_backward_splits(int64_t slots, int64_t batch, int64_t n, int64_t m, i
 int64_t max_slots() { return (int64_t)device_cus() * kMaxBlocksPerCU; }
 
 // grad [batch, n, d] of the first operand (x2's gradient: pass x2 as x1, n <-> m, TR).
-template <int MODE, int PK, bool TR, bool WGRAD, bool PRE>
+template <int MODE, int PK, bool TR, bool WGRAD, bool PRE, int FW>
 int launch_backward(const float *g, const float *aux0, const float *aux1, const float *x1,
                     const float *x2, const float *w, int64_t batch, int64_t n, int64_t m, int64_t d,
                     double p, float *grad, float *part, hipStream_t s) {
     // the direct layout's staging lanes span two rows of m: their byte offsets are 32-bit
     TPW_REQUIRE(TR || 4 * m + 128 < ((int64_t)1 << 32),
                 "backward: %lld columns exceed the kernel's 32-bit staging offsets", (long long)m);
-    auto kern = lp_backward_kernel<MODE, PK, TR, WGRAD, PRE>;
+    auto kern = lp_backward_kernel<MODE, PK, TR, WGRAD, PRE, FW>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, 0) != hipSuccess || per_cu <= 0)
         per_cu = 2;
     if (per_cu > kMaxBlocksPerCU) per_cu = kMaxBlocksPerCU;
-    const int64_t splits = lp_backward_splits((int64_t)device_cus() * per_cu, batch, n, m, d);
+    const int64_t splits = lp_backward_splits((int64_t)device_cus() * per_cu, batch, n, m, d, FW);
     const int64_t jps = cdiv(cdiv(m, splits), kBJ) * kBJ;
-    dim3 grid((unsigned)cdiv(d, kBFeat), (unsigned)cdiv(n, kBRows), (unsigned)(splits * batch));
+    dim3 grid((unsigned)cdiv(d, FW), (unsigned)cdiv(n, kBRows), (unsigned)(splits * batch));
     float *dst = splits > 1 ? part : grad;
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s, g, aux0, aux1, x1, x2, w, n, m, d, (float)p,
                        jps, batch, dst);
@@ -883,11 +1095,10 @@ struct BwdJob {
     bool x1_transposed;  // single-direction call for x2's gradient (x1/x2 already swapped)
 };
 
-template <int MODE, int PK>
-int run_backward(const BwdJob &j, hipStream_t s) {
-    constexpr bool PRE = kPrecomputed<MODE, PK>;
+template <int MODE, int PK, int FW, bool PRE>
+int run_backward_fw(const BwdJob &j, hipStream_t s) {
     // staging reads the per-pair arrays only where the weights need them
-    constexpr bool kAux = PRE || (MODE == kRoot && PK == kPInf);
+    constexpr bool kAux = PRE || (MODE == kRoot && PK != kP1);
     const float *a0 = kAux ? j.aux0 : nullptr, *a1 = kAux ? j.aux1 : nullptr;
     if constexpr (PRE) {
         constexpr bool two = MODE == kBrayDen;
@@ -900,21 +1111,33 @@ int run_backward(const BwdJob &j, hipStream_t s) {
     int rc = TPW_OK;
     if (j.gx1) {
         if (j.x1_transposed)  // n, m are already those of the operand whose grad is wanted
-            rc = launch_backward<MODE, PK, true, false, PRE>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
+            rc = launch_backward<MODE, PK, true, false, PRE, FW>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
                                                               j.m, j.d, j.p, j.gx1, j.part, s);
         else
-            rc = launch_backward<MODE, PK, false, false, PRE>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
+            rc = launch_backward<MODE, PK, false, false, PRE, FW>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
                                                                j.m, j.d, j.p, j.gx1, j.part, s);
     }
     if (rc == TPW_OK && j.gx2)
-        rc = launch_backward<MODE, PK, true, false, PRE>(j.g, a0, a1, j.x2, j.x1, j.w, j.batch, j.m, j.n,
+        rc = launch_backward<MODE, PK, true, false, PRE, FW>(j.g, a0, a1, j.x2, j.x1, j.w, j.batch, j.m, j.n,
                                                           j.d, j.p, j.gx2, j.part, s);
     if constexpr (MODE == kWeighted) {
         if (rc == TPW_OK && j.rows)
-            rc = launch_backward<MODE, PK, false, true, PRE>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
+            rc = launch_backward<MODE, PK, false, true, PRE, FW>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
                                                               j.m, j.d, j.p, j.rows, j.part, s);
     }
     return rc;
+}
+
+// The wide kernel above 64 features where it serves the case and its 16-byte staging fits
+// (aligned arrays, n, m and d multiples of 4); else the narrow one.
+template <int MODE, int PK>
+int run_backward(const BwdJob &j, hipStream_t s) {
+    if constexpr (kWide<MODE, PK>) {
+        const bool fits = j.d > kBFeat && j.n % 4 == 0 && j.m % 4 == 0 && j.d % 4 == 0 && aligned16(j.g) &&
+                          aligned16(j.aux0) && aligned16(j.x1) && aligned16(j.x2);
+        if (fits) return run_backward_fw<MODE, PK, kBFeatWide, false>(j, s);
+    }
+    return run_backward_fw<MODE, PK, kBFeat, kPrecomputed<MODE, PK>>(j, s);
 }
 
 template <int MODE>
@@ -943,7 +1166,13 @@ struct Workspace {
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 Workspace workspace_layout(int metric, int64_t batch, int64_t n, int64_t m, int64_t d) {
     const int64_t slots = max_slots();
-    const int64_t s1 = lp_backward_splits(slots, batch, n, m, d), s2 = lp_backward_splits(slots, batch, m, n, d);
+    // the wide kernel's grid has fewer feature blocks, so it may take more splits
+    int64_t s1 = lp_backward_splits(slots, batch, n, m, d, kBFeatWide);
+    int64_t s2 = lp_backward_splits(slots, batch, m, n, d, kBFeatWide);
+    const int64_t s1n = lp_backward_splits(slots, batch, n, m, d, kBFeat);
+    const int64_t s2n = lp_backward_splits(slots, batch, m, n, d, kBFeat);
+    s1 = s1 > s1n ? s1 : s1n;
+    s2 = s2 > s2n ? s2 : s2n;
     Workspace w{};
     const int64_t part1 = s1 > 1 ? s1 * batch * n * d : 0, part2 = s2 > 1 ? s2 * batch * m * d : 0;
     w.part = align256(sizeof(float) * (size_t)(part1 > part2 ? part1 : part2));

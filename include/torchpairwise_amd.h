@@ -529,9 +529,12 @@ int tpw_linear_backward(const void *grad, const void *x1, const void *x2, int dt
  * norm is 0).  `norms1`/`norms2` are the fp32 row norms of x1/x2.  `similarity` = 1: the
  * op is cosine_similarity (no 1 - s, no clip); 2: correlation_distances' 1 - s without the
  * clip (pairwise_metrics.cpp:190-204, neg_ then add_(1)) of rows the caller has centred.
+ * `out` (may be NULL): the forward's output [batch,n,m] of the input type.  Given, the
+ * weights come from it (s = out, or 1 - out) with no recomputed x1 x2^T; a distance output
+ * of exactly 0 or 2 then counts as clipped.  NULL: x1 x2^T is recomputed on the matrix cores.
  * When x2 is x1 (x2=None upstream), the caller adds the two halves. */
 int tpw_cosine_backward(const void *grad, const void *x1, const void *x2,
-                        const float *norms1, const float *norms2, int dtype,
+                        const float *norms1, const float *norms2, const void *out, int dtype,
                         int64_t batch, int64_t n, int64_t m, int64_t d, int similarity,
                         void *grad_x1, void *grad_x2, void *workspace, void *stream);
 

@@ -245,7 +245,10 @@ def test_euclidean_backward(B, n, m, d, dtype):
                                      (2, 128, 192, 64), (1, 1088, 1024, 72)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("similarity", [False, True])
-def test_cosine_backward(B, n, m, d, dtype, similarity):
+@pytest.mark.parametrize("from_output", [False, True])
+def test_cosine_backward(B, n, m, d, dtype, similarity, from_output):
+    """Both routes of the cosine backward: x1 . x2^T recomputed, or the weights formed from the
+    forward's output (as autograd passes it)."""
     x1 = randn(B, n, d, seed=0, dtype=dtype)
     x2 = randn(B, m, d, seed=1, dtype=dtype)
     g = randn(B, n, m, seed=2, dtype=dtype)
@@ -253,7 +256,10 @@ def test_cosine_backward(B, n, m, d, dtype, similarity):
     b = x2.double().requires_grad_()
     f = P.cosine_similarity if similarity else P.cosine_distances
     gx1_ref, gx2_ref = torch.autograd.grad(f(a, b), (a, b), g.double())
-    gx1, gx2 = capi.cosine_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), similarity=similarity)
+    out = None
+    if from_output:
+        out = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_COSINE_SIM if similarity else capi.EPI_COSINE_DIST)
+    gx1, gx2 = capi.cosine_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), similarity=similarity, out=out)
     rtol = 1e-4 if dtype == torch.float32 else 1e-2
     for got, want, nm in ((gx1, gx1_ref, "grad_x1"), (gx2, gx2_ref, "grad_x2")):
         assert_close(got.float(), want, rtol=rtol, atol=rtol * float(want.abs().max()),

@@ -59,7 +59,7 @@ _SIGNATURES = {
     "tpw_inner_backward_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "tpw_euclidean_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "tpw_sqeuclidean_backward": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
-    "tpw_cosine_backward": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p]),
+    "tpw_cosine_backward": (_i, [_p, _p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p]),
     "tpw_linear_backward": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "tpw_sqmahalanobis_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64]),
     "tpw_sqmahalanobis": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _p]),
@@ -471,19 +471,22 @@ def euclidean_backward(grad, x1, x2, res):
     return gx1, gx2
 
 
-def cosine_backward(grad, x1, x2, similarity=False):
+def cosine_backward(grad, x1, x2, similarity=False, out=None):
+    """(grad_x1, grad_x2) of the cosine family; with `out` (the forward's output) the weights
+    come from it instead of a recomputed x1 . x2^T."""
     import torch
 
     a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
     g = _as3(grad).contiguous()
+    o = None if out is None else _as3(out).contiguous()
     B, n, d = a.shape
     m = b.shape[1]
     n1, n2 = row_norms(a, False), row_norms(b, False)
     gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
     ws = torch.empty((lib().tpw_inner_backward_workspace_size(B, n, m, d),), dtype=torch.uint8,
                      device=a.device)
-    call("tpw_cosine_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(n1), _ptr(n2), _dtype_code(a), B, n,
-         m, d, int(similarity), _ptr(gx1), _ptr(gx2), _ptr(ws), _stream())
+    call("tpw_cosine_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(n1), _ptr(n2), _ptr(o), _dtype_code(a), B,
+         n, m, d, int(similarity), _ptr(gx1), _ptr(gx2), _ptr(ws), _stream())
     if x1.dim() == 2:
         return gx1[0], gx2[0]
     return gx1, gx2

@@ -46,6 +46,18 @@ __device__ __forceinline__ void store_nt4(float *p, floatx4 v) {
 // 1-ulp v_sqrt_f32; sqrtf / __builtin_sqrtf get the fma-based rounding fix-up.)
 __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 
+// x / y within 2 ulp: the hardware reciprocal (v_rcp_f32, 1 ulp) times x, where the IEEE
+// divide takes about ten instructions.  Denominators outside [2^-126, 2^126] (zero, denormal,
+// inf, NaN, or a reciprocal that could flush) take the IEEE divide, behind a branch that whole
+// waves of ordinary values skip.  For the floating-point backward weights, whose results carry
+// summation error anyway; bit-exact paths keep the IEEE divide.
+__device__ __forceinline__ float fast_div(float x, float y) {
+    const float ay = __builtin_fabsf(y);
+    float q = x * __builtin_amdgcn_rcpf(y);
+    if (__builtin_expect(!(ay >= 0x1p-126f && ay <= 0x1p126f), 0)) q = __fdiv_rn(x, y);
+    return q;
+}
+
 // bf16 (stored as uint16_t bits) <-> fp32; fp32 -> bf16 rounds to nearest even, as
 // c10::BFloat16 does.
 // fp32 -> bf16, round to nearest even, on gfx950's v_cvt_pk_bf16_f32; NaN becomes 0x7fc0, as

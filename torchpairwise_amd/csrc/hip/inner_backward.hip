@@ -40,7 +40,15 @@
 namespace tpw {
 namespace {
 
-enum Mode { kEuclid = 0, kCosDist = 1, kCosSim = 2, kSqEuclid = 3, kPoly = 4, kSigmoid = 5, kCosCorr = 6, kDot = 7 };
+enum Mode {
+    kEuclid = 0, kCosDist = 1, kCosSim = 2, kSqEuclid = 3, kPoly = 4, kSigmoid = 5, kCosCorr = 6, kDot = 7,
+    // the cosine modes with the weights formed from the forward's output instead of a recomputed S
+    kCosDistO = 8, kCosSimO = 9, kCosCorrO = 10
+};
+// S-based cosine modes, output-based ones, and either
+template <int MODE> constexpr bool kCosS = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+template <int MODE> constexpr bool kCosO = MODE == kCosDistO || MODE == kCosSimO || MODE == kCosCorrO;
+template <int MODE> constexpr bool kCosAny = kCosS<MODE> || kCosO<MODE>;
 
 // x^k for an integral k as ATen's pow with a scalar exponent computes it on the GPU.
 __device__ __forceinline__ float ipow(float x, int k) {
@@ -58,7 +66,9 @@ constexpr int kPWCols = 256;
 // One pair's stored weight w (for BF16W the euclidean / sqeuclidean weight is already rounded
 // to bf16, as the reference's bf16 autograd rounds its ratio tensor), its row-sum term rt and
 // column-sum term ct, from the upstream grad gv, av (res for euclid / sigmoid, S for the
-// polynomial and cosine modes), and for cosine the row and column norms nv, a2.
+// polynomial and the S-based cosine modes, the forward's output o for the output-based ones),
+// and for cosine the row and column norms nv, a2.  Quotients by res and by the norm product
+// use fast_div (the reciprocal, within 2 ulp of the reference's divide).
 template <int MODE, bool BF16W>
 __device__ __forceinline__ void weight_terms(float gv, float av, float nv, float a2, const KerParams &kp, float &w,
                                              float &rt, float &ct) {
@@ -66,7 +76,7 @@ __device__ __forceinline__ void weight_terms(float gv, float av, float nv, float
     rt = 0.0f;
     ct = 0.0f;
     if constexpr (MODE == kEuclid) {
-        w = av == 0.0f ? 0.0f : __fdiv_rn(gv, av);
+        w = av == 0.0f ? 0.0f : fast_div(gv, av);
         if constexpr (BF16W) w = bf16_to_f32(f32_to_bf16_rne(w));
         rt = w;
         ct = w;
@@ -86,6 +96,22 @@ __device__ __forceinline__ void weight_terms(float gv, float av, float nv, float
         w = (gv * (1.0f - av * av)) * kp.gamma;
     } else if constexpr (MODE == kDot) {
         w = gv;  // matmul's backward: the products with grad itself
+    } else if constexpr (kCosO<MODE>) {
+        // q = S / den from the output o: o itself (similarity), 1 - o (distance, correlation).
+        // The distance's clip passes the gradient where 0 <= 1 - q <= 2; from o alone the
+        // bounds o = 0 and o = 2 cannot tell an exact 1 - q = 0 (or 2) from a clipped one, and
+        // both count as clipped.  (An unclipped q of exactly +-1 belongs to a pair whose
+        // gradient terms cancel to rounding level: gS (x2 - q (n2 / n1) x1) for parallel rows.)
+        const float a1 = nv, den = a1 * a2;
+        const float q = MODE == kCosSimO ? av : 1.0f - av;
+        float gq = MODE == kCosSimO ? gv : -gv;
+        if constexpr (MODE == kCosDistO) gq = (av > 0.0f && av < 2.0f) ? gq : 0.0f;
+        const float gS = den != 0.0f ? fast_div(gq, den) : gq;
+        // gden = gS * -S / den = -gS q (0 where den == 0, as prf_div's backward)
+        const float gden = den != 0.0f ? -(gS * q) : 0.0f;
+        w = gS;
+        rt = gden * a2;
+        ct = gden * a1;
     } else {
         const float sv = av, a1 = nv;
         const float den = a1 * a2;
@@ -97,8 +123,8 @@ __device__ __forceinline__ void weight_terms(float gv, float av, float nv, float
         } else if constexpr (MODE == kCosCorr) {
             gq = -gv;  // neg_ then add_(1): no clamp
         }
-        const float gS = den != 0.0f ? __fdiv_rn(gq, den) : gq;
-        const float gden = den != 0.0f ? __fdiv_rn(gS * -sv, den) : 0.0f;
+        const float gS = den != 0.0f ? fast_div(gq, den) : gq;
+        const float gden = den != 0.0f ? fast_div(gS * -sv, den) : 0.0f;
         w = gS;
         rt = gden * a2;
         ct = gden * a1;
@@ -128,14 +154,14 @@ __global__ __launch_bounds__(256) void pair_weights_kernel(
     const int64_t j = tj * kPWCols + tid;
     const bool jok = j < m;
     float a2 = 0.0f;
-    if constexpr (MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr) a2 = jok ? n2[b * m + j] : 0.0f;
+    if constexpr (kCosAny<MODE>) a2 = jok ? n2[b * m + j] : 0.0f;
     float csum = 0.0f;
     // One element from its loaded operands (gv = grad; av = res for euclid / sigmoid, S for
     // polynomial / cosine; nv = n1[i] for cosine): the stored weight (wf, or its bf16 bits wb)
     // and the row-sum term rt.
-    constexpr bool kRes = MODE == kEuclid || MODE == kSigmoid;
-    constexpr bool kS = MODE == kPoly || MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
-    constexpr bool kCos = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+    constexpr bool kRes = MODE == kEuclid || MODE == kSigmoid || kCosO<MODE>;
+    constexpr bool kS = MODE == kPoly || kCosS<MODE>;
+    constexpr bool kCos = kCosAny<MODE>;
     auto element = [&](bool ok, int64_t idx, float gv, float av, float nv, float &wf, uint16_t &wb, float &rt) {
         wf = 0.0f;
         wb = 0;
@@ -280,9 +306,9 @@ __global__ __launch_bounds__(256) void pair_weights_vec_kernel(
     float *__restrict__ rowpart, float *__restrict__ colpart, int64_t tiles_i, int64_t tiles_j,
     float *__restrict__ Wo, KerParams kp) {
 #pragma clang fp contract(off)
-    constexpr bool kRes = MODE == kEuclid || MODE == kSigmoid;
-    constexpr bool kS = MODE == kPoly || MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
-    constexpr bool kCos = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+    constexpr bool kRes = MODE == kEuclid || MODE == kSigmoid || kCosO<MODE>;
+    constexpr bool kS = MODE == kPoly || kCosS<MODE>;
+    constexpr bool kCos = kCosAny<MODE>;
     __shared__ floatx4 red[4][64];
     const int64_t b = blockIdx.z, ti = blockIdx.y, tj = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1185,7 +1211,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     T *x1t = static_cast<T *>(w.x1t), *x2t = static_cast<T *>(w.x2t);
     int rc;
     constexpr bool kBf16 = sizeof(T) == 2;
-    constexpr bool kCosMode = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+    constexpr bool kCosMode = kCosS<MODE>;  // S recomputed (the output-based modes read res)
     // bf16: the tile kernel reads x2 (for gx1) and W, x1 (for gx2) k-major in place where the
     // shapes allow (no W^T, no transposed inputs)
     bool bf16_kmajor = false;
@@ -1269,7 +1295,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     int64_t tj = cdiv(m, kPWCols);
     bool vec_pass = false;
     if constexpr (!kBf16) {
-        const void *av = (MODE == kEuclid || MODE == kSigmoid) ? static_cast<const void *>(res) : w.S;
+        const void *av = (MODE == kEuclid || MODE == kSigmoid || kCosO<MODE>) ? static_cast<const void *>(res) : w.S;
         vec_pass = m % 4 == 0 && aligned16(g) && aligned16(av) && aligned16(W) && aligned16(w.colpart) &&
                    (n2 == nullptr || aligned16(n2));
     }
@@ -1294,7 +1320,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
         rc = check_launch("pair_weights_kernel");
     }
     if (rc) return rc;
-    const bool cosine = MODE == kCosDist || MODE == kCosSim || MODE == kCosCorr;
+    const bool cosine = kCosAny<MODE>;
     const float *div1 = cosine ? n1 : nullptr;
     const float *div2 = cosine ? n2 : nullptr;
     hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)cdiv(batch * n, 256)), dim3(256), 0, s,
@@ -1382,7 +1408,7 @@ extern "C" int tpw_euclidean_backward(const void *grad, const void *x1, const vo
 }
 
 extern "C" int tpw_cosine_backward(const void *grad, const void *x1, const void *x2,
-                                   const float *norms1, const float *norms2, int dtype,
+                                   const float *norms1, const float *norms2, const void *out, int dtype,
                                    int64_t batch, int64_t n, int64_t m, int64_t d, int similarity,
                                    void *grad_x1, void *grad_x2, void *workspace, void *stream) {
     TPW_REQUIRE(dtype == TPW_F32 || dtype == TPW_BF16, "unsupported dtype %d", dtype);
@@ -1396,19 +1422,28 @@ extern "C" int tpw_cosine_backward(const void *grad, const void *x1, const void 
                     cdiv(n, kGT) <= kMaxGridYZ && batch <= kMaxGridYZ,
                 "sizes exceed the launch grid");
     hipStream_t s = as_stream(stream);
+    // with the forward's output, the weights come from it (no recomputed S)
     if (dtype == TPW_F32) {
-        auto run = similarity == 2 ? run_backward<float, kCosCorr>
-                   : similarity ? run_backward<float, kCosSim> : run_backward<float, kCosDist>;
+        auto run = out ? (similarity == 2 ? run_backward<float, kCosCorrO>
+                          : similarity    ? run_backward<float, kCosSimO>
+                                          : run_backward<float, kCosDistO>)
+                       : (similarity == 2 ? run_backward<float, kCosCorr>
+                          : similarity    ? run_backward<float, kCosSim>
+                                          : run_backward<float, kCosDist>);
         return run(static_cast<const float *>(grad), static_cast<const float *>(x1),
-                   static_cast<const float *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
-                   static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s,
+                   static_cast<const float *>(x2), static_cast<const float *>(out), norms1, norms2, dtype, batch,
+                   n, m, d, static_cast<float *>(grad_x1), static_cast<float *>(grad_x2), workspace, s,
                    KerParams{});
     }
-    auto run = similarity == 2 ? run_backward<uint16_t, kCosCorr>
-               : similarity ? run_backward<uint16_t, kCosSim> : run_backward<uint16_t, kCosDist>;
+    auto run = out ? (similarity == 2 ? run_backward<uint16_t, kCosCorrO>
+                      : similarity    ? run_backward<uint16_t, kCosSimO>
+                                      : run_backward<uint16_t, kCosDistO>)
+                   : (similarity == 2 ? run_backward<uint16_t, kCosCorr>
+                      : similarity    ? run_backward<uint16_t, kCosSim>
+                                      : run_backward<uint16_t, kCosDist>);
     return run(static_cast<const uint16_t *>(grad), static_cast<const uint16_t *>(x1),
-               static_cast<const uint16_t *>(x2), nullptr, norms1, norms2, dtype, batch, n, m, d,
-               static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s,
+               static_cast<const uint16_t *>(x2), static_cast<const uint16_t *>(out), norms1, norms2, dtype, batch,
+               n, m, d, static_cast<uint16_t *>(grad_x1), static_cast<uint16_t *>(grad_x2), workspace, s,
                KerParams{});
 }
 

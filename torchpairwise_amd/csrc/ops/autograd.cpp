@@ -25,7 +25,11 @@ class PwInnerFunction : public torch::autograd::Function<PwInnerFunction> {
                             int64_t epilogue) {
         at::AutoDispatchBelowADInplaceOrView g;
         auto out = pw_inner(x1, x2, epilogue);
-        if (epilogue == kEuclidean)
+        // euclidean's backward divides by the output; the cosine family's forms its weights
+        // from it on the GPU (no recomputed x1 . x2^T)
+        const bool cos_family = epilogue == TPW_EPI_COSINE_SIM || epilogue == TPW_EPI_COSINE_DIST ||
+                                epilogue == TPW_EPI_CORRELATION;
+        if (epilogue == kEuclidean || (cos_family && out.is_cuda()))
             ctx->save_for_backward({x1, x2, out});
         else
             ctx->save_for_backward({x1, x2});

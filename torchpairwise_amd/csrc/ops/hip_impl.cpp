@@ -164,8 +164,10 @@ std::tuple<at::Tensor, at::Tensor> pw_inner_backward_cuda(const at::Tensor &grad
         auto n2 = at::empty({B, m}, a.options().dtype(at::kFloat));
         check_rc(tpw_row_norms(a.data_ptr(), dt, B * n, d, 0, n1.data_ptr<float>(), s), "row norms");
         check_rc(tpw_row_norms(b.data_ptr(), dt, B * m, d, 0, n2.data_ptr<float>(), s), "row norms");
+        // the forward's output, when autograd saved it: the weights come from it
+        at::Tensor o = res.defined() ? res.reshape({B, n, m}).contiguous() : at::Tensor();
         check_rc(tpw_cosine_backward(g.data_ptr(), a.data_ptr(), b.data_ptr(), n1.data_ptr<float>(),
-                                     n2.data_ptr<float>(), dt, B, n, m, d,
+                                     n2.data_ptr<float>(), o.defined() ? o.data_ptr() : nullptr, dt, B, n, m, d,
                                      epilogue == TPW_EPI_CORRELATION ? 2 : epilogue == TPW_EPI_COSINE_SIM,
                                      gx1.data_ptr(), gx2.data_ptr(), ws.data_ptr(), s),
                  "cosine backward");

@@ -609,8 +609,12 @@ int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t batch, int6
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): it calls no hipMalloc / hipFree.  Sizes whose
  * tpw_hausdorff_workspace_size exceeds the buffer are rejected with TPW_ERR_INVALID (the
- * [16, 65536, 3] x [16, 65536, 3] case needs 67 MiB).  Every call on one GPU shares that
- * GPU's buffer: calls that overlap on one GPU (concurrent streams or threads) race. */
+ * [16, 65536, 3] x [16, 65536, 3] case needs 67 MiB).  The array is in a code object of its
+ * own: a GPU holds it from this entry point's first call there, and processes that never call
+ * it hold none.  Every call on one GPU shares that GPU's buffer, so calls are serialised: each
+ * call's stream waits for the previous call's work on that GPU (one event per device, created
+ * at the first call) before its own.  Under HIP graph capture that wait is left out and the
+ * graph's order is the caller's to give: captured calls that overlap on one GPU race. */
 int tpw_directed_hausdorff_noalloc(const float *x1, const float *x2, int64_t batch, int64_t b1,
                                    int64_t p1, int64_t b2, int64_t p2, int64_t d,
                                    const int64_t *perm1, const int64_t *perm2, float *out,

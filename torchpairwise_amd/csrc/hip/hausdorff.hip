@@ -1686,62 +1686,3 @@ extern "C" int tpw_directed_hausdorff_backward(const float *grad, const float *x
                        s, grad, x1, x2, out, idx1, idx2, batch, b1, p1, b2, p2, d, grad_x2);
     return check_launch("hausdorff backward");
 }
-
-// ---------------------------------------------------------------------------------------
-// Allocation-free variant: the same kernels with their scratch in a static device array.
-// Every GPU the library runs on holds its own copy of `scratch` (at its own address) until
-// the process ends; calls on one GPU share it, so overlapping calls on one GPU race.  The
-// kernels initialise every part of the scratch they read (the presets fill above), so the
-// previous call's contents never leak into a result.
-// ---------------------------------------------------------------------------------------
-namespace tpw {
-namespace {
-
-constexpr size_t kNoAllocScratchBytes = (size_t)TPW_HAUSDORFF_NOALLOC_SCRATCH_MIB << 20;
-static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
-
-// The device address of `scratch` on the current device, looked up once per device with
-// hipGetSymbolAddress (the array's name is only a host-side stand-in in host code).
-int noalloc_scratch(void **out) {
-    constexpr int kMaxDevices = 64;
-    static std::mutex mu;
-    static void *ptrs[kMaxDevices] = {};
-    int dev = -1;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        set_error("directed_hausdorff_noalloc: no usable current device (%s)", hipGetErrorString(e));
-        return TPW_ERR_LAUNCH;
-    }
-    std::lock_guard<std::mutex> lock(mu);
-    if (ptrs[dev] == nullptr) {
-        void *p = nullptr;
-        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || p == nullptr) {
-            set_error("directed_hausdorff_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
-                      hipGetErrorString(e));
-            return TPW_ERR_LAUNCH;
-        }
-        ptrs[dev] = p;
-    }
-    *out = ptrs[dev];
-    return TPW_OK;
-}
-
-}  // namespace
-}  // namespace tpw
-
-extern "C" int tpw_directed_hausdorff_noalloc(const float *x1, const float *x2, int64_t batch, int64_t b1,
-                                              int64_t p1, int64_t b2, int64_t p2, int64_t d,
-                                              const int64_t *perm1, const int64_t *perm2, float *out,
-                                              int64_t *idx1, int64_t *idx2, void *stream) {
-    TPW_REQUIRE(batch >= 0 && b1 >= 0 && b2 >= 0 && p1 >= 0 && p2 >= 0 && d >= 0, "invalid sizes");
-    const size_t need = tpw_hausdorff_workspace_size(batch, b1, p1, b2, p2, d);
-    TPW_REQUIRE(need <= tpw::kNoAllocScratchBytes,
-                "directed_hausdorff_noalloc: these sizes need %zu bytes of scratch, more than the %zu-byte "
-                "static buffer; call tpw_directed_hausdorff with a workspace instead",
-                need, tpw::kNoAllocScratchBytes);
-    void *ws = nullptr;
-    const int rc = tpw::noalloc_scratch(&ws);
-    if (rc != TPW_OK) return rc;
-    return tpw_directed_hausdorff(x1, x2, batch, b1, p1, b2, p2, d, perm1, perm2, out, idx1, idx2, ws, stream);
-}

@@ -235,9 +235,15 @@ def test_euclidean_backward(B, n, m, d, dtype):
     gx1_ref, gx2_ref = torch.autograd.grad(res, (a, b), g.double())
     res_dev = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_EUCLIDEAN)
     gx1, gx2 = capi.euclidean_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), res_dev)
-    rtol = 1e-4 if dtype == torch.float32 else 1e-2
+    if dtype == torch.float32:  # the derived per-element bound, per batch
+        from tests import _gradbound as GB
+        for bb in range(B):
+            GB.check(gx1[bb].cpu(), gx1_ref[bb], GB.euclidean_grad_bound(x1[bb], x2[bb], g[bb]), "euclidean grad_x1")
+            GB.check(gx2[bb].cpu(), gx2_ref[bb], GB.euclidean_grad_bound(x2[bb], x1[bb], g[bb].T),
+                     "euclidean grad_x2")
+        return
     for got, want, nm in ((gx1, gx1_ref, "grad_x1"), (gx2, gx2_ref, "grad_x2")):
-        assert_close(got.float(), want, rtol=rtol, atol=rtol * float(want.abs().max()),
+        assert_close(got.float(), want, rtol=1e-2, atol=1e-2 * float(want.abs().max()),
                      what=f"euclidean {dtype} {nm}")
 
 
@@ -260,7 +266,15 @@ def test_cosine_backward(B, n, m, d, dtype, similarity, from_output):
     if from_output:
         out = capi.pairwise_inner(x1.to(DEV), x2.to(DEV), capi.EPI_COSINE_SIM if similarity else capi.EPI_COSINE_DIST)
     gx1, gx2 = capi.cosine_backward(g.to(DEV), x1.to(DEV), x2.to(DEV), similarity=similarity, out=out)
-    rtol = 1e-4 if dtype == torch.float32 else 1e-2
+    if dtype == torch.float32:  # the derived per-element bound, per batch
+        from tests import _gradbound as GB
+        for bb in range(B):
+            GB.check(gx1[bb].cpu(), gx1_ref[bb], GB.cosine_grad_bound(x1[bb], x2[bb], g[bb], similarity),
+                     f"cosine sim={similarity} grad_x1")
+            GB.check(gx2[bb].cpu(), gx2_ref[bb], GB.cosine_grad_bound(x2[bb], x1[bb], g[bb].T, similarity),
+                     f"cosine sim={similarity} grad_x2")
+        return
+    rtol = 1e-2
     for got, want, nm in ((gx1, gx1_ref, "grad_x1"), (gx2, gx2_ref, "grad_x2")):
         assert_close(got.float(), want, rtol=rtol, atol=rtol * float(want.abs().max()),
                      what=f"cosine sim={similarity} {dtype} {nm}")

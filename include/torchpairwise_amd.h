@@ -309,6 +309,20 @@ int tpw_pairwise_inner(const void *x1, const void *x2, int dtype, int64_t batch,
 int tpw_lp_distances(const float *x1, const float *x2, int64_t batch, int64_t n,
                      int64_t m, int64_t d, double p, float *out, void *stream);
 
+/* tpw_lp_distances with a bf16 output [batch,n,m] (uint16 bits): the fp32 result rounded once
+ * to nearest even (NaN to 0x7fc0), written directly, where a float output would be written,
+ * read back and converted.  x1, x2 are fp32 (bf16 inputs widened by the caller).  Replaces
+ * at::cdist on bf16 tensors for p != 2 (csrc/ops/pairwise_metrics.cpp:42-49,160-168,299-306). */
+int tpw_lp_distances_bf16(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                          int64_t d, double p, uint16_t *out, void *stream);
+
+/* out[b,i,j] = v1[b,i] / sum_k (a[b,i,k] - b[b,j,k])^2 (an IEEE divide) for rows a, b
+ * centred by the caller and v1 = sum_k a^2: the forward of _snr as one pass, where the
+ * reference's GPU route writes the squared distances and divides in a second pass
+ * (csrc/ops/cpu/snr_kernel.cpp:13-33, cuda/snr_kernel.cu:100-105).  fp32. */
+int tpw_snr_centered(const float *a, const float *b, const float *v1, int64_t batch, int64_t n,
+                     int64_t m, int64_t d, float *out, void *stream);
+
 /* Workspace (bytes) of tpw_lp_distances_backward (either direction: the same size serves
  * the transposed call) and tpw_lp_distances_backward2 for these sizes. */
 size_t tpw_lp_backward_workspace_size(int64_t batch, int64_t n, int64_t m, int64_t d);

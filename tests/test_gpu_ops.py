@@ -8,6 +8,7 @@ import torchpairwise_amd as tp
 from oracle import cref
 from oracle import pairwise as P
 from tests._util import assert_close, assert_equal, rand, randn
+from torchpairwise_amd import _capi as capi
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -444,6 +445,41 @@ def test_public_ops_gpu_equal_reference(tmp_path):
     if not ref_runner.available():
         pytest.skip("oracle/_ref not built")
     _check_public_cases(torch.ops.torchpairwise, DEV, tmp_path, rtol=1e-5, grad_rtol=1e-4)
+
+
+@pytest.mark.parametrize("fn,p", [("manhattan_distances", 1.0), ("chebyshev_distances", float("inf")),
+                                  ("minkowski_distances", 3.0)])
+def test_bf16_lp_output_written_by_the_kernel(fn, p):
+    """bf16 cdist metrics without a gradient to form: the kernel rounds its fp32 result to bf16
+    and writes it once; bit for bit what the fp32 kernel plus a bf16 conversion gives (the route
+    taken when a gradient is needed), including a ragged row length and NaN rows."""
+    x1 = randn(300, 70, seed=0).bfloat16()
+    x2 = randn(257, 70, seed=1).bfloat16()
+    x1[5, 3] = float("nan")
+    a, b = x1.to(DEV), x2.to(DEV)
+    args = (p,) if fn == "minkowski_distances" else ()
+    with torch.no_grad():
+        got = getattr(tp, fn)(a, b, *args)
+    want = capi.lp_distances(a.float(), b.float(), p).to(torch.bfloat16)
+    assert got.dtype == torch.bfloat16
+    assert_equal(got, want, f"{fn} bf16")
+    # with a gradient to form the autograd route runs; same values
+    ag = a.clone().requires_grad_()
+    out = getattr(tp, fn)(ag, b, *args)
+    assert_equal(out.detach(), want, f"{fn} bf16 autograd route")
+
+
+def test_snr_fused_equals_composition():
+    """_snr on float32 GPU tensors: the squared distances of the centred rows and the divide in
+    one pass (tpw_snr_centered), bit for bit the composition it replaces (variance numerator over
+    _ppminkowski p = 2, an IEEE divide), batched and not."""
+    ops = torch.ops.torchpairwise
+    for s1, s2 in (((130, 33), (257, 33)), ((2, 40, 17), (2, 50, 17))):
+        x1, x2 = randn(*s1, seed=3).to(DEV), randn(*s2, seed=4).to(DEV)
+        got = ops._snr(x1, x2)
+        a, b = x1 - x1.mean(-1, True), x2 - x2.mean(-1, True)
+        want = (a * a).sum(-1, True) / ops._ppminkowski(a, b, 2.0)
+        assert_equal(got, want, f"snr {s1}")
 
 
 def test_sqeuclidean_identical_points_are_zero():

@@ -53,6 +53,8 @@ _SIGNATURES = {
     "tpw_pairwise_kernel_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, C.c_float,
                                           C.c_float, _i, _p, _p, _p, _p]),
     "tpw_lp_distances": (_i, [_p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
+    "tpw_lp_distances_bf16": (_i, [_p, _p, _i64, _i64, _i64, _i64, _d, _p, _p]),
+    "tpw_snr_centered": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]),
     "tpw_lp_backward_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "tpw_lp_distances_backward": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _i, _p, _p, _p]),
     "tpw_lp_distances_backward2": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _d, _p, _p, _p, _p]),
@@ -412,6 +414,31 @@ def lp_distances(x1, x2, p):
     out = torch.empty((B, n, m), dtype=torch.float32, device=x1.device)
     call("tpw_lp_distances", _ptr(a), _ptr(b), B, n, m, d, float(p), _ptr(out), _stream())
     return out if x1.dim() == 3 else out[0]
+
+
+def lp_distances_bf16(x1, x2, p):
+    """Lp distances of fp32 rows with the output rounded to bf16 by the kernel."""
+    import torch
+
+    a, b = _as3(x1).contiguous(), _as3(x2).contiguous()
+    B, n, d = a.shape
+    m = b.shape[1]
+    out = torch.empty((B, n, m), dtype=torch.bfloat16, device=x1.device)
+    call("tpw_lp_distances_bf16", _ptr(a), _ptr(b), B, n, m, d, float(p), _ptr(out), _stream())
+    return out if x1.dim() == 3 else out[0]
+
+
+def snr_centered(a, b, v1):
+    """v1[i] / sum_k (a[i, k] - b[j, k])^2 for centred rows a, b (fp32)."""
+    import torch
+
+    a3, b3 = _as3(a).contiguous(), _as3(b).contiguous()
+    B, n, d = a3.shape
+    m = b3.shape[1]
+    v = v1.reshape(B, n).contiguous()
+    out = torch.empty((B, n, m), dtype=torch.float32, device=a.device)
+    call("tpw_snr_centered", _ptr(a3), _ptr(b3), _ptr(v), B, n, m, d, _ptr(out), _stream())
+    return out if a.dim() == 3 else out[0]
 
 
 def lp_distances_backward(grad, x1, x2, dist, p):

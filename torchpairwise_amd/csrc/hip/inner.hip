@@ -67,6 +67,9 @@ constexpr int kEpiRadiusB = 105;
 // EPI = kEpiTopK + 2 log2(C / 2) for C = 2, 4, 8, 16, + 1 when the distance is first rounded to
 // bf16, as the bf16 distance op stores it.
 constexpr int kEpiTopK = 106;
+// The polynomial kernel for degree 0 .. 3 (products, no powf): the same values as kEpiPoly, on
+// the tile kernel, whose four blocks per CU the general degree's powf would spill.
+constexpr int kEpiPolySmall = 120;
 // Output stores: non-temporal for fp32 and bf16 (matrix-core or data-path bound: plain stores
 // cost 1-4 %), plain for the radius mask's bool bytes (0.553 -> 0.540 ms at 16384^2).
 template <typename OutT>
@@ -87,6 +90,15 @@ constexpr bool kAux1 = EPI == TPW_EPI_EUCLIDEAN || EPI == TPW_EPI_SQEUCLIDEAN ||
 template <int EPI>
 constexpr bool kAux2 = kAux1<EPI> && EPI != kEpiGrad;
 
+// x^k for k = 0 .. 3 as ipow below computes it (products).
+__device__ __forceinline__ float ipow_small(float x, int k) {
+#pragma clang fp contract(off)
+    if (k == 2) return x * x;
+    if (k == 3) return x * x * x;
+    if (k == 1) return x;
+    return 1.0f;
+}
+
 // x^k for an integral k as ATen's pow with a scalar exponent computes it on the GPU: k = 2, 3
 // as products, otherwise the float power function.
 __device__ __forceinline__ float ipow(float x, int k) {
@@ -101,9 +113,10 @@ __device__ __forceinline__ float ipow(float x, int k) {
 template <int EPI>
 __device__ __forceinline__ float epilogue(float s, float a1, float a2, const KerParams &kp) {
 #pragma clang fp contract(off)
-    if constexpr (EPI == kEpiPoly || EPI == kEpiSigmoid) {
+    if constexpr (EPI == kEpiPoly || EPI == kEpiPolySmall || EPI == kEpiSigmoid) {
         // the reference's matmul(...).mul_(gamma).add_(coef0), then pow_ / tanh_
         const float base = s * kp.gamma + kp.coef0;
+        if constexpr (EPI == kEpiPolySmall) return ipow_small(base, kp.degree);
         return EPI == kEpiPoly ? ipow(base, kp.degree) : tanhf(base);
     } else if constexpr (EPI == TPW_EPI_DOT || EPI == kEpiGrad) {
         return s;
@@ -1074,12 +1087,18 @@ extern "C" int tpw_pairwise_kernel(const void *x1, const void *x2, int dtype, in
     if (dtype == TPW_F32) {
         auto a = static_cast<const float *>(x1), b = static_cast<const float *>(x2);
         auto o = static_cast<float *>(out);
+        if (kind == TPW_KER_POLYNOMIAL && degree >= 0 && degree <= 3)
+            return launch_inner<float, kEpiPolySmall, float>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr,
+                                                             1.0f, kp);
         return kind == TPW_KER_POLYNOMIAL
                    ? launch_inner<float, kEpiPoly, float>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr, 1.0f, kp)
                    : launch_inner<float, kEpiSigmoid, float>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr, 1.0f, kp);
     }
     auto a = static_cast<const uint16_t *>(x1), b = static_cast<const uint16_t *>(x2);
     auto o = static_cast<uint16_t *>(out);
+    if (kind == TPW_KER_POLYNOMIAL && degree >= 0 && degree <= 3)
+        return launch_inner<uint16_t, kEpiPolySmall, uint16_t>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr,
+                                                               1.0f, kp);
     return kind == TPW_KER_POLYNOMIAL
                ? launch_inner<uint16_t, kEpiPoly, uint16_t>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr, 1.0f, kp)
                : launch_inner<uint16_t, kEpiSigmoid, uint16_t>(a, b, batch, n, m, d, nullptr, nullptr, o, s, nullptr, 1.0f, kp);

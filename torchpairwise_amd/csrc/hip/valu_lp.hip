@@ -197,13 +197,16 @@ __device__ __forceinline__ float fam_finish(float acc, float inv_p, float prev) 
 }
 
 // w: per-feature weights [batch, d] (kWeighted only).  out: read first under kBrayDen.
+// rownum: out = rownum[row] / value (IEEE divide), the signal-to-noise ratio's variance over the
+// pair's squared distance.  out16: the values are stored rounded to bf16 there instead of to
+// out (the cdist of bf16 inputs, computed in fp32 and rounded once).
 // exp_post: out = exp(value * post), the kernel functions exp(-gamma * distance) of
 // rbf_kernel / laplacian_kernel (one rounding per operation, as mul_ then exp_).
 template <int MODE, int PK, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
     int64_t n, int64_t m, int64_t d, float p, float inv_p, float *__restrict__ out, int exp_post,
-    float post) {
+    float post, const float *__restrict__ rownum, uint16_t *__restrict__ out16) {
     __shared__ float As[kBK][kTile + kPad];
     __shared__ float Bs[kBK][kTile + kPad];
     __shared__ float Wk[MODE == kWeighted ? kBK : 1];
@@ -344,6 +347,11 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll
                             for (int c = 0; c < 4; ++c) v[c] = expf(v[c] * post);
                         }
+                        if (rownum) {
+                            const float num = row < n ? rownum[b * n + row] : 0.0f;
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) v[c] = __fdiv_rn(num, v[c]);
+                        }
 #pragma unroll
                         for (int c = 0; c < 4; ++c) st[(8 * ty + i - 64 * rh) * kSt + 4 * tx + c] = v[c];
                     }
@@ -353,7 +361,10 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll 4
                 for (int r = 16 * wave; r < 16 * wave + 16; ++r) {
                     const int64_t row = row0 + 64 * rh + r;
-                    if (row < n && col < m) store_nt(out + (b * n + row) * m + col, st[r * kSt + lane]);
+                    if (row < n && col < m) {
+                        if (out16) out16[(b * n + row) * m + col] = f32_to_bf16_rne(st[r * kSt + lane]);
+                        else store_nt(out + (b * n + row) * m + col, st[r * kSt + lane]);
+                    }
                 }
                 __syncthreads();  // the quarter is written before the next one is staged
             }
@@ -385,7 +396,24 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll
                 for (int c = 0; c < 4; ++c) v[c] = expf(v[c] * post);
             }
-            if (vec_store && col + 3 < m) {
+            if (rownum) {
+                const float num = rownum[b * n + row];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = __fdiv_rn(num, v[c]);
+            }
+            if (out16) {
+                uint16_t *o16 = out16 + (b * n + row) * m;
+                if (vec_store && col + 3 < m) {
+                    const uint2 pk = make_uint2((uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16),
+                                                (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16));
+                    __builtin_nontemporal_store(pk.x, reinterpret_cast<uint32_t *>(o16 + col));
+                    __builtin_nontemporal_store(pk.y, reinterpret_cast<uint32_t *>(o16 + col) + 1);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (col + c < m) o16[col + c] = f32_to_bf16_rne(v[c]);
+                }
+            } else if (vec_store && col + 3 < m) {
                 store_nt4(orow + col, v);
             } else {
 #pragma unroll
@@ -976,32 +1004,34 @@ int pkind_of(double p) {
 template <int MODE, int PK>
 int launch_forward(const float *x1, const float *x2, const float *w, int64_t batch, int64_t n,
                    int64_t m, int64_t d, double p, float *out, hipStream_t s, bool exp_post = false,
-                   float post = 0.0f) {
+                   float post = 0.0f, const float *rownum = nullptr, uint16_t *out16 = nullptr) {
     dim3 grid((unsigned)cdiv(m, kTile), (unsigned)cdiv(n, kTile), (unsigned)batch);
-    const bool vec = (d % 4 == 0) && aligned16(x1) && aligned16(x2) && aligned16(out);
+    const bool vec = (d % 4 == 0) && aligned16(x1) && aligned16(x2) && aligned16(out) && aligned16(out16);
     const float pf = (float)p, inv_p = (float)(1.0 / p);
     const LaunchEvents ev = launch_events("lp_forward_kernel");
     if (vec)
         hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, true>), grid, dim3(kThreads), 0, s, ev.start, ev.stop, 0, x1, x2,
-                           w, n, m, d, pf, inv_p, out, (int)exp_post, post);
+                           w, n, m, d, pf, inv_p, out, (int)exp_post, post, rownum, out16);
     else
         hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, false>), grid, dim3(kThreads), 0, s, ev.start, ev.stop, 0, x1,
-                           x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post);
+                           x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post, rownum, out16);
     return check_launch("lp_forward_kernel");
 }
 
 template <int MODE>
 int dispatch_forward(int pk, const float *x1, const float *x2, const float *w, int64_t batch,
-                     int64_t n, int64_t m, int64_t d, double p, float *out, hipStream_t s) {
+                     int64_t n, int64_t m, int64_t d, double p, float *out, hipStream_t s,
+                     uint16_t *out16 = nullptr) {
     switch (pk) {
-        case kP0: return launch_forward<MODE, kP0>(x1, x2, w, batch, n, m, d, p, out, s);
-        case kP1: return launch_forward<MODE, kP1>(x1, x2, w, batch, n, m, d, p, out, s);
-        case kP2: return launch_forward<MODE, kP2>(x1, x2, w, batch, n, m, d, p, out, s);
-        case kP3: return launch_forward<MODE, kP3>(x1, x2, w, batch, n, m, d, p, out, s);
-        case kPInf: return launch_forward<MODE, kPInf>(x1, x2, w, batch, n, m, d, p, out, s);
-        case kPNInf: return launch_forward<MODE, kPNInf>(x1, x2, w, batch, n, m, d, p, out, s);
-        case kPLt2: return launch_forward<MODE, kPLt2>(x1, x2, w, batch, n, m, d, p, out, s);
-        default: return launch_forward<MODE, kPGen>(x1, x2, w, batch, n, m, d, p, out, s);
+        case kP0: return launch_forward<MODE, kP0>(x1, x2, w, batch, n, m, d, p, out, s, false, 0.0f, nullptr, out16);
+        case kP1: return launch_forward<MODE, kP1>(x1, x2, w, batch, n, m, d, p, out, s, false, 0.0f, nullptr, out16);
+        case kP2: return launch_forward<MODE, kP2>(x1, x2, w, batch, n, m, d, p, out, s, false, 0.0f, nullptr, out16);
+        case kP3: return launch_forward<MODE, kP3>(x1, x2, w, batch, n, m, d, p, out, s, false, 0.0f, nullptr, out16);
+        case kPInf: return launch_forward<MODE, kPInf>(x1, x2, w, batch, n, m, d, p, out, s, false, 0.0f, nullptr, out16);
+        case kPNInf:
+            return launch_forward<MODE, kPNInf>(x1, x2, w, batch, n, m, d, p, out, s, false, 0.0f, nullptr, out16);
+        case kPLt2: return launch_forward<MODE, kPLt2>(x1, x2, w, batch, n, m, d, p, out, s, false, 0.0f, nullptr, out16);
+        default: return launch_forward<MODE, kPGen>(x1, x2, w, batch, n, m, d, p, out, s, false, 0.0f, nullptr, out16);
     }
 }
 
@@ -1206,6 +1236,24 @@ extern "C" int tpw_lp_distances(const float *x1, const float *x2, int64_t batch,
     TPW_REQUIRE(x1 && x2 && out, "null pointer");
     return dispatch_forward<kRoot>(pkind_of(p), x1, x2, nullptr, batch, n, m, d, p, out,
                                    as_stream(stream));
+}
+
+extern "C" int tpw_lp_distances_bf16(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
+                                     int64_t d, double p, uint16_t *out, void *stream) {
+    TPW_FAM_CHECKS();
+    TPW_REQUIRE(p >= 0.0, "p must be non-negative, got %g", p);
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(x1 && x2 && out, "null pointer");
+    return dispatch_forward<kRoot>(pkind_of(p), x1, x2, nullptr, batch, n, m, d, p, nullptr, as_stream(stream),
+                                   out);
+}
+
+extern "C" int tpw_snr_centered(const float *a, const float *b, const float *v1, int64_t batch, int64_t n,
+                                int64_t m, int64_t d, float *out, void *stream) {
+    TPW_FAM_CHECKS();
+    if (batch == 0 || n == 0 || m == 0) return TPW_OK;
+    TPW_REQUIRE(a && b && v1 && out, "null pointer");
+    return launch_forward<kSum, kP2>(a, b, nullptr, batch, n, m, d, 2.0, out, as_stream(stream), false, 0.0f, v1);
 }
 
 extern "C" size_t tpw_lp_backward_workspace_size(int64_t batch, int64_t n, int64_t m, int64_t d) {

@@ -507,6 +507,19 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_cuda(
 
 }  // namespace
 
+at::Tensor lp_distances_bf16_cuda(const at::Tensor &x1, const at::Tensor &x2, double p) {
+    check_cuda_pair("cdist", x1, x2);
+    TORCH_CHECK(x1.scalar_type() == at::kFloat && x2.scalar_type() == at::kFloat, "cdist: float32 rows expected");
+    DeviceGuard guard(x1.device());
+    auto a = as3(x1), b = as3(x2);
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options().dtype(at::kBFloat16));
+    check_rc(tpw_lp_distances_bf16(a.data_ptr<float>(), b.data_ptr<float>(), B, n, m, d, p,
+                                   reinterpret_cast<uint16_t *>(out.data_ptr()), current_stream()),
+             "cdist");
+    return out_shape(out, x1);
+}
+
 std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_indexed_cuda(
     const at::Tensor &grad, const at::Tensor &x1, const at::Tensor &x2, const at::Tensor &out,
     const at::Tensor &i1, const at::Tensor &i2) {

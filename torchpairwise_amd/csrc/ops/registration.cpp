@@ -84,8 +84,13 @@ at::Tensor route_cdist(const at::Tensor &x1, const at::Tensor &x2, double p) {
     auto ab = broadcast_batch(x1, x2);
     const at::Tensor &a = ab.first, &b = ab.second;
     if (p == 2.0 && (a.size(-2) > 25 || b.size(-2) > 25)) return pw_inner(a, b, kEuclidean);
-    if (a.scalar_type() == at::kBFloat16)
+    if (a.scalar_type() == at::kBFloat16) {
+        // without a gradient to form, the kernel writes the bf16 output itself (one pass over
+        // the N x M output instead of a float32 matrix written, read back and converted)
+        if (!(at::GradMode::is_enabled() && (a.requires_grad() || b.requires_grad())))
+            return lp_distances_bf16_cuda(a.to(at::kFloat), b.to(at::kFloat), p);
         return pw_lp(a.to(at::kFloat), b.to(at::kFloat), p).to(at::kBFloat16);
+    }
     return pw_lp(a, b, p);
 }
 

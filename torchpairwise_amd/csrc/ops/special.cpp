@@ -285,9 +285,27 @@ void snr_check_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     check_float_dispatch(x1.scalar_type(), false, "_snr_forward_cuda");
 }
 
+// Below autograd (the backward recomputes through the composition): for float32 the centred
+// rows and the numerator are O((n + m) d), and the pairs' squared distances and the divide are
+// one pass of the VALU kernel (tpw_snr_centered), which writes the output once.
 at::Tensor snr_cuda(const at::Tensor &x1, const at::Tensor &x2) {
     snr_check_cuda(x1, x2);
-    return snr_composite(x1, x2);
+    if (x1.scalar_type() != at::kFloat || x2.scalar_type() != at::kFloat || x1.dim() != x2.dim() ||
+        (x1.dim() != 2 && x1.dim() != 3))
+        return snr_composite(x1, x2);
+    DeviceGuard guard(x1.device());
+    auto a3 = x1.dim() == 3 ? x1 : x1.unsqueeze(0);
+    auto b3 = x2.dim() == 3 ? x2 : x2.unsqueeze(0);
+    if (a3.size(0) != b3.size(0)) return snr_composite(x1, x2);
+    auto a = (a3 - a3.mean(-1, true)).contiguous();
+    auto b = (b3 - b3.mean(-1, true)).contiguous();
+    auto v1 = (a * a).sum(-1).contiguous();
+    const int64_t B = a.size(0), n = a.size(1), m = b.size(1), d = a.size(2);
+    auto out = at::empty({B, n, m}, a.options());
+    check_rc(tpw_snr_centered(a.data_ptr<float>(), b.data_ptr<float>(), v1.data_ptr<float>(), B, n, m, d,
+                              out.data_ptr<float>(), current_stream()),
+             "_snr");
+    return x1.dim() == 3 ? out : out[0];
 }
 
 // Gradients of a GPU composition by autograd, whatever the caller's grad mode.

@@ -134,6 +134,9 @@ std::tuple<at::Tensor, at::Tensor> pw_kernel_backward(const at::Tensor &grad, co
                                                       int64_t kind, double gamma, double coef0,
                                                       int64_t degree);
 at::Tensor pw_lp(const at::Tensor &x1, const at::Tensor &x2, double p);
+// at::cdist's Lp distances of float32 GPU rows with the output written as bfloat16 by the kernel
+// (no autograd: for callers that need no gradient; hip_impl.cpp)
+at::Tensor lp_distances_bf16_cuda(const at::Tensor &x1, const at::Tensor &x2, double p);
 std::tuple<at::Tensor, at::Tensor> pw_lp_backward(const at::Tensor &grad, const at::Tensor &x1,
                                                   const at::Tensor &x2, const at::Tensor &dist,
                                                   double p);

@@ -67,6 +67,11 @@ int tpw_launch_timer_arm(const char *family, int capacity);
  * NULL) = launches past the armed capacity. */
 int tpw_launch_timer_read(float *ms, int capacity, int *count, int *dropped);
 
+/* Launches `count` empty kernels (one wave each) back to back on `stream` (measurement
+ * support; no counterpart in the reference): the floor a chain of that many dependent launches
+ * costs on the device, against which a multi-launch operation can be measured. */
+int tpw_empty_launches(int count, void *stream);
+
 /* ------------------------------------------------------------------------- */
 /* Bit-packed boolean family (hamming, jaccard, pw*_sum / pw*_mean on bool)   */
 /* ------------------------------------------------------------------------- */
@@ -614,6 +619,16 @@ int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t batch, int6
                            const int64_t *perm1, const int64_t *perm2, float *out,
                            int64_t *idx1, int64_t *idx2, void *workspace, void *stream);
 
+/* Work counters of tpw_directed_hausdorff (measurement support; no counterpart in the
+ * reference).  arm != 0: waits for the current device, zeroes the counters and starts counting
+ * the calls made on that device (out is not used).  arm == 0: waits for the device, stops
+ * counting and writes out[0] = point pairs whose squared distance the kernels evaluated,
+ * out[1] = cell-box tests of the sorted mode's cell scan (one box against one x2 point),
+ * out[2] = kernel launches, summed over the calls since arming.  Pairs are counted on the
+ * cell-grid paths (d <= 3); the d >= 4 kernels do not count.  Not for concurrent use from
+ * several threads. */
+int tpw_hausdorff_counters(int arm, unsigned long long *out);
+
 /* Size of the static scratch buffer of tpw_directed_hausdorff_noalloc, in MiB (per GPU). */
 #define TPW_HAUSDORFF_NOALLOC_SCRATCH_MIB 96
 
@@ -623,7 +638,7 @@ int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t batch, int6
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): it calls no hipMalloc / hipFree.  Sizes whose
  * tpw_hausdorff_workspace_size exceeds the buffer are rejected with TPW_ERR_INVALID (the
- * [16, 65536, 3] x [16, 65536, 3] case needs 67 MiB).  The array is in a code object of its
+ * [16, 65536, 3] x [16, 65536, 3] case needs 45 MiB).  The array is in a code object of its
  * own: a GPU holds it from this entry point's first call there, and processes that never call
  * it hold none.  Every call on one GPU shares that GPU's buffer, so calls are serialised: each
  * call's stream waits for the previous call's work on that GPU (one event per device, created

@@ -360,6 +360,68 @@ def test_hausdorff_plan_variants_bit_exact(shape):
     assert_equal(i2.cpu(), torch.from_numpy(w_i2), f"idx2 {shape}")
 
 
+@pytest.mark.parametrize("case", ["offset", "flat", "tiny_x2", "one_x2", "shuffled_many_clouds"])
+def test_hausdorff_cell_scan_edges_bit_exact(case):
+    """Cases aimed at the sorted mode's whole-cell test (an x1 cell's exact box against x2
+    points) and its window pass: coordinates far from the origin (rounding of every difference),
+    an axis with zero span (one cell along it), x2 clouds of fewer points than the cell test
+    takes, and a shuffle through the one-block-per-cloud sort."""
+    g = torch.Generator().manual_seed(77)
+    perm1 = perm2 = None
+    if case == "offset":
+        x1 = 1.0e4 + torch.rand(2, 3000, 3, generator=g)
+        x2 = 1.0e4 + torch.rand(3, 2500, 3, generator=g) + 0.05
+    elif case == "flat":
+        x1 = torch.rand(2, 3000, 3, generator=g)
+        x2 = torch.rand(2, 2000, 3, generator=g) + 0.05
+        x1[..., 2] = 0.25
+        x2[..., 2] = 0.25
+    elif case == "tiny_x2":
+        x1 = torch.rand(2, 2000, 3, generator=g)
+        x2 = torch.rand(3, 3, 3, generator=g)
+    elif case == "one_x2":
+        x1 = torch.rand(2, 1500, 2, generator=g)
+        x2 = torch.rand(2, 1, 2, generator=g)
+    else:
+        x1 = torch.rand(1100, 1, 40, 3, generator=g)
+        x2 = torch.rand(1100, 1, 50, 3, generator=g) + 0.05
+        perm1, perm2 = P.hausdorff_permutations(1100, 40, 50, torch.Generator().manual_seed(8))
+    print(case, tuple(x1.shape), tuple(x2.shape), flush=True)
+    dev = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV), dev(perm1), dev(perm2))
+    w = cref.directed_hausdorff(x1.numpy(), x2.numpy(), None if perm1 is None else perm1.numpy(),
+                                None if perm2 is None else perm2.numpy(), threads=8)
+    for got, want, nm in zip((out, i1, i2), w, ("value", "idx1", "idx2")):
+        assert_equal(got.cpu(), torch.from_numpy(want), f"{case} {nm}")
+
+
+def test_hausdorff_counters():
+    """The work counters: the kernels evaluate far fewer pairs than brute force, the sorted
+    mode's cell scan runs its box tests, the forward of a few clouds is ten launches, and
+    counting changes no result."""
+    x1, x2 = _hd_inputs(None, 3, 20000, 3, 20000, 3, seed=5)
+    a, b = x1.to(DEV), x2.to(DEV)
+    plain = capi.directed_hausdorff(a, b)
+    c = capi.HausdorffCounters().arm()
+    counted = capi.directed_hausdorff(a, b)
+    n = c.read()
+    print(n, flush=True)
+    for got, want, nm in zip(counted, plain, ("value", "idx1", "idx2")):
+        assert_equal(got, want, f"counted {nm}")
+    pairs = 9
+    assert 0 < n["pairs"] < pairs * 20000 * 20000 // 100
+    assert 0 < n["cell_tests"] <= pairs * 4096  # one box test per (pair, cell)
+    assert n["launches"] == 10
+    c2 = capi.HausdorffCounters().arm()
+    capi.directed_hausdorff(a, b)
+    capi.directed_hausdorff(a, b)
+    n2 = c2.read()
+    # box tests do not depend on T; the pairs do (T rises as waves fold their mins, in no fixed
+    # order), so two calls count about twice as many
+    assert n2["launches"] == 20 and n2["cell_tests"] == 2 * n["cell_tests"]
+    assert 1.5 * n["pairs"] < n2["pairs"] < 2.5 * n["pairs"]
+
+
 def test_hausdorff_ties_bit_exact():
     # integer grid points: many equal distances, so the tie rules decide the indices
     g = torch.Generator().manual_seed(11)

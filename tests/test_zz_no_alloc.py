@@ -26,7 +26,7 @@ def _both(x1, x2, perm1=None, perm2=None):
 
 @pytest.mark.gpu
 def test_noalloc_matches_workspace_entry_point_twice():
-    # call 1: the C5 shape (16 x 65536 points per side, d = 3: 67 MiB of scratch)
+    # call 1: the C5 shape (16 x 65536 points per side, d = 3: 45 MiB of scratch)
     x1 = rand(16, 65536, 3, seed=0)
     x2 = rand(16, 65536, 3, seed=1) + 0.05
     print("[noalloc] call 1: [16, 65536, 3] x [16, 65536, 3]", flush=True)
@@ -104,7 +104,7 @@ def test_noalloc_scratch_is_held_only_by_callers_of_the_entry_point():
 
 def test_noalloc_rejects_sizes_beyond_the_buffer():
     l = capi.lib()
-    big = (1, 1, 1 << 21, 1, 1 << 21, 3)
+    big = (1, 1, 1 << 22, 1, 1 << 22, 3)
     assert l.tpw_hausdorff_workspace_size(*big) > LIMIT
     rc = l.tpw_directed_hausdorff_noalloc(None, None, *big, None, None, None, None, None, None)
     assert rc == 1

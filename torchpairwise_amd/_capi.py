@@ -30,6 +30,7 @@ _SIGNATURES = {
     "tpw_runtime_version": (_i, []),
     "tpw_launch_timer_arm": (_i, [C.c_char_p, _i]),
     "tpw_launch_timer_read": (_i, [_p, _i, _p, _p]),
+    "tpw_empty_launches": (_i, [_i, _p]),
     "tpw_packed_words": (_i64, [_i64]),
     "tpw_pack_bool_rows": (_i, [_p, _i64, _i64, _p, _p, _p]),
     "tpw_bool_pairwise_reduce": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, _i, _p, _p]),
@@ -71,6 +72,7 @@ _SIGNATURES = {
     "tpw_prf_div_scalar_backward": (_i, [_p, _p, _d, _i, _i64, _i, _i, _p, _p]),
     "tpw_hausdorff_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "tpw_directed_hausdorff": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
+    "tpw_hausdorff_counters": (_i, [_i, _p]),
     "tpw_directed_hausdorff_noalloc": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "tpw_directed_hausdorff_backward": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),
     "tpw_row_smallest_mask": (_i, [_p, _i, _i64, _i64, _i64, _p, _p]),
@@ -159,6 +161,26 @@ class LaunchTimer:
         count, dropped = C.c_int(0), C.c_int(0)
         call("tpw_launch_timer_read", C.cast(buf, C.c_void_p), self.capacity, C.byref(count), C.byref(dropped))
         return [float(buf[i]) for i in range(min(count.value, self.capacity))], dropped.value
+
+
+class HausdorffCounters:
+    """Work of the directed Hausdorff forward calls made while armed (``tpw_hausdorff_counters``):
+    read() returns {"pairs": point pairs whose squared distance was evaluated, "cell_tests":
+    cell-box tests, "launches": kernel launches}."""
+
+    def arm(self):
+        call("tpw_hausdorff_counters", 1, None)
+        return self
+
+    def read(self):
+        buf = (C.c_ulonglong * 3)()
+        call("tpw_hausdorff_counters", 0, C.cast(buf, C.c_void_p))
+        return {"pairs": int(buf[0]), "cell_tests": int(buf[1]), "launches": int(buf[2])}
+
+
+def empty_launches(count: int):
+    """`count` empty kernel launches back to back on torch's current stream."""
+    call("tpw_empty_launches", count, _stream())
 
 
 def _ptr(t):

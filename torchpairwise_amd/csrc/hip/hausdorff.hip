@@ -66,6 +66,15 @@ __device__ __forceinline__ float sqdist_fixed(const float (&a)[D], const float *
 
 __device__ __forceinline__ int64_t cdiv_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Work unit of a 1-D grid's block: blocks go round-robin over the 8 XCDs (blockIdx.x % 8 picks
+// the XCD), so when total % 8 == 0 each XCD is given a contiguous range of units.  Kernels order
+// their units by the cloud they read most, so that an XCD works through a few clouds at a time
+// and keeps them in its own L2.
+__device__ __forceinline__ int64_t xcd_unit(int64_t total) {
+    const int64_t L = blockIdx.x;
+    return (total & 7) == 0 ? (L & 7) * (total >> 3) + (L >> 3) : L;
+}
+
 __device__ __forceinline__ float wave_min(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
@@ -80,6 +89,38 @@ __device__ __forceinline__ float threshold_of(const unsigned long long *key) {
 __device__ __forceinline__ void fold_key(unsigned long long *key, float mn, int64_t m) {
     const unsigned long long k = ((unsigned long long)__float_as_uint(mn) << 32) | (uint64_t)m;
     atomicMax(key, k);
+}
+
+// Measurement counters of the cell-grid path (d <= 3), armed by tpw_hausdorff_counters: [0]
+// point pairs whose squared distance a kernel evaluated, [1] cell-box tests of the cell scan.
+// Kernels take the array's device address, or null when counting is off; each wave adds its
+// own totals once, at its end.
+__device__ unsigned long long g_hd_counts[2];
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, 64);
+    return v;
+}
+__device__ __forceinline__ void add_counts(unsigned long long *counts, uint32_t evals, uint32_t tests) {
+    if (!counts) return;  // the same in every lane
+    evals = wave_sum_u32(evals);
+    tests = wave_sum_u32(tests);
+    if ((threadIdx.x & 63) == 0) {
+        if (evals) atomicAdd(&counts[0], (unsigned long long)evals);
+        if (tests) atomicAdd(&counts[1], (unsigned long long)tests);
+    }
+}
+
+// Point at iteration position `pos` of cloud c of an input [clouds][p][D] as given (the
+// shuffle permutation perm[batch][p], batch = c / cpb, maps positions to rows when given).
+template <int D>
+__device__ __forceinline__ void point_at(const float *x, const int64_t *perm, int64_t c, int64_t cpb, int64_t p,
+                                         int64_t pos, float (&a)[D]) {
+    const int64_t src = perm ? perm[(c / cpb) * p + pos] : pos;
+    const float *s = x + (c * p + src) * D;
+#pragma unroll
+    for (int k = 0; k < D; ++k) a[k] = s[k];
 }
 
 // A cell-sorted point is one 16-byte record: its D <= 3 coordinates, then (dword 3) its
@@ -788,6 +829,12 @@ __global__ void backward_x2_kernel(const float *__restrict__ g, const float *__r
 // with mins near T) are spread evenly over the waves.
 constexpr int kCells = 4096;
 
+// The cell scan takes a pair's cells in a scattered order, position (c * 0x9b1) mod 4096 for
+// cell c (an odd multiplier: a permutation, which mixes every bit of c into the high bits), so
+// that cells that need more work, which cluster in space, spread evenly over its blocks.
+// Per-cell data it reads is stored by position, so that its loads stay contiguous.
+__device__ __forceinline__ int pos_cell(int c) { return (c * 0x9b1) & (kCells - 1); }
+
 
 template <int D>
 __device__ __forceinline__ uint32_t spread_bits(uint32_t v) {
@@ -801,6 +848,23 @@ __device__ __forceinline__ uint32_t spread_bits(uint32_t v) {
         v = (v | (v << 4)) & 0x30fu;
         v = (v | (v << 2)) & 0x333u;
         v = (v | (v << 1)) & 0x555u;
+        return v;
+    }
+}
+
+// Inverse of spread_bits: every third (D = 3) or second (D = 2) bit back to 4 or 6 bits.
+template <int D>
+__device__ __forceinline__ uint32_t compact_bits(uint32_t v) {
+    if constexpr (D == 3) {
+        v &= 0x249u;
+        v = (v | (v >> 2)) & 0x0c3u;
+        v = (v | (v >> 4)) & 0x00fu;
+        return v;
+    } else {
+        v &= 0x555u;
+        v = (v | (v >> 1)) & 0x333u;
+        v = (v | (v >> 2)) & 0x30fu;
+        v = (v | (v >> 4)) & 0x03fu;
         return v;
     }
 }
@@ -834,28 +898,35 @@ __device__ __forceinline__ void frame_of(const float *box, float (&fr)[2 * D]) {
     }
 }
 
-// Counting sort of one cloud (block) by cell, in the frame of boxes[c / clouds_per_box], into
-// records (rec, [cloud][p]), with, when given, the cloud's cell start offsets (cstart,
-// kCells + 1).  Points of one cell land in an unspecified order (LDS
-// atomics); nothing depends on it.
+// One side's clouds for the cell sort: the input as given ([clouds][p][D]; when perm is given,
+// iteration position pos of cloud c is row perm[c / cpb][pos]), the records to write
+// ([clouds][p]) and the frames (boxes[c / cpf][D][2]).
+struct CellSet {
+    const float *x;
+    const int64_t *perm;
+    float4 *rec;
+    const float *boxes;
+    int64_t clouds, p, cpb, cpf;
+};
+
+// Counting sort of one cloud (block) of S by cell into records, with, when given, the cloud's
+// cell start offsets (cstart[c][kCells + 1]; cstartT[c][pos(cell)] the same starts in the cell
+// scan's order).  Points of one cell land in an unspecified order
+// (LDS atomics); nothing depends on it.
 template <int D>
-__global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__restrict__ xs, int64_t p,
-                                                             const float *__restrict__ boxes,
-                                                             int64_t clouds_per_box,
-                                                             float4 *__restrict__ rec,
-                                                             int32_t *__restrict__ cstart) {
+__global__ __launch_bounds__(kThreads) void cell_sort_kernel(CellSet S, int32_t *__restrict__ cstart,
+                                                             int32_t *__restrict__ cstartT) {
     __shared__ uint32_t cnt[kCells];
     __shared__ uint32_t part[kThreads];
     const int64_t c = blockIdx.x;
-    const float *X = xs + c * D * p;
+    const int64_t p = S.p;
     float fr[2 * D];
-    frame_of<D>(boxes + (c / clouds_per_box) * D * 2, fr);
+    frame_of<D>(S.boxes + (c / S.cpf) * D * 2, fr);
     for (int t = threadIdx.x; t < kCells; t += kThreads) cnt[t] = 0u;
     __syncthreads();
     for (int64_t n = threadIdx.x; n < p; n += kThreads) {
         float a[D];
-#pragma unroll
-        for (int k = 0; k < D; ++k) a[k] = X[k * p + n];
+        point_at<D>(S.x, S.perm, c, S.cpb, p, n, a);
         atomicAdd(&cnt[cell_of<D>(a, fr)], 1u);
     }
     __syncthreads();
@@ -881,15 +952,15 @@ __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__rest
         const uint32_t v = cnt[cell];
         cnt[cell] = run;
         if (cstart) cstart[c * (kCells + 1) + cell] = (int32_t)run;
+        if (cstartT) cstartT[c * kCells + pos_cell(cell)] = (int32_t)run;
         run += v;
     }
     if (cstart && threadIdx.x == 0) cstart[c * (kCells + 1) + kCells] = (int32_t)p;
     __syncthreads();
-    float4 *O = rec + c * p;
+    float4 *O = S.rec + c * p;
     for (int64_t n = threadIdx.x; n < p; n += kThreads) {
         float a[D];
-#pragma unroll
-        for (int k = 0; k < D; ++k) a[k] = X[k * p + n];
+        point_at<D>(S.x, S.perm, c, S.cpb, p, n, a);
         const uint32_t slot = atomicAdd(&cnt[cell_of<D>(a, fr)], 1u);
         O[slot] = make_rec<D>(a, (uint32_t)n);
     }
@@ -899,34 +970,13 @@ __global__ __launch_bounds__(kThreads) void cell_sort_kernel(const float *__rest
 // block per cloud would leave most CUs idle), with no global atomics.  Clouds [0, A.clouds)
 // come from A, the rest from B; hist[cloud][chunk][cell] holds each chunk's histogram and then
 // its first slot in every cell.
-//   cell_count: block (cloud, y) histograms points [y chunk, (y + 1) chunk) in LDS and writes
-//     it out;
-//   cell_prefix / cell_start: per cell, the counts of the earlier chunks; per cloud, the cell
-//     starts (starts[cloud], the x2 clouds' being their cstart);
-//   cell_scatter: block (cloud, y) starts each cell at start + earlier chunks' count and writes
-//     its points, the slot within a cell taken with an LDS atomicAdd.
-struct CellSet {
-    const float *xs;      // [clouds][D][p]
-    float4 *rec;          // [clouds][p] records
-    const float *boxes;   // frames, [clouds / clouds_per_box][D][2]
-    int64_t clouds, p, clouds_per_box;
-};
-
-template <int D>
-__device__ __forceinline__ void chunk_histogram(const CellSet &S, int64_t c, int64_t beg, int64_t end,
-                                                const float (&fr)[2 * D], uint32_t *hist) {
-    for (int t = threadIdx.x; t < kCells; t += kThreads) hist[t] = 0u;
-    __syncthreads();
-    const float *X = S.xs + c * D * S.p;
-    for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
-        float a[D];
-#pragma unroll
-        for (int k = 0; k < D; ++k) a[k] = X[k * S.p + n];
-        atomicAdd(&hist[cell_of<D>(a, fr)], 1u);
-    }
-    __syncthreads();
-}
-
+//   cell_count: block (cloud, y) histograms positions [y chunk, (y + 1) chunk) in LDS and
+//     writes it out;
+//   cell_offsets: per cloud, the cell starts (starts[cloud], A's clouds first; A's also in the
+//     cell scan's order, startsA_T, when given) and each chunk's first slot in every cell (the
+//     start plus the earlier chunks' counts);
+//   cell_scatter: block (cloud, y) writes its points from those slots on, the slot within a
+//     cell taken with an LDS atomicAdd.
 template <int D>
 __global__ __launch_bounds__(kThreads) void cell_count_kernel(CellSet A, CellSet B, int64_t chunk, int64_t chunks,
                                                               uint32_t *__restrict__ hist_out) {
@@ -938,70 +988,94 @@ __global__ __launch_bounds__(kThreads) void cell_count_kernel(CellSet A, CellSet
     const int64_t beg = (int64_t)blockIdx.y * chunk;
     const int64_t end = beg + chunk < S.p ? beg + chunk : S.p;  // empty when beg >= p
     float fr[2 * D];
-    frame_of<D>(S.boxes + (c / S.clouds_per_box) * D * 2, fr);
-    chunk_histogram<D>(S, c, beg, end, fr, hist);
+    frame_of<D>(S.boxes + (c / S.cpf) * D * 2, fr);
+    for (int t = threadIdx.x; t < kCells; t += kThreads) hist[t] = 0u;
+    __syncthreads();
+    for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
+        float a[D];
+        point_at<D>(S.x, S.perm, c, S.cpb, S.p, n, a);
+        atomicAdd(&hist[cell_of<D>(a, fr)], 1u);
+    }
+    __syncthreads();
     uint32_t *H = hist_out + (g * chunks + blockIdx.y) * kCells;
     for (int t = threadIdx.x; t < kCells; t += kThreads) H[t] = hist[t];
 }
 
-// One thread per (cloud, cell): the counts of the earlier chunks in the cell replace each
-// chunk's count, and the cell's total goes to totals[cloud][cell].
-__global__ __launch_bounds__(kThreads) void cell_prefix_kernel(int64_t chunks, uint32_t *__restrict__ hist,
-                                                               uint32_t *__restrict__ totals) {
-    const int64_t g = blockIdx.x;
-    const int cell = blockIdx.y * kThreads + threadIdx.x;
-    uint32_t *H = hist + g * chunks * kCells + cell;
-    uint32_t run = 0;
-    for (int64_t y = 0; y < chunks; ++y) {
-        const uint32_t n = H[y * kCells];
-        H[y * kCells] = run;
-        run += n;
-    }
-    totals[g * kCells + cell] = run;
-}
+constexpr int kOffThreads = 1024;
 
-// One block per cloud: starts[cloud][cell] = exclusive scan of the cell totals, and
-// starts[cloud][kCells] = p.
-__global__ __launch_bounds__(kThreads) void cell_start_kernel(CellSet A, CellSet B,
-                                                              const uint32_t *__restrict__ totals,
-                                                              int32_t *__restrict__ starts) {
-    __shared__ uint32_t part[kThreads];
+__global__ __launch_bounds__(kOffThreads) void cell_offsets_kernel(CellSet A, CellSet B, int64_t chunks,
+                                                                   uint32_t *__restrict__ hist,
+                                                                   int32_t *__restrict__ starts,
+                                                                   int32_t *__restrict__ startsA_T) {
+    __shared__ uint32_t tot[kCells];
+    __shared__ uint32_t wsum[kOffThreads / 64];
     const int64_t g = blockIdx.x;
     const CellSet &S = g < A.clouds ? A : B;
-    const uint32_t *Tc = totals + g * kCells;
-    constexpr int kPer = kCells / kThreads;  // 16 consecutive cells per thread
-    uint32_t v[kPer];
-    uint32_t local = 0;
+    uint32_t *H = hist + g * chunks * kCells;
+    constexpr int kPer = kCells / kOffThreads;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // per-cell totals: thread t sums cells t + 1024 e over the chunks
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-        v[e] = Tc[threadIdx.x * kPer + e];
+        const int cell = t + e * kOffThreads;
+        uint32_t run = 0;
+#pragma unroll 8
+        for (int64_t y = 0; y < chunks; ++y) run += H[y * kCells + cell];
+        tot[cell] = run;
+    }
+    __syncthreads();
+    // exclusive scan over cells: thread t owns cells kPer t .. kPer t + kPer - 1
+    uint32_t v[kPer], local = 0;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+        v[e] = tot[kPer * t + e];
         local += v[e];
     }
-    part[threadIdx.x] = local;
+    uint32_t incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
+        if (lane >= off) incl += o;
+    }
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (t == 0) {
         uint32_t run = 0;
-        for (int t = 0; t < kThreads; ++t) {
-            const uint32_t x = part[t];
-            part[t] = run;
+        for (int w = 0; w < kOffThreads / 64; ++w) {
+            const uint32_t x = wsum[w];
+            wsum[w] = run;
             run += x;
         }
     }
     __syncthreads();
-    uint32_t run = part[threadIdx.x];
+    uint32_t run = wsum[wave] + incl - local;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+        tot[kPer * t + e] = run;
+        run += v[e];
+    }
+    __syncthreads();
+    // starts, and each chunk's first slot per cell
     int32_t *St = starts + g * (kCells + 1);
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-        St[threadIdx.x * kPer + e] = (int32_t)run;
-        run += v[e];
+        const int cell = t + e * kOffThreads;
+        uint32_t s = tot[cell];
+        St[cell] = (int32_t)s;
+        if (startsA_T && g < A.clouds) startsA_T[g * kCells + pos_cell(cell)] = (int32_t)s;
+#pragma unroll 8
+        for (int64_t y = 0; y < chunks; ++y) {
+            const uint32_t n = H[y * kCells + cell];
+            H[y * kCells + cell] = s;
+            s += n;
+        }
     }
-    if (threadIdx.x == 0) St[kCells] = (int32_t)S.p;
+    if (t == 0) St[kCells] = (int32_t)S.p;
 }
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellSet B, int64_t chunk, int64_t chunks,
-                                                                const uint32_t *__restrict__ slots,
-                                                                const int32_t *__restrict__ starts) {
+                                                                const uint32_t *__restrict__ slots) {
     __shared__ uint32_t next[kCells];
     const int64_t g = blockIdx.x;
     const bool inA = g < A.clouds;
@@ -1011,17 +1085,14 @@ __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellS
     if (beg >= S.p) return;  // the same for the whole block
     const int64_t end = beg + chunk < S.p ? beg + chunk : S.p;
     float fr[2 * D];
-    frame_of<D>(S.boxes + (c / S.clouds_per_box) * D * 2, fr);
+    frame_of<D>(S.boxes + (c / S.cpf) * D * 2, fr);
     const uint32_t *H = slots + (g * chunks + blockIdx.y) * kCells;
-    const int32_t *St = starts + g * (kCells + 1);
-    for (int t = threadIdx.x; t < kCells; t += kThreads) next[t] = (uint32_t)St[t] + H[t];
+    for (int t = threadIdx.x; t < kCells; t += kThreads) next[t] = H[t];
     __syncthreads();
-    const float *X = S.xs + c * D * S.p;
     float4 *O = S.rec + c * S.p;
     for (int64_t n = beg + threadIdx.x; n < end; n += kThreads) {
         float a[D];
-#pragma unroll
-        for (int k = 0; k < D; ++k) a[k] = X[k * S.p + n];
+        point_at<D>(S.x, S.perm, c, S.cpb, S.p, n, a);
         const uint32_t slot = atomicAdd(&next[cell_of<D>(a, fr)], 1u);
         O[slot] = make_rec<D>(a, (uint32_t)n);
     }
@@ -1041,6 +1112,7 @@ __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellS
 //     with position mpos into key (returns false);
 //   kBallMin: return the exact min (out_min);
 //   kBallFirst: return the smallest position of a point with d == H (all ones if none).
+// evals (per lane) is raised by the number of points the lane evaluated.
 constexpr int kBallPrune = 0, kBallMin = 1, kBallFirst = 2;
 
 template <int D>
@@ -1098,7 +1170,7 @@ __device__ __forceinline__ void ring_cell(int R, int64_t t, int (&o)[D]) {
 template <int D, int MODE>
 __device__ unsigned long long wave_ball_query(const float (&q)[D], const float4 *X2, const int32_t *CS,
                                               const float (&fr)[2 * D], float T, unsigned long long *key,
-                                              int64_t mpos, float *out_min) {
+                                              int64_t mpos, float *out_min, uint32_t &evals) {
     constexpr int G = grid_side<D>();
     constexpr float kMargin = 0.01f, kShrink = 1.0f - 0x1p-12f;
     const int lane = threadIdx.x & 63;
@@ -1165,6 +1237,7 @@ __device__ unsigned long long wave_ball_query(const float (&q)[D], const float4 
                     const bool ok = n < e;
                     const float4 v = X2[ok ? n : s];
                     const float d = ok ? rec_dist<D>(q, v) : INFINITY;
+                    evals += ok ? 1u : 0u;
                     if constexpr (MODE == kBallPrune) {
                         if (__any(d < T)) return 1ull;
                     }
@@ -1201,59 +1274,46 @@ __device__ __forceinline__ int64_t window_start(const float (&a)[D], const float
     return s0 > wstart ? wstart : s0;
 }
 
-// Block = 2048 consecutive m of one pair; each wave takes 64 m at a time, one per lane.  A
-// lane checks the 64 sorted x2 points of its window, first the head of its own cell (which
-// almost always holds a point within T), and stops at the first d < T.  The pair's seeds have
-// their exact mins in the key already and are skipped.
-//   SORTED (x1 as cell-sorted records in the batch frame): neighbouring lanes share windows,
-//     so the loads coalesce; a lane left sets bit m position of its pair's flag bits (preset
-//     to 0), and scan_flagged_kernel scans those m in iteration order.
-//   otherwise (x1 in iteration order, x2 sorted in its cloud's own frame): the lanes left
-//     (ballot) are taken in turn by the whole wave through a ball query.
-template <int D, bool SORTED>
+// Scan of the unsorted mode (x1 in iteration order, SoA; x2 sorted in its cloud's own frame):
+// block = 2048 consecutive m of one pair; each wave takes 64 m at a time, one per lane.  A lane
+// checks the 64 sorted x2 points of its window, first the head of its own cell (which almost
+// always holds a point within T), and stops at the first d < T; the pair's seeds have their
+// exact mins in the key already and are skipped.  The lanes left (ballot) are taken in turn by
+// the whole wave through a ball query.
+template <int D>
 __global__ __launch_bounds__(kThreads) void scan_window_kernel(
-    const float *__restrict__ xs1, const float4 *__restrict__ xs1r, const float4 *__restrict__ xs2r,
-    const int32_t *__restrict__ cstart2, const float *__restrict__ boxes, int64_t b1, int64_t b2,
-    int64_t p1, int64_t p2, int64_t m_per_block, const uint32_t *__restrict__ seedm,
-    unsigned long long *__restrict__ keys, uint32_t *__restrict__ flagbits) {
+    const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
+    const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t m_per_block,
+    const uint32_t *__restrict__ seedm, unsigned long long *__restrict__ keys, unsigned long long *__restrict__ counts) {
     const int64_t pair = blockIdx.y;
     const int64_t per_batch = b1 * b2;
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
     const int64_t i = rem / b2, j = rem - i * b2;
-    const float *X1 = SORTED ? nullptr : xs1 + (bb * b1 + i) * D * p1;
-    const float4 *X1r = SORTED ? xs1r + (bb * b1 + i) * p1 : nullptr;
+    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
     const float4 *X2 = xs2r + (bb * b2 + j) * p2;
     const int32_t *CS = cstart2 + (bb * b2 + j) * (kCells + 1);
     float fr[2 * D];
-    frame_of<D>(boxes + (SORTED ? bb : bb * b2 + j) * D * 2, fr);
+    frame_of<D>(boxes + (bb * b2 + j) * D * 2, fr);
     const int lane = threadIdx.x & 63;
     const int64_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the same in every lane
     const int64_t mbeg = (int64_t)blockIdx.x * m_per_block;
     const int64_t mend = mbeg + m_per_block < p1 ? mbeg + m_per_block : p1;
     const int64_t wlen = p2 < 64 ? p2 : 64;
-    const int64_t fwords = cdiv_dev(p1, 32);
     unsigned long long *key = &keys[pair];
+    uint32_t evals = 0;
     // four groups of 64 m per step (m0, m0 + 256, ...), so that their dependent loads (point,
     // cell start, window) overlap
     constexpr int kG = 4;
     for (int64_t m0 = mbeg + 64 * wave; m0 < mend; m0 += kG * kThreads) {
         float a[kG][D];
-        int64_t mpos[kG], s0[kG];
+        int64_t s0[kG];
         bool done[kG];
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
             const int64_t m = m0 + g * kThreads + lane;
             const bool valid = m < mend;
-            mpos[g] = m;
-            if constexpr (SORTED) {
-                const float4 v = X1r[valid ? m : mbeg];  // mbeg < p1; an invalid lane is done
 #pragma unroll
-                for (int k = 0; k < D; ++k) a[g][k] = rec_coord(v, k);
-                mpos[g] = rec_pos(v);
-            } else {
-#pragma unroll
-                for (int k = 0; k < D; ++k) a[g][k] = X1[k * p1 + (valid ? m : mbeg)];
-            }
+            for (int k = 0; k < D; ++k) a[g][k] = X1[k * p1 + (valid ? m : mbeg)];  // mbeg < p1
             done[g] = !valid;
         }
 #pragma unroll
@@ -1264,10 +1324,13 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
             bool hit = false;
+            if (!done[g]) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
-                if (u < wlen) hit = hit | (rec_dist<D>(a[g], X2[s0[g] + u]) < T);
-            done[g] = done[g] || hit || is_seed(seedm, pair, mpos[g]);
+                for (int u = 0; u < 2; ++u)
+                    if (u < wlen) hit = hit | (rec_dist<D>(a[g], X2[s0[g] + u]) < T);
+                evals += wlen < 2 ? (uint32_t)wlen : 2u;
+            }
+            done[g] = done[g] || hit || is_seed(seedm, pair, m0 + g * kThreads + lane);
         }
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
@@ -1276,52 +1339,55 @@ __global__ __launch_bounds__(kThreads) void scan_window_kernel(
 #pragma unroll
                 for (int u = 0; u < 8; ++u)
                     if (t + u < wlen) hit = hit | (rec_dist<D>(a[g], X2[s0[g] + t + u]) < T);
+                evals += wlen - t < 8 ? (uint32_t)(wlen - t) : 8u;
                 done[g] = hit;
             }
         }
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
-            if constexpr (SORTED) {
-                if (!done[g]) atomicOr(&flagbits[pair * fwords + (mpos[g] >> 5)], 1u << (mpos[g] & 31));
-            } else {
-                unsigned long long left = __ballot(!done[g]);
-                while (left) {
-                    const int l = __builtin_ctzll(left);
-                    left &= left - 1;
-                    float b[D];
+            unsigned long long left = __ballot(!done[g]);
+            while (left) {
+                const int l = __builtin_ctzll(left);
+                left &= left - 1;
+                float b[D];
 #pragma unroll
-                    for (int k = 0; k < D; ++k)
-                        b[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[g][k]), l));
-                    wave_ball_query<D, kBallPrune>(b, X2, CS, fr, threshold_of(key), key, m0 + g * kThreads + l,
-                                                   nullptr);
-                }
+                for (int k = 0; k < D; ++k)
+                    b[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[g][k]), l));
+                wave_ball_query<D, kBallPrune>(b, X2, CS, fr, threshold_of(key), key, m0 + g * kThreads + l,
+                                               nullptr, evals);
             }
         }
     }
+    add_counts(counts, evals, 0u);
 }
 
-// The m the window pass of the sorted mode left (flag bits), in iteration order: block =
-// 256 words = 8192 m of one pair, each lane one word; each flagged m is taken by its whole wave
-// through an exact ball query (dropped at the first d < T, or folded with its exact min).
+// The m the cell scan left (flag bits), in iteration order: block = 256 words = 8192 m of one
+// pair (blocks ordered by x2 cloud), each lane one word; each flagged m is taken by its whole wave through an exact ball
+// query (dropped at the first d < T, or folded with its exact min).
 template <int D>
 __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
-    const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
-    const float *__restrict__ boxes, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
-    unsigned long long *__restrict__ keys, const uint32_t *__restrict__ flagbits) {
-    const int64_t pair = blockIdx.y;
-    const int64_t per_batch = b1 * b2;
-    const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
-    const int64_t i = rem / b2, j = rem - i * b2;
-    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
-    const float4 *X2 = xs2r + (bb * b2 + j) * p2;
-    const int32_t *CS = cstart2 + (bb * b2 + j) * (kCells + 1);
+    const float *__restrict__ x1, const int64_t *__restrict__ perm1, const float4 *__restrict__ xs2r,
+    const int32_t *__restrict__ cstart2, const float *__restrict__ boxes, int64_t clouds2, int64_t b1, int64_t b2,
+    int64_t p1, int64_t p2, unsigned long long *__restrict__ keys, const uint32_t *__restrict__ flagbits,
+    unsigned long long *__restrict__ counts) {
+    // units ordered (x2 cloud, x1 cloud of the batch, block of m): an XCD reads few x2 clouds
+    const int64_t nbx = cdiv_dev(p1, 32 * kThreads);
+    const int64_t unit = xcd_unit(clouds2 * b1 * nbx);
+    const int64_t g2 = unit / (b1 * nbx);
+    const int64_t rest = unit - g2 * b1 * nbx;
+    const int64_t i = rest / nbx, bx = rest - i * nbx;
+    const int64_t bb = g2 / b2, j = g2 - bb * b2;
+    const int64_t pair = (bb * b1 + i) * b2 + j;
+    const float4 *X2 = xs2r + g2 * p2;
+    const int32_t *CS = cstart2 + g2 * (kCells + 1);
     float fr[2 * D];
     frame_of<D>(boxes + bb * D * 2, fr);
     unsigned long long *key = &keys[pair];
     const int64_t fwords = cdiv_dev(p1, 32);
-    const int64_t wi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t wi = bx * kThreads + threadIdx.x;
     const uint32_t word = wi < fwords ? flagbits[pair * fwords + wi] : 0u;
-    const int64_t wbase = ((int64_t)blockIdx.x * kThreads + 64 * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * 32;
+    const int64_t wbase = (bx * kThreads + 64 * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * 32;
+    uint32_t evals = 0;
     unsigned long long left = __ballot(word != 0u);
     while (left) {
         const int l = __builtin_ctzll(left);
@@ -1332,47 +1398,76 @@ __global__ __launch_bounds__(kThreads) void scan_flagged_kernel(
             bits &= bits - 1;
             const int64_t mm = wbase + 32 * l + bit;  // < p1: only real m are flagged
             float b[D];
-#pragma unroll
-            for (int k = 0; k < D; ++k) b[k] = X1[k * p1 + mm];
-            wave_ball_query<D, kBallPrune>(b, X2, CS, fr, threshold_of(key), key, mm, nullptr);
+            point_at<D>(x1, perm1, bb * b1 + i, b1, p1, mm, b);
+            wave_ball_query<D, kBallPrune>(b, X2, CS, fr, threshold_of(key), key, mm, nullptr, evals);
         }
     }
+    add_counts(counts, evals, 0u);
 }
 
-// Seeds on the cell grid: one wave per (pair, seed) finds the seed's exact min with a ball
-// query and folds it into the pair's key.
+// Seeds on the cell grid: one wave per (pair, seed s), waves ordered by x2 cloud.  The pair's
+// ncand candidate keys (squared distance to x2's box << 32 | x1 position + 1; 0 = none) are
+// distinct, so every wave of the pair takes the kSeeds largest in the same order (each round
+// the largest key below the previous one) and keeps the s-th: seedm[pair][s] = its position
+// (0xffffffff when there are fewer candidates).  The wave finds that point's exact min with a
+// ball query and folds it into the pair's key.
 template <int D>
 __global__ __launch_bounds__(kThreads) void seed_ball_kernel(
-    const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
-    const float *__restrict__ boxes, bool batch_frame, const uint32_t *__restrict__ seedm, int64_t b1, int64_t b2,
-    int64_t p1, int64_t p2, int64_t pairs, unsigned long long *__restrict__ keys) {
-    const int64_t t = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    if (t >= pairs * kSeeds) return;  // the same in every lane
-    const int64_t pair = t / kSeeds;
-    const uint32_t m = seedm[t];
+    const float *__restrict__ x1, const int64_t *__restrict__ perm1, const float4 *__restrict__ xs2r,
+    const int32_t *__restrict__ cstart2, const float *__restrict__ boxes, bool batch_frame,
+    const unsigned long long *__restrict__ cand, int64_t ncand, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
+    int64_t pairs, uint32_t *__restrict__ seedm, unsigned long long *__restrict__ keys,
+    unsigned long long *__restrict__ counts) {
+    // waves ordered (x2 cloud, x1 cloud of the batch, seed): an XCD reads few x2 clouds
+    const int64_t v = xcd_unit(cdiv_dev(pairs * kSeeds, kThreads / 64)) * (kThreads / 64) + (threadIdx.x >> 6);
+    if (v >= pairs * kSeeds) return;  // the same in every lane
+    const int64_t g2 = v / (b1 * kSeeds);
+    const int64_t vr = v - g2 * b1 * kSeeds;
+    const int64_t bb0 = g2 / b2;
+    const int64_t pair = (bb0 * b1 + vr / kSeeds) * b2 + (g2 - bb0 * b2);
+    const int s = (int)(vr % kSeeds);
+    const int64_t t = pair * kSeeds + s;
+    const int lane = threadIdx.x & 63;
+    const unsigned long long *C = cand + pair * ncand;
+    unsigned long long prev = ~0ull, pick = 0;
+    for (int r = 0; r <= s; ++r) {  // every lane holds the same reduced values
+        unsigned long long best = 0;
+        for (int64_t e = lane; e < ncand; e += 64) {
+            const unsigned long long v = C[e];
+            if (v < prev && v > best) best = v;
+        }
+        pick = wave_max_u64(best);
+        if (!pick) break;
+        prev = pick;
+    }
+    const uint32_t m = pick ? (uint32_t)(pick & 0xffffffffull) - 1u : 0xffffffffu;
+    if (lane == 0) seedm[t] = m;
     if (m == 0xffffffffu) return;
     const int64_t per_batch = b1 * b2;
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
     const int64_t i = rem / b2, j = rem - i * b2;
-    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
     float fr[2 * D];
     frame_of<D>(boxes + (batch_frame ? bb : bb * b2 + j) * D * 2, fr);
     float q[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) q[k] = X1[k * p1 + m];
+    point_at<D>(x1, perm1, bb * b1 + i, b1, p1, m, q);
     float mn = INFINITY;
+    uint32_t evals = 0;
     wave_ball_query<D, kBallMin>(q, xs2r + (bb * b2 + j) * p2, cstart2 + (bb * b2 + j) * (kCells + 1), fr, 0.0f,
-                                 nullptr, 0, &mn);
-    if ((threadIdx.x & 63) == 0) fold_key(&keys[pair], mn, m);
+                                 nullptr, 0, &mn, evals);
+    if (lane == 0) fold_key(&keys[pair], mn, m);
+    add_counts(counts, evals, 0u);
 }
 
-// Final rescan on the cell grid: one wave per pair finds the smallest position of an x2 point
-// at the winning m's min with a ball query.
+// Final rescan on the cell grid: one wave per pair finds the smallest position n of an x2 point
+// at the winning m's min with a ball query, then writes sqrt of the min and the (permuted)
+// positions of m and n.
 template <int D>
 __global__ __launch_bounds__(kThreads) void first_ball_kernel(
-    const float *__restrict__ xs1, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
-    const float *__restrict__ boxes, bool batch_frame, const unsigned long long *__restrict__ keys, int64_t b1,
-    int64_t b2, int64_t p1, int64_t p2, int64_t pairs, unsigned long long *__restrict__ first) {
+    const float *__restrict__ x1, const int64_t *__restrict__ perm1, const int64_t *__restrict__ perm2,
+    const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2, const float *__restrict__ boxes,
+    bool batch_frame, const unsigned long long *__restrict__ keys, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
+    int64_t pairs, float *__restrict__ out, int64_t *__restrict__ idx1, int64_t *__restrict__ idx2,
+    unsigned long long *__restrict__ counts) {
     const int64_t pair = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     if (pair >= pairs) return;  // the same in every lane
     const int64_t per_batch = b1 * b2;
@@ -1381,15 +1476,494 @@ __global__ __launch_bounds__(kThreads) void first_ball_kernel(
     const unsigned long long key = keys[pair];
     const int64_t m = (int64_t)(key & 0xffffffffull);
     const float H = __uint_as_float((uint32_t)(key >> 32));
-    const float *X1 = xs1 + (bb * b1 + i) * D * p1;
     float fr[2 * D];
     frame_of<D>(boxes + (batch_frame ? bb : bb * b2 + j) * D * 2, fr);
     float q[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) q[k] = X1[k * p1 + m];
+    point_at<D>(x1, perm1, bb * b1 + i, b1, p1, m, q);
+    uint32_t evals = 0;
     const unsigned long long n = wave_ball_query<D, kBallFirst>(
-        q, xs2r + (bb * b2 + j) * p2, cstart2 + (bb * b2 + j) * (kCells + 1), fr, H, nullptr, 0, nullptr);
-    if ((threadIdx.x & 63) == 0) first[pair] = n;
+        q, xs2r + (bb * b2 + j) * p2, cstart2 + (bb * b2 + j) * (kCells + 1), fr, H, nullptr, 0, nullptr, evals);
+    if ((threadIdx.x & 63) == 0) {
+        out[pair] = sqrt_rn(H);
+        idx1[pair] = perm1 ? perm1[bb * p1 + m] : m;
+        idx2[pair] = n < (unsigned long long)p2 ? (perm2 ? perm2[bb * p2 + (int64_t)n] : (int64_t)n) : 0;
+    }
+    add_counts(counts, evals, 0u);
+}
+
+// ---------------------------------------------------------------------------------------
+// The sorted mode (d <= 3 and the flag bits fit): x1 and x2 both cell-sorted in each batch's
+// frame, read from the inputs as given (no SoA copy):
+//   prep: presets, and every cloud's per-chunk min / max of each coordinate;
+//   frames: each x2 cloud's box (for the seeds) and each batch's box over both sides;
+//   cell sort of both sides (cell_count / cell_offsets / cell_scatter, or cell_sort);
+//   cells: the exact box of every x1 cell's points, the seed candidates, and one
+//     representative point of every x2 cell;
+//   seed_ball: the seeds' exact mins, the first T;
+//   cell_scan: whole cells of x1 dropped by one box test, the m of the cells left by their
+//     windows; flags;
+//   scan_flagged: ball queries for the flagged m;
+//   first_ball: the first x2 position at the winner's min, and the outputs.
+
+// Block (g, y): rows [y chunk, (y + 1) chunk) of cloud g (x1's clouds, then x2's; rows in input
+// order, which a box does not depend on): part[g][y][k][0..1] = their min and max of coordinate
+// k (NaN ignored, as fminf / fmaxf ignore it; +inf / -inf when there is none).  The grid also
+// writes the presets fs.
+template <int D>
+__global__ __launch_bounds__(kThreads) void prep_kernel(const float *__restrict__ x1, int64_t clouds1, int64_t p1,
+                                                        const float *__restrict__ x2, int64_t p2, int64_t chunk,
+                                                        int64_t chunks, float *__restrict__ part, Fills fs) {
+    __shared__ float red[kThreads / 64][2 * D];
+    const int64_t nthr = (int64_t)gridDim.x * gridDim.y * kThreads;
+    const int64_t tid = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * kThreads + threadIdx.x;
+    // constant indices only (a dynamically indexed copy of the argument would live in LDS)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        if (r >= fs.count) break;
+        uint32_t *p = fs.f[r].p;
+        const int64_t n = fs.f[r].n;
+        const uint32_t v0 = fs.f[r].v[0], v1 = fs.f[r].v[1];
+        for (int64_t t = tid; t < n; t += nthr) p[t] = (t & 1) ? v1 : v0;
+    }
+    const int64_t g = blockIdx.x;
+    const bool in1 = g < clouds1;
+    const int64_t p = in1 ? p1 : p2;
+    const float *X = in1 ? x1 + g * p1 * D : x2 + (g - clouds1) * p2 * D;
+    const int64_t beg = (int64_t)blockIdx.y * chunk;
+    const int64_t end = beg + chunk < p ? beg + chunk : p;
+    float lo[D], hi[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        lo[k] = INFINITY;
+        hi[k] = -INFINITY;
+    }
+    int64_t n = beg + threadIdx.x;
+    for (; n + 3 * kThreads < end; n += 4 * kThreads) {  // four rows in flight
+        float v[4][D];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int k = 0; k < D; ++k) v[u][k] = X[(n + u * kThreads) * D + k];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int k = 0; k < D; ++k) {
+                lo[k] = fminf(lo[k], v[u][k]);
+                hi[k] = fmaxf(hi[k], v[u][k]);
+            }
+    }
+    for (; n < end; n += kThreads)
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const float v = X[n * D + k];
+            lo[k] = fminf(lo[k], v);
+            hi[k] = fmaxf(hi[k], v);
+        }
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            lo[k] = fminf(lo[k], __shfl_xor(lo[k], off, 64));
+            hi[k] = fmaxf(hi[k], __shfl_xor(hi[k], off, 64));
+        }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0)
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            red[wave][2 * k] = lo[k];
+            red[wave][2 * k + 1] = hi[k];
+        }
+    __syncthreads();
+    if (threadIdx.x < 2 * D) {
+        const int e = threadIdx.x;
+        float v = red[0][e];
+        for (int w = 1; w < kThreads / 64; ++w) v = (e & 1) ? fmaxf(v, red[w][e]) : fminf(v, red[w][e]);
+        part[(g * chunks + blockIdx.y) * 2 * D + e] = v;
+    }
+}
+
+// Block g < clouds2: x2 cloud g's box bbox2[g][k][0..1] (the seeds' distance) from its chunk
+// partials; block clouds2 + bb: batch bb's box over the partials of its b1 x1 clouds and b2 x2
+// clouds, the cell frame boxb[bb][k][0..1].
+template <int D>
+__global__ __launch_bounds__(kThreads) void frames_kernel(const float *__restrict__ part, int64_t clouds1,
+                                                          int64_t clouds2, int64_t b1, int64_t b2, int64_t chunks,
+                                                          float *__restrict__ bbox2, float *__restrict__ boxb) {
+    __shared__ float red[kThreads / 64][2 * D];
+    const int64_t g = blockIdx.x;
+    // partial rows (row = cloud * chunks + y) [r0, r1) and [r2, r3)
+    int64_t r0, r1, r2 = 0, r3 = 0;
+    float *dst;
+    if (g < clouds2) {
+        r0 = (clouds1 + g) * chunks;
+        r1 = r0 + chunks;
+        dst = bbox2 + g * 2 * D;
+    } else {
+        const int64_t bb = g - clouds2;
+        r0 = bb * b1 * chunks;
+        r1 = r0 + b1 * chunks;
+        r2 = (clouds1 + bb * b2) * chunks;
+        r3 = r2 + b2 * chunks;
+        dst = boxb + bb * 2 * D;
+    }
+    float lo[D], hi[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        lo[k] = INFINITY;
+        hi[k] = -INFINITY;
+    }
+    for (int half = 0; half < 2; ++half) {
+        const int64_t a = half ? r2 : r0, b = half ? r3 : r1;
+        for (int64_t r = a + threadIdx.x; r < b; r += kThreads)
+#pragma unroll
+            for (int k = 0; k < D; ++k) {
+                lo[k] = fminf(lo[k], part[r * 2 * D + 2 * k]);
+                hi[k] = fmaxf(hi[k], part[r * 2 * D + 2 * k + 1]);
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            lo[k] = fminf(lo[k], __shfl_xor(lo[k], off, 64));
+            hi[k] = fmaxf(hi[k], __shfl_xor(hi[k], off, 64));
+        }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0)
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            red[wave][2 * k] = lo[k];
+            red[wave][2 * k + 1] = hi[k];
+        }
+    __syncthreads();
+    if (threadIdx.x < 2 * D) {
+        const int e = threadIdx.x;
+        float v = red[0][e];
+        for (int w = 1; w < kThreads / 64; ++w) v = (e & 1) ? fmaxf(v, red[w][e]) : fminf(v, red[w][e]);
+        dst[e] = v;
+    }
+}
+
+// Per-cell pass over both sides' sorted records, one lane per cell, blocks of 256 cells:
+//   x1 clouds, for the x2 clouds j of one group (kCellsJ per group; units ordered by cloud,
+//   group, cells): the seed candidates, the kCandPerWave largest keys (squared distance to x2
+//   j's box << 32 | position + 1) over the wave's 64 cells, cand[pair][kCandPerWave (c / 64) +
+//   r] (0: none).  Group 0 also writes the cell's record range and the exact box of its points,
+//   info1[cloud][pos(c)] = {start, end (int bits), lo[0..2], hi[0..2]} (two float4; a cell
+//   holding a NaN coordinate gets lo -inf and hi +inf, which no box test passes);
+//   x2 clouds (units spread among those): rep2[cloud][pos(c)] = the record of the cell that is
+//   nearest to covering the cell's region (least squared distance to the region's farthest
+//   corner; any x2 point serves the box test, this one drops the most cells), or, for an empty
+//   cell, the point at its start.
+// Records are loaded kU at a time (indices past the end repeat the last record, which changes
+// no min, max or largest key).
+constexpr int kCandPerWave = 4;
+constexpr int64_t kCellCand = kCells / 64 * kCandPerWave;
+constexpr int kCellsJ = 2;  // x2 clouds per x1 group
+
+template <int D>
+__device__ __forceinline__ void x2_rep_cell(const float4 *__restrict__ X, const int32_t *__restrict__ CS,
+                                            const float *__restrict__ frame, int c, int64_t p2,
+                                            float4 *__restrict__ rep) {
+    constexpr int kU = 8;
+    const int32_t s = CS[c], e = CS[c + 1];
+    float fr[2 * D];
+    frame_of<D>(frame, fr);
+    float lo[D], hi[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        const uint32_t u = D == 1 ? (uint32_t)c : compact_bits<D>((uint32_t)c >> k);
+        const float step = fr[2 * k + 1] > 0.0f ? 1.0f / fr[2 * k + 1] : 0.0f;
+        lo[k] = fr[2 * k] + (float)u * step;
+        hi[k] = lo[k] + step;
+    }
+    float4 best = X[s < p2 ? s : p2 - 1];
+    float bestv = INFINITY;
+    for (int32_t n0 = s; n0 < e; n0 += kU) {
+        float4 v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = X[n0 + u < e ? n0 + u : e - 1];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            float mc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < D; ++k) {
+                const float a = rec_coord(v[u], k);
+                const float ek = fmaxf(hi[k] - a, a - lo[k]);
+                mc = mc + ek * ek;
+            }
+            if (mc < bestv) {
+                bestv = mc;
+                best = v[u];
+            }
+        }
+    }
+    *rep = best;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void cells_kernel(const float4 *__restrict__ xs1r,
+                                                         const float4 *__restrict__ xs2r,
+                                                         const int32_t *__restrict__ cstart,
+                                                         const float *__restrict__ bbox2,
+                                                         const float *__restrict__ boxb, int64_t clouds1,
+                                                         int64_t clouds2, int64_t b1, int64_t b2, int64_t p1,
+                                                         int64_t p2, float4 *__restrict__ info1,
+                                                         float4 *__restrict__ rep2,
+                                                         unsigned long long *__restrict__ cand) {
+    constexpr int kJ = kCellsJ, kU = 8;
+    constexpr int64_t kBlocksPerCloud = kCells / kThreads;
+    const int64_t groups = cdiv_dev(b2, kJ);
+    const int64_t units1 = clouds1 * groups * kBlocksPerCloud, units2 = clouds2 * kBlocksPerCloud;
+    const int64_t total = units1 + units2;
+    // the x2 units spread evenly among the x1 units (n2(p) of them before place p), so that
+    // every XCD's range holds its share of both
+    const int64_t place = xcd_unit(total);
+    const int64_t n2 = place * units2 / total;
+    if ((place + 1) * units2 / total > n2) {  // the same in every lane
+        const int64_t g2 = n2 / kBlocksPerCloud;
+        const int c = (int)(n2 - g2 * kBlocksPerCloud) * kThreads + threadIdx.x;
+        x2_rep_cell<D>(xs2r + g2 * p2, cstart + g2 * (kCells + 1), boxb + (g2 / b2) * 2 * D, c, p2,
+                       rep2 + g2 * kCells + pos_cell(c));
+        return;
+    }
+    const int64_t unit = place - n2;
+    const int64_t g1 = unit / (groups * kBlocksPerCloud);
+    const int64_t rest = unit - g1 * groups * kBlocksPerCloud;
+    const int64_t z = rest / kBlocksPerCloud;
+    const int64_t bb = g1 / b1;
+    const int64_t j0 = z * kJ;
+    const bool first = z == 0;
+    const int c = (int)(rest - z * kBlocksPerCloud) * kThreads + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int32_t *CS = cstart + (clouds2 + g1) * (kCells + 1);
+    const int32_t s = CS[c], e = CS[c + 1];
+    const float4 *X = xs1r + g1 * p1;
+    float box[kJ][2 * D];
+#pragma unroll
+    for (int jj = 0; jj < kJ; ++jj)
+#pragma unroll
+        for (int k = 0; k < 2 * D; ++k) box[jj][k] = j0 + jj < b2 ? bbox2[(bb * b2 + j0 + jj) * 2 * D + k] : 0.0f;
+    float lo[D], hi[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        lo[k] = INFINITY;
+        hi[k] = -INFINITY;
+    }
+    bool nan = false;
+    unsigned long long best[kJ];
+#pragma unroll
+    for (int jj = 0; jj < kJ; ++jj) best[jj] = 0;
+    for (int32_t n0 = s; n0 < e; n0 += kU) {
+        float4 v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = X[n0 + u < e ? n0 + u : e - 1];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            float a[D];
+#pragma unroll
+            for (int k = 0; k < D; ++k) a[k] = rec_coord(v[u], k);
+            if (first) {
+#pragma unroll
+                for (int k = 0; k < D; ++k) {
+                    nan = nan || a[k] != a[k];
+                    lo[k] = fminf(lo[k], a[k]);
+                    hi[k] = fmaxf(hi[k], a[k]);
+                }
+            }
+            const uint64_t pos1 = (uint64_t)rec_pos(v[u]) + 1;
+#pragma unroll
+            for (int jj = 0; jj < kJ; ++jj) {
+                float L = 0.0f;
+#pragma unroll
+                for (int k = 0; k < D; ++k) {
+                    const float ex = fmaxf(fmaxf(box[jj][2 * k] - a[k], a[k] - box[jj][2 * k + 1]), 0.0f);
+                    L = L + ex * ex;
+                }
+                const unsigned long long key = ((unsigned long long)__float_as_uint(L) << 32) | pos1;
+                best[jj] = key > best[jj] ? key : best[jj];
+            }
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < kJ; ++jj) {
+        if (j0 + jj >= b2) break;  // the same in every lane
+        unsigned long long *C = cand + (g1 * b2 + j0 + jj) * kCellCand + (c / 64) * kCandPerWave;
+        unsigned long long mine = best[jj];
+        for (int r = 0; r < kCandPerWave; ++r) {
+            const unsigned long long mx = wave_max_u64(mine);
+            if (lane == 0) C[r] = mx;
+            if (mine == mx) mine = 0;  // keys of distinct points differ
+        }
+    }
+    if (first) {
+        float f[8] = {__int_as_float(s), __int_as_float(e), 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            f[2 + k] = nan ? -INFINITY : lo[k];
+            f[5 + k] = nan ? INFINITY : hi[k];
+        }
+        float4 *I = info1 + (g1 * kCells + pos_cell(c)) * 2;
+        I[0] = make_float4(f[0], f[1], f[2], f[3]);
+        I[1] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+}
+
+__device__ __forceinline__ unsigned long long wave_or_u64(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v |= shfl_xor_u64(v, off);
+    return v;
+}
+
+// One cell by the whole wave: lane = window point W (the cell's 64-point window of sorted x2,
+// from x2's start of the cell clamped to a full window; lanes past wlen repeat its last
+// point), R = the cell's records in lanes 0 .. cnt - 1 (cnt <= 64).  Each lane tests every m_i
+// (broadcast, four at a time) against its point and keeps bit i when d(m_i, point) < T; the OR
+// over the wave marks the m some window point drops, the test a lane-per-m scan of the window
+// makes.  An m left, not a seed, sets bit (its iteration position) of the pair's flag bits
+// (preset to 0) for scan_flagged_kernel.
+template <int D>
+__device__ __forceinline__ void window_check(const float4 &W, const float4 &R, int cnt, float T, int64_t wlen,
+                                             int64_t pair, const uint32_t *seedm, uint32_t *flagbits, int64_t fwords,
+                                             uint32_t &evals) {
+    const int lane = threadIdx.x & 63;
+    float w[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) w[k] = rec_coord(W, k);
+    unsigned long long mine = 0;
+    for (int i0 = 0; i0 < cnt; i0 += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u < cnt ? i0 + u : cnt - 1;  // a repeated m sets a bit it already sets
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < D; ++k) {
+                const float mk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rec_coord(R, k)), i));
+                const float diff = mk - w[k];
+                s = s + diff * diff;
+            }
+            mine |= (unsigned long long)(s < T) << i;
+        }
+    }
+    const unsigned long long hits = wave_or_u64(mine);
+    if (lane == 0) evals += (uint32_t)(cnt * wlen);
+    if (lane < cnt && !((hits >> lane) & 1ull)) {
+        const uint32_t mpos = rec_pos(R);
+        if (!is_seed(seedm, pair, mpos)) atomicOr(&flagbits[pair * fwords + (mpos >> 5)], 1u << (mpos & 31));
+    }
+}
+
+// Scan of the sorted mode: block = kScanCells cells of one pair (positions pos(c); kScanCols
+// per lane), 16 waves; blocks ordered (x2 cloud, x1 cloud of the batch, block) so that an XCD
+// reads few x2 clouds.  The x1 points of cell c are the records start .. end (x1 is sorted in
+// the batch frame x2 shares), inside the exact box of info1.  First each lane tests that box
+// against x2's representative point q of cell c (rep2, an x2 point): when the box's farthest
+// corner from q, computed as d is (coordinate differences, squared and summed in order in
+// fp32), is below T, every m of the cell has d(m, q) < T and the whole cell is dropped.  That
+// holds bit for bit: rounding is monotone, so each |fl(a_k - q_k)| is at most the corner's
+// rounded difference, and the squares and the in-order sums keep that order.  Special values
+// (inf, NaN; a NaN cell's box) make the corner's value inf or NaN, which drops nothing.  The
+// cells left go to a list in LDS (their record range and window start), and the block's waves
+// then take them in turn, two at a time so that their loads overlap (window_check).
+constexpr int kScanThreads = 1024;
+#ifndef TPW_SCAN_COLS
+#define TPW_SCAN_COLS 1
+#endif
+constexpr int kScanCols = TPW_SCAN_COLS;
+constexpr int kScanCells = kScanThreads * kScanCols;
+constexpr int kScanBlocksPerPair = kCells / kScanCells;
+
+template <int D>
+__global__ __launch_bounds__(kScanThreads) void cell_scan_kernel(
+    const float4 *__restrict__ xs1r, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstT,
+    const float4 *__restrict__ info1, const float4 *__restrict__ rep2, int64_t clouds2, int64_t b1, int64_t b2,
+    int64_t p1, int64_t p2, const uint32_t *__restrict__ seedm, unsigned long long *__restrict__ keys,
+    uint32_t *__restrict__ flagbits, unsigned long long *__restrict__ counts) {
+    __shared__ int32_t lst[kScanCells][3];  // start, count, window start of each cell left
+    __shared__ uint32_t nlst;
+    // the index math is 32-bit (pairs <= 65535)
+    const uint32_t ub1 = (uint32_t)b1, ub2 = (uint32_t)b2;
+    const uint32_t unit = (uint32_t)xcd_unit(clouds2 * b1 * kScanBlocksPerPair);
+    const uint32_t g2 = unit / (ub1 * kScanBlocksPerPair);
+    const uint32_t rest = unit - g2 * ub1 * kScanBlocksPerPair;
+    const uint32_t i = rest / kScanBlocksPerPair, blk = rest - i * kScanBlocksPerPair;
+    const uint32_t bb = g2 / ub2, j = g2 - bb * ub2;
+    const uint32_t g1 = bb * ub1 + i;
+    const int64_t pair = (int64_t)g1 * ub2 + j;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (threadIdx.x == 0) nlst = 0;
+    __syncthreads();
+    unsigned long long *key = &keys[pair];
+    float T = threshold_of(key);
+    const int64_t wlen = p2 < 64 ? p2 : 64;
+    uint32_t evals = 0, tests = 0;
+#pragma unroll
+    for (int h = 0; h < kScanCols; ++h) {
+        const int t = (int)blk * kScanCells + h * kScanThreads + threadIdx.x;  // position of a cell
+        const float4 A = info1[((int64_t)g1 * kCells + t) * 2], Bq = info1[((int64_t)g1 * kCells + t) * 2 + 1];
+        const float4 q = rep2[(int64_t)g2 * kCells + t];
+        const int32_t s2 = cstT[(int64_t)g2 * kCells + t];
+        const float f[6] = {A.z, A.w, Bq.x, Bq.y, Bq.z, Bq.w};
+        const int32_t s1 = __float_as_int(A.x), e1 = __float_as_int(A.y);
+        bool todo = e1 > s1;
+        if (todo) {
+            float mc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < D; ++k) {
+                const float qk = rec_coord(q, k);
+                const float ek = fmaxf(f[3 + k] - qk, qk - f[k]);
+                mc = mc + ek * ek;
+            }
+            todo = !(mc < T);
+            ++tests;
+        }
+        const unsigned long long left = __ballot(todo);
+        if (left) {  // the same in every lane
+            uint32_t base = 0;
+            if (lane == 0) base = atomicAdd(&nlst, (uint32_t)__popcll(left));  // LDS
+            base = __builtin_amdgcn_readfirstlane(base);
+            if (todo) {
+                const uint32_t e = base + __popcll(left & ((1ull << lane) - 1ull));
+                lst[e][0] = s1;
+                lst[e][1] = e1 - s1;
+                lst[e][2] = s2 < p2 - wlen ? s2 : (int32_t)(p2 - wlen);
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t n = nlst;
+    if (n) T = threshold_of(key);
+    const int wl = lane < wlen ? lane : (int)wlen - 1;
+    const int64_t fwords = cdiv_dev(p1, 32);
+    const float4 *X1 = xs1r + (int64_t)g1 * p1;
+    const float4 *X2 = xs2r + (int64_t)g2 * p2;
+    constexpr uint32_t kWaves = kScanThreads / 64;
+    for (uint32_t e0 = wave; e0 < n; e0 += 2 * kWaves) {
+        const bool two = e0 + kWaves < n;
+        int32_t cs[2], cn[2];
+        float4 W[2], R[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t e = u && two ? e0 + kWaves : e0;
+            cs[u] = __builtin_amdgcn_readfirstlane(lst[e][0]);
+            cn[u] = __builtin_amdgcn_readfirstlane(lst[e][1]);
+            const int32_t cw = __builtin_amdgcn_readfirstlane(lst[e][2]);
+            W[u] = X2[cw + wl];
+            R[u] = X1[cs[u] + (lane < cn[u] ? lane : cn[u] - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (u == 1 && !two) break;  // the same in every lane
+            window_check<D>(W[u], R[u], cn[u] < 64 ? cn[u] : 64, T, wlen, pair, seedm, flagbits, fwords, evals);
+            for (int32_t off = 64; off < cn[u]; off += 64) {
+                const int32_t rem = cn[u] - off;
+                const float4 r = X1[cs[u] + off + (lane < rem ? lane : rem - 1)];
+                window_check<D>(W[u], r, rem < 64 ? rem : 64, T, wlen, pair, seedm, flagbits, fwords, evals);
+            }
+        }
+    }
+    add_counts(counts, evals, tests);
 }
 
 // The sorted mode keeps one flag bit per (pair, m): up to 32 MiB of them.
@@ -1405,7 +1979,8 @@ struct Plan {
     bool cells = false;       // d <= 3 and int32 cell starts: the cell-sorted scan
     bool sorted = false;      // cells and the flags fit: x1 sorted too, in a shared frame
     bool multi_sort = false;  // few clouds to sort: the counting sort spread over blocks
-    int64_t box_rows1 = 0, box_rows2 = 0, box_chunk = 1, box_chunks = 0;
+    int64_t box_rows1 = 0, box_rows2 = 0, box_chunk = 1, box_chunks = 0;  // unsorted boxes
+    int64_t prep_chunk = 1, prep_chunks = 0;  // sorted boxes: rows per prep block
     int64_t chunk1 = 1, ncand = 0;   // x1 points per seed_select block; candidates per pair
     int64_t chunk2 = 1, nch2 = 0;    // x2 points per first_hit block
     int64_t chunkL = 1, nchL = 0;    // x2 points per list_scan block of the seeds
@@ -1423,14 +1998,19 @@ Plan make_plan(int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, in
     P.fast = d <= 4;
     P.cells = d <= 3 && p2 < (int64_t)0x7fffffff - 64;
     P.sorted = P.cells && sorted_mode(P.pairs, p1);
-    P.box_rows1 = P.sorted ? P.clouds1 * d : 0;
-    P.box_rows2 = P.clouds2 * d;
-    const int64_t pbox = P.sorted && p1 > p2 ? p1 : p2;
-    P.box_chunk = std::max<int64_t>(8192, round_up(cdiv(pbox, kMaxGridYZ), kThreads));
-    P.box_chunks = cdiv(pbox, P.box_chunk);
-    // at most 64 seed_select blocks (256 candidates) per pair, at least 4096 points each
-    P.chunk1 = std::max<int64_t>(4096, round_up(cdiv(p1, 64), kThreads));
-    P.ncand = cdiv(p1, P.chunk1) * (kThreads / 64);
+    const int64_t pmax = std::max(p1, p2);
+    if (P.sorted) {
+        P.prep_chunk = std::max<int64_t>(2048, round_up(cdiv(pmax, kMaxGridYZ), kThreads));
+        P.prep_chunks = cdiv(pmax, P.prep_chunk);
+        P.ncand = kCellCand;
+    } else {
+        P.box_rows2 = P.clouds2 * d;
+        P.box_chunk = std::max<int64_t>(8192, round_up(cdiv(p2, kMaxGridYZ), kThreads));
+        P.box_chunks = cdiv(p2, P.box_chunk);
+        // at most 64 seed_select blocks (256 candidates) per pair, at least 4096 points each
+        P.chunk1 = std::max<int64_t>(4096, round_up(cdiv(p1, 64), kThreads));
+        P.ncand = cdiv(p1, P.chunk1) * (kThreads / 64);
+    }
     P.chunk2 = std::max<int64_t>(4096, round_up(cdiv(p2, kMaxGridYZ), kThreads));
     P.nch2 = cdiv(p2, P.chunk2);
     P.chunkL = std::max<int64_t>(16384, round_up(cdiv(p2, kMaxGridYZ), kThreads));
@@ -1439,7 +2019,7 @@ Plan make_plan(int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, in
         P.sort_clouds = P.clouds2 + (P.sorted ? P.clouds1 : 0);
         P.multi_sort = P.sort_clouds <= 2048;
         // chunks of >= 4096 points, at most 4096 (cloud, chunk) histograms (64 MiB)
-        const int64_t psort = P.sorted && p1 > p2 ? p1 : p2;
+        const int64_t psort = P.sorted ? pmax : p2;
         const int64_t most = std::max<int64_t>(1, 4096 / std::max<int64_t>(1, P.sort_clouds));
         P.sort_chunks = std::min<int64_t>(cdiv(psort, 4096), most);
         P.sort_chunk = round_up(cdiv(psort, P.sort_chunks), kThreads);
@@ -1449,20 +2029,22 @@ Plan make_plan(int64_t batch, int64_t b1, int64_t p1, int64_t b2, int64_t p2, in
 }
 
 struct Workspace {
-    float *xs1, *xs2, *bbox, *bbox1, *boxb;
-    float4 *xs2r, *xs1r;
+    float *xs1, *xs2, *bbox, *boxb, *part;
+    float4 *xs2r, *xs1r, *info1, *rep2;
     unsigned long long *keys, *cand, *first;
-    int32_t *cstart2;
+    int32_t *cstart2, *cstT;
     int *boxkeys;
-    uint32_t *seedmin, *seedm, *cellhist, *celltot;
+    uint32_t *seedmin, *seedm, *cellhist;
     uint32_t *flagbits;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// [keys | x2 boxes | x1 SoA | x2 SoA | box keys | seeds, candidates, first hits (fast) |
-//  x2 records, x2 cell starts (cells) | x1 boxes, batch boxes, x1 records, flag bits
-//  (sorted) | per-chunk cell histograms (multi_sort)]
+// [keys | x2 boxes | x1, x2 SoA (unsorted) | box keys (unsorted) | box partials, batch boxes
+//  (sorted) | seeds, candidates, first hits (fast) | x2 records, cell starts (cells; x2's,
+//  then x1's when sorted) | x1 records, x1 cell ranges and boxes, x2 representatives and cell
+//  starts in the cell scan's order, flag bits (sorted) | per-chunk cell histograms
+//  (multi_sort)]
 Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size_t *total = nullptr) {
     char *base = static_cast<char *>(ws), *p = base;
     auto take = [&](bool on, size_t bytes) {
@@ -1470,127 +2052,175 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
         if (on) p += align256(bytes);
         return on ? r : nullptr;
     };
+    const bool uns = !P.sorted;
     Workspace w;
     w.keys = reinterpret_cast<unsigned long long *>(take(true, 8 * P.pairs));
     w.bbox = reinterpret_cast<float *>(take(true, 4 * P.clouds2 * d * 2));
-    w.xs1 = reinterpret_cast<float *>(take(true, 4 * P.clouds1 * p1 * d));
-    w.xs2 = reinterpret_cast<float *>(take(true, 4 * P.clouds2 * p2 * d));
-    w.boxkeys = reinterpret_cast<int *>(take(P.active, 4 * (P.box_rows1 + P.box_rows2) * 2));
+    w.xs1 = reinterpret_cast<float *>(take(uns, 4 * P.clouds1 * p1 * d));
+    w.xs2 = reinterpret_cast<float *>(take(uns, 4 * P.clouds2 * p2 * d));
+    w.boxkeys = reinterpret_cast<int *>(take(uns && P.active, 4 * P.box_rows2 * 2));
+    w.part = reinterpret_cast<float *>(take(P.sorted, 4 * (P.clouds1 + P.clouds2) * P.prep_chunks * d * 2));
+    w.boxb = reinterpret_cast<float *>(take(P.sorted, 4 * P.batch * d * 2));
     w.seedmin = reinterpret_cast<uint32_t *>(take(P.fast, 4 * P.pairs * kSeeds));
     w.seedm = reinterpret_cast<uint32_t *>(take(P.fast, 4 * P.pairs * kSeeds));
     w.cand = reinterpret_cast<unsigned long long *>(take(P.fast, 8 * P.pairs * P.ncand));
     w.first = reinterpret_cast<unsigned long long *>(take(P.fast, 8 * P.pairs));
     w.xs2r = reinterpret_cast<float4 *>(take(P.cells, 16 * P.clouds2 * p2));
-    // multi_sort: cell starts of every sorted cloud, x2's first (they are x2's cstart)
-    w.cstart2 = reinterpret_cast<int32_t *>(
-        take(P.cells, 4 * (P.multi_sort ? P.sort_clouds : P.clouds2) * (kCells + 1)));
-    w.bbox1 = reinterpret_cast<float *>(take(P.sorted, 4 * P.clouds1 * d * 2));
-    w.boxb = reinterpret_cast<float *>(take(P.sorted, 4 * P.batch * d * 2));
+    w.cstart2 = reinterpret_cast<int32_t *>(take(P.cells, 4 * P.sort_clouds * (kCells + 1)));
     w.xs1r = reinterpret_cast<float4 *>(take(P.sorted, 16 * P.clouds1 * p1));
+    w.info1 = reinterpret_cast<float4 *>(take(P.sorted, 32 * P.clouds1 * kCells));
+    w.rep2 = reinterpret_cast<float4 *>(take(P.sorted, 16 * P.clouds2 * kCells));
+    w.cstT = reinterpret_cast<int32_t *>(take(P.sorted, 4 * P.clouds2 * kCells));
     w.flagbits = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * P.pairs * cdiv(p1, 32)));
     w.cellhist = reinterpret_cast<uint32_t *>(take(P.multi_sort, 4 * P.sort_clouds * P.sort_chunks * kCells));
-    w.celltot = reinterpret_cast<uint32_t *>(take(P.multi_sort, 4 * P.sort_clouds * kCells));
     if (total) *total = (size_t)(p - base);
     return w;
 }
 
-// Cell sort of x2 (and, in the sorted mode, of x1) into records.
+// Host side of the measurement counters: armed on one device, whose device address of
+// g_hd_counts the kernels get (null otherwise); launches of the forward are counted on the host.
+struct Counters {
+    std::mutex mu;
+    bool armed = false;
+    int device = -1;
+    unsigned long long *ptr = nullptr;
+    unsigned long long launches = 0;
+};
+Counters g_counters;
+
+unsigned long long *counts_arg() {
+    if (!__atomic_load_n(&g_counters.armed, __ATOMIC_RELAXED)) return nullptr;
+    std::lock_guard<std::mutex> lk(g_counters.mu);
+    int dev = -1;
+    if (!g_counters.armed || hipGetDevice(&dev) != hipSuccess || dev != g_counters.device) return nullptr;
+    return g_counters.ptr;
+}
+
+void note_launch() {
+    if (!__atomic_load_n(&g_counters.armed, __ATOMIC_RELAXED)) return;
+    std::lock_guard<std::mutex> lk(g_counters.mu);
+    int dev = -1;
+    if (g_counters.armed && hipGetDevice(&dev) == hipSuccess && dev == g_counters.device) ++g_counters.launches;
+}
+
+#define HD_LAUNCH(...)                    \
+    do {                                  \
+        hipLaunchKernelGGL(__VA_ARGS__);  \
+        note_launch();                    \
+    } while (0)
+
+// Counting sort into records: x2's clouds (sets S2), then, when S1 has clouds, x1's; cell starts
+// of every sorted cloud in that order.
 template <int D>
-void launch_sort(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2, hipStream_t s) {
-    const CellSet S2{w.xs2, w.xs2r, P.sorted ? w.boxb : w.bbox, P.clouds2, p2, P.sorted ? b2 : 1};
-    const CellSet S1{w.xs1, w.xs1r, w.boxb, P.sorted ? P.clouds1 : 0, p1, b1};
+void launch_sort(const Plan &P, const Workspace &w, const CellSet &S2, const CellSet &S1, hipStream_t s) {
     if (P.multi_sort) {
         const dim3 grid((unsigned)P.sort_clouds, (unsigned)P.sort_chunks);
-        hipLaunchKernelGGL(cell_count_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, P.sort_chunks,
-                           w.cellhist);
-        hipLaunchKernelGGL(cell_prefix_kernel, dim3((unsigned)P.sort_clouds, kCells / kThreads), dim3(kThreads), 0,
-                           s, P.sort_chunks, w.cellhist, w.celltot);
-        hipLaunchKernelGGL(cell_start_kernel, dim3((unsigned)P.sort_clouds), dim3(kThreads), 0, s, S2, S1,
-                           w.celltot, w.cstart2);
-        hipLaunchKernelGGL(cell_scatter_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, P.sort_chunks,
-                           w.cellhist, w.cstart2);
+        HD_LAUNCH(cell_count_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, P.sort_chunks, w.cellhist);
+        HD_LAUNCH(cell_offsets_kernel, dim3((unsigned)P.sort_clouds), dim3(kOffThreads), 0, s, S2, S1,
+                  P.sort_chunks, w.cellhist, w.cstart2, w.cstT);
+        HD_LAUNCH(cell_scatter_kernel<D>, grid, dim3(kThreads), 0, s, S2, S1, P.sort_chunk, P.sort_chunks,
+                  static_cast<const uint32_t *>(w.cellhist));
     } else {
-        hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)P.clouds2), dim3(kThreads), 0, s, w.xs2, p2,
-                           S2.boxes, S2.clouds_per_box, w.xs2r, w.cstart2);
-        if (P.sorted)
-            hipLaunchKernelGGL(cell_sort_kernel<D>, dim3((unsigned)P.clouds1), dim3(kThreads), 0, s, w.xs1, p1,
-                               w.boxb, b1, w.xs1r, static_cast<int32_t *>(nullptr));
+        HD_LAUNCH(cell_sort_kernel<D>, dim3((unsigned)S2.clouds), dim3(kThreads), 0, s, S2, w.cstart2, w.cstT);
+        if (S1.clouds > 0)
+            HD_LAUNCH(cell_sort_kernel<D>, dim3((unsigned)S1.clouds), dim3(kThreads), 0, s, S1,
+                      w.cstart2 + S2.clouds * (kCells + 1), static_cast<int32_t *>(nullptr));
     }
 }
 
-// The cell-sorted scan (d <= 3): window pass, then, in the sorted mode, the flagged m.
+// The sorted mode, every launch (d <= 3).
 template <int D>
-void launch_cell_scan(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
-                      hipStream_t s) {
-    const int64_t m_per_block = 2048;
-    const dim3 grid((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs);
-    if (P.sorted) {
-        hipLaunchKernelGGL((scan_window_kernel<D, true>), grid, dim3(kThreads), 0, s,
-                           static_cast<const float *>(nullptr), w.xs1r, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2,
-                           m_per_block, w.seedm, w.keys, w.flagbits);
-        hipLaunchKernelGGL(scan_flagged_kernel<D>, dim3((unsigned)cdiv(p1, 32 * kThreads), (unsigned)P.pairs),
-                           dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, w.boxb, b1, b2, p1, p2, w.keys,
-                           w.flagbits);
-    } else {
-        hipLaunchKernelGGL((scan_window_kernel<D, false>), grid, dim3(kThreads), 0, s, w.xs1,
-                           static_cast<const float4 *>(nullptr), w.xs2r, w.cstart2, w.bbox, b1, b2, p1, p2,
-                           m_per_block, w.seedm, w.keys, static_cast<uint32_t *>(nullptr));
-    }
+int launch_sorted(const Plan &P, const Workspace &w, const float *x1, const float *x2, int64_t b1, int64_t p1,
+                  int64_t b2, int64_t p2, const int64_t *perm1, const int64_t *perm2, float *out, int64_t *idx1,
+                  int64_t *idx2, hipStream_t s) {
+    unsigned long long *counts = counts_arg();
+    Fills fs{};
+    fs.f[fs.count++] = Fill{reinterpret_cast<uint32_t *>(w.keys), 2 * P.pairs, {0u, 0u}};
+    fs.f[fs.count++] = Fill{w.flagbits, P.pairs * cdiv(p1, 32), {0u, 0u}};
+    HD_LAUNCH(prep_kernel<D>, dim3((unsigned)(P.clouds1 + P.clouds2), (unsigned)P.prep_chunks), dim3(kThreads), 0,
+              s, x1, P.clouds1, p1, x2, p2, P.prep_chunk, P.prep_chunks, w.part, fs);
+    HD_LAUNCH(frames_kernel<D>, dim3((unsigned)(P.clouds2 + P.batch)), dim3(kThreads), 0, s, w.part, P.clouds1,
+              P.clouds2, b1, b2, P.prep_chunks, w.bbox, w.boxb);
+    int rc = check_launch("hausdorff frames");
+    if (rc) return rc;
+    const CellSet S2{x2, perm2, w.xs2r, w.boxb, P.clouds2, p2, b2, b2};
+    const CellSet S1{x1, perm1, w.xs1r, w.boxb, P.clouds1, p1, b1, b1};
+    launch_sort<D>(P, w, S2, S1, s);
+    HD_LAUNCH(cells_kernel<D>,
+              dim3((unsigned)((P.clouds1 * cdiv(b2, kCellsJ) + P.clouds2) * (kCells / kThreads))), dim3(kThreads),
+              0, s, w.xs1r, w.xs2r, w.cstart2, w.bbox, w.boxb, P.clouds1, P.clouds2, b1, b2, p1, p2, w.info1, w.rep2,
+              w.cand);
+    HD_LAUNCH(seed_ball_kernel<D>, dim3((unsigned)cdiv(P.pairs * kSeeds, kThreads / 64)), dim3(kThreads), 0, s, x1,
+              perm1, w.xs2r, w.cstart2, w.boxb, true, w.cand, P.ncand, b1, b2, p1, p2, P.pairs, w.seedm, w.keys,
+              counts);
+    rc = check_launch("hausdorff seeds");
+    if (rc) return rc;
+    HD_LAUNCH(cell_scan_kernel<D>, dim3((unsigned)(P.pairs * kScanBlocksPerPair)), dim3(kScanThreads), 0, s, w.xs1r,
+              w.xs2r, w.cstT, w.info1, w.rep2, P.clouds2, b1, b2, p1, p2, w.seedm, w.keys, w.flagbits, counts);
+    HD_LAUNCH(scan_flagged_kernel<D>, dim3((unsigned)(cdiv(p1, 32 * kThreads) * P.pairs)), dim3(kThreads), 0, s, x1,
+              perm1, w.xs2r, w.cstart2, w.boxb, P.clouds2, b1, b2, p1, p2, w.keys, w.flagbits, counts);
+    HD_LAUNCH(first_ball_kernel<D>, dim3((unsigned)cdiv(P.pairs, kThreads / 64)), dim3(kThreads), 0, s, x1, perm1,
+              perm2, w.xs2r, w.cstart2, w.boxb, true, w.keys, b1, b2, p1, p2, P.pairs, out, idx1, idx2, counts);
+    return check_launch("hausdorff scan");
 }
 
-// d = 1..4 after the relayout and the boxes: (cell sort,) seeds, scan, final rescan, outputs.
+// d = 1..4 in the unsorted modes, after the relayout and the boxes: (cell sort of x2,) seeds,
+// scan, final rescan, outputs.
 template <int D>
-int launch_fast(const Plan &P, const Workspace &w, int64_t b1, int64_t p1, int64_t b2, int64_t p2,
+int launch_fast(const Plan &P, const Workspace &w, const float *x1, const float *x2, int64_t b1, int64_t p1,
+                int64_t b2, int64_t p2,
                 const int64_t *perm1, const int64_t *perm2, float *out, int64_t *idx1, int64_t *idx2,
                 hipStream_t s) {
     constexpr bool kCellsOk = D <= 3;
     const bool cells = kCellsOk && P.cells;
-    const float *frames = P.sorted ? w.boxb : w.bbox;
+    unsigned long long *counts = counts_arg();
     const unsigned per_wave_blocks = (unsigned)cdiv(P.pairs, kThreads / 64);
     if constexpr (kCellsOk) {
-        if (cells) launch_sort<D>(P, w, b1, p1, b2, p2, s);
+        if (cells) {
+            const CellSet S2{x2, perm2, w.xs2r, w.bbox, P.clouds2, p2, b2, 1};
+            const CellSet none{nullptr, nullptr, nullptr, w.bbox, 0, 1, 1, 1};
+            launch_sort<D>(P, w, S2, none, s);
+        }
     }
-    hipLaunchKernelGGL(seed_select_kernel<D>, dim3((unsigned)P.pairs, (unsigned)cdiv(p1, P.chunk1)),
-                       dim3(kThreads), 0, s, w.xs1, w.bbox, b1, b2, p1, P.chunk1, P.ncand, w.cand);
-    hipLaunchKernelGGL(seed_pick_kernel, dim3(per_wave_blocks), dim3(kThreads), 0, s, w.cand, P.ncand, P.pairs,
-                       w.seedm);
+    HD_LAUNCH(seed_select_kernel<D>, dim3((unsigned)P.pairs, (unsigned)cdiv(p1, P.chunk1)), dim3(kThreads), 0, s,
+              w.xs1, w.bbox, b1, b2, p1, P.chunk1, P.ncand, w.cand);
     if constexpr (kCellsOk) {
         if (cells)
-            hipLaunchKernelGGL(seed_ball_kernel<D>, dim3((unsigned)cdiv(P.pairs * kSeeds, kThreads / 64)),
-                               dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, frames, P.sorted, w.seedm, b1, b2, p1,
-                               p2, P.pairs, w.keys);
+            HD_LAUNCH(seed_ball_kernel<D>, dim3((unsigned)cdiv(P.pairs * kSeeds, kThreads / 64)), dim3(kThreads), 0,
+                      s, x1, perm1, w.xs2r, w.cstart2, w.bbox, false, w.cand,
+                      P.ncand, b1, b2, p1, p2, P.pairs, w.seedm, w.keys, counts);
     }
     if (!cells) {
-        hipLaunchKernelGGL(list_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nchL), dim3(kThreads), 0, s,
-                           w.xs1, w.xs2, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2,
-                           p1, p2, P.chunkL, w.seedmin);
-        hipLaunchKernelGGL(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s,
-                           w.seedmin, w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, P.pairs,
-                           w.keys);
+        HD_LAUNCH(seed_pick_kernel, dim3(per_wave_blocks), dim3(kThreads), 0, s, w.cand, P.ncand, P.pairs, w.seedm);
+        HD_LAUNCH(list_scan_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nchL), dim3(kThreads), 0, s, w.xs1, w.xs2,
+                  w.seedm, static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, b1, b2, p1, p2, P.chunkL,
+                  w.seedmin);
+        HD_LAUNCH(list_fold_kernel, dim3((unsigned)cdiv(P.pairs * kSeeds, 256)), dim3(256), 0, s, w.seedmin, w.seedm,
+                  static_cast<const uint32_t *>(nullptr), (int64_t)kSeeds, P.pairs, w.keys);
     }
     int rc = check_launch("hausdorff seeds");
     if (rc) return rc;
     if constexpr (kCellsOk) {
         if (cells) {
-            launch_cell_scan<D>(P, w, b1, p1, b2, p2, s);
-            hipLaunchKernelGGL(first_ball_kernel<D>, dim3(per_wave_blocks), dim3(kThreads), 0, s, w.xs1, w.xs2r,
-                               w.cstart2, frames, P.sorted, w.keys, b1, b2, p1, p2, P.pairs, w.first);
+            const int64_t m_per_block = 2048;
+            HD_LAUNCH(scan_window_kernel<D>, dim3((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs),
+                      dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, w.bbox, b1, b2, p1, p2, m_per_block, w.seedm,
+                      w.keys, counts);
+            HD_LAUNCH(first_ball_kernel<D>, dim3(per_wave_blocks), dim3(kThreads), 0, s, x1, perm1, perm2, w.xs2r,
+                      w.cstart2, w.bbox, false, w.keys, b1, b2, p1, p2, P.pairs, out, idx1, idx2, counts);
         }
     }
     if (!cells) {
         const int64_t m_per_block = 2048;
         const int64_t lds_points = (kLdsFloats / D) / 64 * 64;
-        hipLaunchKernelGGL(scan_kernel<D>, dim3((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs),
-                           dim3(kThreads), 0, s, w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.seedm,
-                           w.keys);
-        hipLaunchKernelGGL(first_hit_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s,
-                           w.xs1, w.xs2, w.keys, b1, b2, p1, p2, P.chunk2, w.first);
+        HD_LAUNCH(scan_kernel<D>, dim3((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs), dim3(kThreads), 0, s,
+                  w.xs1, w.xs2, b1, b2, p1, p2, m_per_block, lds_points, w.seedm, w.keys);
+        HD_LAUNCH(first_hit_kernel<D>, dim3((unsigned)P.pairs, (unsigned)P.nch2), dim3(kThreads), 0, s, w.xs1, w.xs2,
+                  w.keys, b1, b2, p1, p2, P.chunk2, w.first);
+        HD_LAUNCH(write_out_kernel, dim3((unsigned)cdiv(P.pairs, 256)), dim3(256), 0, s, w.keys, w.first, perm1,
+                  perm2, P.pairs, b1, b2, p1, p2, out, idx1, idx2);
     }
-    rc = check_launch("hausdorff scan");
-    if (rc) return rc;
-    hipLaunchKernelGGL(write_out_kernel, dim3((unsigned)cdiv(P.pairs, 256)), dim3(256), 0, s, w.keys, w.first,
-                       perm1, perm2, P.pairs, b1, b2, p1, p2, out, idx1, idx2);
-    return check_launch("hausdorff final rescan");
+    return check_launch("hausdorff scan");
 }
 
 }  // namespace
@@ -1604,6 +2234,38 @@ extern "C" size_t tpw_hausdorff_workspace_size(int64_t batch, int64_t b1, int64_
     size_t total = 0;
     carve(nullptr, make_plan(batch, b1, p1, b2, p2, d), p1, p2, d, &total);
     return total;
+}
+
+extern "C" int tpw_hausdorff_counters(int arm, unsigned long long *out) {
+    std::lock_guard<std::mutex> lk(g_counters.mu);
+    if (arm) {
+        int dev = -1;
+        TPW_REQUIRE(hipGetDevice(&dev) == hipSuccess, "no current HIP device");
+        void *ptr = nullptr;
+        TPW_REQUIRE(hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_hd_counts)) == hipSuccess && ptr,
+                    "hipGetSymbolAddress failed");
+        TPW_REQUIRE(hipDeviceSynchronize() == hipSuccess, "hipDeviceSynchronize failed");
+        TPW_REQUIRE(hipMemset(ptr, 0, sizeof(g_hd_counts)) == hipSuccess, "hipMemset failed");
+        TPW_REQUIRE(hipDeviceSynchronize() == hipSuccess, "hipDeviceSynchronize failed");
+        g_counters.device = dev;
+        g_counters.ptr = static_cast<unsigned long long *>(ptr);
+        g_counters.launches = 0;
+        __atomic_store_n(&g_counters.armed, true, __ATOMIC_RELAXED);
+        return TPW_OK;
+    }
+    TPW_REQUIRE(out, "null pointer");
+    TPW_REQUIRE(g_counters.armed, "the counters are not armed");
+    __atomic_store_n(&g_counters.armed, false, __ATOMIC_RELAXED);
+    int dev = -1;
+    TPW_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev == g_counters.device,
+                "read the counters with the device they were armed on current");
+    TPW_REQUIRE(hipDeviceSynchronize() == hipSuccess, "hipDeviceSynchronize failed");
+    unsigned long long c[2] = {0, 0};
+    TPW_REQUIRE(hipMemcpy(c, g_counters.ptr, sizeof(c), hipMemcpyDeviceToHost) == hipSuccess, "hipMemcpy failed");
+    out[0] = c[0];
+    out[1] = c[1];
+    out[2] = g_counters.launches;
+    return TPW_OK;
 }
 
 extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t batch, int64_t b1,
@@ -1622,7 +2284,14 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     hipStream_t s = as_stream(stream);
     const Plan P = make_plan(batch, b1, p1, b2, p2, d);
     const Workspace w = carve(workspace, P, p1, p2, d);
-    // presets: keys 0, box keys (+inf, -inf), seed mins +inf, first hits all ones, flags 0
+    if (P.sorted) {
+        switch (d) {
+            case 1: return launch_sorted<1>(P, w, x1, x2, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+            case 2: return launch_sorted<2>(P, w, x1, x2, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+            default: return launch_sorted<3>(P, w, x1, x2, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+        }
+    }
+    // presets: keys 0, box keys (+inf, -inf), seed mins +inf, first hits all ones
     Fills fs{};
     int64_t most = 0;
     auto add = [&](void *ptr, int64_t words, uint32_t v0, uint32_t v1) {
@@ -1631,42 +2300,41 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
         most = std::max(most, words);
     };
     add(w.keys, 2 * pairs, 0u, 0u);
-    add(w.boxkeys, 2 * (P.box_rows1 + P.box_rows2), kOrderedPosInf, kOrderedNegInf);
+    add(w.boxkeys, 2 * P.box_rows2, kOrderedPosInf, kOrderedNegInf);
     add(w.seedmin, pairs * kSeeds, 0x7f800000u, 0x7f800000u);
     add(w.first, 2 * pairs, 0xffffffffu, 0xffffffffu);
-    add(w.flagbits, P.pairs * cdiv(p1, 32), 0u, 0u);
-    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)std::min<int64_t>(cdiv(most, 256), 2048)), dim3(256), 0, s, fs);
+    HD_LAUNCH(fill_kernel, dim3((unsigned)std::min<int64_t>(cdiv(most, 256), 2048)), dim3(256), 0, s, fs);
     int rc = check_launch("hausdorff presets");
     if (rc) return rc;
     if (P.active) {
-        hipLaunchKernelGGL(soa_kernel, dim3((unsigned)cdiv(batch * b1 * p1, 256)), dim3(256), 0, s,
-                           x1, perm1, batch * b1, b1, p1, (int)d, w.xs1);
-        hipLaunchKernelGGL(soa_kernel, dim3((unsigned)cdiv(batch * b2 * p2, 256)), dim3(256), 0, s,
-                           x2, perm2, batch * b2, b2, p2, (int)d, w.xs2);
-        hipLaunchKernelGGL(bbox_rows_kernel, dim3((unsigned)(P.box_rows1 + P.box_rows2), (unsigned)P.box_chunks),
-                           dim3(kThreads), 0, s, w.xs1, P.box_rows1, p1, w.xs2, p2, P.box_chunk, w.boxkeys);
-        const int64_t fin = P.box_rows1 + P.box_rows2 + (P.sorted ? batch * d : 0);
-        hipLaunchKernelGGL(box_finish_kernel, dim3((unsigned)cdiv(fin, 256)), dim3(256), 0, s, w.boxkeys,
-                           P.box_rows1, P.box_rows2, w.bbox1, w.bbox, batch, b1, b2, (int)d, w.boxb);
+        HD_LAUNCH(soa_kernel, dim3((unsigned)cdiv(batch * b1 * p1, 256)), dim3(256), 0, s, x1, perm1, batch * b1, b1,
+                  p1, (int)d, w.xs1);
+        HD_LAUNCH(soa_kernel, dim3((unsigned)cdiv(batch * b2 * p2, 256)), dim3(256), 0, s, x2, perm2, batch * b2, b2,
+                  p2, (int)d, w.xs2);
+        HD_LAUNCH(bbox_rows_kernel, dim3((unsigned)P.box_rows2, (unsigned)P.box_chunks), dim3(kThreads), 0, s,
+                  w.xs1, (int64_t)0, p1, w.xs2, p2, P.box_chunk, w.boxkeys);
+        HD_LAUNCH(box_finish_kernel, dim3((unsigned)cdiv(P.box_rows2, 256)), dim3(256), 0, s, w.boxkeys,
+                  (int64_t)0, P.box_rows2, static_cast<float *>(nullptr), w.bbox, batch, b1, b2, (int)d,
+                  static_cast<float *>(nullptr));
         rc = check_launch("hausdorff prologue");
         if (rc) return rc;
         if (P.fast) {
             switch (d) {
-                case 1: return launch_fast<1>(P, w, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
-                case 2: return launch_fast<2>(P, w, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
-                case 3: return launch_fast<3>(P, w, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
-                default: return launch_fast<4>(P, w, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+                case 1: return launch_fast<1>(P, w, x1, x2, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+                case 2: return launch_fast<2>(P, w, x1, x2, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+                case 3: return launch_fast<3>(P, w, x1, x2, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
+                default: return launch_fast<4>(P, w, x1, x2, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
             }
         }
-        hipLaunchKernelGGL(seed_kernel<0>, dim3((unsigned)pairs), dim3(kThreads), 0, s, w.xs1, w.xs2, w.bbox, b1,
-                           b2, p1, p2, (int)d, w.keys);
-        hipLaunchKernelGGL(scan_kernel_any, dim3((unsigned)cdiv(p1, 2048), (unsigned)pairs), dim3(kThreads), 0, s,
-                           w.xs1, w.xs2, b1, b2, p1, p2, (int)d, (int64_t)2048, w.keys);
+        HD_LAUNCH(seed_kernel<0>, dim3((unsigned)pairs), dim3(kThreads), 0, s, w.xs1, w.xs2, w.bbox, b1, b2, p1, p2,
+                  (int)d, w.keys);
+        HD_LAUNCH(scan_kernel_any, dim3((unsigned)cdiv(p1, 2048), (unsigned)pairs), dim3(kThreads), 0, s, w.xs1,
+                  w.xs2, b1, b2, p1, p2, (int)d, (int64_t)2048, w.keys);
         rc = check_launch("hausdorff scan_kernel_any");
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(finalize_kernel<0>, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads), 0, s,
-                       w.xs1, w.xs2, w.keys, perm1, perm2, pairs, b1, b2, p1, p2, (int)d, out, idx1, idx2);
+    HD_LAUNCH(finalize_kernel<0>, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads), 0, s, w.xs1, w.xs2,
+              w.keys, perm1, perm2, pairs, b1, b2, p1, p2, (int)d, out, idx1, idx2);
     return check_launch("hausdorff finalize_kernel");
 }
 

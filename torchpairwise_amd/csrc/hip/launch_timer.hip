@@ -46,9 +46,17 @@ LaunchEvents launch_events(const char *family) {
     return e;
 }
 
+__global__ void empty_kernel() {}
+
 }  // namespace tpw
 
 using namespace tpw;
+
+extern "C" int tpw_empty_launches(int count, void *stream) {
+    TPW_REQUIRE(count >= 0, "count must be >= 0");
+    for (int i = 0; i < count; ++i) hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, as_stream(stream));
+    return check_launch("tpw_empty_launches");
+}
 
 extern "C" int tpw_launch_timer_arm(const char *family, int capacity) {
     TPW_REQUIRE(family && strlen(family) > 0 && strlen(family) < sizeof(g_timer.family), "invalid kernel family");

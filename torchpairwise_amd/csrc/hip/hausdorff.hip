@@ -1106,8 +1106,9 @@ __global__ __launch_bounds__(kThreads) void cell_scatter_kernel(CellSet A, CellS
 // bound; the search ends at the first ring whose lower bound is above it.  Both bounds are
 // conservative: a point's cell comes from the rounded (x - lo) * scale (off by far less than the
 // 0.01-cell margin taken off every gap), edge cells reach to infinity (clamping), and the bound
-// is scaled by 1 - 2^-12 for the rounding of the computed distances.  Visiting order does not
-// change a min, so the result is that of a scan of all of x2.
+// is scaled by 1 - 2^-12 for the rounding of the computed distances.  The ring's cells are
+// taken 64 at a time: the candidates among them are scanned together, their points packed 64 to
+// a step.  Visiting order does not change a min, so the result is that of a scan of all of x2.
 //   kBallPrune: drop the query at the first d < T (returns true); otherwise fold the exact min
 //     with position mpos into key (returns false);
 //   kBallMin: return the exact min (out_min);
@@ -1205,7 +1206,7 @@ __device__ unsigned long long wave_ball_query(const float (&q)[D], const float4 
         const int64_t count = ring_count<D>(R);
         for (int64_t t0 = 0; t0 < count; t0 += 64) {
             const int64_t t = t0 + lane;
-            int cell = -1;
+            int32_t cs = 0, cn = 0;  // the lane's candidate cell: its points (none: cn = 0)
             if (t < count) {
                 int o[D];
                 ring_cell<D>(R, t, o);
@@ -1224,29 +1225,41 @@ __device__ unsigned long long wave_ball_query(const float (&q)[D], const float4 
                     if constexpr (D == 1) morton = u;
                     else morton |= spread_bits<D>(u) << k;
                 }
-                if (in && !(lbc * kShrink > bound) && CS[morton + 1] > CS[morton]) cell = (int)morton;
+                if (in && !(lbc * kShrink > bound)) {
+                    cs = CS[morton];
+                    cn = CS[morton + 1] - cs;
+                }
             }
-            unsigned long long cand = __ballot(cell >= 0);
-            while (cand) {
-                const int l = __builtin_ctzll(cand);
-                cand &= cand - 1;
-                const int cl = __builtin_amdgcn_readlane(cell, l);
-                const int64_t s = CS[cl], e = CS[cl + 1];
-                for (int64_t n0 = s; n0 < e; n0 += 64) {
-                    const int64_t n = n0 + lane;
-                    const bool ok = n < e;
-                    const float4 v = X2[ok ? n : s];
-                    const float d = ok ? rec_dist<D>(q, v) : INFINITY;
-                    evals += ok ? 1u : 0u;
-                    if constexpr (MODE == kBallPrune) {
-                        if (__any(d < T)) return 1ull;
-                    }
-                    if constexpr (MODE == kBallFirst) {
-                        const unsigned long long pos = rec_pos(v);
-                        if (ok && d == T && pos < first) first = pos;
-                    } else {
-                        best = fminf(best, d);
-                    }
+            // the candidate cells' points, packed 64 per step: point g of the chunk belongs to
+            // the lane r with the largest exclusive prefix of the counts that is <= g (prefixes
+            // do not decrease over the lanes; a lane after the owner starts past g)
+            uint32_t incl = (uint32_t)cn;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
+                if (lane >= off) incl += o;
+            }
+            const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            const uint32_t excl = incl - (uint32_t)cn;
+            for (uint32_t b0 = 0; b0 < total; b0 += 64) {
+                const uint32_t g = b0 + (uint32_t)lane;
+                const bool ok = g < total;
+                int r = 0;
+#pragma unroll
+                for (int step = 32; step > 0; step >>= 1)
+                    if ((uint32_t)__shfl((int)excl, r + step, 64) <= g) r += step;
+                const int32_t n = __shfl(cs, r, 64) + (int32_t)(g - (uint32_t)__shfl((int)excl, r, 64));
+                const float4 v = X2[ok ? n : 0];
+                const float d = ok ? rec_dist<D>(q, v) : INFINITY;
+                evals += ok ? 1u : 0u;
+                if constexpr (MODE == kBallPrune) {
+                    if (__any(d < T)) return 1ull;
+                }
+                if constexpr (MODE == kBallFirst) {
+                    const unsigned long long pos = rec_pos(v);
+                    if (ok && d == T && pos < first) first = pos;
+                } else {
+                    best = fminf(best, d);
                 }
             }
         }
@@ -1429,10 +1442,18 @@ __global__ __launch_bounds__(kThreads) void seed_ball_kernel(
     const int64_t t = pair * kSeeds + s;
     const int lane = threadIdx.x & 63;
     const unsigned long long *C = cand + pair * ncand;
+    // up to kHeld candidates per lane stay in registers over the rounds (any more are re-read)
+    constexpr int kHeld = 4;
+    unsigned long long held[kHeld];
+#pragma unroll
+    for (int h = 0; h < kHeld; ++h) held[h] = lane + 64 * h < ncand ? C[lane + 64 * h] : 0ull;
     unsigned long long prev = ~0ull, pick = 0;
     for (int r = 0; r <= s; ++r) {  // every lane holds the same reduced values
         unsigned long long best = 0;
-        for (int64_t e = lane; e < ncand; e += 64) {
+#pragma unroll
+        for (int h = 0; h < kHeld; ++h)
+            if (held[h] < prev && held[h] > best) best = held[h];
+        for (int64_t e = lane + 64 * kHeld; e < ncand; e += 64) {
             const unsigned long long v = C[e];
             if (v < prev && v > best) best = v;
         }

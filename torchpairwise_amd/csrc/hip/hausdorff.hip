@@ -1014,15 +1014,26 @@ __global__ __launch_bounds__(kOffThreads) void cell_offsets_kernel(CellSet A, Ce
     uint32_t *H = hist + g * chunks * kCells;
     constexpr int kPer = kCells / kOffThreads;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    // per-cell totals: thread t sums cells t + 1024 e over the chunks
+    // per-cell totals: thread t sums cells t + 1024 e over the chunks, four chunks of its four
+    // cells in flight at a time
+    uint32_t run4[kPer] = {};
+    int64_t y = 0;
+    for (; y + 4 <= chunks; y += 4) {
+        uint32_t v[4][kPer];
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) {
-        const int cell = t + e * kOffThreads;
-        uint32_t run = 0;
-#pragma unroll 8
-        for (int64_t y = 0; y < chunks; ++y) run += H[y * kCells + cell];
-        tot[cell] = run;
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) v[u][e] = H[(y + u) * kCells + t + e * kOffThreads];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) run4[e] += v[u][e];
     }
+    for (; y < chunks; ++y)
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) run4[e] += H[y * kCells + t + e * kOffThreads];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) tot[t + e * kOffThreads] = run4[e];
     __syncthreads();
     // exclusive scan over cells: thread t owns cells kPer t .. kPer t + kPer - 1
     uint32_t v[kPer], local = 0;
@@ -1055,21 +1066,38 @@ __global__ __launch_bounds__(kOffThreads) void cell_offsets_kernel(CellSet A, Ce
         run += v[e];
     }
     __syncthreads();
-    // starts, and each chunk's first slot per cell
+    // starts, and each chunk's first slot per cell (four chunks of the four cells at a time)
     int32_t *St = starts + g * (kCells + 1);
+    uint32_t sl[kPer];
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
         const int cell = t + e * kOffThreads;
-        uint32_t s = tot[cell];
-        St[cell] = (int32_t)s;
-        if (startsA_T && g < A.clouds) startsA_T[g * kCells + pos_cell(cell)] = (int32_t)s;
-#pragma unroll 8
-        for (int64_t y = 0; y < chunks; ++y) {
-            const uint32_t n = H[y * kCells + cell];
-            H[y * kCells + cell] = s;
-            s += n;
-        }
+        sl[e] = tot[cell];
+        St[cell] = (int32_t)sl[e];
+        if (startsA_T && g < A.clouds) startsA_T[g * kCells + pos_cell(cell)] = (int32_t)sl[e];
     }
+    y = 0;
+    for (; y + 4 <= chunks; y += 4) {
+        uint32_t v[4][kPer];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) v[u][e] = H[(y + u) * kCells + t + e * kOffThreads];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) {
+                H[(y + u) * kCells + t + e * kOffThreads] = sl[e];
+                sl[e] += v[u][e];
+            }
+    }
+    for (; y < chunks; ++y)
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) {
+            const uint32_t n = H[y * kCells + t + e * kOffThreads];
+            H[y * kCells + t + e * kOffThreads] = sl[e];
+            sl[e] += n;
+        }
     if (t == 0) St[kCells] = (int32_t)S.p;
 }
 

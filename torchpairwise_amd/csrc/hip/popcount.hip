@@ -67,6 +67,13 @@ __device__ __forceinline__ float sat_count(uint32_t c) {
     return (float)(c < kFloatExactLimit ? c : kFloatExactLimit);
 }
 
+// Bitwise select of a (where the lane's c is set) or b: a conditional around a divide compiles
+// to an exec-masked branch per output, whose scalar bookkeeping costs more than the divide.
+__device__ __forceinline__ float select_bits(bool c, float a, float b) {
+    const uint32_t m = 0u - (uint32_t)c;
+    return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
+}
+
 // Output value from the tile's count (of OP) and, for jaccard and the count metrics, the two
 // rows' popcounts.  The count metrics reproduce the reference's float32 composites over the
 // separate pw*_sum passes (pairwise_metrics.cpp:224-243,339-399): every count is what a
@@ -91,7 +98,7 @@ __device__ __forceinline__ float finish(uint32_t cnt, uint32_t pa, uint32_t pb, 
     } else if constexpr (EPI == kJaccard) {
         const uint32_t sum = pa + pb;
         const float xf = sat_count(sum - 2u * cnt), of = sat_count(sum - cnt);
-        return of != 0.0f ? __fdiv_rn(xf, of) : 0.0f;
+        return select_bits(of != 0.0f, __fdiv_rn(xf, of), 0.0f);
     } else {
         constexpr int MET = EPI - kCountMetric;
         const uint32_t n11 = cnt, x = pa + pb - 2u * n11;  // and, xor counts
@@ -101,7 +108,7 @@ __device__ __forceinline__ float finish(uint32_t cnt, uint32_t pa, uint32_t pb, 
             return __fdiv_rn(S, df);
         } else if constexpr (MET == TPW_BMET_JACCARD) {  // prf_div(xor, or, "zero")
             const float O = sat_count(pa + pb - n11);
-            return O != 0.0f ? __fdiv_rn(S, O) : 0.0f;
+            return select_bits(O != 0.0f, __fdiv_rn(S, O), 0.0f);
         } else if constexpr (MET == TPW_BMET_DICE) {  // R / (2 and + R), R = xor
             return __fdiv_rn(S, 2.0f * A + S);
         } else if constexpr (MET == TPW_BMET_KULCZYNSKI1) {  // and / xor
@@ -126,7 +133,7 @@ __device__ __forceinline__ float finish(uint32_t cnt, uint32_t pa, uint32_t pb, 
             const float num = 2.0f * hR;
             const float prod = A * n00;
             const float den = prod + hR;
-            return den != 0.0f ? __fdiv_rn(num, den) : 0.0f;
+            return select_bits(den != 0.0f, __fdiv_rn(num, den), 0.0f);
         }
     }
 }
@@ -162,9 +169,10 @@ __device__ __forceinline__ float div_count(float x, float o) {
     return div_count_r(x, o, y);
 }
 
-// x / o as __fdiv_rn gives it, o = 0 included (x / 0 = +inf, 0 / 0 = NaN).
+// x / o as __fdiv_rn gives it, o = 0 included (x / 0 = +inf, 0 / 0 = NaN): both values formed,
+// one selected.
 __device__ __forceinline__ float div_count_z(float x, float o) {
-    return o != 0.0f ? div_count(x, o) : x * __builtin_inff();
+    return select_bits(o == 0.0f, x * __builtin_inff(), div_count(x, o));
 }
 
 // finish<> for rows of at most kSmallRowLimit features, on float counts: c is the AND count
@@ -213,7 +221,7 @@ __device__ __forceinline__ float finish_small(float c, float pa, float pb, float
             const float num = 2.0f * hR;
             const float prod = A * n00;
             const float den = prod + hR;
-            return den != 0.0f ? __fdiv_rn(num, den) : 0.0f;
+            return select_bits(den != 0.0f, __fdiv_rn(num, den), 0.0f);
         }
     }
 }

@@ -395,6 +395,83 @@ def test_hausdorff_cell_scan_edges_bit_exact(case):
         assert_equal(got.cpu(), torch.from_numpy(want), f"{case} {nm}")
 
 
+def _hd_nonfinite(case):
+    """Inputs holding NaN, +-inf, or coordinates whose squared differences overflow, for each
+    launch plan: the sorted mode (d <= 3, few pairs), d = 4 (seeds and scan without the grid),
+    d = 5 (the generic scan) and the unsorted cell scan (pairs x p1 > 2^28)."""
+    g = torch.Generator().manual_seed(91)
+    perm1 = perm2 = None
+    x1 = torch.rand(3, 500, 3, generator=g)
+    x2 = torch.rand(2, 400, 3, generator=g) + 0.05
+    if case == "nan_x1":
+        x1[0, 10, 1] = float("nan")
+    elif case == "nan_x2":
+        x2[1, 7, 0] = float("nan")
+    elif case == "nan_x2_last":  # the loop's last s of every row is NaN: no row is folded
+        x2[0, -1, 2] = float("nan")
+    elif case == "inf_x1":
+        x1[1, 33, 0] = float("inf")
+    elif case == "ninf_x2":
+        x2[0, 5, 1] = float("-inf")
+    elif case == "nan_cloud":
+        x1[2] = float("nan")
+    elif case == "overflow":  # finite inputs, every squared difference +inf
+        x1 = x1 * 1e20
+        x2 = x2 * -1e20
+    elif case == "overflow_rows":  # a few rows whose every squared difference is +inf
+        x1[0, 40:43] = 3e38
+    elif case in ("mixed_d1", "mixed_d2"):
+        d = int(case[-1])
+        x1 = torch.rand(2, 300, d, generator=g)
+        x2 = torch.rand(2, 200, d, generator=g)
+        x1[0, 3, 0] = float("nan")
+        x2[1, 9, 0] = float("inf")
+    elif case == "batched":  # only batch 1 holds a NaN: batches 0 and 2 keep the pruned path
+        x1 = torch.rand(3, 2, 300, 3, generator=g)
+        x2 = torch.rand(3, 2, 200, 3, generator=g) + 0.05
+        x1[1, 0, 17, 2] = float("nan")
+    elif case == "shuffled":
+        x1 = torch.rand(2, 2, 300, 3, generator=g)
+        x2 = torch.rand(2, 3, 400, 3, generator=g) + 0.05
+        x2[0, 1, 50, 0] = float("nan")
+        x1[1, 1, 60, 1] = float("-inf")
+        perm1, perm2 = P.hausdorff_permutations(2, 300, 400, torch.Generator().manual_seed(6))
+    elif case == "d4":
+        x1 = torch.rand(2, 700, 4, generator=g)
+        x2 = torch.rand(3, 900, 4, generator=g)
+        x2[2, 100, 3] = float("inf")
+    elif case == "d5":
+        x1 = torch.rand(2, 150, 5, generator=g)
+        x2 = torch.rand(3, 90, 5, generator=g)
+        x1[1, 20, 4] = float("nan")
+    elif case == "unsorted_cells":  # batch 1 holds a NaN, batch 0 keeps the pruned path
+        x1 = torch.rand(2, 64, 65537, 2, generator=g)
+        x2 = torch.rand(2, 64, 4, 2, generator=g)
+        x1[1, 5, 1000, 0] = float("nan")
+    return x1, x2, perm1, perm2
+
+
+@pytest.mark.parametrize("case", ["nan_x1", "nan_x2", "nan_x2_last", "inf_x1", "ninf_x2", "nan_cloud", "overflow",
+                                  "overflow_rows", "mixed_d1", "mixed_d2", "batched", "shuffled", "d4", "d5",
+                                  "unsorted_cells"])
+def test_hausdorff_nonfinite_bit_exact(case):
+    """NaN and infinities follow the reference's loop: its early exits compare with NaN, a row
+    whose last s is NaN is not folded, and a row that never improves on +inf carries the
+    previous row's indices.  The pruned kernels cannot reproduce that from the mins alone, so
+    a batch with a value that is not finite (or a pair whose winning min is +inf) takes the
+    loop itself; the values match bit for bit (NaN at the same positions) and so do the
+    indices."""
+    x1, x2, perm1, perm2 = _hd_nonfinite(case)
+    print(case, tuple(x1.shape), tuple(x2.shape), flush=True)
+    dev = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    out, i1, i2 = capi.directed_hausdorff(x1.to(DEV), x2.to(DEV), dev(perm1), dev(perm2))
+    w = cref.directed_hausdorff(x1.numpy(), x2.numpy(), None if perm1 is None else perm1.numpy(),
+                                None if perm2 is None else perm2.numpy(), threads=8)
+    assert_equal(out.cpu(), torch.from_numpy(w[0]), f"{case} value", nan_payload=False)
+    assert_equal(i1.cpu(), torch.from_numpy(w[1]), f"{case} idx1")
+    assert_equal(i2.cpu(), torch.from_numpy(w[2]), f"{case} idx2")
+
+
 def test_hausdorff_counters():
     """The work counters: the kernels evaluate far fewer pairs than brute force, the sorted
     mode's cell scan runs its box tests, the forward of a few clouds is ten launches, and

@@ -27,11 +27,17 @@
 //      its min, and writes sqrt, and the (permuted) indices.
 //
 // Non-negative fp32 bit patterns order like the values, so the packed key orders by
-// (value, m position) exactly.
+// (value, m position) exactly.  That argument needs finite coordinates: with a NaN or an
+// infinity the loop's updates depend on the order of the NaN sums (a row whose last sum is NaN
+// is never folded, and the candidate indices then carry over from earlier rows).  Each batch is
+// therefore checked for values that are not finite while its points are first read, and the
+// pairs of a batch that holds one take the reference's loop in its own order instead
+// (hdx::exact_pair), written over whatever the pruned kernels left.
 #include <algorithm>
 #include <mutex>
 
 #include "common.hpp"
+#include "hausdorff_exact.hpp"
 
 #pragma clang fp contract(off)
 
@@ -152,17 +158,24 @@ __device__ __forceinline__ bool is_seed(const uint32_t *seedm, int64_t pair, int
     return r;
 }
 
-// xs[c][k][pos] = x[c][perm ? perm[batch_of(c)][pos] : pos][k]
+// xs[c][k][pos] = x[c][perm ? perm[batch_of(c)][pos] : pos][k]; a point with a coordinate that
+// is not finite (v - v != 0: NaN or an infinity) sets its batch's word of nonfin (preset to 0).
 __global__ void soa_kernel(const float *__restrict__ x, const int64_t *__restrict__ perm,
                            int64_t clouds, int64_t clouds_per_batch, int64_t p, int d,
-                           float *__restrict__ xs) {
+                           float *__restrict__ xs, uint32_t *__restrict__ nonfin) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= clouds * p) return;
     const int64_t c = t / p, pos = t - c * p;
     const int64_t src = perm ? perm[(c / clouds_per_batch) * p + pos] : pos;
     const float *s = x + (c * p + src) * d;
     float *o = xs + c * d * p + pos;
-    for (int k = 0; k < d; ++k) o[(int64_t)k * p] = s[k];
+    bool bad = false;
+    for (int k = 0; k < d; ++k) {
+        const float v = s[k];
+        bad = bad || !(v - v == 0.0f);
+        o[(int64_t)k * p] = v;
+    }
+    if (bad) atomicOr(&nonfin[c / clouds_per_batch], 1u);
 }
 
 // A signed int that orders like the float (NaN excluded): the bit pattern, with the magnitude
@@ -1509,13 +1522,18 @@ __global__ __launch_bounds__(kThreads) void seed_ball_kernel(
 
 // Final rescan on the cell grid: one wave per pair finds the smallest position n of an x2 point
 // at the winning m's min with a ball query, then writes sqrt of the min and the (permuted)
-// positions of m and n.
+// positions of m and n.  A pair whose batch holds a value that is not finite (nonfin[bb]), or
+// whose winning min is +inf (squared sums that overflow), takes the reference's loop instead
+// (hdx::exact_pair on the inputs as given): its early exits on NaN, and the indices it carries
+// over from an earlier row when a row never improves on +inf, are no property of the mins that
+// pruning could reproduce.
 template <int D>
 __global__ __launch_bounds__(kThreads) void first_ball_kernel(
-    const float *__restrict__ x1, const int64_t *__restrict__ perm1, const int64_t *__restrict__ perm2,
-    const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2, const float *__restrict__ boxes,
-    bool batch_frame, const unsigned long long *__restrict__ keys, int64_t b1, int64_t b2, int64_t p1, int64_t p2,
-    int64_t pairs, float *__restrict__ out, int64_t *__restrict__ idx1, int64_t *__restrict__ idx2,
+    const float *__restrict__ x1, const float *__restrict__ x2, const int64_t *__restrict__ perm1,
+    const int64_t *__restrict__ perm2, const float4 *__restrict__ xs2r, const int32_t *__restrict__ cstart2,
+    const float *__restrict__ boxes, bool batch_frame, const unsigned long long *__restrict__ keys,
+    const uint32_t *__restrict__ nonfin, int64_t b1, int64_t b2, int64_t p1, int64_t p2, int64_t pairs,
+    float *__restrict__ out, int64_t *__restrict__ idx1, int64_t *__restrict__ idx2,
     unsigned long long *__restrict__ counts) {
     const int64_t pair = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     if (pair >= pairs) return;  // the same in every lane
@@ -1523,6 +1541,18 @@ __global__ __launch_bounds__(kThreads) void first_ball_kernel(
     const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
     const int64_t i = rem / b2, j = rem - i * b2;
     const unsigned long long key = keys[pair];
+    if (__builtin_amdgcn_readfirstlane(nonfin[bb]) || __uint_as_float((uint32_t)(key >> 32)) == INFINITY) {
+        float best;
+        int64_t mb, nb;
+        hdx::exact_pair<TPW_F32>(x1 + (bb * b1 + i) * p1 * D, x2 + (bb * b2 + j) * p2 * D, p1, p2, D,
+                                 perm1 ? perm1 + bb * p1 : nullptr, perm2 ? perm2 + bb * p2 : nullptr, best, mb, nb);
+        if ((threadIdx.x & 63) == 0) {
+            out[pair] = sqrt_rn(best);
+            idx1[pair] = mb;
+            idx2[pair] = nb;
+        }
+        return;
+    }
     const int64_t m = (int64_t)(key & 0xffffffffull);
     const float H = __uint_as_float((uint32_t)(key >> 32));
     float fr[2 * D];
@@ -1538,6 +1568,35 @@ __global__ __launch_bounds__(kThreads) void first_ball_kernel(
         idx2[pair] = n < (unsigned long long)p2 ? (perm2 ? perm2[bb * p2 + (int64_t)n] : (int64_t)n) : 0;
     }
     add_counts(counts, evals, 0u);
+}
+
+// The unsorted modes without the cell grid: after the outputs, one wave per pair whose batch
+// holds a value that is not finite (nonfin[bb]), or whose winning min is +inf, overwrites them
+// with the reference's loop (as first_ball_kernel does).
+__global__ __launch_bounds__(kThreads) void exact_fix_kernel(const float *__restrict__ x1, const float *__restrict__ x2,
+                                                             const int64_t *__restrict__ perm1,
+                                                             const int64_t *__restrict__ perm2,
+                                                             const uint32_t *__restrict__ nonfin, int64_t b1,
+                                                             int64_t b2, int64_t p1, int64_t p2, int64_t d,
+                                                             int64_t pairs, float *__restrict__ out,
+                                                             int64_t *__restrict__ idx1, int64_t *__restrict__ idx2,
+                                                             const unsigned long long *__restrict__ keys) {
+    const int64_t pair = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (pair >= pairs) return;  // the same in every lane
+    const int64_t per_batch = b1 * b2;
+    const int64_t bb = pair / per_batch, rem = pair - bb * per_batch;
+    const int64_t i = rem / b2, j = rem - i * b2;
+    if (!__builtin_amdgcn_readfirstlane(nonfin[bb]) && !(__uint_as_float((uint32_t)(keys[pair] >> 32)) == INFINITY))
+        return;
+    float best;
+    int64_t mb, nb;
+    hdx::exact_pair<TPW_F32>(x1 + (bb * b1 + i) * p1 * d, x2 + (bb * b2 + j) * p2 * d, p1, p2, d,
+                             perm1 ? perm1 + bb * p1 : nullptr, perm2 ? perm2 + bb * p2 : nullptr, best, mb, nb);
+    if ((threadIdx.x & 63) == 0) {
+        out[pair] = sqrt_rn(best);
+        idx1[pair] = mb;
+        idx2[pair] = nb;
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1556,13 +1615,16 @@ __global__ __launch_bounds__(kThreads) void first_ball_kernel(
 
 // Block (g, y): rows [y chunk, (y + 1) chunk) of cloud g (x1's clouds, then x2's; rows in input
 // order, which a box does not depend on): part[g][y][k][0..1] = their min and max of coordinate
-// k (NaN ignored, as fminf / fmaxf ignore it; +inf / -inf when there is none).  The grid also
-// writes the presets fs.
+// k (NaN ignored, as fminf / fmaxf ignore it; +inf / -inf when there is none), and bad[g][y] = 1
+// when one of their values is not finite (v - v != 0), else 0.  The grid also writes the
+// presets fs.
 template <int D>
 __global__ __launch_bounds__(kThreads) void prep_kernel(const float *__restrict__ x1, int64_t clouds1, int64_t p1,
                                                         const float *__restrict__ x2, int64_t p2, int64_t chunk,
-                                                        int64_t chunks, float *__restrict__ part, Fills fs) {
+                                                        int64_t chunks, float *__restrict__ part,
+                                                        uint32_t *__restrict__ bad, Fills fs) {
     __shared__ float red[kThreads / 64][2 * D];
+    __shared__ uint32_t red_bad[kThreads / 64];
     const int64_t nthr = (int64_t)gridDim.x * gridDim.y * kThreads;
     const int64_t tid = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * kThreads + threadIdx.x;
     // constant indices only (a dynamically indexed copy of the argument would live in LDS)
@@ -1586,6 +1648,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(const float *__restrict_
         lo[k] = INFINITY;
         hi[k] = -INFINITY;
     }
+    bool nf = false;  // a value that is not finite
     int64_t n = beg + threadIdx.x;
     for (; n + 3 * kThreads < end; n += 4 * kThreads) {  // four rows in flight
         float v[4][D];
@@ -1599,6 +1662,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(const float *__restrict_
             for (int k = 0; k < D; ++k) {
                 lo[k] = fminf(lo[k], v[u][k]);
                 hi[k] = fmaxf(hi[k], v[u][k]);
+                nf = nf || !(v[u][k] - v[u][k] == 0.0f);
             }
     }
     for (; n < end; n += kThreads)
@@ -1607,7 +1671,9 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(const float *__restrict_
             const float v = X[n * D + k];
             lo[k] = fminf(lo[k], v);
             hi[k] = fmaxf(hi[k], v);
+            nf = nf || !(v - v == 0.0f);
         }
+    const bool wave_nf = __ballot(nf) != 0ull;
 #pragma unroll
     for (int k = 0; k < D; ++k)
 #pragma unroll
@@ -1616,12 +1682,14 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(const float *__restrict_
             hi[k] = fmaxf(hi[k], __shfl_xor(hi[k], off, 64));
         }
     const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0)
+    if ((threadIdx.x & 63) == 0) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             red[wave][2 * k] = lo[k];
             red[wave][2 * k + 1] = hi[k];
         }
+        red_bad[wave] = wave_nf ? 1u : 0u;
+    }
     __syncthreads();
     if (threadIdx.x < 2 * D) {
         const int e = threadIdx.x;
@@ -1629,16 +1697,25 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(const float *__restrict_
         for (int w = 1; w < kThreads / 64; ++w) v = (e & 1) ? fmaxf(v, red[w][e]) : fminf(v, red[w][e]);
         part[(g * chunks + blockIdx.y) * 2 * D + e] = v;
     }
+    if (threadIdx.x == 0) {
+        uint32_t b = 0;
+        for (int w = 0; w < kThreads / 64; ++w) b |= red_bad[w];
+        bad[g * chunks + blockIdx.y] = b;
+    }
 }
 
 // Block g < clouds2: x2 cloud g's box bbox2[g][k][0..1] (the seeds' distance) from its chunk
 // partials; block clouds2 + bb: batch bb's box over the partials of its b1 x1 clouds and b2 x2
-// clouds, the cell frame boxb[bb][k][0..1].
+// clouds, the cell frame boxb[bb][k][0..1], and nonfin[bb] = whether any of its chunks holds a
+// value that is not finite.
 template <int D>
-__global__ __launch_bounds__(kThreads) void frames_kernel(const float *__restrict__ part, int64_t clouds1,
+__global__ __launch_bounds__(kThreads) void frames_kernel(const float *__restrict__ part,
+                                                          const uint32_t *__restrict__ bad, int64_t clouds1,
                                                           int64_t clouds2, int64_t b1, int64_t b2, int64_t chunks,
-                                                          float *__restrict__ bbox2, float *__restrict__ boxb) {
+                                                          float *__restrict__ bbox2, float *__restrict__ boxb,
+                                                          uint32_t *__restrict__ nonfin) {
     __shared__ float red[kThreads / 64][2 * D];
+    __shared__ uint32_t red_bad[kThreads / 64];
     const int64_t g = blockIdx.x;
     // partial rows (row = cloud * chunks + y) [r0, r1) and [r2, r3)
     int64_t r0, r1, r2 = 0, r3 = 0;
@@ -1661,15 +1738,19 @@ __global__ __launch_bounds__(kThreads) void frames_kernel(const float *__restric
         lo[k] = INFINITY;
         hi[k] = -INFINITY;
     }
+    uint32_t nf = 0;
     for (int half = 0; half < 2; ++half) {
         const int64_t a = half ? r2 : r0, b = half ? r3 : r1;
-        for (int64_t r = a + threadIdx.x; r < b; r += kThreads)
+        for (int64_t r = a + threadIdx.x; r < b; r += kThreads) {
 #pragma unroll
             for (int k = 0; k < D; ++k) {
                 lo[k] = fminf(lo[k], part[r * 2 * D + 2 * k]);
                 hi[k] = fmaxf(hi[k], part[r * 2 * D + 2 * k + 1]);
             }
+            nf |= bad[r];
+        }
     }
+    const bool wave_nf = __ballot(nf != 0u) != 0ull;
 #pragma unroll
     for (int k = 0; k < D; ++k)
 #pragma unroll
@@ -1678,18 +1759,25 @@ __global__ __launch_bounds__(kThreads) void frames_kernel(const float *__restric
             hi[k] = fmaxf(hi[k], __shfl_xor(hi[k], off, 64));
         }
     const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0)
+    if ((threadIdx.x & 63) == 0) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             red[wave][2 * k] = lo[k];
             red[wave][2 * k + 1] = hi[k];
         }
+        red_bad[wave] = wave_nf ? 1u : 0u;
+    }
     __syncthreads();
     if (threadIdx.x < 2 * D) {
         const int e = threadIdx.x;
         float v = red[0][e];
         for (int w = 1; w < kThreads / 64; ++w) v = (e & 1) ? fmaxf(v, red[w][e]) : fminf(v, red[w][e]);
         dst[e] = v;
+    }
+    if (threadIdx.x == 0 && g >= clouds2) {
+        uint32_t b = 0;
+        for (int w = 0; w < kThreads / 64; ++w) b |= red_bad[w];
+        nonfin[g - clouds2] = b;
     }
 }
 
@@ -2084,12 +2172,12 @@ struct Workspace {
     int32_t *cstart2, *cstT;
     int *boxkeys;
     uint32_t *seedmin, *seedm, *cellhist;
-    uint32_t *flagbits;
+    uint32_t *flagbits, *nonfin, *chunkbad;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// [keys | x2 boxes | x1, x2 SoA (unsorted) | box keys (unsorted) | box partials, batch boxes
+// [keys | non-finite flags per batch, per prep chunk (sorted) | x2 boxes | x1, x2 SoA (unsorted) | box keys (unsorted) | box partials, batch boxes
 //  (sorted) | seeds, candidates, first hits (fast) | x2 records, cell starts (cells; x2's,
 //  then x1's when sorted) | x1 records, x1 cell ranges and boxes, x2 representatives and cell
 //  starts in the cell scan's order, flag bits (sorted) | per-chunk cell histograms
@@ -2104,6 +2192,8 @@ Workspace carve(void *ws, const Plan &P, int64_t p1, int64_t p2, int64_t d, size
     const bool uns = !P.sorted;
     Workspace w;
     w.keys = reinterpret_cast<unsigned long long *>(take(true, 8 * P.pairs));
+    w.nonfin = reinterpret_cast<uint32_t *>(take(P.active, 4 * P.batch));
+    w.chunkbad = reinterpret_cast<uint32_t *>(take(P.sorted, 4 * (P.clouds1 + P.clouds2) * P.prep_chunks));
     w.bbox = reinterpret_cast<float *>(take(true, 4 * P.clouds2 * d * 2));
     w.xs1 = reinterpret_cast<float *>(take(uns, 4 * P.clouds1 * p1 * d));
     w.xs2 = reinterpret_cast<float *>(take(uns, 4 * P.clouds2 * p2 * d));
@@ -2187,9 +2277,9 @@ int launch_sorted(const Plan &P, const Workspace &w, const float *x1, const floa
     fs.f[fs.count++] = Fill{reinterpret_cast<uint32_t *>(w.keys), 2 * P.pairs, {0u, 0u}};
     fs.f[fs.count++] = Fill{w.flagbits, P.pairs * cdiv(p1, 32), {0u, 0u}};
     HD_LAUNCH(prep_kernel<D>, dim3((unsigned)(P.clouds1 + P.clouds2), (unsigned)P.prep_chunks), dim3(kThreads), 0,
-              s, x1, P.clouds1, p1, x2, p2, P.prep_chunk, P.prep_chunks, w.part, fs);
-    HD_LAUNCH(frames_kernel<D>, dim3((unsigned)(P.clouds2 + P.batch)), dim3(kThreads), 0, s, w.part, P.clouds1,
-              P.clouds2, b1, b2, P.prep_chunks, w.bbox, w.boxb);
+              s, x1, P.clouds1, p1, x2, p2, P.prep_chunk, P.prep_chunks, w.part, w.chunkbad, fs);
+    HD_LAUNCH(frames_kernel<D>, dim3((unsigned)(P.clouds2 + P.batch)), dim3(kThreads), 0, s, w.part, w.chunkbad,
+              P.clouds1, P.clouds2, b1, b2, P.prep_chunks, w.bbox, w.boxb, w.nonfin);
     int rc = check_launch("hausdorff frames");
     if (rc) return rc;
     const CellSet S2{x2, perm2, w.xs2r, w.boxb, P.clouds2, p2, b2, b2};
@@ -2208,8 +2298,9 @@ int launch_sorted(const Plan &P, const Workspace &w, const float *x1, const floa
               w.xs2r, w.cstT, w.info1, w.rep2, P.clouds2, b1, b2, p1, p2, w.seedm, w.keys, w.flagbits, counts);
     HD_LAUNCH(scan_flagged_kernel<D>, dim3((unsigned)(cdiv(p1, 32 * kThreads) * P.pairs)), dim3(kThreads), 0, s, x1,
               perm1, w.xs2r, w.cstart2, w.boxb, P.clouds2, b1, b2, p1, p2, w.keys, w.flagbits, counts);
-    HD_LAUNCH(first_ball_kernel<D>, dim3((unsigned)cdiv(P.pairs, kThreads / 64)), dim3(kThreads), 0, s, x1, perm1,
-              perm2, w.xs2r, w.cstart2, w.boxb, true, w.keys, b1, b2, p1, p2, P.pairs, out, idx1, idx2, counts);
+    HD_LAUNCH(first_ball_kernel<D>, dim3((unsigned)cdiv(P.pairs, kThreads / 64)), dim3(kThreads), 0, s, x1, x2,
+              perm1, perm2, w.xs2r, w.cstart2, w.boxb, true, w.keys, w.nonfin, b1, b2, p1, p2, P.pairs, out, idx1,
+              idx2, counts);
     return check_launch("hausdorff scan");
 }
 
@@ -2255,8 +2346,9 @@ int launch_fast(const Plan &P, const Workspace &w, const float *x1, const float 
             HD_LAUNCH(scan_window_kernel<D>, dim3((unsigned)cdiv(p1, m_per_block), (unsigned)P.pairs),
                       dim3(kThreads), 0, s, w.xs1, w.xs2r, w.cstart2, w.bbox, b1, b2, p1, p2, m_per_block, w.seedm,
                       w.keys, counts);
-            HD_LAUNCH(first_ball_kernel<D>, dim3(per_wave_blocks), dim3(kThreads), 0, s, x1, perm1, perm2, w.xs2r,
-                      w.cstart2, w.bbox, false, w.keys, b1, b2, p1, p2, P.pairs, out, idx1, idx2, counts);
+            HD_LAUNCH(first_ball_kernel<D>, dim3(per_wave_blocks), dim3(kThreads), 0, s, x1, x2, perm1, perm2,
+                      w.xs2r, w.cstart2, w.bbox, false, w.keys, w.nonfin, b1, b2, p1, p2, P.pairs, out, idx1, idx2,
+                      counts);
         }
     }
     if (!cells) {
@@ -2268,6 +2360,8 @@ int launch_fast(const Plan &P, const Workspace &w, const float *x1, const float 
                   w.keys, b1, b2, p1, p2, P.chunk2, w.first);
         HD_LAUNCH(write_out_kernel, dim3((unsigned)cdiv(P.pairs, 256)), dim3(256), 0, s, w.keys, w.first, perm1,
                   perm2, P.pairs, b1, b2, p1, p2, out, idx1, idx2);
+        HD_LAUNCH(exact_fix_kernel, dim3(per_wave_blocks), dim3(kThreads), 0, s, x1, x2, perm1, perm2, w.nonfin, b1,
+                  b2, p1, p2, (int64_t)D, P.pairs, out, idx1, idx2, w.keys);
     }
     return check_launch("hausdorff scan");
 }
@@ -2340,7 +2434,7 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
             default: return launch_sorted<3>(P, w, x1, x2, b1, p1, b2, p2, perm1, perm2, out, idx1, idx2, s);
         }
     }
-    // presets: keys 0, box keys (+inf, -inf), seed mins +inf, first hits all ones
+    // presets: keys 0, non-finite flags 0, box keys (+inf, -inf), seed mins +inf, first hits all ones
     Fills fs{};
     int64_t most = 0;
     auto add = [&](void *ptr, int64_t words, uint32_t v0, uint32_t v1) {
@@ -2349,6 +2443,7 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
         most = std::max(most, words);
     };
     add(w.keys, 2 * pairs, 0u, 0u);
+    add(w.nonfin, batch, 0u, 0u);
     add(w.boxkeys, 2 * P.box_rows2, kOrderedPosInf, kOrderedNegInf);
     add(w.seedmin, pairs * kSeeds, 0x7f800000u, 0x7f800000u);
     add(w.first, 2 * pairs, 0xffffffffu, 0xffffffffu);
@@ -2357,9 +2452,9 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     if (rc) return rc;
     if (P.active) {
         HD_LAUNCH(soa_kernel, dim3((unsigned)cdiv(batch * b1 * p1, 256)), dim3(256), 0, s, x1, perm1, batch * b1, b1,
-                  p1, (int)d, w.xs1);
+                  p1, (int)d, w.xs1, w.nonfin);
         HD_LAUNCH(soa_kernel, dim3((unsigned)cdiv(batch * b2 * p2, 256)), dim3(256), 0, s, x2, perm2, batch * b2, b2,
-                  p2, (int)d, w.xs2);
+                  p2, (int)d, w.xs2, w.nonfin);
         HD_LAUNCH(bbox_rows_kernel, dim3((unsigned)P.box_rows2, (unsigned)P.box_chunks), dim3(kThreads), 0, s,
                   w.xs1, (int64_t)0, p1, w.xs2, p2, P.box_chunk, w.boxkeys);
         HD_LAUNCH(box_finish_kernel, dim3((unsigned)cdiv(P.box_rows2, 256)), dim3(256), 0, s, w.boxkeys,
@@ -2384,6 +2479,9 @@ extern "C" int tpw_directed_hausdorff(const float *x1, const float *x2, int64_t 
     }
     HD_LAUNCH(finalize_kernel<0>, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads), 0, s, w.xs1, w.xs2,
               w.keys, perm1, perm2, pairs, b1, b2, p1, p2, (int)d, out, idx1, idx2);
+    if (P.active)
+        HD_LAUNCH(exact_fix_kernel, dim3((unsigned)cdiv(pairs, kThreads / 64)), dim3(kThreads), 0, s, x1, x2, perm1,
+                  perm2, w.nonfin, b1, b2, p1, p2, d, pairs, out, idx1, idx2, w.keys);
     return check_launch("hausdorff finalize_kernel");
 }
 

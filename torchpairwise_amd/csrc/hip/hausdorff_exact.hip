@@ -1,31 +1,12 @@
 // Directed Hausdorff distance for float64 and float16 (and float32, where it cross-checks the
 // pruned cell-grid pipeline of hausdorff.hip): the reference's loop
 // (cpu/hausdorff_kernel.cpp:12-100, cuda/hausdorff_kernel.cu:16-105) executed in its own order,
-// one wave per cloud pair:
-//
-//   best = 0
-//   for m in (shuffled) order:                       row_min = inf
-//       for n in (shuffled) order:                   s = sum_k (x1[m,k] - x2[n,k])^2
-//           if s < best: break                       (early exit: this m cannot raise best)
-//           if s < row_min: row_min = s, (m_c, n_c) = (m, n)
-//       if row_min >= best and s >= best: best = row_min, (m_best, n_best) = (m_c, n_c)
-//   out = sqrt(best), indices (m_best, n_best)
-//
-// The wave takes the n loop 64 points at a time: each lane forms one point's s, a ballot finds
-// the first lane that breaks, and the strict running minimum over the lanes before it is the
-// chunk's minimum with its first lane, which is what the sequential loop records.  The state
-// (best, row_min, the last s, the candidate indices, which carry over from one m to the next as
-// in the loop) is the same in every lane.  So outputs and indices equal the CPU loop's bit for
-// bit, ties, NaN and overflowing sums included.
-//
-// Arithmetic follows the element type as c10 does: double in double, float in float, and half
-// with every difference, square and sum computed in float and rounded to half (c10::Half's
-// operators).  Contraction is off in this file.
+// one wave per cloud pair (exact_pair, hausdorff_exact.hpp).
 //
 // The backward follows the CPU loop too (cpu/hausdorff_kernel.cpp:187-235): one thread per
 // (cloud, k) owns that feature column of its cloud's gradient and adds g * diff / out for every
 // cloud pair in order, so there are no atomics and the sums are the loop's.
-#include "common.hpp"
+#include "hausdorff_exact.hpp"
 
 #include <math.h>
 
@@ -34,47 +15,7 @@
 namespace tpw {
 namespace {
 
-// Element arithmetic of each dtype: load to the accumulation type, and round a result as the
-// element type would hold it.
-template <int DT>
-struct HdT;
-template <>
-struct HdT<TPW_F64> {
-    using S = double;
-    using A = double;
-    static __device__ __forceinline__ A ld(S v) { return v; }
-    static __device__ __forceinline__ A rn(A v) { return v; }
-    static __device__ __forceinline__ S st(A v) { return v; }
-    static __device__ __forceinline__ A root(A v) { return sqrt(v); }
-};
-template <>
-struct HdT<TPW_F32> {
-    using S = float;
-    using A = float;
-    static __device__ __forceinline__ A ld(S v) { return v; }
-    static __device__ __forceinline__ A rn(A v) { return v; }
-    static __device__ __forceinline__ S st(A v) { return v; }
-    static __device__ __forceinline__ A root(A v) { return sqrt_rn(v); }
-};
-template <>
-struct HdT<TPW_F16> {
-    using S = _Float16;
-    using A = float;
-    static __device__ __forceinline__ A ld(S v) { return (float)v; }
-    static __device__ __forceinline__ A rn(A v) { return (float)(_Float16)v; }
-    static __device__ __forceinline__ S st(A v) { return (_Float16)v; }
-    static __device__ __forceinline__ A root(A v) { return sqrt_rn(v); }
-};
-
-template <typename A>
-__device__ __forceinline__ A wave_min(A v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const A o = __shfl_xor(v, off, 64);
-        v = o < v ? o : v;
-    }
-    return v;
-}
+using hdx::HdT;
 
 template <int DT>
 __global__ __launch_bounds__(256) void hd_exact_kernel(
@@ -83,52 +24,14 @@ __global__ __launch_bounds__(256) void hd_exact_kernel(
     const int64_t *__restrict__ perm2, typename HdT<DT>::S *__restrict__ out, int64_t *__restrict__ idx1,
     int64_t *__restrict__ idx2) {
     using H = HdT<DT>;
-    using A = typename H::A;
     const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (pair >= pairs) return;  // the whole wave leaves together
     const int64_t j = pair % b2, i = (pair / b2) % b1, bb = pair / (b1 * b2);
-    const typename H::S *P = x1 + (bb * b1 + i) * p1 * d, *Q = x2 + (bb * b2 + j) * p2 * d;
-    const A inf = (A)INFINITY;
-    A best = 0, s_last = 0;
-    int64_t m_best = 0, n_best = 0, m_c = 0, n_c = 0;
-    for (int64_t mp = 0; mp < p1; ++mp) {
-        const int64_t mi = perm1 ? perm1[bb * p1 + mp] : mp;
-        const typename H::S *u = P + mi * d;
-        A row_min = inf;
-        for (int64_t base = 0; base < p2; base += 64) {
-            const int64_t np = base + lane;
-            const bool act = np < p2;
-            const int64_t ni = act ? (perm2 ? perm2[bb * p2 + np] : np) : 0;
-            const typename H::S *v = Q + ni * d;
-            A s = 0;
-            for (int64_t k = 0; k < d; ++k) {
-                const A diff = H::rn(H::ld(u[k]) - H::ld(v[k]));
-                s = H::rn(s + H::rn(diff * diff));
-            }
-            const uint64_t brk = __ballot(act && s < best);
-            const int nact = p2 - base < 64 ? (int)(p2 - base) : 64;
-            const int limit = brk ? __builtin_ctzll(brk) : nact;
-            // candidates: the lanes the loop reaches whose s improves on the row's minimum; the
-            // chunk's smallest candidate, first lane on ties, is the loop's last strict update
-            const bool cand = lane < limit && s < row_min;
-            const A cmin = wave_min(cand ? s : inf);
-            if (cmin < row_min) {
-                const uint64_t hit = __ballot(cand && s == cmin);
-                const int fl = __builtin_ctzll(hit);
-                row_min = cmin;
-                m_c = mi;
-                n_c = __shfl(ni, fl, 64);
-            }
-            s_last = __shfl(s, brk ? limit : nact - 1, 64);
-            if (brk) break;
-        }
-        if (row_min >= best && s_last >= best) {
-            best = row_min;
-            m_best = m_c;
-            n_best = n_c;
-        }
-    }
+    typename H::A best;
+    int64_t m_best, n_best;
+    hdx::exact_pair<DT>(x1 + (bb * b1 + i) * p1 * d, x2 + (bb * b2 + j) * p2 * d, p1, p2, d,
+                        perm1 ? perm1 + bb * p1 : nullptr, perm2 ? perm2 + bb * p2 : nullptr, best, m_best, n_best);
     if (lane == 0) {
         out[pair] = H::st(H::root(best));
         idx1[pair] = m_best;

@@ -141,6 +141,35 @@ __device__ __forceinline__ float epilogue(float s, float a1, float a2, const Ker
     }
 }
 
+// bf16 cosine-family outputs: where every norm of a tile lies in [2^-60, 2^60] (so each n1 n2 is
+// a normal nonzero float and the quotient branch above applies), q = s r1 r2 from the rows' and
+// columns' reciprocals r = RN(1 / norm) instead of an IEEE divide per element: within 2 ulp of
+// the quotient before the output's bf16 rounding (2^-9).  Tiles with another norm (zero
+// included) keep epilogue<>.
+template <int EPI, typename OutT>
+constexpr bool kCosRcp = sizeof(OutT) == 2 && (EPI == TPW_EPI_COSINE_SIM || EPI == TPW_EPI_COSINE_DIST ||
+                                               EPI == TPW_EPI_CORRELATION);
+
+template <int EPI>
+__device__ __forceinline__ float cos_epilogue_rcp(float s, float r1, float r2) {
+#pragma clang fp contract(off)
+    const float q = s * (r1 * r2);
+    if constexpr (EPI == TPW_EPI_COSINE_SIM) return q;
+    const float v = 1.0f - q;
+    if constexpr (EPI == TPW_EPI_CORRELATION) return v;
+    return fminf(fmaxf(v, 0.0f), 2.0f);
+}
+
+// The tile's 256 norms (rows, then columns; thread t owns entry t) replaced by their reciprocals
+// when all of them lie in [2^-60, 2^60]; whether they were (the same in every thread).
+__device__ __forceinline__ bool cos_norms_to_rcp(float *s_aux, int tid) {
+    const float v = s_aux[tid];
+    if (!__syncthreads_and(v >= 0x1p-60f && v <= 0x1p60f)) return false;
+    s_aux[tid] = __fdiv_rn(1.0f, v);
+    __syncthreads();
+    return true;
+}
+
 // Selection order of the neighbour masks: ascending distance (distances are >= 0 or -0; -0 ==
 // +0, NaN after +inf), then ascending column.  Columns past the edge take the largest key.
 __device__ __forceinline__ uint64_t topk_key(float v, uint32_t col) {
@@ -368,6 +397,14 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
         __syncthreads();
     }
 
+    bool rcp = false;  // bf16 cosine family: s_aux holds reciprocals
+    if constexpr (kCosRcp<EPI, OutT>) rcp = cos_norms_to_rcp(&s_aux[0][0], tid);
+    // the output value of accumulator s
+    auto value = [&](float s, float a1, float a2) {
+        if constexpr (kCosRcp<EPI, OutT>)
+            if (rcp) return cos_epilogue_rcp<EPI>(s, a1, a2);
+        return epilogue<EPI>(s, a1, a2, kp);
+    };
     // Accumulator layout of the 32 x 32 MFMA: register r of lane l holds
     // row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
     const bool full = row0 + kTile <= n && col0 + kTile <= m;
@@ -399,7 +436,7 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
                         const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
                         const float a1 = a1q[r >> 2][r & 3];
                         stage[rr * kStageStride + ni * 32 + l32] =
-                            EPI == kEpiGrad ? sign * acc[mi][ni][r] : epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni], kp);
+                            EPI == kEpiGrad ? sign * acc[mi][ni][r] : value(acc[mi][ni][r], a1, a2v[ni]);
                     }
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
                 __builtin_amdgcn_wave_barrier();
@@ -462,7 +499,7 @@ __global__ __launch_bounds__(kThreads, 2) void pairwise_inner_kernel(
                 const int rr = mi * 32 + 8 * (r >> 2) + (r & 3);  // row in the wave tile, less 4 h
                 const float a1 = kAux1<EPI> ? s_aux[0][wr + 4 * h + rr] : 0.0f;
                 if (full || (row0 + wr + 4 * h + rr < n && col_ok)) {
-                    float v = epilogue<EPI>(acc[mi][ni][r], a1, a2v[ni], kp);
+                    float v = value(acc[mi][ni][r], a1, a2v[ni]);
                     if constexpr (EPI == kEpiGrad) v = sign * v + a1 * to_f32(X[(obase - out) + rr * m + ni * 32]);
                     store_out(obase + rr * m + ni * 32, v);
                 }
@@ -569,6 +606,8 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
         }
     }
     barrier_lds();  // the operand buffer becomes the output stage
+    bool rcp = false;  // bf16 cosine family: s_aux holds reciprocals
+    if constexpr (kCosRcp<EPI, OutT>) rcp = cos_norms_to_rcp(s_aux, tid);
 
     float a1v[2];
 #pragma unroll
@@ -654,6 +693,13 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
             } else {
                 const floatx4 a2 = kAux2<EPI> ? *reinterpret_cast<const floatx4 *>(&s_aux[kT + wc + ni * 32 + 8 * g + 4 * h])
                                               : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (kCosRcp<EPI, OutT>) {
+                    if (rcp) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[e] = cos_epilogue_rcp<EPI>(acc[mi][ni][4 * g + e], a1v[mi], a2[e]);
+                        return o;
+                    }
+                }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) o[e] = epilogue<EPI>(acc[mi][ni][4 * g + e], a1v[mi], a2[e], kp);
             }

@@ -131,6 +131,38 @@ __device__ __forceinline__ void weight_terms(float gv, float av, float nv, float
     }
 }
 
+// The output-based cosine terms for a pair whose norms both lie in [2^-60, 2^60] (so den = n1 n2
+// is a normal nonzero float and weight_terms takes its quotient branch), from the reciprocals
+// r1 = RN(1 / n1), r2 = RN(1 / n2): gS = gq r1 r2, rt = gden n2 = -gq q r1, ct = gden n1 =
+// -gq q r2.  Within 2 ulp of weight_terms's values (which divide by the rounded n1 n2), with
+// seven VALU operations against its twenty and a reciprocal.
+template <int MODE>
+__device__ __forceinline__ void cos_terms_fast(float gv, float av, float r1, float r2, float &w, float &rt,
+                                               float &ct) {
+#pragma clang fp contract(off)
+    const float q = MODE == kCosSimO ? av : 1.0f - av;
+    float gq = MODE == kCosSimO ? gv : -gv;
+    if constexpr (MODE == kCosDistO) gq = (av > 0.0f && av < 2.0f) ? gq : 0.0f;
+    const float t = gq * q;
+    w = gq * (r1 * r2);
+    rt = -(t * r1);
+    ct = -(t * r2);
+}
+
+// Norms in [2^-60, 2^60] (NaN excluded): the pairs of two such rows take cos_terms_fast.
+__device__ __forceinline__ bool cos_norm_fast(float v) { return v >= 0x1p-60f && v <= 0x1p60f; }
+
+// rn2[t] = RN(1 / n2[t]); *slow |= 1 when one of the len1 + len2 norms n1, n2 lies outside
+// [2^-60, 2^60] (*slow preset to 0; one atomic per wave that finds one).
+__global__ void cos_norm_prep_kernel(const float *__restrict__ n1, int64_t len1, const float *__restrict__ n2,
+                                     int64_t len2, float *__restrict__ rn2, uint32_t *__restrict__ slow) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool in = t < len1 + len2;
+    const float v = !in ? 1.0f : t < len1 ? n1[t] : n2[t - len1];
+    if (in && t >= len1) rn2[t - len1] = __fdiv_rn(1.0f, v);
+    if (__ballot(!cos_norm_fast(v)) != 0ull && (threadIdx.x & 63) == 0) atomicOr(slow, 1u);
+}
+
 // Pass 1.  W (type T: fp32, or bf16 rounded as the reference's bf16 autograd rounds its
 // ratio tensor) is written [n, m] to Wo and, when WTo is given, transposed [m, n] to WTo,
 // so that both gradient products read their operands k-contiguous.  The row / column sums
@@ -679,11 +711,13 @@ int run_gemm(const float *A, const T *B, int64_t batch, int64_t M, int64_t N, in
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct BwdWs {
-    float *S, *rowpart, *colpart, *coef1, *coef2, *part;
+    float *S, *rowpart, *colpart, *coef1, *coef2, *part, *rn2;
+    uint32_t *slow;
     void *W, *WT, *x1t, *x2t;  // element type of the inputs
 };
 
-// [S fp32 (cosine) | row partials | column partials | coef1 | coef2 | W | W^T | x1^T | x2^T |
+// [S fp32 (cosine) | row partials | column partials | coef1 | coef2 | column reciprocals and
+// the norm-range flag (fused fp32 cosine) | W | W^T | x1^T | x2^T |
 // GEMM split partials], W and the transposes in the inputs' element type (sized for fp32;
 // the fp32 path uses W and the split partials, the bf16 path W, W^T and the transposes).
 BwdWs carve(void *ws, int64_t batch, int64_t n, int64_t m, int64_t d, size_t *total = nullptr) {
@@ -699,9 +733,13 @@ BwdWs carve(void *ws, int64_t batch, int64_t n, int64_t m, int64_t d, size_t *to
     // halves of 128 x 128 tiles, whichever are more
     const int64_t tjp = cdiv(m, kPWCols) > 2 * cdiv(m, 128) ? cdiv(m, kPWCols) : 2 * cdiv(m, 128);
     w.rowpart = reinterpret_cast<float *>(take(sizeof(float) * batch * tjp * n));
-    w.colpart = reinterpret_cast<float *>(take(sizeof(float) * batch * 2 * cdiv(n, 128) * m));
+    // column partials: two per 128 x 128 tile (the cosine tile kernel), four per 128-row block
+    // (the fused fp32 cosine kernel), or one per weight-pass tile
+    w.colpart = reinterpret_cast<float *>(take(sizeof(float) * batch * 4 * cdiv(n, 128) * m));
     w.coef1 = reinterpret_cast<float *>(take(sizeof(float) * batch * n));
     w.coef2 = reinterpret_cast<float *>(take(sizeof(float) * batch * m));
+    w.rn2 = reinterpret_cast<float *>(take(sizeof(float) * batch * m));
+    w.slow = reinterpret_cast<uint32_t *>(take(sizeof(uint32_t)));
     w.W = take(sizeof(float) * batch * n * m);
     w.WT = take(sizeof(float) * batch * n * m);
     w.x1t = take(sizeof(float) * batch * n * d);
@@ -742,8 +780,8 @@ __global__ void zero_words_kernel(uint16_t *__restrict__ p, int64_t len) {
     if (t < len) p[t] = 0;
 }
 
-// Weight pass and grad_x1 product in one kernel (fp32; the modes whose row terms are the
-// weights themselves or zero: euclidean, sqeuclidean, polynomial, sigmoid).  A block owns a
+// Weight pass and grad_x1 product in one kernel (fp32; euclidean, sqeuclidean, polynomial,
+// sigmoid, and the output-based cosine modes).  A block owns a
 // 128 x 256 tile of grad_x1 = sign * W . x2 + coef1 * x1, K = m in 32-column chunks: grad
 // (and res / S) of the tile's rows travel by DMA into k-contiguous panels (tile_mfma.hpp's
 // layout), x2's chunk (32 rows x 256 columns, k-major) into a third panel.  Wave w owns rows
@@ -753,6 +791,12 @@ __global__ void zero_words_kernel(uint16_t *__restrict__ p, int64_t len) {
 // lane in K order (each lane sums its half of every chunk; the halves are added at the end).
 // The weights of step q + 1 are formed while step q's products run.  One 64 KiB buffer, two
 // blocks per CU.
+// The cosine modes read the forward's output as the second panel and the norms: the lane's row
+// norm n1 once, the chunk's 32 column norms n2 with the chunk's DMA.  Their row terms divide by
+// n1 at the end (coef1 = sum_j rt / n1, 0 where n1 = 0, as reduce_parts_kernel does), and their
+// column terms ct are summed per chunk over each wave's 32 rows (a butterfly over the lanes) and
+// written as partials colpart[b][4 tr + wave][j] (column blocks tc > 0 repeat the same weights
+// and write none); reduce_parts_kernel adds the 4 cdiv(n, 128) partials in order for coef2.
 constexpr int kFCols = 256;
 
 // The fused grad_x1 kernels own a 128 x 256 tile of grad_x1 ([n, d]) and loop over all of m,
@@ -763,13 +807,23 @@ constexpr int kFCols = 256;
 bool fused_grid_fills(int64_t batch, int64_t n, int64_t m, int64_t d) {
     return cdiv(n, tile::kT) * cdiv(d, kFCols) * batch >= 2 * device_cus() && tile_grid_fills(batch, m, d);
 }
-template <int MODE>
+template <int MODE, bool FAST = false>
 __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
     const float *__restrict__ g, const float *__restrict__ av, const float *__restrict__ x2,
     const float *__restrict__ x1, int64_t n, int64_t m, int64_t d, float *__restrict__ W, float *__restrict__ gx1,
-    int64_t tiles_n, int64_t tiles_c, int64_t total, KerParams kp, float sign) {
+    int64_t tiles_n, int64_t tiles_c, int64_t total, KerParams kp, float sign, const float *__restrict__ n1,
+    const float *__restrict__ n2, float *__restrict__ colpart, const float *__restrict__ rn2,
+    const uint32_t *__restrict__ slow) {
     using namespace tile;
-    constexpr bool kAv = MODE == kEuclid || MODE == kSigmoid || MODE == kPoly;
+    constexpr bool kCos = kCosO<MODE>;
+    // column terms summed into partials: cosine's gden n1, and the weights themselves for
+    // euclidean / sqeuclidean (coef2 = sum_i W)
+    constexpr bool kColT = kCos || MODE == kEuclid || MODE == kSqEuclid;
+    // the cosine pair of launches: the FAST instance runs when every norm lies in [2^-60, 2^60],
+    // the other one otherwise (the flag is the same for every block)
+    if constexpr (kCos)
+        if ((__builtin_amdgcn_readfirstlane(*slow) != 0u) == FAST) return;
+    constexpr bool kAv = MODE == kEuclid || MODE == kSigmoid || MODE == kPoly || kCos;
     __shared__ uint4 smem[4 * kPanel];  // grad | res or S | x2 (two panels)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -810,6 +864,10 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
     const int64_t wrow = row0 + r < n ? row0 + r : n - 1;
     float *Wrow = W + (b * n + wrow) * m;
     const uint4 *Gs = smem, *As = smem + kPanel, *Bs = smem + 2 * kPanel;
+    const float a1 = kCos ? n1[b * n + wrow] : 0.0f;  // the lane's row norm
+    const float r1 = kCos && FAST ? __fdiv_rn(1.0f, a1) : 0.0f;
+    // the lane's 16 column norms (reciprocals for FAST) and column terms of the chunk (K = 16 h + v)
+    floatx16 n2c, ctv;
     // the weights of the lane's piece at step q of the chunk (K = 16 h + 4 q + e), and their row
     // terms into rsum (vector types, not arrays: an array here is placed in LDS by the compiler)
     auto weights = [&](int q) {
@@ -817,15 +875,49 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
         const floatx4 gv = __builtin_bit_cast(floatx4, piece(Gs, r, c));
         const floatx4 avv = kAv ? __builtin_bit_cast(floatx4, piece(As, r, c)) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         floatx4 w;
+        if constexpr (MODE == kEuclid) {
+            // g / res by the reciprocal without fast_div's branch per pair: one test of the
+            // piece's four quotients, and fast_div itself (weight_terms) when one of them has a
+            // denominator outside [2^-126, 2^126] other than 0, inf and NaN (where the product
+            // with the reciprocal is already the quotient; the forward's res never is)
+            bool odd = false;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ay = __builtin_fabsf(avv[e]);
+                odd = odd || (ay < 0x1p-126f && ay != 0.0f) || (ay > 0x1p126f && ay != __builtin_inff());
+                w[e] = avv[e] == 0.0f ? 0.0f : gv[e] * __builtin_amdgcn_rcpf(avv[e]);
+            }
+            if (__builtin_expect(__ballot(odd) != 0ull, 0)) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float we, rt, ct;
+                    weight_terms<MODE, false>(gv[e], avv[e], 0.0f, 0.0f, kp, we, rt, ct);
+                    w[e] = we;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                rsum += w[e];
+                ctv[4 * q + e] = w[e];
+            }
+            return w;
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float we, rt, ct;
-            weight_terms<MODE, false>(gv[e], avv[e], 0.0f, 0.0f, kp, we, rt, ct);
+            if constexpr (kCos && FAST) cos_terms_fast<MODE>(gv[e], avv[e], r1, n2c[4 * q + e], we, rt, ct);
+            else weight_terms<MODE, false>(gv[e], avv[e], a1, kCos ? n2c[4 * q + e] : 0.0f, kp, we, rt, ct);
             w[e] = we;
             rsum += rt;
+            if constexpr (kColT) ctv[4 * q + e] = ct;
         }
         return w;
     };
+    // column partials: only the first column block, and zeros for a wave past the last row (n is
+    // a multiple of 32, so a wave's rows are all valid or all past the end)
+    const bool col_writer = tc == 0;
+    const bool rows_ok = row0 + wr < n;
+    float *cp = kColT ? colpart + (b * 4 * tiles_n + 4 * tr + wave) * m : nullptr;
     const int nchunks = (int)(m / 32);
     for (int kc = 0; kc < nchunks; ++kc) {
         if (kc > 0) barrier_lds();  // every wave is done with chunk kc - 1
@@ -837,6 +929,15 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
                                       : first < 2 * kPanel ? AV + (int64_t)kc * 128
                                                            : X2 + (int64_t)kc * 128 * d;
                 dma16(base, off[j], lds_addr(smem + first));
+            }
+        }
+        if constexpr (kCos) {
+            const floatx4 *np = reinterpret_cast<const floatx4 *>((FAST ? rn2 : n2) + b * m + (int64_t)kc * 32 + 16 * h);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const floatx4 v = np[q];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) n2c[4 * q + e] = v[e];
             }
         }
         barrier_all();
@@ -867,9 +968,38 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
                 }
             }
         }
+        if constexpr (kColT) {
+            // the chunk's column terms summed over the wave's 32 rows (lanes of equal h): each
+            // step hands half of the lane's values to its partner; lane (l32, h) ends with
+            // column 16 h + (l32 >> 1), in both lanes of a pair
+            float t8[8], t4[4], t2[2];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const bool up = (l32 & 16) != 0;
+                const float mine = up ? ctv[8 + i] : ctv[i], other = up ? ctv[i] : ctv[8 + i];
+                t8[i] = mine + __shfl_xor(other, 16, 64);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool up = (l32 & 8) != 0;
+                const float mine = up ? t8[4 + i] : t8[i], other = up ? t8[i] : t8[4 + i];
+                t4[i] = mine + __shfl_xor(other, 8, 64);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const bool up = (l32 & 4) != 0;
+                const float mine = up ? t4[2 + i] : t4[i], other = up ? t4[i] : t4[2 + i];
+                t2[i] = mine + __shfl_xor(other, 4, 64);
+            }
+            const bool up2 = (l32 & 2) != 0;
+            float t1 = (up2 ? t2[1] : t2[0]) + __shfl_xor(up2 ? t2[0] : t2[1], 2, 64);
+            t1 += __shfl_xor(t1, 1, 64);
+            if (col_writer && (l32 & 1) == 0) cp[(int64_t)kc * 32 + 16 * h + (l32 >> 1)] = rows_ok ? t1 : 0.0f;
+        }
     }
     barrier_lds();  // the buffer becomes the output stage
-    const float a1v = rsum + __shfl_xor(rsum, 32, 64);  // both K halves
+    float a1v = rsum + __shfl_xor(rsum, 32, 64);  // both K halves
+    if constexpr (kCos) a1v = a1 == 0.0f ? 0.0f : __fdiv_rn(a1v, a1);
     floatx4 *sl = reinterpret_cast<floatx4 *>(smem) + wave * 1024;  // 16 KiB per wave
 #pragma unroll
     for (int half = 0; half < 2; ++half)
@@ -953,6 +1083,31 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
         const uint4 ap = kAv ? piece(As, r, c) : make_uint4(0, 0, 0, 0);
         const uint32_t gw[4] = {gp.x, gp.y, gp.z, gp.w}, aw[4] = {ap.x, ap.y, ap.z, ap.w};
         uint32_t o[4];
+        if constexpr (MODE == kEuclid) {
+            // as the fp32 kernel: the reciprocal without a branch per pair, one test of the
+            // piece's eight quotients (weight_terms below when one has a denominator outside
+            // [2^-126, 2^126] other than 0, inf and NaN); each weight rounded to bf16 once and
+            // summed as rounded
+            bool odd = false;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float wv[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const float gvv = __uint_as_float(u ? gw[e] & 0xffff0000u : gw[e] << 16);
+                    const float avv = __uint_as_float(u ? aw[e] & 0xffff0000u : aw[e] << 16);
+                    const float ay = __builtin_fabsf(avv);
+                    odd = odd || (ay < 0x1p-126f && ay != 0.0f) || (ay > 0x1p126f && ay != __builtin_inff());
+                    wv[u] = avv == 0.0f ? 0.0f : gvv * __builtin_amdgcn_rcpf(avv);
+                }
+                o[e] = f32x2_to_bf16x2_rne(wv[0], wv[1]);
+            }
+            if (!__builtin_expect(__ballot(odd) != 0ull, 0)) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rsum += __uint_as_float(o[e] << 16) + __uint_as_float(o[e] & 0xffff0000u);
+                return make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             // rt: the rounded weight for euclidean / sqeuclidean (BF16W), 0 for the kernel functions
@@ -1254,16 +1409,52 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
             const float sign = (MODE == kPoly || MODE == kSigmoid) ? 1.0f : -1.0f;
             const int64_t tiles_n = cdiv(n, tile::kT), tiles_c = cdiv(d, kFCols), total = tiles_n * tiles_c * batch;
             hipLaunchKernelGGL((fused_grad1_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, s, gf, av, x2f, x1f,
-                               n, m, d, Wf, g1, tiles_n, tiles_c, total, kp, sign);
+                               n, m, d, Wf, g1, tiles_n, tiles_c, total, kp, sign, static_cast<const float *>(nullptr),
+                               static_cast<const float *>(nullptr), w.colpart, static_cast<const float *>(nullptr),
+                               static_cast<const uint32_t *>(nullptr));
             rc = check_launch("fused_grad1_kernel");
             if (rc) return rc;
-            if constexpr (MODE == kEuclid || MODE == kSqEuclid)
-                return grad_product_f32(Wf, true, x1f, true, batch, m, d, n, sign, nullptr, x2f, g2, s);
+            if constexpr (MODE == kEuclid || MODE == kSqEuclid) {
+                // coef2 = sum_i W from the kernel's column partials
+                hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)cdiv(batch * m, 256)), dim3(256), 0, s,
+                                   w.colpart, 4 * tiles_n, m, batch, static_cast<const float *>(nullptr), w.coef2);
+                rc = check_launch("reduce_parts_kernel");
+                if (rc) return rc;
+                return grad_product_f32(Wf, true, x1f, true, batch, m, d, n, sign, w.coef2, x2f, g2, s);
+            }
             hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(2 * batch * m, 256)), dim3(256), 0, s,
                                reinterpret_cast<uint16_t *>(w.coef2), 2 * batch * m);
             rc = check_launch("zero_words_kernel");
             if (rc) return rc;
             return grad_product_f32(Wf, true, x1f, true, batch, m, d, n, sign, w.coef2, x2f, g2, s);
+        }
+    }
+    if constexpr (!kBf16 && kCosO<MODE>) {
+        // fp32 cosine from the forward's output: weights, coef1 and the column partials inside
+        // the grad_x1 product; coef2 from the partials; grad_x2 on the tile kernel
+        const float *gf = reinterpret_cast<const float *>(g), *of = reinterpret_cast<const float *>(res);
+        const float *x1f = reinterpret_cast<const float *>(x1), *x2f = reinterpret_cast<const float *>(x2);
+        float *Wf = reinterpret_cast<float *>(W);
+        float *g1 = reinterpret_cast<float *>(gx1), *g2 = reinterpret_cast<float *>(gx2);
+        if (fused_fits(gf, of, x1f, x2f, Wf, g1, g2, n, m, d) && aligned16(n2) && fused_grid_fills(batch, n, m, d)) {
+            const int64_t tiles_n = cdiv(n, tile::kT), tiles_c = cdiv(d, kFCols), total = tiles_n * tiles_c * batch;
+            // the column reciprocals and the norm-range flag, then both instances (one returns)
+            hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<uint16_t *>(w.slow), 2);
+            hipLaunchKernelGGL(cos_norm_prep_kernel, dim3((unsigned)cdiv(batch * (n + m), 256)), dim3(256), 0, s, n1,
+                               batch * n, n2, batch * m, w.rn2, w.slow);
+            hipLaunchKernelGGL((fused_grad1_kernel<MODE, true>), dim3((unsigned)total), dim3(256), 0, s, gf, of, x2f,
+                               x1f, n, m, d, Wf, g1, tiles_n, tiles_c, total, kp, 1.0f, n1, n2, w.colpart, w.rn2,
+                               static_cast<const uint32_t *>(w.slow));
+            hipLaunchKernelGGL((fused_grad1_kernel<MODE, false>), dim3((unsigned)total), dim3(256), 0, s, gf, of, x2f,
+                               x1f, n, m, d, Wf, g1, tiles_n, tiles_c, total, kp, 1.0f, n1, n2, w.colpart, w.rn2,
+                               static_cast<const uint32_t *>(w.slow));
+            rc = check_launch("fused_grad1_kernel");
+            if (rc) return rc;
+            hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)cdiv(batch * m, 256)), dim3(256), 0, s,
+                               w.colpart, 4 * tiles_n, m, batch, n2, w.coef2);
+            rc = check_launch("reduce_parts_kernel");
+            if (rc) return rc;
+            return grad_product_f32(Wf, true, x1f, true, batch, m, d, n, 1.0f, w.coef2, x2f, g2, s);
         }
     }
     if constexpr (kBf16 && (MODE == kEuclid || MODE == kSqEuclid || MODE == kSigmoid || MODE == kPoly)) {

@@ -184,6 +184,37 @@ def test_cosine_backward_fused_grid_ragged(similarity, extreme):
         print(f"sim={similarity} grad_x2 b={bb}: largest |err| / derived bound {worst:.4f}", flush=True)
 
 
+@pytest.mark.parametrize("extreme", [False, True])
+@pytest.mark.parametrize("similarity", [False, True])
+def test_cosine_backward_fused_grid_bf16(similarity, extreme):
+    """The bf16 cosine backward where the fused weight + grad_x1 kernel runs (n % 128 == 0 and a
+    grid of two blocks per CU: 4 x 16384 x 8192 x 256), its grad_x2 coefficient from the
+    projection -(x2 . P) / |x2|^2 of the product P = W^T x1.  With `extreme`, one row's norm lies
+    above 2^60 (the dividing kernel instance).  Sampled rows (the scaled one included) and
+    columns against float64 autograd of the reference's composite, bf16 bar 1e-2 (+ 1e-2 max)."""
+    B, n, m, d = 4, 16384, 8192, 256
+    x1 = randn(B, n, d, seed=70).to(torch.bfloat16)
+    x2 = randn(B, m, d, seed=71).to(torch.bfloat16)
+    if extreme:
+        x1[2, 5000] *= 2.0 ** 58
+    gen = torch.Generator(device=DEV).manual_seed(72)
+    g = torch.randn(B, n, m, device=DEV, generator=gen).to(torch.bfloat16)
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    fn = tp.cosine_similarity if similarity else tp.cosine_distances
+    ref_fn = P.cosine_similarity if similarity else P.cosine_distances
+    fn(a, b).backward(g)
+    f1, f2 = x1.double(), x2.double()
+    for bb in (0, 2):
+        rows = sorted(set(_sample(n, 6, seed=80 + bb)) | {5000})
+        cols = _sample(m, 6, seed=90 + bb)
+        r1 = f1[bb, rows].clone().requires_grad_()
+        ref_fn(r1, f2[bb]).backward(g[bb, rows].double().cpu())
+        _rows_close(a.grad[bb, rows].float().cpu(), r1.grad, 1e-2, f"bf16 cosine sim={similarity} grad_x1 b={bb}")
+        r2 = f2[bb, cols].clone().requires_grad_()
+        ref_fn(f1[bb], r2).backward(g[bb][:, cols].double().cpu())
+        _rows_close(b.grad[bb, cols].float().cpu(), r2.grad, 1e-2, f"bf16 cosine sim={similarity} grad_x2 b={bb}")
+
+
 # ------------------------------------------------- C3: minkowski p=3 fwd+bwd, chebyshev, [16384,128]^2
 def test_c3_minkowski_chebyshev():
     x1 = rand(16384, 128, seed=0) * 2 - 1

@@ -163,6 +163,45 @@ __global__ void cos_norm_prep_kernel(const float *__restrict__ n1, int64_t len1,
     if (__ballot(!cos_norm_fast(v)) != 0ull && (threadIdx.x & 63) == 0) atomicOr(slow, 1u);
 }
 
+// bf16 cosine: grad_x2[j] = P[j] + coef2[j] x2[j], with P = W^T x1 as the product wrote it (bf16,
+// in gx2) and coef2[j] = sum_i gden[i][j] n1[i] / n2[j].  Since gden = -gS q and q n1 / n2 =
+// S / n2^2, coef2[j] = -(x2[j] . sum_i gS[i][j] x1[i]) / n2[j]^2 = -(x2[j] . P[j]) / n2[j]^2
+// (0 where n2[j] = 0): one wave per row, the dot product in fp32, d % 8 == 0.
+__global__ __launch_bounds__(256) void cos_proj_finish_kernel(uint16_t *__restrict__ gx2,
+                                                              const uint16_t *__restrict__ x2,
+                                                              const float *__restrict__ n2, int64_t rows, int64_t d) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;  // the same in every lane
+    uint16_t *P = gx2 + row * d;
+    const uint16_t *X = x2 + row * d;
+    float dot = 0.0f;
+    for (int64_t k = 8 * lane; k < d; k += 512) {
+        const uint4 pv = *reinterpret_cast<const uint4 *>(P + k), xv = *reinterpret_cast<const uint4 *>(X + k);
+        const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w}, xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            dot += __uint_as_float(pw[e] << 16) * __uint_as_float(xw[e] << 16);
+            dot += __uint_as_float(pw[e] & 0xffff0000u) * __uint_as_float(xw[e] & 0xffff0000u);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+    const float nv = n2[row];
+    const float coef = nv == 0.0f ? 0.0f : -__fdiv_rn(__fdiv_rn(dot, nv), nv);
+    for (int64_t k = 8 * lane; k < d; k += 512) {
+        const uint4 pv = *reinterpret_cast<const uint4 *>(P + k), xv = *reinterpret_cast<const uint4 *>(X + k);
+        const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w}, xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = f32x2_to_bf16x2_rne(__uint_as_float(pw[e] << 16) + coef * __uint_as_float(xw[e] << 16),
+                                       __uint_as_float(pw[e] & 0xffff0000u) +
+                                           coef * __uint_as_float(xw[e] & 0xffff0000u));
+        *reinterpret_cast<uint4 *>(P + k) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 // Pass 1.  W (type T: fp32, or bf16 rounded as the reference's bf16 autograd rounds its
 // ratio tensor) is written [n, m] to Wo and, when WTo is given, transposed [m, n] to WTo,
 // so that both gradient products read their operands k-contiguous.  The row / column sums
@@ -1022,14 +1061,25 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
 // weight is formed in fp32 and rounded to bf16 as the weight pass stores it (weight_terms
 // with BF16W, then round to nearest even), fed to v_mfma_f32_32x32x16_bf16 and written to W;
 // coef1 sums the row terms (the rounded weights for euclidean).  grad_x1 leaves as bf16.
-template <int MODE>
+// The output-based cosine modes work as in the fp32 kernel (a FAST instance on reciprocal norms
+// and a dividing one, the norm-range flag choosing): the second panel is the forward's bf16
+// output and the chunk's 64 column reciprocals (or norms) come by DMA into LDS with the panels.
+// Their column coefficients are left to cos_proj_finish_kernel (summing the column terms here
+// took more registers than the two blocks per CU leave: the kernel spilled).
+template <int MODE, bool FAST = false>
 __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
     const uint16_t *__restrict__ g, const uint16_t *__restrict__ av, const uint16_t *__restrict__ x2,
     const uint16_t *__restrict__ x1, int64_t n, int64_t m, int64_t d, uint16_t *__restrict__ W,
-    uint16_t *__restrict__ gx1, int64_t tiles_n, int64_t tiles_c, int64_t total, KerParams kp, float sign) {
+    uint16_t *__restrict__ gx1, int64_t tiles_n, int64_t tiles_c, int64_t total, KerParams kp, float sign,
+    const float *__restrict__ n1, const float *__restrict__ n2, float *__restrict__ colpart,
+    const float *__restrict__ rn2, const uint32_t *__restrict__ slow) {
     using namespace tile;
-    constexpr bool kAv = MODE == kEuclid || MODE == kSigmoid || MODE == kPoly;
+    constexpr bool kCos = kCosO<MODE>;
+    if constexpr (kCos)
+        if ((__builtin_amdgcn_readfirstlane(*slow) != 0u) == FAST) return;
+    constexpr bool kAv = MODE == kEuclid || MODE == kSigmoid || MODE == kPoly || kCos;
     __shared__ uint4 smem[4 * kPanel];  // grad | res or S | x2 (two panels)
+    __shared__ __align__(16) float s_n2[64];  // cosine: the chunk's column reciprocals (FAST) or norms
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr = wave * 32;
@@ -1075,6 +1125,10 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
     const int64_t wrow = row0 + r < n ? row0 + r : n - 1;
     uint16_t *Wrow = W + (b * n + wrow) * m;
     const uint4 *Gs = smem, *As = smem + kPanel, *Bs = smem + 2 * kPanel;
+    // cosine: the lane's row norm and reciprocal
+    const float a1 = kCos ? n1[b * n + wrow] : 0.0f;
+    const float r1 = kCos && FAST ? __fdiv_rn(1.0f, a1) : 0.0f;
+    const uint8_t *NC = kCos ? reinterpret_cast<const uint8_t *>((FAST ? rn2 : n2) + b * m) : nullptr;
     // the bf16 weights of the lane's piece at step q (K = 32 h + 8 q + e), their row terms
     // into rsum
     auto weights = [&](int q) {
@@ -1083,6 +1137,30 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
         const uint4 ap = kAv ? piece(As, r, c) : make_uint4(0, 0, 0, 0);
         const uint32_t gw[4] = {gp.x, gp.y, gp.z, gp.w}, aw[4] = {ap.x, ap.y, ap.z, ap.w};
         uint32_t o[4];
+        if constexpr (kCos) {
+            // the lane's 8 pairs (K = 32 h + 8 q + k): weights and row terms (the column
+            // coefficients come from the grad_x2 product afterwards, cos_proj_finish_kernel)
+            const floatx4 nA = *reinterpret_cast<const floatx4 *>(&s_n2[32 * h + 8 * q]);
+            const floatx4 nB = *reinterpret_cast<const floatx4 *>(&s_n2[32 * h + 8 * q + 4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float wv[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int k = 2 * e + u;
+                    const float gvv = __uint_as_float(u ? gw[e] & 0xffff0000u : gw[e] << 16);
+                    const float avv = __uint_as_float(u ? aw[e] & 0xffff0000u : aw[e] << 16);
+                    const float nv = k < 4 ? nA[k] : nB[k - 4];
+                    float we, rt, ct;
+                    if constexpr (FAST) cos_terms_fast<MODE>(gvv, avv, r1, nv, we, rt, ct);
+                    else weight_terms<MODE, true>(gvv, avv, a1, nv, kp, we, rt, ct);
+                    wv[u] = we;
+                    rsum += rt;
+                }
+                o[e] = f32x2_to_bf16x2_rne(wv[0], wv[1]);
+            }
+            return make_uint4(o[0], o[1], o[2], o[3]);
+        }
         if constexpr (MODE == kEuclid) {
             // as the fp32 kernel: the reciprocal without a branch per pair, one test of the
             // piece's eight quotients (weight_terms below when one has a denominator outside
@@ -1133,6 +1211,8 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
             for (int j = 0; j < 16; ++j)
                 dma16(base + j * jstride, off_par[j & 1], lds_addr(smem + (wave * 16 + j) * 64));
         }
+        if constexpr (kCos)
+            if (wave == 3) dma4(NC + (int64_t)kc * 256, (uint32_t)lane * 4, lds_addr(s_n2));
         barrier_all();
         uint4 an = weights(0);
 #pragma unroll
@@ -1157,7 +1237,8 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
         }
     }
     barrier_lds();  // the buffer becomes the output stage
-    const float a1v = rsum + __shfl_xor(rsum, 32, 64);  // both K halves
+    float a1v = rsum + __shfl_xor(rsum, 32, 64);  // both K halves
+    if constexpr (kCos) a1v = a1 == 0.0f ? 0.0f : __fdiv_rn(a1v, a1);
     uint4 *sl = smem + wave * 1024;  // 16 KiB per wave
     store_wave_rows_bf16<8>(
         sl,
@@ -1469,7 +1550,10 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
                 const float sign = MODE == kSigmoid ? 1.0f : -1.0f;
                 const int64_t tiles_n = cdiv(n, tile::kT), tiles_c = cdiv(d, kFCols), total = tiles_n * tiles_c * batch;
                 hipLaunchKernelGGL((fused_grad1_bf16_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, s, gb, rb,
-                                   x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, sign);
+                                   x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, sign,
+                                   static_cast<const float *>(nullptr), static_cast<const float *>(nullptr),
+                                   static_cast<float *>(nullptr), static_cast<const float *>(nullptr),
+                                   static_cast<const uint32_t *>(nullptr));
                 rc = check_launch("fused_grad1_bf16_kernel");
                 if (rc) return rc;
                 if constexpr (MODE == kEuclid || MODE == kSqEuclid)
@@ -1480,6 +1564,35 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
                 if (rc) return rc;
                 return grad_product_bf16(Wb, true, x1b, true, batch, m, d, n, sign, w.coef2, x2b, g2, s);
             }
+        }
+    }
+    if constexpr (kBf16 && kCosO<MODE>) {
+        // bf16 cosine from the forward's output: the fp32 path's fusion on the bf16 kernel
+        const uint16_t *gb = reinterpret_cast<const uint16_t *>(g), *ob = reinterpret_cast<const uint16_t *>(res);
+        const uint16_t *x1b = reinterpret_cast<const uint16_t *>(x1), *x2b = reinterpret_cast<const uint16_t *>(x2);
+        uint16_t *Wb = reinterpret_cast<uint16_t *>(W);
+        uint16_t *g1 = reinterpret_cast<uint16_t *>(gx1), *g2 = reinterpret_cast<uint16_t *>(gx2);
+        if (fused_bf16_fits(gb, ob, x1b, x2b, Wb, g1, g2, n, m, d) && fused_grid_fills(batch, n, m, d)) {
+            const int64_t tiles_n = cdiv(n, tile::kT), tiles_c = cdiv(d, kFCols), total = tiles_n * tiles_c * batch;
+            hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<uint16_t *>(w.slow), 2);
+            hipLaunchKernelGGL(cos_norm_prep_kernel, dim3((unsigned)cdiv(batch * (n + m), 256)), dim3(256), 0, s, n1,
+                               batch * n, n2, batch * m, w.rn2, w.slow);
+            hipLaunchKernelGGL((fused_grad1_bf16_kernel<MODE, true>), dim3((unsigned)total), dim3(256), 0, s, gb, ob,
+                               x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, 1.0f, n1, n2,
+                               static_cast<float *>(nullptr), w.rn2, static_cast<const uint32_t *>(w.slow));
+            hipLaunchKernelGGL((fused_grad1_bf16_kernel<MODE, false>), dim3((unsigned)total), dim3(256), 0, s, gb,
+                               ob, x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, 1.0f, n1, n2,
+                               static_cast<float *>(nullptr), w.rn2, static_cast<const uint32_t *>(w.slow));
+            int rc = check_launch("fused_grad1_bf16_kernel");
+            if (rc) return rc;
+            // P = W^T x1 into gx2 (zero coefficients), then the projection finish
+            hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(2 * batch * m, 256)), dim3(256), 0, s,
+                               reinterpret_cast<uint16_t *>(w.coef2), 2 * batch * m);
+            rc = grad_product_bf16(Wb, true, x1b, true, batch, m, d, n, 1.0f, w.coef2, x2b, g2, s);
+            if (rc) return rc;
+            hipLaunchKernelGGL(cos_proj_finish_kernel, dim3((unsigned)cdiv(batch * m, 4)), dim3(256), 0, s, g2, x2b,
+                               n2, batch * m, d);
+            return check_launch("cos_proj_finish_kernel");
         }
     }
     int64_t ti = cdiv(n, kPWRows);

@@ -201,7 +201,9 @@ __device__ __forceinline__ float finish_small(float c, float pa, float pb, float
         } else if constexpr (MET == TPW_BMET_JACCARD) {
             return div_count(S, __builtin_fmaxf(S + A, 1.0f));
         } else if constexpr (MET == TPW_BMET_DICE) {
-            return div_count_z(S, 2.0f * A + S);
+            // 2A + S = 0 only with S = 0, and div_count(0, 0) is NaN as 0 / 0 is (the
+            // reciprocal of 0 is inf, and 0 inf poisons the Newton step): no zero test
+            return div_count(S, 2.0f * A + S);
         } else if constexpr (MET == TPW_BMET_KULCZYNSKI1) {
             return div_count_z(A, S);
         } else if constexpr (MET == TPW_BMET_KULSINSKI) {
@@ -213,14 +215,19 @@ __device__ __forceinline__ float finish_small(float c, float pa, float pb, float
             return (df - A) * inv_df;
         } else if constexpr (MET == TPW_BMET_SOKALSNEATH) {
             const float R = 2.0f * S;
-            return div_count_z(R, A + R);
-        } else {  // yule: products past 2^24 round, so the general divide
+            return div_count(R, A + R);  // A + R = 0 only with R = 0: 0 / 0, as for dice
+        } else {  // yule
             const float n10 = pa - A, n01 = pb - A;
             const float n00 = df - ((pa + pb) - A);
             const float hR = n10 * n01;
             const float num = 2.0f * hR;
             const float prod = A * n00;
             const float den = prod + hR;
+            // d <= 2048: n10 + n01 + A + n00 = d bounds n10 n01 and A n00 by d^2 / 4 = 2^20, so
+            // every product and sum is an exact integer, num <= 2^21 and den <= 2^20, inside
+            // div_count's range (den = 0 gives 0 / 0 there, replaced by 0 as below).  Longer
+            // rows: products past 2^24 round, and the general divide.
+            if (df <= 2048.0f) return select_bits(den != 0.0f, div_count(num, den), 0.0f);
             return select_bits(den != 0.0f, __fdiv_rn(num, den), 0.0f);
         }
     }
@@ -771,8 +778,9 @@ __global__ __launch_bounds__(kThreads, 2) void bool_fp4_kernel(
 // output and rows * row bytes < 2^32.
 // Output stores of the tile kernels: plain stores, which let the L2 merge the waves' 256-byte
 // row pieces (32768^2 x 1024 bits: pwxor_sum 0.95 -> 0.83 ms, hamming 0.96 -> 0.86 ms, jaccard
-// 0.97 -> 0.91 ms), except for yule, whose epilogue keeps the general IEEE divide and runs
-// 4 % faster with non-temporal stores (1.13 -> 1.09 ms).
+// 0.97 -> 0.91 ms), except for yule, whose epilogue is the longest and which runs faster with
+// non-temporal stores (general IEEE divide: 1.13 -> 1.09 ms; short divide: yule / hamming 1.25
+// -> 1.18).
 template <int EPI>
 constexpr bool kStoreNT = EPI == kCountMetric + TPW_BMET_YULE;
 

@@ -957,6 +957,20 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
     const bool col_writer = tc == 0;
     const bool rows_ok = row0 + wr < n;
     float *cp = kColT ? colpart + (b * 4 * tiles_n + 4 * tr + wave) * m : nullptr;
+    // Cosine: the lane's 16 weights of a chunk, its 64 contiguous bytes of the W row (half a
+    // 128-byte line; the partner lane writes the other half in the same instructions), stored
+    // together one chunk later.  Stored one step at a time as they are formed, the lines reach
+    // HBM in parts (1.5x W's bytes written).  The cosine kernel gains from the whole lines
+    // (2.49 -> 2.39 ms at C2); the euclidean one, whose reciprocal per pair spreads its steps
+    // further, loses (2.63 -> 2.73-2.82 ms) and keeps the stores per step.
+    constexpr bool kLineStores = kCos;
+    floatx16 wst;
+    auto store_w = [&](int kw) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<floatx4 *>(Wrow + (int64_t)kw * 32 + 4 * (h * 4 + q)) =
+                floatx4{wst[4 * q], wst[4 * q + 1], wst[4 * q + 2], wst[4 * q + 3]};
+    };
     const int nchunks = (int)(m / 32);
     for (int kc = 0; kc < nchunks; ++kc) {
         if (kc > 0) barrier_lds();  // every wave is done with chunk kc - 1
@@ -980,6 +994,9 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
             }
         }
         barrier_all();
+        // the previous chunk's W pieces, now that this chunk's barrier is behind them (the next
+        // barrier waits for them, a chunk later)
+        if (kLineStores && kc > 0) store_w(kc - 1);
         floatx4 wn = weights(0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -991,7 +1008,12 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
                                  ((ni * 32 + l32) ^ (32 * h));
                 bv[ni] = floatx4{f[0], f[kFCols], f[2 * kFCols], f[3 * kFCols]};
             }
-            *reinterpret_cast<floatx4 *>(Wrow + (int64_t)kc * 32 + 4 * (h * 4 + q)) = a;
+            if constexpr (kLineStores) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) wst[4 * q + e] = a[e];
+            } else {
+                *reinterpret_cast<floatx4 *>(Wrow + (int64_t)kc * 32 + 4 * (h * 4 + q)) = a;
+            }
             if (q < 3) wn = weights(q + 1);  // formed while this step's products run
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -1036,6 +1058,7 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
             if (col_writer && (l32 & 1) == 0) cp[(int64_t)kc * 32 + 16 * h + (l32 >> 1)] = rows_ok ? t1 : 0.0f;
         }
     }
+    if constexpr (kLineStores) store_w(nchunks - 1);
     barrier_lds();  // the buffer becomes the output stage
     float a1v = rsum + __shfl_xor(rsum, 32, 64);  // both K halves
     if constexpr (kCos) a1v = a1 == 0.0f ? 0.0f : __fdiv_rn(a1v, a1);

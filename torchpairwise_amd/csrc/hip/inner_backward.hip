@@ -897,11 +897,10 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[ni][r] = 0.0f;
     float rsum = 0.0f;
-    // the lane's W row; rows past n store row n - 1, whose weights they duplicate exactly (the
-    // same clamped inputs), as do the tiles of further column blocks: no branches in the K loop
+    // the lane's row; rows past n read row n - 1 (the same clamped inputs) and store nothing; the
+    // tiles of further column blocks store the same W values again
     const int r = wr + l32;
     const int64_t wrow = row0 + r < n ? row0 + r : n - 1;
-    float *Wrow = W + (b * n + wrow) * m;
     const uint4 *Gs = smem, *As = smem + kPanel, *Bs = smem + 2 * kPanel;
     const float a1 = kCos ? n1[b * n + wrow] : 0.0f;  // the lane's row norm
     const float r1 = kCos && FAST ? __fdiv_rn(1.0f, a1) : 0.0f;
@@ -957,13 +956,17 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
     const bool col_writer = tc == 0;
     const bool rows_ok = row0 + wr < n;
     float *cp = kColT ? colpart + (b * 4 * tiles_n + 4 * tr + wave) * m : nullptr;
-    // Cosine: the lane's 16 weights of a chunk, its 64 contiguous bytes of the W row (half a
-    // 128-byte line; the partner lane writes the other half in the same instructions), stored
-    // together one chunk later.  Stored one step at a time as they are formed, the lines reach
-    // HBM in parts (1.5x W's bytes written).  The cosine kernel gains from the whole lines
-    // (2.49 -> 2.39 ms at C2); the euclidean one, whose reciprocal per pair spreads its steps
-    // further, loses (2.63 -> 2.73-2.82 ms) and keeps the stores per step.
-    constexpr bool kLineStores = kCos;
+    // W leaves as whole 128-byte lines.  Stored piece by piece from the lanes that formed them,
+    // each instruction wrote 16-byte parts of 32 lines, which reached HBM in parts (1.5x W's
+    // bytes).  Euclidean and the kernel functions: each lane puts its weight pieces into the grad
+    // slots they were formed from (only that lane reads them), and at the end of the chunk lane
+    // (lr, lp) = (lane / 8, lane % 8) stores piece lp of row wr + 8 i + lr (i < 4); element
+    // offsets from the batch's W stay below 2^31 (n m 4 < 2^32).  Cosine, whose extra registers
+    // leave no room for that (it spilled): each lane keeps its 16 weights of the chunk, its 64
+    // contiguous bytes of the line (the partner lane has the other 64), and stores them together
+    // one chunk later (after the next barrier, which would otherwise wait for them).
+    constexpr bool kLdsW = !kCos;
+    float *Wrow = kCos ? W + (b * n + wrow) * m : nullptr;
     floatx16 wst;
     auto store_w = [&](int kw) {
 #pragma unroll
@@ -971,6 +974,11 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
             *reinterpret_cast<floatx4 *>(Wrow + (int64_t)kw * 32 + 4 * (h * 4 + q)) =
                 floatx4{wst[4 * q], wst[4 * q + 1], wst[4 * q + 2], wst[4 * q + 3]};
     };
+    const int lr = lane >> 3, lx = (lane & 7) ^ lr;
+    float *Wb = W + b * n * m;
+    const int64_t wrow_l = row0 + wr + lr < n ? row0 + wr + lr : n - 1;
+    const uint32_t woff = (uint32_t)(wrow_l * m + 4 * (lane & 7));
+    const uint32_t wstep = (uint32_t)(8 * m);
     const int nchunks = (int)(m / 32);
     for (int kc = 0; kc < nchunks; ++kc) {
         if (kc > 0) barrier_lds();  // every wave is done with chunk kc - 1
@@ -996,7 +1004,8 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
         barrier_all();
         // the previous chunk's W pieces, now that this chunk's barrier is behind them (the next
         // barrier waits for them, a chunk later)
-        if (kLineStores && kc > 0) store_w(kc - 1);
+        if constexpr (!kLdsW)
+            if (kc > 0) store_w(kc - 1);
         floatx4 wn = weights(0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1008,11 +1017,11 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
                                  ((ni * 32 + l32) ^ (32 * h));
                 bv[ni] = floatx4{f[0], f[kFCols], f[2 * kFCols], f[3 * kFCols]};
             }
-            if constexpr (kLineStores) {
+            if constexpr (kLdsW) {
+                smem[r * 8 + swz(r, h * 4 + q)] = __builtin_bit_cast(uint4, a);  // into its grad slot
+            } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) wst[4 * q + e] = a[e];
-            } else {
-                *reinterpret_cast<floatx4 *>(Wrow + (int64_t)kc * 32 + 4 * (h * 4 + q)) = a;
             }
             if (q < 3) wn = weights(q + 1);  // formed while this step's products run
 #pragma unroll
@@ -1027,6 +1036,17 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
                 }
+            }
+        }
+        if constexpr (kLdsW) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes landed
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // row wr + 8 i + lr, piece lp: slot swz = lp ^ lr ^ (i & 1) (wr is a multiple of 32)
+                const uint4 v = smem[(wr + 8 * i + lr) * 8 + (lx ^ (i & 1))];
+                if (row0 + wr + 8 * i + lr < n)
+                    *reinterpret_cast<uint4 *>(Wb + (uint32_t)(woff + i * wstep + kc * 32)) = v;
             }
         }
         if constexpr (kColT) {
@@ -1058,7 +1078,7 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_kernel(
             if (col_writer && (l32 & 1) == 0) cp[(int64_t)kc * 32 + 16 * h + (l32 >> 1)] = rows_ok ? t1 : 0.0f;
         }
     }
-    if constexpr (kLineStores) store_w(nchunks - 1);
+    if constexpr (!kLdsW) store_w(nchunks - 1);
     barrier_lds();  // the buffer becomes the output stage
     float a1v = rsum + __shfl_xor(rsum, 32, 64);  // both K halves
     if constexpr (kCos) a1v = a1 == 0.0f ? 0.0f : __fdiv_rn(a1v, a1);
@@ -1146,8 +1166,15 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
     // the lane's W row; rows past n store row n - 1, whose weights they duplicate exactly
     const int r = wr + l32;
     const int64_t wrow = row0 + r < n ? row0 + r : n - 1;
-    uint16_t *Wrow = W + (b * n + wrow) * m;
     const uint4 *Gs = smem, *As = smem + kPanel, *Bs = smem + 2 * kPanel;
+    // the W line stores (euclidean and the kernel functions; the cosine kernel has no registers to
+    // spare for them and stores each piece as it is formed): lane (lr, lp) = (lane / 8, lane % 8)
+    // writes piece lp of row wr + 8 i + lr (i < 4) of each chunk; element offsets from the batch's
+    // W below 2^31 (n m 2 < 2^32)
+    constexpr bool kLdsW = !kCos;
+    const int lr = lane >> 3, lx = (lane & 7) ^ lr;
+    uint16_t *Wb = W + b * n * m;
+    const uint32_t woff = (uint32_t)((row0 + wr + lr) * m + 8 * (lane & 7));
     // cosine: the lane's row norm and reciprocal
     const float a1 = kCos ? n1[b * n + wrow] : 0.0f;
     const float r1 = kCos && FAST ? __fdiv_rn(1.0f, a1) : 0.0f;
@@ -1241,7 +1268,13 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint4 a = an;
-            *reinterpret_cast<uint4 *>(Wrow + (int64_t)kc * 64 + 8 * (h * 4 + q)) = a;
+            if constexpr (kLdsW) {
+                // W's piece into the grad slot it was formed from (only this lane reads that
+                // slot, and it has: the weights are formed from it)
+                smem[r * 8 + swz(r, h * 4 + q)] = a;
+            } else {
+                *reinterpret_cast<uint4 *>(W + (b * n + wrow) * m + (int64_t)kc * 64 + 8 * (h * 4 + q)) = a;
+            }
             if (q < 3) an = weights(q + 1);  // formed while this step's products run
 #pragma unroll
             for (int ni = 0; ni < 8; ++ni) {
@@ -1256,6 +1289,19 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
                 }
+            }
+        }
+        if constexpr (kLdsW) {
+            // the wave's 32 W rows of the chunk (128 bytes each) leave as whole lines, 8 rows per
+            // store: stored piece by piece from the lanes that formed them, each instruction wrote
+            // 16-byte parts of 32 lines (W alone cost 0.27 ms of the kernel's 0.88 at C2)
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes landed
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // row wr + 8 i + lr, piece lp: slot swz = lp ^ lr ^ (i & 1) (wr is a multiple of 32)
+                const uint4 v = smem[(wr + 8 * i + lr) * 8 + (lx ^ (i & 1))];
+                *reinterpret_cast<uint4 *>(Wb + (uint32_t)(woff + i * 8 * (uint32_t)m + kc * 64)) = v;
             }
         }
     }

@@ -1114,8 +1114,8 @@ __global__ __launch_bounds__(256, 2) void fused_grad1_bf16_kernel(
     const uint16_t *__restrict__ g, const uint16_t *__restrict__ av, const uint16_t *__restrict__ x2,
     const uint16_t *__restrict__ x1, int64_t n, int64_t m, int64_t d, uint16_t *__restrict__ W,
     uint16_t *__restrict__ gx1, int64_t tiles_n, int64_t tiles_c, int64_t total, KerParams kp, float sign,
-    const float *__restrict__ n1, const float *__restrict__ n2, float *__restrict__ colpart,
-    const float *__restrict__ rn2, const uint32_t *__restrict__ slow) {
+    const float *__restrict__ n1, const float *__restrict__ n2, const float *__restrict__ rn2,
+    const uint32_t *__restrict__ slow) {
     using namespace tile;
     constexpr bool kCos = kCosO<MODE>;
     if constexpr (kCos)
@@ -1514,7 +1514,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
     BwdWs w = carve(ws, batch, n, m, d);
     T *W = static_cast<T *>(w.W), *WT = static_cast<T *>(w.WT);
     T *x1t = static_cast<T *>(w.x1t), *x2t = static_cast<T *>(w.x2t);
-    int rc;
+    int rc = TPW_OK;
     constexpr bool kBf16 = sizeof(T) == 2;
     constexpr bool kCosMode = kCosS<MODE>;  // S recomputed (the output-based modes read res)
     // bf16: the tile kernel reads x2 (for gx1) and W, x1 (for gx2) k-major in place where the
@@ -1621,8 +1621,7 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
                 hipLaunchKernelGGL((fused_grad1_bf16_kernel<MODE>), dim3((unsigned)total), dim3(256), 0, s, gb, rb,
                                    x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, sign,
                                    static_cast<const float *>(nullptr), static_cast<const float *>(nullptr),
-                                   static_cast<float *>(nullptr), static_cast<const float *>(nullptr),
-                                   static_cast<const uint32_t *>(nullptr));
+                                   static_cast<const float *>(nullptr), static_cast<const uint32_t *>(nullptr));
                 rc = check_launch("fused_grad1_bf16_kernel");
                 if (rc) return rc;
                 if constexpr (MODE == kEuclid || MODE == kSqEuclid)
@@ -1647,11 +1646,11 @@ int run_backward(const T *g, const T *x1, const T *x2, const T *res, const float
             hipLaunchKernelGGL(cos_norm_prep_kernel, dim3((unsigned)cdiv(batch * (n + m), 256)), dim3(256), 0, s, n1,
                                batch * n, n2, batch * m, w.rn2, w.slow);
             hipLaunchKernelGGL((fused_grad1_bf16_kernel<MODE, true>), dim3((unsigned)total), dim3(256), 0, s, gb, ob,
-                               x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, 1.0f, n1, n2,
-                               static_cast<float *>(nullptr), w.rn2, static_cast<const uint32_t *>(w.slow));
+                               x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, 1.0f, n1, n2, w.rn2,
+                               static_cast<const uint32_t *>(w.slow));
             hipLaunchKernelGGL((fused_grad1_bf16_kernel<MODE, false>), dim3((unsigned)total), dim3(256), 0, s, gb,
-                               ob, x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, 1.0f, n1, n2,
-                               static_cast<float *>(nullptr), w.rn2, static_cast<const uint32_t *>(w.slow));
+                               ob, x2b, x1b, n, m, d, Wb, g1, tiles_n, tiles_c, total, kp, 1.0f, n1, n2, w.rn2,
+                               static_cast<const uint32_t *>(w.slow));
             int rc = check_launch("fused_grad1_bf16_kernel");
             if (rc) return rc;
             // P = W^T x1 into gx2 (zero coefficients), then the projection finish

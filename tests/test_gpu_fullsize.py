@@ -143,16 +143,16 @@ def test_c2_forward_backward(c2_inputs, metric, dtype):
             _rows_close(got2, r2.grad, grtol, f"{metric} grad_x2 b={bb}")
 
 
-@pytest.mark.parametrize("extreme", [False, True])
-@pytest.mark.parametrize("similarity", [False, True])
-def test_cosine_backward_fused_grid_ragged(similarity, extreme):
-    """The fp32 cosine backward where the fused weight + grad_x1 kernel runs, at a shape that
-    takes its edge cases: n % 128 = 96 (the last row block's fourth wave lies past the end and
-    writes zero column partials), d = 260 (two column blocks, of which only the first writes
-    column partials, and a partial last one).  With `extreme`, one row's norm lies above 2^60,
-    which sends the call to the kernel instance that divides by every norm product.  Sampled
-    rows (the partial block's and the scaled one included) and columns against float64 autograd
-    of the reference's composite, within the derived bound."""
+@pytest.mark.parametrize("metric,extreme", [("cosine", False), ("cosine", True), ("cosine_similarity", False),
+                                           ("cosine_similarity", True), ("euclidean", False)])
+def test_inner_backward_fused_grid_ragged(metric, extreme):
+    """The fp32 backward where the fused weight + grad_x1 kernel runs, at a shape that takes its
+    edge cases: n % 128 = 96 (the last row block's fourth wave lies past the end: it stores no W
+    rows and writes zero column partials), d = 260 (two column blocks, of which only the first
+    writes column partials, and a partial last one).  With `extreme`, one row's norm lies above
+    2^60, which sends a cosine call to the kernel instance that divides by every norm product.
+    Sampled rows (the partial block's and the scaled one included) and columns against float64
+    autograd of the reference's composite (at::cdist for euclidean), within the derived bound."""
     from tests import _gradbound as GB
 
     B, n, m, d = 2, 16352, 11008, 260
@@ -162,8 +162,17 @@ def test_cosine_backward_fused_grid_ragged(similarity, extreme):
     gen = torch.Generator(device=DEV).manual_seed(42)
     g = torch.randn(B, n, m, device=DEV, generator=gen)
     a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
-    fn = tp.cosine_similarity if similarity else tp.cosine_distances
-    ref_fn = P.cosine_similarity if similarity else P.cosine_distances
+    similarity = metric == "cosine_similarity"
+    fn = {"cosine": tp.cosine_distances, "cosine_similarity": tp.cosine_similarity,
+          "euclidean": tp.euclidean_distances}[metric]
+    ref_fn = {"cosine": P.cosine_distances, "cosine_similarity": P.cosine_similarity,
+              "euclidean": lambda u, v: torch.cdist(u, v, 2)}[metric]
+
+    def bound(own, other, gsl):
+        if metric == "euclidean":
+            return GB.euclidean_grad_bound(own, other, gsl)
+        return GB.cosine_grad_bound(own, other, gsl, similarity)
+
     fn(a, b).backward(g)
     f1, f2 = x1.double(), x2.double()
     for bb in range(B):
@@ -172,16 +181,15 @@ def test_cosine_backward_fused_grid_ragged(similarity, extreme):
         r1 = f1[bb, rows].clone().requires_grad_()
         gr = g[bb, rows].double().cpu()
         ref_fn(r1, f2[bb]).backward(gr)
-        worst = GB.check(a.grad[bb, rows].cpu(), r1.grad, GB.cosine_grad_bound(f1[bb, rows], f2[bb], gr, similarity),
-                         f"cosine sim={similarity} grad_x1 b={bb}")
-        print(f"sim={similarity} grad_x1 b={bb}: largest |err| / derived bound {worst:.4f}", flush=True)
+        worst = GB.check(a.grad[bb, rows].cpu(), r1.grad, bound(f1[bb, rows], f2[bb], gr),
+                         f"{metric} grad_x1 b={bb}")
+        print(f"{metric} grad_x1 b={bb}: largest |err| / derived bound {worst:.4f}", flush=True)
         r2 = f2[bb, cols].clone().requires_grad_()
         gc = g[bb][:, cols].double().cpu()
         ref_fn(f1[bb], r2).backward(gc)
-        worst = GB.check(b.grad[bb, cols].cpu(), r2.grad,
-                         GB.cosine_grad_bound(f2[bb, cols], f1[bb], gc.T.contiguous(), similarity),
-                         f"cosine sim={similarity} grad_x2 b={bb}")
-        print(f"sim={similarity} grad_x2 b={bb}: largest |err| / derived bound {worst:.4f}", flush=True)
+        worst = GB.check(b.grad[bb, cols].cpu(), r2.grad, bound(f2[bb, cols], f1[bb], gc.T.contiguous()),
+                         f"{metric} grad_x2 b={bb}")
+        print(f"{metric} grad_x2 b={bb}: largest |err| / derived bound {worst:.4f}", flush=True)
 
 
 @pytest.mark.parametrize("extreme", [False, True])

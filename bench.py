@@ -466,8 +466,8 @@ def run_config(cfg, steps, warmup):
             tp.directed_hausdorff_distances(a, x2)[0].backward(g)
 
         ms, _ = time_op(fb, steps, warmup)
-        # the backward adds two zero fills and the two scatter kernels
-        emit("directed_hausdorff fwd+bwd", ms, pf, floor_of(ms, work["launches"] + 4))
+        # the backward adds two launches: the gradients' zero fill and the scatter
+        emit("directed_hausdorff fwd+bwd", ms, pf, floor_of(ms, work["launches"] + 2))
     elif cfg == "NB":
         # neighbour masks at the metric shape: the selection kernel alone on a resident
         # distance matrix (HBM-bound: 4 B read + 1 B written per entry), the whole drop-in

@@ -651,7 +651,8 @@ int tpw_directed_hausdorff_noalloc(const float *x1, const float *x2, int64_t bat
 
 /* grad_x1[b,i,idx1,k] += grad * (x1[idx1,k] - x2[idx2,k]) / out summed over j in
  * order; grad_x2[b,j,idx2,k] += grad * (x2[idx2,k] - x1[idx1,k]) / out summed over
- * i in order.  grad_x1/grad_x2 must be zero-filled by the caller.
+ * i in order, starting from zero: grad_x1/grad_x2 are overwritten (every element
+ * written; no fill by the caller is needed).
  * Replaces the scatter half of _directed_hausdorff_backward_kernel
  * (csrc/ops/cpu/hausdorff_kernel.cpp:187-235,308-336;
  *  CUDA csrc/ops/cuda/hausdorff_kernel.cu:199-246). */

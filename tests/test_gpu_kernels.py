@@ -515,6 +515,33 @@ def test_hausdorff_ties_bit_exact():
         assert_equal(got, torch.from_numpy(want), f"self {nm}")
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 500, 4, 400, 3), (1, 210, 8192, 210, 8192, 3)])
+def test_hausdorff_backward_paths_bit_exact(shape):
+    """Both routes of tpw_directed_hausdorff_backward on given outputs and indices (many clouds
+    sharing an index, so terms of several pairs meet in one element): the one-launch gather
+    (few clouds per side) and the fill + scatter (210 x 210 clouds of 8192 points, past the
+    gather's work limit), into buffers holding garbage (both write every element), against the
+    reference's scatter loop."""
+    B, b1, p1, b2, p2, d = shape
+    gen = torch.Generator().manual_seed(17)
+    x1 = torch.randn(B, b1, p1, d, generator=gen)
+    x2 = torch.randn(B, b2, p2, d, generator=gen)
+    out = torch.rand(B, b1, b2, generator=gen) + 0.5
+    g = torch.randn(B, b1, b2, generator=gen)
+    i1 = torch.randint(0, 3, (B, b1, b2), generator=gen)  # few distinct positions: shared targets
+    i2 = torch.randint(0, p2, (B, b1, b2), generator=gen)
+    i2[..., 0] = 1
+    # device copies held in names: a temporary freed before the launch could be reused
+    a, b, gd, od, i1d, i2d = (t.to(DEV) for t in (x1, x2, g, out, i1, i2))
+    gx1 = torch.full_like(a, float("nan"))
+    gx2 = torch.full_like(b, 7.0)
+    capi.call("tpw_directed_hausdorff_backward", capi._ptr(gd), capi._ptr(a), capi._ptr(b), capi._ptr(od),
+              capi._ptr(i1d), capi._ptr(i2d), B, b1, p1, b2, p2, d, capi._ptr(gx1), capi._ptr(gx2), capi._stream())
+    w1, w2 = P.directed_hausdorff_backward(g.numpy(), x1.numpy(), x2.numpy(), out.numpy(), i1.numpy(), i2.numpy())
+    assert_equal(gx1.cpu(), torch.from_numpy(w1).reshape(gx1.shape), f"grad_x1 {shape}")
+    assert_equal(gx2.cpu(), torch.from_numpy(w2).reshape(gx2.shape), f"grad_x2 {shape}")
+
+
 @pytest.mark.parametrize("shape", HD_SHAPES[:4])
 def test_hausdorff_backward_bit_exact(shape):
     x1, x2 = _hd_inputs(*shape)

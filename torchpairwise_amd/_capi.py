@@ -646,7 +646,7 @@ def directed_hausdorff_backward(grad, x1, x2, out, idx1, idx2):
     i1, i2 = idx1.contiguous().reshape(g.shape), idx2.contiguous().reshape(g.shape)
     B, b1, p1, d = a.shape
     b2, p2 = b.shape[1], b.shape[2]
-    gx1, gx2 = torch.zeros_like(a), torch.zeros_like(b)
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)  # written whole by the library
     call("tpw_directed_hausdorff_backward", _ptr(g), _ptr(a), _ptr(b), _ptr(o), _ptr(i1), _ptr(i2),
          B, b1, p1, b2, p2, d, _ptr(gx1), _ptr(gx2), _stream())
     if x1.dim() == 3:

@@ -832,6 +832,54 @@ __global__ void backward_x2_kernel(const float *__restrict__ g, const float *__r
     }
 }
 
+// The scatter with a wave per cloud (x1's clouds, then x2's), for at most 64 clouds on the
+// other side, into zero-filled gradients: lane o takes the cloud's o-th pair (x1 cloud
+// c = bb b1 + i: pair (c, o); x2 cloud bb b2 + j: pair (bb b1 + o, j)), its target position and,
+// per feature, its term g (own - other) / out.  Each lane then adds, over the pairs in order
+// from +0, the terms of those with its target, and the last lane of each target stores the sum:
+// the sequential loop's additions in its order, so the same bits, with the pairs' loads in
+// parallel instead of one dependent round of loads and a read-modify-write per pair.
+__global__ __launch_bounds__(256) void backward_wave_kernel(
+    const float *__restrict__ g, const float *__restrict__ x1, const float *__restrict__ x2,
+    const float *__restrict__ out, const int64_t *__restrict__ idx1, const int64_t *__restrict__ idx2, int64_t batch,
+    int64_t b1, int64_t p1, int64_t b2, int64_t p2, int64_t d, float *__restrict__ gx1, float *__restrict__ gx2) {
+    const int64_t cy = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t clouds1 = batch * b1;
+    if (cy >= clouds1 + batch * b2) return;  // the same in every lane
+    const bool side1 = cy < clouds1;
+    const int64_t c = side1 ? cy : cy - clouds1;
+    const int64_t bb = side1 ? c / b1 : c / b2, j2 = c - bb * b2;
+    const int other = (int)(side1 ? b2 : b1);
+    const int64_t pr = lane >= other ? 0 : side1 ? c * b2 + lane : (bb * b1 + lane) * b2 + j2;
+    const int64_t m = idx1[pr], n = idx2[pr];
+    // lanes past the cloud count, and pairs with an index outside its cloud, take no part
+    const bool act = lane < other && m >= 0 && m < p1 && n >= 0 && n < p2;
+    const int64_t tgt = act ? (side1 ? m : n) : -1;
+    const float gv = g[pr], ov = out[pr];
+    // own / other rows of the lane's pair
+    const float *own = side1 ? x1 + (c * p1 + m) * d : x2 + (c * p2 + n) * d;
+    const float *oth = side1 ? x2 + ((bb * b2 + lane) * p2 + n) * d : x1 + ((bb * b1 + lane) * p1 + m) * d;
+    float *dst = side1 ? gx1 + (c * p1 + m) * d : gx2 + (c * p2 + n) * d;
+    // the last lane of each target stores (every lane runs every shuffle: a shuffle from a lane
+    // that is not running returns nothing of use)
+    bool last = act;
+    for (int o = 0; o < other; ++o) {
+        const int64_t to = __shfl(tgt, o, 64);
+        last = last && !(o > lane && to == tgt);
+    }
+    for (int64_t k = 0; k < d; ++k) {
+        const float diff = act ? own[k] - oth[k] : 0.0f;
+        const float term = gv * diff / ov;
+        float acc = 0.0f;
+        for (int o = 0; o < other; ++o) {
+            const float t = __shfl(term, o, 64);
+            if (__shfl(tgt, o, 64) == tgt) acc = acc + t;
+        }
+        if (last) dst[k] = acc;
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Scan with a spatial first guess (D = 1, 2, 3).  Pruning an m needs only one distance below
 // T, and an m that is never pruned gets its exact min whatever order x2 is visited in.  Each
@@ -2495,6 +2543,19 @@ extern "C" int tpw_directed_hausdorff_backward(const float *grad, const float *x
     if (batch * b1 * b2 == 0 || d == 0 || p1 == 0 || p2 == 0) return TPW_OK;
     TPW_REQUIRE(grad && x1 && x2 && out && idx1 && idx2 && grad_x1 && grad_x2, "null pointer");
     hipStream_t s = as_stream(stream);
+    const int64_t n1 = batch * b1 * p1 * d, n2 = batch * b2 * p2 * d;
+    // a fill of both gradients, then the scatter: a wave per cloud for at most 64 clouds per side
+    // (C5: 16), else one thread per (cloud, feature) passing over the other side's clouds
+    Fills fs{};
+    fs.f[fs.count++] = Fill{reinterpret_cast<uint32_t *>(grad_x1), n1, {0u, 0u}};
+    fs.f[fs.count++] = Fill{reinterpret_cast<uint32_t *>(grad_x2), n2, {0u, 0u}};
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)std::min<int64_t>(cdiv(std::max(n1, n2), 256), 2048)), dim3(256),
+                       0, s, fs);
+    if (b1 <= 64 && b2 <= 64) {
+        hipLaunchKernelGGL(backward_wave_kernel, dim3((unsigned)cdiv(batch * (b1 + b2), 4)), dim3(256), 0, s, grad,
+                           x1, x2, out, idx1, idx2, batch, b1, p1, b2, p2, d, grad_x1, grad_x2);
+        return check_launch("hausdorff backward");
+    }
     hipLaunchKernelGGL(backward_x1_kernel, dim3((unsigned)cdiv(batch * b1 * d, 256)), dim3(256), 0,
                        s, grad, x1, x2, out, idx1, idx2, batch, b1, p1, b2, p2, d, grad_x1);
     hipLaunchKernelGGL(backward_x2_kernel, dim3((unsigned)cdiv(batch * b2 * d, 256)), dim3(256), 0,

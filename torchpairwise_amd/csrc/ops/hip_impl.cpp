@@ -494,7 +494,7 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_cuda(
         return {gx1, gx2};
     }
     auto g = grad.to(at::kFloat).reshape(r.out.sizes()).contiguous();
-    auto gx1 = at::zeros_like(r.a), gx2 = at::zeros_like(r.b);
+    auto gx1 = at::empty_like(r.a), gx2 = at::empty_like(r.b);  // written whole by the kernel
     check_rc(tpw_directed_hausdorff_backward(
                  g.data_ptr<float>(), r.a.data_ptr<float>(), r.b.data_ptr<float>(),
                  r.out.data_ptr<float>(), r.i1.data_ptr<int64_t>(), r.i2.data_ptr<int64_t>(),
@@ -541,7 +541,7 @@ std::tuple<at::Tensor, at::Tensor> directed_hausdorff_backward_indexed_cuda(
         return {gx1, gx2};
     }
     auto g = grad.to(at::kFloat).reshape({B, b1, b2}).contiguous();
-    auto gx1 = at::zeros_like(a), gx2 = at::zeros_like(b);
+    auto gx1 = at::empty_like(a), gx2 = at::empty_like(b);  // written whole by the kernels
     check_rc(tpw_directed_hausdorff_backward(
                  g.data_ptr<float>(), a.data_ptr<float>(), b.data_ptr<float>(), o.data_ptr<float>(),
                  m1.data_ptr<int64_t>(), m2.data_ptr<int64_t>(), B, b1, a.size(2), b2, b.size(2), a.size(3),

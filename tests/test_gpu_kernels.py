@@ -517,11 +517,10 @@ def test_hausdorff_ties_bit_exact():
 
 @pytest.mark.parametrize("shape", [(2, 3, 500, 4, 400, 3), (1, 210, 8192, 210, 8192, 3)])
 def test_hausdorff_backward_paths_bit_exact(shape):
-    """Both routes of tpw_directed_hausdorff_backward on given outputs and indices (many clouds
-    sharing an index, so terms of several pairs meet in one element): the one-launch gather
-    (few clouds per side) and the fill + scatter (210 x 210 clouds of 8192 points, past the
-    gather's work limit), into buffers holding garbage (both write every element), against the
-    reference's scatter loop."""
+    """Both scatter routes of tpw_directed_hausdorff_backward on given outputs and indices (many
+    pairs sharing an index, so terms of several pairs meet in one element): a wave per cloud (at
+    most 64 clouds per side) and a thread per (cloud, feature) (210 x 210 clouds), each after the
+    library's zero fill, into buffers holding garbage, against the reference's scatter loop."""
     B, b1, p1, b2, p2, d = shape
     gen = torch.Generator().manual_seed(17)
     x1 = torch.randn(B, b1, p1, d, generator=gen)

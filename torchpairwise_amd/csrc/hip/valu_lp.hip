@@ -23,6 +23,8 @@
 // is deterministic (the reference accumulates with atomics on its GPU path).
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace tpw {
@@ -197,12 +199,15 @@ __device__ __forceinline__ float fam_finish(float acc, float inv_p, float prev) 
 }
 
 // w: per-feature weights [batch, d] (kWeighted only).  out: read first under kBrayDen.
-// rownum: out = rownum[row] / value (IEEE divide), the signal-to-noise ratio's variance over the
-// pair's squared distance.  out16: the values are stored rounded to bf16 there instead of to
-// out (the cdist of bf16 inputs, computed in fp32 and rounded once).
+// OM (output mode) 2, rownum: out = rownum[row] / value (IEEE divide), the signal-to-noise
+// ratio's variance over the pair's squared distance.  OM 1, out16: the values are stored rounded
+// to bf16 there instead of to out (the cdist of bf16 inputs, computed in fp32 and rounded once).
+// Compile-time, so that OM 0 (the fp32 distances) keeps the code it had without them: as runtime
+// branches they took the p = 1 kernel from 159 to 192 VGPRs (3 -> 2 waves per SIMD) and put the
+// p = 3 kernel's epilogue on the stack (C3 forward 2.03 -> 2.46 ms, manhattan 1.21 -> 1.47 ms).
 // exp_post: out = exp(value * post), the kernel functions exp(-gamma * distance) of
 // rbf_kernel / laplacian_kernel (one rounding per operation, as mul_ then exp_).
-template <int MODE, int PK, bool VEC>
+template <int MODE, int PK, bool VEC, int OM = 0>
 __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
     int64_t n, int64_t m, int64_t d, float p, float inv_p, float *__restrict__ out, int exp_post,
@@ -347,7 +352,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll
                             for (int c = 0; c < 4; ++c) v[c] = expf(v[c] * post);
                         }
-                        if (rownum) {
+                        if constexpr (OM == 2) {
                             const float num = row < n ? rownum[b * n + row] : 0.0f;
 #pragma unroll
                             for (int c = 0; c < 4; ++c) v[c] = __fdiv_rn(num, v[c]);
@@ -362,7 +367,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
                 for (int r = 16 * wave; r < 16 * wave + 16; ++r) {
                     const int64_t row = row0 + 64 * rh + r;
                     if (row < n && col < m) {
-                        if (out16) out16[(b * n + row) * m + col] = f32_to_bf16_rne(st[r * kSt + lane]);
+                        if constexpr (OM == 1) out16[(b * n + row) * m + col] = f32_to_bf16_rne(st[r * kSt + lane]);
                         else store_nt(out + (b * n + row) * m + col, st[r * kSt + lane]);
                     }
                 }
@@ -396,12 +401,12 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll
                 for (int c = 0; c < 4; ++c) v[c] = expf(v[c] * post);
             }
-            if (rownum) {
+            if constexpr (OM == 2) {
                 const float num = rownum[b * n + row];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) v[c] = __fdiv_rn(num, v[c]);
             }
-            if (out16) {
+            if constexpr (OM == 1) {
                 uint16_t *o16 = out16 + (b * n + row) * m;
                 if (vec_store && col + 3 < m) {
                     const uint2 pk = make_uint2((uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16),
@@ -1009,12 +1014,26 @@ int launch_forward(const float *x1, const float *x2, const float *w, int64_t bat
     const bool vec = (d % 4 == 0) && aligned16(x1) && aligned16(x2) && aligned16(out) && aligned16(out16);
     const float pf = (float)p, inv_p = (float)(1.0 / p);
     const LaunchEvents ev = launch_events("lp_forward_kernel");
-    if (vec)
-        hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, true>), grid, dim3(kThreads), 0, s, ev.start, ev.stop, 0, x1, x2,
-                           w, n, m, d, pf, inv_p, out, (int)exp_post, post, rownum, out16);
-    else
-        hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, false>), grid, dim3(kThreads), 0, s, ev.start, ev.stop, 0, x1,
-                           x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post, rownum, out16);
+    auto launch = [&](auto om) {
+        constexpr int OM = decltype(om)::value;
+        if (vec)
+            hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, true, OM>), grid, dim3(kThreads), 0, s, ev.start,
+                                  ev.stop, 0, x1, x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post, rownum, out16);
+        else
+            hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, false, OM>), grid, dim3(kThreads), 0, s, ev.start,
+                                  ev.stop, 0, x1, x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post, rownum, out16);
+    };
+    // the bf16 output exists for the cdist metrics (kRoot), the row-numerator divide for the
+    // signal-to-noise ratio (kSum, p = 2): only those instantiations carry them
+    if (out16) {
+        if constexpr (MODE == kRoot) launch(std::integral_constant<int, 1>{});
+        else TPW_REQUIRE(false, "bf16 output is for the cdist metrics");
+    } else if (rownum) {
+        if constexpr (MODE == kSum && PK == kP2) launch(std::integral_constant<int, 2>{});
+        else TPW_REQUIRE(false, "the row-numerator divide is for the signal-to-noise ratio");
+    } else {
+        launch(std::integral_constant<int, 0>{});
+    }
     return check_launch("lp_forward_kernel");
 }
 

@@ -583,7 +583,7 @@ def main():
             "roofline": {"bound": "valu", "achieved": ops / (k_ms * 1e-3) / 1e12,
                          "peak": PEAK_VALU_LANE_OPS / 1e12, "unit": "Tlane-op/s",
                          "frac": ops / (k_ms * 1e-3) / PEAK_VALU_LANE_OPS,
-                         "kernel": "lp_forward_kernel<0,1,true>", "kernel_ms": k_ms,
+                         "kernel": "lp_forward_kernel<0,1,true,0>", "kernel_ms": k_ms,
                          "convention": "2 VALU lane-ops per pair-feature (v_sub_f32, abs-modified "
                                        "v_add_f32) against the FP32 VALU issue rate with dual "
                                        "issue, 256 CU x 4 SIMD x 32 lanes x 2 x 2.4 GHz = 7.86e13 "

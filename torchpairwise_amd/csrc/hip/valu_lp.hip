@@ -120,11 +120,11 @@ __device__ __forceinline__ float min3_abs(float acc, float d0, float d1) {
 }
 
 // Four independent accumulations of one row value a against four column values b[c], for the
-// p = 1, 2, 3 steps of lp_step, with the same operations and roundings: the four
-// subtractions first, then the four squares (p = 3), then the four accumulates.  A wave's
-// consecutive VALU instructions are then independent; as the compiler orders them (each
-// term's sub, mul and accumulate back to back) the SIMD issues the p = 3 step at about 62 %
-// of its rate at two waves per SIMD, interleaved four ways at about 85 %.
+// p = 1, 2 steps of lp_step, with the same operations and roundings: the four subtractions
+// first, then the four accumulates, so that a wave's consecutive VALU instructions are
+// independent.  The p = 3 and p = +-inf forward steps stay in the compiler's order: there the
+// asm groups made every step wait for all of its LDS reads before the first subtraction, and
+// the kernels ran 2-5 % slower than without them.
 template <int PK>
 __device__ __forceinline__ void lp_step4(float &c0, float &c1, float &c2, float &c3, float a, float b0, float b1,
                                          float b2, float b3) {
@@ -137,7 +137,8 @@ __device__ __forceinline__ void lp_step4(float &c0, float &c1, float &c2, float 
             : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [c0] "+v"(c0), [c1] "+v"(c1),
               [c2] "+v"(c2), [c3] "+v"(c3)
             : [a] "v"(a), [b0] "v"(b0), [b1] "v"(b1), [b2] "v"(b2), [b3] "v"(b3));
-    } else if constexpr (PK == kP2) {
+    } else {
+        static_assert(PK == kP2, "lp_step4: p = 1, 2");
         asm("v_sub_f32 %[t0], %[a], %[b0]\n\tv_sub_f32 %[t1], %[a], %[b1]\n\t"
             "v_sub_f32 %[t2], %[a], %[b2]\n\tv_sub_f32 %[t3], %[a], %[b3]\n\t"
             "v_fmac_f32 %[c0], %[t0], %[t0]\n\tv_fmac_f32 %[c1], %[t1], %[t1]\n\t"
@@ -145,41 +146,7 @@ __device__ __forceinline__ void lp_step4(float &c0, float &c1, float &c2, float 
             : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [c0] "+v"(c0), [c1] "+v"(c1),
               [c2] "+v"(c2), [c3] "+v"(c3)
             : [a] "v"(a), [b0] "v"(b0), [b1] "v"(b1), [b2] "v"(b2), [b3] "v"(b3));
-    } else {
-        static_assert(PK == kP3, "lp_step4: p = 1, 2, 3");
-        float u0, u1, u2, u3;
-        asm("v_sub_f32 %[t0], %[a], %[b0]\n\tv_sub_f32 %[t1], %[a], %[b1]\n\t"
-            "v_sub_f32 %[t2], %[a], %[b2]\n\tv_sub_f32 %[t3], %[a], %[b3]\n\t"
-            "v_mul_f32 %[u0], %[t0], %[t0]\n\tv_mul_f32 %[u1], %[t1], %[t1]\n\t"
-            "v_mul_f32 %[u2], %[t2], %[t2]\n\tv_mul_f32 %[u3], %[t3], %[t3]\n\t"
-            "v_fma_f32 %[c0], %[u0], |%[t0]|, %[c0]\n\tv_fma_f32 %[c1], %[u1], |%[t1]|, %[c1]\n\t"
-            "v_fma_f32 %[c2], %[u2], |%[t2]|, %[c2]\n\tv_fma_f32 %[c3], %[u3], |%[t3]|, %[c3]"
-            : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [u0] "=&v"(u0), [u1] "=&v"(u1),
-              [u2] "=&v"(u2), [u3] "=&v"(u3), [c0] "+v"(c0), [c1] "+v"(c1), [c2] "+v"(c2), [c3] "+v"(c3)
-            : [a] "v"(a), [b0] "v"(b0), [b1] "v"(b1), [b2] "v"(b2), [b3] "v"(b3));
     }
-}
-
-// Four max3 (min3) steps of two features each, the eight subtractions first (the p = +-inf
-// steps of the forward's paired loop, interleaved four ways as lp_step4 is).
-template <bool MAX>
-__device__ __forceinline__ void max3_step4(float &c0, float &c1, float &c2, float &c3, float a0, float a1,
-                                           floatx4 b0, floatx4 b1) {
-    float t0, t1, t2, t3, u0, u1, u2, u3;
-#define TPW_MAX3_BODY(OP)                                                                             \
-    asm("v_sub_f32 %[t0], %[a0], %[p0]\n\tv_sub_f32 %[u0], %[a1], %[q0]\n\t"                           \
-        "v_sub_f32 %[t1], %[a0], %[p1]\n\tv_sub_f32 %[u1], %[a1], %[q1]\n\t"                           \
-        "v_sub_f32 %[t2], %[a0], %[p2]\n\tv_sub_f32 %[u2], %[a1], %[q2]\n\t"                           \
-        "v_sub_f32 %[t3], %[a0], %[p3]\n\tv_sub_f32 %[u3], %[a1], %[q3]\n\t"                           \
-        OP " %[c0], %[c0], |%[t0]|, |%[u0]|\n\t" OP " %[c1], %[c1], |%[t1]|, |%[u1]|\n\t"                \
-        OP " %[c2], %[c2], |%[t2]|, |%[u2]|\n\t" OP " %[c3], %[c3], |%[t3]|, |%[u3]|"                     \
-        : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3), [u0] "=&v"(u0), [u1] "=&v"(u1), \
-          [u2] "=&v"(u2), [u3] "=&v"(u3), [c0] "+v"(c0), [c1] "+v"(c1), [c2] "+v"(c2), [c3] "+v"(c3)     \
-        : [a0] "v"(a0), [a1] "v"(a1), [p0] "v"(b0[0]), [p1] "v"(b0[1]), [p2] "v"(b0[2]), [p3] "v"(b0[3]), \
-          [q0] "v"(b1[0]), [q1] "v"(b1[1]), [q2] "v"(b1[2]), [q3] "v"(b1[3]))
-    if constexpr (MAX) TPW_MAX3_BODY("v_max3_f32");
-    else TPW_MAX3_BODY("v_min3_f32");
-#undef TPW_MAX3_BODY
 }
 
 template <int PK>
@@ -204,14 +171,23 @@ __device__ __forceinline__ float fam_finish(float acc, float inv_p, float prev) 
 // to bf16 there instead of to out (the cdist of bf16 inputs, computed in fp32 and rounded once).
 // Compile-time, so that OM 0 (the fp32 distances) keeps the code it had without them: as runtime
 // branches they took the p = 1 kernel from 159 to 192 VGPRs (3 -> 2 waves per SIMD) and put the
-// p = 3 kernel's epilogue on the stack (C3 forward 2.03 -> 2.46 ms, manhattan 1.21 -> 1.47 ms).
-// exp_post: out = exp(value * post), the kernel functions exp(-gamma * distance) of
-// rbf_kernel / laplacian_kernel (one rounding per operation, as mul_ then exp_).
+// p = 3 kernel's epilogue on the stack (C3 forward 2.03 -> 2.46 ms, manhattan 1.21 -> 1.47 ms);
+// the exp of OM 3 as a runtime branch held the p = 3 kernel at 218 VGPRs (2 waves per SIMD,
+// 158 and 3 without it: 2.06 -> 1.97 ms).
+// OM 3: out = exp(value * post), the kernel functions exp(-gamma * distance) of rbf_kernel /
+// laplacian_kernel (one rounding per operation, as mul_ then exp_).
+// Blocks per CU: p = +-inf holds two features' operands per step (32 VGPRs) and the compiler
+// gives it 204 VGPRs at two blocks; held to three blocks it fits in 168 without scratch, and
+// the third wave per SIMD overlaps one block's output stores with the others' steps
+// (chebyshev 16384^2 x 128: 1.16 -> 1.06 ms).
+template <int PK>
+constexpr int kFwdBlocks = (PK == kPInf || PK == kPNInf) ? 3 : 2;
+
 template <int MODE, int PK, bool VEC, int OM = 0>
-__global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
+__global__ __launch_bounds__(kThreads, kFwdBlocks<PK>) void lp_forward_kernel(
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
-    int64_t n, int64_t m, int64_t d, float p, float inv_p, float *__restrict__ out, int exp_post,
-    float post, const float *__restrict__ rownum, uint16_t *__restrict__ out16) {
+    int64_t n, int64_t m, int64_t d, float p, float inv_p, float *__restrict__ out, float post,
+    const float *__restrict__ rownum, uint16_t *__restrict__ out16) {
     __shared__ float As[kBK][kTile + kPad];
     __shared__ float Bs[kBK][kTile + kPad];
     __shared__ float Wk[MODE == kWeighted ? kBK : 1];
@@ -290,10 +266,10 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
 #pragma unroll
-                    for (int j = 0; j < 8; j += 4)
-                        max3_step4<PK == kPInf>(acc[i][j], acc[i][j + 1], acc[i][j + 2], acc[i][j + 3], av[0][i],
-                                                av[1][i], floatx4{bv[0][j], bv[0][j + 1], bv[0][j + 2], bv[0][j + 3]},
-                                                floatx4{bv[1][j], bv[1][j + 1], bv[1][j + 2], bv[1][j + 3]});
+                    for (int j = 0; j < 8; ++j) {
+                        const float d0 = av[0][i] - bv[0][j], d1 = av[1][i] - bv[1][j];
+                        acc[i][j] = PK == kPInf ? max3_abs(acc[i][j], d0, d1) : min3_abs(acc[i][j], d0, d1);
+                    }
             }
         }
         for (int k = kbeg; k < kmax; ++k) {
@@ -304,7 +280,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
             const float wk = MODE == kWeighted ? Wk[MODE == kWeighted ? k : 0] : 0.0f;
             const float av[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
             const float bv[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-            if constexpr ((MODE == kRoot || MODE == kSum) && (PK == kP1 || PK == kP2 || PK == kP3)) {
+            if constexpr ((MODE == kRoot || MODE == kSum) && (PK == kP1 || PK == kP2)) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -347,7 +323,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
                         floatx4 v;
 #pragma unroll
                         for (int c = 0; c < 4; ++c) v[c] = fam_finish<MODE, PK>(acc[i][4 * h + c], inv_p, prev[c]);
-                        if (exp_post) {
+                        if constexpr (OM == 3) {
 #pragma clang fp contract(off)
 #pragma unroll
                             for (int c = 0; c < 4; ++c) v[c] = expf(v[c] * post);
@@ -396,7 +372,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_forward_kernel(
             floatx4 v;
 #pragma unroll
             for (int c = 0; c < 4; ++c) v[c] = fam_finish<MODE, PK>(acc[i][4 * h + c], inv_p, prev[c]);
-            if (exp_post) {
+            if constexpr (OM == 3) {
 #pragma clang fp contract(off)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) v[c] = expf(v[c] * post);
@@ -1018,14 +994,19 @@ int launch_forward(const float *x1, const float *x2, const float *w, int64_t bat
         constexpr int OM = decltype(om)::value;
         if (vec)
             hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, true, OM>), grid, dim3(kThreads), 0, s, ev.start,
-                                  ev.stop, 0, x1, x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post, rownum, out16);
+                                  ev.stop, 0, x1, x2, w, n, m, d, pf, inv_p, out, post, rownum, out16);
         else
             hipExtLaunchKernelGGL((lp_forward_kernel<MODE, PK, false, OM>), grid, dim3(kThreads), 0, s, ev.start,
-                                  ev.stop, 0, x1, x2, w, n, m, d, pf, inv_p, out, (int)exp_post, post, rownum, out16);
+                                  ev.stop, 0, x1, x2, w, n, m, d, pf, inv_p, out, post, rownum, out16);
     };
     // the bf16 output exists for the cdist metrics (kRoot), the row-numerator divide for the
-    // signal-to-noise ratio (kSum, p = 2): only those instantiations carry them
-    if (out16) {
+    // signal-to-noise ratio (kSum, p = 2), the exp for the laplacian (kRoot, p = 1) and rbf
+    // (kSum, p = 2) kernels: only those instantiations carry them
+    if (exp_post) {
+        if constexpr ((MODE == kRoot && PK == kP1) || (MODE == kSum && PK == kP2))
+            launch(std::integral_constant<int, 3>{});
+        else TPW_REQUIRE(false, "the exp epilogue is for the laplacian and rbf kernels");
+    } else if (out16) {
         if constexpr (MODE == kRoot) launch(std::integral_constant<int, 1>{});
         else TPW_REQUIRE(false, "bf16 output is for the cdist metrics");
     } else if (rownum) {

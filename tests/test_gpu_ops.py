@@ -92,6 +92,38 @@ def test_sqeuclidean_forward_backward():
     assert_close(b.grad, rb.grad, rtol=1e-4, atol=1e-4 * float(rb.grad.abs().max()), what="grad x2")
 
 
+@pytest.mark.parametrize("n,m,d", [(260, 132, 128), (256, 200, 200), (130, 70, 96), (258, 131, 128)])
+def test_sqeuclidean_and_rbf_backward_wide(n, m, d):
+    """The p = 2 power-sum backward above 64 features: the wide kernel (n, m, d multiples of 4;
+    it sums d g and doubles the sum) or, for the ragged shapes, the narrow kernel (2 d g per
+    term).  Gradients against the float64 sum with the derived per-element bound of
+    tests/_gradbound.py: each term 2 (a - b) g carries the subtraction's rounding (c_t = 2 to
+    spare), the accumulation its six-sigma part.  rbf_kernel's backward reaches the same kernel
+    with g' = -gamma exp(-gamma s) g."""
+    from tests import _gradbound as GB
+    print(f"sqeuclidean / rbf backward n={n} m={m} d={d}", flush=True)
+    x1, x2 = randn(n, d, seed=10), randn(m, d, seed=11)
+    g = randn(n, m, seed=12)
+    a, b = x1.to(DEV).requires_grad_(), x2.to(DEV).requires_grad_()
+    gd = g.to(DEV)
+    tp.sqeuclidean_distances(a, b).backward(gd)
+    x1d, x2d, gdd = x1.double(), x2.double(), g.double()
+    # grad_x1[i, k] = sum_j 2 (x1[i, k] - x2[j, k]) g[i, j]; grad_x2 by symmetry with g^T
+    for own, other, gsl, got, nm in ((x1d, x2d, gdd, a.grad, "grad x1"), (x2d, x1d, gdd.T, b.grad, "grad x2")):
+        terms = 2.0 * (own[:, None, :] - other[None, :, :]) * gsl[:, :, None]
+        GB.check(got.cpu(), terms.sum(1), GB.sum_bound(terms, 1, 2.0), f"sqeuclidean {nm}")
+    # rbf: out = exp(-gamma s); the same kernel, its g scaled per pair first
+    a.grad = None
+    b.grad = None
+    out = tp.rbf_kernel(a, b, gamma=0.01)
+    out.backward(gd)
+    ra, rb = x1d.clone().requires_grad_(), x2d.clone().requires_grad_()
+    ref = torch.exp(-0.01 * ((ra[:, None, :] - rb[None, :, :]) ** 2).sum(-1))
+    ref.backward(gdd)
+    assert_close(a.grad, ra.grad, rtol=1e-4, atol=1e-4 * float(ra.grad.abs().max()), what="rbf grad x1")
+    assert_close(b.grad, rb.grad, rtol=1e-4, atol=1e-4 * float(rb.grad.abs().max()), what="rbf grad x2")
+
+
 @pytest.mark.parametrize("fn,p", [("manhattan_distances", 1.0), ("chebyshev_distances", float("inf")),
                                   ("minkowski_distances", 3.0), ("minkowski_distances", 1.5),
                                   ("linf_distances", float("inf")), ("l1_distances", 1.0)])

@@ -577,10 +577,11 @@ template <int MODE, int PK>
 constexpr bool kPrecomputed = (MODE == kRoot && (PK == kP2 || PK == kP3 || PK == kPLt2 || PK == kPGen)) ||
                               (MODE == kWeighted && PK != kP1) || MODE == kBrayDen;
 // The cases the wide kernel serves (above 64 features): the cdist backward at p = 2, 3 and
-// p > 2 in general.  p = inf (a second per-pair array), p = 1 (its sign fast path) and
-// 0 < p < 2 would spill its registers at this width.
+// p > 2 in general, and the p = 2 power sum (sqeuclidean, rbf_kernel).  p = inf (a second
+// per-pair array), p = 1 (its sign fast path) and 0 < p < 2 would spill its registers at this
+// width.
 template <int MODE, int PK>
-constexpr bool kWide = MODE == kRoot && (PK == kP2 || PK == kP3 || PK == kPGen);
+constexpr bool kWide = (MODE == kRoot && (PK == kP2 || PK == kP3 || PK == kPGen)) || (MODE == kSum && PK == kP2);
 
 // VEC: every pointer is 16-byte aligned; four pairs per step with 16-byte accesses, and the
 // len % 4 tail by the first threads.
@@ -691,6 +692,11 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     // from one descriptor per array and stage with loop-invariant lane offsets.
     constexpr bool V4 = FW == kBFeatWide;
     static_assert(!V4 || !kTwo, "the wide kernel stages one per-pair array");
+    // The p = 2 power sum on the wide kernel: its terms 2 d g accumulate as d g (the p = 2
+    // step of the cdist backward, one fma each) and the sum is doubled once at the end.
+    // Doubling is exact, so this differs from summing 2 d g only where a partial sum is
+    // subnormal or overflows.
+    constexpr bool kHalfSum = V4 && MODE == kSum && PK == kP2;
     float rg[kReadG ? 16 : 1], ra0[kReadA0 ? 16 : 1], ra1[kReadA1 ? 16 : 1], rx[kPanelQ];
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -900,7 +906,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
 #pragma unroll
                 for (int r = 0; r < 8; ++r) dv[r] = 0.0f;
             }
-            if constexpr (MODE == kRoot && (PK == kP2 || PK == kP3)) {
+            if constexpr ((MODE == kRoot && (PK == kP2 || PK == kP3)) || kHalfSum) {
 #pragma unroll
                 for (int r = 0; r < 8; ++r)
 #pragma unroll
@@ -926,7 +932,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
 #pragma unroll
         for (int c = 0; c < kCW; ++c) {
             const int64_t k = k0 + feat_of(tx, c);
-            if (k < d) o[i * d + k] = acc[r][c];
+            if (k < d) o[i * d + k] = kHalfSum ? 2.0f * acc[r][c] : acc[r][c];
         }
     }
 }

@@ -224,10 +224,11 @@ __device__ __forceinline__ float finish_small(float c, float pa, float pb, float
             const float prod = A * n00;
             const float den = prod + hR;
             // d <= 2048: n10 + n01 + A + n00 = d bounds n10 n01 and A n00 by d^2 / 4 = 2^20, so
-            // every product and sum is an exact integer, num <= 2^21 and den <= 2^20, inside
-            // div_count's range (den = 0 gives 0 / 0 there, replaced by 0 as below).  Longer
-            // rows: products past 2^24 round, and the general divide.
-            if (df <= 2048.0f) return select_bits(den != 0.0f, div_count(num, den), 0.0f);
+            // every product and sum is an exact integer (the fma's too), num <= 2^21 and
+            // den <= 2^20, inside div_count's range.  den = 0 needs both of its terms 0, so
+            // hR = 0 and num = 0: dividing by max(den, 1) gives that case its 0 without a
+            // select.  Longer rows: products past 2^24 round, and the general divide.
+            if (df <= 2048.0f) return div_count(num, __builtin_fmaxf(__builtin_fmaf(A, n00, hR), 1.0f));
             return select_bits(den != 0.0f, __fdiv_rn(num, den), 0.0f);
         }
     }

@@ -172,6 +172,24 @@ int tpw_pairwise_kernel_backward(const void *grad, const void *x1, const void *x
 int tpw_pairwise_exp_kernel(const float *x1, const float *x2, int64_t batch, int64_t n, int64_t m,
                             int64_t d, int kind, float gamma, float *out, void *stream);
 
+/* grad_x1 [batch, n, d] and grad_x2 [batch, m, d] of tpw_pairwise_exp_kernel's out, given the
+ * upstream grad and that out (fp32 [batch, n, m]).  Each pair's gradient of the distance is
+ * (grad * out) * (-gamma), the reference's exp_ backward and then mul_(-gamma)'s, one rounding
+ * each, followed by the _ppminkowski p = 2 (RBF) or cdist p = 1 (LAPLACIAN) backward.  RBF forms
+ * it while the backward kernel stages its pairs (no N x M array written); LAPLACIAN in one
+ * elementwise pass into the workspace (one N x M write instead of two).  Results equal those
+ * two ATen multiplies followed by tpw_ppminkowski_backward (p = 2) or tpw_lp_distances_backward2
+ * (p = 1) bit for bit.  workspace: tpw_pairwise_exp_kernel_backward_workspace_size(kind, ...)
+ * bytes.  Replaces the autograd chain of the reference's rbf_kernel / laplacian_kernel
+ * composites (pairwise_metrics.cpp:92-110): the backward of exp_ and mul_, then
+ * _ppminkowski_backward (ppminkowski_kernel.cpp:125-160) or PyTorch's _cdist_backward. */
+size_t tpw_pairwise_exp_kernel_backward_workspace_size(int kind, int64_t batch, int64_t n, int64_t m,
+                                                       int64_t d);
+int tpw_pairwise_exp_kernel_backward(const float *grad, const float *out, const float *x1,
+                                     const float *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
+                                     int kind, float gamma, float *grad_x1, float *grad_x2,
+                                     void *workspace, void *stream);
+
 /* Boolean count metrics of tpw_bool_count_metric */
 #define TPW_BMET_HAMMING 0
 #define TPW_BMET_JACCARD 1

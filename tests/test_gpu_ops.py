@@ -124,6 +124,37 @@ def test_sqeuclidean_and_rbf_backward_wide(n, m, d):
     assert_close(b.grad, rb.grad, rtol=1e-4, atol=1e-4 * float(rb.grad.abs().max()), what="rbf grad x2")
 
 
+@pytest.mark.parametrize("kind", [capi.KER_RBF, capi.KER_LAPLACIAN])
+@pytest.mark.parametrize("B,n,m,d", [(1, 260, 132, 128), (2, 130, 70, 96), (1, 258, 131, 40)])
+def test_exp_kernel_backward_fused_matches_composite(kind, B, n, m, d):
+    """tpw_pairwise_exp_kernel_backward forms each pair's gradient (grad * out) * -gamma inside
+    the backward kernel (rbf) or in one elementwise pass (laplacian); the composite multiplies in
+    two ATen passes and calls the distance's backward entry point (tpw_ppminkowski_backward
+    p = 2, tpw_lp_distances_backward2 p = 1).  Same weights, same kernels, same order of sums:
+    bit-identical.  Shapes: the wide kernel (rbf, n, m, d multiples of 4), batched, and ragged
+    rows with d <= 64 (narrow kernels)."""
+    print(f"exp kernel backward kind={kind} B={B} n={n} m={m} d={d}", flush=True)
+    gamma = 0.02 if kind == capi.KER_RBF else 0.05
+    x1 = randn(B, n, d, seed=20).to(DEV)
+    x2 = randn(B, m, d, seed=21).to(DEV)
+    g = randn(B, n, m, seed=22).to(DEV)
+    out = capi.pairwise_exp_kernel(x1, x2, kind, gamma)
+    gx1, gx2 = capi.pairwise_exp_kernel_backward(g, out, x1, x2, kind, gamma)
+    gf = g.mul(out).mul(-gamma)
+    if kind == capi.KER_RBF:
+        rx1, rx2 = capi.family_backward(capi.FAM_PPMINKOWSKI, gf, x1, x2, p=2.0)
+    else:
+        rx1, rx2 = capi.lp_distances_backward2(gf, x1, x2, capi.lp_distances(x1, x2, 1.0), 1.0)
+    assert_equal(gx1, rx1, what="grad x1")
+    assert_equal(gx2, rx2, what="grad x2")
+    # through the public op and autograd (fp32 on the GPU takes the fused route)
+    fn = tp.rbf_kernel if kind == capi.KER_RBF else tp.laplacian_kernel
+    a, b = x1.clone().requires_grad_(), x2.clone().requires_grad_()
+    fn(a, b, gamma=gamma).backward(g)
+    assert_equal(a.grad, rx1, what="autograd grad x1")
+    assert_equal(b.grad, rx2, what="autograd grad x2")
+
+
 @pytest.mark.parametrize("fn,p", [("manhattan_distances", 1.0), ("chebyshev_distances", float("inf")),
                                   ("minkowski_distances", 3.0), ("minkowski_distances", 1.5),
                                   ("linf_distances", float("inf")), ("l1_distances", 1.0)])

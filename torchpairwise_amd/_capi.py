@@ -50,6 +50,8 @@ _SIGNATURES = {
     "tpw_pairwise_inner": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i, _p, _p]),
     "tpw_radius_mask_euclidean": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, C.c_float, _p, _p]),
     "tpw_pairwise_exp_kernel": (_i, [_p, _p, _i64, _i64, _i64, _i64, _i, C.c_float, _p, _p]),
+    "tpw_pairwise_exp_kernel_backward_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64]),
+    "tpw_pairwise_exp_kernel_backward": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, C.c_float, _p, _p, _p, _p]),
     "tpw_pairwise_kernel": (_i, [_p, _p, _i, _i64, _i64, _i64, _i64, _i, C.c_float, C.c_float, _i, _p, _p]),
     "tpw_pairwise_kernel_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _i, C.c_float,
                                           C.c_float, _i, _p, _p, _p, _p]),
@@ -825,3 +827,21 @@ def pairwise_exp_kernel(x1, x2, kind, gamma):
     out = torch.empty((B, n, m), dtype=torch.float32, device=a.device)
     call("tpw_pairwise_exp_kernel", _ptr(a), _ptr(b), B, n, m, d, kind, float(gamma), _ptr(out), _stream())
     return out if x1.dim() == 3 else out[0]
+
+
+def pairwise_exp_kernel_backward(grad, out, x1, x2, kind, gamma):
+    """(grad_x1, grad_x2) of pairwise_exp_kernel's out: the pair gradient (grad * out) * -gamma
+    formed inside the backward kernel."""
+    import torch
+
+    a, b = _as3f(x1), _as3f(x2)
+    B, n, d = a.shape
+    m = b.shape[1]
+    g = grad.contiguous().reshape(B, n, m)
+    o = out.contiguous().reshape(B, n, m)
+    gx1, gx2 = torch.empty_like(a), torch.empty_like(b)
+    ws = torch.empty((max(1, lib().tpw_pairwise_exp_kernel_backward_workspace_size(kind, B, n, m, d)),),
+                     dtype=torch.uint8, device=a.device)
+    call("tpw_pairwise_exp_kernel_backward", _ptr(g), _ptr(o), _ptr(a), _ptr(b), B, n, m, d, kind, float(gamma),
+         _ptr(gx1), _ptr(gx2), _ptr(ws), _stream())
+    return (gx1, gx2) if x1.dim() == 3 else (gx1[0], gx2[0])

@@ -625,13 +625,16 @@ __global__ void pair_weight_kernel(const float *__restrict__ g, const float *__r
 // Under PRE, aux0 / aux1 hold the precomputed weights w1 / w2 and g is not read.  FW is the
 // block's feature width: 64 (thread block 8 rows x 4 features) or 128 (8 x 8, the forward's
 // ratio of LDS reads to VALU work: per j step two 16-byte reads of weights and two of x2 for 64
-// pair-features).
-template <int MODE, int PK, bool TR, bool WGRAD, bool PRE, int FW = kBFeat>
+// pair-features).  EXPG: g is the upstream gradient of out = exp(-gamma * value) (rbf_kernel,
+// laplacian_kernel) and eo that out, staged as a second per-pair array; the weight is formed
+// from (g * eo) * es, es = -gamma, with the two roundings of the exp's and the scalar multiply's
+// backward, so no N x M pass forms that gradient first.
+template <int MODE, int PK, bool TR, bool WGRAD, bool PRE, int FW = kBFeat, bool EXPG = false>
 __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     const float *__restrict__ g, const float *__restrict__ aux0, const float *__restrict__ aux1,
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
     int64_t n, int64_t m, int64_t d, float p, int64_t j_per_split, int64_t batch,
-    float *__restrict__ out) {
+    float *__restrict__ out, const float *__restrict__ eo, float es) {
     constexpr bool kTwo = (MODE == kRoot && PK == kPInf) || MODE == kBrayDen;
     constexpr int kCW = FW / 16;                // features per thread
     constexpr int kWavesPerRow = FW / 64;       // waves staging one x2 panel row
@@ -650,6 +653,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     const float *G = g + b * n * m;
     const float *A0 = aux0 ? aux0 + b * n * m : nullptr;
     const float *A1 = aux1 ? aux1 + b * n * m : nullptr;
+    const float *E = EXPG ? eo + b * n * m : nullptr;
     const float *X1 = x1 + b * n * d;
     const float *X2 = x2 + b * m * d;
 
@@ -684,6 +688,12 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     constexpr bool kReadG = !PRE;                               // upstream grad
     constexpr bool kReadA0 = PRE || (MODE == kRoot && PK != kP1);  // weights, or the distance
     constexpr bool kReadA1 = PRE && kTwo;
+    static_assert(!EXPG || (!PRE && !kTwo && !WGRAD), "the exp-scaled gradient: one weight from g");
+    // the upstream gradient of one pair, exp-scaled under EXPG
+    auto gval = [&](float gv, float ev) {
+        if constexpr (EXPG) return __fmul_rn(__fmul_rn(gv, ev), es);
+        else return gv;
+    };
     // The wide kernel (V4) stages with 16-byte loads instead (its launch requires 16-byte
     // aligned arrays and n, m, d multiples of 4): lane (tid) loads float4 q of a stage at
     //   direct:     row ii = (tid >> 3) + 32 q, columns jj = 4 (tid & 7) + 0..3
@@ -697,7 +707,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     // Doubling is exact, so this differs from summing 2 d g only where a partial sum is
     // subnormal or overflows.
     constexpr bool kHalfSum = V4 && MODE == kSum && PK == kP2;
-    float rg[kReadG ? 16 : 1], ra0[kReadA0 ? 16 : 1], ra1[kReadA1 ? 16 : 1], rx[kPanelQ];
+    float rg[kReadG ? 16 : 1], ra0[kReadA0 ? 16 : 1], ra1[kReadA1 ? 16 : 1], re[EXPG ? 16 : 1], rx[kPanelQ];
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lw_i = TR ? (tid & 127) : (tid >> 5), lw_j = TR ? (tid >> 7) : (tid & 31);
@@ -749,6 +759,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         if constexpr (V4) {
             if constexpr (kReadG) load_pairs4(G, rg, j0);
             if constexpr (kReadA0) load_pairs4(A0, ra0, j0);
+            if constexpr (EXPG) load_pairs4(E, re, j0);
             const int64_t off = j0 * d + k0;
             const auto rs = buffer_over(X2 + off, md - off);
 #pragma unroll
@@ -762,6 +773,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         if constexpr (kReadG) load_pairs(G, rg, j0);
         if constexpr (kReadA0) load_pairs(A0, ra0, j0);
         if constexpr (kReadA1) load_pairs(A1, ra1, j0);
+        if constexpr (EXPG) load_pairs(E, re, j0);
 #pragma unroll
         for (int q = 0; q < kPanelQ; ++q) {
             const int64_t off = (j0 + wv / kWavesPerRow + (4 / kWavesPerRow) * q) * d + k0 + 64 * (wv % kWavesPerRow);
@@ -778,8 +790,8 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
                     const int ii = TR ? 4 * (tid & 31) + e : (tid >> 3) + 32 * q;
                     const int jj = TR ? (tid >> 5) + 8 * q : 4 * (tid & 7) + e;
                     float w1, w2;
-                    pair_weights<MODE, PK>(kReadG ? rg[4 * q + e] : 0.0f, kReadA0 ? ra0[4 * q + e] : 0.0f, 0.0f, p,
-                                           w1, w2);
+                    pair_weights<MODE, PK>(kReadG ? gval(rg[4 * q + e], re[EXPG ? 4 * q + e : 0]) : 0.0f,
+                                           kReadA0 ? ra0[4 * q + e] : 0.0f, 0.0f, p, w1, w2);
                     if constexpr (PRE) w1 = ra0[4 * q + e];
                     wq[e] = (i0 + ii < n && j0 + jj < jend) ? w1 : 0.0f;
                 }
@@ -804,7 +816,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
                     w1 = ra0[q];
                     if constexpr (kTwo) w2 = ra1[q];
                 } else {
-                    pair_weights<MODE, PK>(rg[q], kReadA0 ? ra0[q] : 0.0f, 0.0f, p, w1, w2);
+                    pair_weights<MODE, PK>(gval(rg[q], re[EXPG ? q : 0]), kReadA0 ? ra0[q] : 0.0f, 0.0f, p, w1, w2);
                 }
             }
             Ws[jj][ii] = w1;
@@ -973,6 +985,30 @@ __global__ void column_finish_kernel(const float *__restrict__ part, int64_t chu
     out[t] = s;
 }
 
+// g'[t] = (g[t] * o[t]) * es: the gradient of out = exp(-gamma * dist) with respect to dist,
+// es = -gamma, one rounding per product as the backward of exp_ and then of mul_(-gamma).
+// VEC: 16-byte aligned arrays, four per step, the len % 4 tail by the first threads.
+template <bool VEC>
+__global__ void exp_grad_kernel(const float *__restrict__ g, const float *__restrict__ o, float es, int64_t len,
+                                float *__restrict__ out) {
+    const int64_t start = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t tail = 0;
+    if constexpr (VEC) {
+        const int64_t len4 = len >> 2;
+        for (int64_t t = start; t < len4; t += stride) {
+            const floatx4 gv = reinterpret_cast<const floatx4 *>(g)[t];
+            const floatx4 ov = reinterpret_cast<const floatx4 *>(o)[t];
+            floatx4 r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = __fmul_rn(__fmul_rn(gv[e], ov[e]), es);
+            reinterpret_cast<floatx4 *>(out)[t] = r;
+        }
+        tail = len4 << 2;
+    }
+    for (int64_t t = tail + start; t < len; t += stride) out[t] = __fmul_rn(__fmul_rn(g[t], o[t]), es);
+}
+
 __global__ void fill_kernel(float *__restrict__ p, int64_t len, float v) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t < len) p[t] = v;
@@ -1078,14 +1114,15 @@ int64_t lp_backward_splits(int64_t slots, int64_t batch, int64_t n, int64_t m, i
 int64_t max_slots() { return (int64_t)device_cus() * kMaxBlocksPerCU; }
 
 // grad [batch, n, d] of the first operand (x2's gradient: pass x2 as x1, n <-> m, TR).
-template <int MODE, int PK, bool TR, bool WGRAD, bool PRE, int FW>
+template <int MODE, int PK, bool TR, bool WGRAD, bool PRE, int FW, bool EXPG = false>
 int launch_backward(const float *g, const float *aux0, const float *aux1, const float *x1,
                     const float *x2, const float *w, int64_t batch, int64_t n, int64_t m, int64_t d,
-                    double p, float *grad, float *part, hipStream_t s) {
+                    double p, float *grad, float *part, hipStream_t s, const float *eo = nullptr,
+                    float es = 0.0f) {
     // the direct layout's staging lanes span two rows of m: their byte offsets are 32-bit
     TPW_REQUIRE(TR || 4 * m + 128 < ((int64_t)1 << 32),
                 "backward: %lld columns exceed the kernel's 32-bit staging offsets", (long long)m);
-    auto kern = lp_backward_kernel<MODE, PK, TR, WGRAD, PRE, FW>;
+    auto kern = lp_backward_kernel<MODE, PK, TR, WGRAD, PRE, FW, EXPG>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, 0) != hipSuccess || per_cu <= 0)
         per_cu = 2;
@@ -1095,7 +1132,7 @@ int launch_backward(const float *g, const float *aux0, const float *aux1, const 
     dim3 grid((unsigned)cdiv(d, FW), (unsigned)cdiv(n, kBRows), (unsigned)(splits * batch));
     float *dst = splits > 1 ? part : grad;
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s, g, aux0, aux1, x1, x2, w, n, m, d, (float)p,
-                       jps, batch, dst);
+                       jps, batch, dst, eo, es);
     int rc = check_launch("lp_backward_kernel");
     if (rc != TPW_OK || splits == 1) return rc;
     const int64_t len = batch * n * d;
@@ -1129,9 +1166,11 @@ struct BwdJob {
     double p;
     float *gx1, *gx2, *rows, *part, *wbuf1, *wbuf2;
     bool x1_transposed;  // single-direction call for x2's gradient (x1/x2 already swapped)
+    const float *eo = nullptr;  // exp-scaled gradient (EXPG): the exp kernel's output, and -gamma
+    float es = 0.0f;
 };
 
-template <int MODE, int PK, int FW, bool PRE>
+template <int MODE, int PK, int FW, bool PRE, bool EXPG = false>
 int run_backward_fw(const BwdJob &j, hipStream_t s) {
     // staging reads the per-pair arrays only where the weights need them
     constexpr bool kAux = PRE || (MODE == kRoot && PK != kP1);
@@ -1147,15 +1186,15 @@ int run_backward_fw(const BwdJob &j, hipStream_t s) {
     int rc = TPW_OK;
     if (j.gx1) {
         if (j.x1_transposed)  // n, m are already those of the operand whose grad is wanted
-            rc = launch_backward<MODE, PK, true, false, PRE, FW>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
-                                                              j.m, j.d, j.p, j.gx1, j.part, s);
+            rc = launch_backward<MODE, PK, true, false, PRE, FW, EXPG>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
+                                                                    j.m, j.d, j.p, j.gx1, j.part, s, j.eo, j.es);
         else
-            rc = launch_backward<MODE, PK, false, false, PRE, FW>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
-                                                               j.m, j.d, j.p, j.gx1, j.part, s);
+            rc = launch_backward<MODE, PK, false, false, PRE, FW, EXPG>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
+                                                                     j.m, j.d, j.p, j.gx1, j.part, s, j.eo, j.es);
     }
     if (rc == TPW_OK && j.gx2)
-        rc = launch_backward<MODE, PK, true, false, PRE, FW>(j.g, a0, a1, j.x2, j.x1, j.w, j.batch, j.m, j.n,
-                                                          j.d, j.p, j.gx2, j.part, s);
+        rc = launch_backward<MODE, PK, true, false, PRE, FW, EXPG>(j.g, a0, a1, j.x2, j.x1, j.w, j.batch, j.m, j.n,
+                                                                j.d, j.p, j.gx2, j.part, s, j.eo, j.es);
     if constexpr (MODE == kWeighted) {
         if (rc == TPW_OK && j.rows)
             rc = launch_backward<MODE, PK, false, true, PRE, FW>(j.g, a0, a1, j.x1, j.x2, j.w, j.batch, j.n,
@@ -1166,14 +1205,15 @@ int run_backward_fw(const BwdJob &j, hipStream_t s) {
 
 // The wide kernel above 64 features where it serves the case and its 16-byte staging fits
 // (aligned arrays, n, m and d multiples of 4); else the narrow one.
-template <int MODE, int PK>
+template <int MODE, int PK, bool EXPG = false>
 int run_backward(const BwdJob &j, hipStream_t s) {
     if constexpr (kWide<MODE, PK>) {
         const bool fits = j.d > kBFeat && j.n % 4 == 0 && j.m % 4 == 0 && j.d % 4 == 0 && aligned16(j.g) &&
-                          aligned16(j.aux0) && aligned16(j.x1) && aligned16(j.x2);
-        if (fits) return run_backward_fw<MODE, PK, kBFeatWide, false>(j, s);
+                          aligned16(j.aux0) && aligned16(j.x1) && aligned16(j.x2) && aligned16(j.eo);
+        if (fits) return run_backward_fw<MODE, PK, kBFeatWide, false, EXPG>(j, s);
     }
-    return run_backward_fw<MODE, PK, kBFeat, kPrecomputed<MODE, PK>>(j, s);
+    static_assert(!EXPG || !kPrecomputed<MODE, PK>, "the exp-scaled gradient is formed while staging");
+    return run_backward_fw<MODE, PK, kBFeat, kPrecomputed<MODE, PK>, EXPG>(j, s);
 }
 
 template <int MODE>
@@ -1512,4 +1552,46 @@ extern "C" int tpw_pairwise_exp_kernel(const float *x1, const float *x2, int64_t
     if (kind == TPW_KER_RBF)  // sqeuclidean = _ppminkowski p = 2: sum of squares, no root
         return launch_forward<kSum, kP2>(x1, x2, nullptr, batch, n, m, d, 2.0, out, s, true, post);
     return launch_forward<kRoot, kP1>(x1, x2, nullptr, batch, n, m, d, 1.0, out, s, true, post);
+}
+
+extern "C" size_t tpw_pairwise_exp_kernel_backward_workspace_size(int kind, int64_t batch, int64_t n, int64_t m,
+                                                                 int64_t d) {
+    return workspace_layout(kind == TPW_KER_RBF ? TPW_FAM_PPMINKOWSKI : kLpMetric, batch, n, m, d).total;
+}
+
+extern "C" int tpw_pairwise_exp_kernel_backward(const float *grad, const float *out, const float *x1,
+                                                const float *x2, int64_t batch, int64_t n, int64_t m, int64_t d,
+                                                int kind, float gamma, float *grad_x1, float *grad_x2,
+                                                void *workspace, void *stream) {
+    TPW_REQUIRE(kind == TPW_KER_RBF || kind == TPW_KER_LAPLACIAN, "unknown kernel %d", kind);
+    const int metric = kind == TPW_KER_RBF ? TPW_FAM_PPMINKOWSKI : kLpMetric;
+    TPW_FAM_BWD_PROLOGUE(metric);
+    if (n == 0 || m == 0) {
+        int rc = fill(grad_x1, batch * n * d, 0.0f, s);
+        return rc != TPW_OK ? rc : fill(grad_x2, batch * m * d, 0.0f, s);
+    }
+    TPW_REQUIRE(grad && out && x1 && x2 && grad_x1 && grad_x2, "null pointer");
+    // each pair's gradient of the distance is (grad * out) * (-gamma), the backward of exp_ and
+    // then of mul_(-gamma); then the sqeuclidean (_ppminkowski p = 2) or cdist p = 1 backward
+    if (kind == TPW_KER_RBF) {
+        // formed while the backward kernel stages its pairs: no N x M array is written
+        BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 2.0, grad_x1, grad_x2, nullptr, part,
+                 nullptr, nullptr, false, out, -gamma};
+        return run_backward<kSum, kP2, true>(j, s);
+    }
+    // p = 1: a second per-pair array would take the narrow kernel past three waves per SIMD
+    // (156 -> 174 VGPRs), so one elementwise pass writes the gradients into the workspace
+    const int64_t len = batch * n * m;
+    const bool vec = aligned16(grad) && aligned16(out) && aligned16(pair1);
+    const unsigned grid = (unsigned)(cdiv(vec ? cdiv(len, 4) : len, 256) < 16384 ? cdiv(vec ? cdiv(len, 4) : len, 256)
+                                                                                  : 16384);
+    if (vec)
+        hipLaunchKernelGGL(exp_grad_kernel<true>, dim3(grid), dim3(256), 0, s, grad, out, -gamma, len, pair1);
+    else
+        hipLaunchKernelGGL(exp_grad_kernel<false>, dim3(grid), dim3(256), 0, s, grad, out, -gamma, len, pair1);
+    const int rc = check_launch("exp_grad_kernel");
+    if (rc != TPW_OK) return rc;
+    BwdJob j{pair1, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1, grad_x2, nullptr, part,
+             nullptr, nullptr, false};
+    return run_backward<kRoot, kP1>(j, s);
 }

@@ -564,6 +564,29 @@ at::Tensor exp_kernel_cuda(const at::Tensor &x1, const at::Tensor &x2, int64_t k
     return unbatch(out, ub).to(x1.scalar_type());
 }
 
+// Gradients of exp_kernel_cuda's out for fp32 operands: the pair gradient (grad * out) * -gamma
+// formed inside the backward kernel (rbf) or in one elementwise pass (laplacian) by
+// tpw_pairwise_exp_kernel_backward, instead of two ATen passes.
+std::tuple<at::Tensor, at::Tensor> exp_kernel_backward_cuda(const at::Tensor &grad, const at::Tensor &x1,
+                                                            const at::Tensor &x2, const at::Tensor &out,
+                                                            int64_t kind, double gamma) {
+    const char *from = "_pw_exp_kernel_backward";
+    const bool ub = check_family_shapes(from, x1, x2, nullptr);
+    DeviceGuard guard(x1.device());
+    auto a = batched(gpu_f32(x1, from), ub), bb = batched(gpu_f32(x2, from), ub);
+    const int64_t B = a.size(0), n = a.size(1), m = bb.size(1), d = a.size(2);
+    auto g = grad.to(at::kFloat).reshape({B, n, m}).contiguous();
+    auto o = out.to(at::kFloat).reshape({B, n, m}).contiguous();
+    auto gx1 = at::empty_like(a), gx2 = at::empty_like(bb);
+    auto ws = workspace(tpw_pairwise_exp_kernel_backward_workspace_size((int)kind, B, n, m, d), a);
+    check_rc(tpw_pairwise_exp_kernel_backward(g.data_ptr<float>(), o.data_ptr<float>(), a.data_ptr<float>(),
+                                              bb.data_ptr<float>(), B, n, m, d, (int)kind, (float)gamma,
+                                              gx1.data_ptr<float>(), gx2.data_ptr<float>(), ws.data_ptr(),
+                                              current_stream()),
+             from);
+    return {unbatch(gx1, ub), unbatch(gx2, ub)};
+}
+
 // ------------------------------------------------------------------------ dispatcher handles
 template <typename Sig>
 c10::TypedOperatorHandle<Sig> op_handle(const char *name) {
@@ -693,6 +716,13 @@ class ExpKernelFunction : public torch::autograd::Function<ExpKernelFunction> {
     static variable_list backward(AutogradContext *ctx, const variable_list &grad) {
         auto s = ctx->get_saved_variables();
         const double gamma = ctx->saved_data["gamma"].toDouble();
+        if (s[0].is_cuda() && s[0].scalar_type() == at::kFloat && s[1].scalar_type() == at::kFloat &&
+            grad[0].scalar_type() == at::kFloat) {
+            // fp32 on the GPU: (grad * out) * -gamma inside the C entry point, the same two
+            // roundings as the composite below
+            auto r = exp_kernel_backward_cuda(grad[0], s[0], s[1], s[2], ctx->saved_data["kind"].toInt(), gamma);
+            return {std::get<0>(r), std::get<1>(r), Variable(), Variable()};
+        }
         auto gf = grad[0].mul(s[2]).mul(-gamma);
         if (ctx->saved_data["kind"].toInt() == TPW_KER_RBF) {
             T2 r = ppminkowski_backward_op(gf, s[0], s[1], 2.0);  // 16-bit types via fp32 inside

@@ -49,7 +49,7 @@ PEAK_HBM = 8.0e12
 # (two VALU instructions of a wave pair per clock): the dual-issue rate
 PEAK_VALU_LANE_OPS = 256 * 4 * 32 * 2.4e9
 # the headline's dominant kernel as rocprofv3 names it (euclidean epilogue, fp32 in and out)
-HEADLINE_KERNEL = "inner_tile_kernel<float,float,1,1,false,false>"
+HEADLINE_KERNEL = "inner_tile_kernel<float,float,1,1,false,false,false>"
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "traffic_euclidean_manhattan_hamming_16384x128.txt")
 

@@ -206,8 +206,10 @@ def test_backward_products_tile_fp32(name, kw, B, n, m, d):
 # the path that inputs offset by one element take (W^T and transposed copies of x1, x2
 # written first, and the register-staged kernel for their misaligned X); bar: the bf16 tolerance
 # against float64 autograd, 1e-2 (+ 1e-2 * max), and the two device paths within one bf16 ulp of
-# each other (2^-7 relative, the ulp of values in [1, 2), + 1e-3 * max)
-@pytest.mark.parametrize("B,n,m,d", [(2, 128, 192, 64), (1, 1088, 1024, 72), (1, 256, 128, 264)])
+# each other (2^-7 relative, the ulp of values in [1, 2), + 1e-3 * max).  (1, 128, 65536, 256):
+# grad_x2's product (M = 65536, N = 256, K = 128) has 512 tiles of 128 x 256, enough to fill the
+# GPU, and takes the 128 x 256 bf16 product kernel
+@pytest.mark.parametrize("B,n,m,d", [(2, 128, 192, 64), (1, 1088, 1024, 72), (1, 256, 128, 264), (1, 128, 65536, 256)])
 @pytest.mark.parametrize("name", ["euclidean_distances", "cosine_distances", "polynomial_kernel", "sigmoid_kernel"])
 def test_backward_products_kmajor_bf16(name, B, n, m, d):
     import torchpairwise_amd as tp

@@ -689,7 +689,9 @@ __global__ __launch_bounds__(tile::kThreads, NB == 1 ? 4 : 2) void inner_tile_ke
                     }
                 }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = sign * acc[mi][ni][4 * g + e] + a1v[mi] * xv[e];
+                // one rounding for the coefficient product, one for the sum (as an explicit fma: the
+                // compiler contracted the sum either way within one kernel)
+                for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(sign, acc[mi][ni][4 * g + e], a1v[mi] * xv[e]);
             } else {
                 const floatx4 a2 = kAux2<EPI> ? *reinterpret_cast<const floatx4 *>(&s_aux[kT + wc + ni * 32 + 8 * g + 4 * h])
                                               : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -997,6 +999,137 @@ int launch_grad_product(const T *A, const T *B, int64_t batch, int64_t M, int64_
     return check_launch("inner_tile_kernel");
 }
 
+// Compute units of the current device (256 when the query fails), per device.
+static int64_t cu_count() {
+    static int cache[16];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+    int &c = cache[dev & 15];
+    if (c == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        c = cus;
+    }
+    return c;
+}
+
+// The bf16 gradient product of launch_grad_product (out = sign * A'B + coef[row] * X, kEpiGrad,
+// or with coef the row sums of A, kEpiGradA) for both operands k-major (A: [K, M], B: [K, N])
+// on 128 x 256 output tiles, 2 x 2 waves of 64 x 128.  Each wave feeds eight 32x32x16 products
+// per 16-K step from six transposed 16-byte pieces (the 128 x 128 tile kernel's waves: four
+// products from four pieces), and a 64-row K chunk moves 48 KiB into LDS for 128 x 256 outputs
+// (the tile kernel 64 KiB).  The products, their order (chunks, then the four 16-K steps), the
+// row sums of A (in K order) and the epilogue's fma are the tile kernel's, so the outputs are
+// the same bit for bit.  M % 128 == 0, N % 256 == 0, K % 64 == 0.  C2 bf16 backward: euclidean
+// 1.11 -> 1.07 ms, cosine 1.185 -> 1.135 ms (same box).
+template <int EPI>
+__global__ __launch_bounds__(tile::kThreads, 2) void grad_wide_bf16_kernel(
+    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, int64_t M, int64_t N, int64_t K,
+    const float *__restrict__ coef, const uint16_t *__restrict__ X, uint16_t *__restrict__ out, int64_t tiles_n,
+    int64_t tiles_c, int64_t total, float sign) {
+    using namespace tile;
+    constexpr int kAP = 1024, kBP = 2048, kBufW = kAP + kBP;  // uint4 per A / B panel, per buffer
+    __shared__ uint4 smem[kBufW];  // 48 KiB: two blocks per CU
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 128;  // 2 x 2 waves of 64 x 128
+    const int l32 = lane & 31, h = lane >> 5;
+    const int grp = ((lane >> 4) & 1) * 16;
+    int64_t b, tr, tc;
+    xcd_tile_of(blockIdx.x, tiles_n, tiles_c, total, b, tr, tc);
+    const int64_t row0 = tr * kT, col0 = tc * 256;
+    const uint8_t *Ab = reinterpret_cast<const uint8_t *>(A + b * K * M);
+    const uint8_t *Bb = reinterpret_cast<const uint8_t *>(B + b * K * N);
+    // 12 DMA slots per lane and chunk: slot s = (12 wave + j) 64 + lane, A's 1024 first (K row
+    // s / 16, position s % 16), then B's 2048 (K row s' / 32, position s' % 32); the piece at
+    // position p of K row kr is logical piece p ^ 4 (kr & 3), the layout kpiece_bf16 reads; a
+    // wave's 64 slots of one j lie in one panel
+    uint32_t off[12];
+#pragma unroll
+    for (int j = 0; j < 12; ++j) {
+        const int s = (wave * 12 + j) * 64 + lane;
+        if (s < kAP) {
+            const int kr = s >> 4, lp = (s & 15) ^ (4 * (kr & 3));
+            off[j] = (uint32_t)(kr * M * 2 + (row0 + 8 * lp) * 2);
+        } else {
+            const int t = s - kAP, kr = t >> 5, lp = (t & 31) ^ (4 * (kr & 3));
+            off[j] = (uint32_t)(kr * N * 2 + (col0 + 8 * lp) * 2);
+        }
+    }
+    auto dma = [&](int kc, uint4 *buf) {
+#pragma unroll
+        for (int j = 0; j < 12; ++j) {
+            const int first = (wave * 12 + j) * 64;
+            const uint8_t *base = first < kAP ? Ab + (int64_t)kc * 64 * M * 2 : Bb + (int64_t)kc * 64 * N * 2;
+            dma16(base, off[j], lds_addr(buf + first));
+        }
+    };
+    floatx16 acc[2][4];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
+    float rsum[2] = {0.0f, 0.0f};
+    const int nchunks = (int)(K / 64);
+    dma(0, smem);
+    for (int kc = 0; kc < nchunks; ++kc) {
+        if (kc > 0) {
+            barrier_lds();  // every wave is done with chunk kc - 1
+            dma(kc, smem);
+        }
+        barrier_all();  // chunk kc has landed
+        const uint4 *As = smem, *Bs = As + kAP;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint4 a[2], bv[4];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) a[mi] = kpiece_bf16<256>(As, wr + mi * 32 + grp, lane, h, q);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) bv[ni] = kpiece_bf16<512>(Bs, wc + ni * 32 + grp, lane, h, q);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, bv[ni]), __builtin_bit_cast(bf16x8, a[mi]), acc[mi][ni], 0, 0, 0);
+            if constexpr (EPI == kEpiGradA) {
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi) {
+                    const uint32_t w4[4] = {a[mi].x, a[mi].y, a[mi].z, a[mi].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        rsum[mi] += __uint_as_float(w4[e] << 16);
+                        rsum[mi] += __uint_as_float(w4[e] & 0xffff0000u);
+                    }
+                }
+            }
+        }
+    }
+    barrier_lds();  // the buffer becomes the output stage
+    uint4 *sl = smem + wave * 512;  // 8 KiB per wave
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+        const int64_t row = row0 + wr + mi * 32 + l32;
+        const float a1v = EPI == kEpiGradA ? rsum[mi] + __shfl_xor(rsum[mi], 32, 64) : coef[b * M + row];
+        store_wave_rows_bf16<4>(
+            sl,
+            [&](int ni, int gq) {
+                const int64_t col = col0 + wc + ni * 32 + 8 * gq + 4 * h;
+                const uint2 qv = *reinterpret_cast<const uint2 *>(X + (b * M + row) * N + col);
+                const floatx4 xv = {__uint_as_float(qv.x << 16), __uint_as_float(qv.x & 0xffff0000u),
+                                    __uint_as_float(qv.y << 16), __uint_as_float(qv.y & 0xffff0000u)};
+                floatx4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(sign, acc[mi][ni][4 * gq + e], a1v * xv[e]);
+                return o;
+            },
+            out, b, row0 + wr + mi * 32, col0 + wc, M, N);
+    }
+}
+
 bool grad_product_f32_fits(const float *A, bool a_kmajor, const float *B, bool b_kmajor, int64_t M, int64_t N,
                            int64_t K, const float *X, const float *out) {
     return grad_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out);
@@ -1024,6 +1157,20 @@ int grad_product_bf16(const uint16_t *A, bool a_kmajor, const uint16_t *B, bool 
                       hipStream_t s) {
     TPW_REQUIRE(grad_fits(A, a_kmajor, B, b_kmajor, M, N, K, X, out), "unsupported product shape");
     TPW_REQUIRE(b_kmajor, "k-contiguous B: inner_grad_gemm");
+    // 128 x 256 tiles where they fill every CU with two blocks (else the 128 x 128 kernel's
+    // grid is the larger one); offsets within a batch below 2^32 bytes
+    const int64_t wide_tiles = (M / 128) * (N / 256) * batch;
+    if (a_kmajor && M % 128 == 0 && N % 256 == 0 && K % 64 == 0 && K * M * 2 < ((int64_t)1 << 32) &&
+        K * N * 2 < ((int64_t)1 << 32) && wide_tiles >= 2 * cu_count()) {
+        const LaunchEvents ev = launch_events("grad_wide_bf16_kernel");
+        if (coef == nullptr)
+            hipExtLaunchKernelGGL((grad_wide_bf16_kernel<kEpiGradA>), dim3((unsigned)wide_tiles), dim3(tile::kThreads), 0,
+                                  s, ev.start, ev.stop, 0, A, B, M, N, K, coef, X, out, M / 128, N / 256, wide_tiles, sign);
+        else
+            hipExtLaunchKernelGGL((grad_wide_bf16_kernel<kEpiGrad>), dim3((unsigned)wide_tiles), dim3(tile::kThreads), 0,
+                                  s, ev.start, ev.stop, 0, A, B, M, N, K, coef, X, out, M / 128, N / 256, wide_tiles, sign);
+        return check_launch("grad_wide_bf16_kernel");
+    }
     if (coef == nullptr)
         return a_kmajor
                    ? launch_grad_product<uint16_t, kEpiGradA, true, true>(A, B, batch, M, N, K, sign, coef, X, out, s)

@@ -122,8 +122,15 @@ def public_dtype_cases():
     return out
 
 
-def dtype_tolerance(dtype):
-    return {torch.float64: 1e-10, torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 3e-2}.get(dtype, 0.0)
+def dtype_tolerance(dtype, op=None):
+    """The bar for a floating output of `op` in `dtype` against the reference's own result in the
+    same dtype.  bfloat16 Mahalanobis takes 3e-2: the reference's loop
+    (cpu/sqmahalanobis_kernel.cpp:23-29) adds the quadratic form's d^2 terms (256 at d = 16)
+    into a bfloat16 variable, rounding to 8 significant bits after every addition, while this
+    build accumulates in float32; every other op and dtype pair holds 1e-2."""
+    if op == "mahalanobis_distances" and dtype == torch.bfloat16:
+        return 3e-2
+    return {torch.float64: 1e-10, torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}.get(dtype, 0.0)
 
 
 CDIST_METRICS = ["braycurtis", "canberra", "chebyshev", "cityblock", "correlation", "cosine", "dice",

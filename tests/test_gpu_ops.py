@@ -889,7 +889,7 @@ def test_public_ops_dtypes_gpu_equal_reference(tmp_path):
             if case["op"] == "euclidean_distances" and len(case["args"]) == 1 and dt.is_floating_point:
                 a = t["a"].double()
                 floor = 4 * float((torch.finfo(dt).eps * 2 * (a * a).sum(-1).max()) ** 0.5)
-            _dtype_sweep_compare(ours, r, what, floor)
+            _dtype_sweep_compare(ours, r, what, floor, op=case["op"])
         except AssertionError as e:
             failures.append(str(e).splitlines()[0][:300])
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures[:30])

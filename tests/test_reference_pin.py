@@ -188,7 +188,7 @@ def _check_public_cases(ops, device, tmp_path, rtol=1e-5, grad_rtol=1e-5):
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures)
 
 
-def _dtype_sweep_compare(ours, ref, what, floor=0.0):
+def _dtype_sweep_compare(ours, ref, what, floor=0.0, op=None):
     """Errors equal; bool / integer outputs equal; floating outputs within the dtype's bar
     (NaN positions equal)."""
     from tests._public_cases import dtype_tolerance
@@ -206,7 +206,7 @@ def _dtype_sweep_compare(ours, ref, what, floor=0.0):
         on, rn = torch.isnan(o), torch.isnan(r)
         assert torch.equal(on, rn), f"{what}[{k}]: NaN positions differ"
         of, rf = o.double().masked_fill(on, 0), r.double().masked_fill(rn, 0)
-        tol = dtype_tolerance(o.dtype)
+        tol = dtype_tolerance(o.dtype, op)
         atol = tol * max(1.0, float(rf.abs().max())) + floor
         assert torch.allclose(of, rf, rtol=tol, atol=atol), f"{what}[{k}]: max diff {float((of - rf).abs().max())}"
 
@@ -226,7 +226,7 @@ def test_public_ops_dtypes_cpu_equal_reference(tmp_path):
     for (case, t), r in zip(cs, ref):
         what = f"{case['op']} {[str(v.dtype) for v in t.values()]} {[tuple(v.shape) for v in t.values()]}"
         try:
-            _dtype_sweep_compare(ref_runner.run_op_case(ops, case, t, "cpu"), r, what)
+            _dtype_sweep_compare(ref_runner.run_op_case(ops, case, t, "cpu"), r, what, op=case["op"])
         except AssertionError as e:
             failures.append(str(e).splitlines()[0][:300])
     assert not failures, f"{len(failures)} of {len(cs)} cases differ:\n" + "\n".join(failures[:30])

@@ -216,6 +216,38 @@ def test_lp_backward_p1_sign_exact(entry):
     assert_equal(gx2.cpu(), torch.from_numpy(_sign_counts(b, a).astype(np.float32)), "p=1 grad_x2")
 
 
+@pytest.mark.parametrize("outside", [False, True])
+@pytest.mark.parametrize("entry", ["single", "both"])
+def test_lp_backward_p1_wide_gated(entry, outside):
+    """p = 1 above 64 features with n, m, d multiples of 4 (here 128): a range scan of x1 and x2
+    picks the wide kernel's pre-scaled sign path (every value in the scalable range: ties,
+    neighbours one ulp apart and the range's ends 2^-52, 2^52) or, with one value outside
+    (`outside`: 2^-60, a denormal, 2^60, inf or NaN), the narrow kernel with its per-tile test;
+    both are launched with the same split count.  grad = 1 makes every gradient an integer
+    count: sign counts bit for bit either way."""
+    n, m, d = 300, 1100, 128
+    rng = np.random.default_rng(12)
+    a = (rng.integers(-8, 9, size=(n, d)) * 0.125).astype(np.float32)
+    b = (rng.integers(-8, 9, size=(m, d)) * 0.125).astype(np.float32)
+    one_up = np.nextafter(np.float32(1.0), np.float32(2.0))
+    a[140, 0], b[50, 0], b[51, 0], b[52, 0] = 1.0, one_up, 1.0, np.nextafter(np.float32(1), np.float32(0))
+    lo, hi = np.float32(2.0 ** -52), np.float32(2.0 ** 52)
+    a[150, 1], a[151, 1], b[60, 1], b[61, 1] = lo, -lo, np.nextafter(lo, np.float32(1)), hi
+    a[152, 127], b[62, 127], b[63, 127] = hi, np.nextafter(hi, np.float32(0)), -hi
+    if outside:
+        a[5, 3] = np.float32(2.0 ** -60)
+        b[330, 100] = np.nan
+        b[610, 40], b[611, 41] = np.inf, -np.inf
+        b[1000, 2] = np.float32(1e-40)
+    x1, x2 = torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV)
+    g = torch.ones(n, m, device=DEV)
+    dist = capi.lp_distances(x1, x2, 1.0)
+    fn = capi.lp_distances_backward if entry == "single" else capi.lp_distances_backward2
+    gx1, gx2 = fn(g, x1, x2, dist, 1.0)
+    assert_equal(gx1.cpu(), torch.from_numpy(_sign_counts(a, b).astype(np.float32)), "p=1 grad_x1")
+    assert_equal(gx2.cpu(), torch.from_numpy(_sign_counts(b, a).astype(np.float32)), "p=1 grad_x2")
+
+
 # --------------------------------------------------------------------------------------
 # inner-product backward
 # --------------------------------------------------------------------------------------

@@ -578,8 +578,8 @@ constexpr bool kPrecomputed = (MODE == kRoot && (PK == kP2 || PK == kP3 || PK ==
                               (MODE == kWeighted && PK != kP1) || MODE == kBrayDen;
 // The cases the wide kernel serves (above 64 features): the cdist backward at p = 2, 3 and
 // p > 2 in general, and the p = 2 power sum (sqeuclidean, rbf_kernel).  p = inf (a second
-// per-pair array), p = 1 (its sign fast path) and 0 < p < 2 would spill its registers at this
-// width.
+// per-pair array) and 0 < p < 2 would spill its registers at this width; p = 1 takes it only
+// through run_backward_p1_gated (the sign path alone, chosen by a range scan).
 template <int MODE, int PK>
 constexpr bool kWide = (MODE == kRoot && (PK == kP2 || PK == kP3 || PK == kPGen)) || (MODE == kSum && PK == kP2);
 
@@ -628,13 +628,17 @@ __global__ void pair_weight_kernel(const float *__restrict__ g, const float *__r
 // pair-features).  EXPG: g is the upstream gradient of out = exp(-gamma * value) (rbf_kernel,
 // laplacian_kernel) and eo that out, staged as a second per-pair array; the weight is formed
 // from (g * eo) * es, es = -gamma, with the two roundings of the exp's and the scalar multiply's
-// backward, so no N x M pass forms that gradient first.
+// backward, so no N x M pass forms that gradient first.  gate: when not null, the block runs
+// only if *gate == gate_run (two instances of one backward launched together, a flag set by an
+// earlier launch choosing which one computes).
 template <int MODE, int PK, bool TR, bool WGRAD, bool PRE, int FW = kBFeat, bool EXPG = false>
 __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     const float *__restrict__ g, const float *__restrict__ aux0, const float *__restrict__ aux1,
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ w,
     int64_t n, int64_t m, int64_t d, float p, int64_t j_per_split, int64_t batch,
-    float *__restrict__ out, const float *__restrict__ eo, float es) {
+    float *__restrict__ out, const float *__restrict__ eo, float es, const uint32_t *__restrict__ gate,
+    uint32_t gate_run) {
+    if (gate != nullptr && __builtin_amdgcn_readfirstlane(*gate) != gate_run) return;
     constexpr bool kTwo = (MODE == kRoot && PK == kPInf) || MODE == kBrayDen;
     constexpr int kCW = FW / 16;                // features per thread
     constexpr int kWavesPerRow = FW / 64;       // waves staging one x2 panel row
@@ -707,6 +711,11 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     // Doubling is exact, so this differs from summing 2 d g only where a partial sum is
     // subnormal or overflows.
     constexpr bool kHalfSum = V4 && MODE == kSum && PK == kP2;
+    // p = 1 on the wide kernel: only the pre-scaled sign path (sign_scaled), launched where every
+    // value of x1 and x2 lies in the scalable range (sign_range_kernel); x1 is scaled once, the
+    // x2 panel as it is staged.  The narrow kernel's per-tile test and its signf path would not
+    // fit the wide kernel's registers.
+    constexpr bool kSignOnly = V4 && PK == kP1 && (MODE == kRoot || MODE == kSum) && !WGRAD;
     float rg[kReadG ? 16 : 1], ra0[kReadA0 ? 16 : 1], ra1[kReadA1 ? 16 : 1], re[EXPG ? 16 : 1], rx[kPanelQ];
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -802,8 +811,9 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
 #pragma unroll
                     for (int e = 0; e < 4; ++e) Ws[4 * (tid & 7) + e][(tid >> 3) + 32 * q] = wq[e];
                 }
+                const float sc = kSignOnly ? kSignScale : 1.0f;  // exact in the scalable range
                 *reinterpret_cast<floatx4 *>(&Xs[(tid >> 5) + 8 * q][4 * (tid & 31)]) =
-                    floatx4{rx[4 * q], rx[4 * q + 1], rx[4 * q + 2], rx[4 * q + 3]};
+                    floatx4{rx[4 * q] * sc, rx[4 * q + 1] * sc, rx[4 * q + 2] * sc, rx[4 * q + 3] * sc};
             }
             return;
         }
@@ -844,7 +854,12 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     constexpr bool kSignFast = PK == kP1 && (MODE == kRoot || MODE == kSum) && !WGRAD;
     __shared__ int flags[3];
     bool tile_fast = false, xv_scaled = false;  // xv holds x1 * 2^75 while xv_scaled
-    if constexpr (kSignFast) {
+    if constexpr (kSignOnly) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int c = 0; c < kCW; ++c) xv[r][c] *= kSignScale;
+    } else if constexpr (kSignFast) {
         bool ok = true;
 #pragma unroll
         for (int r = 0; r < 8; ++r)
@@ -859,7 +874,7 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
     int stage = 0;
     for (int64_t j0 = jbeg; j0 < jend; j0 += kBJ, ++stage) {
         store(j0);
-        if constexpr (kSignFast) {
+        if constexpr (kSignFast && !kSignOnly) {
             bool ok = true;
 #pragma unroll
             for (int q = 0; q < kPanelQ; ++q) ok = ok && sign_scalable(rx[q]);
@@ -869,7 +884,24 @@ __global__ __launch_bounds__(kThreads, 2) void lp_backward_kernel(
         __syncthreads();
         if (j0 + kBJ < jend) load(j0 + kBJ);
         const int jmax = jend - j0 < kBJ ? (int)(jend - j0) : kBJ;
-        if constexpr (kSignFast) {
+        if constexpr (kSignOnly) {
+            for (int jj = 0; jj < jmax; ++jj) {
+                const floatx4 w0 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty]);
+                const floatx4 w1 = *reinterpret_cast<const floatx4 *>(&Ws[jj][8 * ty + 4]);
+                float x[kCW];
+                load_panel(x, jj, tx);
+                const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+#pragma unroll
+                    for (int c = 0; c < kCW; c += 4)
+                        grad_step4<kP1, true>(acc[r][c], acc[r][c + 1], acc[r][c + 2], acc[r][c + 3], xv[r][c],
+                                              xv[r][c + 1], xv[r][c + 2], xv[r][c + 3], x[c], x[c + 1], x[c + 2],
+                                              x[c + 3], wv[r]);
+            }
+            __syncthreads();
+            continue;
+        } else if constexpr (kSignFast) {
             if (stage == 0) tile_fast = flags[2] == 0;
             const bool fast = tile_fast && flags[stage & 1] == 0;
             if (fast != xv_scaled) {  // exact both ways: the tile is in the scalable range
@@ -956,6 +988,17 @@ __global__ void sum_splits_kernel(const float *__restrict__ part, int64_t splits
     float s = part[t];
     for (int64_t q = 1; q < splits; ++q) s += part[q * len + t];
     out[t] = s;
+}
+
+// *flag = 1 where some value of a [la] or b [lb] lies outside sign_scalable's range (the caller
+// clears the flag first; every writer stores the same 1).
+__global__ void sign_range_kernel(const float *__restrict__ a, int64_t la, const float *__restrict__ b, int64_t lb,
+                                  uint32_t *__restrict__ flag) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    bool bad = false;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < la + lb; t += stride)
+        bad = bad || !sign_scalable(t < la ? a[t] : b[t - la]);
+    if (__any(bad) && (threadIdx.x & 63) == 0) *flag = 1u;
 }
 
 // Column sums of t [batch, n, d] over n, in a fixed order: blocks of 64 columns x 256 rows
@@ -1118,7 +1161,8 @@ template <int MODE, int PK, bool TR, bool WGRAD, bool PRE, int FW, bool EXPG = f
 int launch_backward(const float *g, const float *aux0, const float *aux1, const float *x1,
                     const float *x2, const float *w, int64_t batch, int64_t n, int64_t m, int64_t d,
                     double p, float *grad, float *part, hipStream_t s, const float *eo = nullptr,
-                    float es = 0.0f) {
+                    float es = 0.0f, const uint32_t *gate = nullptr, uint32_t gate_run = 0,
+                    int64_t *shared_splits = nullptr, bool finish = true) {
     // the direct layout's staging lanes span two rows of m: their byte offsets are 32-bit
     TPW_REQUIRE(TR || 4 * m + 128 < ((int64_t)1 << 32),
                 "backward: %lld columns exceed the kernel's 32-bit staging offsets", (long long)m);
@@ -1127,14 +1171,19 @@ int launch_backward(const float *g, const float *aux0, const float *aux1, const 
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, 0) != hipSuccess || per_cu <= 0)
         per_cu = 2;
     if (per_cu > kMaxBlocksPerCU) per_cu = kMaxBlocksPerCU;
-    const int64_t splits = lp_backward_splits((int64_t)device_cus() * per_cu, batch, n, m, d, FW);
+    // gated instances of one backward share the first one's split count (and so the partials'
+    // layout and the one sum_splits pass after the last)
+    int64_t splits = shared_splits && *shared_splits > 0
+                         ? *shared_splits
+                         : lp_backward_splits((int64_t)device_cus() * per_cu, batch, n, m, d, FW);
+    if (shared_splits) *shared_splits = splits;
     const int64_t jps = cdiv(cdiv(m, splits), kBJ) * kBJ;
     dim3 grid((unsigned)cdiv(d, FW), (unsigned)cdiv(n, kBRows), (unsigned)(splits * batch));
     float *dst = splits > 1 ? part : grad;
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s, g, aux0, aux1, x1, x2, w, n, m, d, (float)p,
-                       jps, batch, dst, eo, es);
+                       jps, batch, dst, eo, es, gate, gate_run);
     int rc = check_launch("lp_backward_kernel");
-    if (rc != TPW_OK || splits == 1) return rc;
+    if (rc != TPW_OK || splits == 1 || !finish) return rc;
     const int64_t len = batch * n * d;
     hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)cdiv(len, 256)), dim3(256), 0, s, part,
                        splits, len, grad);
@@ -1168,6 +1217,7 @@ struct BwdJob {
     bool x1_transposed;  // single-direction call for x2's gradient (x1/x2 already swapped)
     const float *eo = nullptr;  // exp-scaled gradient (EXPG): the exp kernel's output, and -gamma
     float es = 0.0f;
+    uint32_t *flag = nullptr;  // a workspace word for the p = 1 range flag (nullptr: no wide p = 1)
 };
 
 template <int MODE, int PK, int FW, bool PRE, bool EXPG = false>
@@ -1203,10 +1253,49 @@ int run_backward_fw(const BwdJob &j, hipStream_t s) {
     return rc;
 }
 
+// p = 1 (the root or the power sum) above 64 features: sign_range_kernel flags x1 and x2 values
+// outside the pre-scaled sign path's range, then the wide kernel (sign path only; runs when the
+// flag is clear) and the narrow one (per-tile test and signf path; runs when it is set) are both
+// launched with the wide kernel's split count, and one sum_splits pass follows.
+template <int MODE>
+int run_backward_p1_gated(const BwdJob &j, hipStream_t s) {
+    int rc = fill(reinterpret_cast<float *>(j.flag), 1, 0.0f, s);
+    if (rc != TPW_OK) return rc;
+    const int64_t l1 = j.batch * j.n * j.d, l2 = j.batch * j.m * j.d;
+    const int64_t blocks = cdiv(l1 + l2, 256 * 8);
+    hipLaunchKernelGGL(sign_range_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, j.x1,
+                       l1, j.x2, l2, j.flag);
+    rc = check_launch("sign_range_kernel");
+    if (rc != TPW_OK) return rc;
+    auto both = [&](auto tr, const float *xa, const float *xb, int64_t na, int64_t nb, float *grad) {
+        constexpr bool TR = decltype(tr)::value;
+        int64_t sp = 0;
+        int r = launch_backward<MODE, kP1, TR, false, false, kBFeatWide>(j.g, nullptr, nullptr, xa, xb, j.w, j.batch,
+                                                                          na, nb, j.d, j.p, grad, j.part, s, nullptr,
+                                                                          0.0f, j.flag, 0u, &sp, false);
+        if (r != TPW_OK) return r;
+        return launch_backward<MODE, kP1, TR, false, false, kBFeat>(j.g, nullptr, nullptr, xa, xb, j.w, j.batch, na,
+                                                                     nb, j.d, j.p, grad, j.part, s, nullptr, 0.0f,
+                                                                     j.flag, 1u, &sp, true);
+    };
+    if (j.gx1) {
+        rc = j.x1_transposed ? both(std::true_type{}, j.x1, j.x2, j.n, j.m, j.gx1)
+                             : both(std::false_type{}, j.x1, j.x2, j.n, j.m, j.gx1);
+        if (rc != TPW_OK) return rc;
+    }
+    if (j.gx2) rc = both(std::true_type{}, j.x2, j.x1, j.m, j.n, j.gx2);
+    return rc;
+}
+
 // The wide kernel above 64 features where it serves the case and its 16-byte staging fits
 // (aligned arrays, n, m and d multiples of 4); else the narrow one.
 template <int MODE, int PK, bool EXPG = false>
 int run_backward(const BwdJob &j, hipStream_t s) {
+    if constexpr (PK == kP1 && (MODE == kRoot || MODE == kSum) && !EXPG) {
+        if (j.flag && j.d > kBFeat && j.n % 4 == 0 && j.m % 4 == 0 && j.d % 4 == 0 && aligned16(j.g) &&
+            aligned16(j.x1) && aligned16(j.x2))
+            return run_backward_p1_gated<MODE>(j, s);
+    }
     if constexpr (kWide<MODE, PK>) {
         const bool fits = j.d > kBFeat && j.n % 4 == 0 && j.m % 4 == 0 && j.d % 4 == 0 && aligned16(j.g) &&
                           aligned16(j.aux0) && aligned16(j.x1) && aligned16(j.x2) && aligned16(j.eo);
@@ -1237,7 +1326,11 @@ int dispatch_backward(int pk, const BwdJob &j, hipStream_t s) {
 // pair buffer 1 | pair buffer 2].  Pair buffers hold the precomputed weights (and, for
 // Bray-Curtis, the denominator that buffer 1 is computed from in place).
 struct Workspace {
-    size_t part, rows, cols, pair1, pair2, total;
+    size_t part, rows, cols, pair1, pair2, flag, total;
+    // the range flag's word (the last 256 bytes)
+    uint32_t *flag_word(void *ws) const {
+        return reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + part + rows + cols + pair1 + pair2);
+    }
 };
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 Workspace workspace_layout(int metric, int64_t batch, int64_t n, int64_t m, int64_t d) {
@@ -1259,7 +1352,9 @@ Workspace workspace_layout(int metric, int64_t batch, int64_t n, int64_t m, int6
     }
     if (metric == TPW_FAM_WMINKOWSKI || metric == TPW_FAM_BRAYCURTIS || metric < 0) w.pair1 = pair;
     if (metric == TPW_FAM_BRAYCURTIS) w.pair2 = pair;
-    w.total = w.part + w.rows + w.cols + w.pair1 + w.pair2;
+    // the p = 1 range flag: the Minkowski (cdist) backward, laplacian_kernel's and the p-power sum's
+    if (metric < 0 || metric == TPW_FAM_PPMINKOWSKI) w.flag = 256;
+    w.total = w.part + w.rows + w.cols + w.pair1 + w.pair2 + w.flag;
     return w;
 }
 constexpr int kLpMetric = -1;  // the Minkowski (cdist) backward in workspace_layout
@@ -1325,6 +1420,7 @@ extern "C" int tpw_lp_distances_backward(const float *grad, const float *x1, con
     BwdJob j{grad, dist, nullptr, x1, x2, nullptr, batch, n, m, d, p, grad_x1, nullptr, nullptr,
              reinterpret_cast<float *>(ws), reinterpret_cast<float *>(ws + lay.part + lay.rows + lay.cols),
              nullptr, transposed != 0};
+    j.flag = lay.flag_word(ws);
     return dispatch_backward<kRoot>(pkind_of(p), j, s);
 }
 
@@ -1348,6 +1444,7 @@ extern "C" int tpw_lp_distances_backward2(const float *grad, const float *x1, co
     BwdJob j{grad, dist, nullptr, x1, x2, nullptr, batch, n, m, d, p, grad_x1, grad_x2, nullptr,
              reinterpret_cast<float *>(ws), reinterpret_cast<float *>(ws + lay.part + lay.rows + lay.cols),
              nullptr, false};
+    j.flag = lay.flag_word(ws);
     return dispatch_backward<kRoot>(pkind_of(p), j, s);
 }
 
@@ -1424,6 +1521,7 @@ extern "C" int tpw_ppminkowski_backward(const float *grad, const float *x1, cons
         return lp_inf_backward(grad, x1, x2, nullptr, batch, n, m, d, p < 0, grad_x1, grad_x2, nullptr, s);
     BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, p, grad_x1, grad_x2, nullptr,
              part, nullptr, nullptr, false};
+    j.flag = lay.flag_word(ws);
     return dispatch_backward<kSum>(pkind_of(p), j, s);
 }
 
@@ -1593,5 +1691,6 @@ extern "C" int tpw_pairwise_exp_kernel_backward(const float *grad, const float *
     if (rc != TPW_OK) return rc;
     BwdJob j{pair1, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1, grad_x2, nullptr, part,
              nullptr, nullptr, false};
+    j.flag = lay.flag_word(ws);
     return run_backward<kRoot, kP1>(j, s);
 }

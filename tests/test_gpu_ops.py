@@ -125,18 +125,23 @@ def test_sqeuclidean_and_rbf_backward_wide(n, m, d):
 
 
 @pytest.mark.parametrize("kind", [capi.KER_RBF, capi.KER_LAPLACIAN])
-@pytest.mark.parametrize("B,n,m,d", [(1, 260, 132, 128), (2, 130, 70, 96), (1, 258, 131, 40)])
-def test_exp_kernel_backward_fused_matches_composite(kind, B, n, m, d):
+@pytest.mark.parametrize("B,n,m,d,outside", [(1, 260, 132, 128, False), (2, 130, 70, 96, False),
+                                             (1, 258, 131, 40, False), (1, 260, 132, 128, True)])
+def test_exp_kernel_backward_fused_matches_composite(kind, B, n, m, d, outside):
     """tpw_pairwise_exp_kernel_backward forms each pair's gradient (grad * out) * -gamma inside
-    the backward kernel (rbf) or in one elementwise pass (laplacian); the composite multiplies in
-    two ATen passes and calls the distance's backward entry point (tpw_ppminkowski_backward
-    p = 2, tpw_lp_distances_backward2 p = 1).  Same weights, same kernels, same order of sums:
-    bit-identical.  Shapes: the wide kernel (rbf, n, m, d multiples of 4), batched, and ragged
-    rows with d <= 64 (narrow kernels)."""
-    print(f"exp kernel backward kind={kind} B={B} n={n} m={m} d={d}", flush=True)
+    the backward kernels (rbf; laplacian on the wide kernel's shapes) or in one elementwise pass
+    (laplacian elsewhere); the composite multiplies in two ATen passes and calls the distance's
+    backward entry point (tpw_ppminkowski_backward p = 2, tpw_lp_distances_backward2 p = 1).
+    Same weights, same kernels, same order of sums: bit-identical.  Shapes: the wide kernels
+    (n, m, d multiples of 4), batched, and ragged rows with d <= 64 (narrow kernels); with
+    `outside`, one x2 value of 2^60 sends laplacian's p = 1 backward to its narrow instance."""
+    print(f"exp kernel backward kind={kind} B={B} n={n} m={m} d={d} outside={outside}", flush=True)
     gamma = 0.02 if kind == capi.KER_RBF else 0.05
     x1 = randn(B, n, d, seed=20).to(DEV)
-    x2 = randn(B, m, d, seed=21).to(DEV)
+    x2 = randn(B, m, d, seed=21)
+    if outside:
+        x2[0, 7, 5] = 2.0 ** 60
+    x2 = x2.to(DEV)
     g = randn(B, n, m, seed=22).to(DEV)
     out = capi.pairwise_exp_kernel(x1, x2, kind, gamma)
     gx1, gx2 = capi.pairwise_exp_kernel_backward(g, out, x1, x2, kind, gamma)

@@ -1257,7 +1257,7 @@ int run_backward_fw(const BwdJob &j, hipStream_t s) {
 // outside the pre-scaled sign path's range, then the wide kernel (sign path only; runs when the
 // flag is clear) and the narrow one (per-tile test and signf path; runs when it is set) are both
 // launched with the wide kernel's split count, and one sum_splits pass follows.
-template <int MODE>
+template <int MODE, bool EXPG = false>
 int run_backward_p1_gated(const BwdJob &j, hipStream_t s) {
     int rc = fill(reinterpret_cast<float *>(j.flag), 1, 0.0f, s);
     if (rc != TPW_OK) return rc;
@@ -1270,13 +1270,13 @@ int run_backward_p1_gated(const BwdJob &j, hipStream_t s) {
     auto both = [&](auto tr, const float *xa, const float *xb, int64_t na, int64_t nb, float *grad) {
         constexpr bool TR = decltype(tr)::value;
         int64_t sp = 0;
-        int r = launch_backward<MODE, kP1, TR, false, false, kBFeatWide>(j.g, nullptr, nullptr, xa, xb, j.w, j.batch,
-                                                                          na, nb, j.d, j.p, grad, j.part, s, nullptr,
-                                                                          0.0f, j.flag, 0u, &sp, false);
+        int r = launch_backward<MODE, kP1, TR, false, false, kBFeatWide, EXPG>(
+            j.g, nullptr, nullptr, xa, xb, j.w, j.batch, na, nb, j.d, j.p, grad, j.part, s, j.eo, j.es, j.flag, 0u,
+            &sp, false);
         if (r != TPW_OK) return r;
-        return launch_backward<MODE, kP1, TR, false, false, kBFeat>(j.g, nullptr, nullptr, xa, xb, j.w, j.batch, na,
-                                                                     nb, j.d, j.p, grad, j.part, s, nullptr, 0.0f,
-                                                                     j.flag, 1u, &sp, true);
+        return launch_backward<MODE, kP1, TR, false, false, kBFeat, EXPG>(j.g, nullptr, nullptr, xa, xb, j.w, j.batch,
+                                                                           na, nb, j.d, j.p, grad, j.part, s, j.eo,
+                                                                           j.es, j.flag, 1u, &sp, true);
     };
     if (j.gx1) {
         rc = j.x1_transposed ? both(std::true_type{}, j.x1, j.x2, j.n, j.m, j.gx1)
@@ -1289,12 +1289,16 @@ int run_backward_p1_gated(const BwdJob &j, hipStream_t s) {
 
 // The wide kernel above 64 features where it serves the case and its 16-byte staging fits
 // (aligned arrays, n, m and d multiples of 4); else the narrow one.
+// Whether run_backward takes run_backward_p1_gated (p = 1: the wide kernel's shapes, and a flag word).
+bool p1_gated_fits(const BwdJob &j) {
+    return j.flag && j.d > kBFeat && j.n % 4 == 0 && j.m % 4 == 0 && j.d % 4 == 0 && aligned16(j.g) &&
+           aligned16(j.x1) && aligned16(j.x2) && aligned16(j.eo);
+}
+
 template <int MODE, int PK, bool EXPG = false>
 int run_backward(const BwdJob &j, hipStream_t s) {
-    if constexpr (PK == kP1 && (MODE == kRoot || MODE == kSum) && !EXPG) {
-        if (j.flag && j.d > kBFeat && j.n % 4 == 0 && j.m % 4 == 0 && j.d % 4 == 0 && aligned16(j.g) &&
-            aligned16(j.x1) && aligned16(j.x2))
-            return run_backward_p1_gated<MODE>(j, s);
+    if constexpr (PK == kP1 && (MODE == kRoot || MODE == kSum)) {
+        if (p1_gated_fits(j)) return run_backward_p1_gated<MODE, EXPG>(j, s);
     }
     if constexpr (kWide<MODE, PK>) {
         const bool fits = j.d > kBFeat && j.n % 4 == 0 && j.m % 4 == 0 && j.d % 4 == 0 && aligned16(j.g) &&
@@ -1677,8 +1681,17 @@ extern "C" int tpw_pairwise_exp_kernel_backward(const float *grad, const float *
                  nullptr, nullptr, false, out, -gamma};
         return run_backward<kSum, kP2, true>(j, s);
     }
-    // p = 1: a second per-pair array would take the narrow kernel past three waves per SIMD
-    // (156 -> 174 VGPRs), so one elementwise pass writes the gradients into the workspace
+    // p = 1: on the wide kernel's shapes (run_backward_p1_gated) the gradient is formed while the
+    // kernels stage their pairs (the narrow fallback instance too, at two waves per SIMD: it runs
+    // only for values outside the sign path's range); elsewhere a second per-pair array would
+    // take the narrow kernel from three waves per SIMD to two (156 -> 174 VGPRs), so one
+    // elementwise pass writes the gradients into the workspace first
+    {
+        BwdJob j{grad, nullptr, nullptr, x1, x2, nullptr, batch, n, m, d, 1.0, grad_x1, grad_x2, nullptr, part,
+                 nullptr, nullptr, false, out, -gamma};
+        j.flag = lay.flag_word(ws);
+        if (p1_gated_fits(j)) return run_backward<kRoot, kP1, true>(j, s);
+    }
     const int64_t len = batch * n * m;
     const bool vec = aligned16(grad) && aligned16(out) && aligned16(pair1);
     const unsigned grid = (unsigned)(cdiv(vec ? cdiv(len, 4) : len, 256) < 16384 ? cdiv(vec ? cdiv(len, 4) : len, 256)

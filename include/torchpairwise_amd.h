@@ -175,9 +175,10 @@ int tpw_pairwise_exp_kernel(const float *x1, const float *x2, int64_t batch, int
 /* grad_x1 [batch, n, d] and grad_x2 [batch, m, d] of tpw_pairwise_exp_kernel's out, given the
  * upstream grad and that out (fp32 [batch, n, m]).  Each pair's gradient of the distance is
  * (grad * out) * (-gamma), the reference's exp_ backward and then mul_(-gamma)'s, one rounding
- * each, followed by the _ppminkowski p = 2 (RBF) or cdist p = 1 (LAPLACIAN) backward.  RBF forms
- * it while the backward kernel stages its pairs (no N x M array written); LAPLACIAN in one
- * elementwise pass into the workspace (one N x M write instead of two).  Results equal those
+ * each, followed by the _ppminkowski p = 2 (RBF) or cdist p = 1 (LAPLACIAN) backward.  It is
+ * formed while the backward kernel stages its pairs (no N x M array written): RBF always,
+ * LAPLACIAN where d > 64 and n, m, d are multiples of 4 with 16-byte aligned arrays (elsewhere
+ * one elementwise pass into the workspace, one N x M write instead of two).  Results equal those
  * two ATen multiplies followed by tpw_ppminkowski_backward (p = 2) or tpw_lp_distances_backward2
  * (p = 1) bit for bit.  workspace: tpw_pairwise_exp_kernel_backward_workspace_size(kind, ...)
  * bytes.  Replaces the autograd chain of the reference's rbf_kernel / laplacian_kernel

@@ -26,10 +26,10 @@
 //     limits the candidates to a few times `count`; they are ranked in LDS and the mask is
 //     written from the lists (see smallest_bound_kernel).  Rows whose lists cannot prove
 //     completeness re-stream the candidates from L2; heavy ties take the radix select.
-//   * count > 256: radix-2 select on the 32-bit order keys (one counting pass per bit below
-//     the common prefix of the row's min and max keys), then, only when the boundary value
-//     is tied, a second radix-2 select on the column index among the tied entries; rows of
-//     up to 16384 keys are held in LDS for the passes.
+//   * count > 256: radix select on the 32-bit order keys (one counting pass per two bits below
+//     the common prefix of the row's min and max keys, its three counts in one reduction),
+//     then, only when the boundary value is tied, a radix-2 select on the column index among
+//     the tied entries; rows of up to 16384 keys are held in LDS for the passes.
 #include "common.hpp"
 
 namespace tpw {
@@ -108,6 +108,22 @@ struct Reducer {
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) r += (uint32_t)s[w];
         return r;
+    }
+    // three counts below 2^21 each (their block sums too), packed into one word: one barrier
+    __device__ void sum3_u32(uint32_t a, uint32_t b, uint32_t c, uint32_t &ra, uint32_t &rb, uint32_t &rc) {
+        uint64_t x = (uint64_t)a | ((uint64_t)b << 21) | ((uint64_t)c << 42);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+        uint64_t *s = slots + phase * kWaves;
+        phase ^= 1;
+        if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = x;
+        __syncthreads();
+        uint64_t r = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) r += s[w];
+        ra = (uint32_t)(r & 0x1fffffu);
+        rb = (uint32_t)((r >> 21) & 0x1fffffu);
+        rc = (uint32_t)(r >> 42);
     }
     // min in the low half, max in the high half
     __device__ void min_max_u32(uint32_t lo, uint32_t hi, uint32_t &mn, uint32_t &mx) {
@@ -226,9 +242,9 @@ __device__ void write_mask_keys(const RowKeys<T, V, CACHED> &keys, uint64_t thr,
     });
 }
 
-// The count-th smallest 64-bit key (order key << 32 | column) of the row: radix-2 select on
-// the order key below the common prefix of the row's min and max keys, then, only when the
-// boundary value is tied, on the column among the tied entries.
+// The count-th smallest 64-bit key (order key << 32 | column) of the row: radix select on the
+// order key below the common prefix of the row's min and max keys (two bits per pass), then,
+// only when the boundary value is tied, on the column among the tied entries (one bit).
 template <typename T, int V, bool CACHED>
 __device__ uint64_t radix_threshold(const RowKeys<T, V, CACHED> &keys, Reducer &red, int count) {
     uint32_t lo = 0xffffffffu, hi = 0;
@@ -242,9 +258,26 @@ __device__ uint64_t radix_threshold(const RowKeys<T, V, CACHED> &keys, Reducer &
     // t = largest value with #(key < t) <= count - 1, i.e. the count-th smallest key
     uint32_t t = kmin;
     if (diff) {
-        const int top = 31 - __builtin_clz(diff);
-        t = kmin & ~((2u << top) - 1u);  // common prefix, zeros below (2u << 31 wraps to 0)
-        for (int b = top; b >= 0; --b) {
+        int b = 31 - __builtin_clz(diff);
+        t = kmin & ~((2u << b) - 1u);  // common prefix, zeros below (2u << 31 wraps to 0)
+        // two bits per pass while rows are shorter than 2^21 (the three counts of a pass share
+        // one reduction): the digit is the largest d in 0..3 with #(key < t | d << (b - 1)) <=
+        // count - 1, the same t as two one-bit steps (the counts grow with d)
+        if (keys.cols < ((int64_t)1 << 21)) {
+            for (; b >= 1; b -= 2) {
+                const uint32_t c1 = t | (1u << (b - 1)), c2 = t | (2u << (b - 1)), c3 = t | (3u << (b - 1));
+                uint32_t n1 = 0, n2 = 0, n3 = 0;
+                keys.for_each([&](uint32_t k, uint32_t) {
+                    n1 += k < c1;
+                    n2 += k < c2;
+                    n3 += k < c3;
+                });
+                red.sum3_u32(n1, n2, n3, n1, n2, n3);
+                const uint32_t lim = (uint32_t)(count - 1);
+                t = n3 <= lim ? c3 : n2 <= lim ? c2 : n1 <= lim ? c1 : t;
+            }
+        }
+        for (; b >= 0; --b) {
             const uint32_t c = t | (1u << b);
             uint32_t n = 0;
             keys.for_each([&](uint32_t k, uint32_t) { n += k < c; });
